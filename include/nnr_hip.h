@@ -1,0 +1,185 @@
+/*
+ * nnr_hip.h -- C ABI of the MI355X (gfx950) backend for NNR's int8 QDQ
+ * compute path.
+ *
+ * The reference (beru/nnr) is a C++ runtime: operators implement
+ * operator_t::init/reshape/exec (src/nnr.h:331-461) and are created through
+ * registry_t::solve (src/registry.cpp:10-27). The HIP backend keeps that
+ * operator interface in C++ (nnr_amd/host/) and every operator crosses into
+ * device code through the functions below: plain pointers and sizes, int
+ * status codes, no exceptions and no C++ or torch types.
+ *
+ * Conventions
+ *   - Pointers named *_dev are device (HBM) pointers; *_host are host pointers.
+ *   - `stream` is a hipStream_t passed as void*; NULL is the default stream.
+ *   - All launches are asynchronous on `stream`; create/destroy calls are
+ *     cold-path and may allocate device memory.
+ *   - Quantized element types: NNRH_U8 / NNRH_S8 (activations), int8 weights.
+ *   - Results are bit-identical to NNR's x64 (AVX-512 VNNI) CPU kernels:
+ *     exact int32 accumulators and the same requantize formula per branch.
+ */
+#ifndef NNR_HIP_H
+#define NNR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ------------------------------------------------------------ */
+enum {
+    NNRH_OK = 0,
+    NNRH_ERR_INVALID = 1,      /* bad argument / shape mismatch            */
+    NNRH_ERR_UNSUPPORTED = 2,  /* valid ONNX, not handled by this backend  */
+    NNRH_ERR_HIP = 3,          /* a HIP runtime call failed                */
+    NNRH_ERR_NOMEM = 4
+};
+enum { NNRH_U8 = 0, NNRH_S8 = 1, NNRH_I32 = 2, NNRH_F32 = 3, NNRH_F16 = 4 };
+
+/* Message of the last failing call on this thread (never NULL). */
+const char* nnrh_last_error(void);
+/* Library version string. */
+const char* nnrh_version(void);
+
+/* ---- device plumbing (the host framework includes no HIP headers) -------
+ * Replaces the host allocations of the reference's memory planner
+ * (src/memory_planner.cpp:282-331) and tensor_t::data ownership (src/nnr.h:236). */
+int nnrh_device_count(int* count);
+int nnrh_set_device(int device);
+int nnrh_malloc(void** ptr_dev, size_t bytes);
+int nnrh_free(void* ptr_dev);
+/* kind: 0 host->device, 1 device->host, 2 device->device */
+int nnrh_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream);
+int nnrh_fill_u8(void* dst_dev, uint8_t value, size_t bytes, void* stream);
+int nnrh_stream_create(void** stream);
+int nnrh_stream_destroy(void* stream);
+int nnrh_stream_synchronize(void* stream);
+int nnrh_device_synchronize(void);
+int nnrh_event_create(void** event);
+int nnrh_event_destroy(void* event);
+int nnrh_event_record(void* event, void* stream);
+int nnrh_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ---- QLinearConv ---------------------------------------------------------
+ * Replaces QLinearConv_operator (src/backend/cpu/QLinearConv.cpp:30-1371):
+ * init() attribute parsing (:91-156), reshape() weight pre-packing and
+ * requantize vectors (QLinearConv_reshape.h:18-340), exec() dispatch over the
+ * kernel branches (:1337-1368). Shapes use NCHW logical dims; x_nhwc / y_nhwc
+ * give the physical layout (tensor_t::format, src/nnr.h:226).            */
+typedef struct nnrh_qconv_desc {
+    int N, C, H, W;                 /* input                                */
+    int OC, kH, kW, group;          /* weights [OC][C/group][kH][kW]        */
+    int sH, sW, dH, dW;
+    int pad_t, pad_l, pad_b, pad_r; /* resolved pads (auto_pad applied)     */
+    int oH, oW;
+    int x_nhwc, y_nhwc;
+    int post_fn;                    /* a unary op was fused (operator_t::post_fn) */
+    int act_dtype;                  /* NNRH_U8 or NNRH_S8 (x and y)          */
+    float x_scale; int x_zp;
+    const float* w_scale_host; int w_scale_count;
+    const int8_t* w_zp_host; int w_zp_count;
+    float y_scale; int y_zp;
+    const int8_t* w_host;           /* OIHW int8                            */
+    const int32_t* bias_host;       /* [OC] or NULL                         */
+} nnrh_qconv_desc;
+
+/* kernel branch of QLinearConv::exec_simd_4d (QLinearConv.cpp:1337-1351) */
+enum {
+    NNRH_BR_DW = 1,          /* exec_dw_int8_nhwc         RQ-A [lo,hi]       */
+    NNRH_BR_FIRST = 2,       /* exec_first_layer_int8     RQ-C (+RQ-A')      */
+    NNRH_BR_DIRECT = 3,      /* exec_direct_int8          RQ-A qmin (+A')    */
+    NNRH_BR_PACKED = 4,      /* exec_packed_nr48 (NR48)   RQ-B (+B')         */
+    NNRH_BR_NR16 = 5,        /* exec_packed_nr48 (NR16)   RQ-B               */
+    NNRH_BR_IM2COL_S1 = 6,   /* exec_vnni_im2col, stride1 RQ-A [lo,hi]       */
+    NNRH_BR_IM2COL = 7,      /* exec_vnni_im2col, tiled   RQ-A qmin (+A')    */
+    NNRH_BR_FLOAT = 8        /* exec_float_fallback       RQ-A qmin (+A')    */
+};
+
+typedef struct nnrh_qconv* nnrh_qconv_t;
+/* Branch the reference would take for this descriptor (no allocation). */
+int nnrh_qconv_dispatch(const nnrh_qconv_desc* d, int* branch);
+/* reshape(): validates, packs weights on the device, precomputes requantize
+ * vectors. Host arrays in `d` are only read during the call.             */
+int nnrh_qconv_create(nnrh_qconv_t* h, const nnrh_qconv_desc* d);
+int nnrh_qconv_branch(nnrh_qconv_t h, int* branch);
+/* exec(): x_dev / y_dev in the layouts given at create time.            */
+int nnrh_qconv_run(nnrh_qconv_t h, const void* x_dev, void* y_dev, void* stream);
+int nnrh_qconv_destroy(nnrh_qconv_t h);
+
+/* ---- QLinearMatMul ------------------------------------------------------
+ * Replaces QLinearMatMul_operator (src/backend/cpu/QLinearMatMul.cpp:14-233)
+ * for a constant B: reshape() pre-pack (:75-91), exec() (:111-232).
+ * Only b_scale[0] / b_zp[0] are used, as in the reference (:118-119).
+ * A: [batch][m][k], Y: [batch][m][n] row-major; B: [k][n] constant.
+ * Scales: scale_dtype NNRH_F32 or NNRH_F16 (fp16 combined scale, :125-132).*/
+typedef struct nnrh_qmatmul_desc {
+    int m, n, k;
+    int a_dtype;                    /* NNRH_U8 / NNRH_S8                      */
+    int b_dtype;                    /* NNRH_U8 / NNRH_S8                      */
+    int y_dtype;                    /* NNRH_U8 / NNRH_S8                      */
+    int scale_dtype;                /* NNRH_F32 / NNRH_F16                    */
+    const void* a_scale_host; const void* a_zp_host;   /* may be overridden per run */
+    const void* b_scale_host; const void* b_zp_host;
+    const void* y_scale_host; const void* y_zp_host;
+    const void* b_host;             /* [k][n]                                 */
+} nnrh_qmatmul_desc;
+typedef struct nnrh_qmatmul* nnrh_qmatmul_t;
+int nnrh_qmatmul_create(nnrh_qmatmul_t* h, const nnrh_qmatmul_desc* d);
+/* a_scale_dev (float32) / a_zp_dev (a_dtype) override the create-time A
+ * quantization with device values, e.g. from DynamicQuantizeLinear; NULL
+ * keeps the create-time ones. a_batch_stride = 0 broadcasts A.          */
+int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a_dev, long long a_batch_stride,
+                     void* y_dev, int batch, const float* a_scale_dev,
+                     const void* a_zp_dev, void* stream);
+int nnrh_qmatmul_destroy(nnrh_qmatmul_t h);
+
+/* ---- MatMulInteger ------------------------------------------------------
+ * Replaces MatMulInteger_operator (src/backend/cpu/MatMulInteger.cpp:11-150):
+ * y[b][m][n] = sum_k (a - a_zp)(b - b_zp) in int32; both operands on the
+ * device, B packed per call (the reference packs per exec, :120).
+ * Strides are in elements; a stride of 0 broadcasts that operand.        */
+typedef struct nnrh_matmul_integer* nnrh_matmul_integer_t;
+int nnrh_matmul_integer_create(nnrh_matmul_integer_t* h, int m, int n, int k,
+                               int a_dtype, int b_dtype, int max_batch);
+int nnrh_matmul_integer_run(nnrh_matmul_integer_t h, const void* a_dev,
+                            long long a_batch_stride, const void* b_dev,
+                            long long b_batch_stride, int a_zp, int b_zp,
+                            int32_t* y_dev, int batch, void* stream);
+int nnrh_matmul_integer_destroy(nnrh_matmul_integer_t h);
+
+/* ---- QuantizeLinear / DequantizeLinear / DynamicQuantizeLinear ----------
+ * QuantizeLinear.cpp:128-194 (per-tensor uint8/int8), DequantizeLinear.cpp:
+ * 100-152, DynamicQuantizeLinear.cpp:27-58.                              */
+int nnrh_quantize_linear(const float* x_dev, size_t n, float scale, int zp,
+                         int y_dtype, void* y_dev, void* stream);
+int nnrh_dequantize_linear(const void* x_dev, int x_dtype, size_t n, float scale,
+                           int zp, float* y_dev, void* stream);
+size_t nnrh_dynamic_quantize_workspace(void);
+int nnrh_dynamic_quantize_linear(const float* x_dev, size_t n, uint8_t* y_dev,
+                                 float* y_scale_dev, uint8_t* y_zp_dev,
+                                 void* workspace_dev, void* stream);
+
+/* ---- QLinearAdd ----------------------------------------------------------
+ * QLinearAdd_operator::exec_typed (src/backend/cpu/QLinearAdd.cpp:33-265).
+ * kind: 0 same shape, 1 B scalar, 2 A scalar, 3 per-channel (B is [C]).
+ * Per-channel: y is [N][C][HW] logical, y_nhwc gives the physical layout. */
+int nnrh_qlinear_add(int kind, const void* a_dev, const void* b_dev, void* y_dev,
+                     size_t n, int C, int HW, int y_nhwc, int dtype,
+                     float a_scale, int a_zp, float b_scale, int b_zp,
+                     float y_scale, int y_zp, void* stream);
+
+/* ---- uint8 MaxPool, NHWC (src/backend/x64/pool_x64.h:396-436) ----------- */
+int nnrh_maxpool_u8_nhwc(const uint8_t* x_dev, uint8_t* y_dev, int N, int C,
+                         int iH, int iW, int oH, int oW, int kH, int kW, int sH,
+                         int sW, int pH, int pW, void* stream);
+
+/* ---- layout: NCHW -> NHWC uint8 (transpose_nchw_nhwc_u8.h:1-126) -------- */
+int nnrh_nchw_to_nhwc_u8(const uint8_t* x_dev, uint8_t* y_dev, int N, int C,
+                         int HW, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NNR_HIP_H */

@@ -1,0 +1,230 @@
+"""nnr_amd -- MI355X (gfx950) backend for NNR's int8 QDQ compute path.
+
+The product is the C ABI in include/nnr_hip.h (nnr_amd/lib/libnnr_hip.so,
+HIP kernels in nnr_amd/csrc) and the C++ operator layer in nnr_amd/host that
+mirrors NNR's operator_t / registry_t interface. This Python module is a thin
+convenience view of the same C ABI for tests and benchmarks: device memory is
+torch tensors, every call goes straight to the HIP library, and a missing
+library raises instead of falling back to anything.
+"""
+from __future__ import annotations
+
+import ctypes as ct
+
+import numpy as np
+
+from ._lib import (BRANCH_NAMES, F16, F32, I32, S8, U8, NnrHipError, QConvDesc,  # noqa: F401
+                   QMatMulDesc, check, cur_stream, lib, ptr)
+
+__all__ = ["QLinearConv", "QLinearMatMul", "MatMulInteger", "quantize_linear",
+           "dequantize_linear", "dynamic_quantize_linear", "qlinear_add", "maxpool_u8_nhwc",
+           "conv_dispatch", "NnrHipError", "lib"]
+
+
+def _dt(np_dtype) -> int:
+    return U8 if np.dtype(np_dtype) == np.uint8 else S8
+
+
+def _conv_desc(N, C, H, W, w, *, group=1, stride=(1, 1), dil=(1, 1), pads=(0, 0, 0, 0),
+               x_nhwc=0, y_nhwc=0, post_fn=0, act_dtype=np.uint8, x_scale=0.02, x_zp=128,
+               w_scale=(0.01,), w_zp=(), y_scale=0.05, y_zp=0, bias=None):
+    w = np.ascontiguousarray(w, np.int8)
+    OC, _, kH, kW = w.shape
+    keep = {
+        "w": w,
+        "w_scale": np.ascontiguousarray(w_scale, np.float32).reshape(-1),
+        "w_zp": np.ascontiguousarray(np.asarray(w_zp).astype(np.int64).astype(np.uint8).view(np.int8)
+                                     if len(np.atleast_1d(w_zp)) else np.zeros(0, np.int8)),
+        "bias": None if bias is None else np.ascontiguousarray(bias, np.int32),
+    }
+    ek_h, ek_w = (kH - 1) * dil[0] + 1, (kW - 1) * dil[1] + 1
+    oH = int(np.floor((H + pads[0] + pads[2] - ek_h) / stride[0] + 1))
+    oW = int(np.floor((W + pads[1] + pads[3] - ek_w) / stride[1] + 1))
+    P = ct.POINTER
+    d = QConvDesc(N, C, H, W, OC, kH, kW, group, stride[0], stride[1], dil[0], dil[1],
+                  pads[0], pads[1], pads[2], pads[3], oH, oW, int(x_nhwc), int(y_nhwc),
+                  int(post_fn), _dt(act_dtype), float(x_scale), int(x_zp),
+                  keep["w_scale"].ctypes.data_as(P(ct.c_float)), keep["w_scale"].size,
+                  keep["w_zp"].ctypes.data_as(P(ct.c_int8)) if keep["w_zp"].size else None,
+                  keep["w_zp"].size, float(y_scale), int(y_zp),
+                  keep["w"].ctypes.data_as(P(ct.c_int8)),
+                  keep["bias"].ctypes.data_as(P(ct.c_int32)) if keep["bias"] is not None else None)
+    return d, keep
+
+
+def conv_dispatch(N, C, H, W, w, **kw) -> int:
+    """Kernel branch NNR's QLinearConv would take (pure host computation)."""
+    d, _keep = _conv_desc(N, C, H, W, w, **kw)
+    br = ct.c_int()
+    check(lib().nnrh_qconv_dispatch(ct.byref(d), ct.byref(br)))
+    return br.value
+
+
+class QLinearConv:
+    """QLinearConv on the GPU: create packs weights, __call__ launches."""
+
+    def __init__(self, N, C, H, W, w, **kw):
+        self.desc, keep = _conv_desc(N, C, H, W, w, **kw)
+        self.act_dtype = np.dtype(kw.get("act_dtype", np.uint8))
+        h = ct.c_void_p()
+        check(lib().nnrh_qconv_create(ct.byref(h), ct.byref(self.desc)))
+        self.h = h
+        br = ct.c_int()
+        check(lib().nnrh_qconv_branch(h, ct.byref(br)))
+        self.branch = br.value
+        d = self.desc
+        self.out_shape = (d.N, d.oH, d.oW, d.OC) if d.y_nhwc else (d.N, d.OC, d.oH, d.oW)
+        self.in_shape = (d.N, d.H, d.W, d.C) if d.x_nhwc else (d.N, d.C, d.H, d.W)
+
+    def __call__(self, x, y=None, stream=None):
+        import torch
+        if tuple(x.shape) != self.in_shape or not x.is_contiguous():
+            raise ValueError(f"x shape {tuple(x.shape)} != {self.in_shape} or not contiguous")
+        if y is None:
+            y = torch.empty(self.out_shape, dtype=torch.uint8 if self.act_dtype == np.uint8
+                            else torch.int8, device=x.device)
+        check(lib().nnrh_qconv_run(self.h, ptr(x), ptr(y),
+                                   cur_stream() if stream is None else stream))
+        return y
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None):
+                lib().nnrh_qconv_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+class QLinearMatMul:
+    """QLinearMatMul with constant B (prepacked at construction)."""
+
+    def __init__(self, b, a_scale, a_zp, b_scale, b_zp, y_scale, y_zp, *, m, a_dtype=np.uint8,
+                 y_dtype=np.uint8, scale_dtype=np.float32):
+        b = np.ascontiguousarray(b)
+        k, n = b.shape
+        sd = np.float16 if scale_dtype == np.float16 else np.float32
+        self._keep = dict(
+            b=b, a_s=np.array([a_scale], sd), a_z=np.array([a_zp], a_dtype),
+            b_s=np.array([b_scale], sd), b_z=np.array([b_zp], b.dtype),
+            y_s=np.array([y_scale], sd), y_z=np.array([y_zp], y_dtype))
+        kp = self._keep
+        self.desc = QMatMulDesc(m, n, k, _dt(a_dtype), _dt(b.dtype), _dt(y_dtype),
+                                F16 if sd == np.float16 else F32,
+                                kp["a_s"].ctypes.data, kp["a_z"].ctypes.data,
+                                kp["b_s"].ctypes.data, kp["b_z"].ctypes.data,
+                                kp["y_s"].ctypes.data, kp["y_z"].ctypes.data, b.ctypes.data)
+        h = ct.c_void_p()
+        check(lib().nnrh_qmatmul_create(ct.byref(h), ct.byref(self.desc)))
+        self.h = h
+        self.m, self.n, self.k = m, n, k
+        self.y_dtype = np.dtype(y_dtype)
+
+    def __call__(self, a, y=None, a_scale_dev=None, a_zp_dev=None, stream=None):
+        import torch
+        if a.shape[-1] != self.k or a.shape[-2] != self.m:
+            raise ValueError("a shape mismatch")
+        batch = int(np.prod(a.shape[:-2])) if a.dim() > 2 else 1
+        if y is None:
+            y = torch.empty(tuple(a.shape[:-1]) + (self.n,),
+                            dtype=torch.uint8 if self.y_dtype == np.uint8 else torch.int8,
+                            device=a.device)
+        check(lib().nnrh_qmatmul_run(self.h, ptr(a), self.m * self.k if batch > 1 else 0, ptr(y),
+                                     batch, ptr(a_scale_dev), ptr(a_zp_dev),
+                                     cur_stream() if stream is None else stream))
+        return y
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None):
+                lib().nnrh_qmatmul_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+class MatMulInteger:
+    def __init__(self, m, n, k, a_dtype=np.uint8, b_dtype=np.int8, max_batch=1):
+        h = ct.c_void_p()
+        check(lib().nnrh_matmul_integer_create(ct.byref(h), m, n, k, _dt(a_dtype), _dt(b_dtype),
+                                               max_batch))
+        self.h, self.m, self.n, self.k = h, m, n, k
+
+    def __call__(self, a, b, a_zp=0, b_zp=0, batch=1, a_bstride=None, b_bstride=None, y=None,
+                 stream=None):
+        import torch
+        if y is None:
+            y = torch.empty((batch, self.m, self.n) if batch > 1 else (self.m, self.n),
+                            dtype=torch.int32, device=a.device)
+        ab = (self.m * self.k if batch > 1 else 0) if a_bstride is None else a_bstride
+        bb = (self.k * self.n if batch > 1 and b.dim() > 2 else 0) if b_bstride is None else b_bstride
+        check(lib().nnrh_matmul_integer_run(self.h, ptr(a), ab, ptr(b), bb, int(a_zp), int(b_zp),
+                                            ptr(y), batch,
+                                            cur_stream() if stream is None else stream))
+        return y
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None):
+                lib().nnrh_matmul_integer_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+def quantize_linear(x, scale, zp, dtype=np.uint8, y=None):
+    import torch
+    if y is None:
+        y = torch.empty(x.shape, dtype=torch.uint8 if np.dtype(dtype) == np.uint8 else torch.int8,
+                        device=x.device)
+    check(lib().nnrh_quantize_linear(ptr(x), x.numel(), float(scale), int(zp), _dt(dtype), ptr(y),
+                                     cur_stream()))
+    return y
+
+
+def dequantize_linear(x, scale, zp, y=None):
+    import torch
+    if y is None:
+        y = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    dt = {torch.uint8: U8, torch.int8: S8, torch.int32: I32}[x.dtype]
+    check(lib().nnrh_dequantize_linear(ptr(x), dt, x.numel(), float(scale), int(zp), ptr(y),
+                                       cur_stream()))
+    return y
+
+
+_dq_ws = {}
+
+
+def dynamic_quantize_linear(x):
+    import torch
+    dev = x.device
+    if dev not in _dq_ws:
+        _dq_ws[dev] = torch.empty(int(lib().nnrh_dynamic_quantize_workspace()), dtype=torch.uint8,
+                                  device=dev)
+    y = torch.empty(x.shape, dtype=torch.uint8, device=dev)
+    s = torch.empty(1, dtype=torch.float32, device=dev)
+    z = torch.empty(1, dtype=torch.uint8, device=dev)
+    check(lib().nnrh_dynamic_quantize_linear(ptr(x), x.numel(), ptr(y), ptr(s), ptr(z),
+                                             ptr(_dq_ws[dev]), cur_stream()))
+    return y, s, z
+
+
+def qlinear_add(kind, a, b, a_s, a_zp, b_s, b_zp, y_s, y_zp, C=0, HW=0, y_nhwc=0, y=None):
+    import torch
+    full = a if a.numel() >= b.numel() else b
+    if y is None:
+        y = torch.empty(full.shape, dtype=full.dtype, device=full.device)
+    dt = U8 if a.dtype == torch.uint8 else S8
+    check(lib().nnrh_qlinear_add(kind, ptr(a), ptr(b), ptr(y), y.numel(), C, HW, y_nhwc, dt,
+                                 float(a_s), int(a_zp), float(b_s), int(b_zp), float(y_s),
+                                 int(y_zp), cur_stream()))
+    return y
+
+
+def maxpool_u8_nhwc(x, kH, kW, sH, sW, pH, pW, oH, oW):
+    import torch
+    N, H, W, C = x.shape
+    y = torch.empty((N, oH, oW, C), dtype=torch.uint8, device=x.device)
+    check(lib().nnrh_maxpool_u8_nhwc(ptr(x), ptr(y), N, C, H, W, oH, oW, kH, kW, sH, sW, pH, pW,
+                                     cur_stream()))
+    return y

@@ -1,0 +1,139 @@
+"""ctypes binding of the C ABI in include/nnr_hip.h.
+
+This is the Python view of the same boundary the C++ host operators use. It
+loads nnr_amd/lib/libnnr_hip.so and fails loudly when the library is missing:
+there is no CPU fallback anywhere in the product path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libnnr_hip.so")
+
+NNRH_OK, NNRH_ERR_INVALID, NNRH_ERR_UNSUPPORTED, NNRH_ERR_HIP, NNRH_ERR_NOMEM = range(5)
+U8, S8, I32, F32, F16 = range(5)
+BRANCH_NAMES = {1: "DW", 2: "FIRST", 3: "DIRECT", 4: "PACKED", 5: "NR16",
+                6: "IM2COL_S1", 7: "IM2COL", 8: "FLOAT"}
+
+# every symbol the header declares (checked by the CPU test suite)
+EXPORTS = [
+    "nnrh_last_error", "nnrh_version", "nnrh_device_count", "nnrh_set_device",
+    "nnrh_malloc", "nnrh_free", "nnrh_memcpy", "nnrh_fill_u8", "nnrh_stream_create",
+    "nnrh_stream_destroy", "nnrh_stream_synchronize", "nnrh_device_synchronize",
+    "nnrh_event_create", "nnrh_event_destroy", "nnrh_event_record", "nnrh_event_elapsed_ms",
+    "nnrh_qconv_dispatch", "nnrh_qconv_create", "nnrh_qconv_branch", "nnrh_qconv_run",
+    "nnrh_qconv_destroy", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
+    "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
+    "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
+    "nnrh_dynamic_quantize_linear", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
+    "nnrh_nchw_to_nhwc_u8",
+]
+
+
+class NnrHipError(RuntimeError):
+    def __init__(self, rc: int, msg: str):
+        super().__init__(f"nnrh error {rc}: {msg}")
+        self.rc = rc
+
+
+class QConvDesc(C.Structure):
+    _fields_ = [(n, C.c_int) for n in (
+        "N", "C", "H", "W", "OC", "kH", "kW", "group", "sH", "sW", "dH", "dW",
+        "pad_t", "pad_l", "pad_b", "pad_r", "oH", "oW", "x_nhwc", "y_nhwc",
+        "post_fn", "act_dtype")] + [
+        ("x_scale", C.c_float), ("x_zp", C.c_int),
+        ("w_scale_host", C.POINTER(C.c_float)), ("w_scale_count", C.c_int),
+        ("w_zp_host", C.POINTER(C.c_int8)), ("w_zp_count", C.c_int),
+        ("y_scale", C.c_float), ("y_zp", C.c_int),
+        ("w_host", C.POINTER(C.c_int8)), ("bias_host", C.POINTER(C.c_int32)),
+    ]
+
+
+class QMatMulDesc(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("m", "n", "k", "a_dtype", "b_dtype", "y_dtype",
+                                        "scale_dtype")] + [
+        (n, C.c_void_p) for n in ("a_scale_host", "a_zp_host", "b_scale_host", "b_zp_host",
+                                  "y_scale_host", "y_zp_host", "b_host")]
+
+
+_lib = None
+
+
+def lib():
+    """Load the HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: run __graft_entry__.build() "
+                          "(hipcc --offload-arch=gfx950) first")
+    L = C.CDLL(LIB_PATH)
+    vp, i, sz, f, ll = C.c_void_p, C.c_int, C.c_size_t, C.c_float, C.c_longlong
+    P = C.POINTER
+    sig = {
+        "nnrh_last_error": (C.c_char_p, []),
+        "nnrh_version": (C.c_char_p, []),
+        "nnrh_device_count": (i, [P(i)]),
+        "nnrh_set_device": (i, [i]),
+        "nnrh_malloc": (i, [P(vp), sz]),
+        "nnrh_free": (i, [vp]),
+        "nnrh_memcpy": (i, [vp, vp, sz, i, vp]),
+        "nnrh_fill_u8": (i, [vp, C.c_uint8, sz, vp]),
+        "nnrh_stream_create": (i, [P(vp)]),
+        "nnrh_stream_destroy": (i, [vp]),
+        "nnrh_stream_synchronize": (i, [vp]),
+        "nnrh_device_synchronize": (i, []),
+        "nnrh_event_create": (i, [P(vp)]),
+        "nnrh_event_destroy": (i, [vp]),
+        "nnrh_event_record": (i, [vp, vp]),
+        "nnrh_event_elapsed_ms": (i, [P(f), vp, vp]),
+        "nnrh_qconv_dispatch": (i, [P(QConvDesc), P(i)]),
+        "nnrh_qconv_create": (i, [P(vp), P(QConvDesc)]),
+        "nnrh_qconv_branch": (i, [vp, P(i)]),
+        "nnrh_qconv_run": (i, [vp, vp, vp, vp]),
+        "nnrh_qconv_destroy": (i, [vp]),
+        "nnrh_qmatmul_create": (i, [P(vp), P(QMatMulDesc)]),
+        "nnrh_qmatmul_run": (i, [vp, vp, ll, vp, i, vp, vp, vp]),
+        "nnrh_qmatmul_destroy": (i, [vp]),
+        "nnrh_matmul_integer_create": (i, [P(vp), i, i, i, i, i, i]),
+        "nnrh_matmul_integer_run": (i, [vp, vp, ll, vp, ll, i, i, vp, i, vp]),
+        "nnrh_matmul_integer_destroy": (i, [vp]),
+        "nnrh_quantize_linear": (i, [vp, sz, f, i, i, vp, vp]),
+        "nnrh_dequantize_linear": (i, [vp, i, sz, f, i, vp, vp]),
+        "nnrh_dynamic_quantize_workspace": (sz, []),
+        "nnrh_dynamic_quantize_linear": (i, [vp, sz, vp, vp, vp, vp, vp]),
+        "nnrh_qlinear_add": (i, [i, vp, vp, vp, sz, i, i, i, i, f, i, f, i, f, i, vp]),
+        "nnrh_maxpool_u8_nhwc": (i, [vp, vp] + [i] * 12 + [vp]),
+        "nnrh_nchw_to_nhwc_u8": (i, [vp, vp, i, i, i, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def check(rc: int) -> None:
+    if rc != NNRH_OK:
+        raise NnrHipError(rc, lib().nnrh_last_error().decode())
+
+
+def ptr(t) -> int:
+    """Device (or host) address of a torch tensor / numpy array / int."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    if hasattr(t, "ctypes"):
+        return t.ctypes.data
+    raise TypeError(type(t))
+
+
+def cur_stream() -> int:
+    import torch
+    return torch.cuda.current_stream().cuda_stream

@@ -1,0 +1,849 @@
+// nnrh_capi.cpp -- implementation of include/nnr_hip.h.
+//
+// Cold path (create): validate, choose the reference's kernel branch, pack
+// weights into the MFMA layout, precompute the requantize vectors with the
+// same float operations as QLinearConv_reshape.h:288-336, upload.
+// Hot path (run): at most a layout transform, an optional zero-point row sum
+// and one GEMM / depthwise launch on the caller's stream. No allocation.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "nnr_hip.h"
+#include "nnrh_elem.h"
+#include "nnrh_internal.h"
+
+using namespace nnrh;
+
+namespace {
+
+thread_local std::string g_err = "no error";
+
+int set_err(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+int hip_err(hipError_t e, const char* what) {
+    return set_err(NNRH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+#define HIP_TRY(expr, what)                       \
+    do {                                          \
+        hipError_t e__ = (expr);                  \
+        if (e__ != hipSuccess) return hip_err(e__, what); \
+    } while (0)
+
+inline hipStream_t S(void* s) { return (hipStream_t)s; }
+inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+template <typename T>
+int upload(T** dst, const T* src, size_t count) {
+    *dst = nullptr;
+    if (count == 0) return NNRH_OK;
+    void* p = nullptr;
+    HIP_TRY(hipMalloc(&p, sizeof(T) * count), "hipMalloc");
+    hipError_t e = hipMemcpy(p, src, sizeof(T) * count, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return hip_err(e, "hipMemcpy");
+    }
+    *dst = (T*)p;
+    return NNRH_OK;
+}
+void dfree(void* p) {
+    if (p) (void)hipFree(p);
+}
+
+// conv_shape.h:21-81 (explicit pads)
+int conv_out_dim(int in, int k, int d, int s, int pb, int pe) {
+    int ek = (k - 1) * d + 1;
+    return (int)floorf((float)(in + pb + pe - ek) / (float)s + 1.0f);
+}
+
+int pick_vec(int c_or_k, int stride, uintptr_t base) {
+    if (c_or_k % 16 == 0 && stride % 16 == 0 && (base & 15) == 0) return 16;
+    if (c_or_k % 8 == 0 && stride % 8 == 0 && (base & 7) == 0) return 8;
+    if (c_or_k % 4 == 0 && stride % 4 == 0 && (base & 3) == 0) return 4;
+    return 1;
+}
+int pick_tile(int N) { return N <= 64 ? TILE_256x64 : TILE_128x128; }
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+const char* nnrh_last_error(void) { return g_err.c_str(); }
+const char* nnrh_version(void) { return "nnr-mi355x 0.1 (gfx950)"; }
+
+int nnrh_device_count(int* count) {
+    if (!count) return set_err(NNRH_ERR_INVALID, "count is NULL");
+    HIP_TRY(hipGetDeviceCount(count), "hipGetDeviceCount");
+    return NNRH_OK;
+}
+int nnrh_set_device(int device) {
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    return NNRH_OK;
+}
+int nnrh_malloc(void** p, size_t bytes) {
+    if (!p) return set_err(NNRH_ERR_INVALID, "ptr is NULL");
+    *p = nullptr;
+    if (bytes == 0) return NNRH_OK;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e == hipErrorOutOfMemory) return set_err(NNRH_ERR_NOMEM, "hipMalloc(%zu): out of memory", bytes);
+    if (e != hipSuccess) return hip_err(e, "hipMalloc");
+    return NNRH_OK;
+}
+int nnrh_free(void* p) {
+    if (p) HIP_TRY(hipFree(p), "hipFree");
+    return NNRH_OK;
+}
+int nnrh_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream) {
+    if (bytes == 0) return NNRH_OK;
+    if (!dst || !src) return set_err(NNRH_ERR_INVALID, "memcpy: NULL pointer");
+    hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice
+                    : kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+    if (kind < 0 || kind > 2) return set_err(NNRH_ERR_INVALID, "memcpy: bad kind %d", kind);
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, k, S(stream)), "hipMemcpyAsync");
+    if (kind == 1) HIP_TRY(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
+    return NNRH_OK;
+}
+int nnrh_fill_u8(void* dst, uint8_t value, size_t bytes, void* stream) {
+    if (bytes && !dst) return set_err(NNRH_ERR_INVALID, "fill: NULL pointer");
+    HIP_TRY(launch_fill_u8(dst, value, (long long)bytes, S(stream)), "fill_u8");
+    return NNRH_OK;
+}
+int nnrh_stream_create(void** s) {
+    if (!s) return set_err(NNRH_ERR_INVALID, "stream is NULL");
+    hipStream_t st;
+    HIP_TRY(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
+    *s = (void*)st;
+    return NNRH_OK;
+}
+int nnrh_stream_destroy(void* s) {
+    if (s) HIP_TRY(hipStreamDestroy(S(s)), "hipStreamDestroy");
+    return NNRH_OK;
+}
+int nnrh_stream_synchronize(void* s) {
+    HIP_TRY(hipStreamSynchronize(S(s)), "hipStreamSynchronize");
+    return NNRH_OK;
+}
+int nnrh_device_synchronize(void) {
+    HIP_TRY(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    return NNRH_OK;
+}
+int nnrh_event_create(void** ev) {
+    if (!ev) return set_err(NNRH_ERR_INVALID, "event is NULL");
+    hipEvent_t e;
+    HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+    *ev = (void*)e;
+    return NNRH_OK;
+}
+int nnrh_event_destroy(void* ev) {
+    if (ev) HIP_TRY(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
+    return NNRH_OK;
+}
+int nnrh_event_record(void* ev, void* s) {
+    HIP_TRY(hipEventRecord((hipEvent_t)ev, S(s)), "hipEventRecord");
+    return NNRH_OK;
+}
+int nnrh_event_elapsed_ms(float* ms, void* a, void* b) {
+    if (!ms) return set_err(NNRH_ERR_INVALID, "ms is NULL");
+    HIP_TRY(hipEventSynchronize((hipEvent_t)b), "hipEventSynchronize");
+    HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b), "hipEventElapsedTime");
+    return NNRH_OK;
+}
+
+}  // extern "C"
+
+// ===========================================================================
+// QLinearConv
+
+namespace {
+
+bool conv_per_channel_zp(const nnrh_qconv_desc* d) {
+    // QLinearConv.cpp:136-153: an all-equal per-channel w_zp is per-tensor
+    if (d->w_zp_count <= 1) return false;
+    for (int i = 1; i < d->w_zp_count; ++i)
+        if (d->w_zp_host[i] != d->w_zp_host[0]) return true;
+    return false;
+}
+
+// First-match dispatch of QLinearConv::exec_simd_4d (QLinearConv.cpp:1337-1351)
+// on an x64 AVX-512 VNNI host, with the prepack preconditions of
+// QLinearConv_reshape.h:36-284.
+int conv_dispatch(const nnrh_qconv_desc* d) {
+    const bool u8 = d->act_dtype == NNRH_U8;
+    const bool pcz = conv_per_channel_zp(d);
+    const int wzp0 = d->w_zp_count > 0 ? d->w_zp_host[0] : 0;
+    const int Cg = d->C / d->group;
+    const bool is_dw = d->group == d->OC && Cg == 1;
+    const bool vnni_ok = u8 && !pcz;
+    const bool dil1 = d->dH == 1 && d->dW == 1;
+    // (1) exec_dw_int8_nhwc (QLinearConv.cpp:467-526)
+    if (vnni_ok && is_dw && d->y_nhwc) return NNRH_BR_DW;
+    // (2) exec_first_layer_int8 (QLinearConv.cpp:665-700; reshape :233-256)
+    if (vnni_ok && d->group == 1 && dil1 && Cg <= 4 && d->kH >= 3 && d->OC >= 16 && wzp0 == 0 &&
+        d->C <= 4 && d->pad_t == d->pad_b && d->pad_l == d->pad_r && !d->x_nhwc)
+        return NNRH_BR_FIRST;
+    // (3) exec_direct_int8 (QLinearConv.cpp:579-652)
+    if (vnni_ok && d->group == 1 && dil1 && wzp0 == 0 && d->oH * d->oW <= 256 && !d->y_nhwc)
+        return NNRH_BR_DIRECT;
+    // (4) exec_packed_nr48, NR16 predicate (QLinearConv.cpp:750-759)
+    if (vnni_ok && d->group == 1) {
+        if (d->kH == 3 && d->kW == 3 && d->sH == 1 && d->sW == 1 && dil1 && d->pad_t == 1 &&
+            d->pad_l == 1 && d->C >= 64 && d->OC >= 64 && (d->OC % 16) == 0 && wzp0 == 0 &&
+            d->y_nhwc)
+            return NNRH_BR_NR16;
+        return NNRH_BR_PACKED;
+    }
+    // (6) exec_vnni_im2col (QLinearConv.cpp:1010-1196)
+    if (vnni_ok) return (d->sH == 1 && d->sW == 1) ? NNRH_BR_IM2COL_S1 : NNRH_BR_IM2COL;
+    // (7) exec_float_fallback (QLinearConv.cpp:1205-1335)
+    return NNRH_BR_FLOAT;
+}
+
+int validate_conv(const nnrh_qconv_desc* d) {
+    if (!d) return set_err(NNRH_ERR_INVALID, "qconv: desc is NULL");
+    if (d->N <= 0 || d->C <= 0 || d->H <= 0 || d->W <= 0 || d->OC <= 0 || d->kH <= 0 ||
+        d->kW <= 0 || d->group <= 0)
+        return set_err(NNRH_ERR_INVALID, "qconv: non-positive dimension");
+    if (d->C % d->group || d->OC % d->group)
+        return set_err(NNRH_ERR_INVALID, "qconv: channels %d/%d not divisible by group %d", d->C,
+                       d->OC, d->group);
+    if (d->sH <= 0 || d->sW <= 0 || d->dH <= 0 || d->dW <= 0 || d->pad_t < 0 || d->pad_l < 0 ||
+        d->pad_b < 0 || d->pad_r < 0)
+        return set_err(NNRH_ERR_INVALID, "qconv: bad stride/dilation/pad");
+    int oh = conv_out_dim(d->H, d->kH, d->dH, d->sH, d->pad_t, d->pad_b);
+    int ow = conv_out_dim(d->W, d->kW, d->dW, d->sW, d->pad_l, d->pad_r);
+    if (oh != d->oH || ow != d->oW || oh <= 0 || ow <= 0)
+        return set_err(NNRH_ERR_INVALID, "qconv: output %dx%d, expected %dx%d", d->oH, d->oW, oh, ow);
+    if (d->act_dtype != NNRH_U8 && d->act_dtype != NNRH_S8)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qconv: activation dtype %d", d->act_dtype);
+    if (!d->w_host || !d->w_scale_host)
+        return set_err(NNRH_ERR_INVALID, "qconv: weights / w_scale missing");
+    if (d->w_scale_count != 1 && d->w_scale_count != d->OC)
+        return set_err(NNRH_ERR_INVALID, "qconv: w_scale count %d (OC %d)", d->w_scale_count, d->OC);
+    if (d->w_zp_count != 0 && d->w_zp_count != 1 && d->w_zp_count != d->OC)
+        return set_err(NNRH_ERR_INVALID, "qconv: w_zp count %d (OC %d)", d->w_zp_count, d->OC);
+    if (d->w_zp_count > 0 && !d->w_zp_host) return set_err(NNRH_ERR_INVALID, "qconv: w_zp NULL");
+    if (!(d->y_scale > 0.0f) || !(d->x_scale > 0.0f))
+        return set_err(NNRH_ERR_INVALID, "qconv: scales must be positive");
+    long long M = (long long)d->N * d->oH * d->oW;
+    if (M >= (1LL << 31) || (long long)d->N * d->H * d->W * d->C >= (1LL << 40))
+        return set_err(NNRH_ERR_UNSUPPORTED, "qconv: tensor too large");
+    if (d->kH * d->kW > 64 * 64) return set_err(NNRH_ERR_UNSUPPORTED, "qconv: kernel too large");
+    return NNRH_OK;
+}
+
+}  // namespace
+
+struct nnrh_qconv {
+    nnrh_qconv_desc d{};
+    int branch = 0;
+    bool use_dw = false;         // depthwise VALU kernel
+    int transform = 0;           // 0 none, 1 NCHW->NHWC, 2 NCHW->NHWC padded to 4 ch
+    int Cx = 0;                  // channels of the tensor the kernel reads
+    int groups = 1;
+    bool need_rowsum = false;
+    int w_zp_scalar = 0;
+    int dw_L = 0, dw_tail = 0, dw_tile_h = 0;
+    float inv_y = 0.f;
+    int tile = 0, vec = 16;
+    GemmArgs g{};
+    // device buffers
+    int8_t* wpack = nullptr;
+    int32_t* colsum = nullptr;
+    int32_t* beta_col = nullptr;
+    float* os = nullptr;
+    float* cs = nullptr;
+    float* bf = nullptr;
+    int32_t* bias = nullptr;
+    uint8_t* xs = nullptr;
+    int32_t* rowsum = nullptr;
+    ~nnrh_qconv() {
+        dfree(wpack); dfree(colsum); dfree(beta_col); dfree(os); dfree(cs); dfree(bf);
+        dfree(bias); dfree(xs); dfree(rowsum);
+    }
+};
+
+extern "C" int nnrh_qconv_dispatch(const nnrh_qconv_desc* d, int* branch) {
+    int rc = validate_conv(d);
+    if (rc) return rc;
+    if (!branch) return set_err(NNRH_ERR_INVALID, "branch is NULL");
+    *branch = conv_dispatch(d);
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
+    if (!out) return set_err(NNRH_ERR_INVALID, "qconv: handle is NULL");
+    *out = nullptr;
+    int rc = validate_conv(d);
+    if (rc) return rc;
+    nnrh_qconv* h = new (std::nothrow) nnrh_qconv();
+    if (!h) return set_err(NNRH_ERR_NOMEM, "qconv: host allocation");
+    h->d = *d;
+    h->d.w_host = nullptr; h->d.w_scale_host = nullptr; h->d.w_zp_host = nullptr; h->d.bias_host = nullptr;
+    const int OC = d->OC, G = d->group, Cg = d->C / G, OCg = OC / G;
+    const int sp = d->oH * d->oW;
+    const bool u8 = d->act_dtype == NNRH_U8;
+    const int lo = u8 ? 0 : -128, hi = u8 ? 255 : 127;
+    const int qmin = d->post_fn ? std::max(lo, d->y_zp) : lo;     // QLinearConv.cpp:419
+    const bool pcz = conv_per_channel_zp(d);
+    h->w_zp_scalar = d->w_zp_count > 0 ? d->w_zp_host[0] : 0;
+    h->branch = conv_dispatch(d);
+    h->groups = G;
+
+    // ---- requantize vectors (QLinearConv_reshape.h:288-321), same float ops
+    const float inv_y = 1.0f / d->y_scale;
+    h->inv_y = inv_y;
+    std::vector<float> cs(OC), os(OC), bf(OC);
+    for (int oc = 0; oc < OC; ++oc) {
+        float ws = d->w_scale_count > 1 ? d->w_scale_host[oc] : d->w_scale_host[0];
+        cs[oc] = d->x_scale * ws;
+        os[oc] = cs[oc] * inv_y;
+        bf[oc] = d->bias_host ? (float)d->bias_host[oc] * cs[oc] : 0.0f;
+    }
+    std::vector<int32_t> bias(OC, 0);
+    if (d->bias_host) std::copy(d->bias_host, d->bias_host + OC, bias.begin());
+
+    // tiled im2col tile height (QLinearConv.cpp:1082-1090)
+    int tile_h = d->oH;
+    {
+        const size_t TILE_BYTES = 256 * 1024;
+        size_t CHW = (size_t)Cg * d->kH * d->kW;
+        if (CHW * (size_t)sp > TILE_BYTES) {
+            long th = (long)(TILE_BYTES / (CHW * (size_t)d->oW));
+            tile_h = (int)std::max(1L, th);
+            tile_h = std::min(tile_h, d->oH);
+        }
+    }
+
+    const int br = h->branch;
+    const bool is_dw = (G == OC && Cg == 1);
+    h->use_dw = is_dw && u8 && !pcz &&
+                (br == NNRH_BR_DW || br == NNRH_BR_IM2COL_S1 || br == NNRH_BR_IM2COL);
+
+    auto fail = [&](int code) { delete h; return code; };
+
+    if ((rc = upload(&h->cs, cs.data(), OC))) return fail(rc);
+    if ((rc = upload(&h->bf, bf.data(), OC))) return fail(rc);
+
+    if (h->use_dw) {
+        // repack_depthwise_weights: [kH*kW][C]
+        std::vector<int8_t> wdw((size_t)d->kH * d->kW * OC);
+        for (int c = 0; c < OC; ++c)
+            for (int t = 0; t < d->kH * d->kW; ++t) wdw[(size_t)t * OC + c] = d->w_host[(size_t)c * d->kH * d->kW + t];
+        if ((rc = upload(&h->wpack, wdw.data(), wdw.size()))) return fail(rc);
+        h->transform = d->x_nhwc ? 0 : 1;
+        h->Cx = d->C;
+        h->dw_L = (br == NNRH_BR_IM2COL) ? qmin : lo;
+        h->dw_tail = (br == NNRH_BR_IM2COL) ? TAIL_TILED : TAIL_NONE;
+        h->dw_tile_h = tile_h;
+    } else {
+        // ---- GEMM plan: groups on blockIdx.z, K order (kh, kw, c)
+        const bool first = br == NNRH_BR_FIRST;
+        const int Cgp = first ? 4 : Cg;
+        const int K = d->kH * d->kW * Cgp;
+        const int Kp = round_up(K, 64);
+        const int Np = round_up(OCg, 64);
+        std::vector<int8_t> wp((size_t)G * Np * Kp, 0);
+        std::vector<int32_t> colsum(OC, 0);
+        for (int g = 0; g < G; ++g)
+            for (int n = 0; n < OCg; ++n) {
+                const int oc = g * OCg + n;
+                int8_t* row = wp.data() + ((size_t)g * Np + packed_row_of_col(n)) * Kp;
+                int32_t s = 0;
+                for (int c = 0; c < Cg; ++c)
+                    for (int a = 0; a < d->kH; ++a)
+                        for (int b = 0; b < d->kW; ++b) {
+                            int8_t v = d->w_host[(((size_t)oc * Cg + c) * d->kH + a) * d->kW + b];
+                            row[(a * d->kW + b) * Cgp + c] = v;
+                            s += v;
+                        }
+                colsum[oc] = s;
+            }
+        if ((rc = upload(&h->wpack, wp.data(), wp.size()))) return fail(rc);
+        if ((rc = upload(&h->colsum, colsum.data(), colsum.size()))) return fail(rc);
+        if ((rc = upload(&h->os, os.data(), OC))) return fail(rc);
+        if ((rc = upload(&h->bias, bias.data(), OC))) return fail(rc);
+        // zero-point row term: any nonzero w_zp
+        std::vector<int32_t> betac(OC);
+        bool any_wzp = false;
+        for (int oc = 0; oc < OC; ++oc) {
+            betac[oc] = pcz ? d->w_zp_host[oc] : h->w_zp_scalar;
+            any_wzp |= betac[oc] != 0;
+        }
+        h->need_rowsum = any_wzp;
+        if (any_wzp && (rc = upload(&h->beta_col, betac.data(), OC))) return fail(rc);
+
+        if (first) { h->transform = 2; h->Cx = 4; }
+        else { h->transform = d->x_nhwc ? 0 : 1; h->Cx = d->C; }
+
+        GemmArgs& g = h->g;
+        g.a_xor = u8 ? 0x80 : 0;
+        g.M = d->N * sp;
+        g.N = OCg;
+        g.K = K;
+        g.Kp = Kp;
+        g.H = d->H; g.W = d->W; g.C = Cgp; g.Cs = h->Cx;
+        g.oH = d->oH; g.oW = d->oW; g.kH = d->kH; g.kW = d->kW;
+        g.sH = d->sH; g.sW = d->sW; g.dH = d->dH; g.dW = d->dW;
+        g.pad_t = d->pad_t; g.pad_l = d->pad_l;
+        g.pad_byte = d->x_zp & 0xff;
+        g.a_bstride = first ? 0 : Cg;   // group channel offset
+        g.b = h->wpack;
+        g.b_bstride = (long long)Np * Kp;
+        g.Np = Np;
+        g.colsum = h->colsum;
+        g.a_sub = u8 ? 128 : 0;
+        g.alpha = d->x_zp - g.a_sub;
+        g.rowsum_bstride = (long long)g.M;
+        g.beta_col = h->beta_col;
+        g.beta = 0;
+        g.param_bstride = OCg;
+        g.os = h->os; g.bias = h->bias; g.cs = h->cs; g.bf = h->bf;
+        g.inv_y = inv_y;
+        g.y_zp = d->y_zp;
+        g.lo = lo; g.hi = hi;
+        g.bprime_from = OCg;
+        g.tile_h = tile_h;
+        g.y_type = u8 ? 0 : 1;
+        g.y_nchw = d->y_nhwc ? 0 : 1;
+        g.ldy = OC;
+        g.y_bstride = d->y_nhwc ? OCg : (long long)OCg * sp;
+        switch (br) {
+        case NNRH_BR_FIRST:
+            g.epi = EPI_RQC; g.L = qmin; g.tail = d->y_nhwc ? TAIL_NONE : TAIL_OW; break;
+        case NNRH_BR_DIRECT:
+        case NNRH_BR_FLOAT:
+            g.epi = EPI_RQA; g.L = qmin; g.tail = TAIL_SPATIAL; break;
+        case NNRH_BR_PACKED:
+            g.epi = EPI_RQB;
+            // RQ-B' on the third sub-panel of a partial NR48 block
+            g.bprime_from = (OCg % 48 > 32) ? OCg - OCg % 48 + 32 : OCg;
+            break;
+        case NNRH_BR_NR16:
+            g.epi = EPI_RQB; break;
+        case NNRH_BR_IM2COL_S1:
+            g.epi = EPI_RQA; g.L = lo; g.tail = TAIL_NONE; break;
+        case NNRH_BR_IM2COL:
+            g.epi = EPI_RQA; g.L = qmin; g.tail = TAIL_TILED; break;
+        default:
+            return fail(set_err(NNRH_ERR_UNSUPPORTED, "qconv: branch %d", br));
+        }
+        h->tile = pick_tile(OCg);
+        h->vec = (h->Cx % 4 == 0 && Cgp % 4 == 0) ? pick_vec(Cgp, h->Cx, 0) : 1;
+        if (G > 1 && (Cg % h->vec)) h->vec = 1;
+    }
+    // scratch: transformed input and row sums
+    if (h->transform) {
+        size_t bytes = (size_t)d->N * d->H * d->W * h->Cx;
+        if ((rc = nnrh_malloc((void**)&h->xs, bytes))) return fail(rc);
+    }
+    if (h->need_rowsum) {
+        if ((rc = nnrh_malloc((void**)&h->rowsum, sizeof(int32_t) * (size_t)d->N * sp * G)))
+            return fail(rc);
+        h->g.rowsum = h->rowsum;
+    }
+    *out = h;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qconv_branch(nnrh_qconv_t h, int* branch) {
+    if (!h || !branch) return set_err(NNRH_ERR_INVALID, "qconv_branch: NULL");
+    *branch = h->branch;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stream) {
+    if (!h || !x || !y) return set_err(NNRH_ERR_INVALID, "qconv_run: NULL argument");
+    const nnrh_qconv_desc& d = h->d;
+    hipStream_t s = S(stream);
+    const uint8_t* src = (const uint8_t*)x;
+    if (h->transform) {
+        HIP_TRY(launch_nchw_to_nhwc_u8(src, h->xs, d.N, d.C, d.H * d.W, h->Cx,
+                                       (uint8_t)(d.x_zp & 0xff), s),
+                "nchw_to_nhwc");
+        src = h->xs;
+    }
+    if (h->use_dw) {
+        HIP_TRY(launch_depthwise(src, h->wpack, (uint8_t*)y, h->cs, h->bf, d.N, d.C, d.H, d.W, d.oH,
+                                 d.oW, d.kH, d.kW, d.sH, d.sW, d.dH, d.dW, d.pad_t, d.pad_l, d.x_zp,
+                                 h->w_zp_scalar, h->inv_y, d.y_zp, h->dw_L, d.act_dtype == NNRH_U8 ? 255 : 127,
+                                 d.act_dtype == NNRH_S8, d.y_nhwc ? 0 : 1, h->dw_tail, h->dw_tile_h, s),
+                "depthwise");
+        return NNRH_OK;
+    }
+    if (h->need_rowsum) {
+        const int Cg = h->g.C;
+        HIP_TRY(launch_rowsum_conv(src, d.N, d.H, d.W, h->Cx, Cg, h->groups, d.oH, d.oW, d.kH, d.kW,
+                                   d.sH, d.sW, d.dH, d.dW, d.pad_t, d.pad_l, d.act_dtype == NNRH_S8,
+                                   d.x_zp, h->rowsum, s),
+                "rowsum_conv");
+    }
+    GemmArgs g = h->g;
+    g.a = src;
+    g.y = y;
+    int vec = h->vec;
+    if (vec > 1 && ((uintptr_t)src & (vec - 1))) vec = 1;
+    HIP_TRY(launch_qgemm(g, h->groups, h->tile, vec, s), "qgemm");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qconv_destroy(nnrh_qconv_t h) {
+    delete h;
+    return NNRH_OK;
+}
+
+// ===========================================================================
+// QLinearMatMul (constant B)
+
+namespace {
+uint16_t f32_to_f16(float v) {   // src/nnrconf.h:147-173 rounding
+    uint32_t u; memcpy(&u, &v, 4);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    int e = (int)((u >> 23) & 0xffu) - 127;
+    uint32_t mant = u & 0x7fffffu;
+    if (e > 15) return (uint16_t)(sign | 0x7c00u);
+    if (e >= -14) {
+        uint32_t rb = mant & 0x1fffu;
+        uint16_t y = (uint16_t)(sign | ((uint16_t)(e + 15) << 10) | (uint16_t)(mant >> 13));
+        if (rb > 0x1000u || (rb == 0x1000u && (y & 1u))) y++;
+        return y;
+    }
+    if (e >= -24) {
+        mant |= 0x800000u;
+        int sh = -e - 14 + 13;
+        uint32_t rb = mant & ((1u << sh) - 1u);
+        uint32_t half = 1u << (sh - 1);
+        uint16_t y = (uint16_t)(sign | (uint16_t)(mant >> sh));
+        if (rb > half || (rb == half && (y & 1u))) y++;
+        return y;
+    }
+    return sign;
+}
+float f16_to_f32(uint16_t v) {   // src/nnrconf.h:175-199
+    uint32_t sign = (uint32_t)(v & 0x8000u) << 16, e = (v >> 10) & 0x1fu, mant = v & 0x3ffu, u;
+    if (e == 0) {
+        if (mant == 0) u = sign;
+        else {
+            int ee = 0;
+            while (!(mant & 0x400u)) { mant <<= 1; ee--; }
+            mant &= 0x3ffu; ee++;
+            u = sign | ((uint32_t)(ee + 127 - 15) << 23) | (mant << 13);
+        }
+    } else if (e == 31) u = sign | 0x7f800000u | (mant << 13);
+    else u = sign | ((e + 127 - 15) << 23) | (mant << 13);
+    float f; memcpy(&f, &u, 4);
+    return f;
+}
+int ld_zp(const void* p, int dt) {
+    if (!p) return 0;
+    return dt == NNRH_U8 ? (int)*(const uint8_t*)p : (int)*(const int8_t*)p;
+}
+}  // namespace
+
+struct nnrh_qmatmul {
+    nnrh_qmatmul_desc d{};
+    GemmArgs g{};
+    int8_t* wpack = nullptr;
+    int32_t* colsum = nullptr;
+    int32_t* rowsum = nullptr;
+    int rowsum_cap = 0;     // batches the rowsum buffer holds
+    int a_zp = 0, b_beta = 0;
+    float b_scale = 0.f, y_scale = 0.f;
+    ~nnrh_qmatmul() { dfree(wpack); dfree(colsum); dfree(rowsum); }
+};
+
+extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc* d) {
+    if (!out || !d) return set_err(NNRH_ERR_INVALID, "qmatmul: NULL argument");
+    *out = nullptr;
+    if (d->m <= 0 || d->n <= 0 || d->k <= 0) return set_err(NNRH_ERR_INVALID, "qmatmul: bad m/n/k");
+    if ((d->a_dtype != NNRH_U8 && d->a_dtype != NNRH_S8) || (d->b_dtype != NNRH_U8 && d->b_dtype != NNRH_S8) ||
+        (d->y_dtype != NNRH_U8 && d->y_dtype != NNRH_S8))
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul: dtypes");
+    if (d->scale_dtype != NNRH_F32 && d->scale_dtype != NNRH_F16)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul: scale dtype");
+    if (!d->b_host || !d->a_scale_host || !d->b_scale_host || !d->y_scale_host)
+        return set_err(NNRH_ERR_INVALID, "qmatmul: missing B or scales");
+    nnrh_qmatmul* h = new (std::nothrow) nnrh_qmatmul();
+    if (!h) return set_err(NNRH_ERR_NOMEM, "qmatmul: host allocation");
+    auto fail = [&](int code) { delete h; return code; };
+    h->d = *d;
+    const int m = d->m, n = d->n, k = d->k;
+    const int Kp = round_up(k, 64), Np = round_up(n, 64);
+    const bool bu8 = d->b_dtype == NNRH_U8;
+    std::vector<int8_t> wp((size_t)Np * Kp, 0);
+    std::vector<int32_t> colsum(n, 0);
+    const uint8_t* braw = (const uint8_t*)d->b_host;
+    for (int j = 0; j < n; ++j) {
+        int8_t* row = wp.data() + (size_t)packed_row_of_col(j) * Kp;
+        int32_t s = 0;
+        for (int i = 0; i < k; ++i) {
+            int8_t v = (int8_t)(braw[(size_t)i * n + j] ^ (bu8 ? 0x80 : 0));
+            row[i] = v;
+            s += v;
+        }
+        colsum[j] = s;
+    }
+    int rc;
+    if ((rc = upload(&h->wpack, wp.data(), wp.size()))) return fail(rc);
+    if ((rc = upload(&h->colsum, colsum.data(), colsum.size()))) return fail(rc);
+    const bool au8 = d->a_dtype == NNRH_U8;
+    h->a_zp = ld_zp(d->a_zp_host, d->a_dtype);
+    const int b_zp = ld_zp(d->b_zp_host, d->b_dtype);   // b_zp[0] only (QLinearMatMul.cpp:119)
+    h->b_beta = b_zp - (bu8 ? 128 : 0);
+    // combined scale (QLinearMatMul.cpp:124-135)
+    float cm;
+    if (d->scale_dtype == NNRH_F16) {
+        float fa = f16_to_f32(*(const uint16_t*)d->a_scale_host);
+        float fb = f16_to_f32(*(const uint16_t*)d->b_scale_host);
+        float fy = f16_to_f32(*(const uint16_t*)d->y_scale_host);
+        uint16_t t = f32_to_f16(fa * fb);
+        t = f32_to_f16(f16_to_f32(t) / fy);
+        cm = f16_to_f32(t);
+        h->b_scale = fb; h->y_scale = fy;
+    } else {
+        float as = *(const float*)d->a_scale_host, bs = *(const float*)d->b_scale_host,
+              ys = *(const float*)d->y_scale_host;
+        float t = as * bs;
+        cm = t / ys;
+        h->b_scale = bs; h->y_scale = ys;
+    }
+    GemmArgs& g = h->g;
+    g.a_xor = au8 ? 0x80 : 0;
+    g.M = m; g.N = n; g.K = k; g.Kp = Kp;
+    g.lda = k;
+    g.b = h->wpack; g.b_bstride = 0; g.Np = Np;
+    g.colsum = h->colsum;
+    g.a_sub = au8 ? 128 : 0;
+    g.alpha = h->a_zp - g.a_sub;
+    g.beta = h->b_beta;
+    g.param_bstride = 0;
+    g.rowsum_bstride = m;
+    g.epi = EPI_RQD;
+    g.cm = cm;
+    g.cm_b = h->b_scale; g.cm_y = h->y_scale;
+    g.y_zp = ld_zp(d->y_zp_host, d->y_dtype);
+    g.lo = d->y_dtype == NNRH_U8 ? 0 : -128;
+    g.hi = d->y_dtype == NNRH_U8 ? 255 : 127;
+    g.y_type = d->y_dtype == NNRH_U8 ? 0 : 1;
+    g.ldy = n;
+    g.y_bstride = (long long)m * n;
+    g.bprime_from = n;
+    *out = h;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a, long long a_bstride, void* y, int batch,
+                                const float* a_scale_dev, const void* a_zp_dev, void* stream) {
+    if (!h || !a || !y) return set_err(NNRH_ERR_INVALID, "qmatmul_run: NULL argument");
+    if (batch <= 0) return set_err(NNRH_ERR_INVALID, "qmatmul_run: batch %d", batch);
+    if (a_scale_dev && h->d.scale_dtype != NNRH_F32)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_run: device a_scale needs float32 scales");
+    hipStream_t s = S(stream);
+    GemmArgs g = h->g;
+    g.a = (const uint8_t*)a;
+    g.a_bstride = a_bstride;
+    g.y = y;
+    g.alpha_zp_dev = a_zp_dev;
+    g.cm_a_scale_dev = a_scale_dev;
+    if (g.beta != 0) {
+        if (h->rowsum_cap < batch) {
+            dfree(h->rowsum);
+            h->rowsum = nullptr;
+            h->rowsum_cap = 0;
+            int rc = nnrh_malloc((void**)&h->rowsum, sizeof(int32_t) * (size_t)batch * h->d.m);
+            if (rc) return rc;
+            h->rowsum_cap = batch;
+        }
+        HIP_TRY(launch_rowsum_dense((const uint8_t*)a, g.lda, a_bstride, g.M, g.K, g.a_xor == 0,
+                                    h->a_zp, a_zp_dev, h->rowsum, batch, s),
+                "rowsum_dense");
+        g.rowsum = h->rowsum;
+    }
+    int vec = pick_vec(g.K, (int)g.lda, (uintptr_t)a);
+    if (a_bstride % vec) vec = 1;
+    HIP_TRY(launch_qgemm(g, batch, pick_tile(g.N), vec, s), "qgemm");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qmatmul_destroy(nnrh_qmatmul_t h) {
+    delete h;
+    return NNRH_OK;
+}
+
+// ===========================================================================
+// MatMulInteger (dynamic A and B)
+
+struct nnrh_matmul_integer {
+    int m = 0, n = 0, k = 0, a_dtype = 0, b_dtype = 0, max_batch = 0, Kp = 0, Np = 0;
+    int8_t* bpack = nullptr;
+    int32_t* colsum = nullptr;
+    int32_t* rowsum = nullptr;
+    ~nnrh_matmul_integer() { dfree(bpack); dfree(colsum); dfree(rowsum); }
+};
+
+extern "C" int nnrh_matmul_integer_create(nnrh_matmul_integer_t* out, int m, int n, int k, int a_dtype,
+                                          int b_dtype, int max_batch) {
+    if (!out) return set_err(NNRH_ERR_INVALID, "matmul_integer: handle NULL");
+    *out = nullptr;
+    if (m <= 0 || n <= 0 || k <= 0 || max_batch <= 0)
+        return set_err(NNRH_ERR_INVALID, "matmul_integer: bad shape");
+    if ((a_dtype != NNRH_U8 && a_dtype != NNRH_S8) || (b_dtype != NNRH_U8 && b_dtype != NNRH_S8))
+        return set_err(NNRH_ERR_UNSUPPORTED, "matmul_integer: dtypes");
+    nnrh_matmul_integer* h = new (std::nothrow) nnrh_matmul_integer();
+    if (!h) return set_err(NNRH_ERR_NOMEM, "matmul_integer: host allocation");
+    h->m = m; h->n = n; h->k = k; h->a_dtype = a_dtype; h->b_dtype = b_dtype; h->max_batch = max_batch;
+    h->Kp = round_up(k, 64); h->Np = round_up(n, 64);
+    int rc;
+    if ((rc = nnrh_malloc((void**)&h->bpack, (size_t)max_batch * h->Np * h->Kp)) ||
+        (rc = nnrh_malloc((void**)&h->colsum, sizeof(int32_t) * (size_t)max_batch * h->Np)) ||
+        (rc = nnrh_malloc((void**)&h->rowsum, sizeof(int32_t) * (size_t)max_batch * m))) {
+        delete h;
+        return rc;
+    }
+    *out = h;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_matmul_integer_run(nnrh_matmul_integer_t h, const void* a, long long a_bstride,
+                                       const void* b, long long b_bstride, int a_zp, int b_zp,
+                                       int32_t* y, int batch, void* stream) {
+    if (!h || !a || !b || !y) return set_err(NNRH_ERR_INVALID, "matmul_integer_run: NULL argument");
+    if (batch <= 0 || batch > h->max_batch)
+        return set_err(NNRH_ERR_INVALID, "matmul_integer_run: batch %d (max %d)", batch, h->max_batch);
+    hipStream_t s = S(stream);
+    const bool au8 = h->a_dtype == NNRH_U8, bu8 = h->b_dtype == NNRH_U8;
+    const int nb_b = b_bstride == 0 ? 1 : batch;
+    HIP_TRY(launch_pack_b_dense(b, b_bstride, h->k, h->n, h->Kp, h->Np, bu8 ? 0x80 : 0, h->bpack,
+                                (long long)h->Np * h->Kp, h->colsum, h->Np, nb_b, s),
+            "pack_b");
+    GemmArgs g{};
+    g.a = (const uint8_t*)a;
+    g.lda = h->k;
+    g.a_bstride = a_bstride;
+    g.a_xor = au8 ? 0x80 : 0;
+    g.M = h->m; g.N = h->n; g.K = h->k; g.Kp = h->Kp;
+    g.b = h->bpack;
+    g.b_bstride = b_bstride == 0 ? 0 : (long long)h->Np * h->Kp;
+    g.Np = h->Np;
+    g.colsum = h->colsum;
+    g.param_bstride = b_bstride == 0 ? 0 : h->Np;
+    g.a_sub = au8 ? 128 : 0;
+    g.alpha = a_zp - g.a_sub;
+    g.beta = b_zp - (bu8 ? 128 : 0);
+    if (g.beta != 0) {
+        HIP_TRY(launch_rowsum_dense((const uint8_t*)a, g.lda, a_bstride, h->m, h->k, !au8, a_zp, nullptr,
+                                    h->rowsum, batch, s),
+                "rowsum_dense");
+        g.rowsum = h->rowsum;
+        g.rowsum_bstride = h->m;
+    }
+    g.epi = EPI_I32;
+    g.y = y;
+    g.ldy = h->n;
+    g.y_bstride = (long long)h->m * h->n;
+    g.y_type = 2;
+    g.bprime_from = h->n;
+    int vec = pick_vec(h->k, h->k, (uintptr_t)a);
+    if (a_bstride % vec) vec = 1;
+    HIP_TRY(launch_qgemm(g, batch, pick_tile(h->n), vec, s), "qgemm");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_matmul_integer_destroy(nnrh_matmul_integer_t h) {
+    delete h;
+    return NNRH_OK;
+}
+
+// ===========================================================================
+// element-wise ops
+
+extern "C" int nnrh_quantize_linear(const float* x, size_t n, float scale, int zp, int y_dtype, void* y,
+                                    void* stream) {
+    if (n && (!x || !y)) return set_err(NNRH_ERR_INVALID, "quantize: NULL");
+    if (y_dtype != NNRH_U8 && y_dtype != NNRH_S8) return set_err(NNRH_ERR_UNSUPPORTED, "quantize: dtype");
+    HIP_TRY(launch_quantize(x, (long long)n, scale, zp, y_dtype == NNRH_U8 ? 0 : 1, y, S(stream)), "quantize");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_dequantize_linear(const void* x, int x_dtype, size_t n, float scale, int zp, float* y,
+                                      void* stream) {
+    if (n && (!x || !y)) return set_err(NNRH_ERR_INVALID, "dequantize: NULL");
+    int dt = x_dtype == NNRH_U8 ? 0 : x_dtype == NNRH_S8 ? 1 : x_dtype == NNRH_I32 ? 2 : -1;
+    if (dt < 0) return set_err(NNRH_ERR_UNSUPPORTED, "dequantize: dtype");
+    HIP_TRY(launch_dequantize(x, (long long)n, dt, scale, zp, y, S(stream)), "dequantize");
+    return NNRH_OK;
+}
+
+extern "C" size_t nnrh_dynamic_quantize_workspace(void) { return dynamic_quantize_workspace(); }
+
+extern "C" int nnrh_dynamic_quantize_linear(const float* x, size_t n, uint8_t* y, float* y_scale,
+                                            uint8_t* y_zp, void* ws, void* stream) {
+    if (!y_scale || !y_zp || !ws || (n && (!x || !y)))
+        return set_err(NNRH_ERR_INVALID, "dynamic_quantize: NULL");
+    HIP_TRY(launch_dynamic_quantize(x, (long long)n, y, y_scale, y_zp, ws, S(stream)), "dynamic_quantize");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qlinear_add(int kind, const void* a, const void* b, void* y, size_t n, int C, int HW,
+                                int y_nhwc, int dtype, float a_scale, int a_zp, float b_scale, int b_zp,
+                                float y_scale, int y_zp, void* stream) {
+    if (n && (!a || !b || !y)) return set_err(NNRH_ERR_INVALID, "qlinear_add: NULL");
+    if (dtype != NNRH_U8 && dtype != NNRH_S8) return set_err(NNRH_ERR_UNSUPPORTED, "qlinear_add: dtype");
+    if (kind < 0 || kind > 3) return set_err(NNRH_ERR_INVALID, "qlinear_add: kind %d", kind);
+    if (kind == 3 && (C <= 0 || HW <= 0 || n % ((size_t)C * HW)))
+        return set_err(NNRH_ERR_INVALID, "qlinear_add: per-channel shape");
+    QAddArgs p{};
+    p.kind = kind; p.a = a; p.b = b; p.y = y; p.n = (long long)n;
+    p.C = C; p.HW = HW; p.y_nhwc = y_nhwc; p.dt = dtype == NNRH_U8 ? 0 : 1;
+    p.sa = a_scale / y_scale;
+    p.sb = b_scale / y_scale;
+    {   // QLinearAdd.cpp:66-67 (no contraction)
+        float t1 = p.sa * (float)a_zp, t2 = p.sb * (float)b_zp;
+        p.fixed = (float)y_zp - (t1 + t2);
+    }
+    p.a_zp = a_zp; p.b_zp = b_zp; p.y_zp = y_zp;
+    p.lo = dtype == NNRH_U8 ? 0 : -128;
+    p.hi = dtype == NNRH_U8 ? 255 : 127;
+    if (kind == 1 || kind == 2) {
+        // scalar operand value is read on the host side by the reference
+        // (QLinearAdd.cpp:109,115); here it is fetched from the device.
+        const void* sc = kind == 1 ? b : a;
+        uint8_t raw = 0;
+        HIP_TRY(hipMemcpyAsync(&raw, sc, 1, hipMemcpyDeviceToHost, S(stream)), "hipMemcpyAsync");
+        HIP_TRY(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
+        int v = dtype == NNRH_U8 ? (int)raw : (int)(int8_t)raw;
+        p.cval = kind == 1 ? p.sb * (float)(v - b_zp) : p.sa * (float)(v - a_zp);
+    }
+    HIP_TRY(launch_qadd(p, S(stream)), "qlinear_add");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH, int iW, int oH,
+                                    int oW, int kH, int kW, int sH, int sW, int pH, int pW, void* stream) {
+    if (!x || !y) return set_err(NNRH_ERR_INVALID, "maxpool: NULL");
+    if (N <= 0 || C <= 0 || oH <= 0 || oW <= 0 || kH <= 0 || kW <= 0 || sH <= 0 || sW <= 0)
+        return set_err(NNRH_ERR_INVALID, "maxpool: bad shape");
+    HIP_TRY(launch_maxpool_u8_nhwc(x, y, N, C, iH, iW, oH, oW, kH, kW, sH, sW, pH, pW, S(stream)), "maxpool");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C, int HW, void* stream) {
+    if (!x || !y) return set_err(NNRH_ERR_INVALID, "nchw_to_nhwc: NULL");
+    HIP_TRY(launch_nchw_to_nhwc_u8(x, y, N, C, HW, C, 0, S(stream)), "nchw_to_nhwc");
+    return NNRH_OK;
+}

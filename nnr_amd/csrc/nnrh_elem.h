@@ -1,0 +1,37 @@
+// nnrh_elem.h -- launchers of the memory-bound int8 kernels (nnrh_elem.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace nnrh {
+
+struct QAddArgs {
+    int kind;            // 0 same shape, 1 B scalar, 2 A scalar, 3 per-channel B[C]
+    const void* a;
+    const void* b;
+    void* y;
+    long long n;
+    int C, HW, y_nhwc;   // per-channel layout
+    int dt;              // 0 u8, 1 s8
+    float sa, sb;        // a_s / y_s, b_s / y_s
+    float fixed;         // same-shape body constant
+    float cval;          // scalar-broadcast constant
+    int a_zp, b_zp, y_zp;
+    int lo, hi;
+};
+
+hipError_t launch_quantize(const float* x, long long n, float scale, int zp, int dt, void* y,
+                           hipStream_t s);
+hipError_t launch_dequantize(const void* x, long long n, int dt, float scale, int zp, float* y,
+                             hipStream_t s);
+size_t dynamic_quantize_workspace();
+hipError_t launch_dynamic_quantize(const float* x, long long n, uint8_t* y, float* y_scale,
+                                   uint8_t* y_zp, void* workspace, hipStream_t s);
+hipError_t launch_qadd(const QAddArgs& p, hipStream_t s);
+hipError_t launch_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH, int iW,
+                                  int oH, int oW, int kH, int kW, int sH, int sW, int pH, int pW,
+                                  hipStream_t s);
+
+}  // namespace nnrh

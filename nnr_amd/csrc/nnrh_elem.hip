@@ -1,0 +1,307 @@
+// nnrh_elem.hip -- memory-bound kernels of the int8 path:
+//   QuantizeLinear        (src/backend/cpu/QuantizeLinear.cpp:128-194)
+//   DequantizeLinear      (src/backend/cpu/DequantizeLinear.cpp:100-152)
+//   DynamicQuantizeLinear (src/backend/cpu/DynamicQuantizeLinear.cpp:27-58)
+//   QLinearAdd            (src/backend/cpu/QLinearAdd.cpp:33-265)
+//   MaxPool uint8 NHWC    (src/backend/x64/pool_x64.h:396-436)
+// Each kernel reproduces the reference's per-element formula, including which
+// elements take the 16-wide SIMD body and which the scalar tail.
+#include "nnrh_elem.h"
+#include "nnrh_rq.h"
+
+namespace nnrh {
+
+__device__ __forceinline__ void st_q(void* y, int dt, long long i, int v) {
+    if (dt == 0) ((uint8_t*)y)[i] = (uint8_t)v;
+    else ((int8_t*)y)[i] = (int8_t)v;
+}
+__device__ __forceinline__ int ld_q(const void* p, int dt, long long i) {
+    return dt == 0 ? (int)((const uint8_t*)p)[i] : (int)((const int8_t*)p)[i];
+}
+
+// ---------------------------------------------------------------------------
+// QuantizeLinear, per-tensor. n >= 64: body multiplies by fl(1/s) on 16-wide
+// chunks of 4096-element blocks, the last n%16 elements divide (4096 is a
+// multiple of 16, so only the final partial chunk is a tail). n < 64: divide.
+__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict x, long long n,
+                                                       float scale, float inv, int zp, int dt,
+                                                       int lo, int hi, void* __restrict y) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long body = n >= 64 ? n - n % 16 : 0;
+    for (; i < n; i += stride) {
+        float xv = x[i];
+        int q;
+        if (i < body) {
+            float v = xv * inv;
+            v = __builtin_rintf(v) + (float)zp;
+            v = clamp_minmax(v, (float)lo, (float)hi);
+            q = (int)v;
+        } else {
+            q = clampi(wrap_add(x86_f2i(__builtin_rintf(xv / scale)), zp), lo, hi);
+        }
+        st_q(y, dt, i, q);
+    }
+}
+
+hipError_t launch_quantize(const float* x, long long n, float scale, int zp, int dt, void* y,
+                           hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    int lo = dt == 0 ? 0 : -128, hi = dt == 0 ? 255 : 127;
+    float inv = 1.0f / scale;
+    long long blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, n, scale, inv,
+                       zp, dt, lo, hi, y);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// DequantizeLinear: y = fl((float(q) - float(zp)) * s); dt 0 u8, 1 s8, 2 i32.
+__global__ __launch_bounds__(256) void dequantize_kernel(const void* __restrict x, long long n,
+                                                         int dt, float scale, int zp,
+                                                         float* __restrict y) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        int q = dt == 2 ? ((const int32_t*)x)[i] : ld_q(x, dt, i);
+        float d = (float)q - (float)zp;
+        y[i] = d * scale;
+    }
+}
+
+hipError_t launch_dequantize(const void* x, long long n, int dt, float scale, int zp, float* y,
+                             hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    long long blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, n, dt,
+                       scale, zp, y);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// DynamicQuantizeLinear: min/max partials -> scale/zp -> quantize (divide).
+// min/max are exact, so the result does not depend on the reduction order.
+constexpr int DQL_BLOCKS = 1024;
+
+__global__ __launch_bounds__(256) void minmax_partial_kernel(const float* __restrict x,
+                                                             long long n, float* __restrict part) {
+    __shared__ float smn[256], smx[256];
+    float mn = 0.0f, mx = 0.0f;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (long long)gridDim.x * 256) {
+        float v = x[i];
+        mn = v < mn ? v : mn;
+        mx = mx < v ? v : mx;
+    }
+    smn[threadIdx.x] = mn;
+    smx[threadIdx.x] = mx;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off) {
+            float a = smn[threadIdx.x + off], b = smx[threadIdx.x + off];
+            smn[threadIdx.x] = a < smn[threadIdx.x] ? a : smn[threadIdx.x];
+            smx[threadIdx.x] = smx[threadIdx.x] < b ? b : smx[threadIdx.x];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        part[2 * blockIdx.x] = smn[0];
+        part[2 * blockIdx.x + 1] = smx[0];
+    }
+}
+
+__global__ __launch_bounds__(256) void dyn_scale_kernel(const float* __restrict part, int nparts,
+                                                        float* __restrict y_scale,
+                                                        uint8_t* __restrict y_zp) {
+    __shared__ float smn[256], smx[256];
+    float mn = 0.0f, mx = 0.0f;
+    for (int i = threadIdx.x; i < nparts; i += 256) {
+        float a = part[2 * i], b = part[2 * i + 1];
+        mn = a < mn ? a : mn;
+        mx = mx < b ? b : mx;
+    }
+    smn[threadIdx.x] = mn;
+    smx[threadIdx.x] = mx;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off) {
+            float a = smn[threadIdx.x + off], b = smx[threadIdx.x + off];
+            smn[threadIdx.x] = a < smn[threadIdx.x] ? a : smn[threadIdx.x];
+            smx[threadIdx.x] = smx[threadIdx.x] < b ? b : smx[threadIdx.x];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        float xmin = smn[0] < 0.0f ? smn[0] : 0.0f;
+        float xmax = smx[0] > 0.0f ? smx[0] : 0.0f;
+        float sc = (xmax - xmin) / 255.0f;
+        if (sc == 0.0f) sc = 1.0f;
+        int zp = clampi(x86_f2i(__builtin_rintf(-xmin / sc)), 0, 255);
+        *y_scale = sc;
+        *y_zp = (uint8_t)zp;
+    }
+}
+
+__global__ __launch_bounds__(256) void dyn_quantize_kernel(const float* __restrict x, long long n,
+                                                           const float* __restrict y_scale,
+                                                           const uint8_t* __restrict y_zp,
+                                                           uint8_t* __restrict y) {
+    const float sc = *y_scale;
+    const int zp = *y_zp;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (long long)gridDim.x * 256) {
+        y[i] = (uint8_t)clampi(wrap_add(x86_f2i(__builtin_rintf(x[i] / sc)), zp), 0, 255);
+    }
+}
+
+size_t dynamic_quantize_workspace() { return sizeof(float) * 2 * DQL_BLOCKS; }
+
+hipError_t launch_dynamic_quantize(const float* x, long long n, uint8_t* y, float* y_scale,
+                                   uint8_t* y_zp, void* workspace, hipStream_t s) {
+    float* part = (float*)workspace;
+    long long nb = (n + 255) / 256;
+    int blocks = (int)(nb < DQL_BLOCKS ? (nb > 0 ? nb : 1) : DQL_BLOCKS);
+    hipLaunchKernelGGL(minmax_partial_kernel, dim3(blocks), dim3(256), 0, s, x, n, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(dyn_scale_kernel, dim3(1), dim3(256), 0, s, part, blocks, y_scale, y_zp);
+    e = hipGetLastError();
+    if (e != hipSuccess || n <= 0) return e;
+    long long qb = (n + 255) / 256;
+    if (qb > 65536) qb = 65536;
+    hipLaunchKernelGGL(dyn_quantize_kernel, dim3((unsigned)qb), dim3(256), 0, s, x, n, y_scale,
+                       y_zp, y);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// QLinearAdd. kind: 0 same shape, 1 B scalar, 2 A scalar, 3 per-channel B[C].
+__global__ __launch_bounds__(256) void qadd_kernel(QAddArgs p) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (; i < p.n; i += stride) {
+        int q;
+        if (p.kind == 0) {
+            const long long body = p.n - p.n % 16;
+            int a = ld_q(p.a, p.dt, i), b = ld_q(p.b, p.dt, i);
+            if (i < body) {
+                // v = fma(fa, sa, fma(fb, sb, fixed)); cvtps2dq; saturating pack
+                float v = __builtin_fmaf((float)b, p.sb, p.fixed);
+                v = __builtin_fmaf((float)a, p.sa, v);
+                q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
+            } else {
+                float t1 = p.sa * (float)(a - p.a_zp);
+                float t2 = p.sb * (float)(b - p.b_zp);
+                float v = (t1 + t2) + (float)p.y_zp;
+                q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
+            }
+        } else if (p.kind == 1 || p.kind == 2) {
+            // scalar loops (QLinearAdd.cpp:108-119)
+            float v;
+            if (p.kind == 1) {
+                float t = p.sa * (float)(ld_q(p.a, p.dt, i) - p.a_zp);
+                v = (t + p.cval) + (float)p.y_zp;
+            } else {
+                float t = p.sb * (float)(ld_q(p.b, p.dt, i) - p.b_zp);
+                v = (p.cval + t) + (float)p.y_zp;
+            }
+            q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
+        } else {
+            // per-channel: a full, b[C] (QLinearAdd.cpp:120-226)
+            int c;
+            long long inner;
+            if (p.y_nhwc) { c = (int)(i % p.C); inner = c; }
+            else { c = (int)((i / p.HW) % p.C); inner = i % p.HW; }
+            const long long body = p.y_nhwc ? (p.C - p.C % 16) : (p.HW - p.HW % 16);
+            int a = ld_q(p.a, p.dt, i);
+            int bc = ld_q(p.b, p.dt, c) - p.b_zp;
+            if (p.y_nhwc) {
+                float t0 = p.sb * (float)bc;
+                float off = t0 + (float)p.y_zp;     // ch_off[c]
+                if (inner < body) {
+                    float v = __builtin_fmaf((float)a - (float)p.a_zp, p.sa, off);
+                    v = clamp_minmax(__builtin_rintf(v), (float)p.lo, (float)p.hi);
+                    q = (int)v;
+                } else {
+                    float t = p.sa * (float)(a - p.a_zp);
+                    q = clampi(x86_f2i(__builtin_rintf(t + off)), p.lo, p.hi);
+                }
+            } else {
+                float chv = p.sb * (float)bc;
+                if (inner < body) {
+                    float voff = chv + (float)p.y_zp;
+                    float v = __builtin_fmaf((float)a - (float)p.a_zp, p.sa, voff);
+                    v = clamp_minmax(__builtin_rintf(v), (float)p.lo, (float)p.hi);
+                    q = (int)v;
+                } else {
+                    float t = p.sa * (float)(a - p.a_zp);
+                    float v = (t + chv) + (float)p.y_zp;
+                    q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
+                }
+            }
+        }
+        st_q(p.y, p.dt, i, q);
+    }
+}
+
+hipError_t launch_qadd(const QAddArgs& p, hipStream_t s) {
+    if (p.n <= 0) return hipSuccess;
+    long long blocks = (p.n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(qadd_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// MaxPool uint8 NHWC: max over the in-image window, starting from 0.
+__global__ __launch_bounds__(256) void maxpool_u8_kernel(const uint8_t* __restrict x,
+                                                         uint8_t* __restrict y, int N, int C,
+                                                         int iH, int iW, int oH, int oW, int kH,
+                                                         int kW, int sH, int sW, int pH,
+                                                         int pW) {
+    const int C4 = (C + 3) >> 2;
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)N * oH * oW * C4;
+    if (idx >= total) return;
+    const int cg = (int)(idx % C4);
+    const long long pix = idx / C4;
+    const int ow = (int)(pix % oW), oh = (int)((pix / oW) % oH), n = (int)(pix / ((long long)oW * oH));
+    const int c0 = cg * 4;
+    const int ih0 = oh * sH - pH, iw0 = ow * sW - pW;
+    const int kh0 = ih0 < 0 ? -ih0 : 0, kh1 = kH < iH - ih0 ? kH : iH - ih0;
+    const int kw0 = iw0 < 0 ? -iw0 : 0, kw1 = kW < iW - iw0 ? kW : iW - iw0;
+    const bool vec_ok = (C & 3) == 0;
+    uint32_t m[4] = {0, 0, 0, 0};
+    for (int a = kh0; a < kh1; ++a)
+        for (int b = kw0; b < kw1; ++b) {
+            const uint8_t* xp = x + (((long long)n * iH + ih0 + a) * iW + iw0 + b) * C + c0;
+            if (vec_ok) {
+                uint32_t w = *(const uint32_t*)xp;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    uint32_t v = (w >> (8 * i)) & 0xff;
+                    m[i] = v > m[i] ? v : m[i];
+                }
+            } else {
+                for (int i = 0; i < 4 && c0 + i < C; ++i) m[i] = xp[i] > m[i] ? xp[i] : m[i];
+            }
+        }
+    uint8_t* yp = y + pix * C + c0;
+    if (vec_ok) *(uint32_t*)yp = m[0] | (m[1] << 8) | (m[2] << 16) | (m[3] << 24);
+    else
+        for (int i = 0; i < 4 && c0 + i < C; ++i) yp[i] = (uint8_t)m[i];
+}
+
+hipError_t launch_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH, int iW,
+                                  int oH, int oW, int kH, int kW, int sH, int sW, int pH, int pW,
+                                  hipStream_t s) {
+    long long total = (long long)N * oH * oW * ((C + 3) / 4);
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(maxpool_u8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x,
+                       y, N, C, iH, iW, oH, oW, kH, kW, sH, sW, pH, pW);
+    return hipGetLastError();
+}
+
+}  // namespace nnrh

@@ -1,0 +1,134 @@
+// nnrh_internal.h -- shared declarations between the HIP kernel files and
+// the C-ABI layer (capi.cpp). Not installed; the public surface is
+// include/nnr_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace nnrh {
+
+// ---------------------------------------------------------------------------
+// Requantize epilogue selectors for the MFMA GEMM kernel.
+enum EpiMode : int {
+    EPI_I32 = 0,   // store the exact int32 accumulator (MatMulInteger)
+    EPI_RQA = 1,   // fma(acc,cs,bf) * inv_y, rne, +y_zp, clamp [L,hi]
+    EPI_RQB = 2,   // (acc+bias)*os, clamp [lo-zp,hi-zp], rne, +zp
+    EPI_RQC = 3,   // fma(fma(acc,cs,bf), inv_y, zp), clamp, rne
+    EPI_RQD = 4,   // acc*cm + zp, nearbyint, clamp
+};
+
+// Which output elements take the reference's scalar-tail expression (RQ-A')
+// instead of the SIMD body (RQ-A / RQ-C).
+enum TailMode : int {
+    TAIL_NONE = 0,
+    TAIL_SPATIAL = 1,   // s = pixel index in image; tail when s >= sp - sp%16
+    TAIL_OW = 2,        // tail when ow >= oW - oW%16
+    TAIL_TILED = 3,     // tiled im2col: tiles of tile_h rows, tail per tile
+};
+
+// A-operand (activation) addressing.
+enum AMode : int {
+    A_DENSE = 0,   // A[m*lda + k]
+    A_CONV = 1,    // implicit im2col over an NHWC tensor, K order (kh,kw,c)
+};
+
+struct GemmArgs {
+    // ---- A (activations) ----
+    const uint8_t* a;     // dense matrix or NHWC tensor base
+    long long lda;        // dense row stride (bytes)
+    long long a_bstride;  // per-batch stride (blockIdx.z)
+    int a_xor;            // 0x80 for uint8 activations (x-128), 0 for int8
+    int M, N, K, Kp;      // K real, Kp = K rounded up to 64 (packed B row length)
+    // conv geometry (A_CONV)
+    int H, W, C, oH, oW, kH, kW, sH, sW, dH, dW, pad_t, pad_l;
+    int Cs;               // channel stride of the NHWC tensor (>= C; groups)
+    int pad_byte;         // raw byte for out-of-image taps (x_zp)
+    // ---- B (weights), packed [Np][Kp] int8 with the 64-column permutation ----
+    const int8_t* b;
+    long long b_bstride;
+    int Np;
+    // ---- zero-point corrections: v = acc' - alpha*colsum[n] - beta*rowsum[m]
+    // alpha = x_zp - a_sub (a_sub = 128 for uint8 activations, else 0); when
+    // alpha_zp_dev is set the activation zero point is read from device memory.
+    const int32_t* colsum;
+    int alpha;
+    const void* alpha_zp_dev;  // nullable: uint8 (a_xor) or int8 zero point
+    int a_sub;
+    const int32_t* rowsum;  // nullable
+    long long rowsum_bstride;
+    int beta;
+    const int32_t* beta_col;  // nullable: per-column beta (per-channel w_zp)
+    // ---- epilogue ----
+    int epi;
+    int tail;
+    int tile_h;             // TAIL_TILED
+    const float* os;        // RQ-B
+    const int32_t* bias;    // RQ-B (nullable)
+    const float* cs;        // RQ-A / RQ-C
+    const float* bf;        // RQ-A / RQ-C
+    long long param_bstride;  // per-batch (z) offset of every per-column array
+                              // (colsum, beta_col, os, bias, cs, bf)
+    float inv_y;
+    float cm;               // RQ-D combined scale fl(fl(a_s*b_s)/y_s)
+    const float* cm_a_scale_dev;  // RQ-D: nullable device a_scale; then
+    float cm_b, cm_y;             //   cm = fl(fl(a_s*cm_b)/cm_y) in-kernel
+    int y_zp;
+    int L, hi, lo;          // clamp bounds
+    int bprime_from;        // RQ-B: columns >= this use roundf (RQ-B')
+    // ---- output ----
+    void* y;
+    long long ldy;          // row stride in elements (NHWC / row-major);
+                            // with y_nchw: total channel count of y
+    long long y_bstride;    // per-batch stride in elements
+    int y_type;             // 0 u8, 1 s8, 2 i32
+    int y_nchw;             // 1: scatter to NCHW [img][n][s] (s = m % (oH*oW))
+};
+
+// Tile shapes available to the launcher (BM x BN, 256 threads).
+enum TileCfg : int { TILE_128x128 = 0, TILE_256x64 = 1, TILE_64x256 = 2 };
+
+hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec,
+                        hipStream_t s);
+
+// ---- misc kernels (nnrh_misc.hip) ----
+hipError_t launch_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C,
+                                  int HW, int Cpad, uint8_t fill, hipStream_t s);
+hipError_t launch_depthwise(const uint8_t* x, const int8_t* w, uint8_t* y,
+                            const float* cs, const float* bf, int N, int C,
+                            int H, int W, int oH, int oW, int kH, int kW,
+                            int sH, int sW, int dH, int dW, int pad_t,
+                            int pad_l, int x_zp, int w_zp, float inv_y,
+                            int y_zp, int L, int hi, int act_signed,
+                            int y_nchw, int tail_mode, int tail_tile_h,
+                            hipStream_t s);
+hipError_t launch_rowsum_dense(const uint8_t* a, long long lda,
+                               long long a_bstride, int M, int K, int a_signed,
+                               int a_zp, const void* a_zp_dev, int32_t* out,
+                               int batch, hipStream_t s);
+hipError_t launch_fill_u8(void* p, uint8_t v, long long n, hipStream_t s);
+hipError_t launch_rowsum_conv(const uint8_t* x, int N, int H, int W, int Cs,
+                              int Cg, int groups, int oH, int oW, int kH,
+                              int kW, int sH, int sW, int dH, int dW,
+                              int pad_t, int pad_l, int a_signed, int x_zp,
+                              int32_t* out, hipStream_t s);
+// Pack a row-major B[K][N] (int8 or uint8) into the kernel's [Np][Kp]
+// permuted layout and compute colsum[n] = sum_k (b - b_sub).
+hipError_t launch_pack_b_dense(const void* b, long long b_bstride, int K,
+                               int N, int Kp, int Np, int b_xor, int8_t* out,
+                               long long out_bstride, int32_t* colsum,
+                               long long colsum_bstride, int batch,
+                               hipStream_t s);
+
+// Row permutation of packed B inside each 64-column group: storage row of
+// logical column n. The MFMA epilogue then sees 16 consecutive columns per
+// lane (see nnrh_qgemm.hip).
+__host__ __device__ inline int packed_row_of_col(int n) {
+    int g = n >> 6, nl = n & 63;
+    int tn = (nl & 15) >> 2;
+    int j = ((nl >> 4) << 2) | (nl & 3);
+    return (g << 6) | (tn << 4) | j;
+}
+
+}  // namespace nnrh

@@ -1,0 +1,664 @@
+/*
+ * nnr_oracle.c -- CPU restatement of NNR's int8 QDQ compute path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see nnr_oracle.h). Not part of the product.
+ * Build: oracle/Makefile (gcc -O3 -ffp-contract=off -fopenmp).
+ *
+ * Citations are path:line into the reference tree (beru/nnr).
+ */
+#include "nnr_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_contract = 0;
+static int g_threads = 0;
+
+void orc_set_contract(int on) { g_contract = on ? 1 : 0; }
+int orc_get_contract(void) { return g_contract; }
+void orc_set_threads(int n) { g_threads = n; }
+int orc_get_threads(void) {
+#ifdef _OPENMP
+    return g_threads > 0 ? g_threads : omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* a*b + c as a C++ expression in the reference: two roundings unless the
+ * compiler contracts it (see header). */
+static inline float mul_add_expr(float a, float b, float c) {
+    if (g_contract) return fmaf(a, b, c);
+    float t = a * b;
+    return t + c;
+}
+
+/* (int32_t)float on x86 (cvttss2si): out of range or NaN -> INT32_MIN */
+static inline int x86_f2i(float r) {
+    return (r >= -2147483648.0f && r < 2147483648.0f) ? (int)r : (int)0x80000000;
+}
+static inline int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+/* _mm512_max_ps(_mm512_min_ps(v, hi), lo) */
+static inline float clampf_minmax(float v, float lo, float hi) {
+    v = v < hi ? v : hi;
+    return v > lo ? v : lo;
+}
+
+/* ---- fp16: src/nnrconf.h:147-199 ----------------------------------- */
+uint16_t orc_f32_to_f16(float v) {
+    uint32_t u; memcpy(&u, &v, 4);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    int e = (int)((u >> 23) & 0xffu) - 127;
+    uint32_t mant = u & 0x7fffffu;
+    if (e > 15) return (uint16_t)(sign | 0x7c00u);
+    if (e >= -14) {
+        uint32_t rb = mant & 0x1fffu;
+        uint16_t y = (uint16_t)(sign | ((uint16_t)(e + 15) << 10) | (uint16_t)(mant >> 13));
+        if (rb > 0x1000u || (rb == 0x1000u && (y & 1u))) y++;
+        return y;
+    }
+    if (e >= -24) {
+        mant |= 0x800000u;
+        int sh = -e - 14 + 13;
+        uint32_t rb = mant & ((1u << sh) - 1u);
+        uint32_t half = 1u << (sh - 1);
+        uint16_t y = (uint16_t)(sign | (uint16_t)(mant >> sh));
+        if (rb > half || (rb == half && (y & 1u))) y++;
+        return y;
+    }
+    return sign;
+}
+
+float orc_f16_to_f32(uint16_t v) {
+    uint32_t sign = (uint32_t)(v & 0x8000u) << 16;
+    uint32_t e = (v >> 10) & 0x1fu, mant = v & 0x3ffu, u;
+    if (e == 0) {
+        if (mant == 0) { u = sign; }
+        else {
+            int ee = 0;
+            while (!(mant & 0x400u)) { mant <<= 1; ee--; }
+            mant &= 0x3ffu; ee++;
+            u = sign | ((uint32_t)(ee + 127 - 15) << 23) | (mant << 13);
+        }
+    } else if (e == 31) {
+        u = sign | 0x7f800000u | (mant << 13);
+    } else {
+        u = sign | ((e + 127 - 15) << 23) | (mant << 13);
+    }
+    float f; memcpy(&f, &u, 4);
+    return f;
+}
+
+/* ---- requantize primitives ------------------------------------------ */
+
+/* RQ-A. SIMD epilogue of the direct / depthwise / im2col paths:
+ * src/backend/cpu/QLinearConv.cpp:630-638 (direct),
+ * src/backend/x64/depthwise_int8_avx512.h:249-255,
+ * src/backend/x64/gemm_int8_avx512.h:727-736 (fused im2col). */
+int orc_rq_a(int32_t acc, float cs, float bf, float inv_y, int y_zp, int L, int hi) {
+    float f = fmaf((float)acc, cs, bf);
+    float q = f * inv_y;
+    q = rintf(q);
+    q = q + (float)y_zp;
+    q = clampf_minmax(q, (float)L, (float)hi);
+    return (int)q;
+}
+
+/* RQ-A'. Scalar tails: QLinearConv.cpp:640-645, :1181-1185;
+ * conv_first_layer_int8_avx512.h:305-313. */
+int orc_rq_a_tail(int32_t acc, float cs, float bf, float inv_y, int y_zp, int L, int hi) {
+    float val = mul_add_expr((float)acc, cs, bf);
+    float t = val * inv_y;
+    int q = (int)((uint32_t)x86_f2i(nearbyintf(t)) + (uint32_t)y_zp);
+    return clampi(q, L, hi);
+}
+
+/* RQ-B. JIT packed NR48 / NHWC-direct NR16 epilogue:
+ * src/backend/x64/jit_conv_int8_ukernel.cpp:950-964 and :1900-1918,
+ * parameters from src/backend/cpu/QLinearConv_reshape.h:323-335. */
+int orc_rq_b(int32_t acc, int32_t bias, float os, int y_zp, int lo, int hi) {
+    int32_t v = (int32_t)((uint32_t)acc + (uint32_t)bias);
+    float f = (float)v * os;
+    f = f > (float)lo - (float)y_zp ? f : (float)lo - (float)y_zp;   /* vmaxps */
+    f = f < (float)hi - (float)y_zp ? f : (float)hi - (float)y_zp;   /* vminps */
+    int r = (int)rintf(f) + y_zp;                                   /* cvtps2dq */
+    /* vpmovusdb: unsigned saturation (r is already inside [lo,hi]) */
+    return r;
+}
+
+/* RQ-B'. Scalar fallback for the third NR48 sub-panel:
+ * src/backend/x64/gemm_int8_avx512.h:1487-1509. */
+int orc_rq_b_roundf(int32_t acc, int32_t bias, float os, int y_zp, int lo, int hi) {
+    int32_t v = (int32_t)((uint32_t)acc + (uint32_t)bias);
+    float f = (float)v * os;
+    float qmin = (float)lo - (float)y_zp, qmax = (float)hi - (float)y_zp;
+    f = f > qmin ? f : qmin;
+    f = f < qmax ? f : qmax;
+    int r = (int)roundf(f) + y_zp;
+    return clampi(r, 0, 255);
+}
+
+/* RQ-C. First-layer epilogue: conv_first_layer_int8_avx512.h:262-273 and
+ * :289-302. */
+int orc_rq_c(int32_t acc, float cs, float bf, float inv_y, int y_zp, int qmin, int qmax) {
+    float t = fmaf((float)acc, cs, bf);
+    float f = fmaf(t, inv_y, (float)y_zp);
+    f = clampf_minmax(f, (float)qmin, (float)qmax);
+    return (int)rintf(f);
+}
+
+/* RQ-D. QLinearMatMul: src/backend/cpu/QLinearMatMul.cpp:188-198. */
+int orc_rq_d(int32_t acc, float cm, int y_zp, int lo, int hi) {
+    float val = mul_add_expr((float)acc, cm, (float)y_zp);
+    int iv = x86_f2i(nearbyintf(val));
+    return clampi(iv, lo, hi);
+}
+
+/* ---- element access -------------------------------------------------- */
+static inline int32_t ld_q(const void* p, int dtype, size_t i) {
+    switch (dtype) {
+    case ORC_U8: return ((const uint8_t*)p)[i];
+    case ORC_S8: return ((const int8_t*)p)[i];
+    case ORC_I32: return ((const int32_t*)p)[i];
+    default: return 0;
+    }
+}
+static inline void st_q(void* p, int dtype, size_t i, int v) {
+    if (dtype == ORC_U8) ((uint8_t*)p)[i] = (uint8_t)v;
+    else if (dtype == ORC_S8) ((int8_t*)p)[i] = (int8_t)v;
+    else ((int32_t*)p)[i] = v;
+}
+static inline void dtype_range(int dtype, int* lo, int* hi) {
+    if (dtype == ORC_U8) { *lo = 0; *hi = 255; } else { *lo = -128; *hi = 127; }
+}
+
+/* ---- QuantizeLinear: src/backend/cpu/QuantizeLinear.cpp:128-194 -------
+ * total >= 64: 4096-element blocks, 16-wide SIMD body multiplies by
+ * fl(1/s); the last (end-i)<16 elements of each block divide by s.
+ * total < 64: scalar divide everywhere. */
+void orc_quantize_linear(const float* x, size_t n, float scale, int zp,
+                         int y_dtype, void* y) {
+    int lo, hi; dtype_range(y_dtype, &lo, &hi);
+    if (n >= 64) {
+        float inv = 1.0f / scale;
+        const size_t BLOCK = 4096;
+        #pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+        for (long long blk = 0; blk < (long long)((n + BLOCK - 1) / BLOCK); blk++) {
+            size_t base = (size_t)blk * BLOCK;
+            size_t end = base + BLOCK < n ? base + BLOCK : n;
+            size_t body_end = end - (end - base) % 16;
+            for (size_t i = base; i < body_end; i++) {
+                float v = x[i] * inv;
+                v = rintf(v) + (float)zp;
+                v = clampf_minmax(v, (float)lo, (float)hi);
+                st_q(y, y_dtype, i, (int)v);
+            }
+            for (size_t i = body_end; i < end; i++)
+                st_q(y, y_dtype, i, clampi((int)nearbyintf(x[i] / scale) + zp, lo, hi));
+        }
+    } else {
+        for (size_t i = 0; i < n; i++)
+            st_q(y, y_dtype, i, clampi((int)nearbyintf(x[i] / scale) + zp, lo, hi));
+    }
+}
+
+/* ---- DequantizeLinear: src/backend/cpu/DequantizeLinear.cpp:100-152 ---- */
+void orc_dequantize_linear(const void* x, int x_dtype, size_t n, float scale,
+                           int zp, float* y) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = ((float)ld_q(x, x_dtype, i) - (float)zp) * scale;
+}
+
+/* ---- DynamicQuantizeLinear: DynamicQuantizeLinear.cpp:27-58 ------------ */
+void orc_dynamic_quantize_linear(const float* x, size_t n, uint8_t* y,
+                                 float* y_scale, uint8_t* y_zp) {
+    float mn = 0.0f, mx = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        mn = x[i] < mn ? x[i] : mn;     /* std::min(x_min, px[i]) */
+        mx = mx < x[i] ? x[i] : mx;     /* std::max(x_max, px[i]) */
+    }
+    mn = mn < 0.0f ? mn : 0.0f;
+    mx = mx > 0.0f ? mx : 0.0f;
+    float s = (mx - mn) / 255.0f;
+    if (s == 0.0f) s = 1.0f;
+    int zp = clampi((int)nearbyintf(-mn / s), 0, 255);
+    *y_scale = s;
+    *y_zp = (uint8_t)zp;
+    for (size_t i = 0; i < n; i++)
+        y[i] = (uint8_t)clampi((int)nearbyintf(x[i] / s) + zp, 0, 255);
+}
+
+/* ---- QLinearMatMul: src/backend/cpu/QLinearMatMul.cpp:111-232 ----------- */
+static float ld_scale(const void* p, int sd) {
+    if (sd == ORC_F16) return orc_f16_to_f32(*(const uint16_t*)p);
+    return *(const float*)p;
+}
+
+float orc_qmatmul_combined_scale(const void* a_s, const void* b_s,
+                                 const void* y_s, int sd) {
+    if (sd == ORC_F16) {
+        /* float16_t *= and /= : compute in float, round to half (float16.h) */
+        float fa = orc_f16_to_f32(*(const uint16_t*)a_s);
+        float fb = orc_f16_to_f32(*(const uint16_t*)b_s);
+        float fy = orc_f16_to_f32(*(const uint16_t*)y_s);
+        uint16_t h = orc_f32_to_f16(fa * fb);
+        h = orc_f32_to_f16(orc_f16_to_f32(h) / fy);
+        return orc_f16_to_f32(h);
+    }
+    float as = *(const float*)a_s, bs = *(const float*)b_s, ys = *(const float*)y_s;
+    float t = as * bs;
+    return t / ys;
+}
+
+int orc_qlinear_matmul(int batch, int m, int n, int k,
+                       const void* a, int a_dtype, int batch_a,
+                       const void* a_scale, const void* a_zp,
+                       const void* b, int b_dtype, int batch_b,
+                       const void* b_scale, const void* b_zp,
+                       const void* y_scale, const void* y_zp,
+                       int sd, void* y, int y_dtype) {
+    (void)b_scale;
+    int azp = ld_q(a_zp, a_dtype, 0);
+    int bzp = ld_q(b_zp, b_dtype, 0);            /* b_zp[0] only (:118-119) */
+    int yzp = ld_q(y_zp, y_dtype, 0);
+    float cm = orc_qmatmul_combined_scale(a_scale, b_scale, y_scale, sd);
+    (void)ld_scale;
+    int lo, hi; dtype_range(y_dtype, &lo, &hi);
+    for (int bi = 0; bi < batch; bi++) {
+        size_t aoff = batch_a <= 1 ? 0 : (size_t)bi * m * k;
+        size_t boff = batch_b <= 1 ? 0 : (size_t)bi * k * n;
+        size_t yoff = (size_t)bi * m * n;
+        #pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+        for (int u = 0; u < m; u++) {
+            int32_t* row = (int32_t*)calloc((size_t)n, sizeof(int32_t));
+            for (int w = 0; w < k; w++) {
+                int32_t av = ld_q(a, a_dtype, aoff + (size_t)u * k + w) - azp;
+                for (int v = 0; v < n; v++) {
+                    int32_t bv = ld_q(b, b_dtype, boff + (size_t)w * n + v) - bzp;
+                    row[v] = (int32_t)((uint32_t)row[v] + (uint32_t)(av * bv));
+                }
+            }
+            for (int v = 0; v < n; v++)
+                st_q(y, y_dtype, yoff + (size_t)u * n + v, orc_rq_d(row[v], cm, yzp, lo, hi));
+            free(row);
+        }
+    }
+    return 0;
+}
+
+/* ---- MatMulInteger: src/backend/cpu/MatMulInteger.cpp:11-150 -----------
+ * y = sum (a - a_zp)(b - b_zp) with numpy broadcasting of leading dims. */
+int orc_matmul_integer(const int* a_dims, int a_nd, const void* a, int a_dtype,
+                       const int* b_dims, int b_nd, const void* b, int b_dtype,
+                       int a_zp, int b_zp, int32_t* y) {
+    int ad[8], bd[8], yd[8], nd;
+    int an = a_nd, bn = b_nd;
+    if (an < 1 || bn < 1 || an > 6 || bn > 6) return -1;
+    /* promote 1-D operands (MatMulInteger.cpp:29-38) */
+    int ta[8], tb[8];
+    if (an == 1) { ta[0] = 1; ta[1] = a_dims[0]; an = 2; } else memcpy(ta, a_dims, sizeof(int) * an);
+    if (bn == 1) { tb[0] = b_dims[0]; tb[1] = 1; bn = 2; } else memcpy(tb, b_dims, sizeof(int) * bn);
+    nd = an > bn ? an : bn;
+    for (int i = 0; i < nd; i++) {
+        int ia = i - (nd - an), ib = i - (nd - bn);
+        ad[i] = ia >= 0 ? ta[ia] : 1;
+        bd[i] = ib >= 0 ? tb[ib] : 1;
+    }
+    int m = ad[nd - 2], k = ad[nd - 1], n = bd[nd - 1];
+    if (bd[nd - 2] != k) return -1;
+    size_t nb = 1;
+    for (int i = 0; i < nd - 2; i++) {
+        if (ad[i] != bd[i] && ad[i] > 1 && bd[i] > 1) return -1;
+        yd[i] = ad[i] > bd[i] ? ad[i] : bd[i];
+        nb *= (size_t)yd[i];
+    }
+    for (size_t bi = 0; bi < nb; bi++) {
+        size_t rem = bi, aoff = 0, boff = 0, astr = 1, bstr = 1;
+        for (int i = nd - 3; i >= 0; i--) {
+            size_t idx = rem % (size_t)yd[i]; rem /= (size_t)yd[i];
+            aoff += (ad[i] > 1 ? idx : 0) * astr;
+            boff += (bd[i] > 1 ? idx : 0) * bstr;
+            astr *= (size_t)ad[i]; bstr *= (size_t)bd[i];
+        }
+        aoff *= (size_t)m * k; boff *= (size_t)k * n;
+        int32_t* yb = y + bi * (size_t)m * n;
+        for (int u = 0; u < m; u++)
+            for (int v = 0; v < n; v++) {
+                uint32_t s = 0;
+                for (int w = 0; w < k; w++)
+                    s += (uint32_t)((ld_q(a, a_dtype, aoff + (size_t)u * k + w) - a_zp) *
+                                    (ld_q(b, b_dtype, boff + (size_t)w * n + v) - b_zp));
+                yb[(size_t)u * n + v] = (int32_t)s;
+            }
+    }
+    return 0;
+}
+
+/* ---- QLinearConv ------------------------------------------------------ */
+
+/* conv_shape.h:21-81, auto_pad NOTSET */
+int orc_conv_out_dim(int in, int k, int d, int s, int pb, int pe) {
+    int ek = (k - 1) * d + 1;
+    return (int)floorf((float)(in + pb + pe - ek) / (float)s + 1.0f);
+}
+
+static int conv_per_channel_zp(const orc_conv_params* p) {
+    /* QLinearConv.cpp:136-153: collapse all-equal per-channel zp */
+    if (p->w_zp_count <= 1) return 0;
+    for (int i = 1; i < p->w_zp_count; i++)
+        if (p->w_zp[i] != p->w_zp[0]) return 1;
+    return 0;
+}
+
+/* First-match dispatch of QLinearConv::exec_simd_4d (QLinearConv.cpp:1337-1351)
+ * with the prepack preconditions of QLinearConv_reshape.h:36-284. */
+int orc_conv_dispatch(const orc_conv_params* p) {
+    const int u8 = p->act_dtype == ORC_U8;
+    const int pcz = conv_per_channel_zp(p);
+    const int wzp0 = p->w_zp_count > 0 ? p->w_zp[0] : 0;
+    const int Cg = p->C / p->group;
+    const int is_dw = (p->group == p->OC && Cg == 1);
+    const int vnni_ok = p->vnni && u8 && !pcz;
+    const int dil1 = (p->dH == 1 && p->dW == 1);
+    /* (1) exec_dw_int8_nhwc: QLinearConv.cpp:467-526 */
+    if (vnni_ok && is_dw && p->y_nhwc) return ORC_BR_DW;
+    /* (2) exec_first_layer_int8: QLinearConv.cpp:665-700; prepack
+     *     QLinearConv_reshape.h:211-256 (group 1, dil 1, IC<=4, kH>=3, OC>=16, w_zp 0) */
+    if (vnni_ok && p->group == 1 && dil1 && Cg <= 4 && p->kH >= 3 && p->OC >= 16 &&
+        wzp0 == 0 && p->C <= 4 && p->pad_t == p->pad_b && p->pad_l == p->pad_r &&
+        !p->x_nhwc)
+        return ORC_BR_FIRST;
+    /* (3) exec_direct_int8: QLinearConv.cpp:579-652 */
+    if (vnni_ok && p->group == 1 && dil1 && wzp0 == 0 && p->oH * p->oW <= 256 && !p->y_nhwc)
+        return ORC_BR_DIRECT;
+    /* (4) exec_packed_nr48: QLinearConv.cpp:706-848, NR16 predicate :750-759 */
+    if (vnni_ok && p->group == 1) {
+        if (p->kH == 3 && p->kW == 3 && p->sH == 1 && p->sW == 1 && dil1 &&
+            p->pad_t == 1 && p->pad_l == 1 && p->C >= 64 && p->OC >= 64 &&
+            (p->OC % 16) == 0 && wzp0 == 0 && p->y_nhwc)
+            return ORC_BR_NR16;
+        return ORC_BR_PACKED;
+    }
+    /* (6) exec_vnni_im2col: QLinearConv.cpp:1010-1196 */
+    if (vnni_ok) return (p->sH == 1 && p->sW == 1) ? ORC_BR_IM2COL_S1 : ORC_BR_IM2COL;
+    /* (7) exec_float_fallback: QLinearConv.cpp:1205-1335 */
+    return ORC_BR_FLOAT;
+}
+
+void orc_conv_acc(const orc_conv_params* p, const void* x, const int8_t* w,
+                  int32_t* acc) {
+    const int N = p->N, C = p->C, H = p->H, W = p->W;
+    const int OC = p->OC, kH = p->kH, kW = p->kW, G = p->group;
+    const int Cg = C / G, OCg = OC / G, oH = p->oH, oW = p->oW;
+    const int pcz = conv_per_channel_zp(p);
+    const int u8 = p->act_dtype == ORC_U8;
+    /* xs: (x - x_zp) as int16, NHWC */
+    int16_t* xs = (int16_t*)malloc(sizeof(int16_t) * (size_t)N * H * W * C);
+    #pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+    for (long long i = 0; i < (long long)N * H * W; i++) {
+        long long n = i / ((long long)H * W), hw = i % ((long long)H * W);
+        for (int c = 0; c < C; c++) {
+            size_t src = p->x_nhwc ? (size_t)i * C + c : ((size_t)(n * C + c) * H * W + hw);
+            int v = u8 ? ((const uint8_t*)x)[src] : ((const int8_t*)x)[src];
+            xs[(size_t)i * C + c] = (int16_t)(v - p->x_zp);
+        }
+    }
+    /* ws: (w - w_zp) as int16, [OC][kH][kW][Cg] */
+    int16_t* ws = (int16_t*)malloc(sizeof(int16_t) * (size_t)OC * kH * kW * Cg);
+    /* The VNNI branches read w_zp through the activation type T
+     * (QLinearConv.cpp:386, `(T*)inputs[5]->data`); the float fallback packs
+     * with the weight type, int8 (QLinearConv_reshape.h:72-78). */
+    const int zp_as_u8 = u8 && orc_conv_dispatch(p) != ORC_BR_FLOAT;
+    for (int oc = 0; oc < OC; oc++) {
+        int8_t zb = pcz ? p->w_zp[oc] : (p->w_zp_count > 0 ? p->w_zp[0] : 0);
+        int zp = zp_as_u8 ? (int)(uint8_t)zb : (int)zb;
+        for (int c = 0; c < Cg; c++)
+            for (int a = 0; a < kH; a++)
+                for (int b = 0; b < kW; b++)
+                    ws[(((size_t)oc * kH + a) * kW + b) * Cg + c] =
+                        (int16_t)(w[(((size_t)oc * Cg + c) * kH + a) * kW + b] - zp);
+    }
+    #pragma omp parallel for schedule(dynamic) num_threads(orc_get_threads())
+    for (long long r = 0; r < (long long)N * oH; r++) {
+        int n = (int)(r / oH), oh = (int)(r % oH);
+        for (int ow = 0; ow < oW; ow++) {
+            for (int oc = 0; oc < OC; oc++) {
+                int g = oc / OCg;
+                int32_t s = 0;
+                for (int a = 0; a < kH; a++) {
+                    int ih = oh * p->sH - p->pad_t + a * p->dH;
+                    if (ih < 0 || ih >= H) continue;
+                    for (int b = 0; b < kW; b++) {
+                        int iw = ow * p->sW - p->pad_l + b * p->dW;
+                        if (iw < 0 || iw >= W) continue;
+                        const int16_t* xp = xs + (((size_t)n * H + ih) * W + iw) * C + (size_t)g * Cg;
+                        const int16_t* wp = ws + (((size_t)oc * kH + a) * kW + b) * Cg;
+                        int32_t t = 0;
+                        for (int c = 0; c < Cg; c++) t += (int32_t)xp[c] * (int32_t)wp[c];
+                        s = (int32_t)((uint32_t)s + (uint32_t)t);
+                    }
+                }
+                acc[(((size_t)n * OC + oc) * oH + oh) * oW + ow] = s;
+            }
+        }
+    }
+    free(xs);
+    free(ws);
+}
+
+int orc_qlinear_conv_from_acc(const orc_conv_params* p, const int32_t* acc, void* y) {
+    const int br = orc_conv_dispatch(p);
+    const int N = p->N, OC = p->OC, oH = p->oH, oW = p->oW, sp = oH * oW;
+    int lo, hi; dtype_range(p->act_dtype, &lo, &hi);
+    const int qmin = p->post_fn ? (lo > p->y_zp ? lo : p->y_zp) : lo;   /* QLinearConv.cpp:419 */
+    const float inv_y = 1.0f / p->y_scale;
+    float* cs = (float*)malloc(sizeof(float) * OC);
+    float* bf = (float*)malloc(sizeof(float) * OC);
+    float* os = (float*)malloc(sizeof(float) * OC);
+    /* QLinearConv_reshape.h:288-321 */
+    for (int oc = 0; oc < OC; oc++) {
+        float wsc = p->w_scale_count > 1 ? p->w_scale[oc] : p->w_scale[0];
+        cs[oc] = p->x_scale * wsc;
+        os[oc] = cs[oc] * inv_y;
+        bf[oc] = p->bias ? (float)p->bias[oc] * cs[oc] : 0.0f;
+    }
+    /* RQ-B' columns: third NR48 sub-panel of the last block (gemm_int8_avx512.h:1465-1510) */
+    const int b_prime_from = (OC % 48 > 32) ? OC - OC % 48 + 32 : OC;
+    /* tiled im2col (QLinearConv.cpp:1082-1090) */
+    int tile_h = oH;
+    {
+        const size_t TILE_BYTES = 256 * 1024;
+        size_t CHW = (size_t)(p->C / p->group) * p->kH * p->kW;
+        if (CHW * (size_t)sp > TILE_BYTES) {
+            long th = (long)(TILE_BYTES / (CHW * (size_t)oW));
+            tile_h = (int)(th < 1 ? 1 : th);
+            if (tile_h > oH) tile_h = oH;
+        }
+    }
+    #pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+    for (long long no = 0; no < (long long)N * OC; no++) {
+        int n = (int)(no / OC), oc = (int)(no % OC);
+        for (int oh = 0; oh < oH; oh++)
+            for (int ow = 0; ow < oW; ow++) {
+                int s = oh * oW + ow;
+                int32_t a = acc[((size_t)n * OC + oc) * sp + s];
+                int q;
+                int32_t b32 = p->bias ? p->bias[oc] : 0;
+                switch (br) {
+                case ORC_BR_DW:
+                case ORC_BR_IM2COL_S1:
+                    q = orc_rq_a(a, cs[oc], bf[oc], inv_y, p->y_zp, lo, hi);
+                    break;
+                case ORC_BR_FIRST:
+                    if (p->y_nhwc || ow < oW - oW % 16)
+                        q = orc_rq_c(a, cs[oc], bf[oc], inv_y, p->y_zp, qmin, hi);
+                    else
+                        q = orc_rq_a_tail(a, cs[oc], bf[oc], inv_y, p->y_zp, qmin, hi);
+                    break;
+                case ORC_BR_DIRECT:
+                case ORC_BR_FLOAT:
+                    if (s < sp - sp % 16)
+                        q = orc_rq_a(a, cs[oc], bf[oc], inv_y, p->y_zp, qmin, hi);
+                    else
+                        q = orc_rq_a_tail(a, cs[oc], bf[oc], inv_y, p->y_zp, qmin, hi);
+                    break;
+                case ORC_BR_IM2COL: {
+                    int oh0 = (oh / tile_h) * tile_h;
+                    int th = oH - oh0 < tile_h ? oH - oh0 : tile_h;
+                    int tsp = th * oW, ts = (oh - oh0) * oW + ow;
+                    if (ts < tsp - tsp % 16)
+                        q = orc_rq_a(a, cs[oc], bf[oc], inv_y, p->y_zp, qmin, hi);
+                    else
+                        q = orc_rq_a_tail(a, cs[oc], bf[oc], inv_y, p->y_zp, qmin, hi);
+                    break;
+                }
+                case ORC_BR_PACKED:
+                    if (oc >= b_prime_from)
+                        q = orc_rq_b_roundf(a, b32, os[oc], p->y_zp, lo, hi);
+                    else
+                        q = orc_rq_b(a, b32, os[oc], p->y_zp, lo, hi);
+                    break;
+                case ORC_BR_NR16:
+                default:
+                    q = orc_rq_b(a, b32, os[oc], p->y_zp, lo, hi);
+                    break;
+                }
+                size_t di = p->y_nhwc ? (((size_t)n * sp + s) * OC + oc)
+                                      : (((size_t)n * OC + oc) * sp + s);
+                st_q(y, p->act_dtype, di, q);
+            }
+    }
+    free(cs); free(bf); free(os);
+    return br;
+}
+
+int orc_qlinear_conv(const orc_conv_params* p, const void* x, const int8_t* w, void* y) {
+    int32_t* acc = (int32_t*)malloc(sizeof(int32_t) * (size_t)p->N * p->OC * p->oH * p->oW);
+    orc_conv_acc(p, x, w, acc);
+    int br = orc_qlinear_conv_from_acc(p, acc, y);
+    free(acc);
+    return br;
+}
+
+/* ---- QLinearAdd: src/backend/cpu/QLinearAdd.cpp:33-265 ----------------- */
+void orc_qlinear_add(int kind, const void* a, const void* b, void* y, size_t n,
+                     int N, int C, int HW, int y_nhwc, int dt,
+                     float a_s, int a_zp, float b_s, int b_zp, float y_s, int y_zp) {
+    int lo, hi; dtype_range(dt, &lo, &hi);
+    const float sa = a_s / y_s, sb = b_s / y_s;
+    if (kind == ORC_ADD_SAME) {
+        /* :61-104; SIMD body on 16-chunks, scalar tail on the last n%16 */
+        float fixed;
+        if (g_contract) fixed = (float)y_zp - fmaf(sa, (float)a_zp, sb * (float)b_zp);
+        else { float t1 = sa * (float)a_zp, t2 = sb * (float)b_zp; fixed = (float)y_zp - (t1 + t2); }
+        size_t body = n - n % 16;
+        #pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+        for (long long ii = 0; ii < (long long)body; ii++) {
+            size_t i = (size_t)ii;
+            float fa = (float)ld_q(a, dt, i), fb = (float)ld_q(b, dt, i);
+            float v = fmaf(fb, sb, fixed);
+            v = fmaf(fa, sa, v);
+            int r = (int)rintf(v);
+            st_q(y, dt, i, clampi(r, lo, hi));   /* max(.,0)+cvtusepi32 / cvtsepi32 */
+        }
+        for (size_t i = body; i < n; i++) {
+            float da = (float)(ld_q(a, dt, i) - a_zp), db = (float)(ld_q(b, dt, i) - b_zp);
+            float v;
+            if (g_contract) v = fmaf(sa, da, sb * db) + (float)y_zp;
+            else { float t1 = sa * da, t2 = sb * db; v = (t1 + t2) + (float)y_zp; }
+            st_q(y, dt, i, clampi((int)nearbyintf(v), lo, hi));
+        }
+        return;
+    }
+    if (kind == ORC_ADD_B_SCALAR || kind == ORC_ADD_A_SCALAR) {
+        /* :108-119 */
+        int sc_is_b = kind == ORC_ADD_B_SCALAR;
+        float cval = sc_is_b ? sb * (float)(ld_q(b, dt, 0) - b_zp)
+                             : sa * (float)(ld_q(a, dt, 0) - a_zp);
+        for (size_t i = 0; i < n; i++) {
+            float v;
+            if (sc_is_b) v = mul_add_expr(sa, (float)(ld_q(a, dt, i) - a_zp), cval) + (float)y_zp;
+            else { float t = sb * (float)(ld_q(b, dt, i) - b_zp); v = (cval + t) + (float)y_zp; }
+            st_q(y, dt, i, clampi((int)nearbyintf(v), lo, hi));
+        }
+        return;
+    }
+    if (kind == ORC_ADD_PER_CHANNEL) {
+        /* a is full [N,C,H,W] (physical per y_nhwc), b is [C] (:120-226) */
+        const float s_full = sa, s_ch = sb;
+        if (y_nhwc) {
+            float* ch_off = (float*)malloc(sizeof(float) * C);
+            for (int c = 0; c < C; c++)
+                ch_off[c] = mul_add_expr(s_ch, (float)(ld_q(b, dt, c) - b_zp), (float)y_zp);
+            for (size_t pos = 0; pos < (size_t)N * HW; pos++) {
+                int cbody = C - C % 16, c = 0;
+                for (; c < cbody; c++) {
+                    float fa = (float)ld_q(a, dt, pos * C + c);
+                    float v = fmaf(fa - (float)a_zp, s_full, ch_off[c]);
+                    v = rintf(v);
+                    v = clampf_minmax(v, (float)lo, (float)hi);
+                    st_q(y, dt, pos * C + c, (int)v);
+                }
+                for (; c < C; c++) {
+                    float v = mul_add_expr(s_full, (float)(ld_q(a, dt, pos * C + c) - a_zp), ch_off[c]);
+                    st_q(y, dt, pos * C + c, clampi((int)nearbyintf(v), lo, hi));
+                }
+            }
+            free(ch_off);
+        } else {
+            for (size_t nc = 0; nc < (size_t)N * C; nc++) {
+                int c = (int)(nc % C);
+                float ch_val = s_ch * (float)(ld_q(b, dt, c) - b_zp);
+                float voff = ch_val + (float)y_zp;
+                int ibody = HW - HW % 16, i = 0;
+                for (; i < ibody; i++) {
+                    float fa = (float)ld_q(a, dt, nc * HW + i);
+                    float v = fmaf(fa - (float)a_zp, s_full, voff);
+                    v = rintf(v);
+                    v = clampf_minmax(v, (float)lo, (float)hi);
+                    st_q(y, dt, nc * HW + i, (int)v);
+                }
+                for (; i < HW; i++) {
+                    float v = mul_add_expr(s_full, (float)(ld_q(a, dt, nc * HW + i) - a_zp), ch_val) + (float)y_zp;
+                    st_q(y, dt, nc * HW + i, clampi((int)nearbyintf(v), lo, hi));
+                }
+            }
+        }
+    }
+}
+
+/* ---- MaxPool uint8 NHWC: src/backend/x64/pool_x64.h:396-436 ------------ */
+void orc_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH,
+                         int iW, int oH, int oW, int kH, int kW, int sH, int sW,
+                         int pH, int pW) {
+    #pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+    for (long long r = 0; r < (long long)N * oH; r++) {
+        int n = (int)(r / oH), oh = (int)(r % oH);
+        int ih0 = oh * sH - pH;
+        int kh0 = ih0 < 0 ? -ih0 : 0, kh1 = kH < iH - ih0 ? kH : iH - ih0;
+        for (int ow = 0; ow < oW; ow++) {
+            int iw0 = ow * sW - pW;
+            int kw0 = iw0 < 0 ? -iw0 : 0, kw1 = kW < iW - iw0 ? kW : iW - iw0;
+            for (int c = 0; c < C; c++) {
+                uint8_t m = 0;
+                for (int a = kh0; a < kh1; a++)
+                    for (int b = kw0; b < kw1; b++) {
+                        uint8_t v = x[(((size_t)n * iH + ih0 + a) * iW + (iw0 + b)) * C + c];
+                        if (v > m) m = v;
+                    }
+                y[(((size_t)n * oH + oh) * oW + ow) * C + c] = m;
+            }
+        }
+    }
+}
+
+void orc_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C, int HW) {
+    for (int n = 0; n < N; n++)
+        for (int c = 0; c < C; c++)
+            for (int s = 0; s < HW; s++)
+                y[((size_t)n * HW + s) * C + c] = x[((size_t)n * C + c) * HW + s];
+}

@@ -1,0 +1,228 @@
+"""GPU parity: every HIP path against the CPU oracle, bit-exact, through the C
+ABI (nnr_amd is a ctypes view of include/nnr_hip.h). Covers every kernel
+branch of QLinearConv's dispatch, QLinearMatMul / MatMulInteger shapes and
+dtypes, and the element-wise ops, including tails and edge shapes."""
+import numpy as np
+import pytest
+
+import nnr_amd as H
+from oracle import pyoracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def to_np(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+# ---------------------------------------------------------------------------
+# QLinearMatMul
+
+def test_qmatmul_config1(dev):
+    """cfg1: A u8[1024,768] x B i8[768,3072] -> u8, per-tensor scales."""
+    rng = np.random.default_rng(1)
+    a = rng.integers(0, 256, (1024, 768), dtype=np.uint8)
+    b = rng.integers(-127, 128, (768, 3072), dtype=np.int8)
+    ref = O.qlinear_matmul(a, 0.02, 128, b, 0.005, 0, 0.05, 128)
+    op = H.QLinearMatMul(b, 0.02, 128, 0.005, 0, 0.05, 128, m=1024)
+    y = to_np(op(to_dev(a, dev)))
+    assert np.array_equal(y, ref)
+
+
+MM_CASES = [
+    # m, n, k, batch, a_dt, b_dt, y_dt, b_zp, scale_dt
+    (5, 70, 100, 1, np.uint8, np.int8, np.uint8, 0, np.float32),
+    (33, 64, 3, 1, np.uint8, np.int8, np.uint8, 0, np.float32),
+    (128, 768, 768, 4, np.uint8, np.int8, np.uint8, 0, np.float32),
+    (17, 130, 72, 3, np.int8, np.int8, np.int8, -3, np.float32),
+    (64, 96, 64, 1, np.uint8, np.uint8, np.uint8, 114, np.float32),
+    (7, 50, 40, 2, np.uint8, np.int8, np.uint8, 0, np.float16),
+    (300, 257, 129, 1, np.int8, np.uint8, np.uint8, 7, np.float32),
+]
+
+
+@pytest.mark.parametrize("m,n,k,batch,adt,bdt,ydt,bzp,sdt", MM_CASES)
+def test_qmatmul_shapes(dev, m, n, k, batch, adt, bdt, ydt, bzp, sdt):
+    rng = np.random.default_rng(m * 1000 + n + k)
+    info = lambda t: (np.iinfo(t).min, np.iinfo(t).max + 1)
+    a = rng.integers(*info(adt), (batch, m, k), dtype=adt)
+    b = rng.integers(*info(bdt), (k, n), dtype=bdt)
+    a_zp = 121 if adt == np.uint8 else -9
+    y_zp = 128 if ydt == np.uint8 else 3
+    ref = O.qlinear_matmul(a, 0.021, a_zp, b, 0.0047, bzp, 0.31, y_zp, ydt, sdt)
+    op = H.QLinearMatMul(b, 0.021, a_zp, 0.0047, bzp, 0.31, y_zp, m=m, a_dtype=adt, y_dtype=ydt,
+                         scale_dtype=sdt)
+    y = to_np(op(to_dev(a, dev)))
+    assert np.array_equal(y, ref)
+
+
+def test_qmatmul_device_quant_params(dev):
+    """a_scale / a_zp from device memory (the DynamicQuantizeLinear hand-off)."""
+    import torch
+    rng = np.random.default_rng(21)
+    a = rng.integers(0, 256, (2, 40, 96), dtype=np.uint8)
+    b = rng.integers(-127, 128, (96, 80), dtype=np.int8)
+    ref = O.qlinear_matmul(a, np.float32(0.0133), 77, b, 0.004, 0, 0.02, 128)
+    op = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, 0.02, 128, m=40)
+    s = torch.tensor([0.0133], dtype=torch.float32, device=dev)
+    z = torch.tensor([77], dtype=torch.uint8, device=dev)
+    y = to_np(op(to_dev(a, dev), a_scale_dev=s, a_zp_dev=z))
+    assert np.array_equal(y, ref)
+
+
+@pytest.mark.parametrize("m,n,k,adt,bdt,azp,bzp,batch", [
+    (64, 64, 64, np.uint8, np.int8, 128, 0, 1),
+    (19, 45, 27, np.int8, np.uint8, -4, 200, 1),
+    (128, 200, 300, np.uint8, np.uint8, 3, 250, 3),
+    (50, 33, 16, np.int8, np.int8, 0, -7, 2),
+])
+def test_matmul_integer(dev, m, n, k, adt, bdt, azp, bzp, batch):
+    rng = np.random.default_rng(5 + m)
+    info = lambda t: (np.iinfo(t).min, np.iinfo(t).max + 1)
+    a = rng.integers(*info(adt), (batch, m, k), dtype=adt)
+    b = rng.integers(*info(bdt), (batch, k, n), dtype=bdt)
+    ref = O.matmul_integer(a, b, azp, bzp)
+    op = H.MatMulInteger(m, n, k, adt, bdt, max_batch=batch)
+    y = to_np(op(to_dev(a, dev), to_dev(b, dev), azp, bzp, batch=batch))
+    assert np.array_equal(y.reshape(ref.shape), ref)
+
+
+# ---------------------------------------------------------------------------
+# QLinearConv
+
+def run_conv_case(dev, N, C, Hh, W, OC, k, seed, expect=None, x_nhwc=0, bias=True, **kw):
+    rng = np.random.default_rng(seed)
+    act = kw.get("act_dtype", np.uint8)
+    G = kw.get("group", 1)
+    info = (0, 256) if act == np.uint8 else (-128, 128)
+    x = rng.integers(*info, (N, C, Hh, W), dtype=act)
+    w = rng.integers(-127, 128, (OC, C // G, k, k), dtype=np.int8)
+    kw.setdefault("w_scale", rng.uniform(0.001, 0.01, OC).astype(np.float32))
+    kw.setdefault("x_scale", 0.02)
+    kw.setdefault("x_zp", 128 if act == np.uint8 else -5)
+    kw.setdefault("y_scale", 0.03)
+    b = rng.integers(-4096, 4097, OC).astype(np.int32) if bias else None
+    xin = x.transpose(0, 2, 3, 1).copy() if x_nhwc else x
+    ocv = O.Conv(N, C, Hh, W, OC, k, k, x_nhwc=x_nhwc, bias=b, **kw)
+    ref, br = ocv.run(xin, w)
+    op = H.QLinearConv(N, C, Hh, W, w, x_nhwc=x_nhwc, bias=b, **kw)
+    assert op.branch == br
+    if expect is not None:
+        assert H.BRANCH_NAMES[br] == expect
+    y = to_np(op(to_dev(xin, dev)))
+    assert y.shape == ref.shape
+    mism = np.count_nonzero(y != ref)
+    assert mism == 0, f"{mism} of {y.size} differ (branch {H.BRANCH_NAMES[br]})"
+
+
+def test_qconv_config2(dev):
+    """cfg2: 3x3 s1 p1, x u8[32,64,56,56] NCHW, per-channel w scales, Relu via
+    y_zp 0 and a fused Relu (post_fn) -> NR16 NHWC-direct, RQ-B."""
+    run_conv_case(dev, 32, 64, 56, 56, 64, 3, seed=2, expect="NR16", pads=(1, 1, 1, 1),
+                  y_nhwc=1, post_fn=1, y_zp=0, x_zp=128)
+
+
+CONV_CASES = [
+    # name, N, C, H, W, OC, k, kwargs
+    ("nr16_nhwc_in", 2, 64, 14, 15, 128, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1, y_zp=3)),
+    ("packed_1x1", 2, 256, 7, 9, 64, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=7)),
+    ("packed_bprime", 1, 32, 6, 7, 48 + 40, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=11)),
+    ("packed_s2", 2, 64, 13, 13, 96, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1)),
+    ("packed_wzp", 1, 48, 9, 9, 40, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, w_zp=(3,))),
+    ("packed_nchw_out", 1, 32, 20, 20, 24, 3, dict(pads=(1, 1, 1, 1), y_nhwc=0)),
+    ("packed_dil", 1, 16, 12, 12, 32, 3, dict(pads=(2, 2, 2, 2), dil=(2, 2), y_nhwc=1)),
+    ("packed_c24", 2, 24, 10, 10, 144, 1, dict(y_nhwc=1, x_nhwc=1)),
+    ("direct", 2, 64, 12, 12, 64, 3, dict(pads=(1, 1, 1, 1), y_nhwc=0, post_fn=1, y_zp=9)),
+    ("direct_tail", 1, 20, 9, 7, 30, 3, dict(pads=(1, 1, 1, 1), y_nhwc=0, y_zp=20)),
+    ("first_nhwc", 2, 3, 40, 40, 64, 7, dict(stride=(2, 2), pads=(3, 3, 3, 3), y_nhwc=1)),
+    ("first_nchw", 1, 3, 37, 37, 32, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=0,
+                                               post_fn=1, y_zp=4)),
+    ("dw_s1", 2, 32, 10, 11, 32, 3, dict(group=32, pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1)),
+    ("dw_s2", 1, 96, 15, 15, 96, 3, dict(group=96, stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1,
+                                          x_nhwc=1, y_zp=2)),
+    ("dw_nchw_s1", 1, 16, 9, 9, 16, 3, dict(group=16, pads=(1, 1, 1, 1), y_nhwc=0)),
+    ("dw_nchw_s2", 1, 16, 9, 9, 16, 3, dict(group=16, stride=(2, 2), pads=(1, 1, 1, 1),
+                                            y_nhwc=0, post_fn=1, y_zp=6)),
+    ("grouped_s1", 1, 16, 8, 8, 32, 3, dict(group=4, pads=(1, 1, 1, 1))),
+    ("grouped_s2", 1, 32, 11, 11, 16, 3, dict(group=2, stride=(2, 2), pads=(1, 1, 1, 1),
+                                              post_fn=1, y_zp=12)),
+    ("float_int8act", 1, 16, 9, 9, 24, 3, dict(pads=(1, 1, 1, 1), act_dtype=np.int8, y_zp=-4)),
+    ("float_pcz", 1, 16, 8, 8, 4, 1, dict(w_zp=(1, -2, 3, 0))),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=[c[0] for c in CONV_CASES])
+def test_qconv_branches(dev, case):
+    name, N, C, Hh, W, OC, k, kw = case
+    kw = dict(kw)
+    x_nhwc = kw.pop("x_nhwc", 0)
+    run_conv_case(dev, N, C, Hh, W, OC, k, seed=sum(name.encode()), x_nhwc=x_nhwc, **kw)
+
+
+def test_qconv_no_bias(dev):
+    run_conv_case(dev, 1, 64, 10, 10, 64, 3, seed=5, bias=False, pads=(1, 1, 1, 1), y_nhwc=1)
+
+
+# ---------------------------------------------------------------------------
+# element-wise
+
+@pytest.mark.parametrize("n", [40, 64, 70, 4096 + 21, 300000])
+@pytest.mark.parametrize("dt", [np.uint8, np.int8])
+def test_quantize(dev, n, dt):
+    rng = np.random.default_rng(n)
+    x = rng.normal(0, 2, n).astype(np.float32)
+    zp = 128 if dt == np.uint8 else -3
+    ref = O.quantize_linear(x, 0.0173, zp, dt)
+    y = to_np(H.quantize_linear(to_dev(x, dev), 0.0173, zp, dt))
+    assert np.array_equal(y, ref)
+
+
+def test_dequantize(dev):
+    rng = np.random.default_rng(3)
+    for dt in (np.uint8, np.int8):
+        q = rng.integers(np.iinfo(dt).min, np.iinfo(dt).max + 1, 10007, dtype=dt)
+        ref = O.dequantize_linear(q, 0.0371, 17)
+        y = to_np(H.dequantize_linear(to_dev(q, dev), 0.0371, 17))
+        assert np.array_equal(y, ref)
+
+
+@pytest.mark.parametrize("n", [6, 1000, 98304 * 3 + 5])
+def test_dynamic_quantize(dev, n):
+    rng = np.random.default_rng(n)
+    x = (rng.normal(0, 1.5, n) + 0.3).astype(np.float32)
+    y_ref, s_ref, z_ref = O.dynamic_quantize_linear(x)
+    y, s, z = H.dynamic_quantize_linear(to_dev(x, dev))
+    assert to_np(s)[0] == np.float32(s_ref) and int(to_np(z)[0]) == z_ref
+    assert np.array_equal(to_np(y), y_ref)
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2, 3])
+@pytest.mark.parametrize("y_nhwc", [0, 1])
+def test_qlinear_add(dev, kind, y_nhwc):
+    rng = np.random.default_rng(kind * 10 + y_nhwc)
+    N, C, HW = 3, 40, 37
+    n = N * C * HW
+    a = rng.integers(0, 256, n, dtype=np.uint8)
+    b = rng.integers(0, 256, {0: n, 1: 1, 2: n, 3: C}[kind], dtype=np.uint8)
+    if kind == 2:
+        a, b = rng.integers(0, 256, 1, dtype=np.uint8), a
+    args = (0.031, 117, 0.017, 131, 0.043, 3)
+    ref = O.qlinear_add(kind, a, b, *args, C=C, HW=HW, y_nhwc=y_nhwc)
+    y = to_np(H.qlinear_add(kind, to_dev(a, dev), to_dev(b, dev), *args, C=C, HW=HW,
+                            y_nhwc=y_nhwc))
+    assert np.array_equal(y, ref)
+
+
+def test_maxpool(dev):
+    rng = np.random.default_rng(6)
+    x = rng.integers(0, 256, (4, 23, 21, 64), dtype=np.uint8)
+    ref = O.maxpool_u8_nhwc(x, 3, 3, 2, 2, 1, 1, 12, 11)
+    y = to_np(H.maxpool_u8_nhwc(to_dev(x, dev), 3, 3, 2, 2, 1, 1, 12, 11))
+    assert np.array_equal(y, ref)

@@ -1,0 +1,416 @@
+"""Pins the CPU oracle (oracle/nnr_oracle.c) before it is trusted as the
+parity checker. Each test checks the oracle against something it does not
+share code with: brute-force integer arithmetic in numpy, exact rational
+arithmetic (fractions), the ONNX specification's published examples, or
+hand-derived known answers that separate the reference's formula variants
+(RNE vs roundf, zero point before vs after rounding, fma vs mul+add,
+multiply-by-reciprocal vs divide)."""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle import pyoracle as O
+
+
+def f32(v):
+    return np.float32(v)
+
+
+def rne_f32(fr: Fraction) -> np.float32:
+    """Round an exact rational to the nearest binary32 (ties to even)."""
+    x = np.float32(float(fr))          # correctly rounded to f64 then f32: fix by search
+    cands = [np.nextafter(x, np.float32(-np.inf)), x, np.nextafter(x, np.float32(np.inf))]
+    best = min(cands, key=lambda c: (abs(Fraction(float(c)) - fr),
+                                     int(np.array(c).view(np.uint32)) & 1))
+    return np.float32(best)
+
+
+def exact_fma(a, b, c):
+    return rne_f32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def rne_int(fr: Fraction) -> int:
+    fl = fr.numerator // fr.denominator
+    rem = fr - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        return fl + 1
+    return fl
+
+
+# --------------------------------------------------------------------------
+# integer accumulators: brute force in int64
+
+
+def brute_conv(x_nchw, w, x_zp, w_zp_oc, stride, dil, pads, group):
+    N, C, H, W = x_nchw.shape
+    OC, Cg, kH, kW = w.shape
+    oH = (H + pads[0] + pads[2] - ((kH - 1) * dil[0] + 1)) // stride[0] + 1
+    oW = (W + pads[1] + pads[3] - ((kW - 1) * dil[1] + 1)) // stride[1] + 1
+    xp = np.full((N, C, H + pads[0] + pads[2], W + pads[1] + pads[3]), x_zp, np.int64)
+    xp[:, :, pads[0]:pads[0] + H, pads[1]:pads[1] + W] = x_nchw
+    xp -= x_zp
+    out = np.zeros((N, OC, oH, oW), np.int64)
+    OCg = OC // group
+    for oc in range(OC):
+        g = oc // OCg
+        wk = w[oc].astype(np.int64) - w_zp_oc[oc]
+        for a in range(kH):
+            for b in range(kW):
+                patch = xp[:, g * Cg:(g + 1) * Cg,
+                           a * dil[0]: a * dil[0] + (oH - 1) * stride[0] + 1: stride[0],
+                           b * dil[1]: b * dil[1] + (oW - 1) * stride[1] + 1: stride[1]]
+                out[:, oc] += np.einsum("nchw,c->nhw", patch, wk[:, a, b])
+    return out
+
+
+CONV_CASES = [
+    # N C H W OC k group stride dil pads  w_zp
+    (2, 8, 7, 6, 5, 3, 1, (1, 1), (1, 1), (1, 1, 1, 1), ()),
+    (1, 6, 9, 9, 6, 3, 6, (2, 2), (1, 1), (1, 1, 1, 1), (3,)),
+    (2, 4, 8, 8, 8, 3, 2, (1, 2), (2, 1), (2, 0, 1, 2), ()),
+    (1, 3, 11, 10, 16, 7, 1, (2, 2), (1, 1), (3, 3, 3, 3), ()),
+    (1, 5, 5, 5, 4, 1, 1, (1, 1), (1, 1), (0, 0, 0, 0), (-7, 2, 0, 5)),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+@pytest.mark.parametrize("x_nhwc", [0, 1])
+def test_conv_acc_bruteforce(case, x_nhwc):
+    N, C, H, W, OC, k, G, st, dl, pads, wzp = case
+    rng = np.random.default_rng(7)
+    x = rng.integers(0, 256, (N, C, H, W), dtype=np.uint8)
+    w = rng.integers(-128, 128, (OC, C // G, k, k), dtype=np.int8)
+    cv = O.Conv(N, C, H, W, OC, k, k, group=G, stride=st, dil=dl, pads=pads, x_nhwc=x_nhwc,
+                x_zp=131, w_zp=np.array(wzp, np.int8) if wzp else ())
+    br = cv.dispatch()
+    # the VNNI branches read w_zp through the activation type (uint8)
+    raw = np.array(wzp if wzp else [0], np.int64)
+    if br != O.BR["FLOAT"]:
+        raw = raw.astype(np.int8).astype(np.uint8).astype(np.int64)
+    zp_oc = np.broadcast_to(raw, (OC,)) if raw.size == 1 else raw
+    xin = x.transpose(0, 2, 3, 1).copy() if x_nhwc else x
+    acc = cv.acc(xin, w)
+    ref = brute_conv(x.astype(np.int64), w, 131, zp_oc, st, dl, pads, G)
+    assert np.array_equal(acc.astype(np.int64), ref)
+
+
+def test_matmul_integer_bruteforce():
+    rng = np.random.default_rng(3)
+    for (ad, bd, at, bt) in [((5, 7), (7, 3), np.uint8, np.int8),
+                             ((2, 4, 9), (9, 6), np.int8, np.uint8),
+                             ((3, 1, 4, 5), (2, 5, 2), np.uint8, np.uint8),
+                             ((6,), (6, 4), np.int8, np.int8)]:
+        a = rng.integers(np.iinfo(at).min, np.iinfo(at).max + 1, ad, dtype=at)
+        b = rng.integers(np.iinfo(bt).min, np.iinfo(bt).max + 1, bd, dtype=bt)
+        y = O.matmul_integer(a, b, 12, -5)
+        ref = np.matmul(a.astype(np.int64) - 12, b.astype(np.int64) + 5)
+        assert np.array_equal(y.reshape(ref.shape), ref)
+
+
+# --------------------------------------------------------------------------
+# requantize known answers
+
+
+def test_rq_b_rne_vs_roundf():
+    L = O.lib()
+    # os = 0.5: acc 1 -> 0.5, 5 -> 2.5: RNE gives 0 / 2, roundf gives 1 / 3
+    assert L.orc_rq_b(1, 0, 0.5, 0, 0, 255) == 0
+    assert L.orc_rq_b_roundf(1, 0, 0.5, 0, 0, 255) == 1
+    assert L.orc_rq_b(5, 0, 0.5, 0, 0, 255) == 2
+    assert L.orc_rq_b_roundf(5, 0, 0.5, 0, 0, 255) == 3
+    # bias is added in int32 before scaling, zero point after rounding
+    assert L.orc_rq_b(3, 2, 0.5, 127, 0, 255) == 127 + 2      # 2.5 -> 2
+    # saturation at both ends and the [lo-zp, hi-zp] clamp
+    assert L.orc_rq_b(10**6, 0, 1.0, 10, 0, 255) == 255
+    assert L.orc_rq_b(-10**6, 0, 1.0, 10, 0, 255) == 0
+    # int32 wrap of acc + bias
+    assert L.orc_rq_b(2**31 - 1, 1, 1e-9, 0, 0, 255) == 0        # wraps to -2^31 -> -2.1 -> 0
+
+
+def test_rq_d_zero_point_before_rounding():
+    L = O.lib()
+    # RQ-D adds y_zp before rounding: 0.5 + 127 = 127.5 -> 128 (RNE)
+    assert L.orc_rq_d(1, 0.5, 127, 0, 255) == 128
+    # RQ-B adds it after: rne(0.5) + 127 = 127
+    assert L.orc_rq_b(1, 0, 0.5, 127, 0, 255) == 127
+    assert L.orc_rq_d(1, 0.5, 128, 0, 255) == 128               # 128.5 -> 128
+    assert L.orc_rq_d(-3, 1.0, -126, -128, 127) == -128
+
+
+def test_rq_a_clamp_floor_and_tail():
+    L = O.lib()
+    # L = qmin (fused Relu with y_zp 10) vs lo
+    assert L.orc_rq_a(-100, 1.0, 0.0, 1.0, 10, 10, 255) == 10
+    assert L.orc_rq_a(-100, 1.0, 0.0, 1.0, 10, 0, 255) == 0
+    assert L.orc_rq_a_tail(-100, 1.0, 0.0, 1.0, 10, 10, 255) == 10
+    # RQ-C: y_zp inside the second fma, clamp before rounding
+    assert L.orc_rq_c(5, 0.5, 0.0, 1.0, 3, 0, 255) == 6        # 2.5 + 3 = 5.5 -> 6
+    assert L.orc_rq_a(5, 0.5, 0.0, 1.0, 3, 0, 255) == 5        # rne(2.5) + 3 = 5
+
+
+def test_rq_a_single_rounding_fma():
+    """RQ-A rounds acc*cs+bf once; RQ-A' (uncontracted) twice. Find inputs
+    where that changes the output and check both against exact arithmetic."""
+    L = O.lib()
+    rng = np.random.default_rng(11)
+    found = 0
+    for _ in range(20000):
+        acc = int(rng.integers(-2**20, 2**20))
+        cs = f32(rng.uniform(1e-4, 1e-2))
+        bf = f32(rng.uniform(-5, 5))
+        inv = f32(1.0) / f32(rng.uniform(0.01, 0.1))
+        fm = exact_fma(f32(acc), cs, bf)
+        two = f32(f32(f32(acc) * cs) + bf)
+        q1 = rne_int(Fraction(float(f32(fm * inv))))
+        q2 = rne_int(Fraction(float(f32(two * inv))))
+        exp_a = int(np.clip(q1 + 7, 0, 255))
+        assert L.orc_rq_a(acc, cs, bf, inv, 7, 0, 255) == exp_a
+        assert L.orc_rq_a_tail(acc, cs, bf, inv, 7, 0, 255) == int(np.clip(q2 + 7, 0, 255))
+        if q1 != q2:
+            found += 1
+    assert found > 0
+
+
+# --------------------------------------------------------------------------
+# Quantize / Dequantize / DynamicQuantize
+
+
+def _div_mul_disagree(rng):
+    """x, s with rne(x*fl(1/s)) != rne(x/s)."""
+    while True:
+        s = f32(rng.uniform(0.003, 0.2))
+        k = int(rng.integers(-100, 100))
+        x = f32((k + 0.5) * float(s))
+        for cand in (x, np.nextafter(x, f32(np.inf)), np.nextafter(x, f32(-np.inf))):
+            a = rne_int(Fraction(float(f32(cand * (f32(1.0) / s)))))
+            b = rne_int(Fraction(float(f32(cand / s))))
+            if a != b and 0 <= a + 100 <= 255 and 0 <= b + 100 <= 255:
+                return cand, s, a, b
+
+
+def test_quantize_body_vs_tail():
+    rng = np.random.default_rng(5)
+    x0, s, q_mul, q_div = _div_mul_disagree(rng)
+    for n in (40, 64, 70, 4096 + 21):
+        x = np.full(n, x0, np.float32)
+        y = O.quantize_linear(x, s, 100).astype(int)
+        if n < 64:
+            assert (y == q_div + 100).all()
+        else:
+            body = n - n % 16
+            assert (y[:body] == q_mul + 100).all()
+            assert (y[body:] == q_div + 100).all()
+
+
+def test_quantize_saturation_int8():
+    y = O.quantize_linear(np.array([-1e6, 1e6, 0.26, -0.26] * 20, np.float32), 0.1, -3, np.int8)
+    assert list(y[:4]) == [-128, 127, 0, -6]
+
+
+def test_dequantize_exact():
+    q = np.arange(256, dtype=np.uint8)
+    y = O.dequantize_linear(q, 0.37, 129)
+    assert np.array_equal(y, ((q.astype(np.float32) - np.float32(129)) * np.float32(0.37)))
+
+
+# ONNX operator documentation examples (DynamicQuantizeLinear)
+DQL_SPEC = [
+    ([0, 2, -3, -2.5, 1.34, 0.5], [153, 255, 0, 26, 221, 179], 0.0196078438, 153),
+    ([-1.0, -2.1, -1.3, -2.5, -3.34, -4.0], [191, 121, 172, 96, 42, 0], 0.0156862754, 255),
+    ([1, 2.1, 1.3, 2.5, 3.34, 4.0, 1.5, 2.6, 3.9, 4.0, 3.0, 2.345],
+     [64, 134, 83, 159, 213, 255, 96, 166, 249, 255, 191, 149], 0.0156862754, 0),
+]
+
+
+@pytest.mark.parametrize("x,y,s,z", DQL_SPEC)
+def test_dynamic_quantize_spec(x, y, s, z):
+    yy, ss, zz = O.dynamic_quantize_linear(np.array(x, np.float32))
+    assert list(yy) == y and zz == z
+    assert abs(ss - s) < 1e-9
+
+
+def test_dynamic_quantize_formula():
+    rng = np.random.default_rng(2)
+    x = rng.normal(0, 3, 1000).astype(np.float32)
+    y, s, z = O.dynamic_quantize_linear(x)
+    mn, mx = min(0.0, float(x.min())), max(0.0, float(x.max()))
+    assert s == f32(f32(mx - mn) / f32(255.0))
+    for v, q in zip(x[:200], y[:200]):
+        assert q == np.clip(rne_int(Fraction(float(f32(v / f32(s))))) + z, 0, 255)
+
+
+# --------------------------------------------------------------------------
+# QLinearMatMul
+
+def test_qlinear_matmul_spec_example():
+    a = np.array([[208, 236, 0, 238], [3, 214, 255, 29]], np.uint8)
+    b = np.array([[152, 51, 244], [60, 26, 255], [0, 127, 246], [127, 254, 247]], np.uint8)
+    y = O.qlinear_matmul(a, 0.0066, 113, b, 0.00705, 114, 0.0107, 118)
+    assert y.tolist() == [[168, 115, 255], [1, 66, 151]]
+
+
+def test_qlinear_matmul_exact_against_rationals():
+    rng = np.random.default_rng(9)
+    a = rng.integers(0, 256, (3, 17), dtype=np.uint8)
+    b = rng.integers(-127, 128, (17, 5), dtype=np.int8)
+    y = O.qlinear_matmul(a, 0.02, 128, b, 0.005, 0, 0.05, 128)
+    acc = (a.astype(np.int64) - 128) @ b.astype(np.int64)
+    cm = f32(f32(f32(0.02) * f32(0.005)) / f32(0.05))
+    for i in range(3):
+        for j in range(5):
+            v = f32(f32(f32(acc[i, j]) * cm) + f32(128))
+            assert y[i, j] == np.clip(rne_int(Fraction(float(v))), 0, 255)
+
+
+def test_f16_conversion_matches_numpy():
+    rng = np.random.default_rng(4)
+    vals = np.concatenate([rng.uniform(-70000, 70000, 3000), rng.uniform(-1, 1, 3000),
+                           rng.uniform(-1e-4, 1e-4, 3000)]).astype(np.float32)
+    L = O.lib()
+    for v in vals:
+        if abs(v) < 2.0 ** -24:       # the reference flushes below 2^-24 (nnrconf.h:172)
+            continue
+        h = L.orc_f32_to_f16(float(v))
+        with np.errstate(over="ignore"):
+            ref = np.float16(v)
+        assert h == int(np.array(ref).view(np.uint16)), v
+        assert L.orc_f16_to_f32(h) == np.float32(ref)
+
+
+def test_combined_scale_fp16():
+    cm = O.qmatmul_combined_scale(0.1, 0.2, 0.3, np.float16)
+    h = np.float16(np.float32(np.float16(np.float32(np.float16(0.1)) * np.float32(np.float16(0.2))))
+                   / np.float32(np.float16(0.3)))
+    assert cm == np.float32(h)
+
+
+# --------------------------------------------------------------------------
+# QLinearAdd
+
+def test_qlinear_add_identity_scales():
+    rng = np.random.default_rng(1)
+    a = rng.integers(0, 256, 1000, dtype=np.uint8)
+    b = rng.integers(0, 256, 1000, dtype=np.uint8)
+    y = O.qlinear_add(0, a, b, 0.1, 0, 0.1, 0, 0.1, 0)
+    assert np.array_equal(y, np.clip(a.astype(int) + b, 0, 255).astype(np.uint8))
+
+
+def test_qlinear_add_same_shape_exact():
+    rng = np.random.default_rng(8)
+    n = 16 * 10 + 7
+    a = rng.integers(0, 256, n, dtype=np.uint8)
+    b = rng.integers(0, 256, n, dtype=np.uint8)
+    a_s, b_s, y_s = f32(0.031), f32(0.017), f32(0.043)
+    y = O.qlinear_add(0, a, b, a_s, 117, b_s, 131, y_s, 3)
+    sa, sb = f32(a_s / y_s), f32(b_s / y_s)
+    fixed = f32(f32(3) - f32(f32(sa * f32(117)) + f32(sb * f32(131))))
+    body = n - n % 16
+    for i in range(n):
+        if i < body:
+            v = exact_fma(f32(a[i]), sa, exact_fma(f32(b[i]), sb, fixed))
+        else:
+            v = f32(f32(f32(sa * f32(int(a[i]) - 117)) + f32(sb * f32(int(b[i]) - 131))) + f32(3))
+        assert y[i] == np.clip(rne_int(Fraction(float(v))), 0, 255)
+
+
+# --------------------------------------------------------------------------
+# MaxPool
+
+def test_maxpool_bruteforce():
+    rng = np.random.default_rng(6)
+    x = rng.integers(0, 256, (2, 9, 10, 5), dtype=np.uint8)
+    y = O.maxpool_u8_nhwc(x, 3, 3, 2, 2, 1, 1, 5, 5)
+    for n in range(2):
+        for oh in range(5):
+            for ow in range(5):
+                h0, w0 = oh * 2 - 1, ow * 2 - 1
+                win = x[n, max(0, h0):h0 + 3, max(0, w0):w0 + 3]
+                assert np.array_equal(y[n, oh, ow], win.reshape(-1, 5).max(0))
+
+
+# --------------------------------------------------------------------------
+# QLinearConv: dispatch table and closed forms
+
+
+def _w(OC, Cg, k):
+    return np.zeros((OC, Cg, k, k), np.int8)
+
+
+@pytest.mark.parametrize("kw,expect", [
+    # cfg2: 3x3 s1 p1, IC/OC 64, NHWC out -> NR16 direct
+    (dict(N=32, C=64, H=56, W=56, OC=64, k=3, pads=(1, 1, 1, 1), y_nhwc=1), "NR16"),
+    # ResNet stem 7x7 s2 IC3, NCHW in -> first layer
+    (dict(N=1, C=3, H=224, W=224, OC=64, k=7, stride=(2, 2), pads=(3, 3, 3, 3), y_nhwc=1), "FIRST"),
+    # 1x1 / strided 3x3 -> packed NR48
+    (dict(N=1, C=256, H=56, W=56, OC=64, k=1, y_nhwc=1), "PACKED"),
+    (dict(N=1, C=128, H=56, W=56, OC=128, k=3, stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1), "PACKED"),
+    # small spatial with NCHW output -> direct
+    (dict(N=1, C=64, H=14, W=14, OC=64, k=3, pads=(1, 1, 1, 1), y_nhwc=0), "DIRECT"),
+    # same with NHWC output -> NR16
+    (dict(N=1, C=64, H=14, W=14, OC=64, k=3, pads=(1, 1, 1, 1), y_nhwc=1), "NR16"),
+    # depthwise NHWC -> DW; depthwise NCHW out -> im2col
+    (dict(N=1, C=32, H=8, W=8, OC=32, k=3, group=32, pads=(1, 1, 1, 1), y_nhwc=1), "DW"),
+    (dict(N=1, C=32, H=8, W=8, OC=32, k=3, group=32, pads=(1, 1, 1, 1), y_nhwc=0), "IM2COL_S1"),
+    (dict(N=1, C=32, H=8, W=8, OC=32, k=3, group=32, stride=(2, 2), pads=(1, 1, 1, 1)), "IM2COL"),
+    # grouped conv
+    (dict(N=1, C=8, H=8, W=8, OC=8, k=3, group=2, pads=(1, 1, 1, 1)), "IM2COL_S1"),
+    # int8 activations / per-channel w_zp -> float fallback
+    (dict(N=1, C=8, H=8, W=8, OC=8, k=3, act_dtype=np.int8, x_zp=0), "FLOAT"),
+    (dict(N=1, C=8, H=8, W=8, OC=4, k=1, w_zp=(1, 2, 3, 4)), "FLOAT"),
+    # all-equal per-channel zp collapses to per-tensor
+    (dict(N=1, C=8, H=8, W=8, OC=4, k=1, w_zp=(2, 2, 2, 2), y_nhwc=1), "PACKED"),
+])
+def test_conv_dispatch_table(kw, expect):
+    kw = dict(kw)
+    k = kw.pop("k")
+    args = [kw.pop(n) for n in ("N", "C", "H", "W", "OC")]
+    cv = O.Conv(*args[:5], k, k, **kw)
+    assert cv.dispatch() == O.BR[expect]
+
+
+@pytest.mark.parametrize("y_nhwc", [0, 1])
+def test_conv_unit_scale_closed_form(y_nhwc):
+    """scales 1 and zero points 0: every branch reduces to clamp(acc + bias)."""
+    rng = np.random.default_rng(12)
+    x = rng.integers(0, 4, (1, 8, 6, 6), dtype=np.uint8)
+    w = rng.integers(-3, 4, (16, 8, 3, 3), dtype=np.int8)
+    bias = rng.integers(-20, 20, 16).astype(np.int32)
+    cv = O.Conv(1, 8, 6, 6, 16, 3, 3, pads=(1, 1, 1, 1), y_nhwc=y_nhwc, x_scale=1.0, x_zp=0,
+                w_scale=[1.0], y_scale=1.0, y_zp=0, bias=bias)
+    y, br = cv.run(x, w)
+    ref = brute_conv(x.astype(np.int64), w, 0, np.zeros(16, np.int64), (1, 1), (1, 1),
+                     (1, 1, 1, 1), 1) + bias[None, :, None, None]
+    ref = np.clip(ref, 0, 255)
+    if y_nhwc:
+        ref = ref.transpose(0, 2, 3, 1)
+    assert np.array_equal(y.astype(np.int64), ref)
+
+
+def test_conv_branch_formulas_from_acc():
+    """Each branch applies its own formula to the same accumulators."""
+    rng = np.random.default_rng(13)
+    N, C, H, W, OC = 1, 64, 4, 5, 48 + 40      # OC % 48 = 40 > 32: RQ-B' columns exist
+    cv = O.Conv(N, C, H, W, OC, 1, 1, y_nhwc=1, x_scale=0.013, x_zp=120,
+                w_scale=rng.uniform(0.001, 0.01, OC).astype(np.float32), y_scale=0.031, y_zp=5,
+                bias=rng.integers(-4096, 4096, OC))
+    assert cv.dispatch() == O.BR["PACKED"]
+    acc = rng.integers(-200000, 200000, (N, OC, H, W)).astype(np.int32)
+    y, br = cv.from_acc(acc)
+    L = O.lib()
+    cs = (np.float32(0.013) * cv.w_scale).astype(np.float32)
+    os_ = (cs * (np.float32(1) / np.float32(0.031))).astype(np.float32)
+    for oc in range(OC):
+        for h in range(H):
+            for w_ in range(W):
+                a = int(acc[0, oc, h, w_])
+                v = a + int(cv.bias[oc])
+                f = f32(f32(v) * os_[oc])
+                f = min(max(f, f32(-5)), f32(250))
+                if oc >= 48 + 32:     # third sub-panel of the partial block: roundf
+                    q = int(np.sign(f) * np.floor(abs(float(f)) + 0.5)) + 5
+                else:
+                    q = rne_int(Fraction(float(f))) + 5
+                assert y[0, h, w_, oc] == np.clip(q, 0, 255)
+    # the roundf columns really differ somewhere from an RNE epilogue
+    assert L.orc_rq_b_roundf(5, 0, 0.5, 0, 0, 255) != L.orc_rq_b(5, 0, 0.5, 0, 0, 255)
