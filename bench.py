@@ -1,0 +1,263 @@
+#!/usr/bin/env python3
+"""Benchmark of the int8 QDQ path on one MI355X.
+
+Prints ONE JSON line (driver contract). Workloads:
+  resnet50  cfg3 (default, the headline metric): ResNet-50 v1.5 int8 QDQ graph,
+            batch 256, 224x224, run through the C++ host framework (QDQ
+            fusion, NHWC layouts, HIP operators); value = images/s
+  qconv     cfg2: QLinearConv 3x3 s1 p1, x u8[32,64,56,56], per-channel w
+A step is one pass of the path over one batch; inputs are resident in HBM
+when the timed region starts. Before timing, the GPU output is checked
+bit-exact against the CPU oracle. The `roofline` object is measured live
+with hipEvents around every launch of the dominant kernel (the library's
+launch profiler); the `cpu_baseline` leg times the oracle on host cores on a
+bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "int8 TOPS + % i8 MFMA peak per layer; ResNet-50-int8 images/sec b256, 1 GPU"
+PEAK_I8_TOPS = 5000.0      # MI355X dense int8 MFMA, TOPS
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, GB/s
+
+
+def host_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except Exception:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def make_qconv(rng, N=32):
+    import numpy as np
+    x = rng.integers(0, 256, (N, 64, 56, 56), dtype=np.uint8)
+    w = rng.integers(-127, 128, (64, 64, 3, 3), dtype=np.int8)
+    ws = rng.uniform(0.001, 0.01, 64).astype(np.float32)
+    b = rng.integers(-4096, 4097, 64).astype(np.int32)
+    kw = dict(pads=(1, 1, 1, 1), y_nhwc=1, post_fn=1, x_scale=0.02, x_zp=128, w_scale=ws,
+              y_scale=0.03, y_zp=0, bias=b)
+    ops = 2.0 * N * 64 * 56 * 56 * 64 * 9
+    # algorithmic bytes: x + y + w + per-channel params (scale f32 + bias i32)
+    nbytes = N * 64 * 56 * 56 * 2 + 64 * 64 * 9 + 64 * 8
+    return x, w, kw, ops, nbytes
+
+
+def run_qconv(args, dev):
+    import numpy as np
+    import torch
+
+    import nnr_amd as H
+    from nnr_amd import _lib
+    rng = np.random.default_rng(2)
+    x, w, kw, ops, nbytes = make_qconv(rng)
+    op = H.QLinearConv(32, 64, 56, 56, w, **kw)
+    xd = torch.from_numpy(x).to(dev)
+    yd = torch.empty(op.out_shape, dtype=torch.uint8, device=dev)
+    # parity gate (bit-exact vs the oracle) before timing
+    from oracle import pyoracle as O
+    ref, br = O.Conv(32, 64, 56, 56, 64, 3, 3, **kw).run(x, w)
+    op(xd, yd)
+    torch.cuda.synchronize()
+    assert br == op.branch and np.array_equal(yd.cpu().numpy(), ref), "parity gate failed"
+    ms = time_steps(lambda: op(xd, yd), args)
+    prof = profile_steps(lambda: op(xd, yd), args)
+    g_launches, g_ms = prof["qgemm"]
+    kern_ms = g_ms / g_launches
+    # cpu baseline: the oracle on a bounded sample (4 of the 32 images)
+    nthr = host_threads()
+    O.set_threads(nthr)
+    xs = x[:4].copy()
+    oc = O.Conv(4, 64, 56, 56, 64, 3, 3, **kw)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        oc.run(xs, w)
+        reps += 1
+        if time.perf_counter() - t0 > 3.0 or reps >= 50:
+            break
+    cpu_s = (time.perf_counter() - t0) / reps
+    cpu_tops = ops / 8 / cpu_s / 1e12
+    tops = ops / (ms * 1e-3) / 1e12
+    return dict(
+        metric=METRIC, value=round(tops, 3), unit="TOPS", ms_per_step=ms,
+        config={"workload": "cfg2 QLinearConv 3x3 s1 p1 x u8[32,64,56,56] w i8[64,64,3,3] "
+                            "per-channel scales, fused Relu, NHWC out (NR16 branch, RQ-B)",
+                "global_batch": 32, "branch": H.BRANCH_NAMES[op.branch]},
+        roofline=roofline(ops, nbytes, kern_ms, prof),
+        cpu_baseline={"value": round(cpu_tops, 4), "unit": "TOPS", "cores": nthr, "kind": "port",
+                      "sample": "oracle QLinearConv (scalar C, OpenMP) on 4 of the 32 images, "
+                                f"mean of {reps} runs"},
+        dtype="u8",
+    )
+
+
+def time_steps(fn, args) -> float:
+    import torch
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / args.steps
+
+
+def profile_steps(fn, args) -> dict:
+    """Per-kernel launch times over K steps (hipEvents around each launch)."""
+    import torch
+    from nnr_amd import _lib
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    for _ in range(args.steps):
+        fn()
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    out = _lib.profile_read()
+    _lib.profile_reset()
+    return out
+
+
+def roofline(ops, nbytes, kern_ms, prof):
+    t_mfma = ops / (PEAK_I8_TOPS * 1e12)
+    t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
+    achieved_tops = ops / (kern_ms * 1e-3) / 1e12
+    r = {"kernel": "qgemm_kernel", "bound": "mfma", "achieved": round(achieved_tops, 2),
+         "peak": PEAK_I8_TOPS, "unit": "TOPS", "frac": round(achieved_tops / PEAK_I8_TOPS, 4),
+         "traffic": None, "avg_launch_ms": round(kern_ms, 5),
+         "alg_ops_per_launch": ops, "alg_bytes_per_launch": nbytes,
+         "bound_model": "mfma" if t_mfma >= t_hbm else "hbm",
+         "launches": {k: {"n": v[0], "avg_ms": round(v[1] / max(1, v[0]), 5)}
+                      for k, v in prof.items()}}
+    return r
+
+
+def run_resnet50(args, dev):
+    import numpy as np
+    import torch
+
+    from nnr_amd import _lib, graph as G, synth
+    from oracle import graph_oracle
+    from oracle import pyoracle as O
+
+    B = args.batch
+    g = synth.resnet50(batch=B, hw=224)
+    rng = np.random.default_rng(10)
+    x = rng.random((B, 3, 224, 224), dtype=np.float32)
+    s = G.Session(g)
+    s.set_input("input", x)
+    s.run()
+    torch.cuda.synchronize()
+    plan = s.plan()
+    fmt = lambda n: s.tensor_info(n)[3]
+    # parity gate: the oracle replays the plan on the first images of the batch
+    ng = 2
+    env = graph_oracle.run_plan(plan, g, {"input": x[:ng]}, fmt)
+    for p in plan:
+        o = p["outputs"][0]
+        dev_t, _ = s.output(o)
+        if dev_t.dtype in (np.uint8, np.int8):
+            assert np.array_equal(dev_t[:ng], env[o]), f"parity gate failed at {p['name']}"
+        else:
+            assert np.allclose(dev_t[:ng], env[o], atol=1e-3, rtol=1e-4), p["name"]
+    ms = time_steps(s.run, args)
+    # per-layer times (hipEvents around every node) and per-kernel times
+    s.enable_profiling(True)
+    for _ in range(args.steps):
+        s.run()
+    torch.cuda.synchronize()
+    prof = s.profile()
+    s.enable_profiling(False)
+    kprof = profile_steps(s.run, args)
+    conv_ops = sum(r["ops"] for r in prof if r["op"] == "QLinearConv")
+    g_launches, g_ms = kprof["qgemm"]
+    qgemm_ms_per_step = g_ms / args.steps
+    layers = []
+    for r in prof:
+        t = r["ms"] / max(1, r["runs"])
+        row = {"name": r["name"], "op": r["op"], "branch": r["variant"], "ms": round(t, 4)}
+        if r["ops"]:
+            row["tops"] = round(r["ops"] / (t * 1e-3) / 1e12, 1)
+            row["pct_i8_peak"] = round(100 * row["tops"] / PEAK_I8_TOPS, 2)
+        else:
+            row["gbs"] = round(r["bytes"] / (t * 1e-3) / 1e9, 1)
+            row["pct_hbm"] = round(100 * row["gbs"] / PEAK_HBM_GBS, 2)
+        layers.append(row)
+    if args.layers_out:
+        with open(args.layers_out, "w") as f:
+            json.dump(layers, f, indent=1)
+    for row in layers:
+        print(json.dumps(row), file=sys.stderr)
+    # roofline of the dominant kernel over all its launches in a step
+    avg_launch = qgemm_ms_per_step / (g_launches / args.steps)
+    ops_per_launch = conv_ops / (g_launches / args.steps)
+    conv_bytes = sum(r["bytes"] for r in prof if r["op"] == "QLinearConv")
+    rl = roofline(ops_per_launch, conv_bytes / (g_launches / args.steps), avg_launch, kprof)
+    rl["note"] = ("achieved = total algorithmic conv ops of one step / total qgemm_kernel time "
+                  "of one step (53 launches, hipEvents per launch)")
+    # cpu baseline: the oracle replays the plan on one image
+    nthr = host_threads()
+    O.set_threads(nthr)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        graph_oracle.run_plan(plan, g, {"input": x[:1]}, fmt)
+        reps += 1
+        if time.perf_counter() - t0 > 5.0 or reps >= 5:
+            break
+    cpu_img_s = reps / (time.perf_counter() - t0)
+    imgs = B / (ms * 1e-3)
+    return dict(
+        metric=METRIC, value=round(imgs, 1), unit="images/s", ms_per_step=ms,
+        config={"workload": f"cfg3 ResNet-50 v1.5 int8 QDQ, batch {B}, 224x224 (53 QLinearConv, "
+                            "16 QLinearAdd, uint8 MaxPool, fp32 GAP+FC)", "global_batch": B,
+                "branches": {b: sum(1 for p in plan if p["variant"] == b)
+                             for b in ("FIRST", "NR16", "PACKED")},
+                "conv_tops": round(conv_ops / (qgemm_ms_per_step * 1e-3) / 1e12, 1),
+                "device_bytes": s.device_bytes()},
+        roofline=rl,
+        cpu_baseline={"value": round(cpu_img_s, 3), "unit": "images/s", "cores": nthr,
+                      "kind": "port", "sample": f"oracle replay of the fused plan on 1 image, "
+                                                f"{reps} runs (scalar C + OpenMP)"},
+        dtype="u8",
+    )
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="resnet50", choices=["resnet50", "qconv"])
+    ap.add_argument("--batch", type=int, default=256)
+    ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    res = run_resnet50(args, dev) if args.config == "resnet50" else run_qconv(args, dev)
+    line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": res["dtype"], "data": "synthetic (seeded, BASELINE.json config)",
+            "config": res["config"], "roofline": res["roofline"],
+            "cpu_baseline": res["cpu_baseline"]}
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

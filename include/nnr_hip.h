@@ -62,6 +62,16 @@ int nnrh_event_destroy(void* event);
 int nnrh_event_record(void* event, void* stream);
 int nnrh_event_elapsed_ms(float* ms, void* start, void* stop);
 
+/* ---- profiling ------------------------------------------------------------
+ * Counterpart of context_t::enable_profiling / dump_profile (src/nnr.h:518-520,
+ * src/nnr.cpp:801-846): when enabled, every kernel launch of this library is
+ * bracketed by hipEvents on its stream and accumulated per kernel name.
+ * Reading the totals synchronizes the recorded events.                    */
+int nnrh_profile_enable(int on);
+int nnrh_profile_reset(void);
+int nnrh_profile_count(int* n_kernels);
+int nnrh_profile_get(int index, const char** name, int* launches, double* total_ms);
+
 /* ---- QLinearConv ---------------------------------------------------------
  * Replaces QLinearConv_operator (src/backend/cpu/QLinearConv.cpp:30-1371):
  * init() attribute parsing (:91-156), reshape() weight pre-packing and
@@ -178,6 +188,19 @@ int nnrh_maxpool_u8_nhwc(const uint8_t* x_dev, uint8_t* y_dev, int N, int C,
 /* ---- layout: NCHW -> NHWC uint8 (transpose_nchw_nhwc_u8.h:1-126) -------- */
 int nnrh_nchw_to_nhwc_u8(const uint8_t* x_dev, uint8_t* y_dev, int N, int C,
                          int HW, void* stream);
+
+/* ---- fp32 glue of the configuration graphs ------------------------------
+ * GlobalAveragePool (src/backend/cpu/global_pool.cpp): x [N][C][HW] or
+ * [N][HW][C] (x_nhwc) -> y [N][C].                                        */
+int nnrh_global_avgpool_f32(const float* x_dev, float* y_dev, int N, int C, int HW,
+                            int x_nhwc, void* stream);
+/* Gemm (src/backend/cpu/Gemm.cpp): Y = alpha*op(A)*op(B) + beta*C, row-major;
+ * c_mode: 0 no C, 1 scalar, 2 [N], 3 [M][N], 4 [M] (broadcast per row).   */
+int nnrh_gemm_f32(const float* a_dev, const float* b_dev, const float* c_dev, float* y_dev,
+                  int M, int N, int K, int trans_a, int trans_b, float alpha, float beta,
+                  int c_mode, void* stream);
+/* Clip / Relu (src/backend/cpu/Clip.cpp, Relu.cpp): y = min(max(x, lo), hi) */
+int nnrh_clip_f32(const float* x_dev, float* y_dev, size_t n, float lo, float hi, void* stream);
 
 #ifdef __cplusplus
 }

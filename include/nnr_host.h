@@ -1,0 +1,77 @@
+/*
+ * nnr_host.h -- C ABI of the host framework (nnr_amd/host, libnnr_host.so).
+ *
+ * The reference's user-facing entry is context_t (src/nnr.h:482-612):
+ * load() a model, prepare(), run(), then read outputs, with
+ * preferred_backend choosing the operator implementations (nnr.h:589) and
+ * enable_profiling()/dump_profile() (nnr.h:518-520). This header exposes the
+ * same lifecycle over a C ABI for language bindings. The configurations are
+ * synthetic graphs built in memory, so graph construction replaces the ONNX
+ * loader: initializers, inputs, outputs and nodes are added one by one
+ * exactly as onnx_build_graph does per NodeProto (onnx_loader.cpp:595-653).
+ */
+#ifndef NNR_HOST_H
+#define NNR_HOST_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct nnr_ctx* nnr_ctx_t;
+
+/* backend ids (registry.h backend_t): 0 CPU, 4 HIP */
+enum { NNR_BACKEND_CPU = 0, NNR_BACKEND_HIP = 4 };
+/* attribute kinds */
+enum { NNR_ATTR_INT = 0, NNR_ATTR_FLOAT = 1, NNR_ATTR_STRING = 2, NNR_ATTR_INTS = 3,
+       NNR_ATTR_FLOATS = 4 };
+
+const char* nnr_last_error(void);
+int nnr_ctx_create(nnr_ctx_t* ctx, int preferred_backend);
+int nnr_ctx_destroy(nnr_ctx_t ctx);
+int nnr_ctx_set_stream(nnr_ctx_t ctx, void* stream);
+int nnr_ctx_set_fusion(nnr_ctx_t ctx, int on);
+
+/* dtype: ONNX TensorProto element type (1 float, 2 uint8, 3 int8, 6 int32, 7 int64, 10 f16) */
+int nnr_ctx_add_initializer(nnr_ctx_t ctx, const char* name, int dtype, const int* dims,
+                            int ndim, const void* host_data);
+int nnr_ctx_add_input(nnr_ctx_t ctx, const char* name, int dtype, const int* dims, int ndim);
+int nnr_ctx_add_output(nnr_ctx_t ctx, const char* name);
+/* attributes: parallel arrays; for each attribute i, kinds[i] selects the
+ * value: INT -> ints[offs[i]], FLOAT -> floats[offs[i]], INTS/FLOATS ->
+ * counts[i] values from offs[i], STRING -> strings[i]. */
+int nnr_ctx_add_node(nnr_ctx_t ctx, const char* op_type, const char* name, int n_in,
+                     const char* const* inputs, int n_out, const char* const* outputs, int n_attr,
+                     const char* const* attr_names, const int* kinds, const int* counts,
+                     const int* offs, const int64_t* ints, const float* floats,
+                     const char* const* strings);
+
+/* graph passes, shape inference and layout assignment only: no device
+ * memory, no kernel state (usable without a GPU) */
+int nnr_ctx_optimize(nnr_ctx_t ctx);
+int nnr_ctx_prepare(nnr_ctx_t ctx);
+int nnr_ctx_run(nnr_ctx_t ctx);
+
+/* device pointer, dtype, dims and layout (0 NCHW, 1 NHWC) of a tensor */
+int nnr_ctx_tensor(nnr_ctx_t ctx, const char* name, void** data_dev, int* dtype, int* dims,
+                   int* ndim, int* format);
+
+/* executed plan after prepare(): active node i */
+int nnr_ctx_node_count(nnr_ctx_t ctx, int* n);
+int nnr_ctx_node_info(nnr_ctx_t ctx, int i, const char** op_type, const char** name,
+                      const char** variant, int* post_fn, int* n_in, int* n_out);
+int nnr_ctx_node_io(nnr_ctx_t ctx, int i, int is_output, int j, const char** tensor_name);
+int nnr_ctx_fusion_stat(nnr_ctx_t ctx, const char* key, int* value);
+size_t nnr_ctx_device_bytes(nnr_ctx_t ctx);
+
+/* per-node hipEvent timing (context_t::enable_profiling / dump_profile) */
+int nnr_ctx_enable_profiling(nnr_ctx_t ctx, int on);
+int nnr_ctx_profile(nnr_ctx_t ctx, int i, double* total_ms, int* runs, double* ops,
+                    double* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NNR_HOST_H */

@@ -23,12 +23,13 @@ EXPORTS = [
     "nnrh_malloc", "nnrh_free", "nnrh_memcpy", "nnrh_fill_u8", "nnrh_stream_create",
     "nnrh_stream_destroy", "nnrh_stream_synchronize", "nnrh_device_synchronize",
     "nnrh_event_create", "nnrh_event_destroy", "nnrh_event_record", "nnrh_event_elapsed_ms",
+    "nnrh_profile_enable", "nnrh_profile_reset", "nnrh_profile_count", "nnrh_profile_get",
     "nnrh_qconv_dispatch", "nnrh_qconv_create", "nnrh_qconv_branch", "nnrh_qconv_run",
     "nnrh_qconv_destroy", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
     "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
     "nnrh_dynamic_quantize_linear", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
-    "nnrh_nchw_to_nhwc_u8",
+    "nnrh_nchw_to_nhwc_u8", "nnrh_global_avgpool_f32", "nnrh_gemm_f32", "nnrh_clip_f32",
 ]
 
 
@@ -89,6 +90,10 @@ def lib():
         "nnrh_event_destroy": (i, [vp]),
         "nnrh_event_record": (i, [vp, vp]),
         "nnrh_event_elapsed_ms": (i, [P(f), vp, vp]),
+        "nnrh_profile_enable": (i, [i]),
+        "nnrh_profile_reset": (i, []),
+        "nnrh_profile_count": (i, [P(i)]),
+        "nnrh_profile_get": (i, [i, P(C.c_char_p), P(i), P(C.c_double)]),
         "nnrh_qconv_dispatch": (i, [P(QConvDesc), P(i)]),
         "nnrh_qconv_create": (i, [P(vp), P(QConvDesc)]),
         "nnrh_qconv_branch": (i, [vp, P(i)]),
@@ -107,6 +112,9 @@ def lib():
         "nnrh_qlinear_add": (i, [i, vp, vp, vp, sz, i, i, i, i, f, i, f, i, f, i, vp]),
         "nnrh_maxpool_u8_nhwc": (i, [vp, vp] + [i] * 12 + [vp]),
         "nnrh_nchw_to_nhwc_u8": (i, [vp, vp, i, i, i, vp]),
+        "nnrh_global_avgpool_f32": (i, [vp, vp, i, i, i, i, vp]),
+        "nnrh_gemm_f32": (i, [vp, vp, vp, vp, i, i, i, i, i, f, f, i, vp]),
+        "nnrh_clip_f32": (i, [vp, vp, sz, f, f, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -132,6 +140,27 @@ def ptr(t) -> int:
     if hasattr(t, "ctypes"):
         return t.ctypes.data
     raise TypeError(type(t))
+
+
+def profile_enable(on: bool = True) -> None:
+    check(lib().nnrh_profile_enable(1 if on else 0))
+
+
+def profile_reset() -> None:
+    check(lib().nnrh_profile_reset())
+
+
+def profile_read() -> dict:
+    """{kernel name: (launches, total_ms)} accumulated since the last reset."""
+    L = lib()
+    n = C.c_int()
+    check(L.nnrh_profile_count(C.byref(n)))
+    out = {}
+    for i in range(n.value):
+        name, cnt, ms = C.c_char_p(), C.c_int(), C.c_double()
+        check(L.nnrh_profile_get(i, C.byref(name), C.byref(cnt), C.byref(ms)))
+        out[name.value.decode()] = (cnt.value, ms.value)
+    return out
 
 
 def cur_stream() -> int:

@@ -18,6 +18,7 @@
 
 #include "nnr_hip.h"
 #include "nnrh_elem.h"
+#include "nnrh_f32.h"
 #include "nnrh_internal.h"
 
 using namespace nnrh;
@@ -70,6 +71,66 @@ int conv_out_dim(int in, int k, int d, int s, int pb, int pe) {
     int ek = (k - 1) * d + 1;
     return (int)floorf((float)(in + pb + pe - ek) / (float)s + 1.0f);
 }
+
+// ---- launch profiler (hipEvent pairs per kernel name) ----------------------
+struct ProfEntry {
+    std::string name;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
+    int launches = 0;
+    double total_ms = 0.0;
+};
+struct Profiler {
+    bool on = false;
+    std::vector<ProfEntry> entries;
+    std::vector<hipEvent_t> pool;
+    hipEvent_t get() {
+        if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        return e;
+    }
+    ProfEntry& entry(const char* n) {
+        for (auto& e : entries) if (e.name == n) return e;
+        entries.push_back(ProfEntry{});
+        entries.back().name = n;
+        return entries.back();
+    }
+    void flush() {
+        for (auto& e : entries) {
+            for (auto& pr : e.ev) {
+                float ms = 0.f;
+                (void)hipEventSynchronize(pr.second);
+                if (hipEventElapsedTime(&ms, pr.first, pr.second) == hipSuccess) {
+                    e.total_ms += ms;
+                    e.launches++;
+                }
+                pool.push_back(pr.first);
+                pool.push_back(pr.second);
+            }
+            e.ev.clear();
+        }
+    }
+};
+Profiler g_prof;
+
+// RAII bracket around one launch
+struct ProfScope {
+    hipEvent_t a = nullptr, b = nullptr;
+    hipStream_t s;
+    const char* name;
+    ProfScope(const char* n, hipStream_t st) : s(st), name(n) {
+        if (!g_prof.on) return;
+        a = g_prof.get();
+        b = g_prof.get();
+        if (a) (void)hipEventRecord(a, s);
+    }
+    ~ProfScope() {
+        if (!a || !b) return;
+        (void)hipEventRecord(b, s);
+        g_prof.entry(name).ev.emplace_back(a, b);
+        if (g_prof.entry(name).ev.size() > 4096) g_prof.flush();
+    }
+};
 
 int pick_vec(int c_or_k, int stride, uintptr_t base) {
     if (c_or_k % 16 == 0 && stride % 16 == 0 && (base & 15) == 0) return 16;
@@ -166,6 +227,31 @@ int nnrh_event_elapsed_ms(float* ms, void* a, void* b) {
 }
 
 }  // extern "C"
+
+extern "C" int nnrh_profile_enable(int on) {
+    g_prof.on = on != 0;
+    return NNRH_OK;
+}
+extern "C" int nnrh_profile_reset(void) {
+    g_prof.flush();
+    g_prof.entries.clear();
+    return NNRH_OK;
+}
+extern "C" int nnrh_profile_count(int* n) {
+    if (!n) return set_err(NNRH_ERR_INVALID, "profile_count: NULL");
+    g_prof.flush();
+    *n = (int)g_prof.entries.size();
+    return NNRH_OK;
+}
+extern "C" int nnrh_profile_get(int i, const char** name, int* launches, double* total_ms) {
+    g_prof.flush();
+    if (i < 0 || i >= (int)g_prof.entries.size() || !name || !launches || !total_ms)
+        return set_err(NNRH_ERR_INVALID, "profile_get: bad index or NULL");
+    *name = g_prof.entries[i].name.c_str();
+    *launches = g_prof.entries[i].launches;
+    *total_ms = g_prof.entries[i].total_ms;
+    return NNRH_OK;
+}
 
 // ===========================================================================
 // QLinearConv
@@ -473,12 +559,14 @@ extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stre
     hipStream_t s = S(stream);
     const uint8_t* src = (const uint8_t*)x;
     if (h->transform) {
+        ProfScope ps("nchw_to_nhwc_u8", s);
         HIP_TRY(launch_nchw_to_nhwc_u8(src, h->xs, d.N, d.C, d.H * d.W, h->Cx,
                                        (uint8_t)(d.x_zp & 0xff), s),
                 "nchw_to_nhwc");
         src = h->xs;
     }
     if (h->use_dw) {
+        ProfScope ps("depthwise", s);
         HIP_TRY(launch_depthwise(src, h->wpack, (uint8_t*)y, h->cs, h->bf, d.N, d.C, d.H, d.W, d.oH,
                                  d.oW, d.kH, d.kW, d.sH, d.sW, d.dH, d.dW, d.pad_t, d.pad_l, d.x_zp,
                                  h->w_zp_scalar, h->inv_y, d.y_zp, h->dw_L, d.act_dtype == NNRH_U8 ? 255 : 127,
@@ -488,6 +576,7 @@ extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stre
     }
     if (h->need_rowsum) {
         const int Cg = h->g.C;
+        ProfScope ps("rowsum", s);
         HIP_TRY(launch_rowsum_conv(src, d.N, d.H, d.W, h->Cx, Cg, h->groups, d.oH, d.oW, d.kH, d.kW,
                                    d.sH, d.sW, d.dH, d.dW, d.pad_t, d.pad_l, d.act_dtype == NNRH_S8,
                                    d.x_zp, h->rowsum, s),
@@ -498,6 +587,7 @@ extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stre
     g.y = y;
     int vec = h->vec;
     if (vec > 1 && ((uintptr_t)src & (vec - 1))) vec = 1;
+    ProfScope ps("qgemm", s);
     HIP_TRY(launch_qgemm(g, h->groups, h->tile, vec, s), "qgemm");
     return NNRH_OK;
 }
@@ -669,6 +759,7 @@ extern "C" int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a, long long a_bst
             if (rc) return rc;
             h->rowsum_cap = batch;
         }
+        ProfScope ps("rowsum", s);
         HIP_TRY(launch_rowsum_dense((const uint8_t*)a, g.lda, a_bstride, g.M, g.K, g.a_xor == 0,
                                     h->a_zp, a_zp_dev, h->rowsum, batch, s),
                 "rowsum_dense");
@@ -676,6 +767,7 @@ extern "C" int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a, long long a_bst
     }
     int vec = pick_vec(g.K, (int)g.lda, (uintptr_t)a);
     if (a_bstride % vec) vec = 1;
+    ProfScope ps("qgemm", s);
     HIP_TRY(launch_qgemm(g, batch, pick_tile(g.N), vec, s), "qgemm");
     return NNRH_OK;
 }
@@ -728,6 +820,7 @@ extern "C" int nnrh_matmul_integer_run(nnrh_matmul_integer_t h, const void* a, l
     hipStream_t s = S(stream);
     const bool au8 = h->a_dtype == NNRH_U8, bu8 = h->b_dtype == NNRH_U8;
     const int nb_b = b_bstride == 0 ? 1 : batch;
+    ProfScope ps0("pack_b", s);
     HIP_TRY(launch_pack_b_dense(b, b_bstride, h->k, h->n, h->Kp, h->Np, bu8 ? 0x80 : 0, h->bpack,
                                 (long long)h->Np * h->Kp, h->colsum, h->Np, nb_b, s),
             "pack_b");
@@ -760,6 +853,7 @@ extern "C" int nnrh_matmul_integer_run(nnrh_matmul_integer_t h, const void* a, l
     g.bprime_from = h->n;
     int vec = pick_vec(h->k, h->k, (uintptr_t)a);
     if (a_bstride % vec) vec = 1;
+    ProfScope ps("qgemm", s);
     HIP_TRY(launch_qgemm(g, batch, pick_tile(h->n), vec, s), "qgemm");
     return NNRH_OK;
 }
@@ -776,6 +870,7 @@ extern "C" int nnrh_quantize_linear(const float* x, size_t n, float scale, int z
                                     void* stream) {
     if (n && (!x || !y)) return set_err(NNRH_ERR_INVALID, "quantize: NULL");
     if (y_dtype != NNRH_U8 && y_dtype != NNRH_S8) return set_err(NNRH_ERR_UNSUPPORTED, "quantize: dtype");
+    ProfScope ps("quantize", S(stream));
     HIP_TRY(launch_quantize(x, (long long)n, scale, zp, y_dtype == NNRH_U8 ? 0 : 1, y, S(stream)), "quantize");
     return NNRH_OK;
 }
@@ -785,6 +880,7 @@ extern "C" int nnrh_dequantize_linear(const void* x, int x_dtype, size_t n, floa
     if (n && (!x || !y)) return set_err(NNRH_ERR_INVALID, "dequantize: NULL");
     int dt = x_dtype == NNRH_U8 ? 0 : x_dtype == NNRH_S8 ? 1 : x_dtype == NNRH_I32 ? 2 : -1;
     if (dt < 0) return set_err(NNRH_ERR_UNSUPPORTED, "dequantize: dtype");
+    ProfScope ps("dequantize", S(stream));
     HIP_TRY(launch_dequantize(x, (long long)n, dt, scale, zp, y, S(stream)), "dequantize");
     return NNRH_OK;
 }
@@ -795,6 +891,7 @@ extern "C" int nnrh_dynamic_quantize_linear(const float* x, size_t n, uint8_t* y
                                             uint8_t* y_zp, void* ws, void* stream) {
     if (!y_scale || !y_zp || !ws || (n && (!x || !y)))
         return set_err(NNRH_ERR_INVALID, "dynamic_quantize: NULL");
+    ProfScope ps("dynamic_quantize", S(stream));
     HIP_TRY(launch_dynamic_quantize(x, (long long)n, y, y_scale, y_zp, ws, S(stream)), "dynamic_quantize");
     return NNRH_OK;
 }
@@ -829,6 +926,7 @@ extern "C" int nnrh_qlinear_add(int kind, const void* a, const void* b, void* y,
         int v = dtype == NNRH_U8 ? (int)raw : (int)(int8_t)raw;
         p.cval = kind == 1 ? p.sb * (float)(v - b_zp) : p.sa * (float)(v - a_zp);
     }
+    ProfScope ps("qlinear_add", S(stream));
     HIP_TRY(launch_qadd(p, S(stream)), "qlinear_add");
     return NNRH_OK;
 }
@@ -838,6 +936,7 @@ extern "C" int nnrh_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, 
     if (!x || !y) return set_err(NNRH_ERR_INVALID, "maxpool: NULL");
     if (N <= 0 || C <= 0 || oH <= 0 || oW <= 0 || kH <= 0 || kW <= 0 || sH <= 0 || sW <= 0)
         return set_err(NNRH_ERR_INVALID, "maxpool: bad shape");
+    ProfScope ps("maxpool_u8", S(stream));
     HIP_TRY(launch_maxpool_u8_nhwc(x, y, N, C, iH, iW, oH, oW, kH, kW, sH, sW, pH, pW, S(stream)), "maxpool");
     return NNRH_OK;
 }
@@ -845,5 +944,32 @@ extern "C" int nnrh_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, 
 extern "C" int nnrh_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C, int HW, void* stream) {
     if (!x || !y) return set_err(NNRH_ERR_INVALID, "nchw_to_nhwc: NULL");
     HIP_TRY(launch_nchw_to_nhwc_u8(x, y, N, C, HW, C, 0, S(stream)), "nchw_to_nhwc");
+    return NNRH_OK;
+}
+
+// ===========================================================================
+// fp32 glue
+
+extern "C" int nnrh_global_avgpool_f32(const float* x, float* y, int N, int C, int HW, int x_nhwc,
+                                       void* stream) {
+    if (!x || !y || N <= 0 || C <= 0 || HW <= 0) return set_err(NNRH_ERR_INVALID, "gap: bad args");
+    ProfScope ps("gap_f32", S(stream));
+    HIP_TRY(launch_gap_f32(x, y, N, C, HW, x_nhwc, S(stream)), "gap_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_gemm_f32(const float* a, const float* b, const float* cb, float* y, int M, int N,
+                             int K, int ta, int tb, float alpha, float beta, int c_mode, void* stream) {
+    if (!a || !b || !y || M <= 0 || N <= 0 || K <= 0 || c_mode < 0 || c_mode > 4 || (c_mode && !cb))
+        return set_err(NNRH_ERR_INVALID, "gemm_f32: bad args");
+    ProfScope ps("gemm_f32", S(stream));
+    HIP_TRY(launch_gemm_f32(a, b, cb, y, M, N, K, ta, tb, alpha, beta, c_mode, S(stream)), "gemm_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_clip_f32(const float* x, float* y, size_t n, float lo, float hi, void* stream) {
+    if (n && (!x || !y)) return set_err(NNRH_ERR_INVALID, "clip_f32: NULL");
+    ProfScope ps("clip_f32", S(stream));
+    HIP_TRY(launch_clip_f32(x, y, (long long)n, lo, hi, S(stream)), "clip_f32");
     return NNRH_OK;
 }

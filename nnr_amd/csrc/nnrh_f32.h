@@ -1,0 +1,17 @@
+// nnrh_f32.h -- launchers of the fp32 glue kernels (nnrh_f32.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace nnrh {
+
+hipError_t launch_gap_f32(const float* x, float* y, int N, int C, int HW, int x_nhwc,
+                          hipStream_t s);
+// c_mode: 0 none, 1 scalar, 2 per-column [N], 3 full [M][N], 4 per-row [M]
+hipError_t launch_gemm_f32(const float* A, const float* B, const float* C, float* Y, int M, int N,
+                           int K, int transA, int transB, float alpha, float beta, int c_mode,
+                           hipStream_t s);
+hipError_t launch_clip_f32(const float* x, float* y, long long n, float lo, float hi,
+                           hipStream_t s);
+
+}  // namespace nnrh

@@ -87,7 +87,7 @@ __device__ __forceinline__ void load_bytes(const GemmArgs& g, const uint8_t* aba
 }
 
 template <int BM, int BN, int VEC, int AMODE>
-__global__ __launch_bounds__(256) void qgemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256, 2) void qgemm_kernel(GemmArgs g) {
     constexpr int WAVES_N = BN / 64;
     constexpr int WAVES_M = BM / 64;
     static_assert(WAVES_N * WAVES_M == 4, "4 waves of 64x64");
@@ -284,7 +284,9 @@ __global__ __launch_bounds__(256) void qgemm_kernel(GemmArgs g) {
         __syncthreads();
     }
 
-    // ---- epilogue: lane owns columns nb..nb+15 of rows m0 + wm*64 + 16*tm + frow
+    // ---- epilogue: lane owns columns nb..nb+15 of rows m0 + wm*64 + 16*tm + frow.
+    // Processed 4 columns (one MFMA tile tn) at a time to keep registers low;
+    // the four bytes of each (tm, tn) pack into one dword, stored per tm.
     const int nb = n0 + wn * 64 + 16 * fchunk;
     if (nb >= g.N) return;
     int alpha = g.alpha;
@@ -299,111 +301,130 @@ __global__ __launch_bounds__(256) void qgemm_kernel(GemmArgs g) {
         cm = t1 / g.cm_y;
     }
     const long long po = (long long)z * g.param_bstride;
-    int32_t colc[16], betac[16];
-    float p0[16], p1[16];
-    int32_t bias[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        int n = nb + i;
-        bool ok = n < g.N;
-        colc[i] = (ok && g.colsum) ? wrap_mul(alpha, g.colsum[po + n]) : 0;
-        betac[i] = g.beta_col ? (ok ? g.beta_col[po + n] : 0) : g.beta;
-        bias[i] = (ok && g.bias) ? g.bias[po + n] : 0;
-        if (g.epi == EPI_RQB) {
-            p0[i] = ok ? g.os[po + n] : 0.f;
-            p1[i] = 0.f;
-        } else if (g.epi == EPI_RQA || g.epi == EPI_RQC) {
-            p0[i] = ok ? g.cs[po + n] : 0.f;
-            p1[i] = ok ? g.bf[po + n] : 0.f;
-        } else {
-            p0[i] = 0.f; p1[i] = 0.f;
-        }
-    }
     const int sp = g.oH * g.oW;
     const bool full16 = (nb + 16 <= g.N);
+    int rs[4];
+    bool tail[4];
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) {
         const int m = m0 + wm * 64 + tm * 16 + frow;
-        if (m >= g.M) continue;
-        const int32_t rs = g.rowsum ? g.rowsum[(long long)z * g.rowsum_bstride + m] : 0;
-        bool tail = false;
-        if (g.tail != TAIL_NONE) {
+        rs[tm] = (g.rowsum && m < g.M) ? g.rowsum[(long long)z * g.rowsum_bstride + m] : 0;
+        bool tl = false;
+        if (g.tail != TAIL_NONE && m < g.M) {
             int s = m % sp;
             if (g.tail == TAIL_SPATIAL) {
-                tail = s >= sp - sp % 16;
+                tl = s >= sp - sp % 16;
             } else if (g.tail == TAIL_OW) {
                 int ow = s % g.oW;
-                tail = ow >= g.oW - g.oW % 16;
+                tl = ow >= g.oW - g.oW % 16;
             } else {
                 int oh = s / g.oW;
                 int oh0 = (oh / g.tile_h) * g.tile_h;
                 int th = g.oH - oh0 < g.tile_h ? g.oH - oh0 : g.tile_h;
                 int tsp = th * g.oW;
                 int ts = s - oh0 * g.oW;
-                tail = ts >= tsp - tsp % 16;
+                tl = ts >= tsp - tsp % 16;
             }
         }
-        int32_t v[16];
+        tail[tm] = tl;
+    }
+    if (g.epi == EPI_I32) {
 #pragma unroll
         for (int tn = 0; tn < 4; ++tn) {
-            v[tn * 4 + 0] = acc[tm][tn].x;
-            v[tn * 4 + 1] = acc[tm][tn].y;
-            v[tn * 4 + 2] = acc[tm][tn].z;
-            v[tn * 4 + 3] = acc[tm][tn].w;
-        }
+            int32_t cc[4], bc[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            v[i] = wrap_add(wrap_add(v[i], -colc[i]), -wrap_mul(betac[i], rs));
-
-        if (g.epi == EPI_I32) {
-            int32_t* yrow = (int32_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
-            if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    *(v4i*)(yrow + 4 * q) = v4i{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    if (nb + i < g.N) yrow[i] = v[i];
+            for (int r = 0; r < 4; ++r) {
+                int n = nb + 4 * tn + r;
+                bool ok = n < g.N;
+                cc[r] = (ok && g.colsum) ? wrap_mul(alpha, g.colsum[po + n]) : 0;
+                bc[r] = g.beta_col ? (ok ? g.beta_col[po + n] : 0) : g.beta;
             }
-            continue;
-        }
-        int q[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+            for (int tm = 0; tm < 4; ++tm) {
+                const int m = m0 + wm * 64 + tm * 16 + frow;
+                if (m >= g.M) continue;
+                int32_t* yrow = (int32_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb + 4 * tn;
+                int32_t v[4] = {acc[tm][tn].x, acc[tm][tn].y, acc[tm][tn].z, acc[tm][tn].w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = wrap_add(wrap_add(v[r], -cc[r]), -wrap_mul(bc[r], rs[tm]));
+                if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
+                    *(v4i*)yrow = v4i{v[0], v[1], v[2], v[3]};
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (nb + 4 * tn + r < g.N) yrow[r] = v[r];
+                }
+            }
+        }
+        return;
+    }
+    uint32_t packed[4][4];
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) {
+        int32_t cc[4], bc[4], bi[4];
+        float p0[4], p1[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            int n = nb + 4 * tn + r;
+            bool ok = n < g.N;
+            cc[r] = (ok && g.colsum) ? wrap_mul(alpha, g.colsum[po + n]) : 0;
+            bc[r] = g.beta_col ? (ok ? g.beta_col[po + n] : 0) : g.beta;
+            bi[r] = (ok && g.bias) ? g.bias[po + n] : 0;
             if (g.epi == EPI_RQB) {
-                int32_t vb = wrap_add(v[i], bias[i]);
-                q[i] = (nb + i >= g.bprime_from) ? rq_b_roundf(vb, p0[i], g.y_zp, g.lo, g.hi)
-                                                 : rq_b(vb, p0[i], g.y_zp, g.lo, g.hi);
-            } else if (g.epi == EPI_RQA) {
-                q[i] = tail ? rq_a_tail(v[i], p0[i], p1[i], g.inv_y, g.y_zp, g.L, g.hi)
-                            : rq_a(v[i], p0[i], p1[i], g.inv_y, g.y_zp, g.L, g.hi);
-            } else if (g.epi == EPI_RQC) {
-                q[i] = tail ? rq_a_tail(v[i], p0[i], p1[i], g.inv_y, g.y_zp, g.L, g.hi)
-                            : rq_c(v[i], p0[i], p1[i], g.inv_y, g.y_zp, g.L, g.hi);
+                p0[r] = ok ? g.os[po + n] : 0.f;
+                p1[r] = 0.f;
+            } else if (g.epi == EPI_RQA || g.epi == EPI_RQC) {
+                p0[r] = ok ? g.cs[po + n] : 0.f;
+                p1[r] = ok ? g.bf[po + n] : 0.f;
             } else {
-                q[i] = rq_d(v[i], cm, g.y_zp, g.lo, g.hi);
+                p0[r] = 0.f; p1[r] = 0.f;
             }
         }
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+            int32_t v[4] = {acc[tm][tn].x, acc[tm][tn].y, acc[tm][tn].z, acc[tm][tn].w};
+            uint32_t w = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                int32_t vv = wrap_add(wrap_add(v[r], -cc[r]), -wrap_mul(bc[r], rs[tm]));
+                int q;
+                if (g.epi == EPI_RQB) {
+                    int32_t vb = wrap_add(vv, bi[r]);
+                    q = (nb + 4 * tn + r >= g.bprime_from) ? rq_b_roundf(vb, p0[r], g.y_zp, g.lo, g.hi)
+                                                           : rq_b(vb, p0[r], g.y_zp, g.lo, g.hi);
+                } else if (g.epi == EPI_RQA) {
+                    q = tail[tm] ? rq_a_tail(vv, p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi)
+                                 : rq_a(vv, p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi);
+                } else if (g.epi == EPI_RQC) {
+                    q = tail[tm] ? rq_a_tail(vv, p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi)
+                                 : rq_c(vv, p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi);
+                } else {
+                    q = rq_d(vv, cm, g.y_zp, g.lo, g.hi);
+                }
+                w |= (uint32_t)(q & 0xff) << (8 * r);
+            }
+            packed[tm][tn] = w;
+        }
+    }
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+        const int m = m0 + wm * 64 + tm * 16 + frow;
+        if (m >= g.M) continue;
         if (g.y_nchw) {
             uint8_t* yb = (uint8_t*)g.y + (long long)z * g.y_bstride;
             int img = m / sp, s = m - img * sp;
 #pragma unroll
             for (int i = 0; i < 16; ++i)
-                if (nb + i < g.N) yb[((long long)img * g.ldy + nb + i) * sp + s] = (uint8_t)q[i];
+                if (nb + i < g.N)
+                    yb[((long long)img * g.ldy + nb + i) * sp + s] = (uint8_t)(packed[tm][i >> 2] >> (8 * (i & 3)));
         } else {
             uint8_t* yrow = (uint8_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
             if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
-                uint32_t w[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    w[k] = (uint32_t)(q[4 * k] & 0xff) | ((uint32_t)(q[4 * k + 1] & 0xff) << 8) |
-                           ((uint32_t)(q[4 * k + 2] & 0xff) << 16) | ((uint32_t)(q[4 * k + 3] & 0xff) << 24);
-                *(v4i*)yrow = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+                *(v4i*)yrow = v4i{(int)packed[tm][0], (int)packed[tm][1], (int)packed[tm][2], (int)packed[tm][3]};
             } else {
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
-                    if (nb + i < g.N) yrow[i] = (uint8_t)q[i];
+                    if (nb + i < g.N) yrow[i] = (uint8_t)(packed[tm][i >> 2] >> (8 * (i & 3)));
             }
         }
     }

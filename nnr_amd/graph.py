@@ -1,0 +1,261 @@
+"""Graph construction and execution through the host framework's C ABI
+(include/nnr_host.h, nnr_amd/lib/libnnr_host.so).
+
+`Graph` collects initializers / inputs / outputs / nodes (what an ONNX
+loader would produce); `Session` hands them to a C++ context_t with the HIP
+backend preferred, prepares it (QDQ fusion, layout assignment, device
+memory) and runs it on a stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+HOST_LIB = os.path.join(_HERE, "lib", "libnnr_host.so")
+
+ONNX_DT = {np.dtype(np.float32): 1, np.dtype(np.uint8): 2, np.dtype(np.int8): 3,
+           np.dtype(np.int32): 6, np.dtype(np.int64): 7, np.dtype(np.float16): 10}
+NP_DT = {v: k for k, v in ONNX_DT.items()}
+BACKEND_HIP = 4
+
+_hl = None
+
+
+def host_lib():
+    global _hl
+    if _hl is None:
+        _lib.lib()          # the HIP library must be loadable first
+        if not os.path.exists(HOST_LIB):
+            raise ImportError(f"{HOST_LIB} is missing: run __graft_entry__.build() first")
+        L = C.CDLL(HOST_LIB)
+        vp, i, cp = C.c_void_p, C.c_int, C.c_char_p
+        P = C.POINTER
+        sig = {
+            "nnr_last_error": (cp, []),
+            "nnr_ctx_create": (i, [P(vp), i]),
+            "nnr_ctx_destroy": (i, [vp]),
+            "nnr_ctx_set_stream": (i, [vp, vp]),
+            "nnr_ctx_set_fusion": (i, [vp, i]),
+            "nnr_ctx_add_initializer": (i, [vp, cp, i, P(i), i, vp]),
+            "nnr_ctx_add_input": (i, [vp, cp, i, P(i), i]),
+            "nnr_ctx_add_output": (i, [vp, cp]),
+            "nnr_ctx_add_node": (i, [vp, cp, cp, i, P(cp), i, P(cp), i, P(cp), P(i), P(i), P(i),
+                                     P(C.c_int64), P(C.c_float), P(cp)]),
+            "nnr_ctx_optimize": (i, [vp]),
+            "nnr_ctx_prepare": (i, [vp]),
+            "nnr_ctx_run": (i, [vp]),
+            "nnr_ctx_tensor": (i, [vp, cp, P(vp), P(i), P(i), P(i), P(i)]),
+            "nnr_ctx_node_count": (i, [vp, P(i)]),
+            "nnr_ctx_node_info": (i, [vp, i, P(cp), P(cp), P(cp), P(i), P(i), P(i)]),
+            "nnr_ctx_node_io": (i, [vp, i, i, i, P(cp)]),
+            "nnr_ctx_fusion_stat": (i, [vp, cp, P(i)]),
+            "nnr_ctx_device_bytes": (C.c_size_t, [vp]),
+            "nnr_ctx_enable_profiling": (i, [vp, i]),
+            "nnr_ctx_profile": (i, [vp, i, P(C.c_double), P(i), P(C.c_double), P(C.c_double)]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(L, n)
+            f.restype = r
+            f.argtypes = a
+        _hl = L
+    return _hl
+
+
+class NnrError(RuntimeError):
+    pass
+
+
+def _chk(rc):
+    if rc != 0:
+        raise NnrError(host_lib().nnr_last_error().decode())
+
+
+@dataclass
+class Node:
+    op: str
+    name: str
+    inputs: list
+    outputs: list
+    attrs: dict = field(default_factory=dict)
+
+
+class Graph:
+    def __init__(self):
+        self.initializers: dict[str, np.ndarray] = {}
+        self.inputs: dict[str, tuple] = {}      # name -> (dtype, shape)
+        self.outputs: list[str] = []
+        self.nodes: list[Node] = []
+        self._n = 0
+
+    def init(self, name, arr):
+        self.initializers[name] = np.ascontiguousarray(arr)
+        return name
+
+    def node(self, op, inputs, outputs=None, name=None, **attrs):
+        self._n += 1
+        name = name or f"{op}_{self._n}"
+        if outputs is None:
+            outputs = [f"{name}_out"]
+        elif isinstance(outputs, str):
+            outputs = [outputs]
+        self.nodes.append(Node(op, name, list(inputs), list(outputs), attrs))
+        return outputs[0] if len(outputs) == 1 else outputs
+
+    def node_by_name(self, name):
+        for n in self.nodes:
+            if n.name == name:
+                return n
+        return None
+
+
+def _attr_arrays(attrs: dict):
+    names, kinds, counts, offs, ints, floats, strs = [], [], [], [], [], [], []
+    for k, v in attrs.items():
+        names.append(k.encode())
+        if isinstance(v, str):
+            kinds.append(2); counts.append(0); offs.append(0); strs.append(v.encode())
+            continue
+        strs.append(None)
+        if isinstance(v, (list, tuple, np.ndarray)):
+            vals = list(v)
+            if all(isinstance(x, (int, np.integer)) for x in vals):
+                kinds.append(3); counts.append(len(vals)); offs.append(len(ints))
+                ints.extend(int(x) for x in vals)
+            else:
+                kinds.append(4); counts.append(len(vals)); offs.append(len(floats))
+                floats.extend(float(x) for x in vals)
+        elif isinstance(v, (int, np.integer)):
+            kinds.append(0); counts.append(1); offs.append(len(ints)); ints.append(int(v))
+        else:
+            kinds.append(1); counts.append(1); offs.append(len(floats)); floats.append(float(v))
+    n = len(names)
+    A = lambda T, xs: (T * max(1, len(xs)))(*xs)
+    return (n, A(C.c_char_p, names), A(C.c_int, kinds), A(C.c_int, counts), A(C.c_int, offs),
+            A(C.c_int64, ints), A(C.c_float, floats), A(C.c_char_p, strs))
+
+
+class Session:
+    """A prepared C++ context_t for `graph` with the HIP backend preferred."""
+
+    def __init__(self, graph: Graph, stream=None, fusion=True, device=True):
+        L = host_lib()
+        self.L = L
+        self.graph = graph
+        h = C.c_void_p()
+        _chk(L.nnr_ctx_create(C.byref(h), BACKEND_HIP))
+        self.h = h
+        if stream is None and device:
+            stream = _lib.cur_stream()
+        _chk(L.nnr_ctx_set_stream(h, stream))
+        _chk(L.nnr_ctx_set_fusion(h, 1 if fusion else 0))
+        for name, arr in graph.initializers.items():
+            dims = (C.c_int * max(1, arr.ndim))(*arr.shape)
+            _chk(L.nnr_ctx_add_initializer(h, name.encode(), ONNX_DT[arr.dtype], dims, arr.ndim,
+                                           arr.ctypes.data))
+        for name, (dt, shape) in graph.inputs.items():
+            dims = (C.c_int * max(1, len(shape)))(*shape)
+            _chk(L.nnr_ctx_add_input(h, name.encode(), ONNX_DT[np.dtype(dt)], dims, len(shape)))
+        for name in graph.outputs:
+            _chk(L.nnr_ctx_add_output(h, name.encode()))
+        for nd in graph.nodes:
+            ins = (C.c_char_p * max(1, len(nd.inputs)))(*[s.encode() if s else None for s in nd.inputs])
+            outs = (C.c_char_p * max(1, len(nd.outputs)))(*[s.encode() for s in nd.outputs])
+            na, an, ak, ac, ao, ai, af, as_ = _attr_arrays(nd.attrs)
+            _chk(L.nnr_ctx_add_node(h, nd.op.encode(), nd.name.encode(), len(nd.inputs), ins,
+                                    len(nd.outputs), outs, na, an, ak, ac, ao, ai, af, as_))
+        # device=False: graph passes + shapes + layouts only (no GPU needed)
+        _chk(L.nnr_ctx_prepare(h) if device else L.nnr_ctx_optimize(h))
+
+    # ---- data ---------------------------------------------------------------
+    def tensor_info(self, name):
+        p, dt, nd, fmt = C.c_void_p(), C.c_int(), C.c_int(), C.c_int()
+        dims = (C.c_int * 8)()
+        _chk(self.L.nnr_ctx_tensor(self.h, name.encode(), C.byref(p), C.byref(dt), dims,
+                                   C.byref(nd), C.byref(fmt)))
+        return p.value, NP_DT.get(dt.value), tuple(dims[:nd.value]), fmt.value
+
+    def set_input(self, name, arr):
+        """Copy a host numpy array or a device torch tensor into a graph tensor."""
+        p, dt, shape, fmt = self.tensor_info(name)
+        if isinstance(arr, np.ndarray):
+            a = np.ascontiguousarray(arr, dtype=dt)
+            assert a.size == int(np.prod(shape)), (a.shape, shape)
+            _lib.check(_lib.lib().nnrh_memcpy(p, a.ctypes.data, a.nbytes, 0, _lib.cur_stream()))
+            _lib.check(_lib.lib().nnrh_stream_synchronize(_lib.cur_stream()))
+        else:
+            nbytes = arr.numel() * arr.element_size()
+            assert arr.is_contiguous() and arr.numel() == int(np.prod(shape))
+            _lib.check(_lib.lib().nnrh_memcpy(p, arr.data_ptr(), nbytes, 2, _lib.cur_stream()))
+
+    def output(self, name):
+        """numpy copy of a tensor in its physical layout, plus the layout flag
+        (1 = NHWC: a 4-D tensor comes back as [N, H, W, C])."""
+        p, dt, shape, fmt = self.tensor_info(name)
+        phys = shape
+        if fmt == 1 and len(shape) == 4:
+            phys = (shape[0], shape[2], shape[3], shape[1])
+        out = np.empty(phys, dtype=dt)
+        _lib.check(_lib.lib().nnrh_stream_synchronize(_lib.cur_stream()))
+        _lib.check(_lib.lib().nnrh_memcpy(out.ctypes.data, p, out.nbytes, 1, _lib.cur_stream()))
+        return out, fmt
+
+    def run(self):
+        _chk(self.L.nnr_ctx_run(self.h))
+
+    # ---- plan introspection ------------------------------------------------------
+    def plan(self):
+        L = self.L
+        n = C.c_int()
+        _chk(L.nnr_ctx_node_count(self.h, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            op, nm, var = C.c_char_p(), C.c_char_p(), C.c_char_p()
+            pf, ni, no = C.c_int(), C.c_int(), C.c_int()
+            _chk(L.nnr_ctx_node_info(self.h, i, C.byref(op), C.byref(nm), C.byref(var),
+                                     C.byref(pf), C.byref(ni), C.byref(no)))
+            ios = []
+            for is_out, cnt in ((0, ni.value), (1, no.value)):
+                lst = []
+                for j in range(cnt):
+                    s = C.c_char_p()
+                    _chk(L.nnr_ctx_node_io(self.h, i, is_out, j, C.byref(s)))
+                    lst.append(s.value.decode())
+                ios.append(lst)
+            out.append(dict(op=op.value.decode(), name=nm.value.decode(), variant=var.value.decode(),
+                            post_fn=pf.value, inputs=ios[0], outputs=ios[1]))
+        return out
+
+    def fusion_stat(self, key):
+        v = C.c_int()
+        _chk(self.L.nnr_ctx_fusion_stat(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def device_bytes(self):
+        return int(self.L.nnr_ctx_device_bytes(self.h))
+
+    def enable_profiling(self, on=True):
+        _chk(self.L.nnr_ctx_enable_profiling(self.h, 1 if on else 0))
+
+    def profile(self):
+        rows = []
+        for i, p in enumerate(self.plan()):
+            ms, runs, ops, nb = C.c_double(), C.c_int(), C.c_double(), C.c_double()
+            _chk(self.L.nnr_ctx_profile(self.h, i, C.byref(ms), C.byref(runs), C.byref(ops),
+                                        C.byref(nb)))
+            rows.append(dict(p, ms=ms.value, runs=runs.value, ops=ops.value, bytes=nb.value))
+        return rows
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None):
+                self.L.nnr_ctx_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+

@@ -1,0 +1,203 @@
+// capi_host.cpp -- implementation of include/nnr_host.h over context_t.
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "nnr.h"
+#include "nnr_host.h"
+
+namespace nnr {
+int hip_backend_op_count();
+}
+
+using namespace nnr;
+
+struct nnr_ctx {
+    context_t ctx;
+    std::vector<operator_t*> plan;   // active nodes after prepare()
+    std::string scratch;
+};
+
+namespace {
+thread_local std::string g_err = "no error";
+int err(const std::string& m) {
+    g_err = m;
+    return 1;
+}
+int ctx_err(nnr_ctx_t c) { return err(c->ctx.last_error); }
+}  // namespace
+
+extern "C" {
+
+const char* nnr_last_error(void) { return g_err.c_str(); }
+
+int nnr_ctx_create(nnr_ctx_t* out, int backend) {
+    if (!out) return err("ctx is NULL");
+    if (hip_backend_op_count() <= 0) return err("no HIP operators registered");
+    nnr_ctx* c = new nnr_ctx();
+    c->ctx.preferred_backend = (backend_t)backend;
+    *out = c;
+    return 0;
+}
+
+int nnr_ctx_destroy(nnr_ctx_t c) {
+    delete c;
+    return 0;
+}
+
+int nnr_ctx_set_stream(nnr_ctx_t c, void* s) {
+    if (!c) return err("ctx is NULL");
+    c->ctx.stream = s;
+    return 0;
+}
+
+int nnr_ctx_set_fusion(nnr_ctx_t c, int on) {
+    if (!c) return err("ctx is NULL");
+    c->ctx.enable_fusion = on != 0;
+    return 0;
+}
+
+int nnr_ctx_add_initializer(nnr_ctx_t c, const char* name, int dtype, const int* dims, int ndim,
+                            const void* data) {
+    if (!c || !name || (ndim && !dims) || !data) return err("add_initializer: NULL argument");
+    std::vector<int> d(dims, dims + ndim);
+    if (!c->ctx.add_initializer(name, (data_type_t)dtype, d, data)) return ctx_err(c);
+    return 0;
+}
+
+int nnr_ctx_add_input(nnr_ctx_t c, const char* name, int dtype, const int* dims, int ndim) {
+    if (!c || !name || (ndim && !dims)) return err("add_input: NULL argument");
+    if (!c->ctx.add_input(name, (data_type_t)dtype, std::vector<int>(dims, dims + ndim))) return ctx_err(c);
+    return 0;
+}
+
+int nnr_ctx_add_output(nnr_ctx_t c, const char* name) {
+    if (!c || !name) return err("add_output: NULL argument");
+    c->ctx.add_output(name);
+    return 0;
+}
+
+int nnr_ctx_add_node(nnr_ctx_t c, const char* op_type, const char* name, int n_in,
+                     const char* const* inputs, int n_out, const char* const* outputs, int n_attr,
+                     const char* const* attr_names, const int* kinds, const int* counts, const int* offs,
+                     const int64_t* ints, const float* floats, const char* const* strings) {
+    if (!c || !op_type || !name) return err("add_node: NULL argument");
+    std::vector<std::string> ins, outs;
+    for (int i = 0; i < n_in; ++i) ins.push_back(inputs[i] ? inputs[i] : "");
+    for (int i = 0; i < n_out; ++i) outs.push_back(outputs[i] ? outputs[i] : "");
+    std::vector<std::pair<std::string, attr_t>> attrs;
+    for (int i = 0; i < n_attr; ++i) {
+        attr_t a;
+        a.kind = (attr_t::kind_t)kinds[i];
+        switch (kinds[i]) {
+        case NNR_ATTR_INT: a.i = ints[offs[i]]; break;
+        case NNR_ATTR_FLOAT: a.f = floats[offs[i]]; break;
+        case NNR_ATTR_STRING: a.s = strings[i] ? strings[i] : ""; break;
+        case NNR_ATTR_INTS: a.ints.assign(ints + offs[i], ints + offs[i] + counts[i]); break;
+        case NNR_ATTR_FLOATS: a.floats.assign(floats + offs[i], floats + offs[i] + counts[i]); break;
+        default: return err("add_node: bad attribute kind");
+        }
+        attrs.emplace_back(attr_names[i], std::move(a));
+    }
+    if (!c->ctx.add_node(op_type, name, ins, outs, std::move(attrs))) return ctx_err(c);
+    return 0;
+}
+
+int nnr_ctx_prepare(nnr_ctx_t c) {
+    if (!c) return err("ctx is NULL");
+    if (!c->ctx.prepare()) return ctx_err(c);
+    c->plan.clear();
+    for (auto* op : c->ctx.nodes)
+        if (!op->skip && !op->folded) c->plan.push_back(op);
+    return 0;
+}
+
+int nnr_ctx_optimize(nnr_ctx_t c) {
+    if (!c) return err("ctx is NULL");
+    if (!c->ctx.optimize()) return ctx_err(c);
+    c->plan.clear();
+    for (auto* op : c->ctx.nodes)
+        if (!op->skip && !op->folded) c->plan.push_back(op);
+    return 0;
+}
+
+int nnr_ctx_run(nnr_ctx_t c) {
+    if (!c) return err("ctx is NULL");
+    if (!c->ctx.run()) return ctx_err(c);
+    return 0;
+}
+
+int nnr_ctx_tensor(nnr_ctx_t c, const char* name, void** data, int* dtype, int* dims, int* ndim,
+                   int* format) {
+    if (!c || !name) return err("tensor: NULL argument");
+    tensor_t* t = c->ctx.find(name);
+    if (!t) return err(std::string("no tensor named ") + name);
+    if (data) *data = t->data;
+    if (dtype) *dtype = (int)t->type;
+    if (ndim) *ndim = t->ndim();
+    if (dims)
+        for (int i = 0; i < t->ndim() && i < 8; ++i) dims[i] = t->dims[i];
+    if (format) *format = t->format == memory_layout_t::NHWC ? 1 : 0;
+    return 0;
+}
+
+int nnr_ctx_node_count(nnr_ctx_t c, int* n) {
+    if (!c || !n) return err("node_count: NULL");
+    *n = (int)c->plan.size();
+    return 0;
+}
+
+int nnr_ctx_node_info(nnr_ctx_t c, int i, const char** op_type, const char** name, const char** variant,
+                      int* post_fn, int* n_in, int* n_out) {
+    if (!c || i < 0 || i >= (int)c->plan.size()) return err("node_info: bad index");
+    operator_t* op = c->plan[i];
+    if (op_type) *op_type = op->op_type.c_str();
+    if (name) *name = op->node_name.c_str();
+    if (variant) {
+        c->scratch = op->variant();
+        *variant = c->scratch.c_str();
+    }
+    if (post_fn) *post_fn = op->post_fn ? 1 : 0;
+    if (n_in) *n_in = (int)op->inputs.size();
+    if (n_out) *n_out = (int)op->outputs.size();
+    return 0;
+}
+
+int nnr_ctx_node_io(nnr_ctx_t c, int i, int is_out, int j, const char** tname) {
+    if (!c || i < 0 || i >= (int)c->plan.size() || !tname) return err("node_io: bad index");
+    auto& v = is_out ? c->plan[i]->outputs : c->plan[i]->inputs;
+    if (j < 0 || j >= (int)v.size()) return err("node_io: bad slot");
+    *tname = v[j] ? v[j]->name.c_str() : "";
+    return 0;
+}
+
+int nnr_ctx_fusion_stat(nnr_ctx_t c, const char* key, int* value) {
+    if (!c || !key || !value) return err("fusion_stat: NULL");
+    auto it = c->ctx.fusion_stats.find(key);
+    *value = it == c->ctx.fusion_stats.end() ? 0 : it->second;
+    return 0;
+}
+
+size_t nnr_ctx_device_bytes(nnr_ctx_t c) { return c ? c->ctx.device_bytes : 0; }
+
+int nnr_ctx_enable_profiling(nnr_ctx_t c, int on) {
+    if (!c) return err("ctx is NULL");
+    c->ctx.enable_profiling = on != 0;
+    for (auto& p : c->ctx.profile) {
+        p.ms = 0;
+        p.runs = 0;
+    }
+    return 0;
+}
+
+int nnr_ctx_profile(nnr_ctx_t c, int i, double* ms, int* runs, double* ops, double* bytes) {
+    if (!c || i < 0 || i >= (int)c->ctx.profile.size()) return err("profile: bad index");
+    auto& p = c->ctx.profile[i];
+    if (ms) *ms = p.ms;
+    if (runs) *runs = p.runs;
+    if (ops) *ops = p.ops;
+    if (bytes) *bytes = p.bytes;
+    return 0;
+}
+
+}  // extern "C"

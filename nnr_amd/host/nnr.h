@@ -1,0 +1,205 @@
+// nnr.h -- host-side operator framework of the MI355X backend.
+//
+// Mirrors the reference's core interface (src/nnr.h:154-612, src/registry.h)
+// so that graph builders, the graph optimizer and the run loop drive the HIP
+// operators the way NNR drives its CPU ones:
+//   tensor_t      dims / type / format / quantization metadata; `data` is a
+//                 device (HBM) pointer, `host` keeps a host mirror for
+//                 initializers because operators read scalar scales and zero
+//                 points as *(float*)t->data (QLinearConv.cpp:395-398);
+//   operator_t    init() / reshape() / exec() / layout_mask / post_fn;
+//   context_t     graph, preferred_backend, prepare() / run(), profiling.
+// Every device operation goes through the C ABI of include/nnr_hip.h; this
+// library includes no HIP header.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <set>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace nnr {
+
+// ONNX TensorProto element types (the reference's data_type_t numbering)
+enum data_type_t : int {
+    NNR_DATA_TYPE_UNDEFINED = 0,
+    NNR_DATA_TYPE_FLOAT32 = 1,
+    NNR_DATA_TYPE_UINT8 = 2,
+    NNR_DATA_TYPE_INT8 = 3,
+    NNR_DATA_TYPE_UINT16 = 4,
+    NNR_DATA_TYPE_INT16 = 5,
+    NNR_DATA_TYPE_INT32 = 6,
+    NNR_DATA_TYPE_INT64 = 7,
+    NNR_DATA_TYPE_BOOL = 9,
+    NNR_DATA_TYPE_FLOAT16 = 10,
+};
+size_t data_type_sizeof(data_type_t t);
+
+enum class memory_layout_t : uint8_t { NCHW = 0, NHWC = 1 };
+constexpr uint8_t LAYOUT_NCHW = 1;
+constexpr uint8_t LAYOUT_NHWC = 2;
+constexpr uint8_t LAYOUT_ALL = 0xff;
+
+struct context_t;
+
+struct tensor_t {
+    std::string name;
+    data_type_t type = NNR_DATA_TYPE_UNDEFINED;
+    memory_layout_t format = memory_layout_t::NCHW;
+    std::vector<int> dims;
+    size_t ndata = 0;
+    void* data = nullptr;          // device pointer
+    bool owns_data = true;         // false for views (Flatten / Reshape)
+    tensor_t* alias_of = nullptr;  // view source
+    std::vector<uint8_t> host;     // host mirror (initializers, folded constants)
+    bool device_only = false;      // produced on the device every run (no host mirror)
+
+    // quantization metadata (src/nnr.h:236-266)
+    float quant_scale = 0.0f;
+    int32_t quant_zero_point = 0;
+
+    int ndim() const { return (int)dims.size(); }
+    size_t nbytes() const { return ndata * data_type_sizeof(type); }
+    bool reshape(const std::vector<int>& d, data_type_t t);
+    bool has_host() const { return !host.empty(); }
+    template <typename T> const T* h() const { return (const T*)host.data(); }
+    // scalar accessors over the host mirror
+    float scalar_f32() const;
+    int32_t scalar_int() const;
+    bool is_quantized() const { return quant_scale != 0.0f; }
+    void set_quant(float s, int32_t zp) { quant_scale = s; quant_zero_point = zp; }
+};
+
+struct attr_t {
+    enum class kind_t : uint8_t { INT = 0, FLOAT, STRING, INTS, FLOATS };
+    kind_t kind = kind_t::INT;
+    int64_t i = 0;
+    float f = 0.0f;
+    std::string s;
+    std::vector<int64_t> ints;
+    std::vector<float> floats;
+};
+
+struct operator_t {
+    virtual ~operator_t() = default;
+
+    context_t* ctx = nullptr;
+    int opset = 13;
+    std::string op_type;
+    std::string node_name;
+    std::vector<tensor_t*> inputs;
+    std::vector<tensor_t*> outputs;
+    std::vector<std::pair<std::string, attr_t>> attrs;
+
+    virtual bool init() { return true; }
+    // default: output has the input's shape and type (src/nnr.h:369-381)
+    virtual bool reshape();
+    virtual bool exec() = 0;
+    // algorithmic work of one exec (per-layer TOPS / GB/s reporting)
+    virtual double num_ops() const { return 0.0; }
+    virtual double num_bytes() const;
+    // output aliases input[view_input_index()] (src/nnr.h:404)
+    virtual int view_input_index() const { return -1; }
+    // kernel branch / variant name for reports
+    virtual std::string variant() const { return std::string(); }
+
+    uint8_t layout_mask = LAYOUT_NCHW;
+    bool skip = false;
+    bool folded = false;
+    bool resolved = true;         // false: placeholder for an op this backend lacks
+    // fused unary post-op (src/nnr.h:437-442). For the int8 operators the
+    // only effect is QLinearConv's qmin (QLinearConv.cpp:419).
+    bool fusable_unary = false;   // set in init() by Relu / Clip
+    bool post_fn = false;
+    operator_t* fused_op = nullptr;
+
+    // attribute accessors
+    const attr_t* find_attr(const std::string& name) const;
+    int64_t attribute(const std::string& name, int64_t def) const;
+    float attribute_f(const std::string& name, float def) const;
+    std::string attribute_s(const std::string& name, const std::string& def) const;
+    std::vector<int64_t> attribute_ints(const std::string& name) const;
+};
+
+// Placeholder for ops with no resolver on any backend (the reference's
+// dummy op whose exec() returns false, onnx_loader.cpp:597-602). Graph
+// passes may rewrite it away (e.g. DQ->Conv->Q into QLinearConv).
+struct unresolved_op_t : operator_t {
+    unresolved_op_t() { resolved = false; }
+    bool reshape() override { return true; }
+    bool exec() override { return false; }
+};
+
+enum class backend_t : uint8_t { CPU = 0, CUDA, SYCL, VULKAN, HIP };
+
+struct node_profile_t {
+    std::string name, op_type, variant;
+    double ms = 0.0;
+    int runs = 0;
+    double ops = 0.0, bytes = 0.0;
+};
+
+struct context_t {
+    context_t();
+    ~context_t();
+    context_t(const context_t&) = delete;
+    context_t& operator=(const context_t&) = delete;
+
+    // ---- graph construction (what the reference's ONNX loader does) ----
+    tensor_t* tensor(const std::string& name);                  // get or create
+    tensor_t* find(const std::string& name) const;
+    bool add_initializer(const std::string& name, data_type_t t, const std::vector<int>& dims,
+                         const void* host_data);
+    bool add_input(const std::string& name, data_type_t t, const std::vector<int>& dims);
+    bool add_output(const std::string& name);
+    bool add_node(const std::string& op_type, const std::string& name,
+                  const std::vector<std::string>& ins, const std::vector<std::string>& outs,
+                  std::vector<std::pair<std::string, attr_t>> attrs);
+
+    // ---- lifecycle (src/nnr.cpp:1378-1483) ----
+    bool optimize();    // graph passes + shape inference + layouts (no device work)
+    bool prepare();     // optimize, reshape, plan memory, upload constants
+    bool run();         // execute active nodes in order on `stream`
+
+    // ---- configuration (src/nnr.h:512-589) ----
+    backend_t preferred_backend = backend_t::HIP;
+    void* stream = nullptr;       // hipStream_t of every launch
+    bool enable_fusion = true;
+    bool enable_profiling = false;
+    bool shape_only = false;      // reshape() computes shapes only (pre-layout pass)
+
+    // ---- state ----
+    std::map<std::string, tensor_t*> map;
+    std::vector<operator_t*> nodes;
+    std::vector<std::string> graph_inputs, graph_outputs;
+    std::set<std::string> initializer_names;
+    std::vector<node_profile_t> profile;
+    std::map<std::string, int> fusion_stats;
+    std::string last_error;
+    bool optimized = false;
+    bool prepared = false;
+    size_t device_bytes = 0;
+
+    bool fail(const std::string& msg);
+
+private:
+    std::vector<void*> allocations_;
+    std::vector<std::pair<void*, void*>> events_;   // per-node hipEvents (profiling)
+    bool plan_memory();
+    bool upload_constants();
+};
+
+// graph optimizer passes (nnr_amd/host/passes.cpp)
+void fold_constants(context_t* ctx);
+void fuse_qdq_compute(context_t* ctx);
+void fuse_qdq(context_t* ctx);
+void fuse_post_ops(context_t* ctx);
+void assign_layouts(context_t* ctx);
+
+// operator creation through the registry (src/backend/cpu/solve_operator.cpp:29-33)
+operator_t* solve_operator(const std::string& op_type, int opset, backend_t preferred);
+
+}  // namespace nnr

@@ -1,0 +1,580 @@
+// ops_hip.cpp -- operators of the HIP backend, registered under
+// backend_t::HIP. Each one keeps the reference operator's inputs, attributes,
+// shape rules and error behaviour (init/reshape return false, exec returns
+// false on a device error) and crosses into device code only through the C
+// ABI of include/nnr_hip.h on the context's stream.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+
+#include "nnr.h"
+#include "nnr_hip.h"
+#include "registry.h"
+
+namespace nnr {
+namespace {
+
+bool ok(operator_t* op, int rc) {
+    if (rc != NNRH_OK) {
+        op->ctx->last_error = nnrh_last_error();
+        return false;
+    }
+    return true;
+}
+bool bad(operator_t* op, const std::string& msg) {
+    op->ctx->last_error = op->op_type + " " + op->node_name + ": " + msg;
+    return false;
+}
+int qdtype(data_type_t t) {
+    return t == NNR_DATA_TYPE_UINT8 ? NNRH_U8 : t == NNR_DATA_TYPE_INT8 ? NNRH_S8
+         : t == NNR_DATA_TYPE_INT32 ? NNRH_I32 : -1;
+}
+tensor_t* in(operator_t* op, size_t i) { return op->inputs.size() > i ? op->inputs[i] : nullptr; }
+bool has_zp(tensor_t* t) { return t && t->ndata > 0; }
+int32_t zp_value(tensor_t* t) { return has_zp(t) ? t->scalar_int() : 0; }
+
+// ===========================================================================
+// QuantizeLinear (src/backend/cpu/QuantizeLinear.cpp), per-tensor
+struct QuantizeLinear_hip : operator_t {
+    bool init() override {
+        layout_mask = LAYOUT_ALL;
+        return inputs.size() >= 2 && outputs.size() == 1;
+    }
+    bool reshape() override {
+        tensor_t *x = inputs[0], *s = inputs[1], *z = in(this, 2), *y = outputs[0];
+        data_type_t t = z ? z->type : NNR_DATA_TYPE_UINT8;
+        if (t != NNR_DATA_TYPE_UINT8 && t != NNR_DATA_TYPE_INT8) return bad(this, "only uint8/int8 output");
+        if (!s->has_host() || s->ndata != 1) return bad(this, "only a constant per-tensor scale");
+        y->format = x->format;
+        return y->reshape(x->dims, t);
+    }
+    bool exec() override {
+        tensor_t* y = outputs[0];
+        return ok(this, nnrh_quantize_linear((const float*)inputs[0]->data, inputs[0]->ndata,
+                                             inputs[1]->scalar_f32(), zp_value(in(this, 2)),
+                                             qdtype(y->type), y->data, ctx->stream));
+    }
+};
+
+// DequantizeLinear (src/backend/cpu/DequantizeLinear.cpp), per-tensor
+struct DequantizeLinear_hip : operator_t {
+    bool init() override {
+        layout_mask = LAYOUT_ALL;
+        return inputs.size() >= 2 && outputs.size() == 1;
+    }
+    bool reshape() override {
+        tensor_t *x = inputs[0], *s = inputs[1], *y = outputs[0];
+        if (!s->has_host() || s->ndata != 1) return bad(this, "only a constant per-tensor scale");
+        if (qdtype(x->type) < 0) return bad(this, "input must be uint8/int8/int32");
+        y->format = x->format;
+        return y->reshape(x->dims, NNR_DATA_TYPE_FLOAT32);
+    }
+    bool exec() override {
+        tensor_t* x = inputs[0];
+        return ok(this, nnrh_dequantize_linear(x->data, qdtype(x->type), x->ndata,
+                                               inputs[1]->scalar_f32(), zp_value(in(this, 2)),
+                                               (float*)outputs[0]->data, ctx->stream));
+    }
+};
+
+// DynamicQuantizeLinear (src/backend/cpu/DynamicQuantizeLinear.cpp)
+struct DynamicQuantizeLinear_hip : operator_t {
+    void* ws = nullptr;
+    ~DynamicQuantizeLinear_hip() override { nnrh_free(ws); }
+    bool init() override {
+        layout_mask = LAYOUT_ALL;
+        return inputs.size() == 1 && outputs.size() == 3;
+    }
+    bool reshape() override {
+        tensor_t* x = inputs[0];
+        outputs[0]->format = x->format;
+        outputs[0]->reshape(x->dims, NNR_DATA_TYPE_UINT8);
+        outputs[1]->reshape({}, NNR_DATA_TYPE_FLOAT32);
+        outputs[2]->reshape({}, NNR_DATA_TYPE_UINT8);
+        outputs[1]->device_only = outputs[2]->device_only = true;
+        if (ctx->shape_only) return true;
+        if (!ws && nnrh_malloc(&ws, nnrh_dynamic_quantize_workspace()) != NNRH_OK)
+            return bad(this, nnrh_last_error());
+        return true;
+    }
+    bool exec() override {
+        return ok(this, nnrh_dynamic_quantize_linear(
+                            (const float*)inputs[0]->data, inputs[0]->ndata, (uint8_t*)outputs[0]->data,
+                            (float*)outputs[1]->data, (uint8_t*)outputs[2]->data, ws, ctx->stream));
+    }
+};
+
+// ===========================================================================
+// QLinearConv (src/backend/cpu/QLinearConv.cpp)
+struct QLinearConv_hip : operator_t {
+    int auto_pad = 0;   // NOTSET, SAME_UPPER, SAME_LOWER, VALID
+    int group = 1;
+    std::vector<int> kernels, dilations, pads, strides;
+    int cpads[4] = {0, 0, 0, 0};
+    nnrh_qconv_t h = nullptr;
+    int branch = 0;
+    ~QLinearConv_hip() override { nnrh_qconv_destroy(h); }
+
+    bool init() override {
+        if (!(inputs.size() >= 8 && inputs.size() <= 9 && outputs.size() == 1)) return false;
+        std::string ap = attribute_s("auto_pad", "NOTSET");
+        auto_pad = ap == "SAME_UPPER" ? 1 : ap == "SAME_LOWER" ? 2 : ap == "VALID" ? 3 : 0;
+        group = (int)attribute("group", 1);
+        for (auto v : attribute_ints("kernel_shape")) kernels.push_back((int)v);
+        if (kernels.empty() && inputs[3])
+            for (int i = 2; i < inputs[3]->ndim(); ++i) kernels.push_back(inputs[3]->dims[i]);
+        auto d = attribute_ints("dilations"), p = attribute_ints("pads"), s = attribute_ints("strides");
+        dilations.assign(kernels.size(), 1);
+        strides.assign(kernels.size(), 1);
+        pads.assign(kernels.size() * 2, 0);
+        for (size_t i = 0; i < d.size() && i < dilations.size(); ++i) dilations[i] = (int)d[i];
+        for (size_t i = 0; i < s.size() && i < strides.size(); ++i) strides[i] = (int)s[i];
+        for (size_t i = 0; i < p.size() && i < pads.size(); ++i) pads[i] = (int)p[i];
+        return true;
+    }
+    bool per_channel_zp() const {
+        tensor_t* z = in((operator_t*)this, 5);
+        if (!z || z->ndata <= 1 || !z->has_host()) return false;
+        for (size_t i = 1; i < z->ndata; ++i)
+            if (z->host[i] != z->host[0]) return true;
+        return false;
+    }
+    bool reshape() override {
+        tensor_t *x = inputs[0], *w = inputs[3], *y = outputs[0];
+        if (x->ndim() != 4 || w->ndim() != 4 || kernels.size() != 2)
+            return bad(this, "only 2-D convolution (4-D tensors)");
+        // conv_shape.h:21-81
+        int out[2];
+        for (int i = 0; i < 2; ++i) {
+            int ek = (kernels[i] - 1) * dilations[i] + 1;
+            int xd = x->dims[i + 2];
+            if (auto_pad == 1 || auto_pad == 2) {
+                int pad = (int)(ceilf(xd / (float)strides[i]) - 1) * strides[i] + ek - xd;
+                if (auto_pad == 1) { cpads[i] = pad / 2; cpads[i + 2] = pad - cpads[i]; }
+                else { cpads[i + 2] = pad / 2; cpads[i] = pad - cpads[i + 2]; }
+                out[i] = (int)ceilf(xd / (float)strides[i]);
+            } else if (auto_pad == 3) {
+                cpads[i] = cpads[i + 2] = 0;
+                out[i] = (int)ceilf((xd - ek + 1) / (float)strides[i]);
+            } else {
+                cpads[i] = pads[i];
+                cpads[i + 2] = pads[i + 2];
+                out[i] = (int)floorf((xd + cpads[i] + cpads[i + 2] - ek) / (float)strides[i] + 1);
+            }
+        }
+        // QLinearConv_reshape.h:36-46: NHWC-capable for uint8, group 1 or depthwise
+        const bool dw = group == w->dims[0] && w->dims[1] == 1;
+        layout_mask = LAYOUT_NCHW;
+        if (x->type == NNR_DATA_TYPE_UINT8 && !per_channel_zp() && (dw || group == 1))
+            layout_mask = LAYOUT_NCHW | LAYOUT_NHWC;
+        if (!y->reshape({x->dims[0], w->dims[0], out[0], out[1]}, x->type)) return false;
+        if (ctx->shape_only) return describe(true);
+        return build();
+    }
+    nnrh_qconv_desc d{};
+    // fill the C-ABI descriptor; with dispatch_only, only resolve the branch
+    bool describe(bool dispatch_only) {
+        tensor_t *x = inputs[0], *w = inputs[3], *y = outputs[0];
+        tensor_t *xs = inputs[1], *xz = inputs[2], *ws = inputs[4], *wz = inputs[5];
+        tensor_t *ys = inputs[6], *yz = inputs[7], *b = in(this, 8);
+        if (w->type != NNR_DATA_TYPE_INT8 || !w->has_host()) return bad(this, "weights must be constant int8");
+        if (!xs->has_host() || !ws->has_host() || !ys->has_host()) return bad(this, "scales must be constant");
+        if ((xz && xz->ndata && !xz->has_host()) || (yz && yz->ndata && !yz->has_host()) ||
+            (wz && wz->ndata && !wz->has_host()) || (b && !b->has_host()))
+            return bad(this, "zero points / bias must be constant");
+        d = nnrh_qconv_desc{};
+        d.N = x->dims[0]; d.C = x->dims[1]; d.H = x->dims[2]; d.W = x->dims[3];
+        d.OC = w->dims[0]; d.kH = w->dims[2]; d.kW = w->dims[3]; d.group = group;
+        d.sH = strides[0]; d.sW = strides[1]; d.dH = dilations[0]; d.dW = dilations[1];
+        d.pad_t = cpads[0]; d.pad_l = cpads[1]; d.pad_b = cpads[2]; d.pad_r = cpads[3];
+        d.oH = y->dims[2]; d.oW = y->dims[3];
+        d.x_nhwc = x->format == memory_layout_t::NHWC;
+        d.y_nhwc = y->format == memory_layout_t::NHWC;
+        d.post_fn = post_fn ? 1 : 0;
+        d.act_dtype = qdtype(x->type);
+        d.x_scale = xs->scalar_f32();
+        d.x_zp = zp_value(xz);
+        d.w_scale_host = ws->h<float>();
+        d.w_scale_count = (int)ws->ndata;
+        d.w_zp_host = (wz && wz->ndata) ? wz->h<int8_t>() : nullptr;
+        d.w_zp_count = wz ? (int)wz->ndata : 0;
+        d.y_scale = ys->scalar_f32();
+        d.y_zp = zp_value(yz);
+        d.w_host = w->h<int8_t>();
+        d.bias_host = (b && b->ndata) ? b->h<int32_t>() : nullptr;
+        if (dispatch_only) return ok(this, nnrh_qconv_dispatch(&d, &branch));
+        return true;
+    }
+    bool build() {
+        if (!describe(false)) return false;
+        nnrh_qconv_destroy(h);
+        h = nullptr;
+        if (!ok(this, nnrh_qconv_create(&h, &d))) return false;
+        nnrh_qconv_branch(h, &branch);
+        return true;
+    }
+    bool exec() override {
+        return ok(this, nnrh_qconv_run(h, inputs[0]->data, outputs[0]->data, ctx->stream));
+    }
+    double num_ops() const override {
+        const tensor_t *w = inputs[3], *y = outputs[0];
+        if (y->ndim() != 4 || w->ndim() != 4) return 0;
+        return 2.0 * y->dims[0] * y->dims[1] * y->dims[2] * y->dims[3] * (double)w->dims[1] * w->dims[2] *
+               w->dims[3];
+    }
+    double num_bytes() const override {
+        const tensor_t *x = inputs[0], *w = inputs[3], *y = outputs[0];
+        return (double)x->nbytes() + (double)y->nbytes() + (double)w->nbytes() + 8.0 * w->dims[0];
+    }
+    std::string variant() const override {
+        static const char* names[] = {"?", "DW", "FIRST", "DIRECT", "PACKED", "NR16", "IM2COL_S1", "IM2COL", "FLOAT"};
+        return branch >= 0 && branch <= 8 ? names[branch] : "?";
+    }
+};
+
+// ===========================================================================
+// QLinearMatMul (src/backend/cpu/QLinearMatMul.cpp), constant B
+struct QLinearMatMul_hip : operator_t {
+    nnrh_qmatmul_t h = nullptr;
+    int m = 0, n = 0, k = 0, batch = 1;
+    ~QLinearMatMul_hip() override { nnrh_qmatmul_destroy(h); }
+    bool init() override {
+        layout_mask = LAYOUT_NCHW;
+        return inputs.size() == 8 && outputs.size() == 1;
+    }
+    bool reshape() override {
+        tensor_t *a = inputs[0], *b = inputs[3], *y = outputs[0];
+        if (a->ndim() < 2 || b->ndim() != 2) return bad(this, "B must be a 2-D matrix");
+        m = a->dims[a->ndim() - 2];
+        k = a->dims[a->ndim() - 1];
+        if (b->dims[0] != k) return bad(this, "inner dimensions differ");
+        n = b->dims[1];
+        batch = 1;
+        std::vector<int> d(a->dims.begin(), a->dims.end() - 1);
+        for (int i = 0; i + 2 < a->ndim(); ++i) batch *= a->dims[i];
+        d.push_back(n);
+        if (!y->reshape(d, inputs[7]->type)) return false;
+        if (ctx->shape_only) return true;
+        if (!b->has_host()) return bad(this, "B must be a constant initializer");
+        nnrh_qmatmul_desc dsc{};
+        dsc.m = m; dsc.n = n; dsc.k = k;
+        dsc.a_dtype = qdtype(a->type);
+        dsc.b_dtype = qdtype(b->type);
+        dsc.y_dtype = qdtype(inputs[7]->type);
+        dsc.scale_dtype = inputs[1]->type == NNR_DATA_TYPE_FLOAT16 ? NNRH_F16 : NNRH_F32;
+        static const float one = 1.0f;
+        static const uint8_t zero_u8 = 0;
+        dsc.a_scale_host = inputs[1]->has_host() ? (const void*)inputs[1]->host.data() : (const void*)&one;
+        dsc.a_zp_host = inputs[2]->has_host() ? (const void*)inputs[2]->host.data() : (const void*)&zero_u8;
+        dsc.b_scale_host = inputs[4]->host.data();
+        dsc.b_zp_host = inputs[5] && inputs[5]->has_host() ? (const void*)inputs[5]->host.data() : (const void*)&zero_u8;
+        dsc.y_scale_host = inputs[6]->host.data();
+        dsc.y_zp_host = inputs[7]->host.data();
+        dsc.b_host = b->host.data();
+        if (!inputs[4]->has_host() || !inputs[6]->has_host() || !inputs[7]->has_host())
+            return bad(this, "b/y quantization must be constant");
+        nnrh_qmatmul_destroy(h);
+        h = nullptr;
+        return ok(this, nnrh_qmatmul_create(&h, &dsc));
+    }
+    bool exec() override {
+        const float* a_s_dev = inputs[1]->has_host() ? nullptr : (const float*)inputs[1]->data;
+        const void* a_z_dev = inputs[2]->has_host() ? nullptr : inputs[2]->data;
+        return ok(this, nnrh_qmatmul_run(h, inputs[0]->data, batch > 1 ? (long long)m * k : 0,
+                                         outputs[0]->data, batch, a_s_dev, a_z_dev, ctx->stream));
+    }
+    double num_ops() const override { return 2.0 * batch * m * (double)n * k; }
+};
+
+// MatMulInteger (src/backend/cpu/MatMulInteger.cpp)
+struct MatMulInteger_hip : operator_t {
+    nnrh_matmul_integer_t h = nullptr;
+    int m = 0, n = 0, k = 0, batch = 1;
+    bool b_batched = false;
+    ~MatMulInteger_hip() override { nnrh_matmul_integer_destroy(h); }
+    bool init() override { return inputs.size() >= 2 && inputs.size() <= 4 && outputs.size() == 1; }
+    bool reshape() override {
+        tensor_t *a = inputs[0], *b = inputs[1], *y = outputs[0];
+        if (a->ndim() < 2 || b->ndim() < 2) return bad(this, "operands must be at least 2-D");
+        m = a->dims[a->ndim() - 2];
+        k = a->dims[a->ndim() - 1];
+        n = b->dims[b->ndim() - 1];
+        if (b->dims[b->ndim() - 2] != k) return bad(this, "inner dimensions differ");
+        batch = 1;
+        for (int i = 0; i + 2 < a->ndim(); ++i) batch *= a->dims[i];
+        int bb = 1;
+        for (int i = 0; i + 2 < b->ndim(); ++i) bb *= b->dims[i];
+        if (bb != 1 && bb != batch) return bad(this, "only equal or broadcast B batches");
+        b_batched = bb > 1;
+        std::vector<int> d(a->dims.begin(), a->dims.end() - 1);
+        d.push_back(n);
+        if (!y->reshape(d, NNR_DATA_TYPE_INT32)) return false;
+        if (ctx->shape_only) return true;
+        for (int i = 2; i < 4; ++i)
+            if (in(this, i) && in(this, i)->ndata && !in(this, i)->has_host())
+                return bad(this, "zero points must be constant");
+        nnrh_matmul_integer_destroy(h);
+        h = nullptr;
+        return ok(this, nnrh_matmul_integer_create(&h, m, n, k, qdtype(a->type), qdtype(b->type), batch));
+    }
+    bool exec() override {
+        return ok(this, nnrh_matmul_integer_run(h, inputs[0]->data, batch > 1 ? (long long)m * k : 0,
+                                                inputs[1]->data, b_batched ? (long long)k * n : 0,
+                                                zp_value(in(this, 2)), zp_value(in(this, 3)),
+                                                (int32_t*)outputs[0]->data, batch, ctx->stream));
+    }
+    double num_ops() const override { return 2.0 * batch * m * (double)n * k; }
+};
+
+// ===========================================================================
+// QLinearAdd (src/backend/cpu/QLinearAdd.cpp)
+struct QLinearAdd_hip : operator_t {
+    int kind = 0;
+    bool swap = false;
+    int C = 0, HW = 0;
+    bool init() override {
+        layout_mask = LAYOUT_ALL;
+        return inputs.size() == 8 && outputs.size() == 1;
+    }
+    bool reshape() override {
+        tensor_t *a = inputs[0], *b = inputs[3], *y = outputs[0];
+        const tensor_t* full = a->ndata >= b->ndata ? a : b;
+        const tensor_t* other = a->ndata >= b->ndata ? b : a;
+        swap = false;
+        if (a->dims == b->dims) {
+            kind = 0;
+        } else if (b->ndata == 1) {
+            kind = 1;
+        } else if (a->ndata == 1) {
+            kind = 2;
+        } else if (full->ndim() == 4 && other->ndata == (size_t)full->dims[1] &&
+                   (other->ndim() == 1 || (other->ndim() == 4 && other->dims[0] == 1 && other->dims[2] == 1 &&
+                                           other->dims[3] == 1))) {
+            kind = 3;
+            swap = full == b;
+            C = full->dims[1];
+            HW = full->dims[2] * full->dims[3];
+        } else {
+            return bad(this, "general broadcasting is not supported");
+        }
+        y->format = full->format;
+        return y->reshape(full->dims, a->type);
+    }
+    bool exec() override {
+        tensor_t *a = inputs[0], *b = inputs[3];
+        float as = inputs[1]->scalar_f32(), bs = inputs[4]->scalar_f32(), ys = inputs[6]->scalar_f32();
+        int az = zp_value(inputs[2]), bz = zp_value(inputs[5]), yz = zp_value(inputs[7]);
+        if (swap)
+            return ok(this, nnrh_qlinear_add(3, b->data, a->data, outputs[0]->data, outputs[0]->ndata, C, HW,
+                                             outputs[0]->format == memory_layout_t::NHWC, qdtype(a->type),
+                                             bs, bz, as, az, ys, yz, ctx->stream));
+        return ok(this, nnrh_qlinear_add(kind, a->data, b->data, outputs[0]->data, outputs[0]->ndata, C, HW,
+                                         outputs[0]->format == memory_layout_t::NHWC, qdtype(a->type), as,
+                                         az, bs, bz, ys, yz, ctx->stream));
+    }
+};
+
+// ===========================================================================
+// MaxPool (src/backend/cpu/MaxPool.cpp); uint8 NHWC after fuse_qdq
+struct MaxPool_hip : operator_t {
+    std::vector<int> kernels, pads, strides;
+    int auto_pad = 0;
+    int cp[4] = {0, 0, 0, 0};
+    bool init() override {
+        for (auto v : attribute_ints("kernel_shape")) kernels.push_back((int)v);
+        if (kernels.size() != 2) return false;
+        auto p = attribute_ints("pads"), s = attribute_ints("strides"), d = attribute_ints("dilations");
+        for (auto v : d)
+            if (v != 1) return false;
+        if (attribute("ceil_mode", 0) != 0 || outputs.size() != 1) return false;
+        std::string ap = attribute_s("auto_pad", "NOTSET");
+        auto_pad = ap == "SAME_UPPER" ? 1 : ap == "SAME_LOWER" ? 2 : ap == "VALID" ? 3 : 0;
+        pads.assign(4, 0);
+        strides.assign(2, 1);
+        for (size_t i = 0; i < p.size() && i < 4; ++i) pads[i] = (int)p[i];
+        for (size_t i = 0; i < s.size() && i < 2; ++i) strides[i] = (int)s[i];
+        return true;
+    }
+    bool reshape() override {
+        tensor_t *x = inputs[0], *y = outputs[0];
+        if (x->ndim() != 4) return bad(this, "only 2-D pooling");
+        int out[2];
+        for (int i = 0; i < 2; ++i) {
+            int xd = x->dims[i + 2];
+            if (auto_pad == 1 || auto_pad == 2) {
+                int pad = (int)(ceilf(xd / (float)strides[i]) - 1) * strides[i] + kernels[i] - xd;
+                if (auto_pad == 1) { cp[i] = pad / 2; cp[i + 2] = pad - cp[i]; }
+                else { cp[i + 2] = pad / 2; cp[i] = pad - cp[i + 2]; }
+                out[i] = (int)ceilf(xd / (float)strides[i]);
+            } else if (auto_pad == 3) {
+                out[i] = (int)ceilf((xd - kernels[i] + 1) / (float)strides[i]);
+            } else {
+                cp[i] = pads[i];
+                cp[i + 2] = pads[i + 2];
+                out[i] = (int)floorf((xd + cp[i] + cp[i + 2] - kernels[i]) / (float)strides[i] + 1);
+            }
+        }
+        layout_mask = x->type == NNR_DATA_TYPE_UINT8 ? (LAYOUT_NCHW | LAYOUT_NHWC) : LAYOUT_NCHW;
+        y->format = x->format;
+        if (x->is_quantized()) y->set_quant(x->quant_scale, x->quant_zero_point);
+        if (!ctx->shape_only && !(x->type == NNR_DATA_TYPE_UINT8 && x->format == memory_layout_t::NHWC))
+            return bad(this, "only uint8 NHWC pooling is implemented on the HIP backend");
+        return y->reshape({x->dims[0], x->dims[1], out[0], out[1]}, x->type);
+    }
+    bool exec() override {
+        tensor_t *x = inputs[0], *y = outputs[0];
+        return ok(this, nnrh_maxpool_u8_nhwc((const uint8_t*)x->data, (uint8_t*)y->data, x->dims[0], x->dims[1],
+                                             x->dims[2], x->dims[3], y->dims[2], y->dims[3], kernels[0], kernels[1],
+                                             strides[0], strides[1], cp[0], cp[1], ctx->stream));
+    }
+};
+
+// GlobalAveragePool (src/backend/cpu/global_pool.cpp), fp32
+struct GlobalAveragePool_hip : operator_t {
+    bool init() override {
+        layout_mask = LAYOUT_NCHW | LAYOUT_NHWC;
+        return inputs.size() == 1 && outputs.size() == 1;
+    }
+    bool reshape() override {
+        tensor_t *x = inputs[0], *y = outputs[0];
+        if (x->ndim() != 4 || x->type != NNR_DATA_TYPE_FLOAT32) return bad(this, "fp32 4-D input");
+        return y->reshape({x->dims[0], x->dims[1], 1, 1}, x->type);
+    }
+    bool exec() override {
+        tensor_t* x = inputs[0];
+        return ok(this, nnrh_global_avgpool_f32((const float*)x->data, (float*)outputs[0]->data, x->dims[0],
+                                                x->dims[1], x->dims[2] * x->dims[3],
+                                                x->format == memory_layout_t::NHWC, ctx->stream));
+    }
+};
+
+// Flatten / Reshape: views of their input (src/backend/cpu/Flatten.cpp, Reshape.cpp)
+struct Flatten_hip : operator_t {
+    bool init() override { return inputs.size() >= 1 && outputs.size() == 1; }
+    int view_input_index() const override { return 0; }
+    bool reshape() override {
+        tensor_t *x = inputs[0], *y = outputs[0];
+        int axis = (int)attribute("axis", 1);
+        if (axis < 0) axis += x->ndim();
+        if (x->format == memory_layout_t::NHWC && x->ndim() == 4 && x->dims[2] * x->dims[3] > 1)
+            return bad(this, "NHWC input with spatial extent > 1");
+        int a = 1, b = 1;
+        for (int i = 0; i < x->ndim(); ++i) (i < axis ? a : b) *= x->dims[i];
+        return y->reshape({a, b}, x->type);
+    }
+    bool exec() override { return true; }
+};
+
+struct Reshape_hip : operator_t {
+    bool init() override { return inputs.size() >= 2 && outputs.size() == 1; }
+    int view_input_index() const override { return 0; }
+    bool reshape() override {
+        tensor_t *x = inputs[0], *s = inputs[1], *y = outputs[0];
+        if (!s->has_host() || s->type != NNR_DATA_TYPE_INT64) return bad(this, "shape must be a constant int64");
+        if (x->format == memory_layout_t::NHWC && x->ndim() == 4 && x->dims[2] * x->dims[3] > 1)
+            return bad(this, "NHWC input with spatial extent > 1");
+        std::vector<int> d;
+        const int64_t* sh = s->h<int64_t>();
+        int neg = -1;
+        size_t known = 1;
+        for (size_t i = 0; i < s->ndata; ++i) {
+            int v = (int)sh[i];
+            if (v == 0 && i < (size_t)x->ndim()) v = x->dims[i];
+            if (v == -1) { neg = (int)i; v = 1; }
+            else known *= (size_t)v;
+            d.push_back(v);
+        }
+        if (neg >= 0) d[neg] = known ? (int)(x->ndata / known) : 0;
+        return y->reshape(d, x->type);
+    }
+    bool exec() override { return true; }
+};
+
+// Gemm (src/backend/cpu/Gemm.cpp), fp32
+struct Gemm_hip : operator_t {
+    int M = 0, N = 0, K = 0, c_mode = 0;
+    bool init() override { return inputs.size() >= 2 && outputs.size() == 1; }
+    bool reshape() override {
+        tensor_t *a = inputs[0], *b = inputs[1], *c = in(this, 2), *y = outputs[0];
+        if (a->ndim() != 2 || b->ndim() != 2 || a->type != NNR_DATA_TYPE_FLOAT32) return bad(this, "fp32 2-D only");
+        int ta = (int)attribute("transA", 0), tb = (int)attribute("transB", 0);
+        M = ta ? a->dims[1] : a->dims[0];
+        K = ta ? a->dims[0] : a->dims[1];
+        N = tb ? b->dims[0] : b->dims[1];
+        if ((tb ? b->dims[1] : b->dims[0]) != K) return bad(this, "inner dimensions differ");
+        c_mode = 0;
+        if (c) {
+            if (c->ndata == 1) c_mode = 1;
+            else if (c->ndata == (size_t)N && (c->ndim() == 1 || c->dims[0] == 1)) c_mode = 2;
+            else if (c->ndata == (size_t)M * N) c_mode = 3;
+            else if (c->ndata == (size_t)M) c_mode = 4;
+            else return bad(this, "bias shape");
+        }
+        return y->reshape({M, N}, NNR_DATA_TYPE_FLOAT32);
+    }
+    bool exec() override {
+        tensor_t* c = in(this, 2);
+        return ok(this, nnrh_gemm_f32((const float*)inputs[0]->data, (const float*)inputs[1]->data,
+                                      c ? (const float*)c->data : nullptr, (float*)outputs[0]->data, M, N, K,
+                                      (int)attribute("transA", 0), (int)attribute("transB", 0),
+                                      attribute_f("alpha", 1.0f), attribute_f("beta", 1.0f), c_mode, ctx->stream));
+    }
+    double num_ops() const override { return 2.0 * M * (double)N * K; }
+};
+
+// Relu / Clip, fp32; fusable into a preceding producer (post_fn)
+struct Clip_hip : operator_t {
+    bool relu = false;
+    bool init() override {
+        layout_mask = LAYOUT_ALL;
+        fusable_unary = true;
+        return inputs.size() >= 1 && outputs.size() == 1;
+    }
+    bool reshape() override {
+        if (inputs[0]->type != NNR_DATA_TYPE_FLOAT32 && !ctx->shape_only && !skip)
+            return bad(this, "only fp32 (int8 Relu/Clip are fused or absorbed into Q)");
+        return operator_t::reshape();
+    }
+    bool exec() override {
+        float lo = relu ? 0.0f : -INFINITY, hi = INFINITY;
+        if (!relu) {
+            if (in(this, 1) && in(this, 1)->has_host()) lo = in(this, 1)->scalar_f32();
+            if (in(this, 2) && in(this, 2)->has_host()) hi = in(this, 2)->scalar_f32();
+        }
+        return ok(this, nnrh_clip_f32((const float*)inputs[0]->data, (float*)outputs[0]->data, inputs[0]->ndata,
+                                      lo, hi, ctx->stream));
+    }
+};
+
+template <typename T>
+operator_t* make(int) { return new T(); }
+operator_t* make_relu(int) {
+    auto* c = new Clip_hip();
+    c->relu = true;
+    return c;
+}
+
+const op_registrar_t reg[] = {
+    {"QuantizeLinear", backend_t::HIP, make<QuantizeLinear_hip>},
+    {"DequantizeLinear", backend_t::HIP, make<DequantizeLinear_hip>},
+    {"DynamicQuantizeLinear", backend_t::HIP, make<DynamicQuantizeLinear_hip>},
+    {"QLinearConv", backend_t::HIP, make<QLinearConv_hip>},
+    {"QLinearMatMul", backend_t::HIP, make<QLinearMatMul_hip>},
+    {"MatMulInteger", backend_t::HIP, make<MatMulInteger_hip>},
+    {"QLinearAdd", backend_t::HIP, make<QLinearAdd_hip>},
+    {"MaxPool", backend_t::HIP, make<MaxPool_hip>},
+    {"GlobalAveragePool", backend_t::HIP, make<GlobalAveragePool_hip>},
+    {"Flatten", backend_t::HIP, make<Flatten_hip>},
+    {"Reshape", backend_t::HIP, make<Reshape_hip>},
+    {"Gemm", backend_t::HIP, make<Gemm_hip>},
+    {"Relu", backend_t::HIP, make_relu},
+    {"Clip", backend_t::HIP, make<Clip_hip>},
+};
+
+}  // namespace
+
+// referenced by the host C ABI so the registrations above are linked in
+int hip_backend_op_count() { return (int)(sizeof(reg) / sizeof(reg[0])); }
+
+}  // namespace nnr

@@ -1,0 +1,432 @@
+// passes.cpp -- the graph-optimizer passes that decide numerics and kernel
+// dispatch on the int8 path, restated for the HIP backend:
+//   fold_constants    src/graph_optimizer/fold_constants.cpp:13-59
+//   fuse_qdq_compute  src/graph_optimizer/fuse_qdq_compute.cpp:25-350
+//   fuse_qdq          src/graph_optimizer/fuse_qdq.cpp:10-170
+//   fuse_post_ops     src/graph_optimizer/fuse_post_ops.cpp:10-73
+//   assign_layouts    src/graph_optimizer/assign_layouts.cpp:84-360 (int8
+//                     chains: force-accepted NHWC, then propagation)
+// The fused operators are created through the registry with the context's
+// preferred backend, exactly where the reference calls solve_operator.
+#include <cstdio>
+#include <unordered_map>
+#include <unordered_set>
+
+#include "nnr.h"
+
+namespace nnr {
+
+namespace {
+
+bool active(const operator_t* op) { return !op->skip && !op->folded; }
+
+int count_consumers(context_t* ctx, tensor_t* t, int skip_idx) {
+    int c = 0;
+    auto& nodes = ctx->nodes;
+    for (int j = 0; j < (int)nodes.size(); ++j) {
+        if (j == skip_idx || !active(nodes[j])) continue;
+        for (auto* x : nodes[j]->inputs)
+            if (x == t) c++;
+    }
+    return c;
+}
+
+tensor_t* input_or_null(operator_t* op, size_t i) {
+    return op->inputs.size() > i ? op->inputs[i] : nullptr;
+}
+
+// fuse_qdq_compute.cpp:7-23 -- uint8 weights become int8 (w - 128, zp - 128)
+void convert_weight_uint8_to_int8(tensor_t* w, tensor_t* w_zp) {
+    if (!w || w->type != NNR_DATA_TYPE_UINT8 || !w->has_host()) return;
+    for (auto& b : w->host) b = (uint8_t)(int8_t)((int)b - 128);
+    w->type = NNR_DATA_TYPE_INT8;
+    if (w_zp && w_zp->type == NNR_DATA_TYPE_UINT8 && w_zp->has_host()) {
+        for (auto& b : w_zp->host) b = (uint8_t)(int8_t)((int)b - 128);
+        w_zp->type = NNR_DATA_TYPE_INT8;
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+void fold_constants(context_t* ctx) {
+    std::unordered_set<const tensor_t*> constants;
+    for (auto& name : ctx->initializer_names) {
+        tensor_t* t = ctx->find(name);
+        if (t) constants.insert(t);
+    }
+    for (auto* n : ctx->nodes) {
+        if (n->skip) continue;
+        bool all_const = !n->inputs.empty();
+        for (auto* t : n->inputs)
+            if (t && !constants.count(t)) { all_const = false; break; }
+        if (!all_const) continue;
+        n->folded = true;
+        for (auto* t : n->outputs)
+            if (t) constants.insert(t);
+    }
+}
+
+// ---------------------------------------------------------------------------
+void fuse_qdq_compute(context_t* ctx) {
+    auto& nodes = ctx->nodes;
+    const int n = (int)nodes.size();
+    std::unordered_map<tensor_t*, int> producer, all_producer;
+    auto rebuild = [&]() {
+        producer.clear();
+        all_producer.clear();
+        for (int i = 0; i < n; ++i) {
+            for (auto* t : nodes[i]->outputs) all_producer[t] = i;
+            if (!active(nodes[i])) continue;
+            for (auto* t : nodes[i]->outputs) producer[t] = i;
+        }
+    };
+    rebuild();
+    auto dq_of = [&](tensor_t* t, bool any) -> operator_t* {
+        auto& m = any ? all_producer : producer;
+        auto it = m.find(t);
+        if (it == m.end()) return nullptr;
+        operator_t* nd = nodes[it->second];
+        return nd->op_type == "DequantizeLinear" ? nd : nullptr;
+    };
+    auto q_consumer = [&](tensor_t* t, int src) -> int {
+        for (int j = 0; j < n; ++j) {
+            if (j == src || !active(nodes[j])) continue;
+            if (nodes[j]->op_type != "QuantizeLinear") continue;
+            if (!nodes[j]->inputs.empty() && nodes[j]->inputs[0] == t) return j;
+        }
+        return -1;
+    };
+
+    int fused = 0;
+    // Phase 1: DQ -> Conv/MatMul -> Q   =>  QLinearConv / QLinearMatMul
+    for (int i = 0; i < n; ++i) {
+        operator_t* op = nodes[i];
+        if (!active(op)) continue;
+        const bool is_conv = op->op_type == "Conv", is_mm = op->op_type == "MatMul";
+        if (!is_conv && !is_mm) continue;
+        if (op->inputs.size() < 2 || !op->inputs[0] || !op->inputs[1]) continue;
+        operator_t* dq_x = dq_of(op->inputs[0], false);
+        if (!dq_x || dq_x->inputs.size() < 2) continue;
+        operator_t* dq_w = dq_of(op->inputs[1], true);
+        if (!dq_w || dq_w->inputs.size() < 2) continue;
+        operator_t* dq_b = nullptr;
+        if (is_conv && op->inputs.size() >= 3 && op->inputs[2]) dq_b = dq_of(op->inputs[2], true);
+        if (op->outputs.empty() || !op->outputs[0]) continue;
+        tensor_t* out = op->outputs[0];
+        if (count_consumers(ctx, out, i) != 1) continue;
+        int qi = q_consumer(out, i);
+        if (qi < 0) continue;
+        operator_t* q_y = nodes[qi];
+        if (q_y->inputs.size() < 2) continue;
+
+        const char* new_type = is_conv ? "QLinearConv" : "QLinearMatMul";
+        operator_t* f = solve_operator(new_type, op->opset, ctx->preferred_backend);
+        if (!f) continue;
+        f->ctx = ctx;
+        f->opset = op->opset;
+        f->op_type = new_type;
+        f->node_name = op->node_name;
+        f->inputs = {dq_x->inputs[0], dq_x->inputs[1], input_or_null(dq_x, 2),
+                     dq_w->inputs[0], dq_w->inputs[1], input_or_null(dq_w, 2),
+                     q_y->inputs[1], input_or_null(q_y, 2)};
+        if (dq_b) f->inputs.push_back(dq_b->inputs[0]);
+        if (is_conv) f->attrs = op->attrs;
+        f->outputs = {q_y->outputs[0]};
+        convert_weight_uint8_to_int8(f->inputs[3], f->inputs[5]);
+        f->init();
+        nodes[i] = f;
+        delete op;
+        if (count_consumers(ctx, dq_x->outputs[0], all_producer[dq_x->outputs[0]]) == 0) dq_x->folded = true;
+        dq_w->folded = true;
+        if (dq_b) dq_b->folded = true;
+        q_y->folded = true;
+        fused++;
+    }
+
+    // Phase 2: DQ + DQ -> Add [-> Relu] -> Q  =>  QLinearAdd
+    rebuild();
+    auto implicit_dq = [&](tensor_t* fp32) -> operator_t* {
+        int qi = -1;
+        for (int j = 0; j < n; ++j) {
+            if (nodes[j]->skip || nodes[j]->op_type != "QuantizeLinear") continue;
+            if (!nodes[j]->inputs.empty() && nodes[j]->inputs[0] == fp32) { qi = j; break; }
+        }
+        if (qi < 0) return nullptr;
+        tensor_t* qo = nodes[qi]->outputs[0];
+        for (int j = 0; j < n; ++j) {
+            if (nodes[j]->skip || nodes[j]->op_type != "DequantizeLinear") continue;
+            if (!nodes[j]->inputs.empty() && nodes[j]->inputs[0] == qo) return nodes[j];
+        }
+        return nullptr;
+    };
+    int add_fused = 0;
+    for (int i = 0; i < n; ++i) {
+        operator_t* op = nodes[i];
+        if (!active(op) || op->op_type != "Add") continue;
+        if (op->inputs.size() < 2 || !op->inputs[0] || !op->inputs[1]) continue;
+        operator_t* dq_a = dq_of(op->inputs[0], false);
+        if (!dq_a) dq_a = implicit_dq(op->inputs[0]);
+        operator_t* dq_b = dq_of(op->inputs[1], false);
+        if (!dq_b) dq_b = implicit_dq(op->inputs[1]);
+        if (!dq_a || dq_a->inputs.size() < 2 || !dq_b || dq_b->inputs.size() < 2) continue;
+        if (op->outputs.empty() || !op->outputs[0]) continue;
+        tensor_t* add_out = op->outputs[0];
+        if (count_consumers(ctx, add_out, i) != 1) continue;
+        int relu = -1;
+        tensor_t* pre_q = add_out;
+        for (int j = 0; j < n; ++j) {
+            if (j == i || !active(nodes[j])) continue;
+            bool uses = false;
+            for (auto* t : nodes[j]->inputs) uses |= (t == add_out);
+            if (!uses) continue;
+            if (nodes[j]->op_type == "Relu") {
+                relu = j;
+                pre_q = nodes[j]->outputs[0];
+            }
+            break;
+        }
+        if (relu >= 0 && count_consumers(ctx, pre_q, relu) != 1) continue;
+        int qi = q_consumer(pre_q, relu >= 0 ? relu : i);
+        if (qi < 0) continue;
+        operator_t* q_y = nodes[qi];
+        if (q_y->inputs.size() < 2) continue;
+        operator_t* f = solve_operator("QLinearAdd", op->opset, ctx->preferred_backend);
+        if (!f) continue;
+        f->ctx = ctx;
+        f->opset = op->opset;
+        f->op_type = "QLinearAdd";
+        f->node_name = op->node_name;
+        f->inputs = {dq_a->inputs[0], dq_a->inputs[1], input_or_null(dq_a, 2),
+                     dq_b->inputs[0], dq_b->inputs[1], input_or_null(dq_b, 2),
+                     q_y->inputs[1], input_or_null(q_y, 2)};
+        f->outputs = {q_y->outputs[0]};
+        f->init();
+        tensor_t* in0 = op->inputs[0];
+        tensor_t* in1 = op->inputs[1];
+        nodes[i] = f;
+        delete op;
+        if (count_consumers(ctx, dq_a->outputs[0], all_producer[in0]) == 0) dq_a->folded = true;
+        if (count_consumers(ctx, dq_b->outputs[0], all_producer[in1]) == 0) dq_b->folded = true;
+        if (relu >= 0) nodes[relu]->folded = true;
+        q_y->folded = true;
+        add_fused++;
+    }
+    ctx->fusion_stats["qdq_compute"] += fused;
+    ctx->fusion_stats["qdq_add"] += add_fused;
+    if (fused || add_fused)
+        fprintf(stderr, "[nnr] Fused %d QDQ compute + %d QDQ add patterns\n", fused, add_fused);
+}
+
+// ---------------------------------------------------------------------------
+void fuse_qdq(context_t* ctx) {
+    auto& nodes = ctx->nodes;
+    const int n = (int)nodes.size();
+    static const std::unordered_set<std::string> quant_capable = {
+        "MaxPool", "AveragePool", "Concat", "Reshape", "Transpose", "Flatten", "Squeeze",
+        "Unsqueeze", "Relu", "Clip", "Pad", "Slice", "Gather", "Split", "Resize"};
+    auto scale_zp = [](operator_t* op, float& s, int32_t& zp) -> bool {
+        if (op->inputs.size() < 2 || !op->inputs[1]) return false;
+        tensor_t* st = op->inputs[1];
+        if (st->ndata != 1 || !st->has_host() || st->type != NNR_DATA_TYPE_FLOAT32) return false;
+        s = st->scalar_f32();
+        zp = 0;
+        if (op->inputs.size() >= 3 && op->inputs[2] && op->inputs[2]->ndata > 0)
+            zp = op->inputs[2]->scalar_int();
+        return true;
+    };
+    int fused = 0;
+    for (int i = 0; i < n; ++i) {
+        operator_t* nd = nodes[i];
+        if (!active(nd) || nd->op_type != "DequantizeLinear" || nd->outputs.empty()) continue;
+        tensor_t* dq_out = nd->outputs[0];
+        tensor_t* dq_in = nd->inputs[0];
+        if (count_consumers(ctx, dq_out, i) != 1) continue;
+        int ci = -1;
+        for (int j = 0; j < n && ci < 0; ++j) {
+            if (j == i || !active(nodes[j])) continue;
+            for (auto* t : nodes[j]->inputs)
+                if (t == dq_out) { ci = j; break; }
+        }
+        if (ci < 0) continue;
+        operator_t* c = nodes[ci];
+        if (c->op_type == "DequantizeLinear" || c->op_type == "QuantizeLinear") continue;
+        if (!quant_capable.count(c->op_type) || !c->resolved) continue;
+        if (c->outputs.empty()) continue;
+        tensor_t* c_out = c->outputs[0];
+        int qi = -1;
+        for (int j = 0; j < n && qi < 0; ++j) {
+            if (j == ci || !active(nodes[j]) || nodes[j]->op_type != "QuantizeLinear") continue;
+            for (auto* t : nodes[j]->inputs)
+                if (t == c_out) { qi = j; break; }
+        }
+        if (qi < 0) continue;
+        operator_t* q = nodes[qi];
+        if (count_consumers(ctx, c_out, ci) != 1) continue;
+        float ds, qs;
+        int32_t dz, qz;
+        if (!scale_zp(nd, ds, dz) || !scale_zp(q, qs, qz)) continue;
+        dq_in->set_quant(ds, dz);
+        tensor_t* q_out = q->outputs[0];
+        q_out->set_quant(qs, qz);
+        for (auto& t : c->inputs)
+            if (t == dq_out) t = dq_in;
+        for (auto& t : c->outputs)
+            if (t == c_out) t = q_out;
+        nd->folded = true;
+        q->folded = true;
+        fused++;
+    }
+    ctx->fusion_stats["qdq_transparent"] += fused;
+    if (fused) fprintf(stderr, "[nnr] Fused %d QDQ patterns\n", fused);
+}
+
+// ---------------------------------------------------------------------------
+void fuse_post_ops(context_t* ctx) {
+    auto& nodes = ctx->nodes;
+    const int n = (int)nodes.size();
+    int fused = 0;
+    for (int i = 0; i + 1 < n; ++i) {
+        operator_t* p = nodes[i];
+        if (p->skip || p->post_fn) continue;
+        const std::string& t = p->op_type;
+        if (t != "Conv" && t != "Gemm" && t != "MatMul" && t != "QLinearConv") continue;
+        if (p->outputs.empty()) continue;
+        tensor_t* eff = p->outputs[0];
+        int j = i + 1;
+        for (; j < n && (nodes[j]->skip || nodes[j]->folded); ++j) {
+            operator_t* sk = nodes[j];
+            if (!sk->inputs.empty() && !sk->outputs.empty() && sk->inputs[0] == eff) eff = sk->outputs[0];
+        }
+        if (j >= n) continue;
+        operator_t* c = nodes[j];
+        if (!c->fusable_unary || c->inputs.empty()) continue;
+        tensor_t* raw = p->outputs[0];
+        tensor_t* matched = nullptr;
+        for (auto* x : c->inputs)
+            if (x == eff || x == raw) { matched = x; break; }
+        if (!matched) continue;
+        if (count_consumers(ctx, matched, -1) != 1) continue;
+        if (c->inputs.size() == 2) continue;   // binary ops are never fused
+        p->post_fn = true;
+        p->fused_op = c;
+        c->skip = true;
+        // a skipped step forwards its input buffer (src/nnr.cpp:914-918)
+        if (!c->outputs.empty()) c->outputs[0]->alias_of = matched;
+        fused++;
+    }
+    ctx->fusion_stats["post_ops"] += fused;
+}
+
+// ---------------------------------------------------------------------------
+void assign_layouts(context_t* ctx) {
+    auto& nodes = ctx->nodes;
+    const int n = (int)nodes.size();
+    std::unordered_map<tensor_t*, int> consumers;
+    std::unordered_map<tensor_t*, int> first_consumer;
+    for (int i = 0; i < n; ++i) {
+        if (!active(nodes[i])) continue;
+        for (auto* t : nodes[i]->inputs) {
+            if (!t) continue;
+            if (!consumers[t]++) first_consumer[t] = i;
+        }
+    }
+    std::unordered_set<tensor_t*> graph_outs;
+    for (auto& s : ctx->graph_outputs) graph_outs.insert(ctx->find(s));
+    std::unordered_set<tensor_t*> nhwc;
+    std::unordered_map<tensor_t*, int> producer;
+    for (int i = 0; i < n; ++i)
+        if (active(nodes[i]))
+            for (auto* t : nodes[i]->outputs) producer[t] = i;
+    auto is_act4d = [&](tensor_t* t) {
+        return t && t->ndim() == 4 && !ctx->initializer_names.count(t->name);
+    };
+    std::vector<bool> visited(n, false);
+    // chain formation from each NHWC-capable QLinearConv (:84-297). Chains of
+    // QLinearConv are force-accepted (all-int8), so no cost model is needed.
+    for (int s = 0; s < n; ++s) {
+        operator_t* op = nodes[s];
+        if (!active(op) || op->op_type != "QLinearConv" || !(op->layout_mask & LAYOUT_NHWC) || visited[s])
+            continue;
+        std::vector<int> chain;
+        int cur = s;
+        while (cur >= 0 && cur < n) {
+            operator_t* nd = nodes[cur];
+            if (!active(nd)) { cur++; continue; }
+            if (!(nd->layout_mask & LAYOUT_NHWC)) break;
+            int n4 = 0, in_chain = 0;
+            for (auto* t : nd->inputs) {
+                if (!is_act4d(t)) continue;
+                n4++;
+                bool ok = false;
+                auto it = producer.find(t);
+                if (it != producer.end())
+                    for (int e : chain) ok |= (e == it->second);
+                if (!ok && nhwc.count(t)) ok = true;
+                in_chain += ok;
+            }
+            if (n4 > 1 && in_chain < n4) break;
+            if (nd->op_type == "Conv") break;   // float chains need the cost model
+            chain.push_back(cur);
+            visited[cur] = true;
+            if (nd->outputs.empty()) break;
+            tensor_t* out = nd->outputs[0];
+            if (graph_outs.count(out) || consumers[out] != 1) break;
+            auto fc = first_consumer.find(out);
+            if (fc == first_consumer.end() || visited[fc->second]) break;
+            cur = fc->second;
+        }
+        for (int e : chain)
+            for (auto* t : nodes[e]->outputs)
+                if (t && t->ndim() == 4 &&
+                    (t->type == NNR_DATA_TYPE_FLOAT32 || t->type == NNR_DATA_TYPE_UINT8 ||
+                     t->type == NNR_DATA_TYPE_INT8)) {
+                    t->format = memory_layout_t::NHWC;
+                    nhwc.insert(t);
+                }
+    }
+    // propagation through NHWC-capable inter-chain nodes (:283-360)
+    auto consumers_safe = [&](tensor_t* t) {
+        for (int j = 0; j < n; ++j) {
+            operator_t* c = nodes[j];
+            if (!active(c)) continue;
+            for (auto* x : c->inputs) {
+                if (x != t) continue;
+                bool out_nhwc = !c->outputs.empty() && nhwc.count(c->outputs[0]);
+                bool sup = c->layout_mask == LAYOUT_ALL || (c->layout_mask & LAYOUT_NHWC);
+                if (!out_nhwc && !sup) return false;
+                break;
+            }
+        }
+        return true;
+    };
+    bool changed = true;
+    while (changed) {
+        changed = false;
+        for (int i = 0; i < n; ++i) {
+            operator_t* nd = nodes[i];
+            if (!active(nd)) continue;
+            bool all = nd->layout_mask == LAYOUT_ALL;
+            if (!all && !(nd->layout_mask & LAYOUT_NHWC)) continue;
+            bool has = false;
+            for (auto* t : nd->inputs) has |= (t && nhwc.count(t));
+            if (!has) continue;
+            if (!all) {
+                bool ok = true;
+                for (auto* t : nd->inputs)
+                    if (is_act4d(t) && !nhwc.count(t)) ok = false;
+                if (!ok) continue;
+            }
+            for (auto* t : nd->outputs) {
+                if (!t || t->ndim() != 4 || nhwc.count(t)) continue;
+                if (!consumers_safe(t)) continue;
+                t->format = memory_layout_t::NHWC;
+                nhwc.insert(t);
+                changed = true;
+            }
+        }
+    }
+    ctx->fusion_stats["nhwc_tensors"] = (int)nhwc.size();
+}
+
+}  // namespace nnr

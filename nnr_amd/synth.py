@@ -1,0 +1,152 @@
+"""Synthetic int8 QDQ graphs of the benchmark configurations.
+
+Each builder returns a `Graph` in the QDQ form the reference fuses
+(fuse_qdq_compute.cpp:100-207): DequantizeLinear -> Conv / MatMul ->
+QuantizeLinear, with Relu absorbed into the output quantization (zero point
+0; NNR does not fuse DQ->Conv->Relu->Q, fuse_qdq_compute.cpp:128-134), and
+residual additions as DQ + DQ -> Add -> Relu -> Q (fused to QLinearAdd,
+fuse_qdq_compute.cpp:209-345). Weights are random-init, quantized per output
+channel to int8 (symmetric, zero point 0); activation scales are drawn from
+[0.01, 0.05] with a seeded generator, so every run rebuilds the same graph.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .graph import Graph
+
+F32 = np.float32
+
+
+class _QDQ:
+    """Helper emitting QDQ patterns into a Graph."""
+
+    def __init__(self, g: Graph, rng):
+        self.g = g
+        self.rng = rng
+        self.n = 0
+
+    def uid(self, p):
+        self.n += 1
+        return f"{p}{self.n}"
+
+    def scale(self):
+        return F32(self.rng.uniform(0.01, 0.05))
+
+    def qparams(self, s, zp, dt=np.uint8):
+        n = self.uid("q")
+        return (self.g.init(n + "_s", np.array(s, F32)),
+                self.g.init(n + "_z", np.array(zp, dt)))
+
+    def quant(self, x_f, s, zp, name=None):
+        sn, zn = self.qparams(s, zp)
+        return self.g.node("QuantizeLinear", [x_f, sn, zn], name=name or self.uid("Q")), (s, zp)
+
+    def dequant(self, x_q, qp, name=None):
+        s, zp = qp
+        sn, zn = self.qparams(s, zp)
+        return self.g.node("DequantizeLinear", [x_q, sn, zn], name=name or self.uid("DQ"))
+
+    def conv(self, x_q, x_qp, cin, cout, k, stride=1, pad=0, relu=True, name=None, group=1,
+             y_scale=None, y_zp=None):
+        """DQ(x) -> Conv(DQ(w), DQ(b)) -> Q(y); returns (y_q, y_qp)."""
+        g, rng = self.g, self.rng
+        name = name or self.uid("conv")
+        fan_in = cin // group * k * k
+        w = rng.normal(0.0, np.sqrt(2.0 / fan_in), (cout, cin // group, k, k)).astype(F32)
+        ws = (np.abs(w).reshape(cout, -1).max(1) / 127.0).astype(F32)
+        ws = np.maximum(ws, F32(1e-8))
+        wq = np.clip(np.rint(w / ws[:, None, None, None]), -127, 127).astype(np.int8)
+        bias_f = rng.normal(0.0, 0.1, cout).astype(F32)
+        bs = (F32(x_qp[0]) * ws).astype(F32)
+        bq = np.rint(bias_f / bs).astype(np.int32)
+        wn = g.init(name + "_w", wq)
+        wsn = g.init(name + "_ws", ws)
+        wzn = g.init(name + "_wz", np.zeros(cout, np.int8))
+        bn = g.init(name + "_b", bq)
+        bsn = g.init(name + "_bs", bs)
+        bzn = g.init(name + "_bz", np.zeros(cout, np.int32))
+        w_f = g.node("DequantizeLinear", [wn, wsn, wzn], name=name + "_wdq", axis=0)
+        b_f = g.node("DequantizeLinear", [bn, bsn, bzn], name=name + "_bdq", axis=0)
+        x_f = self.dequant(x_q, x_qp)
+        y_f = g.node("Conv", [x_f, w_f, b_f], name=name, kernel_shape=[k, k],
+                     strides=[stride, stride], pads=[pad, pad, pad, pad], group=group,
+                     dilations=[1, 1])
+        ys = self.scale() if y_scale is None else F32(y_scale)
+        yz = (0 if relu else 128) if y_zp is None else y_zp
+        return self.quant(y_f, ys, yz)
+
+
+def resnet50(batch=256, hw=224, seed=3, num_classes=1000):
+    """ResNet-50 v1.5 int8 QDQ: stem 7x7/2 + maxpool, bottleneck stages
+    [3,4,6,3] widths 64/128/256/512 (x4 expansion, stride on the 3x3),
+    fp32 GlobalAveragePool + Gemm head."""
+    g = Graph()
+    rng = np.random.default_rng(seed)
+    q = _QDQ(g, rng)
+    g.inputs["input"] = (np.float32, (batch, 3, hw, hw))
+    x_q, x_qp = q.quant("input", F32(1.0 / 255.0), 0, name="input_Q")
+    y_q, y_qp = q.conv(x_q, x_qp, 3, 64, 7, stride=2, pad=3, name="stem")
+    # maxpool in the quantized domain: DQ -> MaxPool -> Q (same scale)
+    mp_f = g.node("MaxPool", [q.dequant(y_q, y_qp)], name="maxpool", kernel_shape=[3, 3],
+                  strides=[2, 2], pads=[1, 1, 1, 1])
+    x_q, x_qp = q.quant(mp_f, *y_qp)
+    cin = 64
+    for si, (width, blocks) in enumerate(zip((64, 128, 256, 512), (3, 4, 6, 3))):
+        for bi in range(blocks):
+            stride = 2 if (bi == 0 and si > 0) else 1
+            nm = f"s{si + 1}b{bi + 1}"
+            a, a_qp = q.conv(x_q, x_qp, cin, width, 1, name=nm + "_c1")
+            a, a_qp = q.conv(a, a_qp, width, width, 3, stride=stride, pad=1, name=nm + "_c2")
+            a, a_qp = q.conv(a, a_qp, width, width * 4, 1, relu=False, name=nm + "_c3")
+            if bi == 0:
+                sc, sc_qp = q.conv(x_q, x_qp, cin, width * 4, 1, stride=stride, relu=False,
+                                   name=nm + "_ds")
+            else:
+                sc, sc_qp = x_q, x_qp
+            s = g.node("Add", [q.dequant(a, a_qp), q.dequant(sc, sc_qp)], name=nm + "_add")
+            r = g.node("Relu", [s], name=nm + "_relu")
+            x_q, x_qp = q.quant(r, q.scale(), 0)
+            cin = width * 4
+    # head: DQ -> GAP -> Flatten -> Gemm (fp32)
+    f = q.dequant(x_q, x_qp, name="head_dq")
+    p = g.node("GlobalAveragePool", [f], name="gap")
+    fl = g.node("Flatten", [p], name="flatten", axis=1)
+    fw = g.init("fc_w", rng.normal(0.0, np.sqrt(1.0 / cin), (num_classes, cin)).astype(F32))
+    fb = g.init("fc_b", rng.normal(0.0, 0.01, num_classes).astype(F32))
+    g.node("Gemm", [fl, fw, fb], outputs="logits", name="fc", transB=1)
+    g.outputs.append("logits")
+    return g
+
+
+def resnet50_conv_ops(hw=224):
+    """Algorithmic int8 ops per image of the ResNet-50 convolutions."""
+    ops = 0.0
+    s = hw // 2
+    ops += 2 * 64 * s * s * 3 * 49
+    s //= 2
+    cin = 64
+    for si, (w, blocks) in enumerate(zip((64, 128, 256, 512), (3, 4, 6, 3))):
+        for bi in range(blocks):
+            stride = 2 if (bi == 0 and si > 0) else 1
+            so = s // stride
+            ops += 2 * w * s * s * cin              # c1 at input resolution
+            ops += 2 * w * so * so * w * 9          # c2
+            ops += 2 * 4 * w * so * so * w          # c3
+            if bi == 0:
+                ops += 2 * 4 * w * so * so * cin    # downsample
+            s = so
+            cin = 4 * w
+    return ops
+
+
+def qconv_graph(batch=32, seed=2):
+    """cfg2 as a graph: Q(input) -> DQ -> Conv 3x3 -> Q (Relu absorbed)."""
+    g = Graph()
+    rng = np.random.default_rng(seed)
+    q = _QDQ(g, rng)
+    g.inputs["input"] = (np.float32, (batch, 64, 56, 56))
+    x_q, x_qp = q.quant("input", F32(0.02), 128, name="input_Q")
+    y, _ = q.conv(x_q, x_qp, 64, 64, 3, pad=1, name="conv", y_scale=0.03, y_zp=0)
+    g.outputs.append(y)
+    return g

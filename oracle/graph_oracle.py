@@ -1,0 +1,114 @@
+"""Replays a prepared plan of the host framework on the CPU oracle.
+
+TEST INFRASTRUCTURE ONLY. Given the active node list of a Session (after
+QDQ fusion and layout assignment) and the Graph it came from, every node is
+executed with the oracle's restatement of the reference operator, on arrays
+kept in the same physical layout as the device tensors (NHWC when the plan
+says so), so any intermediate tensor can be compared bit for bit.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import pyoracle as O
+
+
+def _nchw_to_phys(a, nhwc):
+    return a.transpose(0, 2, 3, 1).copy() if nhwc and a.ndim == 4 else a
+
+
+def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None):
+    """plan: Session.plan(); fmt_of(name) -> 0/1 layout of a tensor.
+    Returns {tensor name: physical numpy array} of every produced tensor."""
+    init = graph.initializers
+    env = {}
+    for k, v in feeds.items():
+        env[k] = v
+
+    def val(name):
+        return env[name] if name in env else init[name]
+
+    def scal(name, default=0):
+        if not name:
+            return default
+        return val(name).reshape(-1)[0]
+
+    for nd in plan:
+        op, ins, outs = nd["op"], nd["inputs"], nd["outputs"]
+        if op == "QuantizeLinear":
+            zdt = init[ins[2]].dtype if len(ins) > 2 and ins[2] else np.uint8
+            y = O.quantize_linear(val(ins[0]), float(scal(ins[1])), int(scal(ins[2])), zdt)
+        elif op == "DequantizeLinear":
+            y = O.dequantize_linear(val(ins[0]), float(scal(ins[1])), int(scal(ins[2])))
+        elif op == "QLinearConv":
+            src = graph.node_by_name(nd["name"])
+            a = src.attrs
+            x = val(ins[0])
+            w = init[ins[3]]
+            x_nhwc, y_nhwc = fmt_of(ins[0]), fmt_of(outs[0])
+            N = x.shape[0]
+            Cc, H, W = (x.shape[3], x.shape[1], x.shape[2]) if x_nhwc else x.shape[1:]
+            k = a.get("kernel_shape", list(w.shape[2:]))
+            cv = O.Conv(N, Cc, H, W, w.shape[0], k[0], k[1], group=a.get("group", 1),
+                        stride=tuple(a.get("strides", [1, 1])), dil=tuple(a.get("dilations", [1, 1])),
+                        pads=tuple(a.get("pads", [0, 0, 0, 0])), x_nhwc=x_nhwc, y_nhwc=y_nhwc,
+                        post_fn=nd["post_fn"], act_dtype=x.dtype.type,
+                        x_scale=float(scal(ins[1])), x_zp=int(scal(ins[2])),
+                        w_scale=init[ins[4]], w_zp=init[ins[5]] if ins[5] else (),
+                        y_scale=float(scal(ins[6])), y_zp=int(scal(ins[7])),
+                        bias=init[ins[8]] if len(ins) > 8 and ins[8] else None)
+            y, br = cv.run(x, w)
+            nd["oracle_branch"] = br
+        elif op == "QLinearMatMul":
+            y = O.qlinear_matmul(val(ins[0]), float(scal(ins[1])), int(scal(ins[2])),
+                                 init[ins[3]], float(scal(ins[4])), int(scal(ins[5])),
+                                 float(scal(ins[6])), int(scal(ins[7])), init[ins[7]].dtype)
+        elif op == "QLinearAdd":
+            a_, b_ = val(ins[0]), val(ins[3])
+            if a_.shape != b_.shape:
+                raise NotImplementedError("broadcast QLinearAdd in the plan replay")
+            y = O.qlinear_add(0, a_, b_, float(scal(ins[1])), int(scal(ins[2])),
+                              float(scal(ins[4])), int(scal(ins[5])), float(scal(ins[6])),
+                              int(scal(ins[7])))
+        elif op == "MaxPool":
+            src = graph.node_by_name(nd["name"])
+            a = src.attrs
+            x = val(ins[0])
+            assert fmt_of(ins[0]) == 1 and x.dtype == np.uint8
+            k, s, p = a["kernel_shape"], a.get("strides", [1, 1]), a.get("pads", [0, 0, 0, 0])
+            oH = (x.shape[1] + p[0] + p[2] - k[0]) // s[0] + 1
+            oW = (x.shape[2] + p[1] + p[3] - k[1]) // s[1] + 1
+            y = O.maxpool_u8_nhwc(x, k[0], k[1], s[0], s[1], p[0], p[1], oH, oW)
+        elif op == "GlobalAveragePool":
+            x = val(ins[0])
+            if fmt_of(ins[0]):
+                y = x.mean(axis=(1, 2), dtype=np.float64).astype(np.float32)[:, :, None, None]
+            else:
+                y = x.mean(axis=(2, 3), dtype=np.float64).astype(np.float32)[:, :, None, None]
+        elif op in ("Flatten",):
+            x = val(ins[0])
+            ax = graph.node_by_name(nd["name"]).attrs.get("axis", 1)
+            y = x.reshape(int(np.prod(x.shape[:ax])), -1)
+        elif op == "Reshape":
+            x = val(ins[0])
+            shp = [int(v) for v in init[ins[1]]]
+            shp = [x.shape[i] if v == 0 else v for i, v in enumerate(shp)]
+            y = x.reshape(shp)
+        elif op == "Gemm":
+            a = graph.node_by_name(nd["name"]).attrs
+            A = val(ins[0]).astype(np.float64)
+            B = val(ins[1]).astype(np.float64)
+            if a.get("transA", 0):
+                A = A.T
+            if a.get("transB", 0):
+                B = B.T
+            y = a.get("alpha", 1.0) * (A @ B)
+            if len(ins) > 2 and ins[2]:
+                y = y + a.get("beta", 1.0) * val(ins[2]).astype(np.float64)
+            y = y.astype(np.float32)
+        else:
+            raise NotImplementedError(op)
+        env[outs[0]] = y
+        if stop_after and nd["name"] == stop_after:
+            break
+    return env

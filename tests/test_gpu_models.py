@@ -1,0 +1,63 @@
+"""End-to-end parity of the configuration graphs through the host framework
+(C++ context_t, HIP backend): every int8 tensor of the executed plan is
+compared bit for bit with the oracle replaying the same plan; fp32 outputs
+within the reference's float tolerance (tensor_equal: |a-b| <= 1e-3)."""
+import numpy as np
+import pytest
+
+from nnr_amd import graph as G
+from nnr_amd import synth
+from oracle import graph_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def check_graph(g, feeds, out_name, atol=1e-3):
+    s = G.Session(g)
+    for k, v in feeds.items():
+        s.set_input(k, v)
+    s.run()
+    plan = s.plan()
+    fmt = lambda n: s.tensor_info(n)[3]
+    env = graph_oracle.run_plan(plan, g, feeds, fmt)
+    n_int = 0
+    for p in plan:
+        o = p["outputs"][0]
+        dev, _ = s.output(o)
+        ref = env[o]
+        assert dev.shape == ref.shape, (p["name"], dev.shape, ref.shape)
+        if dev.dtype in (np.uint8, np.int8):
+            mism = np.count_nonzero(dev != ref)
+            assert mism == 0, f"{p['name']} ({p['op']} {p['variant']}): {mism} of {dev.size} differ"
+            if p["op"] == "QLinearConv":
+                assert p.get("oracle_branch") is not None
+            n_int += 1
+        else:
+            np.testing.assert_allclose(dev, ref, atol=atol, rtol=1e-4, err_msg=p["name"])
+    out, _ = s.output(out_name)
+    return plan, out, n_int
+
+
+def test_resnet50_b2_bitexact(dev):
+    g = synth.resnet50(batch=2, hw=224)
+    rng = np.random.default_rng(10)
+    x = rng.random((2, 3, 224, 224), dtype=np.float32)
+    plan, logits, n_int = check_graph(g, {"input": x}, "logits")
+    assert n_int == 53 + 16 + 1 + 1           # convs, adds, maxpool, input Q
+    assert logits.shape == (2, 1000) and np.isfinite(logits).all()
+
+
+def test_resnet50_small_input(dev):
+    """Same network at 96x96 (ragged spatial sizes 48/24/12/6/3)."""
+    g = synth.resnet50(batch=3, hw=96, seed=11)
+    rng = np.random.default_rng(12)
+    x = rng.random((3, 3, 96, 96), dtype=np.float32)
+    check_graph(g, {"input": x}, "logits")
+
+
+def test_qconv_graph_config2(dev):
+    g = synth.qconv_graph(batch=4)
+    rng = np.random.default_rng(13)
+    x = (rng.random((4, 64, 56, 56), dtype=np.float32) * 5 - 2.5).astype(np.float32)
+    plan, y, _ = check_graph(g, {"input": x}, g.outputs[0])
+    assert [p["variant"] for p in plan if p["op"] == "QLinearConv"] == ["NR16"]

@@ -1,0 +1,91 @@
+"""Graph-layer checks without a GPU: the host framework's passes turn the
+synthetic QDQ graphs into the plan the reference's optimizer produces
+(fuse_qdq_compute, fuse_qdq, assign_layouts) and each QLinearConv resolves to
+the kernel branch QLinearConv::exec_simd_4d would take."""
+import collections
+
+import numpy as np
+import pytest
+
+from nnr_amd import graph as G
+from nnr_amd import synth
+from oracle import pyoracle as O
+
+
+@pytest.fixture(scope="module")
+def resnet_plan():
+    g = synth.resnet50(batch=2, hw=224)
+    s = G.Session(g, device=False)
+    return g, s, s.plan()
+
+
+def test_resnet50_fusion_counts(resnet_plan):
+    g, s, plan = resnet_plan
+    ops = collections.Counter(p["op"] for p in plan)
+    assert ops == {"QLinearConv": 53, "QLinearAdd": 16, "QuantizeLinear": 1, "MaxPool": 1,
+                   "DequantizeLinear": 1, "GlobalAveragePool": 1, "Flatten": 1, "Gemm": 1}
+    assert s.fusion_stat("qdq_compute") == 53
+    assert s.fusion_stat("qdq_add") == 16
+    assert s.fusion_stat("qdq_transparent") == 1
+
+
+def test_resnet50_branches_and_layouts(resnet_plan):
+    g, s, plan = resnet_plan
+    br = collections.Counter(p["variant"] for p in plan if p["op"] == "QLinearConv")
+    # stem -> first-layer (RQ-C); 3x3 s1 -> NR16; 1x1 and 3x3 s2 -> NR48 (RQ-B)
+    assert br == {"FIRST": 1, "NR16": 13, "PACKED": 39}
+    fmt = lambda n: s.tensor_info(n)[3]
+    for p in plan:
+        if p["op"] in ("QLinearConv", "QLinearAdd", "MaxPool"):
+            assert fmt(p["outputs"][0]) == 1, p["name"]      # int8 chains are NHWC
+    assert fmt(plan[0]["outputs"][0]) == 0                    # input Q stays NCHW
+
+
+def test_resnet50_branch_matches_oracle_dispatch(resnet_plan):
+    """Each QLinearConv's branch equals the oracle's dispatch restatement for
+    the same shapes, layouts and post-op flag."""
+    g, s, plan = resnet_plan
+    fmt = lambda n: s.tensor_info(n)[3]
+    for p in plan:
+        if p["op"] != "QLinearConv":
+            continue
+        a = g.node_by_name(p["name"]).attrs
+        ins = p["inputs"]
+        w = g.initializers[ins[3]]
+        _, _, xs, _ = s.tensor_info(ins[0])
+        cv = O.Conv(xs[0], xs[1], xs[2], xs[3], w.shape[0], w.shape[2], w.shape[3],
+                    group=a.get("group", 1), stride=tuple(a["strides"]), pads=tuple(a["pads"]),
+                    x_nhwc=fmt(ins[0]), y_nhwc=fmt(p["outputs"][0]), post_fn=p["post_fn"])
+        assert O.lib().orc_conv_dispatch(__import__("ctypes").byref(cv.p)) == \
+            O.BR[p["variant"]], p["name"]
+
+
+def test_unfusable_graph_fails_loudly():
+    """A float Conv without QDQ around it has no HIP implementation: prepare
+    fails with a message instead of silently running something else."""
+    g = G.Graph()
+    g.inputs["x"] = (np.float32, (1, 4, 8, 8))
+    w = g.init("w", np.zeros((4, 4, 3, 3), np.float32))
+    g.node("Conv", ["x", w], outputs="y", name="plain_conv", kernel_shape=[3, 3], pads=[1, 1, 1, 1])
+    g.outputs.append("y")
+    with pytest.raises(G.NnrError, match="without a HIP implementation"):
+        G.Session(g, device=False)
+
+
+def test_post_op_fusion_sets_qmin():
+    """QLinearConv followed by a Relu: fuse_post_ops marks post_fn and the
+    Relu step is skipped (fuse_post_ops.cpp:24-71)."""
+    g = G.Graph()
+    g.inputs["x"] = (np.uint8, (1, 8, 6, 6))
+    rng = np.random.default_rng(0)
+    ins = ["x", g.init("xs", np.array(0.02, np.float32)), g.init("xz", np.array(128, np.uint8)),
+           g.init("w", rng.integers(-5, 5, (8, 8, 3, 3)).astype(np.int8)),
+           g.init("ws", np.full(8, 0.01, np.float32)), g.init("wz", np.zeros(8, np.int8)),
+           g.init("ys", np.array(0.05, np.float32)), g.init("yz", np.array(10, np.uint8))]
+    g.node("QLinearConv", ins, outputs="c", name="qc", kernel_shape=[3, 3], pads=[1, 1, 1, 1])
+    g.node("Relu", ["c"], outputs="r", name="relu")
+    g.outputs.append("r")
+    s = G.Session(g, device=False)
+    plan = s.plan()
+    assert [p["op"] for p in plan] == ["QLinearConv"] and plan[0]["post_fn"] == 1
+    assert s.fusion_stat("post_ops") == 1
