@@ -85,6 +85,7 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None):
                 y = x.mean(axis=(1, 2), dtype=np.float64).astype(np.float32)[:, :, None, None]
             else:
                 y = x.mean(axis=(2, 3), dtype=np.float64).astype(np.float32)[:, :, None, None]
+            y = _nchw_to_phys(y, fmt_of(outs[0]))
         elif op in ("Flatten",):
             x = val(ins[0])
             ax = graph.node_by_name(nd["name"]).attrs.get("axis", 1)
