@@ -351,6 +351,7 @@ struct nnrh_qconv {
     // device buffers
     int8_t* wpack = nullptr;
     int32_t* colsum = nullptr;
+    int32_t* c0 = nullptr;
     int32_t* beta_col = nullptr;
     float* os = nullptr;
     float* cs = nullptr;
@@ -359,7 +360,7 @@ struct nnrh_qconv {
     uint8_t* xs = nullptr;
     int32_t* rowsum = nullptr;
     ~nnrh_qconv() {
-        dfree(wpack); dfree(colsum); dfree(beta_col); dfree(os); dfree(cs); dfree(bf);
+        dfree(wpack); dfree(colsum); dfree(c0); dfree(beta_col); dfree(os); dfree(cs); dfree(bf);
         dfree(bias); dfree(xs); dfree(rowsum);
     }
 };
@@ -387,8 +388,13 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
     const int lo = u8 ? 0 : -128, hi = u8 ? 255 : 127;
     const int qmin = d->post_fn ? std::max(lo, d->y_zp) : lo;     // QLinearConv.cpp:419
     const bool pcz = conv_per_channel_zp(d);
-    h->w_zp_scalar = d->w_zp_count > 0 ? d->w_zp_host[0] : 0;
     h->branch = conv_dispatch(d);
+    // The VNNI branches read w_zp through the activation type T
+    // (QLinearConv.cpp:386 `(T*)inputs[5]->data`); the float fallback packs
+    // weights with the weight type, int8 (QLinearConv_reshape.h:72-78).
+    const bool zp_as_u8 = u8 && h->branch != NNRH_BR_FLOAT;
+    auto zp_eff = [&](int8_t b) { return zp_as_u8 ? (int)(uint8_t)b : (int)b; };
+    h->w_zp_scalar = d->w_zp_count > 0 ? zp_eff(d->w_zp_host[0]) : 0;
     h->groups = G;
 
     // ---- requantize vectors (QLinearConv_reshape.h:288-321), same float ops
@@ -423,10 +429,9 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
 
     auto fail = [&](int code) { delete h; return code; };
 
-    if ((rc = upload(&h->cs, cs.data(), OC))) return fail(rc);
-    if ((rc = upload(&h->bf, bf.data(), OC))) return fail(rc);
-
     if (h->use_dw) {
+        if ((rc = upload(&h->cs, cs.data(), OC))) return fail(rc);
+        if ((rc = upload(&h->bf, bf.data(), OC))) return fail(rc);
         // repack_depthwise_weights: [kH*kW][C]
         std::vector<int8_t> wdw((size_t)d->kH * d->kW * OC);
         for (int c = 0; c < OC; ++c)
@@ -438,41 +443,53 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
         h->dw_tail = (br == NNRH_BR_IM2COL) ? TAIL_TILED : TAIL_NONE;
         h->dw_tile_h = tile_h;
     } else {
-        // ---- GEMM plan: groups on blockIdx.z, K order (kh, kw, c)
+        // ---- GEMM plan: groups on blockIdx.z, K order (kh, kw, c); every
+        // per-column array is laid out [G][Np] (zero padded)
         const bool first = br == NNRH_BR_FIRST;
         const int Cgp = first ? 4 : Cg;
-        const int K = d->kH * d->kW * Cgp;
+        const int kWp = first ? round_up(d->kW, 4) : d->kW;   // first layer: taps padded to 4
+        const int K = d->kH * kWp * Cgp;
         const int Kp = round_up(K, 64);
         const int Np = round_up(OCg, 64);
+        const int a_sub = u8 ? 128 : 0;
+        const int alpha = d->x_zp - a_sub;
+        const bool rqb = br == NNRH_BR_PACKED || br == NNRH_BR_NR16;
         std::vector<int8_t> wp((size_t)G * Np * Kp, 0);
-        std::vector<int32_t> colsum(OC, 0);
+        std::vector<int32_t> colsum((size_t)G * Np, 0), c0((size_t)G * Np, 0), biasp((size_t)G * Np, 0),
+            betac((size_t)G * Np, 0);
+        std::vector<float> osp((size_t)G * Np, 0.f), csp((size_t)G * Np, 0.f), bfp((size_t)G * Np, 0.f);
+        bool any_wzp = false;
         for (int g = 0; g < G; ++g)
             for (int n = 0; n < OCg; ++n) {
                 const int oc = g * OCg + n;
+                const size_t pi = (size_t)g * Np + n;
                 int8_t* row = wp.data() + ((size_t)g * Np + packed_row_of_col(n)) * Kp;
                 int32_t s = 0;
                 for (int c = 0; c < Cg; ++c)
                     for (int a = 0; a < d->kH; ++a)
                         for (int b = 0; b < d->kW; ++b) {
                             int8_t v = d->w_host[(((size_t)oc * Cg + c) * d->kH + a) * d->kW + b];
-                            row[(a * d->kW + b) * Cgp + c] = v;
+                            row[(a * kWp + b) * Cgp + c] = v;
                             s += v;
                         }
-                colsum[oc] = s;
+                colsum[pi] = s;
+                biasp[pi] = bias[oc];
+                // c0 = (RQ-B: bias) - alpha * colsum, int32 wrap-around
+                uint32_t t = (uint32_t)(rqb ? bias[oc] : 0) - (uint32_t)alpha * (uint32_t)s;
+                c0[pi] = (int32_t)t;
+                osp[pi] = os[oc]; csp[pi] = cs[oc]; bfp[pi] = bf[oc];
+                betac[pi] = pcz ? zp_eff(d->w_zp_host[oc]) : h->w_zp_scalar;
+                any_wzp |= betac[pi] != 0;
             }
         if ((rc = upload(&h->wpack, wp.data(), wp.size()))) return fail(rc);
         if ((rc = upload(&h->colsum, colsum.data(), colsum.size()))) return fail(rc);
-        if ((rc = upload(&h->os, os.data(), OC))) return fail(rc);
-        if ((rc = upload(&h->bias, bias.data(), OC))) return fail(rc);
-        // zero-point row term: any nonzero w_zp
-        std::vector<int32_t> betac(OC);
-        bool any_wzp = false;
-        for (int oc = 0; oc < OC; ++oc) {
-            betac[oc] = pcz ? d->w_zp_host[oc] : h->w_zp_scalar;
-            any_wzp |= betac[oc] != 0;
-        }
+        if ((rc = upload(&h->c0, c0.data(), c0.size()))) return fail(rc);
+        if ((rc = upload(&h->os, osp.data(), osp.size()))) return fail(rc);
+        if ((rc = upload(&h->cs, csp.data(), csp.size()))) return fail(rc);
+        if ((rc = upload(&h->bf, bfp.data(), bfp.size()))) return fail(rc);
+        if ((rc = upload(&h->bias, biasp.data(), biasp.size()))) return fail(rc);
         h->need_rowsum = any_wzp;
-        if (any_wzp && (rc = upload(&h->beta_col, betac.data(), OC))) return fail(rc);
+        if (any_wzp && (rc = upload(&h->beta_col, betac.data(), betac.size()))) return fail(rc);
 
         if (first) { h->transform = 2; h->Cx = 4; }
         else { h->transform = d->x_nhwc ? 0 : 1; h->Cx = d->C; }
@@ -487,18 +504,20 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
         g.oH = d->oH; g.oW = d->oW; g.kH = d->kH; g.kW = d->kW;
         g.sH = d->sH; g.sW = d->sW; g.dH = d->dH; g.dW = d->dW;
         g.pad_t = d->pad_t; g.pad_l = d->pad_l;
+        g.kWp = first ? kWp : 0;
         g.pad_byte = d->x_zp & 0xff;
         g.a_bstride = first ? 0 : Cg;   // group channel offset
         g.b = h->wpack;
         g.b_bstride = (long long)Np * Kp;
         g.Np = Np;
         g.colsum = h->colsum;
-        g.a_sub = u8 ? 128 : 0;
-        g.alpha = d->x_zp - g.a_sub;
+        g.c0 = h->c0;
+        g.a_sub = a_sub;
+        g.alpha = alpha;
         g.rowsum_bstride = (long long)g.M;
         g.beta_col = h->beta_col;
         g.beta = 0;
-        g.param_bstride = OCg;
+        g.param_bstride = Np;
         g.os = h->os; g.bias = h->bias; g.cs = h->cs; g.bf = h->bf;
         g.inv_y = inv_y;
         g.y_zp = d->y_zp;
@@ -650,11 +669,12 @@ struct nnrh_qmatmul {
     GemmArgs g{};
     int8_t* wpack = nullptr;
     int32_t* colsum = nullptr;
+    int32_t* c0 = nullptr;
     int32_t* rowsum = nullptr;
     int rowsum_cap = 0;     // batches the rowsum buffer holds
     int a_zp = 0, b_beta = 0;
     float b_scale = 0.f, y_scale = 0.f;
-    ~nnrh_qmatmul() { dfree(wpack); dfree(colsum); dfree(rowsum); }
+    ~nnrh_qmatmul() { dfree(wpack); dfree(colsum); dfree(c0); dfree(rowsum); }
 };
 
 extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc* d) {
@@ -676,7 +696,7 @@ extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc*
     const int Kp = round_up(k, 64), Np = round_up(n, 64);
     const bool bu8 = d->b_dtype == NNRH_U8;
     std::vector<int8_t> wp((size_t)Np * Kp, 0);
-    std::vector<int32_t> colsum(n, 0);
+    std::vector<int32_t> colsum(Np, 0);
     const uint8_t* braw = (const uint8_t*)d->b_host;
     for (int j = 0; j < n; ++j) {
         int8_t* row = wp.data() + (size_t)packed_row_of_col(j) * Kp;
@@ -689,10 +709,14 @@ extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc*
         colsum[j] = s;
     }
     int rc;
-    if ((rc = upload(&h->wpack, wp.data(), wp.size()))) return fail(rc);
-    if ((rc = upload(&h->colsum, colsum.data(), colsum.size()))) return fail(rc);
     const bool au8 = d->a_dtype == NNRH_U8;
     h->a_zp = ld_zp(d->a_zp_host, d->a_dtype);
+    std::vector<int32_t> c0(Np, 0);
+    for (int j = 0; j < n; ++j)
+        c0[j] = (int32_t)(0u - (uint32_t)(h->a_zp - (au8 ? 128 : 0)) * (uint32_t)colsum[j]);
+    if ((rc = upload(&h->wpack, wp.data(), wp.size()))) return fail(rc);
+    if ((rc = upload(&h->colsum, colsum.data(), colsum.size()))) return fail(rc);
+    if ((rc = upload(&h->c0, c0.data(), c0.size()))) return fail(rc);
     const int b_zp = ld_zp(d->b_zp_host, d->b_dtype);   // b_zp[0] only (QLinearMatMul.cpp:119)
     h->b_beta = b_zp - (bu8 ? 128 : 0);
     // combined scale (QLinearMatMul.cpp:124-135)
@@ -718,6 +742,7 @@ extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc*
     g.lda = k;
     g.b = h->wpack; g.b_bstride = 0; g.Np = Np;
     g.colsum = h->colsum;
+    g.c0 = h->c0;
     g.a_sub = au8 ? 128 : 0;
     g.alpha = h->a_zp - g.a_sub;
     g.beta = h->b_beta;

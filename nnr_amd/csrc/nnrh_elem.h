@@ -20,6 +20,7 @@ struct QAddArgs {
     float cval;          // scalar-broadcast constant
     int a_zp, b_zp, y_zp;
     int lo, hi;
+    int tail_all;        // every element takes the scalar tail expression
 };
 
 hipError_t launch_quantize(const float* x, long long n, float scale, int zp, int dt, void* y,

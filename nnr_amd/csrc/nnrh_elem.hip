@@ -184,7 +184,7 @@ __global__ __launch_bounds__(256) void qadd_kernel(QAddArgs p) {
     for (; i < p.n; i += stride) {
         int q;
         if (p.kind == 0) {
-            const long long body = p.n - p.n % 16;
+            const long long body = p.tail_all ? 0 : p.n - p.n % 16;
             int a = ld_q(p.a, p.dt, i), b = ld_q(p.b, p.dt, i);
             if (i < body) {
                 // v = fma(fa, sa, fma(fb, sb, fixed)); cvtps2dq; saturating pack
@@ -246,8 +246,54 @@ __global__ __launch_bounds__(256) void qadd_kernel(QAddArgs p) {
     }
 }
 
+// Same-shape fast path: 16 elements per thread with 16-byte loads/stores.
+// Chunks never straddle the body/tail boundary (body = n - n%16).
+__global__ __launch_bounds__(256) void qadd_same16_kernel(QAddArgs p) {
+    const long long nchunk = p.n >> 4;
+    for (long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x; c < nchunk;
+         c += (long long)gridDim.x * blockDim.x) {
+        uint4 av = ((const uint4*)p.a)[c];
+        uint4 bv = ((const uint4*)p.b)[c];
+        uint32_t aw[4] = {av.x, av.y, av.z, av.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w}, yw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                int a = (int)((aw[q] >> (8 * r)) & 0xff), b = (int)((bw[q] >> (8 * r)) & 0xff);
+                if (p.dt) { a = (int)(int8_t)a; b = (int)(int8_t)b; }
+                float v = __builtin_fmaf((float)b, p.sb, p.fixed);
+                v = __builtin_fmaf((float)a, p.sa, v);
+                int qv = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
+                w |= (uint32_t)(qv & 0xff) << (8 * r);
+            }
+            yw[q] = w;
+        }
+        ((uint4*)p.y)[c] = make_uint4(yw[0], yw[1], yw[2], yw[3]);
+    }
+}
+
 hipError_t launch_qadd(const QAddArgs& p, hipStream_t s) {
     if (p.n <= 0) return hipSuccess;
+    const bool vec = p.kind == 0 && (((uintptr_t)p.a | (uintptr_t)p.b | (uintptr_t)p.y) & 15) == 0;
+    if (vec && p.n >= 16) {
+        long long chunks = p.n >> 4;
+        long long blocks = (chunks + 255) / 256;
+        if (blocks > 8192) blocks = 8192;
+        hipLaunchKernelGGL(qadd_same16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess || p.n % 16 == 0) return e;
+        // the scalar tail: reuse the generic kernel on the last n%16 elements
+        QAddArgs t = p;
+        const long long off = p.n - p.n % 16;
+        t.a = (const uint8_t*)p.a + off;
+        t.b = (const uint8_t*)p.b + off;
+        t.y = (uint8_t*)p.y + off;
+        t.n = p.n % 16;
+        t.tail_all = 1;
+        hipLaunchKernelGGL(qadd_kernel, dim3(1), dim3(64), 0, s, t);
+        return hipGetLastError();
+    }
     long long blocks = (p.n + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(qadd_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
@@ -294,9 +340,52 @@ __global__ __launch_bounds__(256) void maxpool_u8_kernel(const uint8_t* __restri
         for (int i = 0; i < 4 && c0 + i < C; ++i) yp[i] = (uint8_t)m[i];
 }
 
+__device__ __forceinline__ uint32_t bytemax4(uint32_t a, uint32_t b) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t x = (a >> (8 * i)) & 0xff, y = (b >> (8 * i)) & 0xff;
+        r |= (x > y ? x : y) << (8 * i);
+    }
+    return r;
+}
+
+__global__ __launch_bounds__(256) void maxpool_u8_16_kernel(const uint8_t* __restrict x,
+                                                            uint8_t* __restrict y, int N, int C,
+                                                            int iH, int iW, int oH, int oW, int kH,
+                                                            int kW, int sH, int sW, int pH, int pW) {
+    const int C16 = C >> 4;
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)N * oH * oW * C16;
+    if (idx >= total) return;
+    const int cg = (int)(idx % C16);
+    const long long pix = idx / C16;
+    const int ow = (int)(pix % oW), oh = (int)((pix / oW) % oH), n = (int)(pix / ((long long)oW * oH));
+    const int ih0 = oh * sH - pH, iw0 = ow * sW - pW;
+    const int kh0 = ih0 < 0 ? -ih0 : 0, kh1 = kH < iH - ih0 ? kH : iH - ih0;
+    const int kw0 = iw0 < 0 ? -iw0 : 0, kw1 = kW < iW - iw0 ? kW : iW - iw0;
+    uint32_t m[4] = {0, 0, 0, 0};
+    for (int a = kh0; a < kh1; ++a)
+        for (int b = kw0; b < kw1; ++b) {
+            uint4 v = *(const uint4*)(x + (((long long)n * iH + ih0 + a) * iW + iw0 + b) * C + cg * 16);
+            m[0] = bytemax4(m[0], v.x);
+            m[1] = bytemax4(m[1], v.y);
+            m[2] = bytemax4(m[2], v.z);
+            m[3] = bytemax4(m[3], v.w);
+        }
+    *(uint4*)(y + pix * C + cg * 16) = make_uint4(m[0], m[1], m[2], m[3]);
+}
+
 hipError_t launch_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH, int iW,
                                   int oH, int oW, int kH, int kW, int sH, int sW, int pH, int pW,
                                   hipStream_t s) {
+    if ((C & 15) == 0 && (((uintptr_t)x | (uintptr_t)y) & 15) == 0) {
+        long long total = (long long)N * oH * oW * (C / 16);
+        if (total <= 0) return hipSuccess;
+        hipLaunchKernelGGL(maxpool_u8_16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                           s, x, y, N, C, iH, iW, oH, oW, kH, kW, sH, sW, pH, pW);
+        return hipGetLastError();
+    }
     long long total = (long long)N * oH * oW * ((C + 3) / 4);
     if (total <= 0) return hipSuccess;
     hipLaunchKernelGGL(maxpool_u8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x,

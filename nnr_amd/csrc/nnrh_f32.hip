@@ -25,58 +25,76 @@ __global__ __launch_bounds__(256) void gap_f32_kernel(const float* __restrict x,
     if (lane == 0) y[row] = s / (float)HW;
 }
 
+// NHWC: one thread per (n, c); consecutive threads read consecutive channels
+__global__ __launch_bounds__(256) void gap_f32_nhwc_kernel(const float* __restrict x,
+                                                           float* __restrict y, int N, int C,
+                                                           int HW) {
+    long long row = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (row >= (long long)N * C) return;
+    const int n = (int)(row / C), c = (int)(row % C);
+    const float* p = x + (long long)n * HW * C + c;
+    float s = 0.0f;
+    for (int i = 0; i < HW; ++i) s += p[(long long)i * C];
+    y[row] = s / (float)HW;
+}
+
 hipError_t launch_gap_f32(const float* x, float* y, int N, int C, int HW, int x_nhwc,
                           hipStream_t s) {
     long long rows = (long long)N * C;
     if (rows <= 0) return hipSuccess;
+    if (x_nhwc) {
+        hipLaunchKernelGGL(gap_f32_nhwc_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s,
+                           x, y, N, C, HW);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(gap_f32_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, y, N,
                        C, HW, x_nhwc);
     return hipGetLastError();
 }
 
 // Y[M][N] = alpha * op(A)[M][K] * op(B)[K][N] + beta * Cb (broadcast)
-// 64x64 tile, 16x16 threads, 4x4 outputs per thread, K step 16 through LDS.
+// 32x32 tile, 16x16 threads, 2x2 outputs per thread, K step 32 through LDS.
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict A,
                                                        const float* __restrict B,
                                                        const float* __restrict Cb,
                                                        float* __restrict Y, int M, int N, int K,
                                                        int transA, int transB, float alpha,
                                                        float beta, int c_mode) {
-    __shared__ float As[16][64 + 1];
-    __shared__ float Bs[16][64 + 1];
+    __shared__ float As[32][32 + 1];   // [k][m]
+    __shared__ float Bs[32][32 + 1];   // [k][n]
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-    float acc[4][4] = {};
-    for (int k0 = 0; k0 < K; k0 += 16) {
-        for (int i = threadIdx.x; i < 16 * 64; i += 256) {
-            int kk = i / 64, mm = i % 64;
-            int m = m0 + mm, k = k0 + kk;
-            As[kk][mm] = (m < M && k < K) ? (transA ? A[(long long)k * M + m] : A[(long long)m * K + k]) : 0.f;
-            int nn = mm, n = n0 + nn;
-            Bs[kk][nn] = (n < N && k < K) ? (transB ? B[(long long)n * K + k] : B[(long long)k * N + n]) : 0.f;
+    const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+    float acc[2][2] = {};
+    for (int k0 = 0; k0 < K; k0 += 32) {
+        for (int i = threadIdx.x; i < 32 * 32; i += 256) {
+            int r = i / 32, c = i % 32;
+            // A: walk the contiguous dimension with c
+            int am = m0 + (transA ? c : r), ak = k0 + (transA ? r : c);
+            float av = (am < M && ak < K) ? (transA ? A[(long long)ak * M + am] : A[(long long)am * K + ak]) : 0.f;
+            As[ak - k0][am - m0] = av;
+            int bn = n0 + (transB ? r : c), bk = k0 + (transB ? c : r);
+            float bv = (bn < N && bk < K) ? (transB ? B[(long long)bn * K + bk] : B[(long long)bk * N + bn]) : 0.f;
+            Bs[bk - k0][bn - n0] = bv;
         }
         __syncthreads();
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-            float a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+        for (int kk = 0; kk < 32; ++kk) {
+            float a0 = As[kk][ty * 2], a1 = As[kk][ty * 2 + 1];
+            float b0 = Bs[kk][tx * 2], b1 = Bs[kk][tx * 2 + 1];
+            acc[0][0] = __builtin_fmaf(a0, b0, acc[0][0]);
+            acc[0][1] = __builtin_fmaf(a0, b1, acc[0][1]);
+            acc[1][0] = __builtin_fmaf(a1, b0, acc[1][0]);
+            acc[1][1] = __builtin_fmaf(a1, b1, acc[1][1]);
         }
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int m = m0 + ty * 4 + i;
+    for (int i = 0; i < 2; ++i) {
+        int m = m0 + ty * 2 + i;
         if (m >= M) continue;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            int n = n0 + tx * 4 + j;
+        for (int j = 0; j < 2; ++j) {
+            int n = n0 + tx * 2 + j;
             if (n >= N) continue;
             float v = alpha * acc[i][j];
             if (c_mode == 1) v = v + beta * Cb[0];
@@ -92,7 +110,7 @@ hipError_t launch_gemm_f32(const float* A, const float* B, const float* C, float
                            int K, int transA, int transB, float alpha, float beta, int c_mode,
                            hipStream_t s) {
     if (M <= 0 || N <= 0) return hipSuccess;
-    dim3 grid((N + 63) / 64, (M + 63) / 64);
+    dim3 grid((N + 31) / 32, (M + 31) / 32);
     hipLaunchKernelGGL(gemm_f32_kernel, grid, dim3(256), 0, s, A, B, C, Y, M, N, K, transA, transB,
                        alpha, beta, c_mode);
     return hipGetLastError();

@@ -32,6 +32,7 @@ enum TailMode : int {
 enum AMode : int {
     A_DENSE = 0,   // A[m*lda + k]
     A_CONV = 1,    // implicit im2col over an NHWC tensor, K order (kh,kw,c)
+    A_CONV4 = 2,   // first layer: NHWC with 4 channels, K order (kh, kw < kWp, c)
 };
 
 struct GemmArgs {
@@ -44,6 +45,7 @@ struct GemmArgs {
     // conv geometry (A_CONV)
     int H, W, C, oH, oW, kH, kW, sH, sW, dH, dW, pad_t, pad_l;
     int Cs;               // channel stride of the NHWC tensor (>= C; groups)
+    int kWp;              // > 0: first-layer layout (kW padded to a multiple of 4)
     int pad_byte;         // raw byte for out-of-image taps (x_zp)
     // ---- B (weights), packed [Np][Kp] int8 with the 64-column permutation ----
     const int8_t* b;
@@ -53,6 +55,8 @@ struct GemmArgs {
     // alpha = x_zp - a_sub (a_sub = 128 for uint8 activations, else 0); when
     // alpha_zp_dev is set the activation zero point is read from device memory.
     const int32_t* colsum;
+    const int32_t* c0;    // per-column constant: bias(RQ-B) - alpha*colsum; NULL:
+                          // computed from colsum/bias/alpha in the epilogue
     int alpha;
     const void* alpha_zp_dev;  // nullable: uint8 (a_xor) or int8 zero point
     int a_sub;
@@ -69,7 +73,8 @@ struct GemmArgs {
     const float* cs;        // RQ-A / RQ-C
     const float* bf;        // RQ-A / RQ-C
     long long param_bstride;  // per-batch (z) offset of every per-column array
-                              // (colsum, beta_col, os, bias, cs, bf)
+                              // (colsum, c0, beta_col, os, bias, cs, bf); all
+                              // per-column arrays are padded to Np entries
     float inv_y;
     float cm;               // RQ-D combined scale fl(fl(a_s*b_s)/y_s)
     const float* cm_a_scale_dev;  // RQ-D: nullable device a_scale; then

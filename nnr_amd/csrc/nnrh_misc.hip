@@ -41,9 +41,30 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint8_t* __rest
     }
 }
 
+// small channel counts (first-layer input, C <= 4 padded to 4): one thread
+// per pixel, channel planes read coalesced, one 32-bit store per pixel
+__global__ __launch_bounds__(256) void nchw_to_nhwc4_kernel(const uint8_t* __restrict x,
+                                                            uint32_t* __restrict y, int C, long long HW,
+                                                            long long total, uint8_t fill) {
+    long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    long long n = i / HW, p = i - n * HW;
+    const uint8_t* xn = x + n * C * HW + p;
+    uint32_t w = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w |= (uint32_t)(c < C ? xn[(long long)c * HW] : fill) << (8 * c);
+    y[i] = w;
+}
+
 hipError_t launch_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C, int HW,
                                   int Cpad, uint8_t fill, hipStream_t s) {
     if (N <= 0 || HW <= 0 || Cpad <= 0) return hipSuccess;
+    if (Cpad == 4 && C <= 4 && ((uintptr_t)y & 3) == 0) {
+        long long total = (long long)N * HW;
+        hipLaunchKernelGGL(nchw_to_nhwc4_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                           x, (uint32_t*)y, C, (long long)HW, total, fill);
+        return hipGetLastError();
+    }
     dim3 grid((HW + 63) / 64, N);
     hipLaunchKernelGGL(nchw_to_nhwc_kernel, grid, dim3(256), 0, s, x, y, C, HW, Cpad, fill);
     return hipGetLastError();

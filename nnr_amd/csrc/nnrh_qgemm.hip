@@ -102,55 +102,69 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(GemmArgs g) {
     const int wave = tid >> 6;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
-    // ---- tile id, XCD-aware: consecutive logical tiles share one XCD's L2
+    // ---- persistent tiles, XCD-aware: blocks on XCD x (blockIdx % 8 == x)
+    // walk the x-th contiguous eighth of the tile list (m-major), so the N
+    // tiles of one A row block meet in the same L2.
     const int nbn = (g.N + BN - 1) / BN;
     const int nbm = (g.M + BM - 1) / BM;
     const int total = nbm * nbn;
-    const int bid = blockIdx.x;
-    const int per_xcd = total >> 3;
-    int t = bid;
-    if (bid < (per_xcd << 3)) t = (bid & 7) * per_xcd + (bid >> 3);
-    const int m0 = (t / nbn) * BM;
-    const int n0 = (t % nbn) * BN;
+    const int G = gridDim.x;
     const int z = blockIdx.z;
+    int t_cur, t_end, t_step;
+    if (G >= 8 && (G & 7) == 0) {
+        const int per = G >> 3, xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
+        const int chunk = (total + 7) >> 3;
+        t_cur = xcd * chunk + local;
+        t_end = min(total, (xcd + 1) * chunk);
+        t_step = per;
+    } else {
+        t_cur = blockIdx.x;
+        t_end = total;
+        t_step = G;
+    }
+    if (t_cur >= t_end) return;
 
     const uint8_t* abase = g.a + (long long)z * g.a_bstride;
     const int8_t* bbase = g.b + (long long)z * g.b_bstride;
     const uint32_t xmask = (uint32_t)g.a_xor * 0x01010101u;
     const int c16 = tid & 3;          // this thread's 16-byte chunk in a row
+    const int sp_out = g.oH * g.oW;
 
-    // ---- per-thread A rows
+    // ---- per-thread A rows of the tile being loaded
     int a_row[A_CH];
     bool a_ok[A_CH];
     long long a_base[A_CH];   // dense: row offset; conv: image offset
     int a_ih0[A_CH], a_iw0[A_CH];
+    int ld_m0 = 0, ld_n0 = 0;
+    int kc_ic = 0, kc_kh = 0, kc_kw = 0;   // conv K decode of k = k0 + c16*16 (VEC 16)
+    auto setup_tile = [&](int t) {
+        ld_m0 = (t / nbn) * BM;
+        ld_n0 = (t % nbn) * BN;
 #pragma unroll
-    for (int j = 0; j < A_CH; ++j) {
-        a_row[j] = (tid >> 2) + 64 * j;
-        int m = m0 + a_row[j];
-        a_ok[j] = m < g.M;
-        if constexpr (AMODE == A_DENSE) {
-            a_base[j] = (long long)m * g.lda;
-            a_ih0[j] = 0; a_iw0[j] = 0;
-        } else {
-            int sp = g.oH * g.oW;
-            int mm = a_ok[j] ? m : 0;
-            int img = mm / sp, s = mm - img * sp;
-            int oh = s / g.oW, ow = s - oh * g.oW;
-            a_base[j] = (long long)img * g.H * g.W * g.Cs;
-            a_ih0[j] = oh * g.sH - g.pad_t;
-            a_iw0[j] = ow * g.sW - g.pad_l;
+        for (int j = 0; j < A_CH; ++j) {
+            a_row[j] = (tid >> 2) + 64 * j;
+            int m = ld_m0 + a_row[j];
+            a_ok[j] = m < g.M;
+            if constexpr (AMODE == A_DENSE) {
+                a_base[j] = (long long)m * g.lda;
+                a_ih0[j] = 0; a_iw0[j] = 0;
+            } else {
+                int mm = a_ok[j] ? m : 0;
+                int img = mm / sp_out, s = mm - img * sp_out;
+                int oh = s / g.oW, ow = s - oh * g.oW;
+                a_base[j] = (long long)img * g.H * g.W * g.Cs;
+                a_ih0[j] = oh * g.sH - g.pad_t;
+                a_iw0[j] = ow * g.sW - g.pad_l;
+            }
         }
-    }
-    // conv K decode for k = k0 + c16*16 (VEC == 16 tracks it incrementally)
-    int kc_ic = 0, kc_kh = 0, kc_kw = 0;
-    if constexpr (AMODE == A_CONV && VEC == 16) {
-        int k = c16 * 16;
-        int kp = k / g.C;
-        kc_ic = k - kp * g.C;
-        kc_kh = kp / g.kW;
-        kc_kw = kp - kc_kh * g.kW;
-    }
+        if constexpr (AMODE == A_CONV && VEC == 16) {
+            int k = c16 * 16;
+            int kp = k / g.C;
+            kc_ic = k - kp * g.C;
+            kc_kh = kp / g.kW;
+            kc_kw = kp - kc_kh * g.kW;
+        }
+    };
     const uint32_t padw = (uint32_t)(g.pad_byte & 0xff) * 0x01010101u;
 
     v4i ra[A_CH], rb[B_CH];
@@ -161,7 +175,28 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(GemmArgs g) {
         for (int j = 0; j < A_CH; ++j) {
             uint32_t w[4] = {0u, 0u, 0u, 0u};
             const int kk = k0 + c16 * 16;
-            if constexpr (VEC == 1) {
+            if constexpr (AMODE == A_CONV4) {
+                // first-layer layout: K = (kh, kw < kWp, c < 4); a 16-byte chunk
+                // holds 4 consecutive taps of one input row (4 channels each)
+                const int cpr = g.kWp >> 2;
+                const int q = kk >> 4;
+                const int kh = q / cpr;
+                const int kw0 = (q - kh * cpr) << 2;
+                if (a_ok[j] && kh < g.kH) {
+                    const int ih = a_ih0[j] + kh;
+                    if ((unsigned)ih < (unsigned)g.H) {
+                        const uint8_t* rowp = abase + a_base[j] + (long long)ih * g.W * 4;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            const int iw = a_iw0[j] + kw0 + t;
+                            w[t] = ((unsigned)iw < (unsigned)g.W) ? *(const uint32_t*)(rowp + (long long)iw * 4)
+                                                                  : padw;
+                        }
+                    } else {
+                        w[0] = w[1] = w[2] = w[3] = padw;
+                    }
+                }
+            } else if constexpr (VEC == 1) {
                 load_bytes<AMODE>(g, abase, a_base[j], a_ih0[j], a_iw0[j], a_ok[j], kk, w);
             } else if constexpr (AMODE == A_DENSE) {
                 if (a_ok[j]) {
@@ -222,7 +257,7 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(GemmArgs g) {
         // ---- B (packed [Np][Kp], always in bounds below Np)
 #pragma unroll
         for (int j = 0; j < B_CH; ++j) {
-            int n = n0 + (tid >> 2) + 64 * j;
+            int n = ld_n0 + (tid >> 2) + 64 * j;
             if (n < g.Np) {
                 rb[j] = *(const v4i*)(bbase + (long long)n * g.Kp + k0 + c16 * 16);
             } else {
@@ -249,200 +284,260 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(GemmArgs g) {
     };
 
     v4i acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-
     const int nk = g.Kp >> 6;
-    load_tiles(0);
-    advance_k();
-    store_tiles(0);
-    __syncthreads();
-
     const int frow = lane & 15;
     const int fchunk = lane >> 4;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) {
-            load_tiles((kt + 1) << 6);
-            advance_k();
+    auto epilogue = [&](const int m0, const int n0) {
+        // ---- epilogue: lane owns columns nb..nb+15 of rows m0 + wm*64 + 16*tm + frow.
+        // Per-column constants are padded to Np, so the vector loads need no
+        // guard. c0[n] folds the zero-point column term (and, for RQ-B, the int32
+        // bias): v = acc' + c0[n] - beta*rowsum[m] is the reference's value.
+        const int nb = n0 + wn * 64 + 16 * fchunk;
+        if (nb >= g.N) return;
+        const long long po = (long long)z * g.param_bstride;
+        int alpha = g.alpha;
+        if (g.alpha_zp_dev) {
+            int zp = g.a_xor ? (int)*(const uint8_t*)g.alpha_zp_dev
+                             : (int)*(const int8_t*)g.alpha_zp_dev;
+            alpha = zp - g.a_sub;
         }
-        v4i xf[4], wf[4];
+        float cm = g.cm;
+        if (g.epi == EPI_RQD && g.cm_a_scale_dev) {
+            float t1 = *g.cm_a_scale_dev * g.cm_b;
+            cm = t1 / g.cm_y;
+        }
+        const int sp = g.oH * g.oW;
+        const bool full16 = (nb + 16 <= g.N);
+        // per-row terms
+        int rs[4];
+        bool tail[4];
+        bool any_tail = false;
+    #pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+            const int m = m0 + wm * 64 + tm * 16 + frow;
+            rs[tm] = (g.rowsum && m < g.M) ? g.rowsum[(long long)z * g.rowsum_bstride + m] : 0;
+            bool tl = false;
+            if (g.tail != TAIL_NONE && m < g.M) {
+                int s = m % sp;
+                if (g.tail == TAIL_SPATIAL) {
+                    tl = s >= sp - sp % 16;
+                } else if (g.tail == TAIL_OW) {
+                    int ow = s % g.oW;
+                    tl = ow >= g.oW - g.oW % 16;
+                } else {
+                    int oh = s / g.oW;
+                    int oh0 = (oh / g.tile_h) * g.tile_h;
+                    int th = g.oH - oh0 < g.tile_h ? g.oH - oh0 : g.tile_h;
+                    int tsp = th * g.oW;
+                    int ts = s - oh0 * g.oW;
+                    tl = ts >= tsp - tsp % 16;
+                }
+            }
+            tail[tm] = tl;
+            any_tail |= tl;
+        }
+        const bool use_rows = g.rowsum != nullptr;
+        // slow (reference-expression) path: scalar tails and RQ-B' columns
+        const bool slow = any_tail || (g.epi == EPI_RQB && nb + 16 > g.bprime_from);
+        uint32_t packed[4][4];
+    #pragma unroll
+        for (int tn = 0; tn < 4; ++tn) {
+            const int n4 = nb + 4 * tn;
+            int cc[4];
+            if (g.c0 && !g.alpha_zp_dev) {
+                int4 c = *(const int4*)(g.c0 + po + n4);
+                cc[0] = c.x; cc[1] = c.y; cc[2] = c.z; cc[3] = c.w;
+            } else {
+    #pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    int32_t cs_ = g.colsum ? g.colsum[po + n4 + r] : 0;
+                    int32_t b_ = (g.epi == EPI_RQB && g.bias) ? g.bias[po + n4 + r] : 0;
+                    cc[r] = wrap_add(b_, -wrap_mul(alpha, cs_));
+                }
+            }
+            int bc[4] = {g.beta, g.beta, g.beta, g.beta};
+            if (use_rows && g.beta_col) {
+                int4 b4 = *(const int4*)(g.beta_col + po + n4);
+                bc[0] = b4.x; bc[1] = b4.y; bc[2] = b4.z; bc[3] = b4.w;
+            }
+            float p0[4] = {0.f, 0.f, 0.f, 0.f}, p1[4] = {0.f, 0.f, 0.f, 0.f};
+            if (g.epi == EPI_RQB) {
+                float4 s4 = *(const float4*)(g.os + po + n4);
+                p0[0] = s4.x; p0[1] = s4.y; p0[2] = s4.z; p0[3] = s4.w;
+            } else if (g.epi == EPI_RQA || g.epi == EPI_RQC) {
+                float4 s4 = *(const float4*)(g.cs + po + n4);
+                float4 b4 = *(const float4*)(g.bf + po + n4);
+                p0[0] = s4.x; p0[1] = s4.y; p0[2] = s4.z; p0[3] = s4.w;
+                p1[0] = b4.x; p1[1] = b4.y; p1[2] = b4.z; p1[3] = b4.w;
+            }
+    #pragma unroll
+            for (int tm = 0; tm < 4; ++tm) {
+                int32_t v[4] = {acc[tm][tn].x, acc[tm][tn].y, acc[tm][tn].z, acc[tm][tn].w};
+    #pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    v[r] = wrap_add(v[r], cc[r]);
+                    if (use_rows) v[r] = wrap_add(v[r], -wrap_mul(bc[r], rs[tm]));
+                }
+                if (g.epi == EPI_I32) {
+                    packed[tm][tn] = 0;
+                    acc[tm][tn] = v4i{v[0], v[1], v[2], v[3]};
+                    continue;
+                }
+                uint32_t w = 0;
+                if (!slow) {
+    #pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        uint32_t b;
+                        if (g.epi == EPI_RQB) b = rqb_fast(v[r], p0[r], g.y_zp, g.lo, g.hi);
+                        else if (g.epi == EPI_RQA) b = rqa_fast(v[r], p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi);
+                        else if (g.epi == EPI_RQC) b = rqc_fast(v[r], p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi);
+                        else b = rqd_fast(v[r], cm, g.y_zp, g.lo, g.hi);
+                        w |= (b & 0xffu) << (8 * r);
+                    }
+                } else {
+    #pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        int q;
+                        if (g.epi == EPI_RQB) {
+                            q = (n4 + r >= g.bprime_from) ? rq_b_roundf(v[r], p0[r], g.y_zp, g.lo, g.hi)
+                                                          : rq_b(v[r], p0[r], g.y_zp, g.lo, g.hi);
+                        } else if (g.epi == EPI_RQA) {
+                            q = tail[tm] ? rq_a_tail(v[r], p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi)
+                                         : rq_a(v[r], p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi);
+                        } else if (g.epi == EPI_RQC) {
+                            q = tail[tm] ? rq_a_tail(v[r], p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi)
+                                         : rq_c(v[r], p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi);
+                        } else {
+                            q = rq_d(v[r], cm, g.y_zp, g.lo, g.hi);
+                        }
+                        w |= (uint32_t)(q & 0xff) << (8 * r);
+                    }
+                }
+                packed[tm][tn] = w;
+            }
+        }
+    #pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+            const int m = m0 + wm * 64 + tm * 16 + frow;
+            if (m >= g.M) continue;
+            if (g.epi == EPI_I32) {
+                int32_t* yrow = (int32_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
+                if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
+    #pragma unroll
+                    for (int tn = 0; tn < 4; ++tn) *(v4i*)(yrow + 4 * tn) = acc[tm][tn];
+                } else {
+    #pragma unroll
+                    for (int tn = 0; tn < 4; ++tn) {
+                        int32_t vv[4] = {acc[tm][tn].x, acc[tm][tn].y, acc[tm][tn].z, acc[tm][tn].w};
+    #pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (nb + 4 * tn + r < g.N) yrow[4 * tn + r] = vv[r];
+                    }
+                }
+                continue;
+            }
+            if (g.y_nchw) {
+                uint8_t* yb = (uint8_t*)g.y + (long long)z * g.y_bstride;
+                int img = m / sp, s = m - img * sp;
+    #pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (nb + i < g.N)
+                        yb[((long long)img * g.ldy + nb + i) * sp + s] = (uint8_t)(packed[tm][i >> 2] >> (8 * (i & 3)));
+            } else {
+                uint8_t* yrow = (uint8_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
+                if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
+                    *(v4i*)yrow = v4i{(int)packed[tm][0], (int)packed[tm][1], (int)packed[tm][2], (int)packed[tm][3]};
+                } else {
+    #pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (nb + i < g.N) yrow[i] = (uint8_t)(packed[tm][i >> 2] >> (8 * (i & 3)));
+                }
+            }
+        }
+    };
+
+    setup_tile(t_cur);
+    load_tiles(0);
+    advance_k();
+    for (;;) {
+        const int m0 = ld_m0, n0 = ld_n0;
+        const int t_next = t_cur + t_step;
+        const bool has_next = t_next < t_end;
 #pragma unroll
-        for (int tm = 0; tm < 4; ++tm)
-            xf[tm] = *(const v4i*)(&lds_a[cur][lds_off(wm * 64 + tm * 16 + frow, fchunk)]);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int tn = 0; tn < 4; ++tn)
-            wf[tn] = *(const v4i*)(&lds_b[cur][lds_off(wn * 64 + tn * 16 + frow, fchunk)]);
+            for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+        store_tiles(0);
+        __syncthreads();
+        for (int kt = 0; kt < nk; ++kt) {
+            const int cur = kt & 1;
+            if (kt + 1 < nk) {
+                load_tiles((kt + 1) << 6);
+                advance_k();
+            } else if (has_next) {
+                // first K step of the next tile: in flight during the epilogue
+                setup_tile(t_next);
+                load_tiles(0);
+                advance_k();
+            }
+            v4i xf[4], wf[4];
 #pragma unroll
-        for (int tm = 0; tm < 4; ++tm)
+            for (int tm = 0; tm < 4; ++tm)
+                xf[tm] = *(const v4i*)(&lds_a[cur][lds_off(wm * 64 + tm * 16 + frow, fchunk)]);
 #pragma unroll
             for (int tn = 0; tn < 4; ++tn)
-                acc[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[tn], xf[tm], acc[tm][tn], 0, 0, 0);
-        if (kt + 1 < nk) store_tiles(cur ^ 1);
-        __syncthreads();
+                wf[tn] = *(const v4i*)(&lds_b[cur][lds_off(wn * 64 + tn * 16 + frow, fchunk)]);
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < 4; ++tn)
+                    acc[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[tn], xf[tm], acc[tm][tn], 0, 0, 0);
+            if (kt + 1 < nk) store_tiles(cur ^ 1);
+            __syncthreads();
+        }
+        epilogue(m0, n0);
+        if (!has_next) break;
+        t_cur = t_next;
     }
+}
 
-    // ---- epilogue: lane owns columns nb..nb+15 of rows m0 + wm*64 + 16*tm + frow.
-    // Processed 4 columns (one MFMA tile tn) at a time to keep registers low;
-    // the four bytes of each (tm, tn) pack into one dword, stored per tm.
-    const int nb = n0 + wn * 64 + 16 * fchunk;
-    if (nb >= g.N) return;
-    int alpha = g.alpha;
-    if (g.alpha_zp_dev) {
-        int zp = g.a_xor ? (int)*(const uint8_t*)g.alpha_zp_dev
-                         : (int)*(const int8_t*)g.alpha_zp_dev;
-        alpha = zp - g.a_sub;
-    }
-    float cm = g.cm;
-    if (g.epi == EPI_RQD && g.cm_a_scale_dev) {
-        float t1 = *g.cm_a_scale_dev * g.cm_b;
-        cm = t1 / g.cm_y;
-    }
-    const long long po = (long long)z * g.param_bstride;
-    const int sp = g.oH * g.oW;
-    const bool full16 = (nb + 16 <= g.N);
-    int rs[4];
-    bool tail[4];
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-        const int m = m0 + wm * 64 + tm * 16 + frow;
-        rs[tm] = (g.rowsum && m < g.M) ? g.rowsum[(long long)z * g.rowsum_bstride + m] : 0;
-        bool tl = false;
-        if (g.tail != TAIL_NONE && m < g.M) {
-            int s = m % sp;
-            if (g.tail == TAIL_SPATIAL) {
-                tl = s >= sp - sp % 16;
-            } else if (g.tail == TAIL_OW) {
-                int ow = s % g.oW;
-                tl = ow >= g.oW - g.oW % 16;
-            } else {
-                int oh = s / g.oW;
-                int oh0 = (oh / g.tile_h) * g.tile_h;
-                int th = g.oH - oh0 < g.tile_h ? g.oH - oh0 : g.tile_h;
-                int tsp = th * g.oW;
-                int ts = s - oh0 * g.oW;
-                tl = ts >= tsp - tsp % 16;
-            }
-        }
-        tail[tm] = tl;
-    }
-    if (g.epi == EPI_I32) {
-#pragma unroll
-        for (int tn = 0; tn < 4; ++tn) {
-            int32_t cc[4], bc[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                int n = nb + 4 * tn + r;
-                bool ok = n < g.N;
-                cc[r] = (ok && g.colsum) ? wrap_mul(alpha, g.colsum[po + n]) : 0;
-                bc[r] = g.beta_col ? (ok ? g.beta_col[po + n] : 0) : g.beta;
-            }
-#pragma unroll
-            for (int tm = 0; tm < 4; ++tm) {
-                const int m = m0 + wm * 64 + tm * 16 + frow;
-                if (m >= g.M) continue;
-                int32_t* yrow = (int32_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb + 4 * tn;
-                int32_t v[4] = {acc[tm][tn].x, acc[tm][tn].y, acc[tm][tn].z, acc[tm][tn].w};
-#pragma unroll
-                for (int r = 0; r < 4; ++r) v[r] = wrap_add(wrap_add(v[r], -cc[r]), -wrap_mul(bc[r], rs[tm]));
-                if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
-                    *(v4i*)yrow = v4i{v[0], v[1], v[2], v[3]};
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if (nb + 4 * tn + r < g.N) yrow[r] = v[r];
-                }
-            }
-        }
-        return;
-    }
-    uint32_t packed[4][4];
-#pragma unroll
-    for (int tn = 0; tn < 4; ++tn) {
-        int32_t cc[4], bc[4], bi[4];
-        float p0[4], p1[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            int n = nb + 4 * tn + r;
-            bool ok = n < g.N;
-            cc[r] = (ok && g.colsum) ? wrap_mul(alpha, g.colsum[po + n]) : 0;
-            bc[r] = g.beta_col ? (ok ? g.beta_col[po + n] : 0) : g.beta;
-            bi[r] = (ok && g.bias) ? g.bias[po + n] : 0;
-            if (g.epi == EPI_RQB) {
-                p0[r] = ok ? g.os[po + n] : 0.f;
-                p1[r] = 0.f;
-            } else if (g.epi == EPI_RQA || g.epi == EPI_RQC) {
-                p0[r] = ok ? g.cs[po + n] : 0.f;
-                p1[r] = ok ? g.bf[po + n] : 0.f;
-            } else {
-                p0[r] = 0.f; p1[r] = 0.f;
-            }
-        }
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm) {
-            int32_t v[4] = {acc[tm][tn].x, acc[tm][tn].y, acc[tm][tn].z, acc[tm][tn].w};
-            uint32_t w = 0;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                int32_t vv = wrap_add(wrap_add(v[r], -cc[r]), -wrap_mul(bc[r], rs[tm]));
-                int q;
-                if (g.epi == EPI_RQB) {
-                    int32_t vb = wrap_add(vv, bi[r]);
-                    q = (nb + 4 * tn + r >= g.bprime_from) ? rq_b_roundf(vb, p0[r], g.y_zp, g.lo, g.hi)
-                                                           : rq_b(vb, p0[r], g.y_zp, g.lo, g.hi);
-                } else if (g.epi == EPI_RQA) {
-                    q = tail[tm] ? rq_a_tail(vv, p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi)
-                                 : rq_a(vv, p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi);
-                } else if (g.epi == EPI_RQC) {
-                    q = tail[tm] ? rq_a_tail(vv, p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi)
-                                 : rq_c(vv, p0[r], p1[r], g.inv_y, g.y_zp, g.L, g.hi);
-                } else {
-                    q = rq_d(vv, cm, g.y_zp, g.lo, g.hi);
-                }
-                w |= (uint32_t)(q & 0xff) << (8 * r);
-            }
-            packed[tm][tn] = w;
-        }
-    }
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-        const int m = m0 + wm * 64 + tm * 16 + frow;
-        if (m >= g.M) continue;
-        if (g.y_nchw) {
-            uint8_t* yb = (uint8_t*)g.y + (long long)z * g.y_bstride;
-            int img = m / sp, s = m - img * sp;
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-                if (nb + i < g.N)
-                    yb[((long long)img * g.ldy + nb + i) * sp + s] = (uint8_t)(packed[tm][i >> 2] >> (8 * (i & 3)));
-        } else {
-            uint8_t* yrow = (uint8_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
-            if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
-                *(v4i*)yrow = v4i{(int)packed[tm][0], (int)packed[tm][1], (int)packed[tm][2], (int)packed[tm][3]};
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    if (nb + i < g.N) yrow[i] = (uint8_t)(packed[tm][i >> 2] >> (8 * (i & 3)));
-            }
-        }
-    }
+// Resident blocks of a kernel on the current device (occupancy x CUs),
+// computed once per instantiation.
+template <typename KernelT>
+static int resident_blocks(KernelT kernel) {
+    static int cached = 0;
+    if (cached > 0) return cached;
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;
+    cached = per_cu * cus;
+    return cached;
+}
+
+template <int BM, int BN, int VEC, int AMODE>
+static hipError_t launch_one(const GemmArgs& g, int batch, hipStream_t s) {
+    auto kern = qgemm_kernel<BM, BN, VEC, AMODE>;
+    const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+    int cap = resident_blocks(kern) / batch;
+    cap = cap < 8 ? 8 : (cap & ~7);
+    const int G = tiles < cap ? tiles : cap;
+    hipLaunchKernelGGL(kern, dim3(G, 1, batch), dim3(256), 0, s, g);
+    return hipGetLastError();
 }
 
 template <int BM, int BN, int AMODE>
 static hipError_t launch_vec(const GemmArgs& g, int batch, int vec, hipStream_t s) {
-    const int nbm = (g.M + BM - 1) / BM, nbn = (g.N + BN - 1) / BN;
-    dim3 grid(nbm * nbn, 1, batch);
-    dim3 block(256);
+    if (g.kWp > 0) return launch_one<BM, BN, 4, A_CONV4>(g, batch, s);
     switch (vec) {
-    case 16: hipLaunchKernelGGL((qgemm_kernel<BM, BN, 16, AMODE>), grid, block, 0, s, g); break;
-    case 8: hipLaunchKernelGGL((qgemm_kernel<BM, BN, 8, AMODE>), grid, block, 0, s, g); break;
-    case 4: hipLaunchKernelGGL((qgemm_kernel<BM, BN, 4, AMODE>), grid, block, 0, s, g); break;
-    case 1: hipLaunchKernelGGL((qgemm_kernel<BM, BN, 1, AMODE>), grid, block, 0, s, g); break;
+    case 16: return launch_one<BM, BN, 16, AMODE>(g, batch, s);
+    case 8: return launch_one<BM, BN, 8, AMODE>(g, batch, s);
+    case 4: return launch_one<BM, BN, 4, AMODE>(g, batch, s);
+    case 1: return launch_one<BM, BN, 1, AMODE>(g, batch, s);
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec, hipStream_t s) {

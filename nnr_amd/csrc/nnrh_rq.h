@@ -87,4 +87,56 @@ __device__ __forceinline__ int rq_d(int32_t acc, float cm, int y_zp, int lo, int
     return clampi(x86_f2i(__builtin_rintf(val)), lo, hi);
 }
 
+// ---------------------------------------------------------------------------
+// Fast forms of the same formulas for the GEMM epilogue. Exactness:
+//  * clamp(max then min) == v_med3 for qlo <= qhi and non-NaN input;
+//  * for |x| < 2^22, fl(x + 1.5*2^23) lies in [2^23, 2^24] where the ulp is
+//    1, so it is x rounded to an integer with ties to even (1.5*2^23 is even),
+//    and its bit pattern is 0x4B400000 + rne(x);
+//  * 0x4B400000 has a zero low byte, so the low byte of bits + zp is the
+//    output byte of rne(x) + zp.
+// Inputs that could exceed the window are first clamped to +-2^21, which
+// never changes a result that saturates to an 8-bit range.
+constexpr float RNE_MAGIC = 12582912.0f;   // 1.5 * 2^23
+constexpr int RNE_MAGIC_BITS = 0x4B400000;
+
+__device__ __forceinline__ int rne_bits(float x) { return __float_as_int(x + RNE_MAGIC); }
+__device__ __forceinline__ float med3f(float x, float lo, float hi) {
+    return __builtin_amdgcn_fmed3f(x, lo, hi);
+}
+__device__ __forceinline__ int med3i(int x, int lo, int hi) {
+    return x < lo ? lo : (x > hi ? hi : x);
+}
+
+// RQ-B: f = clamp(float(v) * os, lo - zp, hi - zp); byte(rne(f) + zp)
+__device__ __forceinline__ uint32_t rqb_fast(int32_t v, float os, int y_zp, int lo, int hi) {
+    float f = (float)v * os;
+    f = med3f(f, (float)lo - (float)y_zp, (float)hi - (float)y_zp);
+    return (uint32_t)(rne_bits(f) + y_zp);
+}
+// RQ-A: clamp(rne(fma(v,cs,bf) * inv_y) + zp, L, hi)
+__device__ __forceinline__ uint32_t rqa_fast(int32_t v, float cs, float bf, float inv_y, int y_zp,
+                                             int L, int hi) {
+    float f = __builtin_fmaf((float)v, cs, bf);
+    float q = med3f(f * inv_y, -2097152.0f, 2097152.0f);
+    return (uint32_t)med3i(rne_bits(q) - RNE_MAGIC_BITS + y_zp, L, hi);
+}
+// RQ-C: rne(clamp(fma(fma(v,cs,bf), inv_y, zp), qmin, qmax))
+__device__ __forceinline__ uint32_t rqc_fast(int32_t v, float cs, float bf, float inv_y, int y_zp,
+                                             int qmin, int qmax) {
+    float t = __builtin_fmaf((float)v, cs, bf);
+    float f = __builtin_fmaf(t, inv_y, (float)y_zp);
+    f = med3f(f, (float)qmin, (float)qmax);
+    return (uint32_t)rne_bits(f);
+}
+// RQ-D: clamp(nearbyint(v*cm + zp), lo, hi); |val| >= 2^31 converts to
+// INT32_MIN on x86 and so clamps to lo
+__device__ __forceinline__ uint32_t rqd_fast(int32_t v, float cm, int y_zp, int lo, int hi) {
+    float t = (float)v * cm;
+    float val = t + (float)y_zp;
+    if (!(val < 2147483648.0f && val >= -2147483648.0f)) return (uint32_t)lo;
+    float q = med3f(val, -2097152.0f, 2097152.0f);
+    return (uint32_t)med3i(rne_bits(q) - RNE_MAGIC_BITS, lo, hi);
+}
+
 }  // namespace nnrh

@@ -136,6 +136,9 @@ CONV_CASES = [
     ("packed_bprime", 1, 32, 6, 7, 48 + 40, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=11)),
     ("packed_s2", 2, 64, 13, 13, 96, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1)),
     ("packed_wzp", 1, 48, 9, 9, 40, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, w_zp=(3,))),
+    # a negative int8 w_zp is read through the uint8 activation type (253)
+    ("packed_wzp_neg", 1, 32, 7, 7, 24, 1, dict(y_nhwc=1, w_zp=(-3,), y_scale=3.0, y_zp=40)),
+    ("first_s1_pad", 2, 3, 20, 21, 48, 5, dict(pads=(2, 1, 2, 1), y_nhwc=1, y_zp=17)),
     ("packed_nchw_out", 1, 32, 20, 20, 24, 3, dict(pads=(1, 1, 1, 1), y_nhwc=0)),
     ("packed_dil", 1, 16, 12, 12, 32, 3, dict(pads=(2, 2, 2, 2), dil=(2, 2), y_nhwc=1)),
     ("packed_c24", 2, 24, 10, 10, 144, 1, dict(y_nhwc=1, x_nhwc=1)),
