@@ -89,6 +89,7 @@ struct GemmArgs {
     long long y_bstride;    // per-batch stride in elements
     int y_type;             // 0 u8, 1 s8, 2 i32
     int y_nchw;             // 1: scatter to NCHW [img][n][s] (s = m % (oH*oW))
+    int nbatch;             // batch count (set by the launcher)
 };
 
 // Tile shapes available to the launcher (BM x BN, 256 threads).
@@ -96,6 +97,9 @@ enum TileCfg : int { TILE_128x128 = 0, TILE_256x64 = 1, TILE_64x256 = 2 };
 
 hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec,
                         hipStream_t s);
+// pipelined direct-to-LDS variant (nnrh_qgemm_dma.hip) and its eligibility
+bool qgemm_dma_eligible(const GemmArgs& g, int vec);
+hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t s);
 
 // ---- misc kernels (nnrh_misc.hip) ----
 hipError_t launch_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C,

@@ -501,30 +501,13 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(GemmArgs g) {
     }
 }
 
-// Resident blocks of a kernel on the current device (occupancy x CUs),
-// computed once per instantiation.
-template <typename KernelT>
-static int resident_blocks(KernelT kernel) {
-    static int cached = 0;
-    if (cached > 0) return cached;
-    int per_cu = 0, dev = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu < 1)
-        per_cu = 1;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-        cus = 256;
-    cached = per_cu * cus;
-    return cached;
-}
-
 template <int BM, int BN, int VEC, int AMODE>
 static hipError_t launch_one(const GemmArgs& g, int batch, hipStream_t s) {
-    auto kern = qgemm_kernel<BM, BN, VEC, AMODE>;
+    // one tile per block: this kernel keeps its next-tile prefetch in VGPRs,
+    // and hardware block dispatch overlaps tiles better than a persistent loop
     const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-    int cap = resident_blocks(kern) / batch;
-    cap = cap < 8 ? 8 : (cap & ~7);
-    const int G = tiles < cap ? tiles : cap;
-    hipLaunchKernelGGL(kern, dim3(G, 1, batch), dim3(256), 0, s, g);
+    auto kern = qgemm_kernel<BM, BN, VEC, AMODE>;
+    hipLaunchKernelGGL(kern, dim3(tiles, 1, batch), dim3(256), 0, s, g);
     return hipGetLastError();
 }
 
@@ -545,6 +528,7 @@ hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec, hipStre
     if (g.Kp <= 0 || (g.Kp & 63) || g.Kp < g.K) return hipErrorInvalidValue;
     if (g.a == nullptr || g.b == nullptr || g.y == nullptr) return hipErrorInvalidValue;
     const bool conv = (g.H > 0);
+    if (qgemm_dma_eligible(g, vec)) return launch_qgemm_dma(g, batch, tile, s);
     switch (tile) {
     case TILE_128x128:
         return conv ? launch_vec<128, 128, A_CONV>(g, batch, vec, s)

@@ -1,0 +1,433 @@
+// nnrh_qgemm_dma.hip -- pipelined int8 GEMM / implicit-GEMM convolution for
+// gfx950: persistent blocks, direct global->LDS loads, S-stage LDS ring.
+//
+// Same arithmetic as qgemm_kernel (nnrh_qgemm.hip): i8 MFMA 16x16x64 with
+// exact int32 accumulation, uint8 activations fed as x ^ 0x80 and the
+// zero-point shift folded into the per-column constant c0[n], then one of
+// NNR's requantize epilogues (RQ-B for the packed / NR16 conv drivers,
+// jit_conv_int8_ukernel.cpp:906-967 and :1857-1918; RQ-D for QLinearMatMul,
+// QLinearMatMul.cpp:188-198; RQ-A body for im2col, QLinearConv.cpp:1171-1179).
+// Results are bit-identical to the register-staged kernel; only the data
+// movement differs:
+//  * every 16-byte chunk of the A and B tiles goes straight from global
+//    memory into LDS (global_load_lds_dwordx4). No VGPR staging, so S
+//    K-steps are in flight per block and HBM latency is hidden behind the
+//    MFMA work of the steps before them;
+//  * blocks are persistent: one block walks a list of output tiles and the
+//    load stream runs across tile boundaries, so the next tile's first
+//    K-steps load while the current tile's epilogue runs;
+//  * out-of-image taps, rows past M and K padding load from a constant
+//    16-byte pattern of the pad byte instead of branching around the load;
+//  * the per-column requantize constants of a tile (c0 and the scales) ride
+//    the same DMA stream into a small LDS ring slot, read back in the
+//    epilogue without touching the vector-memory counter.
+// The u8 -> s8 shift is applied to the activation fragments after they are
+// read from LDS (4 v_xor per fragment).
+//
+// Eligibility (checked by the launcher): A rows in 16-byte chunks (conv:
+// channels % 16 == 0; dense: K % 16 == 0), no per-row zero-point term
+// (beta == 0), zero points known on the host, NHWC / row-major output and
+// no scalar-tail or RQ-B' columns. Everything else takes qgemm_kernel.
+#include "nnrh_internal.h"
+#include "nnrh_rq.h"
+
+namespace nnrh {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+#define NNRH_LDS __attribute__((address_space(3)))
+
+namespace {
+
+__device__ __forceinline__ int dma_lds_off(int row, int c) {
+    return row * 64 + ((c ^ ((row >> 1) & 3)) << 4);
+}
+
+// 256 x 16 bytes: chunk b holds 16 copies of byte b (pad source for the DMA)
+struct PadTable {
+    uint32_t w[256 * 4];
+    constexpr PadTable() : w() {
+        for (int i = 0; i < 256 * 4; ++i) w[i] = (uint32_t)(i >> 2) * 0x01010101u;
+    }
+};
+__device__ const PadTable kPadTable{};
+
+// s_waitcnt with vmcnt = n and no wait on expcnt / lgkmcnt (gfx9 encoding)
+#define NNRH_VMCNT(n) ((((n) & 0xF)) | 0x70 | 0xF00 | ((((n) >> 4) & 3) << 14))
+
+__device__ __forceinline__ void dma16(const void* src, uint8_t* lds_dst) {
+    __builtin_amdgcn_global_load_lds(src, (NNRH_LDS void*)lds_dst, 16, 0, 0);
+}
+
+__device__ __forceinline__ void block_barrier() {
+    // plain s_barrier: the waits this kernel needs are explicit s_waitcnt;
+    // the memory clobber keeps the compiler from moving LDS accesses across
+    asm volatile("s_barrier" ::: "memory");
+}
+
+template <int EPI>
+struct EpiParams;
+// number of per-column 32-bit arrays staged per tile
+template <> struct EpiParams<EPI_RQB> { static constexpr int NP = 2; };   // c0, os
+template <> struct EpiParams<EPI_RQA> { static constexpr int NP = 3; };   // c0, cs, bf
+template <> struct EpiParams<EPI_RQD> { static constexpr int NP = 1; };   // c0
+template <> struct EpiParams<EPI_I32> { static constexpr int NP = 1; };   // c0
+
+}  // namespace
+
+template <int BM, int BN, int S, int AMODE, int EPI>
+__global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
+    constexpr int WAVES_N = BN / 64;
+    static_assert((BM / 64) * WAVES_N == 4, "4 waves of 64x64");
+    constexpr int A_CH = BM / 64;            // DMA chunks per thread per step (A)
+    constexpr int B_CH = BN / 64;            // (B)
+    constexpr int LPS = A_CH + B_CH;         // DMA instructions per thread per step
+    constexpr int STAGE = (BM + BN) * 64;    // bytes per K-step
+    constexpr int NP = EpiParams<EPI>::NP;
+    constexpr int PBYTES = NP * BN * 4;
+    constexpr int PWAVES = (PBYTES + 1023) / 1024;   // waves issuing the param DMA
+    constexpr int PSLOT = PWAVES * 1024;
+    static_assert(PWAVES <= 4, "param slot");
+
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE + S * PSLOT];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int frow = lane & 15, fchunk = lane >> 4;
+
+    // ---- tile list: (z, m-block, n-block), n fastest; XCD-aware split
+    const int nbn = (g.N + BN - 1) / BN;
+    const int nbm = (g.M + BM - 1) / BM;
+    const int per_z = nbm * nbn;
+    const int total = per_z * g.nbatch;
+    const int G = gridDim.x;
+    int t_first, t_end, t_step;
+    if ((G & 7) == 0) {
+        const int chunk = (total + 7) >> 3;
+        const int xcd = blockIdx.x & 7;
+        t_first = xcd * chunk + (blockIdx.x >> 3);
+        t_end = min(total, (xcd + 1) * chunk);
+        t_step = G >> 3;
+    } else {
+        t_first = blockIdx.x;
+        t_end = total;
+        t_step = G;
+    }
+    if (t_first >= t_end) return;
+
+    const int nk = g.Kp >> 6;
+    const uint32_t xmask = (uint32_t)g.a_xor * 0x01010101u;
+    const uint8_t* pad16 = (const uint8_t*)&kPadTable.w[(g.pad_byte & 0xff) * 4];
+    const int sp_out = g.oH * g.oW;
+    // this thread's 16-byte chunk of a 64-byte row (pre-swizzled so the LDS
+    // image matches dma_lds_off)
+    const int cdma = (tid & 3) ^ ((tid >> 3) & 3);
+
+    // ---- producer (DMA issue) state
+    int p_t = t_first, p_kt = 0, p_tseq = 0, p_gs = 0;
+    const uint8_t* p_a = nullptr;   // batch base of A
+    const int8_t* p_b = nullptr;    // batch base of B
+    int p_n0 = 0;
+    long long p_pbase = 0;          // batch offset of the per-column arrays
+    long long a_base[A_CH];
+    int a_ih0[A_CH], a_iw0[A_CH];
+    bool a_ok[A_CH];
+    int kc_ic = 0, kc_kh = 0, kc_kw = 0;
+
+    auto p_setup = [&](int t) {
+        const int z = t / per_z;
+        const int r = t - z * per_z;
+        const int m0 = (r / nbn) * BM;
+        p_n0 = (r % nbn) * BN;
+        p_a = g.a + (long long)z * g.a_bstride;
+        p_b = g.b + (long long)z * g.b_bstride;
+        p_pbase = (long long)z * g.param_bstride;
+#pragma unroll
+        for (int j = 0; j < A_CH; ++j) {
+            const int m = m0 + (tid >> 2) + 64 * j;
+            a_ok[j] = m < g.M;
+            if constexpr (AMODE == A_DENSE) {
+                a_base[j] = (long long)m * g.lda;
+                a_ih0[j] = 0; a_iw0[j] = 0;
+            } else {
+                const int mm = a_ok[j] ? m : 0;
+                const int img = mm / sp_out, s = mm - img * sp_out;
+                const int oh = s / g.oW, ow = s - oh * g.oW;
+                a_base[j] = (long long)img * g.H * g.W * g.Cs;
+                a_ih0[j] = oh * g.sH - g.pad_t;
+                a_iw0[j] = ow * g.sW - g.pad_l;
+            }
+        }
+        if constexpr (AMODE == A_CONV) {
+            const int k = cdma * 16;
+            const int kp = k / g.C;
+            kc_ic = k - kp * g.C;
+            kc_kh = kp / g.kW;
+            kc_kw = kp - kc_kh * g.kW;
+        }
+    };
+
+    // issue the DMA of producer step (p_t, p_kt) into stage p_gs % S
+    auto p_issue = [&]() {
+        uint8_t* st = lds + (p_gs % S) * STAGE;
+        const int kk = (p_kt << 6) + cdma * 16;
+#pragma unroll
+        for (int j = 0; j < A_CH; ++j) {
+            const uint8_t* src = pad16;
+            if constexpr (AMODE == A_DENSE) {
+                if (a_ok[j] && kk < g.K) src = p_a + a_base[j] + kk;
+            } else {
+                if (a_ok[j] && kc_kh < g.kH) {
+                    const int ih = a_ih0[j] + kc_kh * g.dH;
+                    const int iw = a_iw0[j] + kc_kw * g.dW;
+                    if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
+                        src = p_a + a_base[j] + ((long long)(ih * g.W + iw) * g.Cs + kc_ic);
+                }
+            }
+            dma16(src, st + wave * 1024 + j * 4096);
+        }
+#pragma unroll
+        for (int j = 0; j < B_CH; ++j) {
+            int n = p_n0 + (tid >> 2) + 64 * j;
+            n = n < g.Np ? n : g.Np - 1;
+            dma16(p_b + (long long)n * g.Kp + kk, st + BM * 64 + wave * 1024 + j * 4096);
+        }
+        if (p_kt == 0 && wave < PWAVES) {
+            // per-column constants of the tile: NP arrays of BN int32/float,
+            // one 16-byte chunk per lane; chunks past the arrays reload the
+            // last one (never read back)
+            const int i = wave * 64 + lane;          // chunk index in the slot
+            const int arr = i / (BN / 4);
+            const int col4 = i - arr * (BN / 4);
+            int c = p_n0 + col4 * 4;
+            c = c + 4 <= g.Np ? c : g.Np - 4;
+            const void* base;
+            if (arr == 0) base = g.c0;
+            else if (EPI == EPI_RQB) base = g.os;
+            else if (arr == 1) base = g.cs;
+            else base = g.bf;
+            if (arr >= NP) base = g.c0;
+            const uint8_t* src = (const uint8_t*)base + (p_pbase + c) * 4;
+            dma16(src, lds + S * STAGE + (p_tseq % S) * PSLOT + wave * 1024);
+        }
+        // advance
+        ++p_gs;
+        if constexpr (AMODE == A_CONV) {
+            kc_ic += 64;
+            while (kc_ic >= g.C) {
+                kc_ic -= g.C;
+                if (++kc_kw == g.kW) { kc_kw = 0; ++kc_kh; }
+            }
+        }
+        if (++p_kt == nk) {
+            p_kt = 0;
+            ++p_tseq;
+            p_t += t_step;
+            if (p_t < t_end) p_setup(p_t);
+        }
+    };
+
+    // ---- consumer state
+    int c_t = t_first, c_kt = 0, c_tseq = 0, c_gs = 0;
+    v4i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    auto epilogue = [&]() {
+        const int z = c_t / per_z;
+        const int r = c_t - z * per_z;
+        const int m0 = (r / nbn) * BM;
+        const int n0 = (r % nbn) * BN;
+        const int nl = wn * 64 + 16 * fchunk;   // first column of this lane in the tile
+        const int nb = n0 + nl;
+        if (nb >= g.N) return;
+        const uint8_t* ps = lds + S * STAGE + (c_tseq % S) * PSLOT;
+        v4i pc[4], p0[4], p1[4];
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) {
+            pc[tn] = *(const v4i*)(ps + (nl + 4 * tn) * 4);
+            if constexpr (NP >= 2) p0[tn] = *(const v4i*)(ps + BN * 4 + (nl + 4 * tn) * 4);
+            if constexpr (NP >= 3) p1[tn] = *(const v4i*)(ps + 2 * BN * 4 + (nl + 4 * tn) * 4);
+        }
+        const bool full16 = nb + 16 <= g.N;
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+            const int m = m0 + wm * 64 + tm * 16 + frow;
+            if (m >= g.M) continue;
+            if constexpr (EPI == EPI_I32) {
+                int32_t* yrow = (int32_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
+                v4i o[4];
+#pragma unroll
+                for (int tn = 0; tn < 4; ++tn) {
+                    o[tn].x = (int)((uint32_t)acc[tm][tn].x + (uint32_t)pc[tn].x);
+                    o[tn].y = (int)((uint32_t)acc[tm][tn].y + (uint32_t)pc[tn].y);
+                    o[tn].z = (int)((uint32_t)acc[tm][tn].z + (uint32_t)pc[tn].z);
+                    o[tn].w = (int)((uint32_t)acc[tm][tn].w + (uint32_t)pc[tn].w);
+                }
+                if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
+#pragma unroll
+                    for (int tn = 0; tn < 4; ++tn) *(v4i*)(yrow + 4 * tn) = o[tn];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (nb + i < g.N) yrow[i] = o[i >> 2][i & 3];
+                }
+            } else {
+                uint32_t packed[4];
+#pragma unroll
+                for (int tn = 0; tn < 4; ++tn) {
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int32_t v = (int32_t)((uint32_t)acc[tm][tn][q] + (uint32_t)pc[tn][q]);
+                        uint32_t b;
+                        if constexpr (EPI == EPI_RQB)
+                            b = rqb_fast(v, __int_as_float(p0[tn][q]), g.y_zp, g.lo, g.hi);
+                        else if constexpr (EPI == EPI_RQA)
+                            b = rqa_fast(v, __int_as_float(p0[tn][q]), __int_as_float(p1[tn][q]),
+                                         g.inv_y, g.y_zp, g.L, g.hi);
+                        else
+                            b = rqd_fast(v, g.cm, g.y_zp, g.lo, g.hi);
+                        w |= (b & 0xffu) << (8 * q);
+                    }
+                    packed[tn] = w;
+                }
+                uint8_t* yrow = (uint8_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
+                if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
+                    *(v4i*)yrow = v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (nb + i < g.N) yrow[i] = (uint8_t)(packed[i >> 2] >> (8 * (i & 3)));
+                }
+            }
+        }
+    };
+
+    // ---- prologue: S-1 steps in flight
+    p_setup(p_t);
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+        if (p_t < t_end) p_issue();
+
+    for (;;) {
+        // wait for this thread's DMAs of step c_gs; later steps stay in flight
+        const int ahead = p_gs - c_gs - 1;
+        if (ahead >= S - 2) __builtin_amdgcn_s_waitcnt(NNRH_VMCNT((S - 2) * LPS));
+        else if (S >= 4 && ahead == 1) __builtin_amdgcn_s_waitcnt(NNRH_VMCNT(LPS));
+        else __builtin_amdgcn_s_waitcnt(NNRH_VMCNT(0));
+        // every wave's DMAs of the step have landed; every wave is done
+        // reading the stage (and param slot) the next issue overwrites
+        block_barrier();
+        if (p_t < t_end) p_issue();
+
+        const uint8_t* st = lds + (c_gs % S) * STAGE;
+        v4i xf[4], wf[4];
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+            v4i v = *(const v4i*)(st + dma_lds_off(wm * 64 + tm * 16 + frow, fchunk));
+            xf[tm] = v4i{(int)((uint32_t)v.x ^ xmask), (int)((uint32_t)v.y ^ xmask),
+                         (int)((uint32_t)v.z ^ xmask), (int)((uint32_t)v.w ^ xmask)};
+        }
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn)
+            wf[tn] = *(const v4i*)(st + BM * 64 + dma_lds_off(wn * 64 + tn * 16 + frow, fchunk));
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < 4; ++tn)
+                acc[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[tn], xf[tm], acc[tm][tn], 0, 0, 0);
+        ++c_gs;
+        if (++c_kt == nk) {
+            epilogue();
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+            c_kt = 0;
+            ++c_tseq;
+            c_t += t_step;
+            if (c_t >= t_end) break;
+        }
+    }
+    // nothing may be left in flight into LDS when the block retires
+    __builtin_amdgcn_s_waitcnt(NNRH_VMCNT(0));
+}
+
+namespace {
+
+template <typename KernelT>
+int dma_resident_blocks(KernelT kernel) {
+    static int cached = 0;
+    if (cached > 0) return cached;
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;
+    cached = per_cu * cus;
+    return cached;
+}
+
+template <int BM, int BN, int S, int AMODE, int EPI>
+hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
+    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI>;
+    const long long tiles = (long long)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN) * batch;
+    long long cap = dma_resident_blocks(kern);
+    cap = cap < 8 ? 8 : (cap & ~7LL);
+    const int G = (int)(tiles < cap ? tiles : cap);
+    if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+    GemmArgs a = g;
+    a.nbatch = batch;
+    hipLaunchKernelGGL(kern, dim3(G, 1, 1), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int BM, int BN, int S, int AMODE>
+hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
+    switch (g.epi) {
+    case EPI_RQB: return launch_dma<BM, BN, S, AMODE, EPI_RQB>(g, batch, s);
+    case EPI_RQA: return launch_dma<BM, BN, S, AMODE, EPI_RQA>(g, batch, s);
+    case EPI_RQD: return launch_dma<BM, BN, S, AMODE, EPI_RQD>(g, batch, s);
+    case EPI_I32: return launch_dma<BM, BN, S, AMODE, EPI_I32>(g, batch, s);
+    default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace
+
+bool qgemm_dma_eligible(const GemmArgs& g, int vec) {
+    if (vec != 16 || g.kWp > 0 || g.y_nchw) return false;
+    if (g.c0 == nullptr || g.alpha_zp_dev != nullptr || g.rowsum != nullptr) return false;
+    if (g.tail != TAIL_NONE) return false;
+    if (g.epi == EPI_RQB && g.bprime_from < g.N) return false;
+    if (g.epi == EPI_RQC) return false;
+    if (g.epi == EPI_RQD && g.cm_a_scale_dev != nullptr) return false;
+    if (g.Np < 4 || (g.Np & 3)) return false;
+    if (g.H > 0 && (g.C % 16 || g.Cs % 16)) return false;
+    if (g.H == 0 && (g.K % 16 || g.lda % 16)) return false;
+    return true;
+}
+
+hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t s) {
+    const bool conv = g.H > 0;
+    switch (tile) {
+    case TILE_128x128:
+        return conv ? launch_dma_epi<128, 128, 4, A_CONV>(g, batch, s)
+                    : launch_dma_epi<128, 128, 4, A_DENSE>(g, batch, s);
+    case TILE_256x64:
+        return conv ? launch_dma_epi<256, 64, 3, A_CONV>(g, batch, s)
+                    : launch_dma_epi<256, 64, 3, A_DENSE>(g, batch, s);
+    case TILE_64x256:
+        return conv ? launch_dma_epi<64, 256, 3, A_CONV>(g, batch, s)
+                    : launch_dma_epi<64, 256, 3, A_DENSE>(g, batch, s);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace nnrh

@@ -158,6 +158,14 @@ CONV_CASES = [
                                               post_fn=1, y_zp=12)),
     ("float_int8act", 1, 16, 9, 9, 24, 3, dict(pads=(1, 1, 1, 1), act_dtype=np.int8, y_zp=-4)),
     ("float_pcz", 1, 16, 8, 8, 4, 1, dict(w_zp=(1, -2, 3, 0))),
+    # direct-to-LDS pipelined GEMM: taps spanning a 64-byte K step (C=48),
+    # a ragged last column block (OC=72), more tiles than resident blocks
+    # (several tiles per persistent block), strided 3x3, grouped RQ-A
+    ("dma_c48_oc72", 2, 48, 11, 13, 72, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1, y_zp=5)),
+    ("dma_persistent_1x1", 16, 64, 56, 56, 256, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=2)),
+    ("dma_s2_3x3", 4, 128, 28, 28, 128, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1,
+                                                x_nhwc=1)),
+    ("dma_grouped_c16", 1, 64, 8, 8, 64, 3, dict(group=4, pads=(1, 1, 1, 1))),
 ]
 
 
