@@ -339,7 +339,8 @@ struct nnrh_qconv {
     nnrh_qconv_desc d{};
     int branch = 0;
     bool use_dw = false;         // depthwise VALU kernel
-    int transform = 0;           // 0 none, 1 NCHW->NHWC, 2 NCHW->NHWC padded to 4 ch
+    int transform = 0;           // 0 none, 1 NCHW->NHWC, 2 NCHW->NHWC padded to 4 ch,
+                                 // 3 first-layer padded multi-copy NHWC4 image
     int Cx = 0;                  // channels of the tensor the kernel reads
     int groups = 1;
     bool need_rowsum = false;
@@ -491,7 +492,11 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
         h->need_rowsum = any_wzp;
         if (any_wzp && (rc = upload(&h->beta_col, betac.data(), betac.size()))) return fail(rc);
 
-        if (first) { h->transform = 2; h->Cx = 4; }
+        // first layer with NHWC output: padded multi-copy image for the
+        // pipelined kernel (its epilogue has no scalar tails then)
+        const bool first_copies = first && d->y_nhwc && G == 1;
+        if (first_copies) { h->transform = 3; h->Cx = 4; }
+        else if (first) { h->transform = 2; h->Cx = 4; }
         else { h->transform = d->x_nhwc ? 0 : 1; h->Cx = d->C; }
 
         GemmArgs& g = h->g;
@@ -506,6 +511,16 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
         g.pad_t = d->pad_t; g.pad_l = d->pad_l;
         g.kWp = first ? kWp : 0;
         g.pad_byte = d->x_zp & 0xff;
+        if (first_copies) {
+            // pads folded into the image; rows long enough for the last
+            // chunk of kWp taps; copies for every start-pixel residue mod 4
+            const int Hp = std::max(d->H + d->pad_t + d->pad_b, (d->oH - 1) * d->sH + d->kH);
+            const int Wc = round_up(std::max(d->W + d->pad_l + d->pad_r, (d->oW - 1) * d->sW + kWp), 4);
+            g.H = Hp; g.W = Wc;
+            g.pad_t = 0; g.pad_l = 0;
+            g.copy_shift = (d->sW % 4 == 0) ? 2 : (d->sW % 2 == 0 ? 1 : 0);
+            g.copy_stride = (long long)d->N * Hp * Wc * 4;
+        }
         g.a_bstride = first ? 0 : Cg;   // group channel offset
         g.b = h->wpack;
         g.b_bstride = (long long)Np * Kp;
@@ -553,7 +568,10 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
         if (G > 1 && (Cg % h->vec)) h->vec = 1;
     }
     // scratch: transformed input and row sums
-    if (h->transform) {
+    if (h->transform == 3) {
+        size_t bytes = (size_t)(4 >> h->g.copy_shift) * (size_t)h->g.copy_stride;
+        if ((rc = nnrh_malloc((void**)&h->xs, bytes))) return fail(rc);
+    } else if (h->transform) {
         size_t bytes = (size_t)d->N * d->H * d->W * h->Cx;
         if ((rc = nnrh_malloc((void**)&h->xs, bytes))) return fail(rc);
     }
@@ -577,7 +595,13 @@ extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stre
     const nnrh_qconv_desc& d = h->d;
     hipStream_t s = S(stream);
     const uint8_t* src = (const uint8_t*)x;
-    if (h->transform) {
+    if (h->transform == 3) {
+        ProfScope ps("first_layer_copies", s);
+        HIP_TRY(launch_first_layer_copies(src, h->xs, d.N, d.C, d.H, d.W, h->g.H, h->g.W, d.pad_t,
+                                          d.pad_l, h->g.copy_shift, (uint8_t)(d.x_zp & 0xff), s),
+                "first_layer_copies");
+        src = h->xs;
+    } else if (h->transform) {
         ProfScope ps("nchw_to_nhwc_u8", s);
         HIP_TRY(launch_nchw_to_nhwc_u8(src, h->xs, d.N, d.C, d.H * d.W, h->Cx,
                                        (uint8_t)(d.x_zp & 0xff), s),

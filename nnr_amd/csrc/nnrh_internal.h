@@ -90,6 +90,11 @@ struct GemmArgs {
     int y_type;             // 0 u8, 1 s8, 2 i32
     int y_nchw;             // 1: scatter to NCHW [img][n][s] (s = m % (oH*oW))
     int nbatch;             // batch count (set by the launcher)
+    // first layer on the pipelined kernel (kWp > 0, copy_stride > 0): A is the
+    // padded multi-copy NHWC4 image of launch_first_layer_copies; H/W are its
+    // padded height / row length and the pads are already applied
+    int copy_shift;
+    long long copy_stride;  // bytes per copy
 };
 
 // Tile shapes available to the launcher (BM x BN, 256 threads).
@@ -117,6 +122,9 @@ hipError_t launch_rowsum_dense(const uint8_t* a, long long lda,
                                int a_zp, const void* a_zp_dev, int32_t* out,
                                int batch, hipStream_t s);
 hipError_t launch_fill_u8(void* p, uint8_t v, long long n, hipStream_t s);
+hipError_t launch_first_layer_copies(const uint8_t* x, uint8_t* y, int N, int C, int H, int W,
+                                     int Hp, int Wc, int pad_t, int pad_l, int copy_shift,
+                                     uint8_t fill, hipStream_t s);
 hipError_t launch_rowsum_conv(const uint8_t* x, int N, int H, int W, int Cs,
                               int Cg, int groups, int oH, int oW, int kH,
                               int kW, int sH, int sW, int dH, int dW,

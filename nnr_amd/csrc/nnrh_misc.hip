@@ -70,6 +70,48 @@ hipError_t launch_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C, in
     return hipGetLastError();
 }
 
+// First-layer input for the pipelined GEMM: NCHW uint8 with C <= 4 becomes
+// zero-point padded NHWC4 rows of Wc pixels, stored as ncopy copies where
+// copy i starts (i << copy_shift) pixels further right. A 4-tap chunk of the
+// implicit im2col starting at padded pixel p then sits 16-byte aligned in
+// copy (p & 3) >> copy_shift, at pixel p - (p & 3).
+// y: [ncopy][N][Hp][Wc] x uint32 (4 channels, padding = fill).
+__global__ __launch_bounds__(256) void first_layer_copies_kernel(
+    const uint8_t* __restrict x, uint32_t* __restrict y, int C, int H, int W, int Hp, int Wc,
+    int pad_t, int pad_l, int copy_shift, long long per_copy, long long total, uint8_t fill) {
+    long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const long long ci = i / per_copy;
+    long long rem = i - ci * per_copy;
+    const int j = (int)(rem % Wc);
+    rem /= Wc;
+    const int ihp = (int)(rem % Hp);
+    const long long n = rem / Hp;
+    const int ih = ihp - pad_t;
+    const int iw = j + ((int)ci << copy_shift) - pad_l;
+    uint32_t w = (uint32_t)fill * 0x01010101u;
+    if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) {
+        const long long HW = (long long)H * W;
+        const uint8_t* xp = x + n * C * HW + (long long)ih * W + iw;
+        w = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) w |= (uint32_t)(c < C ? xp[(long long)c * HW] : fill) << (8 * c);
+    }
+    y[i] = w;
+}
+
+hipError_t launch_first_layer_copies(const uint8_t* x, uint8_t* y, int N, int C, int H, int W,
+                                     int Hp, int Wc, int pad_t, int pad_l, int copy_shift,
+                                     uint8_t fill, hipStream_t s) {
+    if (N <= 0 || C > 4 || ((uintptr_t)y & 15)) return hipErrorInvalidValue;
+    const int ncopy = 4 >> copy_shift;
+    const long long per_copy = (long long)N * Hp * Wc;
+    const long long total = per_copy * ncopy;
+    hipLaunchKernelGGL(first_layer_copies_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       x, (uint32_t*)y, C, H, W, Hp, Wc, pad_t, pad_l, copy_shift, per_copy, total, fill);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Depthwise QLinearConv, NHWC in / NHWC or NCHW out, requantize RQ-A with
 // clamp [L, hi]. Each thread computes 4 consecutive channels of one output

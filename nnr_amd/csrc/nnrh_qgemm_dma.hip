@@ -24,6 +24,11 @@
 // The u8 -> s8 shift is applied to the activation fragments after they are
 // read from LDS (4 v_xor per fragment).
 //
+// The first layer (3-4 input channels, RQ-C, first-layer driver of
+// conv_first_layer_int8_avx512.h:262-273) runs here on a zero-point padded,
+// multi-copy NHWC4 image (launch_first_layer_copies): every 16-byte chunk of
+// its K order (kh, kw < kWp, c < 4) is then 4 aligned, in-bounds taps.
+//
 // Eligibility (checked by the launcher): A rows in 16-byte chunks (conv:
 // channels % 16 == 0; dense: K % 16 == 0), no per-row zero-point term
 // (beta == 0), zero points known on the host, NHWC / row-major output and
@@ -69,6 +74,7 @@ struct EpiParams;
 // number of per-column 32-bit arrays staged per tile
 template <> struct EpiParams<EPI_RQB> { static constexpr int NP = 2; };   // c0, os
 template <> struct EpiParams<EPI_RQA> { static constexpr int NP = 3; };   // c0, cs, bf
+template <> struct EpiParams<EPI_RQC> { static constexpr int NP = 3; };   // c0, cs, bf
 template <> struct EpiParams<EPI_RQD> { static constexpr int NP = 1; };   // c0
 template <> struct EpiParams<EPI_I32> { static constexpr int NP = 1; };   // c0
 
@@ -150,6 +156,16 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
             if constexpr (AMODE == A_DENSE) {
                 a_base[j] = (long long)m * g.lda;
                 a_ih0[j] = 0; a_iw0[j] = 0;
+            } else if constexpr (AMODE == A_CONV4) {
+                // padded multi-copy image: row start of this output pixel
+                const int mm = a_ok[j] ? m : 0;
+                const int img = mm / sp_out, s = mm - img * sp_out;
+                const int oh = s / g.oW, ow = s - oh * g.oW;
+                const int pix0 = ow * g.sW;
+                const int r = pix0 & 3;
+                a_base[j] = (long long)(r >> g.copy_shift) * g.copy_stride +
+                            (((long long)img * g.H + (long long)oh * g.sH) * g.W + (pix0 - r)) * 4;
+                a_ih0[j] = 0; a_iw0[j] = 0;
             } else {
                 const int mm = a_ok[j] ? m : 0;
                 const int img = mm / sp_out, s = mm - img * sp_out;
@@ -177,6 +193,13 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
             const uint8_t* src = pad16;
             if constexpr (AMODE == A_DENSE) {
                 if (a_ok[j] && kk < g.K) src = p_a + a_base[j] + kk;
+            } else if constexpr (AMODE == A_CONV4) {
+                // chunk = 4 taps (kw0..kw0+3) x 4 channels of kernel row kh
+                const int q = kk >> 4;
+                const int cpr = g.kWp >> 2;
+                const int kh = q / cpr;
+                const int kw0 = (q - kh * cpr) << 2;
+                if (a_ok[j] && kh < g.kH) src = p_a + a_base[j] + ((long long)kh * g.W + kw0) * 4;
             } else {
                 if (a_ok[j] && kc_kh < g.kH) {
                     const int ih = a_ih0[j] + kc_kh * g.dH;
@@ -289,6 +312,9 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
                         else if constexpr (EPI == EPI_RQA)
                             b = rqa_fast(v, __int_as_float(p0[tn][q]), __int_as_float(p1[tn][q]),
                                          g.inv_y, g.y_zp, g.L, g.hi);
+                        else if constexpr (EPI == EPI_RQC)
+                            b = rqc_fast(v, __int_as_float(p0[tn][q]), __int_as_float(p1[tn][q]),
+                                         g.inv_y, g.y_zp, g.L, g.hi);
                         else
                             b = rqd_fast(v, g.cm, g.y_zp, g.lo, g.hi);
                         w |= (b & 0xffu) << (8 * q);
@@ -398,14 +424,30 @@ hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
     }
 }
 
+// first layer: RQ-C only
+template <int BM, int BN, int S>
+hipError_t launch_dma_first(const GemmArgs& g, int batch, hipStream_t s) {
+    switch (g.epi) {
+    case EPI_RQC: return launch_dma<BM, BN, S, A_CONV4, EPI_RQC>(g, batch, s);
+    default: return hipErrorNotSupported;
+    }
+}
+
 }  // namespace
 
 bool qgemm_dma_eligible(const GemmArgs& g, int vec) {
-    if (vec != 16 || g.kWp > 0 || g.y_nchw) return false;
+    if (g.y_nchw) return false;
+    if (g.kWp > 0) {
+        // first layer: only on the padded multi-copy image
+        if (g.copy_stride <= 0 || (g.copy_stride & 15) || (g.W & 3) || (g.kWp & 3)) return false;
+        if (g.epi != EPI_RQC || g.c0 == nullptr || g.rowsum != nullptr || g.tail != TAIL_NONE) return false;
+        return g.Np >= 4 && (g.Np & 3) == 0;
+    }
+    if (vec != 16) return false;
     if (g.c0 == nullptr || g.alpha_zp_dev != nullptr || g.rowsum != nullptr) return false;
     if (g.tail != TAIL_NONE) return false;
     if (g.epi == EPI_RQB && g.bprime_from < g.N) return false;
-    if (g.epi == EPI_RQC) return false;
+    if (g.epi == EPI_RQC) return false;   // RQ-C is the first layer's epilogue
     if (g.epi == EPI_RQD && g.cm_a_scale_dev != nullptr) return false;
     if (g.Np < 4 || (g.Np & 3)) return false;
     if (g.H > 0 && (g.C % 16 || g.Cs % 16)) return false;
@@ -415,6 +457,14 @@ bool qgemm_dma_eligible(const GemmArgs& g, int vec) {
 
 hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t s) {
     const bool conv = g.H > 0;
+    if (g.kWp > 0) {
+        switch (tile) {
+        case TILE_128x128: return launch_dma_first<128, 128, 4>(g, batch, s);
+        case TILE_256x64: return launch_dma_first<256, 64, 3>(g, batch, s);
+        case TILE_64x256: return launch_dma_first<64, 256, 3>(g, batch, s);
+        default: return hipErrorInvalidValue;
+        }
+    }
     switch (tile) {
     case TILE_128x128:
         return conv ? launch_dma_epi<128, 128, 4, A_CONV>(g, batch, s)

@@ -166,6 +166,12 @@ CONV_CASES = [
     ("dma_s2_3x3", 4, 128, 28, 28, 128, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1,
                                                 x_nhwc=1)),
     ("dma_grouped_c16", 1, 64, 8, 8, 64, 3, dict(group=4, pads=(1, 1, 1, 1))),
+    # first layer on the padded multi-copy image: strides 2, 3 (4 copies), 4
+    # (1 copy), 4 input channels
+    ("first_mbv2_stem", 2, 3, 32, 32, 32, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1)),
+    ("first_s3", 1, 3, 33, 30, 32, 3, dict(stride=(3, 3), pads=(1, 1, 1, 1), y_nhwc=1, post_fn=1,
+                                          y_zp=6)),
+    ("first_s4_c4", 1, 4, 17, 19, 16, 3, dict(stride=(4, 4), y_nhwc=1, y_zp=1)),
 ]
 
 
