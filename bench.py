@@ -181,7 +181,9 @@ def run_resnet50(args, dev):
     s.enable_profiling(False)
     kprof = profile_steps(s.run, args)
     conv_ops = sum(r["ops"] for r in prof if r["op"] == "QLinearConv")
-    g_launches, g_ms = kprof["qgemm"]
+    # the conv GEMM kernel, with or without a fused residual add
+    g_launches = sum(kprof[k][0] for k in ("qgemm", "qgemm_add") if k in kprof)
+    g_ms = sum(kprof[k][1] for k in ("qgemm", "qgemm_add") if k in kprof)
     qgemm_ms_per_step = g_ms / args.steps
     layers = []
     for r in prof:
@@ -204,8 +206,9 @@ def run_resnet50(args, dev):
     ops_per_launch = conv_ops / (g_launches / args.steps)
     conv_bytes = sum(r["bytes"] for r in prof if r["op"] == "QLinearConv")
     rl = roofline(ops_per_launch, conv_bytes / (g_launches / args.steps), avg_launch, kprof)
-    rl["note"] = ("achieved = total algorithmic conv ops of one step / total qgemm_kernel time "
-                  "of one step (53 launches, hipEvents per launch)")
+    rl["note"] = ("achieved = total algorithmic conv ops of one step / total time of the conv "
+                  "GEMM kernels of one step (53 launches, 16 with the residual add fused; "
+                  "hipEvents per launch)")
     # cpu baseline: the oracle replays the plan on one image
     nthr = host_threads()
     O.set_threads(nthr)
@@ -222,8 +225,9 @@ def run_resnet50(args, dev):
         metric=METRIC, value=round(imgs, 1), unit="images/s", ms_per_step=ms,
         config={"workload": f"cfg3 ResNet-50 v1.5 int8 QDQ, batch {B}, 224x224 (53 QLinearConv, "
                             "16 QLinearAdd, uint8 MaxPool, fp32 GAP+FC)", "global_batch": B,
-                "branches": {b: sum(1 for p in plan if p["variant"] == b)
+                "branches": {b: sum(1 for p in plan if p["variant"].split("+")[0] == b)
                              for b in ("FIRST", "NR16", "PACKED")},
+                "adds_fused_into_conv": s.fusion_stat("conv_add"),
                 "conv_tops": round(conv_ops / (qgemm_ms_per_step * 1e-3) / 1e12, 1),
                 "device_bytes": s.device_bytes()},
         roofline=rl,

@@ -118,6 +118,26 @@ int nnrh_qconv_branch(nnrh_qconv_t h, int* branch);
 int nnrh_qconv_run(nnrh_qconv_t h, const void* x_dev, void* y_dev, void* stream);
 int nnrh_qconv_destroy(nnrh_qconv_t h);
 
+/* QLinearConv followed by a same-shape QLinearAdd of its output, in one
+ * kernel. No counterpart in the reference, which never fuses a binary Add
+ * into a conv (src/graph_optimizer/fuse_post_ops.cpp:67); the result is
+ * identical to nnrh_qconv_run then nnrh_qlinear_add(kind 0): the conv byte
+ * and the other operand go through QLinearAdd's RQ-E body / scalar-tail
+ * expressions (src/backend/cpu/QLinearAdd.cpp:66-104) with the same element
+ * split. conv_is_a: 1 when the conv output is the add's input A. Available
+ * for the RQ-B branches (PACKED, NR16) with group 1, NHWC output and
+ * channels % 16 == 0; otherwise returns NNRH_ERR_UNSUPPORTED and leaves the
+ * handle unchanged. After a successful call, run with nnrh_qconv_run_add. */
+typedef struct nnrh_qadd_fuse_desc {
+    int conv_is_a;
+    float a_scale; int a_zp;
+    float b_scale; int b_zp;
+    float y_scale; int y_zp;
+} nnrh_qadd_fuse_desc;
+int nnrh_qconv_fuse_add(nnrh_qconv_t h, const nnrh_qadd_fuse_desc* d);
+int nnrh_qconv_run_add(nnrh_qconv_t h, const void* x_dev, const void* other_dev,
+                       void* y_dev, void* stream);
+
 /* ---- QLinearMatMul ------------------------------------------------------
  * Replaces QLinearMatMul_operator (src/backend/cpu/QLinearMatMul.cpp:14-233)
  * for a constant B: reshape() pre-pack (:75-91), exec() (:111-232).

@@ -33,6 +33,9 @@ int nnr_ctx_create(nnr_ctx_t* ctx, int preferred_backend);
 int nnr_ctx_destroy(nnr_ctx_t ctx);
 int nnr_ctx_set_stream(nnr_ctx_t ctx, void* stream);
 int nnr_ctx_set_fusion(nnr_ctx_t ctx, int on);
+/* fuse_conv_add (default on, needs fusion on): same-shape QLinearAdds run in
+ * the epilogue of the QLinearConv producing one operand; results unchanged. */
+int nnr_ctx_set_conv_add(nnr_ctx_t ctx, int on);
 
 /* dtype: ONNX TensorProto element type (1 float, 2 uint8, 3 int8, 6 int32, 7 int64, 10 f16) */
 int nnr_ctx_add_initializer(nnr_ctx_t ctx, const char* name, int dtype, const int* dims,
@@ -63,6 +66,12 @@ int nnr_ctx_node_count(nnr_ctx_t ctx, int* n);
 int nnr_ctx_node_info(nnr_ctx_t ctx, int i, const char** op_type, const char** name,
                       const char** variant, int* post_fn, int* n_in, int* n_out);
 int nnr_ctx_node_io(nnr_ctx_t ctx, int i, int is_output, int j, const char** tensor_name);
+/* Same-shape QLinearAdd folded into active node i's kernel (fuse_conv_add,
+ * no counterpart in the reference). j = -1: the add node's name; j = -2: the
+ * operand the conv reads besides its input; j = 0..7: the add's inputs
+ * (slot 0 or 3 is the conv result, which no longer exists as a tensor).
+ * "" when nothing was folded into node i. */
+int nnr_ctx_node_fused_add(nnr_ctx_t ctx, int i, int j, const char** tensor_name);
 int nnr_ctx_fusion_stat(nnr_ctx_t ctx, const char* key, int* value);
 size_t nnr_ctx_device_bytes(nnr_ctx_t ctx);
 

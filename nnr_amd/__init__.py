@@ -13,7 +13,8 @@ import ctypes as ct
 
 import numpy as np
 
-from ._lib import (BRANCH_NAMES, F16, F32, I32, S8, U8, NnrHipError, QConvDesc,  # noqa: F401
+from ._lib import (BRANCH_NAMES, F16, F32, I32, NNRH_ERR_UNSUPPORTED, S8, U8, NnrHipError,  # noqa: F401
+                   QConvDesc,
                    QMatMulDesc, check, cur_stream, lib, ptr)
 
 __all__ = ["QLinearConv", "QLinearMatMul", "MatMulInteger", "quantize_linear",
@@ -85,6 +86,31 @@ class QLinearConv:
                             else torch.int8, device=x.device)
         check(lib().nnrh_qconv_run(self.h, ptr(x), ptr(y),
                                    cur_stream() if stream is None else stream))
+        return y
+
+    def fuse_add(self, conv_is_a, a_scale, a_zp, b_scale, b_zp, y_scale, y_zp):
+        """Fuse a same-shape QLinearAdd of this conv's output into its kernel.
+        Returns False (handle unchanged) when this conv's kernel cannot."""
+        from ._lib import QAddFuseDesc
+        d = QAddFuseDesc(int(bool(conv_is_a)), a_scale, a_zp, b_scale, b_zp, y_scale, y_zp)
+        rc = lib().nnrh_qconv_fuse_add(self.h, ct.byref(d))
+        if rc == 0:
+            return True
+        if rc == NNRH_ERR_UNSUPPORTED:
+            return False
+        check(rc)
+
+    def run_add(self, x, other, y=None, stream=None):
+        """Conv then QLinearAdd with `other` (same layout and shape as y)."""
+        import torch
+        if tuple(x.shape) != self.in_shape or not x.is_contiguous():
+            raise ValueError(f"x shape {tuple(x.shape)} != {self.in_shape} or not contiguous")
+        if tuple(other.shape) != self.out_shape or not other.is_contiguous():
+            raise ValueError(f"other shape {tuple(other.shape)} != {self.out_shape}")
+        if y is None:
+            y = torch.empty(self.out_shape, dtype=other.dtype, device=x.device)
+        check(lib().nnrh_qconv_run_add(self.h, ptr(x), ptr(other), ptr(y),
+                                       cur_stream() if stream is None else stream))
         return y
 
     def __del__(self):

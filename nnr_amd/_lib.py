@@ -25,7 +25,7 @@ EXPORTS = [
     "nnrh_event_create", "nnrh_event_destroy", "nnrh_event_record", "nnrh_event_elapsed_ms",
     "nnrh_profile_enable", "nnrh_profile_reset", "nnrh_profile_count", "nnrh_profile_get",
     "nnrh_qconv_dispatch", "nnrh_qconv_create", "nnrh_qconv_branch", "nnrh_qconv_run",
-    "nnrh_qconv_destroy", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
+    "nnrh_qconv_destroy", "nnrh_qconv_fuse_add", "nnrh_qconv_run_add", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
     "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
     "nnrh_dynamic_quantize_linear", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
@@ -37,6 +37,12 @@ class NnrHipError(RuntimeError):
     def __init__(self, rc: int, msg: str):
         super().__init__(f"nnrh error {rc}: {msg}")
         self.rc = rc
+
+
+class QAddFuseDesc(C.Structure):
+    _fields_ = [("conv_is_a", C.c_int), ("a_scale", C.c_float), ("a_zp", C.c_int),
+                ("b_scale", C.c_float), ("b_zp", C.c_int), ("y_scale", C.c_float),
+                ("y_zp", C.c_int)]
 
 
 class QConvDesc(C.Structure):
@@ -99,6 +105,8 @@ def lib():
         "nnrh_qconv_branch": (i, [vp, P(i)]),
         "nnrh_qconv_run": (i, [vp, vp, vp, vp]),
         "nnrh_qconv_destroy": (i, [vp]),
+        "nnrh_qconv_fuse_add": (i, [vp, P(QAddFuseDesc)]),
+        "nnrh_qconv_run_add": (i, [vp, vp, vp, vp, vp]),
         "nnrh_qmatmul_create": (i, [P(vp), P(QMatMulDesc)]),
         "nnrh_qmatmul_run": (i, [vp, vp, ll, vp, i, vp, vp, vp]),
         "nnrh_qmatmul_destroy": (i, [vp]),

@@ -339,6 +339,7 @@ struct nnrh_qconv {
     nnrh_qconv_desc d{};
     int branch = 0;
     bool use_dw = false;         // depthwise VALU kernel
+    bool fused_add = false;      // nnrh_qconv_fuse_add was called
     int transform = 0;           // 0 none, 1 NCHW->NHWC, 2 NCHW->NHWC padded to 4 ch,
                                  // 3 first-layer padded multi-copy NHWC4 image
     int Cx = 0;                  // channels of the tensor the kernel reads
@@ -632,6 +633,63 @@ extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stre
     if (vec > 1 && ((uintptr_t)src & (vec - 1))) vec = 1;
     ProfScope ps("qgemm", s);
     HIP_TRY(launch_qgemm(g, h->groups, h->tile, vec, s), "qgemm");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qconv_fuse_add(nnrh_qconv_t h, const nnrh_qadd_fuse_desc* a) {
+    if (!h || !a) return set_err(NNRH_ERR_INVALID, "qconv_fuse_add: NULL argument");
+    const nnrh_qconv_desc& d = h->d;
+    GemmArgs g = h->g;
+    const bool rqb = h->branch == NNRH_BR_PACKED || h->branch == NNRH_BR_NR16;
+    if (h->use_dw || h->transform == 3 || h->groups != 1 || !d.y_nhwc || !rqb || g.ldy != g.N ||
+        !qgemm_dma_eligible(g, h->vec))
+        return set_err(NNRH_ERR_UNSUPPORTED, "qconv_fuse_add: this convolution's kernel has no fused add");
+    // QLinearAdd.cpp:46-47,66-67 (no contraction), as nnrh_qlinear_add
+    g.add_sa = a->a_scale / a->y_scale;
+    g.add_sb = a->b_scale / a->y_scale;
+    {
+        float t1 = g.add_sa * (float)a->a_zp, t2 = g.add_sb * (float)a->b_zp;
+        g.add_fixed = (float)a->y_zp - (t1 + t2);
+    }
+    g.add_a_zp = a->a_zp; g.add_b_zp = a->b_zp; g.add_y_zp = a->y_zp;
+    // the kernel's body path needs |fma(a,sa,fma(b,sb,fixed))| < 2^22 for
+    // every byte pair (then clamp-then-round is exact); otherwise no fusion
+    {
+        const double amax = d.act_dtype == NNRH_U8 ? 255.0 : 128.0;
+        const double bound = amax * (std::fabs((double)g.add_sa) + std::fabs((double)g.add_sb)) +
+                             std::fabs((double)g.add_fixed) + 2.0;
+        if (!(bound < 4194304.0))
+            return set_err(NNRH_ERR_UNSUPPORTED, "qconv_fuse_add: add scales out of the fused range");
+    }
+    g.add_conv_is_a = a->conv_is_a ? 1 : 0;
+    const long long n = (long long)d.N * d.oH * d.oW * d.OC;
+    g.add_body = n - n % 16;
+    h->g = g;
+    h->fused_add = true;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qconv_run_add(nnrh_qconv_t h, const void* x, const void* other, void* y, void* stream) {
+    if (!h || !x || !other || !y) return set_err(NNRH_ERR_INVALID, "qconv_run_add: NULL argument");
+    if (!h->fused_add) return set_err(NNRH_ERR_INVALID, "qconv_run_add: nnrh_qconv_fuse_add was not called");
+    const nnrh_qconv_desc& d = h->d;
+    hipStream_t s = S(stream);
+    const uint8_t* src = (const uint8_t*)x;
+    if (h->transform) {
+        ProfScope ps("nchw_to_nhwc_u8", s);
+        HIP_TRY(launch_nchw_to_nhwc_u8(src, h->xs, d.N, d.C, d.H * d.W, h->Cx,
+                                       (uint8_t)(d.x_zp & 0xff), s),
+                "nchw_to_nhwc");
+        src = h->xs;
+    }
+    if (((uintptr_t)src & 15) != 0)
+        return set_err(NNRH_ERR_INVALID, "qconv_run_add: input must be 16-byte aligned");
+    GemmArgs g = h->g;
+    g.a = src;
+    g.y = y;
+    g.add_other = (const uint8_t*)other;
+    ProfScope ps("qgemm_add", s);
+    HIP_TRY(launch_qgemm(g, 1, h->tile, h->vec, s), "qgemm_add");
     return NNRH_OK;
 }
 

@@ -95,6 +95,15 @@ struct GemmArgs {
     // padded height / row length and the pads are already applied
     int copy_shift;
     long long copy_stride;  // bytes per copy
+    // QLinearAdd (same shape) fused into the RQ-B epilogue: the conv byte q
+    // and the residual byte r of the same NHWC element are A and B of the
+    // add (or B and A), requantized with RQ-E. Flat element index >=
+    // add_body takes the scalar-tail expression.
+    const uint8_t* add_other;   // NULL: no fused add
+    int add_conv_is_a;
+    float add_sa, add_sb, add_fixed;
+    int add_a_zp, add_b_zp, add_y_zp;
+    long long add_body;
 };
 
 // Tile shapes available to the launcher (BM x BN, 256 threads).

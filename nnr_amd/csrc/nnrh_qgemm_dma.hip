@@ -80,7 +80,22 @@ template <> struct EpiParams<EPI_I32> { static constexpr int NP = 1; };   // c0
 
 }  // namespace
 
-template <int BM, int BN, int S, int AMODE, int EPI>
+// RQ-E of QLinearAdd (QLinearAdd.cpp:79-104) on one element: body is the
+// 16-wide SIMD expression, tail the scalar one
+__device__ __forceinline__ int qadd_elem(int a, int b, const GemmArgs& g, bool tail) {
+    float v;
+    if (!tail) {
+        v = __builtin_fmaf((float)b, g.add_sb, g.add_fixed);
+        v = __builtin_fmaf((float)a, g.add_sa, v);
+    } else {
+        const float t1 = g.add_sa * (float)(a - g.add_a_zp);
+        const float t2 = g.add_sb * (float)(b - g.add_b_zp);
+        v = (t1 + t2) + (float)g.add_y_zp;
+    }
+    return clampi(x86_f2i(__builtin_rintf(v)), g.lo, g.hi);
+}
+
+template <int BM, int BN, int S, int AMODE, int EPI, bool FADD>
 __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
     constexpr int WAVES_N = BN / 64;
     static_assert((BM / 64) * WAVES_N == 4, "4 waves of 64x64");
@@ -259,6 +274,31 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
+    // fused add: residual bytes of this lane's 4 rows x 16 channels. They
+    // are loaded one tile ahead (at the first K-step of the previous tile,
+    // before that step's DMA issue), so the epilogue's wait for them only
+    // covers loads the pipeline needs by then anyway.
+    v4i rcur[4], rnext[4];
+    auto load_residual = [&](int t, v4i* rr) {
+        const int m0 = (t / nbn) * BM;   // batch 1 (checked by the launcher)
+        const int nb = (t % nbn) * BN + wn * 64 + 16 * fchunk;
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+            rr[tm] = v4i{0, 0, 0, 0};
+            const int m = m0 + wm * 64 + tm * 16 + frow;
+            if (m >= g.M || nb >= g.N) continue;
+            const uint8_t* rp = g.add_other + (long long)m * g.ldy + nb;
+            if (nb + 16 <= g.N && ((((uintptr_t)rp) & 15) == 0)) {
+                rr[tm] = *(const v4i*)rp;
+            } else {
+                uint32_t w[4] = {0u, 0u, 0u, 0u};
+                for (int i = 0; i < 16; ++i)
+                    if (nb + i < g.N) w[i >> 2] |= (uint32_t)rp[i] << (8 * (i & 3));
+                rr[tm] = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+            }
+        }
+    };
+
     auto epilogue = [&]() {
         const int z = c_t / per_z;
         const int r = c_t - z * per_z;
@@ -321,6 +361,57 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
                     }
                     packed[tn] = w;
                 }
+                if constexpr (FADD) {
+                    const bool sgn = g.y_type == 1;
+                    const long long i0 = (long long)m * g.ldy + nb;
+                    if (i0 + 16 <= g.add_body) {
+                        // RQ-E body; |v| < 2^22 is checked on the host, so
+                        // clamp-then-round equals the reference's rint, cvt,
+                        // saturate, and rne_bits is exact
+                        const float lo_f = (float)g.lo, hi_f = (float)g.hi;
+#pragma unroll
+                        for (int tn = 0; tn < 4; ++tn) {
+                            const uint32_t qw = packed[tn], rw = (uint32_t)rcur[tm][tn];
+                            uint32_t w = 0;
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                float qf, rf;
+                                if (sgn) {
+                                    qf = (float)(int)(int8_t)(qw >> (8 * q));
+                                    rf = (float)(int)(int8_t)(rw >> (8 * q));
+                                } else {
+                                    qf = (float)((qw >> (8 * q)) & 0xffu);
+                                    rf = (float)((rw >> (8 * q)) & 0xffu);
+                                }
+                                const float af = g.add_conv_is_a ? qf : rf;
+                                const float bf = g.add_conv_is_a ? rf : qf;
+                                float v = __builtin_fmaf(bf, g.add_sb, g.add_fixed);
+                                v = __builtin_fmaf(af, g.add_sa, v);
+                                v = med3f(v, lo_f, hi_f);
+                                w |= ((uint32_t)rne_bits(v) & 0xffu) << (8 * q);
+                            }
+                            packed[tn] = w;
+                        }
+                    } else {
+                        // the row segment reaches the scalar tail
+#pragma unroll
+                        for (int tn = 0; tn < 4; ++tn) {
+                            uint32_t w = 0;
+                            const uint32_t rw = (uint32_t)rcur[tm][tn];
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                int qc = (int)((packed[tn] >> (8 * q)) & 0xffu);
+                                int rv = (int)((rw >> (8 * q)) & 0xffu);
+                                if (sgn) { qc = (int)(int8_t)qc; rv = (int)(int8_t)rv; }
+                                const int a = g.add_conv_is_a ? qc : rv;
+                                const int b = g.add_conv_is_a ? rv : qc;
+                                const int o = qadd_elem(a, b, g, i0 + 4 * tn + q >= g.add_body);
+                                w |= (uint32_t)(o & 0xff) << (8 * q);
+                            }
+                            packed[tn] = w;
+                        }
+                    }
+                }
                 uint8_t* yrow = (uint8_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
                 if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
                     *(v4i*)yrow = v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
@@ -334,6 +425,7 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
     };
 
     // ---- prologue: S-1 steps in flight
+    if constexpr (FADD) load_residual(t_first, rcur);
     p_setup(p_t);
 #pragma unroll
     for (int s = 0; s < S - 1; ++s)
@@ -348,6 +440,9 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
         // every wave's DMAs of the step have landed; every wave is done
         // reading the stage (and param slot) the next issue overwrites
         block_barrier();
+        if constexpr (FADD) {
+            if (c_kt == 0 && c_t + t_step < t_end) load_residual(c_t + t_step, rnext);
+        }
         if (p_t < t_end) p_issue();
 
         const uint8_t* st = lds + (c_gs % S) * STAGE;
@@ -369,6 +464,10 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
         ++c_gs;
         if (++c_kt == nk) {
             epilogue();
+            if constexpr (FADD) {
+#pragma unroll
+                for (int tm = 0; tm < 4; ++tm) rcur[tm] = rnext[tm];
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -385,25 +484,22 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
 
 namespace {
 
-template <typename KernelT>
-int dma_resident_blocks(KernelT kernel) {
-    static int cached = 0;
-    if (cached > 0) return cached;
-    int per_cu = 0, dev = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu < 1)
-        per_cu = 1;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-        cus = 256;
-    cached = per_cu * cus;
-    return cached;
-}
-
-template <int BM, int BN, int S, int AMODE, int EPI>
+template <int BM, int BN, int S, int AMODE, int EPI, bool FADD = false>
 hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
-    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI>;
+    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI, FADD>;
     const long long tiles = (long long)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN) * batch;
-    long long cap = dma_resident_blocks(kern);
+    // resident blocks of this instantiation (occupancy x CUs), computed once
+    static int resident = 0;
+    if (resident <= 0) {
+        int per_cu = 0, dev = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) != hipSuccess || per_cu < 1)
+            per_cu = 1;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        resident = per_cu * cus;
+    }
+    long long cap = resident;
     cap = cap < 8 ? 8 : (cap & ~7LL);
     const int G = (int)(tiles < cap ? tiles : cap);
     if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
@@ -415,6 +511,12 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
 
 template <int BM, int BN, int S, int AMODE>
 hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
+    if (g.add_other) {
+        if constexpr (AMODE == A_CONV) {
+            if (g.epi == EPI_RQB && batch == 1) return launch_dma<BM, BN, S, AMODE, EPI_RQB, true>(g, batch, s);
+        }
+        return hipErrorNotSupported;
+    }
     switch (g.epi) {
     case EPI_RQB: return launch_dma<BM, BN, S, AMODE, EPI_RQB>(g, batch, s);
     case EPI_RQA: return launch_dma<BM, BN, S, AMODE, EPI_RQA>(g, batch, s);

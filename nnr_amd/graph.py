@@ -42,6 +42,7 @@ def host_lib():
             "nnr_ctx_destroy": (i, [vp]),
             "nnr_ctx_set_stream": (i, [vp, vp]),
             "nnr_ctx_set_fusion": (i, [vp, i]),
+            "nnr_ctx_set_conv_add": (i, [vp, i]),
             "nnr_ctx_add_initializer": (i, [vp, cp, i, P(i), i, vp]),
             "nnr_ctx_add_input": (i, [vp, cp, i, P(i), i]),
             "nnr_ctx_add_output": (i, [vp, cp]),
@@ -54,6 +55,7 @@ def host_lib():
             "nnr_ctx_node_count": (i, [vp, P(i)]),
             "nnr_ctx_node_info": (i, [vp, i, P(cp), P(cp), P(cp), P(i), P(i), P(i)]),
             "nnr_ctx_node_io": (i, [vp, i, i, i, P(cp)]),
+            "nnr_ctx_node_fused_add": (i, [vp, i, i, P(cp)]),
             "nnr_ctx_fusion_stat": (i, [vp, cp, P(i)]),
             "nnr_ctx_device_bytes": (C.c_size_t, [vp]),
             "nnr_ctx_enable_profiling": (i, [vp, i]),
@@ -143,7 +145,7 @@ def _attr_arrays(attrs: dict):
 class Session:
     """A prepared C++ context_t for `graph` with the HIP backend preferred."""
 
-    def __init__(self, graph: Graph, stream=None, fusion=True, device=True):
+    def __init__(self, graph: Graph, stream=None, fusion=True, device=True, conv_add=True):
         L = host_lib()
         self.L = L
         self.graph = graph
@@ -154,6 +156,7 @@ class Session:
             stream = _lib.cur_stream()
         _chk(L.nnr_ctx_set_stream(h, stream))
         _chk(L.nnr_ctx_set_fusion(h, 1 if fusion else 0))
+        _chk(L.nnr_ctx_set_conv_add(h, 1 if conv_add else 0))
         for name, arr in graph.initializers.items():
             dims = (C.c_int * max(1, arr.ndim))(*arr.shape)
             _chk(L.nnr_ctx_add_initializer(h, name.encode(), ONNX_DT[arr.dtype], dims, arr.ndim,
@@ -227,8 +230,15 @@ class Session:
                     _chk(L.nnr_ctx_node_io(self.h, i, is_out, j, C.byref(s)))
                     lst.append(s.value.decode())
                 ios.append(lst)
+            def fused(j):
+                s = C.c_char_p()
+                _chk(L.nnr_ctx_node_fused_add(self.h, i, j, C.byref(s)))
+                return s.value.decode()
+            fadd = None
+            if fused(-1):
+                fadd = dict(name=fused(-1), other=fused(-2), inputs=[fused(j) for j in range(8)])
             out.append(dict(op=op.value.decode(), name=nm.value.decode(), variant=var.value.decode(),
-                            post_fn=pf.value, inputs=ios[0], outputs=ios[1]))
+                            post_fn=pf.value, inputs=ios[0], outputs=ios[1], fused_add=fadd))
         return out
 
     def fusion_stat(self, key):

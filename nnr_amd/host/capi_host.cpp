@@ -57,6 +57,12 @@ int nnr_ctx_set_fusion(nnr_ctx_t c, int on) {
     return 0;
 }
 
+int nnr_ctx_set_conv_add(nnr_ctx_t c, int on) {
+    if (!c) return err("ctx is NULL");
+    c->ctx.enable_conv_add = on != 0;
+    return 0;
+}
+
 int nnr_ctx_add_initializer(nnr_ctx_t c, const char* name, int dtype, const int* dims, int ndim,
                             const void* data) {
     if (!c || !name || (ndim && !dims) || !data) return err("add_initializer: NULL argument");
@@ -168,6 +174,24 @@ int nnr_ctx_node_io(nnr_ctx_t c, int i, int is_out, int j, const char** tname) {
     auto& v = is_out ? c->plan[i]->outputs : c->plan[i]->inputs;
     if (j < 0 || j >= (int)v.size()) return err("node_io: bad slot");
     *tname = v[j] ? v[j]->name.c_str() : "";
+    return 0;
+}
+
+int nnr_ctx_node_fused_add(nnr_ctx_t c, int i, int j, const char** name) {
+    if (!c || i < 0 || i >= (int)c->plan.size() || !name) return err("node_fused_add: bad index");
+    operator_t* op = c->plan[i];
+    *name = "";
+    if (!op->fused_add) return 0;
+    if (j == -1) {
+        *name = op->fused_add->node_name.c_str();
+    } else if (j == -2) {
+        *name = op->fused_other ? op->fused_other->name.c_str() : "";
+    } else if (j >= 0 && j < (int)op->fused_add->inputs.size()) {
+        tensor_t* t = op->fused_add->inputs[j];
+        *name = t ? t->name.c_str() : "";
+    } else {
+        return err("node_fused_add: bad slot");
+    }
     return 0;
 }
 

@@ -115,6 +115,13 @@ struct operator_t {
     bool fusable_unary = false;   // set in init() by Relu / Clip
     bool post_fn = false;
     operator_t* fused_op = nullptr;
+    // a same-shape QLinearAdd folded into this operator's kernel
+    // (fuse_conv_add); the add node is skipped and its output is ours
+    operator_t* fused_add = nullptr;
+    tensor_t* fused_other = nullptr;
+    // accept `add` (whose input conv_side, 0 or 3, is this operator's output)
+    // into the kernel; false leaves everything unchanged
+    virtual bool fuse_residual_add(operator_t* /*add*/, int /*conv_side*/) { return false; }
 
     // attribute accessors
     const attr_t* find_attr(const std::string& name) const;
@@ -168,6 +175,7 @@ struct context_t {
     backend_t preferred_backend = backend_t::HIP;
     void* stream = nullptr;       // hipStream_t of every launch
     bool enable_fusion = true;
+    bool enable_conv_add = true;  // fuse_conv_add after the operators are built
     bool enable_profiling = false;
     bool shape_only = false;      // reshape() computes shapes only (pre-layout pass)
 
@@ -198,6 +206,7 @@ void fuse_qdq_compute(context_t* ctx);
 void fuse_qdq(context_t* ctx);
 void fuse_post_ops(context_t* ctx);
 void assign_layouts(context_t* ctx);
+void fuse_conv_add(context_t* ctx);
 
 // operator creation through the registry (src/backend/cpu/solve_operator.cpp:29-33)
 operator_t* solve_operator(const std::string& op_type, int opset, backend_t preferred);

@@ -215,7 +215,27 @@ struct QLinearConv_hip : operator_t {
         return true;
     }
     bool exec() override {
+        if (fused_add)
+            return ok(this, nnrh_qconv_run_add(h, inputs[0]->data, fused_other->data, outputs[0]->data,
+                                               ctx->stream));
         return ok(this, nnrh_qconv_run(h, inputs[0]->data, outputs[0]->data, ctx->stream));
+    }
+    bool fuse_residual_add(operator_t* add, int conv_side) override {
+        if (!h || add->inputs.size() != 8) return false;
+        for (int i : {1, 2, 4, 5, 6, 7})
+            if (add->inputs[i] && add->inputs[i]->ndata && !add->inputs[i]->has_host()) return false;
+        tensor_t* y = outputs[0];
+        tensor_t* ay = add->outputs[0];
+        if (!ay || ay->dims != y->dims || ay->type != y->type || ay->format != y->format) return false;
+        nnrh_qadd_fuse_desc fd{};
+        fd.conv_is_a = conv_side == 0;
+        fd.a_scale = add->inputs[1]->scalar_f32();
+        fd.a_zp = zp_value(add->inputs[2]);
+        fd.b_scale = add->inputs[4]->scalar_f32();
+        fd.b_zp = zp_value(add->inputs[5]);
+        fd.y_scale = add->inputs[6]->scalar_f32();
+        fd.y_zp = zp_value(add->inputs[7]);
+        return nnrh_qconv_fuse_add(h, &fd) == NNRH_OK;
     }
     double num_ops() const override {
         const tensor_t *w = inputs[3], *y = outputs[0];
@@ -225,11 +245,13 @@ struct QLinearConv_hip : operator_t {
     }
     double num_bytes() const override {
         const tensor_t *x = inputs[0], *w = inputs[3], *y = outputs[0];
-        return (double)x->nbytes() + (double)y->nbytes() + (double)w->nbytes() + 8.0 * w->dims[0];
+        double other = fused_other ? (double)fused_other->nbytes() : 0.0;
+        return (double)x->nbytes() + (double)y->nbytes() + (double)w->nbytes() + 8.0 * w->dims[0] + other;
     }
     std::string variant() const override {
         static const char* names[] = {"?", "DW", "FIRST", "DIRECT", "PACKED", "NR16", "IM2COL_S1", "IM2COL", "FLOAT"};
-        return branch >= 0 && branch <= 8 ? names[branch] : "?";
+        std::string v = branch >= 0 && branch <= 8 ? names[branch] : "?";
+        return fused_add ? v + "+Add" : v;
     }
 };
 

@@ -6,6 +6,10 @@
 //   fuse_post_ops     src/graph_optimizer/fuse_post_ops.cpp:10-73
 //   assign_layouts    src/graph_optimizer/assign_layouts.cpp:84-360 (int8
 //                     chains: force-accepted NHWC, then propagation)
+//   fuse_conv_add     no counterpart (the reference never fuses a binary Add,
+//                     fuse_post_ops.cpp:67): a same-shape QLinearAdd whose
+//                     input is a QLinearConv's only use runs in that conv's
+//                     epilogue, with bit-identical results
 // The fused operators are created through the registry with the context's
 // preferred backend, exactly where the reference calls solve_operator.
 #include <cstdio>
@@ -427,6 +431,58 @@ void assign_layouts(context_t* ctx) {
         }
     }
     ctx->fusion_stats["nhwc_tensors"] = (int)nhwc.size();
+}
+
+// ---------------------------------------------------------------------------
+// Runs after every operator is built (the conv decides whether its kernel
+// can take the add). The residual operand must be produced before the conv
+// runs; when both add inputs are conv outputs, the later conv takes the add.
+void fuse_conv_add(context_t* ctx) {
+    auto& nodes = ctx->nodes;
+    const int n = (int)nodes.size();
+    std::unordered_map<tensor_t*, int> producer;
+    for (int i = 0; i < n; ++i) {
+        if (!active(nodes[i])) continue;
+        for (auto* t : nodes[i]->outputs)
+            if (t) producer[t] = i;
+    }
+    std::unordered_set<tensor_t*> graph_out;
+    for (auto& name : ctx->graph_outputs)
+        if (tensor_t* t = ctx->find(name)) graph_out.insert(t);
+    int fused = 0;
+    for (int i = 0; i < n; ++i) {
+        operator_t* add = nodes[i];
+        if (!active(add) || add->op_type != "QLinearAdd" || add->inputs.size() != 8) continue;
+        tensor_t *a = add->inputs[0], *b = add->inputs[3];
+        if (!a || !b || a->dims != b->dims || a->format != b->format) continue;
+        auto prod = [&](tensor_t* t) {
+            auto it = producer.find(t);
+            return it == producer.end() ? -1 : it->second;
+        };
+        const int pa = prod(a), pb = prod(b);
+        // try the later producer first: the other operand then already exists
+        int order[2][2] = {{pa, 0}, {pb, 3}};
+        if (pb > pa) { std::swap(order[0][0], order[1][0]); std::swap(order[0][1], order[1][1]); }
+        for (auto& o : order) {
+            const int pi = o[0], side = o[1];
+            if (pi < 0) continue;
+            operator_t* conv = nodes[pi];
+            tensor_t* t = side == 0 ? a : b;
+            tensor_t* other = side == 0 ? b : a;
+            if (conv->op_type != "QLinearConv" || conv->fused_add || conv->outputs.size() != 1) continue;
+            if (prod(other) >= pi) continue;
+            if (graph_out.count(t) || count_consumers(ctx, t, -1) != 1) continue;
+            if (!conv->fuse_residual_add(add, side)) continue;
+            conv->fused_add = add;
+            conv->fused_other = other;
+            conv->outputs[0] = add->outputs[0];
+            add->skip = true;
+            producer[add->outputs[0]] = pi;
+            ++fused;
+            break;
+        }
+    }
+    ctx->fusion_stats["conv_add"] = fused;
 }
 
 }  // namespace nnr

@@ -59,6 +59,15 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None):
                         bias=init[ins[8]] if len(ins) > 8 and ins[8] else None)
             y, br = cv.run(x, w)
             nd["oracle_branch"] = br
+            fa = nd.get("fused_add")
+            if fa:
+                # conv + QLinearAdd in one kernel: the conv result is the add
+                # operand that is not `other`, then the add runs as planned
+                ai = fa["inputs"]
+                env[ai[3] if ai[0] == fa["other"] else ai[0]] = y
+                y = O.qlinear_add(0, val(ai[0]), val(ai[3]), float(scal(ai[1])), int(scal(ai[2])),
+                                  float(scal(ai[4])), int(scal(ai[5])), float(scal(ai[6])),
+                                  int(scal(ai[7])))
         elif op == "QLinearMatMul":
             y = O.qlinear_matmul(val(ins[0]), float(scal(ins[1])), int(scal(ins[2])),
                                  init[ins[3]], float(scal(ins[4])), int(scal(ins[5])),

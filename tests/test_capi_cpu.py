@@ -30,6 +30,37 @@ def test_header_symbols_exported():
     assert sorted(_lib.EXPORTS) == syms
 
 
+def test_every_export_has_a_signature():
+    """ctypes passes Python ints as 32-bit C ints when a function has no
+    argtypes, which truncates device pointers: every exported entry point
+    must have its argument types declared."""
+    L = _lib.lib()
+    for s in _lib.EXPORTS:
+        assert getattr(L, s).argtypes is not None, s
+
+
+def test_host_export_signatures():
+    from nnr_amd import graph as G
+    txt = open(os.path.join(ROOT, "include", "nnr_host.h")).read()
+    L = G.host_lib()
+    for s in sorted(set(re.findall(r"\b(nnr_[a-z0-9_]+)\s*\(", txt))):
+        assert getattr(L, s).argtypes is not None, s
+
+
+def test_host_header_symbols_exported():
+    """Every nnr_ctx_* / nnr_* entry of include/nnr_host.h is exported by the
+    host framework library."""
+    import ctypes
+    from nnr_amd import graph as G
+    txt = open(os.path.join(ROOT, "include", "nnr_host.h")).read()
+    syms = sorted(set(re.findall(r"\b(nnr_[a-z0-9_]+)\s*\(", txt)))
+    assert len(syms) >= 15
+    L = G.host_lib()
+    for s in syms:
+        assert hasattr(L, s), s
+    assert isinstance(L, ctypes.CDLL)
+
+
 def test_version_and_errors():
     L = _lib.lib()
     assert b"gfx950" in L.nnrh_version()

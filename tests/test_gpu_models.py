@@ -12,8 +12,8 @@ from oracle import graph_oracle
 pytestmark = pytest.mark.gpu
 
 
-def check_graph(g, feeds, out_name, atol=1e-3):
-    s = G.Session(g)
+def check_graph(g, feeds, out_name, atol=1e-3, conv_add=True):
+    s = G.Session(g, conv_add=conv_add)
     for k, v in feeds.items():
         s.set_input(k, v)
     s.run()
@@ -43,7 +43,10 @@ def test_resnet50_b2_bitexact(dev):
     rng = np.random.default_rng(10)
     x = rng.random((2, 3, 224, 224), dtype=np.float32)
     plan, logits, n_int = check_graph(g, {"input": x}, "logits")
-    assert n_int == 53 + 16 + 1 + 1           # convs, adds, maxpool, input Q
+    # every residual add runs in the epilogue of the conv that produces it
+    fused = sum(1 for p in plan if p["fused_add"])
+    assert fused == 16
+    assert n_int == 53 + (16 - fused) + 1 + 1  # convs (+adds), maxpool, input Q
     assert logits.shape == (2, 1000) and np.isfinite(logits).all()
 
 
@@ -53,6 +56,17 @@ def test_resnet50_small_input(dev):
     rng = np.random.default_rng(12)
     x = rng.random((3, 3, 96, 96), dtype=np.float32)
     check_graph(g, {"input": x}, "logits")
+
+
+def test_resnet50_unfused_adds(dev):
+    """Without the conv+add epilogue fusion every conv and add output is a
+    tensor of its own; all of them are bit-exact too."""
+    g = synth.resnet50(batch=2, hw=64, seed=14)
+    rng = np.random.default_rng(15)
+    x = rng.random((2, 3, 64, 64), dtype=np.float32)
+    plan, _, n_int = check_graph(g, {"input": x}, "logits", conv_add=False)
+    assert not any(p["fused_add"] for p in plan)
+    assert n_int == 53 + 16 + 1 + 1
 
 
 def test_qconv_graph_config2(dev):

@@ -187,6 +187,51 @@ def test_qconv_no_bias(dev):
     run_conv_case(dev, 1, 64, 10, 10, 64, 3, seed=5, bias=False, pads=(1, 1, 1, 1), y_nhwc=1)
 
 
+FUSED_ADD_CASES = [
+    # name, N, C, H, W, OC, k, pads, conv_is_a
+    ("1x1_conv_a", 2, 64, 14, 15, 256, 1, (0, 0, 0, 0), 1),
+    # 63*72 elements: the last 8 take QLinearAdd's scalar-tail expression
+    ("3x3_conv_b_tail", 1, 64, 9, 7, 72, 3, (1, 1, 1, 1), 0),
+    ("persistent", 16, 64, 56, 56, 256, 1, (0, 0, 0, 0), 1),
+]
+
+
+@pytest.mark.parametrize("case", FUSED_ADD_CASES, ids=[c[0] for c in FUSED_ADD_CASES])
+def test_qconv_fused_add(dev, case):
+    """conv + same-shape QLinearAdd in one kernel == oracle conv, then oracle add."""
+    name, N, C, Hh, W, OC, k, pads, conv_is_a = case
+    rng = np.random.default_rng(sum(name.encode()))
+    x = rng.integers(0, 256, (N, Hh, W, C), dtype=np.uint8)
+    w = rng.integers(-127, 128, (OC, C, k, k), dtype=np.int8)
+    b = rng.integers(-4096, 4097, OC).astype(np.int32)
+    kw = dict(pads=pads, x_nhwc=1, y_nhwc=1, x_scale=0.02, x_zp=128, y_scale=0.05, y_zp=3,
+              w_scale=rng.uniform(0.001, 0.01, OC).astype(np.float32), bias=b)
+    conv_ref, _ = O.Conv(N, C, Hh, W, OC, k, k, **kw).run(x, w)
+    other = rng.integers(0, 256, conv_ref.shape, dtype=np.uint8)
+    # add: A, B scales / zps; the conv side's are independent of its y quant
+    sa, za, sb, zb, sy, zy = 0.041, 7, 0.023, 131, 0.06, 2
+    a_, b_ = (conv_ref, other) if conv_is_a else (other, conv_ref)
+    ref = O.qlinear_add(0, a_, b_, sa, za, sb, zb, sy, zy)
+    op = H.QLinearConv(N, C, Hh, W, w, **kw)
+    assert op.fuse_add(conv_is_a, sa, za, sb, zb, sy, zy)
+    y = to_np(op.run_add(to_dev(x, dev), to_dev(other, dev)))
+    mism = np.count_nonzero(y != ref)
+    assert mism == 0, f"{mism} of {y.size} differ"
+
+
+def test_qconv_fuse_add_unsupported(dev):
+    """Convolutions whose kernel has no fused add say so and stay usable."""
+    rng = np.random.default_rng(11)
+    x = rng.integers(0, 256, (1, 3, 20, 20), dtype=np.uint8)
+    w = rng.integers(-127, 128, (16, 3, 3, 3), dtype=np.int8)
+    kw = dict(pads=(1, 1, 1, 1), y_nhwc=1, x_scale=0.02, x_zp=128, y_scale=0.05, y_zp=0,
+              w_scale=np.full(16, 0.004, np.float32))
+    op = H.QLinearConv(1, 3, 20, 20, w, **kw)   # first-layer branch
+    assert not op.fuse_add(1, 0.05, 0, 0.05, 0, 0.05, 0)
+    ref, _ = O.Conv(1, 3, 20, 20, 16, 3, 3, **kw).run(x, w)
+    assert np.array_equal(to_np(op(to_dev(x, dev))), ref)
+
+
 # ---------------------------------------------------------------------------
 # element-wise
 
