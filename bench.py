@@ -100,6 +100,22 @@ def run_qconv(args, dev):
     )
 
 
+def measured_traffic(name):
+    """HBM bytes per launch of the dominant kernel, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes summarized under profiles/ (copy-kernel
+    calibrated); None when no summary exists for this workload."""
+    import re
+    if not name:
+        return None, None
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        txt = open(path).read()
+    except OSError:
+        return None, None
+    m = re.search(r"^hbm_bytes_per_launch: (\d+)$", txt, re.M)
+    return (int(m.group(1)), "profiles/" + name) if m else (None, None)
+
+
 def time_steps(fn, args) -> float:
     import torch
     for _ in range(args.warmup):
@@ -206,6 +222,8 @@ def run_resnet50(args, dev):
     ops_per_launch = conv_ops / (g_launches / args.steps)
     conv_bytes = sum(r["bytes"] for r in prof if r["op"] == "QLinearConv")
     rl = roofline(ops_per_launch, conv_bytes / (g_launches / args.steps), avg_launch, kprof)
+    rl["traffic"], rl["traffic_source"] = measured_traffic(
+        "resnet50_b256_conv_gemm_traffic.md" if B == 256 else None)
     rl["note"] = ("achieved = total algorithmic conv ops of one step / total time of the conv "
                   "GEMM kernels of one step (53 launches, 16 with the residual add fused; "
                   "hipEvents per launch)")
@@ -238,12 +256,39 @@ def run_resnet50(args, dev):
     )
 
 
+def run_hbm_copy(args, dev):
+    """Device-to-device copy of a known size through hipMemcpyAsync: the
+    calibration kernel for the FETCH_SIZE / WRITE_SIZE counters and the
+    achievable-HBM reference for the roofline."""
+    import torch
+
+    from nnr_amd import _lib
+    L = _lib.lib()
+    nbytes = 1 << 30
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(7)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    st = _lib.cur_stream()
+
+    def step():
+        _lib.check(L.nnrh_memcpy(_lib.ptr(dst), _lib.ptr(src), nbytes, 2, st))
+
+    ms = time_steps(step, args)
+    gbs = 2 * nbytes / (ms * 1e-3) / 1e9
+    return dict(metric="HBM device-to-device copy (read + write bytes / s)", value=round(gbs, 1),
+                unit="GB/s", ms_per_step=ms,
+                config={"workload": "hipMemcpyAsync D2D, 1 GiB", "bytes_per_copy": nbytes},
+                roofline={"kernel": "copy", "bound": "hbm", "achieved": round(gbs, 1),
+                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": 2 * nbytes},
+                cpu_baseline=None, dtype="u8")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="resnet50", choices=["resnet50", "qconv"])
+    ap.add_argument("--config", default="resnet50", choices=["resnet50", "qconv", "hbm_copy"])
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
     args = ap.parse_args()
@@ -253,7 +298,8 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
-    res = run_resnet50(args, dev) if args.config == "resnet50" else run_qconv(args, dev)
+    run = {"resnet50": run_resnet50, "qconv": run_qconv, "hbm_copy": run_hbm_copy}[args.config]
+    res = run(args, dev)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 5),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
