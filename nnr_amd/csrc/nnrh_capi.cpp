@@ -483,6 +483,7 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
                 betac[pi] = pcz ? zp_eff(d->w_zp_host[oc]) : h->w_zp_scalar;
                 any_wzp |= betac[pi] != 0;
             }
+        for (int32_t v : c0) h->g.c0_absmax = std::max(h->g.c0_absmax, std::llabs((long long)v));
         if ((rc = upload(&h->wpack, wp.data(), wp.size()))) return fail(rc);
         if ((rc = upload(&h->colsum, colsum.data(), colsum.size()))) return fail(rc);
         if ((rc = upload(&h->c0, c0.data(), c0.size()))) return fail(rc);
@@ -799,6 +800,7 @@ extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc*
     if ((rc = upload(&h->wpack, wp.data(), wp.size()))) return fail(rc);
     if ((rc = upload(&h->colsum, colsum.data(), colsum.size()))) return fail(rc);
     if ((rc = upload(&h->c0, c0.data(), c0.size()))) return fail(rc);
+    for (int32_t v : c0) h->g.c0_absmax = std::max(h->g.c0_absmax, std::llabs((long long)v));
     const int b_zp = ld_zp(d->b_zp_host, d->b_dtype);   // b_zp[0] only (QLinearMatMul.cpp:119)
     h->b_beta = b_zp - (bu8 ? 128 : 0);
     // combined scale (QLinearMatMul.cpp:124-135)

@@ -11,6 +11,12 @@ hipError_t launch_gap_f32(const float* x, float* y, int N, int C, int HW, int x_
 hipError_t launch_gemm_f32(const float* A, const float* B, const float* C, float* Y, int M, int N,
                            int K, int transA, int transB, float alpha, float beta, int c_mode,
                            hipStream_t s);
+// batched: A/B/Y advance by a_bstride/b_bstride/y_bstride elements per batch
+// (0: shared); C is the same for every batch
+hipError_t launch_gemm_f32_batched(const float* A, const float* B, const float* C, float* Y, int M,
+                                   int N, int K, int transA, int transB, float alpha, float beta,
+                                   int c_mode, int batch, long long a_bstride, long long b_bstride,
+                                   long long y_bstride, hipStream_t s);
 hipError_t launch_clip_f32(const float* x, float* y, long long n, float lo, float hi,
                            hipStream_t s);
 

@@ -3,9 +3,11 @@
 // target and their parity bar is the reference's float tolerance (1e-3 abs,
 // tensor_equal, src/nnr.cpp:557-563).
 //   GlobalAveragePool (src/backend/cpu/global_pool.cpp), NCHW or NHWC input
-//   Gemm              (src/backend/cpu/Gemm.cpp), row-major, transA/transB
+//   Gemm / MatMul     (src/backend/cpu/Gemm.cpp, MatMul.cpp), row-major, through rocBLAS
 //   Clip / Relu       (src/backend/cpu/Clip.cpp, Relu.cpp)
 #include "nnrh_f32.h"
+
+#include <rocblas/rocblas.h>
 
 namespace nnrh {
 
@@ -52,68 +54,73 @@ hipError_t launch_gap_f32(const float* x, float* y, int N, int C, int HW, int x_
     return hipGetLastError();
 }
 
-// Y[M][N] = alpha * op(A)[M][K] * op(B)[K][N] + beta * Cb (broadcast)
-// 32x32 tile, 16x16 threads, 2x2 outputs per thread, K step 32 through LDS.
-__global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict A,
-                                                       const float* __restrict B,
-                                                       const float* __restrict Cb,
-                                                       float* __restrict Y, int M, int N, int K,
-                                                       int transA, int transB, float alpha,
-                                                       float beta, int c_mode) {
-    __shared__ float As[32][32 + 1];   // [k][m]
-    __shared__ float Bs[32][32 + 1];   // [k][n]
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
-    float acc[2][2] = {};
-    for (int k0 = 0; k0 < K; k0 += 32) {
-        for (int i = threadIdx.x; i < 32 * 32; i += 256) {
-            int r = i / 32, c = i % 32;
-            // A: walk the contiguous dimension with c
-            int am = m0 + (transA ? c : r), ak = k0 + (transA ? r : c);
-            float av = (am < M && ak < K) ? (transA ? A[(long long)ak * M + am] : A[(long long)am * K + ak]) : 0.f;
-            As[ak - k0][am - m0] = av;
-            int bn = n0 + (transB ? r : c), bk = k0 + (transB ? c : r);
-            float bv = (bn < N && bk < K) ? (transB ? B[(long long)bn * K + bk] : B[(long long)bk * N + bn]) : 0.f;
-            Bs[bk - k0][bn - n0] = bv;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < 32; ++kk) {
-            float a0 = As[kk][ty * 2], a1 = As[kk][ty * 2 + 1];
-            float b0 = Bs[kk][tx * 2], b1 = Bs[kk][tx * 2 + 1];
-            acc[0][0] = __builtin_fmaf(a0, b0, acc[0][0]);
-            acc[0][1] = __builtin_fmaf(a0, b1, acc[0][1]);
-            acc[1][0] = __builtin_fmaf(a1, b0, acc[1][0]);
-            acc[1][1] = __builtin_fmaf(a1, b1, acc[1][1]);
-        }
-        __syncthreads();
+// Y[M][N] = alpha * op(A)[M][K] * op(B)[K][N] + beta * Cb (broadcast), row-major.
+// A plain fp32 GEMM, so it goes to rocBLAS: the broadcast C is written into Y
+// first and rocBLAS accumulates alpha*A*B + beta*Y onto it. Row-major Y is
+// column-major Y^T = op(B)^T op(A)^T, which is the call below.
+__global__ __launch_bounds__(256) void bcast_c_kernel(const float* __restrict C, float* __restrict Y,
+                                                      int M, int N, int c_mode, long long y_bstride) {
+    const long long n = (long long)M * N;
+    float* y = Y + (long long)blockIdx.y * y_bstride;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
+        const long long r = i / N, c = i - r * N;
+        float v;
+        if (c_mode == 1) v = C[0];
+        else if (c_mode == 2) v = C[c];
+        else if (c_mode == 3) v = C[i];
+        else v = C[r];
+        y[i] = v;
     }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        int m = m0 + ty * 2 + i;
-        if (m >= M) continue;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            int n = n0 + tx * 2 + j;
-            if (n >= N) continue;
-            float v = alpha * acc[i][j];
-            if (c_mode == 1) v = v + beta * Cb[0];
-            else if (c_mode == 2) v = v + beta * Cb[n];
-            else if (c_mode == 3) v = v + beta * Cb[(long long)m * N + n];
-            else if (c_mode == 4) v = v + beta * Cb[m];
-            Y[(long long)m * N + n] = v;
-        }
+}
+
+namespace {
+// one rocBLAS handle per (thread, device)
+rocblas_handle blas_handle() {
+    thread_local rocblas_handle handles[16] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
+    if (!handles[dev] && rocblas_create_handle(&handles[dev]) != rocblas_status_success)
+        handles[dev] = nullptr;
+    return handles[dev];
+}
+}  // namespace
+
+hipError_t launch_gemm_f32_batched(const float* A, const float* B, const float* C, float* Y, int M,
+                                   int N, int K, int transA, int transB, float alpha, float beta,
+                                   int c_mode, int batch, long long a_bstride, long long b_bstride,
+                                   long long y_bstride, hipStream_t s) {
+    if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
+    rocblas_handle h = blas_handle();
+    if (!h || rocblas_set_stream(h, s) != rocblas_status_success) return hipErrorNotInitialized;
+    float beta_eff = 0.0f;
+    if (c_mode != 0 && beta != 0.0f) {
+        long long n = (long long)M * N;
+        long long blocks = (n + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(bcast_c_kernel, dim3((unsigned)blocks, batch), dim3(256), 0, s, C, Y, M, N,
+                           c_mode, y_bstride);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        beta_eff = beta;
     }
+    const rocblas_operation opB = transB ? rocblas_operation_transpose : rocblas_operation_none;
+    const rocblas_operation opA = transA ? rocblas_operation_transpose : rocblas_operation_none;
+    const int ldb = transB ? K : N;
+    const int lda = transA ? M : K;
+    rocblas_status st;
+    if (batch == 1)
+        st = rocblas_sgemm(h, opB, opA, N, M, K, &alpha, B, ldb, A, lda, &beta_eff, Y, N);
+    else
+        st = rocblas_sgemm_strided_batched(h, opB, opA, N, M, K, &alpha, B, ldb, b_bstride, A, lda,
+                                           a_bstride, &beta_eff, Y, N, y_bstride, batch);
+    return st == rocblas_status_success ? hipSuccess : hipErrorLaunchFailure;
 }
 
 hipError_t launch_gemm_f32(const float* A, const float* B, const float* C, float* Y, int M, int N,
                            int K, int transA, int transB, float alpha, float beta, int c_mode,
                            hipStream_t s) {
-    if (M <= 0 || N <= 0) return hipSuccess;
-    dim3 grid((N + 31) / 32, (M + 31) / 32);
-    hipLaunchKernelGGL(gemm_f32_kernel, grid, dim3(256), 0, s, A, B, C, Y, M, N, K, transA, transB,
-                       alpha, beta, c_mode);
-    return hipGetLastError();
+    return launch_gemm_f32_batched(A, B, C, Y, M, N, K, transA, transB, alpha, beta, c_mode, 1, 0, 0,
+                                   0, s);
 }
 
 __global__ __launch_bounds__(256) void clip_f32_kernel(const float* __restrict x, float* __restrict y,

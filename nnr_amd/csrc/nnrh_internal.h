@@ -95,6 +95,11 @@ struct GemmArgs {
     // padded height / row length and the pads are already applied
     int copy_shift;
     long long copy_stride;  // bytes per copy
+    // max |c0[n]| (host); the pipelined kernel starts its int32 accumulators
+    // at c0 when 128*128*K + c0_absmax cannot overflow
+    long long c0_absmax;
+    // n / d for n < 2^31 as (n * mul) >> (31 + shift) (set by the launcher)
+    uint32_t div_sp_mul, div_sp_shift, div_ow_mul, div_ow_shift;
     // QLinearAdd (same shape) fused into the RQ-B epilogue: the conv byte q
     // and the residual byte r of the same NHWC element are A and B of the
     // add (or B and A), requantized with RQ-E. Flat element index >=
@@ -105,6 +110,21 @@ struct GemmArgs {
     int add_a_zp, add_b_zp, add_y_zp;
     long long add_body;
 };
+
+// Multiply-shift constants of an unsigned division by d >= 1 for dividends
+// n < 2^31: s = ceil(log2 d), mul = ceil(2^(31+s) / d) < 2^32, and
+// floor(n / d) = (n * mul) >> (31 + s), since the rounding error of mul is
+// below d and n * (mul * d - 2^(31+s)) < 2^(31+s).
+inline void fast_div_consts(uint32_t d, uint32_t* mul, uint32_t* shift) {
+    uint32_t s = 0;
+    while ((1ull << s) < d) ++s;
+    const unsigned long long p = 1ull << (31 + s);
+    *mul = (uint32_t)((p + d - 1) / d);
+    *shift = s;
+}
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t mul, uint32_t shift) {
+    return (uint32_t)(((unsigned long long)n * mul) >> (31 + shift));
+}
 
 // Tile shapes available to the launcher (BM x BN, 256 threads).
 enum TileCfg : int { TILE_128x128 = 0, TILE_256x64 = 1, TILE_64x256 = 2 };

@@ -174,8 +174,10 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
             } else if constexpr (AMODE == A_CONV4) {
                 // padded multi-copy image: row start of this output pixel
                 const int mm = a_ok[j] ? m : 0;
-                const int img = mm / sp_out, s = mm - img * sp_out;
-                const int oh = s / g.oW, ow = s - oh * g.oW;
+                const int img = (int)fast_div((uint32_t)mm, g.div_sp_mul, g.div_sp_shift);
+                const int s = mm - img * sp_out;
+                const int oh = (int)fast_div((uint32_t)s, g.div_ow_mul, g.div_ow_shift);
+                const int ow = s - oh * g.oW;
                 const int pix0 = ow * g.sW;
                 const int r = pix0 & 3;
                 a_base[j] = (long long)(r >> g.copy_shift) * g.copy_stride +
@@ -183,8 +185,10 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
                 a_ih0[j] = 0; a_iw0[j] = 0;
             } else {
                 const int mm = a_ok[j] ? m : 0;
-                const int img = mm / sp_out, s = mm - img * sp_out;
-                const int oh = s / g.oW, ow = s - oh * g.oW;
+                const int img = (int)fast_div((uint32_t)mm, g.div_sp_mul, g.div_sp_shift);
+                const int s = mm - img * sp_out;
+                const int oh = (int)fast_div((uint32_t)s, g.div_ow_mul, g.div_ow_shift);
+                const int ow = s - oh * g.oW;
                 a_base[j] = (long long)img * g.H * g.W * g.Cs;
                 a_ih0[j] = oh * g.sH - g.pad_t;
                 a_iw0[j] = ow * g.sW - g.pad_l;
@@ -268,11 +272,7 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
 
     // ---- consumer state
     int c_t = t_first, c_kt = 0, c_tseq = 0, c_gs = 0;
-    v4i acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    v4i acc[4][4];   // set to c0 at each tile's first K-step
 
     // fused add: residual bytes of this lane's 4 rows x 16 channels. They
     // are loaded one tile ahead (at the first K-step of the previous tile,
@@ -307,11 +307,11 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
         const int nl = wn * 64 + 16 * fchunk;   // first column of this lane in the tile
         const int nb = n0 + nl;
         if (nb >= g.N) return;
+        // the accumulators started at c0 (acc + c0 = the reference's value)
         const uint8_t* ps = lds + S * STAGE + (c_tseq % S) * PSLOT;
-        v4i pc[4], p0[4], p1[4];
+        v4i p0[4], p1[4];
 #pragma unroll
         for (int tn = 0; tn < 4; ++tn) {
-            pc[tn] = *(const v4i*)(ps + (nl + 4 * tn) * 4);
             if constexpr (NP >= 2) p0[tn] = *(const v4i*)(ps + BN * 4 + (nl + 4 * tn) * 4);
             if constexpr (NP >= 3) p1[tn] = *(const v4i*)(ps + 2 * BN * 4 + (nl + 4 * tn) * 4);
         }
@@ -324,12 +324,7 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
                 int32_t* yrow = (int32_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
                 v4i o[4];
 #pragma unroll
-                for (int tn = 0; tn < 4; ++tn) {
-                    o[tn].x = (int)((uint32_t)acc[tm][tn].x + (uint32_t)pc[tn].x);
-                    o[tn].y = (int)((uint32_t)acc[tm][tn].y + (uint32_t)pc[tn].y);
-                    o[tn].z = (int)((uint32_t)acc[tm][tn].z + (uint32_t)pc[tn].z);
-                    o[tn].w = (int)((uint32_t)acc[tm][tn].w + (uint32_t)pc[tn].w);
-                }
+                for (int tn = 0; tn < 4; ++tn) o[tn] = acc[tm][tn];
                 if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
 #pragma unroll
                     for (int tn = 0; tn < 4; ++tn) *(v4i*)(yrow + 4 * tn) = o[tn];
@@ -340,26 +335,46 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
                 }
             } else {
                 uint32_t packed[4];
+                if constexpr (EPI == EPI_RQB) {
+                    // RQ-B: with an even zero point, fl(f + 1.5*2^23 + zp) rounds
+                    // to M + zp + rne(f) (the tie goes to the same even integer),
+                    // so the low byte already holds rne(f) + zp
+                    const float lo_f = (float)g.lo - (float)g.y_zp, hi_f = (float)g.hi - (float)g.y_zp;
+                    const bool zp_even = (g.y_zp & 1) == 0;
+                    const float magic = zp_even ? RNE_MAGIC + (float)g.y_zp : RNE_MAGIC;
+                    const uint32_t zp_add = zp_even ? 0u : (uint32_t)g.y_zp;
 #pragma unroll
-                for (int tn = 0; tn < 4; ++tn) {
-                    uint32_t w = 0;
+                    for (int tn = 0; tn < 4; ++tn) {
+                        uint32_t w = 0;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int32_t v = (int32_t)((uint32_t)acc[tm][tn][q] + (uint32_t)pc[tn][q]);
-                        uint32_t b;
-                        if constexpr (EPI == EPI_RQB)
-                            b = rqb_fast(v, __int_as_float(p0[tn][q]), g.y_zp, g.lo, g.hi);
-                        else if constexpr (EPI == EPI_RQA)
-                            b = rqa_fast(v, __int_as_float(p0[tn][q]), __int_as_float(p1[tn][q]),
-                                         g.inv_y, g.y_zp, g.L, g.hi);
-                        else if constexpr (EPI == EPI_RQC)
-                            b = rqc_fast(v, __int_as_float(p0[tn][q]), __int_as_float(p1[tn][q]),
-                                         g.inv_y, g.y_zp, g.L, g.hi);
-                        else
-                            b = rqd_fast(v, g.cm, g.y_zp, g.lo, g.hi);
-                        w |= (b & 0xffu) << (8 * q);
+                        for (int q = 0; q < 4; ++q) {
+                            float f = (float)acc[tm][tn][q] * __int_as_float(p0[tn][q]);
+                            f = med3f(f, lo_f, hi_f);
+                            const uint32_t b = (uint32_t)__float_as_int(f + magic) + zp_add;
+                            w |= (b & 0xffu) << (8 * q);
+                        }
+                        packed[tn] = w;
                     }
-                    packed[tn] = w;
+                } else {
+#pragma unroll
+                    for (int tn = 0; tn < 4; ++tn) {
+                        uint32_t w = 0;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int32_t v = acc[tm][tn][q];
+                            uint32_t b;
+                            if constexpr (EPI == EPI_RQA)
+                                b = rqa_fast(v, __int_as_float(p0[tn][q]), __int_as_float(p1[tn][q]),
+                                             g.inv_y, g.y_zp, g.L, g.hi);
+                            else if constexpr (EPI == EPI_RQC)
+                                b = rqc_fast(v, __int_as_float(p0[tn][q]), __int_as_float(p1[tn][q]),
+                                             g.inv_y, g.y_zp, g.L, g.hi);
+                            else
+                                b = rqd_fast(v, g.cm, g.y_zp, g.lo, g.hi);
+                            w |= (b & 0xffu) << (8 * q);
+                        }
+                        packed[tn] = w;
+                    }
                 }
                 if constexpr (FADD) {
                     const bool sgn = g.y_type == 1;
@@ -445,6 +460,18 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
         }
         if (p_t < t_end) p_issue();
 
+        if (c_kt == 0) {
+            // the tile's constants landed with its first K-step: start the
+            // accumulators at c0[n] (this lane's 16 columns)
+            const uint8_t* ps = lds + S * STAGE + (c_tseq % S) * PSLOT;
+            const int nl = wn * 64 + 16 * fchunk;
+#pragma unroll
+            for (int tn = 0; tn < 4; ++tn) {
+                const v4i c = *(const v4i*)(ps + (nl + 4 * tn) * 4);
+#pragma unroll
+                for (int tm = 0; tm < 4; ++tm) acc[tm][tn] = c;
+            }
+        }
         const uint8_t* st = lds + (c_gs % S) * STAGE;
         v4i xf[4], wf[4];
 #pragma unroll
@@ -468,10 +495,6 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
 #pragma unroll
                 for (int tm = 0; tm < 4; ++tm) rcur[tm] = rnext[tm];
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
             c_kt = 0;
             ++c_tseq;
             c_t += t_step;
@@ -505,6 +528,10 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
     if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
     GemmArgs a = g;
     a.nbatch = batch;
+    if (g.H > 0) {
+        fast_div_consts((uint32_t)(g.oH * g.oW), &a.div_sp_mul, &a.div_sp_shift);
+        fast_div_consts((uint32_t)g.oW, &a.div_ow_mul, &a.div_ow_shift);
+    }
     hipLaunchKernelGGL(kern, dim3(G, 1, 1), dim3(256), 0, s, a);
     return hipGetLastError();
 }
@@ -539,6 +566,9 @@ hipError_t launch_dma_first(const GemmArgs& g, int batch, hipStream_t s) {
 
 bool qgemm_dma_eligible(const GemmArgs& g, int vec) {
     if (g.y_nchw) return false;
+    // accumulators start at c0: |c0| + 128*128*K must stay inside int32
+    if (g.c0_absmax + 16384LL * (long long)g.Kp >= 0x7fffffffLL) return false;
+    if (g.M > 0x7fffffff / 2) return false;
     if (g.kWp > 0) {
         // first layer: only on the padded multi-copy image
         if (g.copy_stride <= 0 || (g.copy_stride & 15) || (g.W & 3) || (g.kWp & 3)) return false;

@@ -288,3 +288,30 @@ def test_maxpool(dev):
     ref = O.maxpool_u8_nhwc(x, 3, 3, 2, 2, 1, 1, 12, 11)
     y = to_np(H.maxpool_u8_nhwc(to_dev(x, dev), 3, 3, 2, 2, 1, 1, 12, 11))
     assert np.array_equal(y, ref)
+
+
+# ---------------------------------------------------------------------------
+# fp32 glue: Gemm (rocBLAS) with every broadcast mode and transpose, against
+# float64 numpy; the reference's float tolerance (tensor_equal, 1e-3 abs)
+
+@pytest.mark.parametrize("ta,tb,c_mode", [(0, 1, 2), (0, 0, 0), (1, 0, 1), (1, 1, 3), (0, 1, 4)])
+def test_gemm_f32(dev, ta, tb, c_mode):
+    import torch
+    from nnr_amd import _lib
+    rng = np.random.default_rng(ta * 10 + tb * 3 + c_mode)
+    M, N, K = 37, 70, 300
+    A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32) * 0.1
+    B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32) * 0.1
+    Cs = {0: (1,), 1: (1,), 2: (N,), 3: (M, N), 4: (M,)}[c_mode]
+    Cb = rng.standard_normal(Cs).astype(np.float32)
+    alpha, beta = 0.75, 1.5
+    ref = alpha * ((A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64))
+    if c_mode:
+        cb = Cb.astype(np.float64)
+        ref = ref + beta * (cb[:, None] if c_mode == 4 else cb)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    # keep the device copies alive until the asynchronous call has run
+    Ad, Bd, Cd = to_dev(A, dev), to_dev(B, dev), to_dev(Cb, dev)
+    _lib.check(_lib.lib().nnrh_gemm_f32(_lib.ptr(Ad), _lib.ptr(Bd), _lib.ptr(Cd), _lib.ptr(y),
+                                        M, N, K, ta, tb, alpha, beta, c_mode, _lib.cur_stream()))
+    np.testing.assert_allclose(to_np(y), ref, atol=1e-3, rtol=1e-4)
