@@ -524,6 +524,13 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
             g.copy_stride = (long long)d->N * Hp * Wc * 4;
         }
         g.a_bstride = first ? 0 : Cg;   // group channel offset
+        // a 1x1 stride-1 unpadded conv over NHWC is a plain GEMM: row m is
+        // pixel m, row stride = channel stride (no tap decode, no bounds)
+        if (!first && d->kH == 1 && d->kW == 1 && d->sH == 1 && d->sW == 1 && d->pad_t == 0 &&
+            d->pad_l == 0 && d->pad_b == 0 && d->pad_r == 0 && d->oH == d->H && d->oW == d->W) {
+            g.H = 0;
+            g.lda = h->Cx;
+        }
         g.b = h->wpack;
         g.b_bstride = (long long)Np * Kp;
         g.Np = Np;

@@ -33,6 +33,8 @@
 // channels % 16 == 0; dense: K % 16 == 0), no per-row zero-point term
 // (beta == 0), zero points known on the host, NHWC / row-major output and
 // no scalar-tail or RQ-B' columns. Everything else takes qgemm_kernel.
+#include <type_traits>
+
 #include "nnrh_internal.h"
 #include "nnrh_rq.h"
 
@@ -61,6 +63,14 @@ __device__ const PadTable kPadTable{};
 
 __device__ __forceinline__ void dma16(const void* src, uint8_t* lds_dst) {
     __builtin_amdgcn_global_load_lds(src, (NNRH_LDS void*)lds_dst, 16, 0, 0);
+}
+
+// bytes 0 of a, b, c, d -> one dword (a lowest). v_perm_b32 selects bytes
+// of {S0, S1} with S1 as bytes 0-3 and S0 as bytes 4-7; selector 0x0c is 0.
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);   // [a0, b0, 0, 0]
+    const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);   // [c0, d0, 0, 0]
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);              // [a0, b0, c0, d0]
 }
 
 __device__ __forceinline__ void block_barrier() {
@@ -338,23 +348,27 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
                 if constexpr (EPI == EPI_RQB) {
                     // RQ-B: with an even zero point, fl(f + 1.5*2^23 + zp) rounds
                     // to M + zp + rne(f) (the tie goes to the same even integer),
-                    // so the low byte already holds rne(f) + zp
+                    // so the low byte already holds rne(f) + zp; an odd zero point
+                    // is added to the bit pattern
                     const float lo_f = (float)g.lo - (float)g.y_zp, hi_f = (float)g.hi - (float)g.y_zp;
-                    const bool zp_even = (g.y_zp & 1) == 0;
-                    const float magic = zp_even ? RNE_MAGIC + (float)g.y_zp : RNE_MAGIC;
-                    const uint32_t zp_add = zp_even ? 0u : (uint32_t)g.y_zp;
+                    auto rqb_row = [&](auto zp_even) {
+                        constexpr bool EVEN = decltype(zp_even)::value;
+                        const float magic = EVEN ? RNE_MAGIC + (float)g.y_zp : RNE_MAGIC;
 #pragma unroll
-                    for (int tn = 0; tn < 4; ++tn) {
-                        uint32_t w = 0;
+                        for (int tn = 0; tn < 4; ++tn) {
+                            uint32_t b[4];
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            float f = (float)acc[tm][tn][q] * __int_as_float(p0[tn][q]);
-                            f = med3f(f, lo_f, hi_f);
-                            const uint32_t b = (uint32_t)__float_as_int(f + magic) + zp_add;
-                            w |= (b & 0xffu) << (8 * q);
+                            for (int q = 0; q < 4; ++q) {
+                                float f = (float)acc[tm][tn][q] * __int_as_float(p0[tn][q]);
+                                f = med3f(f, lo_f, hi_f);
+                                b[q] = (uint32_t)__float_as_int(f + magic);
+                                if constexpr (!EVEN) b[q] += (uint32_t)g.y_zp;
+                            }
+                            packed[tn] = pack_low_bytes(b[0], b[1], b[2], b[3]);
                         }
-                        packed[tn] = w;
-                    }
+                    };
+                    if ((g.y_zp & 1) == 0) rqb_row(std::true_type{});
+                    else rqb_row(std::false_type{});
                 } else {
 #pragma unroll
                     for (int tn = 0; tn < 4; ++tn) {
@@ -387,7 +401,7 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
 #pragma unroll
                         for (int tn = 0; tn < 4; ++tn) {
                             const uint32_t qw = packed[tn], rw = (uint32_t)rcur[tm][tn];
-                            uint32_t w = 0;
+                            uint32_t ob[4];
 #pragma unroll
                             for (int q = 0; q < 4; ++q) {
                                 float qf, rf;
@@ -403,9 +417,9 @@ __global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
                                 float v = __builtin_fmaf(bf, g.add_sb, g.add_fixed);
                                 v = __builtin_fmaf(af, g.add_sa, v);
                                 v = med3f(v, lo_f, hi_f);
-                                w |= ((uint32_t)rne_bits(v) & 0xffu) << (8 * q);
+                                ob[q] = (uint32_t)rne_bits(v);
                             }
-                            packed[tn] = w;
+                            packed[tn] = pack_low_bytes(ob[0], ob[1], ob[2], ob[3]);
                         }
                     } else {
                         // the row segment reaches the scalar tail
@@ -539,7 +553,7 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
 template <int BM, int BN, int S, int AMODE>
 hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
     if (g.add_other) {
-        if constexpr (AMODE == A_CONV) {
+        if constexpr (AMODE == A_CONV || AMODE == A_DENSE) {
             if (g.epi == EPI_RQB && batch == 1) return launch_dma<BM, BN, S, AMODE, EPI_RQB, true>(g, batch, s);
         }
         return hipErrorNotSupported;
