@@ -2,6 +2,8 @@
 """Benchmark of the int8 QDQ path on one MI355X.
 
 Prints ONE JSON line (driver contract). Workloads:
+  mobilenetv2 cfg4: MobileNetV2 int8 QDQ graph, batch 256 (depthwise VALU path
+            against the pointwise MFMA GEMM); value = images/s
   resnet50  cfg3 (default, the headline metric): ResNet-50 v1.5 int8 QDQ graph,
             batch 256, 224x224, run through the C++ host framework (QDQ
             fusion, NHWC layouts, HIP operators); value = images/s
@@ -159,7 +161,15 @@ def roofline(ops, nbytes, kern_ms, prof):
     return r
 
 
-def run_resnet50(args, dev):
+WORKLOADS = {
+    "resnet50": "cfg3 ResNet-50 v1.5 int8 QDQ, batch {B}, 224x224 (53 QLinearConv, 16 QLinearAdd, "
+                "uint8 MaxPool, fp32 GAP+FC)",
+    "mobilenetv2": "cfg4 MobileNetV2 int8 QDQ, batch {B}, 224x224 (52 QLinearConv incl. 17 "
+                   "depthwise, 10 QLinearAdd, ReLU6 in the quantization range, fp32 GAP+FC)",
+}
+
+
+def run_model(args, dev, model):
     import numpy as np
     import torch
 
@@ -168,7 +178,7 @@ def run_resnet50(args, dev):
     from oracle import pyoracle as O
 
     B = args.batch
-    g = synth.resnet50(batch=B, hw=224)
+    g = {"resnet50": synth.resnet50, "mobilenetv2": synth.mobilenetv2}[model](batch=B, hw=224)
     rng = np.random.default_rng(10)
     x = rng.random((B, 3, 224, 224), dtype=np.float32)
     s = G.Session(g)
@@ -223,10 +233,22 @@ def run_resnet50(args, dev):
     conv_bytes = sum(r["bytes"] for r in prof if r["op"] == "QLinearConv")
     rl = roofline(ops_per_launch, conv_bytes / (g_launches / args.steps), avg_launch, kprof)
     rl["traffic"], rl["traffic_source"] = measured_traffic(
-        "resnet50_b256_conv_gemm_traffic.md" if B == 256 else None)
-    rl["note"] = ("achieved = total algorithmic conv ops of one step / total time of the conv "
-                  "GEMM kernels of one step (53 launches, 16 with the residual add fused; "
-                  "hipEvents per launch)")
+        f"{model}_b256_conv_gemm_traffic.md" if B == 256 else None)
+    n_fused = s.fusion_stat("conv_add")
+    rl["note"] = (f"achieved = total algorithmic conv ops of one step / total time of the conv "
+                  f"GEMM kernels of one step ({round(g_launches / args.steps)} launches, "
+                  f"{n_fused} with the residual add fused; hipEvents per launch)")
+    if "depthwise" in kprof:
+        # the depthwise convolutions are HBM-bound: their own roofline
+        dw_rows = [r for r in prof if r["op"] == "QLinearConv" and r["variant"] == "DW"]
+        dn, dms = kprof["depthwise"]
+        dw_bytes = sum(r["bytes"] for r in dw_rows)
+        dw_gbs = dw_bytes / (dms / args.steps * 1e-3) / 1e9
+        rl["depthwise"] = {"bound": "hbm", "achieved": round(dw_gbs, 1), "peak": PEAK_HBM_GBS,
+                           "unit": "GB/s", "frac": round(dw_gbs / PEAK_HBM_GBS, 4),
+                           "launches_per_step": round(dn / args.steps),
+                           "alg_bytes_per_step": dw_bytes,
+                           "avg_launch_ms": round(dms / dn, 5)}
     # cpu baseline: the oracle replays the plan on one image
     nthr = host_threads()
     O.set_threads(nthr)
@@ -241,10 +263,9 @@ def run_resnet50(args, dev):
     imgs = B / (ms * 1e-3)
     return dict(
         metric=METRIC, value=round(imgs, 1), unit="images/s", ms_per_step=ms,
-        config={"workload": f"cfg3 ResNet-50 v1.5 int8 QDQ, batch {B}, 224x224 (53 QLinearConv, "
-                            "16 QLinearAdd, uint8 MaxPool, fp32 GAP+FC)", "global_batch": B,
+        config={"workload": WORKLOADS[model].format(B=B), "global_batch": B,
                 "branches": {b: sum(1 for p in plan if p["variant"].split("+")[0] == b)
-                             for b in ("FIRST", "NR16", "PACKED")},
+                             for b in ("FIRST", "DW", "NR16", "PACKED")},
                 "adds_fused_into_conv": s.fusion_stat("conv_add"),
                 "conv_tops": round(conv_ops / (qgemm_ms_per_step * 1e-3) / 1e12, 1),
                 "device_bytes": s.device_bytes()},
@@ -288,7 +309,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="resnet50", choices=["resnet50", "qconv", "hbm_copy"])
+    ap.add_argument("--config", default="resnet50",
+                    choices=["resnet50", "mobilenetv2", "qconv", "hbm_copy"])
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
     args = ap.parse_args()
@@ -298,7 +320,9 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
-    run = {"resnet50": run_resnet50, "qconv": run_qconv, "hbm_copy": run_hbm_copy}[args.config]
+    run = {"resnet50": lambda a, d: run_model(a, d, "resnet50"),
+           "mobilenetv2": lambda a, d: run_model(a, d, "mobilenetv2"),
+           "qconv": run_qconv, "hbm_copy": run_hbm_copy}[args.config]
     res = run(args, dev)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 5),

@@ -105,8 +105,12 @@ __device__ __forceinline__ int qadd_elem(int a, int b, const GemmArgs& g, bool t
     return clampi(x86_f2i(__builtin_rintf(v)), g.lo, g.hi);
 }
 
+// blocks per CU the kernel is compiled for: LDS and registers must fit them
+template <int BM, int BN, int S>
+constexpr int dma_min_blocks() { return ((BM + BN) * 64 * S + 4096) * 3 <= 160 * 1024 ? 3 : 2; }
+
 template <int BM, int BN, int S, int AMODE, int EPI, bool FADD>
-__global__ __launch_bounds__(256, 2) void qgemm_dma_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_kernel(GemmArgs g) {
     constexpr int WAVES_N = BN / 64;
     static_assert((BM / 64) * WAVES_N == 4, "4 waves of 64x64");
     constexpr int A_CH = BM / 64;            // DMA chunks per thread per step (A)
@@ -550,11 +554,12 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int BM, int BN, int S, int AMODE>
+template <int BM, int BN, int S, int AMODE, int S_ADD = S>
 hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
     if (g.add_other) {
         if constexpr (AMODE == A_CONV || AMODE == A_DENSE) {
-            if (g.epi == EPI_RQB && batch == 1) return launch_dma<BM, BN, S, AMODE, EPI_RQB, true>(g, batch, s);
+            if (g.epi == EPI_RQB && batch == 1)
+                return launch_dma<BM, BN, S_ADD, AMODE, EPI_RQB, true>(g, batch, s);
         }
         return hipErrorNotSupported;
     }
@@ -613,8 +618,10 @@ hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t 
     }
     switch (tile) {
     case TILE_128x128:
-        return conv ? launch_dma_epi<128, 128, 4, A_CONV>(g, batch, s)
-                    : launch_dma_epi<128, 128, 4, A_DENSE>(g, batch, s);
+        // 3 stages at 3 blocks per CU; the fused-add variant keeps 4 stages at
+        // 2 blocks (it needs the registers of the lookahead residual)
+        return conv ? launch_dma_epi<128, 128, 3, A_CONV, 4>(g, batch, s)
+                    : launch_dma_epi<128, 128, 3, A_DENSE, 4>(g, batch, s);
     case TILE_256x64:
         return conv ? launch_dma_epi<256, 64, 3, A_CONV>(g, batch, s)
                     : launch_dma_epi<256, 64, 3, A_DENSE>(g, batch, s);

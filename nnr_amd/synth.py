@@ -150,3 +150,54 @@ def qconv_graph(batch=32, seed=2):
     y, _ = q.conv(x_q, x_qp, 64, 64, 3, pad=1, name="conv", y_scale=0.03, y_zp=0)
     g.outputs.append(y)
     return g
+
+
+# MobileNetV2 (Sandler et al. 2018, width 1.0): (expansion t, channels c,
+# repeats n, first stride s) of the 17 inverted-residual blocks
+MBV2_BLOCKS = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 96, 3, 1),
+               (6, 160, 3, 2), (6, 320, 1, 1))
+
+
+def mobilenetv2(batch=256, hw=224, seed=4, num_classes=1000):
+    """MobileNetV2 int8 QDQ: stem 3x3/2 (3->32), 17 inverted-residual blocks
+    (1x1 expand, 3x3 depthwise, 1x1 linear project; residual add when the
+    stride is 1 and the width is unchanged), 1x1 to 1280, fp32 GAP + Gemm.
+    ReLU6 is absorbed into the output quantization (y_zp 0, y_scale 6/255),
+    the form NNR fuses; the linear projections and the adds quantize with
+    zero point 128."""
+    g = Graph()
+    rng = np.random.default_rng(seed)
+    q = _QDQ(g, rng)
+    relu6 = F32(6.0 / 255.0)
+    g.inputs["input"] = (np.float32, (batch, 3, hw, hw))
+    x_q, x_qp = q.quant("input", F32(1.0 / 255.0), 0, name="input_Q")
+    x_q, x_qp = q.conv(x_q, x_qp, 3, 32, 3, stride=2, pad=1, name="stem", y_scale=relu6, y_zp=0)
+    cin = 32
+    bi = 0
+    for t, c, n, s in MBV2_BLOCKS:
+        for r in range(n):
+            stride = s if r == 0 else 1
+            bi += 1
+            nm = f"b{bi}"
+            hid = cin * t
+            a, a_qp = x_q, x_qp
+            if t != 1:
+                a, a_qp = q.conv(a, a_qp, cin, hid, 1, name=nm + "_expand", y_scale=relu6, y_zp=0)
+            a, a_qp = q.conv(a, a_qp, hid, hid, 3, stride=stride, pad=1, group=hid, name=nm + "_dw",
+                             y_scale=relu6, y_zp=0)
+            a, a_qp = q.conv(a, a_qp, hid, c, 1, relu=False, name=nm + "_project")
+            if stride == 1 and cin == c:
+                sm = g.node("Add", [q.dequant(a, a_qp), q.dequant(x_q, x_qp)], name=nm + "_add")
+                x_q, x_qp = q.quant(sm, q.scale(), 128)
+            else:
+                x_q, x_qp = a, a_qp
+            cin = c
+    x_q, x_qp = q.conv(x_q, x_qp, cin, 1280, 1, name="last", y_scale=relu6, y_zp=0)
+    f = q.dequant(x_q, x_qp, name="head_dq")
+    p = g.node("GlobalAveragePool", [f], name="gap")
+    fl = g.node("Flatten", [p], name="flatten", axis=1)
+    fw = g.init("fc_w", rng.normal(0.0, np.sqrt(1.0 / 1280), (num_classes, 1280)).astype(F32))
+    fb = g.init("fc_b", rng.normal(0.0, 0.01, num_classes).astype(F32))
+    g.node("Gemm", [fl, fw, fb], outputs="logits", name="fc", transB=1)
+    g.outputs.append("logits")
+    return g

@@ -75,3 +75,23 @@ def test_qconv_graph_config2(dev):
     x = (rng.random((4, 64, 56, 56), dtype=np.float32) * 5 - 2.5).astype(np.float32)
     plan, y, _ = check_graph(g, {"input": x}, g.outputs[0])
     assert [p["variant"] for p in plan if p["op"] == "QLinearConv"] == ["NR16"]
+
+
+def test_mobilenetv2_b2_bitexact(dev):
+    """cfg4 shape at batch 2: stem (first layer), 17 depthwise (RQ-A), 34
+    pointwise (RQ-B), 10 residual adds; every int8 tensor bit-exact."""
+    g = synth.mobilenetv2(batch=2, hw=224)
+    rng = np.random.default_rng(16)
+    x = rng.random((2, 3, 224, 224), dtype=np.float32)
+    plan, logits, n_int = check_graph(g, {"input": x}, "logits")
+    variants = [p["variant"].split("+")[0] for p in plan if p["op"] == "QLinearConv"]
+    assert variants.count("DW") == 17 and variants.count("FIRST") == 1
+    assert logits.shape == (2, 1000) and np.isfinite(logits).all()
+
+
+def test_mobilenetv2_small_input(dev):
+    """96x96 input: odd spatial sizes (48/24/12/6/3) through every stride."""
+    g = synth.mobilenetv2(batch=3, hw=96, seed=17)
+    rng = np.random.default_rng(18)
+    x = rng.random((3, 3, 96, 96), dtype=np.float32)
+    check_graph(g, {"input": x}, "logits")

@@ -89,3 +89,20 @@ def test_post_op_fusion_sets_qmin():
     plan = s.plan()
     assert [p["op"] for p in plan] == ["QLinearConv"] and plan[0]["post_fn"] == 1
     assert s.fusion_stat("post_ops") == 1
+
+
+def test_mobilenetv2_fusion_and_branches():
+    """cfg4: 52 QLinearConv (stem first-layer, 17 depthwise, 34 pointwise
+    NR48), 10 QLinearAdd, every int8 activation NHWC."""
+    g = synth.mobilenetv2(batch=2, hw=224)
+    s = G.Session(g, device=False)
+    plan = s.plan()
+    ops = collections.Counter(p["op"] for p in plan)
+    assert ops == {"QLinearConv": 52, "QLinearAdd": 10, "QuantizeLinear": 1,
+                   "DequantizeLinear": 1, "GlobalAveragePool": 1, "Flatten": 1, "Gemm": 1}
+    br = collections.Counter(p["variant"] for p in plan if p["op"] == "QLinearConv")
+    assert br == {"FIRST": 1, "DW": 17, "PACKED": 34}
+    fmt = lambda n: s.tensor_info(n)[3]
+    for p in plan:
+        if p["op"] in ("QLinearConv", "QLinearAdd"):
+            assert fmt(p["outputs"][0]) == 1, p["name"]
