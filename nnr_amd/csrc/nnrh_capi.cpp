@@ -339,9 +339,11 @@ struct nnrh_qconv {
     nnrh_qconv_desc d{};
     int branch = 0;
     bool use_dw = false;         // depthwise VALU kernel
+    bool dw16 = false;           // ... its dot4 variant (NHWC out, C % 16 == 0, w_zp 0)
     bool fused_add = false;      // nnrh_qconv_fuse_add was called
     int transform = 0;           // 0 none, 1 NCHW->NHWC, 2 NCHW->NHWC padded to 4 ch,
-                                 // 3 first-layer padded multi-copy NHWC4 image
+                                 // 3 first-layer padded multi-copy NHWC4 image,
+                                 // 4 NHWC channels padded to a multiple of 16
     int Cx = 0;                  // channels of the tensor the kernel reads
     int groups = 1;
     bool need_rowsum = false;
@@ -352,8 +354,9 @@ struct nnrh_qconv {
     GemmArgs g{};
     // device buffers
     int8_t* wpack = nullptr;
+    uint32_t* wdot = nullptr;    // depthwise dot4 weights [ceil(taps/4)][C]
     int32_t* colsum = nullptr;
-    int32_t* c0 = nullptr;
+    int32_t* c0 = nullptr;       // GEMM: per-column constant; depthwise: tap-sum correction
     int32_t* beta_col = nullptr;
     float* os = nullptr;
     float* cs = nullptr;
@@ -362,7 +365,7 @@ struct nnrh_qconv {
     uint8_t* xs = nullptr;
     int32_t* rowsum = nullptr;
     ~nnrh_qconv() {
-        dfree(wpack); dfree(colsum); dfree(c0); dfree(beta_col); dfree(os); dfree(cs); dfree(bf);
+        dfree(wpack); dfree(wdot); dfree(colsum); dfree(c0); dfree(beta_col); dfree(os); dfree(cs); dfree(bf);
         dfree(bias); dfree(xs); dfree(rowsum);
     }
 };
@@ -444,11 +447,37 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
         h->dw_L = (br == NNRH_BR_IM2COL) ? qmin : lo;
         h->dw_tail = (br == NNRH_BR_IM2COL) ? TAIL_TILED : TAIL_NONE;
         h->dw_tile_h = tile_h;
+        // dot4 kernel: NHWC out without tails, 16-channel chunks, w_zp 0
+        const int taps = d->kH * d->kW;
+        h->dw16 = h->dw_tail == TAIL_NONE && d->y_nhwc && OC % 16 == 0 && OC <= 4096 &&
+                  h->w_zp_scalar == 0 && taps <= 12;
+        if (h->dw16) {
+            const int G4 = (taps + 3) / 4;
+            std::vector<uint32_t> wdot((size_t)G4 * OC, 0u);
+            std::vector<int32_t> corr(OC, 0);
+            // sum (x - x_zp) w = sum (x ^ 0x80) w + (128 - x_zp) sum w   (uint8)
+            const uint32_t k = (uint32_t)((u8 ? 128 : 0) - d->x_zp);
+            for (int c = 0; c < OC; ++c) {
+                uint32_t sw = 0;
+                for (int t = 0; t < taps; ++t) {
+                    const int8_t v = d->w_host[(size_t)c * taps + t];
+                    wdot[(size_t)(t / 4) * OC + c] |= (uint32_t)(uint8_t)v << (8 * (t % 4));
+                    sw += (uint32_t)(int32_t)v;
+                }
+                corr[c] = (int32_t)(k * sw);
+            }
+            if ((rc = upload(&h->wdot, wdot.data(), wdot.size()))) return fail(rc);
+            if ((rc = upload(&h->c0, corr.data(), corr.size()))) return fail(rc);
+        }
     } else {
         // ---- GEMM plan: groups on blockIdx.z, K order (kh, kw, c); every
         // per-column array is laid out [G][Np] (zero padded)
         const bool first = br == NNRH_BR_FIRST;
-        const int Cgp = first ? 4 : Cg;
+        // channel counts that are not a multiple of 16: the kernel reads a
+        // copy padded with x_zp to the next multiple of 16 (zero weights
+        // there, so the accumulators are unchanged) and keeps 16-byte loads
+        const bool cpad = !first && G == 1 && Cg % 16 != 0;
+        const int Cgp = first ? 4 : (cpad ? round_up(Cg, 16) : Cg);
         const int kWp = first ? round_up(d->kW, 4) : d->kW;   // first layer: taps padded to 4
         const int K = d->kH * kWp * Cgp;
         const int Kp = round_up(K, 64);
@@ -499,6 +528,7 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
         const bool first_copies = first && d->y_nhwc && G == 1;
         if (first_copies) { h->transform = 3; h->Cx = 4; }
         else if (first) { h->transform = 2; h->Cx = 4; }
+        else if (cpad) { h->transform = d->x_nhwc ? 4 : 1; h->Cx = Cgp; }
         else { h->transform = d->x_nhwc ? 0 : 1; h->Cx = d->C; }
 
         GemmArgs& g = h->g;
@@ -610,12 +640,27 @@ extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stre
                                           d.pad_l, h->g.copy_shift, (uint8_t)(d.x_zp & 0xff), s),
                 "first_layer_copies");
         src = h->xs;
+    } else if (h->transform == 4) {
+        ProfScope ps("pad_channels_u8", s);
+        HIP_TRY(launch_pad_channels_u8(src, h->xs, (long long)d.N * d.H * d.W, d.C, h->Cx,
+                                       (uint8_t)(d.x_zp & 0xff), s),
+                "pad_channels");
+        src = h->xs;
     } else if (h->transform) {
         ProfScope ps("nchw_to_nhwc_u8", s);
         HIP_TRY(launch_nchw_to_nhwc_u8(src, h->xs, d.N, d.C, d.H * d.W, h->Cx,
                                        (uint8_t)(d.x_zp & 0xff), s),
                 "nchw_to_nhwc");
         src = h->xs;
+    }
+    if (h->use_dw && h->dw16) {
+        ProfScope ps("depthwise", s);
+        HIP_TRY(launch_depthwise16(src, h->wdot, h->c0, (uint8_t*)y, h->cs, h->bf, d.N, d.C, d.H, d.W,
+                                   d.oH, d.oW, d.kH, d.kW, d.sH, d.sW, d.dH, d.dW, d.pad_t, d.pad_l,
+                                   d.x_zp, d.act_dtype == NNRH_U8 ? 0x80 : 0, h->inv_y, d.y_zp,
+                                   h->dw_L, d.act_dtype == NNRH_U8 ? 255 : 127, s),
+                "depthwise16");
+        return NNRH_OK;
     }
     if (h->use_dw) {
         ProfScope ps("depthwise", s);
@@ -683,7 +728,13 @@ extern "C" int nnrh_qconv_run_add(nnrh_qconv_t h, const void* x, const void* oth
     const nnrh_qconv_desc& d = h->d;
     hipStream_t s = S(stream);
     const uint8_t* src = (const uint8_t*)x;
-    if (h->transform) {
+    if (h->transform == 4) {
+        ProfScope ps("pad_channels_u8", s);
+        HIP_TRY(launch_pad_channels_u8(src, h->xs, (long long)d.N * d.H * d.W, d.C, h->Cx,
+                                       (uint8_t)(d.x_zp & 0xff), s),
+                "pad_channels");
+        src = h->xs;
+    } else if (h->transform) {
         ProfScope ps("nchw_to_nhwc_u8", s);
         HIP_TRY(launch_nchw_to_nhwc_u8(src, h->xs, d.N, d.C, d.H * d.W, h->Cx,
                                        (uint8_t)(d.x_zp & 0xff), s),

@@ -146,11 +146,20 @@ hipError_t launch_depthwise(const uint8_t* x, const int8_t* w, uint8_t* y,
                             int y_zp, int L, int hi, int act_signed,
                             int y_nchw, int tail_mode, int tail_tile_h,
                             hipStream_t s);
+// depthwise, NHWC in/out, C % 16 == 0, w_zp 0, at most 12 taps, no tails
+// (nnrh_misc.hip); wdot [ceil(taps/4)][C] 4 taps per dword, corr[C]
+hipError_t launch_depthwise16(const uint8_t* x, const uint32_t* wdot, const int32_t* corr,
+                              uint8_t* y, const float* cs, const float* bf, int N, int C, int H,
+                              int W, int oH, int oW, int kH, int kW, int sH, int sW, int dH, int dW,
+                              int pad_t, int pad_l, int x_zp, int a_xor, float inv_y, int y_zp,
+                              int L, int hi, hipStream_t s);
 hipError_t launch_rowsum_dense(const uint8_t* a, long long lda,
                                long long a_bstride, int M, int K, int a_signed,
                                int a_zp, const void* a_zp_dev, int32_t* out,
                                int batch, hipStream_t s);
 hipError_t launch_fill_u8(void* p, uint8_t v, long long n, hipStream_t s);
+hipError_t launch_pad_channels_u8(const uint8_t* x, uint8_t* y, long long pixels, int C, int Cpad,
+                                  uint8_t fill, hipStream_t s);
 hipError_t launch_first_layer_copies(const uint8_t* x, uint8_t* y, int N, int C, int H, int W,
                                      int Hp, int Wc, int pad_t, int pad_l, int copy_shift,
                                      uint8_t fill, hipStream_t s);

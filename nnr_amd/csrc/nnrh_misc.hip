@@ -112,6 +112,35 @@ hipError_t launch_first_layer_copies(const uint8_t* x, uint8_t* y, int N, int C,
     return hipGetLastError();
 }
 
+// NHWC [pixels][C] -> [pixels][Cpad] with the tail channels set to `fill`
+// (Cpad % 4 == 0); one thread per output dword.
+__global__ __launch_bounds__(256) void pad_channels_kernel(const uint8_t* __restrict x,
+                                                           uint32_t* __restrict y, long long total,
+                                                           int C, int Cpad4, uint8_t fill) {
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (long long)gridDim.x * 256) {
+        const long long p = i / Cpad4;
+        const int c0 = (int)(i - p * Cpad4) * 4;
+        const uint8_t* xp = x + p * C;
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w |= (uint32_t)(c0 + j < C ? xp[c0 + j] : fill) << (8 * j);
+        y[i] = w;
+    }
+}
+
+hipError_t launch_pad_channels_u8(const uint8_t* x, uint8_t* y, long long pixels, int C, int Cpad,
+                                  uint8_t fill, hipStream_t s) {
+    if (pixels <= 0) return hipSuccess;
+    if (Cpad % 4 || Cpad < C || ((uintptr_t)y & 3)) return hipErrorInvalidValue;
+    const long long total = pixels * (Cpad / 4);
+    long long blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(pad_channels_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, (uint32_t*)y,
+                       total, C, Cpad / 4, fill);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Depthwise QLinearConv, NHWC in / NHWC or NCHW out, requantize RQ-A with
 // clamp [L, hi]. Each thread computes 4 consecutive channels of one output
@@ -217,6 +246,179 @@ hipError_t launch_depthwise(const uint8_t* x, const int8_t* w, uint8_t* y, const
     hipLaunchKernelGGL(depthwise_kernel, dim3(blocks), dim3(256), 0, s, x, w, y, cs, bf, N, C,
                        H, W, oH, oW, kH, kW, sH, sW, dH, dW, pad_t, pad_l, x_zp, w_zp, inv_y,
                        y_zp, L, hi, act_signed, y_nchw, tail_mode, tail_tile_h);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Depthwise QLinearConv, NHWC in and out, 16 channels per thread, RQ-A with
+// clamp [L, hi] and no scalar tails (the DW branch,
+// depthwise_int8_avx512.h:207-351). The tap sum runs on v_dot4_i32_i8:
+//   sum_t (x_t - x_zp) w_t = sum_t x'_t w_t + corr[c],
+//   x' = x ^ a_xor (x - 128 for uint8), corr[c] = (a_sub - x_zp) * sum_t w_t,
+// with the 4-tap byte groups of one channel assembled by a 4x4 byte
+// transpose (v_perm) and the weights pre-packed [group][C] as 4 taps per
+// dword (zero past the last tap). Out-of-image taps read the pad byte x_zp,
+// whose product cancels against corr, so they contribute 0 exactly as the
+// reference's zero_buf does. All int32 arithmetic wraps like vpmulld/vpaddd.
+// Requantize: clamp(rne(u) + zp, L, hi) == rne(clamp(u, L - zp, hi - zp)) + zp
+// for integer bounds, evaluated with the 1.5 * 2^23 rounding constant.
+struct Dw16Args {
+    const uint8_t* x;
+    const uint32_t* wdot;   // [G4][C]
+    const int32_t* corr;    // [C]
+    const float* cs;
+    const float* bf;
+    uint8_t* y;
+    int N, C, H, W, oH, oW, kW, taps, sH, sW, dH, dW, pad_t, pad_l;
+    uint32_t pad4, xmask;
+    float inv_y;
+    int y_zp, L, hi;
+    int c16, groups_per_block;        // channel chunks; pixel groups a block holds
+    uint32_t n_groups;                // rows * owbs
+    uint32_t owbs, owb_mul, owb_shift;
+};
+
+constexpr int DW16_PX = 4;   // output pixels along a row per thread
+
+__device__ __forceinline__ void transpose4x4_bytes(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
+                                                   uint32_t* y) {
+    const uint32_t lo01 = __builtin_amdgcn_perm(x1, x0, 0x05010400u);   // x0b0 x1b0 x0b1 x1b1
+    const uint32_t hi01 = __builtin_amdgcn_perm(x1, x0, 0x07030602u);   // x0b2 x1b2 x0b3 x1b3
+    const uint32_t lo23 = __builtin_amdgcn_perm(x3, x2, 0x05010400u);
+    const uint32_t hi23 = __builtin_amdgcn_perm(x3, x2, 0x07030602u);
+    y[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);              // x0b0 x1b0 x2b0 x3b0
+    y[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);              // x0b1 x1b1 x2b1 x3b1
+    y[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+    y[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+}
+
+// Block = groups_per_block pixel groups x c16 channel chunks (thread ->
+// chunk threadIdx % c16, so each thread keeps one chunk's weights); a pixel
+// group is DW16_PX consecutive output pixels of one row; blocks stride over
+// the pixel groups.
+template <int G4>
+__global__ __launch_bounds__(256) void dw16_kernel(Dw16Args p) {
+    const int tid = threadIdx.x;
+    if (tid >= p.c16 * p.groups_per_block) return;
+    const int cg = tid % p.c16;
+    const int gl = tid / p.c16;
+    const int c0 = cg * 16;
+    uint32_t wd[G4][16];
+#pragma unroll
+    for (int g = 0; g < G4; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 v = *(const uint4*)(p.wdot + (long long)g * p.C + c0 + 4 * q);
+            wd[g][4 * q] = v.x; wd[g][4 * q + 1] = v.y; wd[g][4 * q + 2] = v.z; wd[g][4 * q + 3] = v.w;
+        }
+    int32_t corr[16];
+    float cs[16], bf[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int4 cv = *(const int4*)(p.corr + c0 + 4 * q);
+        const float4 sv = *(const float4*)(p.cs + c0 + 4 * q);
+        const float4 bv = *(const float4*)(p.bf + c0 + 4 * q);
+        corr[4 * q] = cv.x; corr[4 * q + 1] = cv.y; corr[4 * q + 2] = cv.z; corr[4 * q + 3] = cv.w;
+        cs[4 * q] = sv.x; cs[4 * q + 1] = sv.y; cs[4 * q + 2] = sv.z; cs[4 * q + 3] = sv.w;
+        bf[4 * q] = bv.x; bf[4 * q + 1] = bv.y; bf[4 * q + 2] = bv.z; bf[4 * q + 3] = bv.w;
+    }
+    const float lo_f = (float)(p.L - p.y_zp), hi_f = (float)(p.hi - p.y_zp);
+    const bool zp_even = (p.y_zp & 1) == 0;
+    const float magic = zp_even ? 12582912.0f + (float)p.y_zp : 12582912.0f;
+    const uint32_t zp_add = zp_even ? 0u : (uint32_t)p.y_zp;
+    const uint32_t stride = gridDim.x * (uint32_t)p.groups_per_block;
+
+    for (uint32_t pg = blockIdx.x * (uint32_t)p.groups_per_block + gl; pg < p.n_groups; pg += stride) {
+        const int row = (int)fast_div(pg, p.owb_mul, p.owb_shift);
+        const int owb = (int)pg - row * (int)p.owbs;
+        const int n = row / p.oH;
+        const int oh = row - n * p.oH;
+        const uint8_t* xn = p.x + (long long)n * p.H * p.W * p.C + c0;
+        uint8_t* yrow = p.y + (long long)row * p.oW * p.C + c0;
+#pragma unroll 1
+        for (int px = 0; px < DW16_PX; ++px) {
+            const int ow = owb * DW16_PX + px;
+            if (ow >= p.oW) break;
+            int32_t acc[16];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) acc[c] = corr[c];
+#pragma unroll
+            for (int g = 0; g < G4; ++g) {
+                uint32_t xt[4][4];   // [tap in group][dword = 4 channels]
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) {
+                    const int t = 4 * g + tt;
+                    uint4 v = make_uint4(p.pad4, p.pad4, p.pad4, p.pad4);
+                    if (t < p.taps) {
+                        const int a = t / p.kW;
+                        const int b = t - a * p.kW;
+                        const int ih = oh * p.sH - p.pad_t + a * p.dH;
+                        const int iw = ow * p.sW - p.pad_l + b * p.dW;
+                        if ((unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W)
+                            v = *(const uint4*)(xn + ((long long)ih * p.W + iw) * p.C);
+                    }
+                    xt[tt][0] = v.x ^ p.xmask; xt[tt][1] = v.y ^ p.xmask;
+                    xt[tt][2] = v.z ^ p.xmask; xt[tt][3] = v.w ^ p.xmask;
+                }
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    uint32_t tr[4];
+                    transpose4x4_bytes(xt[0][d], xt[1][d], xt[2][d], xt[3][d], tr);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[4 * d + j] = __builtin_amdgcn_sdot4((int)tr[j], (int)wd[g][4 * d + j],
+                                                               acc[4 * d + j], false);
+                }
+            }
+            uint32_t ob[16];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const float t = __builtin_fmaf((float)acc[c], cs[c], bf[c]);
+                float u = t * p.inv_y;
+                u = __builtin_amdgcn_fmed3f(u, lo_f, hi_f);
+                ob[c] = (uint32_t)__float_as_int(u + magic) + zp_add;
+            }
+            uint32_t w4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t ab = __builtin_amdgcn_perm(ob[4 * q + 1], ob[4 * q], 0x0c0c0400u);
+                const uint32_t cd = __builtin_amdgcn_perm(ob[4 * q + 3], ob[4 * q + 2], 0x0c0c0400u);
+                w4[q] = __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+            }
+            *(uint4*)(yrow + (long long)ow * p.C) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+    }
+}
+
+hipError_t launch_depthwise16(const uint8_t* x, const uint32_t* wdot, const int32_t* corr,
+                              uint8_t* y, const float* cs, const float* bf, int N, int C, int H,
+                              int W, int oH, int oW, int kH, int kW, int sH, int sW, int dH, int dW,
+                              int pad_t, int pad_l, int x_zp, int a_xor, float inv_y, int y_zp,
+                              int L, int hi, hipStream_t s) {
+    const int taps = kH * kW;
+    if (C % 16 || C > 16 * 256 || taps < 1 || taps > 12 || N <= 0 || oH <= 0 || oW <= 0)
+        return hipErrorInvalidValue;
+    if ((((uintptr_t)x) | ((uintptr_t)y)) & 15) return hipErrorInvalidValue;
+    Dw16Args a{};
+    a.x = x; a.wdot = wdot; a.corr = corr; a.cs = cs; a.bf = bf; a.y = y;
+    a.N = N; a.C = C; a.H = H; a.W = W; a.oH = oH; a.oW = oW; a.kW = kW; a.taps = taps;
+    a.sH = sH; a.sW = sW; a.dH = dH; a.dW = dW; a.pad_t = pad_t; a.pad_l = pad_l;
+    a.pad4 = (uint32_t)(x_zp & 0xff) * 0x01010101u;
+    a.xmask = (uint32_t)(a_xor & 0xff) * 0x01010101u;
+    a.inv_y = inv_y; a.y_zp = y_zp; a.L = L; a.hi = hi;
+    a.c16 = C / 16;
+    a.groups_per_block = 256 / a.c16;
+    a.owbs = (uint32_t)((oW + DW16_PX - 1) / DW16_PX);
+    const long long groups = (long long)N * oH * a.owbs;
+    if (groups >= (1LL << 31)) return hipErrorInvalidValue;
+    a.n_groups = (uint32_t)groups;
+    fast_div_consts(a.owbs, &a.owb_mul, &a.owb_shift);
+    long long blocks = (groups + a.groups_per_block - 1) / a.groups_per_block;
+    if (blocks > 4096) blocks = 4096;
+    const int G4 = (taps + 3) / 4;
+    if (G4 == 1) hipLaunchKernelGGL(dw16_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    else if (G4 == 2) hipLaunchKernelGGL(dw16_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(dw16_kernel<3>, dim3((unsigned)blocks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

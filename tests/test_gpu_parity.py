@@ -172,6 +172,18 @@ CONV_CASES = [
     ("first_s3", 1, 3, 33, 30, 32, 3, dict(stride=(3, 3), pads=(1, 1, 1, 1), y_nhwc=1, post_fn=1,
                                           y_zp=6)),
     ("first_s4_c4", 1, 4, 17, 19, 16, 3, dict(stride=(4, 4), y_nhwc=1, y_zp=1)),
+    # depthwise dot4 kernel: 2x2 taps (one tap group), dilation, odd zero points,
+    # channels over several 16-channel chunks; 5x5 (25 taps) takes the VALU kernel
+    ("dw16_k2_zpodd", 1, 48, 9, 10, 48, 2, dict(group=48, pads=(0, 0, 1, 1), y_nhwc=1, x_nhwc=1,
+                                               x_zp=3, y_zp=7)),
+    ("dw16_dil2", 2, 64, 11, 12, 64, 3, dict(group=64, dil=(2, 2), pads=(2, 2, 2, 2), y_nhwc=1,
+                                             x_nhwc=1, y_zp=5, post_fn=1)),
+    ("dw16_c960_s2", 1, 960, 7, 8, 960, 3, dict(group=960, stride=(2, 2), pads=(1, 1, 1, 1),
+                                                y_nhwc=1, x_nhwc=1)),
+    ("dw_k5_valu", 1, 32, 9, 9, 32, 5, dict(group=32, pads=(2, 2, 2, 2), y_nhwc=1, x_nhwc=1)),
+    # channel counts off the 16-byte grid run on an x_zp-padded copy
+    ("cpad_c8_3x3", 2, 8, 10, 11, 40, 3, dict(pads=(1, 1, 1, 1), x_nhwc=1, y_nhwc=1, y_zp=9)),
+    ("cpad_c24_wzp", 1, 24, 7, 9, 32, 1, dict(x_nhwc=1, y_nhwc=1, w_zp=(5,), y_zp=2)),
 ]
 
 
