@@ -4,6 +4,8 @@
 Prints ONE JSON line (driver contract). Workloads:
   mobilenetv2 cfg4: MobileNetV2 int8 QDQ graph, batch 256 (depthwise VALU path
             against the pointwise MFMA GEMM); value = images/s
+  bert      cfg5: BERT-base int8 encoder, 12 layers, batch 64, seq 128;
+            value = sequences/s
   resnet50  cfg3 (default, the headline metric): ResNet-50 v1.5 int8 QDQ graph,
             batch 256, 224x224, run through the C++ host framework (QDQ
             fusion, NHWC layouts, HIP operators); value = images/s
@@ -277,6 +279,106 @@ def run_model(args, dev, model):
     )
 
 
+def run_bert(args, dev):
+    """cfg5: BERT-base int8 encoder, 12 layers, batch 64, seq 128."""
+    import numpy as np
+    import torch
+
+    from nnr_amd import graph as G, synth
+    from oracle import graph_oracle
+    from oracle import pyoracle as O
+
+    B = 64 if args.batch == 256 else args.batch
+    S, L = 128, 12
+    g = synth.bert(batch=B, seq=S, layers=L)
+    rng = np.random.default_rng(20)
+    x = rng.uniform(-1.0, 1.0, (B, S, 768)).astype(np.float32)
+    s = G.Session(g)
+    s.set_input("input", x)
+    s.run()
+    torch.cuda.synchronize()
+    plan = s.plan()
+    fmt = lambda n: s.tensor_info(n)[3]
+    # parity gate: every QLinearMatMul of the first layer, recomputed by the
+    # oracle from the device's own inputs (dynamic scale / zero point
+    # included) on the first two sequences
+    ng = 2
+
+    def dev_slice(name):
+        t, _ = s.output(name)
+        return t[:ng] if t.ndim >= 1 and t.shape[0] == B else t
+
+    skip = {p["op"] for p in plan} - {"QLinearMatMul"}
+    env = graph_oracle.run_plan(plan, g, {}, fmt, source=dev_slice, skip_ops=skip,
+                                stop_after="l0_ffn2")
+    checked = 0
+    for p in plan:
+        if p["op"] == "QLinearMatMul" and p["outputs"][0] in env:
+            assert np.array_equal(dev_slice(p["outputs"][0]), env[p["outputs"][0]]), \
+                f"parity gate failed at {p['name']}"
+            checked += 1
+    assert checked == 6
+    ms = time_steps(s.run, args)
+    s.enable_profiling(True)
+    for _ in range(args.steps):
+        s.run()
+    torch.cuda.synchronize()
+    prof = s.profile()
+    s.enable_profiling(False)
+    kprof = profile_steps(s.run, args)
+    mm_ops = sum(r["ops"] for r in prof if r["op"] == "QLinearMatMul")
+    mm_bytes = sum(r["bytes"] for r in prof if r["op"] == "QLinearMatMul")
+    g_launches, g_ms = kprof["qgemm"]
+    per_step = g_launches / args.steps
+    layers = []
+    for r in prof:
+        t = r["ms"] / max(1, r["runs"])
+        row = {"name": r["name"], "op": r["op"], "branch": r["variant"], "ms": round(t, 4)}
+        if r["ops"]:
+            row["tops"] = round(r["ops"] / (t * 1e-3) / 1e12, 1)
+            row["pct_i8_peak"] = round(100 * row["tops"] / PEAK_I8_TOPS, 2)
+        else:
+            row["gbs"] = round(r["bytes"] / (t * 1e-3) / 1e9, 1)
+            row["pct_hbm"] = round(100 * row["gbs"] / PEAK_HBM_GBS, 2)
+        layers.append(row)
+    if args.layers_out:
+        with open(args.layers_out, "w") as f:
+            json.dump(layers, f, indent=1)
+    for row in layers:
+        print(json.dumps(row), file=sys.stderr)
+    rl = roofline(mm_ops / per_step, mm_bytes / per_step, g_ms / g_launches, kprof)
+    rl["traffic"], rl["traffic_source"] = None, None
+    rl["note"] = (f"achieved = algorithmic int8 ops of the {round(per_step)} QLinearMatMul launches of "
+                  "one step / their total kernel time (hipEvents per launch)")
+    # cpu baseline: the oracle replays a batch-1 copy of the same graph
+    g1 = synth.bert(batch=1, seq=S, layers=L)
+    plan1 = G.Session(g1, device=False).plan()
+    nthr = host_threads()
+    O.set_threads(nthr)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        graph_oracle.run_plan(plan1, g1, {"input": x[:1]}, lambda n: 0)
+        reps += 1
+        if time.perf_counter() - t0 > 5.0 or reps >= 5:
+            break
+    cpu_seq_s = reps / (time.perf_counter() - t0)
+    return dict(
+        metric="BERT-base int8 encoder sequences/sec (12 layers, B64, S128), 1 GPU",
+        value=round(B / (ms * 1e-3), 1), unit="sequences/s", ms_per_step=ms,
+        config={"workload": f"cfg5 BERT-base int8, 12 layers, hidden 768, 12 heads, FFN 3072, "
+                            f"seq {S}, batch {B} (72 QLinearMatMul on DynamicQuantizeLinear "
+                            "activations; fp32 attention, Softmax, LayerNorm, Gelu)",
+                "global_batch": B, "seq_len": S,
+                "int8_tops": round(mm_ops / (g_ms / args.steps * 1e-3) / 1e12, 1)},
+        roofline=rl,
+        cpu_baseline={"value": round(cpu_seq_s, 3), "unit": "sequences/s", "cores": nthr,
+                      "kind": "port", "sample": f"oracle replay of the fused plan on 1 sequence, "
+                                                f"{reps} runs (scalar C + OpenMP, numpy fp32 glue)"},
+        dtype="u8",
+    )
+
+
 def run_hbm_copy(args, dev):
     """Device-to-device copy of a known size through hipMemcpyAsync: the
     calibration kernel for the FETCH_SIZE / WRITE_SIZE counters and the
@@ -310,7 +412,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="resnet50",
-                    choices=["resnet50", "mobilenetv2", "qconv", "hbm_copy"])
+                    choices=["resnet50", "mobilenetv2", "bert", "qconv", "hbm_copy"])
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
     args = ap.parse_args()
@@ -322,6 +424,7 @@ def main():
     dev = torch.device("cuda:0")
     run = {"resnet50": lambda a, d: run_model(a, d, "resnet50"),
            "mobilenetv2": lambda a, d: run_model(a, d, "mobilenetv2"),
+           "bert": run_bert,
            "qconv": run_qconv, "hbm_copy": run_hbm_copy}[args.config]
     res = run(args, dev)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,

@@ -219,6 +219,29 @@ int nnrh_global_avgpool_f32(const float* x_dev, float* y_dev, int N, int C, int 
 int nnrh_gemm_f32(const float* a_dev, const float* b_dev, const float* c_dev, float* y_dev,
                   int M, int N, int K, int trans_a, int trans_b, float alpha, float beta,
                   int c_mode, void* stream);
+/* Batched Gemm / MatMul (src/backend/cpu/MatMul.cpp broadcasting over the
+ * leading axes): a, b, y advance by a/b/y_bstride elements per batch (0 =
+ * shared), c is broadcast as in nnrh_gemm_f32.                           */
+int nnrh_gemm_f32_batched(const float* a_dev, const float* b_dev, const float* c_dev, float* y_dev,
+                          int M, int N, int K, int trans_a, int trans_b, float alpha, float beta,
+                          int c_mode, int batch, long long a_bstride, long long b_bstride,
+                          long long y_bstride, void* stream);
+/* Add / Mul / Sub / Div (src/backend/cpu/binary_math.cpp), op 0..3:
+ * y = a op b, or b op a with b_first; b_mode 0 same shape, 1 scalar b,
+ * 2 b of D elements broadcast over the last axis (n % D == 0).            */
+int nnrh_binary_f32(int op, const float* a_dev, const float* b_dev, float* y_dev, size_t n, int D,
+                    int b_mode, int b_first, void* stream);
+/* Softmax over the last axis (src/backend/cpu/Softmax.cpp, opset 13). */
+int nnrh_softmax_f32(const float* x_dev, float* y_dev, size_t rows, int D, void* stream);
+/* LayerNormalization over the last axis (src/backend/cpu/LayerNormalization.cpp:
+ * mean, variance of the row, (x - mean) / sqrt(var + eps) * gamma + beta). */
+int nnrh_layernorm_f32(const float* x_dev, const float* gamma_dev, const float* beta_dev,
+                       float* y_dev, size_t rows, int D, float eps, void* stream);
+/* Gelu, approximate = "none" (src/backend/cpu/Gelu.cpp:43-47). */
+int nnrh_gelu_f32(const float* x_dev, float* y_dev, size_t n, void* stream);
+/* Transpose (src/backend/cpu/Transpose.cpp): ndim <= 6 input dims and perm. */
+int nnrh_transpose_f32(const float* x_dev, float* y_dev, int ndim, const int* dims_host,
+                       const int* perm_host, void* stream);
 /* Clip / Relu (src/backend/cpu/Clip.cpp, Relu.cpp): y = min(max(x, lo), hi) */
 int nnrh_clip_f32(const float* x_dev, float* y_dev, size_t n, float lo, float hi, void* stream);
 

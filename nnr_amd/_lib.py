@@ -30,6 +30,8 @@ EXPORTS = [
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
     "nnrh_dynamic_quantize_linear", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
     "nnrh_nchw_to_nhwc_u8", "nnrh_global_avgpool_f32", "nnrh_gemm_f32", "nnrh_clip_f32",
+    "nnrh_gemm_f32_batched", "nnrh_binary_f32", "nnrh_softmax_f32", "nnrh_layernorm_f32",
+    "nnrh_gelu_f32", "nnrh_transpose_f32",
 ]
 
 
@@ -123,6 +125,12 @@ def lib():
         "nnrh_global_avgpool_f32": (i, [vp, vp, i, i, i, i, vp]),
         "nnrh_gemm_f32": (i, [vp, vp, vp, vp, i, i, i, i, i, f, f, i, vp]),
         "nnrh_clip_f32": (i, [vp, vp, sz, f, f, vp]),
+        "nnrh_gemm_f32_batched": (i, [vp, vp, vp, vp, i, i, i, i, i, f, f, i, i, ll, ll, ll, vp]),
+        "nnrh_binary_f32": (i, [i, vp, vp, vp, sz, i, i, i, vp]),
+        "nnrh_softmax_f32": (i, [vp, vp, sz, i, vp]),
+        "nnrh_layernorm_f32": (i, [vp, vp, vp, vp, sz, i, f, vp]),
+        "nnrh_gelu_f32": (i, [vp, vp, sz, vp]),
+        "nnrh_transpose_f32": (i, [vp, vp, i, P(i), P(i), vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

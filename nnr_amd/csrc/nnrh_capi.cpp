@@ -917,6 +917,7 @@ extern "C" int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a, long long a_bst
     g.y = y;
     g.alpha_zp_dev = a_zp_dev;
     g.cm_a_scale_dev = a_scale_dev;
+    if (a_zp_dev) g.c0 = nullptr;   // the column term needs the zero point of this call
     if (g.beta != 0) {
         if (h->rowsum_cap < batch) {
             dfree(h->rowsum);
@@ -1131,6 +1132,61 @@ extern "C" int nnrh_gemm_f32(const float* a, const float* b, const float* cb, fl
         return set_err(NNRH_ERR_INVALID, "gemm_f32: bad args");
     ProfScope ps("gemm_f32", S(stream));
     HIP_TRY(launch_gemm_f32(a, b, cb, y, M, N, K, ta, tb, alpha, beta, c_mode, S(stream)), "gemm_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_gemm_f32_batched(const float* a, const float* b, const float* cb, float* y, int M,
+                                     int N, int K, int ta, int tb, float alpha, float beta, int c_mode,
+                                     int batch, long long a_bstride, long long b_bstride,
+                                     long long y_bstride, void* stream) {
+    if (!a || !b || !y || M <= 0 || N <= 0 || K <= 0 || batch <= 0 || c_mode < 0 || c_mode > 4 ||
+        (c_mode && !cb))
+        return set_err(NNRH_ERR_INVALID, "gemm_f32_batched: bad args");
+    ProfScope ps("gemm_f32", S(stream));
+    HIP_TRY(launch_gemm_f32_batched(a, b, cb, y, M, N, K, ta, tb, alpha, beta, c_mode, batch, a_bstride,
+                                    b_bstride, y_bstride, S(stream)),
+            "gemm_f32_batched");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_binary_f32(int op, const float* a, const float* b, float* y, size_t n, int D,
+                               int b_mode, int b_first, void* stream) {
+    if (n && (!a || !b || !y)) return set_err(NNRH_ERR_INVALID, "binary_f32: NULL");
+    if (op < 0 || op > 3 || b_mode < 0 || b_mode > 2 || (b_mode == 2 && (D <= 0 || n % (size_t)D)))
+        return set_err(NNRH_ERR_INVALID, "binary_f32: op %d mode %d D %d", op, b_mode, D);
+    ProfScope ps("binary_f32", S(stream));
+    HIP_TRY(launch_binary_f32(a, b, y, (long long)n, D, b_mode, op, b_first, S(stream)), "binary_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_softmax_f32(const float* x, float* y, size_t rows, int D, void* stream) {
+    if (rows && (!x || !y || D <= 0)) return set_err(NNRH_ERR_INVALID, "softmax_f32: bad args");
+    ProfScope ps("softmax_f32", S(stream));
+    HIP_TRY(launch_softmax_f32(x, y, (long long)rows, D, S(stream)), "softmax_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y,
+                                  size_t rows, int D, float eps, void* stream) {
+    if (rows && (!x || !gamma || !y || D <= 0)) return set_err(NNRH_ERR_INVALID, "layernorm_f32: bad args");
+    ProfScope ps("layernorm_f32", S(stream));
+    HIP_TRY(launch_layernorm_f32(x, gamma, beta, y, (long long)rows, D, eps, S(stream)), "layernorm_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_gelu_f32(const float* x, float* y, size_t n, void* stream) {
+    if (n && (!x || !y)) return set_err(NNRH_ERR_INVALID, "gelu_f32: NULL");
+    ProfScope ps("gelu_f32", S(stream));
+    HIP_TRY(launch_gelu_f32(x, y, (long long)n, S(stream)), "gelu_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_transpose_f32(const float* x, float* y, int ndim, const int* dims, const int* perm,
+                                  void* stream) {
+    if (!x || !y || !dims || !perm || ndim < 1 || ndim > 6)
+        return set_err(NNRH_ERR_INVALID, "transpose_f32: bad args");
+    ProfScope ps("transpose_f32", S(stream));
+    HIP_TRY(launch_transpose_f32(x, y, ndim, dims, perm, S(stream)), "transpose_f32");
     return NNRH_OK;
 }
 

@@ -17,6 +17,16 @@ hipError_t launch_gemm_f32_batched(const float* A, const float* B, const float* 
                                    int N, int K, int transA, int transB, float alpha, float beta,
                                    int c_mode, int batch, long long a_bstride, long long b_bstride,
                                    long long y_bstride, hipStream_t s);
+// op: 0 add, 1 mul, 2 sub, 3 div; b_mode: 0 same shape, 1 scalar, 2 last-axis
+// vector of D; b_first: compute b (op) a
+hipError_t launch_binary_f32(const float* a, const float* b, float* y, long long n, int D, int b_mode,
+                             int op, int b_first, hipStream_t s);
+hipError_t launch_softmax_f32(const float* x, float* y, long long rows, int D, hipStream_t s);
+hipError_t launch_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y,
+                                long long rows, int D, float eps, hipStream_t s);
+hipError_t launch_gelu_f32(const float* x, float* y, long long n, hipStream_t s);
+hipError_t launch_transpose_f32(const float* x, float* y, int ndim, const int* in_dims, const int* perm,
+                                hipStream_t s);
 hipError_t launch_clip_f32(const float* x, float* y, long long n, float lo, float hi,
                            hipStream_t s);
 

@@ -5,6 +5,10 @@
 //   GlobalAveragePool (src/backend/cpu/global_pool.cpp), NCHW or NHWC input
 //   Gemm / MatMul     (src/backend/cpu/Gemm.cpp, MatMul.cpp), row-major, through rocBLAS
 //   Clip / Relu       (src/backend/cpu/Clip.cpp, Relu.cpp)
+//   Add / Mul / Sub / Div with scalar or last-axis broadcast (binary_math.cpp)
+//   Softmax, LayerNormalization over the last axis, Gelu (erf form), Transpose
+//   (the BERT encoder's fp32 glue: Softmax.cpp, LayerNormalization.cpp,
+//   Gelu.cpp, Transpose.cpp)
 #include "nnrh_f32.h"
 
 #include <rocblas/rocblas.h>
@@ -139,6 +143,163 @@ hipError_t launch_clip_f32(const float* x, float* y, long long n, float lo, floa
     long long b = (n + 255) / 256;
     if (b > 65536) b = 65536;
     hipLaunchKernelGGL(clip_f32_kernel, dim3((unsigned)b), dim3(256), 0, s, x, y, n, lo, hi);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// y = a (op) b; b_mode: 0 same shape, 1 scalar, 2 broadcast over the last axis
+// (b has D elements); b_first swaps the operands (b op a) for Sub / Div.
+__global__ __launch_bounds__(256) void binary_f32_kernel(const float* __restrict a,
+                                                         const float* __restrict b,
+                                                         float* __restrict y, long long n, int D,
+                                                         int b_mode, int op, int b_first) {
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (long long)gridDim.x * 256) {
+        const float av = a[i];
+        const float bv = b_mode == 0 ? b[i] : (b_mode == 1 ? b[0] : b[i % D]);
+        const float l = b_first ? bv : av, r = b_first ? av : bv;
+        float v;
+        if (op == 0) v = l + r;
+        else if (op == 1) v = l * r;
+        else if (op == 2) v = l - r;
+        else v = l / r;
+        y[i] = v;
+    }
+}
+
+hipError_t launch_binary_f32(const float* a, const float* b, float* y, long long n, int D, int b_mode,
+                             int op, int b_first, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    long long blocks = (n + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(binary_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a, b, y, n,
+                       D > 0 ? D : 1, b_mode, op, b_first);
+    return hipGetLastError();
+}
+
+// softmax over rows of D (one wave per row): exp(x - max) / sum
+__global__ __launch_bounds__(256) void softmax_f32_kernel(const float* __restrict x,
+                                                          float* __restrict y, long long rows, int D) {
+    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + row * D;
+    float* yr = y + row * D;
+    float m = -INFINITY;
+    for (int i = lane; i < D; i += 64) m = fmaxf(m, xr[i]);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float sum = 0.0f;
+    for (int i = lane; i < D; i += 64) sum += expf(xr[i] - m);
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    const float inv = 1.0f / sum;
+    for (int i = lane; i < D; i += 64) yr[i] = expf(xr[i] - m) * inv;
+}
+
+hipError_t launch_softmax_f32(const float* x, float* y, long long rows, int D, hipStream_t s) {
+    if (rows <= 0 || D <= 0) return hipSuccess;
+    hipLaunchKernelGGL(softmax_f32_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, y, rows,
+                       D);
+    return hipGetLastError();
+}
+
+// LayerNormalization over rows of D (one wave per row), two passes over the
+// row: mean, then the mean of squared deviations
+__global__ __launch_bounds__(256) void layernorm_f32_kernel(const float* __restrict x,
+                                                            const float* __restrict gamma,
+                                                            const float* __restrict beta,
+                                                            float* __restrict y, long long rows, int D,
+                                                            float eps) {
+    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + row * D;
+    float* yr = y + row * D;
+    float sum = 0.0f;
+    for (int i = lane; i < D; i += 64) sum += xr[i];
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    const float mean = sum / (float)D;
+    float sq = 0.0f;
+    for (int i = lane; i < D; i += 64) {
+        const float d = xr[i] - mean;
+        sq += d * d;
+    }
+    for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
+    const float inv = 1.0f / sqrtf(sq / (float)D + eps);
+    for (int i = lane; i < D; i += 64) {
+        const float v = (xr[i] - mean) * inv * gamma[i];
+        yr[i] = beta ? v + beta[i] : v;
+    }
+}
+
+hipError_t launch_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y,
+                                long long rows, int D, float eps, hipStream_t s) {
+    if (rows <= 0 || D <= 0) return hipSuccess;
+    hipLaunchKernelGGL(layernorm_f32_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, gamma,
+                       beta, y, rows, D, eps);
+    return hipGetLastError();
+}
+
+// Gelu, erf form: 0.5 x (1 + erf(x / sqrt(2)))
+__global__ __launch_bounds__(256) void gelu_f32_kernel(const float* __restrict x, float* __restrict y,
+                                                       long long n) {
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (long long)gridDim.x * 256) {
+        const float v = x[i];
+        y[i] = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    }
+}
+
+hipError_t launch_gelu_f32(const float* x, float* y, long long n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    long long blocks = (n + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(gelu_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+// Transpose of a tensor of up to 6 axes: out axis i is in axis perm[i]
+struct TransposeArgs {
+    int ndim;
+    long long out_dims[6];
+    long long in_strides_for_out[6];   // stride in x of out axis i
+};
+
+__global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restrict x,
+                                                            float* __restrict y, long long n,
+                                                            TransposeArgs t) {
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (long long)gridDim.x * 256) {
+        long long r = i, src = 0;
+        for (int d = t.ndim - 1; d >= 0; --d) {
+            const long long c = r % t.out_dims[d];
+            r /= t.out_dims[d];
+            src += c * t.in_strides_for_out[d];
+        }
+        y[i] = x[src];
+    }
+}
+
+hipError_t launch_transpose_f32(const float* x, float* y, int ndim, const int* in_dims, const int* perm,
+                                hipStream_t s) {
+    if (ndim < 1 || ndim > 6) return hipErrorInvalidValue;
+    TransposeArgs t{};
+    t.ndim = ndim;
+    long long in_strides[6];
+    long long st = 1, n = 1;
+    for (int d = ndim - 1; d >= 0; --d) {
+        in_strides[d] = st;
+        st *= in_dims[d];
+    }
+    for (int d = 0; d < ndim; ++d) {
+        if (perm[d] < 0 || perm[d] >= ndim) return hipErrorInvalidValue;
+        t.out_dims[d] = in_dims[perm[d]];
+        t.in_strides_for_out[d] = in_strides[perm[d]];
+        n *= t.out_dims[d];
+    }
+    if (n <= 0) return hipSuccess;
+    long long blocks = (n + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(transpose_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, n, t);
     return hipGetLastError();
 }
 

@@ -153,6 +153,18 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
 
     const int nk = g.Kp >> 6;
     const uint32_t xmask = (uint32_t)g.a_xor * 0x01010101u;
+    // zero-point column term from the activation zero point (host value or,
+    // after DynamicQuantizeLinear, one byte in device memory)
+    int alpha = g.alpha;
+    if (g.alpha_zp_dev)
+        alpha = (g.a_xor ? (int)*(const uint8_t*)g.alpha_zp_dev : (int)*(const int8_t*)g.alpha_zp_dev) - g.a_sub;
+    const uint32_t neg_alpha = 0u - (uint32_t)alpha;
+    // RQ-D combined scale, fl(fl(a_s * b_s) / y_s), with a device a_scale
+    float cm = g.cm;
+    if (EPI == EPI_RQD && g.cm_a_scale_dev) {
+        const float t1 = *g.cm_a_scale_dev * g.cm_b;
+        cm = t1 / g.cm_y;
+    }
     const uint8_t* pad16 = (const uint8_t*)&kPadTable.w[(g.pad_byte & 0xff) * 4];
     const int sp_out = g.oH * g.oW;
     // this thread's 16-byte chunk of a 64-byte row (pre-swizzled so the LDS
@@ -258,12 +270,14 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
             const int col4 = i - arr * (BN / 4);
             int c = p_n0 + col4 * 4;
             c = c + 4 <= g.Np ? c : g.Np - 4;
+            // array 0 is c0, or colsum when the zero point arrives with the
+            // call; lanes past the last array reload array 0 (never read back)
+            const void* base0 = g.c0 ? (const void*)g.c0 : (const void*)g.colsum;
             const void* base;
-            if (arr == 0) base = g.c0;
+            if (arr == 0 || arr >= NP) base = base0;
             else if (EPI == EPI_RQB) base = g.os;
             else if (arr == 1) base = g.cs;
             else base = g.bf;
-            if (arr >= NP) base = g.c0;
             const uint8_t* src = (const uint8_t*)base + (p_pbase + c) * 4;
             dma16(src, lds + S * STAGE + (p_tseq % S) * PSLOT + wave * 1024);
         }
@@ -388,7 +402,7 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                                 b = rqc_fast(v, __int_as_float(p0[tn][q]), __int_as_float(p1[tn][q]),
                                              g.inv_y, g.y_zp, g.L, g.hi);
                             else
-                                b = rqd_fast(v, g.cm, g.y_zp, g.lo, g.hi);
+                                b = rqd_fast(v, cm, g.y_zp, g.lo, g.hi);
                             w |= (b & 0xffu) << (8 * q);
                         }
                         packed[tn] = w;
@@ -480,12 +494,17 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
 
         if (c_kt == 0) {
             // the tile's constants landed with its first K-step: start the
-            // accumulators at c0[n] (this lane's 16 columns)
+            // accumulators at c0[n] (this lane's 16 columns), or at
+            // -alpha * colsum[n] when the zero point is only known now
             const uint8_t* ps = lds + S * STAGE + (c_tseq % S) * PSLOT;
             const int nl = wn * 64 + 16 * fchunk;
 #pragma unroll
             for (int tn = 0; tn < 4; ++tn) {
-                const v4i c = *(const v4i*)(ps + (nl + 4 * tn) * 4);
+                v4i c = *(const v4i*)(ps + (nl + 4 * tn) * 4);
+                if (!g.c0) {
+                    c.x = (int)(neg_alpha * (uint32_t)c.x); c.y = (int)(neg_alpha * (uint32_t)c.y);
+                    c.z = (int)(neg_alpha * (uint32_t)c.z); c.w = (int)(neg_alpha * (uint32_t)c.w);
+                }
 #pragma unroll
                 for (int tm = 0; tm < 4; ++tm) acc[tm][tn] = c;
             }
@@ -595,11 +614,18 @@ bool qgemm_dma_eligible(const GemmArgs& g, int vec) {
         return g.Np >= 4 && (g.Np & 3) == 0;
     }
     if (vec != 16) return false;
-    if (g.c0 == nullptr || g.alpha_zp_dev != nullptr || g.rowsum != nullptr) return false;
+    // per-column constant: c0, or -alpha * colsum (GEMMs without bias)
+    if (g.rowsum != nullptr) return false;
+    if (g.c0 == nullptr && (g.colsum == nullptr || (g.epi != EPI_RQD && g.epi != EPI_I32))) return false;
+    if (g.c0 == nullptr && 256LL * 128LL * (long long)g.Kp + 16384LL * (long long)g.Kp >= 0x7fffffffLL)
+        return false;
+    if (g.c0 != nullptr && g.alpha_zp_dev != nullptr) return false;
+    // every per-column array the epilogue stages must exist
+    if (g.epi == EPI_RQB && g.os == nullptr) return false;
+    if ((g.epi == EPI_RQA || g.epi == EPI_RQC) && (g.cs == nullptr || g.bf == nullptr)) return false;
     if (g.tail != TAIL_NONE) return false;
     if (g.epi == EPI_RQB && g.bprime_from < g.N) return false;
     if (g.epi == EPI_RQC) return false;   // RQ-C is the first layer's epilogue
-    if (g.epi == EPI_RQD && g.cm_a_scale_dev != nullptr) return false;
     if (g.Np < 4 || (g.Np & 3)) return false;
     if (g.H > 0 && (g.C % 16 || g.Cs % 16)) return false;
     if (g.H == 0 && (g.K % 16 || g.lda % 16)) return false;

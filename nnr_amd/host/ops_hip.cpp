@@ -569,6 +569,169 @@ struct Clip_hip : operator_t {
     }
 };
 
+// ===========================================================================
+// fp32 glue of the transformer encoder
+
+// Add / Mul / Sub / Div (src/backend/cpu/binary_math.cpp) with the broadcasts
+// the graphs use: same shape, a scalar operand, or a vector over the last axis
+struct Binary_hip : operator_t {
+    int op = 0;   // 0 add, 1 mul, 2 sub, 3 div
+    int b_mode = 0, D = 1;
+    bool swap = false;
+    bool init() override { return inputs.size() == 2 && outputs.size() == 1; }
+    static bool is_last_axis_vector(const tensor_t* v, const tensor_t* full) {
+        if (full->ndim() < 1 || v->ndata != (size_t)full->dims.back()) return false;
+        for (int i = 0; i + 1 < v->ndim(); ++i)
+            if (v->dims[i] != 1) return false;
+        return v->ndim() >= 1 && v->dims.back() == full->dims.back();
+    }
+    bool reshape() override {
+        tensor_t *a = inputs[0], *b = inputs[1], *y = outputs[0];
+        if (a->type != NNR_DATA_TYPE_FLOAT32 || b->type != NNR_DATA_TYPE_FLOAT32)
+            return bad(this, "fp32 only (int8 additions are fused to QLinearAdd)");
+        swap = a->ndata < b->ndata;
+        const tensor_t* full = swap ? b : a;
+        const tensor_t* other = swap ? a : b;
+        if (full->dims == other->dims) b_mode = 0;
+        else if (other->ndata == 1) b_mode = 1;
+        else if (is_last_axis_vector(other, full)) { b_mode = 2; D = full->dims.back(); }
+        else return bad(this, "unsupported broadcast");
+        return y->reshape(full->dims, NNR_DATA_TYPE_FLOAT32);
+    }
+    bool exec() override {
+        tensor_t *a = inputs[0], *b = inputs[1];
+        const float* full = (const float*)(swap ? b : a)->data;
+        const float* other = (const float*)(swap ? a : b)->data;
+        return ok(this, nnrh_binary_f32(op, full, other, (float*)outputs[0]->data, outputs[0]->ndata, D, b_mode,
+                                        swap ? 1 : 0, ctx->stream));
+    }
+};
+template <int OP>
+operator_t* make_binary(int) {
+    auto* b = new Binary_hip();
+    b->op = OP;
+    return b;
+}
+
+// Softmax over the last axis (src/backend/cpu/Softmax.cpp, opset 13)
+struct Softmax_hip : operator_t {
+    bool init() override { return inputs.size() == 1 && outputs.size() == 1; }
+    bool reshape() override {
+        tensor_t* x = inputs[0];
+        int axis = (int)attribute("axis", -1);
+        if (axis < 0) axis += x->ndim();
+        if (axis != x->ndim() - 1 || x->type != NNR_DATA_TYPE_FLOAT32)
+            return bad(this, "fp32 softmax over the last axis only");
+        return outputs[0]->reshape(x->dims, x->type);
+    }
+    bool exec() override {
+        tensor_t* x = inputs[0];
+        const int D = x->dims.back();
+        return ok(this, nnrh_softmax_f32((const float*)x->data, (float*)outputs[0]->data, x->ndata / D, D,
+                                         ctx->stream));
+    }
+};
+
+// LayerNormalization over the last axis (src/backend/cpu/LayerNormalization.cpp)
+struct LayerNormalization_hip : operator_t {
+    bool init() override { return inputs.size() >= 2 && inputs.size() <= 3 && outputs.size() >= 1; }
+    bool reshape() override {
+        tensor_t* x = inputs[0];
+        int axis = (int)attribute("axis", -1);
+        if (axis < 0) axis += x->ndim();
+        if (axis != x->ndim() - 1 || x->type != NNR_DATA_TYPE_FLOAT32)
+            return bad(this, "fp32 layer norm over the last axis only");
+        if (outputs.size() > 1 && (outputs[1] || (outputs.size() > 2 && outputs[2])))
+            return bad(this, "Mean / InvStdDev outputs are not produced");
+        if (inputs[1]->ndata != (size_t)x->dims.back()) return bad(this, "scale shape");
+        return outputs[0]->reshape(x->dims, x->type);
+    }
+    bool exec() override {
+        tensor_t* x = inputs[0];
+        tensor_t* bias = in(this, 2);
+        const int D = x->dims.back();
+        return ok(this, nnrh_layernorm_f32((const float*)x->data, (const float*)inputs[1]->data,
+                                           bias ? (const float*)bias->data : nullptr, (float*)outputs[0]->data,
+                                           x->ndata / D, D, attribute_f("epsilon", 1e-5f), ctx->stream));
+    }
+};
+
+// Gelu (src/backend/cpu/Gelu.cpp), approximate = "none"
+struct Gelu_hip : operator_t {
+    bool init() override { return inputs.size() == 1 && outputs.size() == 1; }
+    bool reshape() override {
+        if (attribute_s("approximate", "none") != "none") return bad(this, "tanh approximation");
+        if (inputs[0]->type != NNR_DATA_TYPE_FLOAT32) return bad(this, "fp32 only");
+        return operator_t::reshape();
+    }
+    bool exec() override {
+        return ok(this, nnrh_gelu_f32((const float*)inputs[0]->data, (float*)outputs[0]->data, inputs[0]->ndata,
+                                      ctx->stream));
+    }
+};
+
+// Transpose (src/backend/cpu/Transpose.cpp), fp32, up to 6 axes
+struct Transpose_hip : operator_t {
+    std::vector<int> perm;
+    bool init() override { return inputs.size() == 1 && outputs.size() == 1; }
+    bool reshape() override {
+        tensor_t* x = inputs[0];
+        if (x->type != NNR_DATA_TYPE_FLOAT32 || x->ndim() > 6) return bad(this, "fp32, <= 6 axes");
+        perm.clear();
+        for (auto v : attribute_ints("perm")) perm.push_back((int)v);
+        if (perm.empty())
+            for (int i = x->ndim() - 1; i >= 0; --i) perm.push_back(i);
+        if ((int)perm.size() != x->ndim()) return bad(this, "perm length");
+        std::vector<int> d;
+        for (int p : perm) {
+            if (p < 0 || p >= x->ndim()) return bad(this, "perm value");
+            d.push_back(x->dims[p]);
+        }
+        return outputs[0]->reshape(d, x->type);
+    }
+    bool exec() override {
+        tensor_t* x = inputs[0];
+        return ok(this, nnrh_transpose_f32((const float*)x->data, (float*)outputs[0]->data, x->ndim(),
+                                           x->dims.data(), perm.data(), ctx->stream));
+    }
+};
+
+// MatMul (src/backend/cpu/MatMul.cpp), fp32: [..., M, K] x [..., K, N] with
+// equal leading axes, or a 2-D right operand shared by every batch
+struct MatMul_hip : operator_t {
+    int M = 0, N = 0, K = 0, batch = 1;
+    bool b_shared = false;
+    bool init() override { return inputs.size() == 2 && outputs.size() == 1; }
+    bool reshape() override {
+        tensor_t *a = inputs[0], *b = inputs[1];
+        if (a->type != NNR_DATA_TYPE_FLOAT32 || b->type != NNR_DATA_TYPE_FLOAT32)
+            return bad(this, "fp32 only (int8 MatMul is fused to QLinearMatMul)");
+        if (a->ndim() < 2 || b->ndim() < 2) return bad(this, "operands must have >= 2 axes");
+        M = a->dims[a->ndim() - 2];
+        K = a->dims[a->ndim() - 1];
+        N = b->dims[b->ndim() - 1];
+        if (b->dims[b->ndim() - 2] != K) return bad(this, "inner dimensions differ");
+        batch = 1;
+        for (int i = 0; i + 2 < a->ndim(); ++i) batch *= a->dims[i];
+        b_shared = b->ndim() == 2;
+        if (!b_shared) {
+            if (b->ndim() != a->ndim()) return bad(this, "batch broadcast");
+            for (int i = 0; i + 2 < a->ndim(); ++i)
+                if (a->dims[i] != b->dims[i]) return bad(this, "batch broadcast");
+        }
+        std::vector<int> d(a->dims.begin(), a->dims.end() - 1);
+        d.push_back(N);
+        return outputs[0]->reshape(d, NNR_DATA_TYPE_FLOAT32);
+    }
+    bool exec() override {
+        return ok(this, nnrh_gemm_f32_batched((const float*)inputs[0]->data, (const float*)inputs[1]->data, nullptr,
+                                              (float*)outputs[0]->data, M, N, K, 0, 0, 1.0f, 0.0f, 0, batch,
+                                              (long long)M * K, b_shared ? 0 : (long long)K * N,
+                                              (long long)M * N, ctx->stream));
+    }
+    double num_ops() const override { return 2.0 * batch * M * (double)N * K; }
+};
+
 template <typename T>
 operator_t* make(int) { return new T(); }
 operator_t* make_relu(int) {
@@ -592,6 +755,15 @@ const op_registrar_t reg[] = {
     {"Gemm", backend_t::HIP, make<Gemm_hip>},
     {"Relu", backend_t::HIP, make_relu},
     {"Clip", backend_t::HIP, make<Clip_hip>},
+    {"Add", backend_t::HIP, make_binary<0>},
+    {"Mul", backend_t::HIP, make_binary<1>},
+    {"Sub", backend_t::HIP, make_binary<2>},
+    {"Div", backend_t::HIP, make_binary<3>},
+    {"Softmax", backend_t::HIP, make<Softmax_hip>},
+    {"LayerNormalization", backend_t::HIP, make<LayerNormalization_hip>},
+    {"Gelu", backend_t::HIP, make<Gelu_hip>},
+    {"Transpose", backend_t::HIP, make<Transpose_hip>},
+    {"MatMul", backend_t::HIP, make<MatMul_hip>},
 };
 
 }  // namespace

@@ -201,3 +201,80 @@ def mobilenetv2(batch=256, hw=224, seed=4, num_classes=1000):
     g.node("Gemm", [fl, fw, fb], outputs="logits", name="fc", transB=1)
     g.outputs.append("logits")
     return g
+
+
+def bert(batch=64, seq=128, layers=12, hidden=768, heads=12, ffn=3072, seed=5):
+    """BERT-base-shaped int8 encoder (cfg5). Every projection is
+    DynamicQuantizeLinear -> DQ -> MatMul(DQ(W int8)) -> Q -> DQ -> + bias,
+    which the QDQ fusion turns into a QLinearMatMul reading the dynamic
+    uint8 activation scale / zero point from device memory. The weights are
+    N(0, 0.02) quantized per tensor: NNR's QLinearMatMul reads b_scale[0] only
+    (QLinearMatMul.cpp:118-119), so per-channel weight scales would not be
+    applied. Attention scores, Softmax, LayerNormalization and Gelu are fp32.
+    Input: seeded uniform token embeddings [batch, seq, hidden]."""
+    g = Graph()
+    rng = np.random.default_rng(seed)
+    dh = hidden // heads
+    g.inputs["input"] = (np.float32, (batch, seq, hidden))
+
+    def dynq(x_f, name):
+        xq, xs, xz = g.node("DynamicQuantizeLinear", [x_f], outputs=[name + "_xq", name + "_xs", name + "_xz"],
+                            name=name + "_dynq")
+        return g.node("DequantizeLinear", [xq, xs, xz], name=name + "_xdq")
+
+    def qlinear(x_f, din, dout, name, y_scale, xdq=None):
+        if xdq is None:
+            xdq = dynq(x_f, name)
+        w = rng.normal(0.0, 0.02, (din, dout)).astype(F32)
+        ws = F32(max(float(np.abs(w).max()) / 127.0, 1e-8))
+        wq = np.clip(np.rint(w / ws), -127, 127).astype(np.int8)
+        wdq = g.node("DequantizeLinear", [g.init(name + "_w", wq), g.init(name + "_ws", np.array(ws, F32)),
+                                          g.init(name + "_wz", np.array(0, np.int8))], name=name + "_wdq")
+        y = g.node("MatMul", [xdq, wdq], name=name)
+        ys = g.init(name + "_ys", np.array(y_scale, F32))
+        yz = g.init(name + "_yz", np.array(128, np.uint8))
+        yq = g.node("QuantizeLinear", [y, ys, yz], name=name + "_q")
+        ydq = g.node("DequantizeLinear", [yq, ys, yz], name=name + "_ydq")
+        b = g.init(name + "_b", rng.normal(0.0, 0.02, dout).astype(F32))
+        return g.node("Add", [ydq, b], name=name + "_bias")
+
+    def shape(name, dims):
+        return g.init(name, np.array(dims, np.int64))
+
+    x = "input"
+    for li in range(layers):
+        p = f"l{li}"
+        xdq = dynq(x, p + "_qkv")   # one dynamic quantization feeds Q, K and V
+        q = qlinear(x, hidden, hidden, p + "_q", 0.03, xdq)
+        k = qlinear(x, hidden, hidden, p + "_k", 0.03, xdq)
+        v = qlinear(x, hidden, hidden, p + "_v", 0.03, xdq)
+        heads4 = shape(p + "_heads", [batch, seq, heads, dh])
+        q4 = g.node("Transpose", [g.node("Reshape", [q, heads4], name=p + "_qr")], name=p + "_qt",
+                    perm=[0, 2, 1, 3])
+        kt = g.node("Transpose", [g.node("Reshape", [k, heads4], name=p + "_kr")], name=p + "_kt",
+                    perm=[0, 2, 3, 1])
+        v4 = g.node("Transpose", [g.node("Reshape", [v, heads4], name=p + "_vr")], name=p + "_vt",
+                    perm=[0, 2, 1, 3])
+        s = g.node("MatMul", [q4, kt], name=p + "_scores")
+        s = g.node("Mul", [s, g.init(p + "_scale", np.array(1.0 / np.sqrt(dh), F32))], name=p + "_scaled")
+        pr = g.node("Softmax", [s], name=p + "_softmax", axis=-1)
+        c = g.node("MatMul", [pr, v4], name=p + "_context")
+        c = g.node("Transpose", [c], name=p + "_ct", perm=[0, 2, 1, 3])
+        c = g.node("Reshape", [c, shape(p + "_merge", [batch, seq, hidden])], name=p + "_cr")
+        o = qlinear(c, hidden, hidden, p + "_o", 0.03)
+        h1 = g.node("LayerNormalization",
+                    [g.node("Add", [x, o], name=p + "_res1"), g.init(p + "_ln1_g", np.ones(hidden, F32)),
+                     g.init(p + "_ln1_b", np.zeros(hidden, F32))], name=p + "_ln1", axis=-1, epsilon=1e-12)
+        f = qlinear(h1, hidden, ffn, p + "_ffn1", 0.04)
+        f = g.node("Gelu", [f], name=p + "_gelu")
+        f2 = qlinear(f, ffn, hidden, p + "_ffn2", 0.04)
+        x = g.node("LayerNormalization",
+                   [g.node("Add", [h1, f2], name=p + "_res2"), g.init(p + "_ln2_g", np.ones(hidden, F32)),
+                    g.init(p + "_ln2_b", np.zeros(hidden, F32))], name=p + "_ln2", axis=-1, epsilon=1e-12)
+    g.outputs.append(x)
+    return g
+
+
+def bert_int8_ops(batch=64, seq=128, layers=12, hidden=768, ffn=3072):
+    """Algorithmic int8 ops of the projections of one forward pass."""
+    return 2.0 * batch * seq * layers * (4 * hidden * hidden + 2 * hidden * ffn)

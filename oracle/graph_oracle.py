@@ -17,16 +17,31 @@ def _nchw_to_phys(a, nhwc):
     return a.transpose(0, 2, 3, 1).copy() if nhwc and a.ndim == 4 else a
 
 
-def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None):
+def _erf(x):
+    from scipy.special import erf
+    return erf(x)
+
+
+def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, skip_ops=()):
     """plan: Session.plan(); fmt_of(name) -> 0/1 layout of a tensor.
-    Returns {tensor name: physical numpy array} of every produced tensor."""
+    Returns {tensor name: physical numpy array} of every produced tensor.
+
+    source: optional callable name -> array. When given, every node reads its
+    non-constant inputs through it (e.g. the device's own tensors), so each
+    node is checked on exactly the inputs the device saw and fp32 rounding
+    differences do not propagate. Nodes whose op is in skip_ops are not run
+    (their outputs must then come from source)."""
     init = graph.initializers
     env = {}
     for k, v in feeds.items():
         env[k] = v
 
     def val(name):
-        return env[name] if name in env else init[name]
+        if name in init:
+            return init[name]
+        if source is not None and name not in feeds:
+            return source(name)
+        return env[name]
 
     def scal(name, default=0):
         if not name:
@@ -35,11 +50,42 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None):
 
     for nd in plan:
         op, ins, outs = nd["op"], nd["inputs"], nd["outputs"]
+        if op in skip_ops:
+            continue
+        extra = {}
         if op == "QuantizeLinear":
             zdt = init[ins[2]].dtype if len(ins) > 2 and ins[2] else np.uint8
             y = O.quantize_linear(val(ins[0]), float(scal(ins[1])), int(scal(ins[2])), zdt)
         elif op == "DequantizeLinear":
             y = O.dequantize_linear(val(ins[0]), float(scal(ins[1])), int(scal(ins[2])))
+        elif op == "DynamicQuantizeLinear":
+            y, ys, yz = O.dynamic_quantize_linear(val(ins[0]))
+            extra = {outs[1]: np.array(ys, np.float32), outs[2]: np.array(yz, np.uint8)}
+        elif op in ("Add", "Mul", "Sub", "Div"):
+            a_, b_ = val(ins[0]).astype(np.float32), val(ins[1]).astype(np.float32)
+            y = {"Add": np.add, "Mul": np.multiply, "Sub": np.subtract, "Div": np.divide}[op](a_, b_)
+            y = y.astype(np.float32)
+        elif op == "Softmax":
+            x = val(ins[0]).astype(np.float64)
+            e = np.exp(x - x.max(axis=-1, keepdims=True))
+            y = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+        elif op == "LayerNormalization":
+            a = graph.node_by_name(nd["name"]).attrs
+            x = val(ins[0]).astype(np.float64)
+            mean = x.mean(axis=-1, keepdims=True)
+            var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+            yv = (x - mean) / np.sqrt(var + a.get("epsilon", 1e-5)) * val(ins[1]).astype(np.float64)
+            if len(ins) > 2 and ins[2]:
+                yv = yv + val(ins[2]).astype(np.float64)
+            y = yv.astype(np.float32)
+        elif op == "Gelu":
+            x = val(ins[0]).astype(np.float64)
+            y = (0.5 * x * (1.0 + _erf(x / np.sqrt(2.0)))).astype(np.float32)
+        elif op == "Transpose":
+            perm = graph.node_by_name(nd["name"]).attrs.get("perm")
+            y = np.ascontiguousarray(np.transpose(val(ins[0]), perm))
+        elif op == "MatMul":
+            y = np.matmul(val(ins[0]).astype(np.float64), val(ins[1]).astype(np.float64)).astype(np.float32)
         elif op == "QLinearConv":
             src = graph.node_by_name(nd["name"])
             a = src.attrs
@@ -69,7 +115,7 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None):
                                   float(scal(ai[4])), int(scal(ai[5])), float(scal(ai[6])),
                                   int(scal(ai[7])))
         elif op == "QLinearMatMul":
-            y = O.qlinear_matmul(val(ins[0]), float(scal(ins[1])), int(scal(ins[2])),
+            y = O.qlinear_matmul(val(ins[0]), np.float32(scal(ins[1])), int(scal(ins[2])),
                                  init[ins[3]], float(scal(ins[4])), int(scal(ins[5])),
                                  float(scal(ins[6])), int(scal(ins[7])), init[ins[7]].dtype)
         elif op == "QLinearAdd":
@@ -119,6 +165,7 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None):
         else:
             raise NotImplementedError(op)
         env[outs[0]] = y
+        env.update(extra)
         if stop_after and nd["name"] == stop_after:
             break
     return env

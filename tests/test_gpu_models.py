@@ -95,3 +95,52 @@ def test_mobilenetv2_small_input(dev):
     rng = np.random.default_rng(18)
     x = rng.random((3, 3, 96, 96), dtype=np.float32)
     check_graph(g, {"input": x}, "logits")
+
+
+def check_graph_per_node(g, feeds, atol=1e-3, rtol=1e-3):
+    """Every node of the executed plan, recomputed by the oracle from the
+    device's own input tensors: int8 outputs bit-exact, fp32 outputs within
+    the reference's tolerance. Used where fp32 nodes feed dynamic
+    quantization, so rounding noise must not propagate between nodes."""
+    s = G.Session(g)
+    for k, v in feeds.items():
+        s.set_input(k, v)
+    s.run()
+    plan = s.plan()
+    fmt = lambda n: s.tensor_info(n)[3]
+    cache = {}
+
+    def dev(name):
+        if name not in cache:
+            cache[name] = s.output(name)[0]
+        return cache[name]
+
+    env = graph_oracle.run_plan(plan, g, feeds, fmt, source=dev)
+    n_int = n_f32 = 0
+    for p in plan:
+        for o in p["outputs"]:
+            if not o or o not in env:
+                continue
+            d, ref = dev(o), env[o]
+            assert d.shape == np.shape(ref), (p["name"], o, d.shape, np.shape(ref))
+            if d.dtype in (np.uint8, np.int8):
+                mism = np.count_nonzero(d != ref)
+                assert mism == 0, f"{p['name']} ({p['op']}) {o}: {mism} of {d.size} differ"
+                n_int += 1
+            else:
+                np.testing.assert_allclose(d, ref, atol=atol, rtol=rtol, err_msg=f"{p['name']} {o}")
+                n_f32 += 1
+    return plan, n_int, n_f32
+
+
+def test_bert_per_node(dev):
+    """cfg5 structure (2 layers, batch 2, seq 64): DynamicQuantizeLinear ->
+    QLinearMatMul with device-side activation scale / zero point, fp32
+    attention (batched MatMul, Softmax), LayerNormalization, Gelu."""
+    g = synth.bert(batch=2, seq=64, layers=2)
+    rng = np.random.default_rng(19)
+    x = rng.uniform(-1.0, 1.0, (2, 64, 768)).astype(np.float32)
+    plan, n_int, n_f32 = check_graph_per_node(g, {"input": x})
+    ops = [p["op"] for p in plan]
+    assert ops.count("QLinearMatMul") == 12 and ops.count("DynamicQuantizeLinear") == 8
+    assert n_int >= 12 + 8 * 2 and n_f32 > 0

@@ -106,3 +106,16 @@ def test_mobilenetv2_fusion_and_branches():
     for p in plan:
         if p["op"] in ("QLinearConv", "QLinearAdd"):
             assert fmt(p["outputs"][0]) == 1, p["name"]
+
+
+def test_bert_fusion():
+    """cfg5: each projection's DynQ -> DQ -> MatMul -> Q becomes a
+    QLinearMatMul (6 per layer, the Q/K/V ones sharing one
+    DynamicQuantizeLinear); attention stays fp32 MatMul."""
+    g = synth.bert(batch=2, seq=16, layers=2)
+    s = G.Session(g, device=False)
+    ops = collections.Counter(p["op"] for p in s.plan())
+    assert ops["QLinearMatMul"] == 12 and ops["DynamicQuantizeLinear"] == 8
+    assert ops["MatMul"] == 4 and ops["Softmax"] == 2 and ops["LayerNormalization"] == 4
+    assert ops["Gelu"] == 2 and "QuantizeLinear" not in ops
+    assert s.fusion_stat("qdq_compute") == 12
