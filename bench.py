@@ -9,6 +9,7 @@ Prints ONE JSON line (driver contract). Workloads:
   resnet50  cfg3 (default, the headline metric): ResNet-50 v1.5 int8 QDQ graph,
             batch 256, 224x224, run through the C++ host framework (QDQ
             fusion, NHWC layouts, HIP operators); value = images/s
+  qmatmul   cfg1: QLinearMatMul u8[1024,768] x i8[768,3072]; value = TOPS
   qconv     cfg2: QLinearConv 3x3 s1 p1, x u8[32,64,56,56], per-channel w
 A step is one pass of the path over one batch; inputs are resident in HBM
 when the timed region starts. Before timing, the GPU output is checked
@@ -100,6 +101,53 @@ def run_qconv(args, dev):
         cpu_baseline={"value": round(cpu_tops, 4), "unit": "TOPS", "cores": nthr, "kind": "port",
                       "sample": "oracle QLinearConv (scalar C, OpenMP) on 4 of the 32 images, "
                                 f"mean of {reps} runs"},
+        dtype="u8",
+    )
+
+
+def run_qmatmul(args, dev):
+    """cfg1: QLinearMatMul A u8[1024,768] x B i8[768,3072] -> u8, per-tensor
+    quantization (a 0.02/128, b 0.005/0, y 0.05/128), seed 1."""
+    import numpy as np
+    import torch
+
+    import nnr_amd as H
+    from oracle import pyoracle as O
+    rng = np.random.default_rng(1)
+    M, K, N = 1024, 768, 3072
+    a = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    b = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    q = (0.02, 128, 0.005, 0, 0.05, 128)
+    op = H.QLinearMatMul(b, q[0], q[1], q[2], q[3], q[4], q[5], m=M)
+    ad = torch.from_numpy(a).to(dev)
+    yd = torch.empty((M, N), dtype=torch.uint8, device=dev)
+    ref = O.qlinear_matmul(a, q[0], q[1], b, q[2], q[3], q[4], q[5])
+    op(ad, yd)
+    torch.cuda.synchronize()
+    assert np.array_equal(yd.cpu().numpy(), ref), "parity gate failed"
+    ms = time_steps(lambda: op(ad, yd), args)
+    prof = profile_steps(lambda: op(ad, yd), args)
+    g_launches, g_ms = prof["qgemm"]
+    ops = 2.0 * M * N * K
+    nbytes = M * K + K * N + M * N
+    # cpu baseline: the oracle on 128 of the 1024 rows
+    nthr = host_threads()
+    O.set_threads(nthr)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        O.qlinear_matmul(a[:128], q[0], q[1], b, q[2], q[3], q[4], q[5])
+        reps += 1
+        if time.perf_counter() - t0 > 3.0 or reps >= 50:
+            break
+    cpu_s = (time.perf_counter() - t0) / reps
+    return dict(
+        metric=METRIC, value=round(ops / (ms * 1e-3) / 1e12, 3), unit="TOPS", ms_per_step=ms,
+        config={"workload": "cfg1 QLinearMatMul A u8[1024,768] x B i8[768,3072] -> u8 (RQ-D)",
+                "global_batch": M},
+        roofline=roofline(ops, nbytes, g_ms / g_launches, prof),
+        cpu_baseline={"value": round(ops / 8 / cpu_s / 1e12, 4), "unit": "TOPS", "cores": nthr,
+                      "kind": "port", "sample": f"oracle on 128 of 1024 rows, {reps} runs"},
         dtype="u8",
     )
 
@@ -412,7 +460,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="resnet50",
-                    choices=["resnet50", "mobilenetv2", "bert", "qconv", "hbm_copy"])
+                    choices=["resnet50", "mobilenetv2", "bert", "qconv", "qmatmul", "hbm_copy"])
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
     args = ap.parse_args()
@@ -425,7 +473,7 @@ def main():
     run = {"resnet50": lambda a, d: run_model(a, d, "resnet50"),
            "mobilenetv2": lambda a, d: run_model(a, d, "mobilenetv2"),
            "bert": run_bert,
-           "qconv": run_qconv, "hbm_copy": run_hbm_copy}[args.config]
+           "qconv": run_qconv, "qmatmul": run_qmatmul, "hbm_copy": run_hbm_copy}[args.config]
     res = run(args, dev)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 5),

@@ -163,6 +163,15 @@ int nnrh_qmatmul_create(nnrh_qmatmul_t* h, const nnrh_qmatmul_desc* d);
 int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a_dev, long long a_batch_stride,
                      void* y_dev, int batch, const float* a_scale_dev,
                      const void* a_zp_dev, void* stream);
+/* QLinearMatMul followed by DequantizeLinear of its output (zero point y_zp,
+ * scale dq_scale) and an fp32 Add of a per-column vector bias[n] (NULL: 0),
+ * in one kernel; after a successful call nnrh_qmatmul_run writes float32
+ * y = fl(fl((q - y_zp) * dq_scale) + bias[col]), identical to running the
+ * three operators (DequantizeLinear.cpp:133-152, binary_math.cpp). No
+ * counterpart in the reference, which keeps them separate. Needs float32
+ * scales, K % 16 == 0, b_zp such that no row-sum term is needed;
+ * NNRH_ERR_UNSUPPORTED otherwise (the handle is unchanged).             */
+int nnrh_qmatmul_fuse_dq_bias(nnrh_qmatmul_t h, float dq_scale, int dq_zp, const float* bias_host);
 int nnrh_qmatmul_destroy(nnrh_qmatmul_t h);
 
 /* ---- MatMulInteger ------------------------------------------------------

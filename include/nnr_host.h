@@ -72,6 +72,10 @@ int nnr_ctx_node_io(nnr_ctx_t ctx, int i, int is_output, int j, const char** ten
  * (slot 0 or 3 is the conv result, which no longer exists as a tensor).
  * "" when nothing was folded into node i. */
 int nnr_ctx_node_fused_add(nnr_ctx_t ctx, int i, int j, const char** tensor_name);
+/* Graph nodes folded into active node i's kernel after it (e.g. the
+ * DequantizeLinear and bias Add after a QLinearMatMul), k = 0, 1, ...; ""
+ * past the last. No counterpart in the reference. */
+int nnr_ctx_node_fused_chain(nnr_ctx_t ctx, int i, int k, const char** node_name);
 int nnr_ctx_fusion_stat(nnr_ctx_t ctx, const char* key, int* value);
 size_t nnr_ctx_device_bytes(nnr_ctx_t ctx);
 

@@ -26,6 +26,7 @@ EXPORTS = [
     "nnrh_profile_enable", "nnrh_profile_reset", "nnrh_profile_count", "nnrh_profile_get",
     "nnrh_qconv_dispatch", "nnrh_qconv_create", "nnrh_qconv_branch", "nnrh_qconv_run",
     "nnrh_qconv_destroy", "nnrh_qconv_fuse_add", "nnrh_qconv_run_add", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
+    "nnrh_qmatmul_fuse_dq_bias",
     "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
     "nnrh_dynamic_quantize_linear", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
@@ -112,6 +113,7 @@ def lib():
         "nnrh_qmatmul_create": (i, [P(vp), P(QMatMulDesc)]),
         "nnrh_qmatmul_run": (i, [vp, vp, ll, vp, i, vp, vp, vp]),
         "nnrh_qmatmul_destroy": (i, [vp]),
+        "nnrh_qmatmul_fuse_dq_bias": (i, [vp, f, i, P(f)]),
         "nnrh_matmul_integer_create": (i, [P(vp), i, i, i, i, i, i]),
         "nnrh_matmul_integer_run": (i, [vp, vp, ll, vp, ll, i, i, vp, i, vp]),
         "nnrh_matmul_integer_destroy": (i, [vp]),

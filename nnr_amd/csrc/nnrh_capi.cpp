@@ -812,10 +812,11 @@ struct nnrh_qmatmul {
     int32_t* colsum = nullptr;
     int32_t* c0 = nullptr;
     int32_t* rowsum = nullptr;
+    float* dq_bias = nullptr;   // nnrh_qmatmul_fuse_dq_bias: padded to Np
     int rowsum_cap = 0;     // batches the rowsum buffer holds
     int a_zp = 0, b_beta = 0;
     float b_scale = 0.f, y_scale = 0.f;
-    ~nnrh_qmatmul() { dfree(wpack); dfree(colsum); dfree(c0); dfree(rowsum); }
+    ~nnrh_qmatmul() { dfree(wpack); dfree(colsum); dfree(c0); dfree(rowsum); dfree(dq_bias); }
 };
 
 extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc* d) {
@@ -901,6 +902,24 @@ extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc*
     g.y_bstride = (long long)m * n;
     g.bprime_from = n;
     *out = h;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qmatmul_fuse_dq_bias(nnrh_qmatmul_t h, float dq_scale, int dq_zp, const float* bias_host) {
+    if (!h) return set_err(NNRH_ERR_INVALID, "qmatmul_fuse_dq_bias: NULL handle");
+    const GemmArgs& g = h->g;
+    if (h->d.scale_dtype != NNRH_F32 || dq_zp != g.y_zp || g.beta != 0 || g.K % 16 || g.lda % 16 ||
+        g.c0_absmax + 16384LL * g.Kp >= 0x7fffffffLL)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_fuse_dq_bias: not available for this QLinearMatMul");
+    const int n = h->d.n, Np = g.Np;
+    std::vector<float> b((size_t)Np, 0.0f);
+    if (bias_host) std::copy(bias_host, bias_host + n, b.begin());
+    dfree(h->dq_bias);
+    h->dq_bias = nullptr;
+    int rc = upload(&h->dq_bias, b.data(), b.size());
+    if (rc) return rc;
+    h->g.dq_bias = h->dq_bias;
+    h->g.dq_scale = dq_scale;
     return NNRH_OK;
 }
 

@@ -104,6 +104,10 @@ struct GemmArgs {
     // and the residual byte r of the same NHWC element are A and B of the
     // add (or B and A), requantized with RQ-E. Flat element index >=
     // add_body takes the scalar-tail expression.
+    // DequantizeLinear + per-column fp32 bias fused after RQ-D: y is float,
+    // y = fl(fl((q - dq_zp) * dq_scale) + dq_bias[n]) with dq_zp = y_zp
+    const float* dq_bias;       // NULL: no fused dequantize (padded to Np)
+    float dq_scale;
     const uint8_t* add_other;   // NULL: no fused add
     int add_conv_is_a;
     float add_sa, add_sb, add_fixed;

@@ -529,7 +529,7 @@ hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec, hipStre
     if (g.a == nullptr || g.b == nullptr || g.y == nullptr) return hipErrorInvalidValue;
     const bool conv = (g.H > 0);
     if (qgemm_dma_eligible(g, vec)) return launch_qgemm_dma(g, batch, tile, s);
-    if (g.add_other) return hipErrorNotSupported;   // fused add: pipelined kernel only
+    if (g.add_other || g.dq_bias) return hipErrorNotSupported;   // fusions: pipelined kernel only
     switch (tile) {
     case TILE_128x128:
         return conv ? launch_vec<128, 128, A_CONV>(g, batch, vec, s)

@@ -79,6 +79,10 @@ __device__ __forceinline__ void block_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
+// epilogue fusions: none, QLinearAdd of a residual (RQ-B), or
+// DequantizeLinear of the output plus a per-column fp32 bias (RQ-D)
+enum { FUSE_NONE = 0, FUSE_ADD = 1, FUSE_DQB = 2 };
+
 template <int EPI>
 struct EpiParams;
 // number of per-column 32-bit arrays staged per tile
@@ -109,7 +113,7 @@ __device__ __forceinline__ int qadd_elem(int a, int b, const GemmArgs& g, bool t
 template <int BM, int BN, int S>
 constexpr int dma_min_blocks() { return ((BM + BN) * 64 * S + 4096) * 3 <= 160 * 1024 ? 3 : 2; }
 
-template <int BM, int BN, int S, int AMODE, int EPI, bool FADD>
+template <int BM, int BN, int S, int AMODE, int EPI, int FUSE>
 __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_kernel(GemmArgs g) {
     constexpr int WAVES_N = BN / 64;
     static_assert((BM / 64) * WAVES_N == 4, "4 waves of 64x64");
@@ -118,7 +122,8 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
     constexpr int LPS = A_CH + B_CH;         // DMA instructions per thread per step
     constexpr int STAGE = (BM + BN) * 64;    // bytes per K-step
     constexpr int NP = EpiParams<EPI>::NP;
-    constexpr int PBYTES = NP * BN * 4;
+    constexpr int NPX = NP + (FUSE == FUSE_DQB ? 1 : 0);   // + the fp32 bias
+    constexpr int PBYTES = NPX * BN * 4;
     constexpr int PWAVES = (PBYTES + 1023) / 1024;   // waves issuing the param DMA
     constexpr int PSLOT = PWAVES * 1024;
     static_assert(PWAVES <= 4, "param slot");
@@ -274,7 +279,8 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
             // call; lanes past the last array reload array 0 (never read back)
             const void* base0 = g.c0 ? (const void*)g.c0 : (const void*)g.colsum;
             const void* base;
-            if (arr == 0 || arr >= NP) base = base0;
+            if (FUSE == FUSE_DQB && arr == NP) base = g.dq_bias;
+            else if (arr == 0 || arr >= NP) base = base0;
             else if (EPI == EPI_RQB) base = g.os;
             else if (arr == 1) base = g.cs;
             else base = g.bf;
@@ -408,7 +414,7 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                         packed[tn] = w;
                     }
                 }
-                if constexpr (FADD) {
+                if constexpr (FUSE == FUSE_ADD) {
                     const bool sgn = g.y_type == 1;
                     const long long i0 = (long long)m * g.ldy + nb;
                     if (i0 + 16 <= g.add_body) {
@@ -459,6 +465,31 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                         }
                     }
                 }
+                if constexpr (FUSE == FUSE_DQB) {
+                    // DequantizeLinear fl((q - zp) * s) (DequantizeLinear.cpp:133-152),
+                    // then the fp32 Add of the column bias, written as fp32
+                    const float zp_f = (float)g.y_zp;
+                    const uint8_t* pb = ps + NP * BN * 4 + nl * 4;
+                    float* frow = (float*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
+                    float o[16];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const uint32_t bq = (packed[i >> 2] >> (8 * (i & 3))) & 0xffu;
+                        const float qf = g.y_type == 1 ? (float)(int)(int8_t)bq : (float)bq;
+                        const float d = (qf - zp_f) * g.dq_scale;
+                        o[i] = d + *(const float*)(pb + 4 * i);
+                    }
+                    if (full16 && ((((uintptr_t)frow) & 15) == 0)) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            *(float4*)(frow + 4 * q) = make_float4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+                            if (nb + i < g.N) frow[i] = o[i];
+                    }
+                    continue;
+                }
                 uint8_t* yrow = (uint8_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
                 if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
                     *(v4i*)yrow = v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
@@ -472,7 +503,7 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
     };
 
     // ---- prologue: S-1 steps in flight
-    if constexpr (FADD) load_residual(t_first, rcur);
+    if constexpr (FUSE == FUSE_ADD) load_residual(t_first, rcur);
     p_setup(p_t);
 #pragma unroll
     for (int s = 0; s < S - 1; ++s)
@@ -487,7 +518,7 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
         // every wave's DMAs of the step have landed; every wave is done
         // reading the stage (and param slot) the next issue overwrites
         block_barrier();
-        if constexpr (FADD) {
+        if constexpr (FUSE == FUSE_ADD) {
             if (c_kt == 0 && c_t + t_step < t_end) load_residual(c_t + t_step, rnext);
         }
         if (p_t < t_end) p_issue();
@@ -528,7 +559,7 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
         ++c_gs;
         if (++c_kt == nk) {
             epilogue();
-            if constexpr (FADD) {
+            if constexpr (FUSE == FUSE_ADD) {
 #pragma unroll
                 for (int tm = 0; tm < 4; ++tm) rcur[tm] = rnext[tm];
             }
@@ -544,9 +575,9 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
 
 namespace {
 
-template <int BM, int BN, int S, int AMODE, int EPI, bool FADD = false>
+template <int BM, int BN, int S, int AMODE, int EPI, int FUSE = FUSE_NONE>
 hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
-    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI, FADD>;
+    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI, FUSE>;
     const long long tiles = (long long)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN) * batch;
     // resident blocks of this instantiation (occupancy x CUs), computed once
     static int resident = 0;
@@ -575,10 +606,16 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
 
 template <int BM, int BN, int S, int AMODE, int S_ADD = S>
 hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
+    if (g.dq_bias) {
+        if constexpr (AMODE == A_DENSE) {
+            if (g.epi == EPI_RQD) return launch_dma<BM, BN, S, AMODE, EPI_RQD, FUSE_DQB>(g, batch, s);
+        }
+        return hipErrorNotSupported;
+    }
     if (g.add_other) {
         if constexpr (AMODE == A_CONV || AMODE == A_DENSE) {
             if (g.epi == EPI_RQB && batch == 1)
-                return launch_dma<BM, BN, S_ADD, AMODE, EPI_RQB, true>(g, batch, s);
+                return launch_dma<BM, BN, S_ADD, AMODE, EPI_RQB, FUSE_ADD>(g, batch, s);
         }
         return hipErrorNotSupported;
     }

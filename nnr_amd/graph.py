@@ -56,6 +56,7 @@ def host_lib():
             "nnr_ctx_node_info": (i, [vp, i, P(cp), P(cp), P(cp), P(i), P(i), P(i)]),
             "nnr_ctx_node_io": (i, [vp, i, i, i, P(cp)]),
             "nnr_ctx_node_fused_add": (i, [vp, i, i, P(cp)]),
+            "nnr_ctx_node_fused_chain": (i, [vp, i, i, P(cp)]),
             "nnr_ctx_fusion_stat": (i, [vp, cp, P(i)]),
             "nnr_ctx_device_bytes": (C.c_size_t, [vp]),
             "nnr_ctx_enable_profiling": (i, [vp, i]),
@@ -237,8 +238,16 @@ class Session:
             fadd = None
             if fused(-1):
                 fadd = dict(name=fused(-1), other=fused(-2), inputs=[fused(j) for j in range(8)])
+            chain = []
+            while True:
+                c = C.c_char_p()
+                _chk(L.nnr_ctx_node_fused_chain(self.h, i, len(chain), C.byref(c)))
+                if not c.value:
+                    break
+                chain.append(c.value.decode())
             out.append(dict(op=op.value.decode(), name=nm.value.decode(), variant=var.value.decode(),
-                            post_fn=pf.value, inputs=ios[0], outputs=ios[1], fused_add=fadd))
+                            post_fn=pf.value, inputs=ios[0], outputs=ios[1], fused_add=fadd,
+                            fused_chain=chain))
         return out
 
     def fusion_stat(self, key):

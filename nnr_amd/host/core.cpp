@@ -358,7 +358,10 @@ bool context_t::prepare() {
         if (vi >= 0 && op->inputs[vi] && !op->outputs.empty()) op->outputs[0]->alias_of = op->inputs[vi];
     }
     // 5b. residual adds into their producing convolutions' kernels
-    if (enable_fusion && enable_conv_add) fuse_conv_add(this);
+    if (enable_fusion && enable_conv_add) {
+        fuse_conv_add(this);
+        fuse_matmul_dq_bias(this);
+    }
     // 6. device memory and constant upload
     if (!plan_memory()) return false;
     if (!upload_constants()) return fail(nnrh_last_error());

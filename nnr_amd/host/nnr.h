@@ -122,6 +122,10 @@ struct operator_t {
     // accept `add` (whose input conv_side, 0 or 3, is this operator's output)
     // into the kernel; false leaves everything unchanged
     virtual bool fuse_residual_add(operator_t* /*add*/, int /*conv_side*/) { return false; }
+    // nodes after this one whose work its kernel now does, in graph order
+    // (fuse_matmul_dq_bias); they are skipped and the last one's output is ours
+    std::vector<operator_t*> fused_chain;
+    virtual bool fuse_dq_bias(operator_t* /*dq*/, operator_t* /*add*/) { return false; }
 
     // attribute accessors
     const attr_t* find_attr(const std::string& name) const;
@@ -175,7 +179,7 @@ struct context_t {
     backend_t preferred_backend = backend_t::HIP;
     void* stream = nullptr;       // hipStream_t of every launch
     bool enable_fusion = true;
-    bool enable_conv_add = true;  // fuse_conv_add after the operators are built
+    bool enable_conv_add = true;  // fuse_conv_add / fuse_matmul_dq_bias after the operators are built
     bool enable_profiling = false;
     bool shape_only = false;      // reshape() computes shapes only (pre-layout pass)
 
@@ -207,6 +211,7 @@ void fuse_qdq(context_t* ctx);
 void fuse_post_ops(context_t* ctx);
 void assign_layouts(context_t* ctx);
 void fuse_conv_add(context_t* ctx);
+void fuse_matmul_dq_bias(context_t* ctx);
 
 // operator creation through the registry (src/backend/cpu/solve_operator.cpp:29-33)
 operator_t* solve_operator(const std::string& op_type, int opset, backend_t preferred);

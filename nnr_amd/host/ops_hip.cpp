@@ -300,6 +300,20 @@ struct QLinearMatMul_hip : operator_t {
         h = nullptr;
         return ok(this, nnrh_qmatmul_create(&h, &dsc));
     }
+    bool fuse_dq_bias(operator_t* dq, operator_t* add) override {
+        if (!h) return false;
+        tensor_t* f = dq->outputs[0];
+        tensor_t* bias = add->inputs[0] == f ? add->inputs[1] : add->inputs[0];
+        tensor_t* y = add->outputs[0];
+        // the bias must be a vector over the last axis of the result
+        if (bias->ndata != (size_t)n) return false;
+        for (int i = 0; i + 1 < bias->ndim(); ++i)
+            if (bias->dims[i] != 1) return false;
+        if (y->dims != f->dims || y->type != NNR_DATA_TYPE_FLOAT32) return false;
+        return nnrh_qmatmul_fuse_dq_bias(h, dq->inputs[1]->scalar_f32(), zp_value(in(dq, 2)),
+                                         bias->h<float>()) == NNRH_OK;
+    }
+    std::string variant() const override { return fused_chain.empty() ? "" : "+DQ+Bias"; }
     bool exec() override {
         const float* a_s_dev = inputs[1]->has_host() ? nullptr : (const float*)inputs[1]->data;
         const void* a_z_dev = inputs[2]->has_host() ? nullptr : inputs[2]->data;

@@ -10,6 +10,9 @@
 //                     fuse_post_ops.cpp:67): a same-shape QLinearAdd whose
 //                     input is a QLinearConv's only use runs in that conv's
 //                     epilogue, with bit-identical results
+//   fuse_matmul_dq_bias  no counterpart: QLinearMatMul -> DequantizeLinear ->
+//                     Add(constant last-axis vector) runs as one kernel with
+//                     an fp32 output, bit-identical to the three operators
 // The fused operators are created through the registry with the context's
 // preferred backend, exactly where the reference calls solve_operator.
 #include <cstdio>
@@ -483,6 +486,58 @@ void fuse_conv_add(context_t* ctx) {
         }
     }
     ctx->fusion_stats["conv_add"] = fused;
+}
+
+// ---------------------------------------------------------------------------
+// QLinearMatMul -> DequantizeLinear (the output's own scale / zero point) ->
+// Add(constant vector over the last axis). Runs after the operators are built.
+void fuse_matmul_dq_bias(context_t* ctx) {
+    auto& nodes = ctx->nodes;
+    const int n = (int)nodes.size();
+    std::unordered_set<tensor_t*> graph_out;
+    for (auto& name : ctx->graph_outputs)
+        if (tensor_t* t = ctx->find(name)) graph_out.insert(t);
+    auto sole_consumer = [&](tensor_t* t) -> operator_t* {
+        operator_t* c = nullptr;
+        for (auto* op : nodes) {
+            if (!active(op)) continue;
+            for (auto* x : op->inputs)
+                if (x == t) {
+                    if (c && c != op) return nullptr;
+                    c = op;
+                }
+        }
+        return c;
+    };
+    auto same_scalar = [](tensor_t* a, tensor_t* b) {
+        if (!a || !b || !a->has_host() || !b->has_host() || a->ndata != 1 || b->ndata != 1) return false;
+        return a->type == b->type && a->host == b->host;
+    };
+    int fused = 0;
+    for (int i = 0; i < n; ++i) {
+        operator_t* mm = nodes[i];
+        if (!active(mm) || mm->op_type != "QLinearMatMul" || mm->outputs.size() != 1) continue;
+        tensor_t* q = mm->outputs[0];
+        if (graph_out.count(q)) continue;
+        operator_t* dq = sole_consumer(q);
+        if (!dq || dq->op_type != "DequantizeLinear" || dq->inputs.size() < 2 || dq->inputs[0] != q) continue;
+        if (!same_scalar(dq->inputs[1], mm->inputs[6])) continue;
+        tensor_t* dz = dq->inputs.size() > 2 ? dq->inputs[2] : nullptr;
+        if (!same_scalar(dz, mm->inputs[7])) continue;
+        tensor_t* f = dq->outputs[0];
+        if (graph_out.count(f)) continue;
+        operator_t* add = sole_consumer(f);
+        if (!add || add->op_type != "Add" || add->inputs.size() != 2) continue;
+        tensor_t* bias = add->inputs[0] == f ? add->inputs[1] : add->inputs[0];
+        if (!bias || !bias->has_host() || bias->type != NNR_DATA_TYPE_FLOAT32) continue;
+        if (!mm->fuse_dq_bias(dq, add)) continue;
+        mm->fused_chain = {dq, add};
+        mm->outputs[0] = add->outputs[0];
+        dq->skip = true;
+        add->skip = true;
+        ++fused;
+    }
+    ctx->fusion_stats["matmul_dq_bias"] = fused;
 }
 
 }  // namespace nnr

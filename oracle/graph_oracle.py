@@ -33,12 +33,15 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
     (their outputs must then come from source)."""
     init = graph.initializers
     env = {}
+    chain_env = {}   # tensors inside a fused chain (they exist only here)
     for k, v in feeds.items():
         env[k] = v
 
     def val(name):
         if name in init:
             return init[name]
+        if name in chain_env:
+            return chain_env[name]
         if source is not None and name not in feeds:
             return source(name)
         return env[name]
@@ -48,10 +51,8 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
             return default
         return val(name).reshape(-1)[0]
 
-    for nd in plan:
+    def exec_node(nd):
         op, ins, outs = nd["op"], nd["inputs"], nd["outputs"]
-        if op in skip_ops:
-            continue
         extra = {}
         if op == "QuantizeLinear":
             zdt = init[ins[2]].dtype if len(ins) > 2 and ins[2] else np.uint8
@@ -110,7 +111,7 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
                 # conv + QLinearAdd in one kernel: the conv result is the add
                 # operand that is not `other`, then the add runs as planned
                 ai = fa["inputs"]
-                env[ai[3] if ai[0] == fa["other"] else ai[0]] = y
+                chain_env[ai[3] if ai[0] == fa["other"] else ai[0]] = y
                 y = O.qlinear_add(0, val(ai[0]), val(ai[3]), float(scal(ai[1])), int(scal(ai[2])),
                                   float(scal(ai[4])), int(scal(ai[5])), float(scal(ai[6])),
                                   int(scal(ai[7])))
@@ -164,8 +165,25 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
             y = y.astype(np.float32)
         else:
             raise NotImplementedError(op)
-        env[outs[0]] = y
-        env.update(extra)
+        return {outs[0]: y, **extra}
+
+    for nd in plan:
+        if nd["op"] in skip_ops:
+            continue
+        res = exec_node(nd)
+        chain = nd.get("fused_chain") or []
+        if chain:
+            # nodes folded into this kernel: the result above is the first
+            # one's input; replay them in order from the graph's definitions
+            first = graph.node_by_name(chain[0])
+            chain_env[first.inputs[0]] = res[nd["outputs"][0]]
+            for name in chain:
+                gn = graph.node_by_name(name)
+                cres = exec_node({"op": gn.op, "name": gn.name, "inputs": list(gn.inputs),
+                                  "outputs": list(gn.outputs), "post_fn": 0})
+                chain_env.update(cres)
+            res = {nd["outputs"][0]: chain_env[nd["outputs"][0]]}
+        env.update(res)
         if stop_after and nd["name"] == stop_after:
             break
     return env

@@ -97,12 +97,12 @@ def test_mobilenetv2_small_input(dev):
     check_graph(g, {"input": x}, "logits")
 
 
-def check_graph_per_node(g, feeds, atol=1e-3, rtol=1e-3):
+def check_graph_per_node(g, feeds, atol=1e-3, rtol=1e-3, **session_kw):
     """Every node of the executed plan, recomputed by the oracle from the
     device's own input tensors: int8 outputs bit-exact, fp32 outputs within
     the reference's tolerance. Used where fp32 nodes feed dynamic
     quantization, so rounding noise must not propagate between nodes."""
-    s = G.Session(g)
+    s = G.Session(g, **session_kw)
     for k, v in feeds.items():
         s.set_input(k, v)
     s.run()
@@ -133,14 +133,24 @@ def check_graph_per_node(g, feeds, atol=1e-3, rtol=1e-3):
     return plan, n_int, n_f32
 
 
-def test_bert_per_node(dev):
+@pytest.mark.parametrize("fused", [True, False])
+def test_bert_per_node(dev, fused):
     """cfg5 structure (2 layers, batch 2, seq 64): DynamicQuantizeLinear ->
     QLinearMatMul with device-side activation scale / zero point, fp32
     attention (batched MatMul, Softmax), LayerNormalization, Gelu."""
     g = synth.bert(batch=2, seq=64, layers=2)
     rng = np.random.default_rng(19)
     x = rng.uniform(-1.0, 1.0, (2, 64, 768)).astype(np.float32)
-    plan, n_int, n_f32 = check_graph_per_node(g, {"input": x})
+    plan, n_int, n_f32 = check_graph_per_node(g, {"input": x}, conv_add=fused)
     ops = [p["op"] for p in plan]
     assert ops.count("QLinearMatMul") == 12 and ops.count("DynamicQuantizeLinear") == 8
-    assert n_int >= 12 + 8 * 2 and n_f32 > 0
+    if not fused:
+        assert not any(p.get("fused_chain") for p in plan)
+        assert n_int >= 12 + 8 * 2 and n_f32 > 0
+        return
+    # every QLinearMatMul absorbs its DequantizeLinear and bias Add, so its
+    # checked output is the fp32 end of the chain; the int8 outputs left are
+    # those of DynamicQuantizeLinear (y and zero point)
+    chains = [p for p in plan if p["op"] == "QLinearMatMul" and p.get("fused_chain")]
+    assert len(chains) == 12
+    assert n_int >= 8 * 2 and n_f32 >= 12

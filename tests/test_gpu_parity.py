@@ -327,3 +327,30 @@ def test_gemm_f32(dev, ta, tb, c_mode):
     _lib.check(_lib.lib().nnrh_gemm_f32(_lib.ptr(Ad), _lib.ptr(Bd), _lib.ptr(Cd), _lib.ptr(y),
                                         M, N, K, ta, tb, alpha, beta, c_mode, _lib.cur_stream()))
     np.testing.assert_allclose(to_np(y), ref, atol=1e-3, rtol=1e-4)
+
+
+def test_qmatmul_fused_dq_bias(dev):
+    """QLinearMatMul -> DequantizeLinear -> + bias in one kernel (fp32 out),
+    against the oracle's three operators; device-side activation quantization
+    parameters as produced by DynamicQuantizeLinear."""
+    import torch
+    rng = np.random.default_rng(23)
+    a = rng.integers(0, 256, (3, 40, 96), dtype=np.uint8)
+    b = rng.integers(-127, 128, (96, 136), dtype=np.int8)
+    bias = rng.standard_normal(136).astype(np.float32)
+    ys, yz = 0.031, 121
+    q = O.qlinear_matmul(a, np.float32(0.0133), 77, b, 0.004, 0, ys, yz)
+    deq = O.dequantize_linear(q, ys, yz)
+    ref = (deq + bias).astype(np.float32)
+    op = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, ys, yz, m=40)
+    from nnr_amd import _lib
+    _lib.check(_lib.lib().nnrh_qmatmul_fuse_dq_bias(op.h, ys, yz, bias.ctypes.data_as(
+        __import__("ctypes").POINTER(__import__("ctypes").c_float))))
+    s = torch.tensor([0.0133], dtype=torch.float32, device=dev)
+    z = torch.tensor([77], dtype=torch.uint8, device=dev)
+    y = torch.empty((3, 40, 136), dtype=torch.float32, device=dev)
+    ad = to_dev(a, dev)
+    op(ad, y=y, a_scale_dev=s, a_zp_dev=z)
+    got = to_np(y)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+        f"{np.count_nonzero(got != ref)} of {got.size} differ"
