@@ -33,6 +33,8 @@ enum AMode : int {
     A_DENSE = 0,   // A[m*lda + k]
     A_CONV = 1,    // implicit im2col over an NHWC tensor, K order (kh,kw,c)
     A_CONV4 = 2,   // first layer: NHWC with 4 channels, K order (kh, kw < kWp, c)
+    A_CONVU = 3,   // A_CONV with C % 64 == 0 and kH*kW <= 32: every 64-byte K step
+                   // lies in one tap, so the tap walk is uniform across the block
 };
 
 struct GemmArgs {
@@ -100,6 +102,8 @@ struct GemmArgs {
     long long c0_absmax;
     // n / d for n < 2^31 as (n * mul) >> (31 + shift) (set by the launcher)
     uint32_t div_sp_mul, div_sp_shift, div_ow_mul, div_ow_shift;
+    // tile index -> (z, m-block, n-block) (set by the pipelined launcher)
+    uint32_t div_pz_mul, div_pz_shift, div_nbn_mul, div_nbn_shift;
     // QLinearAdd (same shape) fused into the RQ-B epilogue: the conv byte q
     // and the residual byte r of the same NHWC element are A and B of the
     // add (or B and A), requantized with RQ-E. Flat element index >=

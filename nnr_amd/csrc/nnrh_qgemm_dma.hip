@@ -132,7 +132,8 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // the wave index as a uniform value, so LDS destinations stay scalar
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int frow = lane & 15, fchunk = lane >> 4;
 
@@ -155,6 +156,14 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
         t_step = G;
     }
     if (t_first >= t_end) return;
+    // tile index -> batch z, first row m0, first column n0
+    auto decode = [&](int t, int& z, int& m0, int& n0) {
+        z = g.nbatch == 1 ? 0 : (int)fast_div((uint32_t)t, g.div_pz_mul, g.div_pz_shift);
+        const int r = t - z * per_z;
+        const int mb = (int)fast_div((uint32_t)r, g.div_nbn_mul, g.div_nbn_shift);
+        m0 = mb * BM;
+        n0 = (r - mb * nbn) * BN;
+    };
 
     const int nk = g.Kp >> 6;
     const uint32_t xmask = (uint32_t)g.a_xor * 0x01010101u;
@@ -170,6 +179,11 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
         const float t1 = *g.cm_a_scale_dev * g.cm_b;
         cm = t1 / g.cm_y;
     }
+    // uint8 output whose clamp is exactly the [0, 255] saturation of
+    // v_cvt_pk_u8_f32 (round to nearest even, saturate, insert one byte):
+    // RQ-B with zero point 0 (clamp [0, 255] then rne) and RQ-D (rne of
+    // acc*cm + zp, clamp [0, 255]) take one instruction for round + clamp + pack
+    const bool sat_u8 = g.y_type == 0 && g.lo == 0 && g.hi == 255 && (EPI == EPI_RQD || g.y_zp == 0);
     const uint8_t* pad16 = (const uint8_t*)&kPadTable.w[(g.pad_byte & 0xff) * 4];
     const int sp_out = g.oH * g.oW;
     // this thread's 16-byte chunk of a 64-byte row (pre-swizzled so the LDS
@@ -177,34 +191,53 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
     const int cdma = (tid & 3) ^ ((tid >> 3) & 3);
 
     // ---- producer (DMA issue) state
-    int p_t = t_first, p_kt = 0, p_tseq = 0, p_gs = 0;
+    int p_t = t_first, p_kt = 0, p_gs = 0;
+    int p_stage = 0, p_pslot = 0;   // byte offsets of the stage / param slot being filled
     const uint8_t* p_a = nullptr;   // batch base of A
-    const int8_t* p_b = nullptr;    // batch base of B
     int p_n0 = 0;
     long long p_pbase = 0;          // batch offset of the per-column arrays
-    long long a_base[A_CH];
+    uint64_t a_addr[A_CH];          // A_DENSE / A_CONVU: address of this thread's chunk of row j
+    uint32_t a_tmask[A_CH];         // A_CONVU: bit t set when tap t of row j is inside the image
+    uint64_t b_addr[B_CH];          // this thread's chunk of weight row j
+    long long a_base[A_CH];         // A_CONV / A_CONV4
     int a_ih0[A_CH], a_iw0[A_CH];
     bool a_ok[A_CH];
-    int kc_ic = 0, kc_kh = 0, kc_kw = 0;
+    int kc_ic = 0, kc_kh = 0, kc_kw = 0;   // A_CONV: tap of this thread's chunk
+    int u_tap = 0, u_ic = 0, u_kh = 0, u_kw = 0, u_off = 0;   // A_CONVU: the step's tap
 
     auto p_setup = [&](int t) {
-        const int z = t / per_z;
-        const int r = t - z * per_z;
-        const int m0 = (r / nbn) * BM;
-        p_n0 = (r % nbn) * BN;
+        int z, m0;
+        decode(t, z, m0, p_n0);
         p_a = g.a + (long long)z * g.a_bstride;
-        p_b = g.b + (long long)z * g.b_bstride;
+        const int8_t* pb = g.b + (long long)z * g.b_bstride;
         p_pbase = (long long)z * g.param_bstride;
 #pragma unroll
         for (int j = 0; j < A_CH; ++j) {
             const int m = m0 + (tid >> 2) + 64 * j;
             a_ok[j] = m < g.M;
+            const int mm = a_ok[j] ? m : 0;
             if constexpr (AMODE == A_DENSE) {
-                a_base[j] = (long long)m * g.lda;
-                a_ih0[j] = 0; a_iw0[j] = 0;
+                a_addr[j] = (uint64_t)(p_a + (long long)mm * g.lda + cdma * 16);
+            } else if constexpr (AMODE == A_CONVU) {
+                const int img = (int)fast_div((uint32_t)mm, g.div_sp_mul, g.div_sp_shift);
+                const int s = mm - img * sp_out;
+                const int oh = (int)fast_div((uint32_t)s, g.div_ow_mul, g.div_ow_shift);
+                const int ow = s - oh * g.oW;
+                const int ih0 = oh * g.sH - g.pad_t, iw0 = ow * g.sW - g.pad_l;
+                // (ih0, iw0) may lie in the padding: the address is only
+                // dereferenced for taps inside the image
+                a_addr[j] = (uint64_t)p_a +
+                            (uint64_t)((((long long)img * g.H + ih0) * g.W + iw0) * g.Cs + cdma * 16);
+                uint32_t hm = 0, wmk = 0, tm = 0;
+                for (int kh = 0; kh < g.kH; ++kh)
+                    hm |= (uint32_t)((unsigned)(ih0 + kh * g.dH) < (unsigned)g.H) << kh;
+                for (int kw = 0; kw < g.kW; ++kw)
+                    wmk |= (uint32_t)((unsigned)(iw0 + kw * g.dW) < (unsigned)g.W) << kw;
+                for (int kh = 0; kh < g.kH; ++kh)
+                    tm |= ((hm >> kh) & 1u) ? (wmk << (kh * g.kW)) : 0u;
+                a_tmask[j] = a_ok[j] ? tm : 0u;
             } else if constexpr (AMODE == A_CONV4) {
                 // padded multi-copy image: row start of this output pixel
-                const int mm = a_ok[j] ? m : 0;
                 const int img = (int)fast_div((uint32_t)mm, g.div_sp_mul, g.div_sp_shift);
                 const int s = mm - img * sp_out;
                 const int oh = (int)fast_div((uint32_t)s, g.div_ow_mul, g.div_ow_shift);
@@ -215,7 +248,6 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                             (((long long)img * g.H + (long long)oh * g.sH) * g.W + (pix0 - r)) * 4;
                 a_ih0[j] = 0; a_iw0[j] = 0;
             } else {
-                const int mm = a_ok[j] ? m : 0;
                 const int img = (int)fast_div((uint32_t)mm, g.div_sp_mul, g.div_sp_shift);
                 const int s = mm - img * sp_out;
                 const int oh = (int)fast_div((uint32_t)s, g.div_ow_mul, g.div_ow_shift);
@@ -225,6 +257,12 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                 a_iw0[j] = ow * g.sW - g.pad_l;
             }
         }
+#pragma unroll
+        for (int j = 0; j < B_CH; ++j) {
+            int n = p_n0 + (tid >> 2) + 64 * j;
+            n = n < g.Np ? n : g.Np - 1;
+            b_addr[j] = (uint64_t)(pb + (long long)n * g.Kp + cdma * 16);
+        }
         if constexpr (AMODE == A_CONV) {
             const int k = cdma * 16;
             const int kp = k / g.C;
@@ -232,20 +270,27 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
             kc_kh = kp / g.kW;
             kc_kw = kp - kc_kh * g.kW;
         }
+        if constexpr (AMODE == A_CONVU) {
+            u_tap = 0; u_ic = 0; u_kh = 0; u_kw = 0; u_off = 0;
+        }
     };
 
-    // issue the DMA of producer step (p_t, p_kt) into stage p_gs % S
+    // issue the DMA of producer step (p_t, p_kt) into the stage at p_stage
     auto p_issue = [&]() {
-        uint8_t* st = lds + (p_gs % S) * STAGE;
-        const int kk = (p_kt << 6) + cdma * 16;
+        uint8_t* st = lds + p_stage;
+        const int k0 = p_kt << 6;
 #pragma unroll
         for (int j = 0; j < A_CH; ++j) {
             const uint8_t* src = pad16;
             if constexpr (AMODE == A_DENSE) {
-                if (a_ok[j] && kk < g.K) src = p_a + a_base[j] + kk;
+                bool ok = a_ok[j];
+                if (k0 + 64 > g.K) ok = ok && (k0 + cdma * 16 < g.K);   // K padding
+                if (ok) src = (const uint8_t*)(a_addr[j] + (uint64_t)k0);
+            } else if constexpr (AMODE == A_CONVU) {
+                if ((a_tmask[j] >> u_tap) & 1u) src = (const uint8_t*)(a_addr[j] + (uint64_t)(long long)u_off);
             } else if constexpr (AMODE == A_CONV4) {
                 // chunk = 4 taps (kw0..kw0+3) x 4 channels of kernel row kh
-                const int q = kk >> 4;
+                const int q = (k0 + cdma * 16) >> 4;
                 const int cpr = g.kWp >> 2;
                 const int kh = q / cpr;
                 const int kw0 = (q - kh * cpr) << 2;
@@ -261,11 +306,8 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
             dma16(src, st + wave * 1024 + j * 4096);
         }
 #pragma unroll
-        for (int j = 0; j < B_CH; ++j) {
-            int n = p_n0 + (tid >> 2) + 64 * j;
-            n = n < g.Np ? n : g.Np - 1;
-            dma16(p_b + (long long)n * g.Kp + kk, st + BM * 64 + wave * 1024 + j * 4096);
-        }
+        for (int j = 0; j < B_CH; ++j)
+            dma16((const void*)(b_addr[j] + (uint64_t)k0), st + BM * 64 + wave * 1024 + j * 4096);
         if (p_kt == 0 && wave < PWAVES) {
             // per-column constants of the tile: NP arrays of BN int32/float,
             // one 16-byte chunk per lane; chunks past the arrays reload the
@@ -285,10 +327,11 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
             else if (arr == 1) base = g.cs;
             else base = g.bf;
             const uint8_t* src = (const uint8_t*)base + (p_pbase + c) * 4;
-            dma16(src, lds + S * STAGE + (p_tseq % S) * PSLOT + wave * 1024);
+            dma16(src, lds + S * STAGE + p_pslot + wave * 1024);
         }
         // advance
         ++p_gs;
+        p_stage = p_stage + STAGE == S * STAGE ? 0 : p_stage + STAGE;
         if constexpr (AMODE == A_CONV) {
             kc_ic += 64;
             while (kc_ic >= g.C) {
@@ -296,17 +339,30 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                 if (++kc_kw == g.kW) { kc_kw = 0; ++kc_kh; }
             }
         }
+        if constexpr (AMODE == A_CONVU) {
+            // C % 64 == 0: the next step is the next 64 channels of this tap,
+            // or the first 64 of the next tap (taps in (kh, kw) order)
+            u_ic += 64;
+            u_off += 64;
+            if (u_ic == g.C) {
+                u_ic = 0;
+                ++u_tap;
+                if (++u_kw == g.kW) { u_kw = 0; ++u_kh; }
+                u_off = (u_kh * g.dH * g.W + u_kw * g.dW) * g.Cs;
+            }
+        }
         if (++p_kt == nk) {
             p_kt = 0;
-            ++p_tseq;
+            p_pslot = p_pslot + PSLOT == S * PSLOT ? 0 : p_pslot + PSLOT;
             p_t += t_step;
             if (p_t < t_end) p_setup(p_t);
         }
     };
 
     // ---- consumer state
-    int c_t = t_first, c_kt = 0, c_tseq = 0, c_gs = 0;
-    v4i acc[4][4];   // set to c0 at each tile's first K-step
+    int c_t = t_first, c_kt = 0, c_gs = 0;
+    int c_stage = 0, c_pslot = 0;
+    v4i acc[4][4];   // started from c0 by the tile's first K-step
 
     // fused add: residual bytes of this lane's 4 rows x 16 channels. They
     // are loaded one tile ahead (at the first K-step of the previous tile,
@@ -314,8 +370,9 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
     // covers loads the pipeline needs by then anyway.
     v4i rcur[4], rnext[4];
     auto load_residual = [&](int t, v4i* rr) {
-        const int m0 = (t / nbn) * BM;   // batch 1 (checked by the launcher)
-        const int nb = (t % nbn) * BN + wn * 64 + 16 * fchunk;
+        int z, m0, n0;
+        decode(t, z, m0, n0);   // batch 1 (checked by the launcher)
+        const int nb = n0 + wn * 64 + 16 * fchunk;
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) {
             rr[tm] = v4i{0, 0, 0, 0};
@@ -334,15 +391,13 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
     };
 
     auto epilogue = [&]() {
-        const int z = c_t / per_z;
-        const int r = c_t - z * per_z;
-        const int m0 = (r / nbn) * BM;
-        const int n0 = (r % nbn) * BN;
+        int z, m0, n0;
+        decode(c_t, z, m0, n0);
         const int nl = wn * 64 + 16 * fchunk;   // first column of this lane in the tile
         const int nb = n0 + nl;
         if (nb >= g.N) return;
         // the accumulators started at c0 (acc + c0 = the reference's value)
-        const uint8_t* ps = lds + S * STAGE + (c_tseq % S) * PSLOT;
+        const uint8_t* ps = lds + S * STAGE + c_pslot;
         v4i p0[4], p1[4];
 #pragma unroll
         for (int tn = 0; tn < 4; ++tn) {
@@ -370,29 +425,60 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
             } else {
                 uint32_t packed[4];
                 if constexpr (EPI == EPI_RQB) {
-                    // RQ-B: with an even zero point, fl(f + 1.5*2^23 + zp) rounds
-                    // to M + zp + rne(f) (the tie goes to the same even integer),
-                    // so the low byte already holds rne(f) + zp; an odd zero point
-                    // is added to the bit pattern
-                    const float lo_f = (float)g.lo - (float)g.y_zp, hi_f = (float)g.hi - (float)g.y_zp;
-                    auto rqb_row = [&](auto zp_even) {
-                        constexpr bool EVEN = decltype(zp_even)::value;
-                        const float magic = EVEN ? RNE_MAGIC + (float)g.y_zp : RNE_MAGIC;
+                    if (sat_u8) {
+                        // zero point 0: rne(clamp(f, 0, 255)) = sat(rne(f))
 #pragma unroll
                         for (int tn = 0; tn < 4; ++tn) {
-                            uint32_t b[4];
+                            uint32_t w = 0;
 #pragma unroll
                             for (int q = 0; q < 4; ++q) {
-                                float f = (float)acc[tm][tn][q] * __int_as_float(p0[tn][q]);
-                                f = med3f(f, lo_f, hi_f);
-                                b[q] = (uint32_t)__float_as_int(f + magic);
-                                if constexpr (!EVEN) b[q] += (uint32_t)g.y_zp;
+                                const float f = (float)acc[tm][tn][q] * __int_as_float(p0[tn][q]);
+                                w = __builtin_amdgcn_cvt_pk_u8_f32(f, q, w);
                             }
-                            packed[tn] = pack_low_bytes(b[0], b[1], b[2], b[3]);
+                            packed[tn] = w;
                         }
-                    };
-                    if ((g.y_zp & 1) == 0) rqb_row(std::true_type{});
-                    else rqb_row(std::false_type{});
+                    } else {
+                        // RQ-B: with an even zero point, fl(f + 1.5*2^23 + zp)
+                        // rounds to M + zp + rne(f) (the tie goes to the same
+                        // even integer), so the low byte already holds
+                        // rne(f) + zp; an odd zero point is added to the bit
+                        // pattern
+                        const float lo_f = (float)g.lo - (float)g.y_zp, hi_f = (float)g.hi - (float)g.y_zp;
+                        auto rqb_row = [&](auto zp_even) {
+                            constexpr bool EVEN = decltype(zp_even)::value;
+                            const float magic = EVEN ? RNE_MAGIC + (float)g.y_zp : RNE_MAGIC;
+#pragma unroll
+                            for (int tn = 0; tn < 4; ++tn) {
+                                uint32_t b[4];
+#pragma unroll
+                                for (int q = 0; q < 4; ++q) {
+                                    float f = (float)acc[tm][tn][q] * __int_as_float(p0[tn][q]);
+                                    f = med3f(f, lo_f, hi_f);
+                                    b[q] = (uint32_t)__float_as_int(f + magic);
+                                    if constexpr (!EVEN) b[q] += (uint32_t)g.y_zp;
+                                }
+                                packed[tn] = pack_low_bytes(b[0], b[1], b[2], b[3]);
+                            }
+                        };
+                        if ((g.y_zp & 1) == 0) rqb_row(std::true_type{});
+                        else rqb_row(std::false_type{});
+                    }
+                } else if (EPI == EPI_RQD && sat_u8) {
+                    // RQ-D into uint8: sat(rne(acc*cm + zp)); a value >= 2^31
+                    // (or NaN) converts to INT32_MIN on x86 and clamps to 0
+                    const float zp_f = (float)g.y_zp;
+#pragma unroll
+                    for (int tn = 0; tn < 4; ++tn) {
+                        uint32_t w = 0;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const float t = (float)acc[tm][tn][q] * cm;
+                            float val = t + zp_f;
+                            val = val < 2147483648.0f ? val : -1.0f;
+                            w = __builtin_amdgcn_cvt_pk_u8_f32(val, q, w);
+                        }
+                        packed[tn] = w;
+                    }
                 } else {
 #pragma unroll
                     for (int tn = 0; tn < 4; ++tn) {
@@ -420,12 +506,14 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                     if (i0 + 16 <= g.add_body) {
                         // RQ-E body; |v| < 2^22 is checked on the host, so
                         // clamp-then-round equals the reference's rint, cvt,
-                        // saturate, and rne_bits is exact
+                        // saturate, and rne_bits is exact. Into uint8 the
+                        // clamp is [0, 255], the saturation of
+                        // v_cvt_pk_u8_f32.
                         const float lo_f = (float)g.lo, hi_f = (float)g.hi;
 #pragma unroll
                         for (int tn = 0; tn < 4; ++tn) {
                             const uint32_t qw = packed[tn], rw = (uint32_t)rcur[tm][tn];
-                            uint32_t ob[4];
+                            uint32_t ob[4], w = 0;
 #pragma unroll
                             for (int q = 0; q < 4; ++q) {
                                 float qf, rf;
@@ -440,10 +528,14 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                                 const float bf = g.add_conv_is_a ? rf : qf;
                                 float v = __builtin_fmaf(bf, g.add_sb, g.add_fixed);
                                 v = __builtin_fmaf(af, g.add_sa, v);
-                                v = med3f(v, lo_f, hi_f);
-                                ob[q] = (uint32_t)rne_bits(v);
+                                if (sgn) {
+                                    v = med3f(v, lo_f, hi_f);
+                                    ob[q] = (uint32_t)rne_bits(v);
+                                } else {
+                                    w = __builtin_amdgcn_cvt_pk_u8_f32(v, q, w);
+                                }
                             }
-                            packed[tn] = pack_low_bytes(ob[0], ob[1], ob[2], ob[3]);
+                            packed[tn] = sgn ? pack_low_bytes(ob[0], ob[1], ob[2], ob[3]) : w;
                         }
                     } else {
                         // the row segment reaches the scalar tail
@@ -523,24 +615,7 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
         }
         if (p_t < t_end) p_issue();
 
-        if (c_kt == 0) {
-            // the tile's constants landed with its first K-step: start the
-            // accumulators at c0[n] (this lane's 16 columns), or at
-            // -alpha * colsum[n] when the zero point is only known now
-            const uint8_t* ps = lds + S * STAGE + (c_tseq % S) * PSLOT;
-            const int nl = wn * 64 + 16 * fchunk;
-#pragma unroll
-            for (int tn = 0; tn < 4; ++tn) {
-                v4i c = *(const v4i*)(ps + (nl + 4 * tn) * 4);
-                if (!g.c0) {
-                    c.x = (int)(neg_alpha * (uint32_t)c.x); c.y = (int)(neg_alpha * (uint32_t)c.y);
-                    c.z = (int)(neg_alpha * (uint32_t)c.z); c.w = (int)(neg_alpha * (uint32_t)c.w);
-                }
-#pragma unroll
-                for (int tm = 0; tm < 4; ++tm) acc[tm][tn] = c;
-            }
-        }
-        const uint8_t* st = lds + (c_gs % S) * STAGE;
+        const uint8_t* st = lds + c_stage;
         v4i xf[4], wf[4];
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) {
@@ -551,12 +626,36 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
 #pragma unroll
         for (int tn = 0; tn < 4; ++tn)
             wf[tn] = *(const v4i*)(st + BM * 64 + dma_lds_off(wn * 64 + tn * 16 + frow, fchunk));
+        if (c_kt == 0) {
+            // the tile's constants landed with its first K-step: the first
+            // MFMAs start from c0[n] (this lane's 16 columns), or from
+            // -alpha * colsum[n] when the zero point is only known now
+            const uint8_t* ps = lds + S * STAGE + c_pslot;
+            const int nl = wn * 64 + 16 * fchunk;
+            v4i ci[4];
 #pragma unroll
-        for (int tm = 0; tm < 4; ++tm)
+            for (int tn = 0; tn < 4; ++tn) {
+                v4i c = *(const v4i*)(ps + (nl + 4 * tn) * 4);
+                if (!g.c0) {
+                    c.x = (int)(neg_alpha * (uint32_t)c.x); c.y = (int)(neg_alpha * (uint32_t)c.y);
+                    c.z = (int)(neg_alpha * (uint32_t)c.z); c.w = (int)(neg_alpha * (uint32_t)c.w);
+                }
+                ci[tn] = c;
+            }
 #pragma unroll
-            for (int tn = 0; tn < 4; ++tn)
-                acc[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[tn], xf[tm], acc[tm][tn], 0, 0, 0);
+            for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < 4; ++tn)
+                    acc[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[tn], xf[tm], ci[tn], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < 4; ++tn)
+                    acc[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[tn], xf[tm], acc[tm][tn], 0, 0, 0);
+        }
         ++c_gs;
+        c_stage = c_stage + STAGE == S * STAGE ? 0 : c_stage + STAGE;
         if (++c_kt == nk) {
             epilogue();
             if constexpr (FUSE == FUSE_ADD) {
@@ -564,7 +663,7 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                 for (int tm = 0; tm < 4; ++tm) rcur[tm] = rnext[tm];
             }
             c_kt = 0;
-            ++c_tseq;
+            c_pslot = c_pslot + PSLOT == S * PSLOT ? 0 : c_pslot + PSLOT;
             c_t += t_step;
             if (c_t >= t_end) break;
         }
@@ -596,6 +695,12 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
     if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
     GemmArgs a = g;
     a.nbatch = batch;
+    {
+        const uint32_t nbn = (uint32_t)((g.N + BN - 1) / BN);
+        const uint32_t per_z = (uint32_t)((g.M + BM - 1) / BM) * nbn;
+        fast_div_consts(per_z, &a.div_pz_mul, &a.div_pz_shift);
+        fast_div_consts(nbn, &a.div_nbn_mul, &a.div_nbn_shift);
+    }
     if (g.H > 0) {
         fast_div_consts((uint32_t)(g.oH * g.oW), &a.div_sp_mul, &a.div_sp_shift);
         fast_div_consts((uint32_t)g.oW, &a.div_ow_mul, &a.div_ow_shift);
@@ -613,7 +718,7 @@ hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
         return hipErrorNotSupported;
     }
     if (g.add_other) {
-        if constexpr (AMODE == A_CONV || AMODE == A_DENSE) {
+        if constexpr (AMODE == A_CONV || AMODE == A_CONVU || AMODE == A_DENSE) {
             if (g.epi == EPI_RQB && batch == 1)
                 return launch_dma<BM, BN, S_ADD, AMODE, EPI_RQB, FUSE_ADD>(g, batch, s);
         }
@@ -669,6 +774,14 @@ bool qgemm_dma_eligible(const GemmArgs& g, int vec) {
     return true;
 }
 
+// the uniform-tap conv producer: every 64-byte K step inside one tap, the
+// tap-validity mask of a row in 32 bits, tap offsets in int32
+static bool conv_uniform_taps(const GemmArgs& g) {
+    if (g.C % 64 || g.Kp != g.K || g.kH * g.kW > 32) return false;
+    const long long span = ((long long)(g.kH - 1) * g.dH * g.W + (long long)(g.kW - 1) * g.dW) * g.Cs + g.C;
+    return span < 0x7fffffffLL;
+}
+
 hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t s) {
     const bool conv = g.H > 0;
     if (g.kWp > 0) {
@@ -679,18 +792,22 @@ hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t 
         default: return hipErrorInvalidValue;
         }
     }
+    const bool uni = conv && conv_uniform_taps(g);
     switch (tile) {
     case TILE_128x128:
         // 3 stages at 3 blocks per CU; the fused-add variant keeps 4 stages at
         // 2 blocks (it needs the registers of the lookahead residual)
-        return conv ? launch_dma_epi<128, 128, 3, A_CONV, 4>(g, batch, s)
-                    : launch_dma_epi<128, 128, 3, A_DENSE, 4>(g, batch, s);
+        if (!conv) return launch_dma_epi<128, 128, 3, A_DENSE, 4>(g, batch, s);
+        return uni ? launch_dma_epi<128, 128, 3, A_CONVU, 4>(g, batch, s)
+                   : launch_dma_epi<128, 128, 3, A_CONV, 4>(g, batch, s);
     case TILE_256x64:
-        return conv ? launch_dma_epi<256, 64, 3, A_CONV>(g, batch, s)
-                    : launch_dma_epi<256, 64, 3, A_DENSE>(g, batch, s);
+        if (!conv) return launch_dma_epi<256, 64, 3, A_DENSE>(g, batch, s);
+        return uni ? launch_dma_epi<256, 64, 3, A_CONVU>(g, batch, s)
+                   : launch_dma_epi<256, 64, 3, A_CONV>(g, batch, s);
     case TILE_64x256:
-        return conv ? launch_dma_epi<64, 256, 3, A_CONV>(g, batch, s)
-                    : launch_dma_epi<64, 256, 3, A_DENSE>(g, batch, s);
+        if (!conv) return launch_dma_epi<64, 256, 3, A_DENSE>(g, batch, s);
+        return uni ? launch_dma_epi<64, 256, 3, A_CONVU>(g, batch, s)
+                   : launch_dma_epi<64, 256, 3, A_CONV>(g, batch, s);
     default:
         return hipErrorInvalidValue;
     }
