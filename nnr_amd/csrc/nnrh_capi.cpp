@@ -694,8 +694,10 @@ extern "C" int nnrh_qconv_fuse_add(nnrh_qconv_t h, const nnrh_qadd_fuse_desc* a)
     const nnrh_qconv_desc& d = h->d;
     GemmArgs g = h->g;
     const bool rqb = h->branch == NNRH_BR_PACKED || h->branch == NNRH_BR_NR16;
+    // the residual tile travels in 16-byte chunks of whole output rows;
+    // uint8 output only (the kernel's fused path is the unsigned one)
     if (h->use_dw || h->transform == 3 || h->groups != 1 || !d.y_nhwc || !rqb || g.ldy != g.N ||
-        !qgemm_dma_eligible(g, h->vec))
+        (g.N % 16) != 0 || g.y_type != 0 || !qgemm_dma_eligible(g, h->vec))
         return set_err(NNRH_ERR_UNSUPPORTED, "qconv_fuse_add: this convolution's kernel has no fused add");
     // QLinearAdd.cpp:46-47,66-67 (no contraction), as nnrh_qlinear_add
     g.add_sa = a->a_scale / a->y_scale;
@@ -743,6 +745,8 @@ extern "C" int nnrh_qconv_run_add(nnrh_qconv_t h, const void* x, const void* oth
     }
     if (((uintptr_t)src & 15) != 0)
         return set_err(NNRH_ERR_INVALID, "qconv_run_add: input must be 16-byte aligned");
+    if (((uintptr_t)other & 15) != 0)
+        return set_err(NNRH_ERR_INVALID, "qconv_run_add: other must be 16-byte aligned");
     GemmArgs g = h->g;
     g.a = src;
     g.y = y;
@@ -908,8 +912,9 @@ extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc*
 extern "C" int nnrh_qmatmul_fuse_dq_bias(nnrh_qmatmul_t h, float dq_scale, int dq_zp, const float* bias_host) {
     if (!h) return set_err(NNRH_ERR_INVALID, "qmatmul_fuse_dq_bias: NULL handle");
     const GemmArgs& g = h->g;
+    // uint8 output only (the kernel's fused path reads the bytes unsigned)
     if (h->d.scale_dtype != NNRH_F32 || dq_zp != g.y_zp || g.beta != 0 || g.K % 16 || g.lda % 16 ||
-        g.c0_absmax + 16384LL * g.Kp >= 0x7fffffffLL)
+        g.y_type != 0 || g.c0_absmax + 16384LL * g.Kp >= 0x7fffffffLL)
         return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_fuse_dq_bias: not available for this QLinearMatMul");
     const int n = h->d.n, Np = g.Np;
     std::vector<float> b((size_t)Np, 0.0f);

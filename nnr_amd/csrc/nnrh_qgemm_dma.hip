@@ -109,12 +109,22 @@ __device__ __forceinline__ int qadd_elem(int a, int b, const GemmArgs& g, bool t
     return clampi(x86_f2i(__builtin_rintf(v)), g.lo, g.hi);
 }
 
+// LDS bytes of one block: S stages of A and B rows plus S per-tile slots,
+// each NPX per-column arrays (1 KB granules) and, with a fused add, the
+// tile's residual bytes
+template <int BM, int BN, int S, int NPX, int FUSE>
+constexpr int dma_pslot_bytes() {
+    return ((NPX * BN * 4 + 1023) / 1024) * 1024 + (FUSE == FUSE_ADD ? BM * BN : 0);
+}
+template <int BM, int BN, int S, int NPX, int FUSE>
+constexpr int dma_lds_bytes() { return S * (BM + BN) * 64 + S * dma_pslot_bytes<BM, BN, S, NPX, FUSE>(); }
 // blocks per CU the kernel is compiled for: LDS and registers must fit them
-template <int BM, int BN, int S>
-constexpr int dma_min_blocks() { return ((BM + BN) * 64 * S + 4096) * 3 <= 160 * 1024 ? 3 : 2; }
+template <int BM, int BN, int S, int NPX, int FUSE>
+constexpr int dma_min_blocks() { return dma_lds_bytes<BM, BN, S, NPX, FUSE>() * 3 <= 160 * 1024 ? 3 : 2; }
 
 template <int BM, int BN, int S, int AMODE, int EPI, int FUSE>
-__global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S, EpiParams<EPI>::NP + (FUSE == FUSE_DQB ? 1 : 0), FUSE>()))
+void qgemm_dma_kernel(GemmArgs g) {
     constexpr int WAVES_N = BN / 64;
     static_assert((BM / 64) * WAVES_N == 4, "4 waves of 64x64");
     constexpr int A_CH = BM / 64;            // DMA chunks per thread per step (A)
@@ -125,10 +135,16 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
     constexpr int NPX = NP + (FUSE == FUSE_DQB ? 1 : 0);   // + the fp32 bias
     constexpr int PBYTES = NPX * BN * 4;
     constexpr int PWAVES = (PBYTES + 1023) / 1024;   // waves issuing the param DMA
-    constexpr int PSLOT = PWAVES * 1024;
     static_assert(PWAVES <= 4, "param slot");
+    // per-tile slot: the per-column arrays, then (fused add) the residual tile
+    // as BM rows of BN bytes, 16-byte chunks XOR-swizzled by row
+    constexpr int PPAR = PWAVES * 1024;
+    constexpr int PSLOT = dma_pslot_bytes<BM, BN, S, NPX, FUSE>();
+    constexpr int RCPR = BN / 16;                    // residual chunks per row
+    constexpr int RCH = FUSE == FUSE_ADD ? BM * BN / 4096 : 0;   // residual DMAs per thread
 
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE + S * PSLOT];
+    static_assert(FUSE != FUSE_ADD || (BM * BN) % 4096 == 0, "residual DMA granule");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -205,9 +221,11 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
     int kc_ic = 0, kc_kh = 0, kc_kw = 0;   // A_CONV: tap of this thread's chunk
     int u_tap = 0, u_ic = 0, u_kh = 0, u_kw = 0, u_off = 0;   // A_CONVU: the step's tap
 
+    int p_setup_m0 = 0;
     auto p_setup = [&](int t) {
         int z, m0;
         decode(t, z, m0, p_n0);
+        p_setup_m0 = m0;
         p_a = g.a + (long long)z * g.a_bstride;
         const int8_t* pb = g.b + (long long)z * g.b_bstride;
         p_pbase = (long long)z * g.param_bstride;
@@ -329,6 +347,24 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
             const uint8_t* src = (const uint8_t*)base + (p_pbase + c) * 4;
             dma16(src, lds + S * STAGE + p_pslot + wave * 1024);
         }
+        if constexpr (FUSE == FUSE_ADD) {
+            if (p_kt == 0) {
+                // the residual tile of the fused QLinearAdd (batch 1, row stride
+                // and base 16-byte aligned, N % 16 == 0: checked by the launcher);
+                // it lands with the tile's first K step, so the step waits cover it
+                const int m0 = p_setup_m0;
+#pragma unroll
+                for (int j = 0; j < RCH; ++j) {
+                    const int p = j * 256 + wave * 64 + lane;   // chunk position in the slot
+                    const int row = p / RCPR, pc = p - row * RCPR;
+                    const int lc = pc ^ (row & (RCPR - 1));
+                    const int m = m0 + row, n = p_n0 + lc * 16;
+                    const uint8_t* src = pad16;
+                    if (m < g.M && n < g.N) src = g.add_other + (long long)m * g.ldy + n;
+                    dma16(src, lds + S * STAGE + p_pslot + PPAR + (j * 256 + wave * 64) * 16);
+                }
+            }
+        }
         // advance
         ++p_gs;
         p_stage = p_stage + STAGE == S * STAGE ? 0 : p_stage + STAGE;
@@ -364,33 +400,9 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
     int c_stage = 0, c_pslot = 0;
     v4i acc[4][4];   // started from c0 by the tile's first K-step
 
-    // fused add: residual bytes of this lane's 4 rows x 16 channels. They
-    // are loaded one tile ahead (at the first K-step of the previous tile,
-    // before that step's DMA issue), so the epilogue's wait for them only
-    // covers loads the pipeline needs by then anyway.
-    v4i rcur[4], rnext[4];
-    auto load_residual = [&](int t, v4i* rr) {
-        int z, m0, n0;
-        decode(t, z, m0, n0);   // batch 1 (checked by the launcher)
-        const int nb = n0 + wn * 64 + 16 * fchunk;
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm) {
-            rr[tm] = v4i{0, 0, 0, 0};
-            const int m = m0 + wm * 64 + tm * 16 + frow;
-            if (m >= g.M || nb >= g.N) continue;
-            const uint8_t* rp = g.add_other + (long long)m * g.ldy + nb;
-            if (nb + 16 <= g.N && ((((uintptr_t)rp) & 15) == 0)) {
-                rr[tm] = *(const v4i*)rp;
-            } else {
-                uint32_t w[4] = {0u, 0u, 0u, 0u};
-                for (int i = 0; i < 16; ++i)
-                    if (nb + i < g.N) w[i >> 2] |= (uint32_t)rp[i] << (8 * (i & 3));
-                rr[tm] = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-            }
-        }
-    };
-
-    auto epilogue = [&]() {
+    // conv_is_a: the conv byte is input A of the fused QLinearAdd (else B)
+    auto epilogue = [&](auto conv_is_a_t) {
+        constexpr bool CONV_A = decltype(conv_is_a_t)::value;
         int z, m0, n0;
         decode(c_t, z, m0, n0);
         const int nl = wn * 64 + 16 * fchunk;   // first column of this lane in the tile
@@ -501,55 +513,42 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                     }
                 }
                 if constexpr (FUSE == FUSE_ADD) {
-                    const bool sgn = g.y_type == 1;
+                    // uint8 output (checked on the host)
                     const long long i0 = (long long)m * g.ldy + nb;
+                    // this lane's 16 residual bytes (row m, columns nb..nb+15)
+                    const int rrow = wm * 64 + tm * 16 + frow;
+                    const int rpc = (wn * 4 + fchunk) ^ (rrow & (RCPR - 1));
+                    const v4i rres = *(const v4i*)(ps + PPAR + (rrow * RCPR + rpc) * 16);
                     if (i0 + 16 <= g.add_body) {
-                        // RQ-E body; |v| < 2^22 is checked on the host, so
-                        // clamp-then-round equals the reference's rint, cvt,
-                        // saturate, and rne_bits is exact. Into uint8 the
-                        // clamp is [0, 255], the saturation of
-                        // v_cvt_pk_u8_f32.
-                        const float lo_f = (float)g.lo, hi_f = (float)g.hi;
+                        // RQ-E body, fma(a, sa, fma(b, sb, fixed)); into uint8
+                        // the reference's rint, cvt and saturation is
+                        // v_cvt_pk_u8_f32 (round to nearest even, clamp [0,255])
 #pragma unroll
                         for (int tn = 0; tn < 4; ++tn) {
-                            const uint32_t qw = packed[tn], rw = (uint32_t)rcur[tm][tn];
-                            uint32_t ob[4], w = 0;
+                            const uint32_t qw = packed[tn], rw = (uint32_t)rres[tn];
+                            uint32_t w = 0;
 #pragma unroll
                             for (int q = 0; q < 4; ++q) {
-                                float qf, rf;
-                                if (sgn) {
-                                    qf = (float)(int)(int8_t)(qw >> (8 * q));
-                                    rf = (float)(int)(int8_t)(rw >> (8 * q));
-                                } else {
-                                    qf = (float)((qw >> (8 * q)) & 0xffu);
-                                    rf = (float)((rw >> (8 * q)) & 0xffu);
-                                }
-                                const float af = g.add_conv_is_a ? qf : rf;
-                                const float bf = g.add_conv_is_a ? rf : qf;
-                                float v = __builtin_fmaf(bf, g.add_sb, g.add_fixed);
-                                v = __builtin_fmaf(af, g.add_sa, v);
-                                if (sgn) {
-                                    v = med3f(v, lo_f, hi_f);
-                                    ob[q] = (uint32_t)rne_bits(v);
-                                } else {
-                                    w = __builtin_amdgcn_cvt_pk_u8_f32(v, q, w);
-                                }
+                                const float qf = (float)((qw >> (8 * q)) & 0xffu);
+                                const float rf = (float)((rw >> (8 * q)) & 0xffu);
+                                float v = __builtin_fmaf(CONV_A ? rf : qf, g.add_sb, g.add_fixed);
+                                v = __builtin_fmaf(CONV_A ? qf : rf, g.add_sa, v);
+                                w = __builtin_amdgcn_cvt_pk_u8_f32(v, q, w);
                             }
-                            packed[tn] = sgn ? pack_low_bytes(ob[0], ob[1], ob[2], ob[3]) : w;
+                            packed[tn] = w;
                         }
                     } else {
                         // the row segment reaches the scalar tail
 #pragma unroll
                         for (int tn = 0; tn < 4; ++tn) {
                             uint32_t w = 0;
-                            const uint32_t rw = (uint32_t)rcur[tm][tn];
+                            const uint32_t rw = (uint32_t)rres[tn];
 #pragma unroll
                             for (int q = 0; q < 4; ++q) {
-                                int qc = (int)((packed[tn] >> (8 * q)) & 0xffu);
-                                int rv = (int)((rw >> (8 * q)) & 0xffu);
-                                if (sgn) { qc = (int)(int8_t)qc; rv = (int)(int8_t)rv; }
-                                const int a = g.add_conv_is_a ? qc : rv;
-                                const int b = g.add_conv_is_a ? rv : qc;
+                                const int qc = (int)((packed[tn] >> (8 * q)) & 0xffu);
+                                const int rv = (int)((rw >> (8 * q)) & 0xffu);
+                                const int a = CONV_A ? qc : rv;
+                                const int b = CONV_A ? rv : qc;
                                 const int o = qadd_elem(a, b, g, i0 + 4 * tn + q >= g.add_body);
                                 w |= (uint32_t)(o & 0xff) << (8 * q);
                             }
@@ -566,8 +565,8 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
                     float o[16];
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
-                        const uint32_t bq = (packed[i >> 2] >> (8 * (i & 3))) & 0xffu;
-                        const float qf = g.y_type == 1 ? (float)(int)(int8_t)bq : (float)bq;
+                        // uint8 output (checked on the host)
+                        const float qf = (float)((packed[i >> 2] >> (8 * (i & 3))) & 0xffu);
                         const float d = (qf - zp_f) * g.dq_scale;
                         o[i] = d + *(const float*)(pb + 4 * i);
                     }
@@ -595,7 +594,6 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
     };
 
     // ---- prologue: S-1 steps in flight
-    if constexpr (FUSE == FUSE_ADD) load_residual(t_first, rcur);
     p_setup(p_t);
 #pragma unroll
     for (int s = 0; s < S - 1; ++s)
@@ -610,9 +608,6 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
         // every wave's DMAs of the step have landed; every wave is done
         // reading the stage (and param slot) the next issue overwrites
         block_barrier();
-        if constexpr (FUSE == FUSE_ADD) {
-            if (c_kt == 0 && c_t + t_step < t_end) load_residual(c_t + t_step, rnext);
-        }
         if (p_t < t_end) p_issue();
 
         const uint8_t* st = lds + c_stage;
@@ -657,11 +652,8 @@ __global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S>())) void qgemm_dma_
         ++c_gs;
         c_stage = c_stage + STAGE == S * STAGE ? 0 : c_stage + STAGE;
         if (++c_kt == nk) {
-            epilogue();
-            if constexpr (FUSE == FUSE_ADD) {
-#pragma unroll
-                for (int tm = 0; tm < 4; ++tm) rcur[tm] = rnext[tm];
-            }
+            if (FUSE == FUSE_ADD && g.add_conv_is_a) epilogue(std::true_type{});
+            else epilogue(std::false_type{});
             c_kt = 0;
             c_pslot = c_pslot + PSLOT == S * PSLOT ? 0 : c_pslot + PSLOT;
             c_t += t_step;
@@ -795,19 +787,19 @@ hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t 
     const bool uni = conv && conv_uniform_taps(g);
     switch (tile) {
     case TILE_128x128:
-        // 3 stages at 3 blocks per CU; the fused-add variant keeps 4 stages at
-        // 2 blocks (it needs the registers of the lookahead residual)
-        if (!conv) return launch_dma_epi<128, 128, 3, A_DENSE, 4>(g, batch, s);
-        return uni ? launch_dma_epi<128, 128, 3, A_CONVU, 4>(g, batch, s)
-                   : launch_dma_epi<128, 128, 3, A_CONV, 4>(g, batch, s);
+        // 3 stages at 3 blocks per CU; the fused-add variant carries a 16 KB
+        // residual tile per slot and runs 2 stages at 2 blocks per CU
+        if (!conv) return launch_dma_epi<128, 128, 3, A_DENSE, 2>(g, batch, s);
+        return uni ? launch_dma_epi<128, 128, 3, A_CONVU, 2>(g, batch, s)
+                   : launch_dma_epi<128, 128, 3, A_CONV, 2>(g, batch, s);
     case TILE_256x64:
-        if (!conv) return launch_dma_epi<256, 64, 3, A_DENSE>(g, batch, s);
-        return uni ? launch_dma_epi<256, 64, 3, A_CONVU>(g, batch, s)
-                   : launch_dma_epi<256, 64, 3, A_CONV>(g, batch, s);
+        if (!conv) return launch_dma_epi<256, 64, 3, A_DENSE, 2>(g, batch, s);
+        return uni ? launch_dma_epi<256, 64, 3, A_CONVU, 2>(g, batch, s)
+                   : launch_dma_epi<256, 64, 3, A_CONV, 2>(g, batch, s);
     case TILE_64x256:
-        if (!conv) return launch_dma_epi<64, 256, 3, A_DENSE>(g, batch, s);
-        return uni ? launch_dma_epi<64, 256, 3, A_CONVU>(g, batch, s)
-                   : launch_dma_epi<64, 256, 3, A_CONV>(g, batch, s);
+        if (!conv) return launch_dma_epi<64, 256, 3, A_DENSE, 2>(g, batch, s);
+        return uni ? launch_dma_epi<64, 256, 3, A_CONVU, 2>(g, batch, s)
+                   : launch_dma_epi<64, 256, 3, A_CONV, 2>(g, batch, s);
     default:
         return hipErrorInvalidValue;
     }

@@ -202,8 +202,10 @@ def test_qconv_no_bias(dev):
 FUSED_ADD_CASES = [
     # name, N, C, H, W, OC, k, pads, conv_is_a
     ("1x1_conv_a", 2, 64, 14, 15, 256, 1, (0, 0, 0, 0), 1),
-    # 63*72 elements: the last 8 take QLinearAdd's scalar-tail expression
-    ("3x3_conv_b_tail", 1, 64, 9, 7, 72, 3, (1, 1, 1, 1), 0),
+    # a ragged last column block (80 of 128) and conv as the add's B input
+    ("3x3_conv_b", 1, 64, 9, 7, 80, 3, (1, 1, 1, 1), 0),
+    # uniform-tap conv (C % 64 == 0), several K steps per tile
+    ("3x3_c256_a", 2, 256, 10, 9, 192, 3, (1, 1, 1, 1), 1),
     ("persistent", 16, 64, 56, 56, 256, 1, (0, 0, 0, 0), 1),
 ]
 
@@ -242,6 +244,16 @@ def test_qconv_fuse_add_unsupported(dev):
     assert not op.fuse_add(1, 0.05, 0, 0.05, 0, 0.05, 0)
     ref, _ = O.Conv(1, 3, 20, 20, 16, 3, 3, **kw).run(x, w)
     assert np.array_equal(to_np(op(to_dev(x, dev))), ref)
+    # output channels off the 16-byte grid: the residual cannot travel in
+    # whole 16-byte chunks, so the add stays a separate operator
+    x2 = rng.integers(0, 256, (1, 9, 7, 64), dtype=np.uint8)
+    w2 = rng.integers(-127, 128, (72, 64, 3, 3), dtype=np.int8)
+    kw2 = dict(pads=(1, 1, 1, 1), x_nhwc=1, y_nhwc=1, x_scale=0.02, x_zp=128, y_scale=0.05,
+               y_zp=3, w_scale=np.full(72, 0.004, np.float32))
+    op2 = H.QLinearConv(1, 64, 9, 7, w2, **kw2)
+    assert not op2.fuse_add(0, 0.041, 7, 0.023, 131, 0.06, 2)
+    ref2, _ = O.Conv(1, 64, 9, 7, 72, 3, 3, **kw2).run(x2, w2)
+    assert np.array_equal(to_np(op2(to_dev(x2, dev))), ref2)
 
 
 # ---------------------------------------------------------------------------
