@@ -126,8 +126,9 @@ int nnrh_qconv_destroy(nnrh_qconv_t h);
  * expressions (src/backend/cpu/QLinearAdd.cpp:66-104) with the same element
  * split. conv_is_a: 1 when the conv output is the add's input A. Available
  * for the RQ-B branches (PACKED, NR16) with group 1, NHWC output and
- * channels % 16 == 0; otherwise returns NNRH_ERR_UNSUPPORTED and leaves the
- * handle unchanged. After a successful call, run with nnrh_qconv_run_add. */
+ * output channels % 16 == 0 and a uint8 output; otherwise returns
+ * NNRH_ERR_UNSUPPORTED and leaves the handle unchanged. After a successful
+ * call, run with nnrh_qconv_run_add; other_dev must be 16-byte aligned.   */
 typedef struct nnrh_qadd_fuse_desc {
     int conv_is_a;
     float a_scale; int a_zp;
@@ -137,6 +138,17 @@ typedef struct nnrh_qadd_fuse_desc {
 int nnrh_qconv_fuse_add(nnrh_qconv_t h, const nnrh_qadd_fuse_desc* d);
 int nnrh_qconv_run_add(nnrh_qconv_t h, const void* x_dev, const void* other_dev,
                        void* y_dev, void* stream);
+/* No counterpart in the reference: the QuantizeLinear that produces a
+ * first-layer conv's uint8 input (QuantizeLinear.cpp:128-194, per-tensor
+ * scale and uint8 zero point) runs inside the kernel that lays the input out
+ * for the conv, reading the fp32 NCHW tensor directly: one pass over it
+ * instead of a quantize pass and a layout pass. Every byte equals
+ * QuantizeLinear's (same body / tail split by flat index). Only for the
+ * first-layer branch with its multi-copy input (nnrh_qconv_branch FIRST
+ * on uint8 NCHW input); otherwise NNRH_ERR_UNSUPPORTED. After a successful
+ * call the handle runs with nnrh_qconv_run_f32 only.                      */
+int nnrh_qconv_fuse_quantize(nnrh_qconv_t h, float scale, int zero_point);
+int nnrh_qconv_run_f32(nnrh_qconv_t h, const float* x_dev, void* y_dev, void* stream);
 
 /* ---- QLinearMatMul ------------------------------------------------------
  * Replaces QLinearMatMul_operator (src/backend/cpu/QLinearMatMul.cpp:14-233)
@@ -223,6 +235,14 @@ int nnrh_nchw_to_nhwc_u8(const uint8_t* x_dev, uint8_t* y_dev, int N, int C,
  * [N][HW][C] (x_nhwc) -> y [N][C].                                        */
 int nnrh_global_avgpool_f32(const float* x_dev, float* y_dev, int N, int C, int HW,
                             int x_nhwc, void* stream);
+/* No counterpart in the reference: DequantizeLinear (DequantizeLinear.cpp:
+ * 133-152, per-tensor scale and zero point, uint8 or int8 x) feeding
+ * GlobalAveragePool, in one pass over the 8-bit tensor. Each value is
+ * fl((q - zp) * s) and the sums run in nnrh_global_avgpool_f32's order, so
+ * y equals the two operators run separately.                              */
+int nnrh_global_avgpool_dequant(const void* x_dev, float* y_dev, int N, int C, int HW,
+                                int x_nhwc, int x_dtype, float scale, int zero_point,
+                                void* stream);
 /* Gemm (src/backend/cpu/Gemm.cpp): Y = alpha*op(A)*op(B) + beta*C, row-major;
  * c_mode: 0 no C, 1 scalar, 2 [N], 3 [M][N], 4 [M] (broadcast per row).   */
 int nnrh_gemm_f32(const float* a_dev, const float* b_dev, const float* c_dev, float* y_dev,

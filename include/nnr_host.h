@@ -76,6 +76,11 @@ int nnr_ctx_node_fused_add(nnr_ctx_t ctx, int i, int j, const char** tensor_name
  * DequantizeLinear and bias Add after a QLinearMatMul), k = 0, 1, ...; ""
  * past the last. No counterpart in the reference. */
 int nnr_ctx_node_fused_chain(nnr_ctx_t ctx, int i, int k, const char** node_name);
+/* Graph nodes folded into active node i's kernel before it (a
+ * QuantizeLinear feeding a first-layer QLinearConv, a DequantizeLinear
+ * feeding GlobalAveragePool), k = 0, 1, ...; "" past the last. Node i then
+ * reads the first one's input. No counterpart in the reference. */
+int nnr_ctx_node_fused_pre(nnr_ctx_t ctx, int i, int k, const char** node_name);
 int nnr_ctx_fusion_stat(nnr_ctx_t ctx, const char* key, int* value);
 size_t nnr_ctx_device_bytes(nnr_ctx_t ctx);
 

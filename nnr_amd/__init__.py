@@ -113,6 +113,24 @@ class QLinearConv:
                                        cur_stream() if stream is None else stream))
         return y
 
+    def fuse_quantize(self, scale, zero_point):
+        """Run the QuantizeLinear producing this first-layer conv's input in the
+        conv's layout kernel; afterwards call run_f32 with the fp32 input."""
+        rc = lib().nnrh_qconv_fuse_quantize(self.h, float(scale), int(zero_point))
+        if rc == NNRH_ERR_UNSUPPORTED:
+            return False
+        check(rc)
+        return True
+
+    def run_f32(self, x, y=None, stream=None):
+        import torch
+        if tuple(x.shape) != self.in_shape or not x.is_contiguous() or x.dtype != torch.float32:
+            raise ValueError(f"x must be contiguous float32 of shape {self.in_shape}")
+        if y is None:
+            y = torch.empty(self.out_shape, dtype=torch.uint8, device=x.device)
+        check(lib().nnrh_qconv_run_f32(self.h, ptr(x), ptr(y), cur_stream() if stream is None else stream))
+        return y
+
     def __del__(self):
         try:
             if getattr(self, "h", None):

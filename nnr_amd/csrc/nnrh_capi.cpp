@@ -341,6 +341,9 @@ struct nnrh_qconv {
     bool use_dw = false;         // depthwise VALU kernel
     bool dw16 = false;           // ... its dot4 variant (NHWC out, C % 16 == 0, w_zp 0)
     bool fused_add = false;      // nnrh_qconv_fuse_add was called
+    bool fused_quant = false;    // nnrh_qconv_fuse_quantize was called: input is fp32
+    float q_scale = 1.0f;
+    int q_zp = 0;
     int transform = 0;           // 0 none, 1 NCHW->NHWC, 2 NCHW->NHWC padded to 4 ch,
                                  // 3 first-layer padded multi-copy NHWC4 image,
                                  // 4 NHWC channels padded to a multiple of 16
@@ -629,8 +632,14 @@ extern "C" int nnrh_qconv_branch(nnrh_qconv_t h, int* branch) {
     return NNRH_OK;
 }
 
+namespace {
+// everything after the input transform (src: the kernel's input image)
+int qconv_compute(nnrh_qconv_t h, const uint8_t* src, void* y, hipStream_t s);
+}  // namespace
+
 extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stream) {
     if (!h || !x || !y) return set_err(NNRH_ERR_INVALID, "qconv_run: NULL argument");
+    if (h->fused_quant) return set_err(NNRH_ERR_INVALID, "qconv_run: quantize fused, use nnrh_qconv_run_f32");
     const nnrh_qconv_desc& d = h->d;
     hipStream_t s = S(stream);
     const uint8_t* src = (const uint8_t*)x;
@@ -653,6 +662,40 @@ extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stre
                 "nchw_to_nhwc");
         src = h->xs;
     }
+    return qconv_compute(h, src, y, s);
+}
+
+extern "C" int nnrh_qconv_fuse_quantize(nnrh_qconv_t h, float scale, int zp) {
+    if (!h) return set_err(NNRH_ERR_INVALID, "qconv_fuse_quantize: NULL handle");
+    if (!(scale > 0.0f) || zp < 0 || zp > 255)
+        return set_err(NNRH_ERR_INVALID, "qconv_fuse_quantize: scale %g / zero point %d", (double)scale, zp);
+    if (h->transform != 3 || h->d.act_dtype != NNRH_U8 || h->fused_add ||
+        h->g.W + ((4 >> h->g.copy_shift) - 1) * (1 << h->g.copy_shift) > 4096)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qconv_fuse_quantize: only the first layer's multi-copy input");
+    h->fused_quant = true;
+    h->q_scale = scale;
+    h->q_zp = zp;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qconv_run_f32(nnrh_qconv_t h, const float* x, void* y, void* stream) {
+    if (!h || !x || !y) return set_err(NNRH_ERR_INVALID, "qconv_run_f32: NULL argument");
+    if (!h->fused_quant) return set_err(NNRH_ERR_INVALID, "qconv_run_f32: nnrh_qconv_fuse_quantize was not called");
+    const nnrh_qconv_desc& d = h->d;
+    hipStream_t s = S(stream);
+    {
+        ProfScope ps("quantize_first_layer_copies", s);
+        HIP_TRY(launch_quantize_first_layer_copies(x, h->xs, d.N, d.C, d.H, d.W, h->g.H, h->g.W, d.pad_t,
+                                                   d.pad_l, h->g.copy_shift, (uint8_t)(d.x_zp & 0xff),
+                                                   h->q_scale, h->q_zp, s),
+                "quantize_first_layer_copies");
+    }
+    return qconv_compute(h, h->xs, y, s);
+}
+
+namespace {
+int qconv_compute(nnrh_qconv_t h, const uint8_t* src, void* y, hipStream_t s) {
+    const nnrh_qconv_desc& d = h->d;
     if (h->use_dw && h->dw16) {
         ProfScope ps("depthwise", s);
         HIP_TRY(launch_depthwise16(src, h->wdot, h->c0, (uint8_t*)y, h->cs, h->bf, d.N, d.C, d.H, d.W,
@@ -688,6 +731,7 @@ extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stre
     HIP_TRY(launch_qgemm(g, h->groups, h->tile, vec, s), "qgemm");
     return NNRH_OK;
 }
+}  // namespace
 
 extern "C" int nnrh_qconv_fuse_add(nnrh_qconv_t h, const nnrh_qadd_fuse_desc* a) {
     if (!h || !a) return set_err(NNRH_ERR_INVALID, "qconv_fuse_add: NULL argument");
@@ -1147,6 +1191,17 @@ extern "C" int nnrh_global_avgpool_f32(const float* x, float* y, int N, int C, i
     if (!x || !y || N <= 0 || C <= 0 || HW <= 0) return set_err(NNRH_ERR_INVALID, "gap: bad args");
     ProfScope ps("gap_f32", S(stream));
     HIP_TRY(launch_gap_f32(x, y, N, C, HW, x_nhwc, S(stream)), "gap_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_global_avgpool_dequant(const void* x, float* y, int N, int C, int HW, int x_nhwc,
+                                           int x_dtype, float scale, int zp, void* stream) {
+    if (!x || !y || N < 0 || C < 0 || HW <= 0) return set_err(NNRH_ERR_INVALID, "global_avgpool_dequant: arguments");
+    if (x_dtype != NNRH_U8 && x_dtype != NNRH_S8)
+        return set_err(NNRH_ERR_UNSUPPORTED, "global_avgpool_dequant: dtype %d", x_dtype);
+    hipStream_t s = S(stream);
+    ProfScope ps("gap_dequant", s);
+    HIP_TRY(launch_gap_dq((const uint8_t*)x, y, N, C, HW, x_nhwc, x_dtype == NNRH_S8, scale, zp, s), "gap_dequant");
     return NNRH_OK;
 }
 

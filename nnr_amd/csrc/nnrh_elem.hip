@@ -350,40 +350,42 @@ __device__ __forceinline__ uint32_t bytemax4(uint32_t a, uint32_t b) {
     return r;
 }
 
+// grid: x over (ow, 16-channel group) of one output row, y = oh, z = image
 __global__ __launch_bounds__(256) void maxpool_u8_16_kernel(const uint8_t* __restrict x,
                                                             uint8_t* __restrict y, int N, int C,
                                                             int iH, int iW, int oH, int oW, int kH,
                                                             int kW, int sH, int sW, int pH, int pW) {
     const int C16 = C >> 4;
-    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long total = (long long)N * oH * oW * C16;
-    if (idx >= total) return;
-    const int cg = (int)(idx % C16);
-    const long long pix = idx / C16;
-    const int ow = (int)(pix % oW), oh = (int)((pix / oW) % oH), n = (int)(pix / ((long long)oW * oH));
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= oW * C16) return;
+    const int ow = t / C16, cg = t - ow * C16;
+    const int oh = blockIdx.y, n = blockIdx.z;
     const int ih0 = oh * sH - pH, iw0 = ow * sW - pW;
     const int kh0 = ih0 < 0 ? -ih0 : 0, kh1 = kH < iH - ih0 ? kH : iH - ih0;
     const int kw0 = iw0 < 0 ? -iw0 : 0, kw1 = kW < iW - iw0 ? kW : iW - iw0;
+    const uint8_t* xi = x + (long long)n * iH * iW * C + cg * 16;
     uint32_t m[4] = {0, 0, 0, 0};
     for (int a = kh0; a < kh1; ++a)
         for (int b = kw0; b < kw1; ++b) {
-            uint4 v = *(const uint4*)(x + (((long long)n * iH + ih0 + a) * iW + iw0 + b) * C + cg * 16);
+            uint4 v = *(const uint4*)(xi + ((long long)(ih0 + a) * iW + iw0 + b) * C);
             m[0] = bytemax4(m[0], v.x);
             m[1] = bytemax4(m[1], v.y);
             m[2] = bytemax4(m[2], v.z);
             m[3] = bytemax4(m[3], v.w);
         }
+    const long long pix = ((long long)n * oH + oh) * oW + ow;
     *(uint4*)(y + pix * C + cg * 16) = make_uint4(m[0], m[1], m[2], m[3]);
 }
 
 hipError_t launch_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH, int iW,
                                   int oH, int oW, int kH, int kW, int sH, int sW, int pH, int pW,
                                   hipStream_t s) {
-    if ((C & 15) == 0 && (((uintptr_t)x | (uintptr_t)y) & 15) == 0) {
-        long long total = (long long)N * oH * oW * (C / 16);
-        if (total <= 0) return hipSuccess;
-        hipLaunchKernelGGL(maxpool_u8_16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                           s, x, y, N, C, iH, iW, oH, oW, kH, kW, sH, sW, pH, pW);
+    if ((C & 15) == 0 && (((uintptr_t)x | (uintptr_t)y) & 15) == 0 && N <= 65535 && oH <= 65535) {
+        const long long row = (long long)oW * (C / 16);
+        if (row <= 0 || N <= 0 || oH <= 0) return hipSuccess;
+        const dim3 grid((unsigned)((row + 255) / 256), (unsigned)oH, (unsigned)N);
+        hipLaunchKernelGGL(maxpool_u8_16_kernel, grid, dim3(256), 0, s, x, y, N, C, iH, iW, oH, oW, kH, kW,
+                           sH, sW, pH, pW);
         return hipGetLastError();
     }
     long long total = (long long)N * oH * oW * ((C + 3) / 4);

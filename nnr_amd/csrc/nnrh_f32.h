@@ -7,6 +7,9 @@ namespace nnrh {
 
 hipError_t launch_gap_f32(const float* x, float* y, int N, int C, int HW, int x_nhwc,
                           hipStream_t s);
+// DequantizeLinear (uint8 or int8, per-tensor) fused into GlobalAveragePool
+hipError_t launch_gap_dq(const uint8_t* x, float* y, int N, int C, int HW, int x_nhwc, int x_signed,
+                         float scale, int zp, hipStream_t s);
 // c_mode: 0 none, 1 scalar, 2 per-column [N], 3 full [M][N], 4 per-row [M]
 hipError_t launch_gemm_f32(const float* A, const float* B, const float* C, float* Y, int M, int N,
                            int K, int transA, int transB, float alpha, float beta, int c_mode,

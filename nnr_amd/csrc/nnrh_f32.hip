@@ -44,6 +44,48 @@ __global__ __launch_bounds__(256) void gap_f32_nhwc_kernel(const float* __restri
     y[row] = s / (float)HW;
 }
 
+// DequantizeLinear fused into GlobalAveragePool: every value is
+// fl((float(q) - float(zp)) * s) (DequantizeLinear.cpp:133-152) and the sums
+// run in the order of the fp32 kernels above, so the result equals
+// DequantizeLinear followed by launch_gap_f32.
+__device__ __forceinline__ float dq_one(const uint8_t* x, long long i, int sgn, float zpf, float sc) {
+    const float q = sgn ? (float)(int)(int8_t)x[i] : (float)x[i];
+    return (q - zpf) * sc;
+}
+__global__ __launch_bounds__(256) void gap_dq_nchw_kernel(const uint8_t* __restrict x, float* __restrict y,
+                                                          int N, int C, int HW, int sgn, float zpf, float sc) {
+    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= (long long)N * C) return;
+    float s = 0.0f;
+    for (int i = lane; i < HW; i += 64) s += dq_one(x, row * HW + i, sgn, zpf, sc);
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+    if (lane == 0) y[row] = s / (float)HW;
+}
+__global__ __launch_bounds__(256) void gap_dq_nhwc_kernel(const uint8_t* __restrict x, float* __restrict y,
+                                                          int N, int C, int HW, int sgn, float zpf, float sc) {
+    const long long row = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (row >= (long long)N * C) return;
+    const int n = (int)(row / C), c = (int)(row % C);
+    const long long base = (long long)n * HW * C + c;
+    float s = 0.0f;
+    for (int i = 0; i < HW; ++i) s += dq_one(x, base + (long long)i * C, sgn, zpf, sc);
+    y[row] = s / (float)HW;
+}
+
+hipError_t launch_gap_dq(const uint8_t* x, float* y, int N, int C, int HW, int x_nhwc, int x_signed,
+                         float scale, int zp, hipStream_t s) {
+    const long long rows = (long long)N * C;
+    if (rows <= 0) return hipSuccess;
+    if (x_nhwc)
+        hipLaunchKernelGGL(gap_dq_nhwc_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, x, y, N,
+                           C, HW, x_signed, (float)zp, scale);
+    else
+        hipLaunchKernelGGL(gap_dq_nchw_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, y, N, C,
+                           HW, x_signed, (float)zp, scale);
+    return hipGetLastError();
+}
+
 hipError_t launch_gap_f32(const float* x, float* y, int N, int C, int HW, int x_nhwc,
                           hipStream_t s) {
     long long rows = (long long)N * C;

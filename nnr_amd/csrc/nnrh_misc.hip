@@ -76,39 +76,136 @@ hipError_t launch_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C, in
 // implicit im2col starting at padded pixel p then sits 16-byte aligned in
 // copy (p & 3) >> copy_shift, at pixel p - (p & 3).
 // y: [ncopy][N][Hp][Wc] x uint32 (4 channels, padding = fill).
+// grid: x over 4-pixel groups of one padded row (copy index fastest), y =
+// padded row, z = image
 __global__ __launch_bounds__(256) void first_layer_copies_kernel(
     const uint8_t* __restrict x, uint32_t* __restrict y, int C, int H, int W, int Hp, int Wc,
-    int pad_t, int pad_l, int copy_shift, long long per_copy, long long total, uint8_t fill) {
-    long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= total) return;
-    const long long ci = i / per_copy;
-    long long rem = i - ci * per_copy;
-    const int j = (int)(rem % Wc);
-    rem /= Wc;
-    const int ihp = (int)(rem % Hp);
-    const long long n = rem / Hp;
+    int pad_t, int pad_l, int copy_shift, int ncopy_log2, long long per_copy, uint8_t fill) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    const int ci = t & ((1 << ncopy_log2) - 1);
+    const int j0 = (t >> ncopy_log2) * 4;
+    if (j0 >= Wc) return;
+    const int ihp = blockIdx.y, n = blockIdx.z;
     const int ih = ihp - pad_t;
-    const int iw = j + ((int)ci << copy_shift) - pad_l;
-    uint32_t w = (uint32_t)fill * 0x01010101u;
-    if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) {
-        const long long HW = (long long)H * W;
-        const uint8_t* xp = x + n * C * HW + (long long)ih * W + iw;
-        w = 0;
+    const long long HW = (long long)H * W;
+    const uint8_t* xr = x + (long long)n * C * HW + (long long)ih * W;
+    uint32_t out[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) w |= (uint32_t)(c < C ? xp[(long long)c * HW] : fill) << (8 * c);
+    for (int k = 0; k < 4; ++k) {
+        const int iw = j0 + k + (ci << copy_shift) - pad_l;
+        uint32_t w = (uint32_t)fill * 0x01010101u;
+        if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) {
+            w = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) w |= (uint32_t)(c < C ? xr[(long long)c * HW + iw] : fill) << (8 * c);
+        }
+        out[k] = w;
     }
-    y[i] = w;
+    uint32_t* yp = y + (long long)ci * per_copy + ((long long)n * Hp + ihp) * Wc + j0;
+    if (j0 + 4 <= Wc) {
+        *(uint4*)yp = make_uint4(out[0], out[1], out[2], out[3]);
+    } else {
+        for (int k = 0; k < 4 && j0 + k < Wc; ++k) yp[k] = out[k];
+    }
 }
 
 hipError_t launch_first_layer_copies(const uint8_t* x, uint8_t* y, int N, int C, int H, int W,
                                      int Hp, int Wc, int pad_t, int pad_l, int copy_shift,
                                      uint8_t fill, hipStream_t s) {
-    if (N <= 0 || C > 4 || ((uintptr_t)y & 15)) return hipErrorInvalidValue;
-    const int ncopy = 4 >> copy_shift;
+    if (N <= 0 || C > 4 || ((uintptr_t)y & 15) || (Wc & 3) || N > 65535 || Hp > 65535)
+        return hipErrorInvalidValue;
+    const int ncopy_log2 = 2 - copy_shift;
     const long long per_copy = (long long)N * Hp * Wc;
-    const long long total = per_copy * ncopy;
-    hipLaunchKernelGGL(first_layer_copies_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                       x, (uint32_t*)y, C, H, W, Hp, Wc, pad_t, pad_l, copy_shift, per_copy, total, fill);
+    const long long threads_x = (long long)(Wc / 4) << ncopy_log2;
+    const dim3 grid((unsigned)((threads_x + 255) / 256), (unsigned)Hp, (unsigned)N);
+    hipLaunchKernelGGL(first_layer_copies_kernel, grid, dim3(256), 0, s, x, (uint32_t*)y, C, H, W, Hp, Wc,
+                       pad_t, pad_l, copy_shift, ncopy_log2, per_copy, fill);
+    return hipGetLastError();
+}
+
+// QuantizeLinear of the fp32 NCHW network input fused into the multi-copy
+// image above: element (n, c, ih, iw) is quantized with the formula
+// quantize_kernel (nnrh_elem.hip) applies at its flat NCHW index -- the
+// 16-wide SIMD body multiplies by fl(1/s), the last n%16 elements (and all
+// of them when n < 64) divide, QuantizeLinear.cpp:128-194 -- and placed
+// where first_layer_copies_kernel places that byte. The copy index varies
+// fastest, so the copies of one pixel read the same input lines.
+__device__ __forceinline__ uint32_t quant_u8(float xv, long long idx, long long body, float scale,
+                                             float inv, int zp) {
+    int q;
+    if (idx < body) {
+        float v = xv * inv;
+        v = __builtin_rintf(v) + (float)zp;
+        v = clamp_minmax(v, 0.0f, 255.0f);
+        q = (int)v;
+    } else {
+        q = clampi(wrap_add(x86_f2i(__builtin_rintf(xv / scale)), zp), 0, 255);
+    }
+    return (uint32_t)q;
+}
+
+// One block per padded row (y = padded row, z = image): the row's input
+// pixels are quantized into LDS as packed 4-channel dwords (fill outside the
+// image), then every copy writes its shifted Wc-pixel row with 16-byte stores.
+// Row staging keeps the global reads contiguous (float4 when the row start
+// is 16-byte aligned) whatever the padding and copy shift.
+constexpr int QFL_MAX_ROW = 4096;   // padded row dwords staged in LDS
+
+__global__ __launch_bounds__(256) void quantize_first_layer_copies_kernel(
+    const float* __restrict x, uint32_t* __restrict y, int C, int H, int W, int Hp, int Wc,
+    int pad_t, int pad_l, int copy_shift, int ncopy, long long per_copy, uint8_t fill,
+    float scale, float inv, int zp, long long qbody) {
+    extern __shared__ uint32_t row[];   // L dwords (launch size)
+    const int ihp = blockIdx.y, n = blockIdx.z;
+    const int ih = ihp - pad_t;
+    // staged pixels: padded columns 0 .. L-1 (input column = p - pad_l)
+    const int L = Wc + ((ncopy - 1) << copy_shift);
+    const uint32_t fill4 = (uint32_t)fill * 0x01010101u;
+    const bool in_row = (unsigned)ih < (unsigned)H;
+    const long long HW = (long long)H * W;
+    const long long base = (long long)n * C * HW + (long long)ih * W;
+    for (int p = threadIdx.x; p < L; p += 256) {
+        const int iw = p - pad_l;
+        uint32_t w = fill4;
+        if (in_row && (unsigned)iw < (unsigned)W) {
+            w = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                uint32_t bt = fill;
+                if (c < C) {
+                    const long long idx = base + (long long)c * HW + iw;
+                    bt = quant_u8(x[idx], idx, qbody, scale, inv, zp);
+                }
+                w |= bt << (8 * c);
+            }
+        }
+        row[p] = w;
+    }
+    __syncthreads();
+    const int q4 = Wc >> 2;   // 16-byte groups per copy row
+    for (int t = threadIdx.x; t < q4 * ncopy; t += 256) {
+        const int ci = t / q4, g = t - ci * q4;
+        const int p0 = (ci << copy_shift) + 4 * g;
+        uint32_t* yp = y + (long long)ci * per_copy + ((long long)n * Hp + ihp) * Wc + 4 * g;
+        *(uint4*)yp = make_uint4(row[p0], row[p0 + 1], row[p0 + 2], row[p0 + 3]);
+    }
+}
+
+hipError_t launch_quantize_first_layer_copies(const float* x, uint8_t* y, int N, int C, int H, int W,
+                                              int Hp, int Wc, int pad_t, int pad_l, int copy_shift,
+                                              uint8_t fill, float scale, int zp, hipStream_t s) {
+    const int ncopy = 4 >> copy_shift;
+    if (N <= 0 || C > 4 || ((uintptr_t)y & 15) || (Wc & 3) || N > 65535 || Hp > 65535 ||
+        Wc + ((ncopy - 1) << copy_shift) > QFL_MAX_ROW)
+        return hipErrorInvalidValue;
+    const long long per_copy = (long long)N * Hp * Wc;
+    const long long qn = (long long)N * C * H * W;
+    const long long qbody = qn >= 64 ? qn - qn % 16 : 0;
+    const float inv = 1.0f / scale;
+    const dim3 grid(1, (unsigned)Hp, (unsigned)N);
+    const size_t lds = sizeof(uint32_t) * (size_t)(Wc + ((ncopy - 1) << copy_shift));
+    hipLaunchKernelGGL(quantize_first_layer_copies_kernel, grid, dim3(256), lds, s, x, (uint32_t*)y, C, H, W,
+                       Hp, Wc, pad_t, pad_l, copy_shift, ncopy, per_copy, fill, scale, inv, zp, qbody);
     return hipGetLastError();
 }
 

@@ -200,6 +200,11 @@ void qgemm_dma_kernel(GemmArgs g) {
     // RQ-B with zero point 0 (clamp [0, 255] then rne) and RQ-D (rne of
     // acc*cm + zp, clamp [0, 255]) take one instruction for round + clamp + pack
     const bool sat_u8 = g.y_type == 0 && g.lo == 0 && g.hi == 255 && (EPI == EPI_RQD || g.y_zp == 0);
+    // RQ-A adds the zero point after rounding (exact with the saturating
+    // convert only for zero point 0); RQ-C rounds after adding it and clamps
+    // to [L, hi] = [qmin, qmax]
+    const bool sat_ac = g.y_type == 0 && g.L == 0 && g.hi == 255 && (EPI == EPI_RQC || g.y_zp == 0);
+    const float zp_c = (float)g.y_zp;
     const uint8_t* pad16 = (const uint8_t*)&kPadTable.w[(g.pad_byte & 0xff) * 4];
     const int sp_out = g.oH * g.oW;
     // this thread's 16-byte chunk of a 64-byte row (pre-swizzled so the LDS
@@ -488,6 +493,22 @@ void qgemm_dma_kernel(GemmArgs g) {
                             float val = t + zp_f;
                             val = val < 2147483648.0f ? val : -1.0f;
                             w = __builtin_amdgcn_cvt_pk_u8_f32(val, q, w);
+                        }
+                        packed[tn] = w;
+                    }
+                } else if ((EPI == EPI_RQA || EPI == EPI_RQC) && sat_ac) {
+                    // clamp [0, 255] into uint8 with zero point 0 (RQ-A) or
+                    // bounds qmin = 0, qmax = 255 (RQ-C): the rounding,
+                    // clamp and byte insert are one v_cvt_pk_u8_f32
+#pragma unroll
+                    for (int tn = 0; tn < 4; ++tn) {
+                        uint32_t w = 0;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const float t = __builtin_fmaf((float)acc[tm][tn][q], __int_as_float(p0[tn][q]),
+                                                           __int_as_float(p1[tn][q]));
+                            const float f = EPI == EPI_RQA ? t * g.inv_y : __builtin_fmaf(t, g.inv_y, zp_c);
+                            w = __builtin_amdgcn_cvt_pk_u8_f32(f, q, w);
                         }
                         packed[tn] = w;
                     }

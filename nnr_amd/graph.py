@@ -57,6 +57,7 @@ def host_lib():
             "nnr_ctx_node_io": (i, [vp, i, i, i, P(cp)]),
             "nnr_ctx_node_fused_add": (i, [vp, i, i, P(cp)]),
             "nnr_ctx_node_fused_chain": (i, [vp, i, i, P(cp)]),
+            "nnr_ctx_node_fused_pre": (i, [vp, i, i, P(cp)]),
             "nnr_ctx_fusion_stat": (i, [vp, cp, P(i)]),
             "nnr_ctx_device_bytes": (C.c_size_t, [vp]),
             "nnr_ctx_enable_profiling": (i, [vp, i]),
@@ -245,9 +246,16 @@ class Session:
                 if not c.value:
                     break
                 chain.append(c.value.decode())
+            pre = []
+            while True:
+                c = C.c_char_p()
+                _chk(L.nnr_ctx_node_fused_pre(self.h, i, len(pre), C.byref(c)))
+                if not c.value:
+                    break
+                pre.append(c.value.decode())
             out.append(dict(op=op.value.decode(), name=nm.value.decode(), variant=var.value.decode(),
                             post_fn=pf.value, inputs=ios[0], outputs=ios[1], fused_add=fadd,
-                            fused_chain=chain))
+                            fused_chain=chain, fused_pre=pre))
         return out
 
     def fusion_stat(self, key):

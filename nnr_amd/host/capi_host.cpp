@@ -202,6 +202,13 @@ int nnr_ctx_node_fused_chain(nnr_ctx_t c, int i, int k, const char** name) {
     return 0;
 }
 
+int nnr_ctx_node_fused_pre(nnr_ctx_t c, int i, int k, const char** name) {
+    if (!c || i < 0 || i >= (int)c->plan.size() || !name) return err("node_fused_pre: bad index");
+    operator_t* op = c->plan[i];
+    *name = (k >= 0 && k < (int)op->fused_pre.size()) ? op->fused_pre[k]->node_name.c_str() : "";
+    return 0;
+}
+
 int nnr_ctx_fusion_stat(nnr_ctx_t c, const char* key, int* value) {
     if (!c || !key || !value) return err("fusion_stat: NULL");
     auto it = c->ctx.fusion_stats.find(key);

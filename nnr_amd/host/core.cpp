@@ -361,6 +361,7 @@ bool context_t::prepare() {
     if (enable_fusion && enable_conv_add) {
         fuse_conv_add(this);
         fuse_matmul_dq_bias(this);
+        fuse_quant_prefix(this);
     }
     // 6. device memory and constant upload
     if (!plan_memory()) return false;

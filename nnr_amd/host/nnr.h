@@ -126,6 +126,11 @@ struct operator_t {
     // (fuse_matmul_dq_bias); they are skipped and the last one's output is ours
     std::vector<operator_t*> fused_chain;
     virtual bool fuse_dq_bias(operator_t* /*dq*/, operator_t* /*add*/) { return false; }
+    // nodes before this one whose work its kernel now does (fuse_quant_prefix):
+    // they are skipped and this operator reads the first one's input
+    std::vector<operator_t*> fused_pre;
+    virtual bool fuse_quantize_input(operator_t* /*q*/) { return false; }
+    virtual bool fuse_dequantize_input(operator_t* /*dq*/) { return false; }
 
     // attribute accessors
     const attr_t* find_attr(const std::string& name) const;
@@ -212,6 +217,7 @@ void fuse_post_ops(context_t* ctx);
 void assign_layouts(context_t* ctx);
 void fuse_conv_add(context_t* ctx);
 void fuse_matmul_dq_bias(context_t* ctx);
+void fuse_quant_prefix(context_t* ctx);
 
 // operator creation through the registry (src/backend/cpu/solve_operator.cpp:29-33)
 operator_t* solve_operator(const std::string& op_type, int opset, backend_t preferred);

@@ -214,11 +214,27 @@ struct QLinearConv_hip : operator_t {
         nnrh_qconv_branch(h, &branch);
         return true;
     }
+    bool fused_quant = false;   // input is the fp32 tensor of a fused QuantizeLinear
     bool exec() override {
         if (fused_add)
             return ok(this, nnrh_qconv_run_add(h, inputs[0]->data, fused_other->data, outputs[0]->data,
                                                ctx->stream));
+        if (fused_quant)
+            return ok(this, nnrh_qconv_run_f32(h, (const float*)inputs[0]->data, outputs[0]->data, ctx->stream));
         return ok(this, nnrh_qconv_run(h, inputs[0]->data, outputs[0]->data, ctx->stream));
+    }
+    // the QuantizeLinear producing this first-layer conv's input (per-tensor
+    // fp32 scale, uint8 zero point, fp32 NCHW input) runs in its layout kernel
+    bool fuse_quantize_input(operator_t* q) override {
+        if (!h || fused_add || q->inputs.size() < 2 || q->outputs.empty()) return false;
+        tensor_t *qx = q->inputs[0], *qs = q->inputs[1], *qz = in(q, 2), *qy = q->outputs[0];
+        if (!qx || qx->type != NNR_DATA_TYPE_FLOAT32 || qx->format != memory_layout_t::NCHW) return false;
+        if (qy->type != NNR_DATA_TYPE_UINT8 || !qs->has_host() || qs->ndata != 1 || qs->type != NNR_DATA_TYPE_FLOAT32)
+            return false;
+        if (qz && (!qz->has_host() || qz->ndata != 1 || qz->type != NNR_DATA_TYPE_UINT8)) return false;
+        if (nnrh_qconv_fuse_quantize(h, qs->scalar_f32(), zp_value(qz)) != NNRH_OK) return false;
+        fused_quant = true;
+        return true;
     }
     bool fuse_residual_add(operator_t* add, int conv_side) override {
         if (!h || add->inputs.size() != 8) return false;
@@ -477,11 +493,35 @@ struct GlobalAveragePool_hip : operator_t {
         if (x->ndim() != 4 || x->type != NNR_DATA_TYPE_FLOAT32) return bad(this, "fp32 4-D input");
         return y->reshape({x->dims[0], x->dims[1], 1, 1}, x->type);
     }
+    // a per-tensor DequantizeLinear of an 8-bit tensor folded into the pool
+    bool fused_dq = false;
+    float dq_scale = 1.0f;
+    int dq_zp = 0, dq_type = 0;
     bool exec() override {
         tensor_t* x = inputs[0];
+        if (fused_dq)
+            return ok(this, nnrh_global_avgpool_dequant(x->data, (float*)outputs[0]->data, x->dims[0], x->dims[1],
+                                                        x->dims[2] * x->dims[3], x->format == memory_layout_t::NHWC,
+                                                        dq_type, dq_scale, dq_zp, ctx->stream));
         return ok(this, nnrh_global_avgpool_f32((const float*)x->data, (float*)outputs[0]->data, x->dims[0],
                                                 x->dims[1], x->dims[2] * x->dims[3],
                                                 x->format == memory_layout_t::NHWC, ctx->stream));
+    }
+    bool fuse_dequantize_input(operator_t* dq) override {
+        if (dq->inputs.size() < 2 || dq->outputs.empty()) return false;
+        tensor_t *x = dq->inputs[0], *s = dq->inputs[1], *z = in(dq, 2);
+        if (!x || (x->type != NNR_DATA_TYPE_UINT8 && x->type != NNR_DATA_TYPE_INT8) || x->ndim() != 4) return false;
+        if (x->format != dq->outputs[0]->format) return false;
+        if (!s->has_host() || s->ndata != 1 || s->type != NNR_DATA_TYPE_FLOAT32) return false;
+        if (z && (!z->has_host() || z->ndata != 1 || z->type != x->type)) return false;
+        dq_scale = s->scalar_f32();
+        dq_zp = zp_value(z);
+        dq_type = qdtype(x->type);
+        fused_dq = true;
+        return true;
+    }
+    double num_bytes() const override {
+        return (double)inputs[0]->nbytes() + (double)outputs[0]->nbytes();
     }
 };
 

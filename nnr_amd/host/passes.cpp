@@ -10,6 +10,9 @@
 //                     fuse_post_ops.cpp:67): a same-shape QLinearAdd whose
 //                     input is a QLinearConv's only use runs in that conv's
 //                     epilogue, with bit-identical results
+//   fuse_quant_prefix  no counterpart: QuantizeLinear -> first-layer
+//                     QLinearConv and DequantizeLinear -> GlobalAveragePool
+//                     run as one kernel each, bit-identical to the two operators
 //   fuse_matmul_dq_bias  no counterpart: QLinearMatMul -> DequantizeLinear ->
 //                     Add(constant last-axis vector) runs as one kernel with
 //                     an fp32 output, bit-identical to the three operators
@@ -538,6 +541,46 @@ void fuse_matmul_dq_bias(context_t* ctx) {
         ++fused;
     }
     ctx->fusion_stats["matmul_dq_bias"] = fused;
+}
+
+// ---------------------------------------------------------------------------
+// QuantizeLinear / DequantizeLinear whose only consumer is an operator that
+// can read their input directly (the first-layer conv's layout kernel, the
+// global average pool): the consumer does the (de)quantization itself.
+void fuse_quant_prefix(context_t* ctx) {
+    auto& nodes = ctx->nodes;
+    std::unordered_set<tensor_t*> graph_out;
+    for (auto& name : ctx->graph_outputs)
+        if (tensor_t* t = ctx->find(name)) graph_out.insert(t);
+    std::unordered_map<tensor_t*, operator_t*> producer;
+    std::unordered_map<tensor_t*, int> uses;
+    for (auto* op : nodes) {
+        if (!active(op)) continue;
+        for (auto* t : op->outputs)
+            if (t) producer[t] = op;
+        for (auto* t : op->inputs)
+            if (t) uses[t]++;
+    }
+    int nq = 0, ndq = 0;
+    for (auto* op : nodes) {
+        if (!active(op) || op->inputs.empty() || !op->inputs[0]) continue;
+        const bool conv = op->op_type == "QLinearConv", gap = op->op_type == "GlobalAveragePool";
+        if (!conv && !gap) continue;
+        tensor_t* x = op->inputs[0];
+        auto it = producer.find(x);
+        if (it == producer.end() || graph_out.count(x) || uses[x] != 1) continue;
+        operator_t* p = it->second;
+        bool done = false;
+        if (conv && p->op_type == "QuantizeLinear") done = op->fuse_quantize_input(p);
+        if (gap && p->op_type == "DequantizeLinear") done = op->fuse_dequantize_input(p);
+        if (!done) continue;
+        op->fused_pre = {p};
+        op->inputs[0] = p->inputs[0];
+        p->skip = true;
+        (conv ? nq : ndq)++;
+    }
+    ctx->fusion_stats["quantize_first_conv"] = nq;
+    ctx->fusion_stats["dequantize_gap"] = ndq;
 }
 
 }  // namespace nnr

@@ -170,7 +170,21 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
     for nd in plan:
         if nd["op"] in skip_ops:
             continue
-        res = exec_node(nd)
+        pre = nd.get("fused_pre") or []
+        if pre:
+            # nodes folded into this kernel before it: replay them from the
+            # graph's definitions; this node then reads the last one's output
+            # (its input 0 before the fusion)
+            for name in pre:
+                gn = graph.node_by_name(name)
+                chain_env.update(exec_node({"op": gn.op, "name": gn.name, "inputs": list(gn.inputs),
+                                            "outputs": list(gn.outputs), "post_fn": 0}))
+            nd2 = dict(nd, inputs=[graph.node_by_name(pre[-1]).outputs[0]] + list(nd["inputs"][1:]))
+            res = exec_node(nd2)
+            if "oracle_branch" in nd2:
+                nd["oracle_branch"] = nd2["oracle_branch"]
+        else:
+            res = exec_node(nd)
         chain = nd.get("fused_chain") or []
         if chain:
             # nodes folded into this kernel: the result above is the first

@@ -46,7 +46,11 @@ def test_resnet50_b2_bitexact(dev):
     # every residual add runs in the epilogue of the conv that produces it
     fused = sum(1 for p in plan if p["fused_add"])
     assert fused == 16
-    assert n_int == 53 + (16 - fused) + 1 + 1  # convs (+adds), maxpool, input Q
+    # the input QuantizeLinear runs in the stem's layout kernel, the head's
+    # DequantizeLinear inside GlobalAveragePool
+    pre = {p["op"]: p["fused_pre"] for p in plan if p["fused_pre"]}
+    assert sorted(pre) == ["GlobalAveragePool", "QLinearConv"]
+    assert n_int == 53 + (16 - fused) + 1  # convs (+adds), maxpool
     assert logits.shape == (2, 1000) and np.isfinite(logits).all()
 
 
@@ -65,7 +69,7 @@ def test_resnet50_unfused_adds(dev):
     rng = np.random.default_rng(15)
     x = rng.random((2, 3, 64, 64), dtype=np.float32)
     plan, _, n_int = check_graph(g, {"input": x}, "logits", conv_add=False)
-    assert not any(p["fused_add"] for p in plan)
+    assert not any(p["fused_add"] or p["fused_pre"] for p in plan)
     assert n_int == 53 + 16 + 1 + 1
 
 

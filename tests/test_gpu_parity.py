@@ -366,3 +366,72 @@ def test_qmatmul_fused_dq_bias(dev):
     got = to_np(y)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
         f"{np.count_nonzero(got != ref)} of {got.size} differ"
+
+
+# ---------------------------------------------------------------------------
+# QuantizeLinear fused into the first layer's input layout, DequantizeLinear
+# fused into GlobalAveragePool
+
+QFIRST_CASES = [
+    # name, N, C, H, W, OC, k, stride, pads, q_scale, q_zp
+    ("rn50_stem", 2, 3, 40, 36, 64, 7, 2, (3, 3, 3, 3), 1.0 / 255, 0),
+    ("mbv2_stem", 3, 3, 33, 31, 32, 3, 2, (1, 1, 1, 1), 0.0237, 131),
+    # 1*3*21*21 = 1323 elements: the last 11 take QuantizeLinear's divide tail
+    ("tail_s1", 1, 3, 21, 21, 16, 3, 1, (1, 1, 1, 1), 0.0113, 17),
+]
+
+
+@pytest.mark.parametrize("case", QFIRST_CASES, ids=[c[0] for c in QFIRST_CASES])
+def test_qconv_fused_quantize(dev, case):
+    """fp32 NCHW input -> QuantizeLinear -> first-layer QLinearConv, with the
+    quantization inside the conv's input layout kernel == oracle Q, then
+    oracle conv."""
+    import torch
+    name, N, C, Hh, W, OC, k, st, pads, qs, qz = case
+    rng = np.random.default_rng(sum(name.encode()))
+    x = (rng.standard_normal((N, C, Hh, W)) * 1.3).astype(np.float32)
+    # exact ties of x / s land on .5 so the rounding mode is exercised
+    x.reshape(-1)[::7] = (np.arange(x.size)[::7] % 40 - 20 + 0.5).astype(np.float32) * np.float32(qs)
+    w = rng.integers(-127, 128, (OC, C, k, k), dtype=np.int8)
+    kw = dict(stride=(st, st), pads=pads, y_nhwc=1, x_scale=qs, x_zp=qz, y_scale=0.05, y_zp=0,
+              w_scale=rng.uniform(0.001, 0.01, OC).astype(np.float32),
+              bias=rng.integers(-4096, 4097, OC).astype(np.int32))
+    xq = O.quantize_linear(x, qs, qz, np.uint8)
+    ref, br = O.Conv(N, C, Hh, W, OC, k, k, **kw).run(xq, w)
+    op = H.QLinearConv(N, C, Hh, W, w, **kw)
+    assert H.BRANCH_NAMES[op.branch] == "FIRST"
+    assert op.fuse_quantize(qs, qz)
+    xd = to_dev(x, dev)
+    y = to_np(op.run_f32(xd))
+    mism = np.count_nonzero(y != ref)
+    assert mism == 0, f"{mism} of {y.size} differ"
+
+
+@pytest.mark.parametrize("nhwc,dt", [(1, np.uint8), (0, np.uint8), (1, np.int8)])
+def test_global_avgpool_dequant(dev, nhwc, dt):
+    """DequantizeLinear + GlobalAveragePool in one pass == the two HIP ops
+    run separately (bit for bit) and the oracle within fp32 tolerance."""
+    import torch
+    from nnr_amd import _lib
+    rng = np.random.default_rng(41 + nhwc)
+    N, C, Hh, W = 3, 72, 7, 7
+    info = (0, 256) if dt == np.uint8 else (-128, 128)
+    shape = (N, Hh, W, C) if nhwc else (N, C, Hh, W)
+    q = rng.integers(*info, shape, dtype=dt)
+    s, z = 0.0371, (9 if dt == np.uint8 else -4)
+    qd = to_dev(q, dev)
+    y = torch.empty((N, C), dtype=torch.float32, device=dev)
+    xdt = H.U8 if dt == np.uint8 else H.S8
+    _lib.check(_lib.lib().nnrh_global_avgpool_dequant(_lib.ptr(qd), _lib.ptr(y), N, C, Hh * W, nhwc, xdt,
+                                                      s, z, _lib.cur_stream()))
+    f = torch.empty(shape, dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().nnrh_dequantize_linear(_lib.ptr(qd), xdt, q.size, s, z, _lib.ptr(f),
+                                                 _lib.cur_stream()))
+    y2 = torch.empty((N, C), dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().nnrh_global_avgpool_f32(_lib.ptr(f), _lib.ptr(y2), N, C, Hh * W, nhwc,
+                                                  _lib.cur_stream()))
+    got, sep = to_np(y), to_np(y2)
+    assert np.array_equal(got.view(np.uint32), sep.view(np.uint32))
+    deq = O.dequantize_linear(q, s, z)
+    ref = deq.mean(axis=(1, 2) if nhwc else (2, 3), dtype=np.float64)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
