@@ -93,6 +93,11 @@ typedef struct nnrh_qconv_desc {
     float y_scale; int y_zp;
     const int8_t* w_host;           /* OIHW int8                            */
     const int32_t* bias_host;       /* [OC] or NULL                         */
+    int spatial_dims;               /* 0 or 2: 4-D tensors; 1: 3-D tensors
+                                       [N][C][W] (H = kH = 1, pads and strides
+                                       along H unused, NCW layout), the
+                                       reference's exec_typed path (RQ-S,
+                                       QLinearConv.cpp:286-334)             */
 } nnrh_qconv_desc;
 
 /* kernel branch of QLinearConv::exec_simd_4d (QLinearConv.cpp:1337-1351) */
@@ -104,7 +109,8 @@ enum {
     NNRH_BR_NR16 = 5,        /* exec_packed_nr48 (NR16)   RQ-B               */
     NNRH_BR_IM2COL_S1 = 6,   /* exec_vnni_im2col, stride1 RQ-A [lo,hi]       */
     NNRH_BR_IM2COL = 7,      /* exec_vnni_im2col, tiled   RQ-A qmin (+A')    */
-    NNRH_BR_FLOAT = 8        /* exec_float_fallback       RQ-A qmin (+A')    */
+    NNRH_BR_FLOAT = 8,       /* exec_float_fallback       RQ-A qmin (+A')    */
+    NNRH_BR_TYPED = 9        /* exec_typed, 3-D tensors   RQ-S               */
 };
 
 typedef struct nnrh_qconv* nnrh_qconv_t;

@@ -28,8 +28,10 @@ def _dt(np_dtype) -> int:
 
 def _conv_desc(N, C, H, W, w, *, group=1, stride=(1, 1), dil=(1, 1), pads=(0, 0, 0, 0),
                x_nhwc=0, y_nhwc=0, post_fn=0, act_dtype=np.uint8, x_scale=0.02, x_zp=128,
-               w_scale=(0.01,), w_zp=(), y_scale=0.05, y_zp=0, bias=None):
+               w_scale=(0.01,), w_zp=(), y_scale=0.05, y_zp=0, bias=None, spatial_dims=2):
     w = np.ascontiguousarray(w, np.int8)
+    if spatial_dims == 1 and w.ndim == 3:
+        w = w[:, :, None, :]
     OC, _, kH, kW = w.shape
     keep = {
         "w": w,
@@ -49,7 +51,8 @@ def _conv_desc(N, C, H, W, w, *, group=1, stride=(1, 1), dil=(1, 1), pads=(0, 0,
                   keep["w_zp"].ctypes.data_as(P(ct.c_int8)) if keep["w_zp"].size else None,
                   keep["w_zp"].size, float(y_scale), int(y_zp),
                   keep["w"].ctypes.data_as(P(ct.c_int8)),
-                  keep["bias"].ctypes.data_as(P(ct.c_int32)) if keep["bias"] is not None else None)
+                  keep["bias"].ctypes.data_as(P(ct.c_int32)) if keep["bias"] is not None else None,
+                  int(spatial_dims))
     return d, keep
 
 
@@ -76,6 +79,8 @@ class QLinearConv:
         d = self.desc
         self.out_shape = (d.N, d.oH, d.oW, d.OC) if d.y_nhwc else (d.N, d.OC, d.oH, d.oW)
         self.in_shape = (d.N, d.H, d.W, d.C) if d.x_nhwc else (d.N, d.C, d.H, d.W)
+        if d.spatial_dims == 1:   # 3-D tensors [N][C][W]
+            self.out_shape, self.in_shape = (d.N, d.OC, d.oW), (d.N, d.C, d.W)
 
     def __call__(self, x, y=None, stream=None):
         import torch

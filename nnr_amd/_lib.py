@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "lib", "libnnr_hip.so")
 NNRH_OK, NNRH_ERR_INVALID, NNRH_ERR_UNSUPPORTED, NNRH_ERR_HIP, NNRH_ERR_NOMEM = range(5)
 U8, S8, I32, F32, F16 = range(5)
 BRANCH_NAMES = {1: "DW", 2: "FIRST", 3: "DIRECT", 4: "PACKED", 5: "NR16",
-                6: "IM2COL_S1", 7: "IM2COL", 8: "FLOAT"}
+                6: "IM2COL_S1", 7: "IM2COL", 8: "FLOAT", 9: "TYPED"}
 
 # every symbol the header declares (checked by the CPU test suite)
 EXPORTS = [
@@ -59,6 +59,7 @@ class QConvDesc(C.Structure):
         ("w_zp_host", C.POINTER(C.c_int8)), ("w_zp_count", C.c_int),
         ("y_scale", C.c_float), ("y_zp", C.c_int),
         ("w_host", C.POINTER(C.c_int8)), ("bias_host", C.POINTER(C.c_int32)),
+        ("spatial_dims", C.c_int),
     ]
 
 

@@ -302,6 +302,11 @@ int conv_dispatch(const nnrh_qconv_desc* d) {
 
 int validate_conv(const nnrh_qconv_desc* d) {
     if (!d) return set_err(NNRH_ERR_INVALID, "qconv: desc is NULL");
+    if (d->spatial_dims != 0 && d->spatial_dims != 1 && d->spatial_dims != 2)
+        return set_err(NNRH_ERR_INVALID, "qconv: spatial_dims %d", d->spatial_dims);
+    if (d->spatial_dims == 1 && (d->H != 1 || d->kH != 1 || d->oH != 1 || d->sH != 1 || d->dH != 1 ||
+                                 d->pad_t || d->pad_b || d->x_nhwc || d->y_nhwc))
+        return set_err(NNRH_ERR_INVALID, "qconv: 1-D convolution needs H = kH = oH = 1 and NCW layouts");
     if (d->N <= 0 || d->C <= 0 || d->H <= 0 || d->W <= 0 || d->OC <= 0 || d->kH <= 0 ||
         d->kW <= 0 || d->group <= 0)
         return set_err(NNRH_ERR_INVALID, "qconv: non-positive dimension");
@@ -367,9 +372,11 @@ struct nnrh_qconv {
     int32_t* bias = nullptr;
     uint8_t* xs = nullptr;
     int32_t* rowsum = nullptr;
+    int8_t* w1d = nullptr;       // 1-D: raw weights [OC][C/group][kW]
+    int32_t* wzp1d = nullptr;    // 1-D: per-channel w_zp read through the activation type
     ~nnrh_qconv() {
         dfree(wpack); dfree(wdot); dfree(colsum); dfree(c0); dfree(beta_col); dfree(os); dfree(cs); dfree(bf);
-        dfree(bias); dfree(xs); dfree(rowsum);
+        dfree(bias); dfree(xs); dfree(rowsum); dfree(w1d); dfree(wzp1d);
     }
 };
 
@@ -377,7 +384,8 @@ extern "C" int nnrh_qconv_dispatch(const nnrh_qconv_desc* d, int* branch) {
     int rc = validate_conv(d);
     if (rc) return rc;
     if (!branch) return set_err(NNRH_ERR_INVALID, "branch is NULL");
-    *branch = conv_dispatch(d);
+    // QLinearConv::exec (QLinearConv.cpp:1355-1368): non-4-D inputs go to exec_typed
+    *branch = d->spatial_dims == 1 ? NNRH_BR_TYPED : conv_dispatch(d);
     return NNRH_OK;
 }
 
@@ -396,6 +404,28 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
     const int lo = u8 ? 0 : -128, hi = u8 ? 255 : 127;
     const int qmin = d->post_fn ? std::max(lo, d->y_zp) : lo;     // QLinearConv.cpp:419
     const bool pcz = conv_per_channel_zp(d);
+    if (d->spatial_dims == 1) {
+        // exec_typed (QLinearConv.cpp:286-334): raw weights, per-channel
+        // constants with the reference's float operations (:301-303)
+        h->branch = NNRH_BR_TYPED;
+        std::vector<float> cs1(OC), bf1(OC);
+        std::vector<int32_t> wz1(OC);
+        for (int oc = 0; oc < OC; ++oc) {
+            const float ws = d->w_scale_count > 1 ? d->w_scale_host[oc] : d->w_scale_host[0];
+            cs1[oc] = d->x_scale * ws;
+            bf1[oc] = d->bias_host ? (float)d->bias_host[oc] * cs1[oc] : 0.0f;
+            const int8_t zb = pcz ? d->w_zp_host[oc] : (d->w_zp_count > 0 ? d->w_zp_host[0] : 0);
+            wz1[oc] = u8 ? (int32_t)(uint8_t)zb : (int32_t)zb;
+        }
+        const size_t wn = (size_t)OC * Cg * d->kW;
+        int rc1 = upload(&h->w1d, d->w_host, wn);
+        if (!rc1) rc1 = upload(&h->cs, cs1.data(), (size_t)OC);
+        if (!rc1) rc1 = upload(&h->bf, bf1.data(), (size_t)OC);
+        if (!rc1) rc1 = upload(&h->wzp1d, wz1.data(), (size_t)OC);
+        if (rc1) { delete h; return rc1; }
+        *out = h;
+        return NNRH_OK;
+    }
     h->branch = conv_dispatch(d);
     // The VNNI branches read w_zp through the activation type T
     // (QLinearConv.cpp:386 `(T*)inputs[5]->data`); the float fallback packs
@@ -696,6 +726,14 @@ extern "C" int nnrh_qconv_run_f32(nnrh_qconv_t h, const float* x, void* y, void*
 namespace {
 int qconv_compute(nnrh_qconv_t h, const uint8_t* src, void* y, hipStream_t s) {
     const nnrh_qconv_desc& d = h->d;
+    if (h->branch == NNRH_BR_TYPED) {
+        ProfScope ps("conv1d_typed", s);
+        HIP_TRY(launch_conv1d_typed(src, h->w1d, h->wzp1d, h->cs, h->bf, (uint8_t*)y, d.N, d.C, d.W, d.OC,
+                                    d.group, d.kW, d.oW, d.sW, d.dW, d.pad_l, d.x_zp, d.y_zp, d.y_scale,
+                                    d.act_dtype == NNRH_U8, s),
+                "conv1d_typed");
+        return NNRH_OK;
+    }
     if (h->use_dw && h->dw16) {
         ProfScope ps("depthwise", s);
         HIP_TRY(launch_depthwise16(src, h->wdot, h->c0, (uint8_t*)y, h->cs, h->bf, d.N, d.C, d.H, d.W,

@@ -168,6 +168,10 @@ hipError_t launch_rowsum_dense(const uint8_t* a, long long lda,
 hipError_t launch_fill_u8(void* p, uint8_t v, long long n, hipStream_t s);
 hipError_t launch_pad_channels_u8(const uint8_t* x, uint8_t* y, long long pixels, int C, int Cpad,
                                   uint8_t fill, hipStream_t s);
+hipError_t launch_conv1d_typed(const uint8_t* x, const int8_t* w, const int32_t* wzp, const float* cs,
+                               const float* bf, uint8_t* y, int N, int C, int iW, int OC, int G, int kW,
+                               int oW, int sW, int dW, int pad_l, int x_zp, int y_zp, float y_scale, int u8,
+                               hipStream_t s);
 hipError_t launch_quantize_first_layer_copies(const float* x, uint8_t* y, int N, int C, int H, int W,
                                               int Hp, int Wc, int pad_t, int pad_l, int copy_shift,
                                               uint8_t fill, float scale, int zp, hipStream_t s);

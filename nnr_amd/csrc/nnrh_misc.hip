@@ -209,6 +209,59 @@ hipError_t launch_quantize_first_layer_copies(const float* x, uint8_t* y, int N,
     return hipGetLastError();
 }
 
+// QLinearConv on 3-D tensors, the reference's exec_typed<T> ndim == 3 loop
+// (QLinearConv.cpp:286-334), one thread per output [n][oc][ow]:
+//   sum = sum_{c,kw} (x - x_zp) * (w - w_zp), with x, x_zp, w and w_zp all read
+//   through the activation type (a uint8 activation makes int8 weight bytes
+//   count as uint8, :194-206); result = fl(fl(float(sum) * cs) + bf), two
+//   roundings (this file is compiled with -ffp-contract=off);
+//   y = clamp((int32)nearbyint(fl(result / y_scale)) + y_zp)   (RQ-S)
+__global__ __launch_bounds__(256) void conv1d_typed_kernel(
+    const uint8_t* __restrict x, const int8_t* __restrict w, const int32_t* __restrict wzp,
+    const float* __restrict cs, const float* __restrict bf, uint8_t* __restrict y, int N, int C, int iW,
+    int OC, int G, int kW, int oW, int sW, int dW, int pad_l, int x_zp, int y_zp, float y_scale, int u8,
+    int lo, int hi) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long total = (long long)N * OC * oW;
+    if (i >= total) return;
+    const int ow = (int)(i % oW);
+    const long long r = i / oW;
+    const int oc = (int)(r % OC), n = (int)(r / OC);
+    const int Cg = C / G, g = oc / (OC / G);
+    const int32_t wz = wzp[oc];
+    uint32_t sum = 0;
+    for (int c = 0; c < Cg; ++c) {
+        const int ic = g * Cg + c;
+        const uint8_t* xr = x + ((long long)n * C + ic) * iW;
+        const int8_t* wr = w + ((long long)oc * Cg + c) * kW;
+        for (int kw = 0; kw < kW; ++kw) {
+            const int iw = ow * sW - pad_l + kw * dW;
+            if (iw < 0 || iw >= iW) continue;
+            const int32_t xv = (u8 ? (int32_t)xr[iw] : (int32_t)(int8_t)xr[iw]) - x_zp;
+            const int32_t wv = (u8 ? (int32_t)(uint8_t)wr[kw] : (int32_t)wr[kw]) - wz;
+            sum += (uint32_t)(xv * wv);
+        }
+    }
+    const float t = (float)(int32_t)sum * cs[oc];
+    const float result = t + bf[oc];
+    const float q = result / y_scale;
+    const int v = wrap_add(x86_f2i(__builtin_rintf(q)), y_zp);
+    y[i] = (uint8_t)clampi(v, lo, hi);
+}
+
+hipError_t launch_conv1d_typed(const uint8_t* x, const int8_t* w, const int32_t* wzp, const float* cs,
+                               const float* bf, uint8_t* y, int N, int C, int iW, int OC, int G, int kW,
+                               int oW, int sW, int dW, int pad_l, int x_zp, int y_zp, float y_scale, int u8,
+                               hipStream_t s) {
+    const long long total = (long long)N * OC * oW;
+    if (total <= 0) return hipSuccess;
+    if ((total + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(conv1d_typed_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, w, wzp,
+                       cs, bf, y, N, C, iW, OC, G, kW, oW, sW, dW, pad_l, x_zp, y_zp, y_scale, u8,
+                       u8 ? 0 : -128, u8 ? 255 : 127);
+    return hipGetLastError();
+}
+
 // NHWC [pixels][C] -> [pixels][Cpad] with the tail channels set to `fill`
 // (Cpad % 4 == 0); one thread per output dword.
 __global__ __launch_bounds__(256) void pad_channels_kernel(const uint8_t* __restrict x,

@@ -140,10 +140,35 @@ struct QLinearConv_hip : operator_t {
             if (z->host[i] != z->host[0]) return true;
         return false;
     }
+    // 3-D tensors: the reference's exec_typed path (QLinearConv.cpp:286-334)
+    bool conv1d() const { return inputs[0]->ndim() == 3; }
     bool reshape() override {
         tensor_t *x = inputs[0], *w = inputs[3], *y = outputs[0];
+        if (x->ndim() == 3) {
+            if (w->ndim() != 3 || kernels.size() != 1) return bad(this, "1-D convolution needs 3-D weights");
+            // conv_shape.h:21-81 along the single spatial axis
+            const int ek = (kernels[0] - 1) * dilations[0] + 1, xd = x->dims[2];
+            int o;
+            if (auto_pad == 1 || auto_pad == 2) {
+                int pad = (int)(ceilf(xd / (float)strides[0]) - 1) * strides[0] + ek - xd;
+                if (auto_pad == 1) { cpads[0] = pad / 2; cpads[1] = pad - cpads[0]; }
+                else { cpads[1] = pad / 2; cpads[0] = pad - cpads[1]; }
+                o = (int)ceilf(xd / (float)strides[0]);
+            } else if (auto_pad == 3) {
+                cpads[0] = cpads[1] = 0;
+                o = (int)ceilf((xd - ek + 1) / (float)strides[0]);
+            } else {
+                cpads[0] = pads[0];
+                cpads[1] = pads[1];
+                o = (int)floorf((xd + cpads[0] + cpads[1] - ek) / (float)strides[0] + 1);
+            }
+            layout_mask = LAYOUT_NCHW;
+            if (!y->reshape({x->dims[0], w->dims[0], o}, x->type)) return false;
+            if (ctx->shape_only) return describe(true);
+            return build();
+        }
         if (x->ndim() != 4 || w->ndim() != 4 || kernels.size() != 2)
-            return bad(this, "only 2-D convolution (4-D tensors)");
+            return bad(this, "only 1-D and 2-D convolution (3-D and 4-D tensors)");
         // conv_shape.h:21-81
         int out[2];
         for (int i = 0; i < 2; ++i) {
@@ -184,13 +209,22 @@ struct QLinearConv_hip : operator_t {
             (wz && wz->ndata && !wz->has_host()) || (b && !b->has_host()))
             return bad(this, "zero points / bias must be constant");
         d = nnrh_qconv_desc{};
-        d.N = x->dims[0]; d.C = x->dims[1]; d.H = x->dims[2]; d.W = x->dims[3];
-        d.OC = w->dims[0]; d.kH = w->dims[2]; d.kW = w->dims[3]; d.group = group;
-        d.sH = strides[0]; d.sW = strides[1]; d.dH = dilations[0]; d.dW = dilations[1];
-        d.pad_t = cpads[0]; d.pad_l = cpads[1]; d.pad_b = cpads[2]; d.pad_r = cpads[3];
-        d.oH = y->dims[2]; d.oW = y->dims[3];
-        d.x_nhwc = x->format == memory_layout_t::NHWC;
-        d.y_nhwc = y->format == memory_layout_t::NHWC;
+        if (conv1d()) {
+            d.N = x->dims[0]; d.C = x->dims[1]; d.H = 1; d.W = x->dims[2];
+            d.OC = w->dims[0]; d.kH = 1; d.kW = w->dims[2]; d.group = group;
+            d.sH = 1; d.sW = strides[0]; d.dH = 1; d.dW = dilations[0];
+            d.pad_l = cpads[0]; d.pad_r = cpads[1];
+            d.oH = 1; d.oW = y->dims[2];
+            d.spatial_dims = 1;
+        } else {
+            d.N = x->dims[0]; d.C = x->dims[1]; d.H = x->dims[2]; d.W = x->dims[3];
+            d.OC = w->dims[0]; d.kH = w->dims[2]; d.kW = w->dims[3]; d.group = group;
+            d.sH = strides[0]; d.sW = strides[1]; d.dH = dilations[0]; d.dW = dilations[1];
+            d.pad_t = cpads[0]; d.pad_l = cpads[1]; d.pad_b = cpads[2]; d.pad_r = cpads[3];
+            d.oH = y->dims[2]; d.oW = y->dims[3];
+            d.x_nhwc = x->format == memory_layout_t::NHWC;
+            d.y_nhwc = y->format == memory_layout_t::NHWC;
+        }
         d.post_fn = post_fn ? 1 : 0;
         d.act_dtype = qdtype(x->type);
         d.x_scale = xs->scalar_f32();
@@ -255,6 +289,8 @@ struct QLinearConv_hip : operator_t {
     }
     double num_ops() const override {
         const tensor_t *w = inputs[3], *y = outputs[0];
+        if (y->ndim() == 3 && w->ndim() == 3)
+            return 2.0 * y->dims[0] * y->dims[1] * y->dims[2] * (double)w->dims[1] * w->dims[2];
         if (y->ndim() != 4 || w->ndim() != 4) return 0;
         return 2.0 * y->dims[0] * y->dims[1] * y->dims[2] * y->dims[3] * (double)w->dims[1] * w->dims[2] *
                w->dims[3];
@@ -265,8 +301,9 @@ struct QLinearConv_hip : operator_t {
         return (double)x->nbytes() + (double)y->nbytes() + (double)w->nbytes() + 8.0 * w->dims[0] + other;
     }
     std::string variant() const override {
-        static const char* names[] = {"?", "DW", "FIRST", "DIRECT", "PACKED", "NR16", "IM2COL_S1", "IM2COL", "FLOAT"};
-        std::string v = branch >= 0 && branch <= 8 ? names[branch] : "?";
+        static const char* names[] = {"?", "DW", "FIRST", "DIRECT", "PACKED", "NR16", "IM2COL_S1", "IM2COL", "FLOAT",
+                                      "TYPED"};
+        std::string v = branch >= 0 && branch <= 9 ? names[branch] : "?";
         return fused_add ? v + "+Add" : v;
     }
 };

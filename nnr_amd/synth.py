@@ -152,6 +152,31 @@ def qconv_graph(batch=32, seed=2):
     return g
 
 
+def qconv1d_graph(batch=4, C=16, W=50, OC=24, k=5, stride=1, pad=2, dil=1, group=1, seed=21):
+    """A 1-D convolution in QDQ form on 3-D tensors: Q(input [N][C][W]) ->
+    DQ -> Conv(kernel k) -> Q. NNR runs the fused QLinearConv through its
+    exec_typed path (QLinearConv.cpp:286-334)."""
+    g = Graph()
+    rng = np.random.default_rng(seed)
+    q = _QDQ(g, rng)
+    g.inputs["input"] = (np.float32, (batch, C, W))
+    x_q, x_qp = q.quant("input", F32(0.021), 120, name="input_Q")
+    w = rng.normal(0.0, 0.3, (OC, C // group, k)).astype(F32)
+    ws = np.maximum((np.abs(w).reshape(OC, -1).max(1) / 127.0).astype(F32), F32(1e-8))
+    wq = np.clip(np.rint(w / ws[:, None, None]), -127, 127).astype(np.int8)
+    bs = (F32(x_qp[0]) * ws).astype(F32)
+    bq = rng.integers(-3000, 3000, OC).astype(np.int32)
+    w_f = g.node("DequantizeLinear", [g.init("c1_w", wq), g.init("c1_ws", ws),
+                                       g.init("c1_wz", np.zeros(OC, np.int8))], name="c1_wdq", axis=0)
+    b_f = g.node("DequantizeLinear", [g.init("c1_b", bq), g.init("c1_bs", bs),
+                                       g.init("c1_bz", np.zeros(OC, np.int32))], name="c1_bdq", axis=0)
+    y_f = g.node("Conv", [q.dequant(x_q, x_qp), w_f, b_f], name="conv1d", kernel_shape=[k],
+                 strides=[stride], pads=[pad, pad], dilations=[dil], group=group)
+    y, _ = q.quant(y_f, F32(0.05), 7, name="out_Q")
+    g.outputs.append(y)
+    return g
+
+
 # MobileNetV2 (Sandler et al. 2018, width 1.0): (expansion t, channels c,
 # repeats n, first stride s) of the 17 inverted-residual blocks
 MBV2_BLOCKS = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 96, 3, 1),

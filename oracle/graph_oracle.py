@@ -87,6 +87,20 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
             y = np.ascontiguousarray(np.transpose(val(ins[0]), perm))
         elif op == "MatMul":
             y = np.matmul(val(ins[0]).astype(np.float64), val(ins[1]).astype(np.float64)).astype(np.float32)
+        elif op == "QLinearConv" and val(ins[0]).ndim == 3:
+            # 3-D tensors: exec_typed (RQ-S), NCW only
+            a = graph.node_by_name(nd["name"]).attrs
+            x = val(ins[0])
+            w = init[ins[3]]
+            pads = a.get("pads", [0, 0])
+            cv = O.Conv1d(x.shape[0], x.shape[1], x.shape[2], w.shape[0], w.shape[2], group=a.get("group", 1),
+                          stride=a.get("strides", [1])[0], dil=a.get("dilations", [1])[0], pads=(pads[0], pads[1]),
+                          act_dtype=x.dtype.type, x_scale=float(scal(ins[1])), x_zp=int(scal(ins[2])),
+                          w_scale=init[ins[4]], w_zp=init[ins[5]] if ins[5] else (),
+                          y_scale=float(scal(ins[6])), y_zp=int(scal(ins[7])),
+                          bias=init[ins[8]] if len(ins) > 8 and ins[8] else None)
+            y, br = cv.run(x, w)
+            nd["oracle_branch"] = br
         elif op == "QLinearConv":
             src = graph.node_by_name(nd["name"])
             a = src.attrs

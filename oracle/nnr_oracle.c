@@ -544,6 +544,57 @@ int orc_qlinear_conv(const orc_conv_params* p, const void* x, const int8_t* w, v
     return br;
 }
 
+/* ---- QLinearConv on 3-D tensors (1-D convolution) ------------------------
+ * QLinearConv::exec() sends every non-4-D input to exec_typed<T>
+ * (QLinearConv.cpp:1355-1368), whose ndim == 3 branch (:286-334) is scalar
+ * loops with requantize RQ-S:
+ *   cs = fl(x_scale * w_scale[oc]); bf = fl(float(bias[oc]) * cs)   (:301-303)
+ *   result = float(sum) * cs + bf       C++ expression (:327), no contraction
+ *                                       unless orc_set_contract(1)
+ *   q = (int32_t)nearbyint(fl(result / y_scale)) + y_zp, clamp  (:328-329)
+ * exec_typed reads x_zp, y_zp, w_zp AND the weights through the activation
+ * type T (:194-206: `const T* pw = (const T*)w->data`), so with uint8
+ * activations an int8 weight byte counts as its uint8 value.
+ * Layout [N][C][W] in and [N][OC][oW] out; p->H == p->kH == 1. */
+int orc_qlinear_conv1d(const orc_conv_params* p, const void* x, const int8_t* w, void* y) {
+    const int N = p->N, C = p->C, iW = p->W, OC = p->OC, kW = p->kW, G = p->group;
+    const int Cg = C / G, OCg = OC / G, oW = p->oW;
+    const int u8 = p->act_dtype == ORC_U8;
+    int lo, hi; dtype_range(p->act_dtype, &lo, &hi);
+    const int pcz = conv_per_channel_zp(p);
+    for (int n = 0; n < N; n++)
+        for (int oc = 0; oc < OC; oc++) {
+            const int g = oc / OCg;
+            const float ws = p->w_scale_count > 1 ? p->w_scale[oc] : p->w_scale[0];
+            const int8_t zb = pcz ? p->w_zp[oc] : (p->w_zp_count > 0 ? p->w_zp[0] : 0);
+            const int32_t wzp = u8 ? (int32_t)(uint8_t)zb : (int32_t)zb;
+            const float cs = p->x_scale * ws;
+            const float bf = p->bias ? (float)p->bias[oc] * cs : 0.0f;
+            for (int ow = 0; ow < oW; ow++) {
+                int32_t sum = 0;
+                for (int c = 0; c < Cg; c++) {
+                    const int ic = g * Cg + c;
+                    for (int kw = 0; kw < kW; kw++) {
+                        const int iw = ow * p->sW - p->pad_l + kw * p->dW;
+                        if (iw < 0 || iw >= iW) continue;
+                        const size_t xi = ((size_t)n * C + ic) * iW + iw;
+                        const int32_t xv = (u8 ? (int32_t)((const uint8_t*)x)[xi]
+                                               : (int32_t)((const int8_t*)x)[xi]) - p->x_zp;
+                        const int8_t wb = w[((size_t)oc * Cg + c) * kW + kw];
+                        const int32_t wv = (u8 ? (int32_t)(uint8_t)wb : (int32_t)wb) - wzp;
+                        sum = (int32_t)((uint32_t)sum + (uint32_t)(xv * wv));
+                    }
+                }
+                const float result = mul_add_expr((float)sum, cs, bf);
+                const float q = result / p->y_scale;
+                int v = x86_f2i(nearbyintf(q));
+                v = (int)((uint32_t)v + (uint32_t)p->y_zp);
+                st_q(y, p->act_dtype, ((size_t)n * OC + oc) * oW + ow, clampi(v, lo, hi));
+            }
+        }
+    return ORC_BR_TYPED;
+}
+
 /* ---- QLinearAdd: src/backend/cpu/QLinearAdd.cpp:33-265 ----------------- */
 void orc_qlinear_add(int kind, const void* a, const void* b, void* y, size_t n,
                      int N, int C, int HW, int y_nhwc, int dt,

@@ -109,7 +109,8 @@ enum orc_conv_branch {
     ORC_BR_NR16 = 5,        /* exec_packed_nr48, NR16      RQ-B              */
     ORC_BR_IM2COL_S1 = 6,   /* exec_vnni_im2col fused      RQ-A, [lo,hi]     */
     ORC_BR_IM2COL = 7,      /* exec_vnni_im2col tiled      RQ-A qmin (+A')   */
-    ORC_BR_FLOAT = 8        /* exec_float_fallback         RQ-A qmin (+A')   */
+    ORC_BR_FLOAT = 8,       /* exec_float_fallback         RQ-A qmin (+A')   */
+    ORC_BR_TYPED = 9        /* exec_typed, 3-D tensors     RQ-S              */
 };
 
 /* output spatial size (conv_shape.h:21-81, NOTSET / explicit pads) */
@@ -121,6 +122,8 @@ void orc_conv_acc(const orc_conv_params* p, const void* x, const int8_t* w,
 /* full op: returns the branch id, writes y in the layout y_nhwc selects */
 int orc_qlinear_conv(const orc_conv_params* p, const void* x, const int8_t* w,
                      void* y);
+/* 1-D convolution on 3-D tensors (exec_typed, RQ-S); H == kH == 1 */
+int orc_qlinear_conv1d(const orc_conv_params* p, const void* x, const int8_t* w, void* y);
 /* same, given precomputed accumulators (lets tests reuse one acc array) */
 int orc_qlinear_conv_from_acc(const orc_conv_params* p, const int32_t* acc,
                               void* y);

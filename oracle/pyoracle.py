@@ -65,6 +65,7 @@ def lib():
             "orc_conv_dispatch": (i, [P(ConvParams)]),
             "orc_conv_acc": (None, [P(ConvParams), vp, vp, vp]),
             "orc_qlinear_conv": (i, [P(ConvParams), vp, vp, vp]),
+            "orc_qlinear_conv1d": (i, [P(ConvParams), vp, vp, vp]),
             "orc_qlinear_conv_from_acc": (i, [P(ConvParams), vp, vp]),
             "orc_qlinear_add": (None, [i, vp, vp, vp, sz, i, i, i, i, i, f, i, f, i, f, i]),
             "orc_maxpool_u8_nhwc": (None, [vp, vp] + [i] * 12),
@@ -236,4 +237,28 @@ class Conv:
     def from_acc(self, acc):
         y = np.empty(self.out_shape, self.act_dtype)
         br = lib().orc_qlinear_conv_from_acc(ct.byref(self.p), _p(np.ascontiguousarray(acc)), _p(y))
+        return y, br
+
+
+class Conv1d:
+    """QLinearConv on 3-D tensors: x [N][C][W], w [OC][C/group][kW]; the
+    reference's exec_typed path (RQ-S)."""
+
+    def __init__(self, N, C, W, OC, kW, group=1, stride=1, dil=1, pads=(0, 0), act_dtype=np.uint8,
+                 x_scale=0.02, x_zp=128, w_scale=(0.01,), w_zp=(), y_scale=0.05, y_zp=0, bias=None):
+        self.c = Conv(N, C, 1, W, OC, 1, kW, group=group, stride=(1, stride), dil=(1, dil),
+                      pads=(0, pads[0], 0, pads[1]), act_dtype=act_dtype, x_scale=x_scale, x_zp=x_zp,
+                      w_scale=w_scale, w_zp=w_zp, y_scale=y_scale, y_zp=y_zp, bias=bias)
+        self.act_dtype = act_dtype
+
+    @property
+    def out_shape(self):
+        p = self.c.p
+        return (p.N, p.OC, p.oW)
+
+    def run(self, x, w):
+        x = np.ascontiguousarray(x)
+        w = np.ascontiguousarray(w, np.int8)
+        y = np.empty(self.out_shape, self.act_dtype)
+        br = lib().orc_qlinear_conv1d(ct.byref(self.c.p), _p(x), _p(w), _p(y))
         return y, br

@@ -81,6 +81,17 @@ def test_qconv_graph_config2(dev):
     assert [p["variant"] for p in plan if p["op"] == "QLinearConv"] == ["NR16"]
 
 
+def test_qconv1d_graph(dev):
+    """A 1-D convolution in QDQ form (3-D tensors) through the host framework:
+    fused to QLinearConv, run on its exec_typed path, bit-exact."""
+    g = synth.qconv1d_graph(batch=3, C=16, W=57, OC=20, k=5, stride=2, pad=2, dil=1, group=4)
+    rng = np.random.default_rng(22)
+    x = rng.uniform(-2.0, 2.0, (3, 16, 57)).astype(np.float32)
+    plan, y, _ = check_graph(g, {"input": x}, g.outputs[0])
+    assert [p["variant"] for p in plan if p["op"] == "QLinearConv"] == ["TYPED"]
+    assert y.shape == (3, 20, 29)
+
+
 def test_mobilenetv2_b2_bitexact(dev):
     """cfg4 shape at batch 2: stem (first layer), 17 depthwise (RQ-A), 34
     pointwise (RQ-B), 10 residual adds; every int8 tensor bit-exact."""

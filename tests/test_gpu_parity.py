@@ -435,3 +435,38 @@ def test_global_avgpool_dequant(dev, nhwc, dt):
     deq = O.dequantize_linear(q, s, z)
     ref = deq.mean(axis=(1, 2) if nhwc else (2, 3), dtype=np.float64)
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# QLinearConv on 3-D tensors: the reference's exec_typed path (RQ-S)
+
+CONV1D_CASES = [
+    # name, N, C, W, OC, k, group, stride, dil, pads, act, w_zp, bias, y_zp
+    ("u8_k3", 2, 16, 37, 24, 3, 1, 1, 1, (1, 1), np.uint8, (0,), True, 7),
+    ("u8_wzp_s2_d2", 3, 12, 50, 9, 5, 3, 2, 2, (4, 3), np.uint8, (3,), True, 130),
+    ("s8_pcz_nobias", 1, 8, 21, 8, 4, 2, 3, 1, (0, 2), np.int8, tuple(range(-4, 4)), False, -5),
+    ("u8_depthwise", 2, 32, 64, 32, 7, 32, 1, 1, (3, 3), np.uint8, (0,), True, 0),
+]
+
+
+@pytest.mark.parametrize("case", CONV1D_CASES, ids=[c[0] for c in CONV1D_CASES])
+def test_qconv1d(dev, case):
+    name, N, C, W, OC, k, group, stride, dil, pads, act, wzp, bias, y_zp = case
+    rng = np.random.default_rng(sum(name.encode()))
+    info = np.iinfo(act)
+    x = rng.integers(info.min, info.max + 1, (N, C, W), dtype=act)
+    w = rng.integers(-127, 128, (OC, C // group, k), dtype=np.int8)
+    b = rng.integers(-5000, 5000, OC).astype(np.int32) if bias else None
+    ws = rng.uniform(0.001, 0.01, OC).astype(np.float32)
+    kw = dict(group=group, pads=pads, act_dtype=act, x_scale=0.02, x_zp=int(info.min + 100),
+              w_scale=ws, w_zp=wzp, y_scale=0.04, y_zp=y_zp, bias=b)
+    ref, br = O.Conv1d(N, C, W, OC, k, stride=stride, dil=dil, **kw).run(x, w)
+    assert br == 9
+    op = H.QLinearConv(N, C, 1, W, w, stride=(1, stride), dil=(1, dil), spatial_dims=1,
+                       **dict(kw, pads=(0, pads[0], 0, pads[1])))
+    assert H.BRANCH_NAMES[op.branch] == "TYPED"
+    xd = to_dev(x, dev)
+    y = to_np(op(xd))
+    assert y.shape == ref.shape
+    mism = np.count_nonzero(y != ref)
+    assert mism == 0, f"{mism} of {y.size} differ"

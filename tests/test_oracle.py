@@ -414,3 +414,72 @@ def test_conv_branch_formulas_from_acc():
                 assert y[0, h, w_, oc] == np.clip(q, 0, 255)
     # the roundf columns really differ somewhere from an RNE epilogue
     assert L.orc_rq_b_roundf(5, 0, 0.5, 0, 0, 255) != L.orc_rq_b(5, 0, 0.5, 0, 0, 255)
+
+
+# ---------------------------------------------------------------------------
+# QLinearConv on 3-D tensors (exec_typed, RQ-S)
+
+def _conv1d_acc_via_2d(N, C, W, OC, k, group, stride, dil, pads, x, w, x_zp, w_zp, act):
+    """accumulators of the independently written 2-D oracle on the H = 1 view"""
+    cv = O.Conv(N, C, 1, W, OC, 1, k, group=group, stride=(1, stride), dil=(1, dil),
+                pads=(0, pads[0], 0, pads[1]), act_dtype=act, x_zp=x_zp, w_zp=w_zp)
+    return cv.acc(x[:, :, None, :], w[:, :, None, :])[:, :, 0, :]
+
+
+@pytest.mark.parametrize("act", [np.int8, np.uint8])
+@pytest.mark.parametrize("case", [(2, 8, 23, 12, 3, 1, 1, 1, (1, 1)), (1, 12, 40, 6, 5, 3, 2, 2, (4, 3)),
+                                  (3, 4, 9, 4, 3, 4, 1, 1, (2, 0))])
+def test_conv1d_acc_matches_2d_oracle(case, act):
+    """With scale 1 / zero point 0 the RQ-S output is clamp(acc), so the 1-D
+    path's accumulation (taps, padding, stride, dilation, groups) is pinned by
+    the 2-D oracle's. uint8 activations use non-negative weights and w_zp so
+    the reference's weight-through-T read does not change them."""
+    N, C, W, OC, k, group, stride, dil, pads = case
+    rng = np.random.default_rng(sum(case[:5]))
+    lo, hi = (-128, 128) if act == np.int8 else (0, 256)
+    x = rng.integers(lo, hi, (N, C, W), dtype=act)
+    wl = -20 if act == np.int8 else 0
+    w = rng.integers(wl, 21, (OC, C // group, k), dtype=np.int8)
+    x_zp = 3 if act == np.int8 else 131
+    acc = _conv1d_acc_via_2d(N, C, W, OC, k, group, stride, dil, pads, x, w, x_zp, (2,), act)
+    cv = O.Conv1d(N, C, W, OC, k, group=group, stride=stride, dil=dil, pads=pads, act_dtype=act,
+                  x_scale=1.0, x_zp=x_zp, w_scale=(1.0,), w_zp=(2,), y_scale=1.0, y_zp=0)
+    y, br = cv.run(x, w)
+    assert br == 9
+    info = np.iinfo(act)
+    assert np.array_equal(y.astype(np.int64), np.clip(acc, info.min, info.max))
+
+
+def test_conv1d_rounding_and_division():
+    """RQ-S known answers: ties go to even (nearbyint, not roundf), and the
+    division by y_scale is not a multiplication by fl(1/y_scale): a case
+    where the two round to different integers is searched and checked."""
+    # one input channel, kernel 1: acc = (x - x_zp) * w
+    def run(xv, wv, y_scale, y_zp=0, act=np.int8):
+        cv = O.Conv1d(1, 1, 1, 1, 1, act_dtype=act, x_scale=1.0, x_zp=0, w_scale=(1.0,),
+                      y_scale=y_scale, y_zp=y_zp)
+        y, _ = cv.run(np.array([[[xv]]], act), np.array([[[wv]]], np.int8))
+        return int(y.reshape(-1)[0])
+    assert run(5, 1, 2.0) == 2 and run(7, 1, 2.0) == 4 and run(-3, 1, 2.0) == -2
+    assert run(-5, 1, 2.0, y_zp=9) == 7
+    # acc = -80 * 113 = -9040 and y_scale = fl(128.22694): acc / s is exactly
+    # -70.5 (a tie, rounds to -70) while acc * fl(1/s) = -70.5000076 (rounds
+    # to -71), so this pins the division of RQ-S against RQ-A's reciprocal
+    s = np.float32(128.22694)
+    assert np.float32(-9040) / s == np.float32(-70.5)
+    assert np.rint(np.float32(-9040) * (np.float32(1) / s)) == -71
+    assert run(-80, 113, float(s)) == -70
+
+
+def test_conv1d_weights_read_through_activation_type():
+    """exec_typed reads the int8 weights through the uint8 activation type
+    (QLinearConv.cpp:206, `const T* pw = (const T*)w->data`): a weight byte of
+    -1 counts as 255, and w_zp -2 as 254."""
+    def run(x, w, w_zp, act):
+        cv = O.Conv1d(1, 1, 1, 1, 1, act_dtype=act, x_scale=1.0, x_zp=0, w_scale=(1.0,),
+                      w_zp=(w_zp,), y_scale=1.0, y_zp=0)
+        y, _ = cv.run(np.array([[[x]]], act), np.array([[[w]]], np.int8))
+        return int(y.reshape(-1)[0])
+    assert run(1, -1, 0, np.uint8) == 255          # 1 * (255 - 0)
+    assert run(1, -1, -2, np.uint8) == 1            # 1 * (255 - 254)
+    assert run(1, -1, 0, np.int8) == -1             # int8 activations: the weight stays -1
