@@ -241,6 +241,15 @@ int nnrh_nchw_to_nhwc_u8(const uint8_t* x_dev, uint8_t* y_dev, int N, int C,
  * [N][HW][C] (x_nhwc) -> y [N][C].                                        */
 int nnrh_global_avgpool_f32(const float* x_dev, float* y_dev, int N, int C, int HW,
                             int x_nhwc, void* stream);
+/* com.microsoft MultiHeadAttention (src/backend/cpu/MultiHeadAttention.cpp,
+ * no mask): q, k, v, y are [B][seq][hidden] fp32 with hidden = num_heads *
+ * head_dim; y = softmax(scale * Q_h K_h^T) V_h per (batch, head), with the
+ * heads read and written in place. workspace: device memory of at least
+ * nnrh_multihead_attention_workspace bytes, 256-byte aligned.              */
+int nnrh_multihead_attention_workspace(int B, int seq, int num_heads, size_t* bytes);
+int nnrh_multihead_attention_f32(const float* q_dev, const float* k_dev, const float* v_dev, float* y_dev,
+                                 int B, int seq, int hidden, int num_heads, float scale,
+                                 void* workspace_dev, void* stream);
 /* No counterpart in the reference: DequantizeLinear (DequantizeLinear.cpp:
  * 133-152, per-tensor scale and zero point, uint8 or int8 x) feeding
  * GlobalAveragePool, in one pass over the 8-bit tensor. Each value is

@@ -26,7 +26,8 @@ EXPORTS = [
     "nnrh_profile_enable", "nnrh_profile_reset", "nnrh_profile_count", "nnrh_profile_get",
     "nnrh_qconv_dispatch", "nnrh_qconv_create", "nnrh_qconv_branch", "nnrh_qconv_run",
     "nnrh_qconv_destroy", "nnrh_qconv_fuse_add", "nnrh_qconv_run_add",
-    "nnrh_qconv_fuse_quantize", "nnrh_qconv_run_f32", "nnrh_global_avgpool_dequant", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
+    "nnrh_qconv_fuse_quantize", "nnrh_qconv_run_f32", "nnrh_global_avgpool_dequant",
+    "nnrh_multihead_attention_workspace", "nnrh_multihead_attention_f32", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
     "nnrh_qmatmul_fuse_dq_bias",
     "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
@@ -115,6 +116,8 @@ def lib():
         "nnrh_qconv_fuse_quantize": (i, [vp, f, i]),
         "nnrh_qconv_run_f32": (i, [vp, vp, vp, vp]),
         "nnrh_global_avgpool_dequant": (i, [vp, vp, i, i, i, i, i, f, i, vp]),
+        "nnrh_multihead_attention_workspace": (i, [i, i, i, P(sz)]),
+        "nnrh_multihead_attention_f32": (i, [vp, vp, vp, vp, i, i, i, i, f, vp, vp]),
         "nnrh_qmatmul_create": (i, [P(vp), P(QMatMulDesc)]),
         "nnrh_qmatmul_run": (i, [vp, vp, ll, vp, i, vp, vp, vp]),
         "nnrh_qmatmul_destroy": (i, [vp]),

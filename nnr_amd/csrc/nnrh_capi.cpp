@@ -1232,6 +1232,24 @@ extern "C" int nnrh_global_avgpool_f32(const float* x, float* y, int N, int C, i
     return NNRH_OK;
 }
 
+extern "C" int nnrh_multihead_attention_workspace(int B, int seq, int num_heads, size_t* bytes) {
+    if (!bytes || B < 0 || seq < 0 || num_heads <= 0) return set_err(NNRH_ERR_INVALID, "mha_workspace: arguments");
+    *bytes = mha_workspace_bytes(B, seq, num_heads);
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_multihead_attention_f32(const float* q, const float* k, const float* v, float* y, int B, int seq,
+                                            int hidden, int num_heads, float scale, void* workspace, void* stream) {
+    if (!q || !k || !v || !y || !workspace) return set_err(NNRH_ERR_INVALID, "mha: NULL argument");
+    if (B < 0 || seq < 0 || hidden <= 0 || num_heads <= 0 || hidden % num_heads)
+        return set_err(NNRH_ERR_INVALID, "mha: hidden %d / heads %d", hidden, num_heads);
+    if (((uintptr_t)workspace & 255) != 0) return set_err(NNRH_ERR_INVALID, "mha: workspace must be 256-byte aligned");
+    hipStream_t s = S(stream);
+    ProfScope ps("multihead_attention", s);
+    HIP_TRY(launch_mha_f32(q, k, v, y, B, seq, hidden, num_heads, scale, workspace, s), "multihead_attention");
+    return NNRH_OK;
+}
+
 extern "C" int nnrh_global_avgpool_dequant(const void* x, float* y, int N, int C, int HW, int x_nhwc,
                                            int x_dtype, float scale, int zp, void* stream) {
     if (!x || !y || N < 0 || C < 0 || HW <= 0) return set_err(NNRH_ERR_INVALID, "global_avgpool_dequant: arguments");

@@ -89,7 +89,15 @@ __global__ __launch_bounds__(256) void minmax_partial_kernel(const float* __rest
                                                              long long n, float* __restrict part) {
     __shared__ float smn[256], smx[256];
     float mn = 0.0f, mx = 0.0f;
-    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n;
+    // 16-byte loads over the aligned body, scalar over the rest
+    const long long n4 = (((uintptr_t)x & 15) == 0) ? n >> 2 : 0;
+    const float4* x4 = (const float4*)x;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long long)gridDim.x * 256) {
+        const float4 v = x4[i];
+        mn = fminf(mn, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
+        mx = fmaxf(mx, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+    }
+    for (long long i = 4 * n4 + (long long)blockIdx.x * 256 + threadIdx.x; i < n;
          i += (long long)gridDim.x * 256) {
         float v = x[i];
         mn = v < mn ? v : mn;
@@ -112,9 +120,13 @@ __global__ __launch_bounds__(256) void minmax_partial_kernel(const float* __rest
     }
 }
 
-__global__ __launch_bounds__(256) void dyn_scale_kernel(const float* __restrict part, int nparts,
-                                                        float* __restrict y_scale,
-                                                        uint8_t* __restrict y_zp) {
+// scale and zero point from the min/max partials (DynamicQuantizeLinear.cpp:
+// 37-48): xmin = min(0, min x), xmax = max(0, max x), s = fl((xmax - xmin) /
+// 255) (1 when 0), zp = clamp(nearbyint(fl(-xmin / s)), 0, 255). Every
+// quantize block reduces the partials itself (they are exact, so every
+// block gets the same values); block 0 also stores them.
+__device__ __forceinline__ void dyn_scale_block(const float* __restrict part, int nparts, float* sc_out,
+                                                int* zp_out) {
     __shared__ float smn[256], smx[256];
     float mn = 0.0f, mx = 0.0f;
     for (int i = threadIdx.x; i < nparts; i += 256) {
@@ -133,27 +145,47 @@ __global__ __launch_bounds__(256) void dyn_scale_kernel(const float* __restrict 
         }
         __syncthreads();
     }
-    if (threadIdx.x == 0) {
-        float xmin = smn[0] < 0.0f ? smn[0] : 0.0f;
-        float xmax = smx[0] > 0.0f ? smx[0] : 0.0f;
-        float sc = (xmax - xmin) / 255.0f;
-        if (sc == 0.0f) sc = 1.0f;
-        int zp = clampi(x86_f2i(__builtin_rintf(-xmin / sc)), 0, 255);
+    const float xmin = smn[0] < 0.0f ? smn[0] : 0.0f;
+    const float xmax = smx[0] > 0.0f ? smx[0] : 0.0f;
+    float sc = (xmax - xmin) / 255.0f;
+    if (sc == 0.0f) sc = 1.0f;
+    *sc_out = sc;
+    *zp_out = clampi(x86_f2i(__builtin_rintf(-xmin / sc)), 0, 255);
+}
+
+__device__ __forceinline__ uint32_t dyn_q1(float v, float sc, int zp) {
+    return (uint32_t)clampi(wrap_add(x86_f2i(__builtin_rintf(v / sc)), zp), 0, 255);
+}
+// y = clamp(nearbyint(fl(x / s)) + zp, 0, 255): 16 elements per thread over the
+// 16-byte aligned body (one 16-byte store), scalar over the rest
+__global__ __launch_bounds__(256) void dyn_quantize_kernel(const float* __restrict x, long long n,
+                                                           const float* __restrict part, int nparts,
+                                                           float* __restrict y_scale,
+                                                           uint8_t* __restrict y_zp,
+                                                           uint8_t* __restrict y) {
+    float sc;
+    int zp;
+    dyn_scale_block(part, nparts, &sc, &zp);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
         *y_scale = sc;
         *y_zp = (uint8_t)zp;
     }
-}
-
-__global__ __launch_bounds__(256) void dyn_quantize_kernel(const float* __restrict x, long long n,
-                                                           const float* __restrict y_scale,
-                                                           const uint8_t* __restrict y_zp,
-                                                           uint8_t* __restrict y) {
-    const float sc = *y_scale;
-    const int zp = *y_zp;
-    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n;
-         i += (long long)gridDim.x * 256) {
-        y[i] = (uint8_t)clampi(wrap_add(x86_f2i(__builtin_rintf(x[i] / sc)), zp), 0, 255);
+    const bool vec = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
+    const long long n16 = vec ? n >> 4 : 0;
+    const float4* x4 = (const float4*)x;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += (long long)gridDim.x * 256) {
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = x4[4 * i + q];
+            w[q] = dyn_q1(v.x, sc, zp) | (dyn_q1(v.y, sc, zp) << 8) | (dyn_q1(v.z, sc, zp) << 16) |
+                   (dyn_q1(v.w, sc, zp) << 24);
+        }
+        *(uint4*)(y + 16 * i) = make_uint4(w[0], w[1], w[2], w[3]);
     }
+    for (long long i = 16 * n16 + (long long)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (long long)gridDim.x * 256)
+        y[i] = (uint8_t)dyn_q1(x[i], sc, zp);
 }
 
 size_t dynamic_quantize_workspace() { return sizeof(float) * 2 * DQL_BLOCKS; }
@@ -166,13 +198,11 @@ hipError_t launch_dynamic_quantize(const float* x, long long n, uint8_t* y, floa
     hipLaunchKernelGGL(minmax_partial_kernel, dim3(blocks), dim3(256), 0, s, x, n, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(dyn_scale_kernel, dim3(1), dim3(256), 0, s, part, blocks, y_scale, y_zp);
-    e = hipGetLastError();
-    if (e != hipSuccess || n <= 0) return e;
-    long long qb = (n + 255) / 256;
-    if (qb > 65536) qb = 65536;
-    hipLaunchKernelGGL(dyn_quantize_kernel, dim3((unsigned)qb), dim3(256), 0, s, x, n, y_scale,
-                       y_zp, y);
+    long long qb = (n / 16 + 255) / 256;
+    if (qb < 1) qb = 1;
+    if (qb > 2048) qb = 2048;
+    hipLaunchKernelGGL(dyn_quantize_kernel, dim3((unsigned)qb), dim3(256), 0, s, x, n, part, blocks,
+                       y_scale, y_zp, y);
     return hipGetLastError();
 }
 

@@ -237,6 +237,26 @@ __global__ __launch_bounds__(256) void softmax_f32_kernel(const float* __restric
     for (int i = lane; i < D; i += 64) yr[i] = expf(xr[i] - m) * inv;
 }
 
+// the same with each input first multiplied by `scale` (fl(x * scale), what
+// a Mul by a constant before the Softmax writes)
+__global__ __launch_bounds__(256) void softmax_scaled_f32_kernel(const float* __restrict x,
+                                                                 float* __restrict y, long long rows, int D,
+                                                                 float scale) {
+    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + row * D;
+    float* yr = y + row * D;
+    float m = -INFINITY;
+    for (int i = lane; i < D; i += 64) m = fmaxf(m, xr[i] * scale);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float sum = 0.0f;
+    for (int i = lane; i < D; i += 64) sum += expf(xr[i] * scale - m);
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    const float inv = 1.0f / sum;
+    for (int i = lane; i < D; i += 64) yr[i] = expf(xr[i] * scale - m) * inv;
+}
+
 hipError_t launch_softmax_f32(const float* x, float* y, long long rows, int D, hipStream_t s) {
     if (rows <= 0 || D <= 0) return hipSuccess;
     hipLaunchKernelGGL(softmax_f32_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, y, rows,
@@ -343,6 +363,66 @@ hipError_t launch_transpose_f32(const float* x, float* y, int ndim, const int* i
     if (blocks > 16384) blocks = 16384;
     hipLaunchKernelGGL(transpose_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, n, t);
     return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Multi-head attention on [B][S][H*hd] fp32 (com.microsoft MultiHeadAttention
+// semantics, src/backend/cpu/MultiHeadAttention.cpp): per (b, h) the head's
+// rows are read in place (row stride H*hd), scores = Q K^T into a [B][H][S][S]
+// workspace, P = softmax(scale * scores) over the key axis, then P V is
+// written straight into the output's head columns. Two pointer-array batched
+// GEMMs; no transposes are materialized.
+__global__ __launch_bounds__(256) void mha_ptrs_kernel(const float* q, const float* k, const float* v, float* y,
+                                                       float* scores, const float** A1, const float** B1,
+                                                       float** C1, const float** A2, const float** B2,
+                                                       float** C2, int B, int S, int Hd, int nh) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= B * nh) return;
+    const int b = i / nh, h = i - b * nh, hd = Hd / nh;
+    const long long off = (long long)b * S * Hd + (long long)h * hd;
+    float* sc = scores + (long long)i * S * S;
+    A1[i] = k + off; B1[i] = q + off; C1[i] = sc;
+    A2[i] = v + off; B2[i] = sc; C2[i] = y + off;
+}
+
+size_t mha_workspace_bytes(int B, int S, int nh) {
+    const size_t nptr = (size_t)B * nh;
+    return ((6 * nptr * sizeof(void*) + 255) & ~(size_t)255) + sizeof(float) * nptr * S * S;
+}
+
+hipError_t launch_mha_f32(const float* q, const float* k, const float* v, float* y, int B, int S, int Hd, int nh,
+                          float scale, void* ws, hipStream_t s) {
+    if (B <= 0 || S <= 0) return hipSuccess;
+    if (nh <= 0 || Hd % nh) return hipErrorInvalidValue;
+    const int hd = Hd / nh, nb = B * nh;
+    const float** A1 = (const float**)ws;
+    const float** B1 = A1 + nb;
+    float** C1 = (float**)(B1 + nb);
+    const float** A2 = (const float**)(C1 + nb);
+    const float** B2 = A2 + nb;
+    float** C2 = (float**)(B2 + nb);
+    float* scores = (float*)((char*)ws + ((6 * (size_t)nb * sizeof(void*) + 255) & ~(size_t)255));
+    hipLaunchKernelGGL(mha_ptrs_kernel, dim3((nb + 255) / 256), dim3(256), 0, s, q, k, v, y, scores, A1, B1, C1,
+                       A2, B2, C2, B, S, Hd, nh);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    rocblas_handle h = blas_handle();
+    if (!h || rocblas_set_stream(h, s) != rocblas_status_success) return hipErrorNotInitialized;
+    const float one = 1.0f, zero = 0.0f;
+    // column-major: scores^T[S x S] = K_h^T-as-stored... i.e. (K rows) . (Q rows)^T:
+    // C1 (ld S) = op(A1 = K, D x S col-major, ld Hd)^T * (B1 = Q, D x S, ld Hd)
+    rocblas_status st = rocblas_sgemm_batched(h, rocblas_operation_transpose, rocblas_operation_none, S, S, hd,
+                                              &one, A1, Hd, B1, Hd, &zero, C1, S, nb);
+    if (st != rocblas_status_success) return hipErrorLaunchFailure;
+    const long long rows = (long long)nb * S;
+    hipLaunchKernelGGL(softmax_scaled_f32_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, scores,
+                       scores, rows, S, scale);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // ctx^T (hd x S, ld Hd) = V^T-as-stored (hd x S, ld Hd) * P^T-as-stored (S x S, ld S)
+    st = rocblas_sgemm_batched(h, rocblas_operation_none, rocblas_operation_none, hd, S, S, &one, A2, Hd, B2, S,
+                               &zero, C2, Hd, nb);
+    return st == rocblas_status_success ? hipSuccess : hipErrorLaunchFailure;
 }
 
 }  // namespace nnrh

@@ -288,6 +288,7 @@ bool context_t::optimize() {
         fuse_qdq_compute(this);
         fuse_qdq(this);
         fuse_post_ops(this);
+        if (enable_conv_add) fuse_attention(this);
     }
     // 2. every active node must be executable here
     std::string missing;

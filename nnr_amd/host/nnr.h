@@ -218,6 +218,7 @@ void assign_layouts(context_t* ctx);
 void fuse_conv_add(context_t* ctx);
 void fuse_matmul_dq_bias(context_t* ctx);
 void fuse_quant_prefix(context_t* ctx);
+void fuse_attention(context_t* ctx);
 
 // operator creation through the registry (src/backend/cpu/solve_operator.cpp:29-33)
 operator_t* solve_operator(const std::string& op_type, int opset, backend_t preferred);

@@ -723,6 +723,55 @@ struct Softmax_hip : operator_t {
     }
 };
 
+// com.microsoft MultiHeadAttention (src/backend/cpu/MultiHeadAttention.cpp)
+// on fp32 [B][S][hidden] q, k, v without masks; created by fuse_attention
+struct MultiHeadAttention_hip : operator_t {
+    int num_heads = 0;
+    float scale = 0.0f;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    ~MultiHeadAttention_hip() override { nnrh_free(ws); }
+    bool init() override {
+        num_heads = (int)attribute("num_heads", 0);
+        scale = attribute_f("scale", 0.0f);
+        return inputs.size() >= 3 && outputs.size() == 1 && num_heads > 0;
+    }
+    bool reshape() override {
+        tensor_t *q = inputs[0], *k = inputs[1], *v = inputs[2];
+        if (q->ndim() != 3 || q->type != NNR_DATA_TYPE_FLOAT32 || k->dims != q->dims || v->dims != q->dims ||
+            k->type != q->type || v->type != q->type)
+            return bad(this, "q, k, v must be fp32 [B][S][hidden] of one shape");
+        for (size_t i = 3; i < inputs.size(); ++i)
+            if (inputs[i] && inputs[i]->ndata) return bad(this, "bias / masks / past state are not supported");
+        if (q->dims[2] % num_heads) return bad(this, "hidden not divisible by num_heads");
+        if (!ctx->shape_only) {
+            size_t need = 0;
+            if (!ok(this, nnrh_multihead_attention_workspace(q->dims[0], q->dims[1], num_heads, &need))) return false;
+            if (need > ws_bytes) {
+                nnrh_free(ws);
+                ws = nullptr;
+                ws_bytes = 0;
+                if (!ok(this, nnrh_malloc(&ws, need))) return false;
+                ws_bytes = need;
+            }
+        }
+        return outputs[0]->reshape(q->dims, q->type);
+    }
+    bool exec() override {
+        tensor_t* q = inputs[0];
+        const int B = q->dims[0], S = q->dims[1], Hd = q->dims[2];
+        // contrib op default: 1 / sqrt(head_dim)
+        const float sc = scale != 0.0f ? scale : 1.0f / sqrtf((float)(Hd / num_heads));
+        return ok(this, nnrh_multihead_attention_f32((const float*)q->data, (const float*)inputs[1]->data,
+                                                     (const float*)inputs[2]->data, (float*)outputs[0]->data, B, S,
+                                                     Hd, num_heads, sc, ws, ctx->stream));
+    }
+    double num_ops() const override {
+        const tensor_t* q = inputs[0];
+        return 4.0 * q->dims[0] * (double)q->dims[1] * q->dims[1] * q->dims[2];
+    }
+};
+
 // LayerNormalization over the last axis (src/backend/cpu/LayerNormalization.cpp)
 struct LayerNormalization_hip : operator_t {
     bool init() override { return inputs.size() >= 2 && inputs.size() <= 3 && outputs.size() >= 1; }
@@ -851,6 +900,7 @@ const op_registrar_t reg[] = {
     {"Sub", backend_t::HIP, make_binary<2>},
     {"Div", backend_t::HIP, make_binary<3>},
     {"Softmax", backend_t::HIP, make<Softmax_hip>},
+    {"MultiHeadAttention", backend_t::HIP, make<MultiHeadAttention_hip>},
     {"LayerNormalization", backend_t::HIP, make<LayerNormalization_hip>},
     {"Gelu", backend_t::HIP, make<Gelu_hip>},
     {"Transpose", backend_t::HIP, make<Transpose_hip>},

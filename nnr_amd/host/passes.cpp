@@ -10,6 +10,10 @@
 //                     fuse_post_ops.cpp:67): a same-shape QLinearAdd whose
 //                     input is a QLinearConv's only use runs in that conv's
 //                     epilogue, with bit-identical results
+//   fuse_attention     the head split / merge and scaled softmax attention of
+//                     a transformer layer become one MultiHeadAttention
+//                     (the com.microsoft contrib op, MultiHeadAttention.cpp);
+//                     the reference's fuse_sdpa.cpp matches a narrower pattern
 //   fuse_quant_prefix  no counterpart: QuantizeLinear -> first-layer
 //                     QLinearConv and DequantizeLinear -> GlobalAveragePool
 //                     run as one kernel each, bit-identical to the two operators
@@ -581,6 +585,124 @@ void fuse_quant_prefix(context_t* ctx) {
     }
     ctx->fusion_stats["quantize_first_conv"] = nq;
     ctx->fusion_stats["dequantize_gap"] = ndq;
+}
+
+// ---------------------------------------------------------------------------
+// Reshape([B,S,nh,hd]) -> Transpose(0,2,1,3) of q and v, Transpose(0,2,3,1) of
+// k, MatMul(q, k^T) -> Mul(scalar) -> Softmax(last axis) -> MatMul(., v) ->
+// Transpose(0,2,1,3) -> Reshape([B,S,nh*hd])  ==>  MultiHeadAttention(q, k, v)
+// with num_heads = nh and scale = the Mul's constant. Every intermediate has
+// one consumer and is not a graph output. Runs before shape inference: the
+// pattern is read from constant shapes and attributes only.
+void fuse_attention(context_t* ctx) {
+    auto& nodes = ctx->nodes;
+    const int n = (int)nodes.size();
+    std::unordered_set<tensor_t*> graph_out;
+    for (auto& name : ctx->graph_outputs)
+        if (tensor_t* t = ctx->find(name)) graph_out.insert(t);
+    std::unordered_map<tensor_t*, int> producer, uses;
+    for (int i = 0; i < n; ++i) {
+        if (!active(nodes[i])) continue;
+        for (auto* t : nodes[i]->outputs)
+            if (t) producer[t] = i;
+        for (auto* t : nodes[i]->inputs)
+            if (t) uses[t]++;
+    }
+    auto only_use = [&](tensor_t* t) { return t && uses[t] == 1 && !graph_out.count(t); };
+    auto prod = [&](tensor_t* t, const char* type) -> operator_t* {
+        auto it = producer.find(t);
+        if (it == producer.end() || nodes[it->second]->op_type != type) return nullptr;
+        return nodes[it->second];
+    };
+    auto perm_is = [](operator_t* op, std::vector<int64_t> p) { return op->attribute_ints("perm") == p; };
+    auto shape_of = [](operator_t* r) -> std::vector<int64_t> {
+        tensor_t* s = r->inputs.size() > 1 ? r->inputs[1] : nullptr;
+        if (!s || !s->has_host() || s->type != NNR_DATA_TYPE_INT64) return {};
+        return std::vector<int64_t>(s->h<int64_t>(), s->h<int64_t>() + s->ndata);
+    };
+    // Reshape(x, [B,S,nh,hd]) -> Transpose(perm) feeding `t`: returns x
+    auto head_split = [&](tensor_t* t, std::vector<int64_t> perm, std::vector<int64_t>& shape,
+                          std::vector<operator_t*>& eaten) -> tensor_t* {
+        operator_t* tr = prod(t, "Transpose");
+        if (!tr || !only_use(t) || !perm_is(tr, perm)) return nullptr;
+        operator_t* rs = prod(tr->inputs[0], "Reshape");
+        if (!rs || !only_use(tr->inputs[0])) return nullptr;
+        std::vector<int64_t> sh = shape_of(rs);
+        if (sh.size() != 4) return nullptr;
+        for (auto d : sh)
+            if (d <= 0) return nullptr;
+        if (!shape.empty() && sh != shape) return nullptr;
+        shape = sh;
+        eaten.push_back(rs);
+        eaten.push_back(tr);
+        return rs->inputs[0];
+    };
+    int fused = 0;
+    for (int i = 0; i < n; ++i) {
+        operator_t* sm = nodes[i];
+        if (!active(sm) || sm->op_type != "Softmax" || sm->inputs.empty() || sm->outputs.empty()) continue;
+        if (sm->attribute("axis", -1) != -1) continue;
+        std::vector<operator_t*> eaten;
+        // Mul(scores, c) -> Softmax
+        operator_t* mul = prod(sm->inputs[0], "Mul");
+        if (!mul || !only_use(sm->inputs[0]) || mul->inputs.size() != 2) continue;
+        tensor_t *a = mul->inputs[0], *b = mul->inputs[1];
+        tensor_t* c = (b && b->has_host()) ? b : ((a && a->has_host()) ? a : nullptr);
+        tensor_t* scores = c == b ? a : b;
+        if (!c || c->ndata != 1 || c->type != NNR_DATA_TYPE_FLOAT32 || !only_use(scores)) continue;
+        operator_t* mm1 = prod(scores, "MatMul");
+        if (!mm1 || mm1->inputs.size() != 2) continue;
+        // Softmax -> MatMul(p, v4) -> Transpose(0,2,1,3) -> Reshape([B,S,H])
+        tensor_t* p = sm->outputs[0];
+        if (!only_use(p)) continue;
+        operator_t* mm2 = nullptr;
+        for (auto* op : nodes)
+            if (active(op) && op->op_type == "MatMul" && op->inputs.size() == 2 && op->inputs[0] == p) mm2 = op;
+        if (!mm2 || !only_use(mm2->outputs[0])) continue;
+        operator_t* tc = nullptr;
+        for (auto* op : nodes)
+            if (active(op) && op->op_type == "Transpose" && !op->inputs.empty() && op->inputs[0] == mm2->outputs[0])
+                tc = op;
+        if (!tc || !perm_is(tc, {0, 2, 1, 3}) || !only_use(tc->outputs[0])) continue;
+        int rc_i = -1;
+        for (int j = 0; j < n; ++j)
+            if (active(nodes[j]) && nodes[j]->op_type == "Reshape" && !nodes[j]->inputs.empty() &&
+                nodes[j]->inputs[0] == tc->outputs[0])
+                rc_i = j;
+        if (rc_i < 0) continue;
+        operator_t* rc = nodes[rc_i];
+        std::vector<int64_t> shape;
+        tensor_t* q = head_split(mm1->inputs[0], {0, 2, 1, 3}, shape, eaten);
+        tensor_t* k = q ? head_split(mm1->inputs[1], {0, 2, 3, 1}, shape, eaten) : nullptr;
+        tensor_t* v = k ? head_split(mm2->inputs[1], {0, 2, 1, 3}, shape, eaten) : nullptr;
+        if (!v) continue;
+        std::vector<int64_t> merged = shape_of(rc);
+        if (merged != std::vector<int64_t>{shape[0], shape[1], shape[2] * shape[3]}) continue;
+        operator_t* f = solve_operator("MultiHeadAttention", sm->opset, ctx->preferred_backend);
+        if (!f) continue;
+        f->ctx = ctx;
+        f->opset = sm->opset;
+        f->op_type = "MultiHeadAttention";
+        f->node_name = sm->node_name;
+        f->inputs = {q, k, v};
+        f->outputs = {rc->outputs[0]};
+        attr_t heads, scale;
+        heads.kind = attr_t::kind_t::INT;
+        heads.i = shape[2];
+        scale.kind = attr_t::kind_t::FLOAT;
+        scale.f = c->scalar_f32();
+        f->attrs = {{"num_heads", heads}, {"scale", scale}};
+        if (!f->init()) {
+            delete f;
+            continue;
+        }
+        for (auto* op : eaten) op->skip = true;
+        mm1->skip = mul->skip = sm->skip = mm2->skip = tc->skip = true;
+        nodes[rc_i] = f;
+        delete rc;
+        ++fused;
+    }
+    ctx->fusion_stats["attention"] = fused;
 }
 
 }  // namespace nnr

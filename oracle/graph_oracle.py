@@ -85,6 +85,24 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
         elif op == "Transpose":
             perm = graph.node_by_name(nd["name"]).attrs.get("perm")
             y = np.ascontiguousarray(np.transpose(val(ins[0]), perm))
+        elif op == "MultiHeadAttention":
+            # com.microsoft MultiHeadAttention (MultiHeadAttention.cpp), created
+            # by the host's attention fusion in place of the Softmax node of
+            # the same name: scale from the Mul before it, heads from q's Reshape
+            sm = graph.node_by_name(nd["name"])
+            mul = next(g_ for g_ in graph.nodes if sm.inputs[0] in g_.outputs)
+            cname = next(t for t in mul.inputs if t in init)
+            scale = float(init[cname].reshape(-1)[0])
+            rs = next(g_ for g_ in graph.nodes if g_.op == "Reshape" and g_.inputs[0] == ins[0])
+            nh = int(init[rs.inputs[1]][2])
+            q, k, v = (val(t).astype(np.float64) for t in ins[:3])
+            B, S, Hd = q.shape
+            hd = Hd // nh
+            split = lambda t: t.reshape(B, S, nh, hd).transpose(0, 2, 1, 3)
+            sc = np.matmul(split(q), split(k).transpose(0, 1, 3, 2)) * scale
+            e = np.exp(sc - sc.max(axis=-1, keepdims=True))
+            p_ = e / e.sum(axis=-1, keepdims=True)
+            y = np.matmul(p_, split(v)).transpose(0, 2, 1, 3).reshape(B, S, Hd).astype(np.float32)
         elif op == "MatMul":
             y = np.matmul(val(ins[0]).astype(np.float64), val(ins[1]).astype(np.float64)).astype(np.float32)
         elif op == "QLinearConv" and val(ins[0]).ndim == 3:

@@ -161,8 +161,12 @@ def test_bert_per_node(dev, fused):
     assert ops.count("QLinearMatMul") == 12 and ops.count("DynamicQuantizeLinear") == 8
     if not fused:
         assert not any(p.get("fused_chain") for p in plan)
+        assert "MultiHeadAttention" not in ops
         assert n_int >= 12 + 8 * 2 and n_f32 > 0
         return
+    # the head split / scaled-softmax attention / head merge of each layer is
+    # one MultiHeadAttention
+    assert ops.count("MultiHeadAttention") == 2 and "Softmax" not in ops and "Transpose" not in ops
     # every QLinearMatMul absorbs its DequantizeLinear and bias Add, so its
     # checked output is the fp32 end of the chain; the int8 outputs left are
     # those of DynamicQuantizeLinear (y and zero point)

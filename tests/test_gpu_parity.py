@@ -470,3 +470,28 @@ def test_qconv1d(dev, case):
     assert y.shape == ref.shape
     mism = np.count_nonzero(y != ref)
     assert mism == 0, f"{mism} of {y.size} differ"
+
+
+@pytest.mark.parametrize("B,S,hidden,heads,scale", [(3, 37, 96, 4, 0.2), (2, 128, 768, 12, 0.125)])
+def test_multihead_attention_f32(dev, B, S, hidden, heads, scale):
+    """MultiHeadAttention (heads read and written in place, batched rocBLAS
+    GEMMs, scaled softmax) against float64 numpy."""
+    import torch
+    from nnr_amd import _lib
+    import ctypes as C
+    rng = np.random.default_rng(B * 100 + S)
+    q, k, v = (rng.standard_normal((B, S, hidden)).astype(np.float32) for _ in range(3))
+    hd = hidden // heads
+    split = lambda t: t.astype(np.float64).reshape(B, S, heads, hd).transpose(0, 2, 1, 3)
+    sc = np.matmul(split(q), split(k).transpose(0, 1, 3, 2)) * np.float32(scale)
+    e = np.exp(sc - sc.max(-1, keepdims=True))
+    ref = np.matmul(e / e.sum(-1, keepdims=True), split(v)).transpose(0, 2, 1, 3).reshape(B, S, hidden)
+    nbytes = C.c_size_t()
+    _lib.check(_lib.lib().nnrh_multihead_attention_workspace(B, S, heads, C.byref(nbytes)))
+    ws = torch.empty(nbytes.value + 256, dtype=torch.uint8, device=dev)
+    wsp = (ws.data_ptr() + 255) & ~255
+    qd, kd, vd = to_dev(q, dev), to_dev(k, dev), to_dev(v, dev)
+    y = torch.empty((B, S, hidden), dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().nnrh_multihead_attention_f32(_lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd), _lib.ptr(y), B, S,
+                                                       hidden, heads, scale, wsp, _lib.cur_stream()))
+    np.testing.assert_allclose(to_np(y), ref, atol=1e-4, rtol=1e-4)

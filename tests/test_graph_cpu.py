@@ -111,11 +111,18 @@ def test_mobilenetv2_fusion_and_branches():
 def test_bert_fusion():
     """cfg5: each projection's DynQ -> DQ -> MatMul -> Q becomes a
     QLinearMatMul (6 per layer, the Q/K/V ones sharing one
-    DynamicQuantizeLinear); attention stays fp32 MatMul."""
+    DynamicQuantizeLinear); the fp32 attention (head split, scaled softmax,
+    head merge) becomes one MultiHeadAttention per layer, or stays ten
+    nodes with the fusions off."""
     g = synth.bert(batch=2, seq=16, layers=2)
     s = G.Session(g, device=False)
     ops = collections.Counter(p["op"] for p in s.plan())
     assert ops["QLinearMatMul"] == 12 and ops["DynamicQuantizeLinear"] == 8
-    assert ops["MatMul"] == 4 and ops["Softmax"] == 2 and ops["LayerNormalization"] == 4
+    assert ops["MultiHeadAttention"] == 2 and ops["LayerNormalization"] == 4
+    assert "MatMul" not in ops and "Softmax" not in ops and "Transpose" not in ops
     assert ops["Gelu"] == 2 and "QuantizeLinear" not in ops
-    assert s.fusion_stat("qdq_compute") == 12
+    assert s.fusion_stat("qdq_compute") == 12 and s.fusion_stat("attention") == 2
+    u = G.Session(g, device=False, conv_add=False)
+    uops = collections.Counter(p["op"] for p in u.plan())
+    assert uops["MatMul"] == 4 and uops["Softmax"] == 2 and uops["Transpose"] == 8
+    assert "MultiHeadAttention" not in uops
