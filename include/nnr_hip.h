@@ -190,6 +190,20 @@ int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a_dev, long long a_batch_stri
  * scales, K % 16 == 0, b_zp such that no row-sum term is needed;
  * NNRH_ERR_UNSUPPORTED otherwise (the handle is unchanged).             */
 int nnrh_qmatmul_fuse_dq_bias(nnrh_qmatmul_t h, float dq_scale, int dq_zp, const float* bias_host);
+/* After nnrh_qmatmul_fuse_dq_bias: the float32 result then goes through
+ * Gelu, erf form (src/backend/cpu/Gelu.cpp:43-47), the same expression as
+ * nnrh_gelu_f32, so the bits equal running the Gelu operator after it. No
+ * counterpart in the reference (a fusion of operators it runs one by one). */
+int nnrh_qmatmul_fuse_gelu(nnrh_qmatmul_t h);
+/* After nnrh_qmatmul_fuse_dq_bias: every run also writes (min, max) pairs of
+ * its float32 outputs (0 stands in where a pair saw only larger / smaller
+ * values) to parts_dev, for nnrh_dynamic_quantize_linear_parts on y; count
+ * gives the pairs a run of `batch` writes, capacity is the buffer's size in
+ * pairs (a run needing more fails), parts_dev NULL turns it off. No
+ * counterpart in the reference: it saves DynamicQuantizeLinear's min/max
+ * pass over y (DynamicQuantizeLinear.cpp:37-41).                          */
+int nnrh_qmatmul_minmax_count(nnrh_qmatmul_t h, int batch, int* count);
+int nnrh_qmatmul_set_minmax_out(nnrh_qmatmul_t h, float* parts_dev, int capacity);
 int nnrh_qmatmul_destroy(nnrh_qmatmul_t h);
 
 /* ---- MatMulInteger ------------------------------------------------------
@@ -217,6 +231,14 @@ size_t nnrh_dynamic_quantize_workspace(void);
 int nnrh_dynamic_quantize_linear(const float* x_dev, size_t n, uint8_t* y_dev,
                                  float* y_scale_dev, uint8_t* y_zp_dev,
                                  void* workspace_dev, void* stream);
+/* DynamicQuantizeLinear whose min / max were found by the operator that wrote
+ * x: parts_dev holds nparts (min, max) pairs covering all of x (written by
+ * nnrh_add_layernorm_f32 or a fused-dequantize nnrh_qmatmul_run). Same
+ * scale, zero point and bytes as nnrh_dynamic_quantize_linear (min and max
+ * are exact in any order). No counterpart in the reference.               */
+int nnrh_dynamic_quantize_linear_parts(const float* x_dev, size_t n, const float* parts_dev,
+                                       int nparts, uint8_t* y_dev, float* y_scale_dev,
+                                       uint8_t* y_zp_dev, void* stream);
 
 /* ---- QLinearAdd ----------------------------------------------------------
  * QLinearAdd_operator::exec_typed (src/backend/cpu/QLinearAdd.cpp:33-265).
@@ -281,6 +303,14 @@ int nnrh_softmax_f32(const float* x_dev, float* y_dev, size_t rows, int D, void*
  * mean, variance of the row, (x - mean) / sqrt(var + eps) * gamma + beta). */
 int nnrh_layernorm_f32(const float* x_dev, const float* gamma_dev, const float* beta_dev,
                        float* y_dev, size_t rows, int D, float eps, void* stream);
+/* LayerNormalization of fl(x + r) (r_dev NULL: of x): a same-shape fp32 Add
+ * (src/backend/cpu/binary_math.cpp) folded into the normalization, so the
+ * sum is never stored. parts_dev (NULL: none) receives one (min, max) pair
+ * of the outputs per row, for nnrh_dynamic_quantize_linear_parts. No
+ * counterpart in the reference, which runs Add and LayerNormalization.   */
+int nnrh_add_layernorm_f32(const float* x_dev, const float* r_dev, const float* gamma_dev,
+                           const float* beta_dev, float* y_dev, size_t rows, int D, float eps,
+                           float* parts_dev, void* stream);
 /* Gelu, approximate = "none" (src/backend/cpu/Gelu.cpp:43-47). */
 int nnrh_gelu_f32(const float* x_dev, float* y_dev, size_t n, void* stream);
 /* Transpose (src/backend/cpu/Transpose.cpp): ndim <= 6 input dims and perm. */

@@ -168,6 +168,30 @@ class QLinearMatMul:
         self.h = h
         self.m, self.n, self.k = m, n, k
         self.y_dtype = np.dtype(y_dtype)
+        self._f32 = False
+
+    def fuse_dq_bias(self, dq_scale, dq_zp, bias=None):
+        """Then DequantizeLinear(y_zp, dq_scale) and + bias[n]: float32 output."""
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self._keep["dq_bias"] = b
+        check(lib().nnrh_qmatmul_fuse_dq_bias(
+            self.h, float(dq_scale), int(dq_zp),
+            None if b is None else b.ctypes.data_as(ct.POINTER(ct.c_float))))
+        self._f32 = True
+
+    def fuse_gelu(self):
+        check(lib().nnrh_qmatmul_fuse_gelu(self.h))
+
+    def minmax_count(self, batch=1):
+        n = ct.c_int()
+        check(lib().nnrh_qmatmul_minmax_count(self.h, batch, ct.byref(n)))
+        return n.value
+
+    def set_minmax_out(self, parts):
+        """parts: float32 device tensor of (min, max) pairs, or None."""
+        check(lib().nnrh_qmatmul_set_minmax_out(self.h, ptr(parts),
+                                                0 if parts is None else parts.numel() // 2))
+        self._keep["parts"] = parts
 
     def __call__(self, a, y=None, a_scale_dev=None, a_zp_dev=None, stream=None):
         import torch
@@ -175,9 +199,8 @@ class QLinearMatMul:
             raise ValueError("a shape mismatch")
         batch = int(np.prod(a.shape[:-2])) if a.dim() > 2 else 1
         if y is None:
-            y = torch.empty(tuple(a.shape[:-1]) + (self.n,),
-                            dtype=torch.uint8 if self.y_dtype == np.uint8 else torch.int8,
-                            device=a.device)
+            dt = torch.float32 if self._f32 else (torch.uint8 if self.y_dtype == np.uint8 else torch.int8)
+            y = torch.empty(tuple(a.shape[:-1]) + (self.n,), dtype=dt, device=a.device)
         check(lib().nnrh_qmatmul_run(self.h, ptr(a), self.m * self.k if batch > 1 else 0, ptr(y),
                                      batch, ptr(a_scale_dev), ptr(a_zp_dev),
                                      cur_stream() if stream is None else stream))
@@ -256,6 +279,29 @@ def dynamic_quantize_linear(x):
     check(lib().nnrh_dynamic_quantize_linear(ptr(x), x.numel(), ptr(y), ptr(s), ptr(z),
                                              ptr(_dq_ws[dev]), cur_stream()))
     return y, s, z
+
+
+def dynamic_quantize_linear_parts(x, parts):
+    """DynamicQuantizeLinear of x from producer-written (min, max) pairs."""
+    import torch
+    dev = x.device
+    y = torch.empty(x.shape, dtype=torch.uint8, device=dev)
+    s = torch.empty(1, dtype=torch.float32, device=dev)
+    z = torch.empty(1, dtype=torch.uint8, device=dev)
+    check(lib().nnrh_dynamic_quantize_linear_parts(ptr(x), x.numel(), ptr(parts), parts.numel() // 2,
+                                                   ptr(y), ptr(s), ptr(z), cur_stream()))
+    return y, s, z
+
+
+def layernorm(x, gamma, beta=None, eps=1e-5, r=None, parts=None):
+    """LayerNormalization over the last axis of x (of x + r when r is given);
+    parts: optional float32 device tensor receiving one (min, max) per row."""
+    import torch
+    D = x.shape[-1]
+    y = torch.empty_like(x)
+    check(lib().nnrh_add_layernorm_f32(ptr(x), ptr(r), ptr(gamma), ptr(beta), ptr(y), x.numel() // D, D,
+                                       float(eps), ptr(parts), cur_stream()))
+    return y
 
 
 def qlinear_add(kind, a, b, a_s, a_zp, b_s, b_zp, y_s, y_zp, C=0, HW=0, y_nhwc=0, y=None):

@@ -28,7 +28,8 @@ EXPORTS = [
     "nnrh_qconv_destroy", "nnrh_qconv_fuse_add", "nnrh_qconv_run_add",
     "nnrh_qconv_fuse_quantize", "nnrh_qconv_run_f32", "nnrh_global_avgpool_dequant",
     "nnrh_multihead_attention_workspace", "nnrh_multihead_attention_f32", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
-    "nnrh_qmatmul_fuse_dq_bias",
+    "nnrh_qmatmul_fuse_dq_bias", "nnrh_qmatmul_fuse_gelu", "nnrh_qmatmul_minmax_count",
+    "nnrh_qmatmul_set_minmax_out", "nnrh_dynamic_quantize_linear_parts", "nnrh_add_layernorm_f32",
     "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
     "nnrh_dynamic_quantize_linear", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
@@ -122,6 +123,11 @@ def lib():
         "nnrh_qmatmul_run": (i, [vp, vp, ll, vp, i, vp, vp, vp]),
         "nnrh_qmatmul_destroy": (i, [vp]),
         "nnrh_qmatmul_fuse_dq_bias": (i, [vp, f, i, P(f)]),
+        "nnrh_qmatmul_fuse_gelu": (i, [vp]),
+        "nnrh_qmatmul_minmax_count": (i, [vp, i, P(i)]),
+        "nnrh_qmatmul_set_minmax_out": (i, [vp, vp, i]),
+        "nnrh_dynamic_quantize_linear_parts": (i, [vp, sz, vp, i, vp, vp, vp, vp]),
+        "nnrh_add_layernorm_f32": (i, [vp, vp, vp, vp, vp, sz, i, f, vp, vp]),
         "nnrh_matmul_integer_create": (i, [P(vp), i, i, i, i, i, i]),
         "nnrh_matmul_integer_run": (i, [vp, vp, ll, vp, ll, i, i, vp, i, vp]),
         "nnrh_matmul_integer_destroy": (i, [vp]),

@@ -900,6 +900,7 @@ struct nnrh_qmatmul {
     int32_t* rowsum = nullptr;
     float* dq_bias = nullptr;   // nnrh_qmatmul_fuse_dq_bias: padded to Np
     int rowsum_cap = 0;     // batches the rowsum buffer holds
+    int parts_cap = 0;      // nnrh_qmatmul_set_minmax_out: pairs the caller's buffer holds
     int a_zp = 0, b_beta = 0;
     float b_scale = 0.f, y_scale = 0.f;
     ~nnrh_qmatmul() { dfree(wpack); dfree(colsum); dfree(c0); dfree(rowsum); dfree(dq_bias); }
@@ -1010,6 +1011,41 @@ extern "C" int nnrh_qmatmul_fuse_dq_bias(nnrh_qmatmul_t h, float dq_scale, int d
     return NNRH_OK;
 }
 
+extern "C" int nnrh_qmatmul_fuse_gelu(nnrh_qmatmul_t h) {
+    if (!h) return set_err(NNRH_ERR_INVALID, "qmatmul_fuse_gelu: NULL handle");
+    if (!h->g.dq_bias) return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_fuse_gelu: needs nnrh_qmatmul_fuse_dq_bias first");
+    h->g.dq_gelu = 1;
+    return NNRH_OK;
+}
+
+// (min, max) pairs a fused-dequantize run writes: one per (tile, wave) of the
+// tile the launcher picks for N
+static long long qmatmul_parts(const GemmArgs& g, int batch) {
+    const bool tall = pick_tile(g.N) == TILE_256x64;
+    const int BM = tall ? 256 : 128, BN = tall ? 64 : 128;
+    return (long long)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN) * batch * 4;
+}
+
+extern "C" int nnrh_qmatmul_minmax_count(nnrh_qmatmul_t h, int batch, int* count) {
+    if (!h || !count || batch <= 0) return set_err(NNRH_ERR_INVALID, "qmatmul_minmax_count: bad arguments");
+    if (!h->g.dq_bias) return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_minmax_count: needs nnrh_qmatmul_fuse_dq_bias first");
+    const long long n = qmatmul_parts(h->g, batch);
+    if (n > 0x7fffffffLL) return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_minmax_count: too many tiles");
+    *count = (int)n;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qmatmul_set_minmax_out(nnrh_qmatmul_t h, float* parts_dev, int capacity) {
+    if (!h) return set_err(NNRH_ERR_INVALID, "qmatmul_set_minmax_out: NULL handle");
+    if (parts_dev && !h->g.dq_bias)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_set_minmax_out: needs nnrh_qmatmul_fuse_dq_bias first");
+    if (parts_dev && (capacity <= 0 || ((uintptr_t)parts_dev & 7)))
+        return set_err(NNRH_ERR_INVALID, "qmatmul_set_minmax_out: capacity %d / alignment", capacity);
+    h->g.mm_parts = parts_dev;
+    h->parts_cap = parts_dev ? capacity : 0;
+    return NNRH_OK;
+}
+
 extern "C" int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a, long long a_bstride, void* y, int batch,
                                 const float* a_scale_dev, const void* a_zp_dev, void* stream) {
     if (!h || !a || !y) return set_err(NNRH_ERR_INVALID, "qmatmul_run: NULL argument");
@@ -1041,6 +1077,9 @@ extern "C" int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a, long long a_bst
     }
     int vec = pick_vec(g.K, (int)g.lda, (uintptr_t)a);
     if (a_bstride % vec) vec = 1;
+    if (g.mm_parts && qmatmul_parts(g, batch) > h->parts_cap)
+        return set_err(NNRH_ERR_INVALID, "qmatmul_run: %lld min/max pairs exceed the buffer's %d",
+                       qmatmul_parts(g, batch), h->parts_cap);
     ProfScope ps("qgemm", s);
     HIP_TRY(launch_qgemm(g, batch, pick_tile(g.N), vec, s), "qgemm");
     return NNRH_OK;
@@ -1167,6 +1206,16 @@ extern "C" int nnrh_dynamic_quantize_linear(const float* x, size_t n, uint8_t* y
         return set_err(NNRH_ERR_INVALID, "dynamic_quantize: NULL");
     ProfScope ps("dynamic_quantize", S(stream));
     HIP_TRY(launch_dynamic_quantize(x, (long long)n, y, y_scale, y_zp, ws, S(stream)), "dynamic_quantize");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_dynamic_quantize_linear_parts(const float* x, size_t n, const float* parts, int nparts,
+                                                  uint8_t* y, float* y_scale, uint8_t* y_zp, void* stream) {
+    if (!y_scale || !y_zp || !parts || nparts <= 0 || (n && (!x || !y)))
+        return set_err(NNRH_ERR_INVALID, "dynamic_quantize_parts: bad arguments");
+    ProfScope ps("dynamic_quantize", S(stream));
+    HIP_TRY(launch_dynamic_quantize_parts(x, (long long)n, parts, nparts, y, y_scale, y_zp, S(stream)),
+            "dynamic_quantize_parts");
     return NNRH_OK;
 }
 
@@ -1305,7 +1354,18 @@ extern "C" int nnrh_layernorm_f32(const float* x, const float* gamma, const floa
                                   size_t rows, int D, float eps, void* stream) {
     if (rows && (!x || !gamma || !y || D <= 0)) return set_err(NNRH_ERR_INVALID, "layernorm_f32: bad args");
     ProfScope ps("layernorm_f32", S(stream));
-    HIP_TRY(launch_layernorm_f32(x, gamma, beta, y, (long long)rows, D, eps, S(stream)), "layernorm_f32");
+    HIP_TRY(launch_layernorm_f32(x, nullptr, gamma, beta, y, (long long)rows, D, eps, nullptr, S(stream)),
+            "layernorm_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_add_layernorm_f32(const float* x, const float* r, const float* gamma, const float* beta,
+                                      float* y, size_t rows, int D, float eps, float* parts, void* stream) {
+    if (rows && (!x || !gamma || !y || D <= 0)) return set_err(NNRH_ERR_INVALID, "add_layernorm_f32: bad args");
+    if (parts && ((uintptr_t)parts & 7)) return set_err(NNRH_ERR_INVALID, "add_layernorm_f32: parts alignment");
+    ProfScope ps("layernorm_f32", S(stream));
+    HIP_TRY(launch_layernorm_f32(x, r, gamma, beta, y, (long long)rows, D, eps, parts, S(stream)),
+            "add_layernorm_f32");
     return NNRH_OK;
 }
 

@@ -30,6 +30,9 @@ hipError_t launch_dequantize(const void* x, long long n, int dt, float scale, in
 size_t dynamic_quantize_workspace();
 hipError_t launch_dynamic_quantize(const float* x, long long n, uint8_t* y, float* y_scale,
                                    uint8_t* y_zp, void* workspace, hipStream_t s);
+// scale / zero point from nparts (min, max) pairs, then the quantize pass
+hipError_t launch_dynamic_quantize_parts(const float* x, long long n, const float* parts, int nparts,
+                                         uint8_t* y, float* y_scale, uint8_t* y_zp, hipStream_t s);
 hipError_t launch_qadd(const QAddArgs& p, hipStream_t s);
 hipError_t launch_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH, int iW,
                                   int oH, int oW, int kH, int kW, int sH, int sW, int pH, int pW,

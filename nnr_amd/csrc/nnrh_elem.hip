@@ -129,6 +129,7 @@ __device__ __forceinline__ void dyn_scale_block(const float* __restrict part, in
                                                 int* zp_out) {
     __shared__ float smn[256], smx[256];
     float mn = 0.0f, mx = 0.0f;
+#pragma unroll 4
     for (int i = threadIdx.x; i < nparts; i += 256) {
         float a = part[2 * i], b = part[2 * i + 1];
         mn = a < mn ? a : mn;
@@ -156,8 +157,59 @@ __device__ __forceinline__ void dyn_scale_block(const float* __restrict part, in
 __device__ __forceinline__ uint32_t dyn_q1(float v, float sc, int zp) {
     return (uint32_t)clampi(wrap_add(x86_f2i(__builtin_rintf(v / sc)), zp), 0, 255);
 }
+// scale and zero point alone, from (min, max) pairs a producer wrote: one
+// block of 1024 threads, two pairs per 16-byte load, the loads of a thread
+// issued together (one memory round trip for up to 8192 pairs)
+__global__ __launch_bounds__(1024) void dyn_scale_parts_kernel(const float* __restrict part, int nparts,
+                                                               float* __restrict y_scale,
+                                                               uint8_t* __restrict y_zp) {
+    __shared__ float smn[16], smx[16];
+    float mn = 0.0f, mx = 0.0f;
+    const int n2 = nparts >> 1;   // whole float4s (the pairs are 8-byte aligned)
+    const bool vec = ((uintptr_t)part & 15) == 0;
+    if (vec) {
+        const float4* p4 = (const float4*)part;
+#pragma unroll 4
+        for (int i = threadIdx.x; i < n2; i += 1024) {
+            const float4 v = p4[i];
+            mn = fminf(mn, fminf(v.x, v.z));
+            mx = fmaxf(mx, fmaxf(v.y, v.w));
+        }
+    }
+    for (int i = (vec ? 2 * n2 : 0) + threadIdx.x; i < nparts; i += 1024) {
+        mn = fminf(mn, part[2 * i]);
+        mx = fmaxf(mx, part[2 * i + 1]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, off, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        smn[w] = mn;
+        smx[w] = mx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < 16; ++i) {
+            mn = fminf(mn, smn[i]);
+            mx = fmaxf(mx, smx[i]);
+        }
+        // as dyn_scale_block
+        const float xmin = mn < 0.0f ? mn : 0.0f;
+        const float xmax = mx > 0.0f ? mx : 0.0f;
+        float sc = (xmax - xmin) / 255.0f;
+        if (sc == 0.0f) sc = 1.0f;
+        *y_scale = sc;
+        *y_zp = (uint8_t)clampi(x86_f2i(__builtin_rintf(-xmin / sc)), 0, 255);
+    }
+}
+
 // y = clamp(nearbyint(fl(x / s)) + zp, 0, 255): 16 elements per thread over the
-// 16-byte aligned body (one 16-byte store), scalar over the rest
+// 16-byte aligned body (one 16-byte store), scalar over the rest. SCALED: the
+// scale / zero point are already in y_scale / y_zp (dyn_scale_parts_kernel)
+template <bool SCALED>
 __global__ __launch_bounds__(256) void dyn_quantize_kernel(const float* __restrict x, long long n,
                                                            const float* __restrict part, int nparts,
                                                            float* __restrict y_scale,
@@ -165,10 +217,15 @@ __global__ __launch_bounds__(256) void dyn_quantize_kernel(const float* __restri
                                                            uint8_t* __restrict y) {
     float sc;
     int zp;
-    dyn_scale_block(part, nparts, &sc, &zp);
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        *y_scale = sc;
-        *y_zp = (uint8_t)zp;
+    if (SCALED) {
+        sc = *y_scale;
+        zp = *y_zp;
+    } else {
+        dyn_scale_block(part, nparts, &sc, &zp);
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            *y_scale = sc;
+            *y_zp = (uint8_t)zp;
+        }
     }
     const bool vec = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
     const long long n16 = vec ? n >> 4 : 0;
@@ -201,7 +258,20 @@ hipError_t launch_dynamic_quantize(const float* x, long long n, uint8_t* y, floa
     long long qb = (n / 16 + 255) / 256;
     if (qb < 1) qb = 1;
     if (qb > 2048) qb = 2048;
-    hipLaunchKernelGGL(dyn_quantize_kernel, dim3((unsigned)qb), dim3(256), 0, s, x, n, part, blocks,
+    hipLaunchKernelGGL(dyn_quantize_kernel<false>, dim3((unsigned)qb), dim3(256), 0, s, x, n, part, blocks,
+                       y_scale, y_zp, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_dynamic_quantize_parts(const float* x, long long n, const float* parts, int nparts,
+                                         uint8_t* y, float* y_scale, uint8_t* y_zp, hipStream_t s) {
+    hipLaunchKernelGGL(dyn_scale_parts_kernel, dim3(1), dim3(1024), 0, s, parts, nparts, y_scale, y_zp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    long long qb = (n / 16 + 255) / 256;
+    if (qb < 1) qb = 1;
+    if (qb > 4096) qb = 4096;
+    hipLaunchKernelGGL(dyn_quantize_kernel<true>, dim3((unsigned)qb), dim3(256), 0, s, x, n, parts, nparts,
                        y_scale, y_zp, y);
     return hipGetLastError();
 }

@@ -25,8 +25,10 @@ hipError_t launch_gemm_f32_batched(const float* A, const float* B, const float* 
 hipError_t launch_binary_f32(const float* a, const float* b, float* y, long long n, int D, int b_mode,
                              int op, int b_first, hipStream_t s);
 hipError_t launch_softmax_f32(const float* x, float* y, long long rows, int D, hipStream_t s);
-hipError_t launch_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y,
-                                long long rows, int D, float eps, hipStream_t s);
+// r (nullable): second same-shape input added first; parts (nullable): one
+// (min, max) pair of the outputs per row
+hipError_t launch_layernorm_f32(const float* x, const float* r, const float* gamma, const float* beta, float* y,
+                                long long rows, int D, float eps, float* parts, hipStream_t s);
 hipError_t launch_gelu_f32(const float* x, float* y, long long n, hipStream_t s);
 hipError_t launch_transpose_f32(const float* x, float* y, int ndim, const int* in_dims, const int* perm,
                                 hipStream_t s);

@@ -10,6 +10,7 @@
 //   (the BERT encoder's fp32 glue: Softmax.cpp, LayerNormalization.cpp,
 //   Gelu.cpp, Transpose.cpp)
 #include "nnrh_f32.h"
+#include "nnrh_rq.h"
 
 #include <rocblas/rocblas.h>
 
@@ -264,40 +265,141 @@ hipError_t launch_softmax_f32(const float* x, float* y, long long rows, int D, h
     return hipGetLastError();
 }
 
-// LayerNormalization over rows of D (one wave per row), two passes over the
-// row: mean, then the mean of squared deviations
-__global__ __launch_bounds__(256) void layernorm_f32_kernel(const float* __restrict x,
+// LayerNormalization over rows of D (one wave per row): mean, then the mean
+// of squared deviations, then (v - mean) * inv * gamma (+ beta). With `r` the
+// row is fl(x + r) of two same-shape inputs (a residual Add folded in), the
+// same bits the Add would have stored. With `parts`, pair 2 * row receives
+// the (min, max) of the row's outputs (0 when smaller / larger), for a
+// DynamicQuantizeLinear that reads y.
+__device__ __forceinline__ void ln_minmax_store(float mn, float mx, float* parts, long long row, int lane) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, off, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    }
+    if (lane == 0) *(float2*)(parts + 2 * row) = make_float2(mn, mx);
+}
+
+// the row in registers: V float4 per lane (D % 4 == 0, D <= 256 V, 16-byte
+// aligned rows); one read of x (and r), one write of y
+template <int V>
+__global__ __launch_bounds__(256) void layernorm_reg_kernel(const float* __restrict x, const float* __restrict r,
                                                             const float* __restrict gamma,
                                                             const float* __restrict beta,
                                                             float* __restrict y, long long rows, int D,
-                                                            float eps) {
+                                                            float eps, float* __restrict parts) {
+    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int D4 = D >> 2;
+    const float4* xr = (const float4*)(x + row * D);
+    const float4* rr = r ? (const float4*)(r + row * D) : nullptr;
+    float4 v[V];
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int c = lane + 64 * j;
+        if (c < D4) {
+            v[j] = xr[c];
+            if (rr) {
+                const float4 t = rr[c];
+                v[j].x = v[j].x + t.x; v[j].y = v[j].y + t.y;
+                v[j].z = v[j].z + t.z; v[j].w = v[j].w + t.w;
+            }
+            sum += v[j].x + v[j].y + v[j].z + v[j].w;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    const float mean = sum / (float)D;
+    float sq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+        if (lane + 64 * j < D4) {
+            const float a = v[j].x - mean, b = v[j].y - mean, c = v[j].z - mean, d = v[j].w - mean;
+            sq += a * a + b * b + c * c + d * d;
+        }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
+    const float inv = 1.0f / sqrtf(sq / (float)D + eps);
+    const float4* g4 = (const float4*)gamma;
+    const float4* b4 = (const float4*)beta;
+    float4* yr = (float4*)(y + row * D);
+    float mn = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int c = lane + 64 * j;
+        if (c < D4) {
+            const float4 gm = g4[c];
+            float4 o;
+            o.x = (v[j].x - mean) * inv * gm.x; o.y = (v[j].y - mean) * inv * gm.y;
+            o.z = (v[j].z - mean) * inv * gm.z; o.w = (v[j].w - mean) * inv * gm.w;
+            if (beta) {
+                const float4 bt = b4[c];
+                o.x = o.x + bt.x; o.y = o.y + bt.y; o.z = o.z + bt.z; o.w = o.w + bt.w;
+            }
+            yr[c] = o;
+            mn = fminf(mn, fminf(fminf(o.x, o.y), fminf(o.z, o.w)));
+            mx = fmaxf(mx, fmaxf(fmaxf(o.x, o.y), fmaxf(o.z, o.w)));
+        }
+    }
+    if (parts) ln_minmax_store(mn, mx, parts, row, lane);
+}
+
+// any D or alignment: three strided passes over the row
+__global__ __launch_bounds__(256) void layernorm_f32_kernel(const float* __restrict x, const float* __restrict r,
+                                                            const float* __restrict gamma,
+                                                            const float* __restrict beta,
+                                                            float* __restrict y, long long rows, int D,
+                                                            float eps, float* __restrict parts) {
     const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float* xr = x + row * D;
+    const float* rr = r ? r + row * D : nullptr;
+    auto at = [&](int i) { return rr ? xr[i] + rr[i] : xr[i]; };
     float* yr = y + row * D;
     float sum = 0.0f;
-    for (int i = lane; i < D; i += 64) sum += xr[i];
+    for (int i = lane; i < D; i += 64) sum += at(i);
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
     const float mean = sum / (float)D;
     float sq = 0.0f;
     for (int i = lane; i < D; i += 64) {
-        const float d = xr[i] - mean;
+        const float d = at(i) - mean;
         sq += d * d;
     }
     for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
     const float inv = 1.0f / sqrtf(sq / (float)D + eps);
+    float mn = 0.0f, mx = 0.0f;
     for (int i = lane; i < D; i += 64) {
-        const float v = (xr[i] - mean) * inv * gamma[i];
-        yr[i] = beta ? v + beta[i] : v;
+        float v = (at(i) - mean) * inv * gamma[i];
+        if (beta) v = v + beta[i];
+        yr[i] = v;
+        mn = fminf(mn, v);
+        mx = fmaxf(mx, v);
     }
+    if (parts) ln_minmax_store(mn, mx, parts, row, lane);
 }
 
-hipError_t launch_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y,
-                                long long rows, int D, float eps, hipStream_t s) {
+hipError_t launch_layernorm_f32(const float* x, const float* r, const float* gamma, const float* beta, float* y,
+                                long long rows, int D, float eps, float* parts, hipStream_t s) {
     if (rows <= 0 || D <= 0) return hipSuccess;
-    hipLaunchKernelGGL(layernorm_f32_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, gamma,
-                       beta, y, rows, D, eps);
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    const uintptr_t al = (uintptr_t)x | (uintptr_t)r | (uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)y;
+    const int v = (D + 255) / 256;
+    if ((D & 3) == 0 && (al & 15) == 0 && v <= 8) {
+        switch (v) {
+#define NNRH_LN_CASE(V)                                                                                    \
+    case V:                                                                                                \
+        hipLaunchKernelGGL(layernorm_reg_kernel<V>, grid, dim3(256), 0, s, x, r, gamma, beta, y, rows, D, \
+                           eps, parts);                                                                    \
+        return hipGetLastError();
+            NNRH_LN_CASE(1) NNRH_LN_CASE(2) NNRH_LN_CASE(3) NNRH_LN_CASE(4)
+            NNRH_LN_CASE(5) NNRH_LN_CASE(6) NNRH_LN_CASE(7) NNRH_LN_CASE(8)
+#undef NNRH_LN_CASE
+        }
+    }
+    hipLaunchKernelGGL(layernorm_f32_kernel, grid, dim3(256), 0, s, x, r, gamma, beta, y, rows, D, eps, parts);
     return hipGetLastError();
 }
 
@@ -305,10 +407,8 @@ hipError_t launch_layernorm_f32(const float* x, const float* gamma, const float*
 __global__ __launch_bounds__(256) void gelu_f32_kernel(const float* __restrict x, float* __restrict y,
                                                        long long n) {
     for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n;
-         i += (long long)gridDim.x * 256) {
-        const float v = x[i];
-        y[i] = 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
-    }
+         i += (long long)gridDim.x * 256)
+        y[i] = gelu_erf(x[i]);
 }
 
 hipError_t launch_gelu_f32(const float* x, float* y, long long n, hipStream_t s) {
@@ -390,10 +490,143 @@ size_t mha_workspace_bytes(int B, int S, int nh) {
     return ((6 * nptr * sizeof(void*) + 255) & ~(size_t)255) + sizeof(float) * nptr * S * S;
 }
 
+// ---------------------------------------------------------------------------
+// Fused attention for head size 64 and S <= 128: one block per (batch, head),
+// K and V of the head staged in LDS, 4 waves of 32 queries. Scores come from
+// fp32 MFMA 16x16x4 as S^T tiles (t rows, s columns): lane l holds
+// S^T[16 tt + 4 (l / 16) + i][16 ts + l % 16] in register i, which is exactly
+// the A operand of the second product P V when its contraction index runs
+// over t = 16 tt + 4 (l / 16) + i. The first product contracts d in the order
+// d = 16 (l / 16) + step, so every lane reads 16 consecutive floats of its K
+// row and Q row. Softmax of the scaled scores per query column, normalized
+// before P V (the order of Softmax then MatMul); padded t rows are -inf.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int MHA_KP = 68;   // K row stride in LDS (floats): rows 16 bytes apart in the banks
+
+__global__ __launch_bounds__(256) void mha_fused_hd64_kernel(const float* __restrict q, const float* __restrict k,
+                                                             const float* __restrict v, float* __restrict y,
+                                                             int S, int Hd, int nh, float scale) {
+    __shared__ __attribute__((aligned(16))) float ks[128 * MHA_KP];
+    __shared__ __attribute__((aligned(16))) float vs[128 * 64];
+    const int b = blockIdx.x / nh, h = blockIdx.x - b * nh;
+    const long long base = (long long)b * S * Hd + (long long)h * 64;
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = threadIdx.x; i < 128 * 16; i += 256) {
+        const int t = i >> 4, c = (i & 15) * 4;
+        const long long off = base + (long long)t * Hd + c;
+        *(float4*)(ks + t * MHA_KP + c) = t < S ? *(const float4*)(k + off) : zero4;
+        *(float4*)(vs + t * 64 + c) = t < S ? *(const float4*)(v + off) : zero4;
+    }
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lr = lane & 15, g = lane >> 4;
+    const int s0 = 32 * w;   // this wave's first query
+    // Q[s][16 g .. 16 g + 15] of the wave's two query tiles
+    float qf[2][16];
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts) {
+        const int sq = s0 + 16 * ts + lr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 t4 = sq < S ? *(const float4*)(q + base + (long long)sq * Hd + 16 * g + 4 * j) : zero4;
+            qf[ts][4 * j] = t4.x; qf[ts][4 * j + 1] = t4.y; qf[ts][4 * j + 2] = t4.z; qf[ts][4 * j + 3] = t4.w;
+        }
+    }
+    __syncthreads();
+    if (s0 >= S) return;   // no query of this wave (after the only barrier)
+
+    f32x4 acc[8][2];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) {
+        acc[tt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc[tt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float kf[16];
+        const float* kr = ks + (16 * tt + lr) * MHA_KP + 16 * g;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 t4 = *(const float4*)(kr + 4 * j);
+            kf[4 * j] = t4.x; kf[4 * j + 1] = t4.y; kf[4 * j + 2] = t4.z; kf[4 * j + 3] = t4.w;
+        }
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+            acc[tt][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[st], qf[0][st], acc[tt][0], 0, 0, 0);
+            acc[tt][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[st], qf[1][st], acc[tt][1], 0, 0, 0);
+        }
+    }
+    // softmax over t of fl(score * scale), per query column
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x = 16 * tt + 4 * g + i < S ? acc[tt][ts][i] * scale : -INFINITY;
+                acc[tt][ts][i] = x;
+                m = fmaxf(m, x);
+            }
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        float sum = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = expf(acc[tt][ts][i] - m);
+                acc[tt][ts][i] = e;
+                sum += e;
+            }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        const float inv = 1.0f / sum;
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[tt][ts][i] = acc[tt][ts][i] * inv;
+    }
+    // O[s][d] = sum_t P[s][t] V[t][d]; output tile td holds d = 4 (l % 16) + td
+    f32x4 o[2][4];
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+        for (int td = 0; td < 4; ++td) o[ts][td] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 vv = *(const float4*)(vs + (16 * tt + 4 * g + i) * 64 + 4 * lr);
+            const float vb[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+                for (int td = 0; td < 4; ++td)
+                    o[ts][td] = __builtin_amdgcn_mfma_f32_16x16x4f32(acc[tt][ts][i], vb[td], o[ts][td], 0, 0, 0);
+        }
+    // o[ts][td][i] = O[s0 + 16 ts + 4 g + i][4 lr + td]
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int sq = s0 + 16 * ts + 4 * g + i;
+            if (sq < S)
+                *(float4*)(y + base + (long long)sq * Hd + 4 * lr) =
+                    make_float4(o[ts][0][i], o[ts][1][i], o[ts][2][i], o[ts][3][i]);
+        }
+}
+
+bool mha_fused_ok(const float* q, const float* k, const float* v, const float* y, int S, int Hd, int nh) {
+    const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)y;
+    return nh > 0 && Hd == 64 * nh && S <= 128 && (al & 15) == 0;
+}
+
 hipError_t launch_mha_f32(const float* q, const float* k, const float* v, float* y, int B, int S, int Hd, int nh,
                           float scale, void* ws, hipStream_t s) {
     if (B <= 0 || S <= 0) return hipSuccess;
     if (nh <= 0 || Hd % nh) return hipErrorInvalidValue;
+    if (mha_fused_ok(q, k, v, y, S, Hd, nh)) {
+        hipLaunchKernelGGL(mha_fused_hd64_kernel, dim3((unsigned)(B * nh)), dim3(256), 0, s, q, k, v, y, S, Hd, nh,
+                           scale);
+        return hipGetLastError();
+    }
     const int hd = Hd / nh, nb = B * nh;
     const float** A1 = (const float**)ws;
     const float** B1 = A1 + nb;

@@ -112,6 +112,10 @@ struct GemmArgs {
     // y = fl(fl((q - dq_zp) * dq_scale) + dq_bias[n]) with dq_zp = y_zp
     const float* dq_bias;       // NULL: no fused dequantize (padded to Np)
     float dq_scale;
+    int dq_gelu;                // then Gelu (erf form) of the fp32 value
+    // fused dequantize: (min, max) of each (tile, wave)'s outputs, pair
+    // 4 * tile + wave, for a DynamicQuantizeLinear that reads y (NULL: none)
+    float* mm_parts;
     const uint8_t* add_other;   // NULL: no fused add
     int add_conv_is_a;
     float add_sa, add_sb, add_fixed;

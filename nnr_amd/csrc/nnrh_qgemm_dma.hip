@@ -405,6 +405,9 @@ void qgemm_dma_kernel(GemmArgs g) {
     int c_stage = 0, c_pslot = 0;
     v4i acc[4][4];   // started from c0 by the tile's first K-step
 
+    // fused dequantize: running min / max of the fp32 outputs of the tile
+    float mm_mn = 0.0f, mm_mx = 0.0f;
+
     // conv_is_a: the conv byte is input A of the fused QLinearAdd (else B)
     auto epilogue = [&](auto conv_is_a_t) {
         constexpr bool CONV_A = decltype(conv_is_a_t)::value;
@@ -591,6 +594,20 @@ void qgemm_dma_kernel(GemmArgs g) {
                         const float d = (qf - zp_f) * g.dq_scale;
                         o[i] = d + *(const float*)(pb + 4 * i);
                     }
+                    if (g.dq_gelu) {
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) o[i] = gelu_erf(o[i]);
+                    }
+                    if (g.mm_parts) {
+                        // min / max of what this lane writes (0 stands in
+                        // for nothing: DynamicQuantizeLinear adds 0 anyway)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+                            if (full16 || nb + i < g.N) {
+                                mm_mn = fminf(mm_mn, o[i]);
+                                mm_mx = fmaxf(mm_mx, o[i]);
+                            }
+                    }
                     if (full16 && ((((uintptr_t)frow) & 15) == 0)) {
 #pragma unroll
                         for (int q = 0; q < 4; ++q)
@@ -675,6 +692,18 @@ void qgemm_dma_kernel(GemmArgs g) {
         if (++c_kt == nk) {
             if (FUSE == FUSE_ADD && g.add_conv_is_a) epilogue(std::true_type{});
             else epilogue(std::false_type{});
+            if (FUSE == FUSE_DQB && g.mm_parts) {
+                // one (min, max) pair per (tile, wave), at 2 * (4 * tile + wave)
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) {
+                    mm_mn = fminf(mm_mn, __shfl_xor(mm_mn, off, 64));
+                    mm_mx = fmaxf(mm_mx, __shfl_xor(mm_mx, off, 64));
+                }
+                if (lane == 0)
+                    *(float2*)(g.mm_parts + 2 * (4 * c_t + wave)) = make_float2(mm_mn, mm_mx);
+                mm_mn = 0.0f;
+                mm_mx = 0.0f;
+            }
             c_kt = 0;
             c_pslot = c_pslot + PSLOT == S * PSLOT ? 0 : c_pslot + PSLOT;
             c_t += t_step;

@@ -28,6 +28,12 @@ __device__ __forceinline__ int32_t wrap_add(int32_t a, int32_t b) {
 __device__ __forceinline__ int32_t wrap_mul(int32_t a, int32_t b) {
     return (int32_t)((uint32_t)a * (uint32_t)b);
 }
+// Gelu, erf form (approximate = "none"): 0.5 x (1 + erf(x / sqrt 2)). The
+// standalone kernel and every fused epilogue call this one expression, so
+// fused and unfused results are the same bits.
+__device__ __forceinline__ float gelu_erf(float v) {
+    return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+}
 
 // RQ-A: SIMD epilogue of the depthwise / direct / im2col paths
 // (QLinearConv.cpp:630-638, depthwise_int8_avx512.h:249-255).

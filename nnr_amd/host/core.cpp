@@ -192,6 +192,14 @@ bool context_t::add_node(const std::string& op_type, const std::string& name,
     return true;
 }
 
+void* context_t::device_alloc(size_t bytes) {
+    void* p = nullptr;
+    if (nnrh_malloc(&p, bytes) != NNRH_OK) return nullptr;
+    allocations_.push_back(p);
+    device_bytes += bytes;
+    return p;
+}
+
 // Memory planning: every active, non-constant, non-view tensor gets its own
 // device allocation (first-touch order). Views alias their source.
 bool context_t::plan_memory() {
@@ -363,6 +371,8 @@ bool context_t::prepare() {
         fuse_conv_add(this);
         fuse_matmul_dq_bias(this);
         fuse_quant_prefix(this);
+        fuse_add_layernorm(this);
+        fuse_dynq_minmax(this);
     }
     // 6. device memory and constant upload
     if (!plan_memory()) return false;

@@ -131,6 +131,20 @@ struct operator_t {
     std::vector<operator_t*> fused_pre;
     virtual bool fuse_quantize_input(operator_t* /*q*/) { return false; }
     virtual bool fuse_dequantize_input(operator_t* /*dq*/) { return false; }
+    // a same-shape fp32 Add before this operator (fuse_add_layernorm): this
+    // operator reads the Add's two inputs; the second one is fused_other
+    virtual bool fuse_residual_input(operator_t* /*add*/) { return false; }
+    // a Gelu after the fused dequantize + bias (fuse_matmul_dq_bias)
+    virtual bool fuse_gelu(operator_t* /*gelu*/) { return false; }
+    // (min, max) pairs this operator can write beside output 0 for a
+    // DynamicQuantizeLinear that reads it (0: it cannot); set_minmax_out
+    // hands over a buffer of that many pairs (fuse_dynq_minmax)
+    virtual int minmax_pairs() const { return 0; }
+    virtual bool set_minmax_out(float* /*parts*/, int /*pairs*/) { return false; }
+    float* minmax_parts = nullptr;
+    int minmax_count = 0;
+    // DynamicQuantizeLinear: the producer that writes its input's min / max
+    operator_t* minmax_src = nullptr;
 
     // attribute accessors
     const attr_t* find_attr(const std::string& name) const;
@@ -201,6 +215,8 @@ struct context_t {
     size_t device_bytes = 0;
 
     bool fail(const std::string& msg);
+    // device memory that lives as long as the context (nullptr on failure)
+    void* device_alloc(size_t bytes);
 
 private:
     std::vector<void*> allocations_;
@@ -218,6 +234,8 @@ void assign_layouts(context_t* ctx);
 void fuse_conv_add(context_t* ctx);
 void fuse_matmul_dq_bias(context_t* ctx);
 void fuse_quant_prefix(context_t* ctx);
+void fuse_add_layernorm(context_t* ctx);
+void fuse_dynq_minmax(context_t* ctx);
 void fuse_attention(context_t* ctx);
 
 // operator creation through the registry (src/backend/cpu/solve_operator.cpp:29-33)

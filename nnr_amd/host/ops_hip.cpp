@@ -98,7 +98,13 @@ struct DynamicQuantizeLinear_hip : operator_t {
             return bad(this, nnrh_last_error());
         return true;
     }
+    std::string variant() const override { return minmax_src ? "MinMaxIn" : ""; }
     bool exec() override {
+        if (minmax_src)
+            return ok(this, nnrh_dynamic_quantize_linear_parts(
+                                (const float*)inputs[0]->data, inputs[0]->ndata, minmax_src->minmax_parts,
+                                minmax_src->minmax_count, (uint8_t*)outputs[0]->data,
+                                (float*)outputs[1]->data, (uint8_t*)outputs[2]->data, ctx->stream));
         return ok(this, nnrh_dynamic_quantize_linear(
                             (const float*)inputs[0]->data, inputs[0]->ndata, (uint8_t*)outputs[0]->data,
                             (float*)outputs[1]->data, (uint8_t*)outputs[2]->data, ws, ctx->stream));
@@ -366,7 +372,23 @@ struct QLinearMatMul_hip : operator_t {
         return nnrh_qmatmul_fuse_dq_bias(h, dq->inputs[1]->scalar_f32(), zp_value(in(dq, 2)),
                                          bias->h<float>()) == NNRH_OK;
     }
-    std::string variant() const override { return fused_chain.empty() ? "" : "+DQ+Bias"; }
+    bool fuse_gelu(operator_t* ge) override {
+        if (ge->attribute_s("approximate", "none") != "none") return false;
+        if (ge->outputs[0]->dims != ge->inputs[0]->dims) return false;
+        return nnrh_qmatmul_fuse_gelu(h) == NNRH_OK;
+    }
+    int minmax_pairs() const override {
+        int c = 0;
+        if (!h || fused_chain.empty() || nnrh_qmatmul_minmax_count(h, batch, &c) != NNRH_OK) return 0;
+        return c;
+    }
+    bool set_minmax_out(float* parts, int pairs) override {
+        return nnrh_qmatmul_set_minmax_out(h, parts, pairs) == NNRH_OK;
+    }
+    std::string variant() const override {
+        if (fused_chain.empty()) return "";
+        return fused_chain.size() > 2 ? "+DQ+Bias+Gelu" : "+DQ+Bias";
+    }
     bool exec() override {
         const float* a_s_dev = inputs[1]->has_host() ? nullptr : (const float*)inputs[1]->data;
         const void* a_z_dev = inputs[2]->has_host() ? nullptr : inputs[2]->data;
@@ -786,13 +808,27 @@ struct LayerNormalization_hip : operator_t {
         if (inputs[1]->ndata != (size_t)x->dims.back()) return bad(this, "scale shape");
         return outputs[0]->reshape(x->dims, x->type);
     }
+    bool fuse_residual_input(operator_t* add) override {
+        return add->outputs[0] == inputs[0] && !fused_other;
+    }
+    // one pair per row
+    int minmax_pairs() const override {
+        const tensor_t* x = inputs[0];
+        const size_t rows = x->ndata / (size_t)x->dims.back();
+        return rows <= 0x7fffffff ? (int)rows : 0;
+    }
+    bool set_minmax_out(float*, int) override { return true; }
+    std::string variant() const override { return fused_other ? "+Add" : ""; }
     bool exec() override {
         tensor_t* x = inputs[0];
         tensor_t* bias = in(this, 2);
         const int D = x->dims.back();
-        return ok(this, nnrh_layernorm_f32((const float*)x->data, (const float*)inputs[1]->data,
-                                           bias ? (const float*)bias->data : nullptr, (float*)outputs[0]->data,
-                                           x->ndata / D, D, attribute_f("epsilon", 1e-5f), ctx->stream));
+        return ok(this, nnrh_add_layernorm_f32((const float*)x->data,
+                                               fused_other ? (const float*)fused_other->data : nullptr,
+                                               (const float*)inputs[1]->data,
+                                               bias ? (const float*)bias->data : nullptr,
+                                               (float*)outputs[0]->data, x->ndata / D, D,
+                                               attribute_f("epsilon", 1e-5f), minmax_parts, ctx->stream));
     }
 };
 

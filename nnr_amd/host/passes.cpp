@@ -18,8 +18,13 @@
 //                     QLinearConv and DequantizeLinear -> GlobalAveragePool
 //                     run as one kernel each, bit-identical to the two operators
 //   fuse_matmul_dq_bias  no counterpart: QLinearMatMul -> DequantizeLinear ->
-//                     Add(constant last-axis vector) runs as one kernel with
-//                     an fp32 output, bit-identical to the three operators
+//                     Add(constant last-axis vector) (-> Gelu) runs as one
+//                     kernel with an fp32 output, bit-identical to the
+//                     operators it replaces
+//   fuse_add_layernorm  no counterpart: a same-shape fp32 Add feeding only a
+//                     LayerNormalization is formed inside the normalization
+//   fuse_dynq_minmax  no counterpart: the producer of a DynamicQuantizeLinear
+//                     input writes its min / max pairs as it stores it
 // The fused operators are created through the registry with the context's
 // preferred backend, exactly where the reference calls solve_operator.
 #include <cstdio>
@@ -520,7 +525,7 @@ void fuse_matmul_dq_bias(context_t* ctx) {
         if (!a || !b || !a->has_host() || !b->has_host() || a->ndata != 1 || b->ndata != 1) return false;
         return a->type == b->type && a->host == b->host;
     };
-    int fused = 0;
+    int fused = 0, gelu = 0;
     for (int i = 0; i < n; ++i) {
         operator_t* mm = nodes[i];
         if (!active(mm) || mm->op_type != "QLinearMatMul" || mm->outputs.size() != 1) continue;
@@ -543,8 +548,19 @@ void fuse_matmul_dq_bias(context_t* ctx) {
         dq->skip = true;
         add->skip = true;
         ++fused;
+        // then a Gelu of the biased value
+        tensor_t* fb = add->outputs[0];
+        if (graph_out.count(fb)) continue;
+        operator_t* ge = sole_consumer(fb);
+        if (!ge || ge->op_type != "Gelu" || ge->inputs.size() != 1 || ge->outputs.size() != 1) continue;
+        if (!mm->fuse_gelu(ge)) continue;
+        mm->fused_chain.push_back(ge);
+        mm->outputs[0] = ge->outputs[0];
+        ge->skip = true;
+        ++gelu;
     }
     ctx->fusion_stats["matmul_dq_bias"] = fused;
+    ctx->fusion_stats["matmul_gelu"] = gelu;
 }
 
 // ---------------------------------------------------------------------------
@@ -585,6 +601,78 @@ void fuse_quant_prefix(context_t* ctx) {
     }
     ctx->fusion_stats["quantize_first_conv"] = nq;
     ctx->fusion_stats["dequantize_gap"] = ndq;
+}
+
+// ---------------------------------------------------------------------------
+// Add(a, b) of two same-shape fp32 tensors whose only consumer is a
+// LayerNormalization (BERT's residual connections): the normalization reads
+// a and b and forms fl(a + b) itself, so the sum is never stored.
+void fuse_add_layernorm(context_t* ctx) {
+    std::unordered_set<tensor_t*> graph_out;
+    for (auto& name : ctx->graph_outputs)
+        if (tensor_t* t = ctx->find(name)) graph_out.insert(t);
+    std::unordered_map<tensor_t*, operator_t*> producer;
+    std::unordered_map<tensor_t*, int> uses;
+    for (auto* op : ctx->nodes) {
+        if (!active(op)) continue;
+        for (auto* t : op->outputs)
+            if (t) producer[t] = op;
+        for (auto* t : op->inputs)
+            if (t) uses[t]++;
+    }
+    int fused = 0;
+    for (auto* op : ctx->nodes) {
+        if (!active(op) || op->op_type != "LayerNormalization" || !op->fused_pre.empty()) continue;
+        tensor_t* x = op->inputs[0];
+        auto it = producer.find(x);
+        if (it == producer.end() || graph_out.count(x) || uses[x] != 1) continue;
+        operator_t* add = it->second;
+        if (add->op_type != "Add" || add->inputs.size() != 2 || add->outputs.size() != 1) continue;
+        tensor_t *a = add->inputs[0], *b = add->inputs[1];
+        if (!a || !b || a->type != NNR_DATA_TYPE_FLOAT32 || b->type != NNR_DATA_TYPE_FLOAT32) continue;
+        if (a->dims != x->dims || b->dims != x->dims) continue;
+        if (!op->fuse_residual_input(add)) continue;
+        op->fused_pre = {add};
+        op->inputs[0] = a;
+        op->fused_other = b;
+        add->skip = true;
+        ++fused;
+    }
+    ctx->fusion_stats["add_layernorm"] = fused;
+}
+
+// ---------------------------------------------------------------------------
+// DynamicQuantizeLinear whose input's producer can write the input's
+// (min, max) pairs as it stores it: the producer gets a buffer for them and
+// the quantizer skips its own min / max pass. The producer still writes the
+// whole tensor; any other consumer reads it as before.
+void fuse_dynq_minmax(context_t* ctx) {
+    std::unordered_map<tensor_t*, operator_t*> producer;
+    for (auto* op : ctx->nodes) {
+        if (!active(op)) continue;
+        for (auto* t : op->outputs)
+            if (t) producer[t] = op;
+    }
+    int fused = 0;
+    for (auto* op : ctx->nodes) {
+        if (!active(op) || op->op_type != "DynamicQuantizeLinear" || op->minmax_src) continue;
+        auto it = producer.find(op->inputs[0]);
+        if (it == producer.end()) continue;
+        operator_t* p = it->second;
+        if (p->outputs.empty() || p->outputs[0] != op->inputs[0]) continue;
+        if (!p->minmax_parts) {
+            const int pairs = p->minmax_pairs();
+            if (pairs <= 0) continue;
+            float* buf = (float*)ctx->device_alloc(sizeof(float) * 2 * (size_t)pairs);
+            if (!buf) continue;
+            if (!p->set_minmax_out(buf, pairs)) continue;
+            p->minmax_parts = buf;
+            p->minmax_count = pairs;
+        }
+        op->minmax_src = p;
+        ++fused;
+    }
+    ctx->fusion_stats["dynq_minmax"] = fused;
 }
 
 // ---------------------------------------------------------------------------

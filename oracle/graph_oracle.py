@@ -228,7 +228,9 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
                 cres = exec_node({"op": gn.op, "name": gn.name, "inputs": list(gn.inputs),
                                   "outputs": list(gn.outputs), "post_fn": 0})
                 chain_env.update(cres)
-            res = {nd["outputs"][0]: chain_env[nd["outputs"][0]]}
+            # the chain's last output is this node's own (a device tensor):
+            # later nodes read it through `source` like any other output
+            res = {nd["outputs"][0]: chain_env.pop(nd["outputs"][0])}
         env.update(res)
         if stop_after and nd["name"] == stop_after:
             break

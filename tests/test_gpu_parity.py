@@ -368,6 +368,112 @@ def test_qmatmul_fused_dq_bias(dev):
         f"{np.count_nonzero(got != ref)} of {got.size} differ"
 
 
+@pytest.mark.parametrize("m,n,batch", [(40, 136, 3), (8192 // 64, 3072, 2), (70, 64, 1)])
+def test_qmatmul_fused_gelu_minmax(dev, m, n, batch):
+    """QLinearMatMul -> DequantizeLinear -> + bias -> Gelu in one kernel that
+    also writes the (min, max) pairs of its output: the Gelu bits equal the
+    standalone Gelu kernel on the unfused result (and the erf form within
+    fp32 rounding of the float64 formula); the pairs cover exactly the
+    output's min / max, and DynamicQuantizeLinear from them matches the
+    two-pass one byte for byte."""
+    import ctypes
+    import math
+    import torch
+    from nnr_amd import _lib
+    rng = np.random.default_rng(m + n)
+    k = 96
+    a = rng.integers(0, 256, (batch, m, k), dtype=np.uint8)
+    b = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    bias = rng.standard_normal(n).astype(np.float32)
+    ys, yz = 0.031, 121
+    s = torch.tensor([0.0133], dtype=torch.float32, device=dev)
+    z = torch.tensor([77], dtype=torch.uint8, device=dev)
+    ad = to_dev(a, dev)
+    plain = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, ys, yz, m=m)
+    plain.fuse_dq_bias(ys, yz, bias)
+    f = plain(ad, a_scale_dev=s, a_zp_dev=z)
+    g_ref = torch.empty_like(f)
+    _lib.check(_lib.lib().nnrh_gelu_f32(f.data_ptr(), g_ref.data_ptr(), f.numel(), _lib.cur_stream()))
+    op = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, ys, yz, m=m)
+    op.fuse_dq_bias(ys, yz, bias)
+    op.fuse_gelu()
+    cnt = op.minmax_count(batch)
+    assert cnt == 4 * batch * -(-m // (256 if n <= 64 else 128)) * -(-n // (64 if n <= 64 else 128))
+    parts = torch.full((2 * cnt,), float("nan"), dtype=torch.float32, device=dev)
+    op.set_minmax_out(parts[: 2 * cnt - 2])
+    with pytest.raises(H.NnrHipError):   # a buffer one pair short is refused
+        op(ad, a_scale_dev=s, a_zp_dev=z)
+    op.set_minmax_out(parts)
+    for _ in range(2):   # the second run rewrites every pair
+        y = op(ad, a_scale_dev=s, a_zp_dev=z)
+        got, ref = to_np(y), to_np(g_ref)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        fv = to_np(f).astype(np.float64)
+        erf = np.vectorize(math.erf)
+        np.testing.assert_allclose(got, 0.5 * fv * (1.0 + erf(fv / math.sqrt(2.0))), rtol=2e-6, atol=1e-7)
+        pr = to_np(parts).reshape(-1, 2)
+        assert not np.isnan(pr).any()
+        assert pr[:, 0].min() == min(0.0, got.min()) and pr[:, 1].max() == max(0.0, got.max())
+        q1, s1, z1 = H.dynamic_quantize_linear_parts(y, parts)
+        q0, s0, z0 = H.dynamic_quantize_linear(y)
+        assert to_np(s1)[0] == to_np(s0)[0] and to_np(z1)[0] == to_np(z0)[0]
+        assert np.array_equal(to_np(q1), to_np(q0))
+        parts.fill_(float("nan"))
+    op.set_minmax_out(None)
+
+
+@pytest.mark.parametrize("rows,D,res,beta", [(37, 768, True, True), (9, 2048, True, False),
+                                             (5, 102, True, True), (3, 3000, False, True),
+                                             (130, 768, False, False)])
+def test_add_layernorm(dev, rows, D, res, beta):
+    """LayerNormalization of x (+ r), register-resident (D % 4 == 0, D <= 2048)
+    and strided rows, against a float64 restatement of LayerNormalization.cpp;
+    the per-row (min, max) pairs are the exact extremes of each output row,
+    and DynamicQuantizeLinear from them matches the two-pass one."""
+    import torch
+    rng = np.random.default_rng(rows * D)
+    x = rng.normal(0.2, 1.3, (rows, D)).astype(np.float32)
+    r = rng.normal(0, 0.7, (rows, D)).astype(np.float32) if res else None
+    gm = rng.normal(1, 0.2, D).astype(np.float32)
+    bt = rng.normal(0, 0.2, D).astype(np.float32) if beta else None
+    parts = torch.full((2 * rows,), float("nan"), dtype=torch.float32, device=dev)
+    y = H.layernorm(to_dev(x, dev), to_dev(gm, dev), None if bt is None else to_dev(bt, dev), 1e-5,
+                    r=None if r is None else to_dev(r, dev), parts=parts)
+    v = (x + r if res else x).astype(np.float64)   # the fp32 sum, as the Add stores it
+    mu = v.mean(-1, keepdims=True)
+    ref = (v - mu) / np.sqrt(((v - mu) ** 2).mean(-1, keepdims=True) + 1e-5) * gm
+    if beta:
+        ref = ref + bt
+    got = to_np(y)
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+    pr = to_np(parts).reshape(rows, 2)
+    assert np.array_equal(pr[:, 0], np.minimum(got.min(-1), 0)) and np.array_equal(pr[:, 1], np.maximum(got.max(-1), 0))
+    q1, s1, z1 = H.dynamic_quantize_linear_parts(y, parts)
+    q0, s0, z0 = H.dynamic_quantize_linear(y)
+    assert to_np(s1)[0] == to_np(s0)[0] and to_np(z1)[0] == to_np(z0)[0]
+    assert np.array_equal(to_np(q1), to_np(q0))
+
+
+@pytest.mark.parametrize("n,nparts", [(6, 1), (1000, 7), (98304 * 3 + 5, 300), (4096 * 17, 6144)])
+def test_dynamic_quantize_from_parts(dev, n, nparts):
+    """DynamicQuantizeLinear from (min, max) pairs of any split of x (the
+    extremes are exact in any order): bytes, scale and zero point equal the
+    oracle's, including all-positive data (the 0 the operator adds)."""
+    import torch
+    rng = np.random.default_rng(n + nparts)
+    for shift in (0.3, 4.0):
+        x = (rng.normal(0, 1.5, n) + shift).astype(np.float32)
+        cuts = np.sort(rng.integers(0, n + 1, nparts - 1)) if nparts > 1 else np.array([], int)
+        pr = np.zeros((nparts, 2), np.float32)
+        for i, c in enumerate(np.split(x, cuts)):
+            if c.size:
+                pr[i] = (min(0.0, c.min()), max(0.0, c.max()))
+        y_ref, s_ref, z_ref = O.dynamic_quantize_linear(x)
+        y, s, z = H.dynamic_quantize_linear_parts(to_dev(x, dev), to_dev(pr.reshape(-1), dev))
+        assert to_np(s)[0] == np.float32(s_ref) and int(to_np(z)[0]) == z_ref
+        assert np.array_equal(to_np(y), y_ref)
+
+
 # ---------------------------------------------------------------------------
 # QuantizeLinear fused into the first layer's input layout, DequantizeLinear
 # fused into GlobalAveragePool
@@ -472,10 +578,18 @@ def test_qconv1d(dev, case):
     assert mism == 0, f"{mism} of {y.size} differ"
 
 
-@pytest.mark.parametrize("B,S,hidden,heads,scale", [(3, 37, 96, 4, 0.2), (2, 128, 768, 12, 0.125)])
+@pytest.mark.parametrize("B,S,hidden,heads,scale", [
+    (3, 37, 96, 4, 0.2),          # head size 24: batched rocBLAS GEMMs + scaled softmax
+    (2, 160, 128, 2, 0.1),        # S > 128: the same
+    (2, 128, 768, 12, 0.125),     # head size 64, S <= 128: the fused kernel
+    (3, 50, 128, 2, 0.3),         # fused, padded key rows and idle waves
+    (2, 1, 64, 1, 0.5),           # fused, one token
+    (1, 97, 192, 3, -0.7),        # fused, negative scale
+])
 def test_multihead_attention_f32(dev, B, S, hidden, heads, scale):
-    """MultiHeadAttention (heads read and written in place, batched rocBLAS
-    GEMMs, scaled softmax) against float64 numpy."""
+    """MultiHeadAttention (heads read and written in place; the fused fp32
+    MFMA kernel for head size 64 and S <= 128, batched rocBLAS GEMMs and a
+    scaled softmax otherwise) against float64 numpy."""
     import torch
     from nnr_amd import _lib
     import ctypes as C
