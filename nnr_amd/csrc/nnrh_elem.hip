@@ -477,6 +477,44 @@ __global__ __launch_bounds__(256) void maxpool_u8_16_kernel(const uint8_t* __res
     *(uint4*)(y + pix * C + cg * 16) = make_uint4(m[0], m[1], m[2], m[3]);
 }
 
+// the same with a compile-time window: every tap's load is issued before the
+// first max (out-of-image taps are skipped by predicate, not by loop bounds)
+template <int KH, int KW>
+__global__ __launch_bounds__(256) void maxpool_u8_16_fixed_kernel(const uint8_t* __restrict x,
+                                                                  uint8_t* __restrict y, int N, int C,
+                                                                  int iH, int iW, int oH, int oW, int sH,
+                                                                  int sW, int pH, int pW) {
+    const int C16 = C >> 4;
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= oW * C16) return;
+    const int ow = t / C16, cg = t - ow * C16;
+    const int oh = blockIdx.y, n = blockIdx.z;
+    const int ih0 = oh * sH - pH, iw0 = ow * sW - pW;
+    const uint8_t* xi = x + (long long)n * iH * iW * C + cg * 16;
+    uint4 v[KH][KW];
+#pragma unroll
+    for (int a = 0; a < KH; ++a)
+#pragma unroll
+        for (int b = 0; b < KW; ++b) {
+            const int ih = ih0 + a, iw = iw0 + b;
+            v[a][b] = ((unsigned)ih < (unsigned)iH && (unsigned)iw < (unsigned)iW)
+                          ? *(const uint4*)(xi + ((long long)ih * iW + iw) * C)
+                          : make_uint4(0u, 0u, 0u, 0u);
+        }
+    uint32_t m[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int a = 0; a < KH; ++a)
+#pragma unroll
+        for (int b = 0; b < KW; ++b) {
+            m[0] = bytemax4(m[0], v[a][b].x);
+            m[1] = bytemax4(m[1], v[a][b].y);
+            m[2] = bytemax4(m[2], v[a][b].z);
+            m[3] = bytemax4(m[3], v[a][b].w);
+        }
+    const long long pix = ((long long)n * oH + oh) * oW + ow;
+    *(uint4*)(y + pix * C + cg * 16) = make_uint4(m[0], m[1], m[2], m[3]);
+}
+
 hipError_t launch_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH, int iW,
                                   int oH, int oW, int kH, int kW, int sH, int sW, int pH, int pW,
                                   hipStream_t s) {
@@ -484,8 +522,15 @@ hipError_t launch_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, in
         const long long row = (long long)oW * (C / 16);
         if (row <= 0 || N <= 0 || oH <= 0) return hipSuccess;
         const dim3 grid((unsigned)((row + 255) / 256), (unsigned)oH, (unsigned)N);
-        hipLaunchKernelGGL(maxpool_u8_16_kernel, grid, dim3(256), 0, s, x, y, N, C, iH, iW, oH, oW, kH, kW,
-                           sH, sW, pH, pW);
+        if (kH == 3 && kW == 3)
+            hipLaunchKernelGGL((maxpool_u8_16_fixed_kernel<3, 3>), grid, dim3(256), 0, s, x, y, N, C, iH, iW, oH,
+                               oW, sH, sW, pH, pW);
+        else if (kH == 2 && kW == 2)
+            hipLaunchKernelGGL((maxpool_u8_16_fixed_kernel<2, 2>), grid, dim3(256), 0, s, x, y, N, C, iH, iW, oH,
+                               oW, sH, sW, pH, pW);
+        else
+            hipLaunchKernelGGL(maxpool_u8_16_kernel, grid, dim3(256), 0, s, x, y, N, C, iH, iW, oH, oW, kH, kW,
+                               sH, sW, pH, pW);
         return hipGetLastError();
     }
     long long total = (long long)N * oH * oW * ((C + 3) / 4);

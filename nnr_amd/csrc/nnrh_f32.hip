@@ -74,10 +74,47 @@ __global__ __launch_bounds__(256) void gap_dq_nhwc_kernel(const uint8_t* __restr
     y[row] = s / (float)HW;
 }
 
+// four consecutive channels per thread (one 4-byte load per pixel), each
+// channel's sum in the same pixel order
+__global__ __launch_bounds__(256) void gap_dq_nhwc4_kernel(const uint8_t* __restrict x, float* __restrict y,
+                                                           int N, int C, int HW, int sgn, float zpf, float sc) {
+    const int C4 = C >> 2;
+    const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (long long)N * C4) return;
+    const int n = (int)(t / C4), cg = (int)(t - (long long)n * C4);
+    const uint32_t* p = (const uint32_t*)(x + (long long)n * HW * C) + cg;
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto add = [&](uint32_t w) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float q = sgn ? (float)(int)(int8_t)(w >> (8 * j)) : (float)((w >> (8 * j)) & 0xffu);
+            s[j] += (q - zpf) * sc;
+        }
+    };
+    // 16 pixels' loads in flight at a time, then summed in pixel order
+    int i = 0;
+    for (; i + 16 <= HW; i += 16) {
+        uint32_t w[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) w[u] = p[(long long)(i + u) * C4];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) add(w[u]);
+    }
+    for (; i < HW; ++i) add(p[(long long)i * C4]);
+    *(float4*)(y + (long long)n * C + 4 * cg) =
+        make_float4(s[0] / (float)HW, s[1] / (float)HW, s[2] / (float)HW, s[3] / (float)HW);
+}
+
 hipError_t launch_gap_dq(const uint8_t* x, float* y, int N, int C, int HW, int x_nhwc, int x_signed,
                          float scale, int zp, hipStream_t s) {
     const long long rows = (long long)N * C;
     if (rows <= 0) return hipSuccess;
+    if (x_nhwc && (C & 3) == 0 && (((uintptr_t)x | (uintptr_t)y) & 15) == 0) {
+        const long long th = rows / 4;
+        hipLaunchKernelGGL(gap_dq_nhwc4_kernel, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, x, y, N, C,
+                           HW, x_signed, (float)zp, scale);
+        return hipGetLastError();
+    }
     if (x_nhwc)
         hipLaunchKernelGGL(gap_dq_nhwc_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, x, y, N,
                            C, HW, x_signed, (float)zp, scale);
@@ -132,11 +169,126 @@ rocblas_handle blas_handle() {
 }
 }  // namespace
 
+// Small fp32 GEMMs (too few 64x64 tiles to fill the chip, e.g. a
+// classifier over one batch): Y = alpha * A[M][K] . op(B) + beta * Cb with
+// fp32 MFMA 16x16x4. A block computes 32x32 outputs; its 4 waves take every
+// 4th 64-wide K chunk and their partial sums are added in LDS in wave order.
+// Within a chunk the contraction runs over k = 16 (l / 16) + step, so each
+// lane reads 16 consecutive floats of its A row (and of its B row when B is
+// stored [N][K]); rows and columns past M / N read a clamped row and are not
+// stored.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int TB>
+__global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(const float* __restrict A, const float* __restrict B,
+                                                            const float* __restrict C, float* __restrict Y, int M,
+                                                            int N, int K, float alpha, float beta, int c_mode) {
+    __shared__ float red[3][32 * 32];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lr = lane & 15, g = lane >> 4;
+    const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+    const float* ar[2] = {A + (long long)min(m0 + lr, M - 1) * K, A + (long long)min(m0 + 16 + lr, M - 1) * K};
+    const int bn[2] = {min(n0 + lr, N - 1), min(n0 + 16 + lr, N - 1)};
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto load = [&](int c, float (&a)[2][16], float (&b)[2][16]) {
+        const int k0 = c * 64 + 16 * g;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = *(const float4*)(ar[t] + k0 + 4 * j);
+                a[t][4 * j] = v.x; a[t][4 * j + 1] = v.y; a[t][4 * j + 2] = v.z; a[t][4 * j + 3] = v.w;
+            }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (TB) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float4 v = *(const float4*)(B + (long long)bn[t] * K + k0 + 4 * j);
+                    b[t][4 * j] = v.x; b[t][4 * j + 1] = v.y; b[t][4 * j + 2] = v.z; b[t][4 * j + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int st = 0; st < 16; ++st) b[t][st] = B[(long long)(k0 + st) * N + bn[t]];
+            }
+        }
+    };
+    auto mma = [&](const float (&a)[2][16], const float (&b)[2][16]) {
+#pragma unroll
+        for (int st = 0; st < 16; ++st)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][st], b[nt][st], acc[mt][nt], 0, 0, 0);
+    };
+    const int nch = K >> 6;
+    float a0[2][16], b0[2][16], a1[2][16], b1[2][16];
+    int c = w;
+    if (c < nch) load(c, a0, b0);
+    for (; c < nch; c += 8) {
+        // the next chunk's loads are in flight while this one multiplies
+        if (c + 4 < nch) load(c + 4, a1, b1);
+        mma(a0, b0);
+        if (c + 4 >= nch) break;
+        if (c + 8 < nch) load(c + 8, a0, b0);
+        mma(a1, b1);
+    }
+    // acc[mt][nt][i] = partial Y[m0 + 16 mt + 4 g + i][n0 + 16 nt + lr]
+    if (w > 0) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[w - 1][(16 * mt + 4 * g + i) * 32 + 16 * nt + lr] = acc[mt][nt][i];
+    }
+    __syncthreads();
+    if (w > 0) return;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * mt + 4 * g + i, cl = 16 * nt + lr;
+                const int m = m0 + r, n = n0 + cl;
+                float v = acc[mt][nt][i];
+                v = v + red[0][r * 32 + cl];
+                v = v + red[1][r * 32 + cl];
+                v = v + red[2][r * 32 + cl];
+                if (m >= M || n >= N) continue;
+                v = alpha * v;
+                if (c_mode != 0 && beta != 0.0f) {
+                    const float cb = c_mode == 1 ? C[0]
+                                     : c_mode == 2 ? C[n]
+                                     : c_mode == 3 ? C[(long long)m * N + n]
+                                                   : C[m];
+                    v = v + beta * cb;
+                }
+                Y[(long long)m * N + n] = v;
+            }
+}
+
 hipError_t launch_gemm_f32_batched(const float* A, const float* B, const float* C, float* Y, int M,
                                    int N, int K, int transA, int transB, float alpha, float beta,
                                    int c_mode, int batch, long long a_bstride, long long b_bstride,
                                    long long y_bstride, hipStream_t s) {
     if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
+    const long long tiles64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
+    if (batch == 1 && !transA && K > 0 && (K & 63) == 0 && tiles64 < 512 && M <= 65535 * 32 &&
+        (((uintptr_t)A | (uintptr_t)B) & 15) == 0) {
+        const dim3 grid((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
+        if (transB)
+            hipLaunchKernelGGL(gemm_f32_mfma_kernel<1>, grid, dim3(256), 0, s, A, B, C, Y, M, N, K, alpha, beta,
+                               c_mode);
+        else
+            hipLaunchKernelGGL(gemm_f32_mfma_kernel<0>, grid, dim3(256), 0, s, A, B, C, Y, M, N, K, alpha, beta,
+                               c_mode);
+        return hipGetLastError();
+    }
     rocblas_handle h = blas_handle();
     if (!h || rocblas_set_stream(h, s) != rocblas_status_success) return hipErrorNotInitialized;
     float beta_eff = 0.0f;
@@ -500,7 +652,6 @@ size_t mha_workspace_bytes(int B, int S, int nh) {
 // d = 16 (l / 16) + step, so every lane reads 16 consecutive floats of its K
 // row and Q row. Softmax of the scaled scores per query column, normalized
 // before P V (the order of Softmax then MatMul); padded t rows are -inf.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int MHA_KP = 68;   // K row stride in LDS (floats): rows 16 bytes apart in the banks
 
 __global__ __launch_bounds__(256) void mha_fused_hd64_kernel(const float* __restrict q, const float* __restrict k,

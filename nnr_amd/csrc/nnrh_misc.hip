@@ -144,49 +144,67 @@ __device__ __forceinline__ uint32_t quant_u8(float xv, long long idx, long long 
     return (uint32_t)q;
 }
 
-// One block per padded row (y = padded row, z = image): the row's input
-// pixels are quantized into LDS as packed 4-channel dwords (fill outside the
-// image), then every copy writes its shifted Wc-pixel row with 16-byte stores.
-// Row staging keeps the global reads contiguous (float4 when the row start
-// is 16-byte aligned) whatever the padding and copy shift.
-constexpr int QFL_MAX_ROW = 4096;   // padded row dwords staged in LDS
+// R <= QFL_ROWS padded rows per block (y = group of rows, z = image), R * L
+// dwords staged (L padded pixels a row): the rows' input pixels are quantized into LDS as packed 4-channel dwords (fill
+// outside the image), then every copy writes its shifted Wc-pixel rows with
+// 16-byte stores. Every load of a thread's pixels over all the block's rows
+// is issued before the first one is used, so each block keeps
+// R * C loads per thread in flight (one row per block leaves the kernel
+// waiting on memory latency).
+constexpr int QFL_MAX_ROW = 4096;   // dwords staged in LDS (all rows of a block)
+constexpr int QFL_ROWS = 8;
 
 __global__ __launch_bounds__(256) void quantize_first_layer_copies_kernel(
     const float* __restrict x, uint32_t* __restrict y, int C, int H, int W, int Hp, int Wc,
     int pad_t, int pad_l, int copy_shift, int ncopy, long long per_copy, uint8_t fill,
-    float scale, float inv, int zp, long long qbody) {
-    extern __shared__ uint32_t row[];   // L dwords (launch size)
-    const int ihp = blockIdx.y, n = blockIdx.z;
-    const int ih = ihp - pad_t;
+    float scale, float inv, int zp, long long qbody, int R) {
+    extern __shared__ uint32_t row[];   // R x L dwords (launch size)
+    const int ihp0 = blockIdx.y * R, n = blockIdx.z;
+    const int nrows = min(R, Hp - ihp0);
     // staged pixels: padded columns 0 .. L-1 (input column = p - pad_l)
     const int L = Wc + ((ncopy - 1) << copy_shift);
     const uint32_t fill4 = (uint32_t)fill * 0x01010101u;
-    const bool in_row = (unsigned)ih < (unsigned)H;
     const long long HW = (long long)H * W;
-    const long long base = (long long)n * C * HW + (long long)ih * W;
     for (int p = threadIdx.x; p < L; p += 256) {
         const int iw = p - pad_l;
-        uint32_t w = fill4;
-        if (in_row && (unsigned)iw < (unsigned)W) {
-            w = 0;
+        const bool in_col = (unsigned)iw < (unsigned)W;
+        float v[QFL_ROWS][4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                uint32_t bt = fill;
-                if (c < C) {
-                    const long long idx = base + (long long)c * HW + iw;
-                    bt = quant_u8(x[idx], idx, qbody, scale, inv, zp);
-                }
-                w |= bt << (8 * c);
-            }
+        for (int r = 0; r < QFL_ROWS; ++r) {
+            const int ih = ihp0 + r - pad_t;
+            const bool ok = r < nrows && in_col && (unsigned)ih < (unsigned)H;
+            const long long base = (long long)n * C * HW + (long long)ih * W + iw;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[r][c] = (ok && c < C) ? x[base + (long long)c * HW] : 0.0f;
         }
-        row[p] = w;
+#pragma unroll
+        for (int r = 0; r < QFL_ROWS; ++r) {
+            const int ih = ihp0 + r - pad_t;
+            if (r >= nrows) break;
+            uint32_t w = fill4;
+            if (in_col && (unsigned)ih < (unsigned)H) {
+                w = 0;
+                const long long base = (long long)n * C * HW + (long long)ih * W + iw;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    uint32_t bt = fill;
+                    if (c < C) {
+                        const long long idx = base + (long long)c * HW;
+                        bt = quant_u8(v[r][c], idx, qbody, scale, inv, zp);
+                    }
+                    w |= bt << (8 * c);
+                }
+            }
+            row[r * L + p] = w;
+        }
     }
     __syncthreads();
     const int q4 = Wc >> 2;   // 16-byte groups per copy row
-    for (int t = threadIdx.x; t < q4 * ncopy; t += 256) {
-        const int ci = t / q4, g = t - ci * q4;
-        const int p0 = (ci << copy_shift) + 4 * g;
-        uint32_t* yp = y + (long long)ci * per_copy + ((long long)n * Hp + ihp) * Wc + 4 * g;
+    for (int t = threadIdx.x; t < q4 * ncopy * nrows; t += 256) {
+        const int r = t / (q4 * ncopy), u = t - r * (q4 * ncopy);
+        const int ci = u / q4, g = u - ci * q4;
+        const int p0 = r * L + (ci << copy_shift) + 4 * g;
+        uint32_t* yp = y + (long long)ci * per_copy + ((long long)n * Hp + ihp0 + r) * Wc + 4 * g;
         *(uint4*)yp = make_uint4(row[p0], row[p0 + 1], row[p0 + 2], row[p0 + 3]);
     }
 }
@@ -195,17 +213,18 @@ hipError_t launch_quantize_first_layer_copies(const float* x, uint8_t* y, int N,
                                               int Hp, int Wc, int pad_t, int pad_l, int copy_shift,
                                               uint8_t fill, float scale, int zp, hipStream_t s) {
     const int ncopy = 4 >> copy_shift;
-    if (N <= 0 || C > 4 || ((uintptr_t)y & 15) || (Wc & 3) || N > 65535 || Hp > 65535 ||
-        Wc + ((ncopy - 1) << copy_shift) > QFL_MAX_ROW)
+    const int L = Wc + ((ncopy - 1) << copy_shift);
+    if (N <= 0 || C > 4 || ((uintptr_t)y & 15) || (Wc & 3) || N > 65535 || Hp > 65535 || L > QFL_MAX_ROW)
         return hipErrorInvalidValue;
+    const int R = min(QFL_ROWS, QFL_MAX_ROW / L);
     const long long per_copy = (long long)N * Hp * Wc;
     const long long qn = (long long)N * C * H * W;
     const long long qbody = qn >= 64 ? qn - qn % 16 : 0;
     const float inv = 1.0f / scale;
-    const dim3 grid(1, (unsigned)Hp, (unsigned)N);
-    const size_t lds = sizeof(uint32_t) * (size_t)(Wc + ((ncopy - 1) << copy_shift));
+    const dim3 grid(1, (unsigned)((Hp + R - 1) / R), (unsigned)N);
+    const size_t lds = sizeof(uint32_t) * (size_t)R * L;
     hipLaunchKernelGGL(quantize_first_layer_copies_kernel, grid, dim3(256), lds, s, x, (uint32_t*)y, C, H, W,
-                       Hp, Wc, pad_t, pad_l, copy_shift, ncopy, per_copy, fill, scale, inv, zp, qbody);
+                       Hp, Wc, pad_t, pad_l, copy_shift, ncopy, per_copy, fill, scale, inv, zp, qbody, R);
     return hipGetLastError();
 }
 

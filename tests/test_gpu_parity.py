@@ -306,11 +306,17 @@ def test_qlinear_add(dev, kind, y_nhwc):
     assert np.array_equal(y, ref)
 
 
-def test_maxpool(dev):
-    rng = np.random.default_rng(6)
-    x = rng.integers(0, 256, (4, 23, 21, 64), dtype=np.uint8)
-    ref = O.maxpool_u8_nhwc(x, 3, 3, 2, 2, 1, 1, 12, 11)
-    y = to_np(H.maxpool_u8_nhwc(to_dev(x, dev), 3, 3, 2, 2, 1, 1, 12, 11))
+@pytest.mark.parametrize("C,k,st,pad", [(64, (3, 3), 2, 1),   # fixed 3x3 window (ResNet stem)
+                                        (48, (2, 2), 2, 0),   # fixed 2x2
+                                        (32, (3, 2), 1, 1),   # any window, 16-channel groups
+                                        (20, (3, 3), 2, 1)])  # 4-channel path
+def test_maxpool(dev, C, k, st, pad):
+    rng = np.random.default_rng(6 + C)
+    x = rng.integers(0, 256, (4, 23, 21, C), dtype=np.uint8)
+    oH = (23 + 2 * pad - k[0]) // st + 1
+    oW = (21 + 2 * pad - k[1]) // st + 1
+    ref = O.maxpool_u8_nhwc(x, k[0], k[1], st, st, pad, pad, oH, oW)
+    y = to_np(H.maxpool_u8_nhwc(to_dev(x, dev), k[0], k[1], st, st, pad, pad, oH, oW))
     assert np.array_equal(y, ref)
 
 
@@ -318,12 +324,15 @@ def test_maxpool(dev):
 # fp32 glue: Gemm (rocBLAS) with every broadcast mode and transpose, against
 # float64 numpy; the reference's float tolerance (tensor_equal, 1e-3 abs)
 
+@pytest.mark.parametrize("M,N,K", [(37, 70, 300),     # rocBLAS (K % 64 != 0)
+                                   (37, 70, 320),     # the MFMA kernel: 5 K chunks over 4 waves
+                                   (5, 3, 64),        # one chunk, clamped rows / columns
+                                   (256, 1000, 2048)])  # ResNet-50's classifier
 @pytest.mark.parametrize("ta,tb,c_mode", [(0, 1, 2), (0, 0, 0), (1, 0, 1), (1, 1, 3), (0, 1, 4)])
-def test_gemm_f32(dev, ta, tb, c_mode):
+def test_gemm_f32(dev, ta, tb, c_mode, M, N, K):
     import torch
     from nnr_amd import _lib
-    rng = np.random.default_rng(ta * 10 + tb * 3 + c_mode)
-    M, N, K = 37, 70, 300
+    rng = np.random.default_rng(ta * 10 + tb * 3 + c_mode + M)
     A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32) * 0.1
     B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32) * 0.1
     Cs = {0: (1,), 1: (1,), 2: (N,), 3: (M, N), 4: (M,)}[c_mode]
@@ -513,14 +522,16 @@ def test_qconv_fused_quantize(dev, case):
     assert mism == 0, f"{mism} of {y.size} differ"
 
 
-@pytest.mark.parametrize("nhwc,dt", [(1, np.uint8), (0, np.uint8), (1, np.int8)])
-def test_global_avgpool_dequant(dev, nhwc, dt):
+@pytest.mark.parametrize("nhwc,dt,C", [(1, np.uint8, 72), (0, np.uint8, 72), (1, np.int8, 72),
+                                       (1, np.uint8, 70)])
+def test_global_avgpool_dequant(dev, nhwc, dt, C):
     """DequantizeLinear + GlobalAveragePool in one pass == the two HIP ops
-    run separately (bit for bit) and the oracle within fp32 tolerance."""
+    run separately (bit for bit) and the oracle within fp32 tolerance; NHWC
+    with C % 4 == 0 reads 4 channels a load, other C one byte."""
     import torch
     from nnr_amd import _lib
-    rng = np.random.default_rng(41 + nhwc)
-    N, C, Hh, W = 3, 72, 7, 7
+    rng = np.random.default_rng(41 + nhwc + C)
+    N, Hh, W = 3, 7, 7
     info = (0, 256) if dt == np.uint8 else (-128, 128)
     shape = (N, Hh, W, C) if nhwc else (N, C, Hh, W)
     q = rng.integers(*info, shape, dtype=dt)
