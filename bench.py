@@ -312,7 +312,8 @@ def run_model(args, dev, model):
     cpu_img_s = reps / (time.perf_counter() - t0)
     imgs = B / (ms * 1e-3)
     return dict(
-        metric=METRIC, value=round(imgs, 1), unit="images/s", ms_per_step=ms,
+        metric=METRIC if model == "resnet50" else "MobileNetV2-int8 images/sec b256 (cfg4), 1 GPU",
+        value=round(imgs, 1), unit="images/s", ms_per_step=ms,
         config={"workload": WORKLOADS[model].format(B=B), "global_batch": B,
                 "branches": {b: sum(1 for p in plan if p["variant"].split("+")[0] == b)
                              for b in ("FIRST", "DW", "NR16", "PACKED")},

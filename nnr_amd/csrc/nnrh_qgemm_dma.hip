@@ -621,6 +621,8 @@ void qgemm_dma_kernel(GemmArgs g) {
                 }
                 uint8_t* yrow = (uint8_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
                 if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
+                    // (a plain store: the next layer reads this output, and a
+                    // streaming store would send it past the caches to HBM)
                     *(v4i*)yrow = v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
                 } else {
 #pragma unroll
@@ -637,19 +639,21 @@ void qgemm_dma_kernel(GemmArgs g) {
     for (int s = 0; s < S - 1; ++s)
         if (p_t < t_end) p_issue();
 
-    for (;;) {
-        // wait for this thread's DMAs of step c_gs; later steps stay in flight
-        const int ahead = p_gs - c_gs - 1;
+    // wait until every wave's DMAs of consumer step cs have landed, then
+    // refill the stage (and param slot) that no wave reads any more
+    auto sync_step = [&](int cs) {
+        // this thread's DMAs of step cs; later steps stay in flight
+        const int ahead = p_gs - cs - 1;
         if (ahead >= S - 2) __builtin_amdgcn_s_waitcnt(NNRH_VMCNT((S - 2) * LPS));
         else if (S >= 4 && ahead == 1) __builtin_amdgcn_s_waitcnt(NNRH_VMCNT(LPS));
         else __builtin_amdgcn_s_waitcnt(NNRH_VMCNT(0));
-        // every wave's DMAs of the step have landed; every wave is done
-        // reading the stage (and param slot) the next issue overwrites
+        // (this wave's LDS reads of the stage being freed were consumed by
+        // its MFMAs / epilogue before it got here)
         block_barrier();
         if (p_t < t_end) p_issue();
-
-        const uint8_t* st = lds + c_stage;
-        v4i xf[4], wf[4];
+    };
+    auto read_frags = [&](int stage, v4i (&xf)[4], v4i (&wf)[4]) {
+        const uint8_t* st = lds + stage;
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) {
             v4i v = *(const v4i*)(st + dma_lds_off(wm * 64 + tm * 16 + frow, fchunk));
@@ -659,6 +663,8 @@ void qgemm_dma_kernel(GemmArgs g) {
 #pragma unroll
         for (int tn = 0; tn < 4; ++tn)
             wf[tn] = *(const v4i*)(st + BM * 64 + dma_lds_off(wn * 64 + tn * 16 + frow, fchunk));
+    };
+    auto mma = [&](const v4i (&xf)[4], const v4i (&wf)[4]) {
         if (c_kt == 0) {
             // the tile's constants landed with its first K-step: the first
             // MFMAs start from c0[n] (this lane's 16 columns), or from
@@ -687,6 +693,10 @@ void qgemm_dma_kernel(GemmArgs g) {
                 for (int tn = 0; tn < 4; ++tn)
                     acc[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[tn], xf[tm], acc[tm][tn], 0, 0, 0);
         }
+    };
+    // after the MFMAs of a step: the epilogue when it was the tile's last;
+    // false when the block has no tile left
+    auto finish_step = [&]() -> bool {
         ++c_gs;
         c_stage = c_stage + STAGE == S * STAGE ? 0 : c_stage + STAGE;
         if (++c_kt == nk) {
@@ -707,8 +717,17 @@ void qgemm_dma_kernel(GemmArgs g) {
             c_kt = 0;
             c_pslot = c_pslot + PSLOT == S * PSLOT ? 0 : c_pslot + PSLOT;
             c_t += t_step;
-            if (c_t >= t_end) break;
+            if (c_t >= t_end) return false;
         }
+        return true;
+    };
+
+    for (;;) {
+        sync_step(c_gs);
+        v4i xf[4], wf[4];
+        read_frags(c_stage, xf, wf);
+        mma(xf, wf);
+        if (!finish_step()) break;
     }
     // nothing may be left in flight into LDS when the block retires
     __builtin_amdgcn_s_waitcnt(NNRH_VMCNT(0));
