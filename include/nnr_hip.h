@@ -266,7 +266,9 @@ int nnrh_global_avgpool_f32(const float* x_dev, float* y_dev, int N, int C, int 
 /* com.microsoft MultiHeadAttention (src/backend/cpu/MultiHeadAttention.cpp,
  * no mask): q, k, v, y are [B][seq][hidden] fp32 with hidden = num_heads *
  * head_dim; y = softmax(scale * Q_h K_h^T) V_h per (batch, head), with the
- * heads read and written in place. workspace: device memory of at least
+ * heads read and written in place. Head size 64 with seq <= 128 runs as
+ * one fused fp32-MFMA kernel per (batch, head); other shapes use batched
+ * GEMMs and a scaled softmax. workspace: device memory of at least
  * nnrh_multihead_attention_workspace bytes, 256-byte aligned.              */
 int nnrh_multihead_attention_workspace(int B, int seq, int num_heads, size_t* bytes);
 int nnrh_multihead_attention_f32(const float* q_dev, const float* k_dev, const float* v_dev, float* y_dev,
