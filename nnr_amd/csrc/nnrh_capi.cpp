@@ -363,6 +363,8 @@ struct nnrh_qconv {
     // device buffers
     int8_t* wpack = nullptr;
     uint32_t* wdot = nullptr;    // depthwise dot4 weights [ceil(taps/4)][C]
+    uint32_t* wrow3 = nullptr;   // 3x3 depthwise: per filter row {w0, w1, w2, 0} [3][C]
+    bool dw3 = false;
     int32_t* colsum = nullptr;
     int32_t* c0 = nullptr;       // GEMM: per-column constant; depthwise: tap-sum correction
     int32_t* beta_col = nullptr;
@@ -375,7 +377,7 @@ struct nnrh_qconv {
     int8_t* w1d = nullptr;       // 1-D: raw weights [OC][C/group][kW]
     int32_t* wzp1d = nullptr;    // 1-D: per-channel w_zp read through the activation type
     ~nnrh_qconv() {
-        dfree(wpack); dfree(wdot); dfree(colsum); dfree(c0); dfree(beta_col); dfree(os); dfree(cs); dfree(bf);
+        dfree(wpack); dfree(wdot); dfree(wrow3); dfree(colsum); dfree(c0); dfree(beta_col); dfree(os); dfree(cs); dfree(bf);
         dfree(bias); dfree(xs); dfree(rowsum); dfree(w1d); dfree(wzp1d);
     }
 };
@@ -501,6 +503,17 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
             }
             if ((rc = upload(&h->wdot, wdot.data(), wdot.size()))) return fail(rc);
             if ((rc = upload(&h->c0, corr.data(), corr.size()))) return fail(rc);
+            // 3x3, stride 1 or 2, dilation 1: one dot4 per filter row
+            h->dw3 = d->kH == 3 && d->kW == 3 && d->dH == 1 && d->dW == 1 && d->sH == d->sW &&
+                     (d->sH == 1 || d->sH == 2);
+            if (h->dw3) {
+                std::vector<uint32_t> wrow((size_t)3 * OC, 0u);
+                for (int c = 0; c < OC; ++c)
+                    for (int t = 0; t < 9; ++t)
+                        wrow[(size_t)(t / 3) * OC + c] |= (uint32_t)(uint8_t)d->w_host[(size_t)c * 9 + t]
+                                                          << (8 * (t % 3));
+                if ((rc = upload(&h->wrow3, wrow.data(), wrow.size()))) return fail(rc);
+            }
         }
     } else {
         // ---- GEMM plan: groups on blockIdx.z, K order (kh, kw, c); every
@@ -732,6 +745,14 @@ int qconv_compute(nnrh_qconv_t h, const uint8_t* src, void* y, hipStream_t s) {
                                     d.group, d.kW, d.oW, d.sW, d.dW, d.pad_l, d.x_zp, d.y_zp, d.y_scale,
                                     d.act_dtype == NNRH_U8, s),
                 "conv1d_typed");
+        return NNRH_OK;
+    }
+    if (h->use_dw && h->dw3) {
+        ProfScope ps("depthwise", s);
+        HIP_TRY(launch_depthwise3x3(src, h->wrow3, h->c0, (uint8_t*)y, h->cs, h->bf, d.N, d.C, d.H, d.W, d.oH,
+                                    d.oW, d.sH, d.pad_t, d.pad_l, d.x_zp, d.act_dtype == NNRH_U8 ? 0x80 : 0,
+                                    h->inv_y, d.y_zp, h->dw_L, d.act_dtype == NNRH_U8 ? 255 : 127, s),
+                "depthwise3x3");
         return NNRH_OK;
     }
     if (h->use_dw && h->dw16) {

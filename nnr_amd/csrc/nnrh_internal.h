@@ -160,6 +160,11 @@ hipError_t launch_depthwise(const uint8_t* x, const int8_t* w, uint8_t* y,
                             hipStream_t s);
 // depthwise, NHWC in/out, C % 16 == 0, w_zp 0, at most 12 taps, no tails
 // (nnrh_misc.hip); wdot [ceil(taps/4)][C] 4 taps per dword, corr[C]
+// 3x3 depthwise, stride 1 or 2, dilation 1, NHWC in and out, C % 8 == 0
+hipError_t launch_depthwise3x3(const uint8_t* x, const uint32_t* wrow, const int32_t* corr, uint8_t* y,
+                               const float* cs, const float* bf, int N, int C, int H, int W, int oH, int oW,
+                               int stride, int pad_t, int pad_l, int x_zp, int a_xor, float inv_y, int y_zp,
+                               int L, int hi, hipStream_t s);
 hipError_t launch_depthwise16(const uint8_t* x, const uint32_t* wdot, const int32_t* corr,
                               uint8_t* y, const float* cs, const float* bf, int N, int C, int H,
                               int W, int oH, int oW, int kH, int kW, int sH, int sW, int dH, int dW,

@@ -559,6 +559,171 @@ __global__ __launch_bounds__(256) void dw16_kernel(Dw16Args p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// 3x3 depthwise, stride 1 or 2, 8 channels (two dwords) a thread and 4
+// consecutive output pixels of one row. A filter row contributes through one
+// sdot4 per (pixel, channel): its weights are packed {w0, w1, w2, 0}, and the
+// window of 4 input bytes starting at the pixel's first column comes from
+// the byte transpose of 4 input columns by v_alignbyte (the 4th byte meets
+// the 0 weight). Each filter row's input columns (6 for stride 1, 9 for
+// stride 2) are loaded once for all 4 pixels, every load issued before the
+// first use. Same arithmetic as dw16_kernel: x ^ 0x80 against signed weights,
+// the per-channel constant (128 - x_zp) * sum(w), RQ-A.
+struct Dw3Args {
+    const uint8_t* x;
+    const uint32_t* wrow;   // [3][C]: {w[c][a][0], w[c][a][1], w[c][a][2], 0}
+    const int32_t* corr;    // [C]
+    const float* cs;
+    const float* bf;
+    uint8_t* y;
+    int N, C, H, W, oH, oW, pad_t, pad_l;
+    uint32_t pad4, xmask;
+    float inv_y;
+    int y_zp, L, hi;
+    int c8, groups_per_block;         // channel chunks; pixel groups a block holds
+    uint32_t n_groups;                // rows * owbs
+    uint32_t owbs, owb_mul, owb_shift;
+};
+
+template <int SW>
+__global__ __launch_bounds__(256) void dw3x3_kernel(Dw3Args p) {
+    constexpr int NCOL = 3 + 3 * SW;            // input columns of 4 output pixels
+    constexpr int NG = (NCOL + 3) / 4;          // 4-column transpose groups
+    const int tid = threadIdx.x;
+    if (tid >= p.c8 * p.groups_per_block) return;
+    const int cg = tid % p.c8;
+    const int gl = tid / p.c8;
+    const int c0 = cg * 8;
+    uint32_t wd[3][8];
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint4 v = *(const uint4*)(p.wrow + (long long)a * p.C + c0 + 4 * q);
+            wd[a][4 * q] = v.x; wd[a][4 * q + 1] = v.y; wd[a][4 * q + 2] = v.z; wd[a][4 * q + 3] = v.w;
+        }
+    int32_t corr[8];
+    float cs[8], bf[8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int4 cv = *(const int4*)(p.corr + c0 + 4 * q);
+        const float4 sv = *(const float4*)(p.cs + c0 + 4 * q);
+        const float4 bv = *(const float4*)(p.bf + c0 + 4 * q);
+        corr[4 * q] = cv.x; corr[4 * q + 1] = cv.y; corr[4 * q + 2] = cv.z; corr[4 * q + 3] = cv.w;
+        cs[4 * q] = sv.x; cs[4 * q + 1] = sv.y; cs[4 * q + 2] = sv.z; cs[4 * q + 3] = sv.w;
+        bf[4 * q] = bv.x; bf[4 * q + 1] = bv.y; bf[4 * q + 2] = bv.z; bf[4 * q + 3] = bv.w;
+    }
+    const float lo_f = (float)(p.L - p.y_zp), hi_f = (float)(p.hi - p.y_zp);
+    const bool zp_even = (p.y_zp & 1) == 0;
+    const float magic = zp_even ? 12582912.0f + (float)p.y_zp : 12582912.0f;
+    const uint32_t zp_add = zp_even ? 0u : (uint32_t)p.y_zp;
+    const uint32_t stride = gridDim.x * (uint32_t)p.groups_per_block;
+
+    for (uint32_t pg = blockIdx.x * (uint32_t)p.groups_per_block + gl; pg < p.n_groups; pg += stride) {
+        const int row = (int)fast_div(pg, p.owb_mul, p.owb_shift);
+        const int owb = (int)pg - row * (int)p.owbs;
+        const int n = row / p.oH;
+        const int oh = row - n * p.oH;
+        const int ow0 = owb * 4;
+        const uint8_t* xn = p.x + (long long)n * p.H * p.W * p.C + c0;
+        int32_t acc[4][8];
+#pragma unroll
+        for (int px = 0; px < 4; ++px)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[px][c] = corr[c];
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            const int ih = oh * SW - p.pad_t + a;
+            const bool row_ok = (unsigned)ih < (unsigned)p.H;
+            const uint8_t* xr = xn + (long long)ih * p.W * p.C;
+            uint2 v[4 * NG];
+#pragma unroll
+            for (int j = 0; j < 4 * NG; ++j) {
+                v[j] = make_uint2(0u, 0u);   // columns past NCOL meet 0 weights only
+                if (j < NCOL) {
+                    const int iw = ow0 * SW - p.pad_l + j;
+                    uint2 t = make_uint2(p.pad4, p.pad4);
+                    if (row_ok && (unsigned)iw < (unsigned)p.W) t = *(const uint2*)(xr + (long long)iw * p.C);
+                    v[j] = make_uint2(t.x ^ p.xmask, t.y ^ p.xmask);
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                uint32_t T[NG][4];   // [column group][channel]: bytes = 4 columns
+#pragma unroll
+                for (int gq = 0; gq < NG; ++gq) {
+                    const uint32_t c0w = d ? v[4 * gq].y : v[4 * gq].x;
+                    const uint32_t c1w = d ? v[4 * gq + 1].y : v[4 * gq + 1].x;
+                    const uint32_t c2w = d ? v[4 * gq + 2].y : v[4 * gq + 2].x;
+                    const uint32_t c3w = d ? v[4 * gq + 3].y : v[4 * gq + 3].x;
+                    transpose4x4_bytes(c0w, c1w, c2w, c3w, T[gq]);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int ch = 4 * d + j;
+                    const int w = (int)wd[a][ch];
+#pragma unroll
+                    for (int px = 0; px < 4; ++px) {
+                        const int b0 = px * SW;          // first column of the pixel's window
+                        const int gq = b0 >> 2, sh = b0 & 3;
+                        const uint32_t win = sh == 0 ? T[gq][j] : __builtin_amdgcn_alignbyte(T[gq + 1][j], T[gq][j], sh);
+                        acc[px][ch] = __builtin_amdgcn_sdot4((int)win, w, acc[px][ch], false);
+                    }
+                }
+            }
+        }
+        uint8_t* yrow = p.y + (long long)row * p.oW * p.C + c0;
+#pragma unroll
+        for (int px = 0; px < 4; ++px) {
+            const int ow = ow0 + px;
+            if (ow >= p.oW) break;
+            uint32_t ob[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const float t = __builtin_fmaf((float)acc[px][c], cs[c], bf[c]);
+                float u = t * p.inv_y;
+                u = __builtin_amdgcn_fmed3f(u, lo_f, hi_f);
+                ob[c] = (uint32_t)__float_as_int(u + magic) + zp_add;
+            }
+            uint32_t w2[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const uint32_t ab = __builtin_amdgcn_perm(ob[4 * q + 1], ob[4 * q], 0x0c0c0400u);
+                const uint32_t cd = __builtin_amdgcn_perm(ob[4 * q + 3], ob[4 * q + 2], 0x0c0c0400u);
+                w2[q] = __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+            }
+            *(uint2*)(yrow + (long long)ow * p.C) = make_uint2(w2[0], w2[1]);
+        }
+    }
+}
+
+hipError_t launch_depthwise3x3(const uint8_t* x, const uint32_t* wrow, const int32_t* corr, uint8_t* y,
+                               const float* cs, const float* bf, int N, int C, int H, int W, int oH, int oW,
+                               int stride, int pad_t, int pad_l, int x_zp, int a_xor, float inv_y, int y_zp,
+                               int L, int hi, hipStream_t s) {
+    if (C % 8 || C > 8 * 256 || (stride != 1 && stride != 2) || N <= 0 || oH <= 0 || oW <= 0)
+        return hipErrorInvalidValue;
+    if ((((uintptr_t)x) | ((uintptr_t)y)) & 7) return hipErrorInvalidValue;
+    Dw3Args a{};
+    a.x = x; a.wrow = wrow; a.corr = corr; a.cs = cs; a.bf = bf; a.y = y;
+    a.N = N; a.C = C; a.H = H; a.W = W; a.oH = oH; a.oW = oW; a.pad_t = pad_t; a.pad_l = pad_l;
+    a.pad4 = (uint32_t)(x_zp & 0xff) * 0x01010101u;
+    a.xmask = (uint32_t)(a_xor & 0xff) * 0x01010101u;
+    a.inv_y = inv_y; a.y_zp = y_zp; a.L = L; a.hi = hi;
+    a.c8 = C / 8;
+    a.groups_per_block = 256 / a.c8;
+    a.owbs = (uint32_t)((oW + 3) / 4);
+    const long long groups = (long long)N * oH * a.owbs;
+    if (groups >= (1LL << 31)) return hipErrorInvalidValue;
+    a.n_groups = (uint32_t)groups;
+    fast_div_consts(a.owbs, &a.owb_mul, &a.owb_shift);
+    long long blocks = (groups + a.groups_per_block - 1) / a.groups_per_block;
+    if (blocks > 8192) blocks = 8192;
+    if (stride == 1) hipLaunchKernelGGL(dw3x3_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(dw3x3_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_depthwise16(const uint8_t* x, const uint32_t* wdot, const int32_t* corr,
                               uint8_t* y, const float* cs, const float* bf, int N, int C, int H,
                               int W, int oH, int oW, int kH, int kW, int sH, int sW, int dH, int dW,

@@ -181,6 +181,19 @@ CONV_CASES = [
     ("dw16_c960_s2", 1, 960, 7, 8, 960, 3, dict(group=960, stride=(2, 2), pads=(1, 1, 1, 1),
                                                 y_nhwc=1, x_nhwc=1)),
     ("dw_k5_valu", 1, 32, 9, 9, 32, 5, dict(group=32, pads=(2, 2, 2, 2), y_nhwc=1, x_nhwc=1)),
+    # 3x3 depthwise, one dot4 per filter row over 4 pixels' shared columns:
+    # ragged last pixel group, asymmetric pads, x_zp != 0, int8 activations,
+    # one / many 8-channel chunks, even and odd widths at stride 2
+    ("dw3_s1_tail_zp", 2, 16, 7, 13, 16, 3, dict(group=16, pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1,
+                                                  x_zp=37, y_zp=3, post_fn=1)),
+    ("dw3_s2_even_asym", 1, 144, 16, 16, 144, 3, dict(group=144, stride=(2, 2), pads=(0, 0, 1, 1),
+                                                       y_nhwc=1, x_nhwc=1, y_zp=11)),
+    ("dw3_s2_odd_w", 3, 32, 13, 17, 32, 3, dict(group=32, stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1,
+                                                 x_nhwc=1, x_zp=200)),
+    ("dw3_s1_int8", 1, 48, 9, 10, 48, 3, dict(group=48, pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1,
+                                               act_dtype=np.int8, x_zp=-5, y_zp=-2)),
+    ("dw3_s1_c960_wide", 1, 960, 5, 29, 960, 3, dict(group=960, pads=(1, 1, 1, 1), y_nhwc=1,
+                                                      x_nhwc=1)),
     # channel counts off the 16-byte grid run on an x_zp-padded copy
     ("cpad_c8_3x3", 2, 8, 10, 11, 40, 3, dict(pads=(1, 1, 1, 1), x_nhwc=1, y_nhwc=1, y_zp=9)),
     ("cpad_c24_wzp", 1, 24, 7, 9, 32, 1, dict(x_nhwc=1, y_nhwc=1, w_zp=(5,), y_zp=2)),
