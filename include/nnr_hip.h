@@ -204,6 +204,20 @@ int nnrh_qmatmul_fuse_gelu(nnrh_qmatmul_t h);
  * pass over y (DynamicQuantizeLinear.cpp:37-41).                          */
 int nnrh_qmatmul_minmax_count(nnrh_qmatmul_t h, int batch, int* count);
 int nnrh_qmatmul_set_minmax_out(nnrh_qmatmul_t h, float* parts_dev, int capacity);
+/* 2..4 QLinearMatMuls, each with nnrh_qmatmul_fuse_dq_bias (no Gelu, no
+ * min/max output), identical in shape and types and reading the same A (a
+ * transformer layer's Q, K and V projections), run as one launch: the
+ * members' weights, column sums and biases are copied side by side at
+ * create (the member handles stay valid and unchanged). group_run takes A
+ * as `rows` x k uint8 / int8 rows and writes member i's float32 result to
+ * ys[i] (rows x n), each equal to nnrh_qmatmul_run of that member over the
+ * same rows. No counterpart in the reference (each QLinearMatMul runs alone,
+ * QLinearMatMul.cpp:155-227); it fills the GPU with 3x the tiles.          */
+typedef struct nnrh_qmatmul_group* nnrh_qmatmul_group_t;
+int nnrh_qmatmul_group_create(nnrh_qmatmul_group_t* h, const nnrh_qmatmul_t* members, int n);
+int nnrh_qmatmul_group_run(nnrh_qmatmul_group_t h, const void* a_dev, int rows, void* const* y_devs,
+                           const float* a_scale_dev, const void* a_zp_dev, void* stream);
+int nnrh_qmatmul_group_destroy(nnrh_qmatmul_group_t h);
 int nnrh_qmatmul_destroy(nnrh_qmatmul_t h);
 
 /* ---- MatMulInteger ------------------------------------------------------

@@ -215,6 +215,33 @@ class QLinearMatMul:
             pass
 
 
+class QLinearMatMulGroup:
+    """2..4 fused-dequantize QLinearMatMuls reading the same A, one launch."""
+
+    def __init__(self, members):
+        self._members = list(members)   # keep the member handles alive
+        arr = (ct.c_void_p * len(members))(*[m.h.value for m in members])
+        h = ct.c_void_p()
+        check(lib().nnrh_qmatmul_group_create(ct.byref(h), arr, len(members)))
+        self.h = h
+        self.n = members[0].n
+
+    def __call__(self, a, ys, a_scale_dev=None, a_zp_dev=None, stream=None):
+        rows = a.numel() // a.shape[-1]
+        arr = (ct.c_void_p * len(ys))(*[y.data_ptr() for y in ys])
+        check(lib().nnrh_qmatmul_group_run(self.h, ptr(a), rows, arr, ptr(a_scale_dev), ptr(a_zp_dev),
+                                           cur_stream() if stream is None else stream))
+        return ys
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None):
+                lib().nnrh_qmatmul_group_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
 class MatMulInteger:
     def __init__(self, m, n, k, a_dtype=np.uint8, b_dtype=np.int8, max_batch=1):
         h = ct.c_void_p()

@@ -30,6 +30,7 @@ EXPORTS = [
     "nnrh_multihead_attention_workspace", "nnrh_multihead_attention_f32", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
     "nnrh_qmatmul_fuse_dq_bias", "nnrh_qmatmul_fuse_gelu", "nnrh_qmatmul_minmax_count",
     "nnrh_qmatmul_set_minmax_out", "nnrh_dynamic_quantize_linear_parts", "nnrh_add_layernorm_f32",
+    "nnrh_qmatmul_group_create", "nnrh_qmatmul_group_run", "nnrh_qmatmul_group_destroy",
     "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
     "nnrh_dynamic_quantize_linear", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
@@ -126,6 +127,9 @@ def lib():
         "nnrh_qmatmul_fuse_gelu": (i, [vp]),
         "nnrh_qmatmul_minmax_count": (i, [vp, i, P(i)]),
         "nnrh_qmatmul_set_minmax_out": (i, [vp, vp, i]),
+        "nnrh_qmatmul_group_create": (i, [P(vp), P(vp), i]),
+        "nnrh_qmatmul_group_run": (i, [vp, vp, i, P(vp), vp, vp, vp]),
+        "nnrh_qmatmul_group_destroy": (i, [vp]),
         "nnrh_dynamic_quantize_linear_parts": (i, [vp, sz, vp, i, vp, vp, vp, vp]),
         "nnrh_add_layernorm_f32": (i, [vp, vp, vp, vp, vp, sz, i, f, vp, vp]),
         "nnrh_matmul_integer_create": (i, [P(vp), i, i, i, i, i, i]),

@@ -1032,6 +1032,111 @@ extern "C" int nnrh_qmatmul_fuse_dq_bias(nnrh_qmatmul_t h, float dq_scale, int d
     return NNRH_OK;
 }
 
+// ---------------------------------------------------------------------------
+// QLinearMatMuls with fused dequantize + bias that read the same A (a
+// transformer layer's Q / K / V projections) as one launch: member z is the
+// GEMM's batch index, with B, colsum / c0 and the bias concatenated [z][..].
+struct nnrh_qmatmul_group {
+    int n = 0;
+    GemmArgs g{};
+    nnrh_qmatmul_desc d{};
+    int8_t* wpack = nullptr;
+    int32_t* colsum = nullptr;
+    int32_t* c0 = nullptr;
+    float* dq_bias = nullptr;
+    ~nnrh_qmatmul_group() { dfree(wpack); dfree(colsum); dfree(c0); dfree(dq_bias); }
+};
+
+extern "C" int nnrh_qmatmul_group_create(nnrh_qmatmul_group_t* out, const nnrh_qmatmul_t* hs, int n) {
+    if (!out || !hs) return set_err(NNRH_ERR_INVALID, "qmatmul_group_create: NULL argument");
+    *out = nullptr;
+    if (n < 2 || n > 4) return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_group_create: %d members (2..4)", n);
+    const nnrh_qmatmul* h0 = hs[0];
+    if (!h0) return set_err(NNRH_ERR_INVALID, "qmatmul_group_create: NULL member");
+    for (int i = 0; i < n; ++i) {
+        const nnrh_qmatmul* h = hs[i];
+        if (!h) return set_err(NNRH_ERR_INVALID, "qmatmul_group_create: NULL member");
+        const GemmArgs& g = h->g;
+        const bool same = h->d.m == h0->d.m && h->d.n == h0->d.n && h->d.k == h0->d.k &&
+                          h->d.a_dtype == h0->d.a_dtype && h->d.b_dtype == h0->d.b_dtype &&
+                          h->d.y_dtype == NNRH_U8 && h->d.scale_dtype == NNRH_F32 &&
+                          g.Np == h0->g.Np && g.Kp == h0->g.Kp && g.alpha == h0->g.alpha &&
+                          g.a_xor == h0->g.a_xor && g.beta == 0 && g.dq_bias && !g.dq_gelu && !g.mm_parts;
+        if (!same)
+            return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_group_create: member %d differs in shape, types, "
+                                                 "A quantization or fusions", i);
+    }
+    nnrh_qmatmul_group* G = new (std::nothrow) nnrh_qmatmul_group();
+    if (!G) return set_err(NNRH_ERR_NOMEM, "qmatmul_group_create: host allocation");
+    auto fail = [&](int code) { delete G; return code; };
+    const int Np = h0->g.Np, Kp = h0->g.Kp;
+    const size_t wsz = (size_t)Np * Kp;
+    int rc;
+    if ((rc = nnrh_malloc((void**)&G->wpack, wsz * n))) return fail(rc);
+    if ((rc = nnrh_malloc((void**)&G->colsum, sizeof(int32_t) * Np * n))) return fail(rc);
+    if ((rc = nnrh_malloc((void**)&G->c0, sizeof(int32_t) * Np * n))) return fail(rc);
+    if ((rc = nnrh_malloc((void**)&G->dq_bias, sizeof(float) * Np * n))) return fail(rc);
+    GemmArgs& g = G->g;
+    g = h0->g;
+    g.c0_absmax = 0;
+    for (int i = 0; i < n; ++i) {
+        const nnrh_qmatmul* h = hs[i];
+        if (hipMemcpy(G->wpack + wsz * i, h->wpack, wsz, hipMemcpyDeviceToDevice) != hipSuccess ||
+            hipMemcpy(G->colsum + (size_t)Np * i, h->colsum, sizeof(int32_t) * Np, hipMemcpyDeviceToDevice) !=
+                hipSuccess ||
+            hipMemcpy(G->c0 + (size_t)Np * i, h->c0, sizeof(int32_t) * Np, hipMemcpyDeviceToDevice) != hipSuccess ||
+            hipMemcpy(G->dq_bias + (size_t)Np * i, h->dq_bias, sizeof(float) * Np, hipMemcpyDeviceToDevice) !=
+                hipSuccess)
+            return fail(set_err(NNRH_ERR_HIP, "qmatmul_group_create: device copy failed"));
+        g.c0_absmax = std::max(g.c0_absmax, h->g.c0_absmax);
+        g.grp_cm[i] = h->g.cm;
+        g.grp_cm_b[i] = h->g.cm_b;
+        g.grp_cm_y[i] = h->g.cm_y;
+        g.grp_dq_scale[i] = h->g.dq_scale;
+        g.grp_y_zp[i] = h->g.y_zp;
+    }
+    g.ngrp = n;
+    g.b = G->wpack;
+    g.b_bstride = (long long)wsz;
+    g.colsum = G->colsum;
+    g.c0 = G->c0;
+    g.dq_bias = G->dq_bias;
+    g.param_bstride = Np;
+    g.a_bstride = 0;
+    G->n = n;
+    G->d = h0->d;
+    *out = G;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qmatmul_group_run(nnrh_qmatmul_group_t G, const void* a, int rows, void* const* ys,
+                                      const float* a_scale_dev, const void* a_zp_dev, void* stream) {
+    if (!G || !a || !ys || rows <= 0) return set_err(NNRH_ERR_INVALID, "qmatmul_group_run: bad arguments");
+    for (int i = 0; i < G->n; ++i)
+        if (!ys[i]) return set_err(NNRH_ERR_INVALID, "qmatmul_group_run: NULL output %d", i);
+    hipStream_t s = S(stream);
+    GemmArgs g = G->g;
+    g.a = (const uint8_t*)a;
+    g.M = rows;
+    g.y = ys[0];
+    g.ldy = G->d.n;
+    for (int i = 0; i < G->n; ++i) g.grp_y[i] = ys[i];
+    g.alpha_zp_dev = a_zp_dev;
+    g.cm_a_scale_dev = a_scale_dev;
+    if (a_zp_dev) g.c0 = nullptr;   // the column term needs the zero point of this call
+    const int vec = pick_vec(g.K, (int)g.lda, (uintptr_t)a);
+    if (vec != 16 || !qgemm_dma_eligible(g, vec))
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_group_run: A must be 16-byte aligned with K %% 16 == 0");
+    ProfScope ps("qgemm", s);
+    HIP_TRY(launch_qgemm(g, G->n, pick_tile(g.N), vec, s), "qgemm_group");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qmatmul_group_destroy(nnrh_qmatmul_group_t G) {
+    delete G;
+    return NNRH_OK;
+}
+
 extern "C" int nnrh_qmatmul_fuse_gelu(nnrh_qmatmul_t h) {
     if (!h) return set_err(NNRH_ERR_INVALID, "qmatmul_fuse_gelu: NULL handle");
     if (!h->g.dq_bias) return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_fuse_gelu: needs nnrh_qmatmul_fuse_dq_bias first");

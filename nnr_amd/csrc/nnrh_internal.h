@@ -116,6 +116,14 @@ struct GemmArgs {
     // fused dequantize: (min, max) of each (tile, wave)'s outputs, pair
     // 4 * tile + wave, for a DynamicQuantizeLinear that reads y (NULL: none)
     float* mm_parts;
+    // grouped fused-dequantize launch (QLinearMatMuls sharing A): batch index
+    // z is the member, with its own combined scale, zero point, dequantize
+    // scale and output; B and the per-column arrays advance by b_bstride /
+    // param_bstride, A is shared (a_bstride 0). ngrp = 0: not grouped
+    int ngrp;
+    float grp_cm[4], grp_cm_b[4], grp_cm_y[4], grp_dq_scale[4];
+    int grp_y_zp[4];
+    void* grp_y[4];
     const uint8_t* add_other;   // NULL: no fused add
     int add_conv_is_a;
     float add_sa, add_sb, add_fixed;

@@ -191,8 +191,9 @@ void qgemm_dma_kernel(GemmArgs g) {
     const uint32_t neg_alpha = 0u - (uint32_t)alpha;
     // RQ-D combined scale, fl(fl(a_s * b_s) / y_s), with a device a_scale
     float cm = g.cm;
+    const float a_scale_dev = (EPI == EPI_RQD && g.cm_a_scale_dev) ? *g.cm_a_scale_dev : 0.0f;
     if (EPI == EPI_RQD && g.cm_a_scale_dev) {
-        const float t1 = *g.cm_a_scale_dev * g.cm_b;
+        const float t1 = a_scale_dev * g.cm_b;
         cm = t1 / g.cm_y;
     }
     // uint8 output whose clamp is exactly the [0, 255] saturation of
@@ -416,6 +417,17 @@ void qgemm_dma_kernel(GemmArgs g) {
         const int nl = wn * 64 + 16 * fchunk;   // first column of this lane in the tile
         const int nb = n0 + nl;
         if (nb >= g.N) return;
+        // a grouped launch: member z's combined scale, zero point, output
+        float cm_t = cm;
+        int yzp_t = g.y_zp;
+        if (FUSE == FUSE_DQB && g.ngrp) {
+            cm_t = g.grp_cm[z];
+            if (g.cm_a_scale_dev) {
+                const float t1 = a_scale_dev * g.grp_cm_b[z];
+                cm_t = t1 / g.grp_cm_y[z];
+            }
+            yzp_t = g.grp_y_zp[z];
+        }
         // the accumulators started at c0 (acc + c0 = the reference's value)
         const uint8_t* ps = lds + S * STAGE + c_pslot;
         v4i p0[4], p1[4];
@@ -486,13 +498,13 @@ void qgemm_dma_kernel(GemmArgs g) {
                 } else if (EPI == EPI_RQD && sat_u8) {
                     // RQ-D into uint8: sat(rne(acc*cm + zp)); a value >= 2^31
                     // (or NaN) converts to INT32_MIN on x86 and clamps to 0
-                    const float zp_f = (float)g.y_zp;
+                    const float zp_f = (float)yzp_t;
 #pragma unroll
                     for (int tn = 0; tn < 4; ++tn) {
                         uint32_t w = 0;
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
-                            const float t = (float)acc[tm][tn][q] * cm;
+                            const float t = (float)acc[tm][tn][q] * cm_t;
                             float val = t + zp_f;
                             val = val < 2147483648.0f ? val : -1.0f;
                             w = __builtin_amdgcn_cvt_pk_u8_f32(val, q, w);
@@ -530,7 +542,7 @@ void qgemm_dma_kernel(GemmArgs g) {
                                 b = rqc_fast(v, __int_as_float(p0[tn][q]), __int_as_float(p1[tn][q]),
                                              g.inv_y, g.y_zp, g.L, g.hi);
                             else
-                                b = rqd_fast(v, cm, g.y_zp, g.lo, g.hi);
+                                b = rqd_fast(v, cm_t, yzp_t, g.lo, g.hi);
                             w |= (b & 0xffu) << (8 * q);
                         }
                         packed[tn] = w;
@@ -583,15 +595,17 @@ void qgemm_dma_kernel(GemmArgs g) {
                 if constexpr (FUSE == FUSE_DQB) {
                     // DequantizeLinear fl((q - zp) * s) (DequantizeLinear.cpp:133-152),
                     // then the fp32 Add of the column bias, written as fp32
-                    const float zp_f = (float)g.y_zp;
+                    const float zp_f = (float)yzp_t;
+                    const float dqs = g.ngrp ? g.grp_dq_scale[z] : g.dq_scale;
                     const uint8_t* pb = ps + NP * BN * 4 + nl * 4;
-                    float* frow = (float*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
+                    float* frow = (g.ngrp ? (float*)g.grp_y[z] : (float*)g.y + (long long)z * g.y_bstride) +
+                                  (long long)m * g.ldy + nb;
                     float o[16];
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         // uint8 output (checked on the host)
                         const float qf = (float)((packed[i >> 2] >> (8 * (i & 3))) & 0xffu);
-                        const float d = (qf - zp_f) * g.dq_scale;
+                        const float d = (qf - zp_f) * dqs;
                         o[i] = d + *(const float*)(pb + 4 * i);
                     }
                     if (g.dq_gelu) {

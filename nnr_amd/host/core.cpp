@@ -373,6 +373,7 @@ bool context_t::prepare() {
         fuse_quant_prefix(this);
         fuse_add_layernorm(this);
         fuse_dynq_minmax(this);
+        fuse_matmul_group(this);
     }
     // 6. device memory and constant upload
     if (!plan_memory()) return false;

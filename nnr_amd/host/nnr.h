@@ -145,6 +145,13 @@ struct operator_t {
     int minmax_count = 0;
     // DynamicQuantizeLinear: the producer that writes its input's min / max
     operator_t* minmax_src = nullptr;
+    // operators of one kind reading the same input, run as one launch
+    // (fuse_matmul_group): the leader launches for all of group_members; a
+    // member's exec does nothing (its output is written by the leader, which
+    // runs first)
+    virtual bool fuse_group(const std::vector<operator_t*>& /*members*/) { return false; }
+    operator_t* group_leader = nullptr;
+    std::vector<operator_t*> group_members;
 
     // attribute accessors
     const attr_t* find_attr(const std::string& name) const;
@@ -235,6 +242,7 @@ void fuse_conv_add(context_t* ctx);
 void fuse_matmul_dq_bias(context_t* ctx);
 void fuse_quant_prefix(context_t* ctx);
 void fuse_add_layernorm(context_t* ctx);
+void fuse_matmul_group(context_t* ctx);
 void fuse_dynq_minmax(context_t* ctx);
 void fuse_attention(context_t* ctx);
 

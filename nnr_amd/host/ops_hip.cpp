@@ -318,8 +318,12 @@ struct QLinearConv_hip : operator_t {
 // QLinearMatMul (src/backend/cpu/QLinearMatMul.cpp), constant B
 struct QLinearMatMul_hip : operator_t {
     nnrh_qmatmul_t h = nullptr;
+    nnrh_qmatmul_group_t grp = nullptr;   // leader of a grouped launch
     int m = 0, n = 0, k = 0, batch = 1;
-    ~QLinearMatMul_hip() override { nnrh_qmatmul_destroy(h); }
+    ~QLinearMatMul_hip() override {
+        nnrh_qmatmul_group_destroy(grp);
+        nnrh_qmatmul_destroy(h);
+    }
     bool init() override {
         layout_mask = LAYOUT_NCHW;
         return inputs.size() == 8 && outputs.size() == 1;
@@ -385,13 +389,38 @@ struct QLinearMatMul_hip : operator_t {
     bool set_minmax_out(float* parts, int pairs) override {
         return nnrh_qmatmul_set_minmax_out(h, parts, pairs) == NNRH_OK;
     }
+    bool fuse_group(const std::vector<operator_t*>& members) override {
+        if (!h || fused_chain.size() != 2) return false;
+        std::vector<nnrh_qmatmul_t> hs{h};
+        for (auto* op : members) {
+            auto* o = dynamic_cast<QLinearMatMul_hip*>(op);
+            if (!o || !o->h || o->fused_chain.size() != 2 || o->m != m || o->n != n || o->k != k ||
+                o->batch != batch)
+                return false;
+            hs.push_back(o->h);
+        }
+        return nnrh_qmatmul_group_create(&grp, hs.data(), (int)hs.size()) == NNRH_OK;
+    }
     std::string variant() const override {
         if (fused_chain.empty()) return "";
-        return fused_chain.size() > 2 ? "+DQ+Bias+Gelu" : "+DQ+Bias";
+        std::string v = fused_chain.size() > 2 ? "+DQ+Bias+Gelu" : "+DQ+Bias";
+        if (grp) v += "+Group" + std::to_string(group_members.size() + 1);
+        else if (group_leader) v += "(grouped)";
+        return v;
     }
     bool exec() override {
+        if (group_leader && group_leader != this) return true;   // written by the leader's launch
         const float* a_s_dev = inputs[1]->has_host() ? nullptr : (const float*)inputs[1]->data;
         const void* a_z_dev = inputs[2]->has_host() ? nullptr : inputs[2]->data;
+        if (grp) {
+            std::vector<void*> ys{outputs[0]->data};
+            for (auto* op : group_members) ys.push_back(op->outputs[0]->data);
+            return ok(this, nnrh_qmatmul_group_run(grp, inputs[0]->data, batch * m, ys.data(), a_s_dev, a_z_dev,
+                                                   ctx->stream));
+        }
+        return exec_single(a_s_dev, a_z_dev);
+    }
+    bool exec_single(const float* a_s_dev, const void* a_z_dev) {
         return ok(this, nnrh_qmatmul_run(h, inputs[0]->data, batch > 1 ? (long long)m * k : 0,
                                          outputs[0]->data, batch, a_s_dev, a_z_dev, ctx->stream));
     }

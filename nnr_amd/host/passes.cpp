@@ -25,6 +25,8 @@
 //                     LayerNormalization is formed inside the normalization
 //   fuse_dynq_minmax  no counterpart: the producer of a DynamicQuantizeLinear
 //                     input writes its min / max pairs as it stores it
+//   fuse_matmul_group no counterpart: fused-dequantize QLinearMatMuls reading
+//                     the same input run as one launch
 // The fused operators are created through the registry with the context's
 // preferred backend, exactly where the reference calls solve_operator.
 #include <cstdio>
@@ -601,6 +603,43 @@ void fuse_quant_prefix(context_t* ctx) {
     }
     ctx->fusion_stats["quantize_first_conv"] = nq;
     ctx->fusion_stats["dequantize_gap"] = ndq;
+}
+
+// ---------------------------------------------------------------------------
+// QLinearMatMuls with a fused dequantize + bias that read the same input with
+// the same quantization (a transformer layer's Q, K and V projections): up
+// to 4 run as one launch, issued by the first in graph order. The others stay
+// in the plan (their outputs and chains unchanged) and do nothing at exec.
+void fuse_matmul_group(context_t* ctx) {
+    int groups = 0;
+    std::unordered_set<operator_t*> taken;
+    auto& nodes = ctx->nodes;
+    for (size_t i = 0; i < nodes.size(); ++i) {
+        operator_t* lead = nodes[i];
+        if (!active(lead) || lead->op_type != "QLinearMatMul" || lead->fused_chain.size() != 2 ||
+            taken.count(lead))
+            continue;
+        std::vector<operator_t*> members;
+        for (size_t j = i + 1; j < nodes.size() && members.size() < 3; ++j) {
+            operator_t* op = nodes[j];
+            if (!active(op) || op->op_type != "QLinearMatMul" || op->fused_chain.size() != 2 || taken.count(op))
+                continue;
+            if (op->inputs[0] != lead->inputs[0] || op->inputs[1] != lead->inputs[1] ||
+                op->inputs[2] != lead->inputs[2])
+                continue;
+            members.push_back(op);
+        }
+        if (members.empty() || !lead->fuse_group(members)) continue;
+        lead->group_leader = lead;
+        lead->group_members = members;
+        taken.insert(lead);
+        for (auto* op : members) {
+            op->group_leader = lead;
+            taken.insert(op);
+        }
+        ++groups;
+    }
+    ctx->fusion_stats["matmul_group"] = groups;
 }
 
 // ---------------------------------------------------------------------------

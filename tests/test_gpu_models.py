@@ -180,4 +180,7 @@ def test_bert_per_node(dev, fused):
     assert [p["variant"] for p in plan if p["op"] == "LayerNormalization"] == ["+Add"] * 4
     assert "Add" not in ops
     assert sum(p["variant"] == "MinMaxIn" for p in plan if p["op"] == "DynamicQuantizeLinear") == 5
+    # each layer's Q / K / V projections run as one grouped launch
+    assert sum(p["variant"].endswith("+Group3") for p in chains) == 2
+    assert sum(p["variant"].endswith("(grouped)") for p in chains) == 4
     assert n_int >= 8 * 2 and n_f32 >= 12

@@ -444,6 +444,47 @@ def test_qmatmul_fused_gelu_minmax(dev, m, n, batch):
     op.set_minmax_out(None)
 
 
+@pytest.mark.parametrize("rows,n,device_q", [(8192 // 64, 768, True), (200, 136, True), (77, 64, False)])
+def test_qmatmul_group(dev, rows, n, device_q):
+    """Three fused-dequantize QLinearMatMuls reading the same A (different
+    weights, scales, zero points, biases) as one grouped launch: every
+    member's fp32 output equals its own launch bit for bit, with the
+    activation quantization on the device (after DynamicQuantizeLinear) or
+    on the host."""
+    import torch
+    rng = np.random.default_rng(rows + n)
+    k = 96
+    a = rng.integers(0, 256, (rows, k), dtype=np.uint8)
+    a_s, a_z = np.float32(0.0173), 119
+    members = []
+    for i in range(3):
+        b = rng.integers(-127, 128, (k, n), dtype=np.int8)
+        bias = rng.standard_normal(n).astype(np.float32)
+        ys, yz = [0.031, 0.047, 0.022][i], [121, 90, 140][i]
+        if device_q:
+            op = H.QLinearMatMul(b, 1.0, 0, [0.004, 0.0031, 0.0057][i], 0, ys, yz, m=rows)
+        else:
+            op = H.QLinearMatMul(b, a_s, a_z, [0.004, 0.0031, 0.0057][i], 0, ys, yz, m=rows)
+        op.fuse_dq_bias(ys, yz, bias)
+        members.append(op)
+    ad = to_dev(a, dev)
+    sd = torch.tensor([a_s], dtype=torch.float32, device=dev) if device_q else None
+    zd = torch.tensor([a_z], dtype=torch.uint8, device=dev) if device_q else None
+    refs = [to_np(op(ad, a_scale_dev=sd, a_zp_dev=zd)) for op in members]
+    grp = H.QLinearMatMulGroup(members)
+    for _ in range(2):
+        ys = [torch.full((rows, n), float("nan"), dtype=torch.float32, device=dev) for _ in members]
+        grp(ad, ys, a_scale_dev=sd, a_zp_dev=zd)
+        for i, (y, ref) in enumerate(zip(ys, refs)):
+            got = to_np(y)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (i, np.count_nonzero(got != ref))
+    # members that differ in shape are refused
+    other = H.QLinearMatMul(rng.integers(-127, 128, (k, n + 64), dtype=np.int8), 1.0, 0, 0.004, 0, 0.03, 0, m=rows)
+    other.fuse_dq_bias(0.03, 0, None)
+    with pytest.raises(H.NnrHipError):
+        H.QLinearMatMulGroup([members[0], other])
+
+
 @pytest.mark.parametrize("rows,D,res,beta", [(37, 768, True, True), (9, 2048, True, False),
                                              (5, 102, True, True), (3, 3000, False, True),
                                              (130, 768, False, False)])
