@@ -424,7 +424,11 @@ struct QLinearMatMul_hip : operator_t {
         return ok(this, nnrh_qmatmul_run(h, inputs[0]->data, batch > 1 ? (long long)m * k : 0,
                                          outputs[0]->data, batch, a_s_dev, a_z_dev, ctx->stream));
     }
-    double num_ops() const override { return 2.0 * batch * m * (double)n * k; }
+    // a grouped launch's work is counted on its leader (members run nothing)
+    double num_ops() const override {
+        if (group_leader && group_leader != this) return 0.0;
+        return 2.0 * batch * m * (double)n * k * (double)(grp ? group_members.size() + 1 : 1);
+    }
 };
 
 // MatMulInteger (src/backend/cpu/MatMulInteger.cpp)
