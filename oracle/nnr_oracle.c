@@ -683,6 +683,193 @@ void orc_qlinear_add(int kind, const void* a, const void* b, void* y, size_t n,
 }
 
 /* ---- MaxPool uint8 NHWC: src/backend/x64/pool_x64.h:396-436 ------------ */
+/* ---- the rest of the QLinear family (QOperator models) ----------------- */
+
+/* QLinearGlobalAveragePool_operator::exec_typed (QLinearGlobalAveragePool.cpp:28-60),
+ * RQ-F: rs = fl(x_s / fl(y_s * float(spatial))); per (n, c) the int32 sum of
+ * the raw values minus (int32)(x_zp * spatial), then nearbyint(fl(sum * rs))
+ * + y_zp and the clamp. x is NCHW, or NHWC with x_nhwc (the same sums). */
+void orc_qlinear_global_avgpool(const void* x, void* y, int N, int C, int spatial, int x_nhwc, int dt,
+                                float x_s, int x_zp, float y_s, int y_zp) {
+    int lo, hi; dtype_range(dt, &lo, &hi);
+    const float rs = x_s / (y_s * (float)spatial);                       /* :46 */
+    for (int n = 0; n < N; n++)
+        for (int c = 0; c < C; c++) {
+            uint32_t sum = 0;                                               /* :52-54 */
+            for (int s = 0; s < spatial; s++) {
+                size_t i = x_nhwc ? ((size_t)n * spatial + s) * C + c : ((size_t)n * C + c) * spatial + s;
+                sum += (uint32_t)ld_q(x, dt, i);
+            }
+            sum -= (uint32_t)x_zp * (uint32_t)spatial;                      /* :55 */
+            int32_t q = x86_f2i(nearbyintf((float)(int32_t)sum * rs));      /* :56 */
+            q = (int32_t)((uint32_t)q + (uint32_t)y_zp);
+            st_q(y, dt, (size_t)n * C + c, clampi(q, lo, hi));              /* :57 */
+        }
+}
+
+/* QLinearAveragePool_operator::exec_typed (QLinearAveragePool.cpp:67-115): 2-D,
+ * count_include_pad never set (:41-42), so the count is the in-image taps;
+ * avg = fl(fl(float(sum) * x_s) / float(count)), q = nearbyint(fl(avg / y_s))
+ * + y_zp, clamp. x / y NCHW, or NHWC with nhwc. */
+void orc_qlinear_avgpool(const void* x, void* y, int N, int C, int iH, int iW, int oH, int oW,
+                         int kH, int kW, int sH, int sW, int pH, int pW, int nhwc, int dt,
+                         float x_s, int x_zp, float y_s, int y_zp) {
+    int lo, hi; dtype_range(dt, &lo, &hi);
+    for (int n = 0; n < N; n++)
+        for (int c = 0; c < C; c++)
+            for (int oh = 0; oh < oH; oh++)
+                for (int ow = 0; ow < oW; ow++) {
+                    int32_t sum = 0;
+                    int count = 0;
+                    for (int kh = 0; kh < kH; kh++) {
+                        int ih = oh * sH - pH + kh;
+                        if (ih < 0 || ih >= iH) continue;
+                        for (int kw = 0; kw < kW; kw++) {
+                            int iw = ow * sW - pW + kw;
+                            if (iw < 0 || iw >= iW) continue;
+                            size_t i = nhwc ? (((size_t)n * iH + ih) * iW + iw) * C + c
+                                            : (((size_t)n * C + c) * iH + ih) * iW + iw;
+                            sum += ld_q(x, dt, i) - x_zp;
+                            count++;
+                        }
+                    }
+                    if (count == 0) count = 1;                              /* :104 */
+                    float avg = (float)sum * x_s / (float)count;            /* :105 */
+                    int32_t q = x86_f2i(nearbyintf(avg / y_s));
+                    q = (int32_t)((uint32_t)q + (uint32_t)y_zp);
+                    size_t o = nhwc ? (((size_t)n * oH + oh) * oW + ow) * C + c
+                                    : (((size_t)n * C + c) * oH + oh) * oW + ow;
+                    st_q(y, dt, o, clampi(q, lo, hi));
+                }
+}
+
+/* QLinearConcat_operator (QLinearConcat.cpp:70-104 requantize_chunk, :119-166
+ * NCHW, :170-236 NHWC): y is `outer` rows of the inputs' chunks side by side
+ * (chunk t = count[t] elements). An input with the output's scale and zero
+ * point is copied; otherwise each chunk is requantized with rs = fl(x_s / y_s):
+ * its first count - count % 16 elements (when count >= 16) by the 16-wide
+ * body, q = rne(clamp(fma(rs, fl(x - x_zp), y_zp), lo, hi)), the rest by the
+ * scalar tail, q = clamp(nearbyint(fl(rs * (x - x_zp)) + y_zp)). */
+void orc_qlinear_concat(int ntens, const void* const* xs, const long long* count, long long outer, int dt,
+                        const float* x_s, const int* x_zp, float y_s, int y_zp, void* y) {
+    int lo, hi; dtype_range(dt, &lo, &hi);
+    long long row = 0;
+    for (int t = 0; t < ntens; t++) row += count[t];
+    for (long long o = 0; o < outer; o++) {
+        long long yoff = o * row;
+        for (int t = 0; t < ntens; t++) {
+            const long long cnt = count[t];
+            const size_t src = (size_t)(o * cnt);
+            const int same = x_s[t] == y_s && x_zp[t] == y_zp;           /* :147 */
+            const float rs = same ? 0.f : x_s[t] / y_s;
+            const long long body = cnt >= 16 ? cnt - cnt % 16 : 0;
+            for (long long i = 0; i < cnt; i++) {
+                int32_t xv = ld_q(xs[t], dt, src + (size_t)i);
+                int q;
+                if (same) q = xv;
+                else if (i < body) {                                        /* :84-100 */
+                    float v = fmaf(rs, (float)xv - (float)x_zp[t], (float)y_zp);
+                    v = v > (float)lo ? v : (float)lo;
+                    v = v < (float)hi ? v : (float)hi;
+                    q = (int)rintf(v);
+                } else {                                                    /* :101-104 */
+                    float v = mul_add_expr(rs, (float)(xv - x_zp[t]), (float)y_zp);
+                    q = clampi(x86_f2i(nearbyintf(v)), lo, hi);
+                }
+                st_q(y, dt, (size_t)(yoff + i), q);
+            }
+            yoff += cnt;
+        }
+    }
+}
+
+/* QLinearMul_operator::exec_typed (QLinearMul.cpp:25-231), AVX-512 build:
+ * cs = fl(fl(a_s * b_s) / y_s). kind as QLinearAdd: 0 same shape (16-wide
+ * body v = fma(fl(fl(a - a_zp) * fl(b - b_zp)), cs, y_zp), rne, clamp; the
+ * last n % 16 by the scalar expression fl(fl(cs * A) * B) + y_zp), 1 B scalar,
+ * 2 A scalar (scalar expression with the constant factor fl(cs * (s - zp))),
+ * 3 per channel: a is the full tensor, b the [C] one (the caller swaps
+ * operands and zero points when A is the per-channel one, as :127-131 do);
+ * 16-wide body over channels (NHWC) or over each plane (NCHW). */
+void orc_qlinear_mul(int kind, const void* a, const void* b, void* y, size_t n,
+                     int N, int C, int HW, int y_nhwc, int dt,
+                     float a_s, int a_zp, float b_s, int b_zp, float y_s, int y_zp) {
+    int lo, hi; dtype_range(dt, &lo, &hi);
+    const float cs = a_s * b_s / y_s;                                       /* :39 */
+    const float yz = (float)y_zp;
+    if (kind == ORC_ADD_SAME) {
+        size_t body = n - n % 16;
+        for (size_t i = 0; i < n; i++) {
+            int32_t av = ld_q(a, dt, i), bv = ld_q(b, dt, i);
+            int q;
+            if (i < body) {                                                 /* :54-74 */
+                float va = (float)av - (float)a_zp, vb = (float)bv - (float)b_zp;
+                float v = fmaf(va * vb, cs, yz);
+                v = rintf(v);
+                v = clampf_minmax(v, (float)lo, (float)hi);
+                q = (int)v;
+            } else {                                                        /* :76-79 */
+                float t1 = cs * (float)(av - a_zp);
+                float v = mul_add_expr(t1, (float)(bv - b_zp), yz);
+                q = clampi(x86_f2i(nearbyintf(v)), lo, hi);
+            }
+            st_q(y, dt, i, q);
+        }
+        return;
+    }
+    if (kind == ORC_ADD_B_SCALAR || kind == ORC_ADD_A_SCALAR) {            /* :88-99 */
+        const int b_sc = kind == ORC_ADD_B_SCALAR;
+        const float cval = b_sc ? cs * (float)(ld_q(b, dt, 0) - b_zp) : cs * (float)(ld_q(a, dt, 0) - a_zp);
+        for (size_t i = 0; i < n; i++) {
+            float d = b_sc ? (float)(ld_q(a, dt, i) - a_zp) : (float)(ld_q(b, dt, i) - b_zp);
+            float v = mul_add_expr(cval, d, yz);
+            st_q(y, dt, i, clampi(x86_f2i(nearbyintf(v)), lo, hi));
+        }
+        return;
+    }
+    /* per channel: a full, b [C] */
+    if (y_nhwc) {                                                           /* :138-177 */
+        for (size_t pos = 0; pos < (size_t)N * HW; pos++) {
+            const int cbody = C - C % 16;
+            for (int c = 0; c < C; c++) {
+                const float cv = cs * (float)(ld_q(b, dt, c) - b_zp);
+                const size_t i = pos * C + c;
+                int32_t xv = ld_q(a, dt, i);
+                int q;
+                if (c < cbody) {
+                    float v = fmaf((float)xv - (float)a_zp, cv, yz);
+                    v = rintf(v);
+                    q = (int)clampf_minmax(v, (float)lo, (float)hi);
+                } else {
+                    float v = mul_add_expr(cv, (float)(xv - a_zp), yz);
+                    q = clampi(x86_f2i(nearbyintf(v)), lo, hi);
+                }
+                st_q(y, dt, i, q);
+            }
+        }
+        return;
+    }
+    for (size_t nc = 0; nc < (size_t)N * C; nc++) {                        /* :180-200 */
+        const int c = (int)(nc % (size_t)C);
+        const float bval = cs * (float)(ld_q(b, dt, c) - b_zp);
+        const int body = HW - HW % 16;
+        for (int i = 0; i < HW; i++) {
+            const size_t k = nc * HW + i;
+            int32_t xv = ld_q(a, dt, k);
+            int q;
+            if (i < body) {
+                float v = fmaf((float)xv - (float)a_zp, bval, yz);
+                v = rintf(v);
+                q = (int)clampf_minmax(v, (float)lo, (float)hi);
+            } else {
+                float v = mul_add_expr(bval, (float)(xv - a_zp), yz);
+                q = clampi(x86_f2i(nearbyintf(v)), lo, hi);
+            }
+            st_q(y, dt, k, q);
+        }
+    }
+}
+
 void orc_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH,
                          int iW, int oH, int oW, int kH, int kW, int sH, int sW,
                          int pH, int pW) {

@@ -136,6 +136,17 @@ void orc_qlinear_add(int kind, const void* a, const void* b, void* y, size_t n,
                      float a_s, int a_zp, float b_s, int b_zp, float y_s, int y_zp);
 
 /* ---- MaxPool, uint8 NHWC (x64/pool_x64.h:396-436) ---------------------- */
+/* QLinearGlobalAveragePool / QLinearAveragePool / QLinearConcat / QLinearMul */
+void orc_qlinear_global_avgpool(const void* x, void* y, int N, int C, int spatial, int x_nhwc, int dt,
+                                float x_s, int x_zp, float y_s, int y_zp);
+void orc_qlinear_avgpool(const void* x, void* y, int N, int C, int iH, int iW, int oH, int oW,
+                         int kH, int kW, int sH, int sW, int pH, int pW, int nhwc, int dt,
+                         float x_s, int x_zp, float y_s, int y_zp);
+void orc_qlinear_concat(int ntens, const void* const* xs, const long long* count, long long outer, int dt,
+                        const float* x_s, const int* x_zp, float y_s, int y_zp, void* y);
+void orc_qlinear_mul(int kind, const void* a, const void* b, void* y, size_t n,
+                     int N, int C, int HW, int y_nhwc, int dt,
+                     float a_s, int a_zp, float b_s, int b_zp, float y_s, int y_zp);
 void orc_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH,
                          int iW, int oH, int oW, int kH, int kW, int sH, int sW,
                          int pH, int pW);

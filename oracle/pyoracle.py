@@ -69,6 +69,10 @@ def lib():
             "orc_qlinear_conv_from_acc": (i, [P(ConvParams), vp, vp]),
             "orc_qlinear_add": (None, [i, vp, vp, vp, sz, i, i, i, i, i, f, i, f, i, f, i]),
             "orc_maxpool_u8_nhwc": (None, [vp, vp] + [i] * 12),
+            "orc_qlinear_global_avgpool": (None, [vp, vp, i, i, i, i, i, f, i, f, i]),
+            "orc_qlinear_avgpool": (None, [vp, vp] + [i] * 14 + [f, i, f, i]),
+            "orc_qlinear_concat": (None, [i, P(vp), P(ct.c_longlong), ct.c_longlong, i, P(f), P(i), f, i, vp]),
+            "orc_qlinear_mul": (None, [i, vp, vp, vp, sz, i, i, i, i, i, f, i, f, i, f, i]),
             "orc_nchw_to_nhwc_u8": (None, [vp, vp, i, i, i]),
         }
         for n, (r, a) in sigs.items():
@@ -174,6 +178,55 @@ def qlinear_add(kind, a, b, a_s, a_zp, b_s, b_zp, y_s, y_zp, C=0, HW=0, y_nhwc=0
     y = np.empty(full.shape, a.dtype)
     N = full.size // (C * HW) if C and HW else 0
     lib().orc_qlinear_add(kind, _p(a), _p(b), _p(y), y.size, N, C, HW, y_nhwc, dt_of(a),
+                          float(a_s), int(a_zp), float(b_s), int(b_zp), float(y_s), int(y_zp))
+    return y
+
+
+def qlinear_global_avgpool(x, x_s, x_zp, y_s, y_zp, nhwc=0):
+    """x: [N, C, *spatial] (or [N, *spatial, C] with nhwc); y: [N, C]."""
+    x = np.ascontiguousarray(x)
+    N = x.shape[0]
+    C = x.shape[-1] if nhwc else x.shape[1]
+    sp = x.size // (N * C)
+    y = np.empty((N, C), x.dtype)
+    lib().orc_qlinear_global_avgpool(_p(x), _p(y), N, C, sp, nhwc, dt_of(x), float(x_s), int(x_zp),
+                                     float(y_s), int(y_zp))
+    return y
+
+
+def qlinear_avgpool(x, k, stride, pads, oH, oW, x_s, x_zp, y_s, y_zp, nhwc=0):
+    x = np.ascontiguousarray(x)
+    if nhwc:
+        N, H, W, Cc = x.shape
+        y = np.empty((N, oH, oW, Cc), x.dtype)
+    else:
+        N, Cc, H, W = x.shape
+        y = np.empty((N, Cc, oH, oW), x.dtype)
+    lib().orc_qlinear_avgpool(_p(x), _p(y), N, Cc, H, W, oH, oW, k[0], k[1], stride[0], stride[1],
+                              pads[0], pads[1], nhwc, dt_of(x), float(x_s), int(x_zp), float(y_s), int(y_zp))
+    return y
+
+
+def qlinear_concat(xs, counts, outer, scales, zps, y_s, y_zp):
+    """xs: arrays of outer x counts[t] elements (flattened); y: outer x sum(counts)."""
+    xs = [np.ascontiguousarray(x) for x in xs]
+    n = len(xs)
+    y = np.empty(outer * sum(counts), xs[0].dtype)
+    ptrs = (ct.c_void_p * n)(*[x.ctypes.data for x in xs])
+    cnt = (ct.c_longlong * n)(*counts)
+    sc = (ct.c_float * n)(*scales)
+    zp = (ct.c_int * n)(*zps)
+    lib().orc_qlinear_concat(n, ptrs, cnt, outer, dt_of(xs[0]), sc, zp, float(y_s), int(y_zp), _p(y))
+    return y
+
+
+def qlinear_mul(kind, a, b, a_s, a_zp, b_s, b_zp, y_s, y_zp, C=0, HW=0, y_nhwc=0):
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    full = a if a.size >= b.size else b
+    y = np.empty(full.shape, a.dtype)
+    N = full.size // (C * HW) if C and HW else 0
+    lib().orc_qlinear_mul(kind, _p(a), _p(b), _p(y), y.size, N, C, HW, y_nhwc, dt_of(a),
                           float(a_s), int(a_zp), float(b_s), int(b_zp), float(y_s), int(y_zp))
     return y
 

@@ -293,6 +293,108 @@ def dynq_case(rng):
         x=x, y=y, y_scale=np.array([s], np.float32), y_zp=np.array([zp], np.uint8))
 
 
+def qgap_case(rng):
+    # QLinearGlobalAveragePool.cpp:46 (rs), :52-57 (int sum, zero-point term, RQ-F)
+    N, C, H, W = 2, 5, 3, 4
+    x_s, x_zp, y_s, y_zp = 0.031, 100, 0.017, 3
+    x = rng.integers(0, 256, (N, C, H, W), dtype=np.uint8)
+    sp = H * W
+    rs = div(float(np.float32(x_s)), mul(float(np.float32(y_s)), float(sp)))
+    y = np.zeros((N, C, 1, 1), np.uint8)
+    for n in range(N):
+        for c in range(C):
+            sm = wrap32(int(x[n, c].astype(np.int64).sum()) - x_zp * sp)
+            q = wrap32(x86_int(rne(mul(i2f(sm), rs))) + y_zp)
+            y[n, c, 0, 0] = clamp(q, 0, 255)
+    return "qlinear_global_avgpool", dict(op="QLinearGlobalAveragePool", x_scale=x_s, x_zp=x_zp,
+                                          y_scale=y_s, y_zp=y_zp), dict(x=x, y=y)
+
+
+def qavgpool_case(rng):
+    # QLinearAveragePool.cpp:90-110: in-image taps only, fl(fl(sum * x_s) / count),
+    # nearbyint(fl(avg / y_s)) + y_zp
+    N, C, H, W, k, st, pd = 1, 3, 6, 7, 3, 2, 1
+    x_s, x_zp, y_s, y_zp = 0.02, 128, 0.013, 128
+    x = rng.integers(0, 256, (N, C, H, W), dtype=np.uint8)
+    oH = (H + 2 * pd - k) // st + 1
+    oW = (W + 2 * pd - k) // st + 1
+    y = np.zeros((N, C, oH, oW), np.uint8)
+    for c in range(C):
+        for oh in range(oH):
+            for ow in range(oW):
+                sm, cnt = 0, 0
+                for kh in range(k):
+                    ih = oh * st - pd + kh
+                    if not 0 <= ih < H:
+                        continue
+                    for kw in range(k):
+                        iw = ow * st - pd + kw
+                        if 0 <= iw < W:
+                            sm += int(x[0, c, ih, iw]) - x_zp
+                            cnt += 1
+                avg = div(mul(i2f(sm), float(np.float32(x_s))), float(max(cnt, 1)))
+                q = wrap32(x86_int(rne(div(avg, float(np.float32(y_s))))) + y_zp)
+                y[0, c, oh, ow] = clamp(q, 0, 255)
+    return "qlinear_avgpool", dict(op="QLinearAveragePool", k=k, stride=st, pad=pd, x_scale=x_s,
+                                   x_zp=x_zp, y_scale=y_s, y_zp=y_zp), dict(x=x, y=y)
+
+
+def qconcat_case(rng):
+    # QLinearConcat.cpp:147 (copy when scale and zero point match), :84-104
+    # (16-wide body fma(rs, x - zp, y_zp), clamp, rne; scalar tail)
+    outer = 3
+    counts = [21, 5, 16]
+    scales = [0.05, 0.02, 0.031]
+    zps = [10, 3, 7]
+    y_s, y_zp = 0.031, 7   # the third input is copied
+    xs = [rng.integers(0, 256, (outer, c), dtype=np.uint8) for c in counts]
+    rows = []
+    for o in range(outer):
+        row = []
+        for t, cnt in enumerate(counts):
+            if scales[t] == y_s and zps[t] == y_zp:
+                row += [int(v) for v in xs[t][o]]
+                continue
+            rs = div(float(np.float32(scales[t])), float(np.float32(y_s)))
+            body = cnt - cnt % 16 if cnt >= 16 else 0
+            for i in range(cnt):
+                xv = int(xs[t][o, i])
+                if i < body:
+                    v = fma(rs, float(xv - zps[t]), float(y_zp))
+                    v = min(max(v, 0.0), 255.0)
+                    row.append(rne(v))
+                else:
+                    v = add(mul(rs, i2f(xv - zps[t])), float(y_zp))
+                    row.append(clamp(x86_int(rne(v)), 0, 255))
+        rows.append(row)
+    y = np.array(rows, np.uint8)
+    arrays = {f"x{t}": xs[t] for t in range(len(xs))}
+    arrays["y"] = y
+    return "qlinear_concat", dict(op="QLinearConcat", scales=scales, zps=zps, y_scale=y_s,
+                                  y_zp=y_zp), arrays
+
+
+def qmul_case(rng):
+    # QLinearMul.cpp:39 (cs), :54-74 (16-wide body), :76-79 (scalar tail)
+    a_s, a_zp, b_s, b_zp, y_s, y_zp = 0.043, 120, 0.029, 135, 0.052, 128
+    n = 37
+    a = rng.integers(0, 256, n, dtype=np.uint8)
+    b = rng.integers(0, 256, n, dtype=np.uint8)
+    cs = div(mul(float(np.float32(a_s)), float(np.float32(b_s))), float(np.float32(y_s)))
+    body = n - n % 16
+    y = np.zeros(n, np.uint8)
+    for i in range(n):
+        da, db = int(a[i]) - a_zp, int(b[i]) - b_zp
+        if i < body:
+            v = fma(mul(float(da), float(db)), cs, float(y_zp))
+            y[i] = clamp(rne(v), 0, 255)
+        else:
+            v = add(mul(mul(cs, i2f(da)), i2f(db)), float(y_zp))
+            y[i] = clamp(x86_int(rne(v)), 0, 255)
+    return "qlinear_mul", dict(op="QLinearMul", a_scale=a_s, a_zp=a_zp, b_scale=b_s, b_zp=b_zp,
+                               y_scale=y_s, y_zp=y_zp), dict(a=a, b=b, y=y)
+
+
 def main():
     rng = np.random.default_rng(20240611)
     cases = [
@@ -315,6 +417,9 @@ def main():
         quantize_case(rng),
         dynq_case(rng),
     ]
+    # the QOperator family (a separate stream, so the fixtures above stay as committed)
+    rng2 = np.random.default_rng(20261201)
+    cases += [qgap_case(rng2), qavgpool_case(rng2), qconcat_case(rng2), qmul_case(rng2)]
     for name, params, arrays in cases:
         path = os.path.join(HERE, name + ".npz")
         np.savez_compressed(path, params=np.array(json.dumps(params, sort_keys=True)), **arrays)

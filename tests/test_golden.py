@@ -30,7 +30,8 @@ def test_fixtures_present():
     names = {os.path.basename(f)[:-4] for f in FILES}
     assert {"conv_packed_bprime", "conv_nr16", "conv_first_nchw_tail", "conv_direct_tail",
             "conv_dw", "conv_im2col_s1", "conv_im2col_s2", "qlinear_matmul", "qlinear_add",
-            "quantize", "dynamic_quantize"} <= names
+            "quantize", "dynamic_quantize", "qlinear_global_avgpool", "qlinear_avgpool",
+            "qlinear_concat", "qlinear_mul"} <= names
 
 
 @pytest.mark.parametrize("path", FILES, ids=[os.path.basename(f)[:-4] for f in FILES])
@@ -53,6 +54,25 @@ def test_oracle_matches_golden(path):
         assert np.array_equal(y, d["y"])
     elif op == "QuantizeLinear":
         y = O.quantize_linear(d["x"], p["scale"], p["zp"], np.uint8)
+        assert np.array_equal(y, d["y"])
+    elif op == "QLinearGlobalAveragePool":
+        y = O.qlinear_global_avgpool(d["x"], p["x_scale"], p["x_zp"], p["y_scale"], p["y_zp"])
+        assert np.array_equal(y.reshape(d["y"].shape), d["y"])
+    elif op == "QLinearAveragePool":
+        k, st, pd = p["k"], p["stride"], p["pad"]
+        oH, oW = d["y"].shape[2:]
+        y = O.qlinear_avgpool(d["x"], (k, k), (st, st), (pd, pd), oH, oW, p["x_scale"], p["x_zp"],
+                              p["y_scale"], p["y_zp"])
+        assert np.array_equal(y, d["y"])
+    elif op == "QLinearConcat":
+        xs = [d[f"x{t}"] for t in range(len(p["scales"]))]
+        outer = xs[0].shape[0]
+        y = O.qlinear_concat([x.reshape(-1) for x in xs], [x.shape[1] for x in xs], outer, p["scales"],
+                             p["zps"], p["y_scale"], p["y_zp"])
+        assert np.array_equal(y.reshape(d["y"].shape), d["y"])
+    elif op == "QLinearMul":
+        y = O.qlinear_mul(0, d["a"], d["b"], p["a_scale"], p["a_zp"], p["b_scale"], p["b_zp"],
+                          p["y_scale"], p["y_zp"])
         assert np.array_equal(y, d["y"])
     elif op == "DynamicQuantizeLinear":
         y, s, z = O.dynamic_quantize_linear(d["x"])

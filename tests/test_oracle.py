@@ -483,3 +483,73 @@ def test_conv1d_weights_read_through_activation_type():
     assert run(1, -1, 0, np.uint8) == 255          # 1 * (255 - 0)
     assert run(1, -1, -2, np.uint8) == 1            # 1 * (255 - 254)
     assert run(1, -1, 0, np.int8) == -1             # int8 activations: the weight stays -1
+
+
+# ---------------------------------------------------------------------------
+# the rest of the QLinear family: closed forms that fix the structure (the
+# golden fixtures, an exact-rational restatement, fix the roundings)
+
+def test_qgap_constant_image_is_its_value():
+    """Power-of-two scales, spatial 16: sum*rs is exact, so a constant image
+    pools to its own value; a zero-point offset shifts it by the same."""
+    for v in (0, 7, 128, 255):
+        x = np.full((2, 3, 4, 4), v, np.uint8)
+        assert np.array_equal(O.qlinear_global_avgpool(x, 0.25, 10, 0.25, 10), np.full((2, 3), v))
+        assert np.array_equal(O.qlinear_global_avgpool(x, 0.25, 10, 0.25, 0), np.full((2, 3), max(v - 10, 0)))
+    x = np.arange(16, dtype=np.uint8).reshape(1, 1, 4, 4)
+    # mean 7.5 -> nearbyint ties to even: 8
+    assert O.qlinear_global_avgpool(x, 1.0, 0, 1.0, 0)[0, 0] == 8
+    # NHWC input gives the same sums
+    xn = np.random.default_rng(3).integers(0, 256, (2, 5, 6, 7), dtype=np.uint8)
+    assert np.array_equal(O.qlinear_global_avgpool(xn, 0.03, 9, 0.02, 4, nhwc=1),
+                          O.qlinear_global_avgpool(xn.transpose(0, 3, 1, 2), 0.03, 9, 0.02, 4))
+
+
+def test_qavgpool_identity_and_padding_count():
+    rng = np.random.default_rng(4)
+    x = rng.integers(0, 256, (2, 3, 5, 6), dtype=np.uint8)
+    # 1x1 window, stride 1, equal power-of-two scales and zero points: identity
+    assert np.array_equal(O.qlinear_avgpool(x, (1, 1), (1, 1), (0, 0), 5, 6, 0.5, 9, 0.5, 9), x)
+    # a 3x3 window at a corner averages only the in-image taps (count_include_pad 0)
+    c = np.full((1, 1, 3, 3), 0, np.uint8)
+    c[0, 0, 0, 0], c[0, 0, 0, 1], c[0, 0, 1, 0], c[0, 0, 1, 1] = 4, 8, 12, 16
+    y = O.qlinear_avgpool(c, (3, 3), (1, 1), (1, 1), 3, 3, 1.0, 0, 1.0, 0)
+    assert y[0, 0, 0, 0] == 10   # (4 + 8 + 12 + 16) / 4
+    # NHWC equals NCHW
+    xn = x.transpose(0, 2, 3, 1).copy()
+    a = O.qlinear_avgpool(x, (3, 3), (2, 2), (1, 1), 3, 3, 0.02, 7, 0.03, 5)
+    b = O.qlinear_avgpool(xn, (3, 3), (2, 2), (1, 1), 3, 3, 0.02, 7, 0.03, 5, nhwc=1)
+    assert np.array_equal(a, b.transpose(0, 3, 1, 2))
+
+
+def test_qconcat_copy_and_identity():
+    rng = np.random.default_rng(5)
+    xs = [rng.integers(0, 256, 4 * c, dtype=np.uint8) for c in (3, 17, 32)]
+    cat = np.concatenate([x.reshape(4, -1) for x in xs], 1).reshape(-1)
+    # matching scale and zero point: a copy
+    y = O.qlinear_concat(xs, [3, 17, 32], 4, [0.1] * 3, [5] * 3, 0.1, 5)
+    assert np.array_equal(y, cat)
+    # scale ratio 1 with another zero point: x - zp + y_zp, clamped, in body and tail
+    y = O.qlinear_concat(xs, [3, 17, 32], 4, [0.25] * 3, [10] * 3, 0.25, 0)
+    assert np.array_equal(y, np.clip(cat.astype(int) - 10, 0, 255))
+
+
+def test_qmul_identity_and_kinds():
+    rng = np.random.default_rng(6)
+    a = rng.integers(0, 256, 100, dtype=np.uint8)
+    one = np.full(100, 65, np.uint8)    # b - b_zp = 1
+    # cs = 0.5 * 2 / 1 = 1: y = a exactly, in the 16-wide body and in the tail
+    assert np.array_equal(O.qlinear_mul(0, a, one, 0.5, 0, 2.0, 64, 1.0, 0), a)
+    # scalar B equals the same-shape result when cs * (b - zp) is exact
+    b1 = np.array([66], np.uint8)
+    y_sc = O.qlinear_mul(1, a, b1, 0.5, 7, 1.0, 64, 1.0, 3)
+    y_full = O.qlinear_mul(0, a, np.full(100, 66, np.uint8), 0.5, 7, 1.0, 64, 1.0, 3)
+    assert np.array_equal(y_sc, y_full)
+    # per channel, NCHW and NHWC, agree on exact products
+    x = rng.integers(0, 256, (2, 4, 3, 5), dtype=np.uint8)
+    ch = rng.integers(60, 70, 4, dtype=np.uint8)
+    n1 = O.qlinear_mul(3, x, ch, 0.25, 0, 1.0, 64, 1.0, 0, C=4, HW=15, y_nhwc=0)
+    n2 = O.qlinear_mul(3, x.transpose(0, 2, 3, 1).copy(), ch, 0.25, 0, 1.0, 64, 1.0, 0, C=4, HW=15, y_nhwc=1)
+    assert np.array_equal(n1, n2.transpose(0, 3, 1, 2))
+    ref = np.clip(np.rint(x.astype(np.float64) * 0.25 * (ch.astype(np.float64) - 64)[None, :, None, None]), 0, 255)
+    assert np.array_equal(n1, ref)
