@@ -263,6 +263,37 @@ int nnrh_qlinear_add(int kind, const void* a_dev, const void* b_dev, void* y_dev
                      float a_scale, int a_zp, float b_scale, int b_zp,
                      float y_scale, int y_zp, void* stream);
 
+/* ---- the rest of the QLinear family (QOperator models) --------------------
+ * QLinearMul_operator::exec_typed (src/backend/cpu/QLinearMul.cpp:25-231):
+ * kind / layout arguments as nnrh_qlinear_add (3: a is the full tensor, b the
+ * [C] one; pass the per-channel operand as b with its scale / zero point).
+ * Bit-exact with the reference's 16-wide body and scalar tail.             */
+int nnrh_qlinear_mul(int kind, const void* a_dev, const void* b_dev, void* y_dev,
+                     size_t n, int C, int HW, int y_nhwc, int dtype,
+                     float a_scale, int a_zp, float b_scale, int b_zp,
+                     float y_scale, int y_zp, void* stream);
+/* QLinearGlobalAveragePool (src/backend/cpu/QLinearGlobalAveragePool.cpp:
+ * 38-60): x [N][C][spatial] (or [N][spatial][C] with x_nhwc) -> y [N][C]. */
+int nnrh_qlinear_global_avgpool(const void* x_dev, void* y_dev, int N, int C, int spatial,
+                                int x_nhwc, int dtype, float x_scale, int x_zp,
+                                float y_scale, int y_zp, void* stream);
+/* QLinearAveragePool (src/backend/cpu/QLinearAveragePool.cpp:67-115): 2-D,
+ * in-image taps counted (count_include_pad is never set, :41-42); NCHW or
+ * NHWC (nhwc) in and out; pads are the leading ones, oH / oW the caller's. */
+int nnrh_qlinear_avgpool(const void* x_dev, void* y_dev, int N, int C, int iH, int iW,
+                         int oH, int oW, int kH, int kW, int sH, int sW, int pH, int pW,
+                         int nhwc, int dtype, float x_scale, int x_zp, float y_scale,
+                         int y_zp, void* stream);
+/* One input of QLinearConcat (src/backend/cpu/QLinearConcat.cpp:70-236):
+ * `outer` chunks of `count` elements of x go to y at o * y_row + y_off,
+ * copied when the input has the output's scale and zero point, requantized
+ * otherwise (16-wide body / scalar tail within each chunk). A concat along
+ * axis a calls this once per input with outer = prod(dims[:a]), count =
+ * dims_t[a] * inner; along channels of NHWC tensors, outer = N*H*W.        */
+int nnrh_qlinear_concat_part(const void* x_dev, void* y_dev, long long outer, long long count,
+                             long long y_row, long long y_off, int dtype, float x_scale,
+                             int x_zp, float y_scale, int y_zp, void* stream);
+
 /* ---- uint8 MaxPool, NHWC (src/backend/x64/pool_x64.h:396-436) ----------- */
 int nnrh_maxpool_u8_nhwc(const uint8_t* x_dev, uint8_t* y_dev, int N, int C,
                          int iH, int iW, int oH, int oW, int kH, int kW, int sH,

@@ -343,6 +343,60 @@ def qlinear_add(kind, a, b, a_s, a_zp, b_s, b_zp, y_s, y_zp, C=0, HW=0, y_nhwc=0
     return y
 
 
+def qlinear_mul(kind, a, b, a_s, a_zp, b_s, b_zp, y_s, y_zp, C=0, HW=0, y_nhwc=0, y=None):
+    import torch
+    full = a if a.numel() >= b.numel() else b
+    if y is None:
+        y = torch.empty(full.shape, dtype=full.dtype, device=full.device)
+    dt = U8 if a.dtype == torch.uint8 else S8
+    check(lib().nnrh_qlinear_mul(kind, ptr(a), ptr(b), ptr(y), y.numel(), C, HW, y_nhwc, dt,
+                                 float(a_s), int(a_zp), float(b_s), int(b_zp), float(y_s),
+                                 int(y_zp), cur_stream()))
+    return y
+
+
+def qlinear_global_avgpool(x, x_s, x_zp, y_s, y_zp, nhwc=0):
+    """x [N, C, *spatial] (or [N, *spatial, C] with nhwc) -> y [N, C]."""
+    import torch
+    N = x.shape[0]
+    C = x.shape[-1] if nhwc else x.shape[1]
+    sp = x.numel() // (N * C)
+    y = torch.empty((N, C), dtype=x.dtype, device=x.device)
+    dt = U8 if x.dtype == torch.uint8 else S8
+    check(lib().nnrh_qlinear_global_avgpool(ptr(x), ptr(y), N, C, sp, nhwc, dt, float(x_s), int(x_zp),
+                                            float(y_s), int(y_zp), cur_stream()))
+    return y
+
+
+def qlinear_avgpool(x, k, stride, pads, oH, oW, x_s, x_zp, y_s, y_zp, nhwc=0):
+    import torch
+    if nhwc:
+        N, H, W, Cc = x.shape
+        y = torch.empty((N, oH, oW, Cc), dtype=x.dtype, device=x.device)
+    else:
+        N, Cc, H, W = x.shape
+        y = torch.empty((N, Cc, oH, oW), dtype=x.dtype, device=x.device)
+    dt = U8 if x.dtype == torch.uint8 else S8
+    check(lib().nnrh_qlinear_avgpool(ptr(x), ptr(y), N, Cc, H, W, oH, oW, k[0], k[1], stride[0], stride[1],
+                                     pads[0], pads[1], nhwc, dt, float(x_s), int(x_zp), float(y_s), int(y_zp),
+                                     cur_stream()))
+    return y
+
+
+def qlinear_concat(xs, counts, outer, scales, zps, y_s, y_zp):
+    """xs: device tensors of outer x counts[t] elements; y: outer x sum(counts)."""
+    import torch
+    row = sum(counts)
+    y = torch.empty(outer * row, dtype=xs[0].dtype, device=xs[0].device)
+    dt = U8 if xs[0].dtype == torch.uint8 else S8
+    off = 0
+    for x, c, sc, zp in zip(xs, counts, scales, zps):
+        check(lib().nnrh_qlinear_concat_part(ptr(x), ptr(y), outer, c, row, off, dt, float(sc), int(zp),
+                                             float(y_s), int(y_zp), cur_stream()))
+        off += c
+    return y
+
+
 def maxpool_u8_nhwc(x, kH, kW, sH, sW, pH, pW, oH, oW):
     import torch
     N, H, W, C = x.shape

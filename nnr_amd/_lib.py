@@ -31,6 +31,7 @@ EXPORTS = [
     "nnrh_qmatmul_fuse_dq_bias", "nnrh_qmatmul_fuse_gelu", "nnrh_qmatmul_minmax_count",
     "nnrh_qmatmul_set_minmax_out", "nnrh_dynamic_quantize_linear_parts", "nnrh_add_layernorm_f32",
     "nnrh_qmatmul_group_create", "nnrh_qmatmul_group_run", "nnrh_qmatmul_group_destroy",
+    "nnrh_qlinear_mul", "nnrh_qlinear_global_avgpool", "nnrh_qlinear_avgpool", "nnrh_qlinear_concat_part",
     "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
     "nnrh_dynamic_quantize_linear", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
@@ -140,6 +141,10 @@ def lib():
         "nnrh_dynamic_quantize_workspace": (sz, []),
         "nnrh_dynamic_quantize_linear": (i, [vp, sz, vp, vp, vp, vp, vp]),
         "nnrh_qlinear_add": (i, [i, vp, vp, vp, sz, i, i, i, i, f, i, f, i, f, i, vp]),
+        "nnrh_qlinear_mul": (i, [i, vp, vp, vp, sz, i, i, i, i, f, i, f, i, f, i, vp]),
+        "nnrh_qlinear_global_avgpool": (i, [vp, vp, i, i, i, i, i, f, i, f, i, vp]),
+        "nnrh_qlinear_avgpool": (i, [vp, vp] + [i] * 14 + [f, i, f, i, vp]),
+        "nnrh_qlinear_concat_part": (i, [vp, vp, ll, ll, ll, ll, i, f, i, f, i, vp]),
         "nnrh_maxpool_u8_nhwc": (i, [vp, vp] + [i] * 12 + [vp]),
         "nnrh_nchw_to_nhwc_u8": (i, [vp, vp, i, i, i, vp]),
         "nnrh_global_avgpool_f32": (i, [vp, vp, i, i, i, i, vp]),

@@ -1380,6 +1380,72 @@ extern "C" int nnrh_qlinear_add(int kind, const void* a, const void* b, void* y,
     return NNRH_OK;
 }
 
+extern "C" int nnrh_qlinear_mul(int kind, const void* a, const void* b, void* y, size_t n, int C, int HW,
+                                int y_nhwc, int dtype, float a_scale, int a_zp, float b_scale, int b_zp,
+                                float y_scale, int y_zp, void* stream) {
+    if (n && (!a || !b || !y)) return set_err(NNRH_ERR_INVALID, "qlinear_mul: NULL");
+    if (dtype != NNRH_U8 && dtype != NNRH_S8) return set_err(NNRH_ERR_UNSUPPORTED, "qlinear_mul: dtype");
+    if (kind < 0 || kind > 3) return set_err(NNRH_ERR_INVALID, "qlinear_mul: kind %d", kind);
+    if (kind == 3 && (C <= 0 || HW <= 0 || n % ((size_t)C * HW)))
+        return set_err(NNRH_ERR_INVALID, "qlinear_mul: per-channel shape");
+    QMulArgs p{};
+    p.kind = kind; p.a = a; p.b = b; p.y = y; p.n = (long long)n;
+    p.C = C; p.HW = HW; p.y_nhwc = y_nhwc; p.dt = dtype == NNRH_U8 ? 0 : 1;
+    p.cs = a_scale * b_scale / y_scale;   // QLinearMul.cpp:39
+    p.a_zp = a_zp; p.b_zp = b_zp; p.y_zp = y_zp;
+    p.lo = dtype == NNRH_U8 ? 0 : -128;
+    p.hi = dtype == NNRH_U8 ? 255 : 127;
+    ProfScope ps("qlinear_mul", S(stream));
+    HIP_TRY(launch_qmul(p, S(stream)), "qlinear_mul");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qlinear_global_avgpool(const void* x, void* y, int N, int C, int spatial, int x_nhwc,
+                                           int dtype, float x_scale, int x_zp, float y_scale, int y_zp,
+                                           void* stream) {
+    if (!x || !y) return set_err(NNRH_ERR_INVALID, "qlinear_global_avgpool: NULL");
+    if (dtype != NNRH_U8 && dtype != NNRH_S8) return set_err(NNRH_ERR_UNSUPPORTED, "qlinear_global_avgpool: dtype");
+    if (N <= 0 || C <= 0 || spatial <= 0) return set_err(NNRH_ERR_INVALID, "qlinear_global_avgpool: bad shape");
+    const float rs = x_scale / (y_scale * (float)spatial);   // QLinearGlobalAveragePool.cpp:46
+    ProfScope ps("qlinear_global_avgpool", S(stream));
+    HIP_TRY(launch_qgap(x, y, N, C, spatial, x_nhwc, dtype == NNRH_U8 ? 0 : 1, rs, x_zp, y_zp,
+                        dtype == NNRH_U8 ? 0 : -128, dtype == NNRH_U8 ? 255 : 127, S(stream)),
+            "qlinear_global_avgpool");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qlinear_avgpool(const void* x, void* y, int N, int C, int iH, int iW, int oH, int oW, int kH,
+                                    int kW, int sH, int sW, int pH, int pW, int nhwc, int dtype, float x_scale,
+                                    int x_zp, float y_scale, int y_zp, void* stream) {
+    if (!x || !y) return set_err(NNRH_ERR_INVALID, "qlinear_avgpool: NULL");
+    if (dtype != NNRH_U8 && dtype != NNRH_S8) return set_err(NNRH_ERR_UNSUPPORTED, "qlinear_avgpool: dtype");
+    if (N <= 0 || C <= 0 || oH <= 0 || oW <= 0 || kH <= 0 || kW <= 0 || sH <= 0 || sW <= 0)
+        return set_err(NNRH_ERR_INVALID, "qlinear_avgpool: bad shape");
+    ProfScope ps("qlinear_avgpool", S(stream));
+    HIP_TRY(launch_qavgpool(x, y, N, C, iH, iW, oH, oW, kH, kW, sH, sW, pH, pW, nhwc, dtype == NNRH_U8 ? 0 : 1,
+                            x_scale, x_zp, y_scale, y_zp, dtype == NNRH_U8 ? 0 : -128,
+                            dtype == NNRH_U8 ? 255 : 127, S(stream)),
+            "qlinear_avgpool");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qlinear_concat_part(const void* x, void* y, long long outer, long long count, long long y_row,
+                                        long long y_off, int dtype, float x_scale, int x_zp, float y_scale,
+                                        int y_zp, void* stream) {
+    if (!x || !y) return set_err(NNRH_ERR_INVALID, "qlinear_concat_part: NULL");
+    if (dtype != NNRH_U8 && dtype != NNRH_S8) return set_err(NNRH_ERR_UNSUPPORTED, "qlinear_concat_part: dtype");
+    if (outer < 0 || count < 0 || y_off < 0 || y_off + count > y_row)
+        return set_err(NNRH_ERR_INVALID, "qlinear_concat_part: bad extents");
+    // QLinearConcat.cpp:147: an input already in the output's quantization is copied
+    const int copy = x_scale == y_scale && x_zp == y_zp;
+    const float rs = copy ? 0.f : x_scale / y_scale;
+    ProfScope ps("qlinear_concat", S(stream));
+    HIP_TRY(launch_qconcat_part(x, y, outer, count, y_row, y_off, dtype == NNRH_U8 ? 0 : 1, copy, rs, x_zp, y_zp,
+                                dtype == NNRH_U8 ? 0 : -128, dtype == NNRH_U8 ? 255 : 127, S(stream)),
+            "qlinear_concat_part");
+    return NNRH_OK;
+}
+
 extern "C" int nnrh_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH, int iW, int oH,
                                     int oW, int kH, int kW, int sH, int sW, int pH, int pW, void* stream) {
     if (!x || !y) return set_err(NNRH_ERR_INVALID, "maxpool: NULL");

@@ -23,6 +23,28 @@ struct QAddArgs {
     int tail_all;        // every element takes the scalar tail expression
 };
 
+struct QMulArgs {
+    int kind;            // 0 same shape, 1 B scalar, 2 A scalar, 3 per-channel B[C]
+    const void* a;
+    const void* b;
+    void* y;
+    long long n;
+    int C, HW, y_nhwc;   // per-channel layout
+    int dt;              // 0 u8, 1 s8
+    float cs;            // fl(fl(a_s * b_s) / y_s)
+    int a_zp, b_zp, y_zp;
+    int lo, hi;
+};
+hipError_t launch_qmul(const QMulArgs& p, hipStream_t s);
+hipError_t launch_qgap(const void* x, void* y, int N, int C, int spatial, int nhwc, int dt, float rs, int x_zp,
+                       int y_zp, int lo, int hi, hipStream_t s);
+hipError_t launch_qavgpool(const void* x, void* y, int N, int C, int iH, int iW, int oH, int oW, int kH, int kW,
+                           int sH, int sW, int pH, int pW, int nhwc, int dt, float x_s, int x_zp, float y_s,
+                           int y_zp, int lo, int hi, hipStream_t s);
+hipError_t launch_qconcat_part(const void* x, void* y, long long outer, long long count, long long y_row,
+                               long long y_off, int dt, int copy, float rs, int x_zp, int y_zp, int lo, int hi,
+                               hipStream_t s);
+
 hipError_t launch_quantize(const float* x, long long n, float scale, int zp, int dt, void* y,
                            hipStream_t s);
 hipError_t launch_dequantize(const void* x, long long n, int dt, float scale, int zp, float* y,

@@ -541,3 +541,201 @@ hipError_t launch_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, in
 }
 
 }  // namespace nnrh
+
+namespace nnrh {
+
+// ---------------------------------------------------------------------------
+// The rest of the QLinear family (QOperator models). Every kernel restates the
+// reference expression element by element, including its 16-wide body /
+// scalar tail split, so results are bit-identical.
+
+// QLinearMul (QLinearMul.cpp:25-231). kind as QLinearAdd: 0 same shape, 1 B
+// scalar, 2 A scalar, 3 per channel (a full, b [C]); cs = fl(fl(a_s*b_s)/y_s)
+__global__ __launch_bounds__(256) void qmul_kernel(QMulArgs p) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < p.n; i += stride) {
+        int q;
+        if (p.kind == 0) {
+            const long long body = p.n - p.n % 16;
+            const int a = ld_q(p.a, p.dt, i), b = ld_q(p.b, p.dt, i);
+            if (i < body) {
+                // fma(fl(fl(a - a_zp) * fl(b - b_zp)), cs, y_zp), roundscale, min / max
+                const float va = (float)a - (float)p.a_zp, vb = (float)b - (float)p.b_zp;
+                float v = __builtin_fmaf(va * vb, p.cs, (float)p.y_zp);
+                v = clamp_minmax(__builtin_rintf(v), (float)p.lo, (float)p.hi);
+                q = (int)v;
+            } else {
+                const float t1 = p.cs * (float)(a - p.a_zp);
+                const float v = t1 * (float)(b - p.b_zp) + (float)p.y_zp;
+                q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
+            }
+        } else if (p.kind == 1 || p.kind == 2) {
+            const bool b_sc = p.kind == 1;
+            const float cval = b_sc ? p.cs * (float)(ld_q(p.b, p.dt, 0) - p.b_zp)
+                                    : p.cs * (float)(ld_q(p.a, p.dt, 0) - p.a_zp);
+            const float d = b_sc ? (float)(ld_q(p.a, p.dt, i) - p.a_zp) : (float)(ld_q(p.b, p.dt, i) - p.b_zp);
+            const float v = cval * d + (float)p.y_zp;
+            q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
+        } else {
+            int c;
+            long long inner;
+            if (p.y_nhwc) { c = (int)(i % p.C); inner = c; }
+            else { c = (int)((i / p.HW) % p.C); inner = i % p.HW; }
+            const long long body = p.y_nhwc ? (p.C - p.C % 16) : (p.HW - p.HW % 16);
+            const int x = ld_q(p.a, p.dt, i);
+            const float chv = p.cs * (float)(ld_q(p.b, p.dt, c) - p.b_zp);
+            if (inner < body) {
+                float v = __builtin_fmaf((float)x - (float)p.a_zp, chv, (float)p.y_zp);
+                v = clamp_minmax(__builtin_rintf(v), (float)p.lo, (float)p.hi);
+                q = (int)v;
+            } else {
+                const float v = chv * (float)(x - p.a_zp) + (float)p.y_zp;
+                q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
+            }
+        }
+        st_q(p.y, p.dt, i, q);
+    }
+}
+
+hipError_t launch_qmul(const QMulArgs& p, hipStream_t s) {
+    if (p.n <= 0) return hipSuccess;
+    long long blocks = (p.n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(qmul_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+// QLinearGlobalAveragePool (QLinearGlobalAveragePool.cpp:38-60), RQ-F: the
+// int32 sum of a (n, c) plane (exact in any order), minus x_zp * spatial,
+// times rs = fl(x_s / fl(y_s * spatial)), nearbyint, + y_zp, clamp.
+// NCHW: one wave per plane; NHWC: one thread per (n, c), channels coalesced.
+__global__ __launch_bounds__(256) void qgap_kernel(const void* __restrict x, void* __restrict y, int N, int C,
+                                                   int spatial, int nhwc, int dt, float rs, int x_zp, int y_zp,
+                                                   int lo, int hi) {
+    long long nc;
+    uint32_t sum = 0;
+    if (nhwc) {
+        nc = (long long)blockIdx.x * 256 + threadIdx.x;
+        if (nc >= (long long)N * C) return;
+        const long long n = nc / C, c = nc - n * C;
+        for (int s = 0; s < spatial; ++s) sum += (uint32_t)ld_q(x, dt, (n * spatial + s) * C + c);
+    } else {
+        nc = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+        const int lane = threadIdx.x & 63;
+        if (nc >= (long long)N * C) return;
+        for (int s = lane; s < spatial; s += 64) sum += (uint32_t)ld_q(x, dt, nc * spatial + s);
+        for (int off = 32; off > 0; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off, 64);
+        if (lane) return;
+    }
+    sum -= (uint32_t)x_zp * (uint32_t)spatial;
+    int32_t q = x86_f2i(__builtin_rintf((float)(int32_t)sum * rs));
+    q = (int32_t)((uint32_t)q + (uint32_t)y_zp);
+    st_q(y, dt, nc, clampi(q, lo, hi));
+}
+
+hipError_t launch_qgap(const void* x, void* y, int N, int C, int spatial, int nhwc, int dt, float rs, int x_zp,
+                       int y_zp, int lo, int hi, hipStream_t s) {
+    const long long rows = (long long)N * C;
+    if (rows <= 0) return hipSuccess;
+    const long long blocks = nhwc ? (rows + 255) / 256 : (rows + 3) / 4;
+    hipLaunchKernelGGL(qgap_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, N, C, spatial, nhwc, dt, rs,
+                       x_zp, y_zp, lo, hi);
+    return hipGetLastError();
+}
+
+// QLinearAveragePool (QLinearAveragePool.cpp:67-115): in-image taps only,
+// avg = fl(fl(sum * x_s) / count), q = nearbyint(fl(avg / y_s)) + y_zp, clamp.
+// One thread per output element, NCHW or NHWC.
+__global__ __launch_bounds__(256) void qavgpool_kernel(const void* __restrict x, void* __restrict y, int N, int C,
+                                                       int iH, int iW, int oH, int oW, int kH, int kW, int sH,
+                                                       int sW, int pH, int pW, int nhwc, int dt, float x_s,
+                                                       int x_zp, float y_s, int y_zp, int lo, int hi) {
+    const long long total = (long long)N * C * oH * oW;
+    for (long long o = (long long)blockIdx.x * 256 + threadIdx.x; o < total; o += (long long)gridDim.x * 256) {
+        int n, c, oh, ow;
+        if (nhwc) {
+            c = (int)(o % C); long long r = o / C;
+            ow = (int)(r % oW); r /= oW;
+            oh = (int)(r % oH); n = (int)(r / oH);
+        } else {
+            ow = (int)(o % oW); long long r = o / oW;
+            oh = (int)(r % oH); r /= oH;
+            c = (int)(r % C); n = (int)(r / C);
+        }
+        int32_t sum = 0;
+        int count = 0;
+        for (int kh = 0; kh < kH; ++kh) {
+            const int ih = oh * sH - pH + kh;
+            if (ih < 0 || ih >= iH) continue;
+            for (int kw = 0; kw < kW; ++kw) {
+                const int iw = ow * sW - pW + kw;
+                if (iw < 0 || iw >= iW) continue;
+                const long long i = nhwc ? (((long long)n * iH + ih) * iW + iw) * C + c
+                                         : (((long long)n * C + c) * iH + ih) * iW + iw;
+                sum += ld_q(x, dt, i) - x_zp;
+                ++count;
+            }
+        }
+        if (count == 0) count = 1;
+        const float t = (float)sum * x_s;
+        const float avg = t / (float)count;
+        int32_t q = x86_f2i(__builtin_rintf(avg / y_s));
+        q = (int32_t)((uint32_t)q + (uint32_t)y_zp);
+        st_q(y, dt, o, clampi(q, lo, hi));
+    }
+}
+
+hipError_t launch_qavgpool(const void* x, void* y, int N, int C, int iH, int iW, int oH, int oW, int kH, int kW,
+                           int sH, int sW, int pH, int pW, int nhwc, int dt, float x_s, int x_zp, float y_s,
+                           int y_zp, int lo, int hi, hipStream_t s) {
+    const long long total = (long long)N * C * oH * oW;
+    if (total <= 0) return hipSuccess;
+    long long blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(qavgpool_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, N, C, iH, iW, oH, oW, kH,
+                       kW, sH, sW, pH, pW, nhwc, dt, x_s, x_zp, y_s, y_zp, lo, hi);
+    return hipGetLastError();
+}
+
+// One input of QLinearConcat (QLinearConcat.cpp:70-104, :119-236): `outer`
+// chunks of `count` elements go to y at o * y_row + y_off. Matching scale and
+// zero point copy; otherwise the first count - count % 16 elements of a chunk
+// (count >= 16) take the 16-wide body rne(clamp(fma(rs, x - x_zp, y_zp))),
+// the rest the scalar nearbyint(fl(rs * (x - x_zp)) + y_zp), clamped.
+__global__ __launch_bounds__(256) void qconcat_kernel(const void* __restrict x, void* __restrict y, long long outer,
+                                                      long long count, long long y_row, long long y_off, int dt,
+                                                      int copy, float rs, int x_zp, int y_zp, int lo, int hi) {
+    const long long total = outer * count;
+    const long long body = count >= 16 ? count - count % 16 : 0;
+    for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
+        const long long o = e / count, i = e - o * count;
+        const int xv = ld_q(x, dt, e);
+        int q;
+        if (copy) {
+            q = xv;
+        } else if (i < body) {
+            float v = __builtin_fmaf(rs, (float)xv - (float)x_zp, (float)y_zp);
+            v = v > (float)lo ? v : (float)lo;
+            v = v < (float)hi ? v : (float)hi;
+            q = (int)__builtin_rintf(v);
+        } else {
+            const float v = rs * (float)(xv - x_zp) + (float)y_zp;
+            q = clampi(x86_f2i(__builtin_rintf(v)), lo, hi);
+        }
+        st_q(y, dt, o * y_row + y_off + i, q);
+    }
+}
+
+hipError_t launch_qconcat_part(const void* x, void* y, long long outer, long long count, long long y_row,
+                               long long y_off, int dt, int copy, float rs, int x_zp, int y_zp, int lo, int hi,
+                               hipStream_t s) {
+    const long long total = outer * count;
+    if (total <= 0) return hipSuccess;
+    long long blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(qconcat_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, outer, count, y_row, y_off,
+                       dt, copy, rs, x_zp, y_zp, lo, hi);
+    return hipGetLastError();
+}
+
+}  // namespace nnrh

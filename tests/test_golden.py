@@ -106,6 +106,21 @@ def test_hip_matches_golden(dev, path):
                           p["b_zp"], p["y_scale"], p["y_zp"]).cpu().numpy()
     elif op == "QuantizeLinear":
         y = H.quantize_linear(to(d["x"]), p["scale"], p["zp"], np.uint8).cpu().numpy()
+    elif op == "QLinearGlobalAveragePool":
+        y = H.qlinear_global_avgpool(to(d["x"]), p["x_scale"], p["x_zp"], p["y_scale"],
+                                     p["y_zp"]).cpu().numpy().reshape(d["y"].shape)
+    elif op == "QLinearAveragePool":
+        k, st, pd = p["k"], p["stride"], p["pad"]
+        oH, oW = d["y"].shape[2:]
+        y = H.qlinear_avgpool(to(d["x"]), (k, k), (st, st), (pd, pd), oH, oW, p["x_scale"], p["x_zp"],
+                              p["y_scale"], p["y_zp"]).cpu().numpy()
+    elif op == "QLinearConcat":
+        xs = [d[f"x{t}"] for t in range(len(p["scales"]))]
+        y = H.qlinear_concat([to(x.reshape(-1)) for x in xs], [x.shape[1] for x in xs], xs[0].shape[0],
+                             p["scales"], p["zps"], p["y_scale"], p["y_zp"]).cpu().numpy().reshape(d["y"].shape)
+    elif op == "QLinearMul":
+        y = H.qlinear_mul(0, to(d["a"]), to(d["b"]), p["a_scale"], p["a_zp"], p["b_scale"],
+                          p["b_zp"], p["y_scale"], p["y_zp"]).cpu().numpy()
     elif op == "DynamicQuantizeLinear":
         yt, s, z = H.dynamic_quantize_linear(to(d["x"]))
         assert np.float32(s.cpu().numpy().reshape(-1)[0]) == d["y_scale"][0]

@@ -319,6 +319,72 @@ def test_qlinear_add(dev, kind, y_nhwc):
     assert np.array_equal(y, ref)
 
 
+# ---------------------------------------------------------------------------
+# the rest of the QLinear family, bit-exact against the oracle
+
+@pytest.mark.parametrize("kind,shape_b,nhwc", [(0, None, 0), (1, (1,), 0), (2, "a1", 0), (3, "c", 0), (3, "c", 1)])
+@pytest.mark.parametrize("dt", [np.uint8, np.int8])
+def test_qlinear_mul(dev, kind, shape_b, nhwc, dt):
+    rng = np.random.default_rng(kind * 7 + nhwc + (dt == np.int8))
+    info = (0, 256) if dt == np.uint8 else (-128, 128)
+    N, C, Hh, W = 2, 19, 5, 7          # 665 per image: a ragged 16-wide body everywhere
+    full = rng.integers(*info, (N, C, Hh, W) if not nhwc else (N, Hh, W, C), dtype=dt)
+    if kind == 0:
+        a, b = full, rng.integers(*info, full.shape, dtype=dt)
+    elif kind == 1:
+        a, b = full, rng.integers(*info, (1,), dtype=dt)
+    elif kind == 2:
+        a, b = rng.integers(*info, (1,), dtype=dt), full
+    else:
+        a, b = full, rng.integers(*info, (C,), dtype=dt)
+    zps = (13, 200, 128) if dt == np.uint8 else (-7, 20, 3)
+    args = (0.037, zps[0], 0.021, zps[1], 0.043, zps[2])
+    kw = dict(C=C, HW=Hh * W, y_nhwc=nhwc) if kind == 3 else {}
+    ref = O.qlinear_mul(kind, a, b, *args, **kw)
+    y = H.qlinear_mul(kind, to_dev(a, dev), to_dev(b, dev), *args, **kw)
+    assert np.array_equal(to_np(y), ref)
+
+
+@pytest.mark.parametrize("nhwc", [0, 1])
+@pytest.mark.parametrize("dt,N,C,Hh,W", [(np.uint8, 3, 70, 7, 7), (np.int8, 2, 16, 1, 1), (np.uint8, 1, 5, 13, 17)])
+def test_qlinear_global_avgpool(dev, nhwc, dt, N, C, Hh, W):
+    rng = np.random.default_rng(N * C + nhwc)
+    info = (0, 256) if dt == np.uint8 else (-128, 128)
+    x = rng.integers(*info, (N, Hh, W, C) if nhwc else (N, C, Hh, W), dtype=dt)
+    zx, zy = (100, 3) if dt == np.uint8 else (-9, 4)
+    ref = O.qlinear_global_avgpool(x, 0.031, zx, 0.017, zy, nhwc=nhwc)
+    y = H.qlinear_global_avgpool(to_dev(x, dev), 0.031, zx, 0.017, zy, nhwc=nhwc)
+    assert np.array_equal(to_np(y), ref)
+
+
+@pytest.mark.parametrize("nhwc", [0, 1])
+@pytest.mark.parametrize("k,st,pad,H_,W_", [((3, 3), (2, 2), (1, 1), 9, 10), ((2, 2), (2, 2), (0, 0), 8, 8),
+                                             ((3, 2), (1, 1), (1, 0), 6, 7), ((7, 7), (1, 1), (0, 0), 7, 7)])
+def test_qlinear_avgpool(dev, nhwc, k, st, pad, H_, W_):
+    rng = np.random.default_rng(H_ * W_ + nhwc)
+    N, C = 2, 24
+    x = rng.integers(0, 256, (N, H_, W_, C) if nhwc else (N, C, H_, W_), dtype=np.uint8)
+    oH = (H_ + 2 * pad[0] - k[0]) // st[0] + 1
+    oW = (W_ + 2 * pad[1] - k[1]) // st[1] + 1
+    ref = O.qlinear_avgpool(x, k, st, pad, oH, oW, 0.02, 128, 0.013, 120, nhwc=nhwc)
+    y = H.qlinear_avgpool(to_dev(x, dev), k, st, pad, oH, oW, 0.02, 128, 0.013, 120, nhwc=nhwc)
+    assert np.array_equal(to_np(y), ref)
+
+
+@pytest.mark.parametrize("counts,outer", [([3, 17, 32], 5), ([64, 64], 1), ([15, 1, 16, 33], 37)])
+@pytest.mark.parametrize("dt", [np.uint8, np.int8])
+def test_qlinear_concat(dev, counts, outer, dt):
+    rng = np.random.default_rng(sum(counts) + outer)
+    info = (0, 256) if dt == np.uint8 else (-128, 128)
+    xs = [rng.integers(*info, outer * c, dtype=dt) for c in counts]
+    scales = [0.05, 0.031, 0.02, 0.07][: len(counts)]
+    zps = ([10, 7, 3, 200] if dt == np.uint8 else [10, 7, -3, -100])[: len(counts)]
+    y_s, y_zp = 0.031, 7                   # input 1 (if present) is copied
+    ref = O.qlinear_concat(xs, counts, outer, scales, zps, y_s, y_zp)
+    y = H.qlinear_concat([to_dev(x, dev) for x in xs], counts, outer, scales, zps, y_s, y_zp)
+    assert np.array_equal(to_np(y), ref)
+
+
 @pytest.mark.parametrize("C,k,st,pad", [(64, (3, 3), 2, 1),   # fixed 3x3 window (ResNet stem)
                                         (48, (2, 2), 2, 0),   # fixed 2x2
                                         (32, (3, 2), 1, 1),   # any window, 16-channel groups
