@@ -519,6 +519,192 @@ struct QLinearAdd_hip : operator_t {
     }
 };
 
+// QLinearMul (src/backend/cpu/QLinearMul.cpp:17-231): the broadcast kinds of
+// classify_broadcast (util.h:50-67) but the general one
+struct QLinearMul_hip : operator_t {
+    int kind = 0;
+    bool swap = false;
+    int C = 0, HW = 0;
+    bool init() override {
+        layout_mask = LAYOUT_ALL;
+        return inputs.size() == 8 && outputs.size() == 1;
+    }
+    bool reshape() override {
+        tensor_t *a = inputs[0], *b = inputs[3], *y = outputs[0];
+        const tensor_t* full = a->ndata >= b->ndata ? a : b;
+        const tensor_t* other = a->ndata >= b->ndata ? b : a;
+        swap = false;
+        if (a->dims == b->dims) {
+            kind = 0;
+        } else if (a->ndata == 1) {     // A_SCALAR is tested first (util.h:56)
+            kind = 2;
+        } else if (b->ndata == 1) {
+            kind = 1;
+        } else if (full->ndim() == 4 && other->ndata == (size_t)full->dims[1] &&
+                   (other->ndim() == 1 || (other->ndim() == 4 && other->dims[0] == 1 && other->dims[2] == 1 &&
+                                           other->dims[3] == 1) ||
+                    (other->ndim() == 3 && other->dims[1] == 1 && other->dims[2] == 1))) {
+            kind = 3;
+            swap = full == b;
+            C = full->dims[1];
+            HW = full->dims[2] * full->dims[3];
+        } else {
+            return bad(this, "general broadcasting is not supported");
+        }
+        y->format = full->format;
+        return y->reshape(full->dims, a->type);
+    }
+    bool exec() override {
+        tensor_t *a = inputs[0], *b = inputs[3];
+        float as = inputs[1]->scalar_f32(), bs = inputs[4]->scalar_f32(), ys = inputs[6]->scalar_f32();
+        int az = zp_value(inputs[2]), bz = zp_value(inputs[5]), yz = zp_value(inputs[7]);
+        const int nhwc = outputs[0]->format == memory_layout_t::NHWC;
+        if (swap)   // per channel with A the [C] operand (QLinearMul.cpp:127-131)
+            return ok(this, nnrh_qlinear_mul(3, b->data, a->data, outputs[0]->data, outputs[0]->ndata, C, HW, nhwc,
+                                             qdtype(a->type), bs, bz, as, az, ys, yz, ctx->stream));
+        return ok(this, nnrh_qlinear_mul(kind, a->data, b->data, outputs[0]->data, outputs[0]->ndata, C, HW, nhwc,
+                                         qdtype(a->type), as, az, bs, bz, ys, yz, ctx->stream));
+    }
+};
+
+// QLinearGlobalAveragePool (src/backend/cpu/QLinearGlobalAveragePool.cpp):
+// the kernel reads NCHW or NHWC (the same integer sums), y is [N][C][1..]
+struct QLinearGlobalAveragePool_hip : operator_t {
+    bool init() override {
+        layout_mask = LAYOUT_ALL;
+        return inputs.size() == 5 && outputs.size() == 1;
+    }
+    bool reshape() override {
+        tensor_t* x = inputs[0];
+        if (x->ndim() < 3) return bad(this, "needs at least 3 dimensions");
+        std::vector<int> d(x->dims.size(), 1);
+        d[0] = x->dims[0];
+        d[1] = x->dims[1];
+        outputs[0]->format = x->format;
+        return outputs[0]->reshape(d, x->type);
+    }
+    bool exec() override {
+        tensor_t* x = inputs[0];
+        const int N = x->dims[0], C = x->dims[1];
+        const int sp = (int)(x->ndata / ((size_t)N * C));
+        return ok(this, nnrh_qlinear_global_avgpool(x->data, outputs[0]->data, N, C, sp,
+                                                    x->format == memory_layout_t::NHWC, qdtype(x->type),
+                                                    inputs[1]->scalar_f32(), zp_value(inputs[2]),
+                                                    inputs[3]->scalar_f32(), zp_value(inputs[4]), ctx->stream));
+    }
+};
+
+// QLinearAveragePool (src/backend/cpu/QLinearAveragePool.cpp): 2-D, the
+// reference's attributes (kernel_shape, strides, pads, ceil_mode; no
+// count_include_pad); NCHW or NHWC
+struct QLinearAveragePool_hip : operator_t {
+    std::vector<int> kernels, pads, strides;
+    int ceil_mode = 0;
+    bool init() override {
+        layout_mask = LAYOUT_ALL;
+        if (inputs.size() != 5 || outputs.size() != 1) return false;
+        for (auto v : attribute_ints("kernel_shape")) kernels.push_back((int)v);
+        if (kernels.size() != 2) return false;   // :28
+        auto s = attribute_ints("strides"), p = attribute_ints("pads");
+        strides = {s.size() > 0 ? (int)s[0] : 1, s.size() > 1 ? (int)s[1] : 1};
+        pads = {0, 0, 0, 0};
+        for (size_t i = 0; i < p.size() && i < 4; ++i) pads[i] = (int)p[i];
+        ceil_mode = (int)attribute("ceil_mode", 0);
+        return true;
+    }
+    bool reshape() override {
+        tensor_t* x = inputs[0];
+        if (x->ndim() != 4) return bad(this, "4-D input only");
+        const int N = x->dims[0], C = x->dims[1], H = x->dims[2], W = x->dims[3];
+        int oH, oW;
+        if (ceil_mode) {   // :55-57
+            oH = (int)ceilf((H + pads[0] + pads[2] - kernels[0]) / (float)strides[0] + 1);
+            oW = (int)ceilf((W + pads[1] + pads[3] - kernels[1]) / (float)strides[1] + 1);
+        } else {
+            oH = (H + pads[0] + pads[2] - kernels[0]) / strides[0] + 1;
+            oW = (W + pads[1] + pads[3] - kernels[1]) / strides[1] + 1;
+        }
+        outputs[0]->format = x->format;
+        return outputs[0]->reshape({N, C, oH, oW}, x->type);
+    }
+    bool exec() override {
+        tensor_t *x = inputs[0], *y = outputs[0];
+        return ok(this, nnrh_qlinear_avgpool(x->data, y->data, x->dims[0], x->dims[1], x->dims[2], x->dims[3],
+                                             y->dims[2], y->dims[3], kernels[0], kernels[1], strides[0], strides[1],
+                                             pads[0], pads[1], x->format == memory_layout_t::NHWC, qdtype(x->type),
+                                             inputs[1]->scalar_f32(), zp_value(inputs[2]), inputs[3]->scalar_f32(),
+                                             zp_value(inputs[4]), ctx->stream));
+    }
+};
+
+// QLinearConcat (src/backend/cpu/QLinearConcat.cpp): inputs (Y_scale, Y_zp,
+// then X, X_scale, X_zp per tensor). Chunks as the reference forms them: the
+// logical NCHW rows (:119-166), or each pixel's channels when all 4-D inputs
+// are NHWC and the axis is 1 (:170-236)
+struct QLinearConcat_hip : operator_t {
+    int axis = 0;
+    bool init() override {
+        layout_mask = LAYOUT_NCHW;
+        if (inputs.size() < 5 || outputs.size() != 1 || (inputs.size() - 2) % 3) return false;
+        axis = (int)attribute("axis", 0);
+        return true;
+    }
+    int ntens() const { return (int)(inputs.size() - 2) / 3; }
+    bool reshape() override {
+        tensor_t* t0 = inputs[2];
+        const int nd = t0->ndim();
+        const int a = axis < 0 ? axis + nd : axis;
+        if (a < 0 || a >= nd) return bad(this, "axis");
+        std::vector<int> d(t0->dims.begin(), t0->dims.end());
+        for (int i = 1; i < ntens(); ++i) {
+            tensor_t* t = inputs[2 + 3 * i];
+            if (t->ndim() != nd) return bad(this, "ranks differ");
+            for (int k = 0; k < nd; ++k) {
+                if (k == a) d[k] += t->dims[k];
+                else if (t->dims[k] != t0->dims[k]) return bad(this, "shapes differ");
+            }
+        }
+        // NHWC only along channels of 4-D int8 tensors (:58-62)
+        layout_mask = (nd == 4 && a == 1) ? (LAYOUT_NCHW | LAYOUT_NHWC) : LAYOUT_NCHW;
+        bool nhwc = true;
+        for (int i = 0; i < ntens(); ++i) nhwc &= inputs[2 + 3 * i]->format == memory_layout_t::NHWC;
+        if (!nhwc)
+            for (int i = 0; i < ntens(); ++i)
+                if (inputs[2 + 3 * i]->format == memory_layout_t::NHWC)
+                    return bad(this, "inputs mix NCHW and NHWC");
+        if (nhwc && !(nd == 4 && a == 1)) return bad(this, "NHWC inputs concatenated along a non-channel axis");
+        outputs[0]->format = nhwc ? memory_layout_t::NHWC : memory_layout_t::NCHW;
+        return outputs[0]->reshape(d, t0->type);
+    }
+    bool exec() override {
+        tensor_t* y = outputs[0];
+        const int nd = y->ndim();
+        const int a = axis < 0 ? axis + nd : axis;
+        const bool nhwc = y->format == memory_layout_t::NHWC;
+        long long outer = 1, inner = 1;
+        if (nhwc) {
+            outer = (long long)y->dims[0] * y->dims[2] * y->dims[3];
+        } else {
+            for (int k = 0; k < a; ++k) outer *= y->dims[k];
+            for (int k = a + 1; k < nd; ++k) inner *= y->dims[k];
+        }
+        const long long row = nhwc ? y->dims[1] : (long long)y->dims[a] * inner;
+        const float ys = inputs[0]->scalar_f32();
+        const int yz = zp_value(inputs[1]);
+        long long off = 0;
+        for (int i = 0; i < ntens(); ++i) {
+            tensor_t* t = inputs[2 + 3 * i];
+            const long long cnt = nhwc ? t->dims[1] : (long long)t->dims[a] * inner;
+            if (!ok(this, nnrh_qlinear_concat_part(t->data, y->data, outer, cnt, row, off, qdtype(t->type),
+                                                   inputs[3 + 3 * i]->scalar_f32(), zp_value(inputs[4 + 3 * i]), ys,
+                                                   yz, ctx->stream)))
+                return false;
+            off += cnt;
+        }
+        return true;
+    }
+};
+
 // ===========================================================================
 // MaxPool (src/backend/cpu/MaxPool.cpp); uint8 NHWC after fuse_qdq
 struct MaxPool_hip : operator_t {
@@ -957,6 +1143,10 @@ const op_registrar_t reg[] = {
     {"QLinearMatMul", backend_t::HIP, make<QLinearMatMul_hip>},
     {"MatMulInteger", backend_t::HIP, make<MatMulInteger_hip>},
     {"QLinearAdd", backend_t::HIP, make<QLinearAdd_hip>},
+    {"QLinearMul", backend_t::HIP, make<QLinearMul_hip>},
+    {"QLinearGlobalAveragePool", backend_t::HIP, make<QLinearGlobalAveragePool_hip>},
+    {"QLinearAveragePool", backend_t::HIP, make<QLinearAveragePool_hip>},
+    {"QLinearConcat", backend_t::HIP, make<QLinearConcat_hip>},
     {"MaxPool", backend_t::HIP, make<MaxPool_hip>},
     {"GlobalAveragePool", backend_t::HIP, make<GlobalAveragePool_hip>},
     {"Flatten", backend_t::HIP, make<Flatten_hip>},

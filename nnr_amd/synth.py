@@ -177,6 +177,60 @@ def qconv1d_graph(batch=4, C=16, W=50, OC=24, k=5, stride=1, pad=2, dil=1, group
     return g
 
 
+def qoperator_net(batch=2, hw=20, seed=22, pool="avg"):
+    """A QOperator-format graph (quantized operators, not QDQ pairs) using the
+    rest of the QLinear family: Q(input) -> QLinearConv 3x3 (16) ->
+    QLinearAveragePool -> two QLinearConv branches (1x1 -> 24, 3x3 -> 8) ->
+    QLinearConcat along channels (the second branch already in the output's
+    quantization, so it is copied) -> QLinearMul by a per-channel constant ->
+    QLinearMul of the tensor with itself -> QLinearGlobalAveragePool ->
+    DQ. The convolution outputs run NHWC; the pooled, concatenated and
+    multiplied tensors follow them."""
+    g = Graph()
+    rng = np.random.default_rng(seed)
+    u8, s8 = np.uint8, np.int8
+    g.inputs["input"] = (np.float32, (batch, 3, hw, hw))
+
+    def qp(name, s, z, dt=u8):
+        return g.init(name + "_s", np.array(s, F32)), g.init(name + "_z", np.array(z, dt))
+
+    def qconv(x, x_qp, cin, cout, k, pad, name, y_qp):
+        w = rng.integers(-90, 91, (cout, cin, k, k), dtype=s8)
+        ws = rng.uniform(0.002, 0.01, cout).astype(F32)
+        b = rng.integers(-2000, 2000, cout).astype(np.int32)
+        ins = [x, x_qp[0], x_qp[1], g.init(name + "_w", w), g.init(name + "_ws", ws),
+               g.init(name + "_wz", np.zeros(cout, s8)), y_qp[0], y_qp[1], g.init(name + "_b", b)]
+        return g.node("QLinearConv", ins, name=name, kernel_shape=[k, k], pads=[pad] * 4, strides=[1, 1])
+
+    xq_qp = qp("xq", 0.02, 120)
+    x = g.node("QuantizeLinear", ["input", *xq_qp], name="input_Q")
+    c1_qp = qp("c1", 0.03, 5)
+    c1 = qconv(x, xq_qp, 3, 16, 3, 1, "c1", c1_qp)
+    p_qp = qp("pool", 0.027, 9)
+    if pool == "avg":
+        pl = g.node("QLinearAveragePool", [c1, *c1_qp, *p_qp], name="avgpool", kernel_shape=[3, 3],
+                    strides=[2, 2], pads=[1, 1, 1, 1])
+    else:
+        pl = g.node("QLinearAveragePool", [c1, *c1_qp, *p_qp], name="avgpool", kernel_shape=[2, 2],
+                    strides=[2, 2], ceil_mode=1)
+    ba_qp = qp("ba", 0.041, 12)
+    cat_qp = qp("cat", 0.036, 10)
+    ba = qconv(pl, p_qp, 16, 24, 1, 0, "ba", ba_qp)
+    bb = qconv(pl, p_qp, 16, 8, 3, 1, "bb", cat_qp)   # already in the concat's quantization
+    cat = g.node("QLinearConcat", [*cat_qp, ba, *ba_qp, bb, *cat_qp], name="concat", axis=1)
+    ch = g.init("mul_ch", rng.integers(100, 200, 32, dtype=u8))
+    ch_qp = qp("mul_chq", 0.011, 128)
+    m1_qp = qp("m1", 0.025, 3)
+    m1 = g.node("QLinearMul", [cat, *cat_qp, ch, *ch_qp, *m1_qp], name="mul_channel")
+    m2_qp = qp("m2", 0.02, 0)
+    m2 = g.node("QLinearMul", [m1, *m1_qp, m1, *m1_qp, *m2_qp], name="mul_square")
+    gp_qp = qp("gap", 0.01, 2)
+    gp = g.node("QLinearGlobalAveragePool", [m2, *m2_qp, *gp_qp], name="gap")
+    y = g.node("DequantizeLinear", [gp, *gp_qp], name="out_DQ")
+    g.outputs.append(y)
+    return g
+
+
 # MobileNetV2 (Sandler et al. 2018, width 1.0): (expansion t, channels c,
 # repeats n, first stride s) of the 17 inverted-residual blocks
 MBV2_BLOCKS = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 96, 3, 1),

@@ -158,6 +158,71 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
             y = O.qlinear_add(0, a_, b_, float(scal(ins[1])), int(scal(ins[2])),
                               float(scal(ins[4])), int(scal(ins[5])), float(scal(ins[6])),
                               int(scal(ins[7])))
+        elif op == "QLinearMul":
+            a_, b_ = val(ins[0]), val(ins[3])
+            args = (float(scal(ins[1])), int(scal(ins[2])), float(scal(ins[4])), int(scal(ins[5])),
+                    float(scal(ins[6])), int(scal(ins[7])))
+            if a_.shape == b_.shape:
+                y = O.qlinear_mul(0, a_, b_, *args)
+            elif a_.size == 1:
+                y = O.qlinear_mul(2, a_, b_, *args)
+            elif b_.size == 1:
+                y = O.qlinear_mul(1, a_, b_, *args)
+            else:
+                # per channel: the full operand first, with its own scale / zero point
+                full_is_a = a_.size >= b_.size
+                nhwc = fmt_of(ins[0] if full_is_a else ins[3])
+                full, ch = (a_, b_) if full_is_a else (b_, a_)
+                C = full.shape[3] if nhwc else full.shape[1]
+                HW = full.size // (full.shape[0] * C)
+                fs, fz, cs_, cz = (args[0], args[1], args[2], args[3]) if full_is_a else \
+                    (args[2], args[3], args[0], args[1])
+                y = O.qlinear_mul(3, full, ch.reshape(-1), fs, fz, cs_, cz, args[4], args[5], C=C, HW=HW,
+                                  y_nhwc=nhwc)
+        elif op == "QLinearGlobalAveragePool":
+            x = val(ins[0])
+            nhwc = fmt_of(ins[0])
+            y = O.qlinear_global_avgpool(x, float(scal(ins[1])), int(scal(ins[2])), float(scal(ins[3])),
+                                         int(scal(ins[4])), nhwc=nhwc)
+            sp = [1] * (x.ndim - 2)
+            y = y.reshape((y.shape[0], *sp, y.shape[1]) if nhwc else (y.shape[0], y.shape[1], *sp))
+        elif op == "QLinearAveragePool":
+            a = graph.node_by_name(nd["name"]).attrs
+            x = val(ins[0])
+            nhwc = fmt_of(ins[0])
+            k, st = a["kernel_shape"], a.get("strides", [1, 1])
+            p_ = list(a.get("pads", [0, 0, 0, 0])) + [0] * 4
+            H, W = (x.shape[1], x.shape[2]) if nhwc else (x.shape[2], x.shape[3])
+            if a.get("ceil_mode", 0):
+                oH = int(np.ceil(np.float32(H + p_[0] + p_[2] - k[0]) / np.float32(st[0]) + 1))
+                oW = int(np.ceil(np.float32(W + p_[1] + p_[3] - k[1]) / np.float32(st[1]) + 1))
+            else:
+                oH = (H + p_[0] + p_[2] - k[0]) // st[0] + 1
+                oW = (W + p_[1] + p_[3] - k[1]) // st[1] + 1
+            y = O.qlinear_avgpool(x, k, st, (p_[0], p_[1]), oH, oW, float(scal(ins[1])), int(scal(ins[2])),
+                                  float(scal(ins[3])), int(scal(ins[4])), nhwc=nhwc)
+        elif op == "QLinearConcat":
+            a = graph.node_by_name(nd["name"]).attrs
+            xs = [val(ins[2 + 3 * i]) for i in range((len(ins) - 2) // 3)]
+            nhwc = fmt_of(ins[2])
+            nd_ = xs[0].ndim
+            ax = a.get("axis", 0) % nd_
+            if nhwc:
+                outer = xs[0].shape[0] * xs[0].shape[1] * xs[0].shape[2]
+                counts = [x.shape[3] for x in xs]
+            else:
+                outer = int(np.prod(xs[0].shape[:ax]))
+                counts = [int(np.prod(x.shape[ax:])) for x in xs]
+            y = O.qlinear_concat([x.reshape(-1) for x in xs], counts, outer,
+                                 [float(scal(ins[3 + 3 * i])) for i in range(len(xs))],
+                                 [int(scal(ins[4 + 3 * i])) for i in range(len(xs))],
+                                 float(scal(ins[0])), int(scal(ins[1])))
+            shp = list(xs[0].shape)
+            if nhwc:
+                shp[3] = sum(counts)
+            else:
+                shp[ax] = sum(x.shape[ax] for x in xs)
+            y = y.reshape(shp)
         elif op == "MaxPool":
             src = graph.node_by_name(nd["name"])
             a = src.attrs

@@ -81,6 +81,23 @@ def test_qconv_graph_config2(dev):
     assert [p["variant"] for p in plan if p["op"] == "QLinearConv"] == ["NR16"]
 
 
+@pytest.mark.parametrize("pool", ["avg", "ceil"])
+def test_qoperator_graph(dev, pool):
+    """QOperator-format graph through the host framework: QLinearConv ->
+    QLinearAveragePool (3x3/2 padded, or 2x2/2 with ceil_mode) -> two conv
+    branches -> QLinearConcat (one input copied) -> QLinearMul per channel and
+    with itself -> QLinearGlobalAveragePool; every int8 tensor bit-exact with
+    the oracle's replay of the plan, in the layouts the plan chose."""
+    g = synth.qoperator_net(batch=3, hw=21, pool=pool)
+    rng = np.random.default_rng(23)
+    x = rng.uniform(-1.0, 1.5, (3, 3, 21, 21)).astype(np.float32)
+    plan, y, n_int = check_graph(g, {"input": x}, g.outputs[0])
+    ops = [p["op"] for p in plan]
+    for op in ("QLinearAveragePool", "QLinearConcat", "QLinearMul", "QLinearGlobalAveragePool"):
+        assert op in ops
+    assert n_int >= 8 and y.size == 3 * 32   # [3, 32, 1, 1] (physically NHWC here)
+
+
 def test_qconv1d_graph(dev):
     """A 1-D convolution in QDQ form (3-D tensors) through the host framework:
     fused to QLinearConv, run on its exec_typed path, bit-exact."""

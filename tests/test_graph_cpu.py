@@ -126,3 +126,18 @@ def test_bert_fusion():
     uops = collections.Counter(p["op"] for p in u.plan())
     assert uops["MatMul"] == 4 and uops["Softmax"] == 2 and uops["Transpose"] == 8
     assert "MultiHeadAttention" not in uops
+
+
+def test_qoperator_graph_layouts():
+    """A QOperator-format graph (QLinearConv, QLinearAveragePool,
+    QLinearConcat, QLinearMul, QLinearGlobalAveragePool) resolves on the HIP
+    registry; the activations after the convolutions stay NHWC (the concat is
+    along channels, the per-channel Mul and the pools read NHWC)."""
+    g = synth.qoperator_net(batch=2, hw=20)
+    s = G.Session(g, device=False)
+    plan = s.plan()
+    ops = collections.Counter(p["op"] for p in plan)
+    assert ops["QLinearConv"] == 3 and ops["QLinearAveragePool"] == 1 and ops["QLinearConcat"] == 1
+    assert ops["QLinearMul"] == 2 and ops["QLinearGlobalAveragePool"] == 1
+    fmt = {p["name"]: s.tensor_info(p["outputs"][0])[3] for p in plan}
+    assert fmt["concat"] == 1 and fmt["mul_channel"] == 1 and fmt["mul_square"] == 1
