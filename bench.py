@@ -9,6 +9,9 @@ Prints ONE JSON line (driver contract). Workloads:
   resnet50  cfg3 (default, the headline metric): ResNet-50 v1.5 int8 QDQ graph,
             batch 256, 224x224, run through the C++ host framework (QDQ
             fusion, NHWC layouts, HIP operators); value = images/s
+  qoperator QOperator-format graph through the rest of the QLinear family
+            (AveragePool, Concat, Mul, GlobalAveragePool), batch 256, 224x224;
+            value = images/s, roofline = HBM of the family kernels
   qmatmul   cfg1: QLinearMatMul u8[1024,768] x i8[768,3072]; value = TOPS
   qconv     cfg2: QLinearConv 3x3 s1 p1, x u8[32,64,56,56], per-channel w
 A step is one pass of the path over one batch; inputs are resident in HBM
@@ -211,6 +214,29 @@ def roofline(ops, nbytes, kern_ms, prof):
     return r
 
 
+def layer_table(prof, args) -> list:
+    """Per-layer rows (hipEvents around every node): TOPS and % of the i8
+    MFMA peak for operators with algorithmic ops, GB/s and % of HBM peak for
+    the others; to stderr and optionally to --layers-out."""
+    layers = []
+    for r in prof:
+        t = r["ms"] / max(1, r["runs"])
+        row = {"name": r["name"], "op": r["op"], "branch": r["variant"], "ms": round(t, 4)}
+        if r["ops"]:
+            row["tops"] = round(r["ops"] / (t * 1e-3) / 1e12, 1)
+            row["pct_i8_peak"] = round(100 * row["tops"] / PEAK_I8_TOPS, 2)
+        else:
+            row["gbs"] = round(r["bytes"] / (t * 1e-3) / 1e9, 1)
+            row["pct_hbm"] = round(100 * row["gbs"] / PEAK_HBM_GBS, 2)
+        layers.append(row)
+    if args.layers_out:
+        with open(args.layers_out, "w") as f:
+            json.dump(layers, f, indent=1)
+    for row in layers:
+        print(json.dumps(row), file=sys.stderr)
+    return layers
+
+
 WORKLOADS = {
     "resnet50": "cfg3 ResNet-50 v1.5 int8 QDQ, batch {B}, 224x224 (53 QLinearConv, 16 QLinearAdd, "
                 "uint8 MaxPool, fp32 GAP+FC)",
@@ -261,22 +287,7 @@ def run_model(args, dev, model):
     g_launches = sum(kprof[k][0] for k in ("qgemm", "qgemm_add") if k in kprof)
     g_ms = sum(kprof[k][1] for k in ("qgemm", "qgemm_add") if k in kprof)
     qgemm_ms_per_step = g_ms / args.steps
-    layers = []
-    for r in prof:
-        t = r["ms"] / max(1, r["runs"])
-        row = {"name": r["name"], "op": r["op"], "branch": r["variant"], "ms": round(t, 4)}
-        if r["ops"]:
-            row["tops"] = round(r["ops"] / (t * 1e-3) / 1e12, 1)
-            row["pct_i8_peak"] = round(100 * row["tops"] / PEAK_I8_TOPS, 2)
-        else:
-            row["gbs"] = round(r["bytes"] / (t * 1e-3) / 1e9, 1)
-            row["pct_hbm"] = round(100 * row["gbs"] / PEAK_HBM_GBS, 2)
-        layers.append(row)
-    if args.layers_out:
-        with open(args.layers_out, "w") as f:
-            json.dump(layers, f, indent=1)
-    for row in layers:
-        print(json.dumps(row), file=sys.stderr)
+    layer_table(prof, args)
     # roofline of the dominant kernel over all its launches in a step
     avg_launch = qgemm_ms_per_step / (g_launches / args.steps)
     ops_per_launch = conv_ops / (g_launches / args.steps)
@@ -383,22 +394,7 @@ def run_bert(args, dev):
     mm_bytes = sum(r["bytes"] for r in prof if r["op"] == "QLinearMatMul")
     g_launches, g_ms = kprof["qgemm"]
     per_step = g_launches / args.steps
-    layers = []
-    for r in prof:
-        t = r["ms"] / max(1, r["runs"])
-        row = {"name": r["name"], "op": r["op"], "branch": r["variant"], "ms": round(t, 4)}
-        if r["ops"]:
-            row["tops"] = round(r["ops"] / (t * 1e-3) / 1e12, 1)
-            row["pct_i8_peak"] = round(100 * row["tops"] / PEAK_I8_TOPS, 2)
-        else:
-            row["gbs"] = round(r["bytes"] / (t * 1e-3) / 1e9, 1)
-            row["pct_hbm"] = round(100 * row["gbs"] / PEAK_HBM_GBS, 2)
-        layers.append(row)
-    if args.layers_out:
-        with open(args.layers_out, "w") as f:
-            json.dump(layers, f, indent=1)
-    for row in layers:
-        print(json.dumps(row), file=sys.stderr)
+    layer_table(prof, args)
     rl = roofline(mm_ops / per_step, mm_bytes / per_step, g_ms / g_launches, kprof)
     rl["traffic"], rl["traffic_source"] = None, None
     rl["note"] = (f"achieved = algorithmic int8 ops of the {round(per_step)} QLinearMatMul launches of "
@@ -428,6 +424,102 @@ def run_bert(args, dev):
         cpu_baseline={"value": round(cpu_seq_s, 3), "unit": "sequences/s", "cores": nthr,
                       "kind": "port", "sample": f"oracle replay of the fused plan on 1 sequence, "
                                                 f"{reps} runs (scalar C + OpenMP, numpy fp32 glue)"},
+        dtype="u8",
+    )
+
+
+# QLinear-family operators of the QOperator graph and the launch-profiler
+# name of the kernel each one runs
+QFAMILY = {"QLinearMul": "qlinear_mul", "QLinearAveragePool": "qlinear_avgpool",
+           "QLinearConcat": "qlinear_concat", "QLinearGlobalAveragePool": "qlinear_global_avgpool"}
+
+
+def run_qoperator(args, dev):
+    """QOperator-format graph (quantized operators instead of QDQ pairs):
+    QLinearConv -> QLinearAveragePool -> two QLinearConv branches ->
+    QLinearConcat -> QLinearMul (per channel, then squared) ->
+    QLinearGlobalAveragePool, batch 256 at 224x224. The roofline is the
+    HBM one of the QLinear-family kernel that takes the most time per step;
+    every family kernel is listed with its own achieved GB/s."""
+    import numpy as np
+    import torch
+
+    from nnr_amd import graph as G, synth
+    from oracle import graph_oracle
+    from oracle import pyoracle as O
+
+    B, HW = args.batch, 224
+    g = synth.qoperator_net(batch=B, hw=HW)
+    rng = np.random.default_rng(24)
+    x = rng.uniform(-1.0, 1.5, (B, 3, HW, HW)).astype(np.float32)
+    s = G.Session(g)
+    s.set_input("input", x)
+    s.run()
+    torch.cuda.synchronize()
+    plan = s.plan()
+    fmt = lambda n: s.tensor_info(n)[3]
+    # parity gate: the oracle replays the plan on the first images
+    ng = 2
+    env = graph_oracle.run_plan(plan, g, {"input": x[:ng]}, fmt)
+    for p in plan:
+        o = p["outputs"][0]
+        dev_t, _ = s.output(o)
+        if dev_t.dtype in (np.uint8, np.int8):
+            assert np.array_equal(dev_t[:ng], env[o]), f"parity gate failed at {p['name']}"
+        else:
+            assert np.allclose(dev_t[:ng], env[o], atol=1e-3, rtol=1e-4), p["name"]
+    ms = time_steps(s.run, args)
+    s.enable_profiling(True)
+    for _ in range(args.steps):
+        s.run()
+    torch.cuda.synchronize()
+    prof = s.profile()
+    s.enable_profiling(False)
+    kprof = profile_steps(s.run, args)
+    layer_table(prof, args)
+    family = {}
+    for op, kern in QFAMILY.items():
+        if kern not in kprof:
+            continue
+        n, kms = kprof[kern]
+        nbytes = sum(r["bytes"] for r in prof if r["op"] == op)   # per run = per step
+        gbs = nbytes / (kms / args.steps * 1e-3) / 1e9
+        family[kern] = {"op": op, "achieved": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+                        "launches_per_step": round(n / args.steps), "alg_bytes_per_step": nbytes,
+                        "avg_launch_ms": round(kms / n, 5), "ms_per_step": round(kms / args.steps, 5)}
+    assert len(family) == len(QFAMILY), sorted(family)
+    top = max(family, key=lambda k: family[k]["ms_per_step"])
+    f = family[top]
+    rl = {"kernel": top, "bound": "hbm", "achieved": f["achieved"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+          "frac": f["frac"], "traffic": None, "avg_launch_ms": f["avg_launch_ms"],
+          "alg_bytes_per_launch": f["alg_bytes_per_step"] / f["launches_per_step"],
+          "family": family,
+          "launches": {k: {"n": v[0], "avg_ms": round(v[1] / max(1, v[0]), 5)} for k, v in kprof.items()},
+          "note": "achieved = algorithmic bytes (inputs read once + output written) of the operator's "
+                  "launches in one step / their kernel time (hipEvents per launch)"}
+    nthr = host_threads()
+    O.set_threads(nthr)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        graph_oracle.run_plan(plan, g, {"input": x[:1]}, fmt)
+        reps += 1
+        if time.perf_counter() - t0 > 5.0 or reps >= 5:
+            break
+    cpu_img_s = reps / (time.perf_counter() - t0)
+    return dict(
+        metric="QOperator-format int8 graph images/sec b256 (QLinearConv, QLinearAveragePool, "
+               "QLinearConcat, QLinearMul, QLinearGlobalAveragePool), 1 GPU",
+        value=round(B / (ms * 1e-3), 1), unit="images/s", ms_per_step=ms,
+        config={"workload": f"QOperator graph, batch {B}, {HW}x{HW}: QLinearConv 3x3 (3->16), "
+                            "QLinearAveragePool 3x3/2 pad 1, QLinearConv 1x1 (16->24) and 3x3 (16->8), "
+                            "QLinearConcat (24+8, one part copied), QLinearMul by a per-channel "
+                            "constant and by itself, QLinearGlobalAveragePool",
+                "global_batch": B, "device_bytes": s.device_bytes(),
+                "ops": [p["op"] + (":" + p["variant"] if p["variant"] else "") for p in plan]},
+        roofline=rl,
+        cpu_baseline={"value": round(cpu_img_s, 3), "unit": "images/s", "cores": nthr, "kind": "port",
+                      "sample": f"oracle replay of the plan on 1 image, {reps} runs (scalar C + OpenMP)"},
         dtype="u8",
     )
 
@@ -465,7 +557,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="resnet50",
-                    choices=["resnet50", "mobilenetv2", "bert", "qconv", "qmatmul", "hbm_copy"])
+                    choices=["resnet50", "mobilenetv2", "bert", "qoperator", "qconv", "qmatmul",
+                             "hbm_copy"])
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
     args = ap.parse_args()
@@ -477,7 +570,7 @@ def main():
     dev = torch.device("cuda:0")
     run = {"resnet50": lambda a, d: run_model(a, d, "resnet50"),
            "mobilenetv2": lambda a, d: run_model(a, d, "mobilenetv2"),
-           "bert": run_bert,
+           "bert": run_bert, "qoperator": run_qoperator,
            "qconv": run_qconv, "qmatmul": run_qmatmul, "hbm_copy": run_hbm_copy}[args.config]
     res = run(args, dev)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,

@@ -549,66 +549,137 @@ namespace nnrh {
 // reference expression element by element, including its 16-wide body /
 // scalar tail split, so results are bit-identical.
 
+// byte k of a word as the quantized type (0 u8, 1 s8)
+__device__ __forceinline__ int byte_q(uint32_t w, int k, int dt) {
+    const uint32_t b = (w >> (8 * k)) & 0xffu;
+    return dt == 0 ? (int)b : (int)(int8_t)b;
+}
+
 // QLinearMul (QLinearMul.cpp:25-231). kind as QLinearAdd: 0 same shape, 1 B
-// scalar, 2 A scalar, 3 per channel (a full, b [C]); cs = fl(fl(a_s*b_s)/y_s)
+// scalar, 2 A scalar, 3 per channel (a full, b [C]); cs = fl(fl(a_s*b_s)/y_s).
+// One element: `a` and `b` are the element's operands (b: B's element for
+// kind 0, B's channel value for kind 3); `body` marks the 16-wide body.
+__device__ __forceinline__ int qmul_elem(const QMulArgs& p, int a, int b, bool body) {
+    if (p.kind == 0) {
+        if (body) {
+            // fma(fl(fl(a - a_zp) * fl(b - b_zp)), cs, y_zp), roundscale, min / max
+            const float va = (float)a - (float)p.a_zp, vb = (float)b - (float)p.b_zp;
+            const float v = __builtin_fmaf(va * vb, p.cs, (float)p.y_zp);
+            return (int)clamp_minmax(__builtin_rintf(v), (float)p.lo, (float)p.hi);
+        }
+        const float t1 = p.cs * (float)(a - p.a_zp);
+        const float v = t1 * (float)(b - p.b_zp) + (float)p.y_zp;
+        return clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
+    }
+    if (p.kind == 1 || p.kind == 2) {
+        // a: the full operand's element, b: the scalar operand's value
+        const bool b_sc = p.kind == 1;
+        const float cval = b_sc ? p.cs * (float)(b - p.b_zp) : p.cs * (float)(b - p.a_zp);
+        const float d = b_sc ? (float)(a - p.a_zp) : (float)(a - p.b_zp);
+        return clampi(x86_f2i(__builtin_rintf(cval * d + (float)p.y_zp)), p.lo, p.hi);
+    }
+    const float chv = p.cs * (float)(b - p.b_zp);
+    if (body) {
+        const float v = __builtin_fmaf((float)a - (float)p.a_zp, chv, (float)p.y_zp);
+        return (int)clamp_minmax(__builtin_rintf(v), (float)p.lo, (float)p.hi);
+    }
+    return clampi(x86_f2i(__builtin_rintf(chv * (float)(a - p.a_zp) + (float)p.y_zp)), p.lo, p.hi);
+}
+
+// one element per thread: any shape, type or alignment
 __global__ __launch_bounds__(256) void qmul_kernel(QMulArgs p) {
     const long long stride = (long long)gridDim.x * blockDim.x;
+    const bool b_sc = p.kind == 1, a_sc = p.kind == 2;
     for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < p.n; i += stride) {
-        int q;
+        int a, b;
+        bool body = false;
         if (p.kind == 0) {
-            const long long body = p.n - p.n % 16;
-            const int a = ld_q(p.a, p.dt, i), b = ld_q(p.b, p.dt, i);
-            if (i < body) {
-                // fma(fl(fl(a - a_zp) * fl(b - b_zp)), cs, y_zp), roundscale, min / max
-                const float va = (float)a - (float)p.a_zp, vb = (float)b - (float)p.b_zp;
-                float v = __builtin_fmaf(va * vb, p.cs, (float)p.y_zp);
-                v = clamp_minmax(__builtin_rintf(v), (float)p.lo, (float)p.hi);
-                q = (int)v;
-            } else {
-                const float t1 = p.cs * (float)(a - p.a_zp);
-                const float v = t1 * (float)(b - p.b_zp) + (float)p.y_zp;
-                q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
-            }
-        } else if (p.kind == 1 || p.kind == 2) {
-            const bool b_sc = p.kind == 1;
-            const float cval = b_sc ? p.cs * (float)(ld_q(p.b, p.dt, 0) - p.b_zp)
-                                    : p.cs * (float)(ld_q(p.a, p.dt, 0) - p.a_zp);
-            const float d = b_sc ? (float)(ld_q(p.a, p.dt, i) - p.a_zp) : (float)(ld_q(p.b, p.dt, i) - p.b_zp);
-            const float v = cval * d + (float)p.y_zp;
-            q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
+            a = ld_q(p.a, p.dt, i);
+            b = ld_q(p.b, p.dt, i);
+            body = i < p.n - p.n % 16;
+        } else if (b_sc || a_sc) {
+            a = b_sc ? ld_q(p.a, p.dt, i) : ld_q(p.b, p.dt, i);
+            b = b_sc ? ld_q(p.b, p.dt, 0) : ld_q(p.a, p.dt, 0);
         } else {
             int c;
             long long inner;
             if (p.y_nhwc) { c = (int)(i % p.C); inner = c; }
             else { c = (int)((i / p.HW) % p.C); inner = i % p.HW; }
-            const long long body = p.y_nhwc ? (p.C - p.C % 16) : (p.HW - p.HW % 16);
-            const int x = ld_q(p.a, p.dt, i);
-            const float chv = p.cs * (float)(ld_q(p.b, p.dt, c) - p.b_zp);
-            if (inner < body) {
-                float v = __builtin_fmaf((float)x - (float)p.a_zp, chv, (float)p.y_zp);
-                v = clamp_minmax(__builtin_rintf(v), (float)p.lo, (float)p.hi);
-                q = (int)v;
-            } else {
-                const float v = chv * (float)(x - p.a_zp) + (float)p.y_zp;
-                q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
-            }
+            a = ld_q(p.a, p.dt, i);
+            b = ld_q(p.b, p.dt, c);
+            body = inner < (p.y_nhwc ? (p.C - p.C % 16) : (p.HW - p.HW % 16));
         }
-        st_q(p.y, p.dt, i, q);
+        st_q(p.y, p.dt, i, qmul_elem(p, a, b, body));
+    }
+}
+
+// 16 elements per thread (one 16-byte load per operand, one store): n % 16
+// == 0, every streamed operand 16-byte aligned and, per channel, C % 16 == 0
+// (NHWC) or HW % 16 == 0 (NCHW). Then every element is in the 16-wide body
+// (kind 0: n - n%16 = n; kind 3: the body bound is C or HW itself).
+__global__ __launch_bounds__(256) void qmul16_kernel(QMulArgs p) {
+    const long long nv = p.n / 16;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    const bool b_sc = p.kind == 1, a_sc = p.kind == 2;
+    const void* full = a_sc ? p.b : p.a;
+    const int sval = b_sc ? ld_q(p.b, p.dt, 0) : (a_sc ? ld_q(p.a, p.dt, 0) : 0);
+    for (long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x; v < nv; v += stride) {
+        const uint4 av = ((const uint4*)full)[v];
+        uint4 bv = make_uint4(0, 0, 0, 0);
+        int bc = 0;
+        if (p.kind == 0) {
+            bv = ((const uint4*)p.b)[v];
+        } else if (p.kind == 3) {
+            const long long i0 = v * 16;
+            if (p.y_nhwc) bv = *(const uint4*)((const uint8_t*)p.b + (i0 % p.C));
+            else bc = ld_q(p.b, p.dt, (i0 / p.HW) % p.C);
+        }
+        const uint32_t aw[4] = {av.x, av.y, av.z, av.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t o = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int a = byte_q(aw[k], j, p.dt);
+                int b;
+                if (p.kind == 0 || (p.kind == 3 && p.y_nhwc)) b = byte_q(bw[k], j, p.dt);
+                else if (p.kind == 3) b = bc;
+                else b = sval;
+                o |= ((uint32_t)qmul_elem(p, a, b, true) & 0xffu) << (8 * j);
+            }
+            ow[k] = o;
+        }
+        ((uint4*)p.y)[v] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
     }
 }
 
 hipError_t launch_qmul(const QMulArgs& p, hipStream_t s) {
     if (p.n <= 0) return hipSuccess;
-    long long blocks = (p.n + 255) / 256;
+    const auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+    bool vec = p.n % 16 == 0 && al(p.y) && al(p.kind == 2 ? p.b : p.a);
+    if (p.kind == 0) vec = vec && al(p.b);
+    if (p.kind == 3) vec = vec && (p.y_nhwc ? (p.C % 16 == 0 && al(p.b)) : p.HW % 16 == 0);
+    const long long work = vec ? p.n / 16 : p.n;
+    long long blocks = (work + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(qmul_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
+    if (vec) hipLaunchKernelGGL(qmul16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(qmul_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
 // QLinearGlobalAveragePool (QLinearGlobalAveragePool.cpp:38-60), RQ-F: the
 // int32 sum of a (n, c) plane (exact in any order), minus x_zp * spatial,
 // times rs = fl(x_s / fl(y_s * spatial)), nearbyint, + y_zp, clamp.
-// NCHW: one wave per plane; NHWC: one thread per (n, c), channels coalesced.
+__device__ __forceinline__ int qgap_out(uint32_t sum, int spatial, float rs, int x_zp, int y_zp, int lo, int hi) {
+    sum -= (uint32_t)x_zp * (uint32_t)spatial;
+    int32_t q = x86_f2i(__builtin_rintf((float)(int32_t)sum * rs));
+    q = (int32_t)((uint32_t)q + (uint32_t)y_zp);
+    return clampi(q, lo, hi);
+}
+
+// Any layout / alignment. NCHW: one wave per plane; NHWC: one thread per
+// (n, c), channels coalesced.
 __global__ __launch_bounds__(256) void qgap_kernel(const void* __restrict x, void* __restrict y, int N, int C,
                                                    int spatial, int nhwc, int dt, float rs, int x_zp, int y_zp,
                                                    int lo, int hi) {
@@ -627,16 +698,164 @@ __global__ __launch_bounds__(256) void qgap_kernel(const void* __restrict x, voi
         for (int off = 32; off > 0; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off, 64);
         if (lane) return;
     }
-    sum -= (uint32_t)x_zp * (uint32_t)spatial;
-    int32_t q = x86_f2i(__builtin_rintf((float)(int32_t)sum * rs));
-    q = (int32_t)((uint32_t)q + (uint32_t)y_zp);
-    st_q(y, dt, nc, clampi(q, lo, hi));
+    st_q(y, dt, nc, qgap_out(sum, spatial, rs, x_zp, y_zp, lo, hi));
+}
+
+// NCHW, spatial % 16 == 0, x 16-byte aligned: one wave per plane, 16 bytes
+// per lane per load, byte sums by v_sad_u8 (int8 is biased to uint8 by
+// flipping the sign bit, then 128 * spatial is taken off)
+__global__ __launch_bounds__(256) void qgap_nchw16_kernel(const void* __restrict x, void* __restrict y, int N, int C,
+                                                          int spatial, int dt, float rs, int x_zp, int y_zp, int lo,
+                                                          int hi) {
+    const long long nc = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (nc >= (long long)N * C) return;
+    const uint4* p = (const uint4*)((const uint8_t*)x + nc * spatial);
+    const uint32_t flip = dt ? 0x80808080u : 0u;
+    uint32_t sum = 0;
+    const int nv = spatial / 16;
+    for (int v = lane; v < nv; v += 64) {
+        const uint4 q = p[v];
+        sum = __builtin_amdgcn_sad_u8(q.x ^ flip, 0u, sum);
+        sum = __builtin_amdgcn_sad_u8(q.y ^ flip, 0u, sum);
+        sum = __builtin_amdgcn_sad_u8(q.z ^ flip, 0u, sum);
+        sum = __builtin_amdgcn_sad_u8(q.w ^ flip, 0u, sum);
+    }
+    for (int off = 32; off > 0; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off, 64);
+    if (lane) return;
+    if (dt) sum -= 128u * (uint32_t)spatial;
+    st_q(y, dt, nc, qgap_out(sum, spatial, rs, x_zp, y_zp, lo, hi));
+}
+
+// NHWC, C % 16 == 0, x 16-byte aligned. Block (n, channel slice): each
+// thread owns one 16-channel group and every P-th pixel of image n, loads
+// 16 bytes per pixel (a wave reads whole pixel rows) and keeps the 16 sums
+// as pairs of 16-bit lanes (bytes 0/2 and 1/3 of each word), flushed to
+// 32-bit totals every 256 pixels (256 * 255 < 2^16). The P partial sums of a
+// channel are added in LDS.
+constexpr int QGAP_NT = 512;
+constexpr int QGAP_UNROLL = 8;
+__global__ __launch_bounds__(QGAP_NT) void qgap_nhwc16_kernel(const void* __restrict x, void* __restrict y, int C,
+                                                              int spatial, int dt, float rs, int x_zp, int y_zp,
+                                                              int lo, int hi) {
+    __shared__ uint32_t red[QGAP_NT * 16];
+    const int G = C / 16;
+    const int n = blockIdx.x;
+    const int t = threadIdx.x;
+    int P, g, pl;
+    if (G >= QGAP_NT) { P = 1; g = blockIdx.y * QGAP_NT + t; pl = 0; }
+    else { P = QGAP_NT / G; g = t % G; pl = t / G; }
+    const bool active = g < G && pl < P;
+    const uint32_t flip = dt ? 0x80808080u : 0u;
+    uint32_t tot[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) tot[j] = 0;
+    if (active) {
+        const uint4* base = (const uint4*)((const uint8_t*)x + (size_t)n * spatial * C) + g;
+        long long s = pl;
+        while (s < spatial) {
+            // one run: at most 256 pixels of this thread before a flush
+            const long long run_end = s + 256LL * P < spatial ? s + 256LL * P : spatial;
+            uint32_t acc[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[k] = 0;
+            for (; s + (QGAP_UNROLL - 1) * (long long)P < run_end; s += QGAP_UNROLL * (long long)P) {
+                uint4 v[QGAP_UNROLL];
+#pragma unroll
+                for (int u = 0; u < QGAP_UNROLL; ++u) v[u] = base[(size_t)(s + u * (long long)P) * G];
+#pragma unroll
+                for (int u = 0; u < QGAP_UNROLL; ++u) {
+                    const uint32_t w[4] = {v[u].x ^ flip, v[u].y ^ flip, v[u].z ^ flip, v[u].w ^ flip};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        acc[2 * k] += w[k] & 0x00ff00ffu;
+                        acc[2 * k + 1] += (w[k] >> 8) & 0x00ff00ffu;
+                    }
+                }
+            }
+            for (; s < run_end; s += P) {
+                const uint4 v = base[(size_t)s * G];
+                const uint32_t w[4] = {v.x ^ flip, v.y ^ flip, v.z ^ flip, v.w ^ flip};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    acc[2 * k] += w[k] & 0x00ff00ffu;
+                    acc[2 * k + 1] += (w[k] >> 8) & 0x00ff00ffu;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                tot[4 * k + 0] += acc[2 * k] & 0xffffu;
+                tot[4 * k + 2] += acc[2 * k] >> 16;
+                tot[4 * k + 1] += acc[2 * k + 1] & 0xffffu;
+                tot[4 * k + 3] += acc[2 * k + 1] >> 16;
+            }
+        }
+    }
+    const uint32_t bias = dt ? 128u * (uint32_t)spatial : 0u;
+    if (P == 1) {
+        if (!active) return;
+        uint32_t ow[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t o = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                o |= ((uint32_t)qgap_out(tot[4 * k + j] - bias, spatial, rs, x_zp, y_zp, lo, hi) & 0xffu) << (8 * j);
+            ow[k] = o;
+        }
+        uint8_t* yp = (uint8_t*)y + (size_t)n * C + (size_t)g * 16;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) yp[4 * k + j] = (uint8_t)(ow[k] >> (8 * j));
+        return;
+    }
+    // partials: red[pl * C + c]
+    if (active) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) red[pl * C + g * 16 + j] = tot[j];
+    }
+    __syncthreads();
+    // with few channels, two levels: thread (c, q) adds partials q, q + Q,
+    // ...; then each channel adds its Q values. R rows of partials are left.
+    const int Q = QGAP_NT / C;
+    int R = P;
+    if (Q >= 2) {
+        uint32_t part = 0;
+        const int c = t % C, q = t / C;
+        if (q < Q)
+            for (int p2 = q; p2 < P; p2 += Q) part += red[p2 * C + c];
+        __syncthreads();
+        if (q < Q) red[q * C + c] = part;
+        __syncthreads();
+        R = Q;
+    }
+    for (int cc = t; cc < C; cc += QGAP_NT) {
+        uint32_t sum = 0;
+        for (int r = 0; r < R; ++r) sum += red[r * C + cc];
+        st_q(y, dt, (long long)n * C + cc, qgap_out(sum - bias, spatial, rs, x_zp, y_zp, lo, hi));
+    }
 }
 
 hipError_t launch_qgap(const void* x, void* y, int N, int C, int spatial, int nhwc, int dt, float rs, int x_zp,
                        int y_zp, int lo, int hi, hipStream_t s) {
     const long long rows = (long long)N * C;
     if (rows <= 0) return hipSuccess;
+    const bool al = ((uintptr_t)x & 15) == 0;
+    if (nhwc && al && C % 16 == 0 && spatial > 0) {
+        const int G = C / 16;
+        const unsigned slices = G >= QGAP_NT ? (unsigned)((G + QGAP_NT - 1) / QGAP_NT) : 1u;
+        if (slices <= 65535u) {
+            hipLaunchKernelGGL(qgap_nhwc16_kernel, dim3((unsigned)N, slices), dim3(QGAP_NT), 0, s, x, y, C, spatial,
+                               dt, rs, x_zp, y_zp, lo, hi);
+            return hipGetLastError();
+        }
+    }
+    if (!nhwc && al && spatial % 16 == 0) {
+        hipLaunchKernelGGL(qgap_nchw16_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, y, N, C,
+                           spatial, dt, rs, x_zp, y_zp, lo, hi);
+        return hipGetLastError();
+    }
     const long long blocks = nhwc ? (rows + 255) / 256 : (rows + 3) / 4;
     hipLaunchKernelGGL(qgap_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, N, C, spatial, nhwc, dt, rs,
                        x_zp, y_zp, lo, hi);
@@ -645,7 +864,16 @@ hipError_t launch_qgap(const void* x, void* y, int N, int C, int spatial, int nh
 
 // QLinearAveragePool (QLinearAveragePool.cpp:67-115): in-image taps only,
 // avg = fl(fl(sum * x_s) / count), q = nearbyint(fl(avg / y_s)) + y_zp, clamp.
-// One thread per output element, NCHW or NHWC.
+__device__ __forceinline__ int qavg_out(int32_t sum, int count, float x_s, float y_s, int y_zp, int lo, int hi) {
+    if (count == 0) count = 1;
+    const float t = (float)sum * x_s;
+    const float avg = t / (float)count;
+    int32_t q = x86_f2i(__builtin_rintf(avg / y_s));
+    q = (int32_t)((uint32_t)q + (uint32_t)y_zp);
+    return clampi(q, lo, hi);
+}
+
+// One thread per output element, NCHW or NHWC, any alignment.
 __global__ __launch_bounds__(256) void qavgpool_kernel(const void* __restrict x, void* __restrict y, int N, int C,
                                                        int iH, int iW, int oH, int oW, int kH, int kW, int sH,
                                                        int sW, int pH, int pW, int nhwc, int dt, float x_s,
@@ -676,12 +904,63 @@ __global__ __launch_bounds__(256) void qavgpool_kernel(const void* __restrict x,
                 ++count;
             }
         }
-        if (count == 0) count = 1;
-        const float t = (float)sum * x_s;
-        const float avg = t / (float)count;
-        int32_t q = x86_f2i(__builtin_rintf(avg / y_s));
-        q = (int32_t)((uint32_t)q + (uint32_t)y_zp);
-        st_q(y, dt, o, clampi(q, lo, hi));
+        st_q(y, dt, o, qavg_out(sum, count, x_s, y_s, y_zp, lo, hi));
+    }
+}
+
+// NHWC, C % 16 == 0, x and y 16-byte aligned, kH * kW <= 256: one thread per
+// (output pixel, 16-channel group), one 16-byte load per in-image tap, the 16
+// sums kept as 16-bit lane pairs (at most 256 taps of 255). The int32 sum of
+// (x - x_zp) over the taps is sum(x) - count * x_zp exactly.
+__global__ __launch_bounds__(256) void qavgpool_nhwc16_kernel(const void* __restrict x, void* __restrict y, int N,
+                                                              int C, int iH, int iW, int oH, int oW, int kH, int kW,
+                                                              int sH, int sW, int pH, int pW, int dt, float x_s,
+                                                              int x_zp, float y_s, int y_zp, int lo, int hi) {
+    const int G = C / 16;
+    const long long total = (long long)N * oH * oW * G;
+    const uint32_t flip = dt ? 0x80808080u : 0u;
+    for (long long o = (long long)blockIdx.x * 256 + threadIdx.x; o < total; o += (long long)gridDim.x * 256) {
+        const int g = (int)(o % G);
+        long long r = o / G;
+        const int ow = (int)(r % oW);
+        r /= oW;
+        const int oh = (int)(r % oH);
+        const int n = (int)(r / oH);
+        uint32_t acc[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] = 0;
+        int count = 0;
+        const int h0 = oh * sH - pH, w0 = ow * sW - pW;
+        for (int kh = 0; kh < kH; ++kh) {
+            const int ih = h0 + kh;
+            if (ih < 0 || ih >= iH) continue;
+            const uint4* row = (const uint4*)((const uint8_t*)x + (((long long)n * iH + ih) * iW) * C) + g;
+            for (int kw = 0; kw < kW; ++kw) {
+                const int iw = w0 + kw;
+                if (iw < 0 || iw >= iW) continue;
+                const uint4 v = row[(long long)iw * G];
+                const uint32_t w[4] = {v.x ^ flip, v.y ^ flip, v.z ^ flip, v.w ^ flip};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    acc[2 * k] += w[k] & 0x00ff00ffu;
+                    acc[2 * k + 1] += (w[k] >> 8) & 0x00ff00ffu;
+                }
+                ++count;
+            }
+        }
+        // channel 4k+j: pair word 2k holds bytes 0 / 2, word 2k+1 bytes 1 / 3
+        const int32_t off = (dt ? 128 : 0) * count + count * x_zp;
+        uint32_t ow_[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int32_t s0 = (int32_t)(acc[2 * k] & 0xffffu), s2 = (int32_t)(acc[2 * k] >> 16);
+            const int32_t s1 = (int32_t)(acc[2 * k + 1] & 0xffffu), s3 = (int32_t)(acc[2 * k + 1] >> 16);
+            ow_[k] = ((uint32_t)qavg_out(s0 - off, count, x_s, y_s, y_zp, lo, hi) & 0xffu) |
+                     (((uint32_t)qavg_out(s1 - off, count, x_s, y_s, y_zp, lo, hi) & 0xffu) << 8) |
+                     (((uint32_t)qavg_out(s2 - off, count, x_s, y_s, y_zp, lo, hi) & 0xffu) << 16) |
+                     (((uint32_t)qavg_out(s3 - off, count, x_s, y_s, y_zp, lo, hi) & 0xffu) << 24);
+        }
+        ((uint4*)y)[o] = make_uint4(ow_[0], ow_[1], ow_[2], ow_[3]);
     }
 }
 
@@ -690,10 +969,15 @@ hipError_t launch_qavgpool(const void* x, void* y, int N, int C, int iH, int iW,
                            int y_zp, int lo, int hi, hipStream_t s) {
     const long long total = (long long)N * C * oH * oW;
     if (total <= 0) return hipSuccess;
-    long long blocks = (total + 255) / 256;
+    const bool vec = nhwc && C % 16 == 0 && (((uintptr_t)x | (uintptr_t)y) & 15) == 0 && kH * kW <= 256;
+    long long blocks = ((vec ? total / 16 : total) + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(qavgpool_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, N, C, iH, iW, oH, oW, kH,
-                       kW, sH, sW, pH, pW, nhwc, dt, x_s, x_zp, y_s, y_zp, lo, hi);
+    if (vec)
+        hipLaunchKernelGGL(qavgpool_nhwc16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, N, C, iH, iW, oH,
+                           oW, kH, kW, sH, sW, pH, pW, dt, x_s, x_zp, y_s, y_zp, lo, hi);
+    else
+        hipLaunchKernelGGL(qavgpool_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, N, C, iH, iW, oH, oW, kH,
+                           kW, sH, sW, pH, pW, nhwc, dt, x_s, x_zp, y_s, y_zp, lo, hi);
     return hipGetLastError();
 }
 
@@ -702,27 +986,61 @@ hipError_t launch_qavgpool(const void* x, void* y, int N, int C, int iH, int iW,
 // zero point copy; otherwise the first count - count % 16 elements of a chunk
 // (count >= 16) take the 16-wide body rne(clamp(fma(rs, x - x_zp, y_zp))),
 // the rest the scalar nearbyint(fl(rs * (x - x_zp)) + y_zp), clamped.
+__device__ __forceinline__ int qconcat_elem(int xv, bool body, float rs, int x_zp, int y_zp, int lo, int hi) {
+    if (body) {
+        float v = __builtin_fmaf(rs, (float)xv - (float)x_zp, (float)y_zp);
+        v = v > (float)lo ? v : (float)lo;
+        v = v < (float)hi ? v : (float)hi;
+        return (int)__builtin_rintf(v);
+    }
+    const float v = rs * (float)(xv - x_zp) + (float)y_zp;
+    return clampi(x86_f2i(__builtin_rintf(v)), lo, hi);
+}
+
+// W bytes per thread (W = 1, 4, 8 or 16, dividing count, y_row and y_off, both
+// pointers W-aligned). W divides 16, so a unit lies wholly in a chunk's body
+// or wholly in its tail.
+template <int W>
 __global__ __launch_bounds__(256) void qconcat_kernel(const void* __restrict x, void* __restrict y, long long outer,
                                                       long long count, long long y_row, long long y_off, int dt,
                                                       int copy, float rs, int x_zp, int y_zp, int lo, int hi) {
-    const long long total = outer * count;
+    const long long units = outer * count / W;
     const long long body = count >= 16 ? count - count % 16 : 0;
-    for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
+    for (long long u = (long long)blockIdx.x * 256 + threadIdx.x; u < units; u += (long long)gridDim.x * 256) {
+        const long long e = u * W;
         const long long o = e / count, i = e - o * count;
-        const int xv = ld_q(x, dt, e);
-        int q;
-        if (copy) {
-            q = xv;
-        } else if (i < body) {
-            float v = __builtin_fmaf(rs, (float)xv - (float)x_zp, (float)y_zp);
-            v = v > (float)lo ? v : (float)lo;
-            v = v < (float)hi ? v : (float)hi;
-            q = (int)__builtin_rintf(v);
+        uint8_t* dst = (uint8_t*)y + o * y_row + y_off + i;
+        if constexpr (W == 1) {
+            const int xv = ld_q(x, dt, e);
+            *dst = (uint8_t)(copy ? xv : qconcat_elem(xv, i < body, rs, x_zp, y_zp, lo, hi));
         } else {
-            const float v = rs * (float)(xv - x_zp) + (float)y_zp;
-            q = clampi(x86_f2i(__builtin_rintf(v)), lo, hi);
+            constexpr int NW = W / 4;
+            uint32_t w[NW];
+            if constexpr (W == 16) {
+                const uint4 v = ((const uint4*)x)[u];
+                w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+            } else if constexpr (W == 8) {
+                const uint2 v = ((const uint2*)x)[u];
+                w[0] = v.x; w[1] = v.y;
+            } else {
+                w[0] = ((const uint32_t*)x)[u];
+            }
+            if (!copy) {
+                const bool bd = i < body;
+#pragma unroll
+                for (int k = 0; k < NW; ++k) {
+                    uint32_t r = 0;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        r |= ((uint32_t)qconcat_elem(byte_q(w[k], j, dt), bd, rs, x_zp, y_zp, lo, hi) & 0xffu)
+                             << (8 * j);
+                    w[k] = r;
+                }
+            }
+            if constexpr (W == 16) *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
+            else if constexpr (W == 8) *(uint2*)dst = make_uint2(w[0], w[1]);
+            else *(uint32_t*)dst = w[0];
         }
-        st_q(y, dt, o * y_row + y_off + i, q);
     }
 }
 
@@ -731,10 +1049,23 @@ hipError_t launch_qconcat_part(const void* x, void* y, long long outer, long lon
                                hipStream_t s) {
     const long long total = outer * count;
     if (total <= 0) return hipSuccess;
-    long long blocks = (total + 255) / 256;
+    const uintptr_t al = (uintptr_t)x | (uintptr_t)y | (uintptr_t)count | (uintptr_t)y_row | (uintptr_t)y_off;
+    const int W = (al & 15) == 0 ? 16 : (al & 7) == 0 ? 8 : (al & 3) == 0 ? 4 : 1;
+    long long blocks = (total / W + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(qconcat_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, outer, count, y_row, y_off,
-                       dt, copy, rs, x_zp, y_zp, lo, hi);
+    const dim3 grid((unsigned)blocks), block(256);
+    if (W == 16)
+        hipLaunchKernelGGL((qconcat_kernel<16>), grid, block, 0, s, x, y, outer, count, y_row, y_off, dt, copy, rs,
+                           x_zp, y_zp, lo, hi);
+    else if (W == 8)
+        hipLaunchKernelGGL((qconcat_kernel<8>), grid, block, 0, s, x, y, outer, count, y_row, y_off, dt, copy, rs,
+                           x_zp, y_zp, lo, hi);
+    else if (W == 4)
+        hipLaunchKernelGGL((qconcat_kernel<4>), grid, block, 0, s, x, y, outer, count, y_row, y_off, dt, copy, rs,
+                           x_zp, y_zp, lo, hi);
+    else
+        hipLaunchKernelGGL((qconcat_kernel<1>), grid, block, 0, s, x, y, outer, count, y_row, y_off, dt, copy, rs,
+                           x_zp, y_zp, lo, hi);
     return hipGetLastError();
 }
 

@@ -61,9 +61,14 @@ bool operator_t::reshape() {
 }
 
 double operator_t::num_bytes() const {
+    // a tensor given as two inputs (QLinearMul of x with x) is read once
     double b = 0;
-    for (auto* t : inputs)
-        if (t) b += (double)t->nbytes();
+    for (size_t i = 0; i < inputs.size(); ++i) {
+        tensor_t* t = inputs[i];
+        bool dup = false;
+        for (size_t j = 0; j < i && !dup; ++j) dup = inputs[j] == t;
+        if (t && !dup) b += (double)t->nbytes();
+    }
     for (auto* t : outputs)
         if (t) b += (double)t->nbytes();
     return b;

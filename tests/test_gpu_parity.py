@@ -324,10 +324,11 @@ def test_qlinear_add(dev, kind, y_nhwc):
 
 @pytest.mark.parametrize("kind,shape_b,nhwc", [(0, None, 0), (1, (1,), 0), (2, "a1", 0), (3, "c", 0), (3, "c", 1)])
 @pytest.mark.parametrize("dt", [np.uint8, np.int8])
-def test_qlinear_mul(dev, kind, shape_b, nhwc, dt):
-    rng = np.random.default_rng(kind * 7 + nhwc + (dt == np.int8))
+@pytest.mark.parametrize("N,C,Hh,W", [(2, 19, 5, 7),     # 665 per image: ragged 16-wide body, one byte a thread
+                                      (3, 32, 4, 8)])    # 16 elements a thread (n, C and HW multiples of 16)
+def test_qlinear_mul(dev, kind, shape_b, nhwc, dt, N, C, Hh, W):
+    rng = np.random.default_rng(kind * 7 + nhwc + (dt == np.int8) + C)
     info = (0, 256) if dt == np.uint8 else (-128, 128)
-    N, C, Hh, W = 2, 19, 5, 7          # 665 per image: a ragged 16-wide body everywhere
     full = rng.integers(*info, (N, C, Hh, W) if not nhwc else (N, Hh, W, C), dtype=dt)
     if kind == 0:
         a, b = full, rng.integers(*info, full.shape, dtype=dt)
@@ -346,7 +347,14 @@ def test_qlinear_mul(dev, kind, shape_b, nhwc, dt):
 
 
 @pytest.mark.parametrize("nhwc", [0, 1])
-@pytest.mark.parametrize("dt,N,C,Hh,W", [(np.uint8, 3, 70, 7, 7), (np.int8, 2, 16, 1, 1), (np.uint8, 1, 5, 13, 17)])
+@pytest.mark.parametrize("dt,N,C,Hh,W", [(np.uint8, 3, 70, 7, 7), (np.int8, 2, 16, 1, 1), (np.uint8, 1, 5, 13, 17),
+                                         # 16-byte paths: pixel lanes + two-level LDS sums (C 32), one-level
+                                         # (C 1024), 16-bit lanes flushed past 256 pixels a thread (400x400),
+                                         # one group a thread (C 4800), channel slices over blocks (C 8192)
+                                         (np.uint8, 3, 32, 56, 56), (np.int8, 2, 32, 12, 12),
+                                         (np.uint8, 2, 1024, 7, 7), (np.int8, 1, 16, 400, 400),
+                                         (np.uint8, 1, 16, 400, 400), (np.int8, 2, 4800, 2, 2),
+                                         (np.uint8, 2, 8192, 3, 1)])
 def test_qlinear_global_avgpool(dev, nhwc, dt, N, C, Hh, W):
     rng = np.random.default_rng(N * C + nhwc)
     info = (0, 256) if dt == np.uint8 else (-128, 128)
@@ -360,18 +368,24 @@ def test_qlinear_global_avgpool(dev, nhwc, dt, N, C, Hh, W):
 @pytest.mark.parametrize("nhwc", [0, 1])
 @pytest.mark.parametrize("k,st,pad,H_,W_", [((3, 3), (2, 2), (1, 1), 9, 10), ((2, 2), (2, 2), (0, 0), 8, 8),
                                              ((3, 2), (1, 1), (1, 0), 6, 7), ((7, 7), (1, 1), (0, 0), 7, 7)])
-def test_qlinear_avgpool(dev, nhwc, k, st, pad, H_, W_):
-    rng = np.random.default_rng(H_ * W_ + nhwc)
-    N, C = 2, 24
-    x = rng.integers(0, 256, (N, H_, W_, C) if nhwc else (N, C, H_, W_), dtype=np.uint8)
+@pytest.mark.parametrize("C,dt", [(24, np.uint8),    # one byte a thread
+                                  (32, np.uint8), (48, np.int8)])   # NHWC: 16 channels a thread
+def test_qlinear_avgpool(dev, nhwc, k, st, pad, H_, W_, C, dt):
+    rng = np.random.default_rng(H_ * W_ + nhwc + C)
+    N = 2
+    info = (0, 256) if dt == np.uint8 else (-128, 128)
+    x = rng.integers(*info, (N, H_, W_, C) if nhwc else (N, C, H_, W_), dtype=dt)
     oH = (H_ + 2 * pad[0] - k[0]) // st[0] + 1
     oW = (W_ + 2 * pad[1] - k[1]) // st[1] + 1
-    ref = O.qlinear_avgpool(x, k, st, pad, oH, oW, 0.02, 128, 0.013, 120, nhwc=nhwc)
-    y = H.qlinear_avgpool(to_dev(x, dev), k, st, pad, oH, oW, 0.02, 128, 0.013, 120, nhwc=nhwc)
+    zx, zy = (128, 120) if dt == np.uint8 else (-5, 9)
+    ref = O.qlinear_avgpool(x, k, st, pad, oH, oW, 0.02, zx, 0.013, zy, nhwc=nhwc)
+    y = H.qlinear_avgpool(to_dev(x, dev), k, st, pad, oH, oW, 0.02, zx, 0.013, zy, nhwc=nhwc)
     assert np.array_equal(to_np(y), ref)
 
 
-@pytest.mark.parametrize("counts,outer", [([3, 17, 32], 5), ([64, 64], 1), ([15, 1, 16, 33], 37)])
+@pytest.mark.parametrize("counts,outer", [([3, 17, 32], 5), ([64, 64], 1), ([15, 1, 16, 33], 37),
+                                          # 16-, 8- and 4-byte units (NHWC pixels of 24 + 8 channels)
+                                          ([16, 32, 48], 7), ([24, 8], 50), ([4, 12], 9)])
 @pytest.mark.parametrize("dt", [np.uint8, np.int8])
 def test_qlinear_concat(dev, counts, outer, dt):
     rng = np.random.default_rng(sum(counts) + outer)
