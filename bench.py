@@ -214,6 +214,35 @@ def roofline(ops, nbytes, kern_ms, prof):
     return r
 
 
+def planned_session(args, g, feeds, ref):
+    """The context that is timed. With --memory-planning 1 (the default) it
+    shares device memory between intermediates (one arena: lifetime slots,
+    in-place outputs, concat parts inside their output); its graph outputs
+    must equal, bit for bit, those of the unplanned context `ref` whose every
+    intermediate tensor the parity gate checked. Returns (session, memory
+    report)."""
+    import numpy as np
+    import torch
+
+    from nnr_amd import graph as G
+    mem = {"planned": bool(args.memory_planning), "device_bytes_unplanned": ref.device_bytes()}
+    if not args.memory_planning:
+        mem["device_bytes"] = ref.device_bytes()
+        return ref, mem
+    s = G.Session(g, memory_planning=True)
+    for k, v in feeds.items():
+        s.set_input(k, v)
+    s.run()
+    torch.cuda.synchronize()
+    for o in g.outputs:
+        assert np.array_equal(s.output(o)[0], ref.output(o)[0]), f"planned context differs at {o}"
+    stats, _ = s.memory_plan()
+    mem.update(device_bytes=s.device_bytes(), arena_bytes=stats["pool_bytes"],
+               pooled_tensors=stats["intermediates"], slots=stats["slots"], inplace=stats["inplace"],
+               concat_parts=stats["concat"])
+    return s, mem
+
+
 def layer_table(prof, args) -> list:
     """Per-layer rows (hipEvents around every node): TOPS and % of the i8
     MFMA peak for operators with algorithmic ops, GB/s and % of HBM peak for
@@ -273,6 +302,7 @@ def run_model(args, dev, model):
             assert np.array_equal(dev_t[:ng], env[o]), f"parity gate failed at {p['name']}"
         else:
             assert np.allclose(dev_t[:ng], env[o], atol=1e-3, rtol=1e-4), p["name"]
+    s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
     # per-layer times (hipEvents around every node) and per-kernel times
     s.enable_profiling(True)
@@ -330,7 +360,7 @@ def run_model(args, dev, model):
                              for b in ("FIRST", "DW", "NR16", "PACKED")},
                 "adds_fused_into_conv": s.fusion_stat("conv_add"),
                 "conv_tops": round(conv_ops / (qgemm_ms_per_step * 1e-3) / 1e12, 1),
-                "device_bytes": s.device_bytes()},
+                "memory": mem},
         roofline=rl,
         cpu_baseline={"value": round(cpu_img_s, 3), "unit": "images/s", "cores": nthr,
                       "kind": "port", "sample": f"oracle replay of the fused plan on 1 image, "
@@ -382,6 +412,7 @@ def run_bert(args, dev):
                 assert np.array_equal(d, ref), f"parity gate failed at {p['name']}"
             checked += 1
     assert checked == 6
+    s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
     s.enable_profiling(True)
     for _ in range(args.steps):
@@ -419,7 +450,7 @@ def run_bert(args, dev):
                             f"seq {S}, batch {B} (72 QLinearMatMul on DynamicQuantizeLinear "
                             "activations; fp32 attention, Softmax, LayerNorm, Gelu)",
                 "global_batch": B, "seq_len": S,
-                "int8_tops": round(mm_ops / (g_ms / args.steps * 1e-3) / 1e12, 1)},
+                "int8_tops": round(mm_ops / (g_ms / args.steps * 1e-3) / 1e12, 1), "memory": mem},
         roofline=rl,
         cpu_baseline={"value": round(cpu_seq_s, 3), "unit": "sequences/s", "cores": nthr,
                       "kind": "port", "sample": f"oracle replay of the fused plan on 1 sequence, "
@@ -468,6 +499,7 @@ def run_qoperator(args, dev):
             assert np.array_equal(dev_t[:ng], env[o]), f"parity gate failed at {p['name']}"
         else:
             assert np.allclose(dev_t[:ng], env[o], atol=1e-3, rtol=1e-4), p["name"]
+    s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
     s.enable_profiling(True)
     for _ in range(args.steps):
@@ -515,7 +547,7 @@ def run_qoperator(args, dev):
                             "QLinearAveragePool 3x3/2 pad 1, QLinearConv 1x1 (16->24) and 3x3 (16->8), "
                             "QLinearConcat (24+8, one part copied), QLinearMul by a per-channel "
                             "constant and by itself, QLinearGlobalAveragePool",
-                "global_batch": B, "device_bytes": s.device_bytes(),
+                "global_batch": B, "memory": mem,
                 "ops": [p["op"] + (":" + p["variant"] if p["variant"] else "") for p in plan]},
         roofline=rl,
         cpu_baseline={"value": round(cpu_img_s, 3), "unit": "images/s", "cores": nthr, "kind": "port",
@@ -561,6 +593,8 @@ def main():
                              "hbm_copy"])
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
+    ap.add_argument("--memory-planning", type=int, default=1, choices=[0, 1],
+                    help="graph configs: time a context whose intermediates share device memory")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",

@@ -84,6 +84,28 @@ int nnr_ctx_node_fused_pre(nnr_ctx_t ctx, int i, int k, const char** node_name);
 int nnr_ctx_fusion_stat(nnr_ctx_t ctx, const char* key, int* value);
 size_t nnr_ctx_device_bytes(nnr_ctx_t ctx);
 
+/* Device memory planning (context_t::enable_memory_planning, src/nnr.h:523-529;
+ * memory_planner_t::analyze / plan / apply, src/memory_planner.cpp:33-331).
+ * Off by default, as in the reference; set before prepare(). Intermediates
+ * whose lifetimes over the executed plan do not overlap share slots of one
+ * device arena (256-byte-aligned offsets); same-size elementwise operators
+ * write over an input read for the last time; the copied parts of a
+ * QLinearConcat along an axis with unit dimensions before it live inside its
+ * output. Graph inputs and outputs, initializers and tensors under 256 bytes
+ * are never pooled. Intermediate tensors then hold valid data only until
+ * their slot's next tenant is written. */
+int nnr_ctx_set_memory_planning(nnr_ctx_t ctx, int on);
+/* the plan without device memory, after optimize() alone (the fusions that
+ * need built operators are not in it), or the applied plan after prepare() */
+int nnr_ctx_plan_memory(nnr_ctx_t ctx);
+int nnr_ctx_memory_stats(nnr_ctx_t ctx, int* n_intermediates, int* n_slots, int* n_inplace, int* n_concat,
+                         unsigned long long* pool_bytes, unsigned long long* unpooled_bytes);
+/* pooled tensor i: live over node positions [first, last]; arena byte
+ * offset and size; kind 0 own slot, 1 in place over `parent`, 2 inside the
+ * QLinearConcat output `parent` (parent: another entry's index, or -1) */
+int nnr_ctx_memory_entry(nnr_ctx_t ctx, int i, const char** name, int* first, int* last,
+                         unsigned long long* offset, unsigned long long* bytes, int* kind, int* parent);
+
 /* per-node hipEvent timing (context_t::enable_profiling / dump_profile) */
 int nnr_ctx_enable_profiling(nnr_ctx_t ctx, int on);
 int nnr_ctx_profile(nnr_ctx_t ctx, int i, double* total_ms, int* runs, double* ops,

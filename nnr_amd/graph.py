@@ -60,6 +60,11 @@ def host_lib():
             "nnr_ctx_node_fused_pre": (i, [vp, i, i, P(cp)]),
             "nnr_ctx_fusion_stat": (i, [vp, cp, P(i)]),
             "nnr_ctx_device_bytes": (C.c_size_t, [vp]),
+            "nnr_ctx_set_memory_planning": (i, [vp, i]),
+            "nnr_ctx_plan_memory": (i, [vp]),
+            "nnr_ctx_memory_stats": (i, [vp, P(i), P(i), P(i), P(i), P(C.c_ulonglong), P(C.c_ulonglong)]),
+            "nnr_ctx_memory_entry": (i, [vp, i, P(cp), P(i), P(i), P(C.c_ulonglong), P(C.c_ulonglong),
+                                         P(i), P(i)]),
             "nnr_ctx_enable_profiling": (i, [vp, i]),
             "nnr_ctx_profile": (i, [vp, i, P(C.c_double), P(i), P(C.c_double), P(C.c_double)]),
         }
@@ -147,7 +152,8 @@ def _attr_arrays(attrs: dict):
 class Session:
     """A prepared C++ context_t for `graph` with the HIP backend preferred."""
 
-    def __init__(self, graph: Graph, stream=None, fusion=True, device=True, conv_add=True):
+    def __init__(self, graph: Graph, stream=None, fusion=True, device=True, conv_add=True,
+                 memory_planning=False):
         L = host_lib()
         self.L = L
         self.graph = graph
@@ -159,6 +165,7 @@ class Session:
         _chk(L.nnr_ctx_set_stream(h, stream))
         _chk(L.nnr_ctx_set_fusion(h, 1 if fusion else 0))
         _chk(L.nnr_ctx_set_conv_add(h, 1 if conv_add else 0))
+        _chk(L.nnr_ctx_set_memory_planning(h, 1 if memory_planning else 0))
         for name, arr in graph.initializers.items():
             dims = (C.c_int * max(1, arr.ndim))(*arr.shape)
             _chk(L.nnr_ctx_add_initializer(h, name.encode(), ONNX_DT[arr.dtype], dims, arr.ndim,
@@ -265,6 +272,30 @@ class Session:
 
     def device_bytes(self):
         return int(self.L.nnr_ctx_device_bytes(self.h))
+
+    def memory_plan(self):
+        """The memory plan: (stats dict, entries). Without a prepared device
+        context this plans the optimized graph without allocating. Entry:
+        dict(name, first, last, offset, bytes, kind 'slot'|'inplace'|'concat',
+        parent index or -1); first / last are node positions."""
+        L = self.L
+        _chk(L.nnr_ctx_plan_memory(self.h))
+        a, b, c, d = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+        pb, ub = C.c_ulonglong(), C.c_ulonglong()
+        _chk(L.nnr_ctx_memory_stats(self.h, C.byref(a), C.byref(b), C.byref(c), C.byref(d),
+                                    C.byref(pb), C.byref(ub)))
+        stats = dict(intermediates=a.value, slots=b.value, inplace=c.value, concat=d.value,
+                     pool_bytes=pb.value, unpooled_bytes=ub.value)
+        entries = []
+        kinds = ("slot", "inplace", "concat")
+        for k in range(a.value):
+            nm, f, l_, o, by, kd, par = (C.c_char_p(), C.c_int(), C.c_int(), C.c_ulonglong(),
+                                         C.c_ulonglong(), C.c_int(), C.c_int())
+            _chk(L.nnr_ctx_memory_entry(self.h, k, C.byref(nm), C.byref(f), C.byref(l_), C.byref(o),
+                                        C.byref(by), C.byref(kd), C.byref(par)))
+            entries.append(dict(name=nm.value.decode(), first=f.value, last=l_.value, offset=o.value,
+                                bytes=by.value, kind=kinds[kd.value], parent=par.value))
+        return stats, entries
 
     def enable_profiling(self, on=True):
         _chk(self.L.nnr_ctx_enable_profiling(self.h, 1 if on else 0))

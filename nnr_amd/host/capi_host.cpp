@@ -63,6 +63,50 @@ int nnr_ctx_set_conv_add(nnr_ctx_t c, int on) {
     return 0;
 }
 
+int nnr_ctx_set_memory_planning(nnr_ctx_t c, int on) {
+    if (!c) return err("ctx is NULL");
+    if (c->ctx.prepared) return err("set_memory_planning: the context is already prepared");
+    c->ctx.enable_memory_planning = on != 0;
+    return 0;
+}
+
+int nnr_ctx_plan_memory(nnr_ctx_t c) {
+    if (!c) return err("ctx is NULL");
+    if (!c->ctx.plan_memory_dry()) return err(c->ctx.last_error);
+    return 0;
+}
+
+int nnr_ctx_memory_stats(nnr_ctx_t c, int* n_intermediates, int* n_slots, int* n_inplace, int* n_concat,
+                         unsigned long long* pool_bytes, unsigned long long* unpooled_bytes) {
+    if (!c || !n_intermediates || !n_slots || !n_inplace || !n_concat || !pool_bytes || !unpooled_bytes)
+        return err("memory_stats: NULL argument");
+    const auto& p = c->ctx.planner;
+    *n_intermediates = p.num_intermediates;
+    *n_slots = p.num_slots;
+    *n_inplace = p.num_inplace;
+    *n_concat = p.num_concat;
+    *pool_bytes = p.total_pool_bytes;
+    *unpooled_bytes = p.total_unpooled_bytes;
+    return 0;
+}
+
+int nnr_ctx_memory_entry(nnr_ctx_t c, int i, const char** name, int* first, int* last,
+                         unsigned long long* offset, unsigned long long* bytes, int* kind, int* parent) {
+    if (!c || !name || !first || !last || !offset || !bytes || !kind || !parent)
+        return err("memory_entry: NULL argument");
+    const auto& L = c->ctx.planner.lifetimes;
+    if (i < 0 || i >= (int)L.size()) return err("memory_entry: index out of range");
+    const auto& lt = L[i];
+    *name = lt.tensor->name.c_str();
+    *first = lt.first;
+    *last = lt.last;
+    *offset = lt.offset;
+    *bytes = lt.bytes;
+    *kind = (int)lt.kind;
+    *parent = lt.parent;
+    return 0;
+}
+
 int nnr_ctx_add_initializer(nnr_ctx_t c, const char* name, int dtype, const int* dims, int ndim,
                             const void* data) {
     if (!c || !name || (ndim && !dims) || !data) return err("add_initializer: NULL argument");

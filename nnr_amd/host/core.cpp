@@ -205,9 +205,27 @@ void* context_t::device_alloc(size_t bytes) {
     return p;
 }
 
-// Memory planning: every active, non-constant, non-view tensor gets its own
-// device allocation (first-touch order). Views alias their source.
+// Device memory: with enable_memory_planning the planner places the
+// intermediates in one shared arena; every other active, non-constant,
+// non-view tensor gets its own device allocation (first-touch order). Views
+// alias their source.
+bool context_t::plan_memory_dry() {
+    if (prepared) return true;
+    if (!optimized && !optimize()) return false;
+    planner.analyze(this);
+    planner.plan();
+    return true;
+}
+
 bool context_t::plan_memory() {
+    // pooled intermediates first (one arena); everything else below gets an
+    // allocation of its own
+    if (enable_memory_planning) {
+        planner.analyze(this);
+        planner.plan();
+        if (!planner.apply()) return false;
+        device_bytes += planner.total_pool_bytes;
+    }
     std::vector<tensor_t*> order;
     std::unordered_set<tensor_t*> seen;
     auto want = [&](tensor_t* t) {

@@ -21,6 +21,8 @@
 #include <utility>
 #include <vector>
 
+#include "memory_planner.h"
+
 namespace nnr {
 
 // ONNX TensorProto element types (the reference's data_type_t numbering)
@@ -199,6 +201,9 @@ struct context_t {
     // ---- lifecycle (src/nnr.cpp:1378-1483) ----
     bool optimize();    // graph passes + shape inference + layouts (no device work)
     bool prepare();     // optimize, reshape, plan memory, upload constants
+    // the memory plan without device memory: after optimize() alone (shapes
+    // known, operators not built) or the applied plan after prepare()
+    bool plan_memory_dry();
     bool run();         // execute active nodes in order on `stream`
 
     // ---- configuration (src/nnr.h:512-589) ----
@@ -208,6 +213,10 @@ struct context_t {
     bool enable_conv_add = true;  // fuse_conv_add / fuse_matmul_dq_bias after the operators are built
     bool enable_profiling = false;
     bool shape_only = false;      // reshape() computes shapes only (pre-layout pass)
+    // share device memory between intermediates (src/nnr.h:523-529; off by
+    // default as in the reference). Set before prepare().
+    bool enable_memory_planning = false;
+    memory_planner_t planner;
 
     // ---- state ----
     std::map<std::string, tensor_t*> map;

@@ -695,6 +695,12 @@ struct QLinearConcat_hip : operator_t {
         for (int i = 0; i < ntens(); ++i) {
             tensor_t* t = inputs[2 + 3 * i];
             const long long cnt = nhwc ? t->dims[1] : (long long)t->dims[a] * inner;
+            // the memory planner placed this part inside y (its producer
+            // wrote it there): nothing to copy
+            if (outer == 1 && (const char*)t->data == (const char*)y->data + off) {
+                off += cnt;
+                continue;
+            }
             if (!ok(this, nnrh_qlinear_concat_part(t->data, y->data, outer, cnt, row, off, qdtype(t->type),
                                                    inputs[3 + 3 * i]->scalar_f32(), zp_value(inputs[4 + 3 * i]), ys,
                                                    yz, ctx->stream)))

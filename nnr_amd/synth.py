@@ -231,6 +231,39 @@ def qoperator_net(batch=2, hw=20, seed=22, pool="avg"):
     return g
 
 
+def concat_net(batch=1, C=16, hw=8, seed=25):
+    """Q(input) -> QLinearMul by a scalar (the input stays live) and
+    QLinearAveragePool 3x3/1 pad 1, both already in the quantization of the
+    QLinearConcat that joins them along channels -> QLinearAdd of the
+    concatenation with itself -> QLinearGlobalAveragePool -> DQ. At batch 1
+    the concatenation's parts can live inside its output (the memory
+    planner's concat aliasing) and the add can write over its input."""
+    g = Graph()
+    rng = np.random.default_rng(seed)
+    u8 = np.uint8
+    g.inputs["input"] = (np.float32, (batch, C, hw, hw))
+
+    def qp(name, s, z):
+        return g.init(name + "_s", np.array(s, F32)), g.init(name + "_z", np.array(z, u8))
+
+    x_qp = qp("x", 0.02, 100)
+    x = g.node("QuantizeLinear", ["input", *x_qp], name="input_Q")
+    cat_qp = qp("cat", 0.03, 20)
+    k = g.init("k", np.array([int(rng.integers(150, 200))], u8))
+    kq = qp("kq", 0.01, 128)
+    b = g.node("QLinearMul", [x, *x_qp, k, *kq, *cat_qp], name="mul")
+    a = g.node("QLinearAveragePool", [x, *x_qp, *cat_qp], name="avgpool", kernel_shape=[3, 3],
+               strides=[1, 1], pads=[1, 1, 1, 1])
+    cat = g.node("QLinearConcat", [*cat_qp, a, *cat_qp, b, *cat_qp], name="concat", axis=1)
+    add_qp = qp("add", 0.05, 10)
+    s2 = g.node("QLinearAdd", [cat, *cat_qp, cat, *cat_qp, *add_qp], name="add_self")
+    gap_qp = qp("gap", 0.04, 3)
+    gp = g.node("QLinearGlobalAveragePool", [s2, *add_qp, *gap_qp], name="gap")
+    y = g.node("DequantizeLinear", [gp, *gap_qp], name="out_DQ")
+    g.outputs.append(y)
+    return g
+
+
 # MobileNetV2 (Sandler et al. 2018, width 1.0): (expansion t, channels c,
 # repeats n, first stride s) of the 17 inverted-residual blocks
 MBV2_BLOCKS = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 96, 3, 1),

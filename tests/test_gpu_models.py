@@ -201,3 +201,44 @@ def test_bert_per_node(dev, fused):
     assert sum(p["variant"].endswith("+Group3") for p in chains) == 2
     assert sum(p["variant"].endswith("(grouped)") for p in chains) == 4
     assert n_int >= 8 * 2 and n_f32 >= 12
+
+
+@pytest.mark.parametrize("name", ["resnet50", "mobilenetv2", "bert", "qoperator", "concat_b1", "concat_b2"])
+def test_memory_planning(dev, name):
+    """The device memory planner (shared arena slots, in-place outputs,
+    concat parts inside their output) changes no result: with the fusions
+    that need built operators in the plan, the graph outputs of two runs are
+    bit-identical to those of a context with one allocation per tensor, and
+    the applied plan keeps every pair of tensors live at once on disjoint
+    bytes."""
+    from test_memory_planner import check_plan
+    rng = np.random.default_rng(30)
+    if name == "resnet50":
+        g, x = synth.resnet50(batch=2, hw=64, seed=14), rng.random((2, 3, 64, 64), dtype=np.float32)
+    elif name == "mobilenetv2":
+        g, x = synth.mobilenetv2(batch=2, hw=96, seed=17), rng.random((2, 3, 96, 96), dtype=np.float32)
+    elif name == "bert":
+        g, x = synth.bert(batch=2, seq=64, layers=2), rng.uniform(-1, 1, (2, 64, 768)).astype(np.float32)
+    elif name == "qoperator":
+        g, x = synth.qoperator_net(batch=3, hw=21), rng.uniform(-1, 1.5, (3, 3, 21, 21)).astype(np.float32)
+    else:
+        b = 1 if name == "concat_b1" else 2
+        g, x = synth.concat_net(batch=b), rng.uniform(-1, 1.5, (b, 16, 8, 8)).astype(np.float32)
+    outs = {}
+    for planned in (False, True):
+        s = G.Session(g, memory_planning=planned)
+        s.set_input("input", x)
+        runs = []
+        for _ in range(2):
+            s.run()
+            runs.append({o: s.output(o)[0].copy() for o in g.outputs})
+        for o in g.outputs:
+            assert np.array_equal(runs[0][o], runs[1][o]), (name, planned, o)
+        outs[planned] = (runs[0], s.device_bytes(), s)
+    for o in g.outputs:
+        assert np.array_equal(outs[False][0][o], outs[True][0][o]), (name, o)
+    stats, entries = outs[True][2].memory_plan()
+    check_plan(stats, entries)
+    assert outs[True][1] < outs[False][1]
+    if name == "concat_b1":
+        assert stats["concat"] == 2
