@@ -226,16 +226,34 @@ def planned_session(args, g, feeds, ref):
 
     from nnr_amd import graph as G
     mem = {"planned": bool(args.memory_planning), "device_bytes_unplanned": ref.device_bytes()}
-    if not args.memory_planning:
+    if not args.memory_planning and not args.onnx:
         mem["device_bytes"] = ref.device_bytes()
         return ref, mem
-    s = G.Session(g, memory_planning=True)
+    if args.onnx:
+        # the model as an ONNX file (initializers in external data, symbolic
+        # batch), loaded by the C++ loader
+        import tempfile
+
+        from nnr_amd import onnx_io
+        d = tempfile.mkdtemp(prefix="nnr_onnx_")
+        path = os.path.join(d, "model.onnx")
+        onnx_io.save(g, path, external_data=True, sym_dims=(0,))
+        t0 = time.perf_counter()
+        s = G.Session(None, onnx=path, sym_dim=next(iter(feeds.values())).shape[0],
+                      memory_planning=bool(args.memory_planning))
+        mem["onnx"] = {"model_bytes": os.path.getsize(path), "external_bytes": os.path.getsize(path + ".data"),
+                       "load_and_prepare_ms": round((time.perf_counter() - t0) * 1e3, 1)}
+    else:
+        s = G.Session(g, memory_planning=True)
     for k, v in feeds.items():
         s.set_input(k, v)
     s.run()
     torch.cuda.synchronize()
     for o in g.outputs:
         assert np.array_equal(s.output(o)[0], ref.output(o)[0]), f"planned context differs at {o}"
+    if not args.memory_planning:
+        mem["device_bytes"] = s.device_bytes()
+        return s, mem
     stats, _ = s.memory_plan()
     mem.update(device_bytes=s.device_bytes(), arena_bytes=stats["pool_bytes"],
                pooled_tensors=stats["intermediates"], slots=stats["slots"], inplace=stats["inplace"],
@@ -593,6 +611,8 @@ def main():
                              "hbm_copy"])
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
+    ap.add_argument("--onnx", type=int, default=0, choices=[0, 1],
+                    help="graph configs: time the model written as an ONNX file and loaded by the C++ loader")
     ap.add_argument("--memory-planning", type=int, default=1, choices=[0, 1],
                     help="graph configs: time a context whose intermediates share device memory")
     args = ap.parse_args()

@@ -84,6 +84,25 @@ int nnr_ctx_node_fused_pre(nnr_ctx_t ctx, int i, int k, const char** node_name);
 int nnr_ctx_fusion_stat(nnr_ctx_t ctx, const char* key, int* value);
 size_t nnr_ctx_device_bytes(nnr_ctx_t ctx);
 
+/* Load an ONNX model (ModelProto bytes) into an empty context: the
+ * replacement of the reference's load_onnx (src/format/onnx/onnx_loader.cpp:
+ * 658-732) building the graph through the calls above. model_dir: where
+ * external-data "location"s are relative to (NULL / "" = the working
+ * directory). sym_dim: value for symbolic input dimensions (<= 0: 1, as the
+ * reference's tensor_from_value_info does, :394-409). Constant nodes become
+ * initializers. Errors (malformed protobuf, unsupported tensor types, missing
+ * external files) return nonzero with nnr_last_error() set. */
+int nnr_ctx_load_onnx(nnr_ctx_t ctx, const void* data, size_t size, const char* model_dir, int sym_dim);
+/* the same from a file; external data relative to the file's directory
+ * (context_t::load_from_file, src/nnr.cpp) */
+int nnr_ctx_load_onnx_file(nnr_ctx_t ctx, const char* path, int sym_dim);
+/* the host copy of an initializer (as loaded or added; graph passes that
+ * rewrite constants update it) */
+int nnr_ctx_initializer(nnr_ctx_t ctx, const char* name, const void** host, size_t* nbytes);
+/* graph inputs (is_output 0) / outputs (1) in declaration order */
+int nnr_ctx_graph_io_count(nnr_ctx_t ctx, int is_output, int* n);
+int nnr_ctx_graph_io(nnr_ctx_t ctx, int is_output, int i, const char** name);
+
 /* Device memory planning (context_t::enable_memory_planning, src/nnr.h:523-529;
  * memory_planner_t::analyze / plan / apply, src/memory_planner.cpp:33-331).
  * Off by default, as in the reference; set before prepare(). Intermediates

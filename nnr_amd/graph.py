@@ -61,6 +61,11 @@ def host_lib():
             "nnr_ctx_fusion_stat": (i, [vp, cp, P(i)]),
             "nnr_ctx_device_bytes": (C.c_size_t, [vp]),
             "nnr_ctx_set_memory_planning": (i, [vp, i]),
+            "nnr_ctx_load_onnx": (i, [vp, vp, C.c_size_t, cp, i]),
+            "nnr_ctx_load_onnx_file": (i, [vp, cp, i]),
+            "nnr_ctx_graph_io_count": (i, [vp, i, P(i)]),
+            "nnr_ctx_initializer": (i, [vp, cp, P(vp), P(C.c_size_t)]),
+            "nnr_ctx_graph_io": (i, [vp, i, i, P(cp)]),
             "nnr_ctx_plan_memory": (i, [vp]),
             "nnr_ctx_memory_stats": (i, [vp, P(i), P(i), P(i), P(i), P(C.c_ulonglong), P(C.c_ulonglong)]),
             "nnr_ctx_memory_entry": (i, [vp, i, P(cp), P(i), P(i), P(C.c_ulonglong), P(C.c_ulonglong),
@@ -152,8 +157,12 @@ def _attr_arrays(attrs: dict):
 class Session:
     """A prepared C++ context_t for `graph` with the HIP backend preferred."""
 
-    def __init__(self, graph: Graph, stream=None, fusion=True, device=True, conv_add=True,
-                 memory_planning=False):
+    def __init__(self, graph: Graph | None, stream=None, fusion=True, device=True, conv_add=True,
+                 memory_planning=False, onnx=None, sym_dim=0):
+        """graph: the in-process description, built into the context through
+        the C ABI. onnx: instead, an ONNX model -- a file path (external data
+        relative to it) or ModelProto bytes -- loaded by the C++ loader;
+        sym_dim: the value of symbolic input dimensions (0: 1)."""
         L = host_lib()
         self.L = L
         self.graph = graph
@@ -166,6 +175,14 @@ class Session:
         _chk(L.nnr_ctx_set_fusion(h, 1 if fusion else 0))
         _chk(L.nnr_ctx_set_conv_add(h, 1 if conv_add else 0))
         _chk(L.nnr_ctx_set_memory_planning(h, 1 if memory_planning else 0))
+        if onnx is not None:
+            if isinstance(onnx, (bytes, bytearray)):
+                buf = C.create_string_buffer(bytes(onnx), len(onnx))
+                _chk(L.nnr_ctx_load_onnx(h, buf, len(onnx), None, sym_dim))
+            else:
+                _chk(L.nnr_ctx_load_onnx_file(h, os.fsencode(onnx), sym_dim))
+            _chk(L.nnr_ctx_prepare(h) if device else L.nnr_ctx_optimize(h))
+            return
         for name, arr in graph.initializers.items():
             dims = (C.c_int * max(1, arr.ndim))(*arr.shape)
             _chk(L.nnr_ctx_add_initializer(h, name.encode(), ONNX_DT[arr.dtype], dims, arr.ndim,
@@ -269,6 +286,23 @@ class Session:
         v = C.c_int()
         _chk(self.L.nnr_ctx_fusion_stat(self.h, key.encode(), C.byref(v)))
         return v.value
+
+    def initializer_bytes(self, name):
+        """The context's host copy of an initializer, as bytes."""
+        p, n = C.c_void_p(), C.c_size_t()
+        _chk(self.L.nnr_ctx_initializer(self.h, name.encode(), C.byref(p), C.byref(n)))
+        return C.string_at(p.value, n.value) if p.value else b""
+
+    def graph_io(self, outputs=True):
+        """Names of the context's graph outputs (or inputs), in order."""
+        n = C.c_int()
+        _chk(self.L.nnr_ctx_graph_io_count(self.h, 1 if outputs else 0, C.byref(n)))
+        out = []
+        for k in range(n.value):
+            nm = C.c_char_p()
+            _chk(self.L.nnr_ctx_graph_io(self.h, 1 if outputs else 0, k, C.byref(nm)))
+            out.append(nm.value.decode())
+        return out
 
     def device_bytes(self):
         return int(self.L.nnr_ctx_device_bytes(self.h))

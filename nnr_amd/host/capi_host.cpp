@@ -63,6 +63,41 @@ int nnr_ctx_set_conv_add(nnr_ctx_t c, int on) {
     return 0;
 }
 
+int nnr_ctx_load_onnx(nnr_ctx_t c, const void* data, size_t size, const char* model_dir, int sym_dim) {
+    if (!c || !data) return err("load_onnx: NULL argument");
+    if (!nnr::load_onnx(&c->ctx, data, size, model_dir ? model_dir : "", sym_dim)) return err(c->ctx.last_error);
+    return 0;
+}
+
+int nnr_ctx_load_onnx_file(nnr_ctx_t c, const char* path, int sym_dim) {
+    if (!c || !path) return err("load_onnx_file: NULL argument");
+    if (!nnr::load_onnx_file(&c->ctx, path, sym_dim)) return err(c->ctx.last_error);
+    return 0;
+}
+
+int nnr_ctx_initializer(nnr_ctx_t c, const char* name, const void** host, size_t* nbytes) {
+    if (!c || !name || !host || !nbytes) return err("initializer: NULL argument");
+    if (!c->ctx.initializer_names.count(name)) return err(std::string("initializer: no initializer ") + name);
+    const nnr::tensor_t* t = c->ctx.find(name);
+    *host = t && t->has_host() ? t->host.data() : nullptr;
+    *nbytes = t ? t->host.size() : 0;
+    return 0;
+}
+
+int nnr_ctx_graph_io_count(nnr_ctx_t c, int is_output, int* n) {
+    if (!c || !n) return err("graph_io_count: NULL argument");
+    *n = (int)(is_output ? c->ctx.graph_outputs.size() : c->ctx.graph_inputs.size());
+    return 0;
+}
+
+int nnr_ctx_graph_io(nnr_ctx_t c, int is_output, int i, const char** name) {
+    if (!c || !name) return err("graph_io: NULL argument");
+    const auto& v = is_output ? c->ctx.graph_outputs : c->ctx.graph_inputs;
+    if (i < 0 || i >= (int)v.size()) return err("graph_io: index out of range");
+    *name = v[i].c_str();
+    return 0;
+}
+
 int nnr_ctx_set_memory_planning(nnr_ctx_t c, int on) {
     if (!c) return err("ctx is NULL");
     if (c->ctx.prepared) return err("set_memory_planning: the context is already prepared");

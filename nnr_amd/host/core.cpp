@@ -183,9 +183,10 @@ bool context_t::add_node(const std::string& op_type, const std::string& name,
                          const std::vector<std::string>& ins, const std::vector<std::string>& outs,
                          std::vector<std::pair<std::string, attr_t>> attrs) {
     // onnx_loader.cpp:595-653: resolve through the registry, wire, init()
-    operator_t* op = solve_operator(op_type, 13, preferred_backend);
+    operator_t* op = solve_operator(op_type, opset, preferred_backend);
     if (!op) op = new unresolved_op_t();
     op->ctx = this;
+    op->opset = opset;
     op->op_type = op_type;
     op->node_name = name;
     for (auto& s : ins) op->inputs.push_back(s.empty() ? nullptr : tensor(s));

@@ -208,6 +208,7 @@ struct context_t {
 
     // ---- configuration (src/nnr.h:512-589) ----
     backend_t preferred_backend = backend_t::HIP;
+    int opset = 13;               // default-domain opset of the operators (the model's)
     void* stream = nullptr;       // hipStream_t of every launch
     bool enable_fusion = true;
     bool enable_conv_add = true;  // fuse_conv_add / fuse_matmul_dq_bias after the operators are built
@@ -254,6 +255,11 @@ void fuse_add_layernorm(context_t* ctx);
 void fuse_matmul_group(context_t* ctx);
 void fuse_dynq_minmax(context_t* ctx);
 void fuse_attention(context_t* ctx);
+
+// ONNX ModelProto -> this context (nnr_amd/host/onnx_loader.cpp); sym_dim
+// replaces symbolic input dimensions (<= 0: 1, as the reference does)
+bool load_onnx(context_t* ctx, const void* data, size_t size, const std::string& model_dir, int sym_dim);
+bool load_onnx_file(context_t* ctx, const std::string& path, int sym_dim);
 
 // operator creation through the registry (src/backend/cpu/solve_operator.cpp:29-33)
 operator_t* solve_operator(const std::string& op_type, int opset, backend_t preferred);

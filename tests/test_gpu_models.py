@@ -242,3 +242,27 @@ def test_memory_planning(dev, name):
     assert outs[True][1] < outs[False][1]
     if name == "concat_b1":
         assert stats["concat"] == 2
+
+
+@pytest.mark.parametrize("name", ["resnet50", "bert", "qoperator"])
+def test_onnx_model_bitexact(dev, name, tmp_path):
+    """A model written as an ONNX file (initializers in an external-data
+    file, symbolic batch) and loaded by the C++ loader runs to the same
+    outputs, bit for bit, as the same graph built in process."""
+    from nnr_amd import onnx_io
+    rng = np.random.default_rng(31)
+    if name == "resnet50":
+        g, x = synth.resnet50(batch=2, hw=64, seed=14), rng.random((2, 3, 64, 64), dtype=np.float32)
+    elif name == "bert":
+        g, x = synth.bert(batch=2, seq=64, layers=2), rng.uniform(-1, 1, (2, 64, 768)).astype(np.float32)
+    else:
+        g, x = synth.qoperator_net(batch=3, hw=21), rng.uniform(-1, 1.5, (3, 3, 21, 21)).astype(np.float32)
+    path = str(tmp_path / f"{name}.onnx")
+    onnx_io.save(g, path, external_data=True, sym_dims=(0,))
+    outs = []
+    for s in (G.Session(g), G.Session(None, onnx=path, sym_dim=x.shape[0])):
+        s.set_input("input", x)
+        s.run()
+        outs.append({o: s.output(o)[0] for o in g.outputs})
+    for o in g.outputs:
+        assert np.array_equal(outs[0][o], outs[1][o]), (name, o)
