@@ -483,7 +483,14 @@ QFAMILY = {"QLinearMul": "qlinear_mul", "QLinearAveragePool": "qlinear_avgpool",
            "QLinearConcat": "qlinear_concat", "QLinearGlobalAveragePool": "qlinear_global_avgpool"}
 
 
-def run_qoperator(args, dev):
+def run_bn(args, dev):
+    """fold_bn_qdq's two patterns at batch 256: Q -> QLinearConv 3x3 (64 -> 64,
+    NHWC) -> DQ -> BN -> Q -> DQ and the fp32 input -> BN -> Q -> DQ, 56x56.
+    The roofline is the folded BatchNormalization kernel's (HBM)."""
+    return run_qoperator(args, dev, graph="bn")
+
+
+def run_qoperator(args, dev, graph="qoperator"):
     """QOperator-format graph (quantized operators instead of QDQ pairs):
     QLinearConv -> QLinearAveragePool -> two QLinearConv branches ->
     QLinearConcat -> QLinearMul (per channel, then squared) ->
@@ -497,10 +504,17 @@ def run_qoperator(args, dev):
     from oracle import graph_oracle
     from oracle import pyoracle as O
 
-    B, HW = args.batch, 224
-    g = synth.qoperator_net(batch=B, hw=HW)
+    B = args.batch
+    if graph == "bn":
+        HW, Cin = 56, 64
+        g = synth.bn_net(batch=B, C=Cin, hw=HW)
+        family_ops = {"BatchNormalization": "batchnorm_u8"}
+    else:
+        HW, Cin = 224, 3
+        g = synth.qoperator_net(batch=B, hw=HW)
+        family_ops = QFAMILY
     rng = np.random.default_rng(24)
-    x = rng.uniform(-1.0, 1.5, (B, 3, HW, HW)).astype(np.float32)
+    x = rng.uniform(-1.0, 1.5, (B, Cin, HW, HW)).astype(np.float32)
     s = G.Session(g)
     s.set_input("input", x)
     s.run()
@@ -528,7 +542,7 @@ def run_qoperator(args, dev):
     kprof = profile_steps(s.run, args)
     layer_table(prof, args)
     family = {}
-    for op, kern in QFAMILY.items():
+    for op, kern in family_ops.items():
         if kern not in kprof:
             continue
         n, kms = kprof[kern]
@@ -537,7 +551,7 @@ def run_qoperator(args, dev):
         family[kern] = {"op": op, "achieved": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
                         "launches_per_step": round(n / args.steps), "alg_bytes_per_step": nbytes,
                         "avg_launch_ms": round(kms / n, 5), "ms_per_step": round(kms / args.steps, 5)}
-    assert len(family) == len(QFAMILY), sorted(family)
+    assert len(family) == len(family_ops), sorted(family)
     top = max(family, key=lambda k: family[k]["ms_per_step"])
     f = family[top]
     rl = {"kernel": top, "bound": "hbm", "achieved": f["achieved"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -557,14 +571,21 @@ def run_qoperator(args, dev):
         if time.perf_counter() - t0 > 5.0 or reps >= 5:
             break
     cpu_img_s = reps / (time.perf_counter() - t0)
+    if graph == "bn":
+        metric = "DQ->BN->Q / BN->Q folded graph images/sec b256 (fold_bn_qdq), 1 GPU"
+        workload = (f"batch {B}, 64x{HW}x{HW}: Q -> QLinearConv 3x3 64->64 (NHWC) -> DQ -> BatchNormalization -> "
+                    "Q -> DQ, and fp32 input -> BatchNormalization -> Q -> DQ (NCHW); both BNs folded to "
+                    "per-channel uint8 affines")
+    else:
+        metric = ("QOperator-format int8 graph images/sec b256 (QLinearConv, QLinearAveragePool, "
+                  "QLinearConcat, QLinearMul, QLinearGlobalAveragePool), 1 GPU")
+        workload = (f"QOperator graph, batch {B}, {HW}x{HW}: QLinearConv 3x3 (3->16), QLinearAveragePool 3x3/2 "
+                    "pad 1, QLinearConv 1x1 (16->24) and 3x3 (16->8), QLinearConcat (24+8, one part copied), "
+                    "QLinearMul by a per-channel constant and by itself, QLinearGlobalAveragePool")
     return dict(
-        metric="QOperator-format int8 graph images/sec b256 (QLinearConv, QLinearAveragePool, "
-               "QLinearConcat, QLinearMul, QLinearGlobalAveragePool), 1 GPU",
+        metric=metric,
         value=round(B / (ms * 1e-3), 1), unit="images/s", ms_per_step=ms,
-        config={"workload": f"QOperator graph, batch {B}, {HW}x{HW}: QLinearConv 3x3 (3->16), "
-                            "QLinearAveragePool 3x3/2 pad 1, QLinearConv 1x1 (16->24) and 3x3 (16->8), "
-                            "QLinearConcat (24+8, one part copied), QLinearMul by a per-channel "
-                            "constant and by itself, QLinearGlobalAveragePool",
+        config={"workload": workload,
                 "global_batch": B, "memory": mem,
                 "ops": [p["op"] + (":" + p["variant"] if p["variant"] else "") for p in plan]},
         roofline=rl,
@@ -607,7 +628,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="resnet50",
-                    choices=["resnet50", "mobilenetv2", "bert", "qoperator", "qconv", "qmatmul",
+                    choices=["resnet50", "mobilenetv2", "bert", "qoperator", "bn", "qconv", "qmatmul",
                              "hbm_copy"])
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
@@ -624,7 +645,7 @@ def main():
     dev = torch.device("cuda:0")
     run = {"resnet50": lambda a, d: run_model(a, d, "resnet50"),
            "mobilenetv2": lambda a, d: run_model(a, d, "mobilenetv2"),
-           "bert": run_bert, "qoperator": run_qoperator,
+           "bert": run_bert, "qoperator": run_qoperator, "bn": run_bn,
            "qconv": run_qconv, "qmatmul": run_qmatmul, "hbm_copy": run_hbm_copy}[args.config]
     res = run(args, dev)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,

@@ -294,6 +294,24 @@ int nnrh_qlinear_concat_part(const void* x_dev, void* y_dev, long long outer, lo
                              long long y_row, long long y_off, int dtype, float x_scale,
                              int x_zp, float y_scale, int y_zp, void* stream);
 
+/* ---- BatchNormalization after fold_bn_qdq (src/graph_optimizer/
+ * fold_bn_qdq.cpp:23-259; BatchNormalization.cpp:246-376) ---------------------
+ * y[n,c,...] = uint8(A[c] * x + B[c]) with the reference's rounding per layout
+ * (NCHW: 16-wide body of each plane fma + clamp + nearest-even, tail
+ * x*A + B + clamp + roundf; NHWC: body of each pixel's channels fma +
+ * nearest-even + unsigned saturation -- negatives become 255 for uint8 input,
+ * clamped first for fp32 input -- tail A*x + B + clamp + lrintf). x is uint8
+ * (DQ->BN->Q folded) or, with x_is_f32, fp32 (BN->Q folded). a, b: device
+ * [C]. HW: product of the dimensions after C.                                */
+int nnrh_batchnorm_u8(const void* x_dev, int x_is_f32, uint8_t* y_dev, const float* a_dev,
+                      const float* b_dev, long long N, int C, long long HW, int nhwc, void* stream);
+/* inference BatchNormalization in fp32 (BatchNormalization.cpp:126-160):
+ * y = alpha[c] * x + beta[c], alpha = scale / sqrt(var + eps) (double),
+ * beta = bias - alpha * mean, both computed by the caller                    */
+int nnrh_batchnorm_f32(const float* x_dev, float* y_dev, const float* alpha_dev,
+                       const float* beta_dev, long long N, int C, long long HW, int nhwc,
+                       void* stream);
+
 /* ---- uint8 MaxPool, NHWC (src/backend/x64/pool_x64.h:396-436) ----------- */
 int nnrh_maxpool_u8_nhwc(const uint8_t* x_dev, uint8_t* y_dev, int N, int C,
                          int iH, int iW, int oH, int oW, int kH, int kW, int sH,

@@ -397,6 +397,19 @@ def qlinear_concat(xs, counts, outer, scales, zps, y_s, y_zp):
     return y
 
 
+def batchnorm_u8(x, a, b, nhwc=0):
+    """Folded BatchNormalization: y = uint8(A[c] * x + B[c]). x: device uint8 or
+    float32 [N, C, ...] (with nhwc, [N, H, W, C]); a, b: device float32 [C]."""
+    import torch
+    N = x.shape[0]
+    C = x.shape[-1] if nhwc else x.shape[1]
+    HW = x.numel() // (N * C)
+    y = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    check(lib().nnrh_batchnorm_u8(ptr(x), 1 if x.dtype == torch.float32 else 0, ptr(y), ptr(a), ptr(b), N, C, HW,
+                                  nhwc, cur_stream()))
+    return y
+
+
 def maxpool_u8_nhwc(x, kH, kW, sH, sW, pH, pW, oH, oW):
     import torch
     N, H, W, C = x.shape

@@ -1429,6 +1429,24 @@ extern "C" int nnrh_qlinear_avgpool(const void* x, void* y, int N, int C, int iH
     return NNRH_OK;
 }
 
+extern "C" int nnrh_batchnorm_u8(const void* x, int x_is_f32, uint8_t* y, const float* a, const float* b,
+                                 long long N, int C, long long HW, int nhwc, void* stream) {
+    if (!x || !y || !a || !b) return set_err(NNRH_ERR_INVALID, "batchnorm_u8: NULL");
+    if (N < 0 || C <= 0 || HW < 0) return set_err(NNRH_ERR_INVALID, "batchnorm_u8: bad extents");
+    ProfScope ps("batchnorm_u8", S(stream));
+    HIP_TRY(launch_bn_affine_u8(x, x_is_f32, y, a, b, N, C, HW, nhwc, S(stream)), "batchnorm_u8");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_batchnorm_f32(const float* x, float* y, const float* alpha, const float* beta, long long N,
+                                  int C, long long HW, int nhwc, void* stream) {
+    if (!x || !y || !alpha || !beta) return set_err(NNRH_ERR_INVALID, "batchnorm_f32: NULL");
+    if (N < 0 || C <= 0 || HW < 0) return set_err(NNRH_ERR_INVALID, "batchnorm_f32: bad extents");
+    ProfScope ps("batchnorm_f32", S(stream));
+    HIP_TRY(launch_bn_f32(x, y, alpha, beta, N, C, HW, nhwc, S(stream)), "batchnorm_f32");
+    return NNRH_OK;
+}
+
 extern "C" int nnrh_qlinear_concat_part(const void* x, void* y, long long outer, long long count, long long y_row,
                                         long long y_off, int dtype, float x_scale, int x_zp, float y_scale,
                                         int y_zp, void* stream) {

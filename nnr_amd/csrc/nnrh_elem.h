@@ -45,6 +45,11 @@ hipError_t launch_qconcat_part(const void* x, void* y, long long outer, long lon
                                long long y_off, int dt, int copy, float rs, int x_zp, int y_zp, int lo, int hi,
                                hipStream_t s);
 
+hipError_t launch_bn_affine_u8(const void* x, int x_f32, uint8_t* y, const float* A, const float* B, long long N,
+                               int C, long long HW, int nhwc, hipStream_t s);
+hipError_t launch_bn_f32(const float* x, float* y, const float* A, const float* B, long long N, int C, long long HW,
+                         int nhwc, hipStream_t s);
+
 hipError_t launch_quantize(const float* x, long long n, float scale, int zp, int dt, void* y,
                            hipStream_t s);
 hipError_t launch_dequantize(const void* x, long long n, int dt, float scale, int zp, float* y,

@@ -1069,4 +1069,198 @@ hipError_t launch_qconcat_part(const void* x, void* y, long long outer, long lon
     return hipGetLastError();
 }
 
+// BatchNormalization after fold_bn_qdq (BatchNormalization.cpp:246-376): per
+// channel y = A[c] * x + B[c] into uint8, x uint8 (DQ -> BN -> Q folded) or
+// fp32 (BN -> Q folded), NCHW or NHWC, with the reference's per-layout
+// 16-wide body / scalar tail:
+//   NCHW, body of each plane: fma(x, A, B), clamp [0, 255], round to nearest
+//         even; tail: fl(x * A) + B, clamp, roundf (ties away from zero)
+//   NHWC, body of each pixel's channels: fma(x, A, B), round to nearest even
+//         (x86 cvtps: INT32_MIN out of range), then an UNSIGNED saturation to
+//         255 -- a negative value becomes 255 -- with no clamp before it for
+//         uint8 input (ops_x64.h:110-129) and a [0, 255] clamp for fp32 input
+//         (:135-155); tail: fl(A * x) + B, clamp, lrintf (nearest even)
+// The scalar clamps are std::max(0, std::min(255, v)).
+__device__ __forceinline__ float std_clamp255(float v) {
+    const float m = v < 255.0f ? v : 255.0f;    // std::min(255.0f, v)
+    return 0.0f < m ? m : 0.0f;                 // std::max(0.0f, m)
+}
+__device__ __forceinline__ float simd_clamp255(float v) {
+    // _mm512_max_ps(_mm512_min_ps(v, 255), 0): NaN takes the second operand
+    const float m = v < 255.0f ? v : 255.0f;
+    return m > 0.0f ? m : 0.0f;
+}
+
+template <bool F32_IN>
+__global__ __launch_bounds__(256) void bn_affine_u8_kernel(const void* __restrict x, uint8_t* __restrict y,
+                                                           const float* __restrict A, const float* __restrict B,
+                                                           long long total, int C, long long HW, int nhwc) {
+    const long long body_hw = HW - HW % 16;
+    const int body_c = C - C % 16;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
+        const float xf = F32_IN ? ((const float*)x)[i] : (float)((const uint8_t*)x)[i];
+        int c;
+        bool body;
+        if (nhwc) {
+            c = (int)(i % C);
+            body = c < body_c;
+        } else {
+            const long long pix = i % HW;
+            c = (int)((i / HW) % C);
+            body = pix < body_hw;
+        }
+        const float a = A[c], b = B[c];
+        uint32_t q;
+        if (body) {
+            float v = __builtin_fmaf(xf, a, b);
+            if (!nhwc || F32_IN) v = simd_clamp255(v);
+            const uint32_t r = (uint32_t)x86_f2i(__builtin_rintf(v));
+            q = r > 255u ? 255u : r;               // unsigned saturation
+        } else if (nhwc) {
+            const float v = std_clamp255(a * xf + b);
+            q = (uint32_t)__builtin_rintf(v);
+        } else {
+            const float v = std_clamp255(xf * a + b);
+            q = (uint32_t)roundf(v);
+        }
+        y[i] = (uint8_t)q;
+    }
+}
+
+// 16 elements per thread: NHWC with C % 16 == 0 (16 channels of one pixel)
+// or NCHW with HW % 16 == 0 (16 pixels of one plane), 16-byte aligned
+// operands. Every element is then in a 16-wide body.
+// the 16 channels' A / B of the vector starting at element i0
+template <bool NHWC>
+__device__ __forceinline__ void bn_coeffs_16(float* a, float* b, const float* __restrict A, const float* __restrict B,
+                                             long long i0, int C, long long HW) {
+    if (NHWC) {
+        const int c0 = (int)(i0 % C);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) { a[k] = A[c0 + k]; b[k] = B[c0 + k]; }
+    } else {
+        const int c = (int)((i0 / HW) % C);
+        const float ac = A[c], bc = B[c];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) { a[k] = ac; b[k] = bc; }
+    }
+}
+
+template <bool F32_IN, bool NHWC>
+__device__ __forceinline__ uint4 bn_affine_16(const float* xf, const float* a, const float* b) {
+    uint32_t o[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        float t = __builtin_fmaf(xf[k], a[k], b[k]);
+        if (!NHWC || F32_IN) t = simd_clamp255(t);
+        const uint32_t r = (uint32_t)x86_f2i(__builtin_rintf(t));
+        o[k >> 2] |= (r > 255u ? 255u : r) << (8 * (k & 3));
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// 16 elements per vector: NHWC with C % 16 == 0 (16 channels of one pixel)
+// or NCHW with HW % 16 == 0 (16 pixels of one plane), 16-byte aligned
+// operands; every element is then in a 16-wide body. uint8 input: each
+// thread has BN_U8_VECS vectors' loads in flight (block-strided, coalesced).
+// NHWC with 256 % (C / 16) == 0: a thread's vectors all start at the same
+// channel (strides are multiples of 256 vectors), so its A / B are loaded
+// once.
+constexpr int BN_U8_VECS = 4;
+template <bool F32_IN, bool NHWC>
+__global__ __launch_bounds__(256) void bn_affine_u8_16_kernel(const void* __restrict x, uint8_t* __restrict y,
+                                                              const float* __restrict A, const float* __restrict B,
+                                                              long long nv, int C, long long HW) {
+    constexpr int U = F32_IN ? 1 : BN_U8_VECS;
+    const bool fixed = NHWC && 256 % (C / 16) == 0;
+    float a[16], b[16];
+    if (fixed) bn_coeffs_16<NHWC>(a, b, A, B, (long long)(threadIdx.x % (C / 16)) * 16, C, HW);
+    for (long long base = (long long)blockIdx.x * 256 * U; base < nv; base += (long long)gridDim.x * 256 * U) {
+        if (F32_IN) {
+            const long long v = base + threadIdx.x;
+            if (v >= nv) continue;
+            float xf[16];
+            const float4* p = (const float4*)x + v * 4;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 q = p[k];
+                xf[4 * k] = q.x; xf[4 * k + 1] = q.y; xf[4 * k + 2] = q.z; xf[4 * k + 3] = q.w;
+            }
+            if (!fixed) bn_coeffs_16<NHWC>(a, b, A, B, v * 16, C, HW);
+            ((uint4*)y)[v] = bn_affine_16<F32_IN, NHWC>(xf, a, b);
+        } else {
+            uint4 q[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const long long v = base + u * 256 + threadIdx.x;
+                q[u] = v < nv ? ((const uint4*)x)[v] : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const long long v = base + u * 256 + threadIdx.x;
+                if (v >= nv) continue;
+                const uint32_t w[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+                float xf[16];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) xf[k] = (float)((w[k >> 2] >> (8 * (k & 3))) & 0xffu);
+                if (!fixed) bn_coeffs_16<NHWC>(a, b, A, B, v * 16, C, HW);
+                ((uint4*)y)[v] = bn_affine_16<F32_IN, NHWC>(xf, a, b);
+            }
+        }
+    }
+}
+
+hipError_t launch_bn_affine_u8(const void* x, int x_f32, uint8_t* y, const float* A, const float* B, long long N,
+                               int C, long long HW, int nhwc, hipStream_t s) {
+    const long long total = N * C * HW;
+    if (total <= 0) return hipSuccess;
+    const bool al = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
+    if (al && (nhwc ? C % 16 == 0 : HW % 16 == 0)) {
+        const long long nv = total / 16;
+        const long long per_block = 256LL * (x_f32 ? 1 : BN_U8_VECS);
+        long long blocks = (nv + per_block - 1) / per_block;
+        if (blocks > 65536) blocks = 65536;
+        const dim3 g((unsigned)blocks), b(256);
+        if (x_f32 && nhwc)
+            hipLaunchKernelGGL((bn_affine_u8_16_kernel<true, true>), g, b, 0, s, x, y, A, B, nv, C, HW);
+        else if (x_f32)
+            hipLaunchKernelGGL((bn_affine_u8_16_kernel<true, false>), g, b, 0, s, x, y, A, B, nv, C, HW);
+        else if (nhwc)
+            hipLaunchKernelGGL((bn_affine_u8_16_kernel<false, true>), g, b, 0, s, x, y, A, B, nv, C, HW);
+        else
+            hipLaunchKernelGGL((bn_affine_u8_16_kernel<false, false>), g, b, 0, s, x, y, A, B, nv, C, HW);
+        return hipGetLastError();
+    }
+    long long blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (x_f32)
+        hipLaunchKernelGGL((bn_affine_u8_kernel<true>), dim3((unsigned)blocks), dim3(256), 0, s, x, y, A, B, total,
+                           C, HW, nhwc);
+    else
+        hipLaunchKernelGGL((bn_affine_u8_kernel<false>), dim3((unsigned)blocks), dim3(256), 0, s, x, y, A, B, total,
+                           C, HW, nhwc);
+    return hipGetLastError();
+}
+
+// inference BatchNormalization in fp32: y = alpha[c] * x + beta[c]
+// (BatchNormalization.cpp:126-160; alpha / beta precomputed on the host)
+__global__ __launch_bounds__(256) void bn_f32_kernel(const float* __restrict x, float* __restrict y,
+                                                     const float* __restrict A, const float* __restrict B,
+                                                     long long total, int C, long long HW, int nhwc) {
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
+        const int c = nhwc ? (int)(i % C) : (int)((i / HW) % C);
+        y[i] = A[c] * x[i] + B[c];
+    }
+}
+
+hipError_t launch_bn_f32(const float* x, float* y, const float* A, const float* B, long long N, int C, long long HW,
+                         int nhwc, hipStream_t s) {
+    const long long total = N * C * HW;
+    if (total <= 0) return hipSuccess;
+    long long blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(bn_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, A, B, total, C, HW, nhwc);
+    return hipGetLastError();
+}
+
 }  // namespace nnrh

@@ -315,6 +315,8 @@ bool context_t::optimize() {
     if (optimized) return true;
     // 1. graph optimizer (pass_graph_optimizer.cpp:333-398): constant folding,
     //    QDQ fusion, post-op fusion
+    // PREPROCESS (pass_graph_optimizer.cpp:333-343): DQ -> BN -> Q first
+    if (enable_fusion) fold_bn_qdq(this);
     fold_constants(this);
     if (enable_fusion) {
         fuse_qdq_compute(this);

@@ -152,6 +152,10 @@ struct operator_t {
     // member's exec does nothing (its output is written by the leader, which
     // runs first)
     virtual bool fuse_group(const std::vector<operator_t*>& /*members*/) { return false; }
+    // BatchNormalization whose scale / bias inputs now hold fold_bn_qdq's
+    // combined per-channel A / B and whose output is uint8 (false: cannot)
+    virtual bool fold_affine_u8() { return false; }
+    virtual bool fold_affine_u8_possible() const { return false; }
     operator_t* group_leader = nullptr;
     std::vector<operator_t*> group_members;
 
@@ -255,6 +259,7 @@ void fuse_add_layernorm(context_t* ctx);
 void fuse_matmul_group(context_t* ctx);
 void fuse_dynq_minmax(context_t* ctx);
 void fuse_attention(context_t* ctx);
+void fold_bn_qdq(context_t* ctx);
 
 // ONNX ModelProto -> this context (nnr_amd/host/onnx_loader.cpp); sym_dim
 // replaces symbolic input dimensions (<= 0: 1, as the reference does)

@@ -712,6 +712,80 @@ struct QLinearConcat_hip : operator_t {
 };
 
 // ===========================================================================
+// BatchNormalization (src/backend/cpu/BatchNormalization.cpp), inference.
+// After fold_bn_qdq its scale / bias inputs hold the combined A / B and it
+// writes uint8 from uint8 (DQ -> BN -> Q) or fp32 (BN -> Q) input
+// (:246-376); otherwise fp32 -> fp32 with alpha = scale / sqrt(var + eps) in
+// double and beta = bias - alpha * mean (:126-134), uploaded at reshape.
+// NCHW or NHWC for 4-D inputs (:30-40).
+struct BatchNormalization_hip : operator_t {
+    float eps = 1e-5f;
+    bool folded_u8 = false;
+    float* ab = nullptr;   // fp32 path: alpha[C] | beta[C] on the device
+    bool init() override {
+        if (inputs.size() < 5 || outputs.empty()) return false;
+        eps = attribute_f("epsilon", 1e-5f);
+        return attribute("training_mode", 0) == 0;   // inference only
+    }
+    bool fold_affine_u8() override {
+        folded_u8 = true;
+        return true;
+    }
+    bool fold_affine_u8_possible() const override { return true; }
+    bool reshape() override {
+        tensor_t* x = inputs[0];
+        if (x->ndim() < 2) return bad(this, "needs at least 2 dimensions");
+        layout_mask = x->ndim() == 4 ? (LAYOUT_NCHW | LAYOUT_NHWC) : LAYOUT_NCHW;
+        outputs[0]->format = x->format;
+        const int C = x->dims[1];
+        for (int k = 1; k <= 4; ++k)
+            if (!inputs[k] || (int)inputs[k]->ndata != C || inputs[k]->type != NNR_DATA_TYPE_FLOAT32)
+                return bad(this, "scale / bias / mean / var must be fp32 [C]");
+        if (folded_u8) {
+            if (x->type != NNR_DATA_TYPE_UINT8 && x->type != NNR_DATA_TYPE_FLOAT32)
+                return bad(this, "folded: uint8 or fp32 input");
+            return outputs[0]->reshape(x->dims, NNR_DATA_TYPE_UINT8);
+        }
+        if (x->type != NNR_DATA_TYPE_FLOAT32) return bad(this, "fp32 input only");
+        if (!ctx->shape_only && !ab) {
+            for (int k = 1; k <= 4; ++k)
+                if (!inputs[k]->has_host()) return bad(this, "scale / bias / mean / var must be constants");
+            const float *sc = inputs[1]->h<float>(), *bi = inputs[2]->h<float>();
+            const float *me = inputs[3]->h<float>(), *va = inputs[4]->h<float>();
+            std::vector<float> h(2 * (size_t)C);
+            for (int c = 0; c < C; ++c) {
+                const float a = (float)(sc[c] / std::sqrt((double)va[c] + eps));
+                h[c] = a;
+                h[C + c] = bi[c] - a * me[c];
+            }
+            ab = (float*)ctx->device_alloc(h.size() * sizeof(float));
+            if (!ab) return bad(this, "device allocation failed");
+            if (nnrh_memcpy(ab, h.data(), h.size() * sizeof(float), 0, ctx->stream) != NNRH_OK ||
+                nnrh_stream_synchronize(ctx->stream) != NNRH_OK)
+                return bad(this, nnrh_last_error());
+        }
+        return outputs[0]->reshape(x->dims, NNR_DATA_TYPE_FLOAT32);
+    }
+    bool exec() override {
+        tensor_t* x = inputs[0];
+        const long long N = x->dims[0];
+        const int C = x->dims[1];
+        const long long HW = (long long)(x->ndata / ((size_t)N * C));
+        const int nhwc = x->format == memory_layout_t::NHWC;
+        if (folded_u8)
+            return ok(this, nnrh_batchnorm_u8(x->data, x->type == NNR_DATA_TYPE_FLOAT32, (uint8_t*)outputs[0]->data,
+                                              (const float*)inputs[1]->data, (const float*)inputs[2]->data, N, C, HW,
+                                              nhwc, ctx->stream));
+        return ok(this, nnrh_batchnorm_f32((const float*)x->data, (float*)outputs[0]->data, ab, ab + C, N, C, HW, nhwc,
+                                           ctx->stream));
+    }
+    std::string variant() const override {
+        if (!folded_u8) return std::string();
+        return inputs[0]->type == NNR_DATA_TYPE_UINT8 ? "DQ-BN-Q" : "BN-Q";
+    }
+};
+
+// ===========================================================================
 // MaxPool (src/backend/cpu/MaxPool.cpp); uint8 NHWC after fuse_qdq
 struct MaxPool_hip : operator_t {
     std::vector<int> kernels, pads, strides;
@@ -1154,6 +1228,7 @@ const op_registrar_t reg[] = {
     {"QLinearAveragePool", backend_t::HIP, make<QLinearAveragePool_hip>},
     {"QLinearConcat", backend_t::HIP, make<QLinearConcat_hip>},
     {"MaxPool", backend_t::HIP, make<MaxPool_hip>},
+    {"BatchNormalization", backend_t::HIP, make<BatchNormalization_hip>},
     {"GlobalAveragePool", backend_t::HIP, make<GlobalAveragePool_hip>},
     {"Flatten", backend_t::HIP, make<Flatten_hip>},
     {"Reshape", backend_t::HIP, make<Reshape_hip>},

@@ -29,6 +29,7 @@
 //                     the same input run as one launch
 // The fused operators are created through the registry with the context's
 // preferred backend, exactly where the reference calls solve_operator.
+#include <cmath>
 #include <cstdio>
 #include <unordered_map>
 #include <unordered_set>
@@ -830,6 +831,147 @@ void fuse_attention(context_t* ctx) {
         ++fused;
     }
     ctx->fusion_stats["attention"] = fused;
+}
+
+}  // namespace nnr
+
+namespace nnr {
+
+namespace {
+
+// a per-tensor fp32 scale held on the host
+bool host_scale(const tensor_t* t, float& v) {
+    if (!t || t->ndata != 1 || t->type != NNR_DATA_TYPE_FLOAT32 || !t->has_host()) return false;
+    v = t->scalar_f32();
+    return true;
+}
+// a uint8 / int8 zero point (absent: 0); fold_bn_qdq.cpp:91-95
+int host_zp(const operator_t* op, size_t i) {
+    const tensor_t* z = op->inputs.size() > i ? op->inputs[i] : nullptr;
+    if (!z || z->ndata == 0 || !z->has_host()) return 0;
+    if (z->type == NNR_DATA_TYPE_UINT8) return *z->h<uint8_t>();
+    if (z->type == NNR_DATA_TYPE_INT8) return *z->h<int8_t>();
+    return 0;
+}
+// the only active consumer of t, if it is of op_type and reads t as input 0
+operator_t* sole_consumer(context_t* ctx, tensor_t* t, int skip_idx, const char* op_type) {
+    if (count_consumers(ctx, t, skip_idx) != 1) return nullptr;
+    for (auto* op : ctx->nodes)
+        if (active(op) && op->op_type == op_type && !op->inputs.empty() && op->inputs[0] == t) return op;
+    return nullptr;
+}
+// operators of this backend whose outputs are fp32
+bool fp32_source(context_t* ctx, tensor_t* t) {
+    if (t->type == NNR_DATA_TYPE_FLOAT32) return true;
+    static const char* const f32_ops[] = {"DequantizeLinear", "Add", "Sub", "Mul", "Div", "Relu", "Clip", "Gelu",
+                                          "Softmax", "LayerNormalization", "MatMul", "Gemm", "GlobalAveragePool",
+                                          "Transpose", "BatchNormalization"};
+    for (auto* op : ctx->nodes) {
+        if (!active(op) || op->outputs.empty() || op->outputs[0] != t) continue;
+        for (const char* s : f32_ops)
+            if (op->op_type == s) return true;
+    }
+    return false;
+}
+
+}  // namespace
+
+// fold_bn_qdq (src/graph_optimizer/fold_bn_qdq.cpp:23-259): DQ -> BN -> Q
+// (each link the only consumer) becomes a BatchNormalization reading the
+// DQ's uint8 input and writing the Q's uint8 output, its scale / bias
+// replaced by the combined per-channel
+//   A = dq_s * gamma / q_s,  B = (beta - dq_zp * dq_s * gamma) / q_s + q_zp
+// with gamma = scale / sqrtf(var + eps), beta = bias - gamma * mean (float,
+// this expression order); then BN -> Q with fp32 input becomes
+//   A = gamma / q_s,  B = beta / q_s + q_zp.
+// Scales must be per tensor and BN's parameters fp32 initializers. The
+// combined A / B go to new initializers (the reference overwrites BN's own
+// scale / bias, which another node may share). The folded DQ and Q are kept
+// as fused_pre / fused_chain for the plan's readers.
+void fold_bn_qdq(context_t* ctx) {
+    auto& nodes = ctx->nodes;
+    const int n = (int)nodes.size();
+    int folded = 0, folded_bnq = 0;
+    auto bn_params = [&](operator_t* bn, std::vector<const float*>& p) {
+        if (bn->inputs.size() < 5 || bn->outputs.empty() || !bn->fold_affine_u8_possible()) return false;
+        const tensor_t* s0 = bn->inputs[1];
+        if (!s0) return false;
+        p.clear();
+        for (int k = 1; k <= 4; ++k) {
+            const tensor_t* t = bn->inputs[k];
+            if (!t || t->ndata == 0 || t->ndata != s0->ndata || t->type != NNR_DATA_TYPE_FLOAT32 ||
+                !t->has_host() || !ctx->initializer_names.count(t->name))
+                return false;
+            p.push_back(t->h<float>());
+        }
+        return true;
+    };
+    auto apply = [&](operator_t* bn, operator_t* dq, operator_t* q, const std::vector<const float*>& p, float dq_s,
+                     int dq_zp, float q_s, int q_zp) {
+        const int C = (int)bn->inputs[1]->ndata;
+        const float eps = bn->attribute_f("epsilon", 1e-5f);
+        std::vector<float> A(C), B(C);
+        for (int c = 0; c < C; ++c) {
+            const float gamma = p[0][c] / sqrtf(p[3][c] + eps);
+            const float beta = p[1][c] - gamma * p[2][c];
+            if (dq) {
+                A[c] = dq_s * gamma / q_s;
+                B[c] = (beta - (float)dq_zp * dq_s * gamma) / q_s + (float)q_zp;
+            } else {
+                A[c] = gamma / q_s;
+                B[c] = beta / q_s + (float)q_zp;
+            }
+        }
+        const std::string a_name = bn->node_name + "_fold_A", b_name = bn->node_name + "_fold_B";
+        ctx->add_initializer(a_name, NNR_DATA_TYPE_FLOAT32, {C}, A.data());
+        ctx->add_initializer(b_name, NNR_DATA_TYPE_FLOAT32, {C}, B.data());
+        bn->inputs[1] = ctx->find(a_name);
+        bn->inputs[2] = ctx->find(b_name);
+        if (dq) {
+            bn->inputs[0] = dq->inputs[0];
+            bn->fused_pre = {dq};
+            dq->skip = true;
+        }
+        bn->outputs[0] = q->outputs[0];
+        bn->fused_chain = {q};
+        q->skip = true;
+        bn->fold_affine_u8();
+    };
+    std::vector<const float*> p;
+    for (int i = 0; i < n; ++i) {
+        operator_t* dq = nodes[i];
+        if (!active(dq) || dq->op_type != "DequantizeLinear" || dq->outputs.empty() || dq->inputs.size() < 2) continue;
+        operator_t* bn = sole_consumer(ctx, dq->outputs[0], i, "BatchNormalization");
+        if (!bn || !bn_params(bn, p)) continue;
+        int bn_idx = -1;
+        for (int j = 0; j < n; ++j)
+            if (nodes[j] == bn) bn_idx = j;
+        operator_t* q = sole_consumer(ctx, bn->outputs[0], bn_idx, "QuantizeLinear");
+        float dq_s, q_s;
+        if (!q || q->inputs.size() < 2 || !host_scale(dq->inputs[1], dq_s) || !host_scale(q->inputs[1], q_s)) continue;
+        // uint8 in and out: the folded kernel writes uint8
+        const tensor_t* qz = q->inputs.size() > 2 ? q->inputs[2] : nullptr;
+        if (qz && qz->type != NNR_DATA_TYPE_UINT8) continue;
+        if (dq->inputs[0]->type != NNR_DATA_TYPE_UINT8 && dq->inputs[0]->type != NNR_DATA_TYPE_UNDEFINED) continue;
+        const tensor_t* dz = dq->inputs.size() > 2 ? dq->inputs[2] : nullptr;
+        if (dz && dz->type != NNR_DATA_TYPE_UINT8) continue;
+        apply(bn, dq, q, p, dq_s, host_zp(dq, 2), q_s, host_zp(q, 2));
+        folded++;
+    }
+    for (int i = 0; i < n; ++i) {
+        operator_t* bn = nodes[i];
+        if (!active(bn) || bn->op_type != "BatchNormalization" || !bn->fused_chain.empty()) continue;
+        if (!bn_params(bn, p) || !bn->inputs[0] || !fp32_source(ctx, bn->inputs[0])) continue;
+        operator_t* q = sole_consumer(ctx, bn->outputs[0], i, "QuantizeLinear");
+        float q_s;
+        if (!q || q->inputs.size() < 2 || !host_scale(q->inputs[1], q_s)) continue;
+        const tensor_t* qz = q->inputs.size() > 2 ? q->inputs[2] : nullptr;
+        if (qz && qz->type != NNR_DATA_TYPE_UINT8) continue;
+        apply(bn, nullptr, q, p, 0.f, 0, q_s, host_zp(q, 2));
+        folded_bnq++;
+    }
+    ctx->fusion_stats["bn_qdq"] += folded;
+    ctx->fusion_stats["bn_q"] += folded_bnq;
 }
 
 }  // namespace nnr

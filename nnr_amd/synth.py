@@ -264,6 +264,34 @@ def concat_net(batch=1, C=16, hw=8, seed=25):
     return g
 
 
+def bn_net(batch=2, C=40, hw=13, seed=26):
+    """BatchNormalization kept after quantization, both forms fold_bn_qdq
+    folds: Q(input) -> QLinearConv 3x3 (NHWC uint8) -> DQ -> BN -> Q -> DQ
+    (output "bn_a"), and the fp32 input -> BN -> Q -> DQ (output "bn_b",
+    NCHW). C = 40 gives the NHWC kernel a 32-channel body and an 8-channel
+    tail, hw = 13 a 160-element NCHW body and a 9-element tail; offsets and
+    zero points put some results below zero."""
+    g = Graph()
+    rng = np.random.default_rng(seed)
+    q = _QDQ(g, rng)
+    g.inputs["input"] = (np.float32, (batch, C, hw, hw))
+
+    def bn(x, name):
+        p = [rng.uniform(0.5, 1.5, C), rng.normal(0.0, 0.6, C), rng.normal(0.0, 0.4, C), rng.uniform(0.3, 2.0, C)]
+        ins = [x] + [g.init(f"{name}_{k}", v.astype(F32)) for k, v in zip(("scale", "bias", "mean", "var"), p)]
+        return g.node("BatchNormalization", ins, name=name, epsilon=1e-3)
+
+    x_q, x_qp = q.quant("input", F32(0.02), 128, name="input_Q")
+    c, c_qp = q.conv(x_q, x_qp, C, C, 3, pad=1, name="conv", y_scale=0.05, y_zp=100)
+    a = bn(q.dequant(c, c_qp, name="bn_a_dq"), "bn_a")
+    a_q, a_qp = q.quant(a, F32(0.04), 6, name="bn_a_q")
+    g.outputs.append(q.dequant(a_q, a_qp, name="out_a"))
+    b = bn("input", "bn_b")
+    b_q, b_qp = q.quant(b, F32(0.03), 4, name="bn_b_q")
+    g.outputs.append(q.dequant(b_q, b_qp, name="out_b"))
+    return g
+
+
 # MobileNetV2 (Sandler et al. 2018, width 1.0): (expansion t, channels c,
 # repeats n, first stride s) of the 17 inverted-residual blocks
 MBV2_BLOCKS = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 96, 3, 1),

@@ -260,12 +260,44 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
             if len(ins) > 2 and ins[2]:
                 y = y + a.get("beta", 1.0) * val(ins[2]).astype(np.float64)
             y = y.astype(np.float32)
+        elif op == "BatchNormalization":
+            # inference, fp32 (BatchNormalization.cpp:126-160), in float64
+            x = val(ins[0]).astype(np.float64)
+            sc, bias, mean, var = (val(t).astype(np.float64) for t in ins[1:5])
+            eps = float(graph.node_by_name(nd["name"]).attrs.get("epsilon", 1e-5))
+            shp = [1] * x.ndim
+            shp[x.ndim - 1 if fmt_of(ins[0]) else 1] = -1
+            r = lambda v: v.reshape(shp)
+            y = ((x - r(mean)) / np.sqrt(r(var) + eps) * r(sc) + r(bias)).astype(np.float32)
         else:
             raise NotImplementedError(op)
         return {outs[0]: y, **extra}
 
+    def folded_bn(nd):
+        """fold_bn_qdq's BatchNormalization: A / B restated from the original
+        BN, DQ and Q definitions (fold_bn_qdq.cpp:138-147, 230-236), then the
+        folded kernel's per-layout rounding."""
+        bn = graph.node_by_name(nd["name"])
+        sc, bias, mean, var = (init[t] for t in bn.inputs[1:5])
+        q = graph.node_by_name(nd["fused_chain"][-1])
+        q_s = float(init[q.inputs[1]].reshape(-1)[0])
+        q_zp = int(init[q.inputs[2]].reshape(-1)[0]) if len(q.inputs) > 2 and q.inputs[2] else 0
+        dq = None
+        if nd.get("fused_pre"):
+            d = graph.node_by_name(nd["fused_pre"][0])
+            dq = (float(init[d.inputs[1]].reshape(-1)[0]),
+                  int(init[d.inputs[2]].reshape(-1)[0]) if len(d.inputs) > 2 and d.inputs[2] else 0)
+        A, B = O.fold_bn(sc, bias, mean, var, float(bn.attrs.get("epsilon", 1e-5)), q_s, q_zp, dq=dq)
+        x = val(nd["inputs"][0])
+        return {nd["outputs"][0]: O.batchnorm_u8(x, A, B, nhwc=fmt_of(nd["inputs"][0]))}
+
     for nd in plan:
         if nd["op"] in skip_ops:
+            continue
+        if nd["op"] == "BatchNormalization" and nd.get("variant") in ("DQ-BN-Q", "BN-Q"):
+            env.update(folded_bn(nd))
+            if stop_after and nd["name"] == stop_after:
+                break
             continue
         pre = nd.get("fused_pre") or []
         if pre:

@@ -900,3 +900,86 @@ void orc_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C, int HW) {
             for (int s = 0; s < HW; s++)
                 y[((size_t)n * HW + s) * C + c] = x[((size_t)n * C + c) * HW + s];
 }
+
+/* fold_bn_qdq (src/graph_optimizer/fold_bn_qdq.cpp:138-147, :230-236), the
+ * combined per-channel scale and offset, in float with the reference's
+ * expression order:
+ *   gamma = sc / sqrtf(var + eps), beta = bias - gamma * mean
+ *   DQ -> BN -> Q (has_dq): A = dq_s * gamma / q_s,
+ *                           B = (beta - dq_zp * dq_s * gamma) / q_s + q_zp
+ *   BN -> Q:                A = gamma / q_s,  B = beta / q_s + q_zp       */
+void orc_fold_bn(int C, const float* sc, const float* bias, const float* mean, const float* var, float eps,
+                 int has_dq, float dq_s, int dq_zp, float q_s, int q_zp, float* A, float* B) {
+    for (int c = 0; c < C; ++c) {
+        const float gamma = sc[c] / sqrtf(var[c] + eps);
+        const float beta = bias[c] - gamma * mean[c];
+        if (has_dq) {
+            A[c] = dq_s * gamma / q_s;
+            B[c] = (beta - (float)dq_zp * dq_s * gamma) / q_s + (float)q_zp;
+        } else {
+            A[c] = gamma / q_s;
+            B[c] = beta / q_s + (float)q_zp;
+        }
+    }
+}
+
+/* BatchNormalization's folded execution (BatchNormalization.cpp:248-376 and
+ * ops_x64.h:110-155, AVX-512 build): y = uint8(A[c] * x + B[c]).
+ *   NCHW: per (n, c) plane, the first HW - HW%16 elements 16 wide:
+ *         fma(x, a, b), _mm512_max_ps(_mm512_min_ps(v, 255), 0),
+ *         cvtps_epi32 (nearest even), cvtusepi32_epi8; the rest
+ *         std::max(0, std::min(255, x * a + b)), roundf.
+ *   NHWC: per pixel, the first C - C%16 channels 16 wide: fma(x, A, B)
+ *         (clamped as above only for fp32 input), cvtps_epi32, then
+ *         cvtusepi32_epi8, an UNSIGNED saturation (a negative int32 is a
+ *         large unsigned value and becomes 255); the rest
+ *         std::max(0, std::min(255, A * x + B)), lrintf.
+ * x: uint8, or fp32 when x_f32. */
+static inline float simd_clamp255(float v) {
+    const float m = v < 255.0f ? v : 255.0f;   /* minps(v, 255): NaN -> 255 */
+    return m > 0.0f ? m : 0.0f;
+}
+static inline float std_clamp255(float v) {
+    const float m = v < 255.0f ? v : 255.0f;   /* std::min(255.0f, v) */
+    return 0.0f < m ? m : 0.0f;                /* std::max(0.0f, m) */
+}
+static inline uint8_t cvtus_epi8(int32_t r) {
+    return (uint32_t)r > 255u ? 255 : (uint8_t)r;
+}
+
+void orc_batchnorm_u8(const void* x, int x_f32, uint8_t* y, const float* A, const float* B, long long N, int C,
+                      long long HW, int nhwc) {
+    const uint8_t* xu = (const uint8_t*)x;
+    const float* xf = (const float*)x;
+#define XV(i) (x_f32 ? xf[i] : (float)xu[i])
+    if (nhwc) {
+        const int body = C - C % 16;
+        for (long long p = 0; p < N * HW; ++p) {
+            const long long o = p * C;
+            for (int c = 0; c < C; ++c) {
+                const float v0 = XV(o + c);
+                if (c < body) {
+                    float v = fmaf(v0, A[c], B[c]);
+                    if (x_f32) v = simd_clamp255(v);
+                    y[o + c] = cvtus_epi8(x86_f2i(nearbyintf(v)));
+                } else {
+                    y[o + c] = (uint8_t)lrintf(std_clamp255(A[c] * v0 + B[c]));
+                }
+            }
+        }
+    } else {
+        const long long body = HW - HW % 16;
+        for (long long nc = 0; nc < N * C; ++nc) {
+            const int c = (int)(nc % C);
+            const long long o = nc * HW;
+            for (long long i = 0; i < HW; ++i) {
+                const float v0 = XV(o + i);
+                if (i < body)
+                    y[o + i] = cvtus_epi8(x86_f2i(nearbyintf(simd_clamp255(fmaf(v0, A[c], B[c])))));
+                else
+                    y[o + i] = (uint8_t)roundf(std_clamp255(v0 * A[c] + B[c]));
+            }
+        }
+    }
+#undef XV
+}

@@ -158,6 +158,14 @@ void orc_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C, int HW);
 void orc_set_threads(int n);
 int  orc_get_threads(void);
 
+
+/* fold_bn_qdq's combined per-channel A / B (fold_bn_qdq.cpp:138-147, 230-236) */
+void orc_fold_bn(int C, const float* sc, const float* bias, const float* mean, const float* var, float eps,
+                 int has_dq, float dq_s, int dq_zp, float q_s, int q_zp, float* A, float* B);
+/* folded BatchNormalization execution (BatchNormalization.cpp:248-376) */
+void orc_batchnorm_u8(const void* x, int x_f32, uint8_t* y, const float* A, const float* B, long long N, int C,
+                      long long HW, int nhwc);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,8 @@ def lib():
             "orc_qlinear_concat": (None, [i, P(vp), P(ct.c_longlong), ct.c_longlong, i, P(f), P(i), f, i, vp]),
             "orc_qlinear_mul": (None, [i, vp, vp, vp, sz, i, i, i, i, i, f, i, f, i, f, i]),
             "orc_nchw_to_nhwc_u8": (None, [vp, vp, i, i, i]),
+            "orc_fold_bn": (None, [i, vp, vp, vp, vp, f, i, f, i, f, i, vp, vp]),
+            "orc_batchnorm_u8": (None, [vp, i, vp, vp, vp, ct.c_longlong, i, ct.c_longlong, i]),
         }
         for n, (r, a) in sigs.items():
             fn = getattr(L, n)
@@ -228,6 +230,30 @@ def qlinear_mul(kind, a, b, a_s, a_zp, b_s, b_zp, y_s, y_zp, C=0, HW=0, y_nhwc=0
     N = full.size // (C * HW) if C and HW else 0
     lib().orc_qlinear_mul(kind, _p(a), _p(b), _p(y), y.size, N, C, HW, y_nhwc, dt_of(a),
                           float(a_s), int(a_zp), float(b_s), int(b_zp), float(y_s), int(y_zp))
+    return y
+
+
+def fold_bn(sc, bias, mean, var, eps, q_s, q_zp, dq=None):
+    """fold_bn_qdq's (A, B) per channel; dq = (dq_scale, dq_zp) for DQ->BN->Q."""
+    C = len(sc)
+    f = lambda a: np.ascontiguousarray(a, np.float32)
+    sc, bias, mean, var = f(sc), f(bias), f(mean), f(var)
+    A = np.empty(C, np.float32)
+    B = np.empty(C, np.float32)
+    lib().orc_fold_bn(C, _p(sc), _p(bias), _p(mean), _p(var), float(eps), 1 if dq else 0,
+                      float(dq[0]) if dq else 0.0, int(dq[1]) if dq else 0, float(q_s), int(q_zp), _p(A), _p(B))
+    return A, B
+
+
+def batchnorm_u8(x, A, B, nhwc=0):
+    x = np.ascontiguousarray(x)
+    N = x.shape[0]
+    C = x.shape[-1] if nhwc else x.shape[1]
+    HW = x.size // (N * C)
+    y = np.empty(x.shape, np.uint8)
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    lib().orc_batchnorm_u8(_p(x), 1 if x.dtype == np.float32 else 0, _p(y), _p(A), _p(B), N, C, HW, nhwc)
     return y
 
 

@@ -266,3 +266,15 @@ def test_onnx_model_bitexact(dev, name, tmp_path):
         outs.append({o: s.output(o)[0] for o in g.outputs})
     for o in g.outputs:
         assert np.array_equal(outs[0][o], outs[1][o]), (name, o)
+
+
+def test_bn_graph(dev):
+    """fold_bn_qdq's two patterns through the host framework: DQ -> BN -> Q
+    after a QLinearConv (NHWC) and fp32 BN -> Q (NCHW), every uint8 tensor
+    bit-exact with the oracle's restatement of the fold and the kernel."""
+    g = synth.bn_net(batch=2, C=40, hw=13)
+    rng = np.random.default_rng(27)
+    x = rng.uniform(-2.5, 2.5, (2, 40, 13, 13)).astype(np.float32)
+    plan, _, n_int = check_graph(g, {"input": x}, g.outputs[0])
+    assert sorted(p["variant"] for p in plan if p["op"] == "BatchNormalization") == ["BN-Q", "DQ-BN-Q"]
+    assert n_int >= 4

@@ -754,3 +754,27 @@ def test_multihead_attention_f32(dev, B, S, hidden, heads, scale):
     _lib.check(_lib.lib().nnrh_multihead_attention_f32(_lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd), _lib.ptr(y), B, S,
                                                        hidden, heads, scale, wsp, _lib.cur_stream()))
     np.testing.assert_allclose(to_np(y), ref, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("nhwc", [0, 1])
+@pytest.mark.parametrize("f32_in", [False, True])
+@pytest.mark.parametrize("N,C,Hh,W", [(2, 40, 13, 13), (1, 16, 4, 4), (3, 7, 5, 3),
+                                      (2, 48, 8, 6),    # 16 elements a thread in both layouts
+                                      (2, 64, 5, 7), (3, 32, 4, 8)])   # NHWC: a thread's channels fixed
+def test_batchnorm_folded(dev, nhwc, f32_in, N, C, Hh, W):
+    """Folded BatchNormalization (uint8 or fp32 in, uint8 out) bit-exact with
+    the oracle: 16-wide bodies and scalar tails in both layouts, offsets that
+    drive results below 0 and above 255, and exact .5 ties."""
+    rng = np.random.default_rng(N * C + nhwc + f32_in)
+    shape = (N, Hh, W, C) if nhwc else (N, C, Hh, W)
+    if f32_in:
+        x = (rng.normal(0, 60, shape) + 0.5 * rng.integers(0, 2, shape)).astype(np.float32)
+    else:
+        x = rng.integers(0, 256, shape, dtype=np.uint8)
+    A = rng.uniform(-2.0, 2.0, C).astype(np.float32)
+    A[::5] = 1.0
+    B = rng.uniform(-300.0, 300.0, C).astype(np.float32)
+    B[::3] = 0.5
+    ref = O.batchnorm_u8(x, A, B, nhwc=nhwc)
+    y = H.batchnorm_u8(to_dev(x, dev), to_dev(A, dev), to_dev(B, dev), nhwc=nhwc)
+    assert np.array_equal(to_np(y), ref)

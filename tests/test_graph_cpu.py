@@ -141,3 +141,20 @@ def test_qoperator_graph_layouts():
     assert ops["QLinearMul"] == 2 and ops["QLinearGlobalAveragePool"] == 1
     fmt = {p["name"]: s.tensor_info(p["outputs"][0])[3] for p in plan}
     assert fmt["concat"] == 1 and fmt["mul_channel"] == 1 and fmt["mul_square"] == 1
+
+
+def test_fold_bn_qdq_patterns():
+    """DQ -> BN -> Q (after a QLinearConv, NHWC) and fp32 BN -> Q both fold
+    (fold_bn_qdq.cpp:23-259): one BatchNormalization each, reading uint8 or
+    fp32 and writing the Q's uint8 tensor; the DQ / Q are skipped."""
+    from nnr_amd import graph as G, synth
+    g = synth.bn_net()
+    s = G.Session(g, device=False)
+    plan = s.plan()
+    bns = {p["name"]: p for p in plan if p["op"] == "BatchNormalization"}
+    assert bns["bn_a"]["variant"] == "DQ-BN-Q" and bns["bn_b"]["variant"] == "BN-Q"
+    assert bns["bn_a"]["fused_pre"] == ["bn_a_dq"] and bns["bn_a"]["fused_chain"] == ["bn_a_q"]
+    assert bns["bn_a"]["outputs"] == ["bn_a_q_out"] and bns["bn_b"]["inputs"][0] == "input"
+    assert "QuantizeLinear" not in [p["op"] for p in plan if p["name"] != "input_Q"]
+    assert s.fusion_stat("bn_qdq") == 1 and s.fusion_stat("bn_q") == 1
+    assert s.tensor_info("bn_a_q_out")[3] == 1      # NHWC after the convolution

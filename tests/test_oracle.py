@@ -553,3 +553,67 @@ def test_qmul_identity_and_kinds():
     assert np.array_equal(n1, n2.transpose(0, 3, 1, 2))
     ref = np.clip(np.rint(x.astype(np.float64) * 0.25 * (ch.astype(np.float64) - 64)[None, :, None, None]), 0, 255)
     assert np.array_equal(n1, ref)
+
+
+# ---------------------------------------------------------------------------
+# fold_bn_qdq and the folded BatchNormalization (fold_bn_qdq.cpp:138-147,
+# BatchNormalization.cpp:248-376)
+
+def test_fold_bn_identity():
+    """scale 1, bias 0, mean 0, var + eps = 1 and equal DQ / Q parameters
+    (power-of-two scale) give A = 1, B = 0 exactly: y = x in every layout."""
+    C = 40
+    one, zero = np.ones(C, np.float32), np.zeros(C, np.float32)
+    A, B = O.fold_bn(one, zero, zero, one, 0.0, 0.03125, 7, dq=(0.03125, 7))
+    assert np.all(A == 1.0) and np.all(B == 0.0)
+    x = np.random.default_rng(1).integers(0, 256, (2, C, 5, 7), dtype=np.uint8)
+    for nhwc in (0, 1):
+        xi = x.transpose(0, 2, 3, 1).copy() if nhwc else x
+        assert np.array_equal(O.batchnorm_u8(xi, A, B, nhwc=nhwc), xi)
+
+
+def test_fold_bn_formula():
+    """A and B against the algebra in float64 (a dropped or misplaced term
+    moves them by far more than float rounding)."""
+    rng = np.random.default_rng(2)
+    C = 33
+    sc, bias, mean = rng.uniform(0.5, 2, C), rng.normal(0, 1, C), rng.normal(0, 1, C)
+    var = rng.uniform(0.1, 3, C)
+    eps, dq_s, dq_zp, q_s, q_zp = 1e-3, 0.021, 131, 0.047, 9
+    A, B = O.fold_bn(sc, bias, mean, var, eps, q_s, q_zp, dq=(dq_s, dq_zp))
+    g = sc / np.sqrt(var + eps)
+    beta = bias - g * mean
+    np.testing.assert_allclose(A, dq_s * g / q_s, rtol=1e-5)
+    np.testing.assert_allclose(B, (beta - dq_zp * dq_s * g) / q_s + q_zp, rtol=1e-4, atol=1e-4)
+    A2, B2 = O.fold_bn(sc, bias, mean, var, eps, q_s, q_zp)
+    np.testing.assert_allclose(A2, g / q_s, rtol=1e-5)
+    np.testing.assert_allclose(B2, beta / q_s + q_zp, rtol=1e-4, atol=1e-4)
+
+
+def test_folded_bn_rounding_per_layout():
+    """x + 0.5 exactly (A = 1, B = 0.5): nearest even in the 16-wide bodies and
+    the NHWC tail (lrintf), away from zero in the NCHW tail (roundf)."""
+    C, H, W = 20, 1, 18       # NHWC: 16 body + 4 tail channels; NCHW: 16 body + 2 tail pixels
+    x = (np.arange(2 * C * H * W) % 250).astype(np.uint8).reshape(2, C, H, W)
+    A, B = np.ones(C, np.float32), np.full(C, 0.5, np.float32)
+    rne = lambda v: (v + (v & 1)).astype(np.uint8)          # (v + 0.5) to even
+    y = O.batchnorm_u8(x, A, B, nhwc=0)
+    assert np.array_equal(y[..., :16], rne(x[..., :16].astype(np.int32)))
+    assert np.array_equal(y[..., 16:], (x[..., 16:].astype(np.int32) + 1).astype(np.uint8))
+    xn = x.transpose(0, 2, 3, 1).copy()
+    yn = O.batchnorm_u8(xn, A, B, nhwc=1)
+    assert np.array_equal(yn, rne(xn.astype(np.int32)))
+
+
+def test_folded_bn_negative_saturation():
+    """A negative result: 0 everywhere except the NHWC 16-wide body with
+    uint8 input, whose unsigned saturation (cvtusepi32_epi8 of a negative
+    int32) gives 255."""
+    C = 20
+    x = np.random.default_rng(3).integers(0, 200, (1, C, 2, 3), dtype=np.uint8)
+    A, B = np.ones(C, np.float32), np.full(C, -300.0, np.float32)
+    assert np.all(O.batchnorm_u8(x, A, B, nhwc=0) == 0)
+    yn = O.batchnorm_u8(x.transpose(0, 2, 3, 1).copy(), A, B, nhwc=1)
+    assert np.all(yn[..., :16] == 255) and np.all(yn[..., 16:] == 0)
+    xf = x.transpose(0, 2, 3, 1).astype(np.float32).copy()
+    assert np.all(O.batchnorm_u8(xf, A, B, nhwc=1) == 0)     # fp32 input: clamped first
