@@ -595,6 +595,63 @@ def run_qoperator(args, dev, graph="qoperator"):
     )
 
 
+def run_convinteger(args, dev):
+    """ConvInteger at cfg2's shape: x u8[32,64,56,56], w i8[64,64,3,3], pad 1,
+    per-channel weight zero points; int32 output. im2col + the i8 MFMA
+    MatMulInteger GEMM + the zero-point correction; value = TOPS of the
+    whole operator."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    import nnr_amd as H
+    from nnr_amd import _lib
+    from oracle import pyoracle as O
+    L = _lib.lib()
+    N, Cc, HW, OC = 32, 64, 56, 64
+    rng = np.random.default_rng(32)
+    x = rng.integers(0, 256, (N, Cc, HW, HW), dtype=np.uint8)
+    w = rng.integers(-128, 128, (OC, Cc, 3, 3), dtype=np.int8)
+    wz = rng.integers(-8, 8, OC).astype(np.int32)
+    xd, wd = torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev)
+    wzd = torch.from_numpy(wz).to(dev)
+    y = torch.empty((N, OC, HW, HW), dtype=torch.int32, device=dev)
+    h = C.c_void_p()
+    _lib.check(L.nnrh_conv_integer_create(C.byref(h), N, Cc, HW, HW, OC, 3, 3, 1, 1, 1, 1, 1, 1, HW, HW, 1,
+                                          H.U8, H.S8))
+    st = _lib.cur_stream()
+
+    def step():
+        _lib.check(L.nnrh_conv_integer_run(h, _lib.ptr(xd), _lib.ptr(wd), 117, 0, _lib.ptr(wzd), _lib.ptr(y), st))
+
+    step()
+    torch.cuda.synchronize()
+    ref = O.conv_integer(x[:2], w, 117, wz, pads=(1, 1))
+    assert np.array_equal(y[:2].cpu().numpy(), ref), "parity gate failed"
+    ms = time_steps(step, args)
+    kprof = profile_steps(step, args)
+    L.nnrh_conv_integer_destroy(h)
+    ops = 2.0 * N * OC * HW * HW * Cc * 9
+    nbytes = x.nbytes + w.nbytes + N * OC * HW * HW * 4
+    g_launches, g_ms = kprof["qgemm"]
+    rl = roofline(ops / (g_launches / args.steps), nbytes, g_ms / g_launches, kprof)
+    rl["traffic"] = None
+    rl["note"] = ("achieved = algorithmic ops of the convolution / the GEMM kernel's time; value = the same ops / "
+                  "the whole operator (im2col, B packing, GEMM, zero-point correction)")
+    t0 = time.perf_counter()
+    O.conv_integer(x[:1], w, 117, wz, pads=(1, 1))
+    cpu_s = time.perf_counter() - t0
+    return dict(metric="ConvInteger int8 TOPS (cfg2 shape: u8[32,64,56,56] x i8[64,64,3,3], pad 1), 1 GPU",
+                value=round(ops / (ms * 1e-3) / 1e12, 1), unit="TOPS", ms_per_step=ms,
+                config={"workload": "ConvInteger 3x3 s1 p1, x u8[32,64,56,56], w i8[64,64,3,3], per-channel "
+                                    "w_zero_point, int32 output", "global_batch": N},
+                roofline=rl,
+                cpu_baseline={"value": round(ops / N / cpu_s / 1e12, 5), "unit": "TOPS", "cores": 1,
+                              "kind": "port", "sample": "oracle integer convolution of 1 image (scalar C)"},
+                dtype="u8")
+
+
 def run_hbm_copy(args, dev):
     """Device-to-device copy of a known size through hipMemcpyAsync: the
     calibration kernel for the FETCH_SIZE / WRITE_SIZE counters and the
@@ -628,7 +685,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="resnet50",
-                    choices=["resnet50", "mobilenetv2", "bert", "qoperator", "bn", "qconv", "qmatmul",
+                    choices=["resnet50", "mobilenetv2", "bert", "qoperator", "bn", "convinteger", "qconv", "qmatmul",
                              "hbm_copy"])
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
@@ -645,7 +702,7 @@ def main():
     dev = torch.device("cuda:0")
     run = {"resnet50": lambda a, d: run_model(a, d, "resnet50"),
            "mobilenetv2": lambda a, d: run_model(a, d, "mobilenetv2"),
-           "bert": run_bert, "qoperator": run_qoperator, "bn": run_bn,
+           "bert": run_bert, "qoperator": run_qoperator, "bn": run_bn, "convinteger": run_convinteger,
            "qconv": run_qconv, "qmatmul": run_qmatmul, "hbm_copy": run_hbm_copy}[args.config]
     res = run(args, dev)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,

@@ -234,6 +234,24 @@ int nnrh_matmul_integer_run(nnrh_matmul_integer_t h, const void* a_dev,
                             int32_t* y_dev, int batch, void* stream);
 int nnrh_matmul_integer_destroy(nnrh_matmul_integer_t h);
 
+/* ---- ConvInteger ----------------------------------------------------------
+ * Replaces ConvInteger_operator's 4-D path (src/backend/cpu/ConvInteger.cpp:
+ * 146-233): y[n][oc][oh][ow] = sum (x - x_zp)(w - w_zp[oc]) in int32, NCHW.
+ * x / w uint8 or int8 (NNRH_U8 / NNRH_S8), w [OC][C/group][kH][kW]. The
+ * reference accumulates in fp32 (im2col + float GEMM) and rounds; that equals
+ * this exact integer result whenever K * max|x - x_zp| * max|w - w_zp| <=
+ * 2^24 (K = C/group * kH * kW), where every partial sum is exact in float.
+ * Output extents and pads are the caller's (the operator's auto_pad rules).
+ * w_zp_dev: per-output-channel zero points (int32 [OC], device) or NULL for
+ * the scalar w_zp. The handle owns the im2col workspace.                  */
+typedef struct nnrh_conv_integer* nnrh_conv_integer_t;
+int nnrh_conv_integer_create(nnrh_conv_integer_t* h, int N, int C, int iH, int iW, int OC,
+                             int kH, int kW, int sH, int sW, int pH, int pW, int dH, int dW,
+                             int oH, int oW, int group, int x_dtype, int w_dtype);
+int nnrh_conv_integer_run(nnrh_conv_integer_t h, const void* x_dev, const void* w_dev, int x_zp,
+                          int w_zp, const int32_t* w_zp_dev, int32_t* y_dev, void* stream);
+int nnrh_conv_integer_destroy(nnrh_conv_integer_t h);
+
 /* ---- QuantizeLinear / DequantizeLinear / DynamicQuantizeLinear ----------
  * QuantizeLinear.cpp:128-194 (per-tensor uint8/int8), DequantizeLinear.cpp:
  * 100-152, DynamicQuantizeLinear.cpp:27-58.                              */

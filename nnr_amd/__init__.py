@@ -397,6 +397,32 @@ def qlinear_concat(xs, counts, outer, scales, zps, y_s, y_zp):
     return y
 
 
+def conv_integer(x, w, x_zp, w_zp, strides=(1, 1), pads=(0, 0), dilations=(1, 1), group=1, out_hw=None):
+    """ConvInteger on the device (nnrh_conv_integer_*): x, w device uint8 /
+    int8 NCHW tensors; w_zp a scalar or a sequence of OC values; int32 y."""
+    import numpy as np
+    import torch
+    N, C, iH, iW = x.shape
+    OC, _, kH, kW = w.shape
+    if out_hw is None:
+        out_hw = tuple((d + 2 * p_ - ((k - 1) * dl + 1)) // s + 1
+                       for d, p_, k, dl, s in zip((iH, iW), pads, (kH, kW), dilations, strides))
+    dt = lambda t: U8 if t.dtype == torch.uint8 else S8
+    h = ct.c_void_p()
+    check(lib().nnrh_conv_integer_create(ct.byref(h), N, C, iH, iW, OC, kH, kW, strides[0], strides[1], pads[0],
+                                         pads[1], dilations[0], dilations[1], out_hw[0], out_hw[1], group, dt(x), dt(w)))
+    y = torch.empty((N, OC, *out_hw), dtype=torch.int32, device=x.device)
+    wz = np.asarray(w_zp, np.int32).reshape(-1)
+    wz_dev = torch.from_numpy(wz).to(x.device) if wz.size > 1 else None
+    try:
+        check(lib().nnrh_conv_integer_run(h, ptr(x), ptr(w), int(x_zp), int(wz[0]) if wz_dev is None else 0,
+                                          ptr(wz_dev) if wz_dev is not None else None, ptr(y), cur_stream()))
+        check(lib().nnrh_stream_synchronize(cur_stream()))
+    finally:
+        lib().nnrh_conv_integer_destroy(h)
+    return y
+
+
 def batchnorm_u8(x, a, b, nhwc=0):
     """Folded BatchNormalization: y = uint8(A[c] * x + B[c]). x: device uint8 or
     float32 [N, C, ...] (with nhwc, [N, H, W, C]); a, b: device float32 [C]."""

@@ -1429,6 +1429,100 @@ extern "C" int nnrh_qlinear_avgpool(const void* x, void* y, int N, int C, int iH
     return NNRH_OK;
 }
 
+// ---- ConvInteger --------------------------------------------------------------
+struct nnrh_conv_integer {
+    Im2colArgs a{};
+    int OC = 0, MM = 0, x_dtype = 0, w_dtype = 0;
+    long long K = 0, P = 0;
+    uint8_t* col = nullptr;
+    int32_t* S = nullptr;
+    nnrh_matmul_integer_t mi = nullptr;
+    ~nnrh_conv_integer() {
+        dfree(col);
+        dfree(S);
+        if (mi) nnrh_matmul_integer_destroy(mi);
+    }
+};
+
+extern "C" int nnrh_conv_integer_create(nnrh_conv_integer_t* out, int N, int C, int iH, int iW, int OC, int kH,
+                                        int kW, int sH, int sW, int pH, int pW, int dH, int dW, int oH, int oW,
+                                        int group, int x_dtype, int w_dtype) {
+    if (!out) return set_err(NNRH_ERR_INVALID, "conv_integer: handle NULL");
+    *out = nullptr;
+    if (N <= 0 || C <= 0 || iH <= 0 || iW <= 0 || OC <= 0 || kH <= 0 || kW <= 0 || sH <= 0 || sW <= 0 || dH <= 0 ||
+        dW <= 0 || oH <= 0 || oW <= 0 || group <= 0 || pH < 0 || pW < 0 || C % group || OC % group)
+        return set_err(NNRH_ERR_INVALID, "conv_integer: bad shape");
+    if ((x_dtype != NNRH_U8 && x_dtype != NNRH_S8) || (w_dtype != NNRH_U8 && w_dtype != NNRH_S8))
+        return set_err(NNRH_ERR_UNSUPPORTED, "conv_integer: dtype");
+    auto* h = new nnrh_conv_integer();
+    h->a = Im2colArgs{nullptr, nullptr, N, C, iH, iW, group, kH, kW, sH, sW, pH, pW, dH, dW, oH, oW, 0};
+    h->OC = OC;
+    h->MM = OC / group;
+    h->x_dtype = x_dtype;
+    h->w_dtype = w_dtype;
+    h->K = (long long)(C / group) * kH * kW;
+    h->P = (long long)oH * oW;
+    const long long batches = (long long)N * group;
+    if (h->K > INT32_MAX || h->P > INT32_MAX) {
+        delete h;
+        return set_err(NNRH_ERR_UNSUPPORTED, "conv_integer: GEMM extents beyond int32");
+    }
+    int rc0 = nnrh_malloc((void**)&h->col, (size_t)(batches * h->K * h->P));
+    if (rc0 == NNRH_OK) rc0 = nnrh_malloc((void**)&h->S, (size_t)(batches * h->P) * sizeof(int32_t));
+    if (rc0 != NNRH_OK) {
+        delete h;
+        return rc0;
+    }
+    // y[b] = W_g[MM][K] . col[b][K][P]: one launch over every image when
+    // group == 1 (W broadcast), else one per image over the groups
+    const int rc = nnrh_matmul_integer_create(&h->mi, h->MM, (int)h->P, (int)h->K, w_dtype, x_dtype,
+                                              group == 1 ? N : group);
+    if (rc != NNRH_OK) {
+        delete h;
+        return rc;
+    }
+    *out = h;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_conv_integer_run(nnrh_conv_integer_t h, const void* x, const void* w, int x_zp, int w_zp,
+                                     const int32_t* w_zp_dev, int32_t* y, void* stream) {
+    if (!h || !x || !w || !y) return set_err(NNRH_ERR_INVALID, "conv_integer_run: NULL argument");
+    hipStream_t s = S(stream);
+    Im2colArgs a = h->a;
+    a.x = (const uint8_t*)x;
+    a.col = h->col;
+    a.pad = (uint8_t)x_zp;
+    {
+        ProfScope ps("im2col", s);
+        HIP_TRY(launch_im2col_u8(a, s), "im2col");
+    }
+    const long long KP = h->K * h->P, wsz = (long long)h->MM * h->K, ysz = (long long)h->MM * h->P;
+    const int wz = w_zp_dev ? 0 : w_zp;
+    if (a.group == 1) {
+        const int rc = nnrh_matmul_integer_run(h->mi, w, 0, h->col, KP, wz, x_zp, y, a.N, stream);
+        if (rc != NNRH_OK) return rc;
+    } else {
+        for (int n = 0; n < a.N; ++n) {
+            const int rc = nnrh_matmul_integer_run(h->mi, w, wsz, h->col + (size_t)n * a.group * KP, KP, wz, x_zp,
+                                                   y + (size_t)n * a.group * ysz, a.group, stream);
+            if (rc != NNRH_OK) return rc;
+        }
+    }
+    if (w_zp_dev) {
+        ProfScope ps("conv_integer_wzp", s);
+        HIP_TRY(launch_conv_integer_wzp(h->col, h->S, y, w_zp_dev, (long long)a.N * a.group, a.group, h->MM, h->K,
+                                        h->P, h->x_dtype == NNRH_S8, x_zp, s),
+                "conv_integer_wzp");
+    }
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_conv_integer_destroy(nnrh_conv_integer_t h) {
+    delete h;
+    return NNRH_OK;
+}
+
 extern "C" int nnrh_batchnorm_u8(const void* x, int x_is_f32, uint8_t* y, const float* a, const float* b,
                                  long long N, int C, long long HW, int nhwc, void* stream) {
     if (!x || !y || !a || !b) return set_err(NNRH_ERR_INVALID, "batchnorm_u8: NULL");

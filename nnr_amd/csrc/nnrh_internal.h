@@ -169,6 +169,16 @@ hipError_t launch_depthwise(const uint8_t* x, const int8_t* w, uint8_t* y,
 // depthwise, NHWC in/out, C % 16 == 0, w_zp 0, at most 12 taps, no tails
 // (nnrh_misc.hip); wdot [ceil(taps/4)][C] 4 taps per dword, corr[C]
 // 3x3 depthwise, stride 1 or 2, dilation 1, NHWC in and out, C % 8 == 0
+// ConvInteger's im2col (nnrh_misc.hip)
+struct Im2colArgs {
+    const uint8_t* x;
+    uint8_t* col;
+    int N, C, iH, iW, group, kH, kW, sH, sW, pH, pW, dH, dW, oH, oW;
+    uint8_t pad;
+};
+hipError_t launch_im2col_u8(const Im2colArgs& a, hipStream_t s);
+hipError_t launch_conv_integer_wzp(const uint8_t* col, int32_t* S, int32_t* y, const int32_t* wzp, long long batches,
+                                   int group, int MM, long long K, long long P, int x_s8, int x_zp, hipStream_t s);
 hipError_t launch_depthwise3x3(const uint8_t* x, const uint32_t* wrow, const int32_t* corr, uint8_t* y,
                                const float* cs, const float* bf, int N, int C, int H, int W, int oH, int oW,
                                int stride, int pad_t, int pad_l, int x_zp, int a_xor, float inv_y, int y_zp,

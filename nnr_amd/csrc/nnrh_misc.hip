@@ -909,4 +909,81 @@ hipError_t launch_fill_u8(void* p, uint8_t v, long long n, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// ConvInteger (ConvInteger.cpp:146-233): im2col of x into col[n*group + g][k][p]
+// (k = (c * kH + kh) * kW + kw over the group's channels, p = oh * oW + ow),
+// taps outside the image filled with the byte of x_zp so that (x - x_zp) is
+// 0 there, as the reference's zero-padded float im2col of (x - x_zp).
+__global__ __launch_bounds__(256) void im2col_u8_kernel(Im2colArgs a) {
+    const int CC = a.C / a.group;
+    const long long P = (long long)a.oH * a.oW;
+    const long long K = (long long)CC * a.kH * a.kW;
+    const long long total = (long long)a.N * a.group * K * P;
+    for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
+        const long long p = e % P;
+        long long r = e / P;
+        const long long k = r % K;
+        const long long b = r / K;                 // n * group + g
+        const int kw = (int)(k % a.kW), kh = (int)((k / a.kW) % a.kH), c = (int)(k / ((long long)a.kW * a.kH));
+        const int ow = (int)(p % a.oW), oh = (int)(p / a.oW);
+        const int ih = oh * a.sH - a.pH + kh * a.dH, iw = ow * a.sW - a.pW + kw * a.dW;
+        const long long n = b / a.group, g = b % a.group;
+        uint8_t v = a.pad;
+        if (ih >= 0 && ih < a.iH && iw >= 0 && iw < a.iW)
+            v = a.x[((n * a.C + g * CC + c) * a.iH + ih) * (long long)a.iW + iw];
+        a.col[e] = v;
+    }
+}
+
+hipError_t launch_im2col_u8(const Im2colArgs& a, hipStream_t s) {
+    const long long total = (long long)a.N * a.group * (a.C / a.group) * a.kH * a.kW * a.oH * a.oW;
+    if (total <= 0) return hipSuccess;
+    long long blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(im2col_u8_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+// per-channel weight zero points: y[b][m][p] -= w_zp[g * MM + m] * S[b][p],
+// S[b][p] = sum_k (col[b][k][p] - x_zp), so that the GEMM's sum_k w (x - x_zp)
+// becomes sum_k (w - w_zp[oc]) (x - x_zp) exactly (int32, wrapping)
+__global__ __launch_bounds__(256) void col_sums_kernel(const uint8_t* __restrict col, int32_t* __restrict S,
+                                                       long long batches, long long K, long long P, int x_s8,
+                                                       int x_zp) {
+    const long long total = batches * P;
+    for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
+        const long long b = e / P, p = e % P;
+        const uint8_t* c = col + b * K * P + p;
+        uint32_t sum = 0;
+        for (long long k = 0; k < K; ++k) sum += (uint32_t)(x_s8 ? (int)(int8_t)c[k * P] : (int)c[k * P]);
+        S[e] = (int32_t)(sum - (uint32_t)x_zp * (uint32_t)K);
+    }
+}
+
+__global__ __launch_bounds__(256) void wzp_correct_kernel(int32_t* __restrict y, const int32_t* __restrict S,
+                                                          const int32_t* __restrict wzp, long long batches, int group,
+                                                          int MM, long long P) {
+    const long long total = batches * MM * P;
+    for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
+        const long long p = e % P;
+        const long long r = e / P;
+        const int m = (int)(r % MM);
+        const long long b = r / MM;
+        const int g = (int)(b % group);
+        y[e] = (int32_t)((uint32_t)y[e] - (uint32_t)wzp[g * MM + m] * (uint32_t)S[b * P + p]);
+    }
+}
+
+hipError_t launch_conv_integer_wzp(const uint8_t* col, int32_t* S, int32_t* y, const int32_t* wzp, long long batches,
+                                   int group, int MM, long long K, long long P, int x_s8, int x_zp, hipStream_t s) {
+    long long blocks = (batches * P + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(col_sums_kernel, dim3((unsigned)blocks), dim3(256), 0, s, col, S, batches, K, P, x_s8, x_zp);
+    blocks = (batches * MM * P + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(wzp_correct_kernel, dim3((unsigned)blocks), dim3(256), 0, s, y, S, wzp, batches, group, MM, P);
+    return hipGetLastError();
+}
+
 }  // namespace nnrh

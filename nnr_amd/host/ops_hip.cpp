@@ -712,6 +712,98 @@ struct QLinearConcat_hip : operator_t {
 };
 
 // ===========================================================================
+// ConvInteger (src/backend/cpu/ConvInteger.cpp): 4-D, int32 NCHW output.
+// Attributes and output extents as :30-143 (auto_pad NOTSET / SAME_UPPER /
+// SAME_LOWER / VALID with the reference's float ceil / floor formulas); the
+// convolution reads the begin pads (:185). x_zero_point scalar, w_zero_point
+// scalar or per output channel (:150-176). Exact int32 (see nnrh_conv_integer).
+struct ConvInteger_hip : operator_t {
+    std::vector<int> kernels, dilations, pads, strides;
+    std::string auto_pad;
+    int group = 1;
+    int cp[4] = {0, 0, 0, 0};
+    nnrh_conv_integer_t h = nullptr;
+    int32_t* wzp_dev = nullptr;
+    ~ConvInteger_hip() override {
+        if (h) nnrh_conv_integer_destroy(h);
+    }
+    bool init() override {
+        if (inputs.size() < 2 || outputs.size() != 1) return false;
+        auto_pad = attribute_s("auto_pad", "NOTSET");
+        group = (int)attribute("group", 1);
+        for (auto v : attribute_ints("kernel_shape")) kernels.push_back((int)v);
+        for (auto v : attribute_ints("dilations")) dilations.push_back((int)v);
+        for (auto v : attribute_ints("pads")) pads.push_back((int)v);
+        for (auto v : attribute_ints("strides")) strides.push_back((int)v);
+        return true;
+    }
+    int zp_at(size_t i, int idx) const {
+        const tensor_t* z = inputs.size() > i ? inputs[i] : nullptr;
+        if (!z || !z->has_host()) return 0;
+        if (z->type == NNR_DATA_TYPE_UINT8) return z->h<uint8_t>()[idx];
+        if (z->type == NNR_DATA_TYPE_INT8) return z->h<int8_t>()[idx];
+        return 0;
+    }
+    bool reshape() override {
+        tensor_t *x = inputs[0], *w = inputs[1];
+        if (x->ndim() != 4 || w->ndim() != 4) return bad(this, "4-D input and weights only");
+        if (x->type != NNR_DATA_TYPE_UINT8 && x->type != NNR_DATA_TYPE_INT8) return bad(this, "uint8 / int8 input");
+        if (kernels.empty()) kernels = {w->dims[2], w->dims[3]};
+        if (dilations.empty()) dilations = {1, 1};
+        if (strides.empty()) strides = {1, 1};
+        if (pads.empty()) pads = {0, 0, 0, 0};
+        if (kernels.size() != 2 || dilations.size() != 2 || strides.size() != 2 || pads.size() != 4)
+            return bad(this, "2-D attributes");
+        int dims[2];
+        for (int i = 0; i < 2; ++i) {
+            const int in = x->dims[2 + i], ke = (kernels[i] - 1) * dilations[i] + 1, st = strides[i];
+            if (auto_pad == "SAME_UPPER" || auto_pad == "SAME_LOWER") {
+                const int pad = (int)(ceilf(in / (float)st) - 1) * st + ke - in;
+                const int small = pad / 2, large = pad - small;
+                cp[i] = auto_pad == "SAME_UPPER" ? small : large;
+                cp[i + 2] = auto_pad == "SAME_UPPER" ? large : small;
+                dims[i] = (int)ceilf(in / (float)st);
+            } else if (auto_pad == "VALID") {
+                cp[i] = cp[i + 2] = 0;
+                dims[i] = (int)ceilf((in - ke + 1) / (float)st);
+            } else {
+                cp[i] = pads[i];
+                cp[i + 2] = pads[i + 2];
+                dims[i] = (int)floorf((in + cp[i] + cp[i + 2] - ke) / (float)st + 1);
+            }
+        }
+        outputs[0]->format = memory_layout_t::NCHW;
+        if (!outputs[0]->reshape({x->dims[0], w->dims[0], dims[0], dims[1]}, NNR_DATA_TYPE_INT32)) return false;
+        if (ctx->shape_only || h) return true;
+        const int OC = w->dims[0];
+        if (x->dims[1] != w->dims[1] * group) return bad(this, "channels != weight channels * group");
+        if (nnrh_conv_integer_create(&h, x->dims[0], x->dims[1], x->dims[2], x->dims[3], OC, kernels[0], kernels[1],
+                                     strides[0], strides[1], cp[0], cp[1], dilations[0], dilations[1], dims[0],
+                                     dims[1], group, qdtype(x->type), qdtype(w->type)) != NNRH_OK)
+            return bad(this, nnrh_last_error());
+        const tensor_t* wz = inputs.size() > 3 ? inputs[3] : nullptr;
+        if (wz && wz->ndata > 1) {
+            if (!wz->has_host() || (int)wz->ndata != OC) return bad(this, "w_zero_point: constant [OC] expected");
+            std::vector<int32_t> v(OC);
+            for (int c = 0; c < OC; ++c) v[c] = zp_at(3, c);
+            wzp_dev = (int32_t*)ctx->device_alloc(v.size() * sizeof(int32_t));
+            if (!wzp_dev || nnrh_memcpy(wzp_dev, v.data(), v.size() * sizeof(int32_t), 0, ctx->stream) != NNRH_OK ||
+                nnrh_stream_synchronize(ctx->stream) != NNRH_OK)
+                return bad(this, "w_zero_point upload failed");
+        }
+        return true;
+    }
+    bool exec() override {
+        return ok(this, nnrh_conv_integer_run(h, inputs[0]->data, inputs[1]->data, zp_at(2, 0), wzp_dev ? 0 : zp_at(3, 0),
+                                              wzp_dev, (int32_t*)outputs[0]->data, ctx->stream));
+    }
+    double num_ops() const override {
+        const tensor_t* w = inputs[1];
+        return 2.0 * (double)outputs[0]->ndata * w->dims[1] * w->dims[2] * w->dims[3];
+    }
+};
+
+// ===========================================================================
 // BatchNormalization (src/backend/cpu/BatchNormalization.cpp), inference.
 // After fold_bn_qdq its scale / bias inputs hold the combined A / B and it
 // writes uint8 from uint8 (DQ -> BN -> Q) or fp32 (BN -> Q) input
@@ -1229,6 +1321,7 @@ const op_registrar_t reg[] = {
     {"QLinearConcat", backend_t::HIP, make<QLinearConcat_hip>},
     {"MaxPool", backend_t::HIP, make<MaxPool_hip>},
     {"BatchNormalization", backend_t::HIP, make<BatchNormalization_hip>},
+    {"ConvInteger", backend_t::HIP, make<ConvInteger_hip>},
     {"GlobalAveragePool", backend_t::HIP, make<GlobalAveragePool_hip>},
     {"Flatten", backend_t::HIP, make<Flatten_hip>},
     {"Reshape", backend_t::HIP, make<Reshape_hip>},

@@ -292,6 +292,26 @@ def bn_net(batch=2, C=40, hw=13, seed=26):
     return g
 
 
+def conv_integer_net(batch=2, C=16, hw=15, OC=24, k=3, seed=28, per_channel=True, auto_pad="NOTSET",
+                     strides=(1, 1), pads=(1, 1, 1, 1), group=1, x_dtype=np.uint8):
+    """Q(input) -> ConvInteger(x, w, x_zp, w_zp) -> int32 output (the form
+    dynamically quantized convolutions take)."""
+    g = Graph()
+    rng = np.random.default_rng(seed)
+    g.inputs["input"] = (np.float32, (batch, C, hw, hw))
+    zdt = x_dtype
+    x_zp = np.array(120 if x_dtype == np.uint8 else -5, zdt)
+    xq = g.node("QuantizeLinear", ["input", g.init("xs", np.array(0.02, F32)), g.init("xz", x_zp)], name="input_Q")
+    w = rng.integers(-128, 128, (OC, C // group, k, k), dtype=np.int8)
+    wz = rng.integers(-20, 20, OC).astype(np.int8) if per_channel else np.array(3, np.int8)
+    attrs = dict(auto_pad=auto_pad, strides=list(strides), group=group)
+    if auto_pad == "NOTSET":
+        attrs["pads"] = list(pads)
+    y = g.node("ConvInteger", [xq, g.init("w", w), "xz", g.init("wz", wz)], name="convint", **attrs)
+    g.outputs.append(y)
+    return g
+
+
 # MobileNetV2 (Sandler et al. 2018, width 1.0): (expansion t, channels c,
 # repeats n, first stride s) of the 17 inverted-residual blocks
 MBV2_BLOCKS = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 96, 3, 1),

@@ -260,6 +260,28 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
             if len(ins) > 2 and ins[2]:
                 y = y + a.get("beta", 1.0) * val(ins[2]).astype(np.float64)
             y = y.astype(np.float32)
+        elif op == "ConvInteger":
+            a = graph.node_by_name(nd["name"]).attrs
+            x, w = val(ins[0]), val(ins[1])
+            k = a.get("kernel_shape", list(w.shape[2:]))
+            st, dl = a.get("strides", [1, 1]), a.get("dilations", [1, 1])
+            pads = list(a.get("pads", [0, 0, 0, 0]))
+            ap = a.get("auto_pad", "NOTSET")
+            out = []
+            for i in range(2):
+                d, ke = x.shape[2 + i], (k[i] - 1) * dl[i] + 1
+                if ap in ("SAME_UPPER", "SAME_LOWER"):
+                    pad = (int(np.ceil(np.float32(d) / np.float32(st[i]))) - 1) * st[i] + ke - d
+                    pads[i] = pad // 2 if ap == "SAME_UPPER" else pad - pad // 2
+                    out.append(int(np.ceil(np.float32(d) / np.float32(st[i]))))
+                elif ap == "VALID":
+                    pads[i] = 0
+                    out.append(int(np.ceil(np.float32(d - ke + 1) / np.float32(st[i]))))
+                else:
+                    out.append(int(np.floor(np.float32(d + pads[i] + pads[i + 2] - ke) / np.float32(st[i]) + 1)))
+            wz = val(ins[3]).reshape(-1).astype(np.int32) if len(ins) > 3 and ins[3] else 0
+            y = O.conv_integer(x, w, int(scal(ins[2])) if len(ins) > 2 and ins[2] else 0, wz, st, pads[:2], dl,
+                               a.get("group", 1), out_hw=tuple(out))
         elif op == "BatchNormalization":
             # inference, fp32 (BatchNormalization.cpp:126-160), in float64
             x = val(ins[0]).astype(np.float64)

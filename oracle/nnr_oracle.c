@@ -983,3 +983,38 @@ void orc_batchnorm_u8(const void* x, int x_f32, uint8_t* y, const float* A, cons
     }
 #undef XV
 }
+
+/* ConvInteger, 4-D (ConvInteger.cpp:236-354, the integer loops; the 4-D
+ * float im2col path :146-233 gives the same values while every partial sum
+ * is exact in float): y[n][oc][oh][ow] = sum (x - x_zp)(w - w_zp[oc]) over
+ * in-image taps, int32 with wrap-around. wzp: int32 [OC]. */
+void orc_conv_integer(const void* x, int x_dt, const void* w, int w_dt, int x_zp, const int32_t* wzp, int N, int C,
+                      int iH, int iW, int OC, int kH, int kW, int sH, int sW, int pH, int pW, int dH, int dW, int oH,
+                      int oW, int group, int32_t* y) {
+    const int CC = C / group, MM = OC / group;
+#define LX(i) (x_dt ? (int)((const int8_t*)x)[i] : (int)((const uint8_t*)x)[i])
+#define LW(i) (w_dt ? (int)((const int8_t*)w)[i] : (int)((const uint8_t*)w)[i])
+    for (int n = 0; n < N; ++n)
+        for (int oc = 0; oc < OC; ++oc) {
+            const int g = oc / MM;
+            for (int oh = 0; oh < oH; ++oh)
+                for (int ow = 0; ow < oW; ++ow) {
+                    uint32_t sum = 0;
+                    for (int c = 0; c < CC; ++c)
+                        for (int kh = 0; kh < kH; ++kh) {
+                            const int ih = oh * sH - pH + kh * dH;
+                            if (ih < 0 || ih >= iH) continue;
+                            for (int kw = 0; kw < kW; ++kw) {
+                                const int iw = ow * sW - pW + kw * dW;
+                                if (iw < 0 || iw >= iW) continue;
+                                const int xv = LX((((size_t)n * C + g * CC + c) * iH + ih) * iW + iw) - x_zp;
+                                const int wv = LW((((size_t)oc * CC + c) * kH + kh) * kW + kw) - wzp[oc];
+                                sum += (uint32_t)xv * (uint32_t)wv;
+                            }
+                        }
+                    y[(((size_t)n * OC + oc) * oH + oh) * oW + ow] = (int32_t)sum;
+                }
+        }
+#undef LX
+#undef LW
+}

@@ -166,6 +166,11 @@ void orc_fold_bn(int C, const float* sc, const float* bias, const float* mean, c
 void orc_batchnorm_u8(const void* x, int x_f32, uint8_t* y, const float* A, const float* B, long long N, int C,
                       long long HW, int nhwc);
 
+/* ConvInteger, 4-D (ConvInteger.cpp:146-354), exact int32 */
+void orc_conv_integer(const void* x, int x_dt, const void* w, int w_dt, int x_zp, const int32_t* wzp, int N, int C,
+                      int iH, int iW, int OC, int kH, int kW, int sH, int sW, int pH, int pW, int dH, int dW, int oH,
+                      int oW, int group, int32_t* y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,6 +75,7 @@ def lib():
             "orc_qlinear_mul": (None, [i, vp, vp, vp, sz, i, i, i, i, i, f, i, f, i, f, i]),
             "orc_nchw_to_nhwc_u8": (None, [vp, vp, i, i, i]),
             "orc_fold_bn": (None, [i, vp, vp, vp, vp, f, i, f, i, f, i, vp, vp]),
+            "orc_conv_integer": (None, [vp, i, vp, i, i, vp] + [i] * 16 + [vp]),
             "orc_batchnorm_u8": (None, [vp, i, vp, vp, vp, ct.c_longlong, i, ct.c_longlong, i]),
         }
         for n, (r, a) in sigs.items():
@@ -254,6 +255,25 @@ def batchnorm_u8(x, A, B, nhwc=0):
     A = np.ascontiguousarray(A, np.float32)
     B = np.ascontiguousarray(B, np.float32)
     lib().orc_batchnorm_u8(_p(x), 1 if x.dtype == np.float32 else 0, _p(y), _p(A), _p(B), N, C, HW, nhwc)
+    return y
+
+
+def conv_integer(x, w, x_zp, w_zp, strides=(1, 1), pads=(0, 0), dilations=(1, 1), group=1, out_hw=None):
+    """ConvInteger, 4-D NCHW: int32 y = sum (x - x_zp)(w - w_zp[oc]); w_zp a
+    scalar or [OC]; pads = the begin pads; out_hw defaults to the explicit-pad
+    extent with the end pads equal to the begin ones."""
+    x = np.ascontiguousarray(x)
+    w = np.ascontiguousarray(w)
+    N, C, iH, iW = x.shape
+    OC, _, kH, kW = w.shape
+    if out_hw is None:
+        out_hw = tuple((d + 2 * p_ - ((k - 1) * dl + 1)) // s + 1
+                       for d, p_, k, dl, s in zip((iH, iW), pads, (kH, kW), dilations, strides))
+    wzp = np.ascontiguousarray(np.broadcast_to(np.asarray(w_zp, np.int32).reshape(-1), (OC,)), np.int32)
+    y = np.empty((N, OC, *out_hw), np.int32)
+    lib().orc_conv_integer(_p(x), dt_of(x), _p(w), dt_of(w), int(x_zp), _p(wzp), N, C, iH, iW, OC, kH, kW,
+                           strides[0], strides[1], pads[0], pads[1], dilations[0], dilations[1], out_hw[0],
+                           out_hw[1], group, _p(y))
     return y
 
 

@@ -26,7 +26,7 @@ def check_graph(g, feeds, out_name, atol=1e-3, conv_add=True):
         dev, _ = s.output(o)
         ref = env[o]
         assert dev.shape == ref.shape, (p["name"], dev.shape, ref.shape)
-        if dev.dtype in (np.uint8, np.int8):
+        if np.issubdtype(dev.dtype, np.integer):
             mism = np.count_nonzero(dev != ref)
             assert mism == 0, f"{p['name']} ({p['op']} {p['variant']}): {mism} of {dev.size} differ"
             if p["op"] == "QLinearConv":
@@ -278,3 +278,16 @@ def test_bn_graph(dev):
     plan, _, n_int = check_graph(g, {"input": x}, g.outputs[0])
     assert sorted(p["variant"] for p in plan if p["op"] == "BatchNormalization") == ["BN-Q", "DQ-BN-Q"]
     assert n_int >= 4
+
+
+@pytest.mark.parametrize("kw", [dict(), dict(per_channel=False, auto_pad="SAME_UPPER", strides=(2, 2)),
+                                dict(auto_pad="VALID", group=2), dict(x_dtype=np.int8, auto_pad="SAME_LOWER",
+                                                                      strides=(2, 1))])
+def test_conv_integer_graph(dev, kw):
+    """ConvInteger through the host framework (auto_pad forms, groups, scalar
+    and per-channel weight zero points): int32 output exact."""
+    g = synth.conv_integer_net(**kw)
+    rng = np.random.default_rng(29)
+    x = rng.uniform(-2.0, 2.0, (2, 16, 15, 15)).astype(np.float32)
+    plan, y, _ = check_graph(g, {"input": x}, g.outputs[0], atol=0)
+    assert [p["op"] for p in plan].count("ConvInteger") == 1 and y.dtype == np.int32

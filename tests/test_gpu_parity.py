@@ -778,3 +778,27 @@ def test_batchnorm_folded(dev, nhwc, f32_in, N, C, Hh, W):
     ref = O.batchnorm_u8(x, A, B, nhwc=nhwc)
     y = H.batchnorm_u8(to_dev(x, dev), to_dev(A, dev), to_dev(B, dev), nhwc=nhwc)
     assert np.array_equal(to_np(y), ref)
+
+
+@pytest.mark.parametrize("xdt,wdt,per_ch,s,p,d,group,shape", [
+    (np.uint8, np.int8, False, (1, 1), (1, 1), (1, 1), 1, (32, 64, 56, 56)),   # cfg2's shape
+    (np.uint8, np.int8, True, (1, 1), (1, 1), (1, 1), 1, (2, 16, 15, 15)),
+    (np.uint8, np.uint8, True, (2, 1), (0, 2), (1, 2), 2, (3, 8, 9, 11)),
+    (np.int8, np.int8, True, (1, 2), (2, 1), (2, 1), 4, (2, 8, 9, 11)),
+    (np.int8, np.uint8, False, (2, 2), (0, 0), (1, 1), 1, (1, 3, 7, 7))])
+def test_conv_integer(dev, xdt, wdt, per_ch, s, p, d, group, shape):
+    """ConvInteger (im2col + the i8 MFMA MatMulInteger GEMM, per-channel
+    weight zero points by a correction pass) bit-exact with the oracle's
+    integer convolution, in the range where the reference's float path is
+    exact (K * 255 * 255 < 2^24 here)."""
+    rng = np.random.default_rng(sum(shape) + group)
+    info = lambda t: (0, 256) if t == np.uint8 else (-128, 128)
+    N, C, Hh, W = shape
+    OC = 64 if C == 64 else 12
+    x = rng.integers(*info(xdt), shape, dtype=xdt)
+    w = rng.integers(*info(wdt), (OC, C // group, 3, 3), dtype=wdt)
+    x_zp = 131 if xdt == np.uint8 else -3
+    w_zp = rng.integers(*info(wdt), OC) if per_ch else (7 if wdt == np.uint8 else -2)
+    ref = O.conv_integer(x, w, x_zp, w_zp, s, p, d, group)
+    y = H.conv_integer(to_dev(x, dev), to_dev(w, dev), x_zp, w_zp, s, p, d, group)
+    assert np.array_equal(to_np(y), ref)

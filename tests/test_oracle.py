@@ -617,3 +617,51 @@ def test_folded_bn_negative_saturation():
     assert np.all(yn[..., :16] == 255) and np.all(yn[..., 16:] == 0)
     xf = x.transpose(0, 2, 3, 1).astype(np.float32).copy()
     assert np.all(O.batchnorm_u8(xf, A, B, nhwc=1) == 0)     # fp32 input: clamped first
+
+
+# ---------------------------------------------------------------------------
+# ConvInteger (ConvInteger.cpp:146-354)
+
+def _conv_int_numpy(x, w, x_zp, w_zp, s, p, d, group):
+    """int64 brute force over zero-padded (x - x_zp) windows."""
+    N, C, H, W = x.shape
+    OC, CC, kH, kW = w.shape
+    xs = np.pad(x.astype(np.int64) - x_zp, ((0, 0), (0, 0), (p[0], p[0]), (p[1], p[1])))
+    ws = w.astype(np.int64) - np.broadcast_to(np.asarray(w_zp, np.int64).reshape(-1), (OC,))[:, None, None, None]
+    oH = (H + 2 * p[0] - ((kH - 1) * d[0] + 1)) // s[0] + 1
+    oW = (W + 2 * p[1] - ((kW - 1) * d[1] + 1)) // s[1] + 1
+    y = np.zeros((N, OC, oH, oW), np.int64)
+    MM = OC // group
+    for oc in range(OC):
+        g = oc // MM
+        for kh in range(kH):
+            for kw in range(kW):
+                win = xs[:, g * CC:(g + 1) * CC, kh * d[0]: kh * d[0] + s[0] * (oH - 1) + 1: s[0],
+                         kw * d[1]: kw * d[1] + s[1] * (oW - 1) + 1: s[1]]
+                y[:, oc] += np.einsum("nchw,c->nhw", win, ws[oc, :, kh, kw])
+    return y.astype(np.int32)
+
+
+@pytest.mark.parametrize("xdt,wdt,per_ch,s,p,d,group", [
+    (np.uint8, np.int8, False, (1, 1), (1, 1), (1, 1), 1),
+    (np.uint8, np.uint8, True, (2, 1), (0, 2), (1, 2), 2),
+    (np.int8, np.int8, True, (1, 2), (2, 1), (2, 1), 4)])
+def test_conv_integer_matches_brute_force(xdt, wdt, per_ch, s, p, d, group):
+    rng = np.random.default_rng(7)
+    info = lambda t: (0, 256) if t == np.uint8 else (-128, 128)
+    x = rng.integers(*info(xdt), (2, 8, 9, 11), dtype=xdt)
+    w = rng.integers(*info(wdt), (12, 8 // group, 3, 3), dtype=wdt)
+    x_zp = 131 if xdt == np.uint8 else -3
+    w_zp = rng.integers(*info(wdt), 12) if per_ch else (7 if wdt == np.uint8 else -2)
+    y = O.conv_integer(x, w, x_zp, w_zp, s, p, d, group)
+    assert np.array_equal(y, _conv_int_numpy(x, w, x_zp, w_zp, s, p, d, group))
+
+
+def test_conv_integer_1x1_is_matmul_integer():
+    """A 1x1 ConvInteger is MatMulInteger of the weights with the pixels."""
+    rng = np.random.default_rng(8)
+    x = rng.integers(0, 256, (1, 16, 5, 6), dtype=np.uint8)
+    w = rng.integers(-128, 128, (10, 16, 1, 1), dtype=np.int8)
+    y = O.conv_integer(x, w, 100, -4)
+    mm = O.matmul_integer(w.reshape(10, 16), x.reshape(16, 30), -4, 100)
+    assert np.array_equal(y.reshape(10, 30), mm)
