@@ -1250,6 +1250,10 @@ extern "C" int nnrh_matmul_integer_create(nnrh_matmul_integer_t* out, int m, int
     return NNRH_OK;
 }
 
+int matmul_integer_gemm(nnrh_matmul_integer* h, const void* a, long long a_bstride, const int8_t* bpack,
+                        const int32_t* colsum, bool b_batched, int a_zp, int b_zp, int32_t* y, int batch,
+                        hipStream_t s);
+
 extern "C" int nnrh_matmul_integer_run(nnrh_matmul_integer_t h, const void* a, long long a_bstride,
                                        const void* b, long long b_bstride, int a_zp, int b_zp,
                                        int32_t* y, int batch, void* stream) {
@@ -1257,23 +1261,34 @@ extern "C" int nnrh_matmul_integer_run(nnrh_matmul_integer_t h, const void* a, l
     if (batch <= 0 || batch > h->max_batch)
         return set_err(NNRH_ERR_INVALID, "matmul_integer_run: batch %d (max %d)", batch, h->max_batch);
     hipStream_t s = S(stream);
-    const bool au8 = h->a_dtype == NNRH_U8, bu8 = h->b_dtype == NNRH_U8;
+    const bool bu8 = h->b_dtype == NNRH_U8;
     const int nb_b = b_bstride == 0 ? 1 : batch;
-    ProfScope ps0("pack_b", s);
-    HIP_TRY(launch_pack_b_dense(b, b_bstride, h->k, h->n, h->Kp, h->Np, bu8 ? 0x80 : 0, h->bpack,
-                                (long long)h->Np * h->Kp, h->colsum, h->Np, nb_b, s),
-            "pack_b");
+    {
+        ProfScope ps0("pack_b", s);
+        HIP_TRY(launch_pack_b_dense(b, b_bstride, h->k, h->n, h->Kp, h->Np, bu8 ? 0x80 : 0, h->bpack,
+                                    (long long)h->Np * h->Kp, h->colsum, h->Np, nb_b, s),
+                "pack_b");
+    }
+    return matmul_integer_gemm(h, a, a_bstride, h->bpack, h->colsum, b_bstride != 0, a_zp, b_zp, y, batch, s);
+}
+
+// the GEMM of MatMulInteger over a packed B ([batch][Np][Kp] int8 and its
+// column sums [batch][Np]; one shared when !b_batched)
+int matmul_integer_gemm(nnrh_matmul_integer* h, const void* a, long long a_bstride, const int8_t* bpack,
+                        const int32_t* colsum, bool b_batched, int a_zp, int b_zp, int32_t* y, int batch,
+                        hipStream_t s) {
+    const bool au8 = h->a_dtype == NNRH_U8, bu8 = h->b_dtype == NNRH_U8;
     GemmArgs g{};
     g.a = (const uint8_t*)a;
     g.lda = h->k;
     g.a_bstride = a_bstride;
     g.a_xor = au8 ? 0x80 : 0;
     g.M = h->m; g.N = h->n; g.K = h->k; g.Kp = h->Kp;
-    g.b = h->bpack;
-    g.b_bstride = b_bstride == 0 ? 0 : (long long)h->Np * h->Kp;
+    g.b = bpack;
+    g.b_bstride = b_batched ? (long long)h->Np * h->Kp : 0;
     g.Np = h->Np;
-    g.colsum = h->colsum;
-    g.param_bstride = b_bstride == 0 ? 0 : h->Np;
+    g.colsum = colsum;
+    g.param_bstride = b_batched ? h->Np : 0;
     g.a_sub = au8 ? 128 : 0;
     g.alpha = a_zp - g.a_sub;
     g.beta = b_zp - (bu8 ? 128 : 0);
@@ -1430,16 +1445,18 @@ extern "C" int nnrh_qlinear_avgpool(const void* x, void* y, int N, int C, int iH
 }
 
 // ---- ConvInteger --------------------------------------------------------------
+// im2col written in the GEMM's packed-B layout (no separate packing pass),
+// then MatMulInteger's GEMM: y[b] = W_g[MM][K] . col[b][K][P]
 struct nnrh_conv_integer {
     Im2colArgs a{};
     int OC = 0, MM = 0, x_dtype = 0, w_dtype = 0;
     long long K = 0, P = 0;
-    uint8_t* col = nullptr;
-    int32_t* S = nullptr;
-    nnrh_matmul_integer_t mi = nullptr;
+    int8_t* bpack = nullptr;
+    int32_t* colsum = nullptr;
+    nnrh_matmul_integer_t mi = nullptr;   // GEMM shape, rowsum workspace
     ~nnrh_conv_integer() {
-        dfree(col);
-        dfree(S);
+        dfree(bpack);
+        dfree(colsum);
         if (mi) nnrh_matmul_integer_destroy(mi);
     }
 };
@@ -1454,29 +1471,21 @@ extern "C" int nnrh_conv_integer_create(nnrh_conv_integer_t* out, int N, int C, 
         return set_err(NNRH_ERR_INVALID, "conv_integer: bad shape");
     if ((x_dtype != NNRH_U8 && x_dtype != NNRH_S8) || (w_dtype != NNRH_U8 && w_dtype != NNRH_S8))
         return set_err(NNRH_ERR_UNSUPPORTED, "conv_integer: dtype");
+    const long long K = (long long)(C / group) * kH * kW, P = (long long)oH * oW;
+    if (K > (1 << 30) || P > (1 << 30)) return set_err(NNRH_ERR_UNSUPPORTED, "conv_integer: GEMM extents too large");
     auto* h = new nnrh_conv_integer();
     h->a = Im2colArgs{nullptr, nullptr, N, C, iH, iW, group, kH, kW, sH, sW, pH, pW, dH, dW, oH, oW, 0};
     h->OC = OC;
     h->MM = OC / group;
     h->x_dtype = x_dtype;
     h->w_dtype = w_dtype;
-    h->K = (long long)(C / group) * kH * kW;
-    h->P = (long long)oH * oW;
+    h->K = K;
+    h->P = P;
+    int rc = nnrh_matmul_integer_create(&h->mi, h->MM, (int)P, (int)K, w_dtype, x_dtype, group == 1 ? N : group);
     const long long batches = (long long)N * group;
-    if (h->K > INT32_MAX || h->P > INT32_MAX) {
-        delete h;
-        return set_err(NNRH_ERR_UNSUPPORTED, "conv_integer: GEMM extents beyond int32");
-    }
-    int rc0 = nnrh_malloc((void**)&h->col, (size_t)(batches * h->K * h->P));
-    if (rc0 == NNRH_OK) rc0 = nnrh_malloc((void**)&h->S, (size_t)(batches * h->P) * sizeof(int32_t));
-    if (rc0 != NNRH_OK) {
-        delete h;
-        return rc0;
-    }
-    // y[b] = W_g[MM][K] . col[b][K][P]: one launch over every image when
-    // group == 1 (W broadcast), else one per image over the groups
-    const int rc = nnrh_matmul_integer_create(&h->mi, h->MM, (int)h->P, (int)h->K, w_dtype, x_dtype,
-                                              group == 1 ? N : group);
+    if (rc == NNRH_OK)
+        rc = nnrh_malloc((void**)&h->bpack, (size_t)(batches * h->mi->Np * (long long)h->mi->Kp));
+    if (rc == NNRH_OK) rc = nnrh_malloc((void**)&h->colsum, (size_t)(batches * h->mi->Np) * sizeof(int32_t));
     if (rc != NNRH_OK) {
         delete h;
         return rc;
@@ -1489,30 +1498,42 @@ extern "C" int nnrh_conv_integer_run(nnrh_conv_integer_t h, const void* x, const
                                      const int32_t* w_zp_dev, int32_t* y, void* stream) {
     if (!h || !x || !w || !y) return set_err(NNRH_ERR_INVALID, "conv_integer_run: NULL argument");
     hipStream_t s = S(stream);
-    Im2colArgs a = h->a;
-    a.x = (const uint8_t*)x;
-    a.col = h->col;
-    a.pad = (uint8_t)x_zp;
+    const int Np = h->mi->Np, Kp = h->mi->Kp;
+    const int x_xor = h->x_dtype == NNRH_U8 ? 0x80 : 0;
+    Im2colPackArgs q{};
+    q.a = h->a;
+    q.a.x = (const uint8_t*)x;
+    q.a.pad = (uint8_t)x_zp;
+    q.bpack = h->bpack;
+    q.colsum = h->colsum;
+    q.Kp = Kp;
+    q.Np = Np;
+    q.K = (int)h->K;
+    q.P = (int)h->P;
+    q.x_xor = x_xor;
     {
-        ProfScope ps("im2col", s);
-        HIP_TRY(launch_im2col_u8(a, s), "im2col");
+        ProfScope ps("im2col_pack", s);
+        HIP_TRY(launch_im2col_pack(q, s), "im2col_pack");
     }
-    const long long KP = h->K * h->P, wsz = (long long)h->MM * h->K, ysz = (long long)h->MM * h->P;
+    const long long pb = (long long)Np * Kp, wsz = (long long)h->MM * h->K, ysz = (long long)h->MM * h->P;
     const int wz = w_zp_dev ? 0 : w_zp;
-    if (a.group == 1) {
-        const int rc = nnrh_matmul_integer_run(h->mi, w, 0, h->col, KP, wz, x_zp, y, a.N, stream);
+    const int G = h->a.group;
+    if (G == 1) {
+        const int rc = matmul_integer_gemm(h->mi, w, 0, h->bpack, h->colsum, true, wz, x_zp, y, h->a.N, s);
         if (rc != NNRH_OK) return rc;
     } else {
-        for (int n = 0; n < a.N; ++n) {
-            const int rc = nnrh_matmul_integer_run(h->mi, w, wsz, h->col + (size_t)n * a.group * KP, KP, wz, x_zp,
-                                                   y + (size_t)n * a.group * ysz, a.group, stream);
+        for (int n = 0; n < h->a.N; ++n) {
+            const int rc = matmul_integer_gemm(h->mi, w, wsz, h->bpack + (size_t)n * G * pb,
+                                               h->colsum + (size_t)n * G * Np, true, wz, x_zp,
+                                               y + (size_t)n * G * ysz, G, s);
             if (rc != NNRH_OK) return rc;
         }
     }
     if (w_zp_dev) {
+        // S = sum_k (x - x_zp) = colsum of the shifted bytes + K * (shift - x_zp)
+        const int s_off = (int)((uint32_t)h->K * (uint32_t)(x_xor ? 128 - x_zp : -x_zp));
         ProfScope ps("conv_integer_wzp", s);
-        HIP_TRY(launch_conv_integer_wzp(h->col, h->S, y, w_zp_dev, (long long)a.N * a.group, a.group, h->MM, h->K,
-                                        h->P, h->x_dtype == NNRH_S8, x_zp, s),
+        HIP_TRY(launch_conv_integer_wzp(y, h->colsum, Np, s_off, w_zp_dev, (long long)h->a.N * G, G, h->MM, h->P, s),
                 "conv_integer_wzp");
     }
     return NNRH_OK;

@@ -176,9 +176,15 @@ struct Im2colArgs {
     int N, C, iH, iW, group, kH, kW, sH, sW, pH, pW, dH, dW, oH, oW;
     uint8_t pad;
 };
-hipError_t launch_im2col_u8(const Im2colArgs& a, hipStream_t s);
-hipError_t launch_conv_integer_wzp(const uint8_t* col, int32_t* S, int32_t* y, const int32_t* wzp, long long batches,
-                                   int group, int MM, long long K, long long P, int x_s8, int x_zp, hipStream_t s);
+struct Im2colPackArgs {
+    Im2colArgs a;
+    int8_t* bpack;
+    int32_t* colsum;
+    int Kp, Np, K, P, x_xor;
+};
+hipError_t launch_im2col_pack(const Im2colPackArgs& q, hipStream_t s);
+hipError_t launch_conv_integer_wzp(int32_t* y, const int32_t* colsum, int Np, int s_off, const int32_t* wzp,
+                                   long long batches, int group, int MM, long long P, hipStream_t s);
 hipError_t launch_depthwise3x3(const uint8_t* x, const uint32_t* wrow, const int32_t* corr, uint8_t* y,
                                const float* cs, const float* bf, int N, int C, int H, int W, int oH, int oW,
                                int stride, int pad_t, int pad_l, int x_zp, int a_xor, float inv_y, int y_zp,

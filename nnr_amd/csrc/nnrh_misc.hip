@@ -910,59 +910,85 @@ hipError_t launch_fill_u8(void* p, uint8_t v, long long n, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// ConvInteger (ConvInteger.cpp:146-233): im2col of x into col[n*group + g][k][p]
-// (k = (c * kH + kh) * kW + kw over the group's channels, p = oh * oW + ow),
-// taps outside the image filled with the byte of x_zp so that (x - x_zp) is
-// 0 there, as the reference's zero-padded float im2col of (x - x_zp).
-__global__ __launch_bounds__(256) void im2col_u8_kernel(Im2colArgs a) {
+// ConvInteger (ConvInteger.cpp:146-233): im2col of x written straight in the
+// GEMM's packed-B layout (pack_b_kernel's: B[K][P] of image n, group g goes to
+// bpack[n * group + g][packed_row_of_col(p)][Kp], uint8 XOR-shifted to int8,
+// zero padded) with colsum[b][p] = sum_k of the packed bytes. Taps outside the
+// image take the byte of x_zp, so (x - x_zp) is 0 there as in the reference's
+// zero-padded float im2col of (x - x_zp). One thread per packed row.
+// IM2COL_LANES neighbouring lanes share a packed row: lane j writes the 16-tap
+// chunks j, j + IM2COL_LANES, ... (together coalesced 16-byte stores), and
+// the row's column sum is reduced over the lane group by shuffles.
+constexpr int IM2COL_LANES = 4;
+__global__ __launch_bounds__(256) void im2col_pack_kernel(Im2colPackArgs q) {
+    const Im2colArgs& a = q.a;
     const int CC = a.C / a.group;
-    const long long P = (long long)a.oH * a.oW;
-    const long long K = (long long)CC * a.kH * a.kW;
-    const long long total = (long long)a.N * a.group * K * P;
-    for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
-        const long long p = e % P;
-        long long r = e / P;
-        const long long k = r % K;
-        const long long b = r / K;                 // n * group + g
-        const int kw = (int)(k % a.kW), kh = (int)((k / a.kW) % a.kH), c = (int)(k / ((long long)a.kW * a.kH));
-        const int ow = (int)(p % a.oW), oh = (int)(p / a.oW);
-        const int ih = oh * a.sH - a.pH + kh * a.dH, iw = ow * a.sW - a.pW + kw * a.dW;
-        const long long n = b / a.group, g = b % a.group;
-        uint8_t v = a.pad;
-        if (ih >= 0 && ih < a.iH && iw >= 0 && iw < a.iW)
-            v = a.x[((n * a.C + g * CC + c) * a.iH + ih) * (long long)a.iW + iw];
-        a.col[e] = v;
+    const int kHW = a.kH * a.kW;
+    const long long rows = (long long)a.N * a.group * q.Np;
+    const int sub = threadIdx.x % IM2COL_LANES;
+    const long long rstride = (long long)gridDim.x * (256 / IM2COL_LANES);
+    // every lane of a group has the same row, so the loop and the shuffles are
+    // uniform over the group
+    for (long long e = (long long)blockIdx.x * (256 / IM2COL_LANES) + threadIdx.x / IM2COL_LANES; e < rows;
+         e += rstride) {
+        const long long b = e / q.Np;
+        const int p = (int)(e % q.Np);
+        int8_t* row = q.bpack + b * q.Np * (long long)q.Kp + (long long)packed_row_of_col(p) * q.Kp;
+        int32_t sum = 0;
+        if (p >= q.P) {
+            for (int kc = sub * 16; kc < q.Kp; kc += 16 * IM2COL_LANES) *(uint4*)(row + kc) = make_uint4(0, 0, 0, 0);
+        } else {
+            const int ow = p % a.oW, oh = p / a.oW;
+            const long long n = b / a.group, g = b % a.group;
+            const uint8_t* xb = a.x + (n * a.C + g * CC) * (long long)a.iH * a.iW;
+            const int h0 = oh * a.sH - a.pH, w0 = ow * a.sW - a.pW;
+            for (int kc = sub * 16; kc < q.Kp; kc += 16 * IM2COL_LANES) {
+                // tap k = (c * kH + kh) * kW + kw, decoded once per chunk
+                int c = kc / kHW, r = kc % kHW;
+                int kh = r / a.kW, kw = r % a.kW;
+                uint32_t w4[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    if (kc + i < q.K) {
+                        const int ih = h0 + kh * a.dH, iw = w0 + kw * a.dW;
+                        uint8_t v = a.pad;
+                        if (ih >= 0 && ih < a.iH && iw >= 0 && iw < a.iW)
+                            v = xb[((long long)c * a.iH + ih) * a.iW + iw];
+                        v ^= (uint8_t)q.x_xor;
+                        sum += (int8_t)v;
+                        w4[i >> 2] |= (uint32_t)v << (8 * (i & 3));
+                        if (++kw == a.kW) {
+                            kw = 0;
+                            if (++kh == a.kH) { kh = 0; ++c; }
+                        }
+                    }
+                }
+                *(uint4*)(row + kc) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+            }
+        }
+#pragma unroll
+        for (int off = 1; off < IM2COL_LANES; off <<= 1) sum += __shfl_xor(sum, off, 64);
+        if (sub == 0) q.colsum[b * q.Np + p] = sum;
     }
 }
 
-hipError_t launch_im2col_u8(const Im2colArgs& a, hipStream_t s) {
-    const long long total = (long long)a.N * a.group * (a.C / a.group) * a.kH * a.kW * a.oH * a.oW;
-    if (total <= 0) return hipSuccess;
-    long long blocks = (total + 255) / 256;
+hipError_t launch_im2col_pack(const Im2colPackArgs& q, hipStream_t s) {
+    const long long rows = (long long)q.a.N * q.a.group * q.Np;
+    if (rows <= 0) return hipSuccess;
+    long long blocks = (rows + 256 / IM2COL_LANES - 1) / (256 / IM2COL_LANES);
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(im2col_u8_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(im2col_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, s, q);
     return hipGetLastError();
 }
 
-// per-channel weight zero points: y[b][m][p] -= w_zp[g * MM + m] * S[b][p],
-// S[b][p] = sum_k (col[b][k][p] - x_zp), so that the GEMM's sum_k w (x - x_zp)
-// becomes sum_k (w - w_zp[oc]) (x - x_zp) exactly (int32, wrapping)
-__global__ __launch_bounds__(256) void col_sums_kernel(const uint8_t* __restrict col, int32_t* __restrict S,
-                                                       long long batches, long long K, long long P, int x_s8,
-                                                       int x_zp) {
-    const long long total = batches * P;
-    for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
-        const long long b = e / P, p = e % P;
-        const uint8_t* c = col + b * K * P + p;
-        uint32_t sum = 0;
-        for (long long k = 0; k < K; ++k) sum += (uint32_t)(x_s8 ? (int)(int8_t)c[k * P] : (int)c[k * P]);
-        S[e] = (int32_t)(sum - (uint32_t)x_zp * (uint32_t)K);
-    }
-}
-
-__global__ __launch_bounds__(256) void wzp_correct_kernel(int32_t* __restrict y, const int32_t* __restrict S,
-                                                          const int32_t* __restrict wzp, long long batches, int group,
-                                                          int MM, long long P) {
+// per-channel weight zero points: y[b][m][p] -= w_zp[g * MM + m] * S[b][p] with
+// S[b][p] = sum_k (x - x_zp) = colsum[b][p] + s_off (s_off = K * (shift -
+// x_zp), shift 128 for XOR-shifted uint8), so that the GEMM's
+// sum_k w (x - x_zp) becomes sum_k (w - w_zp[oc]) (x - x_zp) exactly (int32,
+// wrapping)
+__global__ __launch_bounds__(256) void wzp_correct_kernel(int32_t* __restrict y, const int32_t* __restrict colsum,
+                                                          int Np, int s_off, const int32_t* __restrict wzp,
+                                                          long long batches, int group, int MM, long long P) {
     const long long total = batches * MM * P;
     for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
         const long long p = e % P;
@@ -970,19 +996,18 @@ __global__ __launch_bounds__(256) void wzp_correct_kernel(int32_t* __restrict y,
         const int m = (int)(r % MM);
         const long long b = r / MM;
         const int g = (int)(b % group);
-        y[e] = (int32_t)((uint32_t)y[e] - (uint32_t)wzp[g * MM + m] * (uint32_t)S[b * P + p]);
+        const uint32_t S = (uint32_t)colsum[b * Np + p] + (uint32_t)s_off;
+        y[e] = (int32_t)((uint32_t)y[e] - (uint32_t)wzp[g * MM + m] * S);
     }
 }
 
-hipError_t launch_conv_integer_wzp(const uint8_t* col, int32_t* S, int32_t* y, const int32_t* wzp, long long batches,
-                                   int group, int MM, long long K, long long P, int x_s8, int x_zp, hipStream_t s) {
-    long long blocks = (batches * P + 255) / 256;
+hipError_t launch_conv_integer_wzp(int32_t* y, const int32_t* colsum, int Np, int s_off, const int32_t* wzp,
+                                   long long batches, int group, int MM, long long P, hipStream_t s) {
+    long long blocks = (batches * MM * P + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks <= 0) return hipSuccess;
-    hipLaunchKernelGGL(col_sums_kernel, dim3((unsigned)blocks), dim3(256), 0, s, col, S, batches, K, P, x_s8, x_zp);
-    blocks = (batches * MM * P + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(wzp_correct_kernel, dim3((unsigned)blocks), dim3(256), 0, s, y, S, wzp, batches, group, MM, P);
+    hipLaunchKernelGGL(wzp_correct_kernel, dim3((unsigned)blocks), dim3(256), 0, s, y, colsum, Np, s_off, wzp, batches,
+                       group, MM, P);
     return hipGetLastError();
 }
 
