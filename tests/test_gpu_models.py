@@ -291,3 +291,21 @@ def test_conv_integer_graph(dev, kw):
     x = rng.uniform(-2.0, 2.0, (2, 16, 15, 15)).astype(np.float32)
     plan, y, _ = check_graph(g, {"input": x}, g.outputs[0], atol=0)
     assert [p["op"] for p in plan].count("ConvInteger") == 1 and y.dtype == np.int32
+
+
+@pytest.mark.parametrize("shape", [(2, 24, 7, 9), (3, 5, 4)])
+def test_bn_f32_unfolded(dev, shape):
+    """BatchNormalization with no Q after it stays fp32 (BatchNormalization.cpp:
+    126-160): within the reference's float tolerance of the float64 formula."""
+    g = G.Graph()
+    rng = np.random.default_rng(33)
+    C = shape[1]
+    g.inputs["input"] = (np.float32, shape)
+    ins = ["input"] + [g.init(k, v.astype(np.float32)) for k, v in
+                       (("sc", rng.uniform(0.5, 1.5, C)), ("bi", rng.normal(0, 1, C)),
+                        ("me", rng.normal(0, 1, C)), ("va", rng.uniform(0.2, 2.0, C)))]
+    y = g.node("BatchNormalization", ins, name="bn", epsilon=1e-4)
+    g.outputs.append(y)
+    x = rng.normal(0, 2, shape).astype(np.float32)
+    plan, out, _ = check_graph(g, {"input": x}, y)
+    assert [p["variant"] for p in plan] == [""] and out.dtype == np.float32
