@@ -964,6 +964,66 @@ __global__ __launch_bounds__(256) void qavgpool_nhwc16_kernel(const void* __rest
     }
 }
 
+// the same for a fixed window: every tap's 16-byte load (predicated on the
+// tap lying in the image) is issued before the first sum
+template <int KH, int KW>
+__global__ __launch_bounds__(256) void qavgpool_nhwc16_fixed_kernel(const void* __restrict x, void* __restrict y,
+                                                                    int N, int C, int iH, int iW, int oH, int oW,
+                                                                    int sH, int sW, int pH, int pW, int dt, float x_s,
+                                                                    int x_zp, float y_s, int y_zp, int lo, int hi) {
+    const int G = C / 16;
+    const long long total = (long long)N * oH * oW * G;
+    const uint32_t flip = dt ? 0x80808080u : 0u;
+    for (long long o = (long long)blockIdx.x * 256 + threadIdx.x; o < total; o += (long long)gridDim.x * 256) {
+        const int g = (int)(o % G);
+        long long r = o / G;
+        const int ow = (int)(r % oW);
+        r /= oW;
+        const int oh = (int)(r % oH);
+        const int n = (int)(r / oH);
+        const int h0 = oh * sH - pH, w0 = ow * sW - pW;
+        const uint4* img = (const uint4*)((const uint8_t*)x + (long long)n * iH * iW * C) + g;
+        uint4 v[KH * KW];
+        bool ok[KH * KW];
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < KW; ++kw) {
+                const int ih = h0 + kh, iw = w0 + kw;
+                const bool in = ih >= 0 && ih < iH && iw >= 0 && iw < iW;
+                ok[kh * KW + kw] = in;
+                v[kh * KW + kw] = in ? img[((long long)ih * iW + iw) * G] : make_uint4(0, 0, 0, 0);
+            }
+        uint32_t acc[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] = 0;
+        int count = 0;
+#pragma unroll
+        for (int t = 0; t < KH * KW; ++t) {
+            if (!ok[t]) continue;
+            ++count;
+            const uint32_t w[4] = {v[t].x ^ flip, v[t].y ^ flip, v[t].z ^ flip, v[t].w ^ flip};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                acc[2 * k] += w[k] & 0x00ff00ffu;
+                acc[2 * k + 1] += (w[k] >> 8) & 0x00ff00ffu;
+            }
+        }
+        const int32_t off = (dt ? 128 : 0) * count + count * x_zp;
+        uint32_t ow_[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int32_t s0 = (int32_t)(acc[2 * k] & 0xffffu), s2 = (int32_t)(acc[2 * k] >> 16);
+            const int32_t s1 = (int32_t)(acc[2 * k + 1] & 0xffffu), s3 = (int32_t)(acc[2 * k + 1] >> 16);
+            ow_[k] = ((uint32_t)qavg_out(s0 - off, count, x_s, y_s, y_zp, lo, hi) & 0xffu) |
+                     (((uint32_t)qavg_out(s1 - off, count, x_s, y_s, y_zp, lo, hi) & 0xffu) << 8) |
+                     (((uint32_t)qavg_out(s2 - off, count, x_s, y_s, y_zp, lo, hi) & 0xffu) << 16) |
+                     (((uint32_t)qavg_out(s3 - off, count, x_s, y_s, y_zp, lo, hi) & 0xffu) << 24);
+        }
+        ((uint4*)y)[o] = make_uint4(ow_[0], ow_[1], ow_[2], ow_[3]);
+    }
+}
+
 hipError_t launch_qavgpool(const void* x, void* y, int N, int C, int iH, int iW, int oH, int oW, int kH, int kW,
                            int sH, int sW, int pH, int pW, int nhwc, int dt, float x_s, int x_zp, float y_s,
                            int y_zp, int lo, int hi, hipStream_t s) {
@@ -972,7 +1032,13 @@ hipError_t launch_qavgpool(const void* x, void* y, int N, int C, int iH, int iW,
     const bool vec = nhwc && C % 16 == 0 && (((uintptr_t)x | (uintptr_t)y) & 15) == 0 && kH * kW <= 256;
     long long blocks = ((vec ? total / 16 : total) + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    if (vec)
+    if (vec && kH == 3 && kW == 3)
+        hipLaunchKernelGGL((qavgpool_nhwc16_fixed_kernel<3, 3>), dim3((unsigned)blocks), dim3(256), 0, s, x, y, N, C,
+                           iH, iW, oH, oW, sH, sW, pH, pW, dt, x_s, x_zp, y_s, y_zp, lo, hi);
+    else if (vec && kH == 2 && kW == 2)
+        hipLaunchKernelGGL((qavgpool_nhwc16_fixed_kernel<2, 2>), dim3((unsigned)blocks), dim3(256), 0, s, x, y, N, C,
+                           iH, iW, oH, oW, sH, sW, pH, pW, dt, x_s, x_zp, y_s, y_zp, lo, hi);
+    else if (vec)
         hipLaunchKernelGGL(qavgpool_nhwc16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, N, C, iH, iW, oH,
                            oW, kH, kW, sH, sW, pH, pW, dt, x_s, x_zp, y_s, y_zp, lo, hi);
     else

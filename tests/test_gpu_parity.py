@@ -367,7 +367,8 @@ def test_qlinear_global_avgpool(dev, nhwc, dt, N, C, Hh, W):
 
 @pytest.mark.parametrize("nhwc", [0, 1])
 @pytest.mark.parametrize("k,st,pad,H_,W_", [((3, 3), (2, 2), (1, 1), 9, 10), ((2, 2), (2, 2), (0, 0), 8, 8),
-                                             ((3, 2), (1, 1), (1, 0), 6, 7), ((7, 7), (1, 1), (0, 0), 7, 7)])
+                                             ((3, 2), (1, 1), (1, 0), 6, 7), ((7, 7), (1, 1), (0, 0), 7, 7),
+                                             ((3, 3), (1, 1), (1, 1), 5, 6)])
 @pytest.mark.parametrize("C,dt", [(24, np.uint8),    # one byte a thread
                                   (32, np.uint8), (48, np.int8)])   # NHWC: 16 channels a thread
 def test_qlinear_avgpool(dev, nhwc, k, st, pad, H_, W_, C, dt):
