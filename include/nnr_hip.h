@@ -311,6 +311,13 @@ int nnrh_qlinear_avgpool(const void* x_dev, void* y_dev, int N, int C, int iH, i
 int nnrh_qlinear_concat_part(const void* x_dev, void* y_dev, long long outer, long long count,
                              long long y_row, long long y_off, int dtype, float x_scale,
                              int x_zp, float y_scale, int y_zp, void* stream);
+/* The whole QLinearConcat in one launch: ntens parts (host arrays of device
+ * pointers, chunk lengths, scales and zero points), each contributing
+ * `counts[t]` elements to every one of the `outer` output rows, in order.
+ * Same arithmetic as nnrh_qlinear_concat_part per part.                     */
+int nnrh_qlinear_concat(int ntens, const void* const* xs_dev, const long long* counts,
+                        const float* x_scales, const int* x_zps, long long outer, int dtype,
+                        float y_scale, int y_zp, void* y_dev, void* stream);
 
 /* ---- BatchNormalization after fold_bn_qdq (src/graph_optimizer/
  * fold_bn_qdq.cpp:23-259; BatchNormalization.cpp:246-376) ---------------------

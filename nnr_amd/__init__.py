@@ -389,11 +389,11 @@ def qlinear_concat(xs, counts, outer, scales, zps, y_s, y_zp):
     row = sum(counts)
     y = torch.empty(outer * row, dtype=xs[0].dtype, device=xs[0].device)
     dt = U8 if xs[0].dtype == torch.uint8 else S8
-    off = 0
-    for x, c, sc, zp in zip(xs, counts, scales, zps):
-        check(lib().nnrh_qlinear_concat_part(ptr(x), ptr(y), outer, c, row, off, dt, float(sc), int(zp),
-                                             float(y_s), int(y_zp), cur_stream()))
-        off += c
+    n = len(xs)
+    P = (ct.c_void_p * n)(*[ptr(x) for x in xs])
+    check(lib().nnrh_qlinear_concat(n, P, (ct.c_longlong * n)(*counts), (ct.c_float * n)(*map(float, scales)),
+                                    (ct.c_int * n)(*map(int, zps)), outer, dt, float(y_s), int(y_zp), ptr(y),
+                                    cur_stream()))
     return y
 
 

@@ -32,7 +32,7 @@ EXPORTS = [
     "nnrh_qmatmul_set_minmax_out", "nnrh_dynamic_quantize_linear_parts", "nnrh_add_layernorm_f32",
     "nnrh_qmatmul_group_create", "nnrh_qmatmul_group_run", "nnrh_qmatmul_group_destroy",
     "nnrh_qlinear_mul", "nnrh_qlinear_global_avgpool", "nnrh_qlinear_avgpool", "nnrh_qlinear_concat_part",
-    "nnrh_batchnorm_u8", "nnrh_batchnorm_f32",
+    "nnrh_batchnorm_u8", "nnrh_batchnorm_f32", "nnrh_qlinear_concat",
     "nnrh_conv_integer_create", "nnrh_conv_integer_run", "nnrh_conv_integer_destroy",
     "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
@@ -148,6 +148,7 @@ def lib():
         "nnrh_qlinear_avgpool": (i, [vp, vp] + [i] * 14 + [f, i, f, i, vp]),
         "nnrh_qlinear_concat_part": (i, [vp, vp, ll, ll, ll, ll, i, f, i, f, i, vp]),
         "nnrh_batchnorm_u8": (i, [vp, i, vp, vp, vp, ll, i, ll, i, vp]),
+        "nnrh_qlinear_concat": (i, [i, vp, vp, vp, vp, ll, i, f, i, vp, vp]),
         "nnrh_conv_integer_create": (i, [C.POINTER(vp)] + [i] * 18),
         "nnrh_conv_integer_run": (i, [vp, vp, vp, i, i, vp, vp, vp]),
         "nnrh_conv_integer_destroy": (i, [vp]),

@@ -1564,6 +1564,62 @@ extern "C" int nnrh_batchnorm_f32(const float* x, float* y, const float* alpha, 
 
 extern "C" int nnrh_qlinear_concat_part(const void* x, void* y, long long outer, long long count, long long y_row,
                                         long long y_off, int dtype, float x_scale, int x_zp, float y_scale,
+                                        int y_zp, void* stream);
+
+extern "C" int nnrh_qlinear_concat(int ntens, const void* const* xs, const long long* counts,
+                                   const float* x_scales, const int* x_zps, long long outer, int dtype,
+                                   float y_scale, int y_zp, void* y, void* stream) {
+    if (!xs || !counts || !x_scales || !x_zps || !y) return set_err(NNRH_ERR_INVALID, "qlinear_concat: NULL");
+    if (dtype != NNRH_U8 && dtype != NNRH_S8) return set_err(NNRH_ERR_UNSUPPORTED, "qlinear_concat: dtype");
+    if (ntens <= 0 || outer < 0) return set_err(NNRH_ERR_INVALID, "qlinear_concat: bad extents");
+    long long row = 0;
+    for (int t = 0; t < ntens; ++t) {
+        if ((!xs[t] && counts[t] > 0) || counts[t] < 0) return set_err(NNRH_ERR_INVALID, "qlinear_concat: part %d", t);
+        row += counts[t];
+    }
+    if (ntens > QCONCAT_MAX_PARTS) {   // one launch per part
+        long long off = 0;
+        for (int t = 0; t < ntens; ++t) {
+            if (counts[t] == 0) continue;
+            const int rc = nnrh_qlinear_concat_part(xs[t], y, outer, counts[t], row, off, dtype, x_scales[t],
+                                                    x_zps[t], y_scale, y_zp, stream);
+            if (rc != NNRH_OK) return rc;
+            off += counts[t];
+        }
+        return NNRH_OK;
+    }
+    QConcatRows a{};
+    a.n = 0;
+    long long off = 0;
+    for (int t = 0; t < ntens; ++t) {
+        if (counts[t] == 0) continue;   // an empty part writes nothing
+        const int k = a.n++;
+        a.x[k] = xs[t];
+        a.cnt[k] = counts[t];
+        a.off[k] = off;
+        // QLinearConcat.cpp:147: an input in the output's quantization is copied;
+        // the 16-wide body covers count - count % 16 of a chunk of >= 16
+        a.copy[k] = x_scales[t] == y_scale && x_zps[t] == y_zp;
+        a.rs[k] = a.copy[k] ? 0.f : x_scales[t] / y_scale;
+        a.zp[k] = x_zps[t];
+        a.body[k] = counts[t] >= 16 ? counts[t] - counts[t] % 16 : 0;
+        off += counts[t];
+    }
+    if (a.n == 0) return NNRH_OK;
+    a.y = y;
+    a.row = row;
+    a.outer = outer;
+    a.dt = dtype == NNRH_U8 ? 0 : 1;
+    a.y_zp = y_zp;
+    a.lo = dtype == NNRH_U8 ? 0 : -128;
+    a.hi = dtype == NNRH_U8 ? 255 : 127;
+    ProfScope ps("qlinear_concat", S(stream));
+    HIP_TRY(launch_qconcat_rows(a, S(stream)), "qlinear_concat");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qlinear_concat_part(const void* x, void* y, long long outer, long long count, long long y_row,
+                                        long long y_off, int dtype, float x_scale, int x_zp, float y_scale,
                                         int y_zp, void* stream) {
     if (!x || !y) return set_err(NNRH_ERR_INVALID, "qlinear_concat_part: NULL");
     if (dtype != NNRH_U8 && dtype != NNRH_S8) return set_err(NNRH_ERR_UNSUPPORTED, "qlinear_concat_part: dtype");

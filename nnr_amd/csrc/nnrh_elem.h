@@ -45,6 +45,19 @@ hipError_t launch_qconcat_part(const void* x, void* y, long long outer, long lon
                                long long y_off, int dt, int copy, float rs, int x_zp, int y_zp, int lo, int hi,
                                hipStream_t s);
 
+// QLinearConcat in one launch: up to QCONCAT_MAX_PARTS inputs
+constexpr int QCONCAT_MAX_PARTS = 8;
+struct QConcatRows {
+    int n;
+    const void* x[QCONCAT_MAX_PARTS];
+    long long cnt[QCONCAT_MAX_PARTS], off[QCONCAT_MAX_PARTS], body[QCONCAT_MAX_PARTS];
+    int copy[QCONCAT_MAX_PARTS], zp[QCONCAT_MAX_PARTS];
+    float rs[QCONCAT_MAX_PARTS];
+    void* y;
+    long long row, outer;
+    int dt, y_zp, lo, hi;
+};
+hipError_t launch_qconcat_rows(const QConcatRows& a, hipStream_t s);
 hipError_t launch_bn_affine_u8(const void* x, int x_f32, uint8_t* y, const float* A, const float* B, long long N,
                                int C, long long HW, int nhwc, hipStream_t s);
 hipError_t launch_bn_f32(const float* x, float* y, const float* A, const float* B, long long N, int C, long long HW,

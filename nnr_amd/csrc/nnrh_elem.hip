@@ -1329,4 +1329,97 @@ hipError_t launch_bn_f32(const float* x, float* y, const float* A, const float* 
     return hipGetLastError();
 }
 
+// QLinearConcat in one launch (QLinearConcat.cpp:70-236): every output row of
+// `row` bytes is the concatenation of the parts' chunks; a thread writes one
+// W-byte cell of a row (W divides every chunk length, the row and every
+// pointer's alignment, and 16, so a cell lies in one part and wholly in its
+// 16-wide body or its tail) and reads it from that part.
+// One cell: output bytes [j, j + W) of row o, from part t at offset i.
+template <int W>
+__device__ __forceinline__ void qconcat_cell(const QConcatRows& a, long long o, long long j, int t, long long i) {
+    {
+        const uint8_t* src = (const uint8_t*)a.x[t] + o * a.cnt[t] + i;
+        uint8_t* dst = (uint8_t*)a.y + o * a.row + j;
+        constexpr int NW = W >= 4 ? W / 4 : 1;
+        uint32_t w[NW];
+        if constexpr (W == 16) {
+            const uint4 v = *(const uint4*)src;
+            w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        } else if constexpr (W == 8) {
+            const uint2 v = *(const uint2*)src;
+            w[0] = v.x; w[1] = v.y;
+        } else if constexpr (W == 4) {
+            w[0] = *(const uint32_t*)src;
+        } else {
+            w[0] = *src;
+        }
+        if (!a.copy[t]) {
+            const bool bd = i < a.body[t];
+#pragma unroll
+            for (int k = 0; k < NW; ++k) {
+                uint32_t r = 0;
+#pragma unroll
+                for (int b = 0; b < (W >= 4 ? 4 : 1); ++b)
+                    r |= ((uint32_t)qconcat_elem(byte_q(w[k], b, a.dt), bd, a.rs[t], a.zp[t], a.y_zp, a.lo, a.hi) &
+                          0xffu) << (8 * b);
+                w[k] = r;
+            }
+        }
+        if constexpr (W == 16) *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
+        else if constexpr (W == 8) *(uint2*)dst = make_uint2(w[0], w[1]);
+        else if constexpr (W == 4) *(uint32_t*)dst = w[0];
+        else *dst = (uint8_t)w[0];
+    }
+}
+
+// a thread per cell (long rows)
+template <int W>
+__global__ __launch_bounds__(256) void qconcat_rows_kernel(QConcatRows a) {
+    const long long cpr = a.row / W;
+    const long long cells = a.outer * cpr;
+    for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < cells; e += (long long)gridDim.x * 256) {
+        const long long o = e / cpr;
+        const long long j = (e - o * cpr) * W;
+        int t = 0;
+        while (t + 1 < a.n && j >= a.off[t + 1]) ++t;
+        qconcat_cell<W>(a, o, j, t, j - a.off[t]);
+    }
+}
+
+// a thread per output row (short rows: an NHWC pixel's channels), walking the
+// parts in order with no division per cell
+template <int W>
+__global__ __launch_bounds__(256) void qconcat_row_thread_kernel(QConcatRows a) {
+    for (long long o = (long long)blockIdx.x * 256 + threadIdx.x; o < a.outer; o += (long long)gridDim.x * 256) {
+        for (int t = 0; t < a.n; ++t)
+            for (long long i = 0; i < a.cnt[t]; i += W) qconcat_cell<W>(a, o, a.off[t] + i, t, i);
+    }
+}
+
+hipError_t launch_qconcat_rows(const QConcatRows& a, hipStream_t s) {
+    uintptr_t al = (uintptr_t)a.y | (uintptr_t)a.row;
+    for (int t = 0; t < a.n; ++t) al |= (uintptr_t)a.x[t] | (uintptr_t)a.cnt[t];
+    const int W = (al & 15) == 0 ? 16 : (al & 7) == 0 ? 8 : (al & 3) == 0 ? 4 : 1;
+    const long long cells = a.outer * (a.row / W);
+    if (cells <= 0) return hipSuccess;
+    if (a.row / W <= 8) {   // short rows: a thread per row
+        long long blocks = (a.outer + 255) / 256;
+        if (blocks > 65536) blocks = 65536;
+        const dim3 g((unsigned)blocks), b(256);
+        if (W == 16) hipLaunchKernelGGL((qconcat_row_thread_kernel<16>), g, b, 0, s, a);
+        else if (W == 8) hipLaunchKernelGGL((qconcat_row_thread_kernel<8>), g, b, 0, s, a);
+        else if (W == 4) hipLaunchKernelGGL((qconcat_row_thread_kernel<4>), g, b, 0, s, a);
+        else hipLaunchKernelGGL((qconcat_row_thread_kernel<1>), g, b, 0, s, a);
+        return hipGetLastError();
+    }
+    long long blocks = (cells + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    const dim3 g((unsigned)blocks), b(256);
+    if (W == 16) hipLaunchKernelGGL((qconcat_rows_kernel<16>), g, b, 0, s, a);
+    else if (W == 8) hipLaunchKernelGGL((qconcat_rows_kernel<8>), g, b, 0, s, a);
+    else if (W == 4) hipLaunchKernelGGL((qconcat_rows_kernel<4>), g, b, 0, s, a);
+    else hipLaunchKernelGGL((qconcat_rows_kernel<1>), g, b, 0, s, a);
+    return hipGetLastError();
+}
+
 }  // namespace nnrh

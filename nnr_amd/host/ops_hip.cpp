@@ -691,6 +691,32 @@ struct QLinearConcat_hip : operator_t {
         const long long row = nhwc ? y->dims[1] : (long long)y->dims[a] * inner;
         const float ys = inputs[0]->scalar_f32();
         const int yz = zp_value(inputs[1]);
+        // one launch for all parts, unless the memory planner placed parts
+        // inside y (then only the others are copied, part by part)
+        bool aliased = false;
+        {
+            long long o2 = 0;
+            for (int i = 0; i < ntens(); ++i) {
+                tensor_t* t = inputs[2 + 3 * i];
+                aliased |= outer == 1 && (const char*)t->data == (const char*)y->data + o2;
+                o2 += nhwc ? t->dims[1] : (long long)t->dims[a] * inner;
+            }
+        }
+        if (!aliased) {
+            std::vector<const void*> xs;
+            std::vector<long long> cnts;
+            std::vector<float> scs;
+            std::vector<int> zps;
+            for (int i = 0; i < ntens(); ++i) {
+                tensor_t* t = inputs[2 + 3 * i];
+                xs.push_back(t->data);
+                cnts.push_back(nhwc ? t->dims[1] : (long long)t->dims[a] * inner);
+                scs.push_back(inputs[3 + 3 * i]->scalar_f32());
+                zps.push_back(zp_value(inputs[4 + 3 * i]));
+            }
+            return ok(this, nnrh_qlinear_concat(ntens(), xs.data(), cnts.data(), scs.data(), zps.data(), outer,
+                                                qdtype(inputs[2]->type), ys, yz, y->data, ctx->stream));
+        }
         long long off = 0;
         for (int i = 0; i < ntens(); ++i) {
             tensor_t* t = inputs[2 + 3 * i];

@@ -386,14 +386,16 @@ def test_qlinear_avgpool(dev, nhwc, k, st, pad, H_, W_, C, dt):
 
 @pytest.mark.parametrize("counts,outer", [([3, 17, 32], 5), ([64, 64], 1), ([15, 1, 16, 33], 37),
                                           # 16-, 8- and 4-byte units (NHWC pixels of 24 + 8 channels)
-                                          ([16, 32, 48], 7), ([24, 8], 50), ([4, 12], 9)])
+                                          ([16, 32, 48], 7), ([24, 8], 50), ([4, 12], 9),
+                                          # more parts than one launch takes: part by part
+                                          ([8, 16, 8, 24, 8, 16, 8, 8, 16], 11), ([0, 16, 5], 4)])
 @pytest.mark.parametrize("dt", [np.uint8, np.int8])
 def test_qlinear_concat(dev, counts, outer, dt):
     rng = np.random.default_rng(sum(counts) + outer)
     info = (0, 256) if dt == np.uint8 else (-128, 128)
     xs = [rng.integers(*info, outer * c, dtype=dt) for c in counts]
-    scales = [0.05, 0.031, 0.02, 0.07][: len(counts)]
-    zps = ([10, 7, 3, 200] if dt == np.uint8 else [10, 7, -3, -100])[: len(counts)]
+    scales = [[0.05, 0.031, 0.02, 0.07][t % 4] for t in range(len(counts))]
+    zps = [([10, 7, 3, 200] if dt == np.uint8 else [10, 7, -3, -100])[t % 4] for t in range(len(counts))]
     y_s, y_zp = 0.031, 7                   # input 1 (if present) is copied
     ref = O.qlinear_concat(xs, counts, outer, scales, zps, y_s, y_zp)
     y = H.qlinear_concat([to_dev(x, dev) for x in xs], counts, outer, scales, zps, y_s, y_zp)
