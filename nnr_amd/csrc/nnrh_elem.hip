@@ -636,6 +636,31 @@ __global__ __launch_bounds__(256) void qmul16_kernel(QMulArgs p) {
         }
         const uint32_t aw[4] = {av.x, av.y, av.z, av.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
         uint32_t ow[4];
+        if (p.dt == 0 && (p.kind == 0 || p.kind == 3) && __builtin_isfinite(p.cs)) {
+            // uint8 body: clamp to [0, 255] then nearest even is one
+            // v_cvt_pk_u8_f32 per byte (finite inputs; +-inf saturate alike)
+            const float az = (float)p.a_zp, bz = (float)p.b_zp, yz = (float)p.y_zp;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t o = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float va = (float)((aw[k] >> (8 * j)) & 0xffu) - az;
+                    float v;
+                    if (p.kind == 0) {
+                        const float vb = (float)((bw[k] >> (8 * j)) & 0xffu) - bz;
+                        v = __builtin_fmaf(va * vb, p.cs, yz);
+                    } else {
+                        const int b = p.y_nhwc ? (int)((bw[k] >> (8 * j)) & 0xffu) : bc;
+                        v = __builtin_fmaf(va, p.cs * (float)(b - p.b_zp), yz);
+                    }
+                    o = __builtin_amdgcn_cvt_pk_u8_f32(v, j, o);
+                }
+                ow[k] = o;
+            }
+            ((uint4*)p.y)[v] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+            continue;
+        }
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             uint32_t o = 0;
