@@ -1378,7 +1378,20 @@ __device__ __forceinline__ void qconcat_cell(const QConcatRows& a, long long o, 
         } else {
             w[0] = *src;
         }
-        if (!a.copy[t]) {
+        if (!a.copy[t] && W >= 4 && a.dt == 0 && i < a.body[t] && __builtin_isfinite(a.rs[t])) {
+            // uint8 body: clamp to [0, 255] then nearest even is one
+            // v_cvt_pk_u8_f32 per byte
+            const float zp = (float)a.zp[t], yz = (float)a.y_zp, rs = a.rs[t];
+#pragma unroll
+            for (int k = 0; k < NW; ++k) {
+                uint32_t r = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    r = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(rs, (float)((w[k] >> (8 * b)) & 0xffu) - zp, yz),
+                                                       b, r);
+                w[k] = r;
+            }
+        } else if (!a.copy[t]) {
             const bool bd = i < a.body[t];
 #pragma unroll
             for (int k = 0; k < NW; ++k) {
