@@ -1237,6 +1237,20 @@ __device__ __forceinline__ void bn_coeffs_16(float* a, float* b, const float* __
     }
 }
 
+// NHWC uint8 input with NaN-free A / B: t = fma(x, A, B) is never NaN, and
+// round-to-nearest-even + unsigned saturation (negative -> 255) is
+// t < -0.5 ? 255 : v_cvt_pk_u8_f32(t) (t = -0.5 rounds to -0, i.e. 0)
+__device__ __forceinline__ uint4 bn_affine_16_u8q(const float* xf, const float* a, const float* b) {
+    uint32_t o[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float t = __builtin_fmaf(xf[k], a[k], b[k]);
+        o[k >> 2] = t < -0.5f ? (o[k >> 2] | (0xffu << (8 * (k & 3))))
+                              : __builtin_amdgcn_cvt_pk_u8_f32(t, k & 3, o[k >> 2]);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 template <bool F32_IN, bool NHWC>
 __device__ __forceinline__ uint4 bn_affine_16(const float* xf, const float* a, const float* b) {
     uint32_t o[4] = {0, 0, 0, 0};
@@ -1265,7 +1279,15 @@ __global__ __launch_bounds__(256) void bn_affine_u8_16_kernel(const void* __rest
     constexpr int U = F32_IN ? 1 : BN_U8_VECS;
     const bool fixed = NHWC && 256 % (C / 16) == 0;
     float a[16], b[16];
-    if (fixed) bn_coeffs_16<NHWC>(a, b, A, B, (long long)(threadIdx.x % (C / 16)) * 16, C, HW);
+    bool fast_u8q = false;   // NHWC uint8 body through bn_affine_16_u8q
+    if (fixed) {
+        bn_coeffs_16<NHWC>(a, b, A, B, (long long)(threadIdx.x % (C / 16)) * 16, C, HW);
+        if (NHWC && !F32_IN) {
+            fast_u8q = true;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) fast_u8q &= (a[k] == a[k]) && (b[k] == b[k]);
+        }
+    }
     for (long long base = (long long)blockIdx.x * 256 * U; base < nv; base += (long long)gridDim.x * 256 * U) {
         if (F32_IN) {
             const long long v = base + threadIdx.x;
@@ -1295,7 +1317,7 @@ __global__ __launch_bounds__(256) void bn_affine_u8_16_kernel(const void* __rest
 #pragma unroll
                 for (int k = 0; k < 16; ++k) xf[k] = (float)((w[k >> 2] >> (8 * (k & 3))) & 0xffu);
                 if (!fixed) bn_coeffs_16<NHWC>(a, b, A, B, v * 16, C, HW);
-                ((uint4*)y)[v] = bn_affine_16<F32_IN, NHWC>(xf, a, b);
+                ((uint4*)y)[v] = fast_u8q ? bn_affine_16_u8q(xf, a, b) : bn_affine_16<F32_IN, NHWC>(xf, a, b);
             }
         }
     }

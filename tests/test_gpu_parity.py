@@ -778,6 +778,10 @@ def test_batchnorm_folded(dev, nhwc, f32_in, N, C, Hh, W):
     A[::5] = 1.0
     B = rng.uniform(-300.0, 300.0, C).astype(np.float32)
     B[::3] = 0.5
+    # x = 0 with B = -0.5: the result -0.5 rounds to -0, i.e. 0 (not the 255 a
+    # negative value saturates to in the NHWC uint8 body)
+    B[1::7] = -0.5
+    x.reshape(-1)[::11] = 0
     ref = O.batchnorm_u8(x, A, B, nhwc=nhwc)
     y = H.batchnorm_u8(to_dev(x, dev), to_dev(A, dev), to_dev(B, dev), nhwc=nhwc)
     assert np.array_equal(to_np(y), ref)

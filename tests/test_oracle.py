@@ -665,3 +665,13 @@ def test_conv_integer_1x1_is_matmul_integer():
     y = O.conv_integer(x, w, 100, -4)
     mm = O.matmul_integer(w.reshape(10, 16), x.reshape(16, 30), -4, 100)
     assert np.array_equal(y.reshape(10, 30), mm)
+
+
+def test_folded_bn_half_below_zero():
+    """The NHWC uint8 body rounds before it saturates: -0.5 is -0 -> 0, but
+    -0.51 is -1 -> 255."""
+    C = 16
+    x = np.zeros((1, 2, 2, C), np.uint8)
+    A = np.ones(C, np.float32)
+    assert np.all(O.batchnorm_u8(x, A, np.full(C, -0.5, np.float32), nhwc=1) == 0)
+    assert np.all(O.batchnorm_u8(x, A, np.full(C, -0.51, np.float32), nhwc=1) == 255)
