@@ -97,9 +97,11 @@ int nnr_ctx_load_onnx(nnr_ctx_t ctx, const void* data, size_t size, const char* 
  * (context_t::load_from_file, src/nnr.cpp) */
 int nnr_ctx_load_onnx_file(nnr_ctx_t ctx, const char* path, int sym_dim);
 /* the host copy of an initializer (as loaded or added; graph passes that
- * rewrite constants update it) */
+ * rewrite constants update it). No counterpart in the reference: for tests
+ * and tools that compare a loaded model with an in-process build. */
 int nnr_ctx_initializer(nnr_ctx_t ctx, const char* name, const void** host, size_t* nbytes);
-/* graph inputs (is_output 0) / outputs (1) in declaration order */
+/* graph inputs (is_output 0) / outputs (1) in declaration order
+ * (context_t::graph_inputs / graph_outputs, src/nnr.h) */
 int nnr_ctx_graph_io_count(nnr_ctx_t ctx, int is_output, int* n);
 int nnr_ctx_graph_io(nnr_ctx_t ctx, int is_output, int i, const char** name);
 
