@@ -263,6 +263,18 @@ size_t nnrh_dynamic_quantize_workspace(void);
 int nnrh_dynamic_quantize_linear(const float* x_dev, size_t n, uint8_t* y_dev,
                                  float* y_scale_dev, uint8_t* y_zp_dev,
                                  void* workspace_dev, void* stream);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): nnrh_dynamic_quantize_linear without the workspace
+ * argument. Its min / max partials live in one 8 KiB device array of the
+ * library (a copy per GPU, held until the process ends); the call allocates
+ * nothing. Same scale, zero point and bytes as nnrh_dynamic_quantize_linear.
+ * Calls that overlap on one GPU (other streams, other threads) share that
+ * array and race; serialize them. n above NNRH_DYNQ_NOALLOC_MAX_N is
+ * rejected with NNRH_ERR_INVALID.                                          */
+#define NNRH_DYNQ_NOALLOC_MAX_N ((size_t)1 << 40)
+int nnrh_dynamic_quantize_linear_noalloc(const float* x_dev, size_t n, uint8_t* y_dev,
+                                         float* y_scale_dev, uint8_t* y_zp_dev, void* stream);
 /* DynamicQuantizeLinear whose min / max were found by the operator that wrote
  * x: parts_dev holds nparts (min, max) pairs covering all of x (written by
  * nnrh_add_layernorm_f32 or a fused-dequantize nnrh_qmatmul_run). Same

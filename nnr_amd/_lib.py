@@ -36,7 +36,7 @@ EXPORTS = [
     "nnrh_conv_integer_create", "nnrh_conv_integer_run", "nnrh_conv_integer_destroy",
     "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
-    "nnrh_dynamic_quantize_linear", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
+    "nnrh_dynamic_quantize_linear", "nnrh_dynamic_quantize_linear_noalloc", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
     "nnrh_nchw_to_nhwc_u8", "nnrh_global_avgpool_f32", "nnrh_gemm_f32", "nnrh_clip_f32",
     "nnrh_gemm_f32_batched", "nnrh_binary_f32", "nnrh_softmax_f32", "nnrh_layernorm_f32",
     "nnrh_gelu_f32", "nnrh_transpose_f32",
@@ -142,6 +142,7 @@ def lib():
         "nnrh_dequantize_linear": (i, [vp, i, sz, f, i, vp, vp]),
         "nnrh_dynamic_quantize_workspace": (sz, []),
         "nnrh_dynamic_quantize_linear": (i, [vp, sz, vp, vp, vp, vp, vp]),
+        "nnrh_dynamic_quantize_linear_noalloc": (i, [vp, sz, vp, vp, vp, vp]),
         "nnrh_qlinear_add": (i, [i, vp, vp, vp, sz, i, i, i, i, f, i, f, i, f, i, vp]),
         "nnrh_qlinear_mul": (i, [i, vp, vp, vp, sz, i, i, i, i, f, i, f, i, f, i, vp]),
         "nnrh_qlinear_global_avgpool": (i, [vp, vp, i, i, i, i, i, f, i, f, i, vp]),

@@ -1350,6 +1350,19 @@ extern "C" int nnrh_dynamic_quantize_linear(const float* x, size_t n, uint8_t* y
     return NNRH_OK;
 }
 
+extern "C" int nnrh_dynamic_quantize_linear_noalloc(const float* x, size_t n, uint8_t* y, float* y_scale,
+                                                    uint8_t* y_zp, void* stream) {
+    if (!y_scale || !y_zp || (n && (!x || !y)))
+        return set_err(NNRH_ERR_INVALID, "dynamic_quantize_noalloc: NULL");
+    if (n > NNRH_DYNQ_NOALLOC_MAX_N)
+        return set_err(NNRH_ERR_INVALID,
+                       "dynamic_quantize_noalloc: n = %zu exceeds the maximum of %llu elements", n,
+                       (unsigned long long)NNRH_DYNQ_NOALLOC_MAX_N);
+    HIP_TRY(launch_dynamic_quantize_noalloc(x, (long long)n, y, y_scale, y_zp, S(stream)),
+            "dynamic_quantize_noalloc");
+    return NNRH_OK;
+}
+
 extern "C" int nnrh_dynamic_quantize_linear_parts(const float* x, size_t n, const float* parts, int nparts,
                                                   uint8_t* y, float* y_scale, uint8_t* y_zp, void* stream) {
     if (!y_scale || !y_zp || !parts || nparts <= 0 || (n && (!x || !y)))

@@ -71,6 +71,10 @@ size_t dynamic_quantize_workspace();
 hipError_t launch_dynamic_quantize(const float* x, long long n, uint8_t* y, float* y_scale,
                                    uint8_t* y_zp, void* workspace, hipStream_t s);
 // scale / zero point from nparts (min, max) pairs, then the quantize pass
+// as launch_dynamic_quantize, with the partials in the library's own
+// per-device scratch array (no workspace argument, no allocation)
+hipError_t launch_dynamic_quantize_noalloc(const float* x, long long n, uint8_t* y, float* y_scale,
+                                           uint8_t* y_zp, hipStream_t s);
 hipError_t launch_dynamic_quantize_parts(const float* x, long long n, const float* parts, int nparts,
                                          uint8_t* y, float* y_scale, uint8_t* y_zp, hipStream_t s);
 hipError_t launch_qadd(const QAddArgs& p, hipStream_t s);

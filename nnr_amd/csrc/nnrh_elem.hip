@@ -9,6 +9,9 @@
 #include "nnrh_elem.h"
 #include "nnrh_rq.h"
 
+#include <atomic>
+#include <mutex>
+
 namespace nnrh {
 
 __device__ __forceinline__ void st_q(void* y, int dt, long long i, int v) {
@@ -261,6 +264,53 @@ hipError_t launch_dynamic_quantize(const float* x, long long n, uint8_t* y, floa
     hipLaunchKernelGGL(dyn_quantize_kernel<false>, dim3((unsigned)qb), dim3(256), 0, s, x, n, part, blocks,
                        y_scale, y_zp, y);
     return hipGetLastError();
+}
+
+// DynamicQuantizeLinear with its min / max partials in a file-scope device
+// array instead of a caller's workspace, for callers that cannot allocate.
+// Every GPU the library runs on holds its own copy (8 KiB) until the process
+// ends; calls on one GPU share it, so calls that overlap on one GPU race.
+// Nothing in it needs clearing: the partial kernel writes every pair the
+// quantize kernel then reads.
+constexpr int DQL_SCRATCH_FLOATS = 2 * DQL_BLOCKS;
+static __device__ __align__(256) float scratch[DQL_SCRATCH_FLOATS];
+
+constexpr int DQL_MAX_DEVICES = 64;
+static std::atomic<float*> g_scratch_dev[DQL_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+// Device address of this GPU's copy of `scratch`, looked up once per device
+// with that device current. The array's name is only a host-side stand-in:
+// kernels get this address, never the name.
+static hipError_t dynq_scratch(float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= DQL_MAX_DEVICES) return hipErrorInvalidDevice;
+    float* p = g_scratch_dev[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        p = g_scratch_dev[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            void* sym = nullptr;
+            e = hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return e;
+            if (!sym) return hipErrorInvalidSymbol;
+            p = (float*)sym;
+            g_scratch_dev[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return hipSuccess;
+}
+
+hipError_t launch_dynamic_quantize_noalloc(const float* x, long long n, uint8_t* y, float* y_scale,
+                                           uint8_t* y_zp, hipStream_t s) {
+    static_assert(sizeof(scratch) >= sizeof(float) * 2 * DQL_BLOCKS, "scratch holds every partial");
+    float* part = nullptr;
+    hipError_t e = dynq_scratch(&part);
+    if (e != hipSuccess) return e;
+    return launch_dynamic_quantize(x, n, y, y_scale, y_zp, part, s);
 }
 
 hipError_t launch_dynamic_quantize_parts(const float* x, long long n, const float* parts, int nparts,
