@@ -413,6 +413,12 @@ int nnrh_layernorm_f32(const float* x_dev, const float* gamma_dev, const float* 
 int nnrh_add_layernorm_f32(const float* x_dev, const float* r_dev, const float* gamma_dev,
                            const float* beta_dev, float* y_dev, size_t rows, int D, float eps,
                            float* parts_dev, void* stream);
+/* HardSwish, fp32 (src/backend/cpu/HardSwish.cpp:18-50): y = x * clamp(x/6 +
+ * 0.5, 0, 1), the 16-wide body of the first n - n % 16 elements multiplying
+ * by fl(1/6), the tail dividing by 6 (vec_ops_avx512.h:96-117). post_op: 1
+ * when it runs as a producer's fused post-op (fuse_post_ops.cpp:61-68), which
+ * adds the zero bias of bias_hardswish (vec_ops_avx512.h:74-94) first.     */
+int nnrh_hardswish_f32(const float* x_dev, float* y_dev, size_t n, int post_op, void* stream);
 /* Gelu, approximate = "none" (src/backend/cpu/Gelu.cpp:43-47). */
 int nnrh_gelu_f32(const float* x_dev, float* y_dev, size_t n, void* stream);
 /* Transpose (src/backend/cpu/Transpose.cpp): ndim <= 6 input dims and perm. */

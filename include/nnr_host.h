@@ -37,7 +37,9 @@ int nnr_ctx_set_fusion(nnr_ctx_t ctx, int on);
  * the epilogue of the QLinearConv producing one operand; results unchanged. */
 int nnr_ctx_set_conv_add(nnr_ctx_t ctx, int on);
 
-/* dtype: ONNX TensorProto element type (1 float, 2 uint8, 3 int8, 6 int32, 7 int64, 10 f16) */
+/* dtype: the reference's data_type_t (src/nnr.h:20-56): 1 FLOAT32, 3 FLOAT16,
+ * 5 INT8, 6 INT16, 7 INT32, 8 INT64, 9 UINT8, 10 UINT16, 13 BOOL; other
+ * codes fail. (ONNX TensorProto codes are translated by the ONNX loader.) */
 int nnr_ctx_add_initializer(nnr_ctx_t ctx, const char* name, int dtype, const int* dims,
                             int ndim, const void* host_data);
 int nnr_ctx_add_input(nnr_ctx_t ctx, const char* name, int dtype, const int* dims, int ndim);

@@ -39,7 +39,7 @@ EXPORTS = [
     "nnrh_dynamic_quantize_linear", "nnrh_dynamic_quantize_linear_noalloc", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
     "nnrh_nchw_to_nhwc_u8", "nnrh_global_avgpool_f32", "nnrh_gemm_f32", "nnrh_clip_f32",
     "nnrh_gemm_f32_batched", "nnrh_binary_f32", "nnrh_softmax_f32", "nnrh_layernorm_f32",
-    "nnrh_gelu_f32", "nnrh_transpose_f32",
+    "nnrh_gelu_f32", "nnrh_hardswish_f32", "nnrh_transpose_f32",
 ]
 
 
@@ -164,6 +164,7 @@ def lib():
         "nnrh_softmax_f32": (i, [vp, vp, sz, i, vp]),
         "nnrh_layernorm_f32": (i, [vp, vp, vp, vp, sz, i, f, vp]),
         "nnrh_gelu_f32": (i, [vp, vp, sz, vp]),
+        "nnrh_hardswish_f32": (i, [vp, vp, sz, i, vp]),
         "nnrh_transpose_f32": (i, [vp, vp, i, P(i), P(i), vp]),
     }
     for name, (res, args) in sig.items():

@@ -1393,16 +1393,6 @@ extern "C" int nnrh_qlinear_add(int kind, const void* a, const void* b, void* y,
     p.a_zp = a_zp; p.b_zp = b_zp; p.y_zp = y_zp;
     p.lo = dtype == NNRH_U8 ? 0 : -128;
     p.hi = dtype == NNRH_U8 ? 255 : 127;
-    if (kind == 1 || kind == 2) {
-        // scalar operand value is read on the host side by the reference
-        // (QLinearAdd.cpp:109,115); here it is fetched from the device.
-        const void* sc = kind == 1 ? b : a;
-        uint8_t raw = 0;
-        HIP_TRY(hipMemcpyAsync(&raw, sc, 1, hipMemcpyDeviceToHost, S(stream)), "hipMemcpyAsync");
-        HIP_TRY(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
-        int v = dtype == NNRH_U8 ? (int)raw : (int)(int8_t)raw;
-        p.cval = kind == 1 ? p.sb * (float)(v - b_zp) : p.sa * (float)(v - a_zp);
-    }
     ProfScope ps("qlinear_add", S(stream));
     HIP_TRY(launch_qadd(p, S(stream)), "qlinear_add");
     return NNRH_OK;
@@ -1760,6 +1750,13 @@ extern "C" int nnrh_add_layernorm_f32(const float* x, const float* r, const floa
     ProfScope ps("layernorm_f32", S(stream));
     HIP_TRY(launch_layernorm_f32(x, r, gamma, beta, y, (long long)rows, D, eps, parts, S(stream)),
             "add_layernorm_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_hardswish_f32(const float* x, float* y, size_t n, int post_op, void* stream) {
+    if (n && (!x || !y)) return set_err(NNRH_ERR_INVALID, "hardswish_f32: NULL");
+    ProfScope ps("hardswish_f32", S(stream));
+    HIP_TRY(launch_hardswish_f32(x, y, (long long)n, post_op ? 1 : 0, S(stream)), "hardswish_f32");
     return NNRH_OK;
 }
 

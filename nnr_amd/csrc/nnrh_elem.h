@@ -17,7 +17,6 @@ struct QAddArgs {
     int dt;              // 0 u8, 1 s8
     float sa, sb;        // a_s / y_s, b_s / y_s
     float fixed;         // same-shape body constant
-    float cval;          // scalar-broadcast constant
     int a_zp, b_zp, y_zp;
     int lo, hi;
     int tail_all;        // every element takes the scalar tail expression

@@ -348,14 +348,18 @@ __global__ __launch_bounds__(256) void qadd_kernel(QAddArgs p) {
                 q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
             }
         } else if (p.kind == 1 || p.kind == 2) {
-            // scalar loops (QLinearAdd.cpp:108-119)
+            // scalar loops (QLinearAdd.cpp:108-119); the scalar operand's
+            // term c = s * (q - zp) is formed from the device byte, as the
+            // reference forms it from the host one
             float v;
             if (p.kind == 1) {
+                const float cval = p.sb * (float)(ld_q(p.b, p.dt, 0) - p.b_zp);
                 float t = p.sa * (float)(ld_q(p.a, p.dt, i) - p.a_zp);
-                v = (t + p.cval) + (float)p.y_zp;
+                v = (t + cval) + (float)p.y_zp;
             } else {
+                const float cval = p.sa * (float)(ld_q(p.a, p.dt, 0) - p.a_zp);
                 float t = p.sb * (float)(ld_q(p.b, p.dt, i) - p.b_zp);
-                v = (p.cval + t) + (float)p.y_zp;
+                v = (cval + t) + (float)p.y_zp;
             }
             q = clampi(x86_f2i(__builtin_rintf(v)), p.lo, p.hi);
         } else {
@@ -1287,7 +1291,8 @@ __device__ __forceinline__ void bn_coeffs_16(float* a, float* b, const float* __
     }
 }
 
-// NHWC uint8 input with NaN-free A / B: t = fma(x, A, B) is never NaN, and
+// NHWC uint8 input with finite A / B: t = fma(x, A, B) is never NaN (an
+// infinite A with x = 0, or A*x = +inf with B = -inf, would make it NaN), and
 // round-to-nearest-even + unsigned saturation (negative -> 255) is
 // t < -0.5 ? 255 : v_cvt_pk_u8_f32(t) (t = -0.5 rounds to -0, i.e. 0)
 __device__ __forceinline__ uint4 bn_affine_16_u8q(const float* xf, const float* a, const float* b) {
@@ -1335,7 +1340,7 @@ __global__ __launch_bounds__(256) void bn_affine_u8_16_kernel(const void* __rest
         if (NHWC && !F32_IN) {
             fast_u8q = true;
 #pragma unroll
-            for (int k = 0; k < 16; ++k) fast_u8q &= (a[k] == a[k]) && (b[k] == b[k]);
+            for (int k = 0; k < 16; ++k) fast_u8q &= __builtin_isfinite(a[k]) && __builtin_isfinite(b[k]);
         }
     }
     for (long long base = (long long)blockIdx.x * 256 * U; base < nv; base += (long long)gridDim.x * 256 * U) {

@@ -35,6 +35,7 @@ hipError_t launch_transpose_f32(const float* x, float* y, int ndim, const int* i
 size_t mha_workspace_bytes(int B, int S, int nh);
 hipError_t launch_mha_f32(const float* q, const float* k, const float* v, float* y, int B, int S, int Hd, int nh,
                           float scale, void* ws, hipStream_t s);
+hipError_t launch_hardswish_f32(const float* x, float* y, long long n, int post_op, hipStream_t s);
 hipError_t launch_clip_f32(const float* x, float* y, long long n, float lo, float hi,
                            hipStream_t s);
 

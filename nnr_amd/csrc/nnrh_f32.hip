@@ -342,6 +342,43 @@ hipError_t launch_clip_f32(const float* x, float* y, long long n, float lo, floa
 }
 
 // ---------------------------------------------------------------------------
+// HardSwish (src/backend/cpu/HardSwish.cpp:18-50; vec_ops_avx512.h:74-117):
+// y = x * clamp(x / 6 + 0.5, 0, 1) with the reference's two expressions.
+// 16-wide body (the first n - n % 16 elements): u = fl(fl(x * fl(1/6)) + 0.5),
+// t = min_ps(max_ps(u, 0), 1) -- max_ps / min_ps return their second operand
+// unless the first compares greater / smaller, so a NaN u gives t = 0.
+// Scalar tail: w = fl(fl(x / 6) + 0.5), t = std::max(0, std::min(1, w)) -- a
+// NaN w gives t = 1. As a producer's fused post-op (post_op), x is first
+// fl(x + 0.0f), the zero bias the reference's bias_hardswish adds.
+__global__ __launch_bounds__(256) void hardswish_f32_kernel(const float* __restrict x, float* __restrict y,
+                                                            long long n, long long body, int post_op) {
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (long long)gridDim.x * 256) {
+        float v = x[i];
+        if (post_op) v = v + 0.0f;
+        float t;
+        if (i < body) {
+            const float u = v * (1.0f / 6.0f) + 0.5f;
+            const float m = u > 0.0f ? u : 0.0f;
+            t = m < 1.0f ? m : 1.0f;
+        } else {
+            const float w = v / 6.0f + 0.5f;
+            const float m = w < 1.0f ? w : 1.0f;
+            t = 0.0f < m ? m : 0.0f;
+        }
+        y[i] = v * t;
+    }
+}
+
+hipError_t launch_hardswish_f32(const float* x, float* y, long long n, int post_op, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    long long b = (n + 255) / 256;
+    if (b > 65536) b = 65536;
+    hipLaunchKernelGGL(hardswish_f32_kernel, dim3((unsigned)b), dim3(256), 0, s, x, y, n, n - n % 16, post_op);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // y = a (op) b; b_mode: 0 same shape, 1 scalar, 2 broadcast over the last axis
 // (b has D elements); b_first swaps the operands (b op a) for Sub / Div.
 __global__ __launch_bounds__(256) void binary_f32_kernel(const float* __restrict a,

@@ -21,7 +21,10 @@ HOST_LIB = os.path.join(_HERE, "lib", "libnnr_host.so")
 
 ONNX_DT = {np.dtype(np.float32): 1, np.dtype(np.uint8): 2, np.dtype(np.int8): 3,
            np.dtype(np.int32): 6, np.dtype(np.int64): 7, np.dtype(np.float16): 10}
-NP_DT = {v: k for k, v in ONNX_DT.items()}
+# the reference's data_type_t codes (src/nnr.h:20-56), which the host C ABI takes
+NNR_DT = {np.dtype(np.float32): 1, np.dtype(np.float16): 3, np.dtype(np.int8): 5,
+          np.dtype(np.int32): 7, np.dtype(np.int64): 8, np.dtype(np.uint8): 9}
+NP_DT = {v: k for k, v in NNR_DT.items()}
 BACKEND_HIP = 4
 
 _hl = None
@@ -185,11 +188,11 @@ class Session:
             return
         for name, arr in graph.initializers.items():
             dims = (C.c_int * max(1, arr.ndim))(*arr.shape)
-            _chk(L.nnr_ctx_add_initializer(h, name.encode(), ONNX_DT[arr.dtype], dims, arr.ndim,
+            _chk(L.nnr_ctx_add_initializer(h, name.encode(), NNR_DT[arr.dtype], dims, arr.ndim,
                                            arr.ctypes.data))
         for name, (dt, shape) in graph.inputs.items():
             dims = (C.c_int * max(1, len(shape)))(*shape)
-            _chk(L.nnr_ctx_add_input(h, name.encode(), ONNX_DT[np.dtype(dt)], dims, len(shape)))
+            _chk(L.nnr_ctx_add_input(h, name.encode(), NNR_DT[np.dtype(dt)], dims, len(shape)))
         for name in graph.outputs:
             _chk(L.nnr_ctx_add_output(h, name.encode()))
         for nd in graph.nodes:

@@ -23,13 +23,41 @@ size_t data_type_sizeof(data_type_t t) {
     }
 }
 
-// ---- tensor_t --------------------------------------------------------------
-bool tensor_t::reshape(const std::vector<int>& d, data_type_t t) {
+data_type_t data_type_from_onnx(int onnx) {
+    // TensorProto.DataType codes (onnx.proto3 TensorProto.DataType)
+    static const data_type_t table[] = {
+        NNR_DATA_TYPE_UNDEFINED,      NNR_DATA_TYPE_FLOAT32,        NNR_DATA_TYPE_UINT8,
+        NNR_DATA_TYPE_INT8,           NNR_DATA_TYPE_UINT16,         NNR_DATA_TYPE_INT16,
+        NNR_DATA_TYPE_INT32,          NNR_DATA_TYPE_INT64,          NNR_DATA_TYPE_STRING,
+        NNR_DATA_TYPE_BOOL,           NNR_DATA_TYPE_FLOAT16,        NNR_DATA_TYPE_FLOAT64,
+        NNR_DATA_TYPE_UINT32,         NNR_DATA_TYPE_UINT64,         NNR_DATA_TYPE_COMPLEX64,
+        NNR_DATA_TYPE_COMPLEX128,     NNR_DATA_TYPE_BFLOAT16,       NNR_DATA_TYPE_FLOAT8E4M3FN,
+        NNR_DATA_TYPE_FLOAT8E4M3FNUZ, NNR_DATA_TYPE_FLOAT8E5M2,     NNR_DATA_TYPE_FLOAT8E5M2FNUZ,
+        NNR_DATA_TYPE_UINT4,          NNR_DATA_TYPE_INT4,           NNR_DATA_TYPE_FLOAT4E2M1,
+        NNR_DATA_TYPE_FLOAT8E8M0,     NNR_DATA_TYPE_UINT2,          NNR_DATA_TYPE_INT2,
+    };
+    if (onnx < 0 || onnx >= (int)(sizeof(table) / sizeof(table[0]))) return NNR_DATA_TYPE_UNDEFINED;
+    return table[onnx];
+}
+
+// product of dims, or false when a dimension is negative or the element
+// count or its byte size would not fit in size_t
+bool checked_count(const std::vector<int>& d, size_t elem_size, size_t* count) {
     size_t n = 1;
     for (int v : d) {
         if (v < 0) return false;
+        if (v != 0 && n > SIZE_MAX / (size_t)v) return false;
         n *= (size_t)v;
     }
+    if (elem_size && n > SIZE_MAX / elem_size) return false;
+    *count = n;
+    return true;
+}
+
+// ---- tensor_t --------------------------------------------------------------
+bool tensor_t::reshape(const std::vector<int>& d, data_type_t t) {
+    size_t n = 0;
+    if (!checked_count(d, data_type_sizeof(t), &n)) return false;
     dims = d;
     type = t;
     ndata = n;
@@ -103,24 +131,50 @@ void registry_t::register_op(const std::string& name, backend_t b, resolver_fn f
 bool registry_t::has(const std::string& name, backend_t b) const {
     return ops_.count({name, b}) != 0;
 }
-operator_t* registry_t::solve(const std::string& op_type, int opset, backend_t preferred) {
+operator_t* registry_t::solve(const std::string& op_type, int opset, pool_t& pool, backend_t preferred) {
     if (preferred != backend_t::CPU) {
         auto it = ops_.find({op_type, preferred});
         if (it != ops_.end()) {
-            operator_t* op = it->second(opset);
+            operator_t* op = it->second(opset, pool);
             if (op) return op;
         }
     }
     auto it = ops_.find({op_type, backend_t::CPU});
-    if (it != ops_.end()) return it->second(opset);
+    if (it != ops_.end()) return it->second(opset, pool);
     return nullptr;
 }
 registry_t& global_registry() {
     static registry_t r;
     return r;
 }
-operator_t* solve_operator(const std::string& op_type, int opset, backend_t preferred) {
-    return global_registry().solve(op_type, opset, preferred);
+operator_t* solve_operator(const std::string& op_type, int opset, pool_t& pool, backend_t preferred) {
+    return global_registry().solve(op_type, opset, pool, preferred);
+}
+
+// ---- pool_t ----------------------------------------------------------------
+pool_t::~pool_t() {
+    for (char* b : blocks_) ::operator delete(b);
+}
+void* pool_t::alloc(size_t size, size_t align) {
+    if (size == 0) size = 1;
+    if (size + align > BlockSize) {   // a block of its own, kept before the current one
+        char* b = (char*)::operator new(size + align);
+        blocks_.insert(blocks_.empty() ? blocks_.end() : blocks_.end() - 1, b);
+        return (void*)(((uintptr_t)b + align - 1) & ~(uintptr_t)(align - 1));
+    }
+    if (!blocks_.empty()) {
+        uintptr_t base = (uintptr_t)blocks_.back();
+        uintptr_t p = (base + used_ + align - 1) & ~(uintptr_t)(align - 1);
+        if (p + size <= base + BlockSize) {
+            used_ = p + size - base;
+            return (void*)p;
+        }
+    }
+    char* b = (char*)::operator new(BlockSize);
+    blocks_.push_back(b);
+    uintptr_t p = ((uintptr_t)b + align - 1) & ~(uintptr_t)(align - 1);
+    used_ = p + size - (uintptr_t)b;
+    return (void*)p;
 }
 
 // ---- context_t -------------------------------------------------------------
@@ -132,7 +186,7 @@ context_t::~context_t() {
         nnrh_event_destroy(e.second);
     }
     for (void* p : allocations_) nnrh_free(p);
-    for (auto* n : nodes) delete n;
+    for (auto* n : nodes) destroy_op(n);
     for (auto& kv : map) delete kv.second;
 }
 
@@ -168,7 +222,7 @@ bool context_t::add_initializer(const std::string& name, data_type_t t, const st
 
 bool context_t::add_input(const std::string& name, data_type_t t, const std::vector<int>& dims) {
     tensor_t* x = tensor(name);
-    if (!x || !x->reshape(dims, t)) return fail("input " + name + ": bad dims");
+    if (!x || !x->reshape(dims, t) || data_type_sizeof(t) == 0) return fail("input " + name + ": bad type or dims");
     graph_inputs.push_back(name);
     return true;
 }
@@ -183,8 +237,8 @@ bool context_t::add_node(const std::string& op_type, const std::string& name,
                          const std::vector<std::string>& ins, const std::vector<std::string>& outs,
                          std::vector<std::pair<std::string, attr_t>> attrs) {
     // onnx_loader.cpp:595-653: resolve through the registry, wire, init()
-    operator_t* op = solve_operator(op_type, opset, preferred_backend);
-    if (!op) op = new unresolved_op_t();
+    operator_t* op = solve_operator(op_type, opset, attr_pool, preferred_backend);
+    if (!op) op = pool_new<unresolved_op_t>(attr_pool);
     op->ctx = this;
     op->opset = opset;
     op->op_type = op_type;
@@ -240,6 +294,9 @@ bool context_t::plan_memory() {
         for (auto* t : op->inputs) want(t);
         for (auto* t : op->outputs) want(t);
     }
+    // a graph output no active node writes is the output of a skipped
+    // post-op step: an alias of its producer's buffer, resolved below
+    for (auto& n : graph_outputs) want(find(n));
     for (auto* t : order) {
         if (t->data) continue;
         if (t->alias_of) continue;

@@ -25,20 +25,48 @@
 
 namespace nnr {
 
-// ONNX TensorProto element types (the reference's data_type_t numbering)
-enum data_type_t : int {
+// Element types, in the reference's data_type_t numbering and order
+// (src/nnr.h:20-56), so a tensor_t::type from NNR means the same here. ONNX
+// TensorProto codes are translated by the loader (data_type_from_onnx).
+enum data_type_t : uint8_t {
     NNR_DATA_TYPE_UNDEFINED = 0,
-    NNR_DATA_TYPE_FLOAT32 = 1,
-    NNR_DATA_TYPE_UINT8 = 2,
-    NNR_DATA_TYPE_INT8 = 3,
-    NNR_DATA_TYPE_UINT16 = 4,
-    NNR_DATA_TYPE_INT16 = 5,
-    NNR_DATA_TYPE_INT32 = 6,
-    NNR_DATA_TYPE_INT64 = 7,
-    NNR_DATA_TYPE_BOOL = 9,
-    NNR_DATA_TYPE_FLOAT16 = 10,
+    NNR_DATA_TYPE_FLOAT32,
+    NNR_DATA_TYPE_FLOAT64,
+    NNR_DATA_TYPE_FLOAT16,
+    NNR_DATA_TYPE_BFLOAT16,
+    NNR_DATA_TYPE_INT8,
+    NNR_DATA_TYPE_INT16,
+    NNR_DATA_TYPE_INT32,
+    NNR_DATA_TYPE_INT64,
+    NNR_DATA_TYPE_UINT8,
+    NNR_DATA_TYPE_UINT16,
+    NNR_DATA_TYPE_UINT32,
+    NNR_DATA_TYPE_UINT64,
+    NNR_DATA_TYPE_BOOL,
+    NNR_DATA_TYPE_STRING,
+    NNR_DATA_TYPE_COMPLEX64,
+    NNR_DATA_TYPE_COMPLEX128,
+    NNR_DATA_TYPE_FLOAT8E4M3FN,
+    NNR_DATA_TYPE_FLOAT8E4M3FNUZ,
+    NNR_DATA_TYPE_FLOAT8E5M2,
+    NNR_DATA_TYPE_FLOAT8E5M2FNUZ,
+    NNR_DATA_TYPE_FLOAT8E8M0,
+    NNR_DATA_TYPE_UINT4,
+    NNR_DATA_TYPE_INT4,
+    NNR_DATA_TYPE_FLOAT4E2M1,
+    NNR_DATA_TYPE_UINT2,
+    NNR_DATA_TYPE_INT2,
+    NNR_DATA_TYPE_SEQUENCE,
+    NNR_DATA_TYPE_COUNT,
 };
+// ONNX TensorProto.DataType -> data_type_t (UNDEFINED for codes with no
+// counterpart), as the reference's loader maps them (onnx_loader.cpp:28-58)
+data_type_t data_type_from_onnx(int onnx_elem_type);
+// 0 when this backend stores no element of that type in device memory
 size_t data_type_sizeof(data_type_t t);
+// element count of dims (false: a negative dimension, or a count or byte
+// size past SIZE_MAX)
+bool checked_count(const std::vector<int>& dims, size_t elem_size, size_t* count);
 
 enum class memory_layout_t : uint8_t { NCHW = 0, NHWC = 1 };
 constexpr uint8_t LAYOUT_NCHW = 1;
@@ -73,6 +101,26 @@ struct tensor_t {
     int32_t scalar_int() const;
     bool is_quantized() const { return quant_scale != 0.0f; }
     void set_quant(float s, int32_t zp) { quant_scale = s; quant_zero_point = zp; }
+};
+
+// Arena for operator objects, as the reference's pool_t (src/pool.h:16-60):
+// resolvers placement-new operators into context_t::attr_pool, and the
+// memory goes when the context does. Objects are not freed one by one; a
+// replaced operator has its destructor run (destroy_op) so that the device
+// memory it owns is released at once.
+struct pool_t {
+    static constexpr size_t BlockSize = 64 * 1024;
+    pool_t() = default;
+    pool_t(const pool_t&) = delete;
+    pool_t& operator=(const pool_t&) = delete;
+    ~pool_t();
+    void* alloc(size_t size, size_t align = alignof(std::max_align_t));
+    template <typename T>
+    T* alloc_arr(size_t n) { return (T*)alloc(sizeof(T) * n, alignof(T)); }
+
+private:
+    std::vector<char*> blocks_;
+    size_t used_ = BlockSize;   // bytes used in blocks_.back()
 };
 
 struct attr_t {
@@ -114,9 +162,12 @@ struct operator_t {
     bool resolved = true;         // false: placeholder for an op this backend lacks
     // fused unary post-op (src/nnr.h:437-442). For the int8 operators the
     // only effect is QLinearConv's qmin (QLinearConv.cpp:419).
-    bool fusable_unary = false;   // set in init() by Relu / Clip
+    bool fusable_unary = false;   // set in init() by Relu / Clip / HardSwish
     bool post_fn = false;
     operator_t* fused_op = nullptr;
+    // the fused unary applied in place to an fp32 producer's n outputs (the
+    // reference's fusable_apply with no bias); false: not a post-op provider
+    virtual bool apply_post(void* /*data_dev*/, size_t /*n*/) { return false; }
     // a same-shape QLinearAdd folded into this operator's kernel
     // (fuse_conv_add); the add node is skipped and its output is ours
     operator_t* fused_add = nullptr;
@@ -224,6 +275,7 @@ struct context_t {
     memory_planner_t planner;
 
     // ---- state ----
+    pool_t attr_pool;             // operators live here (src/nnr.h:552)
     std::map<std::string, tensor_t*> map;
     std::vector<operator_t*> nodes;
     std::vector<std::string> graph_inputs, graph_outputs;
@@ -266,7 +318,12 @@ void fold_bn_qdq(context_t* ctx);
 bool load_onnx(context_t* ctx, const void* data, size_t size, const std::string& model_dir, int sym_dim);
 bool load_onnx_file(context_t* ctx, const std::string& path, int sym_dim);
 
-// operator creation through the registry (src/backend/cpu/solve_operator.cpp:29-33)
-operator_t* solve_operator(const std::string& op_type, int opset, backend_t preferred);
+// operator creation through the registry (src/backend/cpu/solve_operator.cpp:29-33);
+// the operator is placed in `pool`
+operator_t* solve_operator(const std::string& op_type, int opset, pool_t& pool, backend_t preferred);
+// runs a pool-placed operator's destructor (its memory stays in the pool)
+inline void destroy_op(operator_t* op) {
+    if (op) op->~operator_t();
+}
 
 }  // namespace nnr

@@ -374,7 +374,7 @@ bool parse_model(reader_t r, model_pb& m) {
 }
 
 // ---- tensor data --------------------------------------------------------------
-bool supported_type(int32_t dt) {
+bool supported_type(data_type_t dt) {
     switch (dt) {
     case NNR_DATA_TYPE_FLOAT32: case NNR_DATA_TYPE_UINT8: case NNR_DATA_TYPE_INT8:
     case NNR_DATA_TYPE_UINT16: case NNR_DATA_TYPE_INT16: case NNR_DATA_TYPE_INT32:
@@ -385,24 +385,34 @@ bool supported_type(int32_t dt) {
     }
 }
 
+// largest initializer the loader will hold on the host (a larger one is a
+// malformed or hostile file, not a model this backend can place in HBM)
+constexpr size_t MAX_INITIALIZER_BYTES = (size_t)64 << 30;
+
 // host bytes of a TensorProto (onnx_tensor_copy_from_proto, :65-200; external
 // data :250-300). Fewer stored values than elements leave zeros, as the
-// reference's min(ndata, stored) copies do.
+// reference's copy does.
 bool tensor_bytes(const tensor_pb& t, const std::string& model_dir, std::vector<uint8_t>& out,
                   std::string& err) {
-    if (!supported_type(t.data_type)) {
+    const data_type_t dt = data_type_from_onnx(t.data_type);
+    if (!supported_type(dt)) {
         err = "tensor " + t.name + ": unsupported data type " + std::to_string(t.data_type);
         return false;
     }
-    size_t n = 1;
+    std::vector<int> dims;
     for (int64_t d : t.dims) {
         if (d < 0 || d > INT32_MAX) {
             err = "tensor " + t.name + ": bad dimension";
             return false;
         }
-        n *= (size_t)d;
+        dims.push_back((int)d);
     }
-    const size_t sz = data_type_sizeof((data_type_t)t.data_type);
+    const size_t sz = data_type_sizeof(dt);
+    size_t n = 0;
+    if (!checked_count(dims, sz, &n) || n * sz > MAX_INITIALIZER_BYTES) {
+        err = "tensor " + t.name + ": element count too large";
+        return false;
+    }
     out.assign(n * sz, 0);
     if (t.data_location == 1) {   // EXTERNAL
         std::string location;
@@ -414,6 +424,10 @@ bool tensor_bytes(const tensor_pb& t, const std::string& model_dir, std::vector<
         }
         if (location.empty()) {
             err = "tensor " + t.name + ": external data without a location";
+            return false;
+        }
+        if (offset < 0) {
+            err = "tensor " + t.name + ": negative external data offset";
             return false;
         }
         const std::string path = model_dir + location;
@@ -435,7 +449,7 @@ bool tensor_bytes(const tensor_pb& t, const std::string& model_dir, std::vector<
         std::memcpy(out.data(), t.raw, std::min(t.raw_size, out.size()));
         return true;
     }
-    switch (t.data_type) {
+    switch (dt) {
     case NNR_DATA_TYPE_FLOAT32:
         std::memcpy(out.data(), t.float_data.data(), std::min(n, t.float_data.size()) * 4);
         break;
@@ -480,16 +494,16 @@ bool load_onnx(context_t* ctx, const void* data, size_t size, const std::string&
     for (auto& t : g.initializer) {
         if (t.name.empty()) continue;
         if (!tensor_bytes(t, dir, bytes, err)) return ctx->fail("load_onnx: " + err);
-        if (!ctx->add_initializer(t.name, (data_type_t)t.data_type, dims_of(t), bytes.data()))
+        if (!ctx->add_initializer(t.name, data_type_from_onnx(t.data_type), dims_of(t), bytes.data()))
             return false;
     }
     for (auto& v : g.input) {
         if (v.name.empty() || ctx->initializer_names.count(v.name)) continue;
-        if (!supported_type(v.elem_type))
+        if (!supported_type(data_type_from_onnx(v.elem_type)))
             return ctx->fail("load_onnx: input " + v.name + ": unsupported element type");
         std::vector<int> d;
         for (int64_t x : v.dims) d.push_back(x > 0 ? (int)x : (sym_dim > 0 ? sym_dim : 1));
-        if (!ctx->add_input(v.name, (data_type_t)v.elem_type, d)) return false;
+        if (!ctx->add_input(v.name, data_type_from_onnx(v.elem_type), d)) return false;
     }
     int unnamed = 0;
     for (auto& n : g.node) {
@@ -500,7 +514,7 @@ bool load_onnx(context_t* ctx, const void* data, size_t size, const std::string&
             for (auto& a : n.attribute) {
                 if (a.name == "value" && a.has_t) {
                     if (!tensor_bytes(a.t, dir, bytes, err)) return ctx->fail("load_onnx: " + err);
-                    done = ctx->add_initializer(n.output[0], (data_type_t)a.t.data_type, dims_of(a.t), bytes.data());
+                    done = ctx->add_initializer(n.output[0], data_type_from_onnx(a.t.data_type), dims_of(a.t), bytes.data());
                 } else if (a.name == "value_float") {
                     done = ctx->add_initializer(n.output[0], NNR_DATA_TYPE_FLOAT32, {}, &a.f);
                 } else if (a.name == "value_int") {

@@ -1067,10 +1067,13 @@ struct Gemm_hip : operator_t {
     }
     bool exec() override {
         tensor_t* c = in(this, 2);
-        return ok(this, nnrh_gemm_f32((const float*)inputs[0]->data, (const float*)inputs[1]->data,
-                                      c ? (const float*)c->data : nullptr, (float*)outputs[0]->data, M, N, K,
-                                      (int)attribute("transA", 0), (int)attribute("transB", 0),
-                                      attribute_f("alpha", 1.0f), attribute_f("beta", 1.0f), c_mode, ctx->stream));
+        if (!ok(this, nnrh_gemm_f32((const float*)inputs[0]->data, (const float*)inputs[1]->data,
+                                    c ? (const float*)c->data : nullptr, (float*)outputs[0]->data, M, N, K,
+                                    (int)attribute("transA", 0), (int)attribute("transB", 0),
+                                    attribute_f("alpha", 1.0f), attribute_f("beta", 1.0f), c_mode, ctx->stream)))
+            return false;
+        // a fused Relu / Clip / HardSwish runs over the whole output (Gemm.cpp:146-151)
+        return !(post_fn && fused_op) || fused_op->apply_post(outputs[0]->data, outputs[0]->ndata);
     }
     double num_ops() const override { return 2.0 * M * (double)N * K; }
 };
@@ -1096,6 +1099,42 @@ struct Clip_hip : operator_t {
         }
         return ok(this, nnrh_clip_f32((const float*)inputs[0]->data, (float*)outputs[0]->data, inputs[0]->ndata,
                                       lo, hi, ctx->stream));
+    }
+    // fused after an fp32 producer: with no bias the reference runs the same
+    // clip over the output in place (Relu.cpp:36-70, Clip.cpp:20-57)
+    bool apply_post(void* data, size_t n) override {
+        float lo = relu ? 0.0f : -INFINITY, hi = INFINITY;
+        if (!relu) {
+            if (in(this, 1) && in(this, 1)->has_host()) lo = in(this, 1)->scalar_f32();
+            if (in(this, 2) && in(this, 2)->has_host()) hi = in(this, 2)->scalar_f32();
+        }
+        return ok(this, nnrh_clip_f32((const float*)data, (float*)data, n, lo, hi, ctx->stream));
+    }
+};
+
+// HardSwish (src/backend/cpu/HardSwish.cpp:18-50), fp32. Not quant-capable
+// (fuse_qdq.cpp:96-100), so DQ -> HardSwish -> Q runs it on fp32 tensors;
+// fusable into a preceding producer like Relu / Clip (on QLinearConv the
+// fusion only sets qmin, QLinearConv.cpp:419).
+struct HardSwish_hip : operator_t {
+    bool init() override {
+        layout_mask = LAYOUT_ALL;
+        fusable_unary = true;
+        return inputs.size() == 1 && outputs.size() == 1;
+    }
+    bool reshape() override {
+        if (inputs[0]->type != NNR_DATA_TYPE_FLOAT32 && !ctx->shape_only && !skip)
+            return bad(this, "fp32 only (a fused HardSwish on QLinearConv only raises qmin)");
+        return operator_t::reshape();
+    }
+    bool exec() override {
+        return ok(this, nnrh_hardswish_f32((const float*)inputs[0]->data, (float*)outputs[0]->data,
+                                           inputs[0]->ndata, 0, ctx->stream));
+    }
+    // bias_hardswish with a zero bias over the producer's output as one row
+    // (Gemm.cpp:146-151, vec_ops_avx512.h:74-94)
+    bool apply_post(void* data, size_t n) override {
+        return ok(this, nnrh_hardswish_f32((const float*)data, (float*)data, n, 1, ctx->stream));
     }
 };
 
@@ -1137,8 +1176,8 @@ struct Binary_hip : operator_t {
     }
 };
 template <int OP>
-operator_t* make_binary(int) {
-    auto* b = new Binary_hip();
+operator_t* make_binary(int, pool_t& pool) {
+    auto* b = pool_new<Binary_hip>(pool);
     b->op = OP;
     return b;
 }
@@ -1317,18 +1356,23 @@ struct MatMul_hip : operator_t {
         return outputs[0]->reshape(d, NNR_DATA_TYPE_FLOAT32);
     }
     bool exec() override {
-        return ok(this, nnrh_gemm_f32_batched((const float*)inputs[0]->data, (const float*)inputs[1]->data, nullptr,
-                                              (float*)outputs[0]->data, M, N, K, 0, 0, 1.0f, 0.0f, 0, batch,
-                                              (long long)M * K, b_shared ? 0 : (long long)K * N,
-                                              (long long)M * N, ctx->stream));
+        if (!ok(this, nnrh_gemm_f32_batched((const float*)inputs[0]->data, (const float*)inputs[1]->data, nullptr,
+                                            (float*)outputs[0]->data, M, N, K, 0, 0, 1.0f, 0.0f, 0, batch,
+                                            (long long)M * K, b_shared ? 0 : (long long)K * N,
+                                            (long long)M * N, ctx->stream)))
+            return false;
+        // a fused unary over the whole output; the reference applies it per
+        // GEMM output tile (gemm_post_t, MatMul.cpp:218-280), which for
+        // HardSwish moves which elements take the scalar-tail expression
+        return !(post_fn && fused_op) || fused_op->apply_post(outputs[0]->data, outputs[0]->ndata);
     }
     double num_ops() const override { return 2.0 * batch * M * (double)N * K; }
 };
 
 template <typename T>
-operator_t* make(int) { return new T(); }
-operator_t* make_relu(int) {
-    auto* c = new Clip_hip();
+operator_t* make(int, pool_t& pool) { return pool_new<T>(pool); }
+operator_t* make_relu(int, pool_t& pool) {
+    auto* c = pool_new<Clip_hip>(pool);
     c->relu = true;
     return c;
 }
@@ -1354,6 +1398,7 @@ const op_registrar_t reg[] = {
     {"Gemm", backend_t::HIP, make<Gemm_hip>},
     {"Relu", backend_t::HIP, make_relu},
     {"Clip", backend_t::HIP, make<Clip_hip>},
+    {"HardSwish", backend_t::HIP, make<HardSwish_hip>},
     {"Add", backend_t::HIP, make_binary<0>},
     {"Mul", backend_t::HIP, make_binary<1>},
     {"Sub", backend_t::HIP, make_binary<2>},

@@ -143,7 +143,7 @@ void fuse_qdq_compute(context_t* ctx) {
         if (q_y->inputs.size() < 2) continue;
 
         const char* new_type = is_conv ? "QLinearConv" : "QLinearMatMul";
-        operator_t* f = solve_operator(new_type, op->opset, ctx->preferred_backend);
+        operator_t* f = solve_operator(new_type, op->opset, ctx->attr_pool, ctx->preferred_backend);
         if (!f) continue;
         f->ctx = ctx;
         f->opset = op->opset;
@@ -158,7 +158,7 @@ void fuse_qdq_compute(context_t* ctx) {
         convert_weight_uint8_to_int8(f->inputs[3], f->inputs[5]);
         f->init();
         nodes[i] = f;
-        delete op;
+        destroy_op(op);
         if (count_consumers(ctx, dq_x->outputs[0], all_producer[dq_x->outputs[0]]) == 0) dq_x->folded = true;
         dq_w->folded = true;
         if (dq_b) dq_b->folded = true;
@@ -213,7 +213,7 @@ void fuse_qdq_compute(context_t* ctx) {
         if (qi < 0) continue;
         operator_t* q_y = nodes[qi];
         if (q_y->inputs.size() < 2) continue;
-        operator_t* f = solve_operator("QLinearAdd", op->opset, ctx->preferred_backend);
+        operator_t* f = solve_operator("QLinearAdd", op->opset, ctx->attr_pool, ctx->preferred_backend);
         if (!f) continue;
         f->ctx = ctx;
         f->opset = op->opset;
@@ -227,7 +227,7 @@ void fuse_qdq_compute(context_t* ctx) {
         tensor_t* in0 = op->inputs[0];
         tensor_t* in1 = op->inputs[1];
         nodes[i] = f;
-        delete op;
+        destroy_op(op);
         if (count_consumers(ctx, dq_a->outputs[0], all_producer[in0]) == 0) dq_a->folded = true;
         if (count_consumers(ctx, dq_b->outputs[0], all_producer[in1]) == 0) dq_b->folded = true;
         if (relu >= 0) nodes[relu]->folded = true;
@@ -333,6 +333,9 @@ void fuse_post_ops(context_t* ctx) {
         p->post_fn = true;
         p->fused_op = c;
         c->skip = true;
+        // an fp32 producer applies the fused op to its output in place
+        // (apply_post); on QLinearConv the fusion only raises qmin
+        if (t != "QLinearConv") p->fused_chain.push_back(c);
         // a skipped step forwards its input buffer (src/nnr.cpp:914-918)
         if (!c->outputs.empty()) c->outputs[0]->alias_of = matched;
         fused++;
@@ -806,7 +809,7 @@ void fuse_attention(context_t* ctx) {
         if (!v) continue;
         std::vector<int64_t> merged = shape_of(rc);
         if (merged != std::vector<int64_t>{shape[0], shape[1], shape[2] * shape[3]}) continue;
-        operator_t* f = solve_operator("MultiHeadAttention", sm->opset, ctx->preferred_backend);
+        operator_t* f = solve_operator("MultiHeadAttention", sm->opset, ctx->attr_pool, ctx->preferred_backend);
         if (!f) continue;
         f->ctx = ctx;
         f->opset = sm->opset;
@@ -821,13 +824,13 @@ void fuse_attention(context_t* ctx) {
         scale.f = c->scalar_f32();
         f->attrs = {{"num_heads", heads}, {"scale", scale}};
         if (!f->init()) {
-            delete f;
+            destroy_op(f);
             continue;
         }
         for (auto* op : eaten) op->skip = true;
         mm1->skip = mul->skip = sm->skip = mm2->skip = tc->skip = true;
         nodes[rc_i] = f;
-        delete rc;
+        destroy_op(rc);
         ++fused;
     }
     ctx->fusion_stats["attention"] = fused;

@@ -318,6 +318,38 @@ MBV2_BLOCKS = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 9
                (6, 160, 3, 2), (6, 320, 1, 1))
 
 
+def hardswish_net(batch=2, hw=32, seed=29, num_classes=10):
+    """MobileNetV3-style QDQ graph around fp32 HardSwish. HardSwish is not
+    quant-capable (fuse_qdq.cpp:96-100), so each DQ -> HardSwish -> Q between
+    the QLinearConvs runs in fp32: stem 3x3/2 (3 -> 16) -> HardSwish -> 1x1
+    (16 -> 20) -> HardSwish -> depthwise 3x3 (20) -> HardSwish -> fp32
+    GlobalAveragePool -> Flatten -> Gemm -> HardSwish, the last one fused into
+    the Gemm as a post-op (fuse_post_ops.cpp:25-68)."""
+    g = Graph()
+    rng = np.random.default_rng(seed)
+    q = _QDQ(g, rng)
+    g.inputs["input"] = (np.float32, (batch, 3, hw, hw))
+    x_q, x_qp = q.quant("input", F32(1.0 / 255.0), 0, name="input_Q")
+    # 20 channels: element counts that are not multiples of 16, so the
+    # HardSwish tail expression is exercised
+    for i, (cin, cout, k, stride, group) in enumerate(((3, 16, 3, 2, 1), (16, 20, 1, 1, 1),
+                                                       (20, 20, 3, 1, 20))):
+        y, y_qp = q.conv(x_q, x_qp, cin, cout, k, stride=stride, pad=k // 2, relu=False,
+                         name=f"conv{i + 1}", group=group, y_zp=128)
+        h = g.node("HardSwish", [q.dequant(y, y_qp)], name=f"hswish{i + 1}")
+        # HardSwish >= -0.375: a zero point low in the range
+        x_q, x_qp = q.quant(h, q.scale(), 16)
+    f = q.dequant(x_q, x_qp, name="head_dq")
+    p = g.node("GlobalAveragePool", [f], name="gap")
+    fl = g.node("Flatten", [p], name="flatten", axis=1)
+    fw = g.init("fc_w", rng.normal(0.0, 1.0, (num_classes, 20)).astype(F32))
+    fb = g.init("fc_b", rng.normal(0.0, 0.5, num_classes).astype(F32))
+    fc = g.node("Gemm", [fl, fw, fb], name="fc", transB=1)
+    g.node("HardSwish", [fc], outputs="logits", name="fc_hswish")
+    g.outputs.append("logits")
+    return g
+
+
 def mobilenetv2(batch=256, hw=224, seed=4, num_classes=1000):
     """MobileNetV2 int8 QDQ: stem 3x3/2 (3->32), 17 inverted-residual blocks
     (1x1 expand, 3x3 depthwise, 1x1 linear project; residual add when the

@@ -82,6 +82,13 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
         elif op == "Gelu":
             x = val(ins[0]).astype(np.float64)
             y = (0.5 * x * (1.0 + _erf(x / np.sqrt(2.0)))).astype(np.float32)
+        elif op == "HardSwish":
+            y = O.hardswish(val(ins[0]), post_op=bool(nd.get("post_op")))
+        elif op in ("Relu", "Clip"):
+            lo, hi = (0.0, np.inf) if op == "Relu" else (
+                float(scal(ins[1], -np.inf)) if len(ins) > 1 else -np.inf,
+                float(scal(ins[2], np.inf)) if len(ins) > 2 else np.inf)
+            y = np.minimum(np.maximum(val(ins[0]).astype(np.float32), np.float32(lo)), np.float32(hi))
         elif op == "Transpose":
             perm = graph.node_by_name(nd["name"]).attrs.get("perm")
             y = np.ascontiguousarray(np.transpose(val(ins[0]), perm))
@@ -342,14 +349,23 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
             # one's input; replay them in order from the graph's definitions
             first = graph.node_by_name(chain[0])
             chain_env[first.inputs[0]] = res[nd["outputs"][0]]
+            # an fp32 producer's fused unary (fuse_post_ops) runs in its
+            # post-op form, on the producer's own output buffer
+            post_op = bool(nd.get("post_fn")) and nd["op"] in ("Gemm", "MatMul", "Conv")
             for name in chain:
                 gn = graph.node_by_name(name)
                 cres = exec_node({"op": gn.op, "name": gn.name, "inputs": list(gn.inputs),
-                                  "outputs": list(gn.outputs), "post_fn": 0})
+                                  "outputs": list(gn.outputs), "post_fn": 0, "post_op": post_op})
                 chain_env.update(cres)
-            # the chain's last output is this node's own (a device tensor):
-            # later nodes read it through `source` like any other output
-            res = {nd["outputs"][0]: chain_env.pop(nd["outputs"][0])}
+            last = graph.node_by_name(chain[-1]).outputs[0]
+            if last == nd["outputs"][0]:
+                # the chain's last output is this node's own (a device tensor):
+                # later nodes read it through `source` like any other output
+                res = {nd["outputs"][0]: chain_env.pop(nd["outputs"][0])}
+            else:
+                # a fused post-op: its output is an alias of this node's
+                v = chain_env.pop(last)
+                res = {nd["outputs"][0]: v, last: v}
         env.update(res)
         if stop_after and nd["name"] == stop_after:
             break

@@ -213,6 +213,35 @@ void orc_dequantize_linear(const void* x, int x_dtype, size_t n, float scale,
         y[i] = ((float)ld_q(x, x_dtype, i) - (float)zp) * scale;
 }
 
+/* ---- HardSwish, fp32: src/backend/cpu/HardSwish.cpp:18-50 --------------
+ * exec(): avx512::hardswish over the whole tensor (vec_ops_avx512.h:96-117):
+ * 16-wide body t = min_ps(max_ps(fl(fl(x * fl(1/6)) + 0.5), 0), 1) -- the
+ * AVX-512 max / min return the second operand unless the first compares
+ * greater / smaller --, scalar tail t = std::max(0, std::min(1, fl(fl(x / 6)
+ * + 0.5))), y = fl(x * t). post_op: the fused form (apply_inplace with no
+ * bias -> bias_hardswish(row, n, 0), vec_ops_avx512.h:74-94), which adds the
+ * zero bias first. */
+void orc_hardswish_f32(const float* x, float* y, size_t n, int post_op) {
+    const size_t body = n - n % 16;
+    for (size_t i = 0; i < n; i++) {
+        float v = x[i];
+        if (post_op) v = v + 0.0f;
+        float t;
+        if (i < body) {
+            float u = v * (1.0f / 6.0f);
+            u = u + 0.5f;
+            float m = u > 0.0f ? u : 0.0f;
+            t = m < 1.0f ? m : 1.0f;
+        } else {
+            float w = v / 6.0f;
+            w = w + 0.5f;
+            float m = (w < 1.0f) ? w : 1.0f;   /* std::min(1.0f, w) */
+            t = (0.0f < m) ? m : 0.0f;         /* std::max(0.0f, m) */
+        }
+        y[i] = v * t;
+    }
+}
+
 /* ---- DynamicQuantizeLinear: DynamicQuantizeLinear.cpp:27-58 ------------ */
 void orc_dynamic_quantize_linear(const float* x, size_t n, uint8_t* y,
                                  float* y_scale, uint8_t* y_zp) {

@@ -55,6 +55,8 @@ enum orc_dtype { ORC_U8 = 0, ORC_S8 = 1, ORC_I32 = 2, ORC_F32 = 3, ORC_F16 = 4 }
 void orc_quantize_linear(const float* x, size_t n, float scale, int zp,
                          int y_dtype, void* y);
 /* ---- DequantizeLinear (per-tensor) ----------------------------------- */
+/* HardSwish fp32 (HardSwish.cpp:18-50); post_op: fused form (zero bias added) */
+void orc_hardswish_f32(const float* x, float* y, size_t n, int post_op);
 void orc_dequantize_linear(const void* x, int x_dtype, size_t n, float scale,
                            int zp, float* y);
 /* ---- DynamicQuantizeLinear ------------------------------------------- */

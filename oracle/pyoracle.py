@@ -56,6 +56,7 @@ def lib():
             "orc_rq_d": (i, [ct.c_int32, f, i, i, i]),
             "orc_quantize_linear": (None, [vp, sz, f, i, i, vp]),
             "orc_dequantize_linear": (None, [vp, i, sz, f, i, vp]),
+            "orc_hardswish_f32": (None, [vp, vp, sz, i]),
             "orc_dynamic_quantize_linear": (None, [vp, sz, vp, vp, vp]),
             "orc_qlinear_matmul": (i, [i, i, i, i, vp, i, i, vp, vp, vp, i, i, vp, vp, vp, vp,
                                        i, vp, i]),
@@ -115,6 +116,14 @@ def dequantize_linear(x, scale, zp):
     x = np.ascontiguousarray(x)
     y = np.empty(x.shape, dtype=np.float32)
     lib().orc_dequantize_linear(_p(x), dt_of(x), x.size, float(scale), int(zp), _p(y))
+    return y
+
+
+def hardswish(x, post_op=False):
+    """fp32 HardSwish with the reference's body / tail split over x's flat order."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.float32)
+    lib().orc_hardswish_f32(_p(x), _p(y), x.size, 1 if post_op else 0)
     return y
 
 

@@ -203,6 +203,23 @@ def test_bert_per_node(dev, fused):
     assert n_int >= 8 * 2 and n_f32 >= 12
 
 
+def test_bert_full_depth_seq128(dev):
+    """cfg5 at its real per-sequence shape: 12 layers, seq 128, hidden 768,
+    12 heads, FFN 3072 (batch 2 of the config's 64: the batch only repeats
+    the same per-sequence work). Every node recomputed by the oracle from the
+    device's own inputs: int8 outputs (DynamicQuantizeLinear bytes and zero
+    points) exact, fp32 outputs within 1e-3. Seq 128 takes the fused
+    head-64 attention kernel."""
+    g = synth.bert(batch=2, seq=128, layers=12)
+    rng = np.random.default_rng(35)
+    x = rng.uniform(-1.0, 1.0, (2, 128, 768)).astype(np.float32)
+    plan, n_int, n_f32 = check_graph_per_node(g, {"input": x})
+    ops = [p["op"] for p in plan]
+    assert ops.count("QLinearMatMul") == 72 and ops.count("MultiHeadAttention") == 12
+    assert ops.count("DynamicQuantizeLinear") == 48
+    assert n_int >= 48 * 2 and n_f32 >= 72
+
+
 @pytest.mark.parametrize("name", ["resnet50", "mobilenetv2", "bert", "qoperator", "concat_b1", "concat_b2"])
 def test_memory_planning(dev, name):
     """The device memory planner (shared arena slots, in-place outputs,
@@ -309,3 +326,30 @@ def test_bn_f32_unfolded(dev, shape):
     x = rng.normal(0, 2, shape).astype(np.float32)
     plan, out, _ = check_graph(g, {"input": x}, y)
     assert [p["variant"] for p in plan] == [""] and out.dtype == np.float32
+
+
+@pytest.mark.parametrize("hw", [32, 29])
+def test_hardswish_graph(dev, hw):
+    """MobileNetV3-style QDQ graph: each DQ -> HardSwish -> Q between the
+    QLinearConvs runs the fp32 HardSwish operator, and the classifier's
+    HardSwish runs fused into the fp32 Gemm. Every int8 tensor is bit-exact
+    and fp32 values are within 1e-3 of the oracle's replay; each standalone
+    HardSwish output also equals the oracle's HardSwish of the device's own
+    input bit for bit (the same IEEE operations and body / tail split)."""
+    from oracle import pyoracle as O
+    g = synth.hardswish_net(batch=3, hw=hw)
+    rng = np.random.default_rng(34)
+    x = rng.random((3, 3, hw, hw), dtype=np.float32)
+    plan, logits, n_int = check_graph(g, {"input": x}, "logits")
+    assert [p["op"] for p in plan].count("HardSwish") == 3 and n_int >= 6
+    assert logits.shape == (3, 10) and np.isfinite(logits).all()
+    s = G.Session(g)
+    s.set_input("input", x)
+    s.run()
+    tails = 0
+    for p in plan:
+        if p["op"] == "HardSwish":
+            xin = s.output(p["inputs"][0])[0]
+            assert np.array_equal(s.output(p["outputs"][0])[0], O.hardswish(xin)), p["name"]
+            tails += xin.size % 16 != 0
+    assert tails >= (1 if hw == 29 else 0)   # 15x15 maps of 20 channels: n % 16 != 0

@@ -158,3 +158,23 @@ def test_fold_bn_qdq_patterns():
     assert "QuantizeLinear" not in [p["op"] for p in plan if p["name"] != "input_Q"]
     assert s.fusion_stat("bn_qdq") == 1 and s.fusion_stat("bn_q") == 1
     assert s.tensor_info("bn_a_q_out")[3] == 1      # NHWC after the convolution
+
+
+def test_hardswish_graph_plan():
+    """DQ -> HardSwish -> Q stays in fp32 between the QLinearConvs (HardSwish
+    is not quant-capable, fuse_qdq.cpp:96-100), and the classifier's
+    HardSwish is fused into the fp32 Gemm as a post-op
+    (fuse_post_ops.cpp:25-68), recorded as the Gemm's fused chain."""
+    g = synth.hardswish_net(batch=2, hw=32)
+    s = G.Session(g, device=False)
+    plan = s.plan()
+    ops = collections.Counter(p["op"] for p in plan)
+    assert ops["QLinearConv"] == 3 and ops["HardSwish"] == 3 and ops["Gemm"] == 1
+    assert s.fusion_stat("qdq_compute") == 3
+    assert [p["variant"] for p in plan if p["op"] == "QLinearConv"] == ["FIRST", "PACKED", "DW"]
+    gemm = next(p for p in plan if p["op"] == "Gemm")
+    assert gemm["post_fn"] == 1 and gemm["fused_chain"] == ["fc_hswish"]
+    for p in plan:
+        if p["op"] == "HardSwish":
+            prev = next(q for q in plan if p["inputs"][0] in q["outputs"])
+            assert prev["op"] == "DequantizeLinear"

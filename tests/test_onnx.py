@@ -205,3 +205,50 @@ def test_protobuf_serialized_model_loads(name):
     for k in g.outputs:
         m.graph.output.add(name=k)
     same_context(g, G.Session(None, device=False, onnx=m.SerializeToString()))
+
+
+@pytest.mark.parametrize("dims", [[65536] * 4, [2**31 - 1] * 3, [2**31 - 1, 2**31 - 1]])
+def test_oversized_initializer_dims_fail_cleanly(dims):
+    """Dimensions whose element count wraps size_t ([65536]*4 is 2^64, which
+    an unchecked product makes 0) or needs more host memory than any model
+    holds are a load error with a message, never a crash or an exception
+    escaping the C ABI."""
+    P = _protobuf_classes()
+    m = P["ModelProto"](ir_version=8)
+    m.opset_import.add(domain="", version=13)
+    m.graph.initializer.add(name="w", dims=dims, data_type=2, raw_data=b"\x01" * 16)
+    m.graph.output.add(name="w")
+    with pytest.raises(G.NnrError, match="too large"):
+        G.Session(None, device=False, onnx=m.SerializeToString())
+
+
+def test_element_types_use_reference_numbering():
+    """The host C ABI takes and returns the reference's data_type_t codes
+    (src/nnr.h:20-56: FLOAT32 1, INT8 5, INT32 7, INT64 8, UINT8 9); a model
+    file's TensorProto codes (FLOAT 1, UINT8 2, INT8 3, INT32 6) are
+    translated by the loader."""
+    assert G.NNR_DT == {np.dtype(np.float32): 1, np.dtype(np.float16): 3, np.dtype(np.int8): 5,
+                        np.dtype(np.int32): 7, np.dtype(np.int64): 8, np.dtype(np.uint8): 9}
+    g = GRAPHS["qoperator"]()
+    model, _ = onnx_io.encode(g)
+    s = G.Session(None, device=False, onnx=model)
+    for name, arr in g.initializers.items():
+        assert s.tensor_info(name)[1] == arr.dtype, name
+    for name, (dt, _) in g.inputs.items():
+        assert s.tensor_info(name)[1] == np.dtype(dt), name
+
+
+def test_bad_element_type_code_rejected():
+    L = G.host_lib()
+    import ctypes as C
+    h = C.c_void_p()
+    G._chk(L.nnr_ctx_create(C.byref(h), 4))
+    try:
+        dims = (C.c_int * 1)(4)
+        data = (C.c_uint8 * 4)()
+        for code in (0, 200, -1):
+            assert L.nnr_ctx_add_initializer(h, b"t", code, dims, 1, data) != 0
+            assert b"data_type_t" in L.nnr_last_error()
+        assert L.nnr_ctx_add_initializer(h, b"t", 9, dims, 1, data) == 0
+    finally:
+        L.nnr_ctx_destroy(h)

@@ -675,3 +675,71 @@ def test_folded_bn_half_below_zero():
     A = np.ones(C, np.float32)
     assert np.all(O.batchnorm_u8(x, A, np.full(C, -0.5, np.float32), nhwc=1) == 0)
     assert np.all(O.batchnorm_u8(x, A, np.full(C, -0.51, np.float32), nhwc=1) == 255)
+
+
+# ---------------------------------------------------------------------------
+# HardSwish, fp32 (HardSwish.cpp:18-50, vec_ops_avx512.h:74-117)
+
+def _hs_exact(x, body):
+    """HardSwish by exact rational arithmetic, one RNE rounding per IEEE
+    operation: body fl(fl(x * fl(1/6)) + 1/2), tail fl(fl(x / 6) + 1/2), each
+    clamped to [0, 1], times x."""
+    X = Fraction(float(x))
+    if body:
+        u = rne_f32(Fraction(float(rne_f32(X * Fraction(float(rne_f32(Fraction(1, 6))))))) + Fraction(1, 2))
+    else:
+        u = rne_f32(Fraction(float(rne_f32(X / 6))) + Fraction(1, 2))
+    t = min(max(Fraction(float(u)), Fraction(0)), Fraction(1))
+    return rne_f32(X * t)
+
+
+def test_hardswish_closed_forms():
+    """x >= 3 passes through, x <= -3 gives (negative) zero, 0 stays 0, at
+    body (first n - n % 16) and tail positions alike; NaN and -inf give NaN
+    (-inf * 0), +inf stays +inf."""
+    vals = np.array([3, 4.5, 100, 1e30, -3, -4, -1e30, 0.0, np.inf, -np.inf, np.nan], np.float32)
+    x = np.concatenate([vals, np.zeros(16 - len(vals) % 16, np.float32), vals])   # body copy, tail copy
+    y = O.hardswish(x)
+    n_t = len(vals)
+    for part in (y[:n_t], y[-n_t:]):
+        assert np.array_equal(part[:4], vals[:4])
+        assert np.all(part[4:7] == 0) and np.all(np.signbit(part[4:7]))
+        assert part[7] == 0 and part[8] == np.inf
+        assert np.isnan(part[9]) and np.isnan(part[10])
+
+
+def test_hardswish_matches_float64_within_ulps():
+    rng = np.random.default_rng(5)
+    x = rng.uniform(-4, 4, 1003).astype(np.float32)
+    y = O.hardswish(x).astype(np.float64)
+    x64 = x.astype(np.float64)
+    ref = x64 * np.clip(x64 / 6 + 0.5, 0, 1)
+    # t = x/6 + 1/2 carries an absolute error of about one ulp of 1/2 (it
+    # cancels near x = -3), which x then scales
+    tol = 4 * np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64) + np.abs(x64) * 2.0 ** -23
+    assert np.all(np.abs(y - ref) <= tol)
+
+
+def test_hardswish_body_and_tail_known_answers():
+    """Values where multiplying by fl(1/6) (the 16-wide body) and dividing by
+    6 (the scalar tail) round differently: the oracle must give each
+    position its own expression, as exact rational arithmetic does."""
+    cand = np.linspace(-2.99, 2.99, 4001).astype(np.float32)
+    diff = [v for v in cand if _hs_exact(v, True) != _hs_exact(v, False)]
+    assert len(diff) > 5
+    for v in diff[:: max(1, len(diff) // 20)]:
+        x = np.full(17, v, np.float32)           # 16 body elements, 1 tail element
+        y = O.hardswish(x)
+        assert y[0] == _hs_exact(v, True) and y[15] == _hs_exact(v, True)
+        assert y[16] == _hs_exact(v, False) and y[16] != y[0]
+
+
+def test_hardswish_post_op_adds_zero_bias():
+    """The fused form adds the zero bias of bias_hardswish: -0.0 becomes +0.0
+    (and stays -0.0 * 0.5 = -0.0 in the standalone operator)."""
+    x = np.full(20, -0.0, np.float32)
+    assert np.all(np.signbit(O.hardswish(x)))
+    assert not np.any(np.signbit(O.hardswish(x, post_op=True)))
+    rng = np.random.default_rng(1)
+    x = rng.uniform(-4, 4, 100).astype(np.float32)
+    assert np.array_equal(O.hardswish(x), O.hardswish(x, post_op=True))
