@@ -17,9 +17,12 @@ Prints ONE JSON line (driver contract). Workloads:
 A step is one pass of the path over one batch; inputs are resident in HBM
 when the timed region starts. Before timing, the GPU output is checked
 bit-exact against the CPU oracle. The `roofline` object is measured live
-with hipEvents around every launch of the dominant kernel (the library's
-launch profiler); the `cpu_baseline` leg times the oracle on host cores on a
-bounded sample of the same workload.
+with hipEvents on the launch stream: every node of the plan is run back to
+back between two events (no event between launches, so short kernels are not
+inflated), and the dominant kernel family's average launch is placed under
+the roof its own algorithmic ops / bytes put it (MFMA or HBM), with each
+layer's roofline fraction beside it; the `cpu_baseline` leg times a CPU
+restatement on host cores on a bounded sample of the same workload.
 """
 from __future__ import annotations
 
@@ -79,7 +82,8 @@ def run_qconv(args, dev):
     ms = time_steps(lambda: op(xd, yd), args)
     prof = profile_steps(lambda: op(xd, yd), args)
     g_launches, g_ms = prof["qgemm"]
-    kern_ms = g_ms / g_launches
+    assert g_launches == args.steps   # one kernel launch per step
+    kern_ms = ms                      # back-to-back steps: the kernel's own duration
     # cpu baseline: the oracle on a bounded sample (4 of the 32 images)
     nthr = host_threads()
     O.set_threads(nthr)
@@ -131,6 +135,7 @@ def run_qmatmul(args, dev):
     ms = time_steps(lambda: op(ad, yd), args)
     prof = profile_steps(lambda: op(ad, yd), args)
     g_launches, g_ms = prof["qgemm"]
+    assert g_launches == args.steps   # one kernel launch per step: its duration is ms
     ops = 2.0 * M * N * K
     nbytes = M * K + K * N + M * N
     # cpu baseline: the oracle on 128 of the 1024 rows
@@ -148,7 +153,7 @@ def run_qmatmul(args, dev):
         metric=METRIC, value=round(ops / (ms * 1e-3) / 1e12, 3), unit="TOPS", ms_per_step=ms,
         config={"workload": "cfg1 QLinearMatMul A u8[1024,768] x B i8[768,3072] -> u8 (RQ-D)",
                 "global_batch": M},
-        roofline=roofline(ops, nbytes, g_ms / g_launches, prof),
+        roofline=roofline(ops, nbytes, ms, prof),
         cpu_baseline={"value": round(ops / 8 / cpu_s / 1e12, 4), "unit": "TOPS", "cores": nthr,
                       "kind": "port", "sample": f"oracle on 128 of 1024 rows, {reps} runs"},
         dtype="u8",
@@ -200,18 +205,92 @@ def profile_steps(fn, args) -> dict:
     return out
 
 
-def roofline(ops, nbytes, kern_ms, prof):
+def roofline(ops, nbytes, kern_ms, prof, kernel="qgemm_dma_kernel"):
+    """Roofline object of the dominant kernel: one average launch does `ops`
+    algorithmic int8 ops and moves `nbytes` algorithmic bytes in `kern_ms`.
+    `bound` is the roof its own model puts it under -- MFMA when ops / peak
+    exceeds bytes / HBM peak, else HBM -- and `achieved` / `frac` are on that
+    roof; the other roof's fraction is reported beside it."""
     t_mfma = ops / (PEAK_I8_TOPS * 1e12)
     t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
-    achieved_tops = ops / (kern_ms * 1e-3) / 1e12
-    r = {"kernel": "qgemm_kernel", "bound": "mfma", "achieved": round(achieved_tops, 2),
-         "peak": PEAK_I8_TOPS, "unit": "TOPS", "frac": round(achieved_tops / PEAK_I8_TOPS, 4),
+    tops = ops / (kern_ms * 1e-3) / 1e12
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    bound = "mfma" if t_mfma >= t_hbm else "hbm"
+    r = {"kernel": kernel, "bound": bound,
+         "achieved": round(tops if bound == "mfma" else gbs, 2),
+         "peak": PEAK_I8_TOPS if bound == "mfma" else PEAK_HBM_GBS,
+         "unit": "TOPS" if bound == "mfma" else "GB/s",
+         "frac": round((tops / PEAK_I8_TOPS) if bound == "mfma" else (gbs / PEAK_HBM_GBS), 4),
          "traffic": None, "avg_launch_ms": round(kern_ms, 5),
          "alg_ops_per_launch": ops, "alg_bytes_per_launch": nbytes,
-         "bound_model": "mfma" if t_mfma >= t_hbm else "hbm",
+         "mfma": {"achieved_tops": round(tops, 1), "frac": round(tops / PEAK_I8_TOPS, 4)},
+         "hbm": {"achieved_gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)},
          "launches": {k: {"n": v[0], "avg_ms": round(v[1] / max(1, v[0]), 5)}
                       for k, v in prof.items()}}
     return r
+
+
+def node_rows(s, args, reps=10):
+    """Per-node rows of the executed plan: device time of each node run
+    `reps` times back to back (no event between launches), its algorithmic
+    ops and bytes, and the roofline each is under: t_roof = max(ops / i8
+    peak, bytes / HBM peak), roof_frac = t_roof / measured."""
+    from nnr_amd import _lib
+    rows = []
+    prof = s.profile()
+    for i, p in enumerate(prof):
+        # kernel launches of this node (one run under the launch profiler)
+        _lib.profile_reset()
+        _lib.profile_enable(True)
+        s.time_node(i, 1)
+        _lib.profile_enable(False)
+        launches = sum(v[0] for v in _lib.profile_read().values())
+        _lib.profile_reset()
+        t = s.time_node(i, reps)
+        t_mfma = p["ops"] / (PEAK_I8_TOPS * 1e12) * 1e3
+        t_hbm = p["bytes"] / (PEAK_HBM_GBS * 1e9) * 1e3
+        rows.append(dict(name=p["name"], op=p["op"], variant=p["variant"], ms=t, ops=p["ops"], launches=launches,
+                         bytes=p["bytes"], t_roof_ms=max(t_mfma, t_hbm),
+                         bound="mfma" if t_mfma >= t_hbm and p["ops"] else "hbm"))
+    return rows
+
+
+def family_roofline(rows, select, kprof, extra_ms=0.0, extra_launches=0, kernel="qgemm_dma_kernel"):
+    """Roofline of a kernel family over one step: the selected nodes (one
+    launch of the family each; `extra_ms` of other kernels inside them is
+    taken out), plus the per-layer aggregate sum(t_roof) / sum(measured)."""
+    sel = [r for r in rows if select(r)]
+    n = len(sel) + extra_launches
+    fam_ms = sum(r["ms"] for r in sel) - extra_ms
+    ops = sum(r["ops"] for r in sel)
+    nbytes = sum(r["bytes"] for r in sel)
+    rl = roofline(ops / n, nbytes / n, fam_ms / n, kprof, kernel=kernel)
+    rl["per_layer"] = {"roof_ms": round(sum(r["t_roof_ms"] for r in sel), 4),
+                       "measured_ms": round(sum(r["ms"] for r in sel), 4),
+                       "roofline_time_frac": round(sum(r["t_roof_ms"] for r in sel) /
+                                                   max(1e-9, sum(r["ms"] for r in sel)), 4),
+                       "layers_mfma_bound": sum(1 for r in sel if r["bound"] == "mfma"),
+                       "layers_hbm_bound": sum(1 for r in sel if r["bound"] == "hbm")}
+    return rl, fam_ms
+
+
+def measured_counters(name):
+    """MFMA / LDS counter figures of the dominant kernel from a rocprofv3
+    --pmc summary under profiles/ (lines `key: value`), or None."""
+    import re
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        txt = open(path).read()
+    except OSError:
+        return None
+    out = {}
+    for k in ("mfma_util_pct", "mfma_i8_ops_executed_per_step", "lds_bank_conflict_pct", "lds_util_pct"):
+        m = re.search(r"^%s: ([0-9.eE+-]+)$" % k, txt, re.M)
+        if m:
+            out[k] = float(m.group(1))
+    if out:
+        out["source"] = "profiles/" + name
+    return out or None
 
 
 def planned_session(args, g, feeds, ref):
@@ -261,20 +340,23 @@ def planned_session(args, g, feeds, ref):
     return s, mem
 
 
-def layer_table(prof, args) -> list:
-    """Per-layer rows (hipEvents around every node): TOPS and % of the i8
+def layer_table(rows, args) -> list:
+    """Per-layer rows (each node timed back to back): TOPS and % of the i8
     MFMA peak for operators with algorithmic ops, GB/s and % of HBM peak for
-    the others; to stderr and optionally to --layers-out."""
+    all, and the fraction of its own roofline (max of the two times); to
+    stderr and optionally to --layers-out."""
     layers = []
-    for r in prof:
-        t = r["ms"] / max(1, r["runs"])
-        row = {"name": r["name"], "op": r["op"], "branch": r["variant"], "ms": round(t, 4)}
+    for r in rows:
+        t = r["ms"]
+        row = {"name": r["name"], "op": r["op"], "branch": r["variant"], "ms": round(t, 4),
+               "launches": r["launches"]}
         if r["ops"]:
             row["tops"] = round(r["ops"] / (t * 1e-3) / 1e12, 1)
             row["pct_i8_peak"] = round(100 * row["tops"] / PEAK_I8_TOPS, 2)
-        else:
-            row["gbs"] = round(r["bytes"] / (t * 1e-3) / 1e9, 1)
-            row["pct_hbm"] = round(100 * row["gbs"] / PEAK_HBM_GBS, 2)
+        row["gbs"] = round(r["bytes"] / (t * 1e-3) / 1e9, 1)
+        row["pct_hbm"] = round(100 * row["gbs"] / PEAK_HBM_GBS, 2)
+        row["bound"] = r["bound"]
+        row["pct_roofline"] = round(100 * r["t_roof_ms"] / t, 1)
         layers.append(row)
     if args.layers_out:
         with open(args.layers_out, "w") as f:
@@ -322,42 +404,47 @@ def run_model(args, dev, model):
             assert np.allclose(dev_t[:ng], env[o], atol=1e-3, rtol=1e-4), p["name"]
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
-    # per-layer times (hipEvents around every node) and per-kernel times
-    s.enable_profiling(True)
-    for _ in range(args.steps):
-        s.run()
-    torch.cuda.synchronize()
-    prof = s.profile()
-    s.enable_profiling(False)
+    # per-kernel launch times (an event pair around every launch) and
+    # per-node times (each node run back to back, no event between launches)
     kprof = profile_steps(s.run, args)
-    conv_ops = sum(r["ops"] for r in prof if r["op"] == "QLinearConv")
-    # the conv GEMM kernel, with or without a fused residual add
-    g_launches = sum(kprof[k][0] for k in ("qgemm", "qgemm_add") if k in kprof)
-    g_ms = sum(kprof[k][1] for k in ("qgemm", "qgemm_add") if k in kprof)
-    qgemm_ms_per_step = g_ms / args.steps
-    layer_table(prof, args)
-    # roofline of the dominant kernel over all its launches in a step
-    avg_launch = qgemm_ms_per_step / (g_launches / args.steps)
-    ops_per_launch = conv_ops / (g_launches / args.steps)
-    conv_bytes = sum(r["bytes"] for r in prof if r["op"] == "QLinearConv")
-    rl = roofline(ops_per_launch, conv_bytes / (g_launches / args.steps), avg_launch, kprof)
+    rows = node_rows(s, args)
+    layer_table(rows, args)
+    conv_ops = sum(r["ops"] for r in rows if r["op"] == "QLinearConv")
+    # the conv GEMM kernel, with or without a fused residual add: one launch
+    # per QLinearConv node; the first layer's node also runs its input
+    # layout kernel, and a conv on channels that are not a multiple of 16 a
+    # channel-padding kernel (timed by the launch profiler), taken out here
+    copies_ms = 0.0
+    for k in ("quantize_first_layer_copies", "first_layer_copies", "pad_channels_u8", "nchw_to_nhwc_u8"):
+        if k in kprof:
+            copies_ms += kprof[k][1] / args.steps
+    is_conv = lambda r: r["op"] == "QLinearConv" and r["variant"] != "DW"
+    rl, fam_ms = family_roofline(rows, is_conv, kprof, extra_ms=copies_ms)
+    rl["kernel"] = "qgemm_dma_kernel (conv GEMM family)"
     rl["traffic"], rl["traffic_source"] = measured_traffic(
         f"{model}_b256_conv_gemm_traffic.md" if B == 256 else None)
+    rl["counters"] = measured_counters(f"{model}_b256_conv_gemm_counters.md") if B == 256 else None
+    g_launches = sum(kprof[k][0] for k in ("qgemm", "qgemm_add") if k in kprof)
+    g_ms = sum(kprof[k][1] for k in ("qgemm", "qgemm_add") if k in kprof)
+    rl["event_per_launch_avg_ms"] = round(g_ms / max(1, g_launches), 5)
     n_fused = s.fusion_stat("conv_add")
-    rl["note"] = (f"achieved = total algorithmic conv ops of one step / total time of the conv "
-                  f"GEMM kernels of one step ({round(g_launches / args.steps)} launches, "
-                  f"{n_fused} with the residual add fused; hipEvents per launch)")
+    n_conv = sum(1 for r in rows if is_conv(r))
+    rl["note"] = (f"one average launch of the {n_conv} conv GEMM launches of a step ({n_fused} with the "
+                  "residual add fused): algorithmic ops and bytes / kernel time, each node timed back to "
+                  "back with no event between launches (the first layer's input-layout kernel taken "
+                  "out); bound = the roof its ops / bytes put it under; per_layer = sum of each layer's "
+                  "max(ops / MFMA peak, bytes / HBM peak) over the sum of measured times")
+    qgemm_ms_per_step = fam_ms
     if "depthwise" in kprof:
         # the depthwise convolutions are HBM-bound: their own roofline
-        dw_rows = [r for r in prof if r["op"] == "QLinearConv" and r["variant"] == "DW"]
-        dn, dms = kprof["depthwise"]
+        dw_rows = [r for r in rows if r["op"] == "QLinearConv" and r["variant"] == "DW"]
+        dw_ms = sum(r["ms"] for r in dw_rows)
         dw_bytes = sum(r["bytes"] for r in dw_rows)
-        dw_gbs = dw_bytes / (dms / args.steps * 1e-3) / 1e9
+        dw_gbs = dw_bytes / (dw_ms * 1e-3) / 1e9
         rl["depthwise"] = {"bound": "hbm", "achieved": round(dw_gbs, 1), "peak": PEAK_HBM_GBS,
                            "unit": "GB/s", "frac": round(dw_gbs / PEAK_HBM_GBS, 4),
-                           "launches_per_step": round(dn / args.steps),
-                           "alg_bytes_per_step": dw_bytes,
-                           "avg_launch_ms": round(dms / dn, 5)}
+                           "launches_per_step": len(dw_rows), "alg_bytes_per_step": dw_bytes,
+                           "avg_launch_ms": round(dw_ms / max(1, len(dw_rows)), 5)}
     # cpu baseline: the oracle replays the plan on one image
     nthr = host_threads()
     O.set_threads(nthr)
@@ -377,7 +464,8 @@ def run_model(args, dev, model):
                 "branches": {b: sum(1 for p in plan if p["variant"].split("+")[0] == b)
                              for b in ("FIRST", "DW", "NR16", "PACKED")},
                 "adds_fused_into_conv": s.fusion_stat("conv_add"),
-                "conv_tops": round(conv_ops / (qgemm_ms_per_step * 1e-3) / 1e12, 1),
+                "conv_gemm_tops": round(sum(r["ops"] for r in rows if is_conv(r)) /
+                                        (qgemm_ms_per_step * 1e-3) / 1e12, 1),
                 "memory": mem},
         roofline=rl,
         cpu_baseline={"value": round(cpu_img_s, 3), "unit": "images/s", "cores": nthr,
@@ -398,7 +486,9 @@ def run_bert(args, dev):
 
     B = 64 if args.batch == 256 else args.batch
     S, L = 128, 12
-    g = synth.bert(batch=B, seq=S, layers=L)
+    pc = bool(args.per_channel)
+    g = synth.bert(batch=B, seq=S, layers=L, per_channel=pc)
+    proj = "MatMulInteger" if pc else "QLinearMatMul"
     rng = np.random.default_rng(20)
     x = rng.uniform(-1.0, 1.0, (B, S, 768)).astype(np.float32)
     s = G.Session(g)
@@ -407,7 +497,8 @@ def run_bert(args, dev):
     torch.cuda.synchronize()
     plan = s.plan()
     fmt = lambda n: s.tensor_info(n)[3]
-    # parity gate: every QLinearMatMul of the first layer, recomputed by the
+    # parity gate: every projection (QLinearMatMul, or MatMulInteger with its
+    # fused Cast / scale / bias chain) of the first layer, recomputed by the
     # oracle from the device's own inputs (dynamic scale / zero point
     # included) on the first two sequences
     ng = 2
@@ -416,12 +507,12 @@ def run_bert(args, dev):
         t, _ = s.output(name)
         return t[:ng] if t.ndim >= 1 and t.shape[0] == B else t
 
-    skip = {p["op"] for p in plan} - {"QLinearMatMul"}
+    skip = {p["op"] for p in plan} - {proj}
     env = graph_oracle.run_plan(plan, g, {}, fmt, source=dev_slice, skip_ops=skip,
                                 stop_after="l0_ffn2")
     checked = 0
     for p in plan:
-        if p["op"] == "QLinearMatMul" and p["outputs"][0] in env:
+        if p["op"] == proj and p["outputs"][0] in env:
             d, ref = dev_slice(p["outputs"][0]), env[p["outputs"][0]]
             if any(g.node_by_name(c).op == "Gelu" for c in p.get("fused_chain") or []):
                 # erf in float64 against the device's fp32 erff: a few ulps
@@ -432,24 +523,26 @@ def run_bert(args, dev):
     assert checked == 6
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
-    s.enable_profiling(True)
-    for _ in range(args.steps):
-        s.run()
-    torch.cuda.synchronize()
-    prof = s.profile()
-    s.enable_profiling(False)
     kprof = profile_steps(s.run, args)
-    mm_ops = sum(r["ops"] for r in prof if r["op"] == "QLinearMatMul")
-    mm_bytes = sum(r["bytes"] for r in prof if r["op"] == "QLinearMatMul")
+    rows = node_rows(s, args)
+    layer_table(rows, args)
+    is_mm = lambda r: r["op"] == proj
+    # the members of a grouped Q / K / V launch run inside their leader's
+    # launch: their work counts, their (empty) launches do not
+    grouped = sum(1 for r in rows if is_mm(r) and r["variant"].endswith("(grouped)"))
+    rl, mm_ms = family_roofline(rows, is_mm, kprof, extra_launches=-grouped)
+    mm_ops = sum(r["ops"] for r in rows if is_mm(r))
+    rl["kernel"] = f"qgemm_dma_kernel ({proj} family)"
+    tag = "bert_b64_s128_pc" if pc else "bert_b64_s128"
+    rl["traffic"], rl["traffic_source"] = measured_traffic(f"{tag}_matmul_traffic.md" if B == 64 else None)
+    rl["counters"] = measured_counters(f"{tag}_matmul_counters.md") if B == 64 else None
     g_launches, g_ms = kprof["qgemm"]
-    per_step = g_launches / args.steps
-    layer_table(prof, args)
-    rl = roofline(mm_ops / per_step, mm_bytes / per_step, g_ms / g_launches, kprof)
-    rl["traffic"], rl["traffic_source"] = None, None
-    rl["note"] = (f"achieved = algorithmic int8 ops of the {round(per_step)} QLinearMatMul launches of "
-                  "one step / their total kernel time (hipEvents per launch)")
+    rl["event_per_launch_avg_ms"] = round(g_ms / max(1, g_launches), 5)
+    rl["note"] = (f"one average launch of the {round(g_launches / args.steps)} {proj} launches of one "
+                  "step: algorithmic ops and bytes / kernel time, each node timed back to back with no "
+                  "event between launches")
     # cpu baseline: the oracle replays a batch-1 copy of the same graph
-    g1 = synth.bert(batch=1, seq=S, layers=L)
+    g1 = synth.bert(batch=1, seq=S, layers=L, per_channel=pc)
     plan1 = G.Session(g1, device=False).plan()
     nthr = host_threads()
     O.set_threads(nthr)
@@ -465,10 +558,12 @@ def run_bert(args, dev):
         metric="BERT-base int8 encoder sequences/sec (12 layers, B64, S128), 1 GPU",
         value=round(B / (ms * 1e-3), 1), unit="sequences/s", ms_per_step=ms,
         config={"workload": f"cfg5 BERT-base int8, 12 layers, hidden 768, 12 heads, FFN 3072, "
-                            f"seq {S}, batch {B} (72 QLinearMatMul on DynamicQuantizeLinear "
-                            "activations; fp32 attention, Softmax, LayerNorm, Gelu)",
-                "global_batch": B, "seq_len": S,
-                "int8_tops": round(mm_ops / (g_ms / args.steps * 1e-3) / 1e12, 1), "memory": mem},
+                            f"seq {S}, batch {B} (72 projections on DynamicQuantizeLinear activations, "
+                            + ("per-channel int8 weights: MatMulInteger -> Cast -> Mul(x_scale * w_scale[N]) "
+                               "-> Add" if pc else "per-tensor int8 weights: QLinearMatMul") +
+                            "; fp32 attention, Softmax, LayerNorm, Gelu)",
+                "global_batch": B, "seq_len": S, "weights": "per-channel" if pc else "per-tensor",
+                "int8_tops": round(mm_ops / (mm_ms * 1e-3) / 1e12, 1), "memory": mem},
         roofline=rl,
         cpu_baseline={"value": round(cpu_seq_s, 3), "unit": "sequences/s", "cores": nthr,
                       "kind": "port", "sample": f"oracle replay of the fused plan on 1 sequence, "
@@ -533,20 +628,17 @@ def run_qoperator(args, dev, graph="qoperator"):
             assert np.allclose(dev_t[:ng], env[o], atol=1e-3, rtol=1e-4), p["name"]
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
-    s.enable_profiling(True)
-    for _ in range(args.steps):
-        s.run()
-    torch.cuda.synchronize()
-    prof = s.profile()
-    s.enable_profiling(False)
     kprof = profile_steps(s.run, args)
-    layer_table(prof, args)
+    rows = node_rows(s, args)
+    layer_table(rows, args)
     family = {}
     for op, kern in family_ops.items():
         if kern not in kprof:
             continue
-        n, kms = kprof[kern]
-        nbytes = sum(r["bytes"] for r in prof if r["op"] == op)   # per run = per step
+        n, _ = kprof[kern]
+        sel = [r for r in rows if r["op"] == op]
+        nbytes = sum(r["bytes"] for r in sel)   # per run = per step
+        kms = sum(r["ms"] for r in sel) * args.steps   # back-to-back node times
         gbs = nbytes / (kms / args.steps * 1e-3) / 1e9
         family[kern] = {"op": op, "achieved": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
                         "launches_per_step": round(n / args.steps), "alg_bytes_per_step": nbytes,
@@ -560,7 +652,8 @@ def run_qoperator(args, dev, graph="qoperator"):
           "family": family,
           "launches": {k: {"n": v[0], "avg_ms": round(v[1] / max(1, v[0]), 5)} for k, v in kprof.items()},
           "note": "achieved = algorithmic bytes (inputs read once + output written) of the operator's "
-                  "launches in one step / their kernel time (hipEvents per launch)"}
+                  "launches in one step / their kernel time (each node timed back to back, no event "
+                  "between launches)"}
     nthr = host_threads()
     O.set_threads(nthr)
     t0 = time.perf_counter()
@@ -691,6 +784,8 @@ def main():
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
     ap.add_argument("--onnx", type=int, default=0, choices=[0, 1],
                     help="graph configs: time the model written as an ONNX file and loaded by the C++ loader")
+    ap.add_argument("--per-channel", type=int, default=0, choices=[0, 1],
+                    help="bert: per-channel weights (DynamicQuantizeLinear -> MatMulInteger -> Cast -> Mul -> Add)")
     ap.add_argument("--memory-planning", type=int, default=1, choices=[0, 1],
                     help="graph configs: time a context whose intermediates share device memory")
     args = ap.parse_args()

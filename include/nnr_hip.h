@@ -232,7 +232,41 @@ int nnrh_matmul_integer_run(nnrh_matmul_integer_t h, const void* a_dev,
                             long long a_batch_stride, const void* b_dev,
                             long long b_batch_stride, int a_zp, int b_zp,
                             int32_t* y_dev, int batch, void* stream);
+/* As nnrh_matmul_integer_run with A's zero point read from device memory
+ * (one byte of A's type, e.g. the zero point DynamicQuantizeLinear wrote),
+ * so the call never waits for the device.                                 */
+int nnrh_matmul_integer_run_dev_zp(nnrh_matmul_integer_t h, const void* a_dev,
+                                   long long a_batch_stride, const void* b_dev,
+                                   long long b_batch_stride, const void* a_zp_dev, int b_zp,
+                                   int32_t* y_dev, int batch, void* stream);
 int nnrh_matmul_integer_destroy(nnrh_matmul_integer_t h);
+
+/* MatMulInteger with a constant B, followed by Cast(to float), Mul by the
+ * per-column scale product fl(a_scale * w_scale[n]) and an fp32 Add of
+ * bias[n]: the per-channel dynamic-quantization pattern
+ * DynamicQuantizeLinear -> MatMulInteger -> Cast -> Mul(Mul(a_scale,
+ * w_scale)) -> Add. No counterpart in the reference, which runs MatMulInteger
+ * (src/backend/cpu/MatMulInteger.cpp:11-150), Cast and the binary Mul / Add
+ * (binary_math.cpp) one by one; the kernel forms
+ *   y = fl(fl(float(acc) * fl(a_scale * w_scale[n])) + bias[n]),
+ * acc = sum_k (a - a_zp)(b - b_zp) exact, so the bits equal theirs. Returns
+ * an nnrh_qmatmul handle: run with nnrh_qmatmul_run (a_scale_dev / a_zp_dev
+ * from DynamicQuantizeLinear replace the desc's a_scale / a_zp), and
+ * nnrh_qmatmul_fuse_gelu, nnrh_qmatmul_minmax_count / _set_minmax_out and
+ * nnrh_qmatmul_group_create (members all of this kind) apply as after
+ * nnrh_qmatmul_fuse_dq_bias. Needs K % 16 == 0 and b_zp = 0 (int8 B) or 128
+ * (uint8 B); NNRH_ERR_UNSUPPORTED otherwise.                                */
+typedef struct nnrh_mmi_scaled_desc {
+    int m, n, k;
+    int a_dtype;                 /* NNRH_U8 / NNRH_S8                          */
+    int b_dtype;                 /* NNRH_U8 / NNRH_S8                          */
+    const void* b_host;          /* [k][n]                                    */
+    int a_zp, b_zp;
+    float a_scale;
+    const float* w_scale_host;   /* [n]                                       */
+    const float* bias_host;      /* [n], or NULL when no Add follows           */
+} nnrh_mmi_scaled_desc;
+int nnrh_matmul_integer_scaled_create(nnrh_qmatmul_t* h, const nnrh_mmi_scaled_desc* d);
 
 /* ---- ConvInteger ----------------------------------------------------------
  * Replaces ConvInteger_operator's 4-D path (src/backend/cpu/ConvInteger.cpp:
@@ -419,6 +453,9 @@ int nnrh_add_layernorm_f32(const float* x_dev, const float* r_dev, const float* 
  * when it runs as a producer's fused post-op (fuse_post_ops.cpp:61-68), which
  * adds the zero bias of bias_hardswish (vec_ops_avx512.h:74-94) first.     */
 int nnrh_hardswish_f32(const float* x_dev, float* y_dev, size_t n, int post_op, void* stream);
+/* Cast to float (src/backend/cpu/Cast.cpp, Cast_array: (float)x) from
+ * NNRH_U8, NNRH_S8 or NNRH_I32 (int32 rounds to nearest, ties to even).    */
+int nnrh_cast_to_f32(const void* x_dev, int x_dtype, float* y_dev, size_t n, void* stream);
 /* Gelu, approximate = "none" (src/backend/cpu/Gelu.cpp:43-47). */
 int nnrh_gelu_f32(const float* x_dev, float* y_dev, size_t n, void* stream);
 /* Transpose (src/backend/cpu/Transpose.cpp): ndim <= 6 input dims and perm. */

@@ -133,6 +133,11 @@ int nnr_ctx_memory_entry(nnr_ctx_t ctx, int i, const char** name, int* first, in
 int nnr_ctx_enable_profiling(nnr_ctx_t ctx, int on);
 int nnr_ctx_profile(nnr_ctx_t ctx, int i, double* total_ms, int* runs, double* ops,
                     double* bytes);
+/* average device time (ms) of active node i (plan order) run `reps` times
+ * back to back between two events on the context's stream: a kernel's
+ * duration without per-launch event overhead (the node's inputs must hold
+ * data, i.e. after one run()) */
+int nnr_ctx_time_node(nnr_ctx_t ctx, int i, int reps, double* ms);
 
 #ifdef __cplusplus
 }

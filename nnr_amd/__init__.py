@@ -17,7 +17,7 @@ from ._lib import (BRANCH_NAMES, F16, F32, I32, NNRH_ERR_UNSUPPORTED, S8, U8, Nn
                    QConvDesc,
                    QMatMulDesc, check, cur_stream, lib, ptr)
 
-__all__ = ["QLinearConv", "QLinearMatMul", "MatMulInteger", "quantize_linear",
+__all__ = ["QLinearConv", "QLinearMatMul", "MatMulIntegerScaled", "MatMulInteger", "quantize_linear",
            "dequantize_linear", "dynamic_quantize_linear", "qlinear_add", "maxpool_u8_nhwc",
            "conv_dispatch", "NnrHipError", "lib"]
 
@@ -213,6 +213,28 @@ class QLinearMatMul:
                 self.h = None
         except Exception:
             pass
+
+
+class MatMulIntegerScaled(QLinearMatMul):
+    """MatMulInteger with constant B followed by Cast -> Mul(fl(a_scale *
+    w_scale[n])) -> Add(bias[n]) in one kernel (float32 output); runs like a
+    fused-dequantize QLinearMatMul (Gelu, min / max pairs, groups)."""
+
+    def __init__(self, b, w_scale, bias=None, *, m, a_scale=1.0, a_zp=0, a_dtype=np.uint8, b_zp=0):
+        b = np.ascontiguousarray(b)
+        k, n = b.shape
+        ws = np.ascontiguousarray(w_scale, np.float32)
+        bi = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self._keep = dict(b=b, ws=ws, bias=bi)
+        from ._lib import MmiScaledDesc
+        self.desc = MmiScaledDesc(m, n, k, _dt(a_dtype), _dt(b.dtype), b.ctypes.data, int(a_zp), int(b_zp),
+                                  float(a_scale), ws.ctypes.data, None if bi is None else bi.ctypes.data)
+        h = ct.c_void_p()
+        check(lib().nnrh_matmul_integer_scaled_create(ct.byref(h), ct.byref(self.desc)))
+        self.h = h
+        self.m, self.n, self.k = m, n, k
+        self.y_dtype = np.dtype(np.float32)
+        self._f32 = True
 
 
 class QLinearMatMulGroup:

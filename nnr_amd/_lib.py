@@ -35,6 +35,7 @@ EXPORTS = [
     "nnrh_batchnorm_u8", "nnrh_batchnorm_f32", "nnrh_qlinear_concat",
     "nnrh_conv_integer_create", "nnrh_conv_integer_run", "nnrh_conv_integer_destroy",
     "nnrh_matmul_integer_create", "nnrh_matmul_integer_run", "nnrh_matmul_integer_destroy",
+    "nnrh_matmul_integer_scaled_create", "nnrh_matmul_integer_run_dev_zp", "nnrh_cast_to_f32",
     "nnrh_quantize_linear", "nnrh_dequantize_linear", "nnrh_dynamic_quantize_workspace",
     "nnrh_dynamic_quantize_linear", "nnrh_dynamic_quantize_linear_noalloc", "nnrh_qlinear_add", "nnrh_maxpool_u8_nhwc",
     "nnrh_nchw_to_nhwc_u8", "nnrh_global_avgpool_f32", "nnrh_gemm_f32", "nnrh_clip_f32",
@@ -74,6 +75,12 @@ class QMatMulDesc(C.Structure):
                                         "scale_dtype")] + [
         (n, C.c_void_p) for n in ("a_scale_host", "a_zp_host", "b_scale_host", "b_zp_host",
                                   "y_scale_host", "y_zp_host", "b_host")]
+
+
+class MmiScaledDesc(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("m", "n", "k", "a_dtype", "b_dtype")] + [
+        ("b_host", C.c_void_p), ("a_zp", C.c_int), ("b_zp", C.c_int), ("a_scale", C.c_float),
+        ("w_scale_host", C.c_void_p), ("bias_host", C.c_void_p)]
 
 
 _lib = None
@@ -138,6 +145,9 @@ def lib():
         "nnrh_matmul_integer_create": (i, [P(vp), i, i, i, i, i, i]),
         "nnrh_matmul_integer_run": (i, [vp, vp, ll, vp, ll, i, i, vp, i, vp]),
         "nnrh_matmul_integer_destroy": (i, [vp]),
+        "nnrh_matmul_integer_scaled_create": (i, [P(vp), P(MmiScaledDesc)]),
+        "nnrh_matmul_integer_run_dev_zp": (i, [vp, vp, ll, vp, ll, vp, i, vp, i, vp]),
+        "nnrh_cast_to_f32": (i, [vp, i, vp, sz, vp]),
         "nnrh_quantize_linear": (i, [vp, sz, f, i, i, vp, vp]),
         "nnrh_dequantize_linear": (i, [vp, i, sz, f, i, vp, vp]),
         "nnrh_dynamic_quantize_workspace": (sz, []),

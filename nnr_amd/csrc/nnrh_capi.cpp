@@ -920,11 +920,12 @@ struct nnrh_qmatmul {
     int32_t* c0 = nullptr;
     int32_t* rowsum = nullptr;
     float* dq_bias = nullptr;   // nnrh_qmatmul_fuse_dq_bias: padded to Np
+    float* colscale = nullptr;  // nnrh_matmul_integer_scaled_create: w_scale, padded to Np
     int rowsum_cap = 0;     // batches the rowsum buffer holds
     int parts_cap = 0;      // nnrh_qmatmul_set_minmax_out: pairs the caller's buffer holds
     int a_zp = 0, b_beta = 0;
     float b_scale = 0.f, y_scale = 0.f;
-    ~nnrh_qmatmul() { dfree(wpack); dfree(colsum); dfree(c0); dfree(rowsum); dfree(dq_bias); }
+    ~nnrh_qmatmul() { dfree(wpack); dfree(colsum); dfree(c0); dfree(rowsum); dfree(dq_bias); dfree(colscale); }
 };
 
 extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc* d) {
@@ -1017,7 +1018,7 @@ extern "C" int nnrh_qmatmul_fuse_dq_bias(nnrh_qmatmul_t h, float dq_scale, int d
     if (!h) return set_err(NNRH_ERR_INVALID, "qmatmul_fuse_dq_bias: NULL handle");
     const GemmArgs& g = h->g;
     // uint8 output only (the kernel's fused path reads the bytes unsigned)
-    if (h->d.scale_dtype != NNRH_F32 || dq_zp != g.y_zp || g.beta != 0 || g.K % 16 || g.lda % 16 ||
+    if (g.epi != EPI_RQD || h->d.scale_dtype != NNRH_F32 || dq_zp != g.y_zp || g.beta != 0 || g.K % 16 || g.lda % 16 ||
         g.y_type != 0 || g.c0_absmax + 16384LL * g.Kp >= 0x7fffffffLL)
         return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_fuse_dq_bias: not available for this QLinearMatMul");
     const int n = h->d.n, Np = g.Np;
@@ -1029,6 +1030,83 @@ extern "C" int nnrh_qmatmul_fuse_dq_bias(nnrh_qmatmul_t h, float dq_scale, int d
     if (rc) return rc;
     h->g.dq_bias = h->dq_bias;
     h->g.dq_scale = dq_scale;
+    return NNRH_OK;
+}
+
+// MatMulInteger with a constant B whose int32 result goes through Cast ->
+// Mul by fl(a_scale * w_scale[n]) -> Add(bias[n]): the per-channel form of
+// dynamic quantization, one GEMM writing fp32.
+extern "C" int nnrh_matmul_integer_scaled_create(nnrh_qmatmul_t* out, const nnrh_mmi_scaled_desc* d) {
+    if (!out || !d) return set_err(NNRH_ERR_INVALID, "matmul_integer_scaled: NULL argument");
+    *out = nullptr;
+    if (d->m <= 0 || d->n <= 0 || d->k <= 0 || !d->b_host || !d->w_scale_host)
+        return set_err(NNRH_ERR_INVALID, "matmul_integer_scaled: bad shape, B or scales");
+    if ((d->a_dtype != NNRH_U8 && d->a_dtype != NNRH_S8) || (d->b_dtype != NNRH_U8 && d->b_dtype != NNRH_S8))
+        return set_err(NNRH_ERR_UNSUPPORTED, "matmul_integer_scaled: dtypes");
+    const bool bu8 = d->b_dtype == NNRH_U8;
+    // the pipelined kernel has no per-row (b zero point) term
+    if (d->b_zp != (bu8 ? 128 : 0))
+        return set_err(NNRH_ERR_UNSUPPORTED, "matmul_integer_scaled: B zero point must be %d", bu8 ? 128 : 0);
+    if (d->k % 16) return set_err(NNRH_ERR_UNSUPPORTED, "matmul_integer_scaled: K %% 16 != 0");
+    nnrh_qmatmul* h = new (std::nothrow) nnrh_qmatmul();
+    if (!h) return set_err(NNRH_ERR_NOMEM, "matmul_integer_scaled: host allocation");
+    auto fail = [&](int code) { delete h; return code; };
+    const int m = d->m, n = d->n, k = d->k;
+    const int Kp = round_up(k, 64), Np = round_up(n, 64);
+    std::vector<int8_t> wp((size_t)Np * Kp, 0);
+    std::vector<int32_t> colsum(Np, 0);
+    const uint8_t* braw = (const uint8_t*)d->b_host;
+    for (int j = 0; j < n; ++j) {
+        int8_t* row = wp.data() + (size_t)packed_row_of_col(j) * Kp;
+        int32_t sum = 0;
+        for (int i = 0; i < k; ++i) {
+            const int8_t v = (int8_t)(braw[(size_t)i * n + j] ^ (bu8 ? 0x80 : 0));
+            row[i] = v;
+            sum += v;
+        }
+        colsum[j] = sum;
+    }
+    const bool au8 = d->a_dtype == NNRH_U8;
+    std::vector<int32_t> c0(Np, 0);
+    for (int j = 0; j < n; ++j)
+        c0[j] = (int32_t)(0u - (uint32_t)(d->a_zp - (au8 ? 128 : 0)) * (uint32_t)colsum[j]);
+    std::vector<float> ws((size_t)Np, 0.0f), b((size_t)Np, 0.0f);
+    std::copy(d->w_scale_host, d->w_scale_host + n, ws.begin());
+    if (d->bias_host) std::copy(d->bias_host, d->bias_host + n, b.begin());
+    int rc;
+    if ((rc = upload(&h->wpack, wp.data(), wp.size()))) return fail(rc);
+    if ((rc = upload(&h->colsum, colsum.data(), colsum.size()))) return fail(rc);
+    if ((rc = upload(&h->c0, c0.data(), c0.size()))) return fail(rc);
+    if ((rc = upload(&h->colscale, ws.data(), ws.size()))) return fail(rc);
+    if ((rc = upload(&h->dq_bias, b.data(), b.size()))) return fail(rc);
+    for (int32_t v : c0) h->g.c0_absmax = std::max(h->g.c0_absmax, std::llabs((long long)v));
+    h->d.m = m; h->d.n = n; h->d.k = k;
+    h->d.a_dtype = d->a_dtype; h->d.b_dtype = d->b_dtype;
+    h->d.y_dtype = NNRH_F32; h->d.scale_dtype = NNRH_F32;
+    h->a_zp = d->a_zp;
+    GemmArgs& g = h->g;
+    g.a_xor = au8 ? 0x80 : 0;
+    g.M = m; g.N = n; g.K = k; g.Kp = Kp;
+    g.lda = k;
+    g.b = h->wpack; g.b_bstride = 0; g.Np = Np;
+    g.colsum = h->colsum;
+    g.c0 = h->c0;
+    g.a_sub = au8 ? 128 : 0;
+    g.alpha = d->a_zp - g.a_sub;
+    g.beta = 0;
+    g.param_bstride = 0;
+    g.epi = EPI_I32S;
+    g.cm = d->a_scale;
+    g.cs = h->colscale;
+    g.dq_bias = h->dq_bias;
+    g.dq_nobias = d->bias_host ? 0 : 1;
+    g.y_type = 3;
+    g.ldy = n;
+    g.y_bstride = (long long)m * n;
+    g.bprime_from = n;
+    if (g.c0_absmax + 16384LL * g.Kp >= 0x7fffffffLL || 256LL * 128LL * Kp + 16384LL * Kp >= 0x7fffffffLL)
+        return fail(set_err(NNRH_ERR_UNSUPPORTED, "matmul_integer_scaled: K too large for int32 accumulators"));
+    *out = h;
     return NNRH_OK;
 }
 
@@ -1044,7 +1122,8 @@ struct nnrh_qmatmul_group {
     int32_t* colsum = nullptr;
     int32_t* c0 = nullptr;
     float* dq_bias = nullptr;
-    ~nnrh_qmatmul_group() { dfree(wpack); dfree(colsum); dfree(c0); dfree(dq_bias); }
+    float* colscale = nullptr;
+    ~nnrh_qmatmul_group() { dfree(wpack); dfree(colsum); dfree(c0); dfree(dq_bias); dfree(colscale); }
 };
 
 extern "C" int nnrh_qmatmul_group_create(nnrh_qmatmul_group_t* out, const nnrh_qmatmul_t* hs, int n) {
@@ -1059,7 +1138,9 @@ extern "C" int nnrh_qmatmul_group_create(nnrh_qmatmul_group_t* out, const nnrh_q
         const GemmArgs& g = h->g;
         const bool same = h->d.m == h0->d.m && h->d.n == h0->d.n && h->d.k == h0->d.k &&
                           h->d.a_dtype == h0->d.a_dtype && h->d.b_dtype == h0->d.b_dtype &&
-                          h->d.y_dtype == NNRH_U8 && h->d.scale_dtype == NNRH_F32 &&
+                          g.epi == h0->g.epi && (g.epi == EPI_I32S || h->d.y_dtype == NNRH_U8) &&
+                          h->d.scale_dtype == NNRH_F32 && g.dq_nobias == h0->g.dq_nobias &&
+                          (g.epi != EPI_I32S || g.cm == h0->g.cm) &&
                           g.Np == h0->g.Np && g.Kp == h0->g.Kp && g.alpha == h0->g.alpha &&
                           g.a_xor == h0->g.a_xor && g.beta == 0 && g.dq_bias && !g.dq_gelu && !g.mm_parts;
         if (!same)
@@ -1076,6 +1157,8 @@ extern "C" int nnrh_qmatmul_group_create(nnrh_qmatmul_group_t* out, const nnrh_q
     if ((rc = nnrh_malloc((void**)&G->colsum, sizeof(int32_t) * Np * n))) return fail(rc);
     if ((rc = nnrh_malloc((void**)&G->c0, sizeof(int32_t) * Np * n))) return fail(rc);
     if ((rc = nnrh_malloc((void**)&G->dq_bias, sizeof(float) * Np * n))) return fail(rc);
+    const bool scaled = h0->g.epi == EPI_I32S;
+    if (scaled && (rc = nnrh_malloc((void**)&G->colscale, sizeof(float) * Np * n))) return fail(rc);
     GemmArgs& g = G->g;
     g = h0->g;
     g.c0_absmax = 0;
@@ -1086,7 +1169,9 @@ extern "C" int nnrh_qmatmul_group_create(nnrh_qmatmul_group_t* out, const nnrh_q
                 hipSuccess ||
             hipMemcpy(G->c0 + (size_t)Np * i, h->c0, sizeof(int32_t) * Np, hipMemcpyDeviceToDevice) != hipSuccess ||
             hipMemcpy(G->dq_bias + (size_t)Np * i, h->dq_bias, sizeof(float) * Np, hipMemcpyDeviceToDevice) !=
-                hipSuccess)
+                hipSuccess ||
+            (scaled && hipMemcpy(G->colscale + (size_t)Np * i, h->colscale, sizeof(float) * Np,
+                                 hipMemcpyDeviceToDevice) != hipSuccess))
             return fail(set_err(NNRH_ERR_HIP, "qmatmul_group_create: device copy failed"));
         g.c0_absmax = std::max(g.c0_absmax, h->g.c0_absmax);
         g.grp_cm[i] = h->g.cm;
@@ -1101,6 +1186,7 @@ extern "C" int nnrh_qmatmul_group_create(nnrh_qmatmul_group_t* out, const nnrh_q
     g.colsum = G->colsum;
     g.c0 = G->c0;
     g.dq_bias = G->dq_bias;
+    if (scaled) g.cs = G->colscale;
     g.param_bstride = Np;
     g.a_bstride = 0;
     G->n = n;
@@ -1252,7 +1338,7 @@ extern "C" int nnrh_matmul_integer_create(nnrh_matmul_integer_t* out, int m, int
 
 int matmul_integer_gemm(nnrh_matmul_integer* h, const void* a, long long a_bstride, const int8_t* bpack,
                         const int32_t* colsum, bool b_batched, int a_zp, int b_zp, int32_t* y, int batch,
-                        hipStream_t s);
+                        hipStream_t s, const void* a_zp_dev = nullptr);
 
 extern "C" int nnrh_matmul_integer_run(nnrh_matmul_integer_t h, const void* a, long long a_bstride,
                                        const void* b, long long b_bstride, int a_zp, int b_zp,
@@ -1272,11 +1358,30 @@ extern "C" int nnrh_matmul_integer_run(nnrh_matmul_integer_t h, const void* a, l
     return matmul_integer_gemm(h, a, a_bstride, h->bpack, h->colsum, b_bstride != 0, a_zp, b_zp, y, batch, s);
 }
 
+extern "C" int nnrh_matmul_integer_run_dev_zp(nnrh_matmul_integer_t h, const void* a, long long a_bstride,
+                                              const void* b, long long b_bstride, const void* a_zp_dev, int b_zp,
+                                              int32_t* y, int batch, void* stream) {
+    if (!h || !a || !b || !y || !a_zp_dev) return set_err(NNRH_ERR_INVALID, "matmul_integer_run_dev_zp: NULL argument");
+    if (batch <= 0 || batch > h->max_batch)
+        return set_err(NNRH_ERR_INVALID, "matmul_integer_run_dev_zp: batch %d (max %d)", batch, h->max_batch);
+    hipStream_t s = S(stream);
+    const bool bu8 = h->b_dtype == NNRH_U8;
+    const int nb_b = b_bstride == 0 ? 1 : batch;
+    {
+        ProfScope ps0("pack_b", s);
+        HIP_TRY(launch_pack_b_dense(b, b_bstride, h->k, h->n, h->Kp, h->Np, bu8 ? 0x80 : 0, h->bpack,
+                                    (long long)h->Np * h->Kp, h->colsum, h->Np, nb_b, s),
+                "pack_b");
+    }
+    return matmul_integer_gemm(h, a, a_bstride, h->bpack, h->colsum, b_bstride != 0, 0, b_zp, y, batch, s,
+                               a_zp_dev);
+}
+
 // the GEMM of MatMulInteger over a packed B ([batch][Np][Kp] int8 and its
 // column sums [batch][Np]; one shared when !b_batched)
 int matmul_integer_gemm(nnrh_matmul_integer* h, const void* a, long long a_bstride, const int8_t* bpack,
                         const int32_t* colsum, bool b_batched, int a_zp, int b_zp, int32_t* y, int batch,
-                        hipStream_t s) {
+                        hipStream_t s, const void* a_zp_dev) {
     const bool au8 = h->a_dtype == NNRH_U8, bu8 = h->b_dtype == NNRH_U8;
     GemmArgs g{};
     g.a = (const uint8_t*)a;
@@ -1291,9 +1396,10 @@ int matmul_integer_gemm(nnrh_matmul_integer* h, const void* a, long long a_bstri
     g.param_bstride = b_batched ? h->Np : 0;
     g.a_sub = au8 ? 128 : 0;
     g.alpha = a_zp - g.a_sub;
+    g.alpha_zp_dev = a_zp_dev;
     g.beta = b_zp - (bu8 ? 128 : 0);
     if (g.beta != 0) {
-        HIP_TRY(launch_rowsum_dense((const uint8_t*)a, g.lda, a_bstride, h->m, h->k, !au8, a_zp, nullptr,
+        HIP_TRY(launch_rowsum_dense((const uint8_t*)a, g.lda, a_bstride, h->m, h->k, !au8, a_zp, a_zp_dev,
                                     h->rowsum, batch, s),
                 "rowsum_dense");
         g.rowsum = h->rowsum;
@@ -1750,6 +1856,15 @@ extern "C" int nnrh_add_layernorm_f32(const float* x, const float* r, const floa
     ProfScope ps("layernorm_f32", S(stream));
     HIP_TRY(launch_layernorm_f32(x, r, gamma, beta, y, (long long)rows, D, eps, parts, S(stream)),
             "add_layernorm_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_cast_to_f32(const void* x, int x_dtype, float* y, size_t n, void* stream) {
+    if (n && (!x || !y)) return set_err(NNRH_ERR_INVALID, "cast_to_f32: NULL");
+    const int dt = x_dtype == NNRH_U8 ? 0 : x_dtype == NNRH_S8 ? 1 : x_dtype == NNRH_I32 ? 2 : -1;
+    if (dt < 0) return set_err(NNRH_ERR_UNSUPPORTED, "cast_to_f32: source type");
+    ProfScope ps("cast_f32", S(stream));
+    HIP_TRY(launch_cast_to_f32(x, dt, y, (long long)n, S(stream)), "cast_to_f32");
     return NNRH_OK;
 }
 

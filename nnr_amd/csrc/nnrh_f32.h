@@ -29,6 +29,7 @@ hipError_t launch_softmax_f32(const float* x, float* y, long long rows, int D, h
 // (min, max) pair of the outputs per row
 hipError_t launch_layernorm_f32(const float* x, const float* r, const float* gamma, const float* beta, float* y,
                                 long long rows, int D, float eps, float* parts, hipStream_t s);
+hipError_t launch_cast_to_f32(const void* x, int dt, float* y, long long n, hipStream_t s);
 hipError_t launch_gelu_f32(const float* x, float* y, long long n, hipStream_t s);
 hipError_t launch_transpose_f32(const float* x, float* y, int ndim, const int* in_dims, const int* perm,
                                 hipStream_t s);

@@ -600,6 +600,27 @@ __global__ __launch_bounds__(256) void gelu_f32_kernel(const float* __restrict x
         y[i] = gelu_erf(x[i]);
 }
 
+// Cast to float (src/backend/cpu/Cast.cpp, Cast_array: (float)x, so int32
+// rounds to the nearest float, ties to even); dt 0 uint8, 1 int8, 2 int32
+__global__ __launch_bounds__(256) void cast_to_f32_kernel(const void* __restrict x, int dt, float* __restrict y,
+                                                          long long n) {
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
+        float v;
+        if (dt == 2) v = (float)((const int32_t*)x)[i];
+        else if (dt == 1) v = (float)((const int8_t*)x)[i];
+        else v = (float)((const uint8_t*)x)[i];
+        y[i] = v;
+    }
+}
+
+hipError_t launch_cast_to_f32(const void* x, int dt, float* y, long long n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    long long b = (n + 255) / 256;
+    if (b > 65536) b = 65536;
+    hipLaunchKernelGGL(cast_to_f32_kernel, dim3((unsigned)b), dim3(256), 0, s, x, dt, y, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_gelu_f32(const float* x, float* y, long long n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     long long blocks = (n + 255) / 256;

@@ -17,6 +17,8 @@ enum EpiMode : int {
     EPI_RQB = 2,   // (acc+bias)*os, clamp [lo-zp,hi-zp], rne, +zp
     EPI_RQC = 3,   // fma(fma(acc,cs,bf), inv_y, zp), clamp, rne
     EPI_RQD = 4,   // acc*cm + zp, nearbyint, clamp
+    EPI_I32S = 5,  // fp32 fl(float(acc) * fl(a_s * cs[n])) (+ bias): MatMulInteger
+                   // -> Cast -> Mul by the per-column scale product (-> Add)
 };
 
 // Which output elements take the reference's scalar-tail expression (RQ-A')
@@ -78,7 +80,8 @@ struct GemmArgs {
                               // (colsum, c0, beta_col, os, bias, cs, bf); all
                               // per-column arrays are padded to Np entries
     float inv_y;
-    float cm;               // RQ-D combined scale fl(fl(a_s*b_s)/y_s)
+    float cm;               // RQ-D combined scale fl(fl(a_s*b_s)/y_s);
+                            // EPI_I32S: the host activation scale a_s
     const float* cm_a_scale_dev;  // RQ-D: nullable device a_scale; then
     float cm_b, cm_y;             //   cm = fl(fl(a_s*cm_b)/cm_y) in-kernel
     int y_zp;
@@ -113,6 +116,7 @@ struct GemmArgs {
     const float* dq_bias;       // NULL: no fused dequantize (padded to Np)
     float dq_scale;
     int dq_gelu;                // then Gelu (erf form) of the fp32 value
+    int dq_nobias;              // EPI_I32S: no bias Add in the fused chain
     // fused dequantize: (min, max) of each (tile, wave)'s outputs, pair
     // 4 * tile + wave, for a DynamicQuantizeLinear that reads y (NULL: none)
     float* mm_parts;

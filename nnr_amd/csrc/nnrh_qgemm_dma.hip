@@ -91,6 +91,7 @@ template <> struct EpiParams<EPI_RQA> { static constexpr int NP = 3; };   // c0,
 template <> struct EpiParams<EPI_RQC> { static constexpr int NP = 3; };   // c0, cs, bf
 template <> struct EpiParams<EPI_RQD> { static constexpr int NP = 1; };   // c0
 template <> struct EpiParams<EPI_I32> { static constexpr int NP = 1; };   // c0
+template <> struct EpiParams<EPI_I32S> { static constexpr int NP = 2; };  // c0, per-column scale
 
 }  // namespace
 
@@ -191,7 +192,7 @@ void qgemm_dma_kernel(GemmArgs g) {
     const uint32_t neg_alpha = 0u - (uint32_t)alpha;
     // RQ-D combined scale, fl(fl(a_s * b_s) / y_s), with a device a_scale
     float cm = g.cm;
-    const float a_scale_dev = (EPI == EPI_RQD && g.cm_a_scale_dev) ? *g.cm_a_scale_dev : 0.0f;
+    const float a_scale_dev = ((EPI == EPI_RQD || EPI == EPI_I32S) && g.cm_a_scale_dev) ? *g.cm_a_scale_dev : 0.0f;
     if (EPI == EPI_RQD && g.cm_a_scale_dev) {
         const float t1 = a_scale_dev * g.cm_b;
         cm = t1 / g.cm_y;
@@ -409,6 +410,35 @@ void qgemm_dma_kernel(GemmArgs g) {
     // fused dequantize: running min / max of the fp32 outputs of the tile
     float mm_mn = 0.0f, mm_mx = 0.0f;
 
+    // fp32 outputs of a fused epilogue (16 columns of one row): the Gelu
+    // when fused, the running min / max for a DynamicQuantizeLinear that
+    // reads them, then the store
+    auto store_f32 = [&](float (&o)[16], float* frow, bool full16, int nb) {
+        if (g.dq_gelu) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[i] = gelu_erf(o[i]);
+        }
+        if (g.mm_parts) {
+            // min / max of what this lane writes (0 stands in for nothing:
+            // DynamicQuantizeLinear adds 0 anyway)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (full16 || nb + i < g.N) {
+                    mm_mn = fminf(mm_mn, o[i]);
+                    mm_mx = fmaxf(mm_mx, o[i]);
+                }
+        }
+        if (full16 && ((((uintptr_t)frow) & 15) == 0)) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *(float4*)(frow + 4 * q) = make_float4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (nb + i < g.N) frow[i] = o[i];
+        }
+    };
+
     // conv_is_a: the conv byte is input A of the fused QLinearAdd (else B)
     auto epilogue = [&](auto conv_is_a_t) {
         constexpr bool CONV_A = decltype(conv_is_a_t)::value;
@@ -441,6 +471,24 @@ void qgemm_dma_kernel(GemmArgs g) {
         for (int tm = 0; tm < 4; ++tm) {
             const int m = m0 + wm * 64 + tm * 16 + frow;
             if (m >= g.M) continue;
+            if constexpr (EPI == EPI_I32S) {
+                // MatMulInteger -> Cast (float(acc), nearest even) -> Mul by
+                // the scale product fl(a_s * w_s[n]) -> Add(bias[n]) (->
+                // Gelu), each an IEEE binary32 operation in that order
+                const float a_s = g.cm_a_scale_dev ? a_scale_dev : g.cm;
+                const uint8_t* pb = ps + NP * BN * 4 + nl * 4;
+                float* frow = (g.ngrp ? (float*)g.grp_y[z] : (float*)g.y + (long long)z * g.y_bstride) +
+                              (long long)m * g.ldy + nb;
+                float o[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float sp = a_s * __int_as_float(p0[i >> 2][i & 3]);
+                    const float v = (float)acc[tm][i >> 2][i & 3] * sp;
+                    o[i] = g.dq_nobias ? v : v + *(const float*)(pb + 4 * i);
+                }
+                store_f32(o, frow, full16, nb);
+                continue;
+            }
             if constexpr (EPI == EPI_I32) {
                 int32_t* yrow = (int32_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
                 v4i o[4];
@@ -608,29 +656,7 @@ void qgemm_dma_kernel(GemmArgs g) {
                         const float d = (qf - zp_f) * dqs;
                         o[i] = d + *(const float*)(pb + 4 * i);
                     }
-                    if (g.dq_gelu) {
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) o[i] = gelu_erf(o[i]);
-                    }
-                    if (g.mm_parts) {
-                        // min / max of what this lane writes (0 stands in
-                        // for nothing: DynamicQuantizeLinear adds 0 anyway)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i)
-                            if (full16 || nb + i < g.N) {
-                                mm_mn = fminf(mm_mn, o[i]);
-                                mm_mx = fmaxf(mm_mx, o[i]);
-                            }
-                    }
-                    if (full16 && ((((uintptr_t)frow) & 15) == 0)) {
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            *(float4*)(frow + 4 * q) = make_float4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 16; ++i)
-                            if (nb + i < g.N) frow[i] = o[i];
-                    }
+                    store_f32(o, frow, full16, nb);
                     continue;
                 }
                 uint8_t* yrow = (uint8_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
@@ -789,6 +815,7 @@ hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
     if (g.dq_bias) {
         if constexpr (AMODE == A_DENSE) {
             if (g.epi == EPI_RQD) return launch_dma<BM, BN, S, AMODE, EPI_RQD, FUSE_DQB>(g, batch, s);
+            if (g.epi == EPI_I32S) return launch_dma<BM, BN, S, AMODE, EPI_I32S, FUSE_DQB>(g, batch, s);
         }
         return hipErrorNotSupported;
     }
@@ -833,7 +860,9 @@ bool qgemm_dma_eligible(const GemmArgs& g, int vec) {
     if (vec != 16) return false;
     // per-column constant: c0, or -alpha * colsum (GEMMs without bias)
     if (g.rowsum != nullptr) return false;
-    if (g.c0 == nullptr && (g.colsum == nullptr || (g.epi != EPI_RQD && g.epi != EPI_I32))) return false;
+    if (g.c0 == nullptr && (g.colsum == nullptr || (g.epi != EPI_RQD && g.epi != EPI_I32 && g.epi != EPI_I32S)))
+        return false;
+    if (g.epi == EPI_I32S && (g.cs == nullptr || g.dq_bias == nullptr || g.H > 0)) return false;
     if (g.c0 == nullptr && 256LL * 128LL * (long long)g.Kp + 16384LL * (long long)g.Kp >= 0x7fffffffLL)
         return false;
     if (g.c0 != nullptr && g.alpha_zp_dev != nullptr) return false;

@@ -75,6 +75,7 @@ def host_lib():
                                          P(i), P(i)]),
             "nnr_ctx_enable_profiling": (i, [vp, i]),
             "nnr_ctx_profile": (i, [vp, i, P(C.c_double), P(i), P(C.c_double), P(C.c_double)]),
+            "nnr_ctx_time_node": (i, [vp, i, i, P(C.c_double)]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -345,6 +346,12 @@ class Session:
                                         C.byref(nb)))
             rows.append(dict(p, ms=ms.value, runs=runs.value, ops=ops.value, bytes=nb.value))
         return rows
+
+    def time_node(self, i, reps=10):
+        """Average ms of plan node i run `reps` times back to back."""
+        ms = C.c_double()
+        _chk(self.L.nnr_ctx_time_node(self.h, i, reps, C.byref(ms)))
+        return ms.value
 
     def __del__(self):
         try:

@@ -398,4 +398,12 @@ int nnr_ctx_profile(nnr_ctx_t c, int i, double* ms, int* runs, double* ops, doub
     });
 }
 
+int nnr_ctx_time_node(nnr_ctx_t c, int i, int reps, double* ms) {
+    return guarded("ctx_time_node", [&]() -> int {
+        if (!c || !ms) return err("time_node: NULL argument");
+        if (!c->ctx.time_node(i, reps, ms)) return ctx_err(c);
+        return 0;
+    });
+}
+
 }  // extern "C"

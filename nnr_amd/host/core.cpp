@@ -453,6 +453,7 @@ bool context_t::prepare() {
     if (enable_fusion && enable_conv_add) {
         fuse_conv_add(this);
         fuse_matmul_dq_bias(this);
+        fuse_matmul_integer_scale(this);
         fuse_quant_prefix(this);
         fuse_add_layernorm(this);
         fuse_dynq_minmax(this);
@@ -505,6 +506,35 @@ bool context_t::run() {
             }
         }
     }
+    return true;
+}
+
+bool context_t::time_node(int i, int reps, double* ms) {
+    if (!prepared && !prepare()) return false;
+    operator_t* op = nullptr;
+    int pi = 0;
+    for (auto* o : nodes) {
+        if (o->skip || o->folded) continue;
+        if (pi++ == i) {
+            op = o;
+            break;
+        }
+    }
+    if (!op || reps < 1 || !ms) return fail("time_node: bad node index or repeat count");
+    void *a = nullptr, *b = nullptr;
+    if (nnrh_event_create(&a) || nnrh_event_create(&b)) {
+        if (a) nnrh_event_destroy(a);
+        return fail(nnrh_last_error());
+    }
+    bool okay = nnrh_event_record(a, stream) == NNRH_OK;
+    for (int r = 0; okay && r < reps; ++r) okay = op->exec();
+    okay = okay && nnrh_event_record(b, stream) == NNRH_OK && nnrh_stream_synchronize(stream) == NNRH_OK;
+    float t = 0.0f;
+    okay = okay && nnrh_event_elapsed_ms(&t, a, b) == NNRH_OK;
+    nnrh_event_destroy(a);
+    nnrh_event_destroy(b);
+    if (!okay) return fail("time_node: " + op->node_name + ": " + nnrh_last_error());
+    *ms = (double)t / reps;
     return true;
 }
 

@@ -203,6 +203,14 @@ struct operator_t {
     // member's exec does nothing (its output is written by the leader, which
     // runs first)
     virtual bool fuse_group(const std::vector<operator_t*>& /*members*/) { return false; }
+    // may lead or join a grouped launch, and reads the same input (and its
+    // quantization) as `other`
+    virtual bool groupable() const { return false; }
+    virtual bool same_group_input(const operator_t* /*other*/) const { return false; }
+    // MatMulInteger with a constant B followed by Cast -> Mul by the scale
+    // product Mul(a_scale, w_scale) [-> Add(bias)] (fuse_matmul_integer_scale):
+    // the kernel forms the fp32 result; bias NULL when no Add follows
+    virtual bool fuse_int_scale(tensor_t* /*a_scale*/, tensor_t* /*w_scale*/, tensor_t* /*bias*/) { return false; }
     // BatchNormalization whose scale / bias inputs now hold fold_bn_qdq's
     // combined per-channel A / B and whose output is uint8 (false: cannot)
     virtual bool fold_affine_u8() { return false; }
@@ -260,6 +268,9 @@ struct context_t {
     // known, operators not built) or the applied plan after prepare()
     bool plan_memory_dry();
     bool run();         // execute active nodes in order on `stream`
+    // average device time of the i-th active node run `reps` times back to
+    // back between two events (no event between the repeats), in ms
+    bool time_node(int i, int reps, double* ms);
 
     // ---- configuration (src/nnr.h:512-589) ----
     backend_t preferred_backend = backend_t::HIP;
@@ -306,6 +317,7 @@ void fuse_post_ops(context_t* ctx);
 void assign_layouts(context_t* ctx);
 void fuse_conv_add(context_t* ctx);
 void fuse_matmul_dq_bias(context_t* ctx);
+void fuse_matmul_integer_scale(context_t* ctx);
 void fuse_quant_prefix(context_t* ctx);
 void fuse_add_layernorm(context_t* ctx);
 void fuse_matmul_group(context_t* ctx);

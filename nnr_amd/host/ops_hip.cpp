@@ -30,7 +30,7 @@ int qdtype(data_type_t t) {
     return t == NNR_DATA_TYPE_UINT8 ? NNRH_U8 : t == NNR_DATA_TYPE_INT8 ? NNRH_S8
          : t == NNR_DATA_TYPE_INT32 ? NNRH_I32 : -1;
 }
-tensor_t* in(operator_t* op, size_t i) { return op->inputs.size() > i ? op->inputs[i] : nullptr; }
+tensor_t* in(const operator_t* op, size_t i) { return op->inputs.size() > i ? op->inputs[i] : nullptr; }
 bool has_zp(tensor_t* t) { return t && t->ndata > 0; }
 int32_t zp_value(tensor_t* t) { return has_zp(t) ? t->scalar_int() : 0; }
 
@@ -389,6 +389,11 @@ struct QLinearMatMul_hip : operator_t {
     bool set_minmax_out(float* parts, int pairs) override {
         return nnrh_qmatmul_set_minmax_out(h, parts, pairs) == NNRH_OK;
     }
+    bool groupable() const override { return h && fused_chain.size() == 2; }
+    bool same_group_input(const operator_t* o) const override {
+        return dynamic_cast<const QLinearMatMul_hip*>(o) && o->inputs[0] == inputs[0] &&
+               o->inputs[1] == inputs[1] && o->inputs[2] == inputs[2];
+    }
     bool fuse_group(const std::vector<operator_t*>& members) override {
         if (!h || fused_chain.size() != 2) return false;
         std::vector<nnrh_qmatmul_t> hs{h};
@@ -431,12 +436,22 @@ struct QLinearMatMul_hip : operator_t {
     }
 };
 
-// MatMulInteger (src/backend/cpu/MatMulInteger.cpp)
+// MatMulInteger (src/backend/cpu/MatMulInteger.cpp). With a constant B and
+// the per-channel dynamic-quantization chain after it (Cast -> Mul by the
+// scale product Mul(a_scale, w_scale) -> Add(bias) [-> Gelu], fused by
+// fuse_matmul_integer_scale), the whole chain runs in one GEMM (sh).
 struct MatMulInteger_hip : operator_t {
     nnrh_matmul_integer_t h = nullptr;
+    nnrh_qmatmul_t sh = nullptr;            // fused chain
+    nnrh_qmatmul_group_t grp = nullptr;     // leader of a grouped launch
+    tensor_t* a_scale = nullptr;            // fused chain: the activation scale
     int m = 0, n = 0, k = 0, batch = 1;
     bool b_batched = false;
-    ~MatMulInteger_hip() override { nnrh_matmul_integer_destroy(h); }
+    ~MatMulInteger_hip() override {
+        nnrh_qmatmul_group_destroy(grp);
+        nnrh_qmatmul_destroy(sh);
+        nnrh_matmul_integer_destroy(h);
+    }
     bool init() override { return inputs.size() >= 2 && inputs.size() <= 4 && outputs.size() == 1; }
     bool reshape() override {
         tensor_t *a = inputs[0], *b = inputs[1], *y = outputs[0];
@@ -455,20 +470,131 @@ struct MatMulInteger_hip : operator_t {
         d.push_back(n);
         if (!y->reshape(d, NNR_DATA_TYPE_INT32)) return false;
         if (ctx->shape_only) return true;
-        for (int i = 2; i < 4; ++i)
-            if (in(this, i) && in(this, i)->ndata && !in(this, i)->has_host())
-                return bad(this, "zero points must be constant");
+        // A's zero point may come from the device (DynamicQuantizeLinear);
+        // B's must be a constant
+        if (in(this, 2) && in(this, 2)->ndata > 1) return bad(this, "per-row A zero points");
+        if (in(this, 3) && in(this, 3)->ndata && !in(this, 3)->has_host())
+            return bad(this, "B's zero point must be constant");
+        if (in(this, 3) && in(this, 3)->ndata > 1) return bad(this, "per-column B zero points");
         nnrh_matmul_integer_destroy(h);
         h = nullptr;
         return ok(this, nnrh_matmul_integer_create(&h, m, n, k, qdtype(a->type), qdtype(b->type), batch));
     }
+    // the chain Cast -> Mul(scale product) [-> Add(bias)] after a constant B
+    bool fuse_int_scale(tensor_t* a_s, tensor_t* w_scale, tensor_t* bias) override {
+        tensor_t* b = inputs[1];
+        if (!b->has_host() || b->ndim() != 2 || b_batched) return false;
+        if (!w_scale->has_host() || w_scale->type != NNR_DATA_TYPE_FLOAT32 || w_scale->ndata != (size_t)n) return false;
+        if (bias && (!bias->has_host() || bias->type != NNR_DATA_TYPE_FLOAT32 || bias->ndata != (size_t)n)) return false;
+        if (a_s->ndata != 1 || a_s->type != NNR_DATA_TYPE_FLOAT32) return false;
+        nnrh_mmi_scaled_desc d{};
+        d.m = m; d.n = n; d.k = k;
+        d.a_dtype = qdtype(inputs[0]->type);
+        d.b_dtype = qdtype(b->type);
+        d.b_host = b->host.data();
+        d.a_zp = in(this, 2) && in(this, 2)->has_host() ? zp_value(in(this, 2)) : 0;
+        d.b_zp = zp_value(in(this, 3));
+        d.a_scale = a_s->has_host() ? a_s->scalar_f32() : 1.0f;
+        d.w_scale_host = w_scale->h<float>();
+        d.bias_host = bias ? bias->h<float>() : nullptr;
+        nnrh_qmatmul_destroy(sh);
+        sh = nullptr;
+        if (nnrh_matmul_integer_scaled_create(&sh, &d) != NNRH_OK) return false;
+        a_scale = a_s;
+        return true;
+    }
+    bool fuse_gelu(operator_t* ge) override {
+        if (!sh || ge->attribute_s("approximate", "none") != "none") return false;
+        if (ge->outputs[0]->dims != ge->inputs[0]->dims) return false;
+        return nnrh_qmatmul_fuse_gelu(sh) == NNRH_OK;
+    }
+    int minmax_pairs() const override {
+        int c = 0;
+        if (!sh || nnrh_qmatmul_minmax_count(sh, batch, &c) != NNRH_OK) return 0;
+        return c;
+    }
+    bool set_minmax_out(float* parts, int pairs) override {
+        return sh && nnrh_qmatmul_set_minmax_out(sh, parts, pairs) == NNRH_OK;
+    }
+    bool groupable() const override {
+        return sh && !fused_chain.empty() && fused_chain.back()->op_type != "Gelu";
+    }
+    bool same_group_input(const operator_t* o) const override {
+        auto* x = dynamic_cast<const MatMulInteger_hip*>(o);
+        return x && x->inputs[0] == inputs[0] && in(x, 2) == in(this, 2) && x->a_scale == a_scale;
+    }
+    bool fuse_group(const std::vector<operator_t*>& members) override {
+        if (!groupable()) return false;
+        std::vector<nnrh_qmatmul_t> hs{sh};
+        for (auto* op : members) {
+            auto* o = dynamic_cast<MatMulInteger_hip*>(op);
+            if (!o || !o->groupable() || o->m != m || o->n != n || o->k != k || o->batch != batch) return false;
+            hs.push_back(o->sh);
+        }
+        return nnrh_qmatmul_group_create(&grp, hs.data(), (int)hs.size()) == NNRH_OK;
+    }
+    std::string variant() const override {
+        if (!sh) return "";
+        std::string v = "+Cast+Scale";
+        for (auto* op : fused_chain) {
+            if (op->op_type == "Add") v += "+Bias";
+            if (op->op_type == "Gelu") v += "+Gelu";
+        }
+        if (grp) v += "+Group" + std::to_string(group_members.size() + 1);
+        else if (group_leader) v += "(grouped)";
+        return v;
+    }
     bool exec() override {
+        tensor_t* az = in(this, 2);
+        const void* az_dev = az && az->ndata && !az->has_host() ? az->data : nullptr;
+        if (sh) {
+            if (group_leader && group_leader != this) return true;   // written by the leader's launch
+            const float* as_dev = a_scale->has_host() ? nullptr : (const float*)a_scale->data;
+            if (grp) {
+                std::vector<void*> ys{outputs[0]->data};
+                for (auto* op : group_members) ys.push_back(op->outputs[0]->data);
+                return ok(this, nnrh_qmatmul_group_run(grp, inputs[0]->data, batch * m, ys.data(), as_dev, az_dev,
+                                                       ctx->stream));
+            }
+            return ok(this, nnrh_qmatmul_run(sh, inputs[0]->data, batch > 1 ? (long long)m * k : 0,
+                                             outputs[0]->data, batch, as_dev, az_dev, ctx->stream));
+        }
+        if (az_dev)
+            return ok(this, nnrh_matmul_integer_run_dev_zp(h, inputs[0]->data, batch > 1 ? (long long)m * k : 0,
+                                                           inputs[1]->data, b_batched ? (long long)k * n : 0, az_dev,
+                                                           zp_value(in(this, 3)), (int32_t*)outputs[0]->data,
+                                                           batch, ctx->stream));
         return ok(this, nnrh_matmul_integer_run(h, inputs[0]->data, batch > 1 ? (long long)m * k : 0,
                                                 inputs[1]->data, b_batched ? (long long)k * n : 0,
                                                 zp_value(in(this, 2)), zp_value(in(this, 3)),
                                                 (int32_t*)outputs[0]->data, batch, ctx->stream));
     }
-    double num_ops() const override { return 2.0 * batch * m * (double)n * k; }
+    double num_ops() const override {
+        if (group_leader && group_leader != this) return 0.0;
+        return 2.0 * batch * m * (double)n * k * (double)(grp ? group_members.size() + 1 : 1);
+    }
+};
+
+// Cast to float (src/backend/cpu/Cast.cpp) from int32 / uint8 / int8
+struct Cast_hip : operator_t {
+    bool init() override {
+        layout_mask = LAYOUT_ALL;
+        return inputs.size() == 1 && outputs.size() == 1;
+    }
+    bool reshape() override {
+        if (attribute("to", 0) != 1) return bad(this, "only Cast to float (to = 1)");
+        const data_type_t t = inputs[0]->type;
+        if (t != NNR_DATA_TYPE_INT32 && t != NNR_DATA_TYPE_UINT8 && t != NNR_DATA_TYPE_INT8)
+            return bad(this, "Cast from int32 / uint8 / int8 only");
+        outputs[0]->format = inputs[0]->format;
+        return outputs[0]->reshape(inputs[0]->dims, NNR_DATA_TYPE_FLOAT32);
+    }
+    bool exec() override {
+        const data_type_t t = inputs[0]->type;
+        const int dt = t == NNR_DATA_TYPE_INT32 ? NNRH_I32 : t == NNR_DATA_TYPE_UINT8 ? NNRH_U8 : NNRH_S8;
+        return ok(this, nnrh_cast_to_f32(inputs[0]->data, dt, (float*)outputs[0]->data, inputs[0]->ndata,
+                                         ctx->stream));
+    }
 };
 
 // ===========================================================================
@@ -1384,6 +1510,7 @@ const op_registrar_t reg[] = {
     {"QLinearConv", backend_t::HIP, make<QLinearConv_hip>},
     {"QLinearMatMul", backend_t::HIP, make<QLinearMatMul_hip>},
     {"MatMulInteger", backend_t::HIP, make<MatMulInteger_hip>},
+    {"Cast", backend_t::HIP, make<Cast_hip>},
     {"QLinearAdd", backend_t::HIP, make<QLinearAdd_hip>},
     {"QLinearMul", backend_t::HIP, make<QLinearMul_hip>},
     {"QLinearGlobalAveragePool", backend_t::HIP, make<QLinearGlobalAveragePool_hip>},

@@ -570,6 +570,96 @@ void fuse_matmul_dq_bias(context_t* ctx) {
 }
 
 // ---------------------------------------------------------------------------
+// MatMulInteger (constant B) -> Cast(to float) -> Mul(., S) [-> Add(bias)]
+// [-> Gelu] with S = Mul(a_scale, w_scale) of the activation's scalar scale
+// and a constant per-column weight scale: the per-channel form of dynamic
+// quantization. The GEMM forms fl(fl(float(acc) * fl(a_scale * w_scale[n]))
+// + bias[n]) itself, so the chain, and the scale product when nothing else
+// reads it, are skipped; the chain is recorded in the order its values are
+// formed (Cast, the scale product, the Mul, the Add, the Gelu).
+void fuse_matmul_integer_scale(context_t* ctx) {
+    auto& nodes = ctx->nodes;
+    std::unordered_set<tensor_t*> graph_out;
+    for (auto& name : ctx->graph_outputs)
+        if (tensor_t* t = ctx->find(name)) graph_out.insert(t);
+    std::unordered_map<tensor_t*, operator_t*> producer;
+    std::unordered_map<tensor_t*, int> uses;
+    for (auto* op : nodes) {
+        if (!active(op)) continue;
+        for (auto* t : op->outputs)
+            if (t) producer[t] = op;
+        for (auto* t : op->inputs)
+            if (t) uses[t]++;
+    }
+    auto sole_consumer = [&](tensor_t* t) -> operator_t* {
+        if (!t || graph_out.count(t) || uses[t] != 1) return nullptr;
+        for (auto* op : nodes)
+            if (active(op))
+                for (auto* x : op->inputs)
+                    if (x == t) return op;
+        return nullptr;
+    };
+    auto is_vector = [](tensor_t* t, int n) {
+        if (!t || !t->has_host() || t->type != NNR_DATA_TYPE_FLOAT32 || t->ndata != (size_t)n) return false;
+        for (int i = 0; i + 1 < t->ndim(); ++i)
+            if (t->dims[i] != 1) return false;
+        return true;
+    };
+    int fused = 0, gelu = 0;
+    for (auto* mm : nodes) {
+        if (!active(mm) || mm->op_type != "MatMulInteger" || mm->outputs.size() != 1) continue;
+        tensor_t* acc = mm->outputs[0];
+        const int n = acc->ndim() ? acc->dims.back() : 0;
+        operator_t* cast = sole_consumer(acc);
+        if (!cast || cast->op_type != "Cast" || cast->attribute("to", 0) != 1) continue;
+        operator_t* mul = sole_consumer(cast->outputs[0]);
+        if (!mul || mul->op_type != "Mul" || mul->inputs.size() != 2) continue;
+        tensor_t* sp = mul->inputs[0] == cast->outputs[0] ? mul->inputs[1] : mul->inputs[0];
+        auto pit = producer.find(sp);
+        if (pit == producer.end()) continue;
+        operator_t* smul = pit->second;   // the scale product Mul(a_scale, w_scale)
+        if (smul->op_type != "Mul" || smul->inputs.size() != 2 || graph_out.count(sp)) continue;
+        tensor_t *a_s = smul->inputs[0], *w_s = smul->inputs[1];
+        if (is_vector(a_s, n)) std::swap(a_s, w_s);
+        if (!is_vector(w_s, n) || !a_s || a_s->ndata != 1 || a_s->type != NNR_DATA_TYPE_FLOAT32) continue;
+        tensor_t* y = mul->outputs[0];
+        operator_t* add = sole_consumer(y);
+        tensor_t* bias = nullptr;
+        if (add && add->op_type == "Add" && add->inputs.size() == 2) {
+            bias = add->inputs[0] == y ? add->inputs[1] : add->inputs[0];
+            if (!is_vector(bias, n) || add->outputs[0]->dims != y->dims) {
+                add = nullptr;
+                bias = nullptr;
+            }
+        } else {
+            add = nullptr;
+        }
+        if (y->dims != acc->dims) continue;
+        if (!mm->fuse_int_scale(a_s, w_s, bias)) continue;
+        mm->fused_chain = {cast, smul, mul};
+        cast->skip = true;
+        mul->skip = true;
+        if (uses[sp] == 1) smul->skip = true;   // else it still runs for its other readers
+        mm->outputs[0] = y;
+        if (add) {
+            mm->fused_chain.push_back(add);
+            mm->outputs[0] = add->outputs[0];
+            add->skip = true;
+        }
+        ++fused;
+        operator_t* ge = sole_consumer(mm->outputs[0]);
+        if (!ge || ge->op_type != "Gelu" || ge->inputs.size() != 1 || ge->outputs.size() != 1) continue;
+        if (!mm->fuse_gelu(ge)) continue;
+        mm->fused_chain.push_back(ge);
+        mm->outputs[0] = ge->outputs[0];
+        ge->skip = true;
+        ++gelu;
+    }
+    ctx->fusion_stats["matmul_integer_scale"] = fused;
+    ctx->fusion_stats["matmul_integer_gelu"] = gelu;
+}
+
+// ---------------------------------------------------------------------------
 // QuantizeLinear / DequantizeLinear whose only consumer is an operator that
 // can read their input directly (the first-layer conv's layout kernel, the
 // global average pool): the consumer does the (de)quantization itself.
@@ -620,17 +710,12 @@ void fuse_matmul_group(context_t* ctx) {
     auto& nodes = ctx->nodes;
     for (size_t i = 0; i < nodes.size(); ++i) {
         operator_t* lead = nodes[i];
-        if (!active(lead) || lead->op_type != "QLinearMatMul" || lead->fused_chain.size() != 2 ||
-            taken.count(lead))
-            continue;
+        if (!active(lead) || !lead->groupable() || taken.count(lead)) continue;
         std::vector<operator_t*> members;
         for (size_t j = i + 1; j < nodes.size() && members.size() < 3; ++j) {
             operator_t* op = nodes[j];
-            if (!active(op) || op->op_type != "QLinearMatMul" || op->fused_chain.size() != 2 || taken.count(op))
-                continue;
-            if (op->inputs[0] != lead->inputs[0] || op->inputs[1] != lead->inputs[1] ||
-                op->inputs[2] != lead->inputs[2])
-                continue;
+            if (!active(op) || op->op_type != lead->op_type || !op->groupable() || taken.count(op)) continue;
+            if (!lead->same_group_input(op)) continue;
             members.push_back(op);
         }
         if (members.empty() || !lead->fuse_group(members)) continue;

@@ -395,26 +395,51 @@ def mobilenetv2(batch=256, hw=224, seed=4, num_classes=1000):
     return g
 
 
-def bert(batch=64, seq=128, layers=12, hidden=768, heads=12, ffn=3072, seed=5):
-    """BERT-base-shaped int8 encoder (cfg5). Every projection is
-    DynamicQuantizeLinear -> DQ -> MatMul(DQ(W int8)) -> Q -> DQ -> + bias,
-    which the QDQ fusion turns into a QLinearMatMul reading the dynamic
-    uint8 activation scale / zero point from device memory. The weights are
-    N(0, 0.02) quantized per tensor: NNR's QLinearMatMul reads b_scale[0] only
-    (QLinearMatMul.cpp:118-119), so per-channel weight scales would not be
-    applied. Attention scores, Softmax, LayerNormalization and Gelu are fp32.
-    Input: seeded uniform token embeddings [batch, seq, hidden]."""
+def bert(batch=64, seq=128, layers=12, hidden=768, heads=12, ffn=3072, seed=5, per_channel=False):
+    """BERT-base-shaped int8 encoder (cfg5). Attention scores, Softmax,
+    LayerNormalization and Gelu are fp32. Input: seeded uniform token
+    embeddings [batch, seq, hidden]. The weights are N(0, 0.02) before
+    quantization; each projection has one of two forms:
+      per_channel=False: DynamicQuantizeLinear -> DQ -> MatMul(DQ(W int8)) ->
+        Q -> DQ -> + bias, which the QDQ fusion turns into a QLinearMatMul
+        reading the dynamic uint8 activation scale / zero point from device
+        memory. W is quantized per tensor: NNR's QLinearMatMul reads
+        b_scale[0] only (QLinearMatMul.cpp:118-119), so per-channel weight
+        scales would not be applied in this form.
+      per_channel=True: W quantized per output channel, as dynamic
+        quantization emits it (and NNR runs it, MatMulInteger.cpp:11-150):
+        DynamicQuantizeLinear -> MatMulInteger(x_q, W_q, x_zp) -> Cast(float)
+        -> Mul(., Mul(x_scale, w_scale[N])) -> + bias."""
     g = Graph()
     rng = np.random.default_rng(seed)
     dh = hidden // heads
     g.inputs["input"] = (np.float32, (batch, seq, hidden))
 
+    def dynq_raw(x_f, name):
+        return g.node("DynamicQuantizeLinear", [x_f], outputs=[name + "_xq", name + "_xs", name + "_xz"],
+                      name=name + "_dynq")
+
     def dynq(x_f, name):
-        xq, xs, xz = g.node("DynamicQuantizeLinear", [x_f], outputs=[name + "_xq", name + "_xs", name + "_xz"],
-                            name=name + "_dynq")
+        if per_channel:
+            return dynq_raw(x_f, name)
+        xq, xs, xz = dynq_raw(x_f, name)
         return g.node("DequantizeLinear", [xq, xs, xz], name=name + "_xdq")
 
+    def qlinear_pc(x_f, din, dout, name, dyn=None):
+        xq, xs, xz = dyn if dyn is not None else dynq_raw(x_f, name)
+        w = rng.normal(0.0, 0.02, (din, dout)).astype(F32)
+        ws = np.maximum(np.abs(w).max(0) / F32(127.0), F32(1e-8)).astype(F32)
+        wq = np.clip(np.rint(w / ws[None, :]), -127, 127).astype(np.int8)
+        sp = g.node("Mul", [xs, g.init(name + "_ws", ws)], name=name + "_scale")
+        acc = g.node("MatMulInteger", [xq, g.init(name + "_w", wq), xz], name=name)
+        af = g.node("Cast", [acc], name=name + "_cast", to=1)
+        y = g.node("Mul", [af, sp], name=name + "_deq")
+        b = g.init(name + "_b", rng.normal(0.0, 0.02, dout).astype(F32))
+        return g.node("Add", [y, b], name=name + "_bias")
+
     def qlinear(x_f, din, dout, name, y_scale, xdq=None):
+        if per_channel:
+            return qlinear_pc(x_f, din, dout, name, xdq)
         if xdq is None:
             xdq = dynq(x_f, name)
         w = rng.normal(0.0, 0.02, (din, dout)).astype(F32)

@@ -82,6 +82,14 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
         elif op == "Gelu":
             x = val(ins[0]).astype(np.float64)
             y = (0.5 * x * (1.0 + _erf(x / np.sqrt(2.0)))).astype(np.float32)
+        elif op == "MatMulInteger":
+            # MatMulInteger.cpp:11-150: exact int32 sum of (a - a_zp)(b - b_zp)
+            a_zp = int(scal(ins[2])) if len(ins) > 2 and ins[2] else 0
+            b_zp = int(scal(ins[3])) if len(ins) > 3 and ins[3] else 0
+            y = O.matmul_integer(val(ins[0]), val(ins[1]), a_zp, b_zp)
+        elif op == "Cast":
+            # Cast.cpp (Cast_array): (float)x, int32 rounding to nearest even
+            y = val(ins[0]).astype(np.float32)
         elif op == "HardSwish":
             y = O.hardswish(val(ins[0]), post_op=bool(nd.get("post_op")))
         elif op in ("Relu", "Clip"):

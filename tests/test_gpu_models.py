@@ -220,6 +220,53 @@ def test_bert_full_depth_seq128(dev):
     assert n_int >= 48 * 2 and n_f32 >= 72
 
 
+@pytest.mark.parametrize("layers,seq,fused", [(12, 128, True), (2, 64, False)])
+def test_bert_per_channel(dev, layers, seq, fused):
+    """cfg5 with per-channel weights in the dynamic-quantization form NNR runs
+    (DynamicQuantizeLinear -> MatMulInteger -> Cast -> Mul(Mul(x_scale,
+    w_scale[N])) -> Add): fused, every projection is one GEMM writing the fp32
+    chain end (Q / K / V grouped, FF1 with its Gelu); unfused, each operator
+    runs alone. Every node recomputed by the oracle from the device's own
+    inputs: int8 exact; the fused projections without Gelu bit-exact, the
+    rest of the fp32 values within 1e-3."""
+    from oracle import graph_oracle as GO
+    g = synth.bert(batch=2, seq=seq, layers=layers, per_channel=True)
+    rng = np.random.default_rng(36)
+    x = rng.uniform(-1.0, 1.0, (2, seq, 768)).astype(np.float32)
+    plan, n_int, n_f32 = check_graph_per_node(g, {"input": x}, conv_add=fused)
+    ops = [p["op"] for p in plan]
+    assert ops.count("MatMulInteger") == 6 * layers
+    if not fused:
+        assert ops.count("Cast") == 6 * layers and not any(p.get("fused_chain") for p in plan)
+        return
+    assert "Cast" not in ops and "Gelu" not in ops
+    mm = [p for p in plan if p["op"] == "MatMulInteger"]
+    assert all(p["variant"].startswith("+Cast+Scale+Bias") for p in mm)
+    assert sum(p["variant"].endswith("+Group3") for p in mm) == layers
+    assert sum("+Gelu" in p["variant"] for p in mm) == layers
+    # bit-exact fused chains (no Gelu): device vs the oracle on the device's inputs
+    s = G.Session(g)
+    s.set_input("input", x)
+    s.run()
+    plan = s.plan()
+    cache = {}
+
+    def dv(name):
+        if name not in cache:
+            cache[name] = s.output(name)[0]
+        return cache[name]
+
+    env = GO.run_plan(plan, g, {"input": x}, lambda n: s.tensor_info(n)[3], source=dv)
+    exact = 0
+    for p in mm:
+        if "+Gelu" in p["variant"]:
+            continue
+        o = p["outputs"][0]
+        assert np.array_equal(dv(o).view(np.uint32), env[o].view(np.uint32)), p["name"]
+        exact += 1
+    assert exact == 5 * layers
+
+
 @pytest.mark.parametrize("name", ["resnet50", "mobilenetv2", "bert", "qoperator", "concat_b1", "concat_b2"])
 def test_memory_planning(dev, name):
     """The device memory planner (shared arena slots, in-place outputs,

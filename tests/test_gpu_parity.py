@@ -817,3 +817,70 @@ def test_conv_integer(dev, xdt, wdt, per_ch, s, p, d, group, shape):
     ref = O.conv_integer(x, w, x_zp, w_zp, s, p, d, group)
     y = H.conv_integer(to_dev(x, dev), to_dev(w, dev), x_zp, w_zp, s, p, d, group)
     assert np.array_equal(to_np(y), ref)
+
+
+@pytest.mark.parametrize("m,n,k,batch,a_dt,b_dt,bias", [
+    (40, 136, 96, 3, np.uint8, np.int8, True), (128, 768, 768, 2, np.uint8, np.int8, True),
+    (70, 64, 48, 1, np.int8, np.int8, False), (33, 200, 64, 2, np.uint8, np.uint8, True)])
+def test_matmul_integer_scaled(dev, m, n, k, batch, a_dt, b_dt, bias):
+    """MatMulInteger (constant B, device zero point of A) -> Cast -> Mul by
+    fl(a_scale * w_scale[n]) -> Add(bias[n]) in one kernel: the bits equal
+    the oracle's exact int32 MatMulInteger followed by the same three IEEE
+    binary32 operations (MatMulInteger.cpp:11-150, Cast.cpp, binary_math)."""
+    import torch
+    rng = np.random.default_rng(m * n + k)
+    lo, hi = (0, 256) if a_dt == np.uint8 else (-128, 128)
+    a = rng.integers(lo, hi, (batch, m, k), dtype=a_dt)
+    b = rng.integers(-127, 128, (k, n), dtype=np.int8) if b_dt == np.int8 else \
+        rng.integers(0, 256, (k, n), dtype=np.uint8)
+    b_zp = 128 if b_dt == np.uint8 else 0
+    ws = rng.uniform(1e-4, 2e-3, n).astype(np.float32)
+    bi = rng.standard_normal(n).astype(np.float32) if bias else None
+    a_s, a_zp = np.float32(0.0173), (91 if a_dt == np.uint8 else -7)
+    op = H.MatMulIntegerScaled(b, ws, bi, m=m, a_dtype=a_dt, b_zp=b_zp)
+    s = torch.tensor([a_s], dtype=torch.float32, device=dev)
+    z = torch.tensor([a_zp], dtype=torch.uint8 if a_dt == np.uint8 else torch.int8, device=dev)
+    y = to_np(op(to_dev(a, dev), a_scale_dev=s, a_zp_dev=z))
+    acc = O.matmul_integer(a, b, a_zp, b_zp)
+    ref = acc.astype(np.float32) * (a_s * ws).astype(np.float32)
+    if bias:
+        ref = (ref + bi).astype(np.float32)
+    assert np.array_equal(y.view(np.uint32), ref.astype(np.float32).view(np.uint32))
+
+
+def test_matmul_integer_scaled_group_gelu_minmax(dev):
+    """Three scaled MatMulIntegers sharing A as one grouped launch, each
+    member equal to its own launch bit for bit; and one with Gelu and
+    min / max pairs whose DynamicQuantizeLinear matches the two-pass one."""
+    import torch
+    rng = np.random.default_rng(41)
+    m, k, n, batch = 128, 192, 136, 2
+    a = to_dev(rng.integers(0, 256, (batch, m, k), dtype=np.uint8), dev)
+    s = torch.tensor([0.021], dtype=torch.float32, device=dev)
+    z = torch.tensor([133], dtype=torch.uint8, device=dev)
+    ops = [H.MatMulIntegerScaled(rng.integers(-127, 128, (k, n), dtype=np.int8),
+                                 rng.uniform(1e-4, 2e-3, n).astype(np.float32),
+                                 rng.standard_normal(n).astype(np.float32), m=m) for _ in range(3)]
+    singles = [to_np(o(a, a_scale_dev=s, a_zp_dev=z)) for o in ops]
+    grp = H.QLinearMatMulGroup(ops)
+    ys = [torch.empty((batch, m, n), dtype=torch.float32, device=dev) for _ in ops]
+    grp(a, ys, a_scale_dev=s, a_zp_dev=z)
+    for y, ref in zip(ys, singles):
+        assert np.array_equal(to_np(y).view(np.uint32), ref.view(np.uint32))
+    g = H.MatMulIntegerScaled(rng.integers(-127, 128, (k, n), dtype=np.int8),
+                              rng.uniform(1e-4, 2e-3, n).astype(np.float32),
+                              rng.standard_normal(n).astype(np.float32), m=m)
+    plain = to_dev(to_np(g(a, a_scale_dev=s, a_zp_dev=z)), dev)
+    g_ref = torch.empty_like(plain)
+    from nnr_amd import _lib
+    _lib.check(_lib.lib().nnrh_gelu_f32(plain.data_ptr(), g_ref.data_ptr(), plain.numel(), _lib.cur_stream()))
+    g.fuse_gelu()
+    cnt = g.minmax_count(batch)
+    parts = torch.full((2 * cnt,), float("nan"), dtype=torch.float32, device=dev)
+    g.set_minmax_out(parts)
+    y = g(a, a_scale_dev=s, a_zp_dev=z)
+    assert np.array_equal(to_np(y).view(np.uint32), to_np(g_ref).view(np.uint32))
+    q1, s1, z1 = H.dynamic_quantize_linear_parts(y, parts)
+    q0, s0, z0 = H.dynamic_quantize_linear(y)
+    assert to_np(s1)[0] == to_np(s0)[0] and to_np(z1)[0] == to_np(z0)[0]
+    assert np.array_equal(to_np(q1), to_np(q0))
