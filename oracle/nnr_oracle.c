@@ -17,6 +17,10 @@
 
 static int g_contract = 0;
 static int g_threads = 0;
+static int g_vnni = 0;   /* 1: accumulators through the AVX-512 VNNI restatement */
+
+void orc_set_vnni(int on) { g_vnni = on && orc_vnni_available(); }
+int orc_get_vnni(void) { return g_vnni; }
 
 void orc_set_contract(int on) { g_contract = on ? 1 : 0; }
 int orc_get_contract(void) { return g_contract; }
@@ -297,6 +301,20 @@ int orc_qlinear_matmul(int batch, int m, int n, int k,
     float cm = orc_qmatmul_combined_scale(a_scale, b_scale, y_scale, sd);
     (void)ld_scale;
     int lo, hi; dtype_range(y_dtype, &lo, &hi);
+    if (g_vnni && batch_b <= 1) {
+        /* the packed VNNI GEMM's exact accumulators, then RQ-D */
+        int32_t* acc = (int32_t*)malloc(sizeof(int32_t) * (size_t)batch * m * n);
+        const int rc = orc_vnni_matmul_integer(batch, m, n, k, a, a_dtype,
+                                               batch_a <= 1 ? 0 : (long long)m * k, b, b_dtype, azp, bzp, acc);
+        if (rc == 0) {
+            #pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+            for (long long i = 0; i < (long long)batch * m * n; i++)
+                st_q(y, y_dtype, (size_t)i, orc_rq_d(acc[i], cm, yzp, lo, hi));
+            free(acc);
+            return 0;
+        }
+        free(acc);
+    }
     for (int bi = 0; bi < batch; bi++) {
         size_t aoff = batch_a <= 1 ? 0 : (size_t)bi * m * k;
         size_t boff = batch_b <= 1 ? 0 : (size_t)bi * k * n;
@@ -339,6 +357,19 @@ int orc_matmul_integer(const int* a_dims, int a_nd, const void* a, int a_dtype,
     }
     int m = ad[nd - 2], k = ad[nd - 1], n = bd[nd - 1];
     if (bd[nd - 2] != k) return -1;
+    if (g_vnni) {
+        /* B shared by every batch: the packed VNNI GEMM */
+        int bshared = 1;
+        long long nbat = 1;
+        for (int i = 0; i < nd - 2; i++) {
+            if (bd[i] != 1) bshared = 0;
+            nbat *= ad[i];
+        }
+        if (bshared && nbat < 0x7fffffff &&
+            orc_vnni_matmul_integer((int)nbat, m, n, k, a, a_dtype, (long long)m * k, b, b_dtype, a_zp, b_zp,
+                                    y) == 0)
+            return 0;
+    }
     size_t nb = 1;
     for (int i = 0; i < nd - 2; i++) {
         if (ad[i] != bd[i] && ad[i] > 1 && bd[i] > 1) return -1;
@@ -420,6 +451,11 @@ int orc_conv_dispatch(const orc_conv_params* p) {
 
 void orc_conv_acc(const orc_conv_params* p, const void* x, const int8_t* w,
                   int32_t* acc) {
+    if (g_vnni) {
+        /* the same exact accumulators from the AVX-512 VNNI restatement */
+        if (p->group == p->C && p->OC == p->C && p->C > 1 && orc_vnni_depthwise_acc(p, x, w, acc) == 0) return;
+        if (p->group == 1 && orc_vnni_conv_acc(p, x, w, acc) == 0) return;
+    }
     const int N = p->N, C = p->C, H = p->H, W = p->W;
     const int OC = p->OC, kH = p->kH, kW = p->kW, G = p->group;
     const int Cg = C / G, OCg = OC / G, oH = p->oH, oW = p->oW;
@@ -479,7 +515,15 @@ void orc_conv_acc(const orc_conv_params* p, const void* x, const int8_t* w,
     free(ws);
 }
 
+/* acc_nhwc: accumulators laid out [N][oH][oW][OC] instead of [N][OC][oH][oW]
+ * (the VNNI restatement's row-major output); the loop then walks pixels */
+static int conv_epilogue(const orc_conv_params* p, const int32_t* acc, void* y, int acc_nhwc);
+
 int orc_qlinear_conv_from_acc(const orc_conv_params* p, const int32_t* acc, void* y) {
+    return conv_epilogue(p, acc, y, 0);
+}
+
+static int conv_epilogue(const orc_conv_params* p, const int32_t* acc, void* y, int acc_nhwc) {
     const int br = orc_conv_dispatch(p);
     const int N = p->N, OC = p->OC, oH = p->oH, oW = p->oW, sp = oH * oW;
     int lo, hi; dtype_range(p->act_dtype, &lo, &hi);
@@ -508,13 +552,18 @@ int orc_qlinear_conv_from_acc(const orc_conv_params* p, const int32_t* acc, void
             if (tile_h > oH) tile_h = oH;
         }
     }
+    /* the same per-element work in either order: (n, oc) planes for
+     * [N][OC][..] accumulators, (n, pixel) rows for [N][..][OC] ones */
+    const long long outer = acc_nhwc ? (long long)N * sp : (long long)N * OC;
+    const int inner = acc_nhwc ? OC : sp;
     #pragma omp parallel for schedule(static) num_threads(orc_get_threads())
-    for (long long no = 0; no < (long long)N * OC; no++) {
-        int n = (int)(no / OC), oc = (int)(no % OC);
-        for (int oh = 0; oh < oH; oh++)
-            for (int ow = 0; ow < oW; ow++) {
-                int s = oh * oW + ow;
-                int32_t a = acc[((size_t)n * OC + oc) * sp + s];
+    for (long long oi = 0; oi < outer; oi++) {
+        for (int ii = 0; ii < inner; ii++) {
+                const int n = (int)(acc_nhwc ? oi / sp : oi / OC);
+                const int oc = acc_nhwc ? ii : (int)(oi % OC);
+                const int s = acc_nhwc ? (int)(oi % sp) : ii;
+                const int oh = s / oW, ow = s % oW;
+                int32_t a = acc_nhwc ? acc[((size_t)n * sp + s) * OC + oc] : acc[((size_t)n * OC + oc) * sp + s];
                 int q;
                 int32_t b32 = p->bias ? p->bias[oc] : 0;
                 switch (br) {
@@ -567,6 +616,11 @@ int orc_qlinear_conv_from_acc(const orc_conv_params* p, const int32_t* acc, void
 
 int orc_qlinear_conv(const orc_conv_params* p, const void* x, const int8_t* w, void* y) {
     int32_t* acc = (int32_t*)malloc(sizeof(int32_t) * (size_t)p->N * p->OC * p->oH * p->oW);
+    if (g_vnni && p->group == 1 && orc_vnni_conv_acc_layout(p, x, w, acc, 1) == 0) {
+        int br = conv_epilogue(p, acc, y, 1);
+        free(acc);
+        return br;
+    }
     orc_conv_acc(p, x, w, acc);
     int br = orc_qlinear_conv_from_acc(p, acc, y);
     free(acc);
@@ -1021,6 +1075,44 @@ void orc_conv_integer(const void* x, int x_dt, const void* w, int w_dt, int x_zp
                       int iH, int iW, int OC, int kH, int kW, int sH, int sW, int pH, int pW, int dH, int dW, int oH,
                       int oW, int group, int32_t* y) {
     const int CC = C / group, MM = OC / group;
+    if (g_vnni && group == 1 && w_dt) {
+        /* the same values from the AVX-512 VNNI convolution: acc = sum
+         * (x - x_zp) w over in-image taps, then y = acc - w_zp[oc] S with
+         * S = sum (x - x_zp) over the output pixel's in-image taps */
+        orc_conv_params p;
+        memset(&p, 0, sizeof p);
+        p.N = N; p.C = C; p.H = iH; p.W = iW; p.OC = OC; p.kH = kH; p.kW = kW; p.group = 1;
+        p.sH = sH; p.sW = sW; p.dH = dH; p.dW = dW; p.pad_t = p.pad_b = pH; p.pad_l = p.pad_r = pW;
+        p.oH = oH; p.oW = oW; p.act_dtype = x_dt ? ORC_S8 : ORC_U8; p.x_zp = x_zp;
+        if (orc_vnni_conv_acc(&p, x, (const int8_t*)w, y) == 0) {
+            #pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+            for (int n = 0; n < N; ++n) {
+                int32_t* xs = (int32_t*)malloc(sizeof(int32_t) * (size_t)iH * iW);
+                for (int i = 0; i < iH * iW; ++i) xs[i] = 0;
+                for (int c = 0; c < C; ++c)
+                    for (int i = 0; i < iH * iW; ++i)
+                        xs[i] += (x_dt ? (int)((const int8_t*)x)[((size_t)n * C + c) * iH * iW + i]
+                                       : (int)((const uint8_t*)x)[((size_t)n * C + c) * iH * iW + i]) - x_zp;
+                for (int oh = 0; oh < oH; ++oh)
+                    for (int ow = 0; ow < oW; ++ow) {
+                        int32_t s = 0;
+                        for (int kh = 0; kh < kH; ++kh) {
+                            const int ih = oh * sH - pH + kh * dH;
+                            if (ih < 0 || ih >= iH) continue;
+                            for (int kw = 0; kw < kW; ++kw) {
+                                const int iw = ow * sW - pW + kw * dW;
+                                if (iw >= 0 && iw < iW) s += xs[ih * iW + iw];
+                            }
+                        }
+                        for (int oc = 0; oc < OC; ++oc)
+                            y[(((size_t)n * OC + oc) * oH + oh) * oW + ow] -=
+                                (int32_t)((uint32_t)wzp[oc] * (uint32_t)s);
+                    }
+                free(xs);
+            }
+            return;
+        }
+    }
 #define LX(i) (x_dt ? (int)((const int8_t*)x)[i] : (int)((const uint8_t*)x)[i])
 #define LW(i) (w_dt ? (int)((const int8_t*)w)[i] : (int)((const uint8_t*)w)[i])
     for (int n = 0; n < N; ++n)

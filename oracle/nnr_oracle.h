@@ -27,6 +27,11 @@ extern "C" {
 #endif
 
 /* ---- configuration -------------------------------------------------- */
+/* 1: conv / matmul accumulators through the AVX-512 VNNI restatement of
+ * nnr_vnni.c (the CPU baseline; same exact int32 values), when the host has
+ * AVX-512 VNNI; 0 (default): the scalar loops */
+void orc_set_vnni(int on);
+int orc_get_vnni(void);
 void orc_set_contract(int on);
 int  orc_get_contract(void);
 
@@ -172,6 +177,28 @@ void orc_batchnorm_u8(const void* x, int x_f32, uint8_t* y, const float* A, cons
 void orc_conv_integer(const void* x, int x_dt, const void* w, int w_dt, int x_zp, const int32_t* wzp, int N, int C,
                       int iH, int iW, int OC, int kH, int kW, int sH, int sW, int pH, int pW, int dH, int dW, int oH,
                       int oW, int group, int32_t* y);
+
+/* ---- AVX-512 VNNI restatement (nnr_vnni.c) -------------------------- */
+int orc_vnni_available(void);
+/* physical cores / logical threads for int8_compute_threads (0: detect) */
+void orc_set_host_threads(int physical, int logical);
+int orc_int8_compute_threads(int work_items, long long total_ops);
+/* 1: keep packed weights across calls (keyed by address, shape and a hash
+ * of the bytes), as the reference packs once in reshape(); 0: pack per
+ * call. Either call drops the cache. */
+void orc_vnni_cache(int on);
+/* group-1 convolution; -1 when not applicable (no VNNI, groups, per-channel
+ * w_zp): exact accumulators [N][OC][oH][oW] as orc_conv_acc */
+int orc_vnni_conv_acc(const orc_conv_params* p, const void* x, const int8_t* w, int32_t* acc);
+/* acc_nhwc: accumulators [N][oH][oW][OC] (the GEMM's own row-major order) */
+int orc_vnni_conv_acc_layout(const orc_conv_params* p, const void* x, const int8_t* w, int32_t* acc,
+                             int acc_nhwc);
+/* depthwise on NHWC input, 16 channels per vector (vpmulld) */
+int orc_vnni_depthwise_acc(const orc_conv_params* p, const void* x, const int8_t* w, int32_t* acc);
+/* y[b][m][n] = sum_k (a - a_zp)(b - b_zp); A [batch] x [m][k] at a_bstride,
+ * B [k][n] shared */
+int orc_vnni_matmul_integer(int batch, int m, int n, int k, const void* a, int a_dtype, long long a_bstride,
+                            const void* b, int b_dtype, int a_zp, int b_zp, int32_t* y);
 
 #ifdef __cplusplus
 }

@@ -44,6 +44,12 @@ def lib():
         P = ct.POINTER
         sigs = {
             "orc_set_contract": (None, [i]),
+            "orc_set_vnni": (None, [i]),
+            "orc_get_vnni": (i, []),
+            "orc_vnni_available": (i, []),
+            "orc_set_host_threads": (None, [i, i]),
+            "orc_int8_compute_threads": (i, [i, ct.c_longlong]),
+            "orc_vnni_cache": (None, [i]),
             "orc_set_threads": (None, [i]),
             "orc_get_threads": (i, []),
             "orc_f32_to_f16": (ct.c_uint16, [f]),
@@ -370,3 +376,16 @@ class Conv1d:
         y = np.empty(self.out_shape, self.act_dtype)
         br = lib().orc_qlinear_conv1d(ct.byref(self.c.p), _p(x), _p(w), _p(y))
         return y, br
+
+
+def set_vnni(on: bool) -> bool:
+    """Route conv / matmul accumulators through the AVX-512 VNNI
+    restatement (nnr_vnni.c); returns whether it is active (needs AVX-512
+    VNNI on this host)."""
+    lib().orc_set_vnni(1 if on else 0)
+    return bool(lib().orc_get_vnni())
+
+
+def vnni_available() -> bool:
+    return bool(lib().orc_vnni_available())
+

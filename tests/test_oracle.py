@@ -743,3 +743,108 @@ def test_hardswish_post_op_adds_zero_bias():
     rng = np.random.default_rng(1)
     x = rng.uniform(-4, 4, 100).astype(np.float32)
     assert np.array_equal(O.hardswish(x), O.hardswish(x, post_op=True))
+
+
+# ---------------------------------------------------------------------------
+# the AVX-512 VNNI restatement (the CPU baseline) against the scalar loops
+
+def _vnni_or_skip():
+    if not O.vnni_available():
+        pytest.skip("host has no AVX-512 VNNI")
+
+
+@pytest.mark.parametrize("N,C,H,W,OC,k,s,p,d,nhwc,act,wzp", [
+    (2, 64, 9, 11, 72, 3, 1, 1, 1, 1, np.uint8, 0),     # NR16-like, OC not a multiple of 48
+    (1, 3, 23, 19, 16, 7, 2, 3, 1, 0, np.uint8, 0),     # first layer, NCHW input
+    (2, 40, 7, 7, 50, 1, 1, 0, 1, 1, np.uint8, 0),      # 1x1, K % 4 != 0
+    (1, 16, 12, 10, 24, 3, 2, 1, 2, 1, np.int8, 3),     # int8 activations, dilation, w_zp
+    (3, 8, 6, 5, 96, 5, 1, 2, 1, 0, np.uint8, 250),     # w_zp read through uint8
+])
+def test_vnni_conv_acc_equals_scalar(N, C, H, W, OC, k, s, p, d, nhwc, act, wzp):
+    _vnni_or_skip()
+    rng = np.random.default_rng(N * C + H + OC)
+    lo, hi = (0, 256) if act == np.uint8 else (-128, 128)
+    shape = (N, H, W, C) if nhwc else (N, C, H, W)
+    x = rng.integers(lo, hi, shape, dtype=act)
+    w = rng.integers(-128, 128, (OC, C, k, k), dtype=np.int8)
+    cv = O.Conv(N, C, H, W, OC, k, k, stride=(s, s), dil=(d, d), pads=(p, p, p, p), x_nhwc=nhwc,
+                act_dtype=act, x_zp=int(rng.integers(lo, hi)), w_zp=(np.int8(np.uint8(wzp).view(np.int8)),))
+    ref = cv.acc(x, w)
+    try:
+        O.set_vnni(True)
+        got = cv.acc(x, w)
+    finally:
+        O.set_vnni(False)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("C,k,s", [(32, 3, 1), (40, 3, 2), (16, 5, 1)])
+def test_vnni_depthwise_acc_equals_scalar(C, k, s):
+    _vnni_or_skip()
+    rng = np.random.default_rng(C + k)
+    N, H, W = 2, 9, 13
+    x = rng.integers(0, 256, (N, H, W, C), dtype=np.uint8)
+    w = rng.integers(-128, 128, (C, 1, k, k), dtype=np.int8)
+    cv = O.Conv(N, C, H, W, C, k, k, group=C, stride=(s, s), pads=(k // 2,) * 4, x_nhwc=1, y_nhwc=1,
+                x_zp=117, w_zp=rng.integers(-5, 5, C).astype(np.int8))
+    ref = cv.acc(x, w)
+    try:
+        O.set_vnni(True)
+        got = cv.acc(x, w)
+    finally:
+        O.set_vnni(False)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("adt,bdt,azp,bzp", [(np.uint8, np.int8, 131, 0), (np.int8, np.int8, -9, 4),
+                                             (np.uint8, np.uint8, 7, 200), (np.int8, np.uint8, 0, 128)])
+def test_vnni_matmul_equals_scalar(adt, bdt, azp, bzp):
+    _vnni_or_skip()
+    rng = np.random.default_rng(abs(azp) + bzp)
+    rnd = lambda dt, shape: rng.integers(0 if dt == np.uint8 else -128, 256 if dt == np.uint8 else 128, shape,
+                                         dtype=dt)
+    a = rnd(adt, (3, 53, 70))
+    b = rnd(bdt, (70, 101))
+    ref = O.matmul_integer(a, b, azp, bzp)
+    try:
+        O.set_vnni(True)
+        got = O.matmul_integer(a, b, azp, bzp)
+        q = O.qlinear_matmul(a[0], 0.02, azp, b, 0.005, bzp, 0.05, 128) if adt == np.uint8 else None
+    finally:
+        O.set_vnni(False)
+    assert np.array_equal(got, ref)
+    if q is not None:
+        assert np.array_equal(q, O.qlinear_matmul(a[0], 0.02, azp, b, 0.005, bzp, 0.05, 128))
+
+
+@pytest.mark.parametrize("xdt,s,p,d", [(np.uint8, 1, 1, 1), (np.int8, 2, 0, 1), (np.uint8, 1, 2, 2)])
+def test_vnni_conv_integer_equals_scalar(xdt, s, p, d):
+    _vnni_or_skip()
+    rng = np.random.default_rng(s + 3 * p + 7 * d)
+    lo, hi = (0, 256) if xdt == np.uint8 else (-128, 128)
+    x = rng.integers(lo, hi, (2, 24, 11, 9), dtype=xdt)
+    w = rng.integers(-128, 128, (40, 24, 3, 3), dtype=np.int8)
+    wz = rng.integers(-8, 8, 40).astype(np.int32)
+    xz = int(rng.integers(lo, hi))
+    ref = O.conv_integer(x, w, xz, wz, (s, s), (p, p), (d, d))
+    try:
+        O.set_vnni(True)
+        got = O.conv_integer(x, w, xz, wz, (s, s), (p, p), (d, d))
+    finally:
+        O.set_vnni(False)
+    assert np.array_equal(got, ref)
+
+
+def test_int8_compute_threads_heuristic():
+    """thread_pool.h:725-737: serial below 2^20 ops, physical cores below
+    phys * 2^22 ops, every logical thread above, never more than the work."""
+    O.lib().orc_set_host_threads(8, 16)
+    try:
+        f = O.lib().orc_int8_compute_threads
+        assert f(100, (1 << 20) - 1) == 1
+        assert f(100, 1 << 20) == 8
+        assert f(100, 8 * (1 << 22) - 1) == 8
+        assert f(100, 8 * (1 << 22)) == 16
+        assert f(3, 1 << 40) == 3
+    finally:
+        O.lib().orc_set_host_threads(0, 0)
