@@ -45,8 +45,14 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 namespace {
 
+// LDS image of a K-step: one row of BK bytes per A / B row, its 16-byte
+// chunks XOR-swizzled by (row >> 1) so that the 16 rows one ds_read_b128
+// touches spread over the banks
+template <int BK>
+__device__ __forceinline__ int dma_swz(int row) { return (row >> 1) & (BK / 16 - 1); }
+template <int BK>
 __device__ __forceinline__ int dma_lds_off(int row, int c) {
-    return row * 64 + ((c ^ ((row >> 1) & 3)) << 4);
+    return row * BK + ((c ^ dma_swz<BK>(row)) << 4);
 }
 
 // 256 x 16 bytes: chunk b holds 16 copies of byte b (pad source for the DMA)
@@ -117,21 +123,31 @@ template <int BM, int BN, int S, int NPX, int FUSE>
 constexpr int dma_pslot_bytes() {
     return ((NPX * BN * 4 + 1023) / 1024) * 1024 + (FUSE == FUSE_ADD ? BM * BN : 0);
 }
-template <int BM, int BN, int S, int NPX, int FUSE>
-constexpr int dma_lds_bytes() { return S * (BM + BN) * 64 + S * dma_pslot_bytes<BM, BN, S, NPX, FUSE>(); }
+template <int BM, int BN, int S, int NPX, int FUSE, int BK>
+constexpr int dma_lds_bytes() { return S * (BM + BN) * BK + S * dma_pslot_bytes<BM, BN, S, NPX, FUSE>(); }
 // blocks per CU the kernel is compiled for: LDS and registers must fit them
-template <int BM, int BN, int S, int NPX, int FUSE>
-constexpr int dma_min_blocks() { return dma_lds_bytes<BM, BN, S, NPX, FUSE>() * 3 <= 160 * 1024 ? 3 : 2; }
+template <int BM, int BN, int S, int NPX, int FUSE, int BK>
+constexpr int dma_min_blocks() { return dma_lds_bytes<BM, BN, S, NPX, FUSE, BK>() * 3 <= 160 * 1024 ? 3 : 2; }
 
-template <int BM, int BN, int S, int AMODE, int EPI, int FUSE>
-__global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S, EpiParams<EPI>::NP + (FUSE == FUSE_DQB ? 1 : 0), FUSE>()))
+// BK: K bytes per pipeline stage, 64 (one MFMA K-step) or 128 (two). A
+// 128-byte stage fetches whole 128-byte rows with each DMA instruction (8
+// rows x 8 lanes instead of 16 rows x 4 lanes: twice the rate out of L2)
+// and halves the barriers per K.
+template <int BM, int BN, int S, int AMODE, int EPI, int FUSE, int BK>
+__global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S, EpiParams<EPI>::NP + (FUSE == FUSE_DQB ? 1 : 0), FUSE,
+                                                  BK>()))
 void qgemm_dma_kernel(GemmArgs g) {
     constexpr int WAVES_N = BN / 64;
     static_assert((BM / 64) * WAVES_N == 4, "4 waves of 64x64");
-    constexpr int A_CH = BM / 64;            // DMA chunks per thread per step (A)
-    constexpr int B_CH = BN / 64;            // (B)
+    static_assert(BK == 64 || BK == 128, "stage width");
+    static_assert(BK == 64 || AMODE != A_CONV4, "first layer: 64-byte stages");
+    constexpr int CPR = BK / 16;             // 16-byte chunks per LDS row
+    constexpr int RPR = 4096 / BK;           // rows one DMA round of 256 threads fills
+    constexpr int A_CH = BM / RPR;           // DMA chunks per thread per step (A)
+    constexpr int B_CH = BN / RPR;           // (B)
+    constexpr int KK = BK / 64;              // MFMA K-steps per stage
     constexpr int LPS = A_CH + B_CH;         // DMA instructions per thread per step
-    constexpr int STAGE = (BM + BN) * 64;    // bytes per K-step
+    constexpr int STAGE = (BM + BN) * BK;    // bytes per K-step
     constexpr int NP = EpiParams<EPI>::NP;
     constexpr int NPX = NP + (FUSE == FUSE_DQB ? 1 : 0);   // + the fp32 bias
     constexpr int PBYTES = NPX * BN * 4;
@@ -182,7 +198,7 @@ void qgemm_dma_kernel(GemmArgs g) {
         n0 = (r - mb * nbn) * BN;
     };
 
-    const int nk = g.Kp >> 6;
+    const int nk = g.Kp / BK;
     const uint32_t xmask = (uint32_t)g.a_xor * 0x01010101u;
     // zero-point column term from the activation zero point (host value or,
     // after DynamicQuantizeLinear, one byte in device memory)
@@ -211,7 +227,7 @@ void qgemm_dma_kernel(GemmArgs g) {
     const int sp_out = g.oH * g.oW;
     // this thread's 16-byte chunk of a 64-byte row (pre-swizzled so the LDS
     // image matches dma_lds_off)
-    const int cdma = (tid & 3) ^ ((tid >> 3) & 3);
+    const int cdma = (tid % CPR) ^ dma_swz<BK>(tid / CPR);
 
     // ---- producer (DMA issue) state
     int p_t = t_first, p_kt = 0, p_gs = 0;
@@ -238,7 +254,7 @@ void qgemm_dma_kernel(GemmArgs g) {
         p_pbase = (long long)z * g.param_bstride;
 #pragma unroll
         for (int j = 0; j < A_CH; ++j) {
-            const int m = m0 + (tid >> 2) + 64 * j;
+            const int m = m0 + tid / CPR + RPR * j;
             a_ok[j] = m < g.M;
             const int mm = a_ok[j] ? m : 0;
             if constexpr (AMODE == A_DENSE) {
@@ -284,7 +300,7 @@ void qgemm_dma_kernel(GemmArgs g) {
         }
 #pragma unroll
         for (int j = 0; j < B_CH; ++j) {
-            int n = p_n0 + (tid >> 2) + 64 * j;
+            int n = p_n0 + tid / CPR + RPR * j;
             n = n < g.Np ? n : g.Np - 1;
             b_addr[j] = (uint64_t)(pb + (long long)n * g.Kp + cdma * 16);
         }
@@ -303,13 +319,13 @@ void qgemm_dma_kernel(GemmArgs g) {
     // issue the DMA of producer step (p_t, p_kt) into the stage at p_stage
     auto p_issue = [&]() {
         uint8_t* st = lds + p_stage;
-        const int k0 = p_kt << 6;
+        const int k0 = p_kt * BK;
 #pragma unroll
         for (int j = 0; j < A_CH; ++j) {
             const uint8_t* src = pad16;
             if constexpr (AMODE == A_DENSE) {
                 bool ok = a_ok[j];
-                if (k0 + 64 > g.K) ok = ok && (k0 + cdma * 16 < g.K);   // K padding
+                if (k0 + BK > g.K) ok = ok && (k0 + cdma * 16 < g.K);   // K padding
                 if (ok) src = (const uint8_t*)(a_addr[j] + (uint64_t)k0);
             } else if constexpr (AMODE == A_CONVU) {
                 if ((a_tmask[j] >> u_tap) & 1u) src = (const uint8_t*)(a_addr[j] + (uint64_t)(long long)u_off);
@@ -332,7 +348,7 @@ void qgemm_dma_kernel(GemmArgs g) {
         }
 #pragma unroll
         for (int j = 0; j < B_CH; ++j)
-            dma16((const void*)(b_addr[j] + (uint64_t)k0), st + BM * 64 + wave * 1024 + j * 4096);
+            dma16((const void*)(b_addr[j] + (uint64_t)k0), st + BM * BK + wave * 1024 + j * 4096);
         if (p_kt == 0 && wave < PWAVES) {
             // per-column constants of the tile: NP arrays of BN int32/float,
             // one 16-byte chunk per lane; chunks past the arrays reload the
@@ -376,17 +392,17 @@ void qgemm_dma_kernel(GemmArgs g) {
         ++p_gs;
         p_stage = p_stage + STAGE == S * STAGE ? 0 : p_stage + STAGE;
         if constexpr (AMODE == A_CONV) {
-            kc_ic += 64;
+            kc_ic += BK;
             while (kc_ic >= g.C) {
                 kc_ic -= g.C;
                 if (++kc_kw == g.kW) { kc_kw = 0; ++kc_kh; }
             }
         }
         if constexpr (AMODE == A_CONVU) {
-            // C % 64 == 0: the next step is the next 64 channels of this tap,
-            // or the first 64 of the next tap (taps in (kh, kw) order)
-            u_ic += 64;
-            u_off += 64;
+            // C % BK == 0: the next step is the next BK channels of this tap,
+            // or the first BK of the next tap (taps in (kh, kw) order)
+            u_ic += BK;
+            u_off += BK;
             if (u_ic == g.C) {
                 u_ic = 0;
                 ++u_tap;
@@ -692,20 +708,22 @@ void qgemm_dma_kernel(GemmArgs g) {
         block_barrier();
         if (p_t < t_end) p_issue();
     };
-    auto read_frags = [&](int stage, v4i (&xf)[4], v4i (&wf)[4]) {
+    // fragments of MFMA K-step kk (of KK) of a stage
+    auto read_frags = [&](int stage, int kk, v4i (&xf)[4], v4i (&wf)[4]) {
         const uint8_t* st = lds + stage;
+        const int c = kk * 4 + fchunk;
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) {
-            v4i v = *(const v4i*)(st + dma_lds_off(wm * 64 + tm * 16 + frow, fchunk));
+            v4i v = *(const v4i*)(st + dma_lds_off<BK>(wm * 64 + tm * 16 + frow, c));
             xf[tm] = v4i{(int)((uint32_t)v.x ^ xmask), (int)((uint32_t)v.y ^ xmask),
                          (int)((uint32_t)v.z ^ xmask), (int)((uint32_t)v.w ^ xmask)};
         }
 #pragma unroll
         for (int tn = 0; tn < 4; ++tn)
-            wf[tn] = *(const v4i*)(st + BM * 64 + dma_lds_off(wn * 64 + tn * 16 + frow, fchunk));
+            wf[tn] = *(const v4i*)(st + BM * BK + dma_lds_off<BK>(wn * 64 + tn * 16 + frow, c));
     };
-    auto mma = [&](const v4i (&xf)[4], const v4i (&wf)[4]) {
-        if (c_kt == 0) {
+    auto mma = [&](const v4i (&xf)[4], const v4i (&wf)[4], bool first) {
+        if (first) {
             // the tile's constants landed with its first K-step: the first
             // MFMAs start from c0[n] (this lane's 16 columns), or from
             // -alpha * colsum[n] when the zero point is only known now
@@ -764,9 +782,12 @@ void qgemm_dma_kernel(GemmArgs g) {
 
     for (;;) {
         sync_step(c_gs);
-        v4i xf[4], wf[4];
-        read_frags(c_stage, xf, wf);
-        mma(xf, wf);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            v4i xf[4], wf[4];
+            read_frags(c_stage, kk, xf, wf);
+            mma(xf, wf, kk == 0 && c_kt == 0);
+        }
         if (!finish_step()) break;
     }
     // nothing may be left in flight into LDS when the block retires
@@ -775,9 +796,9 @@ void qgemm_dma_kernel(GemmArgs g) {
 
 namespace {
 
-template <int BM, int BN, int S, int AMODE, int EPI, int FUSE = FUSE_NONE>
+template <int BM, int BN, int S, int AMODE, int EPI, int FUSE = FUSE_NONE, int BK = 64>
 hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
-    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI, FUSE>;
+    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI, FUSE, BK>;
     const long long tiles = (long long)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN) * batch;
     // resident blocks of this instantiation (occupancy x CUs), computed once
     static int resident = 0;
@@ -810,27 +831,28 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int BM, int BN, int S, int AMODE, int S_ADD = S>
+template <int BM, int BN, int S, int AMODE, int S_ADD = S, int BK = 64>
 hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
     if (g.dq_bias) {
         if constexpr (AMODE == A_DENSE) {
-            if (g.epi == EPI_RQD) return launch_dma<BM, BN, S, AMODE, EPI_RQD, FUSE_DQB>(g, batch, s);
-            if (g.epi == EPI_I32S) return launch_dma<BM, BN, S, AMODE, EPI_I32S, FUSE_DQB>(g, batch, s);
+            if (g.epi == EPI_RQD) return launch_dma<BM, BN, S, AMODE, EPI_RQD, FUSE_DQB, BK>(g, batch, s);
+            if (g.epi == EPI_I32S) return launch_dma<BM, BN, S, AMODE, EPI_I32S, FUSE_DQB, BK>(g, batch, s);
         }
         return hipErrorNotSupported;
     }
     if (g.add_other) {
-        if constexpr (AMODE == A_CONV || AMODE == A_CONVU || AMODE == A_DENSE) {
+        // the residual tile shares the block's LDS: 64-byte stages only
+        if constexpr (BK == 64 && (AMODE == A_CONV || AMODE == A_CONVU || AMODE == A_DENSE)) {
             if (g.epi == EPI_RQB && batch == 1)
                 return launch_dma<BM, BN, S_ADD, AMODE, EPI_RQB, FUSE_ADD>(g, batch, s);
         }
         return hipErrorNotSupported;
     }
     switch (g.epi) {
-    case EPI_RQB: return launch_dma<BM, BN, S, AMODE, EPI_RQB>(g, batch, s);
-    case EPI_RQA: return launch_dma<BM, BN, S, AMODE, EPI_RQA>(g, batch, s);
-    case EPI_RQD: return launch_dma<BM, BN, S, AMODE, EPI_RQD>(g, batch, s);
-    case EPI_I32: return launch_dma<BM, BN, S, AMODE, EPI_I32>(g, batch, s);
+    case EPI_RQB: return launch_dma<BM, BN, S, AMODE, EPI_RQB, FUSE_NONE, BK>(g, batch, s);
+    case EPI_RQA: return launch_dma<BM, BN, S, AMODE, EPI_RQA, FUSE_NONE, BK>(g, batch, s);
+    case EPI_RQD: return launch_dma<BM, BN, S, AMODE, EPI_RQD, FUSE_NONE, BK>(g, batch, s);
+    case EPI_I32: return launch_dma<BM, BN, S, AMODE, EPI_I32, FUSE_NONE, BK>(g, batch, s);
     default: return hipErrorNotSupported;
     }
 }
@@ -897,10 +919,22 @@ hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t 
         }
     }
     const bool uni = conv && conv_uniform_taps(g);
+    // 128-byte stages (2 stages at 2 blocks per CU) where the packed K is a
+    // multiple of 128 with at least two stages per tile and, for the
+    // uniform-tap producer, a step stays inside one tap. Not with a fused
+    // add (its residual tile needs the LDS) nor a fused Gelu, whose long
+    // fp32 epilogue hides better behind a third resident block.
+    const bool wide = (g.Kp % 128) == 0 && g.Kp >= 256 && g.add_other == nullptr &&
+                      !(g.dq_bias != nullptr && g.dq_gelu) && (!uni || g.C % 128 == 0);
     switch (tile) {
     case TILE_128x128:
         // 3 stages at 3 blocks per CU; the fused-add variant carries a 16 KB
         // residual tile per slot and runs 2 stages at 2 blocks per CU
+        if (wide) {
+            if (!conv) return launch_dma_epi<128, 128, 2, A_DENSE, 2, 128>(g, batch, s);
+            return uni ? launch_dma_epi<128, 128, 2, A_CONVU, 2, 128>(g, batch, s)
+                       : launch_dma_epi<128, 128, 2, A_CONV, 2, 128>(g, batch, s);
+        }
         if (!conv) return launch_dma_epi<128, 128, 3, A_DENSE, 2>(g, batch, s);
         return uni ? launch_dma_epi<128, 128, 3, A_CONVU, 2>(g, batch, s)
                    : launch_dma_epi<128, 128, 3, A_CONV, 2>(g, batch, s);
