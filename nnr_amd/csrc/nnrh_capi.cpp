@@ -349,6 +349,9 @@ struct nnrh_qconv {
     bool fused_quant = false;    // nnrh_qconv_fuse_quantize was called: input is fp32
     float q_scale = 1.0f;
     int q_zp = 0;
+    bool use_stem = false;       // first layer: the one-kernel stem for uint8 input ...
+    bool use_stem_f32 = false;   // ... and for fp32 input with the quantize fused
+    StemArgs stem{};             // its arguments but x, y and the quantize
     int transform = 0;           // 0 none, 1 NCHW->NHWC, 2 NCHW->NHWC padded to 4 ch,
                                  // 3 first-layer padded multi-copy NHWC4 image,
                                  // 4 NHWC channels padded to a multiple of 16
@@ -390,6 +393,41 @@ extern "C" int nnrh_qconv_dispatch(const nnrh_qconv_desc* d, int* branch) {
     *branch = d->spatial_dims == 1 ? NNRH_BR_TYPED : conv_dispatch(d);
     return NNRH_OK;
 }
+
+namespace {
+// the first layer as one kernel (nnrh_stem.hip): output rows in groups of R
+// (R * oW pixels for the 4 waves' 16-pixel groups), an LDS ring of the rows
+// one group reads plus the next group's, strips of groups per block
+void stem_setup(nnrh_qconv_t h) {
+    const nnrh_qconv_desc& d = h->d;
+    const GemmArgs& g = h->g;
+    StemArgs a{};
+    a.w = h->wpack; a.c0 = h->c0; a.cs = h->cs; a.bf = h->bf;
+    a.N = d.N; a.C = d.C; a.H = d.H; a.W = d.W; a.oH = d.oH; a.oW = d.oW;
+    a.kH = d.kH; a.sH = d.sH; a.sW = d.sW; a.pad_t = d.pad_t; a.pad_l = d.pad_l;
+    a.cpr = g.kWp / 4; a.Kp = g.Kp; a.KS = g.Kp / 64; a.OC = d.OC;
+    a.L = round_up((d.oW - 1) * d.sW + g.kWp, 2);
+    int R = std::max(1, std::min(8, 448 / std::max(1, d.oW)));
+    while (R > 1 && (long long)R * d.sH * a.L > 2048) --R;
+    a.R = R;
+    a.WR = (R - 1) * d.sH + d.kH + R * d.sH;
+    // strips of at least two groups (the rows of the next group load while
+    // one computes), about 512 blocks over the batch (one round at two
+    // blocks per CU: each strip pays the unpipelined fill of its first rows)
+    const int groups = (d.oH + R - 1) / R;
+    const int per_img = std::max(1, std::min(groups / 2, (512 + d.N - 1) / std::max(1, d.N)));
+    a.strip = R * ((groups + per_img - 1) / per_img);
+    a.align8 = (d.sW % 2 == 0) ? 1 : 0;
+    a.sat = (g.y_type == 0 && g.L == 0 && g.hi == 255) ? 1 : 0;
+    a.inv_y = g.inv_y; a.y_zp = g.y_zp; a.qmin = g.L; a.qmax = g.hi;
+    a.fill = (uint32_t)(d.x_zp & 0xff);
+    a.q_scale = 1.0f; a.q_inv = 1.0f; a.q_zp = 0; a.qbody = 0;
+    h->stem = a;
+    const bool ok = d.dH == 1 && d.dW == 1 && g.y_type == 0;
+    h->use_stem = ok && stem_eligible(a, false);
+    h->use_stem_f32 = ok && stem_eligible(a, true);
+}
+}  // namespace
 
 extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
     if (!out) return set_err(NNRH_ERR_INVALID, "qconv: handle is NULL");
@@ -651,9 +689,11 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
         h->tile = pick_tile(OCg);
         h->vec = (h->Cx % 4 == 0 && Cgp % 4 == 0) ? pick_vec(Cgp, h->Cx, 0) : 1;
         if (G > 1 && (Cg % h->vec)) h->vec = 1;
+        if (first_copies) stem_setup(h);
     }
-    // scratch: transformed input and row sums
-    if (h->transform == 3) {
+    // scratch: transformed input and row sums (the stem kernel reads the
+    // image itself)
+    if (h->transform == 3 && !h->use_stem && !h->use_stem_f32) {
         size_t bytes = (size_t)(4 >> h->g.copy_shift) * (size_t)h->g.copy_stride;
         if ((rc = nnrh_malloc((void**)&h->xs, bytes))) return fail(rc);
     } else if (h->transform) {
@@ -680,13 +720,49 @@ namespace {
 int qconv_compute(nnrh_qconv_t h, const uint8_t* src, void* y, hipStream_t s);
 }  // namespace
 
+namespace {
+// the stem kernel's 16-byte output stores need an aligned output
+bool stem_ok(nnrh_qconv_t h, const void* x, const void* y) {
+    return ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0 && !h->fused_add;
+}
+
+// the multi-copy image of the two-kernel first layer, allocated when a
+// stem-eligible layer is first run the other way (misaligned output)
+int stem_scratch(nnrh_qconv_t h) {
+    if (h->transform != 3 || h->xs) return NNRH_OK;
+    const size_t bytes = (size_t)(4 >> h->g.copy_shift) * (size_t)h->g.copy_stride;
+    return nnrh_malloc((void**)&h->xs, bytes);
+}
+
+int run_stem(nnrh_qconv_t h, const void* x, void* y, bool f32, hipStream_t s) {
+    const nnrh_qconv_desc& d = h->d;
+    StemArgs a = h->stem;
+    a.x = x;
+    a.y = (uint8_t*)y;
+    if (f32) {
+        // QuantizeLinear over the whole [N, C, H, W] tensor: 16-wide body,
+        // scalar tail (the last n % 16 elements; all of them below 64)
+        const long long qn = (long long)d.N * d.C * d.H * d.W;
+        a.q_scale = h->q_scale;
+        a.q_inv = 1.0f / h->q_scale;
+        a.q_zp = h->q_zp;
+        a.qbody = qn >= 64 ? qn - qn % 16 : 0;
+    }
+    ProfScope ps("stem_conv", s);
+    HIP_TRY(launch_stem_conv(a, f32, s), "stem_conv");
+    return NNRH_OK;
+}
+}  // namespace
+
 extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stream) {
     if (!h || !x || !y) return set_err(NNRH_ERR_INVALID, "qconv_run: NULL argument");
     if (h->fused_quant) return set_err(NNRH_ERR_INVALID, "qconv_run: quantize fused, use nnrh_qconv_run_f32");
     const nnrh_qconv_desc& d = h->d;
     hipStream_t s = S(stream);
     const uint8_t* src = (const uint8_t*)x;
+    if (h->use_stem && stem_ok(h, x, y)) return run_stem(h, x, y, false, s);
     if (h->transform == 3) {
+        if (int rc = stem_scratch(h)) return rc;
         ProfScope ps("first_layer_copies", s);
         HIP_TRY(launch_first_layer_copies(src, h->xs, d.N, d.C, d.H, d.W, h->g.H, h->g.W, d.pad_t,
                                           d.pad_l, h->g.copy_shift, (uint8_t)(d.x_zp & 0xff), s),
@@ -726,6 +802,8 @@ extern "C" int nnrh_qconv_run_f32(nnrh_qconv_t h, const float* x, void* y, void*
     if (!h->fused_quant) return set_err(NNRH_ERR_INVALID, "qconv_run_f32: nnrh_qconv_fuse_quantize was not called");
     const nnrh_qconv_desc& d = h->d;
     hipStream_t s = S(stream);
+    if (h->use_stem_f32 && stem_ok(h, x, y)) return run_stem(h, x, y, true, s);
+    if (int rc = stem_scratch(h)) return rc;
     {
         ProfScope ps("quantize_first_layer_copies", s);
         HIP_TRY(launch_quantize_first_layer_copies(x, h->xs, d.N, d.C, d.H, d.W, h->g.H, h->g.W, d.pad_t,

@@ -159,6 +159,36 @@ hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec,
 bool qgemm_dma_eligible(const GemmArgs& g, int vec);
 hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t s);
 
+// ---- first convolution with the input quantize fused (nnrh_stem.hip) ----
+// NCHW fp32 (or uint8) image with C <= 4 channels -> NHWC uint8, RQ-C.
+struct StemArgs {
+    const void* x;          // [N][C][H][W] fp32 or uint8
+    const int8_t* w;        // packed weights [64][Kp], K order (kh, kw < 4 * cpr, c < 4)
+    const int32_t* c0;      // [64] accumulator start (-(x_zp - 128) * colsum)
+    const float* cs;        // [64] RQ-C scale
+    const float* bf;        // [64] RQ-C bias term
+    uint8_t* y;             // [N][oH][oW][OC]
+    int N, C, H, W, oH, oW, kH, sH, sW, pad_t, pad_l;
+    int cpr;                // 16-byte K chunks per kernel row (kWp / 4)
+    int KS, Kp;             // MFMA K-steps (Kp / 64), packed K
+    int OC;                 // output channels (16..64, multiple of 16)
+    int L;                  // padded pixels per staged input row
+    int R;                  // output rows per group
+    int WR;                 // staged rows in the LDS ring
+    int strip;              // output rows per block
+    int align8;             // fragments as 8-byte LDS reads (even stride and L)
+    int sat;                // RQ-C bounds are [0, 255]: one saturating convert
+    float inv_y;
+    int y_zp, qmin, qmax;
+    uint32_t fill;          // the input zero point (pad value), one byte
+    // QuantizeLinear of the fp32 input (body / tail split of the whole tensor)
+    float q_scale, q_inv;
+    int q_zp;
+    long long qbody;
+};
+bool stem_eligible(const StemArgs& a, bool f32);
+hipError_t launch_stem_conv(const StemArgs& a, bool f32, hipStream_t s);
+
 // ---- misc kernels (nnrh_misc.hip) ----
 hipError_t launch_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C,
                                   int HW, int Cpad, uint8_t fill, hipStream_t s);

@@ -1,0 +1,354 @@
+// nnrh_stem.hip -- the first convolution of an image network in one kernel:
+// input quantization (or the raw uint8 image), implicit im2col, i8 MFMA and
+// the RQ-C epilogue of NNR's first-layer driver.
+//
+// The reference runs QuantizeLinear over the fp32 image (QuantizeLinear.cpp:
+// 15-301), then exec_first_layer_int8 (QLinearConv.cpp:665-700) over the
+// uint8 NCHW tensor with 3-4 input channels, requantizing with RQ-C
+// (conv_first_layer_int8_avx512.h:262-273). Here one block walks a strip of
+// output rows of one image:
+//  * the input rows it needs are read from HBM once (fp32 NCHW or uint8
+//    NCHW), quantized with the QuantizeLinear body / tail expressions of the
+//    whole tensor, and written into an LDS ring as zero-point padded
+//    4-channel pixels (one dword: channels 0..C-1, then the zero point),
+//    already shifted to int8 (x ^ 0x80);
+//  * the rows of the next group of output rows load while the current group
+//    runs its MFMAs, so the image streams in once at HBM rate;
+//  * the weights stay in registers ([Np = 64][Kp] packed as for the GEMM
+//    kernels, K order (kh, kw < kWp, c < 4)), each lane holding its 16-byte
+//    K chunks of its 16 output channels;
+//  * every 16 output pixels take Kp / 64 x 4 MFMAs 16x16x64 and go straight
+//    through the epilogue: RQ-C, 16 consecutive channels per lane, 16-byte
+//    stores into the NHWC uint8 output.
+// The accumulators start at c0[n] = -(x_zp - 128) * colsum[n], so
+// acc = sum (x - x_zp) w exactly, as in the GEMM kernels.
+#include "nnrh_internal.h"
+#include "nnrh_rq.h"
+
+#include <type_traits>
+
+namespace nnrh {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int STEM_MGW = 7;    // 16-pixel groups per wave per row group (x 4 waves)
+constexpr int STEM_RING_DW = 10240;    // LDS ring: dwords (staged pixels, mapped twice)
+constexpr int STEM_STAGE_B = 36 * 1024; // LDS staging: raw input bytes of one row group's span
+constexpr int STEM_DMA = 2;    // 16-byte DMA chunks one thread issues per input row (x 256 threads)
+#define LDS_AS __attribute__((address_space(3)))
+
+__device__ __forceinline__ uint32_t stem_quant(float xv, bool body, const StemArgs& a) {
+    int q;
+    if (body) {
+        // QuantizeLinear's 16-wide body: rint(x * (1/s)) + zp, clamped in float
+        float v = xv * a.q_inv;
+        v = __builtin_rintf(v) + (float)a.q_zp;
+        v = clamp_minmax(v, 0.0f, 255.0f);
+        q = (int)v;
+    } else {
+        // scalar tail: rint(x / s) through the x86 convert, + zp, clamped
+        q = clampi(wrap_add(x86_f2i(__builtin_rintf(xv / a.q_scale)), a.q_zp), 0, 255);
+    }
+    return (uint32_t)q;
+}
+
+// every wave's LDS writes done, then a plain s_barrier: __syncthreads'
+// workgroup fence would also wait for this wave's output stores, which the
+// kernel leaves in flight (the memory clobber keeps the compiler from moving
+// LDS accesses across)
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+}
+
+}  // namespace
+
+// CC: input channels (3 or 4); KS: MFMA K-steps (Kp / 64)
+template <bool F32, int CC, int KS>
+__global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
+    // two static arrays: the compiler then tells the ring's reads from the
+    // staging area's in-flight DMA writes and waits for neither
+    __shared__ __attribute__((aligned(16))) uint32_t ring[STEM_RING_DW];    // WR rows x L pixels
+    __shared__ __attribute__((aligned(16))) uint8_t stage[STEM_STAGE_B];    // raw rows of a span
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int frow = lane & 15, fch = lane >> 4;
+    const int n = blockIdx.y;
+    const int oh_begin = blockIdx.x * a.strip;
+    const int oh_end = min(a.oH, oh_begin + a.strip);
+    if (oh_begin >= oh_end) return;
+    const long long HW = (long long)a.H * a.W;
+    const long long img = (long long)n * a.C * HW;
+
+    // ---- weights (B fragments) and per-column constants in registers
+    v4i wf[KS][4];   // [K-step][tn]
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn)
+            wf[ks][tn] = *(const v4i*)(a.w + (long long)(tn * 16 + frow) * a.Kp + ks * 64 + fch * 16);
+    // per-column constants of this lane's 16 columns
+    v4i c0v[4], csv[4], bfv[4];
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) {
+        c0v[tn] = *(const v4i*)(a.c0 + 16 * fch + 4 * tn);
+        csv[tn] = *(const v4i*)(a.cs + 16 * fch + 4 * tn);
+        bfv[tn] = *(const v4i*)(a.bf + 16 * fch + 4 * tn);
+    }
+    // the weights have landed before the row groups start: the compiler
+    // then has no load outstanding from outside the pixel-group loop that
+    // the loop uses, and keeps the row prefetch in flight across it
+    __builtin_amdgcn_s_waitcnt(0);
+
+    // ---- index maps fixed for the whole strip (no divisions in the loop)
+    constexpr int ES = F32 ? 4 : 1;          // input element bytes
+    constexpr int CE = 16 / ES;              // elements per 16-byte DMA chunk
+    const int row_chunks = CC * (a.W / CE);  // DMA chunks of one padded row (all channels)
+    const int row_bytes = CC * a.W * ES;     // staged bytes of one padded row
+    // this thread's DMA chunks of a row (k = 0, 1): element offset c * H * W
+    // + w within the image, -1 past the row
+    int d_off[STEM_DMA];
+#pragma unroll
+    for (int k = 0; k < STEM_DMA; ++k) {
+        const int u = tid + 256 * k;
+        const int c = u / (a.W / CE), w4 = u - c * (a.W / CE);
+        d_off[k] = u < row_chunks ? (int)(c * HW) + w4 * CE : -1;
+    }
+    // this lane's pixel of 16-pixel group i, as a dword offset in the ring
+    // from the group's first row: (r * sH) * L + ow * sW; its output pixel
+    // (r << 16 | ow)
+    int m_off[STEM_MGW], m_rw[STEM_MGW];
+#pragma unroll
+    for (int i = 0; i < STEM_MGW; ++i) {
+        const int p = (wave + 4 * i) * 16 + frow;
+        const int r = p / a.oW, ow = p - (p / a.oW) * a.oW;
+        m_off[i] = r * a.sH * a.L + ow * a.sW;
+        m_rw[i] = (r << 16) | ow;
+    }
+    // K chunk of K-step ks: kernel row (clamped into the kernel: past it the
+    // weights are zero) and first tap
+    int k_kh[KS], k_kw[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const int q = ks * 4 + fch;
+        const int kh = q / a.cpr;
+        k_kh[ks] = min(kh, a.kH - 1);
+        k_kw[ks] = (q - kh * a.cpr) * 4;
+    }
+    // QuantizeLinear's scalar tail lies in the last image's last channel
+    const bool all_body = img + (long long)CC * HW <= a.qbody;
+
+    const uint8_t* xb = (const uint8_t*)a.x + img * ES;
+
+    // raw padded rows [r0, r0 + nr) into the staging area (rows outside the
+    // image load row 0: never read)
+    auto dma_rows = [&](int r0, int nr) {
+        for (int r = 0; r < nr; ++r) {
+            const int ih = r0 + r - a.pad_t;
+            const long long rowe = (long long)((unsigned)ih < (unsigned)a.H ? ih : 0) * a.W;
+#pragma unroll
+            for (int k = 0; k < STEM_DMA; ++k) {
+                if (k * 256 + wave * 64 >= row_chunks) break;
+                if (d_off[k] >= 0)
+                    __builtin_amdgcn_global_load_lds(xb + (rowe + d_off[k]) * ES,
+                                                     (LDS_AS void*)(stage + r * row_bytes + (k * 256 + wave * 64) * 16),
+                                                     16, 0, 0);
+            }
+        }
+    };
+    // staged rows [r0, r0 + nr) quantized into their ring slots, one thread
+    // per padded column; slot0 = slot of row r0. Bytes go in with
+    // v_cvt_pk_u8_f32, exact for the integral values in [0, 255] QuantizeLinear
+    // produces; the pad channels / pixels are the zero point; then ^ 0x80.
+    uint32_t fill4 = 0;
+#pragma unroll
+    for (int c = CC; c < 4; ++c) fill4 |= a.fill << (8 * c);
+    const uint32_t fill_all = a.fill * 0x01010101u;
+    auto quantize_rows = [&](int r0, int nr, int slot0) {
+        for (int r = 0; r < nr; ++r) {
+            const int ih = r0 + r - a.pad_t;
+            const bool row_in = (unsigned)ih < (unsigned)a.H;
+            int slot = slot0 + r;
+            slot -= slot >= a.WR ? a.WR : 0;
+            const uint8_t* srow = stage + r * row_bytes;
+            for (int pc = tid; pc < a.L; pc += 256) {
+                const int iw = pc - a.pad_l;
+                uint32_t w = fill_all;
+                if (row_in && (unsigned)iw < (unsigned)a.W) {
+                    if constexpr (F32) {
+                        const float* sp = (const float*)srow + iw;
+                        if (all_body) {
+                            w = fill4;
+#pragma unroll
+                            for (int c = 0; c < CC; ++c) {
+                                // QuantizeLinear's 16-wide body
+                                float v = __builtin_rintf(sp[c * a.W] * a.q_inv) + (float)a.q_zp;
+                                v = clamp_minmax(v, 0.0f, 255.0f);
+                                w = __builtin_amdgcn_cvt_pk_u8_f32(v, c, w);
+                            }
+                        } else {
+                            w = fill4;
+#pragma unroll
+                            for (int c = 0; c < CC; ++c) {
+                                const long long idx = img + (long long)c * HW + (long long)ih * a.W + iw;
+                                w |= stem_quant(sp[c * a.W], idx < a.qbody, a) << (8 * c);
+                            }
+                        }
+                    } else {
+                        w = fill4;
+#pragma unroll
+                        for (int c = 0; c < CC; ++c) w |= (uint32_t)srow[c * a.W + iw] << (8 * c);
+                    }
+                }
+                // the ring is mapped twice (rows slot and slot + WR): a
+                // group's rows are then contiguous from its first slot
+                ring[slot * a.L + pc] = w ^ 0x80808080u;
+                ring[(slot + a.WR) * a.L + pc] = w ^ 0x80808080u;
+            }
+        }
+    };
+
+    // ---- the strip's first rows; padded row pr sits in ring slot pr mod WR
+    const int span = (a.R - 1) * a.sH + a.kH;   // padded input rows of one row group
+    const int step = a.R * a.sH;                // new rows per group
+    int g_slot = (oh_begin * a.sH) % a.WR;      // slot of the group's first padded row
+    dma_rows(oh_begin * a.sH, span);
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+    quantize_rows(oh_begin * a.sH, span, g_slot);
+    lds_barrier();
+    for (int oh0 = oh_begin; oh0 < oh_end; oh0 += a.R) {
+        // the next group's new rows: raw input into the staging area
+        const bool more = oh0 + a.R < oh_end;
+        const int pre_r0 = oh0 * a.sH + span;
+        if (more) dma_rows(pre_r0, step);
+
+        // MFMAs + epilogue, 16 pixels at a time; ks_base: dword offset of
+        // this lane's kernel row and first tap of K-step ks from the group's
+        // first ring row (the second mapping keeps a group's span contiguous)
+        int ks_base[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) ks_base[ks] = (g_slot + k_kh[ks]) * a.L + k_kw[ks];
+        const int P_here = min(a.R, oh_end - oh0) * a.oW;
+        // outputs of this wave's pixel groups, stored after the ring refill so
+        // that they stay in flight across the next group's DMA and MFMAs
+        uint32_t outv[STEM_MGW][4];
+#pragma unroll
+        for (int i = 0; i < STEM_MGW; ++i) {
+            const int mg = wave + 4 * i;
+            if (mg * 16 < P_here) {
+                v4i acc[4];
+#pragma unroll
+                for (int tn = 0; tn < 4; ++tn) acc[tn] = c0v[tn];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    // this lane's 16-byte chunk: kernel row kh, taps kw0..kw0+3
+                    const uint32_t* px = ring + ks_base[ks] + m_off[i];
+                    v4i xf;
+                    if (a.align8) {
+                        const uint2 lo = *(const uint2*)px, hi = *(const uint2*)(px + 2);
+                        xf = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+                    } else {
+                        xf = v4i{(int)px[0], (int)px[1], (int)px[2], (int)px[3]};
+                    }
+#pragma unroll
+                    for (int tn = 0; tn < 4; ++tn)
+                        acc[tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ks][tn], xf, acc[tn], 0, 0, 0);
+                }
+                // RQ-C: rne(clamp(fma(fma(acc, cs, bf), 1/y_s, zp), qmin, qmax))
+#pragma unroll
+                for (int tn = 0; tn < 4; ++tn) {
+                    const v4i csq = csv[tn], bfq = bfv[tn];
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) {
+                        const float csf = __int_as_float(csq[qq]), bff = __int_as_float(bfq[qq]);
+                        if (a.sat) {
+                            const float t = __builtin_fmaf((float)acc[tn][qq], csf, bff);
+                            const float f = __builtin_fmaf(t, a.inv_y, (float)a.y_zp);
+                            w = __builtin_amdgcn_cvt_pk_u8_f32(f, qq, w);
+                        } else {
+                            const uint32_t b = rqc_fast(acc[tn][qq], csf, bff, a.inv_y, a.y_zp, a.qmin, a.qmax);
+                            w |= (b & 0xffu) << (8 * qq);
+                        }
+                    }
+                    outv[i][tn] = w;
+                }
+            }
+        }
+
+        if (more) {
+            // every wave's DMA has landed and no wave reads this group's ring
+            // slots past its span: quantize the staged rows into the ring
+            __builtin_amdgcn_s_waitcnt(0);
+            lds_barrier();
+            int p_slot = g_slot + span;
+            p_slot -= p_slot >= a.WR ? a.WR : 0;
+            quantize_rows(pre_r0, step, p_slot);
+        }
+#pragma unroll
+        for (int i = 0; i < STEM_MGW; ++i) {
+            const int p = (wave + 4 * i) * 16 + frow;
+            if ((wave + 4 * i) * 16 < P_here && p < P_here && 16 * fch < a.OC) {
+                const int r = m_rw[i] >> 16, ow = m_rw[i] & 0xffff;
+                uint8_t* yp = a.y + (((long long)n * a.oH + oh0 + r) * a.oW + ow) * a.OC + 16 * fch;
+                *(v4i*)yp = v4i{(int)outv[i][0], (int)outv[i][1], (int)outv[i][2], (int)outv[i][3]};
+            }
+        }
+        g_slot += step;
+        g_slot -= g_slot >= a.WR ? a.WR : 0;
+        lds_barrier();
+    }
+}
+
+bool stem_eligible(const StemArgs& a, bool f32) {
+    if (a.C < 3 || a.C > 4 || a.cpr < 1 || a.KS < 1 || a.KS > 4 || a.kH < 1) return false;
+    if (a.Kp != a.KS * 64 || a.kH * a.cpr * 16 > a.Kp) return false;
+    if (a.OC < 16 || a.OC > 64 || (a.OC & 15)) return false;
+    if (a.R < 1 || a.R * a.oW > 4 * 16 * STEM_MGW) return false;
+    // raw rows in 16-byte chunks (4 fp32 or 16 uint8 elements), a row's
+    // chunks over at most STEM_DMA rounds of the 256 threads
+    if (a.W % (f32 ? 4 : 16) || (long long)a.C * a.W > 256LL * STEM_DMA * (f32 ? 4 : 16)) return false;
+    if ((long long)a.C * a.H * a.W >= (1LL << 26)) return false;
+    // the ring holds the rows in use plus the next group's
+    if (a.WR < (a.R - 1) * a.sH + a.kH + a.R * a.sH) return false;
+    // LDS: the ring, and the raw rows of a group's span
+    const long long span = (long long)(a.R - 1) * a.sH + a.kH;
+    if (2LL * a.WR * a.L > STEM_RING_DW || span * a.C * a.W * (f32 ? 4 : 1) > STEM_STAGE_B) return false;
+    if (a.L < (a.oW - 1) * a.sW + 4 * a.cpr || a.L > 4096) return false;
+    if (a.align8 && ((a.sW & 1) || (a.L & 1))) return false;
+    if (((uintptr_t)a.w & 15) || ((uintptr_t)a.c0 & 15) || ((uintptr_t)a.y & 15)) return false;
+    return a.N >= 1 && a.N <= 65535 && a.strip >= 1;
+}
+
+hipError_t launch_stem_conv(const StemArgs& a, bool f32, hipStream_t s) {
+    if (!stem_eligible(a, f32)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.oH + a.strip - 1) / a.strip), (unsigned)a.N);
+    if (((uintptr_t)a.x & 15)) return hipErrorInvalidValue;
+    const size_t lds = 0;
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, a); };
+    auto by_ks = [&](auto f32c, auto ccc) {
+        constexpr bool F = decltype(f32c)::value;
+        constexpr int C = decltype(ccc)::value;
+        switch (a.KS) {
+        case 1: go(stem_conv_kernel<F, C, 1>); break;
+        case 2: go(stem_conv_kernel<F, C, 2>); break;
+        case 3: go(stem_conv_kernel<F, C, 3>); break;
+        default: go(stem_conv_kernel<F, C, 4>); break;
+        }
+    };
+    using T = std::true_type;
+    using Fa = std::false_type;
+    if (a.C == 3) {
+        if (f32) by_ks(T{}, std::integral_constant<int, 3>{});
+        else by_ks(Fa{}, std::integral_constant<int, 3>{});
+    } else {
+        if (f32) by_ks(T{}, std::integral_constant<int, 4>{});
+        else by_ks(Fa{}, std::integral_constant<int, 4>{});
+    }
+    return hipGetLastError();
+}
+
+}  // namespace nnrh

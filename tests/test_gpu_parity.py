@@ -172,6 +172,10 @@ CONV_CASES = [
     ("first_s3", 1, 3, 33, 30, 32, 3, dict(stride=(3, 3), pads=(1, 1, 1, 1), y_nhwc=1, post_fn=1,
                                           y_zp=6)),
     ("first_s4_c4", 1, 4, 17, 19, 16, 3, dict(stride=(4, 4), y_nhwc=1, y_zp=1)),
+    # one-kernel stem on a uint8 image (width % 16 == 0): 4 channels, odd
+    # stride, fused Relu (RQ-C bounds [zp, 255]), 48 output channels
+    ("first_stem_u8_s3_c4", 2, 4, 30, 48, 48, 3, dict(stride=(3, 3), pads=(1, 1, 1, 1), y_nhwc=1, post_fn=1,
+                                                       y_zp=6)),
     # depthwise dot4 kernel: 2x2 taps (one tap group), dilation, odd zero points,
     # channels over several 16-channel chunks; 5x5 (25 taps) takes the VALU kernel
     ("dw16_k2_zpodd", 1, 48, 9, 10, 48, 2, dict(group=48, pads=(0, 0, 1, 1), y_nhwc=1, x_nhwc=1,
@@ -630,6 +634,11 @@ QFIRST_CASES = [
     ("mbv2_stem", 3, 3, 33, 31, 32, 3, 2, (1, 1, 1, 1), 0.0237, 131),
     # 1*3*21*21 = 1323 elements: the last 11 take QuantizeLinear's divide tail
     ("tail_s1", 1, 3, 21, 21, 16, 3, 1, (1, 1, 1, 1), 0.0113, 17),
+    # ResNet-50's stem at its real size: 4-row groups, 14 groups a strip
+    ("rn50_stem_224", 2, 3, 224, 224, 64, 7, 2, (3, 3, 3, 3), 0.0187, 114),
+    # one-kernel stem with 1*3*21*20 = 1260 elements (12 in the divide tail),
+    # stride 1 (4-byte LDS fragment reads), several row groups a strip
+    ("tail_w20", 1, 3, 21, 20, 16, 3, 1, (1, 1, 1, 1), 0.0113, 17),
 ]
 
 
