@@ -716,9 +716,10 @@ def run_qoperator(args, dev, graph="qoperator"):
 
 def run_convinteger(args, dev):
     """ConvInteger at cfg2's shape: x u8[32,64,56,56], w i8[64,64,3,3], pad 1,
-    per-channel weight zero points; int32 output. im2col + the i8 MFMA
-    MatMulInteger GEMM + the zero-point correction; value = TOPS of the
-    whole operator."""
+    per-channel weight zero points; int32 output. NHWC copy of the input,
+    per-call weight packing and per-pixel patch sums, then the implicit-GEMM
+    i8 MFMA kernel whose epilogue adds the weight zero-point term and stores
+    int32 NCHW; value = TOPS of the whole operator."""
     import ctypes as C
 
     import numpy as np
@@ -757,7 +758,7 @@ def run_convinteger(args, dev):
     rl = roofline(ops / (g_launches / args.steps), nbytes, g_ms / g_launches, kprof)
     rl["traffic"] = None
     rl["note"] = ("achieved = algorithmic ops of the convolution / the GEMM kernel's time; value = the same ops / "
-                  "the whole operator (im2col, B packing, GEMM, zero-point correction)")
+                  "the whole operator (NHWC copy, weight packing, patch sums, GEMM)")
     host, nthr, vnni = cpu_setup()
     cpu_s, reps = timed_reps(lambda: O.conv_integer(x, w, 117, wz, pads=(1, 1)), 10.0, 1000)
     cpu_done()

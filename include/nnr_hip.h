@@ -277,7 +277,10 @@ int nnrh_matmul_integer_scaled_create(nnrh_qmatmul_t* h, const nnrh_mmi_scaled_d
  * 2^24 (K = C/group * kH * kW), where every partial sum is exact in float.
  * Output extents and pads are the caller's (the operator's auto_pad rules).
  * w_zp_dev: per-output-channel zero points (int32 [OC], device) or NULL for
- * the scalar w_zp. The handle owns the im2col workspace.                  */
+ * the scalar w_zp. Runs as an implicit GEMM (no im2col in memory); the
+ * handle owns an NHWC copy of the input, the weights packed per call and
+ * the per-pixel patch sums. create returns NNRH_ERR_UNSUPPORTED when
+ * C/group (padded to 16) * kH * kW > 32768 or N * oH * oW > 2^30.         */
 typedef struct nnrh_conv_integer* nnrh_conv_integer_t;
 int nnrh_conv_integer_create(nnrh_conv_integer_t* h, int N, int C, int iH, int iW, int OC,
                              int kH, int kW, int sH, int sW, int pH, int pW, int dH, int dW,

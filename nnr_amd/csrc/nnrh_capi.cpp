@@ -854,9 +854,9 @@ int qconv_compute(nnrh_qconv_t h, const uint8_t* src, void* y, hipStream_t s) {
     if (h->need_rowsum) {
         const int Cg = h->g.C;
         ProfScope ps("rowsum", s);
-        HIP_TRY(launch_rowsum_conv(src, d.N, d.H, d.W, h->Cx, Cg, h->groups, d.oH, d.oW, d.kH, d.kW,
+        HIP_TRY(launch_rowsum_conv(src, d.N, d.H, d.W, h->Cx, Cg, Cg, h->groups, d.oH, d.oW, d.kH, d.kW,
                                    d.sH, d.sW, d.dH, d.dW, d.pad_t, d.pad_l, d.act_dtype == NNRH_S8,
-                                   d.x_zp, h->rowsum, s),
+                                   d.x_zp, h->rowsum, (long long)d.N * d.oH * d.oW, s),
                 "rowsum_conv");
     }
     GemmArgs g = h->g;
@@ -1632,19 +1632,24 @@ extern "C" int nnrh_qlinear_avgpool(const void* x, void* y, int N, int C, int iH
 }
 
 // ---- ConvInteger --------------------------------------------------------------
-// im2col written in the GEMM's packed-B layout (no separate packing pass),
-// then MatMulInteger's GEMM: y[b] = W_g[MM][K] . col[b][K][P]
+// The implicit-GEMM kernel of QLinearConv with an int32 epilogue: the NCHW
+// input goes to an NHWC copy (each group's channels padded to a multiple of
+// 16 with x_zp), the weights are packed per call, and
+//   y = sum (x - x_zp)(w - w_zp) = acc' - alpha * colsum[n] + (b_sub - w_zp[n]) * rowsum[m]
+// with acc' = sum (x - a_sub)(w - b_sub) on the MFMAs (padded taps and
+// channels read x_zp, i.e. x - x_zp = 0, against zero weights), alpha = x_zp -
+// a_sub and rowsum[m] = sum (x - x_zp) over pixel m's patch, which the kernel
+// sums from its A fragments; stored NCHW.
 struct nnrh_conv_integer {
-    Im2colArgs a{};
-    int OC = 0, MM = 0, x_dtype = 0, w_dtype = 0;
-    long long K = 0, P = 0;
-    int8_t* bpack = nullptr;
-    int32_t* colsum = nullptr;
-    nnrh_matmul_integer_t mi = nullptr;   // GEMM shape, rowsum workspace
+    int N = 0, C = 0, iH = 0, iW = 0, OC = 0, G = 0, OCg = 0, Cg = 0, Cgp = 0;
+    int x_dtype = 0, w_dtype = 0, Kp = 0, Np = 0;
+    GemmArgs g{};
+    uint8_t* xs = nullptr;        // NHWC copy [N][iH][iW][G * Cgp]
+    int8_t* wpack = nullptr;      // [G][Np][Kp]
+    int32_t* c0 = nullptr;        // [G][Np]
+    int32_t* coef = nullptr;      // [G][Np] row-term coefficient
     ~nnrh_conv_integer() {
-        dfree(bpack);
-        dfree(colsum);
-        if (mi) nnrh_matmul_integer_destroy(mi);
+        dfree(xs); dfree(wpack); dfree(c0); dfree(coef);
     }
 };
 
@@ -1658,25 +1663,49 @@ extern "C" int nnrh_conv_integer_create(nnrh_conv_integer_t* out, int N, int C, 
         return set_err(NNRH_ERR_INVALID, "conv_integer: bad shape");
     if ((x_dtype != NNRH_U8 && x_dtype != NNRH_S8) || (w_dtype != NNRH_U8 && w_dtype != NNRH_S8))
         return set_err(NNRH_ERR_UNSUPPORTED, "conv_integer: dtype");
-    const long long K = (long long)(C / group) * kH * kW, P = (long long)oH * oW;
-    if (K > (1 << 30) || P > (1 << 30)) return set_err(NNRH_ERR_UNSUPPORTED, "conv_integer: GEMM extents too large");
-    auto* h = new nnrh_conv_integer();
-    h->a = Im2colArgs{nullptr, nullptr, N, C, iH, iW, group, kH, kW, sH, sW, pH, pW, dH, dW, oH, oW, 0};
-    h->OC = OC;
-    h->MM = OC / group;
-    h->x_dtype = x_dtype;
-    h->w_dtype = w_dtype;
-    h->K = K;
-    h->P = P;
-    int rc = nnrh_matmul_integer_create(&h->mi, h->MM, (int)P, (int)K, w_dtype, x_dtype, group == 1 ? N : group);
-    const long long batches = (long long)N * group;
-    if (rc == NNRH_OK)
-        rc = nnrh_malloc((void**)&h->bpack, (size_t)(batches * h->mi->Np * (long long)h->mi->Kp));
-    if (rc == NNRH_OK) rc = nnrh_malloc((void**)&h->colsum, (size_t)(batches * h->mi->Np) * sizeof(int32_t));
-    if (rc != NNRH_OK) {
-        delete h;
-        return rc;
-    }
+    const int G = group, Cg = C / G, OCg = OC / G;
+    const int Cgp = round_up(Cg, 16);
+    const long long K = (long long)kH * kW * Cgp;
+    const long long M = (long long)N * oH * oW;
+    // exact int32 partial sums on the MFMAs: |c0| + 128 * 128 * K per term
+    if (K > 32768 || M > (1LL << 30) || (long long)G * Cgp > (1 << 20) || N > 65535 || G > 65535)
+        return set_err(NNRH_ERR_UNSUPPORTED, "conv_integer: GEMM extents too large");
+    auto* h = new (std::nothrow) nnrh_conv_integer();
+    if (!h) return set_err(NNRH_ERR_NOMEM, "conv_integer: host allocation");
+    h->N = N; h->C = C; h->iH = iH; h->iW = iW; h->OC = OC; h->G = G; h->OCg = OCg; h->Cg = Cg; h->Cgp = Cgp;
+    h->x_dtype = x_dtype; h->w_dtype = w_dtype;
+    h->Kp = (int)round_up(K, 64);
+    h->Np = round_up(OCg, 64);
+    GemmArgs& g = h->g;
+    g.a_xor = x_dtype == NNRH_U8 ? 0x80 : 0;
+    g.M = (int)M; g.N = OCg; g.K = (int)K; g.Kp = h->Kp;
+    g.H = iH; g.W = iW; g.C = Cgp; g.Cs = G * Cgp;
+    g.oH = oH; g.oW = oW; g.kH = kH; g.kW = kW; g.sH = sH; g.sW = sW; g.dH = dH; g.dW = dW;
+    g.pad_t = pH; g.pad_l = pW;
+    g.a_bstride = Cgp;   // group channel offset
+    g.b_bstride = (long long)h->Np * h->Kp;
+    g.Np = h->Np;
+    g.a_sub = x_dtype == NNRH_U8 ? 128 : 0;
+    g.param_bstride = h->Np;
+    g.epi = EPI_I32;
+    g.tail = TAIL_NONE;
+    g.bprime_from = OCg;
+    g.y_type = 2;
+    g.y_nchw = 1;
+    g.ldy = OC;
+    g.y_bstride = (long long)OCg * oH * oW;
+    g.c0_absmax = 16384LL * K;
+    int rc = NNRH_OK;
+    auto fail = [&](int code) { delete h; return code; };
+    if ((rc = nnrh_malloc((void**)&h->xs, (size_t)N * iH * iW * G * Cgp))) return fail(rc);
+    if ((rc = nnrh_malloc((void**)&h->wpack, (size_t)G * h->Np * h->Kp))) return fail(rc);
+    if ((rc = nnrh_malloc((void**)&h->c0, sizeof(int32_t) * (size_t)G * h->Np))) return fail(rc);
+    if ((rc = nnrh_malloc((void**)&h->coef, sizeof(int32_t) * (size_t)G * h->Np))) return fail(rc);
+    // every call must run on the pipelined kernel (its FUSE_ROW epilogue)
+    GemmArgs chk = g;
+    chk.a = h->xs; chk.b = h->wpack; chk.c0 = h->c0; chk.row_coef = h->coef;
+    chk.y = h->xs;
+    if (!qgemm_dma_eligible(chk, 16)) return fail(set_err(NNRH_ERR_UNSUPPORTED, "conv_integer: shape"));
     *out = h;
     return NNRH_OK;
 }
@@ -1685,44 +1714,27 @@ extern "C" int nnrh_conv_integer_run(nnrh_conv_integer_t h, const void* x, const
                                      const int32_t* w_zp_dev, int32_t* y, void* stream) {
     if (!h || !x || !w || !y) return set_err(NNRH_ERR_INVALID, "conv_integer_run: NULL argument");
     hipStream_t s = S(stream);
-    const int Np = h->mi->Np, Kp = h->mi->Kp;
-    const int x_xor = h->x_dtype == NNRH_U8 ? 0x80 : 0;
-    Im2colPackArgs q{};
-    q.a = h->a;
-    q.a.x = (const uint8_t*)x;
-    q.a.pad = (uint8_t)x_zp;
-    q.bpack = h->bpack;
-    q.colsum = h->colsum;
-    q.Kp = Kp;
-    q.Np = Np;
-    q.K = (int)h->K;
-    q.P = (int)h->P;
-    q.x_xor = x_xor;
+    const bool xu8 = h->x_dtype == NNRH_U8, wu8 = h->w_dtype == NNRH_U8;
+    const int alpha = x_zp - (xu8 ? 128 : 0);
+    GemmArgs g = h->g;
     {
-        ProfScope ps("im2col_pack", s);
-        HIP_TRY(launch_im2col_pack(q, s), "im2col_pack");
+        ProfScope ps("conv_integer_prep", s);
+        HIP_TRY(launch_nchw_to_nhwc_group_pad((const uint8_t*)x, h->xs, h->N, h->iH * h->iW, h->G, h->Cg, h->Cgp,
+                                              (uint8_t)(x_zp & 0xff), s),
+                "conv_integer_nhwc");
+        HIP_TRY(launch_conv_integer_pack((const uint8_t*)w, wu8 ? 1 : 0, h->G, h->OCg, h->Cg, h->Cgp, h->g.kH,
+                                         h->g.kW, h->Kp, h->Np, alpha, w_zp, w_zp_dev, h->wpack, h->c0, h->coef, s),
+                "conv_integer_pack");
     }
-    const long long pb = (long long)Np * Kp, wsz = (long long)h->MM * h->K, ysz = (long long)h->MM * h->P;
-    const int wz = w_zp_dev ? 0 : w_zp;
-    const int G = h->a.group;
-    if (G == 1) {
-        const int rc = matmul_integer_gemm(h->mi, w, 0, h->bpack, h->colsum, true, wz, x_zp, y, h->a.N, s);
-        if (rc != NNRH_OK) return rc;
-    } else {
-        for (int n = 0; n < h->a.N; ++n) {
-            const int rc = matmul_integer_gemm(h->mi, w, wsz, h->bpack + (size_t)n * G * pb,
-                                               h->colsum + (size_t)n * G * Np, true, wz, x_zp,
-                                               y + (size_t)n * G * ysz, G, s);
-            if (rc != NNRH_OK) return rc;
-        }
-    }
-    if (w_zp_dev) {
-        // S = sum_k (x - x_zp) = colsum of the shifted bytes + K * (shift - x_zp)
-        const int s_off = (int)((uint32_t)h->K * (uint32_t)(x_xor ? 128 - x_zp : -x_zp));
-        ProfScope ps("conv_integer_wzp", s);
-        HIP_TRY(launch_conv_integer_wzp(y, h->colsum, Np, s_off, w_zp_dev, (long long)h->a.N * G, G, h->MM, h->P, s),
-                "conv_integer_wzp");
-    }
+    g.row_coef = h->coef;
+    g.alpha = alpha;
+    g.a = h->xs;
+    g.b = h->wpack;
+    g.c0 = h->c0;
+    g.pad_byte = x_zp & 0xff;
+    g.y = y;
+    ProfScope ps("qgemm", s);
+    HIP_TRY(launch_qgemm(g, h->G, pick_tile(h->OCg), 16, s), "qgemm");
     return NNRH_OK;
 }
 

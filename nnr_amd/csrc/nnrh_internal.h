@@ -68,6 +68,11 @@ struct GemmArgs {
     long long rowsum_bstride;
     int beta;
     const int32_t* beta_col;  // nullable: per-column beta (per-channel w_zp)
+    // pipelined kernel, EPI_I32 of a convolution only: v = acc' + row_coef[n] *
+    // sum_k (a[m][k] - (alpha + a_sub)) (int32 wrap-around), the row sum over
+    // the Kp bytes of im2col row m (padding reads pad_byte, which must be the
+    // zero point alpha + a_sub) taken from the A fragments in the kernel
+    const int32_t* row_coef;
     // ---- epilogue ----
     int epi;
     int tail;
@@ -203,22 +208,6 @@ hipError_t launch_depthwise(const uint8_t* x, const int8_t* w, uint8_t* y,
 // depthwise, NHWC in/out, C % 16 == 0, w_zp 0, at most 12 taps, no tails
 // (nnrh_misc.hip); wdot [ceil(taps/4)][C] 4 taps per dword, corr[C]
 // 3x3 depthwise, stride 1 or 2, dilation 1, NHWC in and out, C % 8 == 0
-// ConvInteger's im2col (nnrh_misc.hip)
-struct Im2colArgs {
-    const uint8_t* x;
-    uint8_t* col;
-    int N, C, iH, iW, group, kH, kW, sH, sW, pH, pW, dH, dW, oH, oW;
-    uint8_t pad;
-};
-struct Im2colPackArgs {
-    Im2colArgs a;
-    int8_t* bpack;
-    int32_t* colsum;
-    int Kp, Np, K, P, x_xor;
-};
-hipError_t launch_im2col_pack(const Im2colPackArgs& q, hipStream_t s);
-hipError_t launch_conv_integer_wzp(int32_t* y, const int32_t* colsum, int Np, int s_off, const int32_t* wzp,
-                                   long long batches, int group, int MM, long long P, hipStream_t s);
 hipError_t launch_depthwise3x3(const uint8_t* x, const uint32_t* wrow, const int32_t* corr, uint8_t* y,
                                const float* cs, const float* bf, int N, int C, int H, int W, int oH, int oW,
                                int stride, int pad_t, int pad_l, int x_zp, int a_xor, float inv_y, int y_zp,
@@ -245,11 +234,24 @@ hipError_t launch_quantize_first_layer_copies(const float* x, uint8_t* y, int N,
 hipError_t launch_first_layer_copies(const uint8_t* x, uint8_t* y, int N, int C, int H, int W,
                                      int Hp, int Wc, int pad_t, int pad_l, int copy_shift,
                                      uint8_t fill, hipStream_t s);
+// rowsum[z][m] = sum over the patch of pixel m of (x - x_zp), the Cg channels
+// of group z starting at channel z * cg_stride; out + z * out_bstride + m
 hipError_t launch_rowsum_conv(const uint8_t* x, int N, int H, int W, int Cs,
-                              int Cg, int groups, int oH, int oW, int kH,
+                              int Cg, int cg_stride, int groups, int oH, int oW, int kH,
                               int kW, int sH, int sW, int dH, int dW,
                               int pad_t, int pad_l, int a_signed, int x_zp,
-                              int32_t* out, hipStream_t s);
+                              int32_t* out, long long out_bstride, hipStream_t s);
+// NCHW -> NHWC with each group's Cg channels padded to Cgp (a multiple of 16)
+// with the fill byte: y[n][p][z * Cgp + c] = c < Cg ? x[n][z * Cg + c][p] : fill
+hipError_t launch_nchw_to_nhwc_group_pad(const uint8_t* x, uint8_t* y, int N, int HW, int G, int Cg,
+                                         int Cgp, uint8_t fill, hipStream_t s);
+// ConvInteger weights W[G * OCg][Cg][kH][kW] (int8 / uint8) -> packed
+// [G][Np][Kp] int8 (uint8 shifted by 128), K order (kh, kw, c < Cgp), zero
+// padded; c0[n] = -alpha * colsum[n] with alpha = x_zp - a_sub; row_coef[n] =
+// b_sub - w_zp[oc] (w_zp_dev[oc] when given, else w_zp)
+hipError_t launch_conv_integer_pack(const uint8_t* w, int w_u8, int G, int OCg, int Cg, int Cgp, int kH, int kW,
+                                    int Kp, int Np, int alpha, int w_zp, const int32_t* w_zp_dev, int8_t* wpack,
+                                    int32_t* c0, int32_t* row_coef, hipStream_t s);
 // Pack a row-major B[K][N] (int8 or uint8) into the kernel's [Np][Kp]
 // permuted layout and compute colsum[n] = sum_k (b - b_sub).
 hipError_t launch_pack_b_dense(const void* b, long long b_bstride, int K,

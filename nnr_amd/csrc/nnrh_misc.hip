@@ -793,11 +793,12 @@ hipError_t launch_rowsum_dense(const uint8_t* a, long long lda, long long a_bstr
 // [c_off, c_off+Cg) of a Cs-channel tensor): sum over in-image taps of
 // (x - x_zp); out-of-image taps hold x_zp in the reference and contribute 0.
 __global__ __launch_bounds__(256) void rowsum_conv_kernel(const uint8_t* __restrict x, int N,
-                                                          int H, int W, int Cs, int Cg,
+                                                          int H, int W, int Cs, int Cg, int cg_stride,
                                                           int oH, int oW, int kH, int kW,
                                                           int sH, int sW, int dH, int dW,
                                                           int pad_t, int pad_l, int a_signed,
-                                                          int x_zp, int32_t* __restrict out) {
+                                                          int x_zp, int32_t* __restrict out,
+                                                          long long out_bstride) {
     const int z = blockIdx.y;   // group
     const long long m = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -810,25 +811,143 @@ __global__ __launch_bounds__(256) void rowsum_conv_kernel(const uint8_t* __restr
         int a = t / kW, b = t - a * kW;
         int ih = oh * sH - pad_t + a * dH, iw = ow * sW - pad_l + b * dW;
         if ((unsigned)ih >= (unsigned)H || (unsigned)iw >= (unsigned)W) continue;
-        const uint8_t* xp = x + (((long long)n * H + ih) * W + iw) * Cs + (long long)z * Cg;
+        const uint8_t* xp = x + (((long long)n * H + ih) * W + iw) * Cs + (long long)z * cg_stride;
         for (int c = lane; c < Cg; c += 64) {
             int v = a_signed ? (int)(int8_t)xp[c] : (int)xp[c];
             s += v - x_zp;
         }
     }
     for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
-    if (lane == 0) out[(long long)z * M + m] = s;
+    if (lane == 0) out[(long long)z * out_bstride + m] = s;
 }
 
-hipError_t launch_rowsum_conv(const uint8_t* x, int N, int H, int W, int Cs, int Cg, int groups,
+hipError_t launch_rowsum_conv(const uint8_t* x, int N, int H, int W, int Cs, int Cg, int cg_stride, int groups,
                               int oH, int oW, int kH, int kW, int sH, int sW, int dH, int dW,
                               int pad_t, int pad_l, int a_signed, int x_zp, int32_t* out,
-                              hipStream_t s) {
+                              long long out_bstride, hipStream_t s) {
     long long M = (long long)N * oH * oW;
     if (M <= 0) return hipSuccess;
     dim3 grid((unsigned)((M + 3) / 4), groups);
-    hipLaunchKernelGGL(rowsum_conv_kernel, grid, dim3(256), 0, s, x, N, H, W, Cs, Cg, oH, oW, kH,
-                       kW, sH, sW, dH, dW, pad_t, pad_l, a_signed, x_zp, out);
+    hipLaunchKernelGGL(rowsum_conv_kernel, grid, dim3(256), 0, s, x, N, H, W, Cs, Cg, cg_stride, oH, oW, kH,
+                       kW, sH, sW, dH, dW, pad_t, pad_l, a_signed, x_zp, out, out_bstride);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// ConvInteger on the pipelined implicit-GEMM kernel: the NCHW input as NHWC
+// with every group's channels padded to a multiple of 16, and the weights
+// packed per call (they are an input of the operator).
+
+// NCHW -> group-padded NHWC: one thread per (image, 4 consecutive pixels,
+// 16-channel output chunk), the chunk index fastest so that the 4 chunks of a
+// 64-channel pixel row are neighbouring lanes (whole-row stores). A thread
+// loads 16 channel planes x 4 pixels as dwords (bytes when HW % 4 != 0 or x is
+// not 4-byte aligned) and transposes them with byte permutes into 4 pixels x
+// 16 channels.
+__global__ __launch_bounds__(256) void nchw_to_nhwc_group_pad_kernel(const uint8_t* __restrict x,
+                                                                     uint8_t* __restrict y, int N, int HW, int G,
+                                                                     int Cg, int Cgp, uint32_t fill, int vec) {
+    const int cpp = G * Cgp / 16;         // 16-channel chunks per pixel
+    const int qpi = (HW + 3) / 4;         // pixel quads per image
+    const long long total = (long long)N * qpi * cpp;
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int c = (int)(i % cpp);
+    const long long t = i / cpp;
+    const int q = (int)(t % qpi);
+    const int n = (int)(t / qpi);
+    const int z = c * 16 / Cgp, c0 = c * 16 - z * Cgp;
+    const int p = 4 * q;
+    const uint8_t* src = x + ((long long)n * G + z) * Cg * (long long)HW + p;
+    const uint32_t fill4 = fill * 0x01010101u;
+    uint32_t v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int ch = c0 + j;
+        uint32_t d = fill4;
+        if (ch < Cg) {
+            const uint8_t* sp = src + (long long)ch * HW;
+            if (vec) {
+                d = *(const uint32_t*)sp;
+            } else {
+                d = 0;
+                for (int b = 0; b < 4; ++b) d |= (p + b < HW ? (uint32_t)sp[b] : 0u) << (8 * b);
+            }
+        }
+        v[j] = d;
+    }
+    uint8_t* dst = y + ((long long)n * HW + p) * (G * Cgp) + (long long)z * Cgp + c0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        if (p + b >= HW) break;
+        // byte b of v[4k .. 4k + 3] -> dword k
+        const uint32_t sel = (uint32_t)b | ((uint32_t)(4 + b) << 8) | 0x0c0c0000u;
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = __builtin_amdgcn_perm(v[4 * k + 1], v[4 * k], sel);
+            const uint32_t hi = __builtin_amdgcn_perm(v[4 * k + 3], v[4 * k + 2], sel);
+            w[k] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        }
+        *(uint4*)(dst + (long long)b * (G * Cgp)) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+hipError_t launch_nchw_to_nhwc_group_pad(const uint8_t* x, uint8_t* y, int N, int HW, int G, int Cg, int Cgp,
+                                         uint8_t fill, hipStream_t s) {
+    if (Cgp % 16 || Cg > Cgp || G <= 0) return hipErrorInvalidValue;
+    const long long total = (long long)N * ((HW + 3) / 4) * (G * Cgp / 16);
+    if (total <= 0) return hipSuccess;
+    const int vec = (HW % 4 == 0 && (((uintptr_t)x) & 3) == 0) ? 1 : 0;
+    hipLaunchKernelGGL(nchw_to_nhwc_group_pad_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, y,
+                       N, HW, G, Cg, Cgp, (uint32_t)fill, vec);
+    return hipGetLastError();
+}
+
+// one block per packed row (z, n): the row's Kp bytes in (kh, kw, c) order,
+// its column sum, the accumulator start c0 and the row-term coefficient
+__global__ __launch_bounds__(256) void conv_integer_pack_kernel(const uint8_t* __restrict w, int w_u8, int OCg,
+                                                                int Cg, int Cgp, int kH, int kW, int Kp, int Np,
+                                                                int alpha, int w_zp,
+                                                                const int32_t* __restrict w_zp_dev,
+                                                                int8_t* __restrict wpack, int32_t* __restrict c0,
+                                                                int32_t* __restrict row_coef) {
+    const int n = blockIdx.x, z = blockIdx.y;
+    const int oc = z * OCg + n;
+    const int K = kH * kW * Cgp;
+    const uint8_t bx = w_u8 ? 0x80 : 0;
+    int8_t* row = wpack + ((long long)z * Np + packed_row_of_col(n)) * Kp;
+    int32_t s = 0;
+    for (int k = threadIdx.x; k < Kp; k += blockDim.x) {
+        int8_t v = 0;
+        if (n < OCg && k < K) {
+            const int c = k % Cgp, t = k / Cgp;
+            const int kh = t / kW, kw = t - kh * kW;
+            if (c < Cg) v = (int8_t)(w[(((long long)oc * Cg + c) * kH + kh) * kW + kw] ^ bx);
+        }
+        row[k] = v;
+        s += v;
+    }
+    __shared__ int32_t part[4];
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int32_t cs = part[0] + part[1] + part[2] + part[3];
+        const long long pi = (long long)z * Np + n;
+        c0[pi] = (int32_t)(0u - (uint32_t)alpha * (uint32_t)cs);
+        int coef = 0;
+        if (n < OCg) coef = (w_u8 ? 128 : 0) - (w_zp_dev ? w_zp_dev[oc] : w_zp);
+        row_coef[pi] = coef;
+    }
+}
+
+hipError_t launch_conv_integer_pack(const uint8_t* w, int w_u8, int G, int OCg, int Cg, int Cgp, int kH, int kW,
+                                    int Kp, int Np, int alpha, int w_zp, const int32_t* w_zp_dev, int8_t* wpack,
+                                    int32_t* c0, int32_t* row_coef, hipStream_t s) {
+    if (G <= 0 || OCg <= 0 || Np < OCg || (long long)kH * kW * Cgp > Kp) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(conv_integer_pack_kernel, dim3(Np, G), dim3(256), 0, s, w, w_u8, OCg, Cg, Cgp, kH, kW, Kp,
+                       Np, alpha, w_zp, w_zp_dev, wpack, c0, row_coef);
     return hipGetLastError();
 }
 
@@ -906,108 +1025,6 @@ hipError_t launch_fill_u8(void* p, uint8_t v, long long n, hipStream_t s) {
     long long b = (n + 255) / 256;
     if (b > 65536) b = 65536;
     hipLaunchKernelGGL(fill_u8_kernel, dim3((unsigned)b), dim3(256), 0, s, (uint8_t*)p, v, n);
-    return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
-// ConvInteger (ConvInteger.cpp:146-233): im2col of x written straight in the
-// GEMM's packed-B layout (pack_b_kernel's: B[K][P] of image n, group g goes to
-// bpack[n * group + g][packed_row_of_col(p)][Kp], uint8 XOR-shifted to int8,
-// zero padded) with colsum[b][p] = sum_k of the packed bytes. Taps outside the
-// image take the byte of x_zp, so (x - x_zp) is 0 there as in the reference's
-// zero-padded float im2col of (x - x_zp). One thread per packed row.
-// IM2COL_LANES neighbouring lanes share a packed row: lane j writes the 16-tap
-// chunks j, j + IM2COL_LANES, ... (together coalesced 16-byte stores), and
-// the row's column sum is reduced over the lane group by shuffles.
-constexpr int IM2COL_LANES = 4;
-__global__ __launch_bounds__(256) void im2col_pack_kernel(Im2colPackArgs q) {
-    const Im2colArgs& a = q.a;
-    const int CC = a.C / a.group;
-    const int kHW = a.kH * a.kW;
-    const long long rows = (long long)a.N * a.group * q.Np;
-    const int sub = threadIdx.x % IM2COL_LANES;
-    const long long rstride = (long long)gridDim.x * (256 / IM2COL_LANES);
-    // every lane of a group has the same row, so the loop and the shuffles are
-    // uniform over the group
-    for (long long e = (long long)blockIdx.x * (256 / IM2COL_LANES) + threadIdx.x / IM2COL_LANES; e < rows;
-         e += rstride) {
-        const long long b = e / q.Np;
-        const int p = (int)(e % q.Np);
-        int8_t* row = q.bpack + b * q.Np * (long long)q.Kp + (long long)packed_row_of_col(p) * q.Kp;
-        int32_t sum = 0;
-        if (p >= q.P) {
-            for (int kc = sub * 16; kc < q.Kp; kc += 16 * IM2COL_LANES) *(uint4*)(row + kc) = make_uint4(0, 0, 0, 0);
-        } else {
-            const int ow = p % a.oW, oh = p / a.oW;
-            const long long n = b / a.group, g = b % a.group;
-            const uint8_t* xb = a.x + (n * a.C + g * CC) * (long long)a.iH * a.iW;
-            const int h0 = oh * a.sH - a.pH, w0 = ow * a.sW - a.pW;
-            for (int kc = sub * 16; kc < q.Kp; kc += 16 * IM2COL_LANES) {
-                // tap k = (c * kH + kh) * kW + kw, decoded once per chunk
-                int c = kc / kHW, r = kc % kHW;
-                int kh = r / a.kW, kw = r % a.kW;
-                uint32_t w4[4] = {0, 0, 0, 0};
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    if (kc + i < q.K) {
-                        const int ih = h0 + kh * a.dH, iw = w0 + kw * a.dW;
-                        uint8_t v = a.pad;
-                        if (ih >= 0 && ih < a.iH && iw >= 0 && iw < a.iW)
-                            v = xb[((long long)c * a.iH + ih) * a.iW + iw];
-                        v ^= (uint8_t)q.x_xor;
-                        sum += (int8_t)v;
-                        w4[i >> 2] |= (uint32_t)v << (8 * (i & 3));
-                        if (++kw == a.kW) {
-                            kw = 0;
-                            if (++kh == a.kH) { kh = 0; ++c; }
-                        }
-                    }
-                }
-                *(uint4*)(row + kc) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-            }
-        }
-#pragma unroll
-        for (int off = 1; off < IM2COL_LANES; off <<= 1) sum += __shfl_xor(sum, off, 64);
-        if (sub == 0) q.colsum[b * q.Np + p] = sum;
-    }
-}
-
-hipError_t launch_im2col_pack(const Im2colPackArgs& q, hipStream_t s) {
-    const long long rows = (long long)q.a.N * q.a.group * q.Np;
-    if (rows <= 0) return hipSuccess;
-    long long blocks = (rows + 256 / IM2COL_LANES - 1) / (256 / IM2COL_LANES);
-    if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(im2col_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, s, q);
-    return hipGetLastError();
-}
-
-// per-channel weight zero points: y[b][m][p] -= w_zp[g * MM + m] * S[b][p] with
-// S[b][p] = sum_k (x - x_zp) = colsum[b][p] + s_off (s_off = K * (shift -
-// x_zp), shift 128 for XOR-shifted uint8), so that the GEMM's
-// sum_k w (x - x_zp) becomes sum_k (w - w_zp[oc]) (x - x_zp) exactly (int32,
-// wrapping)
-__global__ __launch_bounds__(256) void wzp_correct_kernel(int32_t* __restrict y, const int32_t* __restrict colsum,
-                                                          int Np, int s_off, const int32_t* __restrict wzp,
-                                                          long long batches, int group, int MM, long long P) {
-    const long long total = batches * MM * P;
-    for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
-        const long long p = e % P;
-        const long long r = e / P;
-        const int m = (int)(r % MM);
-        const long long b = r / MM;
-        const int g = (int)(b % group);
-        const uint32_t S = (uint32_t)colsum[b * Np + p] + (uint32_t)s_off;
-        y[e] = (int32_t)((uint32_t)y[e] - (uint32_t)wzp[g * MM + m] * S);
-    }
-}
-
-hipError_t launch_conv_integer_wzp(int32_t* y, const int32_t* colsum, int Np, int s_off, const int32_t* wzp,
-                                   long long batches, int group, int MM, long long P, hipStream_t s) {
-    long long blocks = (batches * MM * P + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    if (blocks <= 0) return hipSuccess;
-    hipLaunchKernelGGL(wzp_correct_kernel, dim3((unsigned)blocks), dim3(256), 0, s, y, colsum, Np, s_off, wzp, batches,
-                       group, MM, P);
     return hipGetLastError();
 }
 

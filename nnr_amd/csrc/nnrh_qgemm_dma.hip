@@ -85,9 +85,11 @@ __device__ __forceinline__ void block_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
-// epilogue fusions: none, QLinearAdd of a residual (RQ-B), or
-// DequantizeLinear of the output plus a per-column fp32 bias (RQ-D)
-enum { FUSE_NONE = 0, FUSE_ADD = 1, FUSE_DQB = 2 };
+// epilogue fusions: none, QLinearAdd of a residual (RQ-B), DequantizeLinear
+// of the output plus a per-column fp32 bias (RQ-D), or a per-row term
+// row_coef[n] * (sum_k (a[m][k] - a_zp)) added to the int32 accumulator
+// (EPI_I32), the row sums taken from the A fragments on the way
+enum { FUSE_NONE = 0, FUSE_ADD = 1, FUSE_DQB = 2, FUSE_ROW = 3 };
 
 template <int EPI>
 struct EpiParams;
@@ -123,6 +125,10 @@ template <int BM, int BN, int S, int NPX, int FUSE>
 constexpr int dma_pslot_bytes() {
     return ((NPX * BN * 4 + 1023) / 1024) * 1024 + (FUSE == FUSE_ADD ? BM * BN : 0);
 }
+// per-column arrays staged per tile: the epilogue's, + the fp32 bias of a
+// fused dequantize, + the row-term coefficient
+template <int EPI, int FUSE>
+constexpr int dma_npx() { return EpiParams<EPI>::NP + (FUSE == FUSE_DQB || FUSE == FUSE_ROW ? 1 : 0); }
 template <int BM, int BN, int S, int NPX, int FUSE, int BK>
 constexpr int dma_lds_bytes() { return S * (BM + BN) * BK + S * dma_pslot_bytes<BM, BN, S, NPX, FUSE>(); }
 // blocks per CU the kernel is compiled for: LDS and registers must fit them
@@ -134,8 +140,7 @@ constexpr int dma_min_blocks() { return dma_lds_bytes<BM, BN, S, NPX, FUSE, BK>(
 // rows x 8 lanes instead of 16 rows x 4 lanes: twice the rate out of L2)
 // and halves the barriers per K.
 template <int BM, int BN, int S, int AMODE, int EPI, int FUSE, int BK>
-__global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S, EpiParams<EPI>::NP + (FUSE == FUSE_DQB ? 1 : 0), FUSE,
-                                                  BK>()))
+__global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S, dma_npx<EPI, FUSE>(), FUSE, BK>()))
 void qgemm_dma_kernel(GemmArgs g) {
     constexpr int WAVES_N = BN / 64;
     static_assert((BM / 64) * WAVES_N == 4, "4 waves of 64x64");
@@ -149,7 +154,7 @@ void qgemm_dma_kernel(GemmArgs g) {
     constexpr int LPS = A_CH + B_CH;         // DMA instructions per thread per step
     constexpr int STAGE = (BM + BN) * BK;    // bytes per K-step
     constexpr int NP = EpiParams<EPI>::NP;
-    constexpr int NPX = NP + (FUSE == FUSE_DQB ? 1 : 0);   // + the fp32 bias
+    constexpr int NPX = dma_npx<EPI, FUSE>();
     constexpr int PBYTES = NPX * BN * 4;
     constexpr int PWAVES = (PBYTES + 1023) / 1024;   // waves issuing the param DMA
     static_assert(PWAVES <= 4, "param slot");
@@ -162,6 +167,7 @@ void qgemm_dma_kernel(GemmArgs g) {
 
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE + S * PSLOT];
     static_assert(FUSE != FUSE_ADD || (BM * BN) % 4096 == 0, "residual DMA granule");
+    static_assert(FUSE != FUSE_ROW || EPI == EPI_I32, "row term: int32 epilogue");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -363,6 +369,7 @@ void qgemm_dma_kernel(GemmArgs g) {
             const void* base0 = g.c0 ? (const void*)g.c0 : (const void*)g.colsum;
             const void* base;
             if (FUSE == FUSE_DQB && arr == NP) base = g.dq_bias;
+            else if (FUSE == FUSE_ROW && arr == NP) base = g.row_coef;
             else if (arr == 0 || arr >= NP) base = base0;
             else if (EPI == EPI_RQB) base = g.os;
             else if (arr == 1) base = g.cs;
@@ -422,6 +429,10 @@ void qgemm_dma_kernel(GemmArgs g) {
     int c_t = t_first, c_kt = 0, c_gs = 0;
     int c_stage = 0, c_pslot = 0;
     v4i acc[4][4];   // started from c0 by the tile's first K-step
+    // FUSE_ROW: this lane's partial sums of (a - a_sub) over its 16-byte
+    // fragment chunks of rows tm * 16 + frow (the 4 lanes of a row hold the
+    // 4 chunks of each 64-byte K step)
+    int rsum[4] = {0, 0, 0, 0};
 
     // fused dequantize: running min / max of the fp32 outputs of the tile
     float mm_mn = 0.0f, mm_mx = 0.0f;
@@ -462,6 +473,15 @@ void qgemm_dma_kernel(GemmArgs g) {
         decode(c_t, z, m0, n0);
         const int nl = wn * 64 + 16 * fchunk;   // first column of this lane in the tile
         const int nb = n0 + nl;
+        if constexpr (FUSE == FUSE_ROW) {
+            // row sums of the 4 lanes holding a row's chunks (lanes l, l ^ 16,
+            // l ^ 32, l ^ 48), while every lane of the wave is active
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm) {
+                rsum[tm] += __shfl_xor(rsum[tm], 16, 64);
+                rsum[tm] += __shfl_xor(rsum[tm], 32, 64);
+            }
+        }
         if (nb >= g.N) return;
         // a grouped launch: member z's combined scale, zero point, output
         float cm_t = cm;
@@ -481,6 +501,11 @@ void qgemm_dma_kernel(GemmArgs g) {
         for (int tn = 0; tn < 4; ++tn) {
             if constexpr (NP >= 2) p0[tn] = *(const v4i*)(ps + BN * 4 + (nl + 4 * tn) * 4);
             if constexpr (NP >= 3) p1[tn] = *(const v4i*)(ps + 2 * BN * 4 + (nl + 4 * tn) * 4);
+        }
+        v4i rcoef[4];
+        if constexpr (FUSE == FUSE_ROW) {
+#pragma unroll
+            for (int tn = 0; tn < 4; ++tn) rcoef[tn] = *(const v4i*)(ps + NP * BN * 4 + (nl + 4 * tn) * 4);
         }
         const bool full16 = nb + 16 <= g.N;
 #pragma unroll
@@ -506,10 +531,33 @@ void qgemm_dma_kernel(GemmArgs g) {
                 continue;
             }
             if constexpr (EPI == EPI_I32) {
-                int32_t* yrow = (int32_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
                 v4i o[4];
 #pragma unroll
                 for (int tn = 0; tn < 4; ++tn) o[tn] = acc[tm][tn];
+                if constexpr (FUSE == FUSE_ROW) {
+                    // + row_coef[n] * sum_k (a - a_zp), int32 wrap-around: the
+                    // Kp shifted bytes of the row (padding reads the zero
+                    // point) sum to the row sum + Kp * alpha
+                    const uint32_t r = (uint32_t)rsum[tm] - (uint32_t)g.Kp * (uint32_t)alpha;
+#pragma unroll
+                    for (int tn = 0; tn < 4; ++tn)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            o[tn][q] = (int)((uint32_t)o[tn][q] + (uint32_t)rcoef[tn][q] * r);
+                    if (g.y_nchw) {
+                        // NCHW [img][n][s]: 16 lanes store 16 consecutive pixels
+                        // of one channel plane
+                        const int img = (int)fast_div((uint32_t)m, g.div_sp_mul, g.div_sp_shift);
+                        const int sp = m - img * sp_out;
+                        int32_t* yb = (int32_t*)g.y + (long long)z * g.y_bstride +
+                                      ((long long)img * g.ldy + nb) * sp_out + sp;
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+                            if (nb + i < g.N) yb[(long long)i * sp_out] = o[i >> 2][i & 3];
+                        continue;
+                    }
+                }
+                int32_t* yrow = (int32_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
                 if (full16 && ((((uintptr_t)yrow) & 15) == 0)) {
 #pragma unroll
                     for (int tn = 0; tn < 4; ++tn) *(v4i*)(yrow + 4 * tn) = o[tn];
@@ -723,6 +771,17 @@ void qgemm_dma_kernel(GemmArgs g) {
             wf[tn] = *(const v4i*)(st + BM * BK + dma_lds_off<BK>(wn * 64 + tn * 16 + frow, c));
     };
     auto mma = [&](const v4i (&xf)[4], const v4i (&wf)[4], bool first) {
+        if constexpr (FUSE == FUSE_ROW) {
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm) {
+                int r = first ? 0 : rsum[tm];
+                r = __builtin_amdgcn_sdot4(xf[tm].x, 0x01010101, r, false);
+                r = __builtin_amdgcn_sdot4(xf[tm].y, 0x01010101, r, false);
+                r = __builtin_amdgcn_sdot4(xf[tm].z, 0x01010101, r, false);
+                r = __builtin_amdgcn_sdot4(xf[tm].w, 0x01010101, r, false);
+                rsum[tm] = r;
+            }
+        }
         if (first) {
             // the tile's constants landed with its first K-step: the first
             // MFMAs start from c0[n] (this lane's 16 columns), or from
@@ -840,6 +899,13 @@ hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
         }
         return hipErrorNotSupported;
     }
+    if (g.row_coef) {
+        if constexpr (AMODE == A_CONV || AMODE == A_CONVU) {
+            if (g.epi == EPI_I32 && g.H > 0)
+                return launch_dma<BM, BN, S, AMODE, EPI_I32, FUSE_ROW, BK>(g, batch, s);
+        }
+        return hipErrorNotSupported;
+    }
     if (g.add_other) {
         // the residual tile shares the block's LDS: 64-byte stages only
         if constexpr (BK == 64 && (AMODE == A_CONV || AMODE == A_CONVU || AMODE == A_DENSE)) {
@@ -869,7 +935,11 @@ hipError_t launch_dma_first(const GemmArgs& g, int batch, hipStream_t s) {
 }  // namespace
 
 bool qgemm_dma_eligible(const GemmArgs& g, int vec) {
-    if (g.y_nchw) return false;
+    // the per-row term and an NCHW store: int32 output of a convolution only
+    const bool row_term = g.row_coef != nullptr && g.epi == EPI_I32;
+    if (g.y_nchw && !(row_term && g.H > 0)) return false;
+    if (row_term && (g.H <= 0 || g.rowsum != nullptr || g.alpha_zp_dev || g.add_other || g.dq_bias || g.kWp > 0))
+        return false;
     // accumulators start at c0: |c0| + 128*128*K must stay inside int32
     if (g.c0_absmax + 16384LL * (long long)g.Kp >= 0x7fffffffLL) return false;
     if (g.M > 0x7fffffff / 2) return false;

@@ -828,6 +828,65 @@ def test_conv_integer(dev, xdt, wdt, per_ch, s, p, d, group, shape):
     assert np.array_equal(to_np(y), ref)
 
 
+@pytest.mark.parametrize("xdt,wdt,wz_mode,k,s,p,group,shape,OC", [
+    # w_zp equal to the packed weights' shift: no patch-sum term
+    (np.uint8, np.int8, "shift", 3, (1, 1), (1, 1), 1, (4, 64, 20, 20), 64),
+    (np.uint8, np.uint8, "shift", 3, (1, 1), (1, 1), 1, (2, 32, 13, 13), 48),
+    # groups of 64 channels (uniform tap walk), stride 2
+    (np.uint8, np.int8, "pc", 3, (2, 2), (1, 1), 2, (2, 128, 17, 17), 128),
+    (np.int8, np.int8, "pc", 5, (1, 1), (2, 2), 1, (2, 64, 14, 14), 96),
+    (np.uint8, np.int8, "scalar", 7, (2, 2), (3, 3), 1, (2, 16, 30, 30), 64),
+    (np.uint8, np.int8, "pc", 1, (1, 1), (0, 0), 1, (3, 256, 7, 7), 200),
+    # K = 2304: 128-byte K stages
+    (np.uint8, np.int8, "pc", 3, (1, 1), (1, 1), 1, (2, 256, 14, 14), 256)])
+def test_conv_integer_shapes(dev, xdt, wdt, wz_mode, k, s, p, group, shape, OC):
+    """ConvInteger on the implicit-GEMM kernel over kernel sizes, groups,
+    strides and the three weight zero-point forms: bit-exact against the
+    oracle's integer convolution."""
+    rng = np.random.default_rng(sum(shape) + k * 7 + OC)
+    info = lambda t: (0, 256) if t == np.uint8 else (-128, 128)
+    N, C, Hh, W = shape
+    x = rng.integers(*info(xdt), shape, dtype=xdt)
+    w = rng.integers(*info(wdt), (OC, C // group, k, k), dtype=wdt)
+    x_zp = 97 if xdt == np.uint8 else 5
+    shift = 128 if wdt == np.uint8 else 0
+    w_zp = {"shift": shift, "scalar": shift + 3, "pc": rng.integers(*info(wdt), OC)}[wz_mode]
+    ref = O.conv_integer(x, w, x_zp, w_zp, s, p, (1, 1), group)
+    y = H.conv_integer(to_dev(x, dev), to_dev(w, dev), x_zp, w_zp, s, p, (1, 1), group)
+    assert np.array_equal(to_np(y), ref)
+
+
+def test_conv_integer_handle_reuse(dev):
+    """One handle, three calls in a row: per-channel zero points (patch sums
+    computed), then the shift zero point (patch sums skipped, their
+    coefficients 0) with other inputs, then per-channel again with another
+    x_zp; each equals the oracle."""
+    import ctypes as ct
+    import torch
+    from nnr_amd import _lib
+    L = _lib.lib()
+    rng = np.random.default_rng(77)
+    N, C, HW, OC = 3, 64, 15, 80
+    h = ct.c_void_p()
+    _lib.check(L.nnrh_conv_integer_create(ct.byref(h), N, C, HW, HW, OC, 3, 3, 1, 1, 1, 1, 1, 1, HW, HW, 1,
+                                          H.U8, H.S8))
+    try:
+        for x_zp, wz_mode in ((128, "pc"), (0, "shift"), (201, "pc")):
+            x = rng.integers(0, 256, (N, C, HW, HW), dtype=np.uint8)
+            w = rng.integers(-128, 128, (OC, C, 3, 3), dtype=np.int8)
+            wz = rng.integers(-128, 128, OC).astype(np.int32) if wz_mode == "pc" else np.zeros(1, np.int32)
+            xd, wd = to_dev(x, dev), to_dev(w, dev)
+            wzd = to_dev(wz, dev) if wz.size > 1 else None
+            y = torch.empty((N, OC, HW, HW), dtype=torch.int32, device=dev)
+            _lib.check(L.nnrh_conv_integer_run(h, _lib.ptr(xd), _lib.ptr(wd), x_zp, 0,
+                                               _lib.ptr(wzd) if wzd is not None else None, _lib.ptr(y),
+                                               _lib.cur_stream()))
+            ref = O.conv_integer(x, w, x_zp, wz if wz.size > 1 else 0, (1, 1), (1, 1), (1, 1), 1)
+            assert np.array_equal(to_np(y), ref), (x_zp, wz_mode)
+    finally:
+        L.nnrh_conv_integer_destroy(h)
+
+
 @pytest.mark.parametrize("m,n,k,batch,a_dt,b_dt,bias", [
     (40, 136, 96, 3, np.uint8, np.int8, True), (128, 768, 768, 2, np.uint8, np.int8, True),
     (70, 64, 48, 1, np.int8, np.int8, False), (33, 200, 64, 2, np.uint8, np.uint8, True)])
