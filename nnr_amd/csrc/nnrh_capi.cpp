@@ -1718,13 +1718,15 @@ extern "C" int nnrh_conv_integer_run(nnrh_conv_integer_t h, const void* x, const
     const int alpha = x_zp - (xu8 ? 128 : 0);
     GemmArgs g = h->g;
     {
+        ConvIntPrepArgs q{};
+        q.x = (const uint8_t*)x; q.xs = h->xs;
+        q.N = h->N; q.HW = h->iH * h->iW; q.G = h->G; q.Cg = h->Cg; q.Cgp = h->Cgp;
+        q.fill = (uint32_t)(x_zp & 0xff);
+        q.w = (const uint8_t*)w; q.w_u8 = wu8 ? 1 : 0; q.OCg = h->OCg; q.kH = h->g.kH; q.kW = h->g.kW;
+        q.Kp = h->Kp; q.Np = h->Np; q.alpha = alpha; q.w_zp = w_zp; q.w_zp_dev = w_zp_dev;
+        q.wpack = h->wpack; q.c0 = h->c0; q.row_coef = h->coef;
         ProfScope ps("conv_integer_prep", s);
-        HIP_TRY(launch_nchw_to_nhwc_group_pad((const uint8_t*)x, h->xs, h->N, h->iH * h->iW, h->G, h->Cg, h->Cgp,
-                                              (uint8_t)(x_zp & 0xff), s),
-                "conv_integer_nhwc");
-        HIP_TRY(launch_conv_integer_pack((const uint8_t*)w, wu8 ? 1 : 0, h->G, h->OCg, h->Cg, h->Cgp, h->g.kH,
-                                         h->g.kW, h->Kp, h->Np, alpha, w_zp, w_zp_dev, h->wpack, h->c0, h->coef, s),
-                "conv_integer_pack");
+        HIP_TRY(launch_conv_integer_prep(q, s), "conv_integer_prep");
     }
     g.row_coef = h->coef;
     g.alpha = alpha;

@@ -241,17 +241,27 @@ hipError_t launch_rowsum_conv(const uint8_t* x, int N, int H, int W, int Cs,
                               int kW, int sH, int sW, int dH, int dW,
                               int pad_t, int pad_l, int a_signed, int x_zp,
                               int32_t* out, long long out_bstride, hipStream_t s);
-// NCHW -> NHWC with each group's Cg channels padded to Cgp (a multiple of 16)
-// with the fill byte: y[n][p][z * Cgp + c] = c < Cg ? x[n][z * Cg + c][p] : fill
-hipError_t launch_nchw_to_nhwc_group_pad(const uint8_t* x, uint8_t* y, int N, int HW, int G, int Cg,
-                                         int Cgp, uint8_t fill, hipStream_t s);
-// ConvInteger weights W[G * OCg][Cg][kH][kW] (int8 / uint8) -> packed
-// [G][Np][Kp] int8 (uint8 shifted by 128), K order (kh, kw, c < Cgp), zero
-// padded; c0[n] = -alpha * colsum[n] with alpha = x_zp - a_sub; row_coef[n] =
-// b_sub - w_zp[oc] (w_zp_dev[oc] when given, else w_zp)
-hipError_t launch_conv_integer_pack(const uint8_t* w, int w_u8, int G, int OCg, int Cg, int Cgp, int kH, int kW,
-                                    int Kp, int Np, int alpha, int w_zp, const int32_t* w_zp_dev, int8_t* wpack,
-                                    int32_t* c0, int32_t* row_coef, hipStream_t s);
+// ConvInteger's per-call preparation, one launch: the NCHW input x to NHWC xs
+// with each group's Cg channels padded to Cgp (a multiple of 16) with the fill
+// byte, xs[n][p][z * Cgp + c] = c < Cg ? x[n][z * Cg + c][p] : fill; and the
+// weights W[G * OCg][Cg][kH][kW] (int8 / uint8) packed to [G][Np][Kp] int8
+// (uint8 shifted by 128), K order (kh, kw, c < Cgp), zero padded, with c0[n] =
+// -alpha * colsum[n] (alpha = x_zp - a_sub) and row_coef[n] = b_sub - w_zp[oc]
+// (w_zp_dev[oc] when given, else w_zp)
+struct ConvIntPrepArgs {
+    const uint8_t* x;
+    uint8_t* xs;
+    int N, HW, G, Cg, Cgp;
+    uint32_t fill;
+    const uint8_t* w;
+    int w_u8, OCg, kH, kW, Kp, Np, alpha, w_zp;
+    const int32_t* w_zp_dev;
+    int8_t* wpack;
+    int32_t* c0;
+    int32_t* row_coef;
+    int copy_blocks, vec;   // set by the launcher
+};
+hipError_t launch_conv_integer_prep(ConvIntPrepArgs a, hipStream_t s);
 // Pack a row-major B[K][N] (int8 or uint8) into the kernel's [Np][Kp]
 // permuted layout and compute colsum[n] = sum_k (b - b_sub).
 hipError_t launch_pack_b_dense(const void* b, long long b_bstride, int K,

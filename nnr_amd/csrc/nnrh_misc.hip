@@ -838,48 +838,46 @@ hipError_t launch_rowsum_conv(const uint8_t* x, int N, int H, int W, int Cs, int
 // with every group's channels padded to a multiple of 16, and the weights
 // packed per call (they are an input of the operator).
 
-// NCHW -> group-padded NHWC: one thread per (image, 4 consecutive pixels,
-// 16-channel output chunk), the chunk index fastest so that the 4 chunks of a
-// 64-channel pixel row are neighbouring lanes (whole-row stores). A thread
-// loads 16 channel planes x 4 pixels as dwords (bytes when HW % 4 != 0 or x is
-// not 4-byte aligned) and transposes them with byte permutes into 4 pixels x
-// 16 channels.
-__global__ __launch_bounds__(256) void nchw_to_nhwc_group_pad_kernel(const uint8_t* __restrict x,
-                                                                     uint8_t* __restrict y, int N, int HW, int G,
-                                                                     int Cg, int Cgp, uint32_t fill, int vec) {
-    const int cpp = G * Cgp / 16;         // 16-channel chunks per pixel
-    const int qpi = (HW + 3) / 4;         // pixel quads per image
-    const long long total = (long long)N * qpi * cpp;
-    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
+// ConvInteger's per-call preparation in one launch: the first blocks copy the
+// NCHW input to group-padded NHWC, the rest pack the weights.
+//
+// Copy: one thread per (image, 4 consecutive pixels, 16-channel output chunk),
+// the chunk index fastest so that the chunks of a pixel row are neighbouring
+// lanes (whole-row stores). A thread loads 16 channel planes x 4 pixels as
+// dwords (bytes when HW % 4 != 0 or x is not 4-byte aligned) and transposes
+// them with byte permutes into 4 pixels x 16 channels.
+__device__ __forceinline__ void ci_copy(const ConvIntPrepArgs& a, long long i) {
+    const int cpp = a.G * a.Cgp / 16;     // 16-channel chunks per pixel
+    const int qpi = (a.HW + 3) / 4;       // pixel quads per image
+    if (i >= (long long)a.N * qpi * cpp) return;
     const int c = (int)(i % cpp);
     const long long t = i / cpp;
     const int q = (int)(t % qpi);
     const int n = (int)(t / qpi);
-    const int z = c * 16 / Cgp, c0 = c * 16 - z * Cgp;
+    const int z = c * 16 / a.Cgp, c0 = c * 16 - z * a.Cgp;
     const int p = 4 * q;
-    const uint8_t* src = x + ((long long)n * G + z) * Cg * (long long)HW + p;
-    const uint32_t fill4 = fill * 0x01010101u;
+    const uint8_t* src = a.x + ((long long)n * a.G + z) * a.Cg * (long long)a.HW + p;
+    const uint32_t fill4 = a.fill * 0x01010101u;
     uint32_t v[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         const int ch = c0 + j;
         uint32_t d = fill4;
-        if (ch < Cg) {
-            const uint8_t* sp = src + (long long)ch * HW;
-            if (vec) {
+        if (ch < a.Cg) {
+            const uint8_t* sp = src + (long long)ch * a.HW;
+            if (a.vec) {
                 d = *(const uint32_t*)sp;
             } else {
                 d = 0;
-                for (int b = 0; b < 4; ++b) d |= (p + b < HW ? (uint32_t)sp[b] : 0u) << (8 * b);
+                for (int b = 0; b < 4; ++b) d |= (p + b < a.HW ? (uint32_t)sp[b] : 0u) << (8 * b);
             }
         }
         v[j] = d;
     }
-    uint8_t* dst = y + ((long long)n * HW + p) * (G * Cgp) + (long long)z * Cgp + c0;
+    uint8_t* dst = a.xs + ((long long)n * a.HW + p) * (a.G * a.Cgp) + (long long)z * a.Cgp + c0;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-        if (p + b >= HW) break;
+        if (p + b >= a.HW) break;
         // byte b of v[4k .. 4k + 3] -> dword k
         const uint32_t sel = (uint32_t)b | ((uint32_t)(4 + b) << 8) | 0x0c0c0000u;
         uint32_t w[4];
@@ -889,65 +887,64 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_group_pad_kernel(const uint8
             const uint32_t hi = __builtin_amdgcn_perm(v[4 * k + 3], v[4 * k + 2], sel);
             w[k] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
         }
-        *(uint4*)(dst + (long long)b * (G * Cgp)) = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint4*)(dst + (long long)b * (a.G * a.Cgp)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
 
-hipError_t launch_nchw_to_nhwc_group_pad(const uint8_t* x, uint8_t* y, int N, int HW, int G, int Cg, int Cgp,
-                                         uint8_t fill, hipStream_t s) {
-    if (Cgp % 16 || Cg > Cgp || G <= 0) return hipErrorInvalidValue;
-    const long long total = (long long)N * ((HW + 3) / 4) * (G * Cgp / 16);
-    if (total <= 0) return hipSuccess;
-    const int vec = (HW % 4 == 0 && (((uintptr_t)x) & 3) == 0) ? 1 : 0;
-    hipLaunchKernelGGL(nchw_to_nhwc_group_pad_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, y,
-                       N, HW, G, Cg, Cgp, (uint32_t)fill, vec);
-    return hipGetLastError();
-}
-
-// one block per packed row (z, n): the row's Kp bytes in (kh, kw, c) order,
-// its column sum, the accumulator start c0 and the row-term coefficient
-__global__ __launch_bounds__(256) void conv_integer_pack_kernel(const uint8_t* __restrict w, int w_u8, int OCg,
-                                                                int Cg, int Cgp, int kH, int kW, int Kp, int Np,
-                                                                int alpha, int w_zp,
-                                                                const int32_t* __restrict w_zp_dev,
-                                                                int8_t* __restrict wpack, int32_t* __restrict c0,
-                                                                int32_t* __restrict row_coef) {
-    const int n = blockIdx.x, z = blockIdx.y;
-    const int oc = z * OCg + n;
-    const int K = kH * kW * Cgp;
-    const uint8_t bx = w_u8 ? 0x80 : 0;
-    int8_t* row = wpack + ((long long)z * Np + packed_row_of_col(n)) * Kp;
+// Pack: one block per packed row (z, n): the row's Kp bytes in (kh, kw, c)
+// order, its column sum, the accumulator start c0 and the row-term coefficient
+__device__ __forceinline__ void ci_pack(const ConvIntPrepArgs& a, int n, int z) {
+    __shared__ int32_t part[4];
+    const int oc = z * a.OCg + n;
+    const int K = a.kH * a.kW * a.Cgp;
+    const uint8_t bx = a.w_u8 ? 0x80 : 0;
+    int8_t* row = a.wpack + ((long long)z * a.Np + packed_row_of_col(n)) * a.Kp;
     int32_t s = 0;
-    for (int k = threadIdx.x; k < Kp; k += blockDim.x) {
+    for (int k = threadIdx.x; k < a.Kp; k += blockDim.x) {
         int8_t v = 0;
-        if (n < OCg && k < K) {
-            const int c = k % Cgp, t = k / Cgp;
-            const int kh = t / kW, kw = t - kh * kW;
-            if (c < Cg) v = (int8_t)(w[(((long long)oc * Cg + c) * kH + kh) * kW + kw] ^ bx);
+        if (n < a.OCg && k < K) {
+            const int c = k % a.Cgp, t = k / a.Cgp;
+            const int kh = t / a.kW, kw = t - kh * a.kW;
+            if (c < a.Cg) v = (int8_t)(a.w[(((long long)oc * a.Cg + c) * a.kH + kh) * a.kW + kw] ^ bx);
         }
         row[k] = v;
         s += v;
     }
-    __shared__ int32_t part[4];
     for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
     __syncthreads();
     if (threadIdx.x == 0) {
         const int32_t cs = part[0] + part[1] + part[2] + part[3];
-        const long long pi = (long long)z * Np + n;
-        c0[pi] = (int32_t)(0u - (uint32_t)alpha * (uint32_t)cs);
+        const long long pi = (long long)z * a.Np + n;
+        a.c0[pi] = (int32_t)(0u - (uint32_t)a.alpha * (uint32_t)cs);
         int coef = 0;
-        if (n < OCg) coef = (w_u8 ? 128 : 0) - (w_zp_dev ? w_zp_dev[oc] : w_zp);
-        row_coef[pi] = coef;
+        if (n < a.OCg) coef = (a.w_u8 ? 128 : 0) - (a.w_zp_dev ? a.w_zp_dev[oc] : a.w_zp);
+        a.row_coef[pi] = coef;
     }
 }
 
-hipError_t launch_conv_integer_pack(const uint8_t* w, int w_u8, int G, int OCg, int Cg, int Cgp, int kH, int kW,
-                                    int Kp, int Np, int alpha, int w_zp, const int32_t* w_zp_dev, int8_t* wpack,
-                                    int32_t* c0, int32_t* row_coef, hipStream_t s) {
-    if (G <= 0 || OCg <= 0 || Np < OCg || (long long)kH * kW * Cgp > Kp) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(conv_integer_pack_kernel, dim3(Np, G), dim3(256), 0, s, w, w_u8, OCg, Cg, Cgp, kH, kW, Kp,
-                       Np, alpha, w_zp, w_zp_dev, wpack, c0, row_coef);
+__global__ __launch_bounds__(256) void conv_integer_prep_kernel(ConvIntPrepArgs a) {
+    // block-uniform split: copy blocks first, then one block per packed row
+    const int b = blockIdx.x;
+    if (b < a.copy_blocks) {
+        ci_copy(a, (long long)b * blockDim.x + threadIdx.x);
+    } else {
+        const int r = b - a.copy_blocks;
+        ci_pack(a, r % a.Np, r / a.Np);
+    }
+}
+
+hipError_t launch_conv_integer_prep(ConvIntPrepArgs a, hipStream_t s) {
+    if (a.Cgp % 16 || a.Cg > a.Cgp || a.G <= 0 || a.OCg <= 0 || a.Np < a.OCg ||
+        (long long)a.kH * a.kW * a.Cgp > a.Kp)
+        return hipErrorInvalidValue;
+    const long long total = (long long)a.N * ((a.HW + 3) / 4) * (a.G * a.Cgp / 16);
+    const long long copy_blocks = (total + 255) / 256;
+    const long long blocks = copy_blocks + (long long)a.Np * a.G;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+    a.copy_blocks = (int)copy_blocks;
+    a.vec = (a.HW % 4 == 0 && (((uintptr_t)a.x) & 3) == 0) ? 1 : 0;
+    hipLaunchKernelGGL(conv_integer_prep_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
