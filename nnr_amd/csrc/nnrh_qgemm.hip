@@ -532,6 +532,7 @@ hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec, hipStre
     if (g.add_other || g.dq_bias) return hipErrorNotSupported;   // fusions: pipelined kernel only
     switch (tile) {
     case TILE_128x128:
+    case TILE_256x128:
         return conv ? launch_vec<128, 128, A_CONV>(g, batch, vec, s)
                     : launch_vec<128, 128, A_DENSE>(g, batch, vec, s);
     case TILE_256x64:

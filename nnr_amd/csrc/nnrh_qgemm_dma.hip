@@ -132,22 +132,31 @@ constexpr int dma_npx() { return EpiParams<EPI>::NP + (FUSE == FUSE_DQB || FUSE 
 template <int BM, int BN, int S, int NPX, int FUSE, int BK>
 constexpr int dma_lds_bytes() { return S * (BM + BN) * BK + S * dma_pslot_bytes<BM, BN, S, NPX, FUSE>(); }
 // blocks per CU the kernel is compiled for: LDS and registers must fit them
+// (4-wave blocks: 3 per CU when the LDS fits them, else 2; 8-wave blocks: 2)
 template <int BM, int BN, int S, int NPX, int FUSE, int BK>
-constexpr int dma_min_blocks() { return dma_lds_bytes<BM, BN, S, NPX, FUSE, BK>() * 3 <= 160 * 1024 ? 3 : 2; }
+constexpr int dma_min_blocks() {
+    return (BM / 64) * (BN / 64) == 8 ? 2 : (dma_lds_bytes<BM, BN, S, NPX, FUSE, BK>() * 3 <= 160 * 1024 ? 3 : 2);
+}
+// threads of a block: a wave per 64 x 64 sub-tile
+template <int BM, int BN>
+constexpr int dma_threads() { return (BM / 64) * (BN / 64) * 64; }
 
 // BK: K bytes per pipeline stage, 64 (one MFMA K-step) or 128 (two). A
 // 128-byte stage fetches whole 128-byte rows with each DMA instruction (8
 // rows x 8 lanes instead of 16 rows x 4 lanes: twice the rate out of L2)
 // and halves the barriers per K.
 template <int BM, int BN, int S, int AMODE, int EPI, int FUSE, int BK>
-__global__ __launch_bounds__(256, (dma_min_blocks<BM, BN, S, dma_npx<EPI, FUSE>(), FUSE, BK>()))
+__global__ __launch_bounds__((dma_threads<BM, BN>()), (dma_min_blocks<BM, BN, S, dma_npx<EPI, FUSE>(), FUSE, BK>()))
 void qgemm_dma_kernel(GemmArgs g) {
     constexpr int WAVES_N = BN / 64;
-    static_assert((BM / 64) * WAVES_N == 4, "4 waves of 64x64");
+    constexpr int WAVES = (BM / 64) * WAVES_N;
+    constexpr int NT = 64 * WAVES;           // threads
+    static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves of 64x64");
     static_assert(BK == 64 || BK == 128, "stage width");
     static_assert(BK == 64 || AMODE != A_CONV4, "first layer: 64-byte stages");
     constexpr int CPR = BK / 16;             // 16-byte chunks per LDS row
-    constexpr int RPR = 4096 / BK;           // rows one DMA round of 256 threads fills
+    constexpr int RND = NT * 16;             // bytes one DMA round of the block fills
+    constexpr int RPR = RND / BK;            // rows one DMA round fills
     constexpr int A_CH = BM / RPR;           // DMA chunks per thread per step (A)
     constexpr int B_CH = BN / RPR;           // (B)
     constexpr int KK = BK / 64;              // MFMA K-steps per stage
@@ -157,16 +166,17 @@ void qgemm_dma_kernel(GemmArgs g) {
     constexpr int NPX = dma_npx<EPI, FUSE>();
     constexpr int PBYTES = NPX * BN * 4;
     constexpr int PWAVES = (PBYTES + 1023) / 1024;   // waves issuing the param DMA
-    static_assert(PWAVES <= 4, "param slot");
+    static_assert(PWAVES <= WAVES, "param slot");
     // per-tile slot: the per-column arrays, then (fused add) the residual tile
     // as BM rows of BN bytes, 16-byte chunks XOR-swizzled by row
     constexpr int PPAR = PWAVES * 1024;
     constexpr int PSLOT = dma_pslot_bytes<BM, BN, S, NPX, FUSE>();
     constexpr int RCPR = BN / 16;                    // residual chunks per row
-    constexpr int RCH = FUSE == FUSE_ADD ? BM * BN / 4096 : 0;   // residual DMAs per thread
+    constexpr int RCH = FUSE == FUSE_ADD ? BM * BN / RND : 0;   // residual DMAs per thread
 
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE + S * PSLOT];
-    static_assert(FUSE != FUSE_ADD || (BM * BN) % 4096 == 0, "residual DMA granule");
+    static_assert(FUSE != FUSE_ADD || (BM * BN) % RND == 0, "residual DMA granule");
+    static_assert(BM % RPR == 0 && BN % RPR == 0, "DMA rounds per tile");
     static_assert(FUSE != FUSE_ROW || EPI == EPI_I32, "row term: int32 epilogue");
 
     const int tid = threadIdx.x;
@@ -350,11 +360,11 @@ void qgemm_dma_kernel(GemmArgs g) {
                         src = p_a + a_base[j] + ((long long)(ih * g.W + iw) * g.Cs + kc_ic);
                 }
             }
-            dma16(src, st + wave * 1024 + j * 4096);
+            dma16(src, st + wave * 1024 + j * RND);
         }
 #pragma unroll
         for (int j = 0; j < B_CH; ++j)
-            dma16((const void*)(b_addr[j] + (uint64_t)k0), st + BM * BK + wave * 1024 + j * 4096);
+            dma16((const void*)(b_addr[j] + (uint64_t)k0), st + BM * BK + wave * 1024 + j * RND);
         if (p_kt == 0 && wave < PWAVES) {
             // per-column constants of the tile: NP arrays of BN int32/float,
             // one 16-byte chunk per lane; chunks past the arrays reload the
@@ -385,13 +395,13 @@ void qgemm_dma_kernel(GemmArgs g) {
                 const int m0 = p_setup_m0;
 #pragma unroll
                 for (int j = 0; j < RCH; ++j) {
-                    const int p = j * 256 + wave * 64 + lane;   // chunk position in the slot
+                    const int p = j * NT + wave * 64 + lane;   // chunk position in the slot
                     const int row = p / RCPR, pc = p - row * RCPR;
                     const int lc = pc ^ (row & (RCPR - 1));
                     const int m = m0 + row, n = p_n0 + lc * 16;
                     const uint8_t* src = pad16;
                     if (m < g.M && n < g.N) src = g.add_other + (long long)m * g.ldy + n;
-                    dma16(src, lds + S * STAGE + p_pslot + PPAR + (j * 256 + wave * 64) * 16);
+                    dma16(src, lds + S * STAGE + p_pslot + PPAR + (j * NT + wave * 64) * 16);
                 }
             }
         }
@@ -820,14 +830,14 @@ void qgemm_dma_kernel(GemmArgs g) {
             if (FUSE == FUSE_ADD && g.add_conv_is_a) epilogue(std::true_type{});
             else epilogue(std::false_type{});
             if (FUSE == FUSE_DQB && g.mm_parts) {
-                // one (min, max) pair per (tile, wave), at 2 * (4 * tile + wave)
+                // one (min, max) pair per (tile, wave), at 2 * (WAVES * tile + wave)
 #pragma unroll
                 for (int off = 32; off > 0; off >>= 1) {
                     mm_mn = fminf(mm_mn, __shfl_xor(mm_mn, off, 64));
                     mm_mx = fmaxf(mm_mx, __shfl_xor(mm_mx, off, 64));
                 }
                 if (lane == 0)
-                    *(float2*)(g.mm_parts + 2 * (4 * c_t + wave)) = make_float2(mm_mn, mm_mx);
+                    *(float2*)(g.mm_parts + 2 * (WAVES * c_t + wave)) = make_float2(mm_mn, mm_mx);
                 mm_mn = 0.0f;
                 mm_mx = 0.0f;
             }
@@ -863,7 +873,8 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
     static int resident = 0;
     if (resident <= 0) {
         int per_cu = 0, dev = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) != hipSuccess || per_cu < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, dma_threads<BM, BN>(), 0) != hipSuccess ||
+            per_cu < 1)
             per_cu = 1;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
@@ -886,7 +897,7 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
         fast_div_consts((uint32_t)(g.oH * g.oW), &a.div_sp_mul, &a.div_sp_shift);
         fast_div_consts((uint32_t)g.oW, &a.div_ow_mul, &a.div_ow_shift);
     }
-    hipLaunchKernelGGL(kern, dim3(G, 1, 1), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(kern, dim3(G, 1, 1), dim3(dma_threads<BM, BN>()), 0, s, a);
     return hipGetLastError();
 }
 
@@ -919,6 +930,26 @@ hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
     case EPI_RQA: return launch_dma<BM, BN, S, AMODE, EPI_RQA, FUSE_NONE, BK>(g, batch, s);
     case EPI_RQD: return launch_dma<BM, BN, S, AMODE, EPI_RQD, FUSE_NONE, BK>(g, batch, s);
     case EPI_I32: return launch_dma<BM, BN, S, AMODE, EPI_I32, FUSE_NONE, BK>(g, batch, s);
+    default: return hipErrorNotSupported;
+    }
+}
+
+// 8-wave tiles: no fused add or dequantize (their LDS slots would not fit
+// two blocks per CU)
+template <int BM, int BN, int S, int AMODE>
+hipError_t launch_dma_plain(const GemmArgs& g, int batch, hipStream_t s) {
+    if (g.add_other || g.dq_bias) return hipErrorNotSupported;
+    if (g.row_coef) {
+        if constexpr (AMODE == A_CONV || AMODE == A_CONVU) {
+            if (g.epi == EPI_I32 && g.H > 0) return launch_dma<BM, BN, S, AMODE, EPI_I32, FUSE_ROW>(g, batch, s);
+        }
+        return hipErrorNotSupported;
+    }
+    switch (g.epi) {
+    case EPI_RQB: return launch_dma<BM, BN, S, AMODE, EPI_RQB>(g, batch, s);
+    case EPI_RQA: return launch_dma<BM, BN, S, AMODE, EPI_RQA>(g, batch, s);
+    case EPI_RQD: return launch_dma<BM, BN, S, AMODE, EPI_RQD>(g, batch, s);
+    case EPI_I32: return launch_dma<BM, BN, S, AMODE, EPI_I32>(g, batch, s);
     default: return hipErrorNotSupported;
     }
 }
@@ -989,6 +1020,21 @@ hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t 
         }
     }
     const bool uni = conv && conv_uniform_taps(g);
+    // 8-wave 256x128 tiles (2 blocks per CU, 16 waves, 3 stages; a quarter
+    // fewer global->LDS bytes per MFMA op than 128x128) where N >= 256 and
+    // they still give at least 384 tiles for the 512 resident blocks: fewer
+    // than that leaves CUs idle, and at N = 128 the 128x128 grid balances
+    // better (measured per ResNet-50 layer)
+    if (tile == TILE_128x128 && g.add_other == nullptr && g.dq_bias == nullptr && g.N >= 256) {
+        const long long t256 = (long long)((g.M + 255) / 256) * ((g.N + 127) / 128) * batch;
+        if (t256 >= 384) tile = TILE_256x128;
+    }
+    if (tile == TILE_256x128) {
+        if (g.add_other || g.dq_bias) tile = TILE_128x128;
+        else if (!conv) return launch_dma_plain<256, 128, 3, A_DENSE>(g, batch, s);
+        else return uni ? launch_dma_plain<256, 128, 3, A_CONVU>(g, batch, s)
+                        : launch_dma_plain<256, 128, 3, A_CONV>(g, batch, s);
+    }
     // 128-byte stages (2 stages at 2 blocks per CU) where the packed K is a
     // multiple of 128 with at least two stages per tile and, for the
     // uniform-tap producer, a step stays inside one tap. Not with a fused

@@ -129,6 +129,35 @@ def test_qconv_config2(dev):
                   y_nhwc=1, post_fn=1, y_zp=0, x_zp=128)
 
 
+@pytest.mark.parametrize("N,C,Hh,W,OC,k,kw", [
+    # 1x1 as a dense GEMM, ragged last row tile (M = 46800), three column tiles
+    (13, 64, 60, 60, 384, 1, dict(x_nhwc=1, y_zp=5)),
+    # 3x3 uniform tap walk (C % 64 == 0), NR16
+    (11, 64, 48, 48, 512, 3, dict(pads=(1, 1, 1, 1), x_nhwc=1, post_fn=1, y_zp=0)),
+    # 3x3 with C = 48: the per-chunk tap walk
+    (11, 48, 48, 48, 512, 3, dict(pads=(1, 1, 1, 1), x_nhwc=1, y_zp=9)),
+    # stride 2
+    (40, 64, 48, 48, 640, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), x_nhwc=1, y_zp=2))])
+def test_qconv_tile_256x128(dev, N, C, Hh, W, OC, k, kw):
+    """Convolutions big enough for the 8-wave 256x128 tile (N >= 256 and at
+    least 384 such tiles): bit-exact with the oracle like the 4-wave tiles."""
+    x_nhwc = kw.pop("x_nhwc", 0)
+    run_conv_case(dev, N, C, Hh, W, OC, k, seed=N + OC, y_nhwc=1, x_nhwc=x_nhwc, **kw)
+
+
+def test_conv_integer_tile_256x128(dev):
+    """ConvInteger on the 8-wave tile: the in-kernel row sums of the weight
+    zero-point term with 8 waves (per-channel w_zp), int32 NCHW output."""
+    rng = np.random.default_rng(88)
+    N, C, HW, OC = 6, 64, 64, 512
+    x = rng.integers(0, 256, (N, C, HW, HW), dtype=np.uint8)
+    w = rng.integers(-128, 128, (OC, C, 3, 3), dtype=np.int8)
+    wz = rng.integers(-128, 128, OC)
+    ref = O.conv_integer(x, w, 113, wz, (1, 1), (1, 1), (1, 1), 1)
+    y = H.conv_integer(to_dev(x, dev), to_dev(w, dev), 113, wz, (1, 1), (1, 1), (1, 1), 1)
+    assert np.array_equal(to_np(y), ref)
+
+
 CONV_CASES = [
     # name, N, C, H, W, OC, k, kwargs
     ("nr16_nhwc_in", 2, 64, 14, 15, 128, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1, y_zp=3)),
