@@ -129,13 +129,16 @@ constexpr int dma_pslot_bytes() {
 // fused dequantize, + the row-term coefficient
 template <int EPI, int FUSE>
 constexpr int dma_npx() { return EpiParams<EPI>::NP + (FUSE == FUSE_DQB || FUSE == FUSE_ROW ? 1 : 0); }
-template <int BM, int BN, int S, int NPX, int FUSE, int BK>
-constexpr int dma_lds_bytes() { return S * (BM + BN) * BK + S * dma_pslot_bytes<BM, BN, S, NPX, FUSE>(); }
+// (KR > 0: the weights stay in registers, so a stage holds A rows only)
+template <int BM, int BN, int S, int NPX, int FUSE, int BK, int KR>
+constexpr int dma_lds_bytes() {
+    return S * (BM + (KR ? 0 : BN)) * BK + S * dma_pslot_bytes<BM, BN, S, NPX, FUSE>();
+}
 // blocks per CU the kernel is compiled for: LDS and registers must fit them
 // (4-wave blocks: 3 per CU when the LDS fits them, else 2; 8-wave blocks: 2)
-template <int BM, int BN, int S, int NPX, int FUSE, int BK>
+template <int BM, int BN, int S, int NPX, int FUSE, int BK, int KR>
 constexpr int dma_min_blocks() {
-    return (BM / 64) * (BN / 64) == 8 ? 2 : (dma_lds_bytes<BM, BN, S, NPX, FUSE, BK>() * 3 <= 160 * 1024 ? 3 : 2);
+    return (BM / 64) * (BN / 64) == 8 ? 2 : (dma_lds_bytes<BM, BN, S, NPX, FUSE, BK, KR>() * 3 <= 160 * 1024 ? 3 : 2);
 }
 // threads of a block: a wave per 64 x 64 sub-tile
 template <int BM, int BN>
@@ -145,8 +148,12 @@ constexpr int dma_threads() { return (BM / 64) * (BN / 64) * 64; }
 // 128-byte stage fetches whole 128-byte rows with each DMA instruction (8
 // rows x 8 lanes instead of 16 rows x 4 lanes: twice the rate out of L2)
 // and halves the barriers per K.
-template <int BM, int BN, int S, int AMODE, int EPI, int FUSE, int BK>
-__global__ __launch_bounds__((dma_threads<BM, BN>()), (dma_min_blocks<BM, BN, S, dma_npx<EPI, FUSE>(), FUSE, BK>()))
+// KR: 0, or the packed K in 64-byte steps (1 or 2) when every tile of a block
+// lies in one column block (the launcher sizes the grid for that, batch 1):
+// each wave then loads its weight fragments once into registers and the
+// stages carry A rows only, which leaves room for another stage or block.
+template <int BM, int BN, int S, int AMODE, int EPI, int FUSE, int BK, int KR = 0>
+__global__ __launch_bounds__((dma_threads<BM, BN>()), (dma_min_blocks<BM, BN, S, dma_npx<EPI, FUSE>(), FUSE, BK, KR>()))
 void qgemm_dma_kernel(GemmArgs g) {
     constexpr int WAVES_N = BN / 64;
     constexpr int WAVES = (BM / 64) * WAVES_N;
@@ -154,14 +161,16 @@ void qgemm_dma_kernel(GemmArgs g) {
     static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves of 64x64");
     static_assert(BK == 64 || BK == 128, "stage width");
     static_assert(BK == 64 || AMODE != A_CONV4, "first layer: 64-byte stages");
+    static_assert(KR == 0 || (KR <= 2 && BK == 64), "register weights: Kp = 64 or 128, 64-byte stages");
+    constexpr int B_ROWS = KR ? 0 : BN;      // weight rows a stage carries
     constexpr int CPR = BK / 16;             // 16-byte chunks per LDS row
     constexpr int RND = NT * 16;             // bytes one DMA round of the block fills
     constexpr int RPR = RND / BK;            // rows one DMA round fills
     constexpr int A_CH = BM / RPR;           // DMA chunks per thread per step (A)
     constexpr int B_CH = BN / RPR;           // (B)
     constexpr int KK = BK / 64;              // MFMA K-steps per stage
-    constexpr int LPS = A_CH + B_CH;         // DMA instructions per thread per step
-    constexpr int STAGE = (BM + BN) * BK;    // bytes per K-step
+    constexpr int LPS = A_CH + (KR ? 0 : B_CH);   // DMA instructions per thread per step
+    constexpr int STAGE = (BM + B_ROWS) * BK;     // bytes per K-step
     constexpr int NP = EpiParams<EPI>::NP;
     constexpr int NPX = dma_npx<EPI, FUSE>();
     constexpr int PBYTES = NPX * BN * 4;
@@ -216,6 +225,22 @@ void qgemm_dma_kernel(GemmArgs g) {
 
     const int nk = g.Kp / BK;
     const uint32_t xmask = (uint32_t)g.a_xor * 0x01010101u;
+    // KR > 0: this wave's weight fragments of the block's column block, for
+    // every K step of the tile (rows past Np repeat the last packed row; their
+    // outputs are never stored)
+    v4i wreg[KR ? KR : 1][4];
+    if constexpr (KR > 0) {
+        int zb, mb0, nb0;
+        decode(t_first, zb, mb0, nb0);
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) {
+            int n = nb0 + wn * 64 + tn * 16 + frow;
+            n = n < g.Np ? n : g.Np - 1;
+#pragma unroll
+            for (int ks = 0; ks < KR; ++ks)
+                wreg[ks][tn] = *(const v4i*)(g.b + (long long)n * g.Kp + ks * 64 + fchunk * 16);
+        }
+    }
     // zero-point column term from the activation zero point (host value or,
     // after DynamicQuantizeLinear, one byte in device memory)
     int alpha = g.alpha;
@@ -362,9 +387,11 @@ void qgemm_dma_kernel(GemmArgs g) {
             }
             dma16(src, st + wave * 1024 + j * RND);
         }
+        if constexpr (KR == 0) {
 #pragma unroll
-        for (int j = 0; j < B_CH; ++j)
-            dma16((const void*)(b_addr[j] + (uint64_t)k0), st + BM * BK + wave * 1024 + j * RND);
+            for (int j = 0; j < B_CH; ++j)
+                dma16((const void*)(b_addr[j] + (uint64_t)k0), st + BM * BK + wave * 1024 + j * RND);
+        }
         if (p_kt == 0 && wave < PWAVES) {
             // per-column constants of the tile: NP arrays of BN int32/float,
             // one 16-byte chunk per lane; chunks past the arrays reload the
@@ -776,9 +803,15 @@ void qgemm_dma_kernel(GemmArgs g) {
             xf[tm] = v4i{(int)((uint32_t)v.x ^ xmask), (int)((uint32_t)v.y ^ xmask),
                          (int)((uint32_t)v.z ^ xmask), (int)((uint32_t)v.w ^ xmask)};
         }
+        if constexpr (KR > 0) {
+            // K step c_kt of the tile (64-byte stages)
 #pragma unroll
-        for (int tn = 0; tn < 4; ++tn)
-            wf[tn] = *(const v4i*)(st + BM * BK + dma_lds_off<BK>(wn * 64 + tn * 16 + frow, c));
+            for (int tn = 0; tn < 4; ++tn) wf[tn] = (KR == 1 || c_kt == 0) ? wreg[0][tn] : wreg[KR - 1][tn];
+        } else {
+#pragma unroll
+            for (int tn = 0; tn < 4; ++tn)
+                wf[tn] = *(const v4i*)(st + BM * BK + dma_lds_off<BK>(wn * 64 + tn * 16 + frow, c));
+        }
     };
     auto mma = [&](const v4i (&xf)[4], const v4i (&wf)[4], bool first) {
         if constexpr (FUSE == FUSE_ROW) {
@@ -865,9 +898,9 @@ void qgemm_dma_kernel(GemmArgs g) {
 
 namespace {
 
-template <int BM, int BN, int S, int AMODE, int EPI, int FUSE = FUSE_NONE, int BK = 64>
+template <int BM, int BN, int S, int AMODE, int EPI, int FUSE = FUSE_NONE, int BK = 64, int KR = 0>
 hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
-    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI, FUSE, BK>;
+    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI, FUSE, BK, KR>;
     const long long tiles = (long long)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN) * batch;
     // resident blocks of this instantiation (occupancy x CUs), computed once
     static int resident = 0;
@@ -883,8 +916,16 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
     }
     long long cap = resident;
     cap = cap < 8 ? 8 : (cap & ~7LL);
-    const int G = (int)(tiles < cap ? tiles : cap);
+    long long G = tiles < cap ? tiles : cap;
     if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+    if constexpr (KR > 0) {
+        // one column block per block: with 8 * nbn | G, every block's tiles
+        // t_first + j * G / 8 share t_first's column block (batch 1)
+        const long long q = 8LL * ((g.N + BN - 1) / BN);
+        if (batch != 1 || g.Kp != 64 * KR) return hipErrorInvalidValue;
+        G = (G / q) * q;
+        if (G < q) return hipErrorInvalidValue;
+    }
     GemmArgs a = g;
     a.nbatch = batch;
     {
@@ -897,7 +938,7 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
         fast_div_consts((uint32_t)(g.oH * g.oW), &a.div_sp_mul, &a.div_sp_shift);
         fast_div_consts((uint32_t)g.oW, &a.div_ow_mul, &a.div_ow_shift);
     }
-    hipLaunchKernelGGL(kern, dim3(G, 1, 1), dim3(dma_threads<BM, BN>()), 0, s, a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)G, 1, 1), dim3(dma_threads<BM, BN>()), 0, s, a);
     return hipGetLastError();
 }
 
@@ -920,8 +961,23 @@ hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
     if (g.add_other) {
         // the residual tile shares the block's LDS: 64-byte stages only
         if constexpr (BK == 64 && (AMODE == A_CONV || AMODE == A_CONVU || AMODE == A_DENSE)) {
-            if (g.epi == EPI_RQB && batch == 1)
+            if (g.epi == EPI_RQB && batch == 1) {
+                if constexpr (AMODE == A_DENSE && BM == 128 && BN == 128) {
+                    // K <= 128: weights in registers, so a slot holds A rows,
+                    // the constants and the residual tile (25 KB): 2 stages
+                    // at 3 blocks per CU (measured: ResNet-50's K = 64
+                    // layers 106 -> 96 us, K = 128 58 -> 55 us; 3 stages at
+                    // 2 blocks per CU gain half that). Only with a few tiles
+                    // for every resident block.
+                    const long long q = 8LL * ((g.N + BN - 1) / BN);
+                    const long long tiles = (long long)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+                    if (tiles >= 4 * q) {
+                        if (g.Kp == 64) return launch_dma<BM, BN, 2, AMODE, EPI_RQB, FUSE_ADD, 64, 1>(g, batch, s);
+                        if (g.Kp == 128) return launch_dma<BM, BN, 2, AMODE, EPI_RQB, FUSE_ADD, 64, 2>(g, batch, s);
+                    }
+                }
                 return launch_dma<BM, BN, S_ADD, AMODE, EPI_RQB, FUSE_ADD>(g, batch, s);
+            }
         }
         return hipErrorNotSupported;
     }

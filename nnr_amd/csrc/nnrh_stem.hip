@@ -116,17 +116,18 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
         const int c = u / (a.W / CE), w4 = u - c * (a.W / CE);
         d_off[k] = u < row_chunks ? (int)(c * HW) + w4 * CE : -1;
     }
-    // this lane's pixel of 16-pixel group i, as a dword offset in the ring
-    // from the group's first row: (r * sH) * L + ow * sW; its output pixel
-    // (r << 16 | ow)
-    int m_off[STEM_MGW], m_rw[STEM_MGW];
+    // this lane's pixel p = r * oW + ow of 16-pixel group i (output pixel
+    // oh0 * oW + p of the image), as a dword offset in the ring from the
+    // group's first row: (r * sH) * L + ow * sW
+    int m_off[STEM_MGW];
 #pragma unroll
     for (int i = 0; i < STEM_MGW; ++i) {
         const int p = (wave + 4 * i) * 16 + frow;
         const int r = p / a.oW, ow = p - (p / a.oW) * a.oW;
         m_off[i] = r * a.sH * a.L + ow * a.sW;
-        m_rw[i] = (r << 16) | ow;
     }
+    // the image's output (NHWC, OC bytes a pixel; offsets within it fit 32 bits)
+    uint8_t* const y_img = a.y + (long long)n * a.oH * a.oW * a.OC;
     // K chunk of K-step ks: kernel row (clamped into the kernel: past it the
     // weights are zero) and first tap
     int k_kh[KS], k_kw[KS];
@@ -166,7 +167,10 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
 #pragma unroll
     for (int c = CC; c < 4; ++c) fill4 |= a.fill << (8 * c);
     const uint32_t fill_all = a.fill * 0x01010101u;
-    auto quantize_rows = [&](int r0, int nr, int slot0) {
+    // (BODY: every element of the block's image takes QuantizeLinear's body
+    // expression, fixed at compile time like the epilogue's variants)
+    auto quantize_rows = [&](int r0, int nr, int slot0, auto body_t) {
+        constexpr bool BODY = decltype(body_t)::value;
         for (int r = 0; r < nr; ++r) {
             const int ih = r0 + r - a.pad_t;
             const bool row_in = (unsigned)ih < (unsigned)a.H;
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
                 if (row_in && (unsigned)iw < (unsigned)a.W) {
                     if constexpr (F32) {
                         const float* sp = (const float*)srow + iw;
-                        if (all_body) {
+                        if constexpr (BODY) {
                             w = fill4;
 #pragma unroll
                             for (int c = 0; c < CC; ++c) {
@@ -217,7 +221,11 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
     dma_rows(oh_begin * a.sH, span);
     __builtin_amdgcn_s_waitcnt(0);
     lds_barrier();
-    quantize_rows(oh_begin * a.sH, span, g_slot);
+    auto quantize = [&](int r0, int nr, int slot0) {
+        if (!F32 || all_body) quantize_rows(r0, nr, slot0, std::true_type{});
+        else quantize_rows(r0, nr, slot0, std::false_type{});
+    };
+    quantize(oh_begin * a.sH, span, g_slot);
     lds_barrier();
     for (int oh0 = oh_begin; oh0 < oh_end; oh0 += a.R) {
         // the next group's new rows: raw input into the staging area
@@ -235,48 +243,67 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
         // outputs of this wave's pixel groups, stored after the ring refill so
         // that they stay in flight across the next group's DMA and MFMAs
         uint32_t outv[STEM_MGW][4];
+        // the pixel groups with the saturating epilogue (SAT) and the 8-byte
+        // fragment reads (A8) fixed at compile time: a run-time test inside
+        // puts a branch around every element and fragment read, and then no
+        // MFMA, LDS read or epilogue instruction overlaps another
+        auto run_groups = [&](auto sat_t, auto a8_t) {
+            constexpr bool SAT = decltype(sat_t)::value;
+            constexpr bool A8 = decltype(a8_t)::value;
 #pragma unroll
-        for (int i = 0; i < STEM_MGW; ++i) {
-            const int mg = wave + 4 * i;
-            if (mg * 16 < P_here) {
-                v4i acc[4];
+            for (int i = 0; i < STEM_MGW; ++i) {
+                const int mg = wave + 4 * i;
+                if (mg * 16 < P_here) {
+                    // this lane's 16-byte chunks: kernel row kh, taps kw0..kw0+3
+                    v4i xf[KS];
 #pragma unroll
-                for (int tn = 0; tn < 4; ++tn) acc[tn] = c0v[tn];
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    // this lane's 16-byte chunk: kernel row kh, taps kw0..kw0+3
-                    const uint32_t* px = ring + ks_base[ks] + m_off[i];
-                    v4i xf;
-                    if (a.align8) {
-                        const uint2 lo = *(const uint2*)px, hi = *(const uint2*)(px + 2);
-                        xf = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
-                    } else {
-                        xf = v4i{(int)px[0], (int)px[1], (int)px[2], (int)px[3]};
-                    }
-#pragma unroll
-                    for (int tn = 0; tn < 4; ++tn)
-                        acc[tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ks][tn], xf, acc[tn], 0, 0, 0);
-                }
-                // RQ-C: rne(clamp(fma(fma(acc, cs, bf), 1/y_s, zp), qmin, qmax))
-#pragma unroll
-                for (int tn = 0; tn < 4; ++tn) {
-                    const v4i csq = csv[tn], bfq = bfv[tn];
-                    uint32_t w = 0;
-#pragma unroll
-                    for (int qq = 0; qq < 4; ++qq) {
-                        const float csf = __int_as_float(csq[qq]), bff = __int_as_float(bfq[qq]);
-                        if (a.sat) {
-                            const float t = __builtin_fmaf((float)acc[tn][qq], csf, bff);
-                            const float f = __builtin_fmaf(t, a.inv_y, (float)a.y_zp);
-                            w = __builtin_amdgcn_cvt_pk_u8_f32(f, qq, w);
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const uint32_t* px = ring + ks_base[ks] + m_off[i];
+                        if constexpr (A8) {
+                            const uint2 lo = *(const uint2*)px, hi = *(const uint2*)(px + 2);
+                            xf[ks] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
                         } else {
-                            const uint32_t b = rqc_fast(acc[tn][qq], csf, bff, a.inv_y, a.y_zp, a.qmin, a.qmax);
-                            w |= (b & 0xffu) << (8 * qq);
+                            xf[ks] = v4i{(int)px[0], (int)px[1], (int)px[2], (int)px[3]};
                         }
                     }
-                    outv[i][tn] = w;
+                    v4i acc[4];
+#pragma unroll
+                    for (int tn = 0; tn < 4; ++tn) acc[tn] = c0v[tn];
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                        for (int tn = 0; tn < 4; ++tn)
+                            acc[tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ks][tn], xf[ks], acc[tn], 0, 0, 0);
+                    // RQ-C: rne(clamp(fma(fma(acc, cs, bf), 1/y_s, zp), qmin, qmax))
+#pragma unroll
+                    for (int tn = 0; tn < 4; ++tn) {
+                        const v4i csq = csv[tn], bfq = bfv[tn];
+                        uint32_t w = 0;
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) {
+                            const float csf = __int_as_float(csq[qq]), bff = __int_as_float(bfq[qq]);
+                            if constexpr (SAT) {
+                                const float t = __builtin_fmaf((float)acc[tn][qq], csf, bff);
+                                const float f = __builtin_fmaf(t, a.inv_y, (float)a.y_zp);
+                                w = __builtin_amdgcn_cvt_pk_u8_f32(f, qq, w);
+                            } else {
+                                const uint32_t b = rqc_fast(acc[tn][qq], csf, bff, a.inv_y, a.y_zp, a.qmin, a.qmax);
+                                w |= (b & 0xffu) << (8 * qq);
+                            }
+                        }
+                        outv[i][tn] = w;
+                    }
                 }
             }
+        };
+        using T = std::true_type;
+        using Fa = std::false_type;
+        if (a.sat) {
+            if (a.align8) run_groups(T{}, T{});
+            else run_groups(T{}, Fa{});
+        } else {
+            if (a.align8) run_groups(Fa{}, T{});
+            else run_groups(Fa{}, Fa{});
         }
 
         if (more) {
@@ -286,14 +313,13 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
             lds_barrier();
             int p_slot = g_slot + span;
             p_slot -= p_slot >= a.WR ? a.WR : 0;
-            quantize_rows(pre_r0, step, p_slot);
+            quantize(pre_r0, step, p_slot);
         }
 #pragma unroll
         for (int i = 0; i < STEM_MGW; ++i) {
             const int p = (wave + 4 * i) * 16 + frow;
             if ((wave + 4 * i) * 16 < P_here && p < P_here && 16 * fch < a.OC) {
-                const int r = m_rw[i] >> 16, ow = m_rw[i] & 0xffff;
-                uint8_t* yp = a.y + (((long long)n * a.oH + oh0 + r) * a.oW + ow) * a.OC + 16 * fch;
+                uint8_t* yp = y_img + (uint32_t)((oh0 * a.oW + p) * a.OC + 16 * fch);
                 *(v4i*)yp = v4i{(int)outv[i][0], (int)outv[i][1], (int)outv[i][2], (int)outv[i][3]};
             }
         }
@@ -312,6 +338,7 @@ bool stem_eligible(const StemArgs& a, bool f32) {
     // chunks over at most STEM_DMA rounds of the 256 threads
     if (a.W % (f32 ? 4 : 16) || (long long)a.C * a.W > 256LL * STEM_DMA * (f32 ? 4 : 16)) return false;
     if ((long long)a.C * a.H * a.W >= (1LL << 26)) return false;
+    if ((long long)a.oH * a.oW * a.OC >= (1LL << 31)) return false;   // 32-bit output offsets
     // the ring holds the rows in use plus the next group's
     if (a.WR < (a.R - 1) * a.sH + a.kH + a.R * a.sH) return false;
     // LDS: the ring, and the raw rows of a group's span

@@ -253,6 +253,11 @@ FUSED_ADD_CASES = [
     # uniform-tap conv (C % 64 == 0), several K steps per tile
     ("3x3_c256_a", 2, 256, 10, 9, 192, 3, (1, 1, 1, 1), 1),
     ("persistent", 16, 64, 56, 56, 256, 1, (0, 0, 0, 0), 1),
+    # K = 64 / 128 with the weights in registers (one column block per
+    # persistent block): ragged last column block (64 of 128) and ragged
+    # rows, conv as B; four column blocks, conv as A
+    ("kr1_n192_b", 8, 64, 30, 31, 192, 1, (0, 0, 0, 0), 0),
+    ("kr2_c128_a", 6, 128, 28, 28, 512, 1, (0, 0, 0, 0), 1),
 ]
 
 
@@ -668,6 +673,10 @@ QFIRST_CASES = [
     # one-kernel stem with 1*3*21*20 = 1260 elements (12 in the divide tail),
     # stride 1 (4-byte LDS fragment reads), several row groups a strip
     ("tail_w20", 1, 3, 21, 20, 16, 3, 1, (1, 1, 1, 1), 0.0113, 17),
+    # output zero point 9 (the RQ-C clamp is not the saturating convert's),
+    # fp32 input, even stride (8-byte fragment reads); then odd stride
+    ("rn50_stem_yzp", 2, 3, 40, 36, 64, 7, 2, (3, 3, 3, 3), 0.0187, 114, 9),
+    ("stem_s1_yzp", 2, 3, 20, 24, 32, 3, 1, (1, 1, 1, 1), 0.0213, 128, 3),
 ]
 
 
@@ -677,13 +686,14 @@ def test_qconv_fused_quantize(dev, case):
     quantization inside the conv's input layout kernel == oracle Q, then
     oracle conv."""
     import torch
-    name, N, C, Hh, W, OC, k, st, pads, qs, qz = case
+    name, N, C, Hh, W, OC, k, st, pads, qs, qz = case[:11]
+    yz = case[11] if len(case) > 11 else 0
     rng = np.random.default_rng(sum(name.encode()))
     x = (rng.standard_normal((N, C, Hh, W)) * 1.3).astype(np.float32)
     # exact ties of x / s land on .5 so the rounding mode is exercised
     x.reshape(-1)[::7] = (np.arange(x.size)[::7] % 40 - 20 + 0.5).astype(np.float32) * np.float32(qs)
     w = rng.integers(-127, 128, (OC, C, k, k), dtype=np.int8)
-    kw = dict(stride=(st, st), pads=pads, y_nhwc=1, x_scale=qs, x_zp=qz, y_scale=0.05, y_zp=0,
+    kw = dict(stride=(st, st), pads=pads, y_nhwc=1, x_scale=qs, x_zp=qz, y_scale=0.05, y_zp=yz,
               w_scale=rng.uniform(0.001, 0.01, OC).astype(np.float32),
               bias=rng.integers(-4096, 4097, OC).astype(np.int32))
     xq = O.quantize_linear(x, qs, qz, np.uint8)
