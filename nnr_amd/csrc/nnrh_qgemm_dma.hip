@@ -66,6 +66,8 @@ __device__ const PadTable kPadTable{};
 
 // s_waitcnt with vmcnt = n and no wait on expcnt / lgkmcnt (gfx9 encoding)
 #define NNRH_VMCNT(n) ((((n) & 0xF)) | 0x70 | 0xF00 | ((((n) >> 4) & 3) << 14))
+// lgkmcnt(0) alone (vmcnt and expcnt at their maxima)
+#define NNRH_LGKMCNT0 0xC07F
 
 __device__ __forceinline__ void dma16(const void* src, uint8_t* lds_dst) {
     __builtin_amdgcn_global_load_lds(src, (NNRH_LDS void*)lds_dst, 16, 0, 0);
@@ -136,13 +138,25 @@ constexpr int dma_lds_bytes() {
 }
 // blocks per CU the kernel is compiled for: LDS and registers must fit them
 // (4-wave blocks: 3 per CU when the LDS fits them, else 2; 8-wave blocks: 2)
-template <int BM, int BN, int S, int NPX, int FUSE, int BK, int KR>
+template <int BM, int BN, int S, int NPX, int FUSE, int BK, int KR, int KSPLIT>
 constexpr int dma_min_blocks() {
-    return (BM / 64) * (BN / 64) == 8 ? 2 : (dma_lds_bytes<BM, BN, S, NPX, FUSE, BK, KR>() * 3 <= 160 * 1024 ? 3 : 2);
+    return (BM / 64) * (BN / 64) * KSPLIT == 8 ? 2
+                                               : (dma_lds_bytes<BM, BN, S, NPX, FUSE, BK, KR>() * 3 <= 160 * 1024 ? 3 : 2);
 }
-// threads of a block: a wave per 64 x 64 sub-tile
-template <int BM, int BN>
-constexpr int dma_threads() { return (BM / 64) * (BN / 64) * 64; }
+// threads of a block: a wave per 64 x 64 sub-tile (and per K half)
+template <int BM, int BN, int KSPLIT = 1>
+constexpr int dma_threads() { return (BM / 64) * (BN / 64) * KSPLIT * 64; }
+// __launch_bounds__'s second argument in HIP is the minimum number of waves
+// per SIMD (it sets the register budget): blocks per CU x waves per block / 4.
+// 8-wave blocks get 128 VGPRs (2 blocks per CU) where the variant fits them;
+// the general im2col producer, RQ-A and the row term do not without spills
+// and keep 256 (one block per CU)
+template <int BM, int BN, int S, int AMODE, int EPI, int FUSE, int BK, int KR, int KSPLIT>
+constexpr int dma_min_waves_per_simd() {
+    constexpr int waves = dma_threads<BM, BN, KSPLIT>() / 64;
+    if (waves == 8 && (AMODE == A_CONV || EPI == EPI_RQA || FUSE == FUSE_ROW)) return 2;
+    return dma_min_blocks<BM, BN, S, dma_npx<EPI, FUSE>(), FUSE, BK, KR, KSPLIT>() * waves / 4;
+}
 
 // BK: K bytes per pipeline stage, 64 (one MFMA K-step) or 128 (two). A
 // 128-byte stage fetches whole 128-byte rows with each DMA instruction (8
@@ -152,13 +166,21 @@ constexpr int dma_threads() { return (BM / 64) * (BN / 64) * 64; }
 // lies in one column block (the launcher sizes the grid for that, batch 1):
 // each wave then loads its weight fragments once into registers and the
 // stages carry A rows only, which leaves room for another stage or block.
-template <int BM, int BN, int S, int AMODE, int EPI, int FUSE, int BK, int KR = 0>
-__global__ __launch_bounds__((dma_threads<BM, BN>()), (dma_min_blocks<BM, BN, S, dma_npx<EPI, FUSE>(), FUSE, BK, KR>()))
+// KSPLIT 2: two waves per 64 x 64 sub-tile, one per MFMA K-step of each
+// 128-byte stage (twice the waves on a grid with few tiles); at the tile's
+// end the halves exchange half-tiles of partial sums through the stage just
+// consumed, and each half finishes two of the four 16-row blocks.
+template <int BM, int BN, int S, int AMODE, int EPI, int FUSE, int BK, int KR = 0, int KSPLIT = 1>
+__global__ __launch_bounds__((dma_threads<BM, BN, KSPLIT>()),
+                             (dma_min_waves_per_simd<BM, BN, S, AMODE, EPI, FUSE, BK, KR, KSPLIT>()))
 void qgemm_dma_kernel(GemmArgs g) {
     constexpr int WAVES_N = BN / 64;
-    constexpr int WAVES = (BM / 64) * WAVES_N;
+    constexpr int WAVES_T = (BM / 64) * WAVES_N;   // waves of a tile's 64 x 64 sub-tiles
+    constexpr int WAVES = WAVES_T * KSPLIT;
     constexpr int NT = 64 * WAVES;           // threads
     static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves of 64x64");
+    static_assert(KSPLIT == 1 || (KSPLIT == 2 && BK == 128 && WAVES_T == 4 && KR == 0 && FUSE == FUSE_NONE),
+                  "K split: 128-byte stages, 4 sub-tiles, no fusion");
     static_assert(BK == 64 || BK == 128, "stage width");
     static_assert(BK == 64 || AMODE != A_CONV4, "first layer: 64-byte stages");
     static_assert(KR == 0 || (KR <= 2 && BK == 64), "register weights: Kp = 64 or 128, 64-byte stages");
@@ -192,7 +214,10 @@ void qgemm_dma_kernel(GemmArgs g) {
     const int lane = tid & 63;
     // the wave index as a uniform value, so LDS destinations stay scalar
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    // KSPLIT 2: K half kg of sub-tile sub
+    const int kg = KSPLIT > 1 ? wave / WAVES_T : 0;
+    const int sub = wave - kg * WAVES_T;
+    const int wm = sub / WAVES_N, wn = sub % WAVES_N;
     const int frow = lane & 15, fchunk = lane >> 4;
 
     // ---- tile list: (z, m-block, n-block), n fastest; XCD-aware split
@@ -547,6 +572,7 @@ void qgemm_dma_kernel(GemmArgs g) {
         const bool full16 = nb + 16 <= g.N;
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) {
+            if (KSPLIT > 1 && (tm >> 1) != kg) continue;   // the other K half's rows
             const int m = m0 + wm * 64 + tm * 16 + frow;
             if (m >= g.M) continue;
             if constexpr (EPI == EPI_I32S) {
@@ -839,6 +865,8 @@ void qgemm_dma_kernel(GemmArgs g) {
                     c.x = (int)(neg_alpha * (uint32_t)c.x); c.y = (int)(neg_alpha * (uint32_t)c.y);
                     c.z = (int)(neg_alpha * (uint32_t)c.z); c.w = (int)(neg_alpha * (uint32_t)c.w);
                 }
+                // (the second K half starts from zero: c0 enters the sum once)
+                if (KSPLIT > 1 && kg != 0) c = v4i{0, 0, 0, 0};
                 ci[tn] = c;
             }
 #pragma unroll
@@ -858,8 +886,52 @@ void qgemm_dma_kernel(GemmArgs g) {
     // false when the block has no tile left
     auto finish_step = [&]() -> bool {
         ++c_gs;
+        const int done_stage = c_stage;
         c_stage = c_stage + STAGE == S * STAGE ? 0 : c_stage + STAGE;
         if (++c_kt == nk) {
+            if constexpr (KSPLIT > 1) {
+                // K halves -> sums, through the stage just consumed (no DMA
+                // targets it before the next step's barrier): the second half
+                // hands over its 16-row blocks 0-1 (8 KB per sub-tile), the
+                // first adds them and hands over its blocks 2-3
+                v4i* xb = (v4i*)(lds + done_stage + sub * 8192) + lane;
+                block_barrier();   // every wave's fragment reads of the stage are done
+                if (kg != 0) {
+#pragma unroll
+                    for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+                        for (int tn = 0; tn < 4; ++tn) xb[(tm * 4 + tn) * 64] = acc[tm][tn];
+                }
+                __builtin_amdgcn_s_waitcnt(NNRH_LGKMCNT0);
+                block_barrier();
+                if (kg == 0) {
+#pragma unroll
+                    for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+                        for (int tn = 0; tn < 4; ++tn) {
+                            const v4i o = xb[(tm * 4 + tn) * 64];
+                            acc[tm][tn] = v4i{(int)((uint32_t)acc[tm][tn].x + (uint32_t)o.x),
+                                              (int)((uint32_t)acc[tm][tn].y + (uint32_t)o.y),
+                                              (int)((uint32_t)acc[tm][tn].z + (uint32_t)o.z),
+                                              (int)((uint32_t)acc[tm][tn].w + (uint32_t)o.w)};
+                            xb[(tm * 4 + tn) * 64] = acc[tm + 2][tn];
+                        }
+                }
+                __builtin_amdgcn_s_waitcnt(NNRH_LGKMCNT0);
+                block_barrier();
+                if (kg != 0) {
+#pragma unroll
+                    for (int tm = 2; tm < 4; ++tm)
+#pragma unroll
+                        for (int tn = 0; tn < 4; ++tn) {
+                            const v4i o = xb[((tm - 2) * 4 + tn) * 64];
+                            acc[tm][tn] = v4i{(int)((uint32_t)acc[tm][tn].x + (uint32_t)o.x),
+                                              (int)((uint32_t)acc[tm][tn].y + (uint32_t)o.y),
+                                              (int)((uint32_t)acc[tm][tn].z + (uint32_t)o.z),
+                                              (int)((uint32_t)acc[tm][tn].w + (uint32_t)o.w)};
+                        }
+                }
+            }
             if (FUSE == FUSE_ADD && g.add_conv_is_a) epilogue(std::true_type{});
             else epilogue(std::false_type{});
             if (FUSE == FUSE_DQB && g.mm_parts) {
@@ -884,11 +956,18 @@ void qgemm_dma_kernel(GemmArgs g) {
 
     for (;;) {
         sync_step(c_gs);
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
+        if constexpr (KSPLIT > 1) {
+            // this wave's K half of the stage
             v4i xf[4], wf[4];
-            read_frags(c_stage, kk, xf, wf);
-            mma(xf, wf, kk == 0 && c_kt == 0);
+            read_frags(c_stage, kg, xf, wf);
+            mma(xf, wf, c_kt == 0);
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                v4i xf[4], wf[4];
+                read_frags(c_stage, kk, xf, wf);
+                mma(xf, wf, kk == 0 && c_kt == 0);
+            }
         }
         if (!finish_step()) break;
     }
@@ -898,15 +977,15 @@ void qgemm_dma_kernel(GemmArgs g) {
 
 namespace {
 
-template <int BM, int BN, int S, int AMODE, int EPI, int FUSE = FUSE_NONE, int BK = 64, int KR = 0>
+template <int BM, int BN, int S, int AMODE, int EPI, int FUSE = FUSE_NONE, int BK = 64, int KR = 0, int KSPLIT = 1>
 hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
-    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI, FUSE, BK, KR>;
+    auto kern = qgemm_dma_kernel<BM, BN, S, AMODE, EPI, FUSE, BK, KR, KSPLIT>;
     const long long tiles = (long long)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN) * batch;
     // resident blocks of this instantiation (occupancy x CUs), computed once
     static int resident = 0;
     if (resident <= 0) {
         int per_cu = 0, dev = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, dma_threads<BM, BN>(), 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, dma_threads<BM, BN, KSPLIT>(), 0) != hipSuccess ||
             per_cu < 1)
             per_cu = 1;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -938,7 +1017,7 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
         fast_div_consts((uint32_t)(g.oH * g.oW), &a.div_sp_mul, &a.div_sp_shift);
         fast_div_consts((uint32_t)g.oW, &a.div_ow_mul, &a.div_ow_shift);
     }
-    hipLaunchKernelGGL(kern, dim3((unsigned)G, 1, 1), dim3(dma_threads<BM, BN>()), 0, s, a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)G, 1, 1), dim3(dma_threads<BM, BN, KSPLIT>()), 0, s, a);
     return hipGetLastError();
 }
 
@@ -1006,6 +1085,20 @@ hipError_t launch_dma_plain(const GemmArgs& g, int batch, hipStream_t s) {
     case EPI_RQA: return launch_dma<BM, BN, S, AMODE, EPI_RQA>(g, batch, s);
     case EPI_RQD: return launch_dma<BM, BN, S, AMODE, EPI_RQD>(g, batch, s);
     case EPI_I32: return launch_dma<BM, BN, S, AMODE, EPI_I32>(g, batch, s);
+    default: return hipErrorNotSupported;
+    }
+}
+
+// 128 x 128 tiles with K split over two waves a sub-tile (128-byte stages,
+// 2 stages, 2 blocks of 8 waves per CU): dense and uniform-tap producers,
+// plain RQ-B / RQ-D / int32 epilogues (the variants that fit 128 VGPRs)
+template <int AMODE>
+hipError_t launch_dma_ksplit(const GemmArgs& g, int batch, hipStream_t s) {
+    static_assert(AMODE == A_DENSE || AMODE == A_CONVU, "K split producers");
+    switch (g.epi) {
+    case EPI_RQB: return launch_dma<128, 128, 2, AMODE, EPI_RQB, FUSE_NONE, 128, 0, 2>(g, batch, s);
+    case EPI_RQD: return launch_dma<128, 128, 2, AMODE, EPI_RQD, FUSE_NONE, 128, 0, 2>(g, batch, s);
+    case EPI_I32: return launch_dma<128, 128, 2, AMODE, EPI_I32, FUSE_NONE, 128, 0, 2>(g, batch, s);
     default: return hipErrorNotSupported;
     }
 }
@@ -1103,6 +1196,13 @@ hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t 
         // 3 stages at 3 blocks per CU; the fused-add variant carries a 16 KB
         // residual tile per slot and runs 2 stages at 2 blocks per CU
         if (wide) {
+            // no more 128 x 128 tiles than resident 8-wave blocks: two waves
+            // per sub-tile, each on one K half (a grid of 392 tiles fills
+            // 1.5 of the 4 SIMD wave slots it could use)
+            const long long t128 = (long long)((g.M + 127) / 128) * ((g.N + 127) / 128) * batch;
+            if (t128 <= 512 && !g.add_other && !g.dq_bias && !g.row_coef && (!conv || uni) &&
+                (g.epi == EPI_RQB || g.epi == EPI_RQD || g.epi == EPI_I32))
+                return conv ? launch_dma_ksplit<A_CONVU>(g, batch, s) : launch_dma_ksplit<A_DENSE>(g, batch, s);
             if (!conv) return launch_dma_epi<128, 128, 2, A_DENSE, 2, 128>(g, batch, s);
             return uni ? launch_dma_epi<128, 128, 2, A_CONVU, 2, 128>(g, batch, s)
                        : launch_dma_epi<128, 128, 2, A_CONV, 2, 128>(g, batch, s);

@@ -45,6 +45,9 @@ MM_CASES = [
     (64, 96, 64, 1, np.uint8, np.uint8, np.uint8, 114, np.float32),
     (7, 50, 40, 2, np.uint8, np.int8, np.uint8, 0, np.float16),
     (300, 257, 129, 1, np.int8, np.uint8, np.uint8, 7, np.float32),
+    # K % 128 == 0 and few 128 x 128 tiles: K split over two waves a sub-tile
+    (300, 200, 384, 1, np.uint8, np.int8, np.uint8, 0, np.float32),
+    (257, 130, 512, 2, np.int8, np.int8, np.int8, -3, np.float32),
 ]
 
 
@@ -82,6 +85,9 @@ def test_qmatmul_device_quant_params(dev):
     (19, 45, 27, np.int8, np.uint8, -4, 200, 1),
     (128, 200, 300, np.uint8, np.uint8, 3, 250, 3),
     (50, 33, 16, np.int8, np.int8, 0, -7, 2),
+    # int32 output with the K split (K % 128 == 0, few tiles)
+    (257, 130, 512, np.uint8, np.int8, 7, 0, 1),
+    (200, 384, 1024, np.int8, np.int8, -3, 0, 2),
 ])
 def test_matmul_integer(dev, m, n, k, adt, bdt, azp, bzp, batch):
     rng = np.random.default_rng(5 + m)
@@ -195,6 +201,11 @@ CONV_CASES = [
     ("dma_s2_3x3", 4, 128, 28, 28, 128, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1,
                                                 x_nhwc=1)),
     ("dma_grouped_c16", 1, 64, 8, 8, 64, 3, dict(group=4, pads=(1, 1, 1, 1))),
+    # few 128 x 128 tiles, K % 128 == 0: two waves a sub-tile, one per K half
+    # (uniform taps with C = 128; 1x1 dense; stride 2; ragged rows / columns)
+    ("ksplit_3x3_c128", 3, 128, 17, 19, 192, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1, y_zp=7)),
+    ("ksplit_1x1_c256", 2, 256, 14, 14, 320, 1, dict(y_nhwc=1, x_nhwc=1, post_fn=1)),
+    ("ksplit_3x3_s2", 4, 128, 28, 28, 256, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1)),
     # first layer on the padded multi-copy image: strides 2, 3 (4 copies), 4
     # (1 copy), 4 input channels
     ("first_mbv2_stem", 2, 3, 32, 32, 32, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1)),
