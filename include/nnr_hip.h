@@ -155,6 +155,20 @@ int nnrh_qconv_run_add(nnrh_qconv_t h, const void* x_dev, const void* other_dev,
  * call the handle runs with nnrh_qconv_run_f32 only.                      */
 int nnrh_qconv_fuse_quantize(nnrh_qconv_t h, float scale, int zero_point);
 int nnrh_qconv_run_f32(nnrh_qconv_t h, const float* x_dev, void* y_dev, void* stream);
+/* No counterpart in the reference: the MaxPool that reads a first-layer
+ * conv's uint8 NHWC output (3x3 window, stride 2, padding 1, no dilation,
+ * floor mode: ResNet's) runs inside the conv's one kernel, which then writes
+ * only the pooled tensor [N][pH][pW][OC], pH = (oH - 1) / 2 + 1 (pW alike).
+ * Every byte equals nnrh_maxpool_u8_nhwc over the conv's output (the uint8
+ * MaxPool of src/backend/cpu/MaxPool.cpp after fuse_qdq). Only for the
+ * one-kernel first layer (FIRST branch, NHWC uint8 output, 16..64 output
+ * channels, output rows of at most 112 pixels, 7x7-class kernels with four
+ * MFMA K steps); otherwise NNRH_ERR_UNSUPPORTED and the handle is unchanged.
+ * After a successful call nnrh_qconv_run / nnrh_qconv_run_f32 (when the
+ * quantize is fused too) write the pooled tensor; x and y must be 16-byte
+ * aligned. */
+int nnrh_qconv_fuse_maxpool(nnrh_qconv_t h, int kH, int kW, int sH, int sW, int pad_t, int pad_l,
+                            int pad_b, int pad_r);
 
 /* ---- QLinearMatMul ------------------------------------------------------
  * Replaces QLinearMatMul_operator (src/backend/cpu/QLinearMatMul.cpp:14-233)

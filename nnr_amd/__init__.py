@@ -127,6 +127,19 @@ class QLinearConv:
         check(rc)
         return True
 
+    def fuse_maxpool(self, k=(3, 3), s=(2, 2), pads=(1, 1, 1, 1)):
+        """Run the MaxPool reading this first-layer conv's uint8 NHWC output in
+        the conv's kernel; afterwards the output is the pooled tensor.
+        Returns False (handle unchanged) when the kernel cannot."""
+        rc = lib().nnrh_qconv_fuse_maxpool(self.h, int(k[0]), int(k[1]), int(s[0]), int(s[1]),
+                                           *[int(p) for p in pads])
+        if rc == NNRH_ERR_UNSUPPORTED:
+            return False
+        check(rc)
+        d = self.desc
+        self.out_shape = (d.N, (d.oH - 1) // 2 + 1, (d.oW - 1) // 2 + 1, d.OC)
+        return True
+
     def run_f32(self, x, y=None, stream=None):
         import torch
         if tuple(x.shape) != self.in_shape or not x.is_contiguous() or x.dtype != torch.float32:

@@ -26,7 +26,7 @@ EXPORTS = [
     "nnrh_profile_enable", "nnrh_profile_reset", "nnrh_profile_count", "nnrh_profile_get",
     "nnrh_qconv_dispatch", "nnrh_qconv_create", "nnrh_qconv_branch", "nnrh_qconv_run",
     "nnrh_qconv_destroy", "nnrh_qconv_fuse_add", "nnrh_qconv_run_add",
-    "nnrh_qconv_fuse_quantize", "nnrh_qconv_run_f32", "nnrh_global_avgpool_dequant",
+    "nnrh_qconv_fuse_quantize", "nnrh_qconv_run_f32", "nnrh_qconv_fuse_maxpool", "nnrh_global_avgpool_dequant",
     "nnrh_multihead_attention_workspace", "nnrh_multihead_attention_f32", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
     "nnrh_qmatmul_fuse_dq_bias", "nnrh_qmatmul_fuse_gelu", "nnrh_qmatmul_minmax_count",
     "nnrh_qmatmul_set_minmax_out", "nnrh_dynamic_quantize_linear_parts", "nnrh_add_layernorm_f32",
@@ -127,6 +127,7 @@ def lib():
         "nnrh_qconv_run_add": (i, [vp, vp, vp, vp, vp]),
         "nnrh_qconv_fuse_quantize": (i, [vp, f, i]),
         "nnrh_qconv_run_f32": (i, [vp, vp, vp, vp]),
+        "nnrh_qconv_fuse_maxpool": (i, [vp, i, i, i, i, i, i, i, i]),
         "nnrh_global_avgpool_dequant": (i, [vp, vp, i, i, i, i, i, f, i, vp]),
         "nnrh_multihead_attention_workspace": (i, [i, i, i, P(sz)]),
         "nnrh_multihead_attention_f32": (i, [vp, vp, vp, vp, i, i, i, i, f, vp, vp]),

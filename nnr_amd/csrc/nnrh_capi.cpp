@@ -352,6 +352,8 @@ struct nnrh_qconv {
     bool use_stem = false;       // first layer: the one-kernel stem for uint8 input ...
     bool use_stem_f32 = false;   // ... and for fp32 input with the quantize fused
     StemArgs stem{};             // its arguments but x, y and the quantize
+    bool pooled = false;         // nnrh_qconv_fuse_maxpool was called: y is the pooled tensor
+    StemArgs stem_pool{};        // the stem's arguments with the MaxPool fused
     int transform = 0;           // 0 none, 1 NCHW->NHWC, 2 NCHW->NHWC padded to 4 ch,
                                  // 3 first-layer padded multi-copy NHWC4 image,
                                  // 4 NHWC channels padded to a multiple of 16
@@ -736,7 +738,7 @@ int stem_scratch(nnrh_qconv_t h) {
 
 int run_stem(nnrh_qconv_t h, const void* x, void* y, bool f32, hipStream_t s) {
     const nnrh_qconv_desc& d = h->d;
-    StemArgs a = h->stem;
+    StemArgs a = h->pooled ? h->stem_pool : h->stem;
     a.x = x;
     a.y = (uint8_t*)y;
     if (f32) {
@@ -748,9 +750,16 @@ int run_stem(nnrh_qconv_t h, const void* x, void* y, bool f32, hipStream_t s) {
         a.q_zp = h->q_zp;
         a.qbody = qn >= 64 ? qn - qn % 16 : 0;
     }
-    ProfScope ps("stem_conv", s);
+    ProfScope ps(h->pooled ? "stem_conv_maxpool" : "stem_conv", s);
     HIP_TRY(launch_stem_conv(a, f32, s), "stem_conv");
     return NNRH_OK;
+}
+
+// the pooled stem has no other path: aligned buffers or an error
+int run_pooled(nnrh_qconv_t h, const void* x, void* y, bool f32, hipStream_t s) {
+    if (!stem_ok(h, x, y))
+        return set_err(NNRH_ERR_INVALID, "qconv: with the MaxPool fused, x and y must be 16-byte aligned");
+    return run_stem(h, x, y, f32, s);
 }
 }  // namespace
 
@@ -760,6 +769,7 @@ extern "C" int nnrh_qconv_run(nnrh_qconv_t h, const void* x, void* y, void* stre
     const nnrh_qconv_desc& d = h->d;
     hipStream_t s = S(stream);
     const uint8_t* src = (const uint8_t*)x;
+    if (h->pooled) return run_pooled(h, x, y, false, s);
     if (h->use_stem && stem_ok(h, x, y)) return run_stem(h, x, y, false, s);
     if (h->transform == 3) {
         if (int rc = stem_scratch(h)) return rc;
@@ -791,6 +801,8 @@ extern "C" int nnrh_qconv_fuse_quantize(nnrh_qconv_t h, float scale, int zp) {
     if (h->transform != 3 || h->d.act_dtype != NNRH_U8 || h->fused_add ||
         h->g.W + ((4 >> h->g.copy_shift) - 1) * (1 << h->g.copy_shift) > 4096)
         return set_err(NNRH_ERR_UNSUPPORTED, "qconv_fuse_quantize: only the first layer's multi-copy input");
+    if (h->pooled && !stem_eligible(h->stem_pool, true))
+        return set_err(NNRH_ERR_UNSUPPORTED, "qconv_fuse_quantize: the pooled first layer has no fp32-input kernel here");
     h->fused_quant = true;
     h->q_scale = scale;
     h->q_zp = zp;
@@ -802,6 +814,7 @@ extern "C" int nnrh_qconv_run_f32(nnrh_qconv_t h, const float* x, void* y, void*
     if (!h->fused_quant) return set_err(NNRH_ERR_INVALID, "qconv_run_f32: nnrh_qconv_fuse_quantize was not called");
     const nnrh_qconv_desc& d = h->d;
     hipStream_t s = S(stream);
+    if (h->pooled) return run_pooled(h, x, y, true, s);
     if (h->use_stem_f32 && stem_ok(h, x, y)) return run_stem(h, x, y, true, s);
     if (int rc = stem_scratch(h)) return rc;
     {
@@ -869,6 +882,33 @@ int qconv_compute(nnrh_qconv_t h, const uint8_t* src, void* y, hipStream_t s) {
     return NNRH_OK;
 }
 }  // namespace
+
+extern "C" int nnrh_qconv_fuse_maxpool(nnrh_qconv_t h, int kH, int kW, int sH, int sW, int pad_t, int pad_l,
+                                       int pad_b, int pad_r) {
+    if (!h) return set_err(NNRH_ERR_INVALID, "qconv_fuse_maxpool: NULL handle");
+    if (kH != 3 || kW != 3 || sH != 2 || sW != 2 || pad_t != 1 || pad_l != 1 || pad_b != 1 || pad_r != 1)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qconv_fuse_maxpool: only 3x3 windows, stride 2, padding 1");
+    if (h->pooled) return set_err(NNRH_ERR_INVALID, "qconv_fuse_maxpool: already fused");
+    if (h->fused_add || !(h->use_stem || h->use_stem_f32))
+        return set_err(NNRH_ERR_UNSUPPORTED, "qconv_fuse_maxpool: only the one-kernel first layer");
+    const nnrh_qconv_desc& d = h->d;
+    // groups of 4 conv rows (2 pooled rows), a ring of one group's span;
+    // strips of pooled rows: about 512 blocks over the batch
+    StemArgs a = h->stem;
+    a.pool = 1;
+    a.R = 4;
+    a.WR = (a.R - 1) * d.sH + d.kH;
+    a.pH = (d.oH - 1) / 2 + 1;
+    a.pW = (d.oW - 1) / 2 + 1;
+    const int groups = (a.pH + 1) / 2;
+    const int per_img = std::max(1, std::min(std::max(1, groups / 2), (512 + d.N - 1) / std::max(1, d.N)));
+    a.strip = 2 * ((groups + per_img - 1) / per_img);
+    if (!stem_eligible(a, h->fused_quant))
+        return set_err(NNRH_ERR_UNSUPPORTED, "qconv_fuse_maxpool: this first layer does not fit the pooled kernel");
+    h->stem_pool = a;
+    h->pooled = true;
+    return NNRH_OK;
+}
 
 extern "C" int nnrh_qconv_fuse_add(nnrh_qconv_t h, const nnrh_qadd_fuse_desc* a) {
     if (!h || !a) return set_err(NNRH_ERR_INVALID, "qconv_fuse_add: NULL argument");

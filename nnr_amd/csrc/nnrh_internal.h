@@ -192,6 +192,9 @@ struct StemArgs {
     float q_scale, q_inv;
     int q_zp;
     long long qbody;
+    // the 3x3 / stride 2 / padding 1 MaxPool after the conv fused (pool = 1):
+    // y is then [N][pH][pW][OC] and strip counts pooled rows (even)
+    int pool, pH, pW;
 };
 bool stem_eligible(const StemArgs& a, bool f32);
 hipError_t launch_stem_conv(const StemArgs& a, bool f32, hipStream_t s);

@@ -22,6 +22,17 @@
 //    stores into the NHWC uint8 output.
 // The accumulators start at c0[n] = -(x_zp - 128) * colsum[n], so
 // acc = sum (x - x_zp) w exactly, as in the GEMM kernels.
+//
+// With the MaxPool after the conv fused (POOL; 3x3, stride 2, padding 1 on
+// the uint8 NHWC conv output, MaxPool.cpp / pool_x64.h:396-436), a block
+// walks a strip of pooled rows [pa, pb): it computes conv row 2 pa - 1
+// first, then conv rows in groups of 4 from 2 pa, writes them into an LDS
+// tile of 5 conv rows (the group's 4 and the previous group's last; a zero
+// column either side) instead of HBM, and after each group writes the two
+// pooled rows it completes. The pooled
+// bytes are the max of the conv's requantized bytes, exactly as when the two
+// operators run apart; out-of-image taps are skipped (a uint8 max with the
+// zero columns changes nothing).
 #include "nnrh_internal.h"
 #include "nnrh_rq.h"
 
@@ -37,6 +48,11 @@ constexpr int STEM_MGW = 7;    // 16-pixel groups per wave per row group (x 4 wa
 constexpr int STEM_RING_DW = 10240;    // LDS ring: dwords (staged pixels, mapped twice)
 constexpr int STEM_STAGE_B = 36 * 1024; // LDS staging: raw input bytes of one row group's span
 constexpr int STEM_DMA = 2;    // 16-byte DMA chunks one thread issues per input row (x 256 threads)
+// with the MaxPool fused: a ring of exactly one group's span, staging for
+// one group's new rows, the 5-row conv tile; 81,904 bytes, two blocks per CU
+constexpr int STEM_P_RING_DW = 5980;
+constexpr int STEM_P_STAGE_B = 21504;
+constexpr int STEM_P_TILE_B = 36480;
 #define LDS_AS __attribute__((address_space(3)))
 
 __device__ __forceinline__ uint32_t stem_quant(float xv, bool body, const StemArgs& a) {
@@ -54,6 +70,16 @@ __device__ __forceinline__ uint32_t stem_quant(float xv, bool body, const StemAr
     return (uint32_t)q;
 }
 
+// running byte-wise max of 4 uint8 lanes, kept as the even bytes (lo) and
+// the odd bytes (hi) in 16-bit lanes: two packed max instructions a dword
+typedef unsigned short stem_us2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void bytemax_acc(uint32_t x, uint32_t& lo, uint32_t& hi) {
+    const stem_us2 xl = __builtin_bit_cast(stem_us2, x & 0x00ff00ffu);
+    const stem_us2 xh = __builtin_bit_cast(stem_us2, (x >> 8) & 0x00ff00ffu);
+    lo = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(stem_us2, lo), xl));
+    hi = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(stem_us2, hi), xh));
+}
+
 // every wave's LDS writes done, then a plain s_barrier: __syncthreads'
 // workgroup fence would also wait for this wave's output stores, which the
 // kernel leaves in flight (the memory clobber keeps the compiler from moving
@@ -65,20 +91,33 @@ __device__ __forceinline__ void lds_barrier() {
 
 }  // namespace
 
-// CC: input channels (3 or 4); KS: MFMA K-steps (Kp / 64)
-template <bool F32, int CC, int KS>
+// CC: input channels (3 or 4); KS: MFMA K-steps (Kp / 64); POOL: the 3x3 /
+// stride 2 / padding 1 MaxPool after the conv fused (strip = pooled rows)
+template <bool F32, int CC, int KS, bool POOL>
 __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
-    // two static arrays: the compiler then tells the ring's reads from the
-    // staging area's in-flight DMA writes and waits for neither
-    __shared__ __attribute__((aligned(16))) uint32_t ring[STEM_RING_DW];    // WR rows x L pixels
-    __shared__ __attribute__((aligned(16))) uint8_t stage[STEM_STAGE_B];    // raw rows of a span
+    // separate static arrays: the compiler then tells the ring's reads from
+    // the staging area's in-flight DMA writes and waits for neither
+    __shared__ __attribute__((aligned(16))) uint32_t ring[POOL ? STEM_P_RING_DW : STEM_RING_DW];   // WR rows x L
+    __shared__ __attribute__((aligned(16))) uint8_t stage[POOL ? STEM_P_STAGE_B : STEM_STAGE_B];   // raw rows
+    __shared__ __attribute__((aligned(16))) uint8_t tile[POOL ? STEM_P_TILE_B : 16];   // 5 conv rows
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int frow = lane & 15, fch = lane >> 4;
     const int n = blockIdx.y;
-    const int oh_begin = blockIdx.x * a.strip;
-    const int oh_end = min(a.oH, oh_begin + a.strip);
-    if (oh_begin >= oh_end) return;
+    // conv rows of the block's groups [oh_begin, oh_end); POOL: pooled rows
+    // [pa, pb), conv rows 2 pa - 1 (computed first, alone) to 2 pb - 1
+    int oh_begin, oh_end, pa = 0, pb = 0;
+    if constexpr (POOL) {
+        pa = blockIdx.x * a.strip;
+        pb = min(a.pH, pa + a.strip);
+        if (pa >= pb) return;
+        oh_begin = 2 * pa;
+        oh_end = min(a.oH, 2 * pb);
+    } else {
+        oh_begin = blockIdx.x * a.strip;
+        oh_end = min(a.oH, oh_begin + a.strip);
+        if (oh_begin >= oh_end) return;
+    }
     const long long HW = (long long)a.H * a.W;
     const long long img = (long long)n * a.C * HW;
 
@@ -120,11 +159,15 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
     // oh0 * oW + p of the image), as a dword offset in the ring from the
     // group's first row: (r * sH) * L + ow * sW
     int m_off[STEM_MGW];
+    // POOL: the pixel's LDS tile offset from its row's slot, (ow + 1) * OC +
+    // 16 fch (below 2^24), with its row in the group, r, in bits 24..
+    int m_tile[POOL ? STEM_MGW : 1];
 #pragma unroll
     for (int i = 0; i < STEM_MGW; ++i) {
         const int p = (wave + 4 * i) * 16 + frow;
         const int r = p / a.oW, ow = p - (p / a.oW) * a.oW;
         m_off[i] = r * a.sH * a.L + ow * a.sW;
+        if constexpr (POOL) m_tile[i] = ((ow + 1) * a.OC + 16 * fch) | (r << 24);
     }
     // the image's output (NHWC, OC bytes a pixel; offsets within it fit 32 bits)
     uint8_t* const y_img = a.y + (long long)n * a.oH * a.oW * a.OC;
@@ -214,23 +257,44 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
         }
     };
 
-    // ---- the strip's first rows; padded row pr sits in ring slot pr mod WR
+    // ---- the strip's first rows, from ring slot 0: a group's span (or,
+    // POOL, the kH rows of the lone conv row 2 pa - 1)
     const int span = (a.R - 1) * a.sH + a.kH;   // padded input rows of one row group
     const int step = a.R * a.sH;                // new rows per group
-    int g_slot = (oh_begin * a.sH) % a.WR;      // slot of the group's first padded row
-    dma_rows(oh_begin * a.sH, span);
-    __builtin_amdgcn_s_waitcnt(0);
-    lds_barrier();
     auto quantize = [&](int r0, int nr, int slot0) {
         if (!F32 || all_body) quantize_rows(r0, nr, slot0, std::true_type{});
         else quantize_rows(r0, nr, slot0, std::false_type{});
     };
-    quantize(oh_begin * a.sH, span, g_slot);
+    const int c_pro = oh_begin - 1;             // POOL: the lone first conv row
+    const int first_r0 = (POOL ? c_pro : oh_begin) * a.sH;
+    const int first_n = POOL ? a.kH : span;
+    int g_slot = 0;                             // ring slot of the group's first row
+    dma_rows(first_r0, first_n);
+    if constexpr (POOL) {
+        // the tile's zero columns (conv columns -1 and oW) of its 5 rows
+        const int C16 = a.OC >> 4, TW = a.oW + 2;
+        if (tid < 10 * C16) {
+            const int row = tid / (2 * C16), u = tid - row * 2 * C16;
+            const int col = u < C16 ? 0 : TW - 1;
+            *(v4i*)(tile + (row * TW + col) * a.OC + 16 * (u % C16)) = v4i{0, 0, 0, 0};
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
     lds_barrier();
-    for (int oh0 = oh_begin; oh0 < oh_end; oh0 += a.R) {
+    quantize(first_r0, first_n, g_slot);
+    lds_barrier();
+    const uint8_t* const yq_img = a.y + (long long)n * a.pH * a.pW * a.OC;   // POOL output
+    // gi = -1 (POOL): the lone conv row c_pro, whose span is kH rows and after
+    // which the ring advances sH rows; the next step rows follow it as they
+    // follow a group, so the first group's span is complete after them
+    for (int gi = POOL ? -1 : 0;; ++gi) {
+        const bool pro = POOL && gi < 0;
+        const int oh0 = pro ? c_pro : oh_begin + a.R * gi;
+        if (!pro && oh0 >= oh_end) break;
+        const int span_g = pro ? a.kH : span;
+        const bool more = pro || oh0 + a.R < oh_end;
         // the next group's new rows: raw input into the staging area
-        const bool more = oh0 + a.R < oh_end;
-        const int pre_r0 = oh0 * a.sH + span;
+        const int pre_r0 = oh0 * a.sH + span_g;
         if (more) dma_rows(pre_r0, step);
 
         // MFMAs + epilogue, 16 pixels at a time; ks_base: dword offset of
@@ -239,7 +303,7 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
         int ks_base[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) ks_base[ks] = (g_slot + k_kh[ks]) * a.L + k_kw[ks];
-        const int P_here = min(a.R, oh_end - oh0) * a.oW;
+        const int P_here = (pro ? 1 : min(a.R, oh_end - oh0)) * a.oW;
         // outputs of this wave's pixel groups, stored after the ring refill so
         // that they stay in flight across the next group's DMA and MFMAs
         uint32_t outv[STEM_MGW][4];
@@ -305,25 +369,79 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
             if (a.align8) run_groups(Fa{}, T{});
             else run_groups(Fa{}, Fa{});
         }
+        if constexpr (POOL) {
+            // conv row c goes to tile row (c - c_pro) mod 5: the group's rows
+            // take the slots after the previous group's last row, which stays
+            const int TW = a.oW + 2;
+            int base = (oh0 - c_pro) % 5;
+#pragma unroll
+            for (int i = 0; i < STEM_MGW; ++i) {
+                const int p = (wave + 4 * i) * 16 + frow;
+                if ((wave + 4 * i) * 16 < P_here && p < P_here && 16 * fch < a.OC) {
+                    int slot = base + (m_tile[i] >> 24);
+                    slot -= slot >= 5 ? 5 : 0;
+                    *(v4i*)(tile + slot * TW * a.OC + (m_tile[i] & 0xffffff)) =
+                        v4i{(int)outv[i][0], (int)outv[i][1], (int)outv[i][2], (int)outv[i][3]};
+                }
+            }
+        }
 
         if (more) {
             // every wave's DMA has landed and no wave reads this group's ring
             // slots past its span: quantize the staged rows into the ring
             __builtin_amdgcn_s_waitcnt(0);
             lds_barrier();
-            int p_slot = g_slot + span;
+            int p_slot = g_slot + span_g;
             p_slot -= p_slot >= a.WR ? a.WR : 0;
             quantize(pre_r0, step, p_slot);
+        } else if constexpr (POOL) {
+            lds_barrier();   // the tile rows are written
         }
+        if constexpr (POOL) {
+            if (!pro) {
+                // pooled rows pa + 2 gi (conv rows oh0 - 1 .. oh0 + 1) and
+                // pa + 2 gi + 1 (oh0 + 1 .. oh0 + 3), one (pixel, 16 channels)
+                // a task; conv rows outside the image are skipped
+                const int C16 = a.OC >> 4, TW = a.oW + 2;
+                const int per_row = a.pW * C16;
+                const int ph0 = pa + 2 * gi;
+                for (int t = tid; t < 2 * per_row; t += 256) {
+                    const int pr = t >= per_row ? 1 : 0;
+                    const int u = t - pr * per_row;
+                    const int pc = u / C16, ch = u - pc * C16;
+                    const int ph = ph0 + pr;
+                    if (ph >= pb) continue;
+                    uint32_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < STEM_MGW; ++i) {
-            const int p = (wave + 4 * i) * 16 + frow;
-            if ((wave + 4 * i) * 16 < P_here && p < P_here && 16 * fch < a.OC) {
-                uint8_t* yp = y_img + (uint32_t)((oh0 * a.oW + p) * a.OC + 16 * fch);
-                *(v4i*)yp = v4i{(int)outv[i][0], (int)outv[i][1], (int)outv[i][2], (int)outv[i][3]};
+                    for (int dr = 0; dr < 3; ++dr) {
+                        const int c = 2 * ph - 1 + dr;
+                        if ((unsigned)c >= (unsigned)a.oH) continue;
+                        const int slot = (c - c_pro) % 5;
+                        // tile column 2 pc holds conv column 2 pc - 1
+                        const uint8_t* tp = tile + (slot * TW + 2 * pc) * a.OC + 16 * ch;
+#pragma unroll
+                        for (int dc = 0; dc < 3; ++dc) {
+                            const v4i v = *(const v4i*)(tp + dc * a.OC);
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) bytemax_acc((uint32_t)v[q], lo[q], hi[q]);
+                        }
+                    }
+                    uint8_t* yp = (uint8_t*)yq_img + (uint32_t)((ph * a.pW + pc) * a.OC + 16 * ch);
+                    *(v4i*)yp = v4i{(int)(lo[0] | (hi[0] << 8)), (int)(lo[1] | (hi[1] << 8)),
+                                    (int)(lo[2] | (hi[2] << 8)), (int)(lo[3] | (hi[3] << 8))};
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < STEM_MGW; ++i) {
+                const int p = (wave + 4 * i) * 16 + frow;
+                if ((wave + 4 * i) * 16 < P_here && p < P_here && 16 * fch < a.OC) {
+                    uint8_t* yp = y_img + (uint32_t)((oh0 * a.oW + p) * a.OC + 16 * fch);
+                    *(v4i*)yp = v4i{(int)outv[i][0], (int)outv[i][1], (int)outv[i][2], (int)outv[i][3]};
+                }
             }
         }
-        g_slot += step;
+        g_slot += pro ? a.sH : step;
         g_slot -= g_slot >= a.WR ? a.WR : 0;
         lds_barrier();
     }
@@ -339,11 +457,25 @@ bool stem_eligible(const StemArgs& a, bool f32) {
     if (a.W % (f32 ? 4 : 16) || (long long)a.C * a.W > 256LL * STEM_DMA * (f32 ? 4 : 16)) return false;
     if ((long long)a.C * a.H * a.W >= (1LL << 26)) return false;
     if ((long long)a.oH * a.oW * a.OC >= (1LL << 31)) return false;   // 32-bit output offsets
-    // the ring holds the rows in use plus the next group's
-    if (a.WR < (a.R - 1) * a.sH + a.kH + a.R * a.sH) return false;
-    // LDS: the ring, and the raw rows of a group's span
     const long long span = (long long)(a.R - 1) * a.sH + a.kH;
-    if (2LL * a.WR * a.L > STEM_RING_DW || span * a.C * a.W * (f32 ? 4 : 1) > STEM_STAGE_B) return false;
+    const long long row_b = (long long)a.C * a.W * (f32 ? 4 : 1);   // raw bytes of one input row
+    if (a.pool) {
+        // groups of 4 conv rows (2 pooled rows); the ring holds one group's
+        // span (the next rows are quantized after the group's MFMAs), the
+        // staging area the kH rows of the lone first row or a group's new
+        // rows; the conv tile 5 rows of oW + 2 pixels
+        if (a.R != 4 || a.KS != 4 || a.WR < span) return false;
+        if (2LL * a.WR * a.L > STEM_P_RING_DW) return false;
+        if ((long long)(a.kH > a.R * a.sH ? a.kH : a.R * a.sH) * row_b > STEM_P_STAGE_B) return false;
+        if (5LL * (a.oW + 2) * a.OC > STEM_P_TILE_B) return false;
+        if (a.pH != (a.oH - 1) / 2 + 1 || a.pW != (a.oW - 1) / 2 + 1 || (a.strip & 1)) return false;
+        if ((long long)a.pH * a.pW * a.OC >= (1LL << 31)) return false;
+    } else {
+        // the ring holds the rows in use plus the next group's
+        if (a.WR < span + a.R * a.sH) return false;
+        // LDS: the ring, and the raw rows of a group's span
+        if (2LL * a.WR * a.L > STEM_RING_DW || span * row_b > STEM_STAGE_B) return false;
+    }
     if (a.L < (a.oW - 1) * a.sW + 4 * a.cpr || a.L > 4096) return false;
     if (a.align8 && ((a.sW & 1) || (a.L & 1))) return false;
     if (((uintptr_t)a.w & 15) || ((uintptr_t)a.c0 & 15) || ((uintptr_t)a.y & 15)) return false;
@@ -352,18 +484,23 @@ bool stem_eligible(const StemArgs& a, bool f32) {
 
 hipError_t launch_stem_conv(const StemArgs& a, bool f32, hipStream_t s) {
     if (!stem_eligible(a, f32)) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((a.oH + a.strip - 1) / a.strip), (unsigned)a.N);
+    const int rows = a.pool ? a.pH : a.oH;
+    const dim3 grid((unsigned)((rows + a.strip - 1) / a.strip), (unsigned)a.N);
     if (((uintptr_t)a.x & 15)) return hipErrorInvalidValue;
     const size_t lds = 0;
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, a); };
     auto by_ks = [&](auto f32c, auto ccc) {
         constexpr bool F = decltype(f32c)::value;
         constexpr int C = decltype(ccc)::value;
+        if (a.pool) {
+            go(stem_conv_kernel<F, C, 4, true>);   // (KS == 4: checked above)
+            return;
+        }
         switch (a.KS) {
-        case 1: go(stem_conv_kernel<F, C, 1>); break;
-        case 2: go(stem_conv_kernel<F, C, 2>); break;
-        case 3: go(stem_conv_kernel<F, C, 3>); break;
-        default: go(stem_conv_kernel<F, C, 4>); break;
+        case 1: go(stem_conv_kernel<F, C, 1, false>); break;
+        case 2: go(stem_conv_kernel<F, C, 2, false>); break;
+        case 3: go(stem_conv_kernel<F, C, 3, false>); break;
+        default: go(stem_conv_kernel<F, C, 4, false>); break;
         }
     };
     using T = std::true_type;

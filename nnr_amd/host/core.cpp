@@ -455,6 +455,7 @@ bool context_t::prepare() {
         fuse_matmul_dq_bias(this);
         fuse_matmul_integer_scale(this);
         fuse_quant_prefix(this);
+        fuse_conv_maxpool(this);
         fuse_add_layernorm(this);
         fuse_dynq_minmax(this);
         fuse_matmul_group(this);

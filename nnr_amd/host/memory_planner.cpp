@@ -51,7 +51,19 @@ void touched_tensors(const operator_t* op, std::vector<tensor_t*>& out) {
     add_op(op);
     if (op->fused_other) out.push_back(op->fused_other);
     if (op->fused_add) add_op(op->fused_add);
-    for (auto* o : op->fused_chain) add_op(o);
+    for (auto* o : op->fused_chain) {
+        // a chain node's first input is the previous stage's result, which
+        // exists only inside the kernel, unless it is this operator's own
+        // output (a post-op applied in place)
+        for (size_t i = 0; i < o->inputs.size(); ++i) {
+            tensor_t* t = o->inputs[i];
+            if (!t) continue;
+            if (i == 0 && std::find(op->outputs.begin(), op->outputs.end(), t) == op->outputs.end()) continue;
+            out.push_back(t);
+        }
+        for (auto* t : o->outputs)
+            if (t) out.push_back(t);
+    }
     for (auto* o : op->fused_pre) add_op(o);
     for (auto* o : op->group_members) add_op(o);
 }

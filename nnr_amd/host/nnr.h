@@ -179,6 +179,14 @@ struct operator_t {
     // (fuse_matmul_dq_bias); they are skipped and the last one's output is ours
     std::vector<operator_t*> fused_chain;
     virtual bool fuse_dq_bias(operator_t* /*dq*/, operator_t* /*add*/) { return false; }
+    // a MaxPool reading this operator's output (fuse_conv_maxpool): k, s =
+    // window and strides (h, w), pads = (top, left, bottom, right)
+    virtual bool fuse_maxpool(operator_t* /*pool*/, const int* /*k*/, const int* /*s*/, const int* /*pads*/) {
+        return false;
+    }
+    // a MaxPool's resolved window, strides and pads (false: not a plain 2-D
+    // MaxPool of this backend)
+    virtual bool pool_params(int* /*k*/, int* /*s*/, int* /*pads*/) const { return false; }
     // nodes before this one whose work its kernel now does (fuse_quant_prefix):
     // they are skipped and this operator reads the first one's input
     std::vector<operator_t*> fused_pre;
@@ -320,6 +328,7 @@ void fuse_matmul_dq_bias(context_t* ctx);
 void fuse_matmul_integer_scale(context_t* ctx);
 void fuse_quant_prefix(context_t* ctx);
 void fuse_add_layernorm(context_t* ctx);
+void fuse_conv_maxpool(context_t* ctx);
 void fuse_matmul_group(context_t* ctx);
 void fuse_dynq_minmax(context_t* ctx);
 void fuse_attention(context_t* ctx);

@@ -255,6 +255,18 @@ struct QLinearConv_hip : operator_t {
         return true;
     }
     bool fused_quant = false;   // input is the fp32 tensor of a fused QuantizeLinear
+    tensor_t* conv_out = nullptr;   // a fused MaxPool's input (the conv's own result)
+    // the MaxPool after this first-layer conv runs in its kernel
+    bool fuse_maxpool(operator_t* pool, const int* k, const int* st, const int* pads) override {
+        if (!h || fused_add || conv_out || pool->outputs.empty()) return false;
+        tensor_t *y = outputs[0], *py = pool->outputs[0];
+        if (y->type != NNR_DATA_TYPE_UINT8 || y->format != memory_layout_t::NHWC || py->format != y->format)
+            return false;
+        if (nnrh_qconv_fuse_maxpool(h, k[0], k[1], st[0], st[1], pads[0], pads[1], pads[2], pads[3]) != NNRH_OK)
+            return false;
+        conv_out = y;
+        return true;
+    }
     bool exec() override {
         if (fused_add)
             return ok(this, nnrh_qconv_run_add(h, inputs[0]->data, fused_other->data, outputs[0]->data,
@@ -294,7 +306,7 @@ struct QLinearConv_hip : operator_t {
         return nnrh_qconv_fuse_add(h, &fd) == NNRH_OK;
     }
     double num_ops() const override {
-        const tensor_t *w = inputs[3], *y = outputs[0];
+        const tensor_t *w = inputs[3], *y = conv_out ? conv_out : outputs[0];
         if (y->ndim() == 3 && w->ndim() == 3)
             return 2.0 * y->dims[0] * y->dims[1] * y->dims[2] * (double)w->dims[1] * w->dims[2];
         if (y->ndim() != 4 || w->ndim() != 4) return 0;
@@ -310,7 +322,7 @@ struct QLinearConv_hip : operator_t {
         static const char* names[] = {"?", "DW", "FIRST", "DIRECT", "PACKED", "NR16", "IM2COL_S1", "IM2COL", "FLOAT",
                                       "TYPED"};
         std::string v = branch >= 0 && branch <= 9 ? names[branch] : "?";
-        return fused_add ? v + "+Add" : v;
+        return fused_add ? v + "+Add" : conv_out ? v + "+MaxPool" : v;
     }
 };
 
@@ -1035,6 +1047,13 @@ struct MaxPool_hip : operator_t {
     std::vector<int> kernels, pads, strides;
     int auto_pad = 0;
     int cp[4] = {0, 0, 0, 0};
+    // after reshape(): the resolved window, strides and pads
+    bool pool_params(int* k, int* s, int* p) const override {
+        if (kernels.size() != 2 || strides.size() != 2) return false;
+        for (int i = 0; i < 2; ++i) { k[i] = kernels[i]; s[i] = strides[i]; }
+        for (int i = 0; i < 4; ++i) p[i] = cp[i];
+        return true;
+    }
     bool init() override {
         for (auto v : attribute_ints("kernel_shape")) kernels.push_back((int)v);
         if (kernels.size() != 2) return false;

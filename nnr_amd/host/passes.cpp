@@ -27,6 +27,9 @@
 //                     input writes its min / max pairs as it stores it
 //   fuse_matmul_group no counterpart: fused-dequantize QLinearMatMuls reading
 //                     the same input run as one launch
+//   fuse_conv_maxpool no counterpart: the uint8 MaxPool reading a first-layer
+//                     QLinearConv's output runs in the conv's kernel, which
+//                     writes only the pooled tensor (bit-identical)
 // The fused operators are created through the registry with the context's
 // preferred backend, exactly where the reference calls solve_operator.
 #include <cmath>
@@ -735,6 +738,36 @@ void fuse_matmul_group(context_t* ctx) {
 // Add(a, b) of two same-shape fp32 tensors whose only consumer is a
 // LayerNormalization (BERT's residual connections): the normalization reads
 // a and b and forms fl(a + b) itself, so the sum is never stored.
+// ---------------------------------------------------------------------------
+// Runs after every operator is built: a QLinearConv whose output feeds only a
+// MaxPool (and is not a graph output) takes the pool into its kernel when it
+// can; the MaxPool is skipped and its output becomes the conv's.
+void fuse_conv_maxpool(context_t* ctx) {
+    std::unordered_set<tensor_t*> graph_out;
+    for (auto& name : ctx->graph_outputs)
+        if (tensor_t* t = ctx->find(name)) graph_out.insert(t);
+    int fused = 0;
+    for (auto* conv : ctx->nodes) {
+        if (!active(conv) || conv->op_type != "QLinearConv" || conv->fused_add || !conv->fused_chain.empty() ||
+            conv->outputs.size() != 1)
+            continue;
+        tensor_t* t = conv->outputs[0];
+        if (!t || graph_out.count(t) || count_consumers(ctx, t, -1) != 1) continue;
+        operator_t* pool = nullptr;
+        for (auto* op : ctx->nodes)
+            if (active(op) && op != conv && op->op_type == "MaxPool" && !op->inputs.empty() && op->inputs[0] == t)
+                pool = op;
+        if (!pool || pool->outputs.size() != 1) continue;
+        int k[2], st[2], pads[4];
+        if (!pool->pool_params(k, st, pads) || !conv->fuse_maxpool(pool, k, st, pads)) continue;
+        conv->fused_chain.push_back(pool);
+        conv->outputs[0] = pool->outputs[0];
+        pool->skip = true;
+        ++fused;
+    }
+    ctx->fusion_stats["conv_maxpool"] = fused;
+}
+
 void fuse_add_layernorm(context_t* ctx) {
     std::unordered_set<tensor_t*> graph_out;
     for (auto& name : ctx->graph_outputs)

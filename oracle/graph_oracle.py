@@ -242,7 +242,9 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
             src = graph.node_by_name(nd["name"])
             a = src.attrs
             x = val(ins[0])
-            assert fmt_of(ins[0]) == 1 and x.dtype == np.uint8
+            # (inside a fused chain the input is the producer's NHWC result,
+            # under the graph's pre-fusion tensor name)
+            assert (ins[0] in chain_env or fmt_of(ins[0]) == 1) and x.dtype == np.uint8
             k, s, p = a["kernel_shape"], a.get("strides", [1, 1]), a.get("pads", [0, 0, 0, 0])
             oH = (x.shape[1] + p[0] + p[2] - k[0]) // s[0] + 1
             oW = (x.shape[2] + p[1] + p[3] - k[1]) // s[1] + 1

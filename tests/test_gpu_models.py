@@ -50,7 +50,11 @@ def test_resnet50_b2_bitexact(dev):
     # DequantizeLinear inside GlobalAveragePool
     pre = {p["op"]: p["fused_pre"] for p in plan if p["fused_pre"]}
     assert sorted(pre) == ["GlobalAveragePool", "QLinearConv"]
-    assert n_int == 53 + (16 - fused) + 1  # convs (+adds), maxpool
+    # the MaxPool after the stem runs in the stem's kernel
+    pooled = [p for p in plan if p["op"] == "QLinearConv" and p.get("fused_chain")]
+    assert len(pooled) == 1 and pooled[0]["variant"] == "FIRST+MaxPool"
+    assert "MaxPool" not in [p["op"] for p in plan]
+    assert n_int == 53 + (16 - fused)  # convs (+adds)
     assert logits.shape == (2, 1000) and np.isfinite(logits).all()
 
 

@@ -718,6 +718,66 @@ def test_qconv_fused_quantize(dev, case):
     assert mism == 0, f"{mism} of {y.size} differ"
 
 
+QPOOL_CASES = [
+    # name, N, C, H, W, OC, fp32 input (quantize fused), y_zp
+    ("rn50_small_f32", 2, 3, 40, 36, 64, True, 0),
+    # ResNet-50's stem at its real size: 14-group strips of pooled rows
+    ("rn50_224_f32", 2, 3, 224, 224, 64, True, 0),
+    # uint8 image, 4 channels, RQ-C clamp not the saturating convert's
+    ("u8_c4_zp", 3, 4, 48, 64, 32, False, 5),
+    # odd conv output height (the last pooled row's third conv row is
+    # padding), 48 channels
+    ("odd_rows_f32", 1, 3, 42, 36, 48, True, 9),
+]
+
+
+@pytest.mark.parametrize("case", QPOOL_CASES, ids=[c[0] for c in QPOOL_CASES])
+def test_qconv_fused_maxpool(dev, case):
+    """first-layer QLinearConv (7x7 / 2, pad 3) with the 3x3 / 2 / pad 1
+    MaxPool after it in the same kernel == oracle conv, then oracle MaxPool."""
+    name, N, C, Hh, W, OC, f32, yz = case
+    rng = np.random.default_rng(sum(name.encode()))
+    qs, qz = 0.0187, 114
+    w = rng.integers(-127, 128, (OC, C, 7, 7), dtype=np.int8)
+    kw = dict(stride=(2, 2), pads=(3, 3, 3, 3), y_nhwc=1, x_scale=qs, x_zp=qz, y_scale=0.05, y_zp=yz,
+              w_scale=rng.uniform(0.001, 0.01, OC).astype(np.float32),
+              bias=rng.integers(-4096, 4097, OC).astype(np.int32))
+    if f32:
+        x = (rng.standard_normal((N, C, Hh, W)) * 1.3).astype(np.float32)
+        xq = O.quantize_linear(x, qs, qz, np.uint8)
+    else:
+        xq = rng.integers(0, 256, (N, C, Hh, W), dtype=np.uint8)
+    conv, _ = O.Conv(N, C, Hh, W, OC, 7, 7, **kw).run(xq, w)
+    oH, oW = conv.shape[1], conv.shape[2]
+    pH, pW = (oH - 1) // 2 + 1, (oW - 1) // 2 + 1
+    ref = O.maxpool_u8_nhwc(conv, 3, 3, 2, 2, 1, 1, pH, pW)
+    op = H.QLinearConv(N, C, Hh, W, w, **kw)
+    assert H.BRANCH_NAMES[op.branch] == "FIRST"
+    if f32:
+        assert op.fuse_quantize(qs, qz)
+    assert op.fuse_maxpool()
+    y = to_np(op.run_f32(to_dev(x, dev)) if f32 else op(to_dev(xq, dev)))
+    assert y.shape == ref.shape
+    mism = np.count_nonzero(y != ref)
+    assert mism == 0, f"{mism} of {y.size} differ"
+
+
+def test_qconv_fuse_maxpool_unsupported(dev):
+    """other windows, and convolutions that are not the one-kernel first
+    layer, are refused with the handle unchanged"""
+    rng = np.random.default_rng(3)
+    w = rng.integers(-127, 128, (64, 3, 7, 7), dtype=np.int8)
+    kw = dict(stride=(2, 2), pads=(3, 3, 3, 3), y_nhwc=1, x_scale=0.02, x_zp=128, y_scale=0.05, y_zp=0,
+              w_scale=np.full(64, 0.004, np.float32))
+    op = H.QLinearConv(1, 3, 32, 32, w, **kw)
+    assert not op.fuse_maxpool(k=(2, 2), s=(2, 2), pads=(0, 0, 0, 0))
+    assert not op.fuse_maxpool(pads=(0, 0, 0, 0))
+    w2 = rng.integers(-127, 128, (64, 64, 1, 1), dtype=np.int8)
+    op2 = H.QLinearConv(1, 64, 16, 16, w2, x_nhwc=1, y_nhwc=1, x_scale=0.02, x_zp=128, y_scale=0.05,
+                        y_zp=0, w_scale=np.full(64, 0.004, np.float32))
+    assert not op2.fuse_maxpool()
+
+
 @pytest.mark.parametrize("nhwc,dt,C", [(1, np.uint8, 72), (0, np.uint8, 72), (1, np.int8, 72),
                                        (1, np.uint8, 70)])
 def test_global_avgpool_dequant(dev, nhwc, dt, C):
