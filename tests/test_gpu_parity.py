@@ -238,6 +238,17 @@ CONV_CASES = [
                                                act_dtype=np.int8, x_zp=-5, y_zp=-2)),
     ("dw3_s1_c960_wide", 1, 960, 5, 29, 960, 3, dict(group=960, pads=(1, 1, 1, 1), y_nhwc=1,
                                                       x_nhwc=1)),
+    # 24 channels (three 8-channel chunks), one / three 16-pixel spans a row,
+    # odd zero points, int8 at stride 2, a larger batch
+    ("dw3_s1_c24", 2, 24, 9, 11, 24, 3, dict(group=24, pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1,
+                                              x_zp=9, y_zp=4)),
+    ("dw3_s1_c144_7x7", 3, 144, 7, 7, 144, 3, dict(group=144, pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1,
+                                                    x_zp=113, y_zp=7)),
+    ("dw3_s1_c64_w40", 2, 64, 11, 40, 64, 3, dict(group=64, pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1,
+                                                   post_fn=1)),
+    ("dw3_s2_int8_c32", 2, 32, 15, 21, 32, 3, dict(group=32, stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1,
+                                                    x_nhwc=1, act_dtype=np.int8, x_zp=-7, y_zp=3)),
+    ("dw3_s1_c384_b16", 16, 384, 14, 14, 384, 3, dict(group=384, pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1)),
     # channel counts off the 16-byte grid run on an x_zp-padded copy
     ("cpad_c8_3x3", 2, 8, 10, 11, 40, 3, dict(pads=(1, 1, 1, 1), x_nhwc=1, y_nhwc=1, y_zp=9)),
     ("cpad_c24_wzp", 1, 24, 7, 9, 32, 1, dict(x_nhwc=1, y_nhwc=1, w_zp=(5,), y_zp=2)),
