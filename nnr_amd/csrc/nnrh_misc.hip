@@ -625,7 +625,6 @@ __global__ __launch_bounds__(256) void dw3x3_kernel(Dw3Args p) {
         const int n = row / p.oH;
         const int oh = row - n * p.oH;
         const int ow0 = owb * 4;
-        const uint8_t* xn = p.x + (long long)n * p.H * p.W * p.C + c0;
         int32_t acc[4][8];
 #pragma unroll
         for (int px = 0; px < 4; ++px)
@@ -635,15 +634,20 @@ __global__ __launch_bounds__(256) void dw3x3_kernel(Dw3Args p) {
         for (int a = 0; a < 3; ++a) {
             const int ih = oh * SW - p.pad_t + a;
             const bool row_ok = (unsigned)ih < (unsigned)p.H;
-            const uint8_t* xr = xn + (long long)ih * p.W * p.C;
+            // 32-bit offsets from the tensor base (N H W C < 2^31: checked by
+            // the launcher); taps outside the image load an in-image byte and
+            // take the zero point instead, with no branch around the load
+            const int rbase = ((n * p.H + (row_ok ? ih : 0)) * p.W) * p.C + c0;
             uint2 v[4 * NG];
 #pragma unroll
             for (int j = 0; j < 4 * NG; ++j) {
                 v[j] = make_uint2(0u, 0u);   // columns past NCOL meet 0 weights only
                 if (j < NCOL) {
                     const int iw = ow0 * SW - p.pad_l + j;
-                    uint2 t = make_uint2(p.pad4, p.pad4);
-                    if (row_ok && (unsigned)iw < (unsigned)p.W) t = *(const uint2*)(xr + (long long)iw * p.C);
+                    const bool ok = row_ok && (unsigned)iw < (unsigned)p.W;
+                    uint2 t = *(const uint2*)(p.x + (uint32_t)(rbase + (ok ? iw : 0) * p.C));
+                    t.x = ok ? t.x : p.pad4;
+                    t.y = ok ? t.y : p.pad4;
                     v[j] = make_uint2(t.x ^ p.xmask, t.y ^ p.xmask);
                 }
             }
@@ -703,6 +707,7 @@ hipError_t launch_depthwise3x3(const uint8_t* x, const uint32_t* wrow, const int
                                int L, int hi, hipStream_t s) {
     if (C % 8 || C > 8 * 256 || (stride != 1 && stride != 2) || N <= 0 || oH <= 0 || oW <= 0)
         return hipErrorInvalidValue;
+    if ((long long)N * H * W * C >= (1LL << 31)) return hipErrorInvalidValue;   // 32-bit input offsets
     if ((((uintptr_t)x) | ((uintptr_t)y)) & 7) return hipErrorInvalidValue;
     Dw3Args a{};
     a.x = x; a.wrow = wrow; a.corr = corr; a.cs = cs; a.bf = bf; a.y = y;
