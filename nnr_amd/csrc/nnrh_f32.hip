@@ -712,11 +712,12 @@ size_t mha_workspace_bytes(int B, int S, int nh) {
 // before P V (the order of Softmax then MatMul); padded t rows are -inf.
 constexpr int MHA_KP = 68;   // K row stride in LDS (floats): rows 16 bytes apart in the banks
 
-__global__ __launch_bounds__(256) void mha_fused_hd64_kernel(const float* __restrict q, const float* __restrict k,
+__global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __restrict q, const float* __restrict k,
                                                              const float* __restrict v, float* __restrict y,
                                                              int S, int Hd, int nh, float scale) {
+    // one buffer: K (row stride MHA_KP) for the scores, then V (stride 64)
     __shared__ __attribute__((aligned(16))) float ks[128 * MHA_KP];
-    __shared__ __attribute__((aligned(16))) float vs[128 * 64];
+    float* const vs = ks;
     const int b = blockIdx.x / nh, h = blockIdx.x - b * nh;
     const long long base = (long long)b * S * Hd + (long long)h * 64;
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -724,7 +725,6 @@ __global__ __launch_bounds__(256) void mha_fused_hd64_kernel(const float* __rest
         const int t = i >> 4, c = (i & 15) * 4;
         const long long off = base + (long long)t * Hd + c;
         *(float4*)(ks + t * MHA_KP + c) = t < S ? *(const float4*)(k + off) : zero4;
-        *(float4*)(vs + t * 64 + c) = t < S ? *(const float4*)(v + off) : zero4;
     }
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int lr = lane & 15, g = lane >> 4;
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(256) void mha_fused_hd64_kernel(const float* __rest
         }
     }
     __syncthreads();
-    if (s0 >= S) return;   // no query of this wave (after the only barrier)
+    const bool active = s0 < S;   // a wave with no query still takes every barrier
 
     f32x4 acc[8][2];
 #pragma unroll
@@ -792,6 +792,15 @@ __global__ __launch_bounds__(256) void mha_fused_hd64_kernel(const float* __rest
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[tt][ts][i] = acc[tt][ts][i] * inv;
     }
+    // every wave's scores are done with K: V takes the buffer
+    __syncthreads();
+    for (int i = threadIdx.x; i < 128 * 16; i += 256) {
+        const int t = i >> 4, c = (i & 15) * 4;
+        const long long off = base + (long long)t * Hd + c;
+        *(float4*)(vs + t * 64 + c) = t < S ? *(const float4*)(v + off) : zero4;
+    }
+    __syncthreads();
+    if (!active) return;   // (after the last barrier)
     // O[s][d] = sum_t P[s][t] V[t][d]; output tile td holds d = 4 (l % 16) + td
     f32x4 o[2][4];
 #pragma unroll
