@@ -1196,11 +1196,14 @@ hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t 
         // 3 stages at 3 blocks per CU; the fused-add variant carries a 16 KB
         // residual tile per slot and runs 2 stages at 2 blocks per CU
         if (wide) {
-            // no more 128 x 128 tiles than resident 8-wave blocks: two waves
-            // per sub-tile, each on one K half (a grid of 392 tiles fills
-            // 1.5 of the 4 SIMD wave slots it could use)
+            // two waves per sub-tile, each on one K half: on grids of no
+            // more 128 x 128 tiles than resident 8-wave blocks (a grid of
+            // 392 tiles fills 1.5 of the 4 SIMD wave slots it could use),
+            // and on every uniform-tap conv grid, whose 9 or more steps per
+            // tile amortize the partial-sum exchange (stage-2 3x3 layers 5 %
+            // faster; dense 1x1 grids of 1568 or more tiles 3-8 % slower)
             const long long t128 = (long long)((g.M + 127) / 128) * ((g.N + 127) / 128) * batch;
-            if (t128 <= 512 && !g.add_other && !g.dq_bias && !g.row_coef && (!conv || uni) &&
+            if ((t128 <= 512 || uni) && !g.add_other && !g.dq_bias && !g.row_coef && (!conv || uni) &&
                 (g.epi == EPI_RQB || g.epi == EPI_RQD || g.epi == EPI_I32))
                 return conv ? launch_dma_ksplit<A_CONVU>(g, batch, s) : launch_dma_ksplit<A_DENSE>(g, batch, s);
             if (!conv) return launch_dma_epi<128, 128, 2, A_DENSE, 2, 128>(g, batch, s);

@@ -206,6 +206,12 @@ CONV_CASES = [
     ("ksplit_3x3_c128", 3, 128, 17, 19, 192, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1, y_zp=7)),
     ("ksplit_1x1_c256", 2, 256, 14, 14, 320, 1, dict(y_nhwc=1, x_nhwc=1, post_fn=1)),
     ("ksplit_3x3_s2", 4, 128, 28, 28, 256, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1)),
+    # uniform-tap convs split K on grids larger than the resident blocks too:
+    # several tiles per persistent block (552 and 588 tiles; a ragged last
+    # column block)
+    ("ksplit_persistent_2x2", 16, 128, 24, 25, 1024, 2, dict(y_nhwc=1, x_nhwc=1, y_zp=3)),
+    ("ksplit_persistent_3x3", 48, 128, 28, 28, 192, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1,
+                                                            x_zp=77)),
     # first layer on the padded multi-copy image: strides 2, 3 (4 copies), 4
     # (1 copy), 4 input channels
     ("first_mbv2_stem", 2, 3, 32, 32, 32, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1)),
