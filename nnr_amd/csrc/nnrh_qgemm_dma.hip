@@ -1214,8 +1214,13 @@ hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t 
         return uni ? launch_dma_epi<128, 128, 3, A_CONVU, 2>(g, batch, s)
                    : launch_dma_epi<128, 128, 3, A_CONV, 2>(g, batch, s);
     case TILE_256x64:
-        if (!conv) return launch_dma_epi<256, 64, 3, A_DENSE, 2>(g, batch, s);
-        return uni ? launch_dma_epi<256, 64, 3, A_CONVU, 2>(g, batch, s)
+        // uniform-tap convs and one-step tiles: 2 stages at 3 blocks per CU
+        // (ResNet-50's stage-1 3x3 layers 17-20 % faster than 3 stages at
+        // 2 blocks); dense K >= 128: 3 stages (15 % faster there)
+        if (!conv)
+            return g.Kp <= 64 ? launch_dma_epi<256, 64, 2, A_DENSE, 2>(g, batch, s)
+                              : launch_dma_epi<256, 64, 3, A_DENSE, 2>(g, batch, s);
+        return uni ? launch_dma_epi<256, 64, 2, A_CONVU, 2>(g, batch, s)
                    : launch_dma_epi<256, 64, 3, A_CONV, 2>(g, batch, s);
     case TILE_64x256:
         if (!conv) return launch_dma_epi<64, 256, 3, A_DENSE, 2>(g, batch, s);

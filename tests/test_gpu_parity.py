@@ -212,6 +212,12 @@ CONV_CASES = [
     ("ksplit_persistent_2x2", 16, 128, 24, 25, 1024, 2, dict(y_nhwc=1, x_nhwc=1, y_zp=3)),
     ("ksplit_persistent_3x3", 48, 128, 28, 28, 192, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1,
                                                             x_zp=77)),
+    # 256 x 64 tiles with 2 stages (3 blocks per CU): a 3x3 uniform-tap conv
+    # with several tiles per persistent block (784 tiles), a one-step 1x1
+    # with a ragged column block
+    ("tall2_persistent_3x3", 64, 64, 56, 56, 64, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1,
+                                                          y_zp=6)),
+    ("tall2_1x1_k64", 16, 64, 56, 56, 48, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=5)),
     # first layer on the padded multi-copy image: strides 2, 3 (4 copies), 4
     # (1 copy), 4 input channels
     ("first_mbv2_stem", 2, 3, 32, 32, 32, 3, dict(stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1)),
