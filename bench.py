@@ -1,7 +1,13 @@
 #!/usr/bin/env python3
 """Benchmark of the int8 QDQ path on one MI355X.
 
-Prints ONE JSON line (driver contract). Workloads:
+Prints ONE JSON line (driver contract). The default, --config all, runs the
+five BASELINE.json configs in one process: the headline (value, roofline,
+cpu_baseline) is cfg3, and `configs` holds one entry per config (cfg1, cfg2,
+cfg3, cfg4, cfg5 with per-tensor weights, cfg5 with per-channel weights),
+each with its own parity gate (run before its timing), value, ms_per_step,
+roofline (with measured HBM traffic where a rocprofv3 summary exists) and
+cpu_baseline. Single workloads (BASELINE.json configs and more):
   mobilenetv2 cfg4: MobileNetV2 int8 QDQ graph, batch 256 (depthwise VALU path
             against the pointwise MFMA GEMM); value = images/s
   bert      cfg5: BERT-base int8 encoder, 12 layers, batch 64, seq 128;
@@ -104,6 +110,19 @@ def timed_reps(fn, min_s, max_reps):
     return (time.perf_counter() - t0) / reps, reps
 
 
+def cpu_seconds(args) -> float:
+    """CPU-baseline time budget of one leg: --cpu-seconds (10 s for a single
+    workload; the headline's in --config all, the other configs 4 s)."""
+    return float(args.cpu_seconds)
+
+
+def gate_images(B: int) -> list:
+    """Images of a batch the parity gate compares: the first two and the
+    last two, so tiles from the end of every persistent block's walk are
+    checked as well as the first ones."""
+    return sorted({0, min(1, B - 1), max(0, B - 2), B - 1})
+
+
 def make_qconv(rng, N=32):
     import numpy as np
     x = rng.integers(0, 256, (N, 64, 56, 56), dtype=np.uint8)
@@ -138,21 +157,30 @@ def run_qconv(args, dev):
     ms = time_steps(lambda: op(xd, yd), args)
     prof = profile_steps(lambda: op(xd, yd), args)
     g_launches, g_ms = prof["qgemm"]
-    assert g_launches == args.steps   # one kernel launch per step
-    kern_ms = ms                      # back-to-back steps: the kernel's own duration
+    assert g_launches == args.steps   # one GEMM launch per step
+    # the GEMM kernel's own duration: the whole step when it is the step's
+    # only launch, else its event-bracketed launches
+    others = sum(v[0] for k, v in prof.items() if k != "qgemm")
+    kern_ms = ms if others == 0 else g_ms / g_launches
     # cpu baseline: the CPU restatement on the whole batch
     host, nthr, vnni = cpu_setup()
     oc = O.Conv(32, 64, 56, 56, 64, 3, 3, **kw)
-    cpu_s, reps = timed_reps(lambda: oc.run(x, w), 10.0, 200)
+    cpu_s, reps = timed_reps(lambda: oc.run(x, w), cpu_seconds(args), 200)
     cpu_done()
     cpu_tops = ops / cpu_s / 1e12
     tops = ops / (ms * 1e-3) / 1e12
+    rl = roofline(ops, nbytes, kern_ms, prof)
+    rl["traffic"], rl["traffic_source"] = measured_traffic("qconv_cfg2_traffic.md")
+    rl["counters"] = measured_counters("qconv_cfg2_counters.md")
+    rl["note"] = ("achieved = the convolution's algorithmic ops and bytes / the GEMM kernel's launch time; "
+                  "value = the same ops / the whole step (%d launches)" % (1 + others // args.steps))
     return dict(
-        metric=METRIC, value=round(tops, 3), unit="TOPS", ms_per_step=ms,
+        metric="QLinearConv 3x3 int8 TOPS (cfg2), 1 GPU", value=round(tops, 3), unit="TOPS", ms_per_step=ms,
         config={"workload": "cfg2 QLinearConv 3x3 s1 p1 x u8[32,64,56,56] w i8[64,64,3,3] "
                             "per-channel scales, fused Relu, NHWC out (NR16 branch, RQ-B)",
                 "global_batch": 32, "branch": H.BRANCH_NAMES[op.branch]},
-        roofline=roofline(ops, nbytes, kern_ms, prof),
+        parity="whole output bit-exact vs the oracle before timing",
+        roofline=rl,
         cpu_baseline={"value": round(cpu_tops, 4), "unit": "TOPS", "cores": nthr, "kind": "port",
                       "sample": f"the whole batch of 32 images, mean of {reps} runs", "host": host},
         dtype="u8",
@@ -187,13 +215,20 @@ def run_qmatmul(args, dev):
     nbytes = M * K + K * N + M * N
     # cpu baseline: the CPU restatement on the whole matrix
     host, nthr, vnni = cpu_setup()
-    cpu_s, reps = timed_reps(lambda: O.qlinear_matmul(a, q[0], q[1], b, q[2], q[3], q[4], q[5]), 10.0, 500)
+    cpu_s, reps = timed_reps(lambda: O.qlinear_matmul(a, q[0], q[1], b, q[2], q[3], q[4], q[5]),
+                             cpu_seconds(args), 500)
     cpu_done()
+    rl = roofline(ops, nbytes, ms, prof)
+    rl["traffic"], rl["traffic_source"] = measured_traffic("qmatmul_cfg1_traffic.md")
+    rl["counters"] = measured_counters("qmatmul_cfg1_counters.md")
+    rl["note"] = "one launch per step: achieved = algorithmic ops and bytes / the step's time"
     return dict(
-        metric=METRIC, value=round(ops / (ms * 1e-3) / 1e12, 3), unit="TOPS", ms_per_step=ms,
+        metric="QLinearMatMul int8 TOPS (cfg1), 1 GPU", value=round(ops / (ms * 1e-3) / 1e12, 3), unit="TOPS",
+        ms_per_step=ms,
         config={"workload": "cfg1 QLinearMatMul A u8[1024,768] x B i8[768,3072] -> u8 (RQ-D)",
                 "global_batch": M},
-        roofline=roofline(ops, nbytes, ms, prof),
+        parity="whole output bit-exact vs the oracle before timing",
+        roofline=rl,
         cpu_baseline={"value": round(ops / cpu_s / 1e12, 4), "unit": "TOPS", "cores": nthr,
                       "kind": "port", "sample": f"the whole 1024 x 768 x 3072 product, {reps} runs", "host": host},
         dtype="u8",
@@ -432,16 +467,22 @@ def run_model(args, dev, model):
     torch.cuda.synchronize()
     plan = s.plan()
     fmt = lambda n: s.tensor_info(n)[3]
-    # parity gate: the oracle replays the plan on the first images of the batch
-    ng = 2
-    env = graph_oracle.run_plan(plan, g, {"input": x[:ng]}, fmt)
+    # parity gate: the oracle replays the plan on the first two and the last
+    # two images of the batch; every int8 tensor of the plan must match
+    idx = gate_images(B)
+    env = graph_oracle.run_plan(plan, g, {"input": x[idx]}, fmt)
+    n_int = 0
     for p in plan:
         o = p["outputs"][0]
         dev_t, _ = s.output(o)
         if dev_t.dtype in (np.uint8, np.int8):
-            assert np.array_equal(dev_t[:ng], env[o]), f"parity gate failed at {p['name']}"
+            assert np.array_equal(dev_t[idx], env[o]), f"parity gate failed at {p['name']}"
+            n_int += 1
         else:
-            assert np.allclose(dev_t[:ng], env[o], atol=1e-3, rtol=1e-4), p["name"]
+            assert np.allclose(dev_t[idx], env[o], atol=1e-3, rtol=1e-4), p["name"]
+        del dev_t
+    parity = (f"oracle replay of the plan on images {idx} of {B}: all {n_int} int8 tensors bit-exact, "
+              "fp32 within 1e-3")
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
     # per-kernel launch times (an event pair around every launch) and
@@ -488,7 +529,7 @@ def run_model(args, dev, model):
     # cpu baseline: the CPU restatement replays the same plan on 8 images
     host, nthr, vnni = cpu_setup()
     ns = min(8, B)
-    cpu_s, reps = timed_reps(lambda: graph_oracle.run_plan(plan, g, {"input": x[:ns]}, fmt), 10.0, 100)
+    cpu_s, reps = timed_reps(lambda: graph_oracle.run_plan(plan, g, {"input": x[:ns]}, fmt), cpu_seconds(args), 100)
     cpu_done()
     cpu_img_s = ns / cpu_s
     imgs = B / (ms * 1e-3)
@@ -502,6 +543,7 @@ def run_model(args, dev, model):
                 "conv_gemm_tops": round(sum(r["ops"] for r in rows if is_conv(r)) /
                                         (qgemm_ms_per_step * 1e-3) / 1e12, 1),
                 "memory": mem},
+        parity=parity,
         roofline=rl,
         cpu_baseline={"value": round(cpu_img_s, 3), "unit": "images/s", "cores": nthr,
                       "kind": "port", "sample": f"replay of the executed plan on {ns} of the {B} images, "
@@ -536,11 +578,11 @@ def run_bert(args, dev):
     # fused Cast / scale / bias chain) of the first layer, recomputed by the
     # oracle from the device's own inputs (dynamic scale / zero point
     # included) on the first two sequences
-    ng = 2
+    idx = gate_images(B)
 
     def dev_slice(name):
         t, _ = s.output(name)
-        return t[:ng] if t.ndim >= 1 and t.shape[0] == B else t
+        return t[idx] if t.ndim >= 1 and t.shape[0] == B else t
 
     skip = {p["op"] for p in plan} - {proj}
     env = graph_oracle.run_plan(plan, g, {}, fmt, source=dev_slice, skip_ops=skip,
@@ -556,6 +598,8 @@ def run_bert(args, dev):
                 assert np.array_equal(d, ref), f"parity gate failed at {p['name']}"
             checked += 1
     assert checked == 6
+    parity = (f"the first layer's {checked} {proj} projections recomputed by the oracle from the device's own "
+              f"inputs on sequences {idx} of {B}: bit-exact (the Gelu chain end within 2e-6)")
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
     kprof = profile_steps(s.run, args)
@@ -581,7 +625,8 @@ def run_bert(args, dev):
     g1 = synth.bert(batch=ns, seq=S, layers=L, per_channel=pc)
     plan1 = G.Session(g1, device=False).plan()
     host, nthr, vnni = cpu_setup()
-    cpu_s, reps = timed_reps(lambda: graph_oracle.run_plan(plan1, g1, {"input": x[:ns]}, lambda n: 0), 10.0, 50)
+    cpu_s, reps = timed_reps(lambda: graph_oracle.run_plan(plan1, g1, {"input": x[:ns]}, lambda n: 0),
+                             cpu_seconds(args), 50)
     cpu_done()
     cpu_seq_s = ns / cpu_s
     return dict(
@@ -594,6 +639,7 @@ def run_bert(args, dev):
                             "; fp32 attention, Softmax, LayerNorm, Gelu)",
                 "global_batch": B, "seq_len": S, "weights": "per-channel" if pc else "per-tensor",
                 "int8_tops": round(mm_ops / (mm_ms * 1e-3) / 1e12, 1), "memory": mem},
+        parity=parity,
         roofline=rl,
         cpu_baseline={"value": round(cpu_seq_s, 3), "unit": "sequences/s", "cores": nthr,
                       "kind": "port", "sample": f"replay of the plan on {ns} sequences, {reps} runs "
@@ -687,7 +733,7 @@ def run_qoperator(args, dev, graph="qoperator"):
                   "between launches)"}
     host, nthr, vnni = cpu_setup()
     ns = min(8, B)
-    cpu_s, reps = timed_reps(lambda: graph_oracle.run_plan(plan, g, {"input": x[:ns]}, fmt), 10.0, 100)
+    cpu_s, reps = timed_reps(lambda: graph_oracle.run_plan(plan, g, {"input": x[:ns]}, fmt), cpu_seconds(args), 100)
     cpu_done()
     cpu_img_s = ns / cpu_s
     if graph == "bn":
@@ -760,7 +806,7 @@ def run_convinteger(args, dev):
     rl["note"] = ("achieved = algorithmic ops of the convolution / the GEMM kernel's time; value = the same ops / "
                   "the whole operator (NHWC copy, weight packing, patch sums, GEMM)")
     host, nthr, vnni = cpu_setup()
-    cpu_s, reps = timed_reps(lambda: O.conv_integer(x, w, 117, wz, pads=(1, 1)), 10.0, 1000)
+    cpu_s, reps = timed_reps(lambda: O.conv_integer(x, w, 117, wz, pads=(1, 1)), cpu_seconds(args), 1000)
     cpu_done()
     return dict(metric="ConvInteger int8 TOPS (cfg2 shape: u8[32,64,56,56] x i8[64,64,3,3], pad 1), 1 GPU",
                 value=round(ops / (ms * 1e-3) / 1e12, 1), unit="TOPS", ms_per_step=ms,
@@ -800,14 +846,71 @@ def run_hbm_copy(args, dev):
                 cpu_baseline=None, dtype="u8")
 
 
+# the five BASELINE.json configs of --config all: key, workload runner, the
+# arguments it runs with (cfg5 in both weight forms)
+ALL_CONFIGS = (
+    ("cfg1", "qmatmul", {}),
+    ("cfg2", "qconv", {}),
+    ("cfg4", "mobilenetv2", {}),
+    ("cfg5", "bert", {"per_channel": 0}),
+    ("cfg5_per_channel", "bert", {"per_channel": 1}),
+)
+CONFIG_KEYS = ("metric", "value", "unit", "ms_per_step", "parity", "roofline", "cpu_baseline", "dtype")
+
+
+def release_device():
+    """Free what the finished leg held on the device before the next one."""
+    import gc
+
+    import torch
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def run_all(args, dev, runners):
+    """cfg3 (the headline) and then cfg1, cfg2, cfg4, cfg5 (per-tensor and
+    per-channel weights) in one process, each leg gated, timed and profiled
+    on its own; the CPU baseline of the headline takes --cpu-seconds, the
+    others --cpu-seconds-other."""
+    import copy
+    t0 = time.perf_counter()
+    print("[bench] cfg3 resnet50", file=sys.stderr, flush=True)
+    head = runners["resnet50"](args, dev)
+    configs = {"cfg3": {k: head.get(k) for k in CONFIG_KEYS}}
+    configs["cfg3"]["workload"] = head["config"]["workload"]
+    for key, name, extra in ALL_CONFIGS:
+        release_device()
+        a = copy.copy(args)
+        a.cpu_seconds = args.cpu_seconds_other
+        a.layers_out = None
+        for k, v in extra.items():
+            setattr(a, k, v)
+        print(f"[bench] {key} {name} {extra}", file=sys.stderr, flush=True)
+        t1 = time.perf_counter()
+        r = runners[name](a, dev)
+        c = {k: r.get(k) for k in CONFIG_KEYS}
+        c["workload"] = r["config"]["workload"]
+        c["leg_s"] = round(time.perf_counter() - t1, 1)
+        configs[key] = c
+    head["configs"] = configs
+    head["config"]["all_configs_wall_s"] = round(time.perf_counter() - t0, 1)
+    return head
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="resnet50",
-                    choices=["resnet50", "mobilenetv2", "bert", "qoperator", "bn", "convinteger", "qconv", "qmatmul",
-                             "hbm_copy"])
+    ap.add_argument("--config", default="all",
+                    choices=["all", "resnet50", "mobilenetv2", "bert", "qoperator", "bn", "convinteger", "qconv",
+                             "qmatmul", "hbm_copy"],
+                    help="all (default): the five BASELINE configs, cfg3 as the headline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="time budget of the CPU-baseline leg (the headline's with --config all)")
+    ap.add_argument("--cpu-seconds-other", type=float, default=4.0,
+                    help="--config all: CPU-baseline budget of the configs other than cfg3")
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--layers-out", default=None, help="write the per-layer table (JSON) here")
     ap.add_argument("--onnx", type=int, default=0, choices=[0, 1],
@@ -823,17 +926,24 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
-    run = {"resnet50": lambda a, d: run_model(a, d, "resnet50"),
-           "mobilenetv2": lambda a, d: run_model(a, d, "mobilenetv2"),
-           "bert": run_bert, "qoperator": run_qoperator, "bn": run_bn, "convinteger": run_convinteger,
-           "qconv": run_qconv, "qmatmul": run_qmatmul, "hbm_copy": run_hbm_copy}[args.config]
-    res = run(args, dev)
+    runners = {"resnet50": lambda a, d: run_model(a, d, "resnet50"),
+               "mobilenetv2": lambda a, d: run_model(a, d, "mobilenetv2"),
+               "bert": run_bert, "qoperator": run_qoperator, "bn": run_bn, "convinteger": run_convinteger,
+               "qconv": run_qconv, "qmatmul": run_qmatmul, "hbm_copy": run_hbm_copy}
+    if args.config == "all":
+        res = run_all(args, dev, runners)
+    else:
+        res = runners[args.config](args, dev)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 5),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": res["dtype"], "data": "synthetic (seeded, BASELINE.json config)",
             "config": res["config"], "roofline": res["roofline"],
             "cpu_baseline": res["cpu_baseline"]}
+    if res.get("parity"):
+        line["parity"] = res["parity"]
+    if res.get("configs"):
+        line["configs"] = res["configs"]
     print(json.dumps(line))
 
 

@@ -66,7 +66,9 @@ int nnrh_event_elapsed_ms(float* ms, void* start, void* stop);
  * Counterpart of context_t::enable_profiling / dump_profile (src/nnr.h:518-520,
  * src/nnr.cpp:801-846): when enabled, every kernel launch of this library is
  * bracketed by hipEvents on its stream and accumulated per kernel name.
- * Reading the totals synchronizes the recorded events.                    */
+ * Reading the totals synchronizes the recorded events. Entries named
+ * "variant:<kernel<template arguments>>" count the launches of each GEMM
+ * kernel instantiation (tile, stages, producer, epilogue) with no time.    */
 int nnrh_profile_enable(int on);
 int nnrh_profile_reset(void);
 int nnrh_profile_count(int* n_kernels);
@@ -322,7 +324,9 @@ int nnrh_dynamic_quantize_linear(const float* x_dev, size_t n, uint8_t* y_dev,
  * nothing. Same scale, zero point and bytes as nnrh_dynamic_quantize_linear.
  * Calls that overlap on one GPU (other streams, other threads) share that
  * array and race; serialize them. n above NNRH_DYNQ_NOALLOC_MAX_N is
- * rejected with NNRH_ERR_INVALID.                                          */
+ * rejected with NNRH_ERR_INVALID. The first call on a device looks up that
+ * device's array address (hipGetSymbolAddress): make it once, eagerly,
+ * before capturing the call into a HIP graph.                              */
 #define NNRH_DYNQ_NOALLOC_MAX_N ((size_t)1 << 40)
 int nnrh_dynamic_quantize_linear_noalloc(const float* x_dev, size_t n, uint8_t* y_dev,
                                          float* y_scale_dev, uint8_t* y_zp_dev, void* stream);

@@ -212,8 +212,10 @@ def profile_reset() -> None:
     check(lib().nnrh_profile_reset())
 
 
-def profile_read() -> dict:
-    """{kernel name: (launches, total_ms)} accumulated since the last reset."""
+def profile_read(variants: bool = False) -> dict:
+    """{kernel name: (launches, total_ms)} accumulated since the last reset.
+    With variants=True only the "variant:..." entries: launches of each
+    GEMM kernel instantiation (tile, stages, producer, epilogue), no time."""
     L = lib()
     n = C.c_int()
     check(L.nnrh_profile_count(C.byref(n)))
@@ -221,7 +223,9 @@ def profile_read() -> dict:
     for i in range(n.value):
         name, cnt, ms = C.c_char_p(), C.c_int(), C.c_double()
         check(L.nnrh_profile_get(i, C.byref(name), C.byref(cnt), C.byref(ms)))
-        out[name.value.decode()] = (cnt.value, ms.value)
+        nm = name.value.decode()
+        if nm.startswith("variant:") == variants:
+            out[nm] = (cnt.value, ms.value)
     return out
 
 

@@ -132,6 +132,19 @@ struct ProfScope {
     }
 };
 
+}  // namespace
+
+namespace nnrh {
+bool prof_enabled() { return g_prof.on; }
+// a launch counted under `name` without events: which kernel instantiation
+// ran (entries "variant:...")
+void prof_count(const char* name) {
+    if (g_prof.on) g_prof.entry(name).launches++;
+}
+}  // namespace nnrh
+
+namespace {
+
 int pick_vec(int c_or_k, int stride, uintptr_t base) {
     if (c_or_k % 16 == 0 && stride % 16 == 0 && (base & 15) == 0) return 16;
     if (c_or_k % 8 == 0 && stride % 8 == 0 && (base & 7) == 0) return 8;

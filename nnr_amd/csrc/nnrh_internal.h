@@ -158,6 +158,11 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t mul, uint32_t 
 // Tile shapes available to the launcher (BM x BN, 256 threads).
 // TILE_256x128: 8 waves (512 threads), pipelined kernel only (the register-
 // staged kernel runs it as 128x128)
+// the launch profiler (nnrh_profile_*): whether it records, and a count of
+// one launch of a kernel instantiation under `name` ("variant:...")
+bool prof_enabled();
+void prof_count(const char* name);
+
 enum TileCfg : int { TILE_128x128 = 0, TILE_256x64 = 1, TILE_64x256 = 2, TILE_256x128 = 3 };
 
 hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec,

@@ -530,6 +530,7 @@ hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec, hipStre
     const bool conv = (g.H > 0);
     if (qgemm_dma_eligible(g, vec)) return launch_qgemm_dma(g, batch, tile, s);
     if (g.add_other || g.dq_bias) return hipErrorNotSupported;   // fusions: pipelined kernel only
+    prof_count("variant:qgemm_reg");
     switch (tile) {
     case TILE_128x128:
     case TILE_256x128:

@@ -35,6 +35,8 @@
 // no scalar-tail or RQ-B' columns. Everything else takes qgemm_kernel.
 #include <type_traits>
 
+#include <cstdio>
+
 #include "nnrh_internal.h"
 #include "nnrh_rq.h"
 
@@ -1016,6 +1018,12 @@ hipError_t launch_dma(const GemmArgs& g, int batch, hipStream_t s) {
     if (g.H > 0) {
         fast_div_consts((uint32_t)(g.oH * g.oW), &a.div_sp_mul, &a.div_sp_shift);
         fast_div_consts((uint32_t)g.oW, &a.div_ow_mul, &a.div_ow_shift);
+    }
+    if (prof_enabled()) {
+        char nm[96];
+        snprintf(nm, sizeof(nm), "variant:dma<%d,%d,%d,%d,%d,%d,%d,%d,%d>", BM, BN, S, AMODE, EPI, FUSE, BK, KR,
+                 KSPLIT);
+        prof_count(nm);
     }
     hipLaunchKernelGGL(kern, dim3((unsigned)G, 1, 1), dim3(dma_threads<BM, BN, KSPLIT>()), 0, s, a);
     return hipGetLastError();

@@ -464,7 +464,9 @@ bool stem_eligible(const StemArgs& a, bool f32) {
         // span (the next rows are quantized after the group's MFMAs), the
         // staging area the kH rows of the lone first row or a group's new
         // rows; the conv tile 5 rows of oW + 2 pixels
-        if (a.R != 4 || a.KS != 4 || a.WR < span) return false;
+        // a group's R * sH new rows overwrite the slots of rows no longer
+        // read; more new rows than ring slots would overwrite each other
+        if (a.R != 4 || a.KS != 4 || a.WR < span || (long long)a.R * a.sH > a.WR) return false;
         if (2LL * a.WR * a.L > STEM_P_RING_DW) return false;
         if ((long long)(a.kH > a.R * a.sH ? a.kH : a.R * a.sH) * row_b > STEM_P_STAGE_B) return false;
         if (5LL * (a.oW + 2) * a.OC > STEM_P_TILE_B) return false;
@@ -473,8 +475,11 @@ bool stem_eligible(const StemArgs& a, bool f32) {
     } else {
         // the ring holds the rows in use plus the next group's
         if (a.WR < span + a.R * a.sH) return false;
-        // LDS: the ring, and the raw rows of a group's span
-        if (2LL * a.WR * a.L > STEM_RING_DW || span * row_b > STEM_STAGE_B) return false;
+        // LDS: the ring, and the raw rows staged at once: the first group's
+        // span, then each later group's R * sH new rows (more than a span
+        // when sH > kH)
+        const long long staged = span > (long long)a.R * a.sH ? span : (long long)a.R * a.sH;
+        if (2LL * a.WR * a.L > STEM_RING_DW || staged * row_b > STEM_STAGE_B) return false;
     }
     if (a.L < (a.oW - 1) * a.sW + 4 * a.cpr || a.L > 4096) return false;
     if (a.align8 && ((a.sW & 1) || (a.L & 1))) return false;

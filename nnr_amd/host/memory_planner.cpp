@@ -51,18 +51,27 @@ void touched_tensors(const operator_t* op, std::vector<tensor_t*>& out) {
     add_op(op);
     if (op->fused_other) out.push_back(op->fused_other);
     if (op->fused_add) add_op(op->fused_add);
-    for (auto* o : op->fused_chain) {
-        // a chain node's first input is the previous stage's result, which
-        // exists only inside the kernel, unless it is this operator's own
-        // output (a post-op applied in place)
-        for (size_t i = 0; i < o->inputs.size(); ++i) {
-            tensor_t* t = o->inputs[i];
-            if (!t) continue;
-            if (i == 0 && std::find(op->outputs.begin(), op->outputs.end(), t) == op->outputs.end()) continue;
-            out.push_back(t);
+    if (!op->fused_chain.empty()) {
+        // the values a chain passes from stage to stage exist only inside the
+        // kernel: the producer's own result (the first stage's first input)
+        // and every stage's output, unless it is this operator's output (a
+        // post-op applied in place). What else a stage reads -- a bias, the
+        // activation scale of a scale product -- the kernel reads itself.
+        auto is_out = [&](const tensor_t* t) {
+            return std::find(op->outputs.begin(), op->outputs.end(), t) != op->outputs.end();
+        };
+        std::unordered_set<const tensor_t*> inner;
+        const operator_t* first = op->fused_chain.front();
+        if (!first->inputs.empty() && first->inputs[0] && !is_out(first->inputs[0])) inner.insert(first->inputs[0]);
+        for (auto* o : op->fused_chain)
+            for (auto* t : o->outputs)
+                if (t && !is_out(t)) inner.insert(t);
+        for (auto* o : op->fused_chain) {
+            for (auto* t : o->inputs)
+                if (t && !inner.count(t)) out.push_back(t);
+            for (auto* t : o->outputs)
+                if (t && !inner.count(t)) out.push_back(t);
         }
-        for (auto* t : o->outputs)
-            if (t) out.push_back(t);
     }
     for (auto* o : op->fused_pre) add_op(o);
     for (auto* o : op->group_members) add_op(o);

@@ -1506,9 +1506,7 @@ struct MatMul_hip : operator_t {
                                             (long long)M * K, b_shared ? 0 : (long long)K * N,
                                             (long long)M * N, ctx->stream)))
             return false;
-        // a fused unary over the whole output; the reference applies it per
-        // GEMM output tile (gemm_post_t, MatMul.cpp:218-280), which for
-        // HardSwish moves which elements take the scalar-tail expression
+        // a fused Relu / Clip (position-free; a HardSwish is not fused here)
         return !(post_fn && fused_op) || fused_op->apply_post(outputs[0]->data, outputs[0]->ndata);
     }
     double num_ops() const override { return 2.0 * batch * M * (double)N * K; }

@@ -333,6 +333,14 @@ void fuse_post_ops(context_t* ctx) {
         if (!matched) continue;
         if (count_consumers(ctx, matched, -1) != 1) continue;
         if (c->inputs.size() == 2) continue;   // binary ops are never fused
+        // HardSwish's bits depend on an element's position (its 16-wide body
+        // multiplies by fl(1/6), the last n % 16 elements divide by 6). Gemm
+        // applies a fused unary over its whole output (Gemm.cpp:146-151), as
+        // the standalone operator does; MatMul applies it per GEMM output
+        // tile of its CPU blocking (gemm_post_t, MatMul.cpp:218-280), whose
+        // positions this backend does not have. So MatMul takes only the
+        // position-free Relu / Clip, and a HardSwish after it runs on its own.
+        if (t == "MatMul" && c->op_type == "HardSwish") continue;
         p->post_fn = true;
         p->fused_op = c;
         c->skip = true;

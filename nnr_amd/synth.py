@@ -318,13 +318,14 @@ MBV2_BLOCKS = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 9
                (6, 160, 3, 2), (6, 320, 1, 1))
 
 
-def hardswish_net(batch=2, hw=32, seed=29, num_classes=10):
+def hardswish_net(batch=2, hw=32, seed=29, num_classes=10, head="gemm"):
     """MobileNetV3-style QDQ graph around fp32 HardSwish. HardSwish is not
     quant-capable (fuse_qdq.cpp:96-100), so each DQ -> HardSwish -> Q between
     the QLinearConvs runs in fp32: stem 3x3/2 (3 -> 16) -> HardSwish -> 1x1
     (16 -> 20) -> HardSwish -> depthwise 3x3 (20) -> HardSwish -> fp32
     GlobalAveragePool -> Flatten -> Gemm -> HardSwish, the last one fused into
-    the Gemm as a post-op (fuse_post_ops.cpp:25-68)."""
+    the Gemm as a post-op (fuse_post_ops.cpp:25-68). head="matmul" ends in
+    MatMul -> HardSwish instead, which stays unfused."""
     g = Graph()
     rng = np.random.default_rng(seed)
     q = _QDQ(g, rng)
@@ -344,7 +345,12 @@ def hardswish_net(batch=2, hw=32, seed=29, num_classes=10):
     fl = g.node("Flatten", [p], name="flatten", axis=1)
     fw = g.init("fc_w", rng.normal(0.0, 1.0, (num_classes, 20)).astype(F32))
     fb = g.init("fc_b", rng.normal(0.0, 0.5, num_classes).astype(F32))
-    fc = g.node("Gemm", [fl, fw, fb], name="fc", transB=1)
+    if head == "gemm":
+        fc = g.node("Gemm", [fl, fw, fb], name="fc", transB=1)
+    else:
+        fwt = g.init("fc_wt", np.ascontiguousarray(g.initializers.pop("fc_w").T))
+        g.initializers.pop(fb)
+        fc = g.node("MatMul", [fl, fwt], name="fc")
     g.node("HardSwish", [fc], outputs="logits", name="fc_hswish")
     g.outputs.append("logits")
     return g

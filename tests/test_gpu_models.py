@@ -58,6 +58,58 @@ def test_resnet50_b2_bitexact(dev):
     assert logits.shape == (2, 1000) and np.isfinite(logits).all()
 
 
+# instantiations of the GEMM kernel (template arguments BM, BN, stages,
+# A producer, epilogue, fusion, K bytes per stage, register-weight K steps,
+# K split) that only the batch-256 plans take
+B256_VARIANTS = {
+    "resnet50": ("variant:dma<256,128,3,",        # 8-wave 256x128 tiles
+                 "variant:dma<256,64,2,3,",       # 2-stage 256x64 uniform-tap conv tiles
+                 ",128,0,2>",                     # K split over two waves a sub-tile
+                 ",64,1,1>"),                     # weights in registers (fused add, K = 64)
+    "mobilenetv2": ("variant:dma<256,64,",),
+}
+
+
+@pytest.mark.parametrize("model", ["resnet50", "mobilenetv2"])
+def test_model_b256_bitexact(dev, model):
+    """cfg3 / cfg4 at the config's own batch (256 at 224x224), where the
+    tile rules take instantiations batch 2 does not (8-wave 256x128 tiles,
+    2-stage 256x64 tiles, K split on persistent grids, register weights for
+    fused adds) and every persistent block walks many tiles: every int8
+    tensor of the plan on images 0, 1, 254 and 255 (tiles from the start
+    and the end of the blocks' walks) bit-exact with the oracle's replay of
+    the plan on those images; fp32 within 1e-3."""
+    from nnr_amd import _lib
+    B = 256
+    g = getattr(synth, model)(batch=B, hw=224)
+    rng = np.random.default_rng(10 if model == "resnet50" else 16)
+    x = rng.random((B, 3, 224, 224), dtype=np.float32)
+    s = G.Session(g)
+    s.set_input("input", x)
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    s.run()
+    _lib.profile_enable(False)
+    variants = _lib.profile_read(variants=True)
+    _lib.profile_reset()
+    for v in B256_VARIANTS[model]:
+        assert any(v in k for k in variants), (v, sorted(variants))
+    plan = s.plan()
+    idx = [0, 1, B - 2, B - 1]
+    env = graph_oracle.run_plan(plan, g, {"input": x[idx]}, lambda n: s.tensor_info(n)[3])
+    n_int = 0
+    for p in plan:
+        o = p["outputs"][0]
+        d = s.output(o)[0][idx]
+        if np.issubdtype(d.dtype, np.integer):
+            mism = np.count_nonzero(d != env[o])
+            assert mism == 0, f"{p['name']} ({p['op']} {p['variant']}): {mism} of {d.size} differ"
+            n_int += 1
+        else:
+            np.testing.assert_allclose(d, env[o], atol=1e-3, rtol=1e-4, err_msg=p["name"])
+    assert n_int >= (53 if model == "resnet50" else 52)
+
+
 def test_resnet50_small_input(dev):
     """Same network at 96x96 (ragged spatial sizes 48/24/12/6/3)."""
     g = synth.resnet50(batch=3, hw=96, seed=11)
@@ -153,6 +205,7 @@ def check_graph_per_node(g, feeds, atol=1e-3, rtol=1e-3, **session_kw):
 
     env = graph_oracle.run_plan(plan, g, feeds, fmt, source=dev)
     n_int = n_f32 = 0
+    exact_chains.clear()
     for p in plan:
         for o in p["outputs"]:
             if not o or o not in env:
@@ -166,7 +219,19 @@ def check_graph_per_node(g, feeds, atol=1e-3, rtol=1e-3, **session_kw):
             else:
                 np.testing.assert_allclose(d, ref, atol=atol, rtol=rtol, err_msg=f"{p['name']} {o}")
                 n_f32 += 1
+                # a projection's fused dequantize / scale / bias chain forms
+                # the same binary32 operations in the same order as the
+                # operators run apart: bit for bit (a Gelu's erf is the one
+                # expression here whose float64 oracle differs by ulps)
+                if (p["op"] in ("QLinearMatMul", "MatMulInteger") and p.get("fused_chain")
+                        and "+Gelu" not in p["variant"]):
+                    assert np.array_equal(d.view(np.uint32), np.asarray(ref, np.float32).view(np.uint32)), \
+                        f"{p['name']} ({p['variant']}) {o}: fused chain not bit-exact"
+                    exact_chains.append(p["name"])
     return plan, n_int, n_f32
+
+
+exact_chains = []   # the fused projection chains the last per-node check compared bit for bit
 
 
 @pytest.mark.parametrize("fused", [True, False])
@@ -205,6 +270,9 @@ def test_bert_per_node(dev, fused):
     assert sum(p["variant"].endswith("+Group3") for p in chains) == 2
     assert sum(p["variant"].endswith("(grouped)") for p in chains) == 4
     assert n_int >= 8 * 2 and n_f32 >= 12
+    # Q, K, V, O and FF2 of each layer: the per-tensor QLinearMatMul ->
+    # DequantizeLinear -> bias Add chains bit-exact
+    assert len(exact_chains) == 5 * 2
 
 
 def test_bert_full_depth_seq128(dev):
@@ -222,6 +290,7 @@ def test_bert_full_depth_seq128(dev):
     assert ops.count("QLinearMatMul") == 72 and ops.count("MultiHeadAttention") == 12
     assert ops.count("DynamicQuantizeLinear") == 48
     assert n_int >= 48 * 2 and n_f32 >= 72
+    assert len(exact_chains) == 5 * 12   # every fused chain without Gelu, bit for bit
 
 
 @pytest.mark.parametrize("layers,seq,fused", [(12, 128, True), (2, 64, False)])
@@ -379,20 +448,22 @@ def test_bn_f32_unfolded(dev, shape):
     assert [p["variant"] for p in plan] == [""] and out.dtype == np.float32
 
 
-@pytest.mark.parametrize("hw", [32, 29])
-def test_hardswish_graph(dev, hw):
+@pytest.mark.parametrize("hw,head", [(32, "gemm"), (29, "gemm"), (29, "matmul")])
+def test_hardswish_graph(dev, hw, head):
     """MobileNetV3-style QDQ graph: each DQ -> HardSwish -> Q between the
     QLinearConvs runs the fp32 HardSwish operator, and the classifier's
     HardSwish runs fused into the fp32 Gemm. Every int8 tensor is bit-exact
     and fp32 values are within 1e-3 of the oracle's replay; each standalone
     HardSwish output also equals the oracle's HardSwish of the device's own
-    input bit for bit (the same IEEE operations and body / tail split)."""
+    input bit for bit (the same IEEE operations and body / tail split).
+    With a MatMul classifier the HardSwish is not fused (its body / tail
+    split would follow the reference's CPU tiles): it runs on its own."""
     from oracle import pyoracle as O
-    g = synth.hardswish_net(batch=3, hw=hw)
+    g = synth.hardswish_net(batch=3, hw=hw, head=head)
     rng = np.random.default_rng(34)
     x = rng.random((3, 3, hw, hw), dtype=np.float32)
     plan, logits, n_int = check_graph(g, {"input": x}, "logits")
-    assert [p["op"] for p in plan].count("HardSwish") == 3 and n_int >= 6
+    assert [p["op"] for p in plan].count("HardSwish") == (3 if head == "gemm" else 4) and n_int >= 6
     assert logits.shape == (3, 10) and np.isfinite(logits).all()
     s = G.Session(g)
     s.set_input("input", x)

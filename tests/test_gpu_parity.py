@@ -711,7 +711,17 @@ QFIRST_CASES = [
     # fp32 input, even stride (8-byte fragment reads); then odd stride
     ("rn50_stem_yzp", 2, 3, 40, 36, 64, 7, 2, (3, 3, 3, 3), 0.0187, 114, 9),
     ("stem_s1_yzp", 2, 3, 20, 24, 32, 3, 1, (1, 1, 1, 1), 0.0213, 128, 3),
+    # stride above the kernel height: each row group stages more new rows
+    # (R * sH) than its span; the one-kernel stem takes it at width 64 ...
+    ("stem_s4_k3", 2, 3, 30, 64, 32, 3, 4, (1, 1, 1, 1), 0.0213, 128),
+    # ... and refuses it at width 640, where 5 staged fp32 rows (38,400 B)
+    # overflow the staging area although a 3-row span (23,040 B) fits: the
+    # multi-copy GEMM path runs it
+    ("stem_s5_w640", 1, 3, 12, 640, 16, 3, 5, (1, 1, 1, 1), 0.0213, 128),
 ]
+
+# the first-layer cases the one-kernel stem must take (True) or refuse
+QFIRST_STEM = {"stem_s4_k3": True, "stem_s5_w640": False, "rn50_stem_224": True}
 
 
 @pytest.mark.parametrize("case", QFIRST_CASES, ids=[c[0] for c in QFIRST_CASES])
@@ -736,9 +746,17 @@ def test_qconv_fused_quantize(dev, case):
     assert H.BRANCH_NAMES[op.branch] == "FIRST"
     assert op.fuse_quantize(qs, qz)
     xd = to_dev(x, dev)
+    from nnr_amd import _lib
+    _lib.profile_reset()
+    _lib.profile_enable(True)
     y = to_np(op.run_f32(xd))
+    _lib.profile_enable(False)
+    kernels = _lib.profile_read()
+    _lib.profile_reset()
     mism = np.count_nonzero(y != ref)
     assert mism == 0, f"{mism} of {y.size} differ"
+    if name in QFIRST_STEM:
+        assert ("stem_conv" in kernels) == QFIRST_STEM[name], sorted(kernels)
 
 
 QPOOL_CASES = [
@@ -795,6 +813,12 @@ def test_qconv_fuse_maxpool_unsupported(dev):
     op = H.QLinearConv(1, 3, 32, 32, w, **kw)
     assert not op.fuse_maxpool(k=(2, 2), s=(2, 2), pads=(0, 0, 0, 0))
     assert not op.fuse_maxpool(pads=(0, 0, 0, 0))
+    # 7x7 at stride 8: a group's 32 new rows exceed its ring of one 31-row
+    # span, so the pooled kernel refuses it (the plain stem still runs it)
+    kw8 = dict(kw, stride=(8, 8))
+    op8 = H.QLinearConv(1, 3, 64, 64, w, **kw8)
+    assert H.BRANCH_NAMES[op8.branch] == "FIRST"
+    assert not op8.fuse_maxpool()
     w2 = rng.integers(-127, 128, (64, 64, 1, 1), dtype=np.int8)
     op2 = H.QLinearConv(1, 64, 16, 16, w2, x_nhwc=1, y_nhwc=1, x_scale=0.02, x_zp=128, y_scale=0.05,
                         y_zp=0, w_scale=np.full(64, 0.004, np.float32))

@@ -114,3 +114,38 @@ def test_checker_catches_overlap():
     bad[b]["offset"] = bad[a]["offset"]
     with pytest.raises(AssertionError):
         check_plan(stats, bad)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_fused_chain_values_get_no_memory(dev, per_channel):
+    """A fused chain's stage-to-stage values (a QLinearMatMul's uint8 result
+    before its DequantizeLinear; MatMulInteger's int32 result, the Cast and
+    scale-Mul outputs before the bias) exist only inside the kernel: they
+    get no arena slot, while what a stage reads from outside the chain (the
+    activation scale the per-channel epilogue reads on the device) stays
+    live at the fused node. (The chains are formed by operators built on
+    the device.)"""
+    g = synth.bert(batch=2, seq=32, layers=2, per_channel=per_channel)
+    s = G.Session(g, memory_planning=True)
+    plan = s.plan()
+    stats, entries = s.memory_plan()
+    check_plan(stats, entries)
+    by = {e["name"]: e for e in entries}
+    inner, reads, chains = set(), [], 0
+    for i, p in enumerate(plan):
+        if not p["fused_chain"]:
+            continue
+        chains += 1
+        nodes = [g.node_by_name(c) for c in p["fused_chain"]]
+        outs = set(p["outputs"])
+        if nodes[0].inputs[0] not in outs:
+            inner.add(nodes[0].inputs[0])
+        inner |= {t for nd in nodes for t in nd.outputs if t not in outs}
+        reads += [(i, t) for nd in nodes for t in nd.inputs
+                  if t not in inner and t not in g.initializers]
+    assert chains >= 8
+    assert not inner & set(by), sorted(inner & set(by))
+    for i, t in reads:
+        if t in by:
+            assert by[t]["first"] <= i <= by[t]["last"], (t, i, by[t])

@@ -70,3 +70,43 @@ def test_dynamic_quantize_noalloc_rejects_oversize(dev):
                                                 z.data_ptr(), torch.cuda.current_stream().cuda_stream)
     assert rc == _lib.NNRH_ERR_INVALID
     assert b"maximum" in L.nnrh_last_error()
+
+
+def test_dynamic_quantize_noalloc_in_hip_graph(dev):
+    """The no-allocation entry point captured into a HIP graph after one
+    eager call on the device (which looks up this GPU's scratch address):
+    each replay, on new data copied into the captured input between
+    replays, equals the workspace entry point's eager result."""
+    import torch
+    L = _lib.lib()
+    rng = np.random.default_rng(11)
+    n = 200_003
+    x = torch.empty(n, dtype=torch.float32, device=dev)
+    y, s, z = _outs(n, dev)
+    ws = torch.empty(int(L.nnrh_dynamic_quantize_workspace()), dtype=torch.uint8, device=dev)
+    wy, wsc, wz = _outs(n, dev)
+    x.copy_(_dev(rng.normal(0, 3.0, n).astype(np.float32), dev))
+    _lib.check(L.nnrh_dynamic_quantize_linear_noalloc(x.data_ptr(), n, y.data_ptr(), s.data_ptr(), z.data_ptr(),
+                                                      torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _lib.check(L.nnrh_dynamic_quantize_linear_noalloc(x.data_ptr(), n, y.data_ptr(), s.data_ptr(),
+                                                          z.data_ptr(), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    for rep, (mu, sd) in enumerate(((-2.0, 7.0), (5.0, 0.25), (0.0, 40.0))):
+        print(f"graph replay {rep}", flush=True)
+        xh = (rng.normal(mu, sd, n)).astype(np.float32)
+        x.copy_(_dev(xh, dev))
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        _lib.check(L.nnrh_dynamic_quantize_linear(x.data_ptr(), n, wy.data_ptr(), wsc.data_ptr(), wz.data_ptr(),
+                                                  ws.data_ptr(), torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        assert s.cpu().numpy()[0] == wsc.cpu().numpy()[0]
+        assert int(z.cpu().numpy()[0]) == int(wz.cpu().numpy()[0])
+        assert np.array_equal(y.cpu().numpy(), wy.cpu().numpy())
+        y_ref, s_ref, z_ref = O.dynamic_quantize_linear(xh)
+        assert s.cpu().numpy()[0] == np.float32(s_ref) and np.array_equal(y.cpu().numpy(), y_ref)
