@@ -165,7 +165,7 @@ def run_qconv(args, dev):
     # cpu baseline: the CPU restatement on the whole batch
     host, nthr, vnni = cpu_setup()
     oc = O.Conv(32, 64, 56, 56, 64, 3, 3, **kw)
-    cpu_s, reps = timed_reps(lambda: oc.run(x, w), cpu_seconds(args), 200)
+    cpu_s, reps = timed_reps(lambda: oc.run(x, w), cpu_seconds(args), 10000)
     cpu_done()
     cpu_tops = ops / cpu_s / 1e12
     tops = ops / (ms * 1e-3) / 1e12
@@ -216,7 +216,7 @@ def run_qmatmul(args, dev):
     # cpu baseline: the CPU restatement on the whole matrix
     host, nthr, vnni = cpu_setup()
     cpu_s, reps = timed_reps(lambda: O.qlinear_matmul(a, q[0], q[1], b, q[2], q[3], q[4], q[5]),
-                             cpu_seconds(args), 500)
+                             cpu_seconds(args), 10000)
     cpu_done()
     rl = roofline(ops, nbytes, ms, prof)
     rl["traffic"], rl["traffic_source"] = measured_traffic("qmatmul_cfg1_traffic.md")
@@ -485,6 +485,7 @@ def run_model(args, dev, model):
               "fp32 within 1e-3")
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
+    mem["hip_graph"] = s.graph_active()
     # per-kernel launch times (an event pair around every launch) and
     # per-node times (each node run back to back, no event between launches)
     kprof = profile_steps(s.run, args)
@@ -602,6 +603,7 @@ def run_bert(args, dev):
               f"inputs on sequences {idx} of {B}: bit-exact (the Gelu chain end within 2e-6)")
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
+    mem["hip_graph"] = s.graph_active()
     kprof = profile_steps(s.run, args)
     rows = node_rows(s, args)
     layer_table(rows, args)
@@ -705,6 +707,7 @@ def run_qoperator(args, dev, graph="qoperator"):
             assert np.allclose(dev_t[:ng], env[o], atol=1e-3, rtol=1e-4), p["name"]
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
+    mem["hip_graph"] = s.graph_active()
     kprof = profile_steps(s.run, args)
     rows = node_rows(s, args)
     layer_table(rows, args)

@@ -62,6 +62,20 @@ int nnrh_event_destroy(void* event);
 int nnrh_event_record(void* event, void* stream);
 int nnrh_event_elapsed_ms(float* ms, void* start, void* stop);
 
+/* ---- whole-plan HIP graphs ----------------------------------------------
+ * No counterpart in the reference, whose CPU runtime executes the nodes one
+ * by one (src/nnr.cpp:908-1050). Launches issued on `stream` between
+ * begin_capture and end_capture are recorded (thread-local capture mode:
+ * a call that would allocate or synchronize fails the capture instead of
+ * running) and instantiated as one executable graph. end_capture leaves
+ * the stream out of capture either way and returns NNRH_OK with
+ * *graph_exec set, or an error with *graph_exec NULL. `stream` must not be
+ * the null stream.                                                         */
+int nnrh_graph_begin_capture(void* stream);
+int nnrh_graph_end_capture(void* stream, void** graph_exec);
+int nnrh_graph_launch(void* graph_exec, void* stream);
+int nnrh_graph_destroy(void* graph_exec);
+
 /* ---- profiling ------------------------------------------------------------
  * Counterpart of context_t::enable_profiling / dump_profile (src/nnr.h:518-520,
  * src/nnr.cpp:801-846): when enabled, every kernel launch of this library is
@@ -70,6 +84,8 @@ int nnrh_event_elapsed_ms(float* ms, void* start, void* stop);
  * "variant:<kernel<template arguments>>" count the launches of each GEMM
  * kernel instantiation (tile, stages, producer, epilogue) with no time.    */
 int nnrh_profile_enable(int on);
+/* 1 while the launch profiler records, else 0 */
+int nnrh_profile_enabled(void);
 int nnrh_profile_reset(void);
 int nnrh_profile_count(int* n_kernels);
 int nnrh_profile_get(int index, const char** name, int* launches, double* total_ms);
@@ -421,11 +437,13 @@ int nnrh_global_avgpool_f32(const float* x_dev, float* y_dev, int N, int C, int 
 /* com.microsoft MultiHeadAttention (src/backend/cpu/MultiHeadAttention.cpp,
  * no mask): q, k, v, y are [B][seq][hidden] fp32 with hidden = num_heads *
  * head_dim; y = softmax(scale * Q_h K_h^T) V_h per (batch, head), with the
- * heads read and written in place. Head size 64 with seq <= 128 runs as
- * one fused fp32-MFMA kernel per (batch, head); other shapes use batched
- * GEMMs and a scaled softmax. workspace: device memory of at least
- * nnrh_multihead_attention_workspace bytes, 256-byte aligned.              */
-int nnrh_multihead_attention_workspace(int B, int seq, int num_heads, size_t* bytes);
+ * heads read and written in place. Head size 64 with seq <= 128 (and q, k,
+ * v, y 16-byte aligned) runs as one fused fp32-MFMA kernel per (batch,
+ * head) and needs no workspace (NULL is accepted); other shapes use batched
+ * GEMMs and a scaled softmax over a workspace of at least
+ * nnrh_multihead_attention_workspace bytes, 256-byte aligned. The size is 0
+ * for the fused shapes.                                                    */
+int nnrh_multihead_attention_workspace(int B, int seq, int hidden, int num_heads, size_t* bytes);
 int nnrh_multihead_attention_f32(const float* q_dev, const float* k_dev, const float* v_dev, float* y_dev,
                                  int B, int seq, int hidden, int num_heads, float scale,
                                  void* workspace_dev, void* stream);

@@ -32,6 +32,15 @@ const char* nnr_last_error(void);
 int nnr_ctx_create(nnr_ctx_t* ctx, int preferred_backend);
 int nnr_ctx_destroy(nnr_ctx_t ctx);
 int nnr_ctx_set_stream(nnr_ctx_t ctx, void* stream);
+/* Whole-plan HIP graph (default on; no counterpart in the reference's CPU
+ * runtime): from its second call on, run() replays the plan's launches as
+ * one graph captured on a private stream and launched on the context's
+ * stream, with the same kernels and results as node-by-node launches. Off
+ * while per-node profiling or the launch profiler records; a capture that
+ * fails turns it off for the context. graph_active: 1 once a graph is in
+ * use. */
+int nnr_ctx_set_graph(nnr_ctx_t ctx, int on);
+int nnr_ctx_graph_active(nnr_ctx_t ctx, int* on);
 int nnr_ctx_set_fusion(nnr_ctx_t ctx, int on);
 /* fuse_conv_add (default on, needs fusion on): same-shape QLinearAdds run in
  * the epilogue of the QLinearConv producing one operand; results unchanged. */

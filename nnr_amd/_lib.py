@@ -24,6 +24,8 @@ EXPORTS = [
     "nnrh_stream_destroy", "nnrh_stream_synchronize", "nnrh_device_synchronize",
     "nnrh_event_create", "nnrh_event_destroy", "nnrh_event_record", "nnrh_event_elapsed_ms",
     "nnrh_profile_enable", "nnrh_profile_reset", "nnrh_profile_count", "nnrh_profile_get",
+    "nnrh_profile_enabled", "nnrh_graph_begin_capture", "nnrh_graph_end_capture", "nnrh_graph_launch",
+    "nnrh_graph_destroy",
     "nnrh_qconv_dispatch", "nnrh_qconv_create", "nnrh_qconv_branch", "nnrh_qconv_run",
     "nnrh_qconv_destroy", "nnrh_qconv_fuse_add", "nnrh_qconv_run_add",
     "nnrh_qconv_fuse_quantize", "nnrh_qconv_run_f32", "nnrh_qconv_fuse_maxpool", "nnrh_global_avgpool_dequant",
@@ -115,6 +117,11 @@ def lib():
         "nnrh_event_record": (i, [vp, vp]),
         "nnrh_event_elapsed_ms": (i, [P(f), vp, vp]),
         "nnrh_profile_enable": (i, [i]),
+        "nnrh_profile_enabled": (i, []),
+        "nnrh_graph_begin_capture": (i, [vp]),
+        "nnrh_graph_end_capture": (i, [vp, P(vp)]),
+        "nnrh_graph_launch": (i, [vp, vp]),
+        "nnrh_graph_destroy": (i, [vp]),
         "nnrh_profile_reset": (i, []),
         "nnrh_profile_count": (i, [P(i)]),
         "nnrh_profile_get": (i, [i, P(C.c_char_p), P(i), P(C.c_double)]),
@@ -129,7 +136,7 @@ def lib():
         "nnrh_qconv_run_f32": (i, [vp, vp, vp, vp]),
         "nnrh_qconv_fuse_maxpool": (i, [vp, i, i, i, i, i, i, i, i]),
         "nnrh_global_avgpool_dequant": (i, [vp, vp, i, i, i, i, i, f, i, vp]),
-        "nnrh_multihead_attention_workspace": (i, [i, i, i, P(sz)]),
+        "nnrh_multihead_attention_workspace": (i, [i, i, i, i, P(sz)]),
         "nnrh_multihead_attention_f32": (i, [vp, vp, vp, vp, i, i, i, i, f, vp, vp]),
         "nnrh_qmatmul_create": (i, [P(vp), P(QMatMulDesc)]),
         "nnrh_qmatmul_run": (i, [vp, vp, ll, vp, i, vp, vp, vp]),

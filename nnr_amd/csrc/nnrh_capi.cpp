@@ -245,6 +245,39 @@ extern "C" int nnrh_profile_enable(int on) {
     g_prof.on = on != 0;
     return NNRH_OK;
 }
+extern "C" int nnrh_profile_enabled(void) { return g_prof.on ? 1 : 0; }
+
+extern "C" int nnrh_graph_begin_capture(void* stream) {
+    if (!stream) return set_err(NNRH_ERR_INVALID, "graph_begin_capture: the null stream cannot be captured");
+    HIP_TRY(hipStreamBeginCapture(S(stream), hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    return NNRH_OK;
+}
+extern "C" int nnrh_graph_end_capture(void* stream, void** graph_exec) {
+    if (!stream || !graph_exec) return set_err(NNRH_ERR_INVALID, "graph_end_capture: NULL argument");
+    *graph_exec = nullptr;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(S(stream), &graph);
+    if (e != hipSuccess || !graph) {
+        if (graph) (void)hipGraphDestroy(graph);
+        (void)hipGetLastError();   // a failed capture's error is not sticky here
+        return hip_err(e != hipSuccess ? e : hipErrorStreamCaptureInvalidated, "hipStreamEndCapture");
+    }
+    hipGraphExec_t ex = nullptr;
+    e = hipGraphInstantiate(&ex, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_err(e, "hipGraphInstantiate");
+    *graph_exec = (void*)ex;
+    return NNRH_OK;
+}
+extern "C" int nnrh_graph_launch(void* graph_exec, void* stream) {
+    if (!graph_exec) return set_err(NNRH_ERR_INVALID, "graph_launch: NULL graph");
+    HIP_TRY(hipGraphLaunch((hipGraphExec_t)graph_exec, S(stream)), "hipGraphLaunch");
+    return NNRH_OK;
+}
+extern "C" int nnrh_graph_destroy(void* graph_exec) {
+    if (graph_exec) HIP_TRY(hipGraphExecDestroy((hipGraphExec_t)graph_exec), "hipGraphExecDestroy");
+    return NNRH_OK;
+}
 extern "C" int nnrh_profile_reset(void) {
     g_prof.flush();
     g_prof.entries.clear();
@@ -1916,17 +1949,21 @@ extern "C" int nnrh_global_avgpool_f32(const float* x, float* y, int N, int C, i
     return NNRH_OK;
 }
 
-extern "C" int nnrh_multihead_attention_workspace(int B, int seq, int num_heads, size_t* bytes) {
-    if (!bytes || B < 0 || seq < 0 || num_heads <= 0) return set_err(NNRH_ERR_INVALID, "mha_workspace: arguments");
-    *bytes = mha_workspace_bytes(B, seq, num_heads);
+extern "C" int nnrh_multihead_attention_workspace(int B, int seq, int hidden, int num_heads, size_t* bytes) {
+    if (!bytes || B < 0 || seq < 0 || num_heads <= 0 || hidden <= 0 || hidden % num_heads)
+        return set_err(NNRH_ERR_INVALID, "mha_workspace: arguments");
+    // the fused head-64 kernel keeps everything in LDS and registers
+    *bytes = mha_fused_shape(seq, hidden, num_heads) ? 0 : mha_workspace_bytes(B, seq, num_heads);
     return NNRH_OK;
 }
 
 extern "C" int nnrh_multihead_attention_f32(const float* q, const float* k, const float* v, float* y, int B, int seq,
                                             int hidden, int num_heads, float scale, void* workspace, void* stream) {
-    if (!q || !k || !v || !y || !workspace) return set_err(NNRH_ERR_INVALID, "mha: NULL argument");
+    if (!q || !k || !v || !y) return set_err(NNRH_ERR_INVALID, "mha: NULL argument");
     if (B < 0 || seq < 0 || hidden <= 0 || num_heads <= 0 || hidden % num_heads)
         return set_err(NNRH_ERR_INVALID, "mha: hidden %d / heads %d", hidden, num_heads);
+    if (!workspace && !mha_fused_ok(q, k, v, y, seq, hidden, num_heads))
+        return set_err(NNRH_ERR_INVALID, "mha: this shape (or unaligned q / k / v / y) needs the workspace");
     if (((uintptr_t)workspace & 255) != 0) return set_err(NNRH_ERR_INVALID, "mha: workspace must be 256-byte aligned");
     hipStream_t s = S(stream);
     ProfScope ps("multihead_attention", s);

@@ -34,6 +34,9 @@ hipError_t launch_gelu_f32(const float* x, float* y, long long n, hipStream_t s)
 hipError_t launch_transpose_f32(const float* x, float* y, int ndim, const int* in_dims, const int* perm,
                                 hipStream_t s);
 size_t mha_workspace_bytes(int B, int S, int nh);
+// the fused head-64 attention kernel's shapes, and those with aligned tensors
+bool mha_fused_shape(int S, int Hd, int nh);
+bool mha_fused_ok(const float* q, const float* k, const float* v, const float* y, int S, int Hd, int nh);
 hipError_t launch_mha_f32(const float* q, const float* k, const float* v, float* y, int B, int S, int Hd, int nh,
                           float scale, void* ws, hipStream_t s);
 hipError_t launch_hardswish_f32(const float* x, float* y, long long n, int post_op, hipStream_t s);

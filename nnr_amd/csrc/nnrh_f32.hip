@@ -831,9 +831,11 @@ __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __r
         }
 }
 
+bool mha_fused_shape(int S, int Hd, int nh) { return nh > 0 && Hd == 64 * nh && S <= 128; }
+
 bool mha_fused_ok(const float* q, const float* k, const float* v, const float* y, int S, int Hd, int nh) {
     const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)y;
-    return nh > 0 && Hd == 64 * nh && S <= 128 && (al & 15) == 0;
+    return mha_fused_shape(S, Hd, nh) && (al & 15) == 0;
 }
 
 hipError_t launch_mha_f32(const float* q, const float* k, const float* v, float* y, int B, int S, int Hd, int nh,

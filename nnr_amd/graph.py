@@ -45,6 +45,8 @@ def host_lib():
             "nnr_ctx_destroy": (i, [vp]),
             "nnr_ctx_set_stream": (i, [vp, vp]),
             "nnr_ctx_set_fusion": (i, [vp, i]),
+            "nnr_ctx_set_graph": (i, [vp, i]),
+            "nnr_ctx_graph_active": (i, [vp, P(i)]),
             "nnr_ctx_set_conv_add": (i, [vp, i]),
             "nnr_ctx_add_initializer": (i, [vp, cp, i, P(i), i, vp]),
             "nnr_ctx_add_input": (i, [vp, cp, i, P(i), i]),
@@ -162,11 +164,12 @@ class Session:
     """A prepared C++ context_t for `graph` with the HIP backend preferred."""
 
     def __init__(self, graph: Graph | None, stream=None, fusion=True, device=True, conv_add=True,
-                 memory_planning=False, onnx=None, sym_dim=0):
+                 memory_planning=False, onnx=None, sym_dim=0, hip_graph=True):
         """graph: the in-process description, built into the context through
         the C ABI. onnx: instead, an ONNX model -- a file path (external data
         relative to it) or ModelProto bytes -- loaded by the C++ loader;
-        sym_dim: the value of symbolic input dimensions (0: 1)."""
+        sym_dim: the value of symbolic input dimensions (0: 1). hip_graph:
+        from the second run() on, replay the plan as one captured HIP graph."""
         L = host_lib()
         self.L = L
         self.graph = graph
@@ -177,6 +180,7 @@ class Session:
             stream = _lib.cur_stream()
         _chk(L.nnr_ctx_set_stream(h, stream))
         _chk(L.nnr_ctx_set_fusion(h, 1 if fusion else 0))
+        _chk(L.nnr_ctx_set_graph(h, 1 if hip_graph else 0))
         _chk(L.nnr_ctx_set_conv_add(h, 1 if conv_add else 0))
         _chk(L.nnr_ctx_set_memory_planning(h, 1 if memory_planning else 0))
         if onnx is not None:
@@ -334,6 +338,12 @@ class Session:
             entries.append(dict(name=nm.value.decode(), first=f.value, last=l_.value, offset=o.value,
                                 bytes=by.value, kind=kinds[kd.value], parent=par.value))
         return stats, entries
+
+    def graph_active(self) -> bool:
+        """True once run() replays a captured HIP graph."""
+        on = C.c_int()
+        _chk(self.L.nnr_ctx_graph_active(self.h, C.byref(on)))
+        return bool(on.value)
 
     def enable_profiling(self, on=True):
         _chk(self.L.nnr_ctx_enable_profiling(self.h, 1 if on else 0))

@@ -74,6 +74,22 @@ int nnr_ctx_set_stream(nnr_ctx_t c, void* s) {
     });
 }
 
+int nnr_ctx_set_graph(nnr_ctx_t c, int on) {
+    return guarded("ctx_set_graph", [&]() -> int {
+        if (!c) return err("ctx is NULL");
+        c->ctx.enable_graph = on != 0;
+        return 0;
+    });
+}
+
+int nnr_ctx_graph_active(nnr_ctx_t c, int* on) {
+    return guarded("ctx_graph_active", [&]() -> int {
+        if (!c || !on) return err("graph_active: NULL argument");
+        *on = c->ctx.enable_graph && c->ctx.graph_active() ? 1 : 0;
+        return 0;
+    });
+}
+
 int nnr_ctx_set_fusion(nnr_ctx_t c, int on) {
     return guarded("ctx_set_fusion", [&]() -> int {
         if (!c) return err("ctx is NULL");

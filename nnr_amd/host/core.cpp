@@ -181,6 +181,8 @@ void* pool_t::alloc(size_t size, size_t align) {
 context_t::context_t() = default;
 
 context_t::~context_t() {
+    if (graph_exec_) nnrh_graph_destroy(graph_exec_);
+    if (cap_stream_) nnrh_stream_destroy(cap_stream_);
     for (auto& e : events_) {
         nnrh_event_destroy(e.first);
         nnrh_event_destroy(e.second);
@@ -478,10 +480,54 @@ bool context_t::prepare() {
     return true;
 }
 
+// run loop (src/nnr.cpp:908-1050): exec active nodes in order on `stream`
+bool context_t::exec_all(bool profiled) {
+    size_t pi = 0;
+    for (auto* op : nodes) {
+        if (op->skip || op->folded) continue;
+        if (profiled) nnrh_event_record(events_[pi].first, stream);
+        if (!op->exec())
+            return fail("exec failed: " + op->node_name + " (" + op->op_type + "): " +
+                        (last_error.empty() ? std::string(nnrh_last_error()) : last_error));
+        if (profiled) nnrh_event_record(events_[pi].second, stream);
+        ++pi;
+    }
+    return true;
+}
+
+// The plan's launches recorded once into a HIP graph on a private stream
+// (every tensor keeps its device address from prepare() on, so the
+// recorded arguments stay valid; inputs are copied into their buffers).
+// Taken after one node-by-node run, which does each operator's first-call
+// set-up. A capture that fails (an operator that allocates or synchronizes
+// inside exec) turns graphs off for this context.
+bool context_t::capture_graph() {
+    if (!cap_stream_ && nnrh_stream_create(&cap_stream_) != NNRH_OK) return false;
+    void* user = stream;
+    stream = cap_stream_;
+    bool ok = nnrh_graph_begin_capture(stream) == NNRH_OK;
+    const bool ran = ok && exec_all(false);
+    void* ge = nullptr;
+    if (ok) ok = nnrh_graph_end_capture(stream, &ge) == NNRH_OK && ran && ge;
+    stream = user;
+    if (!ok) {
+        if (ge) nnrh_graph_destroy(ge);
+        last_error.clear();
+        return false;
+    }
+    graph_exec_ = ge;
+    return true;
+}
+
 bool context_t::run() {
     if (!prepared && !prepare()) return false;
-    // run loop (src/nnr.cpp:908-1050): exec active nodes in order
-    size_t pi = 0;
+    const bool graph = enable_graph && !enable_profiling && !graph_failed_ && !nnrh_profile_enabled();
+    if (graph && !graph_exec_ && eager_runs_ > 0 && !capture_graph()) graph_failed_ = true;
+    if (graph && graph_exec_) {
+        if (nnrh_graph_launch(graph_exec_, stream) != NNRH_OK)
+            return fail(std::string("graph launch failed: ") + nnrh_last_error());
+        return true;
+    }
     if (enable_profiling && events_.size() < profile.size()) {
         while (events_.size() < profile.size()) {
             void *a = nullptr, *b = nullptr;
@@ -489,15 +535,9 @@ bool context_t::run() {
             events_.emplace_back(a, b);
         }
     }
-    for (auto* op : nodes) {
-        if (op->skip || op->folded) continue;
-        if (enable_profiling) nnrh_event_record(events_[pi].first, stream);
-        if (!op->exec())
-            return fail("exec failed: " + op->node_name + " (" + op->op_type + "): " +
-                        (last_error.empty() ? std::string(nnrh_last_error()) : last_error));
-        if (enable_profiling) nnrh_event_record(events_[pi].second, stream);
-        ++pi;
-    }
+    if (!exec_all(enable_profiling)) return false;
+    ++eager_runs_;
+    const size_t pi = profile.size();
     if (enable_profiling) {
         for (size_t i = 0; i < pi; ++i) {
             float ms = 0.f;

@@ -287,6 +287,11 @@ struct context_t {
     bool enable_fusion = true;
     bool enable_conv_add = true;  // fuse_conv_add / fuse_matmul_dq_bias after the operators are built
     bool enable_profiling = false;
+    // run() from its second call on replays the whole plan as one HIP graph
+    // captured on a private stream (off while profiling; falls back to
+    // node-by-node launches for good if the capture fails)
+    bool enable_graph = true;
+    bool graph_active() const { return graph_exec_ != nullptr; }
     bool shape_only = false;      // reshape() computes shapes only (pre-layout pass)
     // share device memory between intermediates (src/nnr.h:523-529; off by
     // default as in the reference). Set before prepare().
@@ -313,6 +318,12 @@ struct context_t {
 private:
     std::vector<void*> allocations_;
     std::vector<std::pair<void*, void*>> events_;   // per-node hipEvents (profiling)
+    void* graph_exec_ = nullptr;   // the captured plan
+    void* cap_stream_ = nullptr;   // the stream it was captured on
+    int eager_runs_ = 0;
+    bool graph_failed_ = false;
+    bool exec_all(bool profiled);
+    bool capture_graph();
     bool plan_memory();
     bool upload_constants();
 };

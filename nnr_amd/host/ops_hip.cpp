@@ -1369,7 +1369,8 @@ struct MultiHeadAttention_hip : operator_t {
         if (q->dims[2] % num_heads) return bad(this, "hidden not divisible by num_heads");
         if (!ctx->shape_only) {
             size_t need = 0;
-            if (!ok(this, nnrh_multihead_attention_workspace(q->dims[0], q->dims[1], num_heads, &need))) return false;
+            if (!ok(this, nnrh_multihead_attention_workspace(q->dims[0], q->dims[1], q->dims[2], num_heads, &need)))
+                return false;
             if (need > ws_bytes) {
                 nnrh_free(ws);
                 ws = nullptr;

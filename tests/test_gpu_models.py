@@ -475,3 +475,38 @@ def test_hardswish_graph(dev, hw, head):
             assert np.array_equal(s.output(p["outputs"][0])[0], O.hardswish(xin)), p["name"]
             tails += xin.size % 16 != 0
     assert tails >= (1 if hw == 29 else 0)   # 15x15 maps of 20 channels: n % 16 != 0
+
+
+@pytest.mark.parametrize("name", ["resnet50", "mobilenetv2", "bert", "bert_pc", "qoperator"])
+def test_hip_graph_replay(dev, name):
+    """From its second call on, run() replays the plan as one captured HIP
+    graph (memory-planned context). Each replay, on a new input copied in
+    between, with eager work and synchronizations between the replays,
+    gives graph outputs bit-identical to a context that launches node by
+    node."""
+    import torch
+    rng = np.random.default_rng(31)
+    if name == "resnet50":
+        g, shape = synth.resnet50(batch=2, hw=64, seed=14), (2, 3, 64, 64)
+    elif name == "mobilenetv2":
+        g, shape = synth.mobilenetv2(batch=2, hw=96, seed=17), (2, 3, 96, 96)
+    elif name.startswith("bert"):
+        g, shape = synth.bert(batch=2, seq=64, layers=2, per_channel=name == "bert_pc"), (2, 64, 768)
+    else:
+        g, shape = synth.qoperator_net(batch=3, hw=21), (3, 3, 21, 21)
+    eager = G.Session(g, hip_graph=False)
+    s = G.Session(g, memory_planning=True)
+    for rep in range(4):
+        print(f"{name} replay {rep}", flush=True)
+        x = rng.uniform(-1.0, 1.5, shape).astype(np.float32)
+        for sess in (eager, s):
+            sess.set_input("input", x)
+            sess.run()
+        torch.cuda.synchronize()
+        assert s.graph_active() == (rep >= 1), rep
+        assert not eager.graph_active()
+        for o in g.outputs:
+            a, b = s.output(o)[0], eager.output(o)[0]
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (rep, o)
+        torch.zeros(1 << 20, device=dev).add_(1.0)   # eager work between the replays
+        torch.cuda.synchronize()

@@ -915,9 +915,14 @@ def test_multihead_attention_f32(dev, B, S, hidden, heads, scale):
     e = np.exp(sc - sc.max(-1, keepdims=True))
     ref = np.matmul(e / e.sum(-1, keepdims=True), split(v)).transpose(0, 2, 1, 3).reshape(B, S, hidden)
     nbytes = C.c_size_t()
-    _lib.check(_lib.lib().nnrh_multihead_attention_workspace(B, S, heads, C.byref(nbytes)))
-    ws = torch.empty(nbytes.value + 256, dtype=torch.uint8, device=dev)
-    wsp = (ws.data_ptr() + 255) & ~255
+    _lib.check(_lib.lib().nnrh_multihead_attention_workspace(B, S, hidden, heads, C.byref(nbytes)))
+    fused = hidden == 64 * heads and S <= 128
+    # the fused kernel needs no workspace: NULL is passed
+    assert (nbytes.value == 0) == fused
+    wsp = None
+    if not fused:
+        ws = torch.empty(nbytes.value + 256, dtype=torch.uint8, device=dev)
+        wsp = (ws.data_ptr() + 255) & ~255
     qd, kd, vd = to_dev(q, dev), to_dev(k, dev), to_dev(v, dev)
     y = torch.empty((B, S, hidden), dtype=torch.float32, device=dev)
     _lib.check(_lib.lib().nnrh_multihead_attention_f32(_lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd), _lib.ptr(y), B, S,
