@@ -41,6 +41,63 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint8_t* __rest
     }
 }
 
+// 4 x 4 byte transpose of dwords a, b, c, d (row i = bytes of the i-th
+// dword): o[j] = {a.byte j, b.byte j, c.byte j, d.byte j}. v_perm_b32's
+// selector picks bytes of {S0 (bytes 4-7), S1 (bytes 0-3)}.
+__device__ __forceinline__ void transpose4x4_u8(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t (&o)[4]) {
+    const uint32_t t0 = __builtin_amdgcn_perm(b, a, 0x06020400u);   // a0 b0 a2 b2
+    const uint32_t t1 = __builtin_amdgcn_perm(b, a, 0x07030501u);   // a1 b1 a3 b3
+    const uint32_t t2 = __builtin_amdgcn_perm(d, c, 0x06020400u);   // c0 d0 c2 d2
+    const uint32_t t3 = __builtin_amdgcn_perm(d, c, 0x07030501u);   // c1 d1 c3 d3
+    o[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);              // a0 b0 c0 d0
+    o[1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);              // a1 b1 c1 d1
+    o[2] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);              // a2 b2 c2 d2
+    o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);              // a3 b3 c3 d3
+}
+
+// NCHW -> NHWC with Cpad % 16 == 0 and HW % 16 == 0 (16-byte aligned
+// tensors): a thread per (image, 16 pixels, 16 channels) loads the 16
+// channel rows of its pixels (one 16-byte load each; channels past C are
+// the fill byte), transposes the 16 x 16 bytes in registers and stores 16
+// pixels of 16 channels (one 16-byte store each). Consecutive threads take
+// consecutive channel groups of one pixel group, so a store instruction
+// writes whole 16 x Cpad-byte pixel runs. One-wave blocks: a thread moves
+// 256 bytes, so the grid is small and is spread over every CU.
+__global__ __launch_bounds__(64) void nchw_to_nhwc16_kernel(const uint8_t* __restrict x, uint8_t* __restrict y,
+                                                            int C, int HW, int Cpad, long long total,
+                                                            uint8_t fill) {
+    const long long t = (long long)blockIdx.x * 64 + threadIdx.x;
+    if (t >= total) return;
+    const int cgs = Cpad >> 4, pgs = HW >> 4;
+    const long long rest = t / cgs;
+    const int cg = (int)(t - rest * cgs);
+    const long long n = rest / pgs;
+    const int pg = (int)(rest - n * pgs);
+    const uint8_t* xp = x + (n * C + cg * 16) * (long long)HW + pg * 16;
+    const uint32_t fw = (uint32_t)fill * 0x01010101u;
+    uint4 r[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        r[i] = cg * 16 + i < C ? *(const uint4*)(xp + (long long)i * HW) : make_uint4(fw, fw, fw, fw);
+    uint8_t* yp = y + (n * HW + pg * 16) * (long long)Cpad + cg * 16;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+        // pixels 4 jb .. 4 jb + 3: dword jb of every channel row
+        uint32_t o[4][4];   // [channel quad q][pixel jj]
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t* a = (const uint32_t*)&r[4 * q];
+            const uint32_t* b = (const uint32_t*)&r[4 * q + 1];
+            const uint32_t* c = (const uint32_t*)&r[4 * q + 2];
+            const uint32_t* d = (const uint32_t*)&r[4 * q + 3];
+            transpose4x4_u8(a[jb], b[jb], c[jb], d[jb], o[q]);
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+            *(uint4*)(yp + (long long)(4 * jb + jj) * Cpad) = make_uint4(o[0][jj], o[1][jj], o[2][jj], o[3][jj]);
+    }
+}
+
 // small channel counts (first-layer input, C <= 4 padded to 4): one thread
 // per pixel, channel planes read coalesced, one 32-bit store per pixel
 __global__ __launch_bounds__(256) void nchw_to_nhwc4_kernel(const uint8_t* __restrict x,
@@ -63,6 +120,12 @@ hipError_t launch_nchw_to_nhwc_u8(const uint8_t* x, uint8_t* y, int N, int C, in
         long long total = (long long)N * HW;
         hipLaunchKernelGGL(nchw_to_nhwc4_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                            x, (uint32_t*)y, C, (long long)HW, total, fill);
+        return hipGetLastError();
+    }
+    if (Cpad % 16 == 0 && HW % 16 == 0 && C <= Cpad && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0) {
+        const long long total = (long long)N * (HW / 16) * (Cpad / 16);
+        hipLaunchKernelGGL(nchw_to_nhwc16_kernel, dim3((unsigned)((total + 63) / 64)), dim3(64), 0, s, x, y, C,
+                           HW, Cpad, total, fill);
         return hipGetLastError();
     }
     dim3 grid((HW + 63) / 64, N);

@@ -633,7 +633,46 @@ void qgemm_dma_kernel(GemmArgs g) {
                 }
             } else {
                 uint32_t packed[4];
-                if constexpr (EPI == EPI_RQB) {
+                // fused QLinearAdd, body rows: the conv byte enters RQ-E as
+                // a float. rne(clamp(f, lo - zp, hi - zp)) + zp is exactly the
+                // value of the byte RQ-B stores (an integer in [lo, hi]), so
+                // it is used as it is, with no byte pack and unpack between
+                // the two requantizations
+                bool add_done = false;
+                if constexpr (FUSE == FUSE_ADD && EPI == EPI_RQB) {
+                    const long long i0 = (long long)m * g.ldy + nb;
+                    if (i0 + 16 <= g.add_body) {
+                        const int rrow = wm * 64 + tm * 16 + frow;
+                        const int rpc = (wn * 4 + fchunk) ^ (rrow & (RCPR - 1));
+                        const v4i rres = *(const v4i*)(ps + PPAR + (rrow * RCPR + rpc) * 16);
+                        const float lo_f = (float)g.lo - (float)g.y_zp, hi_f = (float)g.hi - (float)g.y_zp;
+                        auto add_body = [&](auto zp0_t) {
+                            constexpr bool ZP0 = decltype(zp0_t)::value;
+                            const float zp_f = (float)g.y_zp;
+#pragma unroll
+                            for (int tn = 0; tn < 4; ++tn) {
+                                const uint32_t rw = (uint32_t)rres[tn];
+                                uint32_t w = 0;
+#pragma unroll
+                                for (int q = 0; q < 4; ++q) {
+                                    const float f = (float)acc[tm][tn][q] * __int_as_float(p0[tn][q]);
+                                    float qf = __builtin_rintf(med3f(f, lo_f, hi_f));
+                                    if constexpr (!ZP0) qf = qf + zp_f;
+                                    const float rf = (float)((rw >> (8 * q)) & 0xffu);
+                                    float v = __builtin_fmaf(CONV_A ? rf : qf, g.add_sb, g.add_fixed);
+                                    v = __builtin_fmaf(CONV_A ? qf : rf, g.add_sa, v);
+                                    w = __builtin_amdgcn_cvt_pk_u8_f32(v, q, w);
+                                }
+                                packed[tn] = w;
+                            }
+                        };
+                        if (g.y_zp == 0) add_body(std::true_type{});
+                        else add_body(std::false_type{});
+                        add_done = true;
+                    }
+                }
+                if (add_done) {
+                } else if constexpr (EPI == EPI_RQB) {
                     if (sat_u8) {
                         // zero point 0: rne(clamp(f, 0, 255)) = sat(rne(f))
 #pragma unroll
@@ -725,7 +764,7 @@ void qgemm_dma_kernel(GemmArgs g) {
                         packed[tn] = w;
                     }
                 }
-                if constexpr (FUSE == FUSE_ADD) {
+                if constexpr (FUSE == FUSE_ADD) if (!add_done) {
                     // uint8 output (checked on the host)
                     const long long i0 = (long long)m * g.ldy + nb;
                     // this lane's 16 residual bytes (row m, columns nb..nb+15)

@@ -175,6 +175,10 @@ CONV_CASES = [
     ("packed_wzp_neg", 1, 32, 7, 7, 24, 1, dict(y_nhwc=1, w_zp=(-3,), y_scale=3.0, y_zp=40)),
     ("first_s1_pad", 2, 3, 20, 21, 48, 5, dict(pads=(2, 1, 2, 1), y_nhwc=1, y_zp=17)),
     ("packed_nchw_out", 1, 32, 20, 20, 24, 3, dict(pads=(1, 1, 1, 1), y_nhwc=0)),
+    # NCHW input through the 16 x 16 register transpose (HW % 16 == 0): 40
+    # channels padded to 48 with the zero point; 64 channels, 3 images
+    ("nchw16_c40_pad", 2, 40, 8, 12, 64, 3, dict(pads=(1, 1, 1, 1), y_nhwc=1, y_zp=4)),
+    ("nchw16_c64", 3, 64, 16, 16, 32, 1, dict(y_nhwc=1, x_zp=200)),
     ("packed_dil", 1, 16, 12, 12, 32, 3, dict(pads=(2, 2, 2, 2), dil=(2, 2), y_nhwc=1)),
     ("packed_c24", 2, 24, 10, 10, 144, 1, dict(y_nhwc=1, x_nhwc=1)),
     ("direct", 2, 64, 12, 12, 64, 3, dict(pads=(1, 1, 1, 1), y_nhwc=0, post_fn=1, y_zp=9)),
