@@ -442,11 +442,16 @@ int nnrh_global_avgpool_f32(const float* x_dev, float* y_dev, int N, int C, int 
  * head) and needs no workspace (NULL is accepted); other shapes use batched
  * GEMMs and a scaled softmax over a workspace of at least
  * nnrh_multihead_attention_workspace bytes, 256-byte aligned. The size is 0
- * for the fused shapes.                                                    */
+ * for the fused shapes. minmax_parts (optional, NULL for none; no
+ * counterpart in the reference): the fused kernel also writes (min, max)
+ * pairs of y for a DynamicQuantizeLinear that reads it
+ * (nnrh_dynamic_quantize_linear_parts), nnrh_multihead_attention_minmax_count
+ * of them (0 for shapes without the fused kernel, which reject the buffer). */
 int nnrh_multihead_attention_workspace(int B, int seq, int hidden, int num_heads, size_t* bytes);
+int nnrh_multihead_attention_minmax_count(int B, int seq, int hidden, int num_heads, int* pairs);
 int nnrh_multihead_attention_f32(const float* q_dev, const float* k_dev, const float* v_dev, float* y_dev,
                                  int B, int seq, int hidden, int num_heads, float scale,
-                                 void* workspace_dev, void* stream);
+                                 float* minmax_parts_dev, void* workspace_dev, void* stream);
 /* No counterpart in the reference: DequantizeLinear (DequantizeLinear.cpp:
  * 133-152, per-tensor scale and zero point, uint8 or int8 x) feeding
  * GlobalAveragePool, in one pass over the 8-bit tensor. Each value is

@@ -29,7 +29,7 @@ EXPORTS = [
     "nnrh_qconv_dispatch", "nnrh_qconv_create", "nnrh_qconv_branch", "nnrh_qconv_run",
     "nnrh_qconv_destroy", "nnrh_qconv_fuse_add", "nnrh_qconv_run_add",
     "nnrh_qconv_fuse_quantize", "nnrh_qconv_run_f32", "nnrh_qconv_fuse_maxpool", "nnrh_global_avgpool_dequant",
-    "nnrh_multihead_attention_workspace", "nnrh_multihead_attention_f32", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
+    "nnrh_multihead_attention_workspace", "nnrh_multihead_attention_f32", "nnrh_multihead_attention_minmax_count", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
     "nnrh_qmatmul_fuse_dq_bias", "nnrh_qmatmul_fuse_gelu", "nnrh_qmatmul_minmax_count",
     "nnrh_qmatmul_set_minmax_out", "nnrh_dynamic_quantize_linear_parts", "nnrh_add_layernorm_f32",
     "nnrh_qmatmul_group_create", "nnrh_qmatmul_group_run", "nnrh_qmatmul_group_destroy",
@@ -137,7 +137,8 @@ def lib():
         "nnrh_qconv_fuse_maxpool": (i, [vp, i, i, i, i, i, i, i, i]),
         "nnrh_global_avgpool_dequant": (i, [vp, vp, i, i, i, i, i, f, i, vp]),
         "nnrh_multihead_attention_workspace": (i, [i, i, i, i, P(sz)]),
-        "nnrh_multihead_attention_f32": (i, [vp, vp, vp, vp, i, i, i, i, f, vp, vp]),
+        "nnrh_multihead_attention_f32": (i, [vp, vp, vp, vp, i, i, i, i, f, vp, vp, vp]),
+        "nnrh_multihead_attention_minmax_count": (i, [i, i, i, i, P(i)]),
         "nnrh_qmatmul_create": (i, [P(vp), P(QMatMulDesc)]),
         "nnrh_qmatmul_run": (i, [vp, vp, ll, vp, i, vp, vp, vp]),
         "nnrh_qmatmul_destroy": (i, [vp]),

@@ -1957,17 +1957,28 @@ extern "C" int nnrh_multihead_attention_workspace(int B, int seq, int hidden, in
     return NNRH_OK;
 }
 
+extern "C" int nnrh_multihead_attention_minmax_count(int B, int seq, int hidden, int num_heads, int* pairs) {
+    if (!pairs || B < 0 || seq < 0 || num_heads <= 0 || hidden <= 0 || hidden % num_heads)
+        return set_err(NNRH_ERR_INVALID, "mha_minmax_count: arguments");
+    *pairs = mha_minmax_pairs(B, seq, hidden, num_heads);
+    return NNRH_OK;
+}
+
 extern "C" int nnrh_multihead_attention_f32(const float* q, const float* k, const float* v, float* y, int B, int seq,
-                                            int hidden, int num_heads, float scale, void* workspace, void* stream) {
+                                            int hidden, int num_heads, float scale, float* minmax_parts,
+                                            void* workspace, void* stream) {
     if (!q || !k || !v || !y) return set_err(NNRH_ERR_INVALID, "mha: NULL argument");
     if (B < 0 || seq < 0 || hidden <= 0 || num_heads <= 0 || hidden % num_heads)
         return set_err(NNRH_ERR_INVALID, "mha: hidden %d / heads %d", hidden, num_heads);
-    if (!workspace && !mha_fused_ok(q, k, v, y, seq, hidden, num_heads))
-        return set_err(NNRH_ERR_INVALID, "mha: this shape (or unaligned q / k / v / y) needs the workspace");
+    if ((!workspace || minmax_parts) && !mha_fused_ok(q, k, v, y, seq, hidden, num_heads))
+        return set_err(NNRH_ERR_INVALID, minmax_parts ? "mha: min / max pairs need the fused kernel (head size 64, "
+                                                        "seq <= 128, 16-byte aligned q / k / v / y)"
+                                                      : "mha: this shape (or unaligned q / k / v / y) needs the workspace");
     if (((uintptr_t)workspace & 255) != 0) return set_err(NNRH_ERR_INVALID, "mha: workspace must be 256-byte aligned");
     hipStream_t s = S(stream);
     ProfScope ps("multihead_attention", s);
-    HIP_TRY(launch_mha_f32(q, k, v, y, B, seq, hidden, num_heads, scale, workspace, s), "multihead_attention");
+    HIP_TRY(launch_mha_f32(q, k, v, y, B, seq, hidden, num_heads, scale, minmax_parts, workspace, s),
+            "multihead_attention");
     return NNRH_OK;
 }
 

@@ -160,26 +160,25 @@ __device__ __forceinline__ void dyn_scale_block(const float* __restrict part, in
 __device__ __forceinline__ uint32_t dyn_q1(float v, float sc, int zp) {
     return (uint32_t)clampi(wrap_add(x86_f2i(__builtin_rintf(v / sc)), zp), 0, 255);
 }
-// scale and zero point alone, from (min, max) pairs a producer wrote: one
-// block of 1024 threads, two pairs per 16-byte load, the loads of a thread
-// issued together (one memory round trip for up to 8192 pairs)
-__global__ __launch_bounds__(1024) void dyn_scale_parts_kernel(const float* __restrict part, int nparts,
-                                                               float* __restrict y_scale,
-                                                               uint8_t* __restrict y_zp) {
-    __shared__ float smn[16], smx[16];
+// scale and zero point from producer-written (min, max) pairs, reduced by
+// every block of the quantize kernel (256 threads): every block gets the
+// same values, since min and max are exact in any order
+__device__ __forceinline__ void dyn_scale_parts_block(const float* __restrict part, int nparts, float* sc_out,
+                                                      int* zp_out) {
+    __shared__ float smn[4], smx[4];
     float mn = 0.0f, mx = 0.0f;
     const int n2 = nparts >> 1;   // whole float4s (the pairs are 8-byte aligned)
     const bool vec = ((uintptr_t)part & 15) == 0;
     if (vec) {
         const float4* p4 = (const float4*)part;
 #pragma unroll 4
-        for (int i = threadIdx.x; i < n2; i += 1024) {
+        for (int i = threadIdx.x; i < n2; i += 256) {
             const float4 v = p4[i];
             mn = fminf(mn, fminf(v.x, v.z));
             mx = fmaxf(mx, fmaxf(v.y, v.w));
         }
     }
-    for (int i = (vec ? 2 * n2 : 0) + threadIdx.x; i < nparts; i += 1024) {
+    for (int i = (vec ? 2 * n2 : 0) + threadIdx.x; i < nparts; i += 256) {
         mn = fminf(mn, part[2 * i]);
         mx = fmaxf(mx, part[2 * i + 1]);
     }
@@ -194,25 +193,21 @@ __global__ __launch_bounds__(1024) void dyn_scale_parts_kernel(const float* __re
         smx[w] = mx;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int i = 1; i < 16; ++i) {
-            mn = fminf(mn, smn[i]);
-            mx = fmaxf(mx, smx[i]);
-        }
-        // as dyn_scale_block
-        const float xmin = mn < 0.0f ? mn : 0.0f;
-        const float xmax = mx > 0.0f ? mx : 0.0f;
-        float sc = (xmax - xmin) / 255.0f;
-        if (sc == 0.0f) sc = 1.0f;
-        *y_scale = sc;
-        *y_zp = (uint8_t)clampi(x86_f2i(__builtin_rintf(-xmin / sc)), 0, 255);
-    }
+    mn = fminf(fminf(smn[0], smn[1]), fminf(smn[2], smn[3]));
+    mx = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
+    const float xmin = mn < 0.0f ? mn : 0.0f;
+    const float xmax = mx > 0.0f ? mx : 0.0f;
+    float sc = (xmax - xmin) / 255.0f;
+    if (sc == 0.0f) sc = 1.0f;
+    *sc_out = sc;
+    *zp_out = clampi(x86_f2i(__builtin_rintf(-xmin / sc)), 0, 255);
 }
 
 // y = clamp(nearbyint(fl(x / s)) + zp, 0, 255): 16 elements per thread over the
-// 16-byte aligned body (one 16-byte store), scalar over the rest. SCALED: the
-// scale / zero point are already in y_scale / y_zp (dyn_scale_parts_kernel)
-template <bool SCALED>
+// 16-byte aligned body (one 16-byte store), scalar over the rest. PARTS: part
+// holds nparts producer-written (min, max) pairs, reduced by every block;
+// else the minmax_partial_kernel's pairs (dyn_scale_block)
+template <bool PARTS>
 __global__ __launch_bounds__(256) void dyn_quantize_kernel(const float* __restrict x, long long n,
                                                            const float* __restrict part, int nparts,
                                                            float* __restrict y_scale,
@@ -220,15 +215,11 @@ __global__ __launch_bounds__(256) void dyn_quantize_kernel(const float* __restri
                                                            uint8_t* __restrict y) {
     float sc;
     int zp;
-    if (SCALED) {
-        sc = *y_scale;
-        zp = *y_zp;
-    } else {
-        dyn_scale_block(part, nparts, &sc, &zp);
-        if (blockIdx.x == 0 && threadIdx.x == 0) {
-            *y_scale = sc;
-            *y_zp = (uint8_t)zp;
-        }
+    if (PARTS) dyn_scale_parts_block(part, nparts, &sc, &zp);
+    else dyn_scale_block(part, nparts, &sc, &zp);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *y_scale = sc;
+        *y_zp = (uint8_t)zp;
     }
     const bool vec = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
     const long long n16 = vec ? n >> 4 : 0;
@@ -315,12 +306,12 @@ hipError_t launch_dynamic_quantize_noalloc(const float* x, long long n, uint8_t*
 
 hipError_t launch_dynamic_quantize_parts(const float* x, long long n, const float* parts, int nparts,
                                          uint8_t* y, float* y_scale, uint8_t* y_zp, hipStream_t s) {
-    hipLaunchKernelGGL(dyn_scale_parts_kernel, dim3(1), dim3(1024), 0, s, parts, nparts, y_scale, y_zp);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    // one launch: every block reduces the pairs (nparts * 8 bytes from L2)
+    // and quantizes its share; a grid of at most 512 blocks keeps the
+    // repeated reads of the pairs small against the tensor
     long long qb = (n / 16 + 255) / 256;
     if (qb < 1) qb = 1;
-    if (qb > 4096) qb = 4096;
+    if (qb > 512) qb = 512;
     hipLaunchKernelGGL(dyn_quantize_kernel<true>, dim3((unsigned)qb), dim3(256), 0, s, x, n, parts, nparts,
                        y_scale, y_zp, y);
     return hipGetLastError();

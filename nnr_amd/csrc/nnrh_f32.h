@@ -38,7 +38,10 @@ size_t mha_workspace_bytes(int B, int S, int nh);
 bool mha_fused_shape(int S, int Hd, int nh);
 bool mha_fused_ok(const float* q, const float* k, const float* v, const float* y, int S, int Hd, int nh);
 hipError_t launch_mha_f32(const float* q, const float* k, const float* v, float* y, int B, int S, int Hd, int nh,
-                          float scale, void* ws, hipStream_t s);
+                          float scale, float* parts, void* ws, hipStream_t s);
+// (min, max) pairs the fused kernel writes (4 per (batch, head)); 0 when the
+// shape takes the batched-GEMM path, which writes none
+int mha_minmax_pairs(int B, int S, int Hd, int nh);
 hipError_t launch_hardswish_f32(const float* x, float* y, long long n, int post_op, hipStream_t s);
 hipError_t launch_clip_f32(const float* x, float* y, long long n, float lo, float hi,
                            hipStream_t s);

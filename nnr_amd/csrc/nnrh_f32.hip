@@ -712,9 +712,13 @@ size_t mha_workspace_bytes(int B, int S, int nh) {
 // before P V (the order of Softmax then MatMul); padded t rows are -inf.
 constexpr int MHA_KP = 68;   // K row stride in LDS (floats): rows 16 bytes apart in the banks
 
+// parts (optional): one (min, max) pair per wave, at 2 (4 blockIdx.x + wave),
+// of the values the wave stores (0 stands in for nothing, as for every
+// producer that feeds a DynamicQuantizeLinear, whose range includes 0)
 __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __restrict q, const float* __restrict k,
                                                              const float* __restrict v, float* __restrict y,
-                                                             int S, int Hd, int nh, float scale) {
+                                                             int S, int Hd, int nh, float scale,
+                                                             float* __restrict parts) {
     // one buffer: K (row stride MHA_KP) for the scores, then V (stride 64)
     __shared__ __attribute__((aligned(16))) float ks[128 * MHA_KP];
     float* const vs = ks;
@@ -800,7 +804,10 @@ __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __r
         *(float4*)(vs + t * 64 + c) = t < S ? *(const float4*)(v + off) : zero4;
     }
     __syncthreads();
-    if (!active) return;   // (after the last barrier)
+    if (!active) {   // (after the last barrier)
+        if (parts && lane == 0) *(float2*)(parts + 2 * (4 * blockIdx.x + w)) = make_float2(0.0f, 0.0f);
+        return;
+    }
     // O[s][d] = sum_t P[s][t] V[t][d]; output tile td holds d = 4 (l % 16) + td
     f32x4 o[2][4];
 #pragma unroll
@@ -820,15 +827,36 @@ __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __r
                     o[ts][td] = __builtin_amdgcn_mfma_f32_16x16x4f32(acc[tt][ts][i], vb[td], o[ts][td], 0, 0, 0);
         }
     // o[ts][td][i] = O[s0 + 16 ts + 4 g + i][4 lr + td]
+    float mn = 0.0f, mx = 0.0f;
 #pragma unroll
     for (int ts = 0; ts < 2; ++ts)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int sq = s0 + 16 * ts + 4 * g + i;
-            if (sq < S)
+            if (sq < S) {
                 *(float4*)(y + base + (long long)sq * Hd + 4 * lr) =
                     make_float4(o[ts][0][i], o[ts][1][i], o[ts][2][i], o[ts][3][i]);
+#pragma unroll
+                for (int td = 0; td < 4; ++td) {
+                    mn = fminf(mn, o[ts][td][i]);
+                    mx = fmaxf(mx, o[ts][td][i]);
+                }
+            }
         }
+    if (parts) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            mn = fminf(mn, __shfl_xor(mn, off, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        }
+        if (lane == 0) *(float2*)(parts + 2 * (4 * blockIdx.x + w)) = make_float2(mn, mx);
+    }
+}
+
+int mha_minmax_pairs(int B, int S, int Hd, int nh) {
+    if (!mha_fused_shape(S, Hd, nh) || B <= 0) return 0;
+    const long long p = 4LL * B * nh;
+    return p <= 0x7fffffffLL ? (int)p : 0;
 }
 
 bool mha_fused_shape(int S, int Hd, int nh) { return nh > 0 && Hd == 64 * nh && S <= 128; }
@@ -839,14 +867,15 @@ bool mha_fused_ok(const float* q, const float* k, const float* v, const float* y
 }
 
 hipError_t launch_mha_f32(const float* q, const float* k, const float* v, float* y, int B, int S, int Hd, int nh,
-                          float scale, void* ws, hipStream_t s) {
+                          float scale, float* parts, void* ws, hipStream_t s) {
     if (B <= 0 || S <= 0) return hipSuccess;
     if (nh <= 0 || Hd % nh) return hipErrorInvalidValue;
     if (mha_fused_ok(q, k, v, y, S, Hd, nh)) {
         hipLaunchKernelGGL(mha_fused_hd64_kernel, dim3((unsigned)(B * nh)), dim3(256), 0, s, q, k, v, y, S, Hd, nh,
-                           scale);
+                           scale, parts);
         return hipGetLastError();
     }
+    if (parts) return hipErrorInvalidValue;   // only the fused kernel writes min / max pairs
     const int hd = Hd / nh, nb = B * nh;
     const float** A1 = (const float**)ws;
     const float** B1 = A1 + nb;

@@ -1381,6 +1381,17 @@ struct MultiHeadAttention_hip : operator_t {
         }
         return outputs[0]->reshape(q->dims, q->type);
     }
+    // one (min, max) pair per wave of the fused head-64 kernel, for the
+    // DynamicQuantizeLinear of the output projection's input
+    int minmax_pairs() const override {
+        const tensor_t* q = inputs[0];
+        int c = 0;
+        if (q->ndim() != 3 ||
+            nnrh_multihead_attention_minmax_count(q->dims[0], q->dims[1], q->dims[2], num_heads, &c) != NNRH_OK)
+            return 0;
+        return c;
+    }
+    bool set_minmax_out(float*, int) override { return true; }
     bool exec() override {
         tensor_t* q = inputs[0];
         const int B = q->dims[0], S = q->dims[1], Hd = q->dims[2];
@@ -1388,7 +1399,7 @@ struct MultiHeadAttention_hip : operator_t {
         const float sc = scale != 0.0f ? scale : 1.0f / sqrtf((float)(Hd / num_heads));
         return ok(this, nnrh_multihead_attention_f32((const float*)q->data, (const float*)inputs[1]->data,
                                                      (const float*)inputs[2]->data, (float*)outputs[0]->data, B, S,
-                                                     Hd, num_heads, sc, ws, ctx->stream));
+                                                     Hd, num_heads, sc, minmax_parts, ws, ctx->stream));
     }
     double num_ops() const override {
         const tensor_t* q = inputs[0];

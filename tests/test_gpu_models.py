@@ -259,13 +259,13 @@ def test_bert_per_node(dev, fused):
     chains = [p for p in plan if p["op"] == "QLinearMatMul" and p.get("fused_chain")]
     assert len(chains) == 12
     # FF1 also absorbs its Gelu; each residual Add is formed inside its
-    # LayerNormalization; the DynamicQuantizeLinear after a LayerNormalization
-    # or a fused FF1 reads min / max pairs its producer wrote (2 per layer,
-    # plus the next layer's input after LN2)
+    # LayerNormalization; the DynamicQuantizeLinear after a LayerNormalization,
+    # a fused FF1 or the attention reads min / max pairs its producer wrote
+    # (3 per layer, plus the next layer's input after LN2)
     assert sum(p["variant"].endswith("+Gelu") for p in chains) == 2 and "Gelu" not in ops
     assert [p["variant"] for p in plan if p["op"] == "LayerNormalization"] == ["+Add"] * 4
     assert "Add" not in ops
-    assert sum(p["variant"] == "MinMaxIn" for p in plan if p["op"] == "DynamicQuantizeLinear") == 5
+    assert sum(p["variant"] == "MinMaxIn" for p in plan if p["op"] == "DynamicQuantizeLinear") == 7
     # each layer's Q / K / V projections run as one grouped launch
     assert sum(p["variant"].endswith("+Group3") for p in chains) == 2
     assert sum(p["variant"].endswith("(grouped)") for p in chains) == 4

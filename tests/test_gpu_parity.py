@@ -930,8 +930,29 @@ def test_multihead_attention_f32(dev, B, S, hidden, heads, scale):
     qd, kd, vd = to_dev(q, dev), to_dev(k, dev), to_dev(v, dev)
     y = torch.empty((B, S, hidden), dtype=torch.float32, device=dev)
     _lib.check(_lib.lib().nnrh_multihead_attention_f32(_lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd), _lib.ptr(y), B, S,
-                                                       hidden, heads, scale, wsp, _lib.cur_stream()))
+                                                       hidden, heads, scale, None, wsp, _lib.cur_stream()))
     np.testing.assert_allclose(to_np(y), ref, atol=1e-4, rtol=1e-4)
+    pairs = C.c_int()
+    _lib.check(_lib.lib().nnrh_multihead_attention_minmax_count(B, S, hidden, heads, C.byref(pairs)))
+    if not fused:
+        assert pairs.value == 0
+        return
+    # the fused kernel's (min, max) pairs: the same output bits, and a
+    # DynamicQuantizeLinear from them equals the two-pass operator
+    assert pairs.value == 4 * B * heads
+    parts = torch.empty(2 * pairs.value, dtype=torch.float32, device=dev)
+    y2 = torch.empty_like(y)
+    _lib.check(_lib.lib().nnrh_multihead_attention_f32(_lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd), _lib.ptr(y2), B, S,
+                                                       hidden, heads, scale, _lib.ptr(parts), None,
+                                                       _lib.cur_stream()))
+    yh = to_np(y2)
+    assert np.array_equal(yh.view(np.uint32), to_np(y).view(np.uint32))
+    pr = to_np(parts).reshape(-1, 2)
+    assert pr[:, 0].min() == min(0.0, yh.min()) and pr[:, 1].max() == max(0.0, yh.max())
+    yq, ys, yz = H.dynamic_quantize_linear_parts(y2, parts)
+    y_ref, s_ref, z_ref = O.dynamic_quantize_linear(yh)
+    assert to_np(ys)[0] == np.float32(s_ref) and int(to_np(yz)[0]) == z_ref
+    assert np.array_equal(to_np(yq), y_ref.reshape(to_np(yq).shape))
 
 
 @pytest.mark.parametrize("nhwc", [0, 1])
