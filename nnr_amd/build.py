@@ -76,8 +76,7 @@ def build_hip(jobs: int | None = None, verbose: bool = False) -> str:
             objs.append(f.result())
     os.makedirs(LIBDIR, exist_ok=True)
     tmp = LIB + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
-          "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB)
     if verbose:
         print(f"[nnr_amd.build] {LIB}")

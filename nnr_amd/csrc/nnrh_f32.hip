@@ -3,7 +3,7 @@
 // target and their parity bar is the reference's float tolerance (1e-3 abs,
 // tensor_equal, src/nnr.cpp:557-563).
 //   GlobalAveragePool (src/backend/cpu/global_pool.cpp), NCHW or NHWC input
-//   Gemm / MatMul     (src/backend/cpu/Gemm.cpp, MatMul.cpp), row-major, through rocBLAS
+//   Gemm / MatMul     (src/backend/cpu/Gemm.cpp, MatMul.cpp), row-major, on fp32 MFMA
 //   Clip / Relu       (src/backend/cpu/Clip.cpp, Relu.cpp)
 //   Add / Mul / Sub / Div with scalar or last-axis broadcast (binary_math.cpp)
 //   Softmax, LayerNormalization over the last axis, Gelu (erf form), Transpose
@@ -12,7 +12,6 @@
 #include "nnrh_f32.h"
 #include "nnrh_rq.h"
 
-#include <rocblas/rocblas.h>
 
 namespace nnrh {
 
@@ -138,37 +137,6 @@ hipError_t launch_gap_f32(const float* x, float* y, int N, int C, int HW, int x_
     return hipGetLastError();
 }
 
-// Y[M][N] = alpha * op(A)[M][K] * op(B)[K][N] + beta * Cb (broadcast), row-major.
-// A plain fp32 GEMM, so it goes to rocBLAS: the broadcast C is written into Y
-// first and rocBLAS accumulates alpha*A*B + beta*Y onto it. Row-major Y is
-// column-major Y^T = op(B)^T op(A)^T, which is the call below.
-__global__ __launch_bounds__(256) void bcast_c_kernel(const float* __restrict C, float* __restrict Y,
-                                                      int M, int N, int c_mode, long long y_bstride) {
-    const long long n = (long long)M * N;
-    float* y = Y + (long long)blockIdx.y * y_bstride;
-    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
-        const long long r = i / N, c = i - r * N;
-        float v;
-        if (c_mode == 1) v = C[0];
-        else if (c_mode == 2) v = C[c];
-        else if (c_mode == 3) v = C[i];
-        else v = C[r];
-        y[i] = v;
-    }
-}
-
-namespace {
-// one rocBLAS handle per (thread, device)
-rocblas_handle blas_handle() {
-    thread_local rocblas_handle handles[16] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
-    if (!handles[dev] && rocblas_create_handle(&handles[dev]) != rocblas_status_success)
-        handles[dev] = nullptr;
-    return handles[dev];
-}
-}  // namespace
-
 // Small fp32 GEMMs (too few 64x64 tiles to fill the chip, e.g. a
 // classifier over one batch): Y = alpha * A[M][K] . op(B) + beta * Cb with
 // fp32 MFMA 16x16x4. A block computes 32x32 outputs; its 4 waves take every
@@ -272,6 +240,93 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(const float* __restr
             }
 }
 
+// Any fp32 GEMM: Y(z)[m][n] = alpha * sum_k A(z)(m, k) B(z)(k, n) (+ beta *
+// the broadcast C), with element strides for A and B (so transposes, head
+// splits and row strides are strides) and a two-level batch z = z1 * nb2 +
+// z2 whose offsets are z1 * s1 + z2 * s2 per operand. 64 x 64 output tiles,
+// 4 waves of 32 x 32 (fp32 MFMA 16x16x4); K in steps of 16 staged through
+// LDS, loaded along whichever of an operand's two strides is 1; elements
+// past M, N or K read 0.
+struct GemmF32Gen {
+    const float* A; const float* B; const float* C; float* Y;
+    int M, N, K, nb2;
+    long long sam, sak, as1, as2;   // A(m, k) = A[m * sam + k * sak]
+    long long sbk, sbn, bs1, bs2;   // B(k, n) = B[k * sbk + n * sbn]
+    long long ldy, ys1, ys2;        // Y[m * ldy + n]
+    float alpha, beta;
+    int c_mode;                     // 0 none, 1 scalar, 2 per column, 3 [M][N], 4 per row
+};
+
+__global__ __launch_bounds__(256) void gemm_f32_gen_kernel(GemmF32Gen p) {
+    __shared__ float As[16][64 + 1], Bs[16][64 + 1];   // [k][m], [k][n]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lr = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const long long z = blockIdx.z, z1 = z / p.nb2, z2 = z - z1 * p.nb2;
+    const float* A = p.A + z1 * p.as1 + z2 * p.as2;
+    const float* B = p.B + z1 * p.bs1 + z2 * p.bs2;
+    // element (r, c) of a 64 x 16 operand tile for thread slot e: along k
+    // when the k stride is 1, else along m / n
+    const bool a_k1 = p.sak == 1, b_k1 = p.sbk == 1;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < p.K; k0 += 16) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = tid + 256 * e;
+            const int r = a_k1 ? i >> 4 : i & 63, c = a_k1 ? i & 15 : i >> 6;   // r: m, c: k
+            const int m = m0 + r, k = k0 + c;
+            As[c][r] = (m < p.M && k < p.K) ? A[(long long)m * p.sam + (long long)k * p.sak] : 0.0f;
+            const int rn = b_k1 ? i >> 4 : i & 63, ck = b_k1 ? i & 15 : i >> 6;  // rn: n, ck: k
+            const int n = n0 + rn, kb = k0 + ck;
+            Bs[ck][rn] = (n < p.N && kb < p.K) ? B[(long long)kb * p.sbk + (long long)n * p.sbn] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int k = 4 * st + g;
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(As[k][wm * 32 + 16 * mt + lr],
+                                                                       Bs[k][wn * 32 + 16 * nt + lr], acc[mt][nt],
+                                                                       0, 0, 0);
+        }
+        __syncthreads();
+    }
+    float* Y = p.Y + z1 * p.ys1 + z2 * p.ys2;
+    // acc[mt][nt][i] = Y[m0 + 32 wm + 16 mt + 4 g + i][n0 + 32 wn + 16 nt + lr]
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + 32 * wm + 16 * mt + 4 * g + i, n = n0 + 32 * wn + 16 * nt + lr;
+                if (m >= p.M || n >= p.N) continue;
+                float v = p.alpha * acc[mt][nt][i];
+                if (p.c_mode != 0 && p.beta != 0.0f) {
+                    const float cb = p.c_mode == 1 ? p.C[0]
+                                     : p.c_mode == 2 ? p.C[n]
+                                     : p.c_mode == 3 ? p.C[(long long)m * p.N + n]
+                                                     : p.C[m];
+                    v = v + p.beta * cb;
+                }
+                Y[(long long)m * p.ldy + n] = v;
+            }
+}
+
+hipError_t launch_gemm_f32_gen(const GemmF32Gen& p, long long batch, hipStream_t s) {
+    if (p.M <= 0 || p.N <= 0 || batch <= 0) return hipSuccess;
+    if (p.nb2 <= 0 || batch > 65535 || (p.M + 63) / 64 > 65535) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((p.N + 63) / 64), (unsigned)((p.M + 63) / 64), (unsigned)batch);
+    hipLaunchKernelGGL(gemm_f32_gen_kernel, grid, dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_f32_batched(const float* A, const float* B, const float* C, float* Y, int M,
                                    int N, int K, int transA, int transB, float alpha, float beta,
                                    int c_mode, int batch, long long a_bstride, long long b_bstride,
@@ -289,30 +344,16 @@ hipError_t launch_gemm_f32_batched(const float* A, const float* B, const float* 
                                c_mode);
         return hipGetLastError();
     }
-    rocblas_handle h = blas_handle();
-    if (!h || rocblas_set_stream(h, s) != rocblas_status_success) return hipErrorNotInitialized;
-    float beta_eff = 0.0f;
-    if (c_mode != 0 && beta != 0.0f) {
-        long long n = (long long)M * N;
-        long long blocks = (n + 255) / 256;
-        if (blocks > 4096) blocks = 4096;
-        hipLaunchKernelGGL(bcast_c_kernel, dim3((unsigned)blocks, batch), dim3(256), 0, s, C, Y, M, N,
-                           c_mode, y_bstride);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        beta_eff = beta;
-    }
-    const rocblas_operation opB = transB ? rocblas_operation_transpose : rocblas_operation_none;
-    const rocblas_operation opA = transA ? rocblas_operation_transpose : rocblas_operation_none;
-    const int ldb = transB ? K : N;
-    const int lda = transA ? M : K;
-    rocblas_status st;
-    if (batch == 1)
-        st = rocblas_sgemm(h, opB, opA, N, M, K, &alpha, B, ldb, A, lda, &beta_eff, Y, N);
-    else
-        st = rocblas_sgemm_strided_batched(h, opB, opA, N, M, K, &alpha, B, ldb, b_bstride, A, lda,
-                                           a_bstride, &beta_eff, Y, N, y_bstride, batch);
-    return st == rocblas_status_success ? hipSuccess : hipErrorLaunchFailure;
+    // every other shape: the general kernel (A [M][K] or, transposed,
+    // [K][M]; B [K][N] or [N][K])
+    GemmF32Gen p{};
+    p.A = A; p.B = B; p.C = C; p.Y = Y;
+    p.M = M; p.N = N; p.K = K; p.nb2 = 1;
+    p.sam = transA ? 1 : K; p.sak = transA ? M : 1; p.as1 = a_bstride;
+    p.sbk = transB ? 1 : N; p.sbn = transB ? K : 1; p.bs1 = b_bstride;
+    p.ldy = N; p.ys1 = y_bstride;
+    p.alpha = alpha; p.beta = beta; p.c_mode = c_mode;
+    return launch_gemm_f32_gen(p, batch, s);
 }
 
 hipError_t launch_gemm_f32(const float* A, const float* B, const float* C, float* Y, int M, int N,
@@ -680,25 +721,9 @@ hipError_t launch_transpose_f32(const float* x, float* y, int ndim, const int* i
 // semantics, src/backend/cpu/MultiHeadAttention.cpp): per (b, h) the head's
 // rows are read in place (row stride H*hd), scores = Q K^T into a [B][H][S][S]
 // workspace, P = softmax(scale * scores) over the key axis, then P V is
-// written straight into the output's head columns. Two pointer-array batched
-// GEMMs; no transposes are materialized.
-__global__ __launch_bounds__(256) void mha_ptrs_kernel(const float* q, const float* k, const float* v, float* y,
-                                                       float* scores, const float** A1, const float** B1,
-                                                       float** C1, const float** A2, const float** B2,
-                                                       float** C2, int B, int S, int Hd, int nh) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= B * nh) return;
-    const int b = i / nh, h = i - b * nh, hd = Hd / nh;
-    const long long off = (long long)b * S * Hd + (long long)h * hd;
-    float* sc = scores + (long long)i * S * S;
-    A1[i] = k + off; B1[i] = q + off; C1[i] = sc;
-    A2[i] = v + off; B2[i] = sc; C2[i] = y + off;
-}
-
-size_t mha_workspace_bytes(int B, int S, int nh) {
-    const size_t nptr = (size_t)B * nh;
-    return ((6 * nptr * sizeof(void*) + 255) & ~(size_t)255) + sizeof(float) * nptr * S * S;
-}
+// written straight into the output's head columns: two strided GEMMs over a
+// (batch, head) grid; no transposes are materialized.
+size_t mha_workspace_bytes(int B, int S, int nh) { return sizeof(float) * (size_t)B * nh * S * S; }
 
 // ---------------------------------------------------------------------------
 // Fused attention for head size 64 and S <= 128: one block per (batch, head),
@@ -876,35 +901,28 @@ hipError_t launch_mha_f32(const float* q, const float* k, const float* v, float*
         return hipGetLastError();
     }
     if (parts) return hipErrorInvalidValue;   // only the fused kernel writes min / max pairs
-    const int hd = Hd / nh, nb = B * nh;
-    const float** A1 = (const float**)ws;
-    const float** B1 = A1 + nb;
-    float** C1 = (float**)(B1 + nb);
-    const float** A2 = (const float**)(C1 + nb);
-    const float** B2 = A2 + nb;
-    float** C2 = (float**)(B2 + nb);
-    float* scores = (float*)((char*)ws + ((6 * (size_t)nb * sizeof(void*) + 255) & ~(size_t)255));
-    hipLaunchKernelGGL(mha_ptrs_kernel, dim3((nb + 255) / 256), dim3(256), 0, s, q, k, v, y, scores, A1, B1, C1,
-                       A2, B2, C2, B, S, Hd, nh);
-    hipError_t e = hipGetLastError();
+    // scores = Q_h K_h^T per (batch, head), the scaled softmax, then P V_h,
+    // with the heads read and written in place through strides
+    const int hd = Hd / nh;
+    float* scores = (float*)ws;
+    GemmF32Gen p{};
+    p.M = S; p.N = S; p.K = hd; p.nb2 = nh; p.alpha = 1.0f;
+    p.A = q; p.sam = Hd; p.sak = 1; p.as1 = (long long)S * Hd; p.as2 = hd;
+    p.B = k; p.sbk = 1; p.sbn = Hd; p.bs1 = (long long)S * Hd; p.bs2 = hd;
+    p.Y = scores; p.ldy = S; p.ys1 = (long long)nh * S * S; p.ys2 = (long long)S * S;
+    hipError_t e = launch_gemm_f32_gen(p, (long long)B * nh, s);
     if (e != hipSuccess) return e;
-    rocblas_handle h = blas_handle();
-    if (!h || rocblas_set_stream(h, s) != rocblas_status_success) return hipErrorNotInitialized;
-    const float one = 1.0f, zero = 0.0f;
-    // column-major: scores^T[S x S] = K_h^T-as-stored... i.e. (K rows) . (Q rows)^T:
-    // C1 (ld S) = op(A1 = K, D x S col-major, ld Hd)^T * (B1 = Q, D x S, ld Hd)
-    rocblas_status st = rocblas_sgemm_batched(h, rocblas_operation_transpose, rocblas_operation_none, S, S, hd,
-                                              &one, A1, Hd, B1, Hd, &zero, C1, S, nb);
-    if (st != rocblas_status_success) return hipErrorLaunchFailure;
-    const long long rows = (long long)nb * S;
+    const long long rows = (long long)B * nh * S;
     hipLaunchKernelGGL(softmax_scaled_f32_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, scores,
                        scores, rows, S, scale);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // ctx^T (hd x S, ld Hd) = V^T-as-stored (hd x S, ld Hd) * P^T-as-stored (S x S, ld S)
-    st = rocblas_sgemm_batched(h, rocblas_operation_none, rocblas_operation_none, hd, S, S, &one, A2, Hd, B2, S,
-                               &zero, C2, Hd, nb);
-    return st == rocblas_status_success ? hipSuccess : hipErrorLaunchFailure;
+    GemmF32Gen o{};
+    o.M = S; o.N = hd; o.K = S; o.nb2 = nh; o.alpha = 1.0f;
+    o.A = scores; o.sam = S; o.sak = 1; o.as1 = (long long)nh * S * S; o.as2 = (long long)S * S;
+    o.B = v; o.sbk = Hd; o.sbn = 1; o.bs1 = (long long)S * Hd; o.bs2 = hd;
+    o.Y = y; o.ldy = Hd; o.ys1 = (long long)S * Hd; o.ys2 = hd;
+    return launch_gemm_f32_gen(o, (long long)B * nh, s);
 }
 
 }  // namespace nnrh

@@ -493,12 +493,13 @@ def test_maxpool(dev, C, k, st, pad):
 
 
 # ---------------------------------------------------------------------------
-# fp32 glue: Gemm (rocBLAS) with every broadcast mode and transpose, against
-# float64 numpy; the reference's float tolerance (tensor_equal, 1e-3 abs)
+# fp32 glue: Gemm with every broadcast mode and transpose, against float64
+# numpy; the reference's float tolerance (tensor_equal, 1e-3 abs)
 
-@pytest.mark.parametrize("M,N,K", [(37, 70, 300),     # rocBLAS (K % 64 != 0)
-                                   (37, 70, 320),     # the MFMA kernel: 5 K chunks over 4 waves
+@pytest.mark.parametrize("M,N,K", [(37, 70, 300),     # the general strided kernel (K % 64 != 0)
+                                   (37, 70, 320),     # the small-GEMM kernel: 5 K chunks over 4 waves
                                    (5, 3, 64),        # one chunk, clamped rows / columns
+                                   (600, 1030, 77),   # general kernel, many tiles, ragged M / N / K
                                    (256, 1000, 2048)])  # ResNet-50's classifier
 @pytest.mark.parametrize("ta,tb,c_mode", [(0, 1, 2), (0, 0, 0), (1, 0, 1), (1, 1, 3), (0, 1, 4)])
 def test_gemm_f32(dev, ta, tb, c_mode, M, N, K):
@@ -519,6 +520,29 @@ def test_gemm_f32(dev, ta, tb, c_mode, M, N, K):
     Ad, Bd, Cd = to_dev(A, dev), to_dev(B, dev), to_dev(Cb, dev)
     _lib.check(_lib.lib().nnrh_gemm_f32(_lib.ptr(Ad), _lib.ptr(Bd), _lib.ptr(Cd), _lib.ptr(y),
                                         M, N, K, ta, tb, alpha, beta, c_mode, _lib.cur_stream()))
+    np.testing.assert_allclose(to_np(y), ref, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("ta,tb,shared", [(0, 0, False), (1, 0, True), (0, 1, False), (1, 1, True)])
+def test_gemm_f32_batched(dev, ta, tb, shared):
+    """Batched MatMul on the general strided kernel: per-batch A, B per batch
+    or shared, every transpose, a per-column C, against float64 numpy."""
+    import torch
+    from nnr_amd import _lib
+    rng = np.random.default_rng(ta * 2 + tb + 7 * shared)
+    nb, M, N, K = 5, 45, 67, 83
+    A = rng.standard_normal((nb, K, M) if ta else (nb, M, K)).astype(np.float32) * 0.1
+    Bs = (K, N) if not tb else (N, K)
+    B = rng.standard_normal(Bs if shared else (nb,) + Bs).astype(np.float32) * 0.1
+    Cb = rng.standard_normal(N).astype(np.float32)
+    opA = np.swapaxes(A, -1, -2) if ta else A
+    opB = np.swapaxes(B, -1, -2) if tb else B
+    ref = 0.5 * np.matmul(opA.astype(np.float64), opB.astype(np.float64)) + 2.0 * Cb.astype(np.float64)
+    y = torch.empty((nb, M, N), dtype=torch.float32, device=dev)
+    Ad, Bd, Cd = to_dev(A, dev), to_dev(B, dev), to_dev(Cb, dev)
+    _lib.check(_lib.lib().nnrh_gemm_f32_batched(_lib.ptr(Ad), _lib.ptr(Bd), _lib.ptr(Cd), _lib.ptr(y), M, N, K, ta,
+                                                tb, 0.5, 2.0, 2, nb, M * K, 0 if shared else K * N, M * N,
+                                                _lib.cur_stream()))
     np.testing.assert_allclose(to_np(y), ref, atol=1e-3, rtol=1e-4)
 
 
@@ -897,7 +921,7 @@ def test_qconv1d(dev, case):
 
 
 @pytest.mark.parametrize("B,S,hidden,heads,scale", [
-    (3, 37, 96, 4, 0.2),          # head size 24: batched rocBLAS GEMMs + scaled softmax
+    (3, 37, 96, 4, 0.2),          # head size 24: two strided GEMMs + scaled softmax
     (2, 160, 128, 2, 0.1),        # S > 128: the same
     (2, 128, 768, 12, 0.125),     # head size 64, S <= 128: the fused kernel
     (3, 50, 128, 2, 0.3),         # fused, padded key rows and idle waves
@@ -906,8 +930,9 @@ def test_qconv1d(dev, case):
 ])
 def test_multihead_attention_f32(dev, B, S, hidden, heads, scale):
     """MultiHeadAttention (heads read and written in place; the fused fp32
-    MFMA kernel for head size 64 and S <= 128, batched rocBLAS GEMMs and a
-    scaled softmax otherwise) against float64 numpy."""
+    MFMA kernel for head size 64 and S <= 128, two strided fp32 MFMA GEMMs
+    over a (batch, head) grid and a scaled softmax otherwise) against float64
+    numpy."""
     import torch
     from nnr_amd import _lib
     import ctypes as C
