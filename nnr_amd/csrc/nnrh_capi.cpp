@@ -608,7 +608,13 @@ extern "C" int nnrh_qconv_create(nnrh_qconv_t* out, const nnrh_qconv_desc* d) {
         // channel counts that are not a multiple of 16: the kernel reads a
         // copy padded with x_zp to the next multiple of 16 (zero weights
         // there, so the accumulators are unchanged) and keeps 16-byte loads
-        const bool cpad = !first && G == 1 && Cg % 16 != 0;
+        // (not for a 1x1 stride-1 NHWC conv with C % 8 == 0 and C <= 64: the
+        // short-K direct kernel reads its rows in 8-byte pieces as they are)
+        const bool dense1x1 = d->kH == 1 && d->kW == 1 && d->sH == 1 && d->sW == 1 && d->pad_t == 0 &&
+                              d->pad_l == 0 && d->pad_b == 0 && d->pad_r == 0 && d->oH == d->H && d->oW == d->W;
+        const bool direct_rows = dense1x1 && d->x_nhwc && Cg % 8 == 0 && Cg <= 64 &&
+                                 (br == NNRH_BR_PACKED || br == NNRH_BR_NR16);
+        const bool cpad = !first && G == 1 && Cg % 16 != 0 && !direct_rows;
         const int Cgp = first ? 4 : (cpad ? round_up(Cg, 16) : Cg);
         const int kWp = first ? round_up(d->kW, 4) : d->kW;   // first layer: taps padded to 4
         const int K = d->kH * kWp * Cgp;

@@ -65,8 +65,9 @@ B256_VARIANTS = {
     "resnet50": ("variant:dma<256,128,3,",        # 8-wave 256x128 tiles
                  "variant:dma<256,64,2,3,",       # 2-stage 256x64 uniform-tap conv tiles
                  ",128,0,2>",                     # K split over two waves a sub-tile
-                 ",64,1,1>"),                     # weights in registers (fused add, K = 64)
-    "mobilenetv2": ("variant:dma<256,64,",),
+                 ",64,1,1>",                      # weights in registers (fused add, K = 64)
+                 "variant:direct"),               # the short-K direct kernel (K = 64, no add)
+    "mobilenetv2": ("variant:dma<256,64,", "variant:direct"),
 }
 
 

@@ -181,6 +181,13 @@ CONV_CASES = [
     ("nchw16_c64", 3, 64, 16, 16, 32, 1, dict(y_nhwc=1, x_zp=200)),
     ("packed_dil", 1, 16, 12, 12, 32, 3, dict(pads=(2, 2, 2, 2), dil=(2, 2), y_nhwc=1)),
     ("packed_c24", 2, 24, 10, 10, 144, 1, dict(y_nhwc=1, x_nhwc=1)),
+    # the short-K direct kernel: 1x1 NHWC with one 64-byte K step, rows read
+    # unpadded in 8-byte pieces (C = 24, 40) or 16-byte chunks (C = 16, 64);
+    # ragged column blocks, zero point 0 (saturating store) and odd
+    ("direct_c24", 3, 24, 19, 21, 144, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=3)),
+    ("direct_c40_oc72", 2, 40, 13, 17, 72, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=0, post_fn=1)),
+    ("direct_c16_oc96", 4, 16, 24, 24, 96, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=128)),
+    ("direct_c64_oc16", 2, 64, 30, 30, 16, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=7)),
     ("direct", 2, 64, 12, 12, 64, 3, dict(pads=(1, 1, 1, 1), y_nhwc=0, post_fn=1, y_zp=9)),
     ("direct_tail", 1, 20, 9, 7, 30, 3, dict(pads=(1, 1, 1, 1), y_nhwc=0, y_zp=20)),
     ("first_nhwc", 2, 3, 40, 40, 64, 7, dict(stride=(2, 2), pads=(3, 3, 3, 3), y_nhwc=1)),
