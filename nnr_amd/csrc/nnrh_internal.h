@@ -170,9 +170,8 @@ hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec,
 // pipelined direct-to-LDS variant (nnrh_qgemm_dma.hip) and its eligibility
 bool qgemm_dma_eligible(const GemmArgs& g, int vec);
 hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t s);
-// barrier-free short-K kernel (nnrh_qgemm_dma.hip): dense A, Kp <= 128, RQ-B
+// barrier-free short-K kernel (nnrh_qgemm_dma.hip): dense A, Kp = 64, RQ-B
 bool qgemm_direct_eligible(const GemmArgs& g, int batch);
-bool qgemm_direct_preferred(const GemmArgs& g, int batch);
 hipError_t launch_qgemm_direct(const GemmArgs& g, hipStream_t s);
 
 // ---- first convolution with the input quantize fused (nnrh_stem.hip) ----

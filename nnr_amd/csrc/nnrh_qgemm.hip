@@ -528,7 +528,7 @@ hipError_t launch_qgemm(const GemmArgs& g, int batch, int tile, int vec, hipStre
     if (g.Kp <= 0 || (g.Kp & 63) || g.Kp < g.K) return hipErrorInvalidValue;
     if (g.a == nullptr || g.b == nullptr || g.y == nullptr) return hipErrorInvalidValue;
     const bool conv = (g.H > 0);
-    if (qgemm_direct_preferred(g, batch)) return launch_qgemm_direct(g, s);
+    if (qgemm_direct_eligible(g, batch)) return launch_qgemm_direct(g, s);
     if (qgemm_dma_eligible(g, vec)) return launch_qgemm_dma(g, batch, tile, s);
     if (g.add_other || g.dq_bias) return hipErrorNotSupported;   // fusions: pipelined kernel only
     prof_count("variant:qgemm_reg");

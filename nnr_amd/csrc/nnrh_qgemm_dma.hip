@@ -1016,9 +1016,9 @@ void qgemm_dma_kernel(GemmArgs g) {
     __builtin_amdgcn_s_waitcnt(NNRH_VMCNT(0));
 }
 
-// Dense GEMMs with a short K (Kp <= 128: one or two 64-byte MFMA K steps)
-// and the RQ-B epilogue, optionally with the fused QLinearAdd: the
-// pointwise convolutions at the start of ResNet-50 and MobileNetV2. There is
+// Dense GEMMs with a short K (KS 64-byte MFMA K steps, KS = 1 launched)
+// and the RQ-B epilogue: the pointwise convolutions of MobileNetV2 with
+// C <= 64 and the first of ResNet-50. There is
 // little to stage: each wave keeps the weight fragments and per-column
 // constants of one 64-column block in registers and walks 64-row tiles of
 // A on its own -- fragments loaded straight from global memory (one tile
@@ -1026,7 +1026,7 @@ void qgemm_dma_kernel(GemmArgs g) {
 // and no barrier. A row whose K is not a multiple of 16 (24 channels) is
 // read in 8-byte pieces up to K; the rest of its last chunk is 0, which
 // meets zero weight columns.
-template <int KS, int FUSE>
+template <int KS>
 __global__ __launch_bounds__(256, 2) void qgemm_direct_kernel(GemmArgs g) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int frow = lane & 15, fchunk = lane >> 4;
@@ -1081,8 +1081,6 @@ __global__ __launch_bounds__(256, 2) void qgemm_direct_kernel(GemmArgs g) {
             }
     };
     const bool sat_u8 = g.y_type == 0 && g.lo == 0 && g.hi == 255 && g.y_zp == 0;
-    const float lo_f = (float)g.lo - (float)g.y_zp, hi_f = (float)g.hi - (float)g.y_zp;
-    const float zp_f = (float)g.y_zp;
     const bool full16 = nb + 16 <= g.N;
     v4i xa[KS][4], xb[KS][4];
     load(rt, xa);
@@ -1108,70 +1106,23 @@ __global__ __launch_bounds__(256, 2) void qgemm_direct_kernel(GemmArgs g) {
                 if (m >= g.M) continue;
                 uint8_t* yrow = (uint8_t*)g.y + (long long)m * g.ldy + nb;
                 uint32_t packed[4];
-                bool done = false;
-                if constexpr (FUSE == FUSE_ADD) {
-                    const long long i0 = (long long)m * g.ldy + nb;
-                    const uint8_t* rp = g.add_other + i0;
-                    const v4i rres = full16 ? *(const v4i*)rp : v4i{0, 0, 0, 0};
-                    if (full16 && i0 + 16 <= g.add_body) {
-                        // RQ-B into RQ-E's body as a float (see the pipelined kernel)
+                if (sat_u8) {
 #pragma unroll
-                        for (int tn = 0; tn < 4; ++tn) {
-                            const uint32_t rw = (uint32_t)rres[tn];
-                            uint32_t w = 0;
+                    for (int tn = 0; tn < 4; ++tn) {
+                        uint32_t w = 0;
 #pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                const float f = (float)acc[tm][tn][q] * osv[4 * tn + q];
-                                const float qf = __builtin_rintf(med3f(f, lo_f, hi_f)) + zp_f;
-                                const float rf = (float)((rw >> (8 * q)) & 0xffu);
-                                float v = __builtin_fmaf(g.add_conv_is_a ? rf : qf, g.add_sb, g.add_fixed);
-                                v = __builtin_fmaf(g.add_conv_is_a ? qf : rf, g.add_sa, v);
-                                w = __builtin_amdgcn_cvt_pk_u8_f32(v, q, w);
-                            }
-                            packed[tn] = w;
-                        }
-                        done = true;
+                        for (int q = 0; q < 4; ++q)
+                            w = __builtin_amdgcn_cvt_pk_u8_f32((float)acc[tm][tn][q] * osv[4 * tn + q], q, w);
+                        packed[tn] = w;
                     }
-                }
-                if (!done) {
-                    if (sat_u8) {
+                } else {
 #pragma unroll
-                        for (int tn = 0; tn < 4; ++tn) {
-                            uint32_t w = 0;
+                    for (int tn = 0; tn < 4; ++tn) {
+                        uint32_t b[4];
 #pragma unroll
-                            for (int q = 0; q < 4; ++q)
-                                w = __builtin_amdgcn_cvt_pk_u8_f32((float)acc[tm][tn][q] * osv[4 * tn + q], q, w);
-                            packed[tn] = w;
-                        }
-                    } else {
-#pragma unroll
-                        for (int tn = 0; tn < 4; ++tn) {
-                            uint32_t b[4];
-#pragma unroll
-                            for (int q = 0; q < 4; ++q)
-                                b[q] = rqb_fast(acc[tm][tn][q], osv[4 * tn + q], g.y_zp, g.lo, g.hi);
-                            packed[tn] = pack_low_bytes(b[0], b[1], b[2], b[3]);
-                        }
-                    }
-                    if constexpr (FUSE == FUSE_ADD) {
-                        // the row segment reaches the scalar tail, or the row's
-                        // last columns: element by element
-                        const long long i0 = (long long)m * g.ldy + nb;
-#pragma unroll
-                        for (int tn = 0; tn < 4; ++tn) {
-                            uint32_t w = 0;
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                const int i = 4 * tn + q;
-                                if (nb + i >= g.N) continue;
-                                const int qc = (int)((packed[tn] >> (8 * q)) & 0xffu);
-                                const int rv = (int)g.add_other[i0 + i];
-                                const int a = g.add_conv_is_a ? qc : rv;
-                                const int bb = g.add_conv_is_a ? rv : qc;
-                                w |= (uint32_t)(qadd_elem(a, bb, g, i0 + i >= g.add_body) & 0xff) << (8 * q);
-                            }
-                            packed[tn] = w;
-                        }
+                        for (int q = 0; q < 4; ++q)
+                            b[q] = rqb_fast(acc[tm][tn][q], osv[4 * tn + q], g.y_zp, g.lo, g.hi);
+                        packed[tn] = pack_low_bytes(b[0], b[1], b[2], b[3]);
                     }
                 }
                 if (full16) {
@@ -1381,11 +1332,15 @@ static bool conv_uniform_taps(const GemmArgs& g) {
 }
 
 // the short-K direct kernel's shapes: dense A (K % 8 == 0, rows 8-byte
-// aligned; 16-byte when K % 16 == 0), Kp <= 128, RQ-B with its constants
-// precomputed, uint8 / int8 row-major output with 16-byte aligned rows,
-// optionally the fused QLinearAdd; batch 1
+// aligned; 16-byte when K % 16 == 0) with one K step (Kp = 64), RQ-B with
+// its constants precomputed, uint8 / int8 row-major output with 16-byte
+// aligned rows, no fusion; batch 1. There it is faster than the pipelined
+// kernel (measured per layer on ResNet-50 and MobileNetV2); with Kp = 128
+// the pipelined kernel wins, and so does its fused-add variant with the
+// weights in registers (a version of this kernel with the residual loaded
+// one tile ahead ran ResNet-50's stage-1 conv + add layers 95 -> 121 us).
 bool qgemm_direct_eligible(const GemmArgs& g, int batch) {
-    if (batch != 1 || g.H > 0 || g.kWp > 0 || g.Kp > 128 || g.K <= 0 || (g.K & 7)) return false;
+    if (batch != 1 || g.H > 0 || g.kWp > 0 || g.Kp != 64 || g.K <= 0 || (g.K & 7)) return false;
     if (g.epi != EPI_RQB || !g.c0 || !g.os || g.rowsum || g.alpha_zp_dev || g.row_coef || g.dq_bias) return false;
     if (g.tail != TAIL_NONE || g.bprime_from < g.N || g.y_nchw || g.y_type > 1) return false;
     if (g.Np < ((g.N + 63) & ~63)) return false;
@@ -1393,28 +1348,22 @@ bool qgemm_direct_eligible(const GemmArgs& g, int batch) {
     if ((g.lda & 7) || (a & 7)) return false;
     if ((g.K & 15) == 0 && ((g.lda & 15) || (a & 15))) return false;
     if ((g.ldy & 15) || (y & 15)) return false;
-    if (g.add_other && (((uintptr_t)g.add_other & 15) || g.y_type != 0)) return false;
+    if (g.add_other) return false;
     return g.M > 0 && g.N > 0;
-}
-
-// where it is faster than the pipelined kernel (measured per layer on
-// ResNet-50 and MobileNetV2): one K step and no fused add. With Kp = 128 or a
-// fused add (whose LDS-staged variant keeps the weights in registers too)
-// the pipelined kernel wins.
-bool qgemm_direct_preferred(const GemmArgs& g, int batch) {
-    return g.Kp == 64 && !g.add_other && qgemm_direct_eligible(g, batch);
 }
 
 hipError_t launch_qgemm_direct(const GemmArgs& g, hipStream_t s) {
     auto go = [&](auto kern) {
-        static int per_cu = 0;
-        if (per_cu <= 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) != hipSuccess ||
-                            per_cu < 1))
-            per_cu = 1;
-        int dev = 0, cus = 256;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-            cus = 256;
+        // resident blocks of this instantiation, computed once
+        static int per_cu = 0, cus = 0;
+        if (per_cu <= 0) {
+            int dev = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) != hipSuccess || per_cu < 1)
+                per_cu = 1;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+                cus = 256;
+        }
         const long long nbn = (g.N + 63) / 64, nrt = (g.M + 63) / 64;
         // waves: a multiple of the column blocks, at most the resident ones
         // and at most one per (row tile, column block)
@@ -1427,11 +1376,8 @@ hipError_t launch_qgemm_direct(const GemmArgs& g, hipStream_t s) {
         hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, g);
         return hipGetLastError();
     };
-    if (prof_enabled())
-        prof_count(g.add_other ? "variant:direct_add" : "variant:direct");
-    const bool two = g.Kp > 64;
-    if (g.add_other) return two ? go(qgemm_direct_kernel<2, FUSE_ADD>) : go(qgemm_direct_kernel<1, FUSE_ADD>);
-    return two ? go(qgemm_direct_kernel<2, FUSE_NONE>) : go(qgemm_direct_kernel<1, FUSE_NONE>);
+    if (prof_enabled()) prof_count("variant:direct");
+    return go(qgemm_direct_kernel<1>);
 }
 
 hipError_t launch_qgemm_dma(const GemmArgs& g, int batch, int tile, hipStream_t s) {
