@@ -502,7 +502,7 @@ def run_model(args, dev, model):
             copies_ms += kprof[k][1] / args.steps
     is_conv = lambda r: r["op"] == "QLinearConv" and r["variant"] != "DW"
     rl, fam_ms = family_roofline(rows, is_conv, kprof, extra_ms=copies_ms)
-    rl["kernel"] = "qgemm_dma_kernel (conv GEMM family)"
+    rl["kernel"] = "qgemm_dma_kernel / qgemm_direct_kernel / stem_conv_kernel (conv GEMM family)"
     rl["traffic"], rl["traffic_source"] = measured_traffic(
         f"{model}_b256_conv_gemm_traffic.md" if B == 256 else None)
     rl["counters"] = measured_counters(f"{model}_b256_conv_gemm_counters.md") if B == 256 else None
