@@ -272,6 +272,12 @@ CONV_CASES = [
     ("dw3_s2_int8_c32", 2, 32, 15, 21, 32, 3, dict(group=32, stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1,
                                                     x_nhwc=1, act_dtype=np.int8, x_zp=-7, y_zp=3)),
     ("dw3_s1_c384_b16", 16, 384, 14, 14, 384, 3, dict(group=384, pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1)),
+    # ten 8-channel chunks, an odd output zero point; stride 2 onto 7 x 7 maps
+    # of five images with a fused Relu
+    ("dw3_c80_yzp128", 2, 80, 9, 9, 80, 3, dict(group=80, pads=(1, 1, 1, 1), y_nhwc=1, x_nhwc=1,
+                                              x_zp=3, y_zp=128)),
+    ("dw3_s2_c96_b5", 5, 96, 14, 14, 96, 3, dict(group=96, stride=(2, 2), pads=(1, 1, 1, 1), y_nhwc=1,
+                                                   x_nhwc=1, y_zp=5, post_fn=1)),
     # channel counts off the 16-byte grid run on an x_zp-padded copy
     ("cpad_c8_3x3", 2, 8, 10, 11, 40, 3, dict(pads=(1, 1, 1, 1), x_nhwc=1, y_nhwc=1, y_zp=9)),
     ("cpad_c24_wzp", 1, 24, 7, 9, 32, 1, dict(x_nhwc=1, y_nhwc=1, w_zp=(5,), y_zp=2)),
