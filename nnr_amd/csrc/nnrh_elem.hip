@@ -160,6 +160,22 @@ __device__ __forceinline__ void dyn_scale_block(const float* __restrict part, in
 __device__ __forceinline__ uint32_t dyn_q1(float v, float sc, int zp) {
     return (uint32_t)clampi(wrap_add(x86_f2i(__builtin_rintf(v / sc)), zp), 0, 255);
 }
+// dyn_q1's value, as a float for v_cvt_pk_u8_f32 (which saturates to
+// [0, 255]), without a division per element. q = fl(v * r) with
+// r = fl(1 / sc) differs from v / sc by at most |v / sc| * (2^-23 + 2^-48),
+// and the quotient fl(v / sc) by at most half an ulp, 2^-17 below 256: so
+// for |q| < 256, |q - fl(v / sc)| < 2^-14, and where q lies more than 2^-13
+// from every half-integer both round to the same integer k = rne(q), and
+// k + zp (exact) is the byte before the clamp. Elements near a half-integer
+// (about one in 2^11), |q| >= 256, NaN and infinities take the division.
+__device__ __forceinline__ float dyn_qf(float v, float r, float sc, int zp) {
+    const float q = v * r;
+    const float k = __builtin_rintf(q);
+    const float d = __builtin_fabsf(q - k);   // exact: q and k are within a factor 2 (or k = 0)
+    if (__builtin_expect(!(__builtin_fabsf(q) < 256.0f && __builtin_fabsf(d - 0.5f) > 0x1p-13f), 0))
+        return (float)dyn_q1(v, sc, zp);
+    return k + (float)zp;
+}
 // scale and zero point from producer-written (min, max) pairs, reduced by
 // every block of the quantize kernel (256 threads): every block gets the
 // same values, since min and max are exact in any order
@@ -224,13 +240,18 @@ __global__ __launch_bounds__(256) void dyn_quantize_kernel(const float* __restri
     const bool vec = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
     const long long n16 = vec ? n >> 4 : 0;
     const float4* x4 = (const float4*)x;
+    const float r = 1.0f / sc;
     for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += (long long)gridDim.x * 256) {
+        float4 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = x4[4 * i + q];
         uint32_t w[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float4 v = x4[4 * i + q];
-            w[q] = dyn_q1(v.x, sc, zp) | (dyn_q1(v.y, sc, zp) << 8) | (dyn_q1(v.z, sc, zp) << 16) |
-                   (dyn_q1(v.w, sc, zp) << 24);
+            uint32_t t = __builtin_amdgcn_cvt_pk_u8_f32(dyn_qf(v[q].x, r, sc, zp), 0, 0u);
+            t = __builtin_amdgcn_cvt_pk_u8_f32(dyn_qf(v[q].y, r, sc, zp), 1, t);
+            t = __builtin_amdgcn_cvt_pk_u8_f32(dyn_qf(v[q].z, r, sc, zp), 2, t);
+            w[q] = __builtin_amdgcn_cvt_pk_u8_f32(dyn_qf(v[q].w, r, sc, zp), 3, t);
         }
         *(uint4*)(y + 16 * i) = make_uint4(w[0], w[1], w[2], w[3]);
     }
