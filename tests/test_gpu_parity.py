@@ -391,6 +391,41 @@ def test_dynamic_quantize(dev, n):
     assert np.array_equal(to_np(y), y_ref)
 
 
+def dyn_quant_ties(n, seed):
+    """Data whose scale is exactly 2^-4 (min -4, max 11.9375: range 255 / 16)
+    with most values at or one ulp off a half-integer multiple of it, so
+    x / scale is an exact tie or within 2^-18 of one: the cases where
+    rounding a product by 1/scale instead of the quotient could differ,
+    beside ordinary values and a few with |x / scale| near 255."""
+    rng = np.random.default_rng(seed)
+    k = rng.integers(-64, 191, n).astype(np.float32)
+    x = ((k + 0.5) * np.float32(0.0625)).astype(np.float32)
+    step = rng.integers(-1, 2, n)
+    x = np.where(step < 0, np.nextafter(x, np.float32(-np.inf)), np.where(step > 0, np.nextafter(x, np.float32(np.inf)), x)).astype(np.float32)
+    plain = rng.random(n) < 0.25
+    x[plain] = rng.uniform(-4, 11.9375, plain.sum()).astype(np.float32)
+    x[:2] = (-4.0, 11.9375)
+    x[2:6] = (11.9375, np.nextafter(np.float32(11.9375), np.float32(0)), -4.0, np.float32(-3.96875))
+    return x
+
+
+@pytest.mark.parametrize("n", [4096, 70001])
+def test_dynamic_quantize_ties(dev, n):
+    """DynamicQuantizeLinear on exact and near ties of x / scale, both the
+    two-pass form and the one from producer pairs: bytes equal the oracle's
+    (the kernels take the division for elements near a half-integer)."""
+    x = dyn_quant_ties(n, n)
+    y_ref, s_ref, z_ref = O.dynamic_quantize_linear(x)
+    assert np.float32(s_ref) == np.float32(0.0625)
+    y, s, z = H.dynamic_quantize_linear(to_dev(x, dev))
+    assert to_np(s)[0] == np.float32(s_ref) and int(to_np(z)[0]) == z_ref
+    assert np.array_equal(to_np(y), y_ref)
+    pr = np.array([[x.min(), 0.0], [0.0, x.max()]], np.float32)
+    y2, s2, z2 = H.dynamic_quantize_linear_parts(to_dev(x, dev), to_dev(pr.reshape(-1), dev))
+    assert to_np(s2)[0] == np.float32(s_ref) and int(to_np(z2)[0]) == z_ref
+    assert np.array_equal(to_np(y2), y_ref)
+
+
 @pytest.mark.parametrize("kind", [0, 1, 2, 3])
 @pytest.mark.parametrize("y_nhwc", [0, 1])
 def test_qlinear_add(dev, kind, y_nhwc):
