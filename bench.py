@@ -29,6 +29,13 @@ inflated), and the dominant kernel family's average launch is placed under
 the roof its own algorithmic ops / bytes put it (MFMA or HBM), with each
 layer's roofline fraction beside it; the `cpu_baseline` leg times a CPU
 restatement on host cores on a bounded sample of the same workload.
+ResNet-50 and MobileNetV2 steps run the batch as --split slices (default 2)
+concurrently, one context and stream per slice (graph.SplitSession; their
+graph outputs are checked bit-identical to the whole-batch context's first);
+the parity gate, the per-layer table and the roofline come from the
+whole-batch context, whose own step time is in config.split. BERT's
+DynamicQuantizeLinear takes its scale from the whole batch, so its batch is
+not split.
 """
 from __future__ import annotations
 
@@ -449,6 +456,31 @@ WORKLOADS = {
 }
 
 
+def split_steps(args, make_graph, B, feeds, ref, outputs):
+    """The batch as args.split slices run concurrently (graph.SplitSession:
+    one context and stream per slice, one group step on the current stream).
+    Every image's computation is independent of the others' in these
+    graphs, so the graph outputs must equal the whole-batch context's bit
+    for bit; then the timed steps."""
+    import numpy as np
+    import torch
+    from nnr_amd import graph as G
+    ss = G.SplitSession(make_graph, batch=B, parts=args.split, memory_planning=bool(args.memory_planning))
+    try:
+        for k, v in feeds.items():
+            ss.set_input(k, v)
+        ss.run()
+        torch.cuda.synchronize()
+        for o in outputs:
+            assert np.array_equal(ss.output(o)[0], ref.output(o)[0]), f"split plan differs at {o}"
+        ms = time_steps(ss.run, args)
+        info = {"parts": args.split, "images_per_part": B // args.split, "hip_graph": ss.graph_active(),
+                "device_bytes": ss.device_bytes()}
+    finally:
+        ss.close()
+    return ms, info
+
+
 def run_model(args, dev, model):
     import numpy as np
     import torch
@@ -458,7 +490,8 @@ def run_model(args, dev, model):
     from oracle import pyoracle as O
 
     B = args.batch
-    g = {"resnet50": synth.resnet50, "mobilenetv2": synth.mobilenetv2}[model](batch=B, hw=224)
+    make_graph = lambda b: {"resnet50": synth.resnet50, "mobilenetv2": synth.mobilenetv2}[model](batch=b, hw=224)
+    g = make_graph(B)
     rng = np.random.default_rng(10)
     x = rng.random((B, 3, 224, 224), dtype=np.float32)
     s = G.Session(g)
@@ -486,6 +519,13 @@ def run_model(args, dev, model):
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
     mem["hip_graph"] = s.graph_active()
+    split = None
+    if args.split > 1 and not args.onnx and B % args.split == 0:
+        split_ms, split = split_steps(args, make_graph, B, {"input": x}, s, g.outputs)
+        split["one_context_ms_per_step"] = round(ms, 5)
+        split["one_context_value"] = round(B / (ms * 1e-3), 1)
+        parity += (f"; the batch as {args.split} concurrent slices gives the whole-batch context's "
+                   "graph outputs bit for bit")
     # per-kernel launch times (an event pair around every launch) and
     # per-node times (each node run back to back, no event between launches)
     kprof = profile_steps(s.run, args)
@@ -533,11 +573,12 @@ def run_model(args, dev, model):
     cpu_s, reps = timed_reps(lambda: graph_oracle.run_plan(plan, g, {"input": x[:ns]}, fmt), cpu_seconds(args), 100)
     cpu_done()
     cpu_img_s = ns / cpu_s
-    imgs = B / (ms * 1e-3)
+    step_ms = split_ms if split else ms
+    imgs = B / (step_ms * 1e-3)
     return dict(
         metric=METRIC if model == "resnet50" else "MobileNetV2-int8 images/sec b256 (cfg4), 1 GPU",
-        value=round(imgs, 1), unit="images/s", ms_per_step=ms,
-        config={"workload": WORKLOADS[model].format(B=B), "global_batch": B,
+        value=round(imgs, 1), unit="images/s", ms_per_step=step_ms,
+        config={"workload": WORKLOADS[model].format(B=B), "global_batch": B, "split": split,
                 "branches": {b: sum(1 for p in plan if p["variant"].split("+")[0] == b)
                              for b in ("FIRST", "DW", "NR16", "PACKED")},
                 "adds_fused_into_conv": s.fusion_stat("conv_add"),
@@ -922,6 +963,9 @@ def main():
                     help="bert: per-channel weights (DynamicQuantizeLinear -> MatMulInteger -> Cast -> Mul -> Add)")
     ap.add_argument("--memory-planning", type=int, default=1, choices=[0, 1],
                     help="graph configs: time a context whose intermediates share device memory")
+    ap.add_argument("--split", type=int, default=2,
+                    help="resnet50 / mobilenetv2: the batch as this many slices run concurrently, one "
+                         "context and stream each (1: one context for the whole batch)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",

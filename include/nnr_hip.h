@@ -60,6 +60,8 @@ int nnrh_device_synchronize(void);
 int nnrh_event_create(void** event);
 int nnrh_event_destroy(void* event);
 int nnrh_event_record(void* event, void* stream);
+/* work enqueued on `stream` after this call waits for `event`'s last record */
+int nnrh_stream_wait_event(void* stream, void* event);
 int nnrh_event_elapsed_ms(float* ms, void* start, void* stop);
 
 /* ---- whole-plan HIP graphs ----------------------------------------------

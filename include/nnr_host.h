@@ -68,6 +68,22 @@ int nnr_ctx_optimize(nnr_ctx_t ctx);
 int nnr_ctx_prepare(nnr_ctx_t ctx);
 int nnr_ctx_run(nnr_ctx_t ctx);
 
+/* Concurrent contexts (no counterpart in the reference, whose contexts run
+ * one at a time on the calling thread). A group runs n prepared contexts as
+ * one step: run() makes each context's stream wait for the work already
+ * enqueued on `stream`, runs every context on its own stream (a HIP graph
+ * replay once captured), and makes `stream` wait for all of them. With one
+ * context per slice of a batch (each built for batch / n, inputs and outputs
+ * its own), the slices' kernels share the GPU: one slice's short, latency-
+ * bound launches fill the CUs another slice's leave idle. Each context keeps
+ * its own results, identical to running it alone. The contexts must be
+ * distinct, each with its own non-null stream; a group does not own them
+ * (destroy the group first). */
+typedef struct nnr_group* nnr_group_t;
+int nnr_group_create(const nnr_ctx_t* ctxs, int n, nnr_group_t* group);
+int nnr_group_run(nnr_group_t group, void* stream);
+int nnr_group_destroy(nnr_group_t group);
+
 /* device pointer, dtype, dims and layout (0 NCHW, 1 NHWC) of a tensor */
 int nnr_ctx_tensor(nnr_ctx_t ctx, const char* name, void** data_dev, int* dtype, int* dims,
                    int* ndim, int* format);

@@ -23,6 +23,7 @@ EXPORTS = [
     "nnrh_malloc", "nnrh_free", "nnrh_memcpy", "nnrh_fill_u8", "nnrh_stream_create",
     "nnrh_stream_destroy", "nnrh_stream_synchronize", "nnrh_device_synchronize",
     "nnrh_event_create", "nnrh_event_destroy", "nnrh_event_record", "nnrh_event_elapsed_ms",
+    "nnrh_stream_wait_event",
     "nnrh_profile_enable", "nnrh_profile_reset", "nnrh_profile_count", "nnrh_profile_get",
     "nnrh_profile_enabled", "nnrh_graph_begin_capture", "nnrh_graph_end_capture", "nnrh_graph_launch",
     "nnrh_graph_destroy",
@@ -115,6 +116,7 @@ def lib():
         "nnrh_event_create": (i, [P(vp)]),
         "nnrh_event_destroy": (i, [vp]),
         "nnrh_event_record": (i, [vp, vp]),
+        "nnrh_stream_wait_event": (i, [vp, vp]),
         "nnrh_event_elapsed_ms": (i, [P(f), vp, vp]),
         "nnrh_profile_enable": (i, [i]),
         "nnrh_profile_enabled": (i, []),

@@ -232,6 +232,11 @@ int nnrh_event_record(void* ev, void* s) {
     HIP_TRY(hipEventRecord((hipEvent_t)ev, S(s)), "hipEventRecord");
     return NNRH_OK;
 }
+int nnrh_stream_wait_event(void* s, void* ev) {
+    if (!ev) return set_err(NNRH_ERR_INVALID, "event is NULL");
+    HIP_TRY(hipStreamWaitEvent(S(s), (hipEvent_t)ev, 0), "hipStreamWaitEvent");
+    return NNRH_OK;
+}
 int nnrh_event_elapsed_ms(float* ms, void* a, void* b) {
     if (!ms) return set_err(NNRH_ERR_INVALID, "ms is NULL");
     HIP_TRY(hipEventSynchronize((hipEvent_t)b), "hipEventSynchronize");

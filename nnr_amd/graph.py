@@ -56,6 +56,9 @@ def host_lib():
             "nnr_ctx_optimize": (i, [vp]),
             "nnr_ctx_prepare": (i, [vp]),
             "nnr_ctx_run": (i, [vp]),
+            "nnr_group_create": (i, [P(vp), i, P(vp)]),
+            "nnr_group_run": (i, [vp, vp]),
+            "nnr_group_destroy": (i, [vp]),
             "nnr_ctx_tensor": (i, [vp, cp, P(vp), P(i), P(i), P(i), P(i)]),
             "nnr_ctx_node_count": (i, [vp, P(i)]),
             "nnr_ctx_node_info": (i, [vp, i, P(cp), P(cp), P(cp), P(i), P(i), P(i)]),
@@ -178,6 +181,7 @@ class Session:
         self.h = h
         if stream is None and device:
             stream = _lib.cur_stream()
+        self.stream = stream
         _chk(L.nnr_ctx_set_stream(h, stream))
         _chk(L.nnr_ctx_set_fusion(h, 1 if fusion else 0))
         _chk(L.nnr_ctx_set_graph(h, 1 if hip_graph else 0))
@@ -229,6 +233,9 @@ class Session:
             nbytes = arr.numel() * arr.element_size()
             assert arr.is_contiguous() and arr.numel() == int(np.prod(shape))
             _lib.check(_lib.lib().nnrh_memcpy(p, arr.data_ptr(), nbytes, 2, _lib.cur_stream()))
+            if self.stream != _lib.cur_stream():
+                # the context runs on a stream of its own: the copy lands first
+                _lib.check(_lib.lib().nnrh_stream_synchronize(_lib.cur_stream()))
 
     def output(self, name):
         """numpy copy of a tensor in its physical layout, plus the layout flag
@@ -239,6 +246,8 @@ class Session:
             phys = (shape[0], shape[2], shape[3], shape[1])
         out = np.empty(phys, dtype=dt)
         _lib.check(_lib.lib().nnrh_stream_synchronize(_lib.cur_stream()))
+        if self.stream and self.stream != _lib.cur_stream():
+            _lib.check(_lib.lib().nnrh_stream_synchronize(self.stream))
         _lib.check(_lib.lib().nnrh_memcpy(out.ctypes.data, p, out.nbytes, 1, _lib.cur_stream()))
         return out, fmt
 
@@ -368,6 +377,81 @@ class Session:
             if getattr(self, "h", None):
                 self.L.nnr_ctx_destroy(self.h)
                 self.h = None
+        except Exception:
+            pass
+
+
+class SplitSession:
+    """A batch split into `parts` slices along axis 0, one prepared context
+    per slice (built for batch / parts), run concurrently as one step
+    (nnr_group_run): each context on a stream of its own, so one slice's
+    short, latency-bound launches fill the CUs the other slices leave idle.
+    Every slice's results are those of running it alone, and the plan is the
+    same for every slice. make_graph(batch) builds a slice's graph; or onnx=
+    (a file or bytes), loaded with the slice's batch as the symbolic
+    dimension. set_input / output take and give the whole batch; run()
+    enqueues one step on the current stream: the slices start after the work
+    already on it, and its later work waits for all of them."""
+
+    def __init__(self, make_graph=None, batch=0, parts=2, onnx=None, **kw):
+        if parts < 1 or batch < parts or batch % parts:
+            raise ValueError(f"batch {batch} does not split into {parts} equal parts")
+        self.parts, self.batch, self.sub = parts, batch, batch // parts
+        self.streams, self.sessions, self.g = [], [], None
+        L = _lib.lib()
+        for _ in range(parts):
+            st = C.c_void_p()
+            _lib.check(L.nnrh_stream_create(C.byref(st)))
+            self.streams.append(st.value)
+            if onnx is not None:
+                self.sessions.append(Session(None, stream=st.value, onnx=onnx, sym_dim=self.sub, **kw))
+            else:
+                self.sessions.append(Session(make_graph(self.sub), stream=st.value, **kw))
+        hs = (C.c_void_p * parts)(*[s.h.value for s in self.sessions])
+        g = C.c_void_p()
+        _chk(host_lib().nnr_group_create(hs, parts, C.byref(g)))
+        self.g = g
+
+    def slice(self, k):
+        return slice(k * self.sub, (k + 1) * self.sub)
+
+    def set_input(self, name, arr):
+        for k, s in enumerate(self.sessions):
+            s.set_input(name, arr[self.slice(k)])
+
+    def output(self, name):
+        outs = [s.output(name) for s in self.sessions]
+        return np.concatenate([o for o, _ in outs], axis=0), outs[0][1]
+
+    def run(self):
+        _chk(host_lib().nnr_group_run(self.g, _lib.cur_stream()))
+
+    def plan(self):
+        return self.sessions[0].plan()
+
+    def graph_active(self) -> bool:
+        return all(s.graph_active() for s in self.sessions)
+
+    def device_bytes(self):
+        return sum(s.device_bytes() for s in self.sessions)
+
+    def close(self):
+        L = _lib.lib()
+        for st in self.streams:
+            L.nnrh_stream_synchronize(st)
+        if self.g:
+            host_lib().nnr_group_destroy(self.g)
+            self.g = None
+        self.sessions = []          # the contexts go before their streams
+        import gc
+        gc.collect()
+        for st in self.streams:
+            L.nnrh_stream_destroy(st)
+        self.streams = []
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass
 

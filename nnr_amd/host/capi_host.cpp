@@ -1,11 +1,13 @@
 // capi_host.cpp -- implementation of include/nnr_host.h over context_t.
 #include <cstring>
 #include <exception>
+#include <memory>
 #include <new>
 #include <string>
 #include <vector>
 
 #include "nnr.h"
+#include "nnr_hip.h"
 #include "nnr_host.h"
 
 namespace nnr {
@@ -285,6 +287,68 @@ int nnr_ctx_run(nnr_ctx_t c) {
     return guarded("ctx_run", [&]() -> int {
         if (!c) return err("ctx is NULL");
         if (!c->ctx.run()) return ctx_err(c);
+        return 0;
+    });
+}
+
+// ---- concurrent contexts ---------------------------------------------------
+struct nnr_group {
+    std::vector<nnr_ctx_t> parts;
+    void* fork = nullptr;               // recorded on the caller's stream at run()
+    std::vector<void*> done;            // recorded on each part's stream after its run
+    ~nnr_group() {
+        if (fork) nnrh_event_destroy(fork);
+        for (void* e : done)
+            if (e) nnrh_event_destroy(e);
+    }
+};
+
+int nnr_group_create(const nnr_ctx_t* ctxs, int n, nnr_group_t* out) {
+    return guarded("group_create", [&]() -> int {
+        if (!out) return err("group is NULL");
+        *out = nullptr;
+        if (!ctxs || n < 1) return err("group_create: no contexts");
+        for (int i = 0; i < n; ++i) {
+            if (!ctxs[i]) return err("group_create: context " + std::to_string(i) + " is NULL");
+            if (!ctxs[i]->ctx.stream)
+                return err("group_create: context " + std::to_string(i) + " needs a stream of its own");
+            for (int j = 0; j < i; ++j)
+                if (ctxs[j] == ctxs[i] || ctxs[j]->ctx.stream == ctxs[i]->ctx.stream)
+                    return err("group_create: contexts " + std::to_string(j) + " and " + std::to_string(i) +
+                               " share a context or a stream");
+        }
+        std::unique_ptr<nnr_group> g(new nnr_group());
+        g->parts.assign(ctxs, ctxs + n);
+        if (nnrh_event_create(&g->fork) != 0) return err(nnrh_last_error());
+        g->done.assign((size_t)n, nullptr);
+        for (auto& e : g->done)
+            if (nnrh_event_create(&e) != 0) return err(nnrh_last_error());
+        *out = g.release();
+        return 0;
+    });
+}
+
+int nnr_group_run(nnr_group_t g, void* stream) {
+    return guarded("group_run", [&]() -> int {
+        if (!g) return err("group is NULL");
+        // fork: every part's stream starts after the caller's work so far
+        if (nnrh_event_record(g->fork, stream) != 0) return err(nnrh_last_error());
+        for (size_t i = 0; i < g->parts.size(); ++i) {
+            nnr_ctx_t c = g->parts[i];
+            if (nnrh_stream_wait_event(c->ctx.stream, g->fork) != 0) return err(nnrh_last_error());
+            if (!c->ctx.run()) return ctx_err(c);
+            if (nnrh_event_record(g->done[i], c->ctx.stream) != 0) return err(nnrh_last_error());
+        }
+        // join: the caller's later work waits for every part
+        for (void* e : g->done)
+            if (nnrh_stream_wait_event(stream, e) != 0) return err(nnrh_last_error());
+        return 0;
+    });
+}
+
+int nnr_group_destroy(nnr_group_t g) {
+    return guarded("group_destroy", [&]() -> int {
+        delete g;
         return 0;
     });
 }

@@ -98,3 +98,16 @@ def test_dispatch_matches_oracle(C, k, s, xn, yn, grp, post):
         br = nnr_amd.conv_dispatch(1, C, H, W, w, **kw)
         ocv = O.Conv(1, C, H, W, OC, k, k, **kw)
         assert br == ocv.dispatch(), (C, k, s, xn, yn, grp, post, act, wzp)
+
+
+def test_group_create_errors():
+    """nnr_group_create refuses a missing context list before touching a
+    GPU; destroying a NULL group is a no-op."""
+    import ctypes as C
+    from nnr_amd import graph as G
+    L = G.host_lib()
+    g = C.c_void_p()
+    assert L.nnr_group_create(None, 0, C.byref(g)) != 0
+    assert b"no contexts" in L.nnr_last_error()
+    assert g.value is None
+    assert L.nnr_group_destroy(None) == 0

@@ -511,3 +511,56 @@ def test_hip_graph_replay(dev, name):
             assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (rep, o)
         torch.zeros(1 << 20, device=dev).add_(1.0)   # eager work between the replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("name,parts", [("resnet50", 2), ("mobilenetv2", 4), ("qoperator", 3)])
+def test_split_session(dev, name, parts):
+    """The batch as `parts` slices run concurrently (SplitSession: one
+    context and stream per slice, nnr_group_run) gives the whole-batch
+    context's graph outputs bit for bit, on several steps with new inputs
+    (the slices' graphs replay from the second step on), and the caller's
+    stream waits for every slice."""
+    import torch
+    from nnr_amd import _lib
+    rng = np.random.default_rng(41)
+    if name == "resnet50":
+        make, B, shape = (lambda b: synth.resnet50(batch=b, hw=64, seed=14)), 4, (3, 64, 64)
+    elif name == "mobilenetv2":
+        make, B, shape = (lambda b: synth.mobilenetv2(batch=b, hw=96, seed=17)), 4, (3, 96, 96)
+    else:
+        make, B, shape = (lambda b: synth.qoperator_net(batch=b, hw=21)), 6, (3, 21, 21)
+    g = make(B)
+    whole = G.Session(g, memory_planning=True)
+    split = G.SplitSession(make, batch=B, parts=parts, memory_planning=True)
+    try:
+        for step in range(3):
+            print(f"{name} split step {step}", flush=True)
+            x = rng.uniform(-1.0, 1.5, (B,) + shape).astype(np.float32)
+            whole.set_input("input", x)
+            split.set_input("input", x)
+            whole.run()
+            torch.cuda.synchronize()
+            split.run()
+            # a copy enqueued on the caller's stream right after run() reads
+            # the last slice's finished output (the join), with no other sync
+            o0 = g.outputs[0]
+            p, dt, oshape, _ = split.sessions[-1].tensor_info(o0)
+            nbytes = int(np.prod(oshape)) * np.dtype(dt).itemsize
+            buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            _lib.check(_lib.lib().nnrh_memcpy(buf.data_ptr(), p, nbytes, 2, _lib.cur_stream()))
+            torch.cuda.current_stream().synchronize()
+            last = whole.output(o0)[0][split.slice(parts - 1)]
+            assert np.array_equal(buf.cpu().numpy(), np.ascontiguousarray(last).view(np.uint8).reshape(-1)), step
+            torch.cuda.synchronize()
+            assert split.graph_active() == (step >= 1), step
+            for o in g.outputs:
+                a, b = split.output(o)[0], whole.output(o)[0]
+                assert a.shape == b.shape
+                assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (step, o)
+    finally:
+        split.close()
+
+
+def test_split_session_rejects_ragged_batch(dev):
+    with pytest.raises(ValueError):
+        G.SplitSession(lambda b: synth.resnet50(batch=b, hw=64), batch=5, parts=2)
