@@ -77,6 +77,36 @@ __device__ __forceinline__ void dma16(const void* src, uint8_t* lds_dst) {
 
 // bytes 0 of a, b, c, d -> one dword (a lowest). v_perm_b32 selects bytes
 // of {S0, S1} with S1 as bytes 0-3 and S0 as bytes 4-7; selector 0x0c is 0.
+// the first `valid` (1..16) output bytes of {w0, w1, w2, w3} to p: 8- and
+// 4-byte stores where p is 8-byte aligned, single bytes for the rest (a
+// ragged last column chunk: 24 output channels take one 16-byte and one
+// 8-byte store a row, or two 8-byte stores, instead of byte stores). The
+// words stay in registers: every index is a constant.
+__device__ __forceinline__ void store_bytes_prefix(uint8_t* p, uint32_t w0, uint32_t w1, uint32_t w2,
+                                                   uint32_t w3, int valid) {
+    auto bytes_of = [&](int from, uint32_t w, int n) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < n) p[from + i] = (uint8_t)(w >> (8 * i));
+    };
+    if ((((uintptr_t)p) & 7) == 0 && valid >= 8) {
+        *(uint2*)p = make_uint2(w0, w1);
+        if (valid == 16) {
+            *(uint2*)(p + 8) = make_uint2(w2, w3);
+        } else if (valid >= 12) {
+            *(uint32_t*)(p + 8) = w2;
+            bytes_of(12, w3, valid - 12);
+        } else {
+            bytes_of(8, w2, valid - 8);
+        }
+        return;
+    }
+    bytes_of(0, w0, valid);
+    if (valid > 4) bytes_of(4, w1, valid - 4);
+    if (valid > 8) bytes_of(8, w2, valid - 8);
+    if (valid > 12) bytes_of(12, w3, valid - 12);
+}
+
 __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);   // [a0, b0, 0, 0]
     const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);   // [c0, d0, 0, 0]
@@ -832,10 +862,13 @@ void qgemm_dma_kernel(GemmArgs g) {
                     // (a plain store: the next layer reads this output, and a
                     // streaming store would send it past the caches to HBM)
                     *(v4i*)yrow = v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
-                } else {
+                } else if constexpr (FUSE == FUSE_ADD) {
+                    // (a fused add has output channels % 16 == 0: never ragged)
 #pragma unroll
                     for (int i = 0; i < 16; ++i)
                         if (nb + i < g.N) yrow[i] = (uint8_t)(packed[i >> 2] >> (8 * (i & 3)));
+                } else {
+                    store_bytes_prefix(yrow, packed[0], packed[1], packed[2], packed[3], g.N - nb < 16 ? g.N - nb : 16);
                 }
             }
         }
@@ -1128,9 +1161,7 @@ __global__ __launch_bounds__(256, 2) void qgemm_direct_kernel(GemmArgs g) {
                 if (full16) {
                     *(v4i*)yrow = v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
                 } else {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i)
-                        if (nb + i < g.N) yrow[i] = (uint8_t)(packed[i >> 2] >> (8 * (i & 3)));
+                    store_bytes_prefix(yrow, packed[0], packed[1], packed[2], packed[3], g.N - nb < 16 ? g.N - nb : 16);
                 }
             }
         }
