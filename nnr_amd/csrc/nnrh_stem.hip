@@ -93,8 +93,14 @@ __device__ __forceinline__ void lds_barrier() {
 
 // CC: input channels (3 or 4); KS: MFMA K-steps (Kp / 64); POOL: the 3x3 /
 // stride 2 / padding 1 MaxPool after the conv fused (strip = pooled rows)
-template <bool F32, int CC, int KS, bool POOL>
+// NT: 16-column MFMA blocks computed (OC = 16 NT, or 64 with NT = 4): lane
+// (fch, frow) holds output channels 4 NT fch .. 4 NT fch + 4 NT - 1 of its
+// pixel, so a 16- or 32-channel layer issues NT MFMAs a K-step and its
+// epilogue touches only real channels
+template <bool F32, int CC, int KS, bool POOL, int NT = 4>
 __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
+    static_assert(NT == 4 || NT == 2 || NT == 1, "16, 32 or 64 output channels");
+    static_assert(!POOL || NT == 4, "the fused MaxPool takes 64 channels");
     // separate static arrays: the compiler then tells the ring's reads from
     // the staging area's in-flight DMA writes and waits for neither
     __shared__ __attribute__((aligned(16))) uint32_t ring[POOL ? STEM_P_RING_DW : STEM_RING_DW];   // WR rows x L
@@ -122,19 +128,23 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
     const long long img = (long long)n * a.C * HW;
 
     // ---- weights (B fragments) and per-column constants in registers
-    v4i wf[KS][4];   // [K-step][tn]
+    // MFMA block tn's row frow is output channel (frow / 4) * 4 NT + 4 tn +
+    // frow % 4 (with NT = 4 the packed weight row tn * 16 + frow itself)
+    v4i wf[KS][NT];   // [K-step][tn]
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int tn = 0; tn < 4; ++tn)
-            wf[ks][tn] = *(const v4i*)(a.w + (long long)(tn * 16 + frow) * a.Kp + ks * 64 + fch * 16);
-    // per-column constants of this lane's 16 columns
-    v4i c0v[4], csv[4], bfv[4];
+        for (int tn = 0; tn < NT; ++tn) {
+            const int row = packed_row_of_col((frow >> 2) * 4 * NT + 4 * tn + (frow & 3));
+            wf[ks][tn] = *(const v4i*)(a.w + (long long)row * a.Kp + ks * 64 + fch * 16);
+        }
+    // per-column constants of this lane's 4 NT columns
+    v4i c0v[NT], csv[NT], bfv[NT];
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) {
-        c0v[tn] = *(const v4i*)(a.c0 + 16 * fch + 4 * tn);
-        csv[tn] = *(const v4i*)(a.cs + 16 * fch + 4 * tn);
-        bfv[tn] = *(const v4i*)(a.bf + 16 * fch + 4 * tn);
+    for (int tn = 0; tn < NT; ++tn) {
+        c0v[tn] = *(const v4i*)(a.c0 + 4 * NT * fch + 4 * tn);
+        csv[tn] = *(const v4i*)(a.cs + 4 * NT * fch + 4 * tn);
+        bfv[tn] = *(const v4i*)(a.bf + 4 * NT * fch + 4 * tn);
     }
     // the weights have landed before the row groups start: the compiler
     // then has no load outstanding from outside the pixel-group loop that
@@ -306,7 +316,7 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
         const int P_here = (pro ? 1 : min(a.R, oh_end - oh0)) * a.oW;
         // outputs of this wave's pixel groups, stored after the ring refill so
         // that they stay in flight across the next group's DMA and MFMAs
-        uint32_t outv[STEM_MGW][4];
+        uint32_t outv[STEM_MGW][NT];
         // the pixel groups with the saturating epilogue (SAT) and the 8-byte
         // fragment reads (A8) fixed at compile time: a run-time test inside
         // puts a branch around every element and fragment read, and then no
@@ -330,17 +340,17 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
                             xf[ks] = v4i{(int)px[0], (int)px[1], (int)px[2], (int)px[3]};
                         }
                     }
-                    v4i acc[4];
+                    v4i acc[NT];
 #pragma unroll
-                    for (int tn = 0; tn < 4; ++tn) acc[tn] = c0v[tn];
+                    for (int tn = 0; tn < NT; ++tn) acc[tn] = c0v[tn];
 #pragma unroll
                     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-                        for (int tn = 0; tn < 4; ++tn)
+                        for (int tn = 0; tn < NT; ++tn)
                             acc[tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ks][tn], xf[ks], acc[tn], 0, 0, 0);
                     // RQ-C: rne(clamp(fma(fma(acc, cs, bf), 1/y_s, zp), qmin, qmax))
 #pragma unroll
-                    for (int tn = 0; tn < 4; ++tn) {
+                    for (int tn = 0; tn < NT; ++tn) {
                         const v4i csq = csv[tn], bfq = bfv[tn];
                         uint32_t w = 0;
 #pragma unroll
@@ -435,9 +445,14 @@ __global__ __launch_bounds__(256, 2) void stem_conv_kernel(StemArgs a) {
 #pragma unroll
             for (int i = 0; i < STEM_MGW; ++i) {
                 const int p = (wave + 4 * i) * 16 + frow;
-                if ((wave + 4 * i) * 16 < P_here && p < P_here && 16 * fch < a.OC) {
-                    uint8_t* yp = y_img + (uint32_t)((oh0 * a.oW + p) * a.OC + 16 * fch);
-                    *(v4i*)yp = v4i{(int)outv[i][0], (int)outv[i][1], (int)outv[i][2], (int)outv[i][3]};
+                if ((wave + 4 * i) * 16 < P_here && p < P_here && 4 * NT * fch < a.OC) {
+                    uint8_t* yp = y_img + (uint32_t)((oh0 * a.oW + p) * a.OC + 4 * NT * fch);
+                    if constexpr (NT == 4)
+                        *(v4i*)yp = v4i{(int)outv[i][0], (int)outv[i][1], (int)outv[i][2], (int)outv[i][3]};
+                    else if constexpr (NT == 2)
+                        *(uint2*)yp = make_uint2(outv[i][0], outv[i][1]);
+                    else
+                        *(uint32_t*)yp = outv[i][0];
                 }
             }
         }
@@ -502,7 +517,12 @@ hipError_t launch_stem_conv(const StemArgs& a, bool f32, hipStream_t s) {
             return;
         }
         switch (a.KS) {
-        case 1: go(stem_conv_kernel<F, C, 1, false>); break;
+        case 1:
+            // 16 or 32 output channels: only their MFMA blocks
+            if (a.OC == 16) go(stem_conv_kernel<F, C, 1, false, 1>);
+            else if (a.OC == 32) go(stem_conv_kernel<F, C, 1, false, 2>);
+            else go(stem_conv_kernel<F, C, 1, false>);
+            break;
         case 2: go(stem_conv_kernel<F, C, 2, false>); break;
         case 3: go(stem_conv_kernel<F, C, 3, false>); break;
         default: go(stem_conv_kernel<F, C, 4, false>); break;
