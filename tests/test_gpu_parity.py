@@ -188,6 +188,11 @@ CONV_CASES = [
     ("direct_c40_oc72", 2, 40, 13, 17, 72, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=0, post_fn=1)),
     ("direct_c16_oc96", 4, 16, 24, 24, 96, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=128)),
     ("direct_c64_oc16", 2, 64, 30, 30, 16, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=7)),
+    # 32- and 16-column blocks of the direct kernel: 32 and 24 channels (a
+    # ragged 8-byte chunk), 8 channels with K = 24
+    ("direct_c32_oc32", 3, 32, 17, 19, 32, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=0, post_fn=1)),
+    ("direct_c48_oc24", 2, 48, 21, 13, 24, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=9)),
+    ("direct_c24_oc8", 2, 24, 11, 12, 8, 1, dict(y_nhwc=1, x_nhwc=1, y_zp=130)),
     ("direct", 2, 64, 12, 12, 64, 3, dict(pads=(1, 1, 1, 1), y_nhwc=0, post_fn=1, y_zp=9)),
     ("direct_tail", 1, 20, 9, 7, 30, 3, dict(pads=(1, 1, 1, 1), y_nhwc=0, y_zp=20)),
     ("first_nhwc", 2, 3, 40, 40, 64, 7, dict(stride=(2, 2), pads=(3, 3, 3, 3), y_nhwc=1)),
