@@ -628,12 +628,17 @@ def run_bert(args, dev):
 
     skip = {p["op"] for p in plan} - {proj}
     env = graph_oracle.run_plan(plan, g, {}, fmt, source=dev_slice, skip_ops=skip,
-                                stop_after="l0_ffn2")
+                                stop_after="l0_ffn2", keep_chain=True)
     checked = 0
     for p in plan:
         if p["op"] == proj and p["outputs"][0] in env:
             d, ref = dev_slice(p["outputs"][0]), env[p["outputs"][0]]
-            if any(g.node_by_name(c).op == "Gelu" for c in p.get("fused_chain") or []):
+            if p["variant"].endswith("+Codes"):
+                # the chain stores its uint8 QLinearMatMul bytes for the
+                # DynamicQuantizeLinear after it
+                ref = env[g.node_by_name(p["fused_chain"][0]).inputs[0]]
+                assert np.array_equal(d, ref), f"parity gate failed at {p['name']}"
+            elif any(g.node_by_name(c).op == "Gelu" for c in p.get("fused_chain") or []):
                 # erf in float64 against the device's fp32 erff: a few ulps
                 assert np.allclose(d, ref, rtol=2e-6, atol=1e-7), f"parity gate failed at {p['name']}"
             else:
@@ -641,7 +646,22 @@ def run_bert(args, dev):
             checked += 1
     assert checked == 6
     parity = (f"the first layer's {checked} {proj} projections recomputed by the oracle from the device's own "
-              f"inputs on sequences {idx} of {B}: bit-exact (the Gelu chain end within 2e-6)")
+              f"inputs on sequences {idx} of {B}: bit-exact (an fp32 Gelu chain end within 2e-6)")
+    codes = [p for p in plan if p["op"] == "DynamicQuantizeLinear" and p["variant"] == "Codes"]
+    if codes:
+        # the DynamicQuantizeLinears that rebuild their input from stored
+        # bytes, against a context that materializes the fp32 tensors (whose
+        # quantizer the per-node tests check): every layer, the whole batch
+        ref_s = G.Session(g, dynq_codes=False)
+        ref_s.set_input("input", x)
+        ref_s.run()
+        for p in codes:
+            for o in p["outputs"]:
+                a, b = np.atleast_1d(s.output(o)[0]), np.atleast_1d(ref_s.output(o)[0])
+                assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"parity gate failed at {p['name']}"
+        del ref_s
+        parity += (f"; the {len(codes)} DynamicQuantizeLinears fed by stored FF1 bytes equal, bit for bit "
+                   f"over the whole batch, a context that materializes the fp32 FF1 output")
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
     mem["hip_graph"] = s.graph_active()

@@ -238,6 +238,26 @@ int nnrh_qmatmul_fuse_gelu(nnrh_qmatmul_t h);
  * pass over y (DynamicQuantizeLinear.cpp:37-41).                          */
 int nnrh_qmatmul_minmax_count(nnrh_qmatmul_t h, int batch, int* count);
 int nnrh_qmatmul_set_minmax_out(nnrh_qmatmul_t h, float* parts_dev, int capacity);
+/* After nnrh_qmatmul_fuse_dq_bias (+ _fuse_gelu) and _set_minmax_out, for a
+ * chain whose float32 result is read only by a DynamicQuantizeLinear
+ * (DynamicQuantizeLinear.cpp:27-58 on the output of QLinearMatMul.cpp:
+ * 188-198 -> DequantizeLinear -> Add [-> Gelu]): on = 1 makes
+ * nnrh_qmatmul_run write, instead of the float32 values, the uint8
+ * QLinearMatMul bytes they are computed from (y then holds batch x m x n
+ * bytes, same element layout) together with the values' (min, max) pairs.
+ * nnrh_qmatmul_dynamic_quantize_codes then writes the DynamicQuantizeLinear
+ * outputs (y, y_scale, y_zp of the run's batch) from those bytes: the chain
+ * value of byte q in column j depends on (j, q) alone, so a per-column table
+ * of the 256 quantized values (built after the pairs give the scale / zero
+ * point) maps every byte, and the results equal running the chain and the
+ * quantizer on the float32 values bit for bit. The handle owns the table
+ * (256 x n rounded up to 64 bytes); a handle in codes mode serves one run at
+ * a time (the table is rebuilt by each quantize call). on = 0 returns to
+ * float32 output. No counterpart in the reference, which materializes the
+ * float32 tensor between the operators.                                   */
+int nnrh_qmatmul_set_codes_out(nnrh_qmatmul_t h, int on);
+int nnrh_qmatmul_dynamic_quantize_codes(nnrh_qmatmul_t h, const void* codes_dev, int batch, uint8_t* y_dev,
+                                        float* y_scale_dev, uint8_t* y_zp_dev, void* stream);
 /* 2..4 QLinearMatMuls, each with nnrh_qmatmul_fuse_dq_bias (no Gelu, no
  * min/max output), identical in shape and types and reading the same A (a
  * transformer layer's Q, K and V projections), run as one launch: the

@@ -206,13 +206,35 @@ class QLinearMatMul:
                                                 0 if parts is None else parts.numel() // 2))
         self._keep["parts"] = parts
 
+    def set_codes_out(self, on=True):
+        """After fuse_dq_bias (+ fuse_gelu) and set_minmax_out: runs write the
+        uint8 QLinearMatMul bytes and the chain values' (min, max) pairs
+        instead of the float32 values; dynamic_quantize_codes then gives the
+        DynamicQuantizeLinear of those values."""
+        check(lib().nnrh_qmatmul_set_codes_out(self.h, 1 if on else 0))
+        self._codes = bool(on)
+
+    def dynamic_quantize_codes(self, codes, stream=None):
+        """(y, y_scale, y_zp) of DynamicQuantizeLinear over the chain values
+        of a codes-mode run's output `codes` (its (min, max) pairs must be
+        the last ones written)."""
+        import torch
+        batch = codes.numel() // (self.m * self.n)
+        y = torch.empty(tuple(codes.shape), dtype=torch.uint8, device=codes.device)
+        ys = torch.empty(1, dtype=torch.float32, device=codes.device)
+        yz = torch.empty(1, dtype=torch.uint8, device=codes.device)
+        check(lib().nnrh_qmatmul_dynamic_quantize_codes(self.h, ptr(codes), batch, ptr(y), ptr(ys), ptr(yz),
+                                                        cur_stream() if stream is None else stream))
+        return y, ys, yz
+
     def __call__(self, a, y=None, a_scale_dev=None, a_zp_dev=None, stream=None):
         import torch
         if a.shape[-1] != self.k or a.shape[-2] != self.m:
             raise ValueError("a shape mismatch")
         batch = int(np.prod(a.shape[:-2])) if a.dim() > 2 else 1
         if y is None:
-            dt = torch.float32 if self._f32 else (torch.uint8 if self.y_dtype == np.uint8 else torch.int8)
+            dt = torch.float32 if self._f32 and not getattr(self, "_codes", False) else (
+                torch.uint8 if self.y_dtype == np.uint8 else torch.int8)
             y = torch.empty(tuple(a.shape[:-1]) + (self.n,), dtype=dt, device=a.device)
         check(lib().nnrh_qmatmul_run(self.h, ptr(a), self.m * self.k if batch > 1 else 0, ptr(y),
                                      batch, ptr(a_scale_dev), ptr(a_zp_dev),

@@ -32,7 +32,8 @@ EXPORTS = [
     "nnrh_qconv_fuse_quantize", "nnrh_qconv_run_f32", "nnrh_qconv_fuse_maxpool", "nnrh_global_avgpool_dequant",
     "nnrh_multihead_attention_workspace", "nnrh_multihead_attention_f32", "nnrh_multihead_attention_minmax_count", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
     "nnrh_qmatmul_fuse_dq_bias", "nnrh_qmatmul_fuse_gelu", "nnrh_qmatmul_minmax_count",
-    "nnrh_qmatmul_set_minmax_out", "nnrh_dynamic_quantize_linear_parts", "nnrh_add_layernorm_f32",
+    "nnrh_qmatmul_set_minmax_out", "nnrh_qmatmul_set_codes_out", "nnrh_qmatmul_dynamic_quantize_codes",
+    "nnrh_dynamic_quantize_linear_parts", "nnrh_add_layernorm_f32",
     "nnrh_qmatmul_group_create", "nnrh_qmatmul_group_run", "nnrh_qmatmul_group_destroy",
     "nnrh_qlinear_mul", "nnrh_qlinear_global_avgpool", "nnrh_qlinear_avgpool", "nnrh_qlinear_concat_part",
     "nnrh_batchnorm_u8", "nnrh_batchnorm_f32", "nnrh_qlinear_concat",
@@ -148,6 +149,8 @@ def lib():
         "nnrh_qmatmul_fuse_gelu": (i, [vp]),
         "nnrh_qmatmul_minmax_count": (i, [vp, i, P(i)]),
         "nnrh_qmatmul_set_minmax_out": (i, [vp, vp, i]),
+        "nnrh_qmatmul_set_codes_out": (i, [vp, i]),
+        "nnrh_qmatmul_dynamic_quantize_codes": (i, [vp, vp, i, vp, vp, vp, vp]),
         "nnrh_qmatmul_group_create": (i, [P(vp), P(vp), i]),
         "nnrh_qmatmul_group_run": (i, [vp, vp, i, P(vp), vp, vp, vp]),
         "nnrh_qmatmul_group_destroy": (i, [vp]),

@@ -1098,9 +1098,12 @@ struct nnrh_qmatmul {
     float* colscale = nullptr;  // nnrh_matmul_integer_scaled_create: w_scale, padded to Np
     int rowsum_cap = 0;     // batches the rowsum buffer holds
     int parts_cap = 0;      // nnrh_qmatmul_set_minmax_out: pairs the caller's buffer holds
+    uint8_t* codes_table = nullptr;   // nnrh_qmatmul_set_codes_out: [256][Np] quantized chain values
     int a_zp = 0, b_beta = 0;
     float b_scale = 0.f, y_scale = 0.f;
-    ~nnrh_qmatmul() { dfree(wpack); dfree(colsum); dfree(c0); dfree(rowsum); dfree(dq_bias); dfree(colscale); }
+    ~nnrh_qmatmul() {
+        dfree(wpack); dfree(colsum); dfree(c0); dfree(rowsum); dfree(dq_bias); dfree(colscale); dfree(codes_table);
+    }
 };
 
 extern "C" int nnrh_qmatmul_create(nnrh_qmatmul_t* out, const nnrh_qmatmul_desc* d) {
@@ -1433,6 +1436,45 @@ extern "C" int nnrh_qmatmul_set_minmax_out(nnrh_qmatmul_t h, float* parts_dev, i
     return NNRH_OK;
 }
 
+extern "C" int nnrh_qmatmul_set_codes_out(nnrh_qmatmul_t h, int on) {
+    if (!h) return set_err(NNRH_ERR_INVALID, "qmatmul_set_codes_out: NULL handle");
+    if (!on) {
+        h->g.dq_codes = 0;
+        return NNRH_OK;
+    }
+    if (h->g.epi != EPI_RQD || !h->g.dq_bias || !h->g.mm_parts)
+        return set_err(NNRH_ERR_UNSUPPORTED,
+                       "qmatmul_set_codes_out: needs nnrh_qmatmul_fuse_dq_bias and nnrh_qmatmul_set_minmax_out first");
+    if (!h->codes_table) {
+        int rc = nnrh_malloc((void**)&h->codes_table, dynamic_quantize_codes_table_bytes(h->g.Np));
+        if (rc) return rc;
+    }
+    h->g.dq_codes = 1;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qmatmul_dynamic_quantize_codes(nnrh_qmatmul_t h, const void* codes, int batch, uint8_t* y,
+                                                   float* y_scale, uint8_t* y_zp, void* stream) {
+    if (!h || !codes || !y || !y_scale || !y_zp || batch <= 0)
+        return set_err(NNRH_ERR_INVALID, "qmatmul_dynamic_quantize_codes: bad arguments");
+    const GemmArgs& g = h->g;
+    if (!g.dq_codes || !g.mm_parts || !h->codes_table)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_dynamic_quantize_codes: needs nnrh_qmatmul_set_codes_out");
+    const long long nparts = qmatmul_parts(g, batch);
+    if (nparts > h->parts_cap)
+        return set_err(NNRH_ERR_INVALID, "qmatmul_dynamic_quantize_codes: %lld min/max pairs exceed the buffer's %d",
+                       nparts, h->parts_cap);
+    const long long rows = (long long)batch * g.M;
+    if ((rows + 255) / 256 > 65535)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_dynamic_quantize_codes: %lld rows", rows);
+    ProfScope ps("dynamic_quantize", S(stream));
+    HIP_TRY(launch_dynamic_quantize_codes((const uint8_t*)codes, rows, g.N, g.Np, g.dq_bias, g.dq_scale, g.y_zp,
+                                          g.dq_gelu, g.mm_parts, (int)nparts, h->codes_table, y, y_scale, y_zp,
+                                          S(stream)),
+            "dynamic_quantize_codes");
+    return NNRH_OK;
+}
+
 extern "C" int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a, long long a_bstride, void* y, int batch,
                                 const float* a_scale_dev, const void* a_zp_dev, void* stream) {
     if (!h || !a || !y) return set_err(NNRH_ERR_INVALID, "qmatmul_run: NULL argument");
@@ -1467,6 +1509,8 @@ extern "C" int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a, long long a_bst
     if (g.mm_parts && qmatmul_parts(g, batch) > h->parts_cap)
         return set_err(NNRH_ERR_INVALID, "qmatmul_run: %lld min/max pairs exceed the buffer's %d",
                        qmatmul_parts(g, batch), h->parts_cap);
+    if (g.dq_codes && !g.mm_parts)
+        return set_err(NNRH_ERR_INVALID, "qmatmul_run: uint8 codes out without min/max pairs");
     ProfScope ps("qgemm", s);
     HIP_TRY(launch_qgemm(g, batch, pick_tile(g.N), vec, s), "qgemm");
     return NNRH_OK;

@@ -76,6 +76,16 @@ hipError_t launch_dynamic_quantize_noalloc(const float* x, long long n, uint8_t*
                                            uint8_t* y_zp, hipStream_t s);
 hipError_t launch_dynamic_quantize_parts(const float* x, long long n, const float* parts, int nparts,
                                          uint8_t* y, float* y_scale, uint8_t* y_zp, hipStream_t s);
+// DynamicQuantizeLinear of a fused dequantize chain from its GEMM's uint8
+// bytes (codes, rows x N contiguous) and (min, max) pairs: the chain's value
+// of byte q in column n is [Gelu](fl(fl((q - q_zp) * dq_scale) + bias[n]));
+// table: dynamic_quantize_codes_table_bytes(Np) bytes (Np = N rounded up to
+// 64, bias padded to Np), 16-byte aligned
+size_t dynamic_quantize_codes_table_bytes(int Np);
+hipError_t launch_dynamic_quantize_codes(const uint8_t* codes, long long rows, int N, int Np, const float* bias,
+                                         float dq_scale, int q_zp, int gelu, const float* parts, int nparts,
+                                         uint8_t* table, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                                         hipStream_t s);
 hipError_t launch_qadd(const QAddArgs& p, hipStream_t s);
 hipError_t launch_maxpool_u8_nhwc(const uint8_t* x, uint8_t* y, int N, int C, int iH, int iW,
                                   int oH, int oW, int kH, int kW, int sH, int sW, int pH, int pW,

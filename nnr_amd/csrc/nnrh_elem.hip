@@ -177,24 +177,25 @@ __device__ __forceinline__ float dyn_qf(float v, float r, float sc, int zp) {
     return k + (float)zp;
 }
 // scale and zero point from producer-written (min, max) pairs, reduced by
-// every block of the quantize kernel (256 threads): every block gets the
+// every block of the quantize kernel (NT threads): every block gets the
 // same values, since min and max are exact in any order
+template <int NT = 256>
 __device__ __forceinline__ void dyn_scale_parts_block(const float* __restrict part, int nparts, float* sc_out,
                                                       int* zp_out) {
-    __shared__ float smn[4], smx[4];
+    __shared__ float smn[NT / 64], smx[NT / 64];
     float mn = 0.0f, mx = 0.0f;
     const int n2 = nparts >> 1;   // whole float4s (the pairs are 8-byte aligned)
     const bool vec = ((uintptr_t)part & 15) == 0;
     if (vec) {
         const float4* p4 = (const float4*)part;
 #pragma unroll 4
-        for (int i = threadIdx.x; i < n2; i += 256) {
+        for (int i = threadIdx.x; i < n2; i += NT) {
             const float4 v = p4[i];
             mn = fminf(mn, fminf(v.x, v.z));
             mx = fmaxf(mx, fmaxf(v.y, v.w));
         }
     }
-    for (int i = (vec ? 2 * n2 : 0) + threadIdx.x; i < nparts; i += 256) {
+    for (int i = (vec ? 2 * n2 : 0) + threadIdx.x; i < nparts; i += NT) {
         mn = fminf(mn, part[2 * i]);
         mx = fmaxf(mx, part[2 * i + 1]);
     }
@@ -209,8 +210,13 @@ __device__ __forceinline__ void dyn_scale_parts_block(const float* __restrict pa
         smx[w] = mx;
     }
     __syncthreads();
-    mn = fminf(fminf(smn[0], smn[1]), fminf(smn[2], smn[3]));
-    mx = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
+    mn = smn[0];
+    mx = smx[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) {
+        mn = fminf(mn, smn[i]);
+        mx = fmaxf(mx, smx[i]);
+    }
     const float xmin = mn < 0.0f ? mn : 0.0f;
     const float xmax = mx > 0.0f ? mx : 0.0f;
     float sc = (xmax - xmin) / 255.0f;
@@ -335,6 +341,150 @@ hipError_t launch_dynamic_quantize_parts(const float* x, long long n, const floa
     if (qb > 512) qb = 512;
     hipLaunchKernelGGL(dyn_quantize_kernel<true>, dim3((unsigned)qb), dim3(256), 0, s, x, n, parts, nparts,
                        y_scale, y_zp, y);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// DynamicQuantizeLinear after a fused QLinearMatMul -> DequantizeLinear ->
+// Add(bias) [-> Gelu] chain whose GEMM stored the uint8 QLinearMatMul bytes
+// instead of the fp32 chain values, with the (min, max) pairs of those values.
+// The fp32 value of byte q in column n depends on (n, q) alone,
+//   f(n, q) = [Gelu] (fl(fl((q - q_zp) * dq_scale) + bias[n])),
+// the GEMM epilogue's expression operation for operation, so its quantized
+// byte does too. The table kernel reduces the pairs to the scale / zero point
+// (DynamicQuantizeLinear.cpp:37-48) and builds T[q][n] = quantize(f(n, q)) for
+// every column and byte; the gather kernel maps every stored byte through its
+// column's table. The bytes equal quantizing the fp32 tensor (each element
+// gets the same value and the same scale / zero point).
+constexpr int DQC_SLICE = 256;     // gather: columns a block (table slice 256 x 256 bytes of LDS)
+constexpr int DQC_THREADS = 512;   // gather: 8 waves a block
+constexpr int DQC_RPT = 32;        // gather: rows a thread at most (a block: 8 x 32 rows)
+constexpr int DQC_RESIDENT = 512;  // gather blocks resident at once (2 a CU: 64 KiB of LDS each)
+
+// grid (Np / 64, 4), 1024 threads: columns 64 bx .. + 63, bytes 64 by .. + 63
+__global__ __launch_bounds__(1024) void dynq_codes_table_kernel(const float* __restrict part, int nparts,
+                                                               const float* __restrict bias, float dq_scale,
+                                                               int q_zp, int gelu, int Np,
+                                                               uint8_t* __restrict table,
+                                                               float* __restrict y_scale,
+                                                               uint8_t* __restrict y_zp) {
+    float sc;
+    int zp;
+    dyn_scale_parts_block<1024>(part, nparts, &sc, &zp);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+        *y_scale = sc;
+        *y_zp = (uint8_t)zp;
+    }
+    const float r = 1.0f / sc;
+    const int n = blockIdx.x * 64 + (threadIdx.x & 63);
+    const float b = bias[n];
+    const float zp_f = (float)q_zp;
+    const int q_end = blockIdx.y * 64 + 64;
+#pragma unroll
+    for (int q = blockIdx.y * 64 + (threadIdx.x >> 6); q < q_end; q += 16) {
+        const float d = ((float)q - zp_f) * dq_scale;
+        float v = d + b;
+        if (gelu) v = gelu_erf(v);
+        table[(long long)q * Np + n] = (uint8_t)__builtin_amdgcn_cvt_pk_u8_f32(dyn_qf(v, r, sc, zp), 0, 0u);
+    }
+}
+
+// 4 bytes of one row through the table slice (tl: the slice at the first of
+// the 4 columns; byte value q of column j sits at tl[q * DQC_SLICE + j]).
+// With a lane's 4 columns at 4 lane, the 64 lanes of a wave read 64
+// different dwords of each table row: no two lanes share a bank
+__device__ __forceinline__ uint32_t codes_lut4(const uint8_t* tl, uint32_t x) {
+    const uint32_t b0 = tl[(x & 0xffu) * DQC_SLICE];
+    const uint32_t b1 = tl[((x >> 8) & 0xffu) * DQC_SLICE + 1];
+    const uint32_t b2 = tl[((x >> 16) & 0xffu) * DQC_SLICE + 2];
+    const uint32_t b3 = tl[(x >> 24) * DQC_SLICE + 3];
+    return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+}
+
+// grid (ceil(Np / 256), ceil(rows / R)), R <= 8 x 32 rows a block (a
+// multiple of 8, chosen so that the grid fits the resident blocks): lane l of
+// every wave holds columns 4 l .. 4 l + 3 of the block's slice, so each load
+// or store instruction of a wave covers 256 contiguous bytes of one row; wave
+// w holds rows w, w + 8, ... The block's table slice (a full one: 8 16-byte
+// chunks a thread) and all of a thread's rows are loaded with no wait in
+// between; the slice goes to LDS as its loads land.
+__global__ __launch_bounds__(DQC_THREADS) void dynq_codes_gather_kernel(const uint8_t* __restrict codes,
+                                                                        long long rows, int N, int Np, int R,
+                                                                        const uint8_t* __restrict table,
+                                                                        uint8_t* __restrict y) {
+    __shared__ __attribute__((aligned(16))) uint8_t t[256 * DQC_SLICE];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c0 = blockIdx.x * DQC_SLICE;
+    const int cl = 4 * lane;   // this thread's first column in the slice
+    const int c = c0 + cl;
+    const long long rw = (long long)blockIdx.y * R + wave;   // this wave's first row
+    const long long re = min(rows, (long long)(blockIdx.y + 1) * R);
+    // dword loads and stores: N % 4 == 0 and 4-byte aligned buffers (then a
+    // lane with c < N has all 4 columns)
+    const bool vec = (N & 3) == 0 && ((((uintptr_t)codes) | (uintptr_t)y) & 3) == 0;
+    const int w = min(DQC_SLICE, Np - c0);   // a multiple of 64
+    // the table slice, 16-byte chunk i = row i / 16, columns 16 (i % 16) ..;
+    // in a partial slice the chunks past w load the last one and land in
+    // LDS columns no lane reads
+    constexpr int TCH = 256 * DQC_SLICE / 16 / DQC_THREADS;   // chunks a thread
+    uint4 tv[TCH];
+#pragma unroll
+    for (int k = 0; k < TCH; ++k) {
+        const int i = threadIdx.x + k * DQC_THREADS;
+        tv[k] = *(const uint4*)(table + (long long)(i >> 4) * Np + c0 + min(16 * (i & 15), w - 16));
+    }
+    uint32_t x[DQC_RPT];
+    if (vec) {
+        // rows past the block's end load its last row, lanes past N the
+        // last 4 columns; neither is stored
+        const int cc = min(c, N - 4);
+#pragma unroll
+        for (int i = 0; i < DQC_RPT; ++i) {
+            const long long r = min(rw + 8 * i, re - 1);
+            x[i] = *(const uint32_t*)(codes + r * N + cc);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < TCH; ++k) {
+        const int i = threadIdx.x + k * DQC_THREADS;
+        *(uint4*)(t + (i >> 4) * DQC_SLICE + 16 * (i & 15)) = tv[k];
+    }
+    __syncthreads();
+    if (c >= N) return;   // (no barrier below)
+    const uint8_t* tl = t + cl;
+    if (vec) {
+        // (a row past the block's end stores the last row's bytes again)
+#pragma unroll
+        for (int i = 0; i < DQC_RPT; ++i) {
+            const long long r = min(rw + 8 * i, re - 1);
+            *(uint32_t*)(y + r * N + c) = codes_lut4(tl, x[i]);
+        }
+        return;
+    }
+    const int nc = min(4, N - c);
+    for (long long r = rw; r < re; r += 8)
+        for (int j = 0; j < nc; ++j) y[r * N + c + j] = tl[codes[r * N + c + j] * DQC_SLICE + j];
+}
+
+size_t dynamic_quantize_codes_table_bytes(int Np) { return (size_t)256 * (size_t)Np; }
+
+hipError_t launch_dynamic_quantize_codes(const uint8_t* codes, long long rows, int N, int Np, const float* bias,
+                                         float dq_scale, int q_zp, int gelu, const float* parts, int nparts,
+                                         uint8_t* table, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                                         hipStream_t s) {
+    hipLaunchKernelGGL(dynq_codes_table_kernel, dim3((unsigned)(Np / 64), 4), dim3(1024), 0, s, parts, nparts,
+                       bias, dq_scale, q_zp, gelu, Np, table, y_scale, y_zp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || rows == 0) return e;
+    // rows a block: the fewest (a multiple of 8, at most 256) that keep the
+    // grid within the resident blocks, else 256
+    const long long slices = (Np + DQC_SLICE - 1) / DQC_SLICE;
+    const long long per = (rows * slices + DQC_RESIDENT - 1) / DQC_RESIDENT;
+    long long R = (per + 7) / 8 * 8;
+    R = R < 8 ? 8 : R > 8 * DQC_RPT ? 8 * DQC_RPT : R;
+    while (R < 8 * DQC_RPT && ((rows + R - 1) / R) * slices > DQC_RESIDENT) R += 8;
+    hipLaunchKernelGGL(dynq_codes_gather_kernel, dim3((unsigned)slices, (unsigned)((rows + R - 1) / R)),
+                       dim3(DQC_THREADS), 0, s, codes, rows, N, Np, (int)R, table, y);
     return hipGetLastError();
 }
 

@@ -125,6 +125,10 @@ struct GemmArgs {
     // fused dequantize: (min, max) of each (tile, wave)'s outputs, pair
     // 4 * tile + wave, for a DynamicQuantizeLinear that reads y (NULL: none)
     float* mm_parts;
+    // with mm_parts: the fp32 values feed only the (min, max) pairs, and y
+    // receives the uint8 QLinearMatMul bytes (same element strides) from
+    // which the DynamicQuantizeLinear rebuilds them per column
+    int dq_codes;
     // grouped fused-dequantize launch (QLinearMatMuls sharing A): batch index
     // z is the member, with its own combined scale, zero point, dequantize
     // scale and output; B and the per-column arrays advance by b_bstride /

@@ -122,8 +122,11 @@ __device__ __forceinline__ void block_barrier() {
 // epilogue fusions: none, QLinearAdd of a residual (RQ-B), DequantizeLinear
 // of the output plus a per-column fp32 bias (RQ-D), or a per-row term
 // row_coef[n] * (sum_k (a[m][k] - a_zp)) added to the int32 accumulator
-// (EPI_I32), the row sums taken from the A fragments on the way
-enum { FUSE_NONE = 0, FUSE_ADD = 1, FUSE_DQB = 2, FUSE_ROW = 3 };
+// (EPI_I32), the row sums taken from the A fragments on the way. FUSE_DQC:
+// the dequantize chain's values feed only its (min, max) pairs and the
+// uint8 RQ-D bytes are stored (GemmArgs::dq_codes)
+enum { FUSE_NONE = 0, FUSE_ADD = 1, FUSE_DQB = 2, FUSE_ROW = 3, FUSE_DQC = 4 };
+constexpr bool fuse_dq(int f) { return f == FUSE_DQB || f == FUSE_DQC; }
 
 template <int EPI>
 struct EpiParams;
@@ -162,7 +165,7 @@ constexpr int dma_pslot_bytes() {
 // per-column arrays staged per tile: the epilogue's, + the fp32 bias of a
 // fused dequantize, + the row-term coefficient
 template <int EPI, int FUSE>
-constexpr int dma_npx() { return EpiParams<EPI>::NP + (FUSE == FUSE_DQB || FUSE == FUSE_ROW ? 1 : 0); }
+constexpr int dma_npx() { return EpiParams<EPI>::NP + (fuse_dq(FUSE) || FUSE == FUSE_ROW ? 1 : 0); }
 // (KR > 0: the weights stay in registers, so a stage holds A rows only)
 template <int BM, int BN, int S, int NPX, int FUSE, int BK, int KR>
 constexpr int dma_lds_bytes() {
@@ -462,7 +465,7 @@ void qgemm_dma_kernel(GemmArgs g) {
             // call; lanes past the last array reload array 0 (never read back)
             const void* base0 = g.c0 ? (const void*)g.c0 : (const void*)g.colsum;
             const void* base;
-            if (FUSE == FUSE_DQB && arr == NP) base = g.dq_bias;
+            if (fuse_dq(FUSE) && arr == NP) base = g.dq_bias;
             else if (FUSE == FUSE_ROW && arr == NP) base = g.row_coef;
             else if (arr == 0 || arr >= NP) base = base0;
             else if (EPI == EPI_RQB) base = g.os;
@@ -534,7 +537,7 @@ void qgemm_dma_kernel(GemmArgs g) {
     // fp32 outputs of a fused epilogue (16 columns of one row): the Gelu
     // when fused, the running min / max for a DynamicQuantizeLinear that
     // reads them, then the store
-    auto store_f32 = [&](float (&o)[16], float* frow, bool full16, int nb) {
+    auto post_f32 = [&](float (&o)[16], bool full16, int nb) {
         if (g.dq_gelu) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[i] = gelu_erf(o[i]);
@@ -549,6 +552,9 @@ void qgemm_dma_kernel(GemmArgs g) {
                     mm_mx = fmaxf(mm_mx, o[i]);
                 }
         }
+    };
+    auto store_f32 = [&](float (&o)[16], float* frow, bool full16, int nb) {
+        post_f32(o, full16, nb);
         if (full16 && ((((uintptr_t)frow) & 15) == 0)) {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -838,14 +844,12 @@ void qgemm_dma_kernel(GemmArgs g) {
                         }
                     }
                 }
-                if constexpr (FUSE == FUSE_DQB) {
+                if constexpr (fuse_dq(FUSE)) {
                     // DequantizeLinear fl((q - zp) * s) (DequantizeLinear.cpp:133-152),
                     // then the fp32 Add of the column bias, written as fp32
                     const float zp_f = (float)yzp_t;
                     const float dqs = g.ngrp ? g.grp_dq_scale[z] : g.dq_scale;
                     const uint8_t* pb = ps + NP * BN * 4 + nl * 4;
-                    float* frow = (g.ngrp ? (float*)g.grp_y[z] : (float*)g.y + (long long)z * g.y_bstride) +
-                                  (long long)m * g.ldy + nb;
                     float o[16];
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
@@ -854,6 +858,20 @@ void qgemm_dma_kernel(GemmArgs g) {
                         const float d = (qf - zp_f) * dqs;
                         o[i] = d + *(const float*)(pb + 4 * i);
                     }
+                    if constexpr (FUSE == FUSE_DQC) {
+                        // the values only feed the (min, max) pairs; y gets
+                        // the bytes they were computed from (not grouped)
+                        post_f32(o, full16, nb);
+                        uint8_t* crow = (uint8_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
+                        if (full16 && ((((uintptr_t)crow) & 15) == 0))
+                            *(v4i*)crow = v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
+                        else
+                            store_bytes_prefix(crow, packed[0], packed[1], packed[2], packed[3],
+                                               g.N - nb < 16 ? g.N - nb : 16);
+                        continue;
+                    }
+                    float* frow = (g.ngrp ? (float*)g.grp_y[z] : (float*)g.y + (long long)z * g.y_bstride) +
+                                  (long long)m * g.ldy + nb;
                     store_f32(o, frow, full16, nb);
                     continue;
                 }
@@ -1008,7 +1026,7 @@ void qgemm_dma_kernel(GemmArgs g) {
             }
             if (FUSE == FUSE_ADD && g.add_conv_is_a) epilogue(std::true_type{});
             else epilogue(std::false_type{});
-            if (FUSE == FUSE_DQB && g.mm_parts) {
+            if (fuse_dq(FUSE) && g.mm_parts) {
                 // one (min, max) pair per (tile, wave), at 2 * (WAVES * tile + wave)
 #pragma unroll
                 for (int off = 32; off > 0; off >>= 1) {
@@ -1229,7 +1247,9 @@ template <int BM, int BN, int S, int AMODE, int S_ADD = S, int BK = 64>
 hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
     if (g.dq_bias) {
         if constexpr (AMODE == A_DENSE) {
-            if (g.epi == EPI_RQD) return launch_dma<BM, BN, S, AMODE, EPI_RQD, FUSE_DQB, BK>(g, batch, s);
+            if (g.epi == EPI_RQD)
+                return g.dq_codes ? launch_dma<BM, BN, S, AMODE, EPI_RQD, FUSE_DQC, BK>(g, batch, s)
+                                  : launch_dma<BM, BN, S, AMODE, EPI_RQD, FUSE_DQB, BK>(g, batch, s);
             if (g.epi == EPI_I32S) return launch_dma<BM, BN, S, AMODE, EPI_I32S, FUSE_DQB, BK>(g, batch, s);
         }
         return hipErrorNotSupported;

@@ -108,6 +108,14 @@ int nnr_ctx_set_conv_add(nnr_ctx_t c, int on) {
     });
 }
 
+int nnr_ctx_set_dynq_codes(nnr_ctx_t c, int on) {
+    return guarded("ctx_set_dynq_codes", [&]() -> int {
+        if (!c) return err("ctx is NULL");
+        c->ctx.enable_dynq_codes = on != 0;
+        return 0;
+    });
+}
+
 int nnr_ctx_load_onnx(nnr_ctx_t c, const void* data, size_t size, const char* model_dir, int sym_dim) {
     return guarded("ctx_load_onnx", [&]() -> int {
         if (!c || !data) return err("load_onnx: NULL argument");

@@ -461,6 +461,7 @@ bool context_t::prepare() {
         fuse_add_layernorm(this);
         fuse_dynq_minmax(this);
         fuse_matmul_group(this);
+        if (enable_dynq_codes) fuse_dynq_codes(this);
     }
     // 6. device memory and constant upload
     if (!plan_memory()) return false;

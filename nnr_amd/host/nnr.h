@@ -206,6 +206,14 @@ struct operator_t {
     int minmax_count = 0;
     // DynamicQuantizeLinear: the producer that writes its input's min / max
     operator_t* minmax_src = nullptr;
+    // fuse_dynq_codes: a producer with min / max pairs whose output is read
+    // only by a DynamicQuantizeLinear stores, instead of its fp32 values, the
+    // uint8 bytes they are computed from (set_codes_out; false: cannot), and
+    // quantize_codes writes the quantizer's three outputs from them
+    virtual bool set_codes_out(bool /*on*/) { return false; }
+    virtual bool quantize_codes(tensor_t* /*y*/, tensor_t* /*y_scale*/, tensor_t* /*y_zp*/) { return false; }
+    // DynamicQuantizeLinear: the producer holding its input as codes
+    operator_t* codes_src = nullptr;
     // operators of one kind reading the same input, run as one launch
     // (fuse_matmul_group): the leader launches for all of group_members; a
     // member's exec does nothing (its output is written by the leader, which
@@ -286,6 +294,9 @@ struct context_t {
     void* stream = nullptr;       // hipStream_t of every launch
     bool enable_fusion = true;
     bool enable_conv_add = true;  // fuse_conv_add / fuse_matmul_dq_bias after the operators are built
+    // fuse_dynq_codes (needs enable_conv_add): a fused FF1-style chain stores
+    // uint8 bytes for its DynamicQuantizeLinear instead of fp32 values
+    bool enable_dynq_codes = true;
     bool enable_profiling = false;
     // run() from its second call on replays the whole plan as one HIP graph
     // captured on a private stream (off while profiling; falls back to
@@ -342,6 +353,7 @@ void fuse_add_layernorm(context_t* ctx);
 void fuse_conv_maxpool(context_t* ctx);
 void fuse_matmul_group(context_t* ctx);
 void fuse_dynq_minmax(context_t* ctx);
+void fuse_dynq_codes(context_t* ctx);
 void fuse_attention(context_t* ctx);
 void fold_bn_qdq(context_t* ctx);
 

@@ -98,8 +98,9 @@ struct DynamicQuantizeLinear_hip : operator_t {
             return bad(this, nnrh_last_error());
         return true;
     }
-    std::string variant() const override { return minmax_src ? "MinMaxIn" : ""; }
+    std::string variant() const override { return codes_src ? "Codes" : minmax_src ? "MinMaxIn" : ""; }
     bool exec() override {
+        if (codes_src) return codes_src->quantize_codes(outputs[0], outputs[1], outputs[2]);
         if (minmax_src)
             return ok(this, nnrh_dynamic_quantize_linear_parts(
                                 (const float*)inputs[0]->data, inputs[0]->ndata, minmax_src->minmax_parts,
@@ -332,6 +333,7 @@ struct QLinearMatMul_hip : operator_t {
     nnrh_qmatmul_t h = nullptr;
     nnrh_qmatmul_group_t grp = nullptr;   // leader of a grouped launch
     int m = 0, n = 0, k = 0, batch = 1;
+    bool codes = false;   // set_codes_out: output 0 holds the uint8 bytes of the chain
     ~QLinearMatMul_hip() override {
         nnrh_qmatmul_group_destroy(grp);
         nnrh_qmatmul_destroy(h);
@@ -401,7 +403,18 @@ struct QLinearMatMul_hip : operator_t {
     bool set_minmax_out(float* parts, int pairs) override {
         return nnrh_qmatmul_set_minmax_out(h, parts, pairs) == NNRH_OK;
     }
-    bool groupable() const override { return h && fused_chain.size() == 2; }
+    bool set_codes_out(bool on) override {
+        if (!h || grp || group_leader || fused_chain.empty()) return false;
+        if (nnrh_qmatmul_set_codes_out(h, on ? 1 : 0) != NNRH_OK) return false;
+        codes = on;
+        return true;
+    }
+    bool quantize_codes(tensor_t* y, tensor_t* y_scale, tensor_t* y_zp) override {
+        return ok(this, nnrh_qmatmul_dynamic_quantize_codes(h, outputs[0]->data, batch, (uint8_t*)y->data,
+                                                            (float*)y_scale->data, (uint8_t*)y_zp->data,
+                                                            ctx->stream));
+    }
+    bool groupable() const override { return h && fused_chain.size() == 2 && !codes; }
     bool same_group_input(const operator_t* o) const override {
         return dynamic_cast<const QLinearMatMul_hip*>(o) && o->inputs[0] == inputs[0] &&
                o->inputs[1] == inputs[1] && o->inputs[2] == inputs[2];
@@ -423,6 +436,7 @@ struct QLinearMatMul_hip : operator_t {
         std::string v = fused_chain.size() > 2 ? "+DQ+Bias+Gelu" : "+DQ+Bias";
         if (grp) v += "+Group" + std::to_string(group_members.size() + 1);
         else if (group_leader) v += "(grouped)";
+        if (codes) v += "+Codes";
         return v;
     }
     bool exec() override {

@@ -27,6 +27,10 @@
 //                     input writes its min / max pairs as it stores it
 //   fuse_matmul_group no counterpart: fused-dequantize QLinearMatMuls reading
 //                     the same input run as one launch
+//   fuse_dynq_codes   no counterpart: a fused dequantize chain read only by
+//                     a DynamicQuantizeLinear stores its uint8 QLinearMatMul
+//                     bytes; the quantizer maps them through a per-column
+//                     table of the chain's quantized values (bit-identical)
 //   fuse_conv_maxpool no counterpart: the uint8 MaxPool reading a first-layer
 //                     QLinearConv's output runs in the conv's kernel, which
 //                     writes only the pooled tensor (bit-identical)
@@ -842,6 +846,40 @@ void fuse_dynq_minmax(context_t* ctx) {
         ++fused;
     }
     ctx->fusion_stats["dynq_minmax"] = fused;
+}
+
+// ---------------------------------------------------------------------------
+// DynamicQuantizeLinear reading min / max pairs from a producer whose output
+// it alone reads (no other operator, no fused chain, not a graph output): a
+// producer that can (a fused QLinearMatMul -> DequantizeLinear -> Add [->
+// Gelu], not grouped) stores the uint8 QLinearMatMul bytes instead of the
+// fp32 chain values, the tensor becomes uint8 (a quarter of the bytes), and
+// the quantizer rebuilds each value's byte from the bytes through a table per
+// column. Runs after fuse_dynq_minmax and fuse_matmul_group.
+void fuse_dynq_codes(context_t* ctx) {
+    std::unordered_set<tensor_t*> graph_out;
+    for (auto& name : ctx->graph_outputs)
+        if (tensor_t* t = ctx->find(name)) graph_out.insert(t);
+    std::unordered_map<tensor_t*, int> uses;
+    for (auto* op : ctx->nodes) {
+        if (op->folded) continue;
+        for (auto* t : op->inputs)
+            if (t) uses[t]++;
+        if (op->fused_other) uses[op->fused_other]++;
+    }
+    int fused = 0;
+    for (auto* op : ctx->nodes) {
+        if (!active(op) || op->op_type != "DynamicQuantizeLinear" || !op->minmax_src || op->codes_src) continue;
+        tensor_t* t = op->inputs[0];
+        if (!t || uses[t] != 1 || graph_out.count(t) || t->type != NNR_DATA_TYPE_FLOAT32) continue;
+        operator_t* p = op->minmax_src;
+        if (p->group_leader || !p->set_codes_out(true)) continue;
+        const std::vector<int> dims = t->dims;
+        t->reshape(dims, NNR_DATA_TYPE_UINT8);
+        op->codes_src = p;
+        ++fused;
+    }
+    ctx->fusion_stats["dynq_codes"] = fused;
 }
 
 // ---------------------------------------------------------------------------

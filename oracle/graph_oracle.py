@@ -22,9 +22,11 @@ def _erf(x):
     return erf(x)
 
 
-def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, skip_ops=()):
+def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, skip_ops=(), keep_chain=False):
     """plan: Session.plan(); fmt_of(name) -> 0/1 layout of a tensor.
-    Returns {tensor name: physical numpy array} of every produced tensor.
+    Returns {tensor name: physical numpy array} of every produced tensor
+    (keep_chain: also the tensors inside fused chains, e.g. the uint8 output
+    of a QLinearMatMul whose dequantize chain was fused into it).
 
     source: optional callable name -> array. When given, every node reads its
     non-constant inputs through it (e.g. the device's own tensors), so each
@@ -379,4 +381,6 @@ def run_plan(plan, graph, feeds: dict, fmt_of, stop_after=None, source=None, ski
         env.update(res)
         if stop_after and nd["name"] == stop_after:
             break
+    if keep_chain:
+        env.update(chain_env)
     return env

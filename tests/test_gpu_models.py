@@ -190,7 +190,12 @@ def check_graph_per_node(g, feeds, atol=1e-3, rtol=1e-3, **session_kw):
     """Every node of the executed plan, recomputed by the oracle from the
     device's own input tensors: int8 outputs bit-exact, fp32 outputs within
     the reference's tolerance. Used where fp32 nodes feed dynamic
-    quantization, so rounding noise must not propagate between nodes."""
+    quantization, so rounding noise must not propagate between nodes. The
+    fp32 tensors a fused chain would store as uint8 bytes for its
+    DynamicQuantizeLinear are materialized (dynq_codes off), so that the
+    quantizer is checked on the device's own fp32 input; test_bert_dynq_codes
+    checks the bytes path against this one."""
+    session_kw.setdefault("dynq_codes", False)
     s = G.Session(g, **session_kw)
     for k, v in feeds.items():
         s.set_input(k, v)
@@ -292,6 +297,56 @@ def test_bert_full_depth_seq128(dev):
     assert ops.count("DynamicQuantizeLinear") == 48
     assert n_int >= 48 * 2 and n_f32 >= 72
     assert len(exact_chains) == 5 * 12   # every fused chain without Gelu, bit for bit
+
+
+def test_bert_dynq_codes(dev):
+    """fuse_dynq_codes: each FF1 chain (QLinearMatMul -> DequantizeLinear ->
+    Add -> Gelu, read only by a DynamicQuantizeLinear) stores its uint8
+    QLinearMatMul bytes, and the quantizer rebuilds its outputs from them
+    through per-column tables. Against a context that materializes the fp32
+    tensor: every DynamicQuantizeLinear output (bytes, scale, zero point) and
+    every graph output bit-identical, on two inputs; the stored bytes equal
+    the oracle's QLinearMatMul bytes from the device's own inputs; the FF1
+    tensors take a quarter of the bytes."""
+    layers, B, S = 3, 2, 128
+    g = synth.bert(batch=B, seq=S, layers=layers)
+    rng = np.random.default_rng(37)
+    on, off = G.Session(g), G.Session(g, dynq_codes=False)
+    plan = on.plan()
+    codes = [p for p in plan if p["op"] == "QLinearMatMul" and p["variant"].endswith("+Codes")]
+    assert [p["variant"] for p in codes] == ["+DQ+Bias+Gelu+Codes"] * layers
+    dq = [p for p in plan if p["op"] == "DynamicQuantizeLinear"]
+    assert sum(p["variant"] == "Codes" for p in dq) == layers
+    assert not any("Codes" in p["variant"] for p in off.plan())
+    for p in codes:
+        t = p["outputs"][0]
+        assert on.tensor_info(t)[1] == np.uint8 and off.tensor_info(t)[1] == np.float32
+    assert on.device_bytes() < off.device_bytes()
+    for rep in range(2):
+        x = rng.uniform(-1.0, 1.0, (B, S, 768)).astype(np.float32)
+        for s in (on, off):
+            s.set_input("input", x)
+            s.run()
+        for p in dq:
+            for o in p["outputs"]:
+                a, b = np.atleast_1d(on.output(o)[0]), np.atleast_1d(off.output(o)[0])
+                assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (rep, p["name"], o)
+        for o in g.outputs:
+            assert np.array_equal(on.output(o)[0].view(np.uint8), off.output(o)[0].view(np.uint8)), (rep, o)
+    cache = {}
+
+    def dev_t(name):
+        if name not in cache:
+            cache[name] = on.output(name)[0]
+        return cache[name]
+
+    skip = {p["op"] for p in plan} - {"QLinearMatMul"}
+    env = graph_oracle.run_plan(plan, g, {"input": x}, lambda n: on.tensor_info(n)[3], source=dev_t,
+                                skip_ops=skip, keep_chain=True)
+    for p in codes:
+        q = g.node_by_name(p["fused_chain"][0]).inputs[0]
+        assert env[q].dtype == np.uint8
+        assert np.array_equal(dev_t(p["outputs"][0]), env[q]), p["name"]
 
 
 @pytest.mark.parametrize("layers,seq,fused", [(12, 128, True), (2, 64, False)])

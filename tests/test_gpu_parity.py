@@ -680,6 +680,83 @@ def test_qmatmul_fused_gelu_minmax(dev, m, n, batch):
     op.set_minmax_out(None)
 
 
+@pytest.mark.parametrize("m,n,batch,gelu", [(40, 136, 3, True), (8192 // 64, 3072, 2, True), (70, 64, 1, False),
+                                             (50, 320, 2, True), (33, 200, 2, False), (21, 131, 2, True)])
+def test_qmatmul_codes_dynamic_quantize(dev, m, n, batch, gelu):
+    """The fused QLinearMatMul -> DequantizeLinear -> + bias (-> Gelu) chain
+    in codes mode: a run stores the uint8 QLinearMatMul bytes (equal to the
+    unfused QLinearMatMul's) and the chain values' (min, max) pairs, and
+    DynamicQuantizeLinear from the bytes gives the bytes, scale and zero
+    point of DynamicQuantizeLinear over the fp32 chain output. Two inputs in a
+    row (the per-column table is rebuilt), N % 16 != 0 (ragged GEMM stores),
+    N % 4 != 0 (bytewise gather), a last column slice of 64, rows not a
+    multiple of the gather's 256."""
+    import torch
+    rng = np.random.default_rng(m * n + batch)
+    k = 96
+    b = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    bias = (rng.standard_normal(n) * 0.5).astype(np.float32)
+    ys, yz = 0.031, 121
+    s = torch.tensor([0.0133], dtype=torch.float32, device=dev)
+    z = torch.tensor([77], dtype=torch.uint8, device=dev)
+    plain = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, ys, yz, m=m)
+
+    def chain(codes):
+        op = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, ys, yz, m=m)
+        op.fuse_dq_bias(ys, yz, bias)
+        if gelu:
+            op.fuse_gelu()
+        cnt = op.minmax_count(batch)
+        parts = torch.full((2 * cnt,), float("nan"), dtype=torch.float32, device=dev)
+        op.set_minmax_out(parts)
+        if codes:
+            op.set_codes_out()
+        return op, parts
+
+    f32op, f32parts = chain(False)
+    cop, cparts = chain(True)
+    for rep in range(2):
+        a = to_dev(rng.integers(0, 256, (batch, m, k), dtype=np.uint8), dev)
+        q = to_np(plain(a, a_scale_dev=s, a_zp_dev=z))
+        f = f32op(a, a_scale_dev=s, a_zp_dev=z)
+        q0, s0, z0 = H.dynamic_quantize_linear_parts(f, f32parts)
+        c = cop(a, a_scale_dev=s, a_zp_dev=z)
+        assert c.dtype == torch.uint8 and tuple(c.shape) == (batch, m, n)
+        assert np.array_equal(to_np(c), q), rep
+        # the codes run's pairs are the fp32 run's (same values, same tiles)
+        assert np.array_equal(to_np(cparts), to_np(f32parts)), rep
+        q1, s1, z1 = cop.dynamic_quantize_codes(c)
+        assert to_np(s1)[0] == to_np(s0)[0] and to_np(z1)[0] == to_np(z0)[0], rep
+        mism = np.count_nonzero(to_np(q1) != to_np(q0))
+        assert mism == 0, f"rep {rep}: {mism} of {q1.numel()} bytes differ"
+    # back to fp32 output: the same bits as the fp32 handle
+    cop.set_codes_out(False)
+    assert np.array_equal(to_np(cop(a, a_scale_dev=s, a_zp_dev=z)).view(np.uint32), to_np(f).view(np.uint32))
+
+
+def test_qmatmul_codes_errors(dev):
+    """Codes mode needs the fused dequantize and the (min, max) pairs; the
+    quantize call needs codes mode."""
+    import torch
+    b = np.ones((64, 64), np.int8)
+    op = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, 0.03, 128, m=16)
+    with pytest.raises(H.NnrHipError):
+        op.set_codes_out()
+    op.fuse_dq_bias(0.03, 128, None)
+    with pytest.raises(H.NnrHipError):
+        op.set_codes_out()
+    c = torch.zeros((16, 64), dtype=torch.uint8, device=dev)
+    with pytest.raises(H.NnrHipError):
+        op.dynamic_quantize_codes(c)
+    parts = torch.zeros(2 * op.minmax_count(1), dtype=torch.float32, device=dev)
+    op.set_minmax_out(parts)
+    op.set_codes_out()
+    op.set_minmax_out(None)
+    a = torch.zeros((16, 64), dtype=torch.uint8, device=dev)
+    with pytest.raises(H.NnrHipError):   # codes without pairs
+        op(a)
+
+
 @pytest.mark.parametrize("rows,n,device_q", [(8192 // 64, 768, True), (200, 136, True), (77, 64, False)])
 def test_qmatmul_group(dev, rows, n, device_q):
     """Three fused-dequantize QLinearMatMuls reading the same A (different
