@@ -647,21 +647,33 @@ def run_bert(args, dev):
     assert checked == 6
     parity = (f"the first layer's {checked} {proj} projections recomputed by the oracle from the device's own "
               f"inputs on sequences {idx} of {B}: bit-exact (an fp32 Gelu chain end within 2e-6)")
-    codes = [p for p in plan if p["op"] == "DynamicQuantizeLinear" and p["variant"] == "Codes"]
-    if codes:
-        # the DynamicQuantizeLinears that rebuild their input from stored
-        # bytes, against a context that materializes the fp32 tensors (whose
-        # quantizer the per-node tests check): every layer, the whole batch
-        ref_s = G.Session(g, dynq_codes=False)
+    readers = [p for p in plan if "Codes" in p["variant"] and p["op"] != proj]
+    if readers:
+        # the operators that form their input from stored chain bytes
+        # (DynamicQuantizeLinear after FF1, the attention, the LayerNorms)
+        # and every quantizer and the graph output, against a context that
+        # materializes the fp32 tensors (whose operators the per-node tests
+        # check): every layer, the whole batch
+        ref_s = G.Session(g, codes=False)
         ref_s.set_input("input", x)
         ref_s.run()
-        for p in codes:
+        cmp = [p for p in plan if p["op"] in ("DynamicQuantizeLinear", "MultiHeadAttention", "LayerNormalization")]
+        n = 0
+        for p in cmp:
             for o in p["outputs"]:
+                if not o or s.tensor_info(o)[1] != ref_s.tensor_info(o)[1]:
+                    continue
                 a, b = np.atleast_1d(s.output(o)[0]), np.atleast_1d(ref_s.output(o)[0])
                 assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"parity gate failed at {p['name']}"
+                n += 1
+        for o in g.outputs:
+            assert np.array_equal(s.output(o)[0].view(np.uint8), ref_s.output(o)[0].view(np.uint8)), \
+                "parity gate failed at the graph output"
         del ref_s
-        parity += (f"; the {len(codes)} DynamicQuantizeLinears fed by stored FF1 bytes equal, bit for bit "
-                   f"over the whole batch, a context that materializes the fp32 FF1 output")
+        parity += (f"; with the projections storing uint8 bytes that {len(readers)} readers turn back into "
+                   f"values, the outputs of every quantizer, attention and LayerNorm ({n} tensors) and the "
+                   f"graph output equal, bit for bit over the whole batch, a context that materializes the "
+                   f"fp32 projection outputs")
     s, mem = planned_session(args, g, {"input": x}, s)
     ms = time_steps(s.run, args)
     mem["hip_graph"] = s.graph_active()

@@ -245,17 +245,25 @@ int nnrh_qmatmul_set_minmax_out(nnrh_qmatmul_t h, float* parts_dev, int capacity
  * nnrh_qmatmul_run write, instead of the float32 values, the uint8
  * QLinearMatMul bytes they are computed from (y then holds batch x m x n
  * bytes, same element layout) together with the values' (min, max) pairs.
+ * (Without _set_minmax_out, and without Gelu, the bytes serve the readers
+ * of nnrh_dq_codes below.)
  * nnrh_qmatmul_dynamic_quantize_codes then writes the DynamicQuantizeLinear
  * outputs (y, y_scale, y_zp of the run's batch) from those bytes: the chain
  * value of byte q in column j depends on (j, q) alone, so a per-column table
  * of the 256 quantized values (built after the pairs give the scale / zero
  * point) maps every byte, and the results equal running the chain and the
  * quantizer on the float32 values bit for bit. The handle owns the table
- * (256 x n rounded up to 64 bytes); a handle in codes mode serves one run at
- * a time (the table is rebuilt by each quantize call). on = 0 returns to
- * float32 output. No counterpart in the reference, which materializes the
- * float32 tensor between the operators.                                   */
+ * (256 x n rounded up to 64 bytes, allocated here when the pairs are set:
+ * call _set_minmax_out first); a handle in codes mode serves one run at a
+ * time (the table is rebuilt by each quantize call). A later fuse_dq_bias /
+ * fuse_gelu turns codes mode off; on = 0 returns to float32 output. No
+ * counterpart in the reference, which materializes the float32 tensor
+ * between the operators.                                                  */
 int nnrh_qmatmul_set_codes_out(nnrh_qmatmul_t h, int on);
+/* The chain's dequantize parameters for a reader of its bytes (no Gelu):
+ * zero point, scale and the handle's device bias vector (padded to a
+ * multiple of 64 columns, 16-byte aligned, valid while the handle lives). */
+int nnrh_qmatmul_dq_params(nnrh_qmatmul_t h, int* zp, float* dq_scale, const float** bias_dev);
 int nnrh_qmatmul_dynamic_quantize_codes(nnrh_qmatmul_t h, const void* codes_dev, int batch, uint8_t* y_dev,
                                         float* y_scale_dev, uint8_t* y_zp_dev, void* stream);
 /* 2..4 QLinearMatMuls, each with nnrh_qmatmul_fuse_dq_bias (no Gelu, no
@@ -271,6 +279,10 @@ typedef struct nnrh_qmatmul_group* nnrh_qmatmul_group_t;
 int nnrh_qmatmul_group_create(nnrh_qmatmul_group_t* h, const nnrh_qmatmul_t* members, int n);
 int nnrh_qmatmul_group_run(nnrh_qmatmul_group_t h, const void* a_dev, int rows, void* const* y_devs,
                            const float* a_scale_dev, const void* a_zp_dev, void* stream);
+/* The group's launch writes the members' uint8 QLinearMatMul bytes instead
+ * of their fp32 chain values (as nnrh_qmatmul_set_codes_out; the members'
+ * own handles give the readers their nnrh_qmatmul_dq_params).            */
+int nnrh_qmatmul_group_set_codes_out(nnrh_qmatmul_group_t h, int on);
 int nnrh_qmatmul_group_destroy(nnrh_qmatmul_group_t h);
 int nnrh_qmatmul_destroy(nnrh_qmatmul_t h);
 
@@ -474,6 +486,25 @@ int nnrh_multihead_attention_minmax_count(int B, int seq, int hidden, int num_he
 int nnrh_multihead_attention_f32(const float* q_dev, const float* k_dev, const float* v_dev, float* y_dev,
                                  int B, int seq, int hidden, int num_heads, float scale,
                                  float* minmax_parts_dev, void* workspace_dev, void* stream);
+/* A fused QLinearMatMul -> DequantizeLinear -> Add(bias) chain stored as its
+ * uint8 QLinearMatMul bytes (nnrh_qmatmul_set_codes_out, no Gelu): element
+ * j of a row, byte b, stands for fl(fl((b - zp) * scale) + bias[j]), which
+ * the readers below form exactly as the GEMM would have stored it. bias: the
+ * producer's device vector (nnrh_qmatmul_dq_params), 16-byte aligned. No
+ * counterpart in the reference, which materializes the fp32 tensor.      */
+typedef struct nnrh_dq_codes {
+    const uint8_t* codes_dev;
+    int zp;
+    float scale;
+    const float* bias_dev;
+} nnrh_dq_codes;
+/* nnrh_multihead_attention_f32's fused kernel (head size 64, seq <= 128;
+ * y 16-byte aligned, the byte tensors 4-byte aligned) with q, k, v given as
+ * chain bytes: the same y bit for bit as on their fp32 values; other shapes
+ * are rejected (NNRH_ERR_UNSUPPORTED).                                    */
+int nnrh_multihead_attention_codes_f32(const nnrh_dq_codes* q, const nnrh_dq_codes* k, const nnrh_dq_codes* v,
+                                       float* y_dev, int B, int seq, int hidden, int num_heads, float scale,
+                                       float* minmax_parts_dev, void* stream);
 /* No counterpart in the reference: DequantizeLinear (DequantizeLinear.cpp:
  * 133-152, per-tensor scale and zero point, uint8 or int8 x) feeding
  * GlobalAveragePool, in one pass over the 8-bit tensor. Each value is
@@ -513,6 +544,12 @@ int nnrh_layernorm_f32(const float* x_dev, const float* gamma_dev, const float* 
 int nnrh_add_layernorm_f32(const float* x_dev, const float* r_dev, const float* gamma_dev,
                            const float* beta_dev, float* y_dev, size_t rows, int D, float eps,
                            float* parts_dev, void* stream);
+/* nnrh_add_layernorm_f32 with x given as chain bytes (nnrh_dq_codes; its
+ * columns are the normalized axis): the same y and pairs bit for bit as on
+ * x's fp32 values.                                                        */
+int nnrh_add_layernorm_codes_f32(const nnrh_dq_codes* x, const float* r_dev, const float* gamma_dev,
+                                 const float* beta_dev, float* y_dev, size_t rows, int D, float eps,
+                                 float* parts_dev, void* stream);
 /* HardSwish, fp32 (src/backend/cpu/HardSwish.cpp:18-50): y = x * clamp(x/6 +
  * 0.5, 0, 1), the 16-wide body of the first n - n % 16 elements multiplying
  * by fl(1/6), the tail dividing by 6 (vec_ops_avx512.h:96-117). post_op: 1

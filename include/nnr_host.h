@@ -45,13 +45,16 @@ int nnr_ctx_set_fusion(nnr_ctx_t ctx, int on);
 /* fuse_conv_add (default on, needs fusion on): same-shape QLinearAdds run in
  * the epilogue of the QLinearConv producing one operand; results unchanged. */
 int nnr_ctx_set_conv_add(nnr_ctx_t ctx, int on);
-/* fuse_dynq_codes (default on, needs fusion and conv_add on; no counterpart
- * in the reference): a fused QLinearMatMul -> DequantizeLinear -> Add
- * [-> Gelu] chain whose fp32 result only a DynamicQuantizeLinear reads
- * stores the uint8 QLinearMatMul bytes instead (that tensor then reads back
- * as uint8), and the quantizer rebuilds its outputs from them bit for bit.
- * Off: the fp32 tensor is materialized. Set before prepare(). */
-int nnr_ctx_set_dynq_codes(nnr_ctx_t ctx, int on);
+/* fuse_dynq_codes and fuse_codes_readers (default on, need fusion and
+ * conv_add on; no counterpart in the reference): a fused QLinearMatMul ->
+ * DequantizeLinear -> Add [-> Gelu] chain whose fp32 result is read only by
+ * an operator that can form it from the chain's uint8 QLinearMatMul bytes
+ * (a DynamicQuantizeLinear; without Gelu also a LayerNormalization with its
+ * residual Add or the fused MultiHeadAttention) stores those bytes instead
+ * (that tensor then reads back as uint8), and the reader's outputs are the
+ * same bit for bit. Off: the fp32 tensors are materialized. Set before
+ * prepare(). */
+int nnr_ctx_set_codes(nnr_ctx_t ctx, int on);
 
 /* dtype: the reference's data_type_t (src/nnr.h:20-56): 1 FLOAT32, 3 FLOAT16,
  * 5 INT8, 6 INT16, 7 INT32, 8 INT64, 9 UINT8, 10 UINT16, 13 BOOL; other

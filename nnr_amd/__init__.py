@@ -214,6 +214,13 @@ class QLinearMatMul:
         check(lib().nnrh_qmatmul_set_codes_out(self.h, 1 if on else 0))
         self._codes = bool(on)
 
+    def dq_params(self):
+        """(zero point, scale, device bias pointer) of the fused chain, for a
+        reader of its bytes (dq_codes)."""
+        zp, sc, b = ct.c_int(), ct.c_float(), ct.c_void_p()
+        check(lib().nnrh_qmatmul_dq_params(self.h, ct.byref(zp), ct.byref(sc), ct.byref(b)))
+        return zp.value, sc.value, b.value
+
     def dynamic_quantize_codes(self, codes, stream=None):
         """(y, y_scale, y_zp) of DynamicQuantizeLinear over the chain values
         of a codes-mode run's output `codes` (its (min, max) pairs must be
@@ -282,6 +289,10 @@ class QLinearMatMulGroup:
         check(lib().nnrh_qmatmul_group_create(ct.byref(h), arr, len(members)))
         self.h = h
         self.n = members[0].n
+
+    def set_codes_out(self, on=True):
+        """The launch writes the members' uint8 QLinearMatMul bytes."""
+        check(lib().nnrh_qmatmul_group_set_codes_out(self.h, 1 if on else 0))
 
     def __call__(self, a, ys, a_scale_dev=None, a_zp_dev=None, stream=None):
         rows = a.numel() // a.shape[-1]
@@ -385,6 +396,39 @@ def layernorm(x, gamma, beta=None, eps=1e-5, r=None, parts=None):
     y = torch.empty_like(x)
     check(lib().nnrh_add_layernorm_f32(ptr(x), ptr(r), ptr(gamma), ptr(beta), ptr(y), x.numel() // D, D,
                                        float(eps), ptr(parts), cur_stream()))
+    return y
+
+
+def dq_codes(codes, op):
+    """nnrh_dq_codes for the bytes `codes` of fused QLinearMatMul `op`'s chain."""
+    from ._lib import DqCodes
+    zp, sc, b = op.dq_params()
+    return DqCodes(codes.data_ptr(), zp, sc, b)
+
+
+def layernorm_codes(xc, gamma, beta=None, eps=1e-5, r=None, parts=None):
+    """layernorm with x given as chain bytes: xc = (uint8 device tensor, the
+    QLinearMatMul whose chain they belong to)."""
+    import torch
+    codes, op = xc
+    D = codes.shape[-1]
+    y = torch.empty(tuple(codes.shape), dtype=torch.float32, device=codes.device)
+    d = dq_codes(codes, op)
+    check(lib().nnrh_add_layernorm_codes_f32(ct.byref(d), ptr(r), ptr(gamma), ptr(beta), ptr(y), codes.numel() // D,
+                                             D, float(eps), ptr(parts), cur_stream()))
+    return y
+
+
+def multihead_attention_codes(qc, kc, vc, num_heads, scale, parts=None):
+    """The fused attention on q, k, v given as chain bytes ((tensor, op)
+    pairs); y fp32 of the same [B][S][hidden] shape."""
+    import torch
+    codes = qc[0]
+    B, S, Hd = codes.shape
+    y = torch.empty((B, S, Hd), dtype=torch.float32, device=codes.device)
+    dq = [dq_codes(c, o) for c, o in (qc, kc, vc)]
+    check(lib().nnrh_multihead_attention_codes_f32(ct.byref(dq[0]), ct.byref(dq[1]), ct.byref(dq[2]), ptr(y), B, S,
+                                                   Hd, num_heads, float(scale), ptr(parts), cur_stream()))
     return y
 
 

@@ -33,6 +33,8 @@ EXPORTS = [
     "nnrh_multihead_attention_workspace", "nnrh_multihead_attention_f32", "nnrh_multihead_attention_minmax_count", "nnrh_qmatmul_create", "nnrh_qmatmul_run", "nnrh_qmatmul_destroy",
     "nnrh_qmatmul_fuse_dq_bias", "nnrh_qmatmul_fuse_gelu", "nnrh_qmatmul_minmax_count",
     "nnrh_qmatmul_set_minmax_out", "nnrh_qmatmul_set_codes_out", "nnrh_qmatmul_dynamic_quantize_codes",
+    "nnrh_qmatmul_dq_params", "nnrh_qmatmul_group_set_codes_out", "nnrh_add_layernorm_codes_f32",
+    "nnrh_multihead_attention_codes_f32",
     "nnrh_dynamic_quantize_linear_parts", "nnrh_add_layernorm_f32",
     "nnrh_qmatmul_group_create", "nnrh_qmatmul_group_run", "nnrh_qmatmul_group_destroy",
     "nnrh_qlinear_mul", "nnrh_qlinear_global_avgpool", "nnrh_qlinear_avgpool", "nnrh_qlinear_concat_part",
@@ -85,6 +87,10 @@ class MmiScaledDesc(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("m", "n", "k", "a_dtype", "b_dtype")] + [
         ("b_host", C.c_void_p), ("a_zp", C.c_int), ("b_zp", C.c_int), ("a_scale", C.c_float),
         ("w_scale_host", C.c_void_p), ("bias_host", C.c_void_p)]
+
+
+class DqCodes(C.Structure):
+    _fields_ = [("codes_dev", C.c_void_p), ("zp", C.c_int), ("scale", C.c_float), ("bias_dev", C.c_void_p)]
 
 
 _lib = None
@@ -150,6 +156,10 @@ def lib():
         "nnrh_qmatmul_minmax_count": (i, [vp, i, P(i)]),
         "nnrh_qmatmul_set_minmax_out": (i, [vp, vp, i]),
         "nnrh_qmatmul_set_codes_out": (i, [vp, i]),
+        "nnrh_qmatmul_dq_params": (i, [vp, P(i), P(f), P(vp)]),
+        "nnrh_qmatmul_group_set_codes_out": (i, [vp, i]),
+        "nnrh_add_layernorm_codes_f32": (i, [P(DqCodes), vp, vp, vp, vp, sz, i, f, vp, vp]),
+        "nnrh_multihead_attention_codes_f32": (i, [P(DqCodes), P(DqCodes), P(DqCodes), vp, i, i, i, i, f, vp, vp]),
         "nnrh_qmatmul_dynamic_quantize_codes": (i, [vp, vp, i, vp, vp, vp, vp]),
         "nnrh_qmatmul_group_create": (i, [P(vp), P(vp), i]),
         "nnrh_qmatmul_group_run": (i, [vp, vp, i, P(vp), vp, vp, vp]),

@@ -1208,6 +1208,7 @@ extern "C" int nnrh_qmatmul_fuse_dq_bias(nnrh_qmatmul_t h, float dq_scale, int d
     if (rc) return rc;
     h->g.dq_bias = h->dq_bias;
     h->g.dq_scale = dq_scale;
+    h->g.dq_codes = 0;   // the chain changed: codes mode is set again after it
     return NNRH_OK;
 }
 
@@ -1320,7 +1321,8 @@ extern "C" int nnrh_qmatmul_group_create(nnrh_qmatmul_group_t* out, const nnrh_q
                           h->d.scale_dtype == NNRH_F32 && g.dq_nobias == h0->g.dq_nobias &&
                           (g.epi != EPI_I32S || g.cm == h0->g.cm) &&
                           g.Np == h0->g.Np && g.Kp == h0->g.Kp && g.alpha == h0->g.alpha &&
-                          g.a_xor == h0->g.a_xor && g.beta == 0 && g.dq_bias && !g.dq_gelu && !g.mm_parts;
+                          g.a_xor == h0->g.a_xor && g.beta == 0 && g.dq_bias && !g.dq_gelu && !g.mm_parts &&
+                          !g.dq_codes;
         if (!same)
             return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_group_create: member %d differs in shape, types, "
                                                  "A quantization or fusions", i);
@@ -1340,6 +1342,7 @@ extern "C" int nnrh_qmatmul_group_create(nnrh_qmatmul_group_t* out, const nnrh_q
     GemmArgs& g = G->g;
     g = h0->g;
     g.c0_absmax = 0;
+    g.dq_codes = 0;   // nnrh_qmatmul_group_set_codes_out
     for (int i = 0; i < n; ++i) {
         const nnrh_qmatmul* h = hs[i];
         if (hipMemcpy(G->wpack + wsz * i, h->wpack, wsz, hipMemcpyDeviceToDevice) != hipSuccess ||
@@ -1396,6 +1399,14 @@ extern "C" int nnrh_qmatmul_group_run(nnrh_qmatmul_group_t G, const void* a, int
     return NNRH_OK;
 }
 
+extern "C" int nnrh_qmatmul_group_set_codes_out(nnrh_qmatmul_group_t G, int on) {
+    if (!G) return set_err(NNRH_ERR_INVALID, "qmatmul_group_set_codes_out: NULL group");
+    if (on && G->g.epi != EPI_RQD)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_group_set_codes_out: QLinearMatMul members only");
+    G->g.dq_codes = on ? 1 : 0;
+    return NNRH_OK;
+}
+
 extern "C" int nnrh_qmatmul_group_destroy(nnrh_qmatmul_group_t G) {
     delete G;
     return NNRH_OK;
@@ -1405,6 +1416,7 @@ extern "C" int nnrh_qmatmul_fuse_gelu(nnrh_qmatmul_t h) {
     if (!h) return set_err(NNRH_ERR_INVALID, "qmatmul_fuse_gelu: NULL handle");
     if (!h->g.dq_bias) return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_fuse_gelu: needs nnrh_qmatmul_fuse_dq_bias first");
     h->g.dq_gelu = 1;
+    h->g.dq_codes = 0;   // the chain changed: codes mode is set again after it
     return NNRH_OK;
 }
 
@@ -1442,14 +1454,24 @@ extern "C" int nnrh_qmatmul_set_codes_out(nnrh_qmatmul_t h, int on) {
         h->g.dq_codes = 0;
         return NNRH_OK;
     }
-    if (h->g.epi != EPI_RQD || !h->g.dq_bias || !h->g.mm_parts)
-        return set_err(NNRH_ERR_UNSUPPORTED,
-                       "qmatmul_set_codes_out: needs nnrh_qmatmul_fuse_dq_bias and nnrh_qmatmul_set_minmax_out first");
-    if (!h->codes_table) {
+    if (h->g.epi != EPI_RQD || !h->g.dq_bias)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_set_codes_out: needs nnrh_qmatmul_fuse_dq_bias first");
+    // the quantizer's table, when the run writes pairs for one
+    if (h->g.mm_parts && !h->codes_table) {
         int rc = nnrh_malloc((void**)&h->codes_table, dynamic_quantize_codes_table_bytes(h->g.Np));
         if (rc) return rc;
     }
     h->g.dq_codes = 1;
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_qmatmul_dq_params(nnrh_qmatmul_t h, int* zp, float* dq_scale, const float** bias_dev) {
+    if (!h || !zp || !dq_scale || !bias_dev) return set_err(NNRH_ERR_INVALID, "qmatmul_dq_params: NULL argument");
+    if (h->g.epi != EPI_RQD || !h->g.dq_bias || h->g.dq_gelu)
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_dq_params: needs nnrh_qmatmul_fuse_dq_bias (no Gelu)");
+    *zp = h->g.y_zp;
+    *dq_scale = h->g.dq_scale;
+    *bias_dev = h->dq_bias;
     return NNRH_OK;
 }
 
@@ -1459,7 +1481,8 @@ extern "C" int nnrh_qmatmul_dynamic_quantize_codes(nnrh_qmatmul_t h, const void*
         return set_err(NNRH_ERR_INVALID, "qmatmul_dynamic_quantize_codes: bad arguments");
     const GemmArgs& g = h->g;
     if (!g.dq_codes || !g.mm_parts || !h->codes_table)
-        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_dynamic_quantize_codes: needs nnrh_qmatmul_set_codes_out");
+        return set_err(NNRH_ERR_UNSUPPORTED, "qmatmul_dynamic_quantize_codes: needs nnrh_qmatmul_set_minmax_out, "
+                                             "then nnrh_qmatmul_set_codes_out");
     const long long nparts = qmatmul_parts(g, batch);
     if (nparts > h->parts_cap)
         return set_err(NNRH_ERR_INVALID, "qmatmul_dynamic_quantize_codes: %lld min/max pairs exceed the buffer's %d",
@@ -1509,8 +1532,6 @@ extern "C" int nnrh_qmatmul_run(nnrh_qmatmul_t h, const void* a, long long a_bst
     if (g.mm_parts && qmatmul_parts(g, batch) > h->parts_cap)
         return set_err(NNRH_ERR_INVALID, "qmatmul_run: %lld min/max pairs exceed the buffer's %d",
                        qmatmul_parts(g, batch), h->parts_cap);
-    if (g.dq_codes && !g.mm_parts)
-        return set_err(NNRH_ERR_INVALID, "qmatmul_run: uint8 codes out without min/max pairs");
     ProfScope ps("qgemm", s);
     HIP_TRY(launch_qgemm(g, batch, pick_tile(g.N), vec, s), "qgemm");
     return NNRH_OK;
@@ -2104,6 +2125,40 @@ extern "C" int nnrh_add_layernorm_f32(const float* x, const float* r, const floa
     ProfScope ps("layernorm_f32", S(stream));
     HIP_TRY(launch_layernorm_f32(x, r, gamma, beta, y, (long long)rows, D, eps, parts, S(stream)),
             "add_layernorm_f32");
+    return NNRH_OK;
+}
+
+static DqCodes dq_codes_arg(const nnrh_dq_codes* c) { return DqCodes{c->codes_dev, c->zp, c->scale, c->bias_dev}; }
+
+extern "C" int nnrh_add_layernorm_codes_f32(const nnrh_dq_codes* x, const float* r, const float* gamma,
+                                            const float* beta, float* y, size_t rows, int D, float eps, float* parts,
+                                            void* stream) {
+    if (!x || (rows && (!x->codes_dev || !x->bias_dev || !gamma || !y || D <= 0)))
+        return set_err(NNRH_ERR_INVALID, "add_layernorm_codes_f32: bad args");
+    if (parts && ((uintptr_t)parts & 7)) return set_err(NNRH_ERR_INVALID, "add_layernorm_codes_f32: parts alignment");
+    ProfScope ps("layernorm_f32", S(stream));
+    HIP_TRY(launch_layernorm_codes_f32(dq_codes_arg(x), r, gamma, beta, y, (long long)rows, D, eps, parts,
+                                       S(stream)),
+            "add_layernorm_codes_f32");
+    return NNRH_OK;
+}
+
+extern "C" int nnrh_multihead_attention_codes_f32(const nnrh_dq_codes* q, const nnrh_dq_codes* k,
+                                                  const nnrh_dq_codes* v, float* y, int B, int seq, int hidden,
+                                                  int num_heads, float scale, float* minmax_parts, void* stream) {
+    if (!q || !k || !v || !y || B < 0 || seq < 0 || !q->codes_dev || !k->codes_dev || !v->codes_dev ||
+        !q->bias_dev || !k->bias_dev || !v->bias_dev)
+        return set_err(NNRH_ERR_INVALID, "mha_codes: bad arguments");
+    const uintptr_t a4 = (uintptr_t)q->codes_dev | (uintptr_t)k->codes_dev | (uintptr_t)v->codes_dev;
+    const uintptr_t a16 = (uintptr_t)y | (uintptr_t)q->bias_dev | (uintptr_t)k->bias_dev | (uintptr_t)v->bias_dev;
+    if (!mha_fused_shape(seq, hidden, num_heads) || (a4 & 3) || (a16 & 15))
+        return set_err(NNRH_ERR_UNSUPPORTED, "mha_codes: the fused shapes (head size 64, seq <= 128) and alignment "
+                                             "only");
+    if (minmax_parts && ((uintptr_t)minmax_parts & 7)) return set_err(NNRH_ERR_INVALID, "mha_codes: parts alignment");
+    ProfScope ps("multihead_attention", S(stream));
+    HIP_TRY(launch_mha_codes_f32(dq_codes_arg(q), dq_codes_arg(k), dq_codes_arg(v), y, B, seq, hidden, num_heads,
+                                 scale, minmax_parts, S(stream)),
+            "mha_codes_f32");
     return NNRH_OK;
 }
 

@@ -5,6 +5,17 @@
 
 namespace nnrh {
 
+// A fused QLinearMatMul -> DequantizeLinear -> Add(bias) chain stored as its
+// uint8 QLinearMatMul bytes: the fp32 value of byte b in column n is
+// fl(fl((b - zp) * scale) + bias[n]), the GEMM epilogue's operations in its
+// order (bias padded past the last column, 16-byte aligned)
+struct DqCodes {
+    const uint8_t* q;
+    int zp;
+    float scale;
+    const float* bias;
+};
+
 hipError_t launch_gap_f32(const float* x, float* y, int N, int C, int HW, int x_nhwc,
                           hipStream_t s);
 // DequantizeLinear (uint8 or int8, per-tensor) fused into GlobalAveragePool
@@ -29,6 +40,9 @@ hipError_t launch_softmax_f32(const float* x, float* y, long long rows, int D, h
 // (min, max) pair of the outputs per row
 hipError_t launch_layernorm_f32(const float* x, const float* r, const float* gamma, const float* beta, float* y,
                                 long long rows, int D, float eps, float* parts, hipStream_t s);
+// the same with the first input given as chain bytes (columns = the D axis)
+hipError_t launch_layernorm_codes_f32(const DqCodes& x, const float* r, const float* gamma, const float* beta,
+                                      float* y, long long rows, int D, float eps, float* parts, hipStream_t s);
 hipError_t launch_cast_to_f32(const void* x, int dt, float* y, long long n, hipStream_t s);
 hipError_t launch_gelu_f32(const float* x, float* y, long long n, hipStream_t s);
 hipError_t launch_transpose_f32(const float* x, float* y, int ndim, const int* in_dims, const int* perm,
@@ -39,6 +53,10 @@ bool mha_fused_shape(int S, int Hd, int nh);
 bool mha_fused_ok(const float* q, const float* k, const float* v, const float* y, int S, int Hd, int nh);
 hipError_t launch_mha_f32(const float* q, const float* k, const float* v, float* y, int B, int S, int Hd, int nh,
                           float scale, float* parts, void* ws, hipStream_t s);
+// the fused kernel with q, k, v given as chain bytes (columns = the hidden
+// axis; 4-byte aligned, y 16-byte aligned, mha_fused_shape)
+hipError_t launch_mha_codes_f32(const DqCodes& q, const DqCodes& k, const DqCodes& v, float* y, int B, int S,
+                                int Hd, int nh, float scale, float* parts, hipStream_t s);
 // (min, max) pairs the fused kernel writes (4 per (batch, head)); 0 when the
 // shape takes the batched-GEMM path, which writes none
 int mha_minmax_pairs(int B, int S, int Hd, int nh);

@@ -510,10 +510,23 @@ __device__ __forceinline__ void ln_minmax_store(float mn, float mx, float* parts
     if (lane == 0) *(float2*)(parts + 2 * row) = make_float2(mn, mx);
 }
 
+// value of chain byte b in a column with bias bn (DqCodes)
+__device__ __forceinline__ float dq_codes_value(uint32_t b, float zp_f, float scale, float bn) {
+    const float d = ((float)b - zp_f) * scale;
+    return d + bn;
+}
+// 4 consecutive columns: bytes of one dword, their 4 biases
+__device__ __forceinline__ float4 dq_codes_value4(uint32_t w, float zp_f, float scale, float4 bn) {
+    return make_float4(dq_codes_value(w & 0xffu, zp_f, scale, bn.x), dq_codes_value((w >> 8) & 0xffu, zp_f, scale, bn.y),
+                       dq_codes_value((w >> 16) & 0xffu, zp_f, scale, bn.z), dq_codes_value(w >> 24, zp_f, scale, bn.w));
+}
+
 // the row in registers: V float4 per lane (D % 4 == 0, D <= 256 V, 16-byte
-// aligned rows); one read of x (and r), one write of y
-template <int V>
-__global__ __launch_bounds__(256) void layernorm_reg_kernel(const float* __restrict x, const float* __restrict r,
+// aligned rows; CODES: x given as chain bytes, 4-byte aligned rows); one
+// read of x (and r), one write of y
+template <int V, bool CODES>
+__global__ __launch_bounds__(256) void layernorm_reg_kernel(const float* __restrict x, DqCodes xq,
+                                                            const float* __restrict r,
                                                             const float* __restrict gamma,
                                                             const float* __restrict beta,
                                                             float* __restrict y, long long rows, int D,
@@ -523,6 +536,8 @@ __global__ __launch_bounds__(256) void layernorm_reg_kernel(const float* __restr
     if (row >= rows) return;
     const int D4 = D >> 2;
     const float4* xr = (const float4*)(x + row * D);
+    const uint32_t* xqr = (const uint32_t*)(xq.q + row * D);
+    const float zp_f = (float)xq.zp;
     const float4* rr = r ? (const float4*)(r + row * D) : nullptr;
     float4 v[V];
     float sum = 0.0f;
@@ -530,7 +545,8 @@ __global__ __launch_bounds__(256) void layernorm_reg_kernel(const float* __restr
     for (int j = 0; j < V; ++j) {
         const int c = lane + 64 * j;
         if (c < D4) {
-            v[j] = xr[c];
+            if constexpr (CODES) v[j] = dq_codes_value4(xqr[c], zp_f, xq.scale, ((const float4*)xq.bias)[c]);
+            else v[j] = xr[c];
             if (rr) {
                 const float4 t = rr[c];
                 v[j].x = v[j].x + t.x; v[j].y = v[j].y + t.y;
@@ -577,7 +593,9 @@ __global__ __launch_bounds__(256) void layernorm_reg_kernel(const float* __restr
 }
 
 // any D or alignment: three strided passes over the row
-__global__ __launch_bounds__(256) void layernorm_f32_kernel(const float* __restrict x, const float* __restrict r,
+template <bool CODES>
+__global__ __launch_bounds__(256) void layernorm_f32_kernel(const float* __restrict x, DqCodes xq,
+                                                            const float* __restrict r,
                                                             const float* __restrict gamma,
                                                             const float* __restrict beta,
                                                             float* __restrict y, long long rows, int D,
@@ -586,8 +604,14 @@ __global__ __launch_bounds__(256) void layernorm_f32_kernel(const float* __restr
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float* xr = x + row * D;
+    const uint8_t* xqr = xq.q + row * D;
+    const float zp_f = (float)xq.zp;
     const float* rr = r ? r + row * D : nullptr;
-    auto at = [&](int i) { return rr ? xr[i] + rr[i] : xr[i]; };
+    auto xv = [&](int i) {
+        if constexpr (CODES) return dq_codes_value(xqr[i], zp_f, xq.scale, xq.bias[i]);
+        else return xr[i];
+    };
+    auto at = [&](int i) { return rr ? xv(i) + rr[i] : xv(i); };
     float* yr = y + row * D;
     float sum = 0.0f;
     for (int i = lane; i < D; i += 64) sum += at(i);
@@ -611,26 +635,42 @@ __global__ __launch_bounds__(256) void layernorm_f32_kernel(const float* __restr
     if (parts) ln_minmax_store(mn, mx, parts, row, lane);
 }
 
-hipError_t launch_layernorm_f32(const float* x, const float* r, const float* gamma, const float* beta, float* y,
-                                long long rows, int D, float eps, float* parts, hipStream_t s) {
+template <bool CODES>
+static hipError_t launch_layernorm_any(const float* x, const DqCodes& xq, const float* r, const float* gamma,
+                                       const float* beta, float* y, long long rows, int D, float eps, float* parts,
+                                       hipStream_t s) {
     if (rows <= 0 || D <= 0) return hipSuccess;
     const dim3 grid((unsigned)((rows + 3) / 4));
-    const uintptr_t al = (uintptr_t)x | (uintptr_t)r | (uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)y;
+    const uintptr_t al = (uintptr_t)x | (uintptr_t)r | (uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)y |
+                         (CODES ? (uintptr_t)xq.bias : 0);
+    const bool q4 = !CODES || ((uintptr_t)xq.q & 3) == 0;
     const int v = (D + 255) / 256;
-    if ((D & 3) == 0 && (al & 15) == 0 && v <= 8) {
+    if ((D & 3) == 0 && (al & 15) == 0 && q4 && v <= 8) {
         switch (v) {
-#define NNRH_LN_CASE(V)                                                                                    \
-    case V:                                                                                                \
-        hipLaunchKernelGGL(layernorm_reg_kernel<V>, grid, dim3(256), 0, s, x, r, gamma, beta, y, rows, D, \
-                           eps, parts);                                                                    \
+#define NNRH_LN_CASE(V)                                                                                        \
+    case V:                                                                                                    \
+        hipLaunchKernelGGL((layernorm_reg_kernel<V, CODES>), grid, dim3(256), 0, s, x, xq, r, gamma, beta, y, \
+                           rows, D, eps, parts);                                                               \
         return hipGetLastError();
             NNRH_LN_CASE(1) NNRH_LN_CASE(2) NNRH_LN_CASE(3) NNRH_LN_CASE(4)
             NNRH_LN_CASE(5) NNRH_LN_CASE(6) NNRH_LN_CASE(7) NNRH_LN_CASE(8)
 #undef NNRH_LN_CASE
         }
     }
-    hipLaunchKernelGGL(layernorm_f32_kernel, grid, dim3(256), 0, s, x, r, gamma, beta, y, rows, D, eps, parts);
+    hipLaunchKernelGGL((layernorm_f32_kernel<CODES>), grid, dim3(256), 0, s, x, xq, r, gamma, beta, y, rows, D, eps,
+                       parts);
     return hipGetLastError();
+}
+
+hipError_t launch_layernorm_f32(const float* x, const float* r, const float* gamma, const float* beta, float* y,
+                                long long rows, int D, float eps, float* parts, hipStream_t s) {
+    return launch_layernorm_any<false>(x, DqCodes{nullptr, 0, 0.0f, nullptr}, r, gamma, beta, y, rows, D, eps, parts,
+                                       s);
+}
+
+hipError_t launch_layernorm_codes_f32(const DqCodes& xq, const float* r, const float* gamma, const float* beta,
+                                      float* y, long long rows, int D, float eps, float* parts, hipStream_t s) {
+    return launch_layernorm_any<true>(nullptr, xq, r, gamma, beta, y, rows, D, eps, parts, s);
 }
 
 // Gelu, erf form: 0.5 x (1 + erf(x / sqrt(2)))
@@ -740,8 +780,12 @@ constexpr int MHA_KP = 68;   // K row stride in LDS (floats): rows 16 bytes apar
 // parts (optional): one (min, max) pair per wave, at 2 (4 blockIdx.x + wave),
 // of the values the wave stores (0 stands in for nothing, as for every
 // producer that feeds a DynamicQuantizeLinear, whose range includes 0)
+// CODES: q, k, v given as chain bytes (DqCodes; columns = the hidden axis),
+// each element formed as the producing GEMM's epilogue would have stored it
+template <bool CODES>
 __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __restrict q, const float* __restrict k,
-                                                             const float* __restrict v, float* __restrict y,
+                                                             const float* __restrict v, DqCodes qq, DqCodes kq,
+                                                             DqCodes vq, float* __restrict y,
                                                              int S, int Hd, int nh, float scale,
                                                              float* __restrict parts) {
     // one buffer: K (row stride MHA_KP) for the scores, then V (stride 64)
@@ -750,10 +794,18 @@ __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __r
     const int b = blockIdx.x / nh, h = blockIdx.x - b * nh;
     const long long base = (long long)b * S * Hd + (long long)h * 64;
     const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    // 4 elements of row t, columns h * 64 + c .. + 3, of an input
+    auto load4 = [&](const float* x, const DqCodes& xq, long long off, int c) -> float4 {
+        if constexpr (CODES)
+            return dq_codes_value4(*(const uint32_t*)(xq.q + off), (float)xq.zp, xq.scale,
+                                   *(const float4*)(xq.bias + h * 64 + c));
+        else
+            return *(const float4*)(x + off);
+    };
     for (int i = threadIdx.x; i < 128 * 16; i += 256) {
         const int t = i >> 4, c = (i & 15) * 4;
         const long long off = base + (long long)t * Hd + c;
-        *(float4*)(ks + t * MHA_KP + c) = t < S ? *(const float4*)(k + off) : zero4;
+        *(float4*)(ks + t * MHA_KP + c) = t < S ? load4(k, kq, off, c) : zero4;
     }
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int lr = lane & 15, g = lane >> 4;
@@ -765,7 +817,7 @@ __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __r
         const int sq = s0 + 16 * ts + lr;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float4 t4 = sq < S ? *(const float4*)(q + base + (long long)sq * Hd + 16 * g + 4 * j) : zero4;
+            const float4 t4 = sq < S ? load4(q, qq, base + (long long)sq * Hd + 16 * g + 4 * j, 16 * g + 4 * j) : zero4;
             qf[ts][4 * j] = t4.x; qf[ts][4 * j + 1] = t4.y; qf[ts][4 * j + 2] = t4.z; qf[ts][4 * j + 3] = t4.w;
         }
     }
@@ -826,7 +878,7 @@ __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __r
     for (int i = threadIdx.x; i < 128 * 16; i += 256) {
         const int t = i >> 4, c = (i & 15) * 4;
         const long long off = base + (long long)t * Hd + c;
-        *(float4*)(vs + t * 64 + c) = t < S ? *(const float4*)(v + off) : zero4;
+        *(float4*)(vs + t * 64 + c) = t < S ? load4(v, vq, off, c) : zero4;
     }
     __syncthreads();
     if (!active) {   // (after the last barrier)
@@ -878,6 +930,17 @@ __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __r
     }
 }
 
+hipError_t launch_mha_codes_f32(const DqCodes& q, const DqCodes& k, const DqCodes& v, float* y, int B, int S,
+                                int Hd, int nh, float scale, float* parts, hipStream_t s) {
+    if (B <= 0 || S <= 0) return hipSuccess;
+    const uintptr_t a4 = (uintptr_t)q.q | (uintptr_t)k.q | (uintptr_t)v.q;
+    const uintptr_t a16 = (uintptr_t)y | (uintptr_t)q.bias | (uintptr_t)k.bias | (uintptr_t)v.bias;
+    if (!mha_fused_shape(S, Hd, nh) || (a4 & 3) || (a16 & 15)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mha_fused_hd64_kernel<true>, dim3((unsigned)(B * nh)), dim3(256), 0, s, nullptr, nullptr,
+                       nullptr, q, k, v, y, S, Hd, nh, scale, parts);
+    return hipGetLastError();
+}
+
 int mha_minmax_pairs(int B, int S, int Hd, int nh) {
     if (!mha_fused_shape(S, Hd, nh) || B <= 0) return 0;
     const long long p = 4LL * B * nh;
@@ -896,8 +959,9 @@ hipError_t launch_mha_f32(const float* q, const float* k, const float* v, float*
     if (B <= 0 || S <= 0) return hipSuccess;
     if (nh <= 0 || Hd % nh) return hipErrorInvalidValue;
     if (mha_fused_ok(q, k, v, y, S, Hd, nh)) {
-        hipLaunchKernelGGL(mha_fused_hd64_kernel, dim3((unsigned)(B * nh)), dim3(256), 0, s, q, k, v, y, S, Hd, nh,
-                           scale, parts);
+        const DqCodes none{nullptr, 0, 0.0f, nullptr};
+        hipLaunchKernelGGL(mha_fused_hd64_kernel<false>, dim3((unsigned)(B * nh)), dim3(256), 0, s, q, k, v, none,
+                           none, none, y, S, Hd, nh, scale, parts);
         return hipGetLastError();
     }
     if (parts) return hipErrorInvalidValue;   // only the fused kernel writes min / max pairs

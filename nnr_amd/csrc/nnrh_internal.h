@@ -125,9 +125,9 @@ struct GemmArgs {
     // fused dequantize: (min, max) of each (tile, wave)'s outputs, pair
     // 4 * tile + wave, for a DynamicQuantizeLinear that reads y (NULL: none)
     float* mm_parts;
-    // with mm_parts: the fp32 values feed only the (min, max) pairs, and y
-    // receives the uint8 QLinearMatMul bytes (same element strides) from
-    // which the DynamicQuantizeLinear rebuilds them per column
+    // fused dequantize: y receives the uint8 QLinearMatMul bytes (same
+    // element strides) instead of the fp32 values, which the reader forms
+    // from them per column; the values still feed mm_parts when it is set
     int dq_codes;
     // grouped fused-dequantize launch (QLinearMatMuls sharing A): batch index
     // z is the member, with its own combined scale, zero point, dequantize

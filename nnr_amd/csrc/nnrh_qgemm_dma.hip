@@ -123,8 +123,8 @@ __device__ __forceinline__ void block_barrier() {
 // of the output plus a per-column fp32 bias (RQ-D), or a per-row term
 // row_coef[n] * (sum_k (a[m][k] - a_zp)) added to the int32 accumulator
 // (EPI_I32), the row sums taken from the A fragments on the way. FUSE_DQC:
-// the dequantize chain's values feed only its (min, max) pairs and the
-// uint8 RQ-D bytes are stored (GemmArgs::dq_codes)
+// the dequantize chain stores the uint8 RQ-D bytes (GemmArgs::dq_codes); its
+// values are formed only for the (min, max) pairs, when those are written
 enum { FUSE_NONE = 0, FUSE_ADD = 1, FUSE_DQB = 2, FUSE_ROW = 3, FUSE_DQC = 4 };
 constexpr bool fuse_dq(int f) { return f == FUSE_DQB || f == FUSE_DQC; }
 
@@ -586,7 +586,7 @@ void qgemm_dma_kernel(GemmArgs g) {
         // a grouped launch: member z's combined scale, zero point, output
         float cm_t = cm;
         int yzp_t = g.y_zp;
-        if (FUSE == FUSE_DQB && g.ngrp) {
+        if (fuse_dq(FUSE) && g.ngrp) {
             cm_t = g.grp_cm[z];
             if (g.cm_a_scale_dev) {
                 const float t1 = a_scale_dev * g.grp_cm_b[z];
@@ -851,18 +851,25 @@ void qgemm_dma_kernel(GemmArgs g) {
                     const float dqs = g.ngrp ? g.grp_dq_scale[z] : g.dq_scale;
                     const uint8_t* pb = ps + NP * BN * 4 + nl * 4;
                     float o[16];
+                    auto chain_values = [&]() {
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        // uint8 output (checked on the host)
-                        const float qf = (float)((packed[i >> 2] >> (8 * (i & 3))) & 0xffu);
-                        const float d = (qf - zp_f) * dqs;
-                        o[i] = d + *(const float*)(pb + 4 * i);
-                    }
+                        for (int i = 0; i < 16; ++i) {
+                            // uint8 output (checked on the host)
+                            const float qf = (float)((packed[i >> 2] >> (8 * (i & 3))) & 0xffu);
+                            const float d = (qf - zp_f) * dqs;
+                            o[i] = d + *(const float*)(pb + 4 * i);
+                        }
+                    };
                     if constexpr (FUSE == FUSE_DQC) {
-                        // the values only feed the (min, max) pairs; y gets
-                        // the bytes they were computed from (not grouped)
-                        post_f32(o, full16, nb);
-                        uint8_t* crow = (uint8_t*)g.y + (long long)z * g.y_bstride + (long long)m * g.ldy + nb;
+                        // y gets the bytes; the values are formed only for
+                        // the (min, max) pairs (the reader of the bytes
+                        // forms them itself)
+                        if (g.mm_parts) {
+                            chain_values();
+                            post_f32(o, full16, nb);
+                        }
+                        uint8_t* crow = (g.ngrp ? (uint8_t*)g.grp_y[z] : (uint8_t*)g.y + (long long)z * g.y_bstride) +
+                                        (long long)m * g.ldy + nb;
                         if (full16 && ((((uintptr_t)crow) & 15) == 0))
                             *(v4i*)crow = v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
                         else
@@ -870,6 +877,7 @@ void qgemm_dma_kernel(GemmArgs g) {
                                                g.N - nb < 16 ? g.N - nb : 16);
                         continue;
                     }
+                    chain_values();
                     float* frow = (g.ngrp ? (float*)g.grp_y[z] : (float*)g.y + (long long)z * g.y_bstride) +
                                   (long long)m * g.ldy + nb;
                     store_f32(o, frow, full16, nb);

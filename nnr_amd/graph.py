@@ -48,7 +48,7 @@ def host_lib():
             "nnr_ctx_set_graph": (i, [vp, i]),
             "nnr_ctx_graph_active": (i, [vp, P(i)]),
             "nnr_ctx_set_conv_add": (i, [vp, i]),
-            "nnr_ctx_set_dynq_codes": (i, [vp, i]),
+            "nnr_ctx_set_codes": (i, [vp, i]),
             "nnr_ctx_add_initializer": (i, [vp, cp, i, P(i), i, vp]),
             "nnr_ctx_add_input": (i, [vp, cp, i, P(i), i]),
             "nnr_ctx_add_output": (i, [vp, cp]),
@@ -168,14 +168,15 @@ class Session:
     """A prepared C++ context_t for `graph` with the HIP backend preferred."""
 
     def __init__(self, graph: Graph | None, stream=None, fusion=True, device=True, conv_add=True,
-                 memory_planning=False, onnx=None, sym_dim=0, hip_graph=True, dynq_codes=True):
+                 memory_planning=False, onnx=None, sym_dim=0, hip_graph=True, codes=True):
         """graph: the in-process description, built into the context through
         the C ABI. onnx: instead, an ONNX model -- a file path (external data
         relative to it) or ModelProto bytes -- loaded by the C++ loader;
         sym_dim: the value of symbolic input dimensions (0: 1). hip_graph:
         from the second run() on, replay the plan as one captured HIP graph.
-        dynq_codes: a fused dequantize chain read only by a
-        DynamicQuantizeLinear stores its uint8 QLinearMatMul bytes (that
+        codes: a fused dequantize chain read only by an operator that can
+        form its values from the uint8 QLinearMatMul bytes (DynamicQuantizeLinear,
+        LayerNormalization, MultiHeadAttention) stores those bytes (that
         tensor reads back as uint8) instead of its fp32 values."""
         L = host_lib()
         self.L = L
@@ -190,7 +191,7 @@ class Session:
         _chk(L.nnr_ctx_set_fusion(h, 1 if fusion else 0))
         _chk(L.nnr_ctx_set_graph(h, 1 if hip_graph else 0))
         _chk(L.nnr_ctx_set_conv_add(h, 1 if conv_add else 0))
-        _chk(L.nnr_ctx_set_dynq_codes(h, 1 if dynq_codes else 0))
+        _chk(L.nnr_ctx_set_codes(h, 1 if codes else 0))
         _chk(L.nnr_ctx_set_memory_planning(h, 1 if memory_planning else 0))
         if onnx is not None:
             if isinstance(onnx, (bytes, bytearray)):

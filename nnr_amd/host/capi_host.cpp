@@ -108,10 +108,10 @@ int nnr_ctx_set_conv_add(nnr_ctx_t c, int on) {
     });
 }
 
-int nnr_ctx_set_dynq_codes(nnr_ctx_t c, int on) {
-    return guarded("ctx_set_dynq_codes", [&]() -> int {
+int nnr_ctx_set_codes(nnr_ctx_t c, int on) {
+    return guarded("ctx_set_codes", [&]() -> int {
         if (!c) return err("ctx is NULL");
-        c->ctx.enable_dynq_codes = on != 0;
+        c->ctx.enable_codes = on != 0;
         return 0;
     });
 }

@@ -461,7 +461,10 @@ bool context_t::prepare() {
         fuse_add_layernorm(this);
         fuse_dynq_minmax(this);
         fuse_matmul_group(this);
-        if (enable_dynq_codes) fuse_dynq_codes(this);
+        if (enable_codes) {
+            fuse_dynq_codes(this);
+            fuse_codes_readers(this);
+        }
     }
     // 6. device memory and constant upload
     if (!plan_memory()) return false;

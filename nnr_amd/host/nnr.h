@@ -212,8 +212,17 @@ struct operator_t {
     // quantize_codes writes the quantizer's three outputs from them
     virtual bool set_codes_out(bool /*on*/) { return false; }
     virtual bool quantize_codes(tensor_t* /*y*/, tensor_t* /*y_scale*/, tensor_t* /*y_zp*/) { return false; }
-    // DynamicQuantizeLinear: the producer holding its input as codes
+    // a reader of a producer's chain bytes (DynamicQuantizeLinear,
+    // LayerNormalization): that producer
     operator_t* codes_src = nullptr;
+    // fuse_codes_readers: this operator's byte input `which` (its own
+    // numbering) will hold the uint8 bytes of producer p's fused dequantize
+    // chain, whose meaning p->codes_params gives; false: it cannot read them
+    // (nothing recorded). p NULL clears what was recorded.
+    virtual bool set_codes_input(int /*which*/, operator_t* /*p*/) { return false; }
+    // a fused QLinearMatMul -> DequantizeLinear -> Add(bias) chain (no Gelu):
+    // its zero point, scale and device bias vector
+    virtual bool codes_params(int* /*zp*/, float* /*scale*/, const float** /*bias*/) const { return false; }
     // operators of one kind reading the same input, run as one launch
     // (fuse_matmul_group): the leader launches for all of group_members; a
     // member's exec does nothing (its output is written by the leader, which
@@ -294,9 +303,9 @@ struct context_t {
     void* stream = nullptr;       // hipStream_t of every launch
     bool enable_fusion = true;
     bool enable_conv_add = true;  // fuse_conv_add / fuse_matmul_dq_bias after the operators are built
-    // fuse_dynq_codes (needs enable_conv_add): a fused FF1-style chain stores
-    // uint8 bytes for its DynamicQuantizeLinear instead of fp32 values
-    bool enable_dynq_codes = true;
+    // fuse_dynq_codes / fuse_codes_readers (need enable_conv_add): fused
+    // dequantize chains store uint8 bytes for readers that form the values
+    bool enable_codes = true;
     bool enable_profiling = false;
     // run() from its second call on replays the whole plan as one HIP graph
     // captured on a private stream (off while profiling; falls back to
@@ -354,6 +363,7 @@ void fuse_conv_maxpool(context_t* ctx);
 void fuse_matmul_group(context_t* ctx);
 void fuse_dynq_minmax(context_t* ctx);
 void fuse_dynq_codes(context_t* ctx);
+void fuse_codes_readers(context_t* ctx);
 void fuse_attention(context_t* ctx);
 void fold_bn_qdq(context_t* ctx);
 

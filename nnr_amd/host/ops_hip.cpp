@@ -404,10 +404,18 @@ struct QLinearMatMul_hip : operator_t {
         return nnrh_qmatmul_set_minmax_out(h, parts, pairs) == NNRH_OK;
     }
     bool set_codes_out(bool on) override {
-        if (!h || grp || group_leader || fused_chain.empty()) return false;
-        if (nnrh_qmatmul_set_codes_out(h, on ? 1 : 0) != NNRH_OK) return false;
+        if (!h || fused_chain.empty()) return false;
+        if (group_leader && group_leader != this) {
+            codes = on;   // its bytes come from the leader's launch
+            return true;
+        }
+        const int rc = grp ? nnrh_qmatmul_group_set_codes_out(grp, on ? 1 : 0) : nnrh_qmatmul_set_codes_out(h, on ? 1 : 0);
+        if (rc != NNRH_OK) return false;
         codes = on;
         return true;
+    }
+    bool codes_params(int* zp, float* scale, const float** bias) const override {
+        return h && nnrh_qmatmul_dq_params(h, zp, scale, bias) == NNRH_OK;
     }
     bool quantize_codes(tensor_t* y, tensor_t* y_scale, tensor_t* y_zp) override {
         return ok(this, nnrh_qmatmul_dynamic_quantize_codes(h, outputs[0]->data, batch, (uint8_t*)y->data,
@@ -1406,11 +1414,40 @@ struct MultiHeadAttention_hip : operator_t {
         return c;
     }
     bool set_minmax_out(float*, int) override { return true; }
+    // q, k, v as chain bytes (fuse_codes_readers): the fused head-64 kernel's
+    // shapes only (those with (min, max) pairs); used when all three are set
+    nnrh_dq_codes cq[3] = {};
+    int ncodes = 0;
+    bool set_codes_input(int which, operator_t* p) override {
+        if (which < 0 || which > 2) return false;
+        if (!p) {
+            if (cq[which].bias_dev) --ncodes;
+            cq[which] = nnrh_dq_codes{};
+            return true;
+        }
+        int zp = 0;
+        float sc = 0.0f;
+        const float* b = nullptr;
+        if (cq[which].bias_dev || minmax_pairs() <= 0 || !p->codes_params(&zp, &sc, &b)) return false;
+        cq[which] = nnrh_dq_codes{nullptr, zp, sc, b};
+        ++ncodes;
+        return true;
+    }
+    std::string variant() const override { return ncodes == 3 ? "Codes" : ""; }
     bool exec() override {
         tensor_t* q = inputs[0];
         const int B = q->dims[0], S = q->dims[1], Hd = q->dims[2];
         // contrib op default: 1 / sqrt(head_dim)
         const float sc = scale != 0.0f ? scale : 1.0f / sqrtf((float)(Hd / num_heads));
+        if (ncodes == 3) {
+            nnrh_dq_codes c[3];
+            for (int i = 0; i < 3; ++i) {
+                c[i] = cq[i];
+                c[i].codes_dev = (const uint8_t*)inputs[i]->data;
+            }
+            return ok(this, nnrh_multihead_attention_codes_f32(&c[0], &c[1], &c[2], (float*)outputs[0]->data, B, S,
+                                                               Hd, num_heads, sc, minmax_parts, ctx->stream));
+        }
         return ok(this, nnrh_multihead_attention_f32((const float*)q->data, (const float*)inputs[1]->data,
                                                      (const float*)inputs[2]->data, (float*)outputs[0]->data, B, S,
                                                      Hd, num_heads, sc, minmax_parts, ws, ctx->stream));
@@ -1445,11 +1482,45 @@ struct LayerNormalization_hip : operator_t {
         return rows <= 0x7fffffff ? (int)rows : 0;
     }
     bool set_minmax_out(float*, int) override { return true; }
-    std::string variant() const override { return fused_other ? "+Add" : ""; }
+    // one operand as chain bytes (fuse_codes_readers): 0 the normalized
+    // input, 1 the residual Add's other operand
+    int codes_which = -1;
+    nnrh_dq_codes cq{};
+    bool set_codes_input(int which, operator_t* p) override {
+        if (!p) {
+            codes_src = nullptr;
+            codes_which = -1;
+            return true;
+        }
+        int zp = 0;
+        float sc = 0.0f;
+        const float* b = nullptr;
+        if (codes_src || which < 0 || which > 1 || (which == 1 && !fused_other) || !p->codes_params(&zp, &sc, &b))
+            return false;
+        cq = nnrh_dq_codes{nullptr, zp, sc, b};
+        codes_src = p;
+        codes_which = which;
+        return true;
+    }
+    std::string variant() const override {
+        return std::string(fused_other ? "+Add" : "") + (codes_src ? (fused_other ? "+Codes" : "Codes") : "");
+    }
     bool exec() override {
         tensor_t* x = inputs[0];
         tensor_t* bias = in(this, 2);
         const int D = x->dims.back();
+        if (codes_src) {
+            // the sum fl(a + b) is the same either way round
+            tensor_t* ct = codes_which == 0 ? x : fused_other;
+            tensor_t* other = codes_which == 0 ? fused_other : x;
+            nnrh_dq_codes c = cq;
+            c.codes_dev = (const uint8_t*)ct->data;
+            return ok(this, nnrh_add_layernorm_codes_f32(&c, other ? (const float*)other->data : nullptr,
+                                                         (const float*)inputs[1]->data,
+                                                         bias ? (const float*)bias->data : nullptr,
+                                                         (float*)outputs[0]->data, ct->ndata / D, D,
+                                                         attribute_f("epsilon", 1e-5f), minmax_parts, ctx->stream));
+        }
         return ok(this, nnrh_add_layernorm_f32((const float*)x->data,
                                                fused_other ? (const float*)fused_other->data : nullptr,
                                                (const float*)inputs[1]->data,

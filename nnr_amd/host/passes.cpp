@@ -31,6 +31,10 @@
 //                     a DynamicQuantizeLinear stores its uint8 QLinearMatMul
 //                     bytes; the quantizer maps them through a per-column
 //                     table of the chain's quantized values (bit-identical)
+//   fuse_codes_readers no counterpart: a fused dequantize chain (no Gelu)
+//                     read only by a LayerNormalization (with its residual
+//                     Add) or by the fused attention stores its bytes, from
+//                     which the reader forms the values (bit-identical)
 //   fuse_conv_maxpool no counterpart: the uint8 MaxPool reading a first-layer
 //                     QLinearConv's output runs in the conv's kernel, which
 //                     writes only the pooled tensor (bit-identical)
@@ -880,6 +884,106 @@ void fuse_dynq_codes(context_t* ctx) {
         ++fused;
     }
     ctx->fusion_stats["dynq_codes"] = fused;
+}
+
+// ---------------------------------------------------------------------------
+// fp32 results of fused QLinearMatMul -> DequantizeLinear -> Add(bias)
+// chains (no Gelu) whose only reader at run time can form each value from the
+// chain's uint8 QLinearMatMul byte with the GEMM epilogue's two operations:
+// a LayerNormalization (either operand of its residual Add), or the fused
+// MultiHeadAttention (q, k and v together, from ungrouped chains or from one
+// grouped launch of exactly those three). The chains store their bytes, the
+// tensors become uint8 (a quarter of the bytes), the readers record the
+// chains' parameters. Runs after fuse_dynq_codes.
+void fuse_codes_readers(context_t* ctx) {
+    std::unordered_set<tensor_t*> graph_out;
+    for (auto& name : ctx->graph_outputs)
+        if (tensor_t* t = ctx->find(name)) graph_out.insert(t);
+    // readers at run time: the active operators' inputs and fused operands
+    std::unordered_map<tensor_t*, int> uses;
+    std::unordered_map<tensor_t*, operator_t*> producer;
+    for (auto* op : ctx->nodes) {
+        if (!active(op)) continue;
+        for (auto* t : op->inputs)
+            if (t) uses[t]++;
+        if (op->fused_other) uses[op->fused_other]++;
+        if (!op->outputs.empty() && op->outputs[0]) producer[op->outputs[0]] = op;
+    }
+    // the chain producing t, when t can be stored as its bytes for one reader
+    auto chain_of = [&](tensor_t* t) -> operator_t* {
+        if (!t || t->type != NNR_DATA_TYPE_FLOAT32 || graph_out.count(t) || uses[t] != 1) return nullptr;
+        auto it = producer.find(t);
+        if (it == producer.end()) return nullptr;
+        operator_t* p = it->second;
+        int zp = 0;
+        float sc = 0.0f;
+        const float* b = nullptr;
+        if (p->op_type != "QLinearMatMul" || p->fused_chain.size() != 2 || !p->codes_params(&zp, &sc, &b))
+            return nullptr;
+        return p;
+    };
+    auto to_bytes = [](tensor_t* t) {
+        const std::vector<int> dims = t->dims;
+        t->reshape(dims, NNR_DATA_TYPE_UINT8);
+    };
+    int ln = 0, mha = 0;
+    for (auto* op : ctx->nodes) {
+        if (!active(op)) continue;
+        if (op->op_type == "LayerNormalization") {
+            tensor_t* cand[2] = {op->inputs[0], op->fused_other};
+            for (int w = 0; w < 2; ++w) {
+                operator_t* p = chain_of(cand[w]);
+                if (!p || p->group_leader || !op->set_codes_input(w, p)) continue;
+                if (!p->set_codes_out(true)) {
+                    op->set_codes_input(w, nullptr);
+                    continue;
+                }
+                to_bytes(cand[w]);
+                ++ln;
+                break;
+            }
+        } else if (op->op_type == "MultiHeadAttention" && op->inputs.size() >= 3) {
+            operator_t* ps[3];
+            bool all = op->inputs[0] != op->inputs[1] && op->inputs[0] != op->inputs[2] &&
+                       op->inputs[1] != op->inputs[2];
+            for (int i = 0; i < 3; ++i) {
+                ps[i] = chain_of(op->inputs[i]);
+                all = all && ps[i];
+            }
+            if (!all) continue;
+            operator_t* lead = ps[0]->group_leader;
+            if (lead) {
+                // one launch writes exactly these three
+                std::unordered_set<operator_t*> grp(lead->group_members.begin(), lead->group_members.end());
+                grp.insert(lead);
+                bool same = grp.size() == 3;
+                for (int i = 0; i < 3; ++i) same = same && ps[i]->group_leader == lead && grp.count(ps[i]);
+                if (!same) continue;
+            } else if (ps[1]->group_leader || ps[2]->group_leader) {
+                continue;
+            }
+            int rec = 0;
+            while (rec < 3 && op->set_codes_input(rec, ps[rec])) ++rec;
+            bool good = rec == 3;
+            // the launch that writes the bytes first: the group's leader
+            std::vector<operator_t*> order;
+            if (lead) order.push_back(lead);
+            for (int i = 0; i < 3; ++i)
+                if (ps[i] != lead) order.push_back(ps[i]);
+            size_t set = 0;
+            while (good && set < order.size() && order[set]->set_codes_out(true)) ++set;
+            good = good && set == order.size();
+            if (!good) {
+                for (size_t i = 0; i < set; ++i) order[i]->set_codes_out(false);
+                for (int i = 0; i < rec; ++i) op->set_codes_input(i, nullptr);
+                continue;
+            }
+            for (int i = 0; i < 3; ++i) to_bytes(op->inputs[i]);
+            ++mha;
+        }
+    }
+    ctx->fusion_stats["codes_layernorm"] = ln;
+    ctx->fusion_stats["codes_attention"] = mha;
 }
 
 // ---------------------------------------------------------------------------

@@ -734,27 +734,136 @@ def test_qmatmul_codes_dynamic_quantize(dev, m, n, batch, gelu):
     assert np.array_equal(to_np(cop(a, a_scale_dev=s, a_zp_dev=z)).view(np.uint32), to_np(f).view(np.uint32))
 
 
+def _chain_pair(dev, rng, m, n, k=96, batch=1):
+    """A fused QLinearMatMul -> DequantizeLinear -> + bias chain twice: one
+    handle writing fp32 values, one writing its uint8 bytes (no pairs), on
+    the same A; returns (fp32 output, bytes, bytes handle)."""
+    import torch
+    b = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    bias = (rng.standard_normal(n) * 0.5).astype(np.float32)
+    ys, yz = float(rng.uniform(0.01, 0.05)), int(rng.integers(90, 160))
+    s = torch.tensor([0.0133], dtype=torch.float32, device=dev)
+    z = torch.tensor([77], dtype=torch.uint8, device=dev)
+    a = to_dev(rng.integers(0, 256, (batch, m, k), dtype=np.uint8), dev)
+    f32op = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, ys, yz, m=m)
+    f32op.fuse_dq_bias(ys, yz, bias)
+    cop = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, ys, yz, m=m)
+    cop.fuse_dq_bias(ys, yz, bias)
+    cop.set_codes_out()
+    f = f32op(a, a_scale_dev=s, a_zp_dev=z)
+    c = cop(a, a_scale_dev=s, a_zp_dev=z)
+    assert c.dtype == torch.uint8
+    return f, c, cop
+
+
+@pytest.mark.parametrize("rows,D,side", [(256, 768, 0), (96, 768, 1), (40, 130, 0), (33, 130, 1), (64, 200, 2)])
+def test_layernorm_codes(dev, rows, D, side):
+    """LayerNormalization (with its residual Add) reading one operand as the
+    uint8 bytes of a fused dequantize chain: the output and the (min, max)
+    pairs equal, bit for bit, those of the fp32 kernel on the chain's fp32
+    values (side 0: the normalized input, 1: the residual operand, 2: no
+    residual). D = 130: the strided kernel (rows not 4-byte aligned)."""
+    import torch
+    rng = np.random.default_rng(rows * D + side)
+    f, c, cop = _chain_pair(dev, rng, rows, D)
+    f, c = f.reshape(rows, D), c.reshape(rows, D)
+    gamma = to_dev(rng.uniform(0.5, 1.5, D).astype(np.float32), dev)
+    beta = to_dev(rng.standard_normal(D).astype(np.float32), dev)
+    r = None if side == 2 else to_dev(rng.standard_normal((rows, D)).astype(np.float32), dev)
+    p0 = torch.full((2 * rows,), float("nan"), dtype=torch.float32, device=dev)
+    p1 = torch.full((2 * rows,), float("nan"), dtype=torch.float32, device=dev)
+    if side == 1:
+        y0 = H.layernorm(r, gamma, beta, r=f, parts=p0)
+        y1 = H.layernorm_codes((c, cop), gamma, beta, r=r, parts=p1)
+    else:
+        y0 = H.layernorm(f, gamma, beta, r=r, parts=p0)
+        y1 = H.layernorm_codes((c, cop), gamma, beta, r=r, parts=p1)
+    assert np.array_equal(to_np(y1).view(np.uint32), to_np(y0).view(np.uint32))
+    assert np.array_equal(to_np(p1).view(np.uint32), to_np(p0).view(np.uint32))
+
+
+@pytest.mark.parametrize("B,S", [(3, 128), (2, 77)])
+def test_mha_codes(dev, B, S):
+    """The fused attention reading q, k and v as the uint8 bytes of three
+    fused dequantize chains: y and its (min, max) pairs equal, bit for bit,
+    those of the fp32 kernel on the chains' fp32 values."""
+    import ctypes as C
+    import torch
+    from nnr_amd import _lib
+    heads, hidden = 12, 768
+    rng = np.random.default_rng(B * S)
+    fq, cq, oq = _chain_pair(dev, rng, S, hidden, batch=B)
+    fk, ck, ok_ = _chain_pair(dev, rng, S, hidden, batch=B)
+    fv, cv, ov = _chain_pair(dev, rng, S, hidden, batch=B)
+    scale = 0.125
+    pairs = 4 * B * heads
+    p0 = torch.full((2 * pairs,), float("nan"), dtype=torch.float32, device=dev)
+    p1 = torch.full((2 * pairs,), float("nan"), dtype=torch.float32, device=dev)
+    y0 = torch.empty((B, S, hidden), dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().nnrh_multihead_attention_f32(_lib.ptr(fq), _lib.ptr(fk), _lib.ptr(fv), _lib.ptr(y0), B, S,
+                                                       hidden, heads, scale, _lib.ptr(p0), None, _lib.cur_stream()))
+    y1 = H.multihead_attention_codes((cq, oq), (ck, ok_), (cv, ov), heads, scale, parts=p1)
+    assert np.array_equal(to_np(y1).view(np.uint32), to_np(y0).view(np.uint32))
+    assert np.array_equal(to_np(p1).view(np.uint32), to_np(p0).view(np.uint32))
+    # other shapes are refused
+    with pytest.raises(H.NnrHipError):
+        H.multihead_attention_codes((cq, oq), (ck, ok_), (cv, ov), 6, scale)
+
+
+def test_qmatmul_group_codes(dev):
+    """A grouped launch of three fused-dequantize QLinearMatMuls in codes
+    mode writes each member's uint8 QLinearMatMul bytes: those of the member
+    run unfused."""
+    import torch
+    rng = np.random.default_rng(57)
+    rows, k, n = 300, 96, 768
+    a = to_dev(rng.integers(0, 256, (rows, k), dtype=np.uint8), dev)
+    s = torch.tensor([0.0173], dtype=torch.float32, device=dev)
+    z = torch.tensor([119], dtype=torch.uint8, device=dev)
+    members, plain = [], []
+    for i in range(3):
+        b = rng.integers(-127, 128, (k, n), dtype=np.int8)
+        bias = rng.standard_normal(n).astype(np.float32)
+        ys, yz = [0.031, 0.047, 0.022][i], [121, 90, 140][i]
+        op = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, ys, yz, m=rows)
+        op.fuse_dq_bias(ys, yz, bias)
+        members.append(op)
+        plain.append(to_np(H.QLinearMatMul(b, 1.0, 0, 0.004, 0, ys, yz, m=rows)(a, a_scale_dev=s, a_zp_dev=z)))
+    g = H.QLinearMatMulGroup(members)
+    g.set_codes_out()
+    ys_ = [torch.empty((rows, n), dtype=torch.uint8, device=dev) for _ in range(3)]
+    g(a, ys_, a_scale_dev=s, a_zp_dev=z)
+    for i in range(3):
+        assert np.array_equal(to_np(ys_[i]), plain[i]), i
+
+
 def test_qmatmul_codes_errors(dev):
-    """Codes mode needs the fused dequantize and the (min, max) pairs; the
-    quantize call needs codes mode."""
+    """Codes mode needs the fused dequantize; the quantize call needs the
+    pairs, then codes mode; a later fusion turns codes mode off; readers'
+    parameters exist for chains without Gelu only."""
     import torch
     b = np.ones((64, 64), np.int8)
     op = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, 0.03, 128, m=16)
-    with pytest.raises(H.NnrHipError):
+    with pytest.raises(H.NnrHipError):   # no fused dequantize
         op.set_codes_out()
+    with pytest.raises(H.NnrHipError):
+        op.dq_params()
     op.fuse_dq_bias(0.03, 128, None)
-    with pytest.raises(H.NnrHipError):
-        op.set_codes_out()
+    op.set_codes_out()
     c = torch.zeros((16, 64), dtype=torch.uint8, device=dev)
-    with pytest.raises(H.NnrHipError):
+    with pytest.raises(H.NnrHipError):   # the quantizer needs the pairs
         op.dynamic_quantize_codes(c)
     parts = torch.zeros(2 * op.minmax_count(1), dtype=torch.float32, device=dev)
     op.set_minmax_out(parts)
+    with pytest.raises(H.NnrHipError):   # ... set before codes mode
+        op.dynamic_quantize_codes(c)
     op.set_codes_out()
-    op.set_minmax_out(None)
-    a = torch.zeros((16, 64), dtype=torch.uint8, device=dev)
-    with pytest.raises(H.NnrHipError):   # codes without pairs
-        op(a)
+    op.dynamic_quantize_codes(c)
+    op.fuse_gelu()   # a later fusion turns codes mode off
+    with pytest.raises(H.NnrHipError):
+        op.dynamic_quantize_codes(c)
+    with pytest.raises(H.NnrHipError):   # no parameters for readers of a Gelu chain
+        op.dq_params()
 
 
 @pytest.mark.parametrize("rows,n,device_q", [(8192 // 64, 768, True), (200, 136, True), (77, 64, False)])
