@@ -753,6 +753,9 @@ def _chain_pair(dev, rng, m, n, k=96, batch=1):
     f = f32op(a, a_scale_dev=s, a_zp_dev=z)
     c = cop(a, a_scale_dev=s, a_zp_dev=z)
     assert c.dtype == torch.uint8
+    # the bytes are the unfused QLinearMatMul's
+    q = H.QLinearMatMul(b, 1.0, 0, 0.004, 0, ys, yz, m=m)(a, a_scale_dev=s, a_zp_dev=z)
+    assert np.array_equal(to_np(c), to_np(q))
     return f, c, cop
 
 
