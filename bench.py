@@ -683,7 +683,7 @@ def run_bert(args, dev):
     is_mm = lambda r: r["op"] == proj
     # the members of a grouped Q / K / V launch run inside their leader's
     # launch: their work counts, their (empty) launches do not
-    grouped = sum(1 for r in rows if is_mm(r) and r["variant"].endswith("(grouped)"))
+    grouped = sum(1 for r in rows if is_mm(r) and "(grouped)" in r["variant"])
     rl, mm_ms = family_roofline(rows, is_mm, kprof, extra_launches=-grouped)
     mm_ops = sum(r["ops"] for r in rows if is_mm(r))
     rl["kernel"] = f"qgemm_dma_kernel ({proj} family)"

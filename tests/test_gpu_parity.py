@@ -553,6 +553,8 @@ def test_maxpool(dev, C, k, st, pad):
                                    (37, 70, 320),     # the small-GEMM kernel: 5 K chunks over 4 waves
                                    (5, 3, 64),        # one chunk, clamped rows / columns
                                    (600, 1030, 77),   # general kernel, many tiles, ragged M / N / K
+                                   (37, 70, 1344),    # 21 K chunks over 4 waves
+                                   (256, 1000, 1280),  # MobileNetV2's classifier
                                    (256, 1000, 2048)])  # ResNet-50's classifier
 @pytest.mark.parametrize("ta,tb,c_mode", [(0, 1, 2), (0, 0, 0), (1, 0, 1), (1, 1, 3), (0, 1, 4)])
 def test_gemm_f32(dev, ta, tb, c_mode, M, N, K):
