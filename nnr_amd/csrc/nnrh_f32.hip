@@ -802,10 +802,31 @@ __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __r
         else
             return *(const float4*)(x + off);
     };
-    for (int i = threadIdx.x; i < 128 * 16; i += 256) {
-        const int t = i >> 4, c = (i & 15) * 4;
-        const long long off = base + (long long)t * Hd + c;
-        *(float4*)(ks + t * MHA_KP + c) = t < S ? load4(k, kq, off, c) : zero4;
+    // K: all 8 of a thread's 16-byte pieces in flight before the LDS writes
+    {
+        float4 kv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = threadIdx.x + 256 * j;
+            const int t = i >> 4, c = (i & 15) * 4;
+            kv[j] = t < S ? load4(k, kq, base + (long long)t * Hd + c, c) : zero4;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = threadIdx.x + 256 * j;
+            *(float4*)(ks + (i >> 4) * MHA_KP + (i & 15) * 4) = kv[j];
+        }
+    }
+    // CODES: V's bytes (4 per dword, 8 dwords a thread) load now, with K's
+    // and Q's, and become values only when V takes the LDS buffer
+    uint32_t vpre[CODES ? 8 : 1];
+    if constexpr (CODES) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = threadIdx.x + 256 * j;
+            const int t = i >> 4, c = (i & 15) * 4;
+            vpre[j] = t < S ? *(const uint32_t*)(vq.q + base + (long long)t * Hd + c) : 0u;
+        }
     }
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int lr = lane & 15, g = lane >> 4;
@@ -875,10 +896,21 @@ __global__ __launch_bounds__(256, 3) void mha_fused_hd64_kernel(const float* __r
     }
     // every wave's scores are done with K: V takes the buffer
     __syncthreads();
-    for (int i = threadIdx.x; i < 128 * 16; i += 256) {
-        const int t = i >> 4, c = (i & 15) * 4;
-        const long long off = base + (long long)t * Hd + c;
-        *(float4*)(vs + t * 64 + c) = t < S ? load4(v, vq, off, c) : zero4;
+    if constexpr (CODES) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = threadIdx.x + 256 * j;
+            const int t = i >> 4, c = (i & 15) * 4;
+            *(float4*)(vs + t * 64 + c) =
+                t < S ? dq_codes_value4(vpre[j], (float)vq.zp, vq.scale, *(const float4*)(vq.bias + h * 64 + c))
+                      : zero4;
+        }
+    } else {
+        for (int i = threadIdx.x; i < 128 * 16; i += 256) {
+            const int t = i >> 4, c = (i & 15) * 4;
+            const long long off = base + (long long)t * Hd + c;
+            *(float4*)(vs + t * 64 + c) = t < S ? load4(v, vq, off, c) : zero4;
+        }
     }
     __syncthreads();
     if (!active) {   // (after the last barrier)
