@@ -539,8 +539,9 @@ int nnrh_layernorm_f32(const float* x_dev, const float* gamma_dev, const float* 
 /* LayerNormalization of fl(x + r) (r_dev NULL: of x): a same-shape fp32 Add
  * (src/backend/cpu/binary_math.cpp) folded into the normalization, so the
  * sum is never stored. parts_dev (NULL: none) receives one (min, max) pair
- * of the outputs per row, for nnrh_dynamic_quantize_linear_parts. No
- * counterpart in the reference, which runs Add and LayerNormalization.   */
+ * of the outputs per group of 4 rows (rows 4i .. 4i+3 -> pair i, ceil(rows
+ * / 4) pairs), for nnrh_dynamic_quantize_linear_parts. No counterpart in the
+ * reference, which runs Add and LayerNormalization.                      */
 int nnrh_add_layernorm_f32(const float* x_dev, const float* r_dev, const float* gamma_dev,
                            const float* beta_dev, float* y_dev, size_t rows, int D, float eps,
                            float* parts_dev, void* stream);

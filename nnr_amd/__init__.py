@@ -390,7 +390,8 @@ def dynamic_quantize_linear_parts(x, parts):
 
 def layernorm(x, gamma, beta=None, eps=1e-5, r=None, parts=None):
     """LayerNormalization over the last axis of x (of x + r when r is given);
-    parts: optional float32 device tensor receiving one (min, max) per row."""
+    parts: optional float32 device tensor receiving one (min, max) per group
+    of 4 rows."""
     import torch
     D = x.shape[-1]
     y = torch.empty_like(x)

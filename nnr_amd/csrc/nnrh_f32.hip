@@ -495,19 +495,27 @@ hipError_t launch_softmax_f32(const float* x, float* y, long long rows, int D, h
     return hipGetLastError();
 }
 
-// LayerNormalization over rows of D (one wave per row): mean, then the mean
-// of squared deviations, then (v - mean) * inv * gamma (+ beta). With `r` the
-// row is fl(x + r) of two same-shape inputs (a residual Add folded in), the
-// same bits the Add would have stored. With `parts`, pair 2 * row receives
-// the (min, max) of the row's outputs (0 when smaller / larger), for a
-// DynamicQuantizeLinear that reads y.
-__device__ __forceinline__ void ln_minmax_store(float mn, float mx, float* parts, long long row, int lane) {
+// LayerNormalization over rows of D (one wave per row, 4 rows a block):
+// mean, then the mean of squared deviations, then (v - mean) * inv * gamma
+// (+ beta). With `r` the row is fl(x + r) of two same-shape inputs (a
+// residual Add folded in), the same bits the Add would have stored. With
+// `parts`, pair i receives the (min, max) of the outputs of rows 4 i .. 4 i
+// + 3 (0 when smaller / larger), for a DynamicQuantizeLinear that reads y.
+// Every wave of the block reaches the pairs' barrier (a wave past the last
+// row brings the pair (0, 0)).
+__device__ __forceinline__ void ln_minmax_store(float mn, float mx, float* parts, int lane) {
+    __shared__ float2 wp[4];
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         mn = fminf(mn, __shfl_xor(mn, off, 64));
         mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     }
-    if (lane == 0) *(float2*)(parts + 2 * row) = make_float2(mn, mx);
+    if (lane == 0) wp[threadIdx.x >> 6] = make_float2(mn, mx);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *(float2*)(parts + 2 * blockIdx.x) =
+            make_float2(fminf(fminf(wp[0].x, wp[1].x), fminf(wp[2].x, wp[3].x)),
+                        fmaxf(fmaxf(wp[0].y, wp[1].y), fmaxf(wp[2].y, wp[3].y)));
 }
 
 // value of chain byte b in a column with bias bn (DqCodes)
@@ -533,8 +541,8 @@ __global__ __launch_bounds__(256) void layernorm_reg_kernel(const float* __restr
                                                             float eps, float* __restrict parts) {
     const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const int D4 = D >> 2;
+    const bool live = row < rows;   // (a wave past the last row still takes the pairs' barrier)
+    const int D4 = live ? D >> 2 : 0;
     const float4* xr = (const float4*)(x + row * D);
     const uint32_t* xqr = (const uint32_t*)(xq.q + row * D);
     const float zp_f = (float)xq.zp;
@@ -589,7 +597,7 @@ __global__ __launch_bounds__(256) void layernorm_reg_kernel(const float* __restr
             mx = fmaxf(mx, fmaxf(fmaxf(o.x, o.y), fmaxf(o.z, o.w)));
         }
     }
-    if (parts) ln_minmax_store(mn, mx, parts, row, lane);
+    if (parts) ln_minmax_store(mn, mx, parts, lane);
 }
 
 // any D or alignment: three strided passes over the row
@@ -602,7 +610,8 @@ __global__ __launch_bounds__(256) void layernorm_f32_kernel(const float* __restr
                                                             float eps, float* __restrict parts) {
     const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
+    const bool live = row < rows;   // (a wave past the last row still takes the pairs' barrier)
+    const int Dl = live ? D : 0;
     const float* xr = x + row * D;
     const uint8_t* xqr = xq.q + row * D;
     const float zp_f = (float)xq.zp;
@@ -614,25 +623,25 @@ __global__ __launch_bounds__(256) void layernorm_f32_kernel(const float* __restr
     auto at = [&](int i) { return rr ? xv(i) + rr[i] : xv(i); };
     float* yr = y + row * D;
     float sum = 0.0f;
-    for (int i = lane; i < D; i += 64) sum += at(i);
+    for (int i = lane; i < Dl; i += 64) sum += at(i);
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
     const float mean = sum / (float)D;
     float sq = 0.0f;
-    for (int i = lane; i < D; i += 64) {
+    for (int i = lane; i < Dl; i += 64) {
         const float d = at(i) - mean;
         sq += d * d;
     }
     for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
     const float inv = 1.0f / sqrtf(sq / (float)D + eps);
     float mn = 0.0f, mx = 0.0f;
-    for (int i = lane; i < D; i += 64) {
+    for (int i = lane; i < Dl; i += 64) {
         float v = (at(i) - mean) * inv * gamma[i];
         if (beta) v = v + beta[i];
         yr[i] = v;
         mn = fminf(mn, v);
         mx = fmaxf(mx, v);
     }
-    if (parts) ln_minmax_store(mn, mx, parts, row, lane);
+    if (parts) ln_minmax_store(mn, mx, parts, lane);
 }
 
 template <bool CODES>

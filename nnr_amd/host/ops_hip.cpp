@@ -1475,11 +1475,11 @@ struct LayerNormalization_hip : operator_t {
     bool fuse_residual_input(operator_t* add) override {
         return add->outputs[0] == inputs[0] && !fused_other;
     }
-    // one pair per row
+    // one pair per 4 rows
     int minmax_pairs() const override {
         const tensor_t* x = inputs[0];
-        const size_t rows = x->ndata / (size_t)x->dims.back();
-        return rows <= 0x7fffffff ? (int)rows : 0;
+        const size_t groups = (x->ndata / (size_t)x->dims.back() + 3) / 4;
+        return groups <= 0x7fffffff ? (int)groups : 0;
     }
     bool set_minmax_out(float*, int) override { return true; }
     // one operand as chain bytes (fuse_codes_readers): 0 the normalized

@@ -918,8 +918,8 @@ def test_qmatmul_group(dev, rows, n, device_q):
 def test_add_layernorm(dev, rows, D, res, beta):
     """LayerNormalization of x (+ r), register-resident (D % 4 == 0, D <= 2048)
     and strided rows, against a float64 restatement of LayerNormalization.cpp;
-    the per-row (min, max) pairs are the exact extremes of each output row,
-    and DynamicQuantizeLinear from them matches the two-pass one."""
+    the (min, max) pairs are the exact extremes of each group of 4 output
+    rows, and DynamicQuantizeLinear from them matches the two-pass one."""
     import torch
     rng = np.random.default_rng(rows * D)
     x = rng.normal(0.2, 1.3, (rows, D)).astype(np.float32)
@@ -936,8 +936,13 @@ def test_add_layernorm(dev, rows, D, res, beta):
         ref = ref + bt
     got = to_np(y)
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+    ng = (rows + 3) // 4
     pr = to_np(parts).reshape(rows, 2)
-    assert np.array_equal(pr[:, 0], np.minimum(got.min(-1), 0)) and np.array_equal(pr[:, 1], np.maximum(got.max(-1), 0))
+    assert np.isnan(pr[ng:]).all()   # one pair per 4 rows, nothing past them
+    for i in range(ng):
+        blk = got[4 * i:4 * i + 4]
+        assert pr[i, 0] == min(0.0, blk.min()) and pr[i, 1] == max(0.0, blk.max()), i
+    parts = parts[:2 * ng]
     q1, s1, z1 = H.dynamic_quantize_linear_parts(y, parts)
     q0, s0, z0 = H.dynamic_quantize_linear(y)
     assert to_np(s1)[0] == to_np(s0)[0] and to_np(z1)[0] == to_np(z0)[0]
