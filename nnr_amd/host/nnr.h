@@ -175,6 +175,10 @@ struct operator_t {
     // accept `add` (whose input conv_side, 0 or 3, is this operator's output)
     // into the kernel; false leaves everything unchanged
     virtual bool fuse_residual_add(operator_t* /*add*/, int /*conv_side*/) { return false; }
+    // a 1x1, stride-1, unpadded, ungrouped convolution (a dense GEMM over
+    // the NHWC pixels): its kernel takes a fused add at HBM rate, where a
+    // strided or spatial one (implicit im2col) is slower with it
+    virtual bool dense_pointwise() const { return false; }
     // nodes after this one whose work its kernel now does, in graph order
     // (fuse_matmul_dq_bias); they are skipped and the last one's output is ours
     std::vector<operator_t*> fused_chain;

@@ -140,6 +140,13 @@ struct QLinearConv_hip : operator_t {
         for (size_t i = 0; i < p.size() && i < pads.size(); ++i) pads[i] = (int)p[i];
         return true;
     }
+    bool dense_pointwise() const override {
+        if (group != 1 || kernels.size() != 2 || auto_pad == 1 || auto_pad == 2) return false;
+        for (size_t i = 0; i < 2; ++i)
+            if (kernels[i] != 1 || strides[i] != 1 || dilations[i] != 1 || pads[i] != 0 || pads[i + 2] != 0)
+                return false;
+        return true;
+    }
     bool per_channel_zp() const {
         tensor_t* z = in((operator_t*)this, 5);
         if (!z || z->ndata <= 1 || !z->has_host()) return false;

@@ -40,6 +40,7 @@
 //                     writes only the pooled tensor (bit-identical)
 // The fused operators are created through the registry with the context's
 // preferred backend, exactly where the reference calls solve_operator.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <unordered_map>
@@ -481,15 +482,19 @@ void fuse_conv_add(context_t* ctx) {
     auto& nodes = ctx->nodes;
     const int n = (int)nodes.size();
     std::unordered_map<tensor_t*, int> producer;
-    for (int i = 0; i < n; ++i) {
-        if (!active(nodes[i])) continue;
-        for (auto* t : nodes[i]->outputs)
-            if (t) producer[t] = i;
-    }
+    auto rebuild_producer = [&]() {
+        producer.clear();
+        for (int j = 0; j < n; ++j) {
+            if (!active(nodes[j])) continue;
+            for (auto* t : nodes[j]->outputs)
+                if (t) producer[t] = j;
+        }
+    };
+    rebuild_producer();
     std::unordered_set<tensor_t*> graph_out;
     for (auto& name : ctx->graph_outputs)
         if (tensor_t* t = ctx->find(name)) graph_out.insert(t);
-    int fused = 0;
+    int fused = 0, moved = 0;
     for (int i = 0; i < n; ++i) {
         operator_t* add = nodes[i];
         if (!active(add) || add->op_type != "QLinearAdd" || add->inputs.size() != 8) continue;
@@ -499,7 +504,37 @@ void fuse_conv_add(context_t* ctx) {
             auto it = producer.find(t);
             return it == producer.end() ? -1 : it->second;
         };
-        const int pa = prod(a), pb = prod(b);
+        int pa = prod(a), pb = prod(b);
+        int moved_at = -1, moved_from = -1;
+        // both operands from convolutions, the later one strided or spatial
+        // and the earlier one a dense 1x1 (a bottleneck's downsample and
+        // last conv): the later one moves before the earlier one when its
+        // inputs exist by then, so that the dense conv, now later, takes the
+        // add (its kernel streams the residual at HBM rate)
+        if (pa >= 0 && pb >= 0 && pa != pb) {
+            const int lo = std::min(pa, pb), hi = std::max(pa, pb);
+            operator_t *early = nodes[lo], *late = nodes[hi];
+            bool movable = early->op_type == "QLinearConv" && late->op_type == "QLinearConv" &&
+                           early->dense_pointwise() && !late->dense_pointwise() && !early->fused_add &&
+                           !late->fused_add;
+            for (auto* t : late->inputs)
+                if (movable && t && prod(t) >= lo) movable = false;
+            for (int j = lo; movable && j < hi; ++j) {
+                if (!active(nodes[j])) continue;
+                for (auto* t : nodes[j]->inputs)
+                    for (auto* o : late->outputs)
+                        if (t && t == o) movable = false;
+            }
+            if (movable) {
+                nodes.erase(nodes.begin() + hi);
+                nodes.insert(nodes.begin() + lo, late);
+                rebuild_producer();
+                pa = prod(a);
+                pb = prod(b);
+                moved_at = lo;
+                moved_from = hi;
+            }
+        }
         // try the later producer first: the other operand then already exists
         int order[2][2] = {{pa, 0}, {pb, 3}};
         if (pb > pa) { std::swap(order[0][0], order[1][0]); std::swap(order[0][1], order[1][1]); }
@@ -521,8 +556,20 @@ void fuse_conv_add(context_t* ctx) {
             ++fused;
             break;
         }
+        if (moved_at >= 0) {
+            if (add->skip) {
+                ++moved;
+            } else {
+                // the dense conv did not take the add: the original order back
+                operator_t* late = nodes[moved_at];
+                nodes.erase(nodes.begin() + moved_at);
+                nodes.insert(nodes.begin() + moved_from, late);
+                rebuild_producer();
+            }
+        }
     }
     ctx->fusion_stats["conv_add"] = fused;
+    ctx->fusion_stats["conv_add_reordered"] = moved;
 }
 
 // ---------------------------------------------------------------------------
