@@ -120,6 +120,11 @@ int nnr_ctx_node_fused_chain(nnr_ctx_t ctx, int i, int k, const char** node_name
 int nnr_ctx_node_fused_pre(nnr_ctx_t ctx, int i, int k, const char** node_name);
 int nnr_ctx_fusion_stat(nnr_ctx_t ctx, const char* key, int* value);
 size_t nnr_ctx_device_bytes(nnr_ctx_t ctx);
+/* Bytes of the context's shared operator workspace (the reference's
+ * context_t::workspace_size, src/nnr.h:557-558): the largest scratch one
+ * active operator's exec needs, allocated once by prepare and included in
+ * nnr_ctx_device_bytes; 0 when no operator needs scratch. */
+size_t nnr_ctx_workspace_bytes(nnr_ctx_t ctx);
 
 /* Load an ONNX model (ModelProto bytes) into an empty context: the
  * replacement of the reference's load_onnx (src/format/onnx/onnx_loader.cpp:

@@ -69,6 +69,7 @@ def host_lib():
             "nnr_ctx_node_fused_pre": (i, [vp, i, i, P(cp)]),
             "nnr_ctx_fusion_stat": (i, [vp, cp, P(i)]),
             "nnr_ctx_device_bytes": (C.c_size_t, [vp]),
+            "nnr_ctx_workspace_bytes": (C.c_size_t, [vp]),
             "nnr_ctx_set_memory_planning": (i, [vp, i]),
             "nnr_ctx_load_onnx": (i, [vp, vp, C.c_size_t, cp, i]),
             "nnr_ctx_load_onnx_file": (i, [vp, cp, i]),
@@ -329,6 +330,10 @@ class Session:
 
     def device_bytes(self):
         return int(self.L.nnr_ctx_device_bytes(self.h))
+
+    def workspace_bytes(self):
+        """Bytes of the operators' shared scratch buffer (0: none needed)."""
+        return int(self.L.nnr_ctx_workspace_bytes(self.h))
 
     def memory_plan(self):
         """The memory plan: (stats dict, entries). Without a prepared device

@@ -461,6 +461,7 @@ int nnr_ctx_fusion_stat(nnr_ctx_t c, const char* key, int* value) {
 }
 
 size_t nnr_ctx_device_bytes(nnr_ctx_t c) { return c ? c->ctx.device_bytes : 0; }
+size_t nnr_ctx_workspace_bytes(nnr_ctx_t c) { return c ? c->ctx.workspace_bytes : 0; }
 
 int nnr_ctx_enable_profiling(nnr_ctx_t c, int on) {
     return guarded("ctx_enable_profiling", [&]() -> int {

@@ -466,8 +466,17 @@ bool context_t::prepare() {
             fuse_codes_readers(this);
         }
     }
-    // 6. device memory and constant upload
+    // 6. device memory and constant upload; the shared operator workspace is
+    // sized after the fusions, which change what some operators need
     if (!plan_memory()) return false;
+    size_t ws = 0;
+    for (auto* op : nodes)
+        if (!op->skip && !op->folded) ws = std::max(ws, op->workspace_size());
+    if (ws) {
+        workspace = device_alloc((ws + 255) & ~size_t(255));
+        if (!workspace) return fail(std::string("workspace allocation failed: ") + nnrh_last_error());
+        workspace_bytes = ws;
+    }
     if (!upload_constants()) return fail(nnrh_last_error());
     profile.clear();
     for (auto* op : nodes) {

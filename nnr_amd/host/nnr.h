@@ -148,6 +148,10 @@ struct operator_t {
     // default: output has the input's shape and type (src/nnr.h:369-381)
     virtual bool reshape();
     virtual bool exec() = 0;
+    // device scratch one exec needs; it lives only for that exec, so every
+    // operator of the context shares one buffer, ctx->workspace, of the
+    // largest size (src/nnr.h:384, src/nnr.cpp:1067-1069)
+    virtual size_t workspace_size() const { return 0; }
     // algorithmic work of one exec (per-layer TOPS / GB/s reporting)
     virtual double num_ops() const { return 0.0; }
     virtual double num_bytes() const;
@@ -334,6 +338,10 @@ struct context_t {
     bool optimized = false;
     bool prepared = false;
     size_t device_bytes = 0;
+    // the operators' shared scratch (src/nnr.h:557-558): max workspace_size()
+    // over the active operators, allocated in prepare(); nullptr when 0
+    void* workspace = nullptr;
+    size_t workspace_bytes = 0;
 
     bool fail(const std::string& msg);
     // device memory that lives as long as the context (nullptr on failure)

@@ -80,8 +80,6 @@ struct DequantizeLinear_hip : operator_t {
 
 // DynamicQuantizeLinear (src/backend/cpu/DynamicQuantizeLinear.cpp)
 struct DynamicQuantizeLinear_hip : operator_t {
-    void* ws = nullptr;
-    ~DynamicQuantizeLinear_hip() override { nnrh_free(ws); }
     bool init() override {
         layout_mask = LAYOUT_ALL;
         return inputs.size() == 1 && outputs.size() == 3;
@@ -93,10 +91,12 @@ struct DynamicQuantizeLinear_hip : operator_t {
         outputs[1]->reshape({}, NNR_DATA_TYPE_FLOAT32);
         outputs[2]->reshape({}, NNR_DATA_TYPE_UINT8);
         outputs[1]->device_only = outputs[2]->device_only = true;
-        if (ctx->shape_only) return true;
-        if (!ws && nnrh_malloc(&ws, nnrh_dynamic_quantize_workspace()) != NNRH_OK)
-            return bad(this, nnrh_last_error());
         return true;
+    }
+    // the (min, max) partials of the two-pass quantize; the producer's pairs
+    // or bytes replace them when a fusion set minmax_src / codes_src
+    size_t workspace_size() const override {
+        return codes_src || minmax_src ? 0 : nnrh_dynamic_quantize_workspace();
     }
     std::string variant() const override { return codes_src ? "Codes" : minmax_src ? "MinMaxIn" : ""; }
     bool exec() override {
@@ -108,7 +108,7 @@ struct DynamicQuantizeLinear_hip : operator_t {
                                 (float*)outputs[1]->data, (uint8_t*)outputs[2]->data, ctx->stream));
         return ok(this, nnrh_dynamic_quantize_linear(
                             (const float*)inputs[0]->data, inputs[0]->ndata, (uint8_t*)outputs[0]->data,
-                            (float*)outputs[1]->data, (uint8_t*)outputs[2]->data, ws, ctx->stream));
+                            (float*)outputs[1]->data, (uint8_t*)outputs[2]->data, ctx->workspace, ctx->stream));
     }
 };
 
@@ -1380,9 +1380,7 @@ struct Softmax_hip : operator_t {
 struct MultiHeadAttention_hip : operator_t {
     int num_heads = 0;
     float scale = 0.0f;
-    void* ws = nullptr;
-    size_t ws_bytes = 0;
-    ~MultiHeadAttention_hip() override { nnrh_free(ws); }
+    size_t ws_need = 0;   // score matrix of the general path; 0 on the fused head-64 path
     bool init() override {
         num_heads = (int)attribute("num_heads", 0);
         scale = attribute_f("scale", 0.0f);
@@ -1396,20 +1394,11 @@ struct MultiHeadAttention_hip : operator_t {
         for (size_t i = 3; i < inputs.size(); ++i)
             if (inputs[i] && inputs[i]->ndata) return bad(this, "bias / masks / past state are not supported");
         if (q->dims[2] % num_heads) return bad(this, "hidden not divisible by num_heads");
-        if (!ctx->shape_only) {
-            size_t need = 0;
-            if (!ok(this, nnrh_multihead_attention_workspace(q->dims[0], q->dims[1], q->dims[2], num_heads, &need)))
-                return false;
-            if (need > ws_bytes) {
-                nnrh_free(ws);
-                ws = nullptr;
-                ws_bytes = 0;
-                if (!ok(this, nnrh_malloc(&ws, need))) return false;
-                ws_bytes = need;
-            }
-        }
+        if (!ok(this, nnrh_multihead_attention_workspace(q->dims[0], q->dims[1], q->dims[2], num_heads, &ws_need)))
+            return false;
         return outputs[0]->reshape(q->dims, q->type);
     }
+    size_t workspace_size() const override { return ws_need; }
     // one (min, max) pair per wave of the fused head-64 kernel, for the
     // DynamicQuantizeLinear of the output projection's input
     int minmax_pairs() const override {
@@ -1457,7 +1446,7 @@ struct MultiHeadAttention_hip : operator_t {
         }
         return ok(this, nnrh_multihead_attention_f32((const float*)q->data, (const float*)inputs[1]->data,
                                                      (const float*)inputs[2]->data, (float*)outputs[0]->data, B, S,
-                                                     Hd, num_heads, sc, minmax_parts, ws, ctx->stream));
+                                                     Hd, num_heads, sc, minmax_parts, ctx->workspace, ctx->stream));
     }
     double num_ops() const override {
         const tensor_t* q = inputs[0];

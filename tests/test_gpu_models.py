@@ -281,6 +281,26 @@ def test_bert_per_node(dev, fused):
     assert len(exact_chains) == 5 * 2
 
 
+def test_operator_workspace(dev):
+    """One scratch buffer per context, sized by the largest operator need
+    (src/nnr.h:384,557-558, src/nnr.cpp:1067-1069): in BERT only the graph
+    input's DynamicQuantizeLinear needs scratch once the other quantizers read
+    their producers' pairs or bytes; with the fusions off all eight share the
+    one buffer (test_bert_per_node checks those quantizers' bytes against
+    the oracle, fused and unfused)."""
+    from nnr_amd._lib import lib
+    need = int(lib().nnrh_dynamic_quantize_workspace())
+    g = synth.bert(batch=2, seq=64, layers=1)
+    x = np.random.default_rng(23).uniform(-1.0, 1.0, (2, 64, 768)).astype(np.float32)
+    for fused in (True, False):
+        s = G.Session(g, conv_add=fused)
+        s.set_input("input", x)
+        s.run()
+        assert s.workspace_bytes() == need, (fused, s.workspace_bytes(), need)
+        for o in g.outputs:
+            assert np.isfinite(s.output(o)[0]).all()
+
+
 def test_bert_full_depth_seq128(dev):
     """cfg5 at its real per-sequence shape: 12 layers, seq 128, hidden 768,
     12 heads, FFN 3072 (batch 2 of the config's 64: the batch only repeats
