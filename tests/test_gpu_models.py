@@ -299,6 +299,20 @@ def test_operator_workspace(dev):
         assert s.workspace_bytes() == need, (fused, s.workspace_bytes(), need)
         for o in g.outputs:
             assert np.isfinite(s.output(o)[0]).all()
+    # head size 32: the attention's general path, whose score matrix is the
+    # largest need; every node of that plan checked against the oracle
+    import ctypes as C
+    g2 = synth.bert(batch=2, seq=64, layers=1, hidden=256, heads=8, ffn=1024)
+    x2 = np.random.default_rng(29).uniform(-1.0, 1.0, (2, 64, 256)).astype(np.float32)
+    att = C.c_size_t()
+    assert lib().nnrh_multihead_attention_workspace(2, 64, 256, 8, C.byref(att)) == 0
+    assert att.value > need
+    s = G.Session(g2)
+    s.set_input("input", x2)
+    s.run()
+    assert "MultiHeadAttention" in [p["op"] for p in s.plan()]
+    assert s.workspace_bytes() == att.value
+    check_graph_per_node(g2, {"input": x2})
 
 
 def test_bert_full_depth_seq128(dev):
