@@ -125,8 +125,12 @@ __device__ __forceinline__ void block_barrier() {
 // (EPI_I32), the row sums taken from the A fragments on the way. FUSE_DQC:
 // the dequantize chain stores the uint8 RQ-D bytes (GemmArgs::dq_codes); its
 // values are formed only for the (min, max) pairs, when those are written
-enum { FUSE_NONE = 0, FUSE_ADD = 1, FUSE_DQB = 2, FUSE_ROW = 3, FUSE_DQC = 4 };
+// FUSE_ADD1: the fused add with one residual buffer for the block instead of
+// one per slot (tiles of at least S K-steps; the residual then loads with the
+// tile's step S - 1, after every wave's epilogue of the tile before)
+enum { FUSE_NONE = 0, FUSE_ADD = 1, FUSE_DQB = 2, FUSE_ROW = 3, FUSE_DQC = 4, FUSE_ADD1 = 5 };
 constexpr bool fuse_dq(int f) { return f == FUSE_DQB || f == FUSE_DQC; }
+constexpr bool fuse_add(int f) { return f == FUSE_ADD || f == FUSE_ADD1; }
 
 template <int EPI>
 struct EpiParams;
@@ -169,7 +173,8 @@ constexpr int dma_npx() { return EpiParams<EPI>::NP + (fuse_dq(FUSE) || FUSE == 
 // (KR > 0: the weights stay in registers, so a stage holds A rows only)
 template <int BM, int BN, int S, int NPX, int FUSE, int BK, int KR>
 constexpr int dma_lds_bytes() {
-    return S * (BM + (KR ? 0 : BN)) * BK + S * dma_pslot_bytes<BM, BN, S, NPX, FUSE>();
+    return S * (BM + (KR ? 0 : BN)) * BK + S * dma_pslot_bytes<BM, BN, S, NPX, FUSE>() +
+           (FUSE == FUSE_ADD1 ? BM * BN : 0);
 }
 // blocks per CU the kernel is compiled for: LDS and registers must fit them
 // (4-wave blocks: 3 per CU when the LDS fits them, else 2; 8-wave blocks: 2)
@@ -238,10 +243,12 @@ void qgemm_dma_kernel(GemmArgs g) {
     constexpr int PPAR = PWAVES * 1024;
     constexpr int PSLOT = dma_pslot_bytes<BM, BN, S, NPX, FUSE>();
     constexpr int RCPR = BN / 16;                    // residual chunks per row
-    constexpr int RCH = FUSE == FUSE_ADD ? BM * BN / RND : 0;   // residual DMAs per thread
+    constexpr int RCH = fuse_add(FUSE) ? BM * BN / RND : 0;   // residual DMAs per thread
+    // FUSE_ADD1: the one residual buffer, after the slots
+    constexpr int RES1 = S * STAGE + S * PSLOT;
 
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE + S * PSLOT];
-    static_assert(FUSE != FUSE_ADD || (BM * BN) % RND == 0, "residual DMA granule");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE + S * PSLOT + (FUSE == FUSE_ADD1 ? BM * BN : 0)];
+    static_assert(!fuse_add(FUSE) || (BM * BN) % RND == 0, "residual DMA granule");
     static_assert(BM % RPR == 0 && BN % RPR == 0, "DMA rounds per tile");
     static_assert(FUSE != FUSE_ROW || EPI == EPI_I32, "row term: int32 epilogue");
 
@@ -474,11 +481,14 @@ void qgemm_dma_kernel(GemmArgs g) {
             const uint8_t* src = (const uint8_t*)base + (p_pbase + c) * 4;
             dma16(src, lds + S * STAGE + p_pslot + wave * 1024);
         }
-        if constexpr (FUSE == FUSE_ADD) {
-            if (p_kt == 0) {
+        if constexpr (fuse_add(FUSE)) {
+            if (p_kt == (FUSE == FUSE_ADD1 ? S - 1 : 0)) {
                 // the residual tile of the fused QLinearAdd (batch 1, row stride
                 // and base 16-byte aligned, N % 16 == 0: checked by the launcher);
-                // it lands with the tile's first K step, so the step waits cover it
+                // it lands with the tile's first K step (FUSE_ADD1: step S - 1),
+                // so the step waits cover it. FUSE_ADD1's one buffer: this step
+                // issues after the barrier that follows the last wave's epilogue
+                // of the tile before, whose residual it overwrites
                 const int m0 = p_setup_m0;
 #pragma unroll
                 for (int j = 0; j < RCH; ++j) {
@@ -488,7 +498,7 @@ void qgemm_dma_kernel(GemmArgs g) {
                     const int m = m0 + row, n = p_n0 + lc * 16;
                     const uint8_t* src = pad16;
                     if (m < g.M && n < g.N) src = g.add_other + (long long)m * g.ldy + n;
-                    dma16(src, lds + S * STAGE + p_pslot + PPAR + (j * NT + wave * 64) * 16);
+                    dma16(src, lds + (FUSE == FUSE_ADD1 ? RES1 : S * STAGE + p_pslot + PPAR) + (j * NT + wave * 64) * 16);
                 }
             }
         }
@@ -596,6 +606,8 @@ void qgemm_dma_kernel(GemmArgs g) {
         }
         // the accumulators started at c0 (acc + c0 = the reference's value)
         const uint8_t* ps = lds + S * STAGE + c_pslot;
+        // the tile's residual bytes (fused add)
+        const uint8_t* rtile = FUSE == FUSE_ADD1 ? lds + RES1 : ps + PPAR;
         v4i p0[4], p1[4];
 #pragma unroll
         for (int tn = 0; tn < 4; ++tn) {
@@ -675,12 +687,12 @@ void qgemm_dma_kernel(GemmArgs g) {
                 // it is used as it is, with no byte pack and unpack between
                 // the two requantizations
                 bool add_done = false;
-                if constexpr (FUSE == FUSE_ADD && EPI == EPI_RQB) {
+                if constexpr (fuse_add(FUSE) && EPI == EPI_RQB) {
                     const long long i0 = (long long)m * g.ldy + nb;
                     if (i0 + 16 <= g.add_body) {
                         const int rrow = wm * 64 + tm * 16 + frow;
                         const int rpc = (wn * 4 + fchunk) ^ (rrow & (RCPR - 1));
-                        const v4i rres = *(const v4i*)(ps + PPAR + (rrow * RCPR + rpc) * 16);
+                        const v4i rres = *(const v4i*)(rtile + (rrow * RCPR + rpc) * 16);
                         const float lo_f = (float)g.lo - (float)g.y_zp, hi_f = (float)g.hi - (float)g.y_zp;
                         auto add_body = [&](auto zp0_t) {
                             constexpr bool ZP0 = decltype(zp0_t)::value;
@@ -800,13 +812,13 @@ void qgemm_dma_kernel(GemmArgs g) {
                         packed[tn] = w;
                     }
                 }
-                if constexpr (FUSE == FUSE_ADD) if (!add_done) {
+                if constexpr (fuse_add(FUSE)) if (!add_done) {
                     // uint8 output (checked on the host)
                     const long long i0 = (long long)m * g.ldy + nb;
                     // this lane's 16 residual bytes (row m, columns nb..nb+15)
                     const int rrow = wm * 64 + tm * 16 + frow;
                     const int rpc = (wn * 4 + fchunk) ^ (rrow & (RCPR - 1));
-                    const v4i rres = *(const v4i*)(ps + PPAR + (rrow * RCPR + rpc) * 16);
+                    const v4i rres = *(const v4i*)(rtile + (rrow * RCPR + rpc) * 16);
                     if (i0 + 16 <= g.add_body) {
                         // RQ-E body, fma(a, sa, fma(b, sb, fixed)); into uint8
                         // the reference's rint, cvt and saturation is
@@ -888,7 +900,7 @@ void qgemm_dma_kernel(GemmArgs g) {
                     // (a plain store: the next layer reads this output, and a
                     // streaming store would send it past the caches to HBM)
                     *(v4i*)yrow = v4i{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
-                } else if constexpr (FUSE == FUSE_ADD) {
+                } else if constexpr (fuse_add(FUSE)) {
                     // (a fused add has output channels % 16 == 0: never ragged)
 #pragma unroll
                     for (int i = 0; i < 16; ++i)
@@ -1032,7 +1044,7 @@ void qgemm_dma_kernel(GemmArgs g) {
                         }
                 }
             }
-            if (FUSE == FUSE_ADD && g.add_conv_is_a) epilogue(std::true_type{});
+            if (fuse_add(FUSE) && g.add_conv_is_a) epilogue(std::true_type{});
             else epilogue(std::false_type{});
             if (fuse_dq(FUSE) && g.mm_parts) {
                 // one (min, max) pair per (tile, wave), at 2 * (WAVES * tile + wave)
@@ -1286,6 +1298,13 @@ hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
                         if (g.Kp == 64) return launch_dma<BM, BN, 2, AMODE, EPI_RQB, FUSE_ADD, 64, 1>(g, batch, s);
                         if (g.Kp == 128) return launch_dma<BM, BN, 2, AMODE, EPI_RQB, FUSE_ADD, 64, 2>(g, batch, s);
                     }
+                }
+                // one residual buffer where that gains a third block per CU
+                // (tiles of at least S_ADD K-steps)
+                constexpr int NPX = dma_npx<EPI_RQB, FUSE_ADD>();
+                if constexpr (dma_min_blocks<BM, BN, S_ADD, NPX, FUSE_ADD1, 64, 0, 1>() >
+                              dma_min_blocks<BM, BN, S_ADD, NPX, FUSE_ADD, 64, 0, 1>()) {
+                    if (g.Kp >= 64 * S_ADD) return launch_dma<BM, BN, S_ADD, AMODE, EPI_RQB, FUSE_ADD1>(g, batch, s);
                 }
                 return launch_dma<BM, BN, S_ADD, AMODE, EPI_RQB, FUSE_ADD>(g, batch, s);
             }
