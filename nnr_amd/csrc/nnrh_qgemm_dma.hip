@@ -1286,18 +1286,18 @@ hipError_t launch_dma_epi(const GemmArgs& g, int batch, hipStream_t s) {
         if constexpr (BK == 64 && (AMODE == A_CONV || AMODE == A_CONVU || AMODE == A_DENSE)) {
             if (g.epi == EPI_RQB && batch == 1) {
                 if constexpr (AMODE == A_DENSE && BM == 128 && BN == 128) {
-                    // K <= 128: weights in registers, so a slot holds A rows,
+                    // K = 64: weights in registers, so a slot holds A rows,
                     // the constants and the residual tile (25 KB): 2 stages
                     // at 3 blocks per CU (measured: ResNet-50's K = 64
-                    // layers 106 -> 96 us, K = 128 58 -> 55 us; 3 stages at
-                    // 2 blocks per CU gain half that). Only with a few tiles
-                    // for every resident block.
+                    // layers 106 -> 96 us; 3 stages at 2 blocks per CU gain
+                    // half that). Only with a few tiles for every resident
+                    // block. (K = 128 in registers spills at 3 blocks per CU;
+                    // the one-residual-buffer kernel below is 2 % faster
+                    // over ResNet-50.)
                     const long long q = 8LL * ((g.N + BN - 1) / BN);
                     const long long tiles = (long long)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-                    if (tiles >= 4 * q) {
-                        if (g.Kp == 64) return launch_dma<BM, BN, 2, AMODE, EPI_RQB, FUSE_ADD, 64, 1>(g, batch, s);
-                        if (g.Kp == 128) return launch_dma<BM, BN, 2, AMODE, EPI_RQB, FUSE_ADD, 64, 2>(g, batch, s);
-                    }
+                    if (tiles >= 4 * q && g.Kp == 64)
+                        return launch_dma<BM, BN, 2, AMODE, EPI_RQB, FUSE_ADD, 64, 1>(g, batch, s);
                 }
                 // one residual buffer where that gains a third block per CU
                 // (tiles of at least S_ADD K-steps)
