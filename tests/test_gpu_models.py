@@ -66,6 +66,7 @@ B256_VARIANTS = {
                  "variant:dma<256,64,2,3,",       # 2-stage 256x64 uniform-tap conv tiles
                  ",128,0,2>",                     # K split over two waves a sub-tile
                  ",64,1,1>",                      # weights in registers (fused add, K = 64)
+                 ",2,5,64,0,1>",                  # one residual buffer a block (fused add, K >= 128)
                  "variant:direct"),               # the short-K direct kernel (K = 64, no add)
     "mobilenetv2": ("variant:dma<256,64,", "variant:direct"),
 }
